@@ -1,0 +1,155 @@
+/*
+ * librte_hip — C ABI of the MI355X (gfx950) kernels behind the recursive_macro
+ * hot path.  Plain pointers and sizes only: device pointers to caller-owned
+ * buffers, `stream` is a hipStream_t passed as void*.  Nothing here allocates
+ * device memory; workspaces are sized by the *_workspace_bytes helpers and
+ * passed in.  Every int-returning entry point returns 0 on success, otherwise a
+ * nonzero code with a message in rte_last_error() (per host thread).
+ *
+ * Element types: "bf16" buffers hold raw bfloat16 words (uint16), "f32" IEEE
+ * float, index buffers int32.  Matrices are row-major unless stated.
+ *
+ * Reference interfaces replaced (paths relative to the reference repository,
+ * src/recursive_training_engine = rte/):
+ *   rte/kernels/optimized.py:58-154 k_* dispatch symbols, backend_status :27-43
+ *   rte/kernels/cluster_pool_ffn.py:32-87 Triton slot/pack/gather kernels,
+ *       :129-241 routing, pack-index build, preindexed pooled FFN, grad scatter
+ *   rte/kernels/active_swiglu_triton.py:20-102 fused SwiGLU fwd/bwd
+ *   rte/layers.py:53-87 fused QKV attention projection + dense SwiGLU
+ */
+#ifndef RTE_HIP_H
+#define RTE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status (replaces backend_status(), rte/kernels/optimized.py:27-43) ---- */
+int rte_abi_version(void);
+const char* rte_last_error(void);
+/* Writes "arch=gfx950;cus=256;lds_per_block=...;..." for the current device. */
+int rte_device_info(char* buf, int buf_len);
+
+/* ---- generic bf16 MFMA GEMM:  C[m,n] = alpha * sum_k A(m,k) B(n,k) (+beta C) (+resid) ----
+ * a_t == 0: A(m,k) = a[m*lda + k]   a_t == 1: A(m,k) = a[k*lda + m]  (same for B with n)
+ * a_rows / b_rows (optional, int32): memory-row indirection, applied to m (a_t=0) or k (a_t=1).
+ * c_f32 selects fp32 or bf16 output; resid (fp32, optional) is added element-wise.
+ * Replaces the torch matmuls behind nn.Linear in rte/layers.py:53-87. */
+int rte_gemm_bf16(const void* a, int64_t lda, int a_t, const int32_t* a_rows,
+                  const void* b, int64_t ldb, int b_t, const int32_t* b_rows,
+                  void* c, int64_t ldc, int c_f32, int M, int N, int K,
+                  float alpha, float beta, const float* resid, int64_t ld_resid, void* stream);
+
+/* Same, with attention-layout operands: row r -> (r / rdiv)*rs_hi + (r % rdiv)*ld and
+ * contiguous index c -> (c / cdiv)*cs_hi + c % cdiv  (rdiv/cdiv = 0: plain).
+ * layout[] = {ld, rdiv, rs_hi, cdiv, cs_hi}.  Used for [B,H,S,hd] attention outputs
+ * feeding the output projection (rte/layers.py:73-75). */
+int rte_gemm_bf16_split(const void* a, const int64_t* a_layout, int a_t,
+                        const void* b, const int64_t* b_layout, int b_t,
+                        void* c, int64_t ldc, int c_f32, int M, int N, int K,
+                        float alpha, float beta, const float* resid, int64_t ld_resid, void* stream);
+
+/* ---- routing (rte/kernels/cluster_pool_ffn.py:129-140 generalised to per-token top-k;
+ *      rte/models.py:300-309 softmax-over-selected combine rule) ----
+ * ids[t*k + j]: j-th best cluster (value descending, ties -> lower index, NaN first).
+ * weights: softmax over the k selected logits.  C <= 1024, k <= 16. */
+int rte_route_topk(const float* logits, int T, int C, int k, int32_t* ids, float* weights, void* stream);
+
+/* ---- deterministic pack index (replaces build_static_pack_gather_indices
+ *      rte/kernels/cluster_pool_ffn.py:165-189 and _assign_slots_kernel :32-45) ----
+ * cl[p] = cluster of pair p (p = t*k + j).  Stable counting sort by cluster:
+ *   offsets[C+1], tok_of_slot[P] = p / k, pair_of_slot[P], slot_of_pair[P] (-1 if cl invalid),
+ *   w_of_slot[P] = w[p] (1 if w is NULL).  invalid (optional, int32, caller-zeroed) counts
+ *   pairs whose cluster id is outside [0, C).  Any output pointer may be NULL. */
+size_t rte_pack_workspace_bytes(int P, int C);
+int rte_pack_index(const int32_t* cl, int P, int C, int k, const float* w, int32_t* offsets,
+                   int32_t* tok_of_slot, int32_t* pair_of_slot, int32_t* slot_of_pair,
+                   float* w_of_slot, int32_t* invalid, void* workspace, size_t workspace_bytes,
+                   void* stream);
+
+/* out[t] = resid[t] + extra[t] + sum_{j<k} rows[t*k + j]  (j ascending; fp32 accumulation)
+ * rows, extra: bf16; resid: f32 (optional); out: f32 (out_f32=1) or bf16.
+ * Replaces _gather_y_kernel (rte/kernels/cluster_pool_ffn.py:69-87) plus the top-k sum. */
+int rte_combine_rows(const void* rows, int T, int k, int d, const void* extra, const float* resid,
+                     void* out, int out_f32, void* stream);
+
+/* Routing-weight backward: dlogits[t, ids[t,j]] = w_j (dw_j - sum_i w_i dw_i), zero elsewhere.
+ * dw_slot is indexed by slot (slot_of_pair maps pairs).  Either output may be NULL. */
+int rte_route_bwd(const int32_t* ids, const float* w, const float* dw_slot, const int32_t* slot_of_pair,
+                  int T, int C, int k, void* dlogits_bf16, float* dlogits_f32, void* stream);
+
+/* ---- routed cluster-pool SwiGLU (rte/kernels/cluster_pool_ffn.py:192-241,
+ *      rte/layers.py:119-220 StaticClusterPoolSwiGLU, rte/layers.py:731-779 BankedSwiGLU) ----
+ * Cluster g owns neurons [g*n, (g+1)*n) of a d_ff = G*n SwiGLU:
+ *   wug: bf16 [2*d_ff, d] rows [W_up ; W_gate] (nn.Linear(d, 2*d_ff).weight layout)
+ *   wd : bf16 [d, ld_wd] with column g*n + j = W_down row of neuron j of cluster g
+ *        (nn.Linear(d_ff, d).weight layout when ld_wd = d_ff)
+ * Slots come from rte_pack_index.  Forward writes
+ *   ug [P, 2n] bf16 pre-activations (per 64 columns: 32 up | 32 gate),
+ *   zw [P, n]  bf16 w_of_slot * up * silu(gate),
+ *   y_pairs [T*k, d] bf16 in pair order, y = zw @ W_down_g   (combine with rte_combine_rows).
+ * max_tiles bound: P/128 + G + 1 is always enough. */
+int rte_grouped_swiglu_fwd(const void* x, int T, int d, const int32_t* offsets, int G, int n, int P,
+                           const int32_t* tok_of_slot, const int32_t* pair_of_slot, const float* w_of_slot,
+                           const void* wug, const void* wd, int64_t ld_wd,
+                           void* ug, void* zw, void* y_pairs, void* stream);
+
+/* Backward.  dout [T, d] bf16 is dL/d(out) of the combined output.  Writes
+ *   dug     [P, 2n] bf16 (workspace-like output),
+ *   dw_slot [P] f32    = <dout[t], y_unweighted>  (routing-weight gradient per slot),
+ *   dx_pairs[T*k, d] bf16 in pair order (combine them for dx),
+ *   dwug    [2*d_ff, d] f32 and dwd [d, ld_wd] f32 (overwritten; every neuron row is
+ *           owned by exactly one cluster, so no reduction across clusters is needed). */
+int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const int32_t* offsets, int G,
+                           int n, int P, const int32_t* tok_of_slot, const int32_t* pair_of_slot,
+                           const float* w_of_slot, const void* wug, const void* wd, int64_t ld_wd,
+                           const void* ug, const void* zw, void* dug, float* dw_slot, void* dx_pairs,
+                           float* dwug, float* dwd, void* stream);
+
+/* ---- dense SwiGLU (rte/layers.py:78-116 DenseSwiGLU / PackedDenseSwiGLU;
+ *      rte/kernels/active_swiglu_triton.py:62-102 fused activation fwd/bwd) ----
+ * wug bf16 [2F, d] rows [up ; gate].  wd_rows = 0: wd is [d, F] (nn.Linear(F, d).weight),
+ * wd_rows = 1: wd is [F, d] (the packed "wdown_rows" layout).
+ * out [T,d] = resid + (up * silu(gate)) @ W_down, f32 (out_f32=1) or bf16; resid f32 optional.
+ * ug [T, 2F] bf16 (interleaved per 64: 32 up | 32 gate), z [T, F] bf16. */
+int rte_dense_swiglu_fwd(const void* x, int T, int d, int F, const void* wug, const void* wd, int wd_rows,
+                         const float* resid, void* ug, void* z, void* out, int out_f32, void* stream);
+/* dout bf16 [T, d]; writes dug [T, 2F] bf16, dx [T, d] bf16, dwug [2F, d] f32,
+ * dwd f32 in the layout of wd (overwritten). */
+int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, const void* wug,
+                         const void* wd, int wd_rows, const void* ug, const void* z, void* dug, void* dx,
+                         float* dwug, float* dwd, void* stream);
+
+/* ---- fused QKV projection + interleaved RoPE (rte/layers.py:53-75, rte/kernels/reference.py:20-37) ----
+ * x [B*S, d] bf16, wqkv [3d, d] bf16 (nn.Linear(d, 3d).weight), cos/sin [S, hd] f32.
+ * q, k, v written as contiguous [B, H, S, hd] bf16. */
+int rte_qkv_rope_fwd(const void* x, const void* wqkv, const float* cos_t, const float* sin_t, int B, int S,
+                     int H, int hd, void* q, void* k, void* v, void* stream);
+/* dq/dk/dv: [B,H,S,hd] bf16 with element strides s*[4] (innermost must be 1).
+ * dqkv: [B*S, 3d] bf16 workspace; dx [B*S, d] bf16; dw [3d, d] f32 (overwritten). */
+int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const int64_t* sk, const void* dv,
+                     const int64_t* sv, const void* x, const void* wqkv, const float* cos_t,
+                     const float* sin_t, int B, int S, int H, int hd, void* dqkv, void* dx, float* dw,
+                     void* stream);
+
+/* ---- RMSNorm (rte/kernels/reference.py:9-17, rte/layers.py:26-33) ----
+ * out bf16 = bf16(x * rsqrt(mean(x^2) + eps) * w), rstd [T] f32 saved for backward. */
+int rte_rmsnorm_fwd(const float* x, const float* w, int T, int d, float eps, void* out, float* rstd,
+                    void* stream);
+size_t rte_rmsnorm_bwd_workspace_bytes(int T, int d);
+/* dy bf16; dx f32 (= dres + norm backward, dres optional); dw f32 [d] (accumulated if dw_accumulate). */
+int rte_rmsnorm_bwd(const void* dy, const float* x, const float* w, const float* rstd, const float* dres,
+                    int T, int d, float* dx, float* dw, int dw_accumulate, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* fp32 -> bf16 (round to nearest even) */
+int rte_cast_f32_bf16(const float* x, int64_t n, void* y, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RTE_HIP_H */

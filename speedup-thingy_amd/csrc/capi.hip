@@ -1,0 +1,497 @@
+// extern "C" entry points of librte_hip (declared in include/rte_hip.h).
+// Composite operators are sequences of GEMM launches from gemm.hip plus the
+// routing / norm helpers; nothing here allocates device memory.
+#include "../../include/rte_hip.h"
+#include "gemm.hpp"
+
+#include <stdio.h>
+#include <string.h>
+
+namespace rte {
+const char* last_error();
+int route_topk(const float* logits, int T, int C, int k, int32_t* ids, float* weights, hipStream_t s);
+size_t pack_workspace_bytes(int P, int C);
+int pack_pairs(const int32_t* cl, int P, int C, int k, const float* w, int32_t* offsets,
+               int32_t* tok_of_slot, int32_t* pair_of_slot, int32_t* slot_of_pair, float* w_of_slot,
+               int32_t* invalid, void* ws, size_t ws_bytes, hipStream_t s);
+int combine_rows(const bf16* rows, int T, int k, int d, const bf16* extra, const float* resid, void* out,
+                 int out_f32, hipStream_t s);
+int route_bwd(const int32_t* ids, const float* w, const float* dw_slot, const int32_t* slot_of_pair, int T,
+              int C, int k, bf16* dlogits, float* dlogits_f32, hipStream_t s);
+int rmsnorm_fwd(const float* x, const float* w, int T, int d, float eps, bf16* out, float* rstd,
+                hipStream_t s);
+size_t rmsnorm_bwd_workspace_bytes(int T, int d);
+int rmsnorm_bwd(const bf16* dy, const float* x, const float* w, const float* rstd, const float* dres, int T,
+                int d, float* dx, float* dw, int dw_accumulate, void* ws, size_t ws_bytes, hipStream_t s);
+int rope_bwd_pack(const bf16* dq, const int64_t* sq, const bf16* dk, const int64_t* sk, const bf16* dv,
+                  const int64_t* sv, const float* cos_t, const float* sin_t, int B, int H, int S, int hd,
+                  bf16* dqkv, hipStream_t s);
+int cast_f32_bf16(const float* x, int64_t n, bf16* y, hipStream_t s);
+}  // namespace rte
+
+using namespace rte;
+
+namespace {
+
+inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+inline const bf16* B16(const void* p) { return static_cast<const bf16*>(p); }
+inline bf16* B16(void* p) { return static_cast<bf16*>(p); }
+
+Operand plain(const void* p, int64_t ld) {
+  Operand o;
+  o.ptr = B16(p);
+  o.ld = ld;
+  return o;
+}
+
+Operand from_layout(const void* p, const int64_t* L) {
+  Operand o;
+  o.ptr = B16(p);
+  o.ld = L[0];
+  o.rdiv = (int32_t)L[1];
+  o.rs_hi = L[2];
+  o.cdiv = (int32_t)L[3];
+  o.cs_hi = L[4];
+  return o;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rte_abi_version(void) { return 1; }
+
+const char* rte_last_error(void) { return last_error(); }
+
+int rte_device_info(char* buf, int buf_len) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("hipGetDevice: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, dev);
+  if (e != hipSuccess) {
+    set_error("hipGetDeviceProperties: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  int lds_optin = 0;
+  hipDeviceGetAttribute(&lds_optin, hipDeviceAttributeSharedMemPerBlockOptin, dev);
+  snprintf(buf, buf_len, "arch=%s;name=%s;cus=%d;lds_per_block=%zu;lds_optin=%d;clock_khz=%d;hbm_bytes=%zu",
+           prop.gcnArchName, prop.name, prop.multiProcessorCount, (size_t)prop.sharedMemPerBlock, lds_optin,
+           prop.clockRate, (size_t)prop.totalGlobalMem);
+  return 0;
+}
+
+int rte_gemm_bf16(const void* a, int64_t lda, int a_t, const int32_t* a_rows, const void* b, int64_t ldb,
+                  int b_t, const int32_t* b_rows, void* c, int64_t ldc, int c_f32, int M, int N, int K,
+                  float alpha, float beta, const float* resid, int64_t ld_resid, void* stream) {
+  GemmArgs p;
+  p.a = plain(a, lda);
+  p.a.rows = a_rows;
+  p.b = plain(b, ldb);
+  p.b.rows = b_rows;
+  p.a_t = a_t;
+  p.b_t = b_t;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.epi.c = c;
+  p.epi.ldc = ldc;
+  p.epi.c_f32 = c_f32;
+  p.epi.alpha = alpha;
+  p.epi.beta = beta;
+  p.epi.resid = resid;
+  p.epi.ld_resid = ld_resid;
+  return gemm_launch(p, EPI_STORE, S(stream));
+}
+
+int rte_gemm_bf16_split(const void* a, const int64_t* a_layout, int a_t, const void* b, const int64_t* b_layout,
+                        int b_t, void* c, int64_t ldc, int c_f32, int M, int N, int K, float alpha, float beta,
+                        const float* resid, int64_t ld_resid, void* stream) {
+  GemmArgs p;
+  p.a = from_layout(a, a_layout);
+  p.b = from_layout(b, b_layout);
+  p.a_t = a_t;
+  p.b_t = b_t;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.epi.c = c;
+  p.epi.ldc = ldc;
+  p.epi.c_f32 = c_f32;
+  p.epi.alpha = alpha;
+  p.epi.beta = beta;
+  p.epi.resid = resid;
+  p.epi.ld_resid = ld_resid;
+  // split columns must keep 8-element vectors inside one segment
+  if (p.a.cdiv) RTE_REQUIRE(p.a.cdiv % 8 == 0, "gemm_split: A cdiv must be a multiple of 8");
+  if (p.b.cdiv) RTE_REQUIRE(p.b.cdiv % 8 == 0, "gemm_split: B cdiv must be a multiple of 8");
+  return gemm_launch(p, EPI_STORE, S(stream));
+}
+
+int rte_route_topk(const float* logits, int T, int C, int k, int32_t* ids, float* weights, void* stream) {
+  return route_topk(logits, T, C, k, ids, weights, S(stream));
+}
+
+size_t rte_pack_workspace_bytes(int P, int C) { return pack_workspace_bytes(P, C); }
+
+int rte_pack_index(const int32_t* cl, int P, int C, int k, const float* w, int32_t* offsets,
+                   int32_t* tok_of_slot, int32_t* pair_of_slot, int32_t* slot_of_pair, float* w_of_slot,
+                   int32_t* invalid, void* workspace, size_t workspace_bytes, void* stream) {
+  return pack_pairs(cl, P, C, k, w, offsets, tok_of_slot, pair_of_slot, slot_of_pair, w_of_slot, invalid,
+                    workspace, workspace_bytes, S(stream));
+}
+
+int rte_combine_rows(const void* rows, int T, int k, int d, const void* extra, const float* resid, void* out,
+                     int out_f32, void* stream) {
+  return combine_rows(B16(rows), T, k, d, B16(extra), resid, out, out_f32, S(stream));
+}
+
+int rte_route_bwd(const int32_t* ids, const float* w, const float* dw_slot, const int32_t* slot_of_pair, int T,
+                  int C, int k, void* dlogits_bf16, float* dlogits_f32, void* stream) {
+  return route_bwd(ids, w, dw_slot, slot_of_pair, T, C, k, B16(dlogits_bf16), dlogits_f32, S(stream));
+}
+
+int rte_grouped_swiglu_fwd(const void* x, int T, int d, const int32_t* offsets, int G, int n, int P,
+                           const int32_t* tok_of_slot, const int32_t* pair_of_slot, const float* w_of_slot,
+                           const void* wug, const void* wd, int64_t ld_wd, void* ug, void* zw, void* y_pairs,
+                           void* stream) {
+  RTE_REQUIRE(n % 32 == 0, "grouped_swiglu: neurons per cluster must be a multiple of 32");
+  RTE_REQUIRE(d % 8 == 0, "grouped_swiglu: d_model must be a multiple of 8");
+  RTE_REQUIRE(T >= 0 && P >= 0 && G >= 1, "grouped_swiglu: bad sizes");
+  if (P == 0) return 0;
+  const int dff = G * n;
+  const int tiles = P / kGroupTileM + G + 1;
+  // stage 1: UG = x[tok] @ [W_up_g ; W_gate_g]^T  (interleaved per 32), SwiGLU -> zw
+  {
+    GemmArgs p;
+    p.mode = MODE_GROUP_M;
+    p.goff = offsets;
+    p.G = G;
+    p.max_tiles_m = tiles;
+    p.M = P;
+    p.N = 2 * n;
+    p.K = d;
+    p.a = plain(x, d);
+    p.a.rows = tok_of_slot;
+    p.b = plain(wug, d);
+    p.b.growstride = 2 * n;
+    p.b.ilv = dff;
+    p.epi.ug = B16(ug);
+    p.epi.ld_ug = 2 * n;
+    p.epi.z = B16(zw);
+    p.epi.ld_z = n;
+    p.epi.row_scale = w_of_slot;
+    RTE_TRY(gemm_launch(p, EPI_SWIGLU_FWD, S(stream)));
+  }
+  // stage 2: y_pairs[pair] = zw @ W_down_g    (B(n=dcol, k=j) = wd[dcol*ld_wd + g*n + j])
+  {
+    GemmArgs p;
+    p.mode = MODE_GROUP_M;
+    p.goff = offsets;
+    p.G = G;
+    p.max_tiles_m = tiles;
+    p.M = P;
+    p.N = d;
+    p.K = n;
+    p.a = plain(zw, n);
+    p.b = plain(wd, ld_wd);
+    p.b.gstride = n;
+    p.epi.c = y_pairs;
+    p.epi.ldc = d;
+    p.epi.c_rows = pair_of_slot;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  (void)T;
+  return 0;
+}
+
+int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const int32_t* offsets, int G, int n,
+                           int P, const int32_t* tok_of_slot, const int32_t* pair_of_slot,
+                           const float* w_of_slot, const void* wug, const void* wd, int64_t ld_wd, const void* ug,
+                           const void* zw, void* dug, float* dw_slot, void* dx_pairs, float* dwug, float* dwd,
+                           void* stream) {
+  RTE_REQUIRE(n % 32 == 0 && n <= 128, "grouped_swiglu_bwd: n must be a multiple of 32 and <= 128");
+  RTE_REQUIRE(d % 8 == 0, "grouped_swiglu_bwd: d_model must be a multiple of 8");
+  const int dff = G * n;
+  const int tiles = P / kGroupTileM + G + 1;
+  if (P > 0) {
+    // dZw = dout[tok] @ W_down_g^T  -> SwiGLU backward epilogue (dz = w * dZw), dw_slot = <z, dZw>
+    GemmArgs p;
+    p.mode = MODE_GROUP_M;
+    p.goff = offsets;
+    p.G = G;
+    p.max_tiles_m = tiles;
+    p.M = P;
+    p.N = n;
+    p.K = d;
+    p.a = plain(dout, d);
+    p.a.rows = tok_of_slot;
+    p.b = plain(wd, ld_wd);  // B(n=j, k=dcol) = wd[dcol*ld_wd + g*n + j]  -> layout T
+    p.b.gstride = n;
+    p.b_t = 1;
+    p.epi.ug_in = B16(ug);
+    p.epi.ug = B16(dug);
+    p.epi.ld_ug = 2 * n;
+    p.epi.row_scale = w_of_slot;
+    p.epi.dw_row = dw_slot;
+    RTE_TRY(gemm_launch(p, EPI_SWIGLU_BWD, S(stream)));
+  }
+  if (P > 0) {
+    // dx_pairs[pair] = dUG @ [W_up_g ; W_gate_g]   (B(n=dcol, k=c) = wug[ilv(g*2n + c)][dcol] -> layout T)
+    GemmArgs p;
+    p.mode = MODE_GROUP_M;
+    p.goff = offsets;
+    p.G = G;
+    p.max_tiles_m = tiles;
+    p.M = P;
+    p.N = d;
+    p.K = 2 * n;
+    p.a = plain(dug, 2 * n);
+    p.b = plain(wug, d);
+    p.b.growstride = 2 * n;
+    p.b.ilv = dff;
+    p.b_t = 1;
+    p.epi.c = dx_pairs;
+    p.epi.ldc = d;
+    p.epi.c_rows = pair_of_slot;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  {
+    // dWug_g[c, :] = sum_slot dUG[slot, c] x[tok(slot), :]
+    GemmArgs p;
+    p.mode = MODE_GROUP_K;
+    p.goff = offsets;
+    p.G = G;
+    p.M = 2 * n;
+    p.N = d;
+    p.K = P;
+    p.a = plain(dug, 2 * n);
+    p.a_t = 1;
+    p.b = plain(x, d);
+    p.b.rows = tok_of_slot;
+    p.b_t = 1;
+    p.epi.c = dwug;
+    p.epi.ldc = d;
+    p.epi.c_f32 = 1;
+    p.epi.c_growstride = 2 * n;
+    p.epi.c_ilv = dff;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  {
+    // dWd[:, g*n + j] = sum_slot dout[tok(slot), :] zw[slot, j]
+    GemmArgs p;
+    p.mode = MODE_GROUP_K;
+    p.goff = offsets;
+    p.G = G;
+    p.M = d;
+    p.N = n;
+    p.K = P;
+    p.a = plain(dout, d);
+    p.a.rows = tok_of_slot;
+    p.a_t = 1;
+    p.b = plain(zw, n);
+    p.b_t = 1;
+    p.epi.c = dwd;
+    p.epi.ldc = ld_wd;
+    p.epi.c_f32 = 1;
+    p.epi.c_gstride = n;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  (void)T;
+  (void)pair_of_slot;
+  return 0;
+}
+
+int rte_dense_swiglu_fwd(const void* x, int T, int d, int F, const void* wug, const void* wd, int wd_rows,
+                         const float* resid, void* ug, void* z, void* out, int out_f32, void* stream) {
+  RTE_REQUIRE(F % 32 == 0 && d % 8 == 0, "dense_swiglu: F %% 32 and d %% 8 must be 0");
+  {
+    GemmArgs p;
+    p.M = T;
+    p.N = 2 * F;
+    p.K = d;
+    p.a = plain(x, d);
+    p.b = plain(wug, d);
+    p.b.ilv = F;
+    p.epi.ug = B16(ug);
+    p.epi.ld_ug = 2 * F;
+    p.epi.z = B16(z);
+    p.epi.ld_z = F;
+    RTE_TRY(gemm_launch(p, EPI_SWIGLU_FWD, S(stream)));
+  }
+  {
+    // out = z @ W_down:  B(n=dcol, k=f) = wd[dcol][f] (layout N) or wd[f][dcol] (layout T)
+    GemmArgs p;
+    p.M = T;
+    p.N = d;
+    p.K = F;
+    p.a = plain(z, F);
+    p.b = plain(wd, wd_rows ? d : F);
+    p.b_t = wd_rows ? 1 : 0;
+    p.epi.c = out;
+    p.epi.ldc = d;
+    p.epi.c_f32 = out_f32;
+    p.epi.resid = resid;
+    p.epi.ld_resid = d;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  return 0;
+}
+
+int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, const void* wug, const void* wd,
+                         int wd_rows, const void* ug, const void* z, void* dug, void* dx, float* dwug,
+                         float* dwd, void* stream) {
+  RTE_REQUIRE(F % 32 == 0 && d % 8 == 0, "dense_swiglu: F %% 32 and d %% 8 must be 0");
+  {
+    // dZ = dout @ W_down^T: B(n=f, k=dcol) = wd[dcol][f] (layout T) or wd[f][dcol] (layout N)
+    GemmArgs p;
+    p.M = T;
+    p.N = F;
+    p.K = d;
+    p.a = plain(dout, d);
+    p.b = plain(wd, wd_rows ? d : F);
+    p.b_t = wd_rows ? 0 : 1;
+    p.epi.ug_in = B16(ug);
+    p.epi.ug = B16(dug);
+    p.epi.ld_ug = 2 * F;
+    RTE_TRY(gemm_launch(p, EPI_SWIGLU_BWD, S(stream)));
+  }
+  {
+    // dx = dUG @ W_ug   (B(n=dcol, k=c) = wug[ilv(c)][dcol] -> layout T)
+    GemmArgs p;
+    p.M = T;
+    p.N = d;
+    p.K = 2 * F;
+    p.a = plain(dug, 2 * F);
+    p.b = plain(wug, d);
+    p.b.ilv = F;
+    p.b_t = 1;
+    p.epi.c = dx;
+    p.epi.ldc = d;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  {
+    // dW_ug[ilv(c), :] = sum_t dUG[t, c] x[t, :]
+    GemmArgs p;
+    p.M = 2 * F;
+    p.N = d;
+    p.K = T;
+    p.a = plain(dug, 2 * F);
+    p.a_t = 1;
+    p.b = plain(x, d);
+    p.b_t = 1;
+    p.epi.c = dwug;
+    p.epi.ldc = d;
+    p.epi.c_f32 = 1;
+    p.epi.c_ilv = F;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  {
+    GemmArgs p;
+    p.K = T;
+    p.a_t = 1;
+    p.b_t = 1;
+    p.epi.c = dwd;
+    p.epi.c_f32 = 1;
+    if (wd_rows) {
+      // dW_rows[f, dcol] = sum_t z[t, f] dout[t, dcol]
+      p.M = F;
+      p.N = d;
+      p.a = plain(z, F);
+      p.b = plain(dout, d);
+      p.epi.ldc = d;
+    } else {
+      // dW_d[dcol, f] = sum_t dout[t, dcol] z[t, f]
+      p.M = d;
+      p.N = F;
+      p.a = plain(dout, d);
+      p.b = plain(z, F);
+      p.epi.ldc = F;
+    }
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  return 0;
+}
+
+int rte_qkv_rope_fwd(const void* x, const void* wqkv, const float* cos_t, const float* sin_t, int B, int S_,
+                     int H, int hd, void* q, void* k, void* v, void* stream) {
+  const int d = H * hd;
+  RTE_REQUIRE(d % 8 == 0 && hd % 2 == 0, "qkv_rope: bad head layout");
+  GemmArgs p;
+  p.M = B * S_;
+  p.N = 3 * d;
+  p.K = d;
+  p.a = plain(x, d);
+  p.b = plain(wqkv, d);
+  p.epi.q = B16(q);
+  p.epi.k = B16(k);
+  p.epi.v = B16(v);
+  p.epi.cos_t = cos_t;
+  p.epi.sin_t = sin_t;
+  p.epi.S = S_;
+  p.epi.H = H;
+  p.epi.hd = hd;
+  p.epi.dmodel = d;
+  return gemm_launch(p, EPI_ROPE_QKV, S(stream));
+}
+
+int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const int64_t* sk, const void* dv,
+                     const int64_t* sv, const void* x, const void* wqkv, const float* cos_t, const float* sin_t,
+                     int B, int S_, int H, int hd, void* dqkv, void* dx, float* dw, void* stream) {
+  const int d = H * hd;
+  const int T = B * S_;
+  RTE_TRY(rope_bwd_pack(B16(dq), sq, B16(dk), sk, B16(dv), sv, cos_t, sin_t, B, H, S_, hd, B16(dqkv),
+                        S(stream)));
+  {
+    // dx = dqkv @ Wqkv   (B(n=dcol, k=c) = wqkv[c][dcol] -> layout T)
+    GemmArgs p;
+    p.M = T;
+    p.N = d;
+    p.K = 3 * d;
+    p.a = plain(dqkv, 3 * d);
+    p.b = plain(wqkv, d);
+    p.b_t = 1;
+    p.epi.c = dx;
+    p.epi.ldc = d;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  {
+    // dW[c, :] = sum_t dqkv[t, c] x[t, :]
+    GemmArgs p;
+    p.M = 3 * d;
+    p.N = d;
+    p.K = T;
+    p.a = plain(dqkv, 3 * d);
+    p.a_t = 1;
+    p.b = plain(x, d);
+    p.b_t = 1;
+    p.epi.c = dw;
+    p.epi.ldc = d;
+    p.epi.c_f32 = 1;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  return 0;
+}
+
+int rte_rmsnorm_fwd(const float* x, const float* w, int T, int d, float eps, void* out, float* rstd,
+                    void* stream) {
+  return rmsnorm_fwd(x, w, T, d, eps, B16(out), rstd, S(stream));
+}
+
+size_t rte_rmsnorm_bwd_workspace_bytes(int T, int d) { return rmsnorm_bwd_workspace_bytes(T, d); }
+
+int rte_rmsnorm_bwd(const void* dy, const float* x, const float* w, const float* rstd, const float* dres, int T,
+                    int d, float* dx, float* dw, int dw_accumulate, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  return rmsnorm_bwd(B16(dy), x, w, rstd, dres, T, d, dx, dw, dw_accumulate, workspace, workspace_bytes,
+                     S(stream));
+}
+
+int rte_cast_f32_bf16(const float* x, int64_t n, void* y, void* stream) {
+  return cast_f32_bf16(x, n, B16(y), S(stream));
+}
+
+}  // extern "C"

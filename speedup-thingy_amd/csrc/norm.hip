@@ -1,0 +1,245 @@
+// Elementwise / row-reduction kernels around the GEMMs: RMSNorm forward and
+// backward (deterministic two-stage weight-gradient reduction), the inverse
+// RoPE + [B,H,S,hd] -> [T, 3d] repack for the fused-QKV backward, dtype casts,
+// fills, and the library's error state.
+#include "common.hpp"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+namespace rte {
+
+static thread_local char g_err[1024] = "";
+
+void set_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+}
+
+const char* last_error() { return g_err; }
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+    return (int)e;
+  }
+  return 0;
+}
+
+namespace {
+
+template <typename T>
+__global__ void fill_kernel(T* p, T v, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// One wave per row.  x fp32 [T, d]; out bf16 = bf16(x * rstd * w); rstd [T].
+__global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const float* __restrict__ x,
+                                                          const float* __restrict__ w, int T, int d,
+                                                          float eps, bf16* __restrict__ out,
+                                                          float* __restrict__ rstd_out) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float* xr = x + (int64_t)t * d;
+  float ss = 0.0f;
+  for (int c = lane * 4; c < d; c += 256) {
+    const float4 v = *reinterpret_cast<const float4*>(xr + c);
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  ss = wave_sum(ss);
+  const float rstd = rsqrtf(ss / (float)d + eps);
+  if (lane == 0 && rstd_out) rstd_out[t] = rstd;
+  bf16* orow = out + (int64_t)t * d;
+  for (int c = lane * 4; c < d; c += 256) {
+    const float4 v = *reinterpret_cast<const float4*>(xr + c);
+    const float4 g = *reinterpret_cast<const float4*>(w + c);
+    uint2 o;
+    o.x = (uint32_t)f2bf(v.x * rstd * g.x) | ((uint32_t)f2bf(v.y * rstd * g.y) << 16);
+    o.y = (uint32_t)f2bf(v.z * rstd * g.z) | ((uint32_t)f2bf(v.w * rstd * g.w) << 16);
+    *reinterpret_cast<uint2*>(orow + c) = o;
+  }
+}
+
+// dx = rstd * (w*dy) - x * rstd^3 * mean(w*dy*x)  (+ dres);   partial dw per row block.
+constexpr int kNormRowsPerBlock = 64;
+
+__global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
+    const bf16* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
+    const float* __restrict__ rstd, const float* __restrict__ dres, int T, int d,
+    float* __restrict__ dx, float* __restrict__ dw_part) {
+  // each wave walks rows blockIdx.x*64 + wave, +4, ...; dw partial kept per lane column chunk
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  extern __shared__ float sdw[];  // [4][d]
+  for (int c = threadIdx.x; c < 4 * d; c += 256) sdw[c] = 0.0f;
+  __syncthreads();
+  const int r0 = blockIdx.x * kNormRowsPerBlock;
+  for (int rr = wave; rr < kNormRowsPerBlock; rr += 4) {
+    const int t = r0 + rr;
+    if (t >= T) break;
+    const float rs = rstd[t];
+    const bf16* dyr = dy + (int64_t)t * d;
+    const float* xr = x + (int64_t)t * d;
+    float dot = 0.0f;
+    for (int c = lane; c < d; c += 64) dot += w[c] * bf2f(dyr[c]) * xr[c];
+    dot = wave_sum(dot);
+    const float coef = rs * rs * rs * dot / (float)d;
+    for (int c = lane; c < d; c += 64) {
+      const float g = bf2f(dyr[c]);
+      float v = rs * w[c] * g - xr[c] * coef;
+      if (dres) v += dres[(int64_t)t * d + c];
+      dx[(int64_t)t * d + c] = v;
+      sdw[wave * d + c] += g * xr[c] * rs;
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < d; c += 256)
+    dw_part[(int64_t)blockIdx.x * d + c] = ((sdw[c] + sdw[d + c]) + sdw[2 * d + c]) + sdw[3 * d + c];
+}
+
+__global__ void __launch_bounds__(256) colsum_kernel(const float* __restrict__ part, int nrows, int d,
+                                                     float* __restrict__ out, int accumulate) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= d) return;
+  float s = 0.0f;
+  for (int r = 0; r < nrows; ++r) s += part[(int64_t)r * d + c];
+  out[c] = accumulate ? out[c] + s : s;
+}
+
+// dq/dk/dv: [B,H,S,hd] with arbitrary element strides; dqkv: [B*S, 3*H*hd] bf16.
+// Inverse of the interleaved rotation y_e = x_e c - x_o s, y_o = x_o c + x_e s.
+__global__ void __launch_bounds__(256) rope_bwd_pack_kernel(
+    const bf16* __restrict__ dq, const bf16* __restrict__ dk, const bf16* __restrict__ dv,
+    int64_t sb, int64_t sh, int64_t ss, int64_t sbk, int64_t shk, int64_t ssk, int64_t sbv, int64_t shv,
+    int64_t ssv, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int B, int H, int S,
+    int hd, bf16* __restrict__ dqkv) {
+  const int d = H * hd;
+  const int64_t npairs = (int64_t)B * S * 3 * d / 2;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= npairs) return;
+  const int64_t e = idx * 2;  // even column of the output row
+  const int64_t t = e / (3 * d);
+  const int col = (int)(e % (3 * d));
+  const int part = col / d;
+  const int within = col % d;
+  const int h = within / hd, dim = within % hd;
+  const int b = (int)(t / S), s = (int)(t % S);
+  const bf16* src;
+  int64_t off;
+  if (part == 0) {
+    src = dq;
+    off = b * sb + h * sh + s * ss + dim;
+  } else if (part == 1) {
+    src = dk;
+    off = b * sbk + h * shk + s * ssk + dim;
+  } else {
+    src = dv;
+    off = b * sbv + h * shv + s * ssv + dim;
+  }
+  float ye = bf2f(src[off]), yo = bf2f(src[off + 1]);
+  float xe = ye, xo = yo;
+  if (part < 2) {
+    const float c0 = cos_t[(int64_t)s * hd + dim], s0 = sin_t[(int64_t)s * hd + dim];
+    const float c1 = cos_t[(int64_t)s * hd + dim + 1], s1 = sin_t[(int64_t)s * hd + dim + 1];
+    xe = ye * c0 + yo * s1;
+    xo = yo * c1 - ye * s0;
+  }
+  uint32_t packed = (uint32_t)f2bf(xe) | ((uint32_t)f2bf(xo) << 16);
+  *reinterpret_cast<uint32_t*>(dqkv + t * 3 * d + col) = packed;
+}
+
+__global__ void __launch_bounds__(256) cast_f32_bf16_kernel(const float* __restrict__ x, int64_t n,
+                                                            bf16* __restrict__ y) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 3 < n) {
+    const float4 v = *reinterpret_cast<const float4*>(x + i);
+    uint2 o;
+    o.x = (uint32_t)f2bf(v.x) | ((uint32_t)f2bf(v.y) << 16);
+    o.y = (uint32_t)f2bf(v.z) | ((uint32_t)f2bf(v.w) << 16);
+    *reinterpret_cast<uint2*>(y + i) = o;
+  } else {
+    for (int64_t j = i; j < n; ++j) y[j] = f2bf(x[j]);
+  }
+}
+
+}  // namespace
+
+int fill_i32(int32_t* p, int32_t value, int64_t n, hipStream_t s) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(fill_kernel<int32_t>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, value, n);
+  return check_launch("fill_i32");
+}
+
+int fill_f32(float* p, float value, int64_t n, hipStream_t s) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(fill_kernel<float>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, p, value, n);
+  return check_launch("fill_f32");
+}
+
+int rmsnorm_fwd(const float* x, const float* w, int T, int d, float eps, bf16* out, float* rstd,
+                hipStream_t s) {
+  RTE_REQUIRE(d % 4 == 0, "rmsnorm: d must be a multiple of 4");
+  if (T == 0) return 0;
+  hipLaunchKernelGGL(rmsnorm_fwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, x, w, T, d, eps, out, rstd);
+  return check_launch("rmsnorm_fwd");
+}
+
+size_t rmsnorm_bwd_workspace_bytes(int T, int d) {
+  const int nblk = (T + kNormRowsPerBlock - 1) / kNormRowsPerBlock;
+  return (size_t)(nblk > 0 ? nblk : 1) * d * sizeof(float);
+}
+
+int rmsnorm_bwd(const bf16* dy, const float* x, const float* w, const float* rstd, const float* dres, int T,
+                int d, float* dx, float* dw, int dw_accumulate, void* ws, size_t ws_bytes, hipStream_t s) {
+  RTE_REQUIRE(ws_bytes >= rmsnorm_bwd_workspace_bytes(T, d), "rmsnorm_bwd: workspace too small");
+  RTE_REQUIRE((size_t)4 * d * sizeof(float) <= 65536, "rmsnorm_bwd: d too large");
+  const int nblk = (T + kNormRowsPerBlock - 1) / kNormRowsPerBlock;
+  float* part = static_cast<float*>(ws);
+  if (nblk > 0) {
+    hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3(nblk), dim3(256), 4 * d * sizeof(float), s, dy, x, w, rstd,
+                       dres, T, d, dx, part);
+    RTE_TRY(check_launch("rmsnorm_bwd"));
+  }
+  if (dw) {
+    if (nblk == 0) return dw_accumulate ? 0 : fill_f32(dw, 0.0f, d, s);
+    hipLaunchKernelGGL(colsum_kernel, dim3((d + 255) / 256), dim3(256), 0, s, part, nblk, d, dw, dw_accumulate);
+    RTE_TRY(check_launch("rmsnorm_dw"));
+  }
+  return 0;
+}
+
+int rope_bwd_pack(const bf16* dq, const int64_t* sq, const bf16* dk, const int64_t* sk, const bf16* dv,
+                  const int64_t* sv, const float* cos_t, const float* sin_t, int B, int H, int S, int hd,
+                  bf16* dqkv, hipStream_t s) {
+  RTE_REQUIRE(hd % 2 == 0, "rope_bwd: head_dim must be even");
+  for (int i = 0; i < 3; ++i) {
+    const int64_t* st = i == 0 ? sq : (i == 1 ? sk : sv);
+    RTE_REQUIRE(st[3] == 1, "rope_bwd: innermost stride must be 1");
+  }
+  const int64_t npairs = (int64_t)B * S * 3 * H * hd / 2;
+  if (npairs == 0) return 0;
+  hipLaunchKernelGGL(rope_bwd_pack_kernel, dim3((unsigned)((npairs + 255) / 256)), dim3(256), 0, s, dq, dk, dv,
+                     sq[0], sq[1], sq[2], sk[0], sk[1], sk[2], sv[0], sv[1], sv[2], cos_t, sin_t, B, H, S, hd,
+                     dqkv);
+  return check_launch("rope_bwd_pack");
+}
+
+int cast_f32_bf16(const float* x, int64_t n, bf16* y, hipStream_t s) {
+  if (n <= 0) return 0;
+  const int64_t threads = (n + 3) / 4;
+  hipLaunchKernelGGL(cast_f32_bf16_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, x, n, y);
+  return check_launch("cast_f32_bf16");
+}
+
+}  // namespace rte

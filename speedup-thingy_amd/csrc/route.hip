@@ -1,0 +1,326 @@
+// Token -> cluster routing, deterministic packing and fixed-order combine.
+//
+//  route_topk  : one wave64 per token; k rounds of a wave arg-max over the C
+//                router logits (value descending, index ascending on ties,
+//                NaN above everything as torch.topk does), then softmax over
+//                the k selected logits.
+//  pack        : stable counting sort of the T*k (token, cluster) pairs by
+//                cluster.  Slots inside a cluster follow ascending pair index,
+//                i.e. ascending token, like the nonzero()-based index build of
+//                the reference.  Three launches, integer-only, no atomics whose
+//                order could leak into the result.
+//  combine     : out[t] = extra[t] + resid[t] + sum_j rows[t*k + j], j in order.
+#include "common.hpp"
+
+namespace rte {
+
+namespace {
+
+__device__ __forceinline__ bool better(float a, int ia, float b, int ib) {
+  const bool na = a != a, nb = b != b;
+  if (na != nb) return na;
+  if (!na && a != b) return a > b;
+  return ia < ib;
+}
+
+constexpr int kMaxPerLane = 16;  // C <= 1024
+
+__global__ void __launch_bounds__(256) route_topk_kernel(const float* __restrict__ logits, int T, int C,
+                                                         int k, int32_t* __restrict__ ids,
+                                                         float* __restrict__ weights) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float* row = logits + (int64_t)t * C;
+  float v[kMaxPerLane];
+  bool used[kMaxPerLane];
+  const int per = (C + 63) / 64;
+#pragma unroll
+  for (int i = 0; i < kMaxPerLane; ++i) {
+    const int c = lane + 64 * i;
+    used[i] = !(i < per && c < C);
+    v[i] = used[i] ? 0.0f : row[c];
+  }
+  float my_v = 0.0f;
+  int my_i = 0;
+  for (int r = 0; r < k; ++r) {
+    // lane-local best among unused
+    float bv = 0.0f;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i) {
+      if (used[i]) continue;
+      const int c = lane + 64 * i;
+      if (bi == 0x7fffffff || better(v[i], c, bv, bi)) {
+        bv = v[i];
+        bi = c;
+      }
+    }
+    // wave arg-max (butterfly: every lane ends with the winner); empty lanes carry INT_MAX
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float ov = __shfl_xor(bv, off, 64);
+      const int oi = __shfl_xor(bi, off, 64);
+      if (oi != 0x7fffffff && (bi == 0x7fffffff || better(ov, oi, bv, bi))) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+    if (bi != 0x7fffffff && (bi & 63) == lane) {
+#pragma unroll
+      for (int i = 0; i < kMaxPerLane; ++i)
+        if (i == (bi >> 6)) used[i] = true;
+    }
+    if (lane == r) {
+      my_v = bv;
+      my_i = bi;
+    }
+  }
+  // lane j < k holds the j-th selection; softmax over the selected logits
+  const float mx = __shfl(my_v, 0, 64);
+  const float ex = lane < k ? expf(my_v - mx) : 0.0f;
+  float denom = ex;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) denom += __shfl_xor(denom, off, 64);
+  if (lane < k) {
+    ids[(int64_t)t * k + lane] = my_i;
+    weights[(int64_t)t * k + lane] = ex / denom;
+  }
+}
+
+constexpr int kPackChunk = 256;
+
+// hist layout: hist[c * nblk + b] = pairs of block b routed to cluster c.
+__global__ void __launch_bounds__(256) pack_count_kernel(const int32_t* __restrict__ cl, int P, int C,
+                                                         int32_t* __restrict__ hist, int nblk,
+                                                         int32_t* __restrict__ invalid) {
+  extern __shared__ int32_t sh[];
+  for (int c = threadIdx.x; c < C; c += blockDim.x) sh[c] = 0;
+  __syncthreads();
+  const int p = blockIdx.x * kPackChunk + threadIdx.x;
+  if (p < P) {
+    const int c = cl[p];
+    if (c >= 0 && c < C) {
+      atomicAdd(&sh[c], 1);
+    } else if (invalid) {
+      atomicAdd(invalid, 1);
+    }
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < C; c += blockDim.x) hist[(int64_t)c * nblk + blockIdx.x] = sh[c];
+}
+
+// Exclusive scan of hist (length L = C * nblk) in place, single workgroup of 1024.
+__global__ void __launch_bounds__(1024) pack_scan_kernel(int32_t* __restrict__ hist, int C, int nblk,
+                                                         int32_t* __restrict__ offsets, int P) {
+  __shared__ int32_t part[1024];
+  const int64_t L = (int64_t)C * nblk;
+  const int tid = threadIdx.x;
+  const int64_t seg = (L + 1023) / 1024;
+  const int64_t b0 = tid * seg, b1 = b0 + seg < L ? b0 + seg : L;
+  int32_t s = 0;
+  for (int64_t i = b0; i < b1; ++i) s += hist[i];
+  part[tid] = s;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int32_t y = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += y;
+    __syncthreads();
+  }
+  int32_t run = part[tid] - s;
+  for (int64_t i = b0; i < b1; ++i) {
+    const int32_t h = hist[i];
+    hist[i] = run;
+    run += h;
+  }
+  __syncthreads();
+  for (int c = tid; c < C; c += 1024) offsets[c] = hist[(int64_t)c * nblk];
+  if (tid == 0) offsets[C] = part[1023];
+  (void)P;
+}
+
+__global__ void __launch_bounds__(256) pack_scatter_kernel(const int32_t* __restrict__ cl, int P, int C,
+                                                           int k, const int32_t* __restrict__ hist,
+                                                           int nblk, const float* __restrict__ w,
+                                                           int32_t* __restrict__ tok_of_slot,
+                                                           int32_t* __restrict__ pair_of_slot,
+                                                           int32_t* __restrict__ slot_of_pair,
+                                                           float* __restrict__ w_of_slot) {
+  __shared__ int32_t sc[kPackChunk];
+  const int p0 = blockIdx.x * kPackChunk;
+  const int n = P - p0 < kPackChunk ? P - p0 : kPackChunk;
+  if (threadIdx.x < n) sc[threadIdx.x] = cl[p0 + threadIdx.x];
+  __syncthreads();
+  if (slot_of_pair && threadIdx.x < n) {
+    const int c = sc[threadIdx.x];
+    if (c < 0 || c >= C) slot_of_pair[p0 + threadIdx.x] = -1;
+  }
+  for (int c = threadIdx.x; c < C; c += blockDim.x) {
+    int32_t slot = hist[(int64_t)c * nblk + blockIdx.x];
+    for (int i = 0; i < n; ++i) {
+      if (sc[i] != c) continue;
+      const int p = p0 + i;
+      if (tok_of_slot) tok_of_slot[slot] = p / k;
+      if (pair_of_slot) pair_of_slot[slot] = p;
+      if (slot_of_pair) slot_of_pair[p] = slot;
+      if (w_of_slot) w_of_slot[slot] = w ? w[p] : 1.0f;
+      ++slot;
+    }
+  }
+}
+
+template <typename OutT>
+__device__ __forceinline__ void store8(OutT* dst, const float* v);
+
+template <>
+__device__ __forceinline__ void store8<float>(float* dst, const float* v) {
+  reinterpret_cast<float4*>(dst)[0] = make_float4(v[0], v[1], v[2], v[3]);
+  reinterpret_cast<float4*>(dst)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
+template <>
+__device__ __forceinline__ void store8<bf16>(bf16* dst, const float* v) {
+  uint4 o;
+  o.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+  o.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+  o.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
+  o.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+  *reinterpret_cast<uint4*>(dst) = o;
+}
+
+__device__ __forceinline__ void add8_bf16(float* acc, uint4 u) {
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc[2 * i] += __uint_as_float(w[i] << 16);
+    acc[2 * i + 1] += __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+// rows: [T*k, d] bf16 in pair order; extra: [T, d] bf16 or null; resid: [T, d] fp32 or null.
+template <typename OutT>
+__global__ void __launch_bounds__(256) combine_kernel(const bf16* __restrict__ rows, int T, int k, int d,
+                                                      const bf16* __restrict__ extra,
+                                                      const float* __restrict__ resid,
+                                                      OutT* __restrict__ out) {
+  const int per_row = d / 8;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)T * per_row) return;
+  const int t = (int)(idx / per_row);
+  const int c = (int)(idx % per_row) * 8;
+  float acc[8];
+  if (resid) {
+    const float4 a = *reinterpret_cast<const float4*>(resid + (int64_t)t * d + c);
+    const float4 b = *reinterpret_cast<const float4*>(resid + (int64_t)t * d + c + 4);
+    acc[0] = a.x; acc[1] = a.y; acc[2] = a.z; acc[3] = a.w;
+    acc[4] = b.x; acc[5] = b.y; acc[6] = b.z; acc[7] = b.w;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.0f;
+  }
+  float sum[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sum[i] = 0.0f;
+  for (int j = 0; j < k; ++j)
+    add8_bf16(sum, *reinterpret_cast<const uint4*>(rows + ((int64_t)t * k + j) * d + c));
+  if (extra) add8_bf16(sum, *reinterpret_cast<const uint4*>(extra + (int64_t)t * d + c));
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] += sum[i];
+  store8<OutT>(out + (int64_t)t * d + c, acc);
+}
+
+// Routing-weight gradient: weights are softmax over the k selected logits, so
+// dlogit_j = w_j * (dw_j - sum_i w_i dw_i); everything else in the row is 0.
+__global__ void __launch_bounds__(256) route_bwd_kernel(const int32_t* __restrict__ ids,
+                                                        const float* __restrict__ w,
+                                                        const float* __restrict__ dw_slot,
+                                                        const int32_t* __restrict__ slot_of_pair, int T,
+                                                        int C, int k, bf16* __restrict__ dlogits,
+                                                        float* __restrict__ dlogits_f32) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= T) return;
+  float dw[16];
+  float s = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    const int slot = slot_of_pair[(int64_t)t * k + j];
+    dw[j] = slot >= 0 ? dw_slot[slot] : 0.0f;
+    s += w[(int64_t)t * k + j] * dw[j];
+  }
+  if (dlogits)
+    for (int c = 0; c < C; ++c) dlogits[(int64_t)t * C + c] = 0;
+  if (dlogits_f32)
+    for (int c = 0; c < C; ++c) dlogits_f32[(int64_t)t * C + c] = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    const float g = w[(int64_t)t * k + j] * (dw[j] - s);
+    const int c = ids[(int64_t)t * k + j];
+    if (dlogits) dlogits[(int64_t)t * C + c] = f2bf(g);
+    if (dlogits_f32) dlogits_f32[(int64_t)t * C + c] = g;
+  }
+}
+
+}  // namespace
+
+int route_topk(const float* logits, int T, int C, int k, int32_t* ids, float* weights, hipStream_t s) {
+  RTE_REQUIRE(T >= 0 && C >= 1 && C <= 64 * kMaxPerLane, "route_topk: C must be in [1, 1024]");
+  RTE_REQUIRE(k >= 1 && k <= 16 && k <= C, "route_topk: k must be in [1, min(16, C)]");
+  if (T == 0) return 0;
+  hipLaunchKernelGGL(route_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, C, k, ids, weights);
+  return check_launch("route_topk");
+}
+
+size_t pack_workspace_bytes(int P, int C) {
+  const int nblk = (P + kPackChunk - 1) / kPackChunk;
+  return (size_t)C * (size_t)(nblk > 0 ? nblk : 1) * sizeof(int32_t);
+}
+
+int pack_pairs(const int32_t* cl, int P, int C, int k, const float* w, int32_t* offsets,
+               int32_t* tok_of_slot, int32_t* pair_of_slot, int32_t* slot_of_pair, float* w_of_slot,
+               int32_t* invalid, void* ws, size_t ws_bytes, hipStream_t s) {
+  RTE_REQUIRE(P >= 0 && C >= 1 && k >= 1, "pack: bad sizes");
+  RTE_REQUIRE(ws_bytes >= pack_workspace_bytes(P, C), "pack: workspace too small (%zu < %zu)", ws_bytes,
+              pack_workspace_bytes(P, C));
+  const int nblk = (P + kPackChunk - 1) / kPackChunk;
+  int32_t* hist = static_cast<int32_t*>(ws);
+  if (nblk == 0) return fill_i32(offsets, 0, C + 1, s);
+  {
+    hipLaunchKernelGGL(pack_count_kernel, dim3(nblk), dim3(kPackChunk), C * sizeof(int32_t), s, cl, P, C,
+                       hist, nblk, invalid);
+    RTE_TRY(check_launch("pack_count"));
+  }
+  hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(1024), 0, s, hist, C, nblk, offsets, P);
+  RTE_TRY(check_launch("pack_scan"));
+  {
+    hipLaunchKernelGGL(pack_scatter_kernel, dim3(nblk), dim3(256), 0, s, cl, P, C, k, hist, nblk, w,
+                       tok_of_slot, pair_of_slot, slot_of_pair, w_of_slot);
+    RTE_TRY(check_launch("pack_scatter"));
+  }
+  return 0;
+}
+
+int combine_rows(const bf16* rows, int T, int k, int d, const bf16* extra, const float* resid, void* out,
+                 int out_f32, hipStream_t s) {
+  RTE_REQUIRE(d % 8 == 0, "combine: d must be a multiple of 8");
+  RTE_REQUIRE(k >= 0, "combine: k must be >= 0");
+  const int64_t n = (int64_t)T * (d / 8);
+  if (n == 0) return 0;
+  const dim3 grid((unsigned)((n + 255) / 256));
+  if (out_f32)
+    hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(256), 0, s, rows, T, k, d, extra, resid,
+                       static_cast<float*>(out));
+  else
+    hipLaunchKernelGGL(combine_kernel<bf16>, grid, dim3(256), 0, s, rows, T, k, d, extra, resid,
+                       static_cast<bf16*>(out));
+  return check_launch("combine");
+}
+
+int route_bwd(const int32_t* ids, const float* w, const float* dw_slot, const int32_t* slot_of_pair, int T,
+              int C, int k, bf16* dlogits, float* dlogits_f32, hipStream_t s) {
+  RTE_REQUIRE(k >= 1 && k <= 16, "route_bwd: k must be in [1, 16]");
+  if (T == 0) return 0;
+  hipLaunchKernelGGL(route_bwd_kernel, dim3((T + 255) / 256), dim3(256), 0, s, ids, w, dw_slot, slot_of_pair,
+                     T, C, k, dlogits, dlogits_f32);
+  return check_launch("route_bwd");
+}
+
+}  // namespace rte

@@ -1,0 +1,411 @@
+"""Autograd operators over librte_hip (the gfx950 HIP kernels).
+
+Every operator here launches hand-written HIP kernels through the C ABI on the
+current torch stream; torch is only used to allocate outputs/workspaces.  They
+raise RuntimeError when the library or a ROCm device is missing: there is no
+CPU or reference-math fallback on this path.
+
+Precision contract (mirrors bf16 autocast in the reference, rte/training.py:356-363):
+activations and GEMM operands are bf16, accumulation is fp32, master weights and
+their gradients are fp32, the residual stream is fp32.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from rte_amd import _lib
+from rte_amd._lib import call, ptr
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+
+
+def _s() -> int:
+    return _lib.stream_ptr()
+
+
+def cast_bf16(x: torch.Tensor) -> torch.Tensor:
+    """fp32 -> bf16 (round to nearest even) with the HIP cast kernel."""
+    if x.dtype == BF16:
+        return x.contiguous()
+    _lib.require_device_tensors("cast_bf16", x)
+    x = x.contiguous().to(F32)
+    y = torch.empty(x.shape, dtype=BF16, device=x.device)
+    call("rte_cast_f32_bf16", ptr(x), x.numel(), ptr(y), _s())
+    return y
+
+
+# ----------------------------------------------------------------------------- GEMM
+
+def gemm(
+    a: torch.Tensor,
+    b: torch.Tensor,
+    *,
+    a_t: bool = False,
+    b_t: bool = False,
+    out_f32: bool = False,
+    alpha: float = 1.0,
+    resid: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+    beta: float = 0.0,
+) -> torch.Tensor:
+    """C[m, n] = alpha * sum_k A(m, k) B(n, k) (+ beta C) (+ resid).
+
+    a: [M, K] (a_t False) or [K, M] (a_t True); b: [N, K] (b_t False) or [K, N] (b_t True).
+    bf16 operands, fp32 accumulation.
+    """
+    _lib.require_device_tensors("gemm", a, b, resid, out)
+    if a.dtype != BF16 or b.dtype != BF16:
+        raise TypeError("gemm operands must be bfloat16")
+    a = a.contiguous()
+    b = b.contiguous()
+    M = a.shape[1] if a_t else a.shape[0]
+    K = a.shape[0] if a_t else a.shape[1]
+    N = b.shape[1] if b_t else b.shape[0]
+    Kb = b.shape[0] if b_t else b.shape[1]
+    if K != Kb:
+        raise ValueError(f"gemm: reduction sizes differ ({K} vs {Kb})")
+    if out is None:
+        out = torch.empty((M, N), dtype=F32 if out_f32 else BF16, device=a.device)
+    if resid is not None:
+        resid = resid.contiguous().to(F32)
+    call(
+        "rte_gemm_bf16",
+        ptr(a), a.shape[1], int(a_t), None,
+        ptr(b), b.shape[1], int(b_t), None,
+        ptr(out), out.shape[1], int(out.dtype == F32), M, N, K,
+        float(alpha), float(beta), ptr(resid), 0 if resid is None else resid.shape[1], _s(),
+    )
+    return out
+
+
+def _attn_layout(y: torch.Tensor) -> tuple[list[int], int, int]:
+    """Layout descriptor reading a [B, H, S, hd] tensor as rows t = b*S + s, cols c = h*hd + dim."""
+    B, H, S, hd = y.shape
+    sb, sh, ss, sd = y.stride()
+    if sd != 1:
+        raise ValueError("attention tensor needs a unit innermost stride")
+    return [ss, S, sb, hd, sh], B * S, H * hd
+
+
+# ----------------------------------------------------------------------------- RMSNorm
+
+class RMSNormFn(torch.autograd.Function):
+    """bf16(x * rsqrt(mean(x^2) + eps) * w) for an fp32 residual stream (rte/kernels/reference.py:9-17)."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, w: torch.Tensor, eps: float):
+        _lib.require_device_tensors("rmsnorm", x, w)
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1]).contiguous().to(F32)
+        w32 = w.contiguous().to(F32)
+        T, d = x2.shape
+        out = torch.empty((T, d), dtype=BF16, device=x.device)
+        rstd = torch.empty((T,), dtype=F32, device=x.device)
+        call("rte_rmsnorm_fwd", ptr(x2), ptr(w32), T, d, float(eps), ptr(out), ptr(rstd), _s())
+        ctx.save_for_backward(x2, w32, rstd)
+        ctx.shape = shape
+        ctx.w_dtype = w.dtype
+        return out.view(*shape[:-1], d)
+
+    @staticmethod
+    def backward(ctx, dy: torch.Tensor):
+        x2, w32, rstd = ctx.saved_tensors
+        T, d = x2.shape
+        dy = dy.reshape(T, d).contiguous().to(BF16)
+        dx = torch.empty((T, d), dtype=F32, device=x2.device)
+        dw = torch.empty((d,), dtype=F32, device=x2.device)
+        nbytes = _lib.load().rte_rmsnorm_bwd_workspace_bytes(T, d)
+        ws = torch.empty((max(1, nbytes // 4),), dtype=F32, device=x2.device)
+        call("rte_rmsnorm_bwd", ptr(dy), ptr(x2), ptr(w32), ptr(rstd), None, T, d, ptr(dx), ptr(dw), 0,
+             ptr(ws), nbytes, _s())
+        return dx.view(ctx.shape), dw.to(ctx.w_dtype), None
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    return RMSNormFn.apply(x, w, eps)
+
+
+# ----------------------------------------------------------------------------- fused QKV + RoPE
+
+class QKVRopeFn(torch.autograd.Function):
+    """q, k, v = split(x @ Wqkv^T) with interleaved RoPE on q, k, written as [B, H, S, hd]."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_heads: int):
+        _lib.require_device_tensors("qkv_rope", x, w, cos, sin)
+        B, S, d = x.shape
+        hd = d // n_heads
+        if w.shape != (3 * d, d):
+            raise ValueError(f"wqkv must be [3d, d], got {tuple(w.shape)}")
+        xb = x.contiguous().to(BF16)
+        wb = cast_bf16(w)
+        cos = cos[:S].contiguous().to(F32)
+        sin = sin[:S].contiguous().to(F32)
+        q = torch.empty((B, n_heads, S, hd), dtype=BF16, device=x.device)
+        k = torch.empty_like(q)
+        v = torch.empty_like(q)
+        call("rte_qkv_rope_fwd", ptr(xb), ptr(wb), ptr(cos), ptr(sin), B, S, n_heads, hd, ptr(q), ptr(k),
+             ptr(v), _s())
+        ctx.save_for_backward(xb, wb, cos, sin)
+        ctx.dims = (B, S, n_heads, hd)
+        ctx.w_dtype = w.dtype
+        return q, k, v
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        xb, wb, cos, sin = ctx.saved_tensors
+        B, S, H, hd = ctx.dims
+        d = H * hd
+        grads = []
+        for g in (dq, dk, dv):
+            if g is None:
+                g = torch.zeros((B, H, S, hd), dtype=BF16, device=xb.device)
+            g = g.to(BF16)
+            if g.stride(-1) != 1:
+                g = g.contiguous()
+            grads.append(g)
+        strides = [torch.tensor(g.stride(), dtype=torch.int64) for g in grads]
+        dqkv = torch.empty((B * S, 3 * d), dtype=BF16, device=xb.device)
+        dx = torch.empty((B * S, d), dtype=BF16, device=xb.device)
+        dw = torch.empty((3 * d, d), dtype=F32, device=xb.device)
+        call("rte_qkv_rope_bwd", ptr(grads[0]), strides[0].data_ptr(), ptr(grads[1]), strides[1].data_ptr(),
+             ptr(grads[2]), strides[2].data_ptr(), ptr(xb), ptr(wb), ptr(cos), ptr(sin), B, S, H, hd,
+             ptr(dqkv), ptr(dx), ptr(dw), _s())
+        return dx.view(B, S, d), dw.to(ctx.w_dtype), None, None, None
+
+
+def qkv_rope(x, w, cos, sin, n_heads):
+    return QKVRopeFn.apply(x, w, cos, sin, n_heads)
+
+
+# ----------------------------------------------------------------------------- attention output projection
+
+class AttnOutProjFn(torch.autograd.Function):
+    """out = resid + y @ Wo^T where y is the [B, H, S, hd] attention output (any strides)."""
+
+    @staticmethod
+    def forward(ctx, y: torch.Tensor, w: torch.Tensor, resid: torch.Tensor | None):
+        _lib.require_device_tensors("attn_out_proj", y, w, resid)
+        yb = y.to(BF16)
+        if yb.stride(-1) != 1:
+            yb = yb.contiguous()
+        layout, T, K = _attn_layout(yb)
+        wb = cast_bf16(w)
+        N = wb.shape[0]
+        out = torch.empty((T, N), dtype=F32, device=y.device)
+        r = None if resid is None else resid.reshape(T, N).contiguous().to(F32)
+        L = torch.tensor(layout, dtype=torch.int64)
+        Lw = torch.tensor([K, 0, 0, 0, 0], dtype=torch.int64)
+        call("rte_gemm_bf16_split", ptr(yb), L.data_ptr(), 0, ptr(wb), Lw.data_ptr(), 0, ptr(out), N, 1, T, N, K,
+             1.0, 0.0, ptr(r), 0 if r is None else N, _s())
+        ctx.save_for_backward(yb, wb)
+        ctx.has_resid = resid is not None
+        ctx.w_dtype = w.dtype
+        B, H, S, hd = y.shape
+        return out.view(B, S, N)
+
+    @staticmethod
+    def backward(ctx, dout: torch.Tensor):
+        yb, wb = ctx.saved_tensors
+        B, H, S, hd = yb.shape
+        T, K, N = B * S, H * hd, wb.shape[0]
+        db = cast_bf16(dout.reshape(T, N))
+        # dy = dout @ Wo    (B(n=c, k=o) = Wo[o][c]: layout T)
+        dy = gemm(db, wb, b_t=True)
+        # dWo[o, c] = sum_t dout[t, o] y[t, c]
+        layout, _, _ = _attn_layout(yb)
+        L = torch.tensor(layout, dtype=torch.int64)
+        Ld = torch.tensor([N, 0, 0, 0, 0], dtype=torch.int64)
+        dw = torch.empty((N, K), dtype=F32, device=yb.device)
+        call("rte_gemm_bf16_split", ptr(db), Ld.data_ptr(), 1, ptr(yb), L.data_ptr(), 1, ptr(dw), K, 1, N, K, T,
+             1.0, 0.0, None, 0, _s())
+        dy4 = dy.view(B, S, H, hd).transpose(1, 2)
+        dres = dout if ctx.has_resid else None
+        return dy4, dw.to(ctx.w_dtype), dres
+
+
+def attn_out_proj(y, w, resid=None):
+    return AttnOutProjFn.apply(y, w, resid)
+
+
+# ----------------------------------------------------------------------------- dense SwiGLU
+
+class DenseSwiGLUFn(torch.autograd.Function):
+    """out = resid + (up * silu(gate)) @ W_down with the SwiGLU activation fused into the GEMMs.
+
+    wug: [2F, d] rows [up ; gate] (rte/layers.py:78-87 chunk order).  wd_rows=False: wd is the
+    nn.Linear(F, d) weight [d, F]; wd_rows=True: wd is [F, d] (PackedDenseSwiGLU.wdown_rows).
+    """
+
+    @staticmethod
+    def forward(ctx, x, wug, wd, resid, wd_rows: bool, out_f32: bool):
+        _lib.require_device_tensors("dense_swiglu", x, wug, wd, resid)
+        shape = x.shape
+        d = shape[-1]
+        xb = x.reshape(-1, d).contiguous().to(BF16)
+        T = xb.shape[0]
+        F = wug.shape[0] // 2
+        wugb = cast_bf16(wug)
+        wdb = cast_bf16(wd)
+        ug = torch.empty((T, 2 * F), dtype=BF16, device=x.device)
+        z = torch.empty((T, F), dtype=BF16, device=x.device)
+        out = torch.empty((T, d), dtype=F32 if out_f32 else BF16, device=x.device)
+        r = None if resid is None else resid.reshape(T, d).contiguous().to(F32)
+        call("rte_dense_swiglu_fwd", ptr(xb), T, d, F, ptr(wugb), ptr(wdb), int(wd_rows), ptr(r), ptr(ug), ptr(z),
+             ptr(out), int(out_f32), _s())
+        ctx.save_for_backward(xb, wugb, wdb, ug, z)
+        ctx.meta = (shape, F, wd_rows, resid is not None, wug.dtype, wd.dtype)
+        return out.view(shape)
+
+    @staticmethod
+    def backward(ctx, dout):
+        xb, wugb, wdb, ug, z = ctx.saved_tensors
+        shape, F, wd_rows, has_resid, wug_dtype, wd_dtype = ctx.meta
+        T, d = xb.shape
+        db = cast_bf16(dout.reshape(T, d)) if dout.dtype != BF16 else dout.reshape(T, d).contiguous()
+        dug = torch.empty((T, 2 * F), dtype=BF16, device=xb.device)
+        dx = torch.empty((T, d), dtype=BF16, device=xb.device)
+        dwug = torch.empty((2 * F, d), dtype=F32, device=xb.device)
+        dwd = torch.empty(wdb.shape, dtype=F32, device=xb.device)
+        call("rte_dense_swiglu_bwd", ptr(db), ptr(xb), T, d, F, ptr(wugb), ptr(wdb), int(wd_rows), ptr(ug), ptr(z),
+             ptr(dug), ptr(dx), ptr(dwug), ptr(dwd), _s())
+        dres = dout if has_resid else None
+        return dx.view(shape), dwug.to(wug_dtype), dwd.to(wd_dtype), dres, None, None
+
+
+def dense_swiglu(x, wug, wd, resid=None, *, wd_rows: bool = False, out_f32: bool = True):
+    return DenseSwiGLUFn.apply(x, wug, wd, resid, wd_rows, out_f32)
+
+
+# ----------------------------------------------------------------------------- routing / packing
+
+@dataclass
+class PackIndex:
+    """Deterministic cluster packing of the T*k (token, cluster) pairs.
+
+    offsets[C+1]: slot range of each cluster; slots inside a cluster follow ascending token.
+    """
+
+    offsets: torch.Tensor
+    tok_of_slot: torch.Tensor
+    pair_of_slot: torch.Tensor
+    slot_of_pair: torch.Tensor
+    w_of_slot: torch.Tensor
+    n_clusters: int
+    k: int
+
+
+def route_topk(logits: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-token top-k of fp32 router logits: ids int32 [T, k], softmax weights fp32 [T, k]."""
+    _lib.require_device_tensors("route_topk", logits)
+    lg = logits.contiguous().to(F32)
+    T, C = lg.shape
+    ids = torch.empty((T, k), dtype=torch.int32, device=lg.device)
+    w = torch.empty((T, k), dtype=F32, device=lg.device)
+    call("rte_route_topk", ptr(lg), T, C, k, ptr(ids), ptr(w), _s())
+    return ids, w
+
+
+def pack_index(ids: torch.Tensor, n_clusters: int, weights: torch.Tensor | None = None,
+               invalid: torch.Tensor | None = None) -> PackIndex:
+    _lib.require_device_tensors("pack_index", ids, weights, invalid)
+    cl = ids.contiguous().to(torch.int32)
+    k = cl.shape[-1] if cl.ndim == 2 else 1
+    P = cl.numel()
+    dev = cl.device
+    offsets = torch.empty((n_clusters + 1,), dtype=torch.int32, device=dev)
+    tok = torch.empty((P,), dtype=torch.int32, device=dev)
+    pos = torch.empty((P,), dtype=torch.int32, device=dev)
+    sop = torch.empty((P,), dtype=torch.int32, device=dev)
+    wos = torch.empty((P,), dtype=F32, device=dev)
+    nbytes = _lib.load().rte_pack_workspace_bytes(P, n_clusters)
+    ws = torch.empty((max(1, nbytes // 4),), dtype=torch.int32, device=dev)
+    w = None if weights is None else weights.contiguous().to(F32)
+    call("rte_pack_index", ptr(cl), P, n_clusters, k, ptr(w), ptr(offsets), ptr(tok), ptr(pos), ptr(sop), ptr(wos),
+         ptr(invalid), ptr(ws), nbytes, _s())
+    return PackIndex(offsets, tok, pos, sop, wos, n_clusters, k)
+
+
+def combine_rows(rows: torch.Tensor, T: int, k: int, *, extra=None, resid=None, out_f32=True) -> torch.Tensor:
+    _lib.require_device_tensors("combine_rows", rows, extra, resid)
+    d = rows.shape[-1]
+    out = torch.empty((T, d), dtype=F32 if out_f32 else BF16, device=rows.device)
+    r = None if resid is None else resid.reshape(T, d).contiguous().to(F32)
+    e = None if extra is None else extra.reshape(T, d).contiguous().to(BF16)
+    call("rte_combine_rows", ptr(rows.contiguous()), T, k, d, ptr(e), ptr(r), ptr(out), int(out_f32), _s())
+    return out
+
+
+# ----------------------------------------------------------------------------- routed cluster-pool SwiGLU
+
+class RoutedClusterPoolFn(torch.autograd.Function):
+    """Top-k routed cluster-pool SwiGLU FFN (cluster g owns neurons [g*n, (g+1)*n)).
+
+    logits = x @ Wr^T (fp32), ids/weights = top-k + softmax over the selected logits,
+    out[t] = resid[t] + sum_j w_tj * SwiGLU_{ids_tj}(x_t).  k = 1 with one cluster per token is the
+    reference static cluster pool (rte/kernels/cluster_pool_ffn.py:143-162, :192-215).
+    """
+
+    @staticmethod
+    def forward(ctx, x, wr, wug, wd, resid, k: int):
+        _lib.require_device_tensors("routed_cluster_pool", x, wr, wug, wd, resid)
+        shape = x.shape
+        d = shape[-1]
+        xb = x.reshape(-1, d).contiguous().to(BF16)
+        T = xb.shape[0]
+        C = wr.shape[0]
+        F = wug.shape[0] // 2
+        if F % C != 0:
+            raise ValueError("d_ff must be divisible by the cluster count")
+        n = F // C
+        wrb = cast_bf16(wr)
+        wugb = cast_bf16(wug)
+        wdb = cast_bf16(wd)
+        logits = gemm(xb, wrb, out_f32=True)
+        ids, w = route_topk(logits, k)
+        pk = pack_index(ids, C, w)
+        P = T * k
+        ug = torch.empty((P, 2 * n), dtype=BF16, device=x.device)
+        zw = torch.empty((P, n), dtype=BF16, device=x.device)
+        yp = torch.empty((P, d), dtype=BF16, device=x.device)
+        call("rte_grouped_swiglu_fwd", ptr(xb), T, d, ptr(pk.offsets), C, n, P, ptr(pk.tok_of_slot),
+             ptr(pk.pair_of_slot), ptr(pk.w_of_slot), ptr(wugb), ptr(wdb), F, ptr(ug), ptr(zw), ptr(yp), _s())
+        out = combine_rows(yp, T, k, resid=resid, out_f32=True)
+        ctx.save_for_backward(xb, wrb, wugb, wdb, ids, w, pk.offsets, pk.tok_of_slot, pk.pair_of_slot,
+                              pk.slot_of_pair, pk.w_of_slot, ug, zw)
+        ctx.meta = (shape, k, C, n, resid is not None, wr.dtype, wug.dtype, wd.dtype)
+        ctx.mark_non_differentiable(ids, w)
+        return out.view(shape), ids, w
+
+    @staticmethod
+    def backward(ctx, dout, _dids, _dw):
+        (xb, wrb, wugb, wdb, ids, w, offsets, tok, pos, sop, wos, ug, zw) = ctx.saved_tensors
+        shape, k, C, n, has_resid, wr_dt, wug_dt, wd_dt = ctx.meta
+        T, d = xb.shape
+        F = C * n
+        P = T * k
+        dev = xb.device
+        db = cast_bf16(dout.reshape(T, d))
+        dug = torch.empty((P, 2 * n), dtype=BF16, device=dev)
+        dw_slot = torch.empty((P,), dtype=F32, device=dev)
+        dxp = torch.empty((P, d), dtype=BF16, device=dev)
+        dwug = torch.empty((2 * F, d), dtype=F32, device=dev)
+        dwd = torch.empty((d, F), dtype=F32, device=dev)
+        call("rte_grouped_swiglu_bwd", ptr(db), ptr(xb), T, d, ptr(offsets), C, n, P, ptr(tok), ptr(pos), ptr(wos),
+             ptr(wugb), ptr(wdb), F, ptr(ug), ptr(zw), ptr(dug), ptr(dw_slot), ptr(dxp), ptr(dwug), ptr(dwd), _s())
+        dlog = torch.empty((T, C), dtype=BF16, device=dev)
+        call("rte_route_bwd", ptr(ids), ptr(w), ptr(dw_slot), ptr(sop), T, C, k, ptr(dlog), None, _s())
+        dx_router = gemm(dlog, wrb, b_t=True)              # [T, d] = dlogits @ Wr
+        dwr = gemm(dlog, xb, a_t=True, b_t=True, out_f32=True)  # [C, d] = dlogits^T @ x
+        dx = combine_rows(dxp, T, k, extra=dx_router, out_f32=False)
+        dres = dout if has_resid else None
+        return dx.view(shape), dwr.to(wr_dt), dwug.to(wug_dt), dwd.to(wd_dt), dres, None
+
+
+def routed_cluster_pool_swiglu(x, wr, wug, wd, k: int, resid=None):
+    """Returns (out, ids, weights); ids/weights are the routing decisions (no gradient)."""
+    return RoutedClusterPoolFn.apply(x, wr, wug, wd, resid, k)

@@ -1,0 +1,282 @@
+"""Pins the CPU oracle before it is trusted as the checker of the HIP kernels.
+
+The reference holds no literal golden vectors for this path (every reference
+test is relational), so each oracle function is pinned by an independent route:
+brute force, closed forms, finite differences, torch autograd on the CPU, and the
+reference's own invariants (full pool == dense, rte/kernels test_kernels.py:82-148).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as A
+from oracle import cluster_pool as CP
+from oracle import routing as R
+from oracle import swiglu as SW
+
+
+def _rng(seed=0):
+    return np.random.default_rng(seed)
+
+
+# ---------------------------------------------------------------- routing
+
+def _brute_topk(row, k):
+    keyed = sorted(range(len(row)), key=lambda i: (not np.isnan(row[i]), -row[i] if not np.isnan(row[i]) else 0, i))
+    return keyed[:k]
+
+
+@pytest.mark.parametrize("C,k", [(8, 1), (32, 4), (64, 8), (100, 16)])
+def test_topk_matches_brute_force_with_ties(C, k):
+    rng = _rng(C)
+    lg = rng.integers(-3, 4, size=(50, C)).astype(np.float32)  # heavy ties
+    lg[3, 5 % C] = np.nan
+    ids, w = R.route_topk(lg, k)
+    for t in range(lg.shape[0]):
+        assert list(ids[t]) == _brute_topk(lg[t], k)
+    finite = ~np.isnan(lg).any(-1)
+    np.testing.assert_allclose(w[finite].sum(-1), 1.0, rtol=1e-6)
+
+
+def test_topk_k1_is_argmax_routing():
+    # route_to_static_centers uses argmax (rte/kernels/cluster_pool_ffn.py:140)
+    lg = _rng(1).standard_normal((200, 32)).astype(np.float32)
+    ids, w = R.route_topk(lg, 1)
+    np.testing.assert_array_equal(ids[:, 0], lg.argmax(-1))
+    np.testing.assert_array_equal(w, 1.0)
+
+
+def test_topk_matches_torch_topk_on_distinct_values():
+    lg = _rng(2).standard_normal((300, 64)).astype(np.float32)
+    ids, w = R.route_topk(lg, 8)
+    tv, ti = torch.topk(torch.from_numpy(lg), 8, dim=-1)
+    np.testing.assert_array_equal(ids, ti.numpy())
+    np.testing.assert_allclose(w, torch.softmax(tv, -1).numpy(), rtol=1e-6)
+
+
+def test_pack_index_brute_force_and_roundtrip():
+    rng = _rng(3)
+    T, k, C = 97, 3, 11
+    cl = np.stack([rng.permutation(C)[:k] for _ in range(T)]).astype(np.int32)
+    pk = R.pack_index(cl, C, k)
+    flat = cl.reshape(-1)
+    for c in range(C):
+        lo, hi = pk["offsets"][c], pk["offsets"][c + 1]
+        expect = [p for p in range(T * k) if flat[p] == c]
+        assert list(pk["pair_of_slot"][lo:hi]) == expect
+        assert list(pk["tok_of_slot"][lo:hi]) == [p // k for p in expect]
+    np.testing.assert_array_equal(pk["pair_of_slot"][pk["slot_of_pair"]], np.arange(T * k))
+    assert pk["invalid"] == 0
+
+
+def test_pack_index_invalid_ids_are_dropped():
+    cl = np.array([0, 5, 1, -1, 1], dtype=np.int32)
+    pk = R.pack_index(cl, 2, 1)
+    assert pk["invalid"] == 2
+    assert list(pk["offsets"]) == [0, 1, 3]
+    assert list(pk["slot_of_pair"]) == [0, -1, 1, -1, 2]
+
+
+def test_static_pack_gather_roundtrip():
+    a = _rng(4).integers(0, 5, size=40)
+    pack, flat, counts, mx = R.static_pack_gather(a, 5)
+    assert counts.sum() == 40 and mx == counts.max()
+    for t in range(40):
+        c, r = divmod(int(flat[t]), mx)
+        assert c == a[t] and pack[c, r] == t
+
+
+def test_route_softmax_bwd_finite_difference():
+    rng = _rng(5)
+    T, C, k = 4, 7, 3
+    lg = rng.standard_normal((T, C))
+    ids, _ = R.route_topk(lg.astype(np.float32), k)
+    dw = rng.standard_normal((T, k))
+
+    def f(L):
+        sel = np.take_along_axis(L, ids.astype(np.int64), -1)
+        e = np.exp(sel - sel.max(-1, keepdims=True))
+        return ((e / e.sum(-1, keepdims=True)) * dw).sum()
+
+    _, w = R.route_topk(lg.astype(np.float32), k)
+    g = R.route_softmax_bwd(ids, np.take_along_axis(
+        np.exp(lg - lg.max(-1, keepdims=True)), ids.astype(np.int64), -1) / np.take_along_axis(
+        np.exp(lg - lg.max(-1, keepdims=True)), ids.astype(np.int64), -1).sum(-1, keepdims=True), dw, C)
+    eps = 1e-6
+    num = np.zeros_like(lg)
+    for i in range(T):
+        for j in range(C):
+            Lp = lg.copy(); Lp[i, j] += eps
+            Lm = lg.copy(); Lm[i, j] -= eps
+            num[i, j] = (f(Lp) - f(Lm)) / (2 * eps)
+    np.testing.assert_allclose(g, num, atol=1e-7)
+    assert w.shape == (T, k)
+
+
+# ---------------------------------------------------------------- SwiGLU
+
+@pytest.mark.parametrize("wd_rows", [False, True])
+def test_dense_swiglu_matches_torch_autograd(wd_rows):
+    rng = _rng(6)
+    T, d, F = 9, 8, 12
+    x = rng.standard_normal((T, d))
+    wug = rng.standard_normal((2 * F, d)) * 0.3
+    wd = rng.standard_normal((F, d) if wd_rows else (d, F)) * 0.3
+    dy = rng.standard_normal((T, d))
+    y, cache = SW.dense_swiglu_fwd(x, wug, wd, wd_rows=wd_rows)
+    dx, dwug, dwd = SW.dense_swiglu_bwd(dy, x, wug, wd, cache, wd_rows=wd_rows)
+    tx, tug, td = (torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (x, wug, wd))
+    up, gate = (tx @ tug.t()).chunk(2, dim=-1)
+    z = up * torch.nn.functional.silu(gate)
+    ty = z @ (td if wd_rows else td.t())
+    ty.backward(torch.tensor(dy))
+    np.testing.assert_allclose(y, ty.detach().numpy(), rtol=1e-12)
+    np.testing.assert_allclose(dx, tx.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dwug, tug.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dwd, td.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_dense_swiglu_backward_finite_difference():
+    rng = _rng(7)
+    T, d, F = 3, 4, 5
+    x = rng.standard_normal((T, d))
+    wug = rng.standard_normal((2 * F, d))
+    wd = rng.standard_normal((d, F))
+    dy = rng.standard_normal((T, d))
+    _, cache = SW.dense_swiglu_fwd(x, wug, wd)
+    dx, _, _ = SW.dense_swiglu_bwd(dy, x, wug, wd, cache)
+    eps = 1e-6
+    for i in range(T):
+        for j in range(d):
+            xp = x.copy(); xp[i, j] += eps
+            xm = x.copy(); xm[i, j] -= eps
+            num = ((SW.dense_swiglu_fwd(xp, wug, wd)[0] - SW.dense_swiglu_fwd(xm, wug, wd)[0]) * dy).sum() / (2 * eps)
+            assert abs(num - dx[i, j]) < 1e-6
+
+
+# ---------------------------------------------------------------- cluster pool
+
+def _pool_problem(seed, T=40, d=16, C=4, n=8, k=2):
+    rng = _rng(seed)
+    x = rng.standard_normal((T, d))
+    wr = rng.standard_normal((C, d)) * 0.5
+    wug = rng.standard_normal((2 * C * n, d)) * 0.2
+    wd = rng.standard_normal((d, C * n)) * 0.2
+    return x, wr, wug, wd
+
+
+def test_all_clusters_uniform_weights_equal_dense_over_C():
+    # the reference invariant "full pool == dense" (tests/test_kernels.py:82-107) in routed form
+    x, wr, wug, wd = _pool_problem(8)
+    C, k = 4, 4
+    ids, w = R.route_topk(np.zeros((x.shape[0], C), np.float32), k)
+    out = CP.routed_fwd(x, wug, wd, ids, w, C)
+    dense, _ = SW.dense_swiglu_fwd(x, wug, wd)
+    np.testing.assert_allclose(out * C, dense, rtol=1e-10, atol=1e-12)
+
+
+def test_k1_matches_reference_loop_oracle():
+    x, wr, wug, wd = _pool_problem(9, C=4, n=8)
+    C, n, F = 4, 8, 32
+    logits = (x @ wr.T).astype(np.float32)
+    ids, w = R.route_topk(logits, 1)
+    out = CP.routed_fwd(x, wug, wd, ids, w, C)
+    cand = np.arange(F).reshape(C, n)
+    wup_pool, wgate_pool, wdown_pool = CP.prepare_pools(wug[:F], wug[F:], wd.T, cand)
+    ref = CP.cluster_pool_reference_loop(x, ids[:, 0], wup_pool, wgate_pool, wdown_pool)
+    np.testing.assert_allclose(out, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_routed_backward_matches_torch_autograd():
+    x, wr, wug, wd = _pool_problem(10, T=30, d=8, C=4, n=4, k=2)
+    C, k = 4, 2
+    T, d = x.shape
+    F = wug.shape[0] // 2
+    n = F // C
+    dout = _rng(11).standard_normal((T, d))
+    logits = x @ wr.T
+    ids, _ = R.route_topk(logits.astype(np.float32), k)
+    tx, twr, tug, twd = (torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (x, wr, wug, wd))
+    tl = tx @ twr.t()
+    tids = torch.from_numpy(ids.astype(np.int64))
+    tw = torch.softmax(torch.gather(tl, 1, tids), -1)
+    out = torch.zeros(T, d, dtype=torch.float64)
+    for j in range(k):
+        for t in range(T):
+            c = int(ids[t, j])
+            up = tug[c * n:(c + 1) * n] @ tx[t]
+            gate = tug[F + c * n:F + (c + 1) * n] @ tx[t]
+            out = out.index_add(0, torch.tensor([t]), (tw[t, j] * (up * torch.nn.functional.silu(gate)) @ twd[:, c * n:(c + 1) * n].t()).unsqueeze(0))
+    out.backward(torch.tensor(dout))
+    w = tw.detach().numpy()
+    o = CP.routed_fwd(x, wug, wd, ids, w, C)
+    np.testing.assert_allclose(o, out.detach().numpy(), rtol=1e-10, atol=1e-12)
+    dx, dwr, dwug, dwd, _ = CP.routed_bwd(dout, x, wr, wug, wd, ids, w, C)
+    np.testing.assert_allclose(dx, tx.grad.numpy(), rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(dwr, twr.grad.numpy(), rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(dwug, tug.grad.numpy(), rtol=1e-9, atol=1e-11)
+    np.testing.assert_allclose(dwd, twd.grad.numpy(), rtol=1e-9, atol=1e-11)
+
+
+# ---------------------------------------------------------------- attention pieces
+
+def test_rmsnorm_matches_manual_and_backward():
+    rng = _rng(12)
+    x = rng.standard_normal((5, 16))
+    w = rng.standard_normal(16)
+    manual = x / np.sqrt((x**2).mean(-1, keepdims=True) + 1e-5) * w
+    np.testing.assert_allclose(A.rmsnorm(x, w), manual, rtol=1e-12)
+    tx = torch.tensor(x, requires_grad=True)
+    tw = torch.tensor(w, requires_grad=True)
+    y = tx * torch.rsqrt(tx.pow(2).mean(-1, keepdim=True) + 1e-5) * tw
+    dy = rng.standard_normal((5, 16))
+    y.backward(torch.tensor(dy))
+    dx, dw = A.rmsnorm_bwd(dy, x, w)
+    np.testing.assert_allclose(dx, tx.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dw, tw.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_rope_is_complex_rotation():
+    hd, S = 8, 7
+    cos, sin = A.rope_tables(hd, S)
+    x = _rng(13).standard_normal((2, 3, S, hd))
+    y = A.rope_apply(x, cos, sin)
+    inv = 1.0 / (10_000.0 ** (np.arange(0, hd, 2) / hd))
+    theta = np.arange(S)[:, None] * inv[None, :]
+    zc = (x[..., 0::2] + 1j * x[..., 1::2]) * np.exp(1j * theta)
+    np.testing.assert_allclose(y[..., 0::2], zc.real, atol=1e-12)
+    np.testing.assert_allclose(y[..., 1::2], zc.imag, atol=1e-12)
+    np.testing.assert_allclose(y[:, :, 0], x[:, :, 0], atol=1e-15)  # position 0 is identity
+    dy = _rng(14).standard_normal(y.shape)
+    dx = A.rope_apply_bwd(dy, cos, sin)
+    np.testing.assert_allclose((dy * y).sum(), (dx * x).sum(), rtol=1e-12)  # adjoint identity
+
+
+def test_qkv_rope_backward_matches_torch():
+    rng = _rng(15)
+    B, S, H, hd = 2, 5, 2, 4
+    d = H * hd
+    cos, sin = A.rope_tables(hd, S)
+    x = rng.standard_normal((B, S, d))
+    w = rng.standard_normal((3 * d, d))
+    q, k, v = A.qkv_rope(x, w, H, cos, sin)
+    dq, dk, dv = (rng.standard_normal(q.shape) for _ in range(3))
+    tx = torch.tensor(x, requires_grad=True)
+    tw = torch.tensor(w, requires_grad=True)
+    qkv = (tx @ tw.t()).view(B, S, 3, H, hd)
+    tq, tk, tv = (t.transpose(1, 2) for t in qkv.unbind(2))
+    tc, ts = torch.tensor(cos), torch.tensor(sin)
+
+    def rot(t):
+        return torch.stack((-t[..., 1::2], t[..., ::2]), -1).flatten(-2)
+
+    tq = tq * tc + rot(tq) * ts
+    tk = tk * tc + rot(tk) * ts
+    np.testing.assert_allclose(q, tq.detach().numpy(), rtol=1e-12)
+    (tq * torch.tensor(dq) + tk * torch.tensor(dk) + tv * torch.tensor(dv)).sum().backward()
+    dx, dw = A.qkv_rope_bwd(dq, dk, dv, x, w, cos, sin)
+    np.testing.assert_allclose(dx, tx.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dw, tw.grad.numpy(), rtol=1e-10, atol=1e-12)
