@@ -1,0 +1,185 @@
+"""Control-variate audit of the macro hot path (rte/audit.py:20-387).
+
+A sampled subset of the batch is replayed exactly; its per-sample loss replaces the hot
+loss through corrected = hot + (exact - hot) / p (gradient-corrected mode), which keeps
+the loss estimate unbiased for inclusion probability p.
+"""
+
+from __future__ import annotations
+
+from contextlib import nullcontext
+from dataclasses import dataclass
+
+import torch
+
+from rte_amd.config import TrainingConfig
+from rte_amd.macro import macro_alignment_metrics, macro_distill_loss
+from rte_amd.models import ModelMeta, ModelOutput, RecursiveModel
+
+
+@dataclass(slots=True)
+class AuditResult:
+    audit_mask: torch.Tensor
+    p_audit: torch.Tensor
+    exact: ModelOutput | None
+    corrected_loss_per_sample: torch.Tensor
+    macro_aux: dict[str, torch.Tensor]
+    metrics: dict[str, torch.Tensor]
+
+
+class AuditEngine:
+    def __init__(self, config: TrainingConfig):
+        self.config = config
+        self.recent_residual = 0.0
+        self.recipe_audit_ema: torch.Tensor | None = None
+        self.last_candidate_count = 0
+        self.last_capped_fraction = 0.0
+        self.last_sample_mode = "bernoulli"
+
+    def state_dict(self) -> dict[str, object]:
+        return {
+            "recent_residual": self.recent_residual,
+            "recipe_audit_ema": self.recipe_audit_ema,
+            "last_candidate_count": self.last_candidate_count,
+            "last_capped_fraction": self.last_capped_fraction,
+            "last_sample_mode": self.last_sample_mode,
+        }
+
+    def load_state_dict(self, state: dict[str, object]) -> None:
+        self.recent_residual = float(state.get("recent_residual", 0.0))
+        ema = state.get("recipe_audit_ema")
+        self.recipe_audit_ema = ema if isinstance(ema, torch.Tensor) else None
+        self.last_candidate_count = int(state.get("last_candidate_count", 0))
+        self.last_capped_fraction = float(state.get("last_capped_fraction", 0.0))
+        self.last_sample_mode = str(state.get("last_sample_mode", "bernoulli"))
+
+    def _coverage_deficit(self, recipe_ids, recipe_count):
+        if self.recipe_audit_ema is None or self.recipe_audit_ema.numel() != recipe_count:
+            self.recipe_audit_ema = torch.zeros(recipe_count, dtype=torch.float32, device=recipe_ids.device)
+        ema = self.recipe_audit_ema.to(recipe_ids.device)
+        return (self.config.coverage_min - ema[recipe_ids]).clamp_min(0.0) / max(self.config.coverage_min, 1e-12)
+
+    def _update_coverage(self, recipe_ids, mask):
+        if self.recipe_audit_ema is None:
+            return
+        ema = self.recipe_audit_ema.to(recipe_ids.device)
+        counts = torch.zeros_like(ema).index_add_(0, recipe_ids.long(), mask.float())
+        probs = counts / counts.sum().clamp_min(1.0)
+        ema.mul_(self.config.coverage_beta).add_(probs, alpha=1.0 - self.config.coverage_beta)
+        self.recipe_audit_ema = ema.detach()
+
+    def compute_audit_prob(self, meta: ModelMeta) -> torch.Tensor:
+        """rte/audit.py:79-97."""
+        r = meta.router
+        unc = r.router_entropy / (r.recipe_logits.shape[-1] + r.depth_logits.shape[-1])
+        p = (self.config.audit_p_min + self.config.audit_alpha * unc
+             + self.config.audit_beta * torch.full_like(unc, self.recent_residual)
+             + self.config.audit_gamma * self._coverage_deficit(meta.recipe_ids, r.recipe_logits.shape[-1]))
+        return p.clamp(self.config.audit_p_min, self.config.audit_p_max)
+
+    def sample_mask_with_prob(self, p: torch.Tensor, seed: int):
+        """rte/audit.py:99-132.  Returns (mask, inclusion_p, chosen_index or None, count or None);
+        the fixed-count sampler knows its count on the host, so it needs no device sync."""
+        gen = torch.Generator(device=p.device)
+        gen.manual_seed(seed)
+        fixed = self.config.audit_fixed_count_per_batch
+        if fixed is not None:
+            n = p.numel()
+            k = min(int(fixed), n)
+            mask = torch.zeros_like(p, dtype=torch.bool)
+            incl = torch.zeros_like(p)
+            self.last_sample_mode, self.last_candidate_count, self.last_capped_fraction = "fixed_count", k, 0.0
+            chosen = None
+            if k > 0 and n > 0:
+                chosen = torch.randperm(n, device=p.device, generator=gen)[:k]
+                mask[chosen] = True
+                incl.fill_(float(k) / float(n))
+            return mask, incl, chosen, k
+        self.last_sample_mode = "bernoulli"
+        mask = torch.bernoulli(p, generator=gen).bool()
+        incl = p.clone()
+        self.last_candidate_count = int(mask.sum().item())
+        self.last_capped_fraction = 0.0
+        cap = self.config.audit_cap
+        if cap is not None and self.last_candidate_count > cap:
+            sel = mask.nonzero(as_tuple=False).flatten()
+            perm = torch.randperm(sel.numel(), device=p.device, generator=gen)
+            capped = torch.zeros_like(mask)
+            capped[sel[perm[:cap]]] = True
+            self.last_capped_fraction = float((sel.numel() - cap) / max(sel.numel(), 1))
+            incl = p * (float(cap) / float(sel.numel()))
+            mask = capped
+        return mask, incl, None, None
+
+    def correction(self, model: RecursiveModel, tokens, targets, hot: ModelOutput, *, seed: int) -> AuditResult:
+        """rte/audit.py:245-387."""
+        if hot.loss_per_sample is None:
+            raise ValueError("hot output must include per-sample losses")
+        if self.config.audit_fixed_count_per_batch is None:
+            self.flush_pending()  # the Bernoulli sampler's probability depends on the last residual
+        req = self.compute_audit_prob(hot.meta)
+        mask, p, chosen, count = self.sample_mask_with_prob(req, seed=seed)
+        corrected = hot.loss_per_sample.clone()
+        zero = hot.loss_per_sample.new_zeros(())
+        aux = {k: zero for k in ("hid", "cos", "kl", "norm", "cons", "delta_dir", "delta_rms", "endpoint_normed",
+                                 "endpoint_raw", "rms_trust")}
+        metrics: dict[str, torch.Tensor] = {
+            "audit_probability": p.mean(),
+            "audit_requested_probability": req.mean(),
+            "audit_rate": mask.float().mean(),
+            "audit_count": mask.float().sum(),
+            "audit_inclusion_prob": p.mean(),
+        }
+        idx = chosen if chosen is not None else mask.nonzero(as_tuple=False).flatten()
+        has_audit = (count > 0) if count is not None else idx.numel() > 0
+        exact = None
+        if has_audit:
+            grad_corr = self.config.audit_mode == "gradient_corrected"
+            with (nullcontext() if grad_corr else torch.no_grad()):
+                exact = model.forward_exact_subset(tokens, targets, idx, reuse_router_decisions=hot.meta.router,
+                                                   cached_h0=hot.meta.h0)
+            hot_sub = hot.loss_per_sample.index_select(0, idx)
+            residual = exact.loss_per_sample - hot_sub
+            metrics["audit_residual_mean"] = residual.mean()
+            metrics["audit_residual_std"] = residual.float().std(unbiased=False)
+            metrics["audit_residual_var"] = residual.float().var(unbiased=False)
+            if self.config.audit_residual_clip is not None:
+                residual = residual.clamp(-self.config.audit_residual_clip, self.config.audit_residual_clip)
+            if not grad_corr:
+                residual = residual.detach()
+            p_sub = p.index_select(0, idx).clamp_min(1e-12)
+            metrics["corrected_metric_loss"] = (hot_sub + residual.detach() / p_sub).mean()
+            if grad_corr:
+                corrected = corrected.index_copy(0, idx, hot_sub + residual / p_sub)
+            hot_end = hot.meta.recurrent_hidden.index_select(0, idx)
+            h0_sub = hot.meta.h0.index_select(0, idx)
+            hot_logits = hot.meta.logits.index_select(0, idx) if hot.meta.logits is not None else None
+            tr = self.config
+            aux.update(macro_distill_loss(
+                hot_end, exact.meta.recurrent_hidden, hot_logits, exact.meta.logits, h0=h0_sub,
+                lambda_hid=tr.effective_lambda_hid, lambda_cos=tr.effective_lambda_cos, lambda_kl=tr.effective_lambda_kl,
+                lambda_norm=tr.lambda_norm, lambda_delta_dir=tr.lambda_delta_dir, lambda_delta_rms=tr.lambda_delta_rms,
+                lambda_endpoint_normed=tr.lambda_endpoint_normed, lambda_endpoint_raw=tr.lambda_endpoint_raw,
+                lambda_macro_rms_trust=tr.lambda_macro_rms_trust if tr.macro_rms_trust_region else 0.0,
+                temperature=tr.distill_temperature,
+            ))
+            align = macro_alignment_metrics(hot_end.detach(), exact.meta.recurrent_hidden, h0=h0_sub,
+                                            hot_logits=None if hot_logits is None else hot_logits.detach(),
+                                            exact_logits=exact.meta.logits)
+            metrics.update(align)
+            metrics["loss_residual"] = (exact.loss_per_sample - hot_sub).mean()
+            # recent residual feeds the next step's audit probability; kept on device
+            self._pending_residual = (1.0 - align["hidden_cosine_exact_macro"]).detach().clamp_min(0)
+        if hot.meta.recipe_ids is not None:
+            self._update_coverage(hot.meta.recipe_ids, mask)
+        if self.config.lambda_cons != 0.0 and hot.meta.h0 is not None and hot.meta.recipe_ids is not None:
+            aux["cons"] = self.config.lambda_cons * model.macro.consistency_loss(hot.meta.h0, hot.meta.h0,
+                                                                                 hot.meta.recipe_ids)
+        return AuditResult(mask, p, exact, corrected, aux, metrics)
+
+    def flush_pending(self) -> None:
+        """Materialise the residual used by compute_audit_prob (one host read, done off the timed path)."""
+        pend = getattr(self, "_pending_residual", None)
+        if pend is not None:
+            self.recent_residual = float(pend.item())
+            self._pending_residual = None

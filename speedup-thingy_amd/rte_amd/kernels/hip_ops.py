@@ -399,8 +399,13 @@ class RoutedClusterPoolFn(torch.autograd.Function):
              ptr(wugb), ptr(wdb), F, ptr(ug), ptr(zw), ptr(dug), ptr(dw_slot), ptr(dxp), ptr(dwug), ptr(dwd), _s())
         dlog = torch.empty((T, C), dtype=BF16, device=dev)
         call("rte_route_bwd", ptr(ids), ptr(w), ptr(dw_slot), ptr(sop), T, C, k, ptr(dlog), None, _s())
-        dx_router = gemm(dlog, wrb, b_t=True)              # [T, d] = dlogits @ Wr
-        dwr = gemm(dlog, xb, a_t=True, b_t=True, out_f32=True)  # [C, d] = dlogits^T @ x
+        wr_k = wrb
+        c8 = (C + 7) // 8 * 8  # the GEMM reads 8-element vectors along C
+        if c8 != C:
+            dlog = torch.nn.functional.pad(dlog, (0, c8 - C))
+            wr_k = torch.nn.functional.pad(wrb, (0, 0, 0, c8 - C))
+        dx_router = gemm(dlog, wr_k, b_t=True)                        # [T, d] = dlogits @ Wr
+        dwr = gemm(dlog, xb, a_t=True, b_t=True, out_f32=True)[:C]    # [C, d] = dlogits^T @ x
         dx = combine_rows(dxp, T, k, extra=dx_router, out_f32=False)
         dres = dout if has_resid else None
         return dx.view(shape), dwr.to(wr_dt), dwug.to(wug_dt), dwd.to(wd_dt), dres, None
@@ -409,3 +414,33 @@ class RoutedClusterPoolFn(torch.autograd.Function):
 def routed_cluster_pool_swiglu(x, wr, wug, wd, k: int, resid=None):
     """Returns (out, ids, weights); ids/weights are the routing decisions (no gradient)."""
     return RoutedClusterPoolFn.apply(x, wr, wug, wd, resid, k)
+
+
+# ----------------------------------------------------------------------------- plain linear (LM head)
+
+class LinearFn(torch.autograd.Function):
+    """out = x @ W^T on the MFMA GEMM (bf16 operands, fp32 accumulate), fp32 or bf16 output."""
+
+    @staticmethod
+    def forward(ctx, x, w, out_f32: bool):
+        _lib.require_device_tensors("linear", x, w)
+        shape = x.shape
+        xb = x.reshape(-1, shape[-1]).contiguous().to(BF16)
+        wb = cast_bf16(w)
+        out = gemm(xb, wb, out_f32=out_f32)
+        ctx.save_for_backward(xb, wb)
+        ctx.meta = (shape, x.dtype, w.dtype)
+        return out.view(*shape[:-1], wb.shape[0])
+
+    @staticmethod
+    def backward(ctx, dout):
+        xb, wb = ctx.saved_tensors
+        shape, x_dt, w_dt = ctx.meta
+        db = cast_bf16(dout.reshape(-1, wb.shape[0]))
+        dx = gemm(db, wb, b_t=True)                              # [T, K]
+        dw = gemm(db, xb, a_t=True, b_t=True, out_f32=True)      # [N, K]
+        return dx.view(shape).to(x_dt), dw.to(w_dt), None
+
+
+def linear(x, w, *, out_f32: bool = True):
+    return LinearFn.apply(x, w, out_f32)

@@ -1,0 +1,274 @@
+"""Macro operators Phi_{recipe, depth}: a per-sample low-rank update that stands in for
+`depth` exact recursive passes (rte/macro.py:42-391), plus the distillation losses and
+alignment metrics the audit uses (rte/macro.py:394-546).
+
+Parameter shapes and initialisation order follow the reference so state dicts load.
+Compute is torch on the device (a few small batched matmuls per step).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from rte_amd.config import ModelConfig
+
+
+def _rms(x, *, dim=-1, keepdim=False):
+    return x.float().pow(2).mean(dim=dim, keepdim=keepdim).sqrt().to(x.dtype)
+
+
+def _rmsnorm(x, eps: float = 1e-5):
+    return x * torch.rsqrt(x.float().pow(2).mean(dim=-1, keepdim=True) + eps).to(x.dtype)
+
+
+def _inverse_softplus(v):
+    v = v.clamp_min(1e-8)
+    return v + torch.log(-torch.expm1(-v))
+
+
+@dataclass(slots=True)
+class MacroTrace:
+    states: dict[int, torch.Tensor]
+    stride_sequence: list[list[int]]
+    physical_passes: torch.Tensor
+    decomposition_error: torch.Tensor | None = None
+
+
+class MacroOperators(nn.Module):
+    def __init__(self, config: ModelConfig):
+        super().__init__()
+        self.config = config
+        self.strides = list(config.depth_choices)
+        self.stride_to_idx = {s: i for i, s in enumerate(self.strides)}
+        r, k, d, m = config.recipe_count, len(self.strides), config.d_model, config.macro_rank
+        if config.macro_type == "v2_delta_radius":
+            input_dim = 3 * d + (d if (config.macro_use_delta_to_h0 or config.macro_include_delta_to_h0) else 0)
+            if config.macro_use_depth_embedding:
+                input_dim += d
+                self.depth_embed = nn.Parameter(torch.randn(k, d) * (1.0 / max(d, 1) ** 0.5))
+            else:
+                self.register_parameter("depth_embed", None)
+            if config.macro_use_recipe_embedding:
+                input_dim += d
+                self.recipe_embed = nn.Parameter(torch.randn(r, d) * (1.0 / max(d, 1) ** 0.5))
+            else:
+                self.register_parameter("recipe_embed", None)
+            hidden = max(m, m * config.macro_hidden_mult)
+            self.v = nn.Parameter(torch.randn(r, k, input_dim, hidden) * (1.0 / input_dim**0.5))
+            self.v2 = nn.Parameter(torch.randn(r, k, hidden, m) * (1.0 / hidden**0.5))
+            self.u = nn.Parameter(torch.randn(r, k, m, d) * 1e-3)
+            self.bias = nn.Parameter(torch.zeros(r, k, d))
+            radius = max(float(config.macro_update_scale_init), float(config.macro_update_scale), 1e-3)
+            self.rho_base_raw = nn.Parameter(_inverse_softplus(torch.full((r, k), radius)))
+            self.rho_head = nn.Parameter(torch.zeros(r, k, d, 1))
+            self.register_buffer("teacher_delta_rms", torch.zeros(r, k), persistent=True)
+            for name in ("d_gain", "update_scale", "gate_v", "gate_u", "gate_bias"):
+                self.register_parameter(name, None)
+        else:
+            input_dim = 3 * d + (d if config.macro_include_delta_to_h0 else 0)
+            if config.macro_use_depth_embedding:
+                input_dim += d
+                self.depth_embed = nn.Parameter(torch.randn(k, d) * (1.0 / max(d, 1) ** 0.5))
+            else:
+                self.register_parameter("depth_embed", None)
+            self.register_parameter("recipe_embed", None)
+            hidden = max(m, m * config.macro_hidden_mult)
+            self.d_gain = nn.Parameter(torch.zeros(r, k, d))
+            self.v = nn.Parameter(torch.randn(r, k, input_dim, hidden) * (1.0 / input_dim**0.5))
+            if hidden != m:
+                self.v2 = nn.Parameter(torch.randn(r, k, hidden, m) * (1.0 / hidden**0.5))
+            else:
+                self.register_parameter("v2", None)
+            self.u = nn.Parameter(torch.randn(r, k, m, d) * 1e-3)
+            update_scale = torch.full((r, k, d), float(config.macro_update_scale_init))
+            legacy = (
+                config.macro_hidden_mult == 1
+                and not config.macro_use_gated_update
+                and not config.macro_include_delta_to_h0
+                and not config.macro_use_depth_embedding
+                and config.macro_update_scale_init == 1.0
+            )
+            if legacy:
+                self.register_buffer("update_scale", update_scale, persistent=True)
+            else:
+                self.update_scale = nn.Parameter(update_scale)
+            self.bias = nn.Parameter(torch.zeros(r, k, d))
+            if config.macro_use_gated_update:
+                self.gate_v = nn.Parameter(torch.randn(r, k, input_dim, m) * (1.0 / input_dim**0.5))
+                self.gate_u = nn.Parameter(torch.randn(r, k, m, d) * 1e-3)
+                self.gate_bias = nn.Parameter(torch.zeros(r, k, d))
+            else:
+                for name in ("gate_v", "gate_u", "gate_bias"):
+                    self.register_parameter(name, None)
+            self.register_parameter("rho_base_raw", None)
+            self.register_parameter("rho_head", None)
+            self.register_buffer("teacher_delta_rms", torch.zeros(r, k), persistent=True)
+        self.register_buffer("depth_values", torch.tensor(self.strides, dtype=torch.long), persistent=False)
+        pairs = [(i, self.stride_to_idx[s * 2]) for i, s in enumerate(self.strides) if s * 2 in self.stride_to_idx]
+        self.register_buffer("cons_src_idx", torch.tensor([p[0] for p in pairs], dtype=torch.long), persistent=False)
+        self.register_buffer("cons_dst_idx", torch.tensor([p[1] for p in pairs], dtype=torch.long), persistent=False)
+
+    def stride_ids_for_depths(self, depths: torch.Tensor) -> torch.Tensor:
+        matches = depths.unsqueeze(-1) == self.depth_values.to(depths.device).unsqueeze(0)
+        return matches.float().argmax(dim=-1)
+
+    def apply_vectorized(self, h, h0, recipe_ids, stride_ids):
+        if self.config.macro_type == "v2_delta_radius":
+            return self._apply_v2(h, h0, recipe_ids, stride_ids)
+        return self._apply_bounded(h, h0, recipe_ids, stride_ids)
+
+    def _apply_bounded(self, h, h0, recipe_ids, stride_ids):
+        """rte/macro.py:201-236."""
+        gain = self.d_gain[recipe_ids, stride_ids]
+        v = self.v[recipe_ids, stride_ids]
+        u = self.u[recipe_ids, stride_ids]
+        bias = self.bias[recipe_ids, stride_ids]
+        scale = self.update_scale[recipe_ids, stride_ids]
+        normed = _rmsnorm(h)
+        parts = [normed, normed.mean(dim=1, keepdim=True).expand_as(normed), h0]
+        if self.config.macro_include_delta_to_h0:
+            parts.append(normed - _rmsnorm(h0))
+        if self.depth_embed is not None:
+            parts.append(self.depth_embed[stride_ids].unsqueeze(1).expand_as(normed))
+        z = torch.cat(parts, dim=-1)
+        low = F.silu(torch.bmm(z, v))
+        if self.v2 is not None:
+            low = F.silu(torch.bmm(low, self.v2[recipe_ids, stride_ids]))
+        low = torch.bmm(low, u)
+        update = gain.unsqueeze(1) * h + low + bias.unsqueeze(1)
+        if self.gate_v is not None:
+            gate = torch.sigmoid(
+                torch.bmm(F.silu(torch.bmm(z, self.gate_v[recipe_ids, stride_ids])), self.gate_u[recipe_ids, stride_ids])
+                + self.gate_bias[recipe_ids, stride_ids].unsqueeze(1)
+            )
+        else:
+            gate = 1.0
+        return h + self.config.macro_update_scale * scale.unsqueeze(1) * gate * torch.tanh(update)
+
+    def _apply_v2(self, h, h0, recipe_ids, stride_ids):
+        """rte/macro.py:238-279."""
+        normed = _rmsnorm(h0)
+        pooled = normed.mean(dim=1)
+        parts = [normed, pooled.unsqueeze(1).expand_as(normed), h0]
+        if self.config.macro_use_delta_to_h0 or self.config.macro_include_delta_to_h0:
+            parts.append(normed - _rmsnorm(h0))
+        if self.depth_embed is not None:
+            parts.append(self.depth_embed[stride_ids].unsqueeze(1).expand_as(normed))
+        if self.recipe_embed is not None:
+            parts.append(self.recipe_embed[recipe_ids].unsqueeze(1).expand_as(normed))
+        z = torch.cat(parts, dim=-1)
+        raw = torch.bmm(F.silu(torch.bmm(F.silu(torch.bmm(z, self.v[recipe_ids, stride_ids])),
+                                         self.v2[recipe_ids, stride_ids])), self.u[recipe_ids, stride_ids])
+        raw = raw + self.bias[recipe_ids, stride_ids].unsqueeze(1)
+        direction = raw / _rms(raw, dim=(1, 2), keepdim=True).clamp_min(1e-6)
+        rho_head = torch.bmm(pooled.unsqueeze(1), self.rho_head[recipe_ids, stride_ids]).squeeze(-1).squeeze(-1)
+        rho = F.softplus(self.rho_base_raw[recipe_ids, stride_ids] + rho_head)
+        teacher = self.teacher_delta_rms[recipe_ids, stride_ids].to(rho.device)
+        if self.config.macro_radius_init_from_teacher:
+            has = teacher > 0
+            clamped = torch.clamp(rho, min=teacher * self.config.macro_radius_clamp_mult_min,
+                                  max=teacher * self.config.macro_radius_clamp_mult_max)
+            rho = torch.where(has, clamped, rho)
+        return h0 + rho.view(-1, 1, 1).to(direction.dtype) * direction
+
+    def forward(self, h, h0, recipe_ids, depths, *, return_states: bool = False):
+        del return_states
+        if self.config.macro_decomposition != "direct":
+            raise NotImplementedError("only macro_decomposition='direct' is on the accelerated path")
+        stride_ids = self.stride_ids_for_depths(depths)
+        out = self.apply_vectorized(h, h0, recipe_ids, stride_ids)
+        trace = MacroTrace(
+            states={},
+            stride_sequence=[],  # filled lazily by callers that need it (avoids a host sync)
+            physical_passes=torch.ones(depths.shape[0], dtype=torch.float32, device=h.device),
+            decomposition_error=h.new_zeros(()),
+        )
+        return out, trace
+
+    def consistency_loss(self, h, h0, recipe_ids):
+        """rte/macro.py:342-359: Phi_{2s}(h) vs Phi_s(Phi_s(h))."""
+        if self.cons_src_idx.numel() == 0:
+            return h.new_zeros(())
+        pc, b = self.cons_src_idx.numel(), h.shape[0]
+        h_rep = h.unsqueeze(0).expand(pc, *h.shape).reshape(pc * b, *h.shape[1:])
+        h0_rep = h0.unsqueeze(0).expand(pc, *h0.shape).reshape(pc * b, *h0.shape[1:])
+        r_rep = recipe_ids.unsqueeze(0).expand(pc, b).reshape(-1)
+        src = self.cons_src_idx.unsqueeze(1).expand(pc, b).reshape(-1)
+        dst = self.cons_dst_idx.unsqueeze(1).expand(pc, b).reshape(-1)
+        direct = self.apply_vectorized(h_rep, h0_rep, r_rep, dst)
+        twice = self.apply_vectorized(self.apply_vectorized(h_rep, h0_rep, r_rep, src), h0_rep, r_rep, src)
+        return F.mse_loss(direct, twice)
+
+
+def macro_distill_loss(hot_hidden, exact_hidden, hot_logits, exact_logits, *, h0=None, lambda_hid=0.0,
+                       lambda_cos=0.0, lambda_kl=0.0, lambda_norm=0.0, lambda_delta_dir=0.0, lambda_delta_rms=0.0,
+                       lambda_endpoint_normed=0.0, lambda_endpoint_raw=0.0, lambda_macro_rms_trust=0.0,
+                       temperature=1.0):
+    """rte/macro.py:394-471."""
+    exact_hidden = exact_hidden.detach()
+    if exact_logits is not None:
+        exact_logits = exact_logits.detach()
+    zero = hot_hidden.new_zeros(())
+    if h0 is not None:
+        h0d = h0.detach()
+        dp, de = hot_hidden - h0d, exact_hidden - h0d
+        delta_dir = 1.0 - F.cosine_similarity(dp.flatten(1), de.flatten(1), dim=-1, eps=1e-8).mean()
+        pr = _rms(dp, dim=(1, 2)).clamp_min(1e-8)
+        er = _rms(de, dim=(1, 2)).clamp_min(1e-8)
+        delta_rms = (torch.log(pr) - torch.log(er)).square().mean()
+        endpoint_normed = F.smooth_l1_loss(_rmsnorm(hot_hidden), _rmsnorm(exact_hidden))
+        endpoint_raw = F.smooth_l1_loss(hot_hidden, exact_hidden)
+        ratio = _rms(hot_hidden, dim=(1, 2)).clamp_min(1e-8) / _rms(exact_hidden, dim=(1, 2)).clamp_min(1e-8)
+        rms_trust = torch.log(ratio).square().mean().to(hot_hidden.dtype)
+        hid = cos = norm = zero
+    else:
+        hid = F.mse_loss(hot_hidden, exact_hidden)
+        cos = 1.0 - F.cosine_similarity(hot_hidden.flatten(1), exact_hidden.flatten(1), dim=-1, eps=1e-8).mean()
+        hr = hot_hidden.float().pow(2).mean(dim=-1).sqrt()
+        er = exact_hidden.float().pow(2).mean(dim=-1).sqrt()
+        norm = (hr - er).abs().mean().to(hot_hidden.dtype)
+        delta_dir = delta_rms = endpoint_normed = endpoint_raw = rms_trust = zero
+    if hot_logits is not None and exact_logits is not None and hot_logits.shape == exact_logits.shape:
+        t = max(float(temperature), 1e-6)
+        kl = F.kl_div(F.log_softmax(hot_logits / t, dim=-1), F.softmax(exact_logits / t, dim=-1),
+                      reduction="batchmean") * (t**2)
+    else:
+        kl = zero
+    return {
+        "hid": lambda_hid * hid,
+        "cos": lambda_cos * cos,
+        "kl": lambda_kl * kl,
+        "norm": lambda_norm * norm,
+        "delta_dir": lambda_delta_dir * delta_dir,
+        "delta_rms": lambda_delta_rms * delta_rms,
+        "endpoint_normed": lambda_endpoint_normed * endpoint_normed,
+        "endpoint_raw": lambda_endpoint_raw * endpoint_raw,
+        "rms_trust": lambda_macro_rms_trust * rms_trust,
+    }
+
+
+def macro_alignment_metrics(hot_hidden, exact_hidden, *, h0, hot_logits=None, exact_logits=None):
+    """rte/macro.py:499-546."""
+    exact_hidden = exact_hidden.detach()
+    m = {
+        "hidden_cosine_exact_macro": F.cosine_similarity(hot_hidden.flatten(1), exact_hidden.flatten(1), dim=-1,
+                                                         eps=1e-8).mean(),
+        "hidden_mse_exact_macro": (hot_hidden - exact_hidden).square().mean(),
+    }
+    macro_norm = _rms(hot_hidden, dim=(1, 2)).mean()
+    exact_norm = _rms(exact_hidden, dim=(1, 2)).mean()
+    m.update(macro_norm=macro_norm, exact_norm=exact_norm, macro_exact_norm_ratio=macro_norm / exact_norm.clamp_min(1e-8))
+    if h0 is not None:
+        dp, de = hot_hidden - h0.detach(), exact_hidden - h0.detach()
+        m["delta_cosine_exact_macro"] = F.cosine_similarity(dp.flatten(1), de.flatten(1), dim=-1, eps=1e-8).mean()
+        pr, er = _rms(dp, dim=(1, 2)).mean(), _rms(de, dim=(1, 2)).mean()
+        m.update(delta_rms_exact=er, delta_rms_pred=pr, delta_rms_ratio=pr / er.clamp_min(1e-8))
+    if hot_logits is not None and exact_logits is not None and hot_logits.shape == exact_logits.shape:
+        te = F.log_softmax(exact_logits.detach(), dim=-1)
+        th = F.log_softmax(hot_logits, dim=-1)
+        m["logit_kl_exact_macro"] = (te.exp() * (te - th)).sum(dim=-1).mean()
+    return m

@@ -1,0 +1,173 @@
+"""Dense and recursive decoders (rte/models.py:73-723) on the HIP blocks.
+
+RecursiveModel.forward_macro (rte/models.py:681-723) is the recursive_macro hot path:
+prelude blocks -> per-sample router -> macro operator Phi -> coda blocks -> logits.
+forward_exact_from_h0 / forward_exact_subset replay audited samples exactly through the
+banked recursive core (rte/models.py:416-512, :605-679).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from rte_amd.config import ModelConfig, OutputConfig
+from rte_amd.kernels import optimized as K
+from rte_amd.layers import BankedRecursiveCore, RMSNorm, TransformerBlock
+from rte_amd.macro import MacroOperators, MacroTrace
+from rte_amd.output import ShortlistHead, ShortlistResult
+from rte_amd.recipes import RecipeBank
+from rte_amd.routing import Router, RouterOutput
+
+
+@dataclass(slots=True)
+class ModelMeta:
+    router: RouterOutput | None = None
+    recipe_ids: torch.Tensor | None = None
+    depths: torch.Tensor | None = None
+    h0: torch.Tensor | None = None
+    recurrent_hidden: torch.Tensor | None = None
+    hidden: torch.Tensor | None = None
+    logits: torch.Tensor | None = None
+    states: dict[int, torch.Tensor] | None = None
+    macro_trace: MacroTrace | None = None
+    shortlist: ShortlistResult | None = None
+    active_touches: torch.Tensor | None = None
+
+
+@dataclass(slots=True)
+class ModelOutput:
+    loss: torch.Tensor | None
+    loss_per_sample: torch.Tensor | None
+    logits: torch.Tensor | None
+    meta: ModelMeta
+
+
+def lm_loss_per_sample(logits: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
+    """Sum over the sequence of token cross-entropy (rte/models.py:73-75)."""
+    tok = F.cross_entropy(logits.float().flatten(0, -2), targets.flatten(), reduction="none")
+    return tok.view_as(targets).sum(dim=-1)
+
+
+class DenseModel(nn.Module):
+    def __init__(self, config: ModelConfig):
+        super().__init__()
+        if config.topology != "dense":
+            raise ValueError("DenseModel requires topology='dense'")
+        self.config = config
+        self.embed = nn.Embedding(config.vocab_size, config.d_model)
+        self.blocks = nn.Sequential(*[TransformerBlock(config) for _ in range(config.n_dense_layers)])
+        self.final_norm = RMSNorm(config.d_model)
+        self.lm_head = None if config.tie_embeddings else nn.Linear(config.d_model, config.vocab_size, bias=False)
+
+    @property
+    def vocab_weight(self) -> torch.Tensor:
+        return self.embed.weight if self.lm_head is None else self.lm_head.weight
+
+    def forward(self, tokens, targets=None, return_loss_per_sample=False, return_states=False) -> ModelOutput:
+        x = self.embed(tokens)
+        for block in self.blocks:
+            x = block(x)
+        hidden = self.final_norm(x)
+        logits = K.k_logits_full(hidden, self.vocab_weight)
+        lps = lm_loss_per_sample(logits, targets) if targets is not None else None
+        return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
+                           ModelMeta(hidden=hidden, logits=logits))
+
+
+class RecursiveModel(nn.Module):
+    def __init__(self, config: ModelConfig, output_config: OutputConfig | None = None):
+        super().__init__()
+        if config.topology != "recursive":
+            raise ValueError("RecursiveModel requires topology='recursive'")
+        self.config = config
+        self.output_config = output_config or OutputConfig()
+        self.recipe_bank = RecipeBank(config)
+        self.register_buffer("active_touch_table", self.recipe_bank.active_touch_table, persistent=False)
+        self.embed = nn.Embedding(config.vocab_size, config.d_model)
+        self.prelude = nn.Sequential(*[TransformerBlock(config) for _ in range(config.n_prelude)])
+        self.router = Router(config)
+        self.core = BankedRecursiveCore(config, self.recipe_bank)
+        self.macro = MacroOperators(config)
+        self.coda = nn.Sequential(*[TransformerBlock(config) for _ in range(config.n_coda)])
+        self.final_norm = RMSNorm(config.d_model)
+        self.lm_head = None if config.tie_embeddings else nn.Linear(config.d_model, config.vocab_size, bias=False)
+        self.shortlist_head = ShortlistHead(config.d_model, config.vocab_size, self.output_config)
+
+    @property
+    def vocab_weight(self) -> torch.Tensor:
+        return self.embed.weight if self.lm_head is None else self.lm_head.weight
+
+    def _prelude(self, tokens):
+        x = self.embed(tokens)
+        for block in self.prelude:
+            x = block(x)
+        return x
+
+    def _coda_hidden(self, h):
+        for block in self.coda:
+            h = block(h)
+        return self.final_norm(h)
+
+    def _coda_logits(self, h):
+        hidden = self._coda_hidden(h)
+        return hidden, K.k_logits_full(hidden, self.vocab_weight)
+
+    def forward_exact_from_h0(self, h0, targets=None, return_states=False, return_loss_per_sample=False, *,
+                              router_decisions: RouterOutput | None = None, fixed_recipe=None, fixed_depth=None):
+        route = router_decisions or self.router(h0, fixed_recipe=fixed_recipe, fixed_depth=fixed_depth)
+        h = h0
+        states: dict[int, torch.Tensor] = {}
+        for t in range(self.config.t_max):
+            active = route.depth > t
+            rid = route.recipe_id_by_pass[:, t] if route.recipe_id_by_pass is not None else route.recipe_id
+            h = self.core.forward_step(h, h0, rid, active, pass_idx=t)
+            if return_states and (t + 1) in self.config.depth_choices:
+                states[t + 1] = h.clone()
+        hidden, logits = self._coda_logits(h)
+        lps = lm_loss_per_sample(logits, targets) if targets is not None else None
+        meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
+                         hidden=hidden, logits=logits, states=states if return_states else None,
+                         active_touches=self.active_touch_table[route.recipe_id])
+        return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
+                           meta)
+
+    def forward_exact(self, tokens, targets=None, return_states=False, return_loss_per_sample=False, **kw):
+        return self.forward_exact_from_h0(self._prelude(tokens), targets, return_states, return_loss_per_sample, **kw)
+
+    def forward_exact_subset(self, tokens, targets, audit_index, *, reuse_router_decisions: RouterOutput,
+                             cached_h0=None, return_states=True, return_loss_per_sample=True):
+        """Exact replay of the audited samples (audit_index: long indices or a bool mask),
+        reusing the hot path's routing decisions and cached prelude state (rte/models.py:605-679)."""
+        idx = audit_index.nonzero(as_tuple=False).flatten() if audit_index.dtype == torch.bool else audit_index
+        route = reuse_router_decisions.subset(idx)
+        if cached_h0 is not None:
+            h0 = cached_h0.index_select(0, idx)
+        else:
+            h0 = self._prelude(tokens.index_select(0, idx))
+        return self.forward_exact_from_h0(h0, targets.index_select(0, idx), return_states, return_loss_per_sample,
+                                          router_decisions=route)
+
+    def forward_macro(self, tokens, targets=None, return_states=False, return_loss_per_sample=False, *,
+                      shortlist=False, seed=0, fixed_recipe=None, fixed_depth=None) -> ModelOutput:
+        h0 = self._prelude(tokens)
+        route = self.router(h0, fixed_recipe=fixed_recipe, fixed_depth=fixed_depth)
+        h, trace = self.macro(h0, h0, route.recipe_id, route.depth, return_states=return_states)
+        sl = None
+        if shortlist and targets is not None:
+            hidden = self._coda_hidden(h)
+            full_logits = None
+            sl = self.shortlist_head.loss(hidden, targets, self.vocab_weight, seed=seed)
+            lps, logits = sl.loss_per_sample, sl.logits
+        else:
+            hidden, full_logits = self._coda_logits(h)
+            logits = full_logits
+            lps = lm_loss_per_sample(full_logits, targets) if targets is not None else None
+        meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
+                         hidden=hidden, logits=full_logits, states=trace.states if return_states else None,
+                         macro_trace=trace, shortlist=sl, active_touches=self.active_touch_table[route.recipe_id])
+        return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
+                           meta)

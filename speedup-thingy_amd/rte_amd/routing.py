@@ -1,0 +1,111 @@
+"""Per-sample recipe / depth router on the pooled prelude state (rte/routing.py:47-188).
+
+Tiny MLPs on [B, d]; kept as torch ops on the device (it is glue, not a hot kernel).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from rte_amd.config import ModelConfig
+from rte_amd.recipes import factor_slot_counts
+
+
+@dataclass(slots=True)
+class RouterOutput:
+    recipe_logits: torch.Tensor
+    recipe_probs: torch.Tensor
+    recipe_id: torch.Tensor
+    recipe_onehot_st: torch.Tensor
+    depth_logits: torch.Tensor
+    depth_probs: torch.Tensor
+    depth_id: torch.Tensor
+    depth: torch.Tensor
+    depth_onehot_st: torch.Tensor
+    router_entropy: torch.Tensor
+    recipe_entropy: torch.Tensor
+    depth_entropy: torch.Tensor
+    expected_depth: torch.Tensor
+    recipe_logits_by_pass: torch.Tensor | None = None
+    recipe_probs_by_pass: torch.Tensor | None = None
+    recipe_id_by_pass: torch.Tensor | None = None
+
+    def subset(self, mask: torch.Tensor) -> "RouterOutput":
+        vals = {}
+        for name in self.__dataclass_fields__:
+            v = getattr(self, name)
+            vals[name] = v[mask] if isinstance(v, torch.Tensor) else v
+        return RouterOutput(**vals)
+
+
+def _entropy(p: torch.Tensor) -> torch.Tensor:
+    return -(p.clamp_min(1e-9).log() * p).sum(dim=-1)
+
+
+class Router(nn.Module):
+    def __init__(self, config: ModelConfig):
+        super().__init__()
+        hidden = config.router_hidden or max(32, config.d_model)
+        self.config = config
+        self.recipe_mlp = nn.Sequential(nn.Linear(config.d_model, hidden), nn.SiLU(), nn.Linear(hidden, config.recipe_count))
+        self.pass_recipe_bias = nn.Parameter(torch.zeros(config.t_max, config.recipe_count))
+        head_slots, ffn_slots = factor_slot_counts(config)
+        self.factor_mlp = nn.Sequential(nn.Linear(config.d_model, hidden), nn.SiLU(), nn.Linear(hidden, hidden))
+        self.pass_factor_bias = nn.Parameter(torch.zeros(config.t_max, hidden))
+        self.attn_bank_head = nn.Linear(hidden, config.attn_banks)
+        self.ffn_bank_head = nn.Linear(hidden, config.ffn_banks)
+        self.head_slot_head = nn.Linear(hidden, head_slots)
+        self.ffn_slot_head = nn.Linear(hidden, ffn_slots)
+        self.depth_mlp = nn.Sequential(nn.Linear(config.d_model, hidden), nn.SiLU(), nn.Linear(hidden, len(config.depth_choices)))
+        self.register_buffer("depth_values", torch.tensor(config.depth_choices, dtype=torch.long), persistent=False)
+
+    def forward(self, h0: torch.Tensor, *, fixed_recipe: int | None = None, fixed_depth: int | None = None,
+                temperature: float = 1.0) -> RouterOutput:
+        pooled = h0.mean(dim=1)
+        inv_t = 1.0 / max(temperature, 1e-6)
+        recipe_logits = self.recipe_mlp(pooled) * inv_t
+        depth_logits = self.depth_mlp(pooled) * inv_t
+        recipe_logits_by_pass = recipe_logits.unsqueeze(1) + self.pass_recipe_bias.unsqueeze(0) * inv_t
+        recipe_probs = F.softmax(recipe_logits, dim=-1)
+        recipe_probs_by_pass = F.softmax(recipe_logits_by_pass, dim=-1)
+        depth_probs = F.softmax(depth_logits, dim=-1)
+        B = h0.shape[0]
+        if fixed_recipe is None:
+            recipe_id = recipe_probs.argmax(dim=-1)
+            recipe_id_by_pass = recipe_probs_by_pass.argmax(dim=-1)
+        else:
+            recipe_id = torch.full((B,), fixed_recipe, device=h0.device, dtype=torch.long)
+            recipe_id_by_pass = torch.full((B, self.config.t_max), fixed_recipe, device=h0.device, dtype=torch.long)
+        if fixed_depth is None:
+            depth_id = depth_probs.argmax(dim=-1)
+        else:
+            if fixed_depth not in self.config.depth_choices:
+                raise ValueError(f"fixed_depth={fixed_depth} is not in depth_choices")
+            depth_id = torch.full((B,), self.config.depth_choices.index(fixed_depth), device=h0.device, dtype=torch.long)
+        recipe_hard = F.one_hot(recipe_id, recipe_probs.shape[-1]).to(recipe_probs.dtype)
+        depth_hard = F.one_hot(depth_id, depth_probs.shape[-1]).to(depth_probs.dtype)
+        depth_values = self.depth_values.to(depth_probs.dtype)
+        recipe_entropy = _entropy(recipe_probs)
+        depth_entropy = _entropy(depth_probs)
+        return RouterOutput(
+            recipe_logits=recipe_logits,
+            recipe_probs=recipe_probs,
+            recipe_id=recipe_id,
+            recipe_onehot_st=recipe_hard + recipe_probs - recipe_probs.detach(),
+            depth_logits=depth_logits,
+            depth_probs=depth_probs,
+            depth_id=depth_id,
+            depth=self.depth_values[depth_id],
+            depth_onehot_st=depth_hard + depth_probs - depth_probs.detach(),
+            router_entropy=recipe_entropy + depth_entropy,
+            recipe_entropy=recipe_entropy,
+            depth_entropy=depth_entropy,
+            expected_depth=(depth_probs * depth_values).sum(dim=-1),
+            recipe_logits_by_pass=recipe_logits_by_pass,
+            recipe_probs_by_pass=recipe_probs_by_pass,
+            recipe_id_by_pass=recipe_id_by_pass,
+        )

@@ -1,0 +1,278 @@
+"""Training engine for the accelerated modes (rte/training.py:42-1701 restated for
+dense_exact, recursive_exact, recursive_macro and recursive_macro_shortlist).
+
+The step keeps the reference's loss composition (corrected CE / seq_len + macro aux +
+router aux, rte/training.py:1381-1385), bf16 autocast for torch glue, fused AdamW with
+the reference's parameter groups, non-finite skip, grad accumulation and clipping.
+Differences that only change where numbers live: metrics stay on the device until
+`metrics_to_host` (one copy instead of one sync per value), and gradient/param norms use
+torch._foreach_norm.
+"""
+
+from __future__ import annotations
+
+import time
+from contextlib import nullcontext
+from dataclasses import dataclass
+from typing import Any
+
+import torch
+
+from rte_amd.audit import AuditEngine, AuditResult
+from rte_amd.config import ExperimentConfig, TrainingConfig
+from rte_amd.kernels import optimized
+from rte_amd.models import DenseModel, ModelOutput, RecursiveModel
+
+ACCELERATED_MODES = {"dense_exact", "recursive_exact", "recursive_macro", "recursive_macro_shortlist"}
+
+
+def set_seed(seed: int) -> None:
+    import random
+
+    import numpy as np
+
+    random.seed(seed)
+    np.random.seed(seed % (2**32))
+    torch.manual_seed(seed)
+
+
+def router_aux_losses(recipe_probs, expected_depth, usage_ema, tr: TrainingConfig) -> dict[str, torch.Tensor]:
+    """rte/metrics.py:97-112."""
+    r = recipe_probs.shape[-1]
+    mean_prob = recipe_probs.float().mean(dim=0)
+    load = r * mean_prob.square().sum() - 1.0
+    cover = torch.relu(tr.coverage_min - usage_ema.to(recipe_probs.device)).square().sum()
+    return {
+        "load": tr.lambda_load * load,
+        "cover": tr.lambda_cover * cover,
+        "depth": tr.lambda_depth * expected_depth.float().mean(),
+    }
+
+
+@dataclass
+class TrainStepResult:
+    loss: torch.Tensor
+    model_output: ModelOutput
+    metrics: dict[str, Any]
+    audit: AuditResult | None = None
+
+
+class TrainEngine:
+    def __init__(self, config: ExperimentConfig, *, device: torch.device | None = None,
+                 dense_model: DenseModel | None = None, recursive_model: RecursiveModel | None = None):
+        self.config = config
+        tr = config.training
+        if tr.mode not in ACCELERATED_MODES:
+            raise NotImplementedError(f"mode {tr.mode!r} is outside the accelerated path ({sorted(ACCELERATED_MODES)})")
+        self.device = device or torch.device("cuda")
+        set_seed(tr.seed)
+        if tr.strict_cuda and self.device.type != "cuda":
+            raise RuntimeError("strict_cuda requires a ROCm device")
+        optimized.set_strict_cuda(tr.strict_cuda, require_flash=tr.require_flash_attention)
+        if tr.allow_tf32:
+            torch.backends.cuda.matmul.allow_tf32 = True
+        self.dense_model = dense_model
+        self.recursive_model = recursive_model
+        if self.dense_model is None and config.model.topology == "dense":
+            self.dense_model = DenseModel(config.model)
+        if self.recursive_model is None and config.model.topology == "recursive":
+            self.recursive_model = RecursiveModel(config.model, config.output)
+        for m in (self.dense_model, self.recursive_model):
+            if m is not None:
+                m.to(self.device)
+        self.optimizer = self._build_optimizer(self._param_groups())
+        self.optimizer.zero_grad(set_to_none=True)
+        self.audit_engine = AuditEngine(tr)
+        self.global_step = 0
+        self.global_micro_step = 0
+        self.tokens_seen = 0
+        self.last_grad_metrics: dict[str, Any] = {}
+
+    # ------------------------------------------------------------------ optimizer
+    def _param_groups(self) -> list[dict[str, Any]]:
+        tr = self.config.training
+        if self.dense_model is not None:
+            return [{"params": list(self.dense_model.parameters()), "lr": tr.effective_lr_base,
+                     "base_lr": tr.effective_lr_base, "name": "dense"}]
+        m = self.recursive_model
+        seen: set[int] = set()
+        specs = [
+            ("embedding", tr.effective_lr_base, list(m.embed.parameters())),
+            ("prelude", tr.effective_lr_base, list(m.prelude.parameters())),
+            ("core", tr.effective_lr_base, list(m.core.parameters())),
+            ("macro", tr.effective_lr_macro, list(m.macro.parameters())),
+            ("coda", tr.effective_lr_coda, [*m.coda.parameters(), *m.final_norm.parameters()]),
+            ("output", tr.effective_lr_output,
+             [*(m.lm_head.parameters() if m.lm_head is not None else []), *m.shortlist_head.parameters()]),
+            ("router", tr.effective_lr_router, list(m.router.parameters())),
+        ]
+        groups = []
+        for name, lr, params in specs:
+            uniq = [p for p in params if id(p) not in seen and not seen.add(id(p))]
+            if uniq:
+                groups.append({"params": uniq, "lr": lr, "base_lr": lr, "name": name})
+        return groups
+
+    def _build_optimizer(self, groups):
+        kw: dict[str, Any] = {"weight_decay": self.config.training.weight_decay}
+        if self.device.type == "cuda" and self.config.training.fused_optimizer:
+            kw["fused"] = True
+        elif self.config.training.foreach_optimizer:
+            kw["foreach"] = True
+        return torch.optim.AdamW(groups, **kw)
+
+    def _autocast(self):
+        if self.config.training.precision != "bf16":
+            return nullcontext()
+        return torch.autocast(device_type=self.device.type, dtype=torch.bfloat16)
+
+    def _loss_scale(self, targets) -> float:
+        return float(targets.shape[1]) if self.config.training.loss_normalization == "token_mean" else 1.0
+
+    # ------------------------------------------------------------------ step
+    def _grad_metrics(self) -> dict[str, torch.Tensor]:
+        out: dict[str, torch.Tensor] = {}
+        for g in self.optimizer.param_groups:
+            name = str(g.get("name", "group"))
+            params = [p for p in g["params"]]
+            grads = [p.grad for p in params if p.grad is not None]
+            pn = torch.linalg.vector_norm(torch.stack(torch._foreach_norm([p.detach().float() for p in params])))
+            gn = (torch.linalg.vector_norm(torch.stack(torch._foreach_norm([x.float() for x in grads])))
+                  if grads else pn.new_zeros(()))
+            out[f"grad_norm_{name}"] = gn
+            out[f"update_ratio_{name}"] = float(g["lr"]) * gn / pn.clamp_min(1e-12)
+        return out
+
+    def _finish_step(self, loss: torch.Tensor, *, check_finite: bool = True) -> bool:
+        """rte/training.py:445-468.  The finiteness check reads one scalar from the device."""
+        tr = self.config.training
+        self.last_grad_metrics = {}
+        if check_finite and not bool(torch.isfinite(loss.detach()).item()):
+            self.optimizer.zero_grad(set_to_none=True)
+            self.global_micro_step += 1
+            self.last_grad_metrics = {"skipped_nonfinite_loss": 1.0}
+            return False
+        (loss / tr.grad_accum_steps).backward()
+        self.global_micro_step += 1
+        step = self.global_micro_step % tr.grad_accum_steps == 0
+        if step and tr.grad_clip_norm is not None:
+            params = [p for g in self.optimizer.param_groups for p in g["params"]]
+            torch.nn.utils.clip_grad_norm_(params, tr.grad_clip_norm, foreach=True)
+        if step:
+            self.last_grad_metrics = self._grad_metrics()
+            self.optimizer.step()
+            self.optimizer.zero_grad(set_to_none=True)
+            self.global_step += 1
+        return step
+
+    def _move(self, batch):
+        return batch[0].to(self.device, non_blocking=True), batch[1].to(self.device, non_blocking=True)
+
+    def train_step(self, batch, *, check_finite: bool = True) -> TrainStepResult:
+        mode = self.config.training.mode
+        if mode == "dense_exact":
+            return self._step_dense(batch, check_finite)
+        if mode == "recursive_exact":
+            return self._step_recursive_exact(batch, check_finite)
+        return self._step_macro(batch, shortlist=mode == "recursive_macro_shortlist", check_finite=check_finite)
+
+    def _step_dense(self, batch, check_finite):
+        tokens, targets = self._move(batch)
+        t0 = time.perf_counter()
+        with self._autocast():
+            out = self.dense_model(tokens, targets, return_loss_per_sample=True)
+        loss = out.loss_per_sample.mean() / self._loss_scale(targets)
+        stepped = self._finish_step(loss, check_finite=check_finite)
+        self.tokens_seen += tokens.numel()
+        return TrainStepResult(loss, out, {"mode": "dense_exact", "loss": loss, "stepped": stepped,
+                                           "host_time": time.perf_counter() - t0, **self.last_grad_metrics})
+
+    def _step_recursive_exact(self, batch, check_finite):
+        tr = self.config.training
+        tokens, targets = self._move(batch)
+        m = self.recursive_model
+        with self._autocast():
+            out = m.forward_exact(tokens, targets, return_loss_per_sample=True, fixed_recipe=tr.fixed_recipe,
+                                  fixed_depth=tr.fixed_depth)
+            aux = self._router_aux(out)
+        loss = out.loss_per_sample.mean() / self._loss_scale(targets) + sum(aux.values())
+        stepped = self._finish_step(loss, check_finite=check_finite)
+        m.recipe_bank.update_usage(out.meta.recipe_ids, beta=tr.coverage_beta)
+        self.tokens_seen += tokens.numel()
+        return TrainStepResult(loss, out, {"mode": "recursive_exact", "loss": loss, "stepped": stepped,
+                                           **self.last_grad_metrics})
+
+    def _router_aux(self, out: ModelOutput) -> dict[str, torch.Tensor]:
+        r = out.meta.router
+        if self.config.training.disable_router_aux:
+            z = r.recipe_probs.new_zeros(())
+            return {"load": z, "cover": z, "depth": z}
+        return router_aux_losses(r.recipe_probs, r.expected_depth, self.recursive_model.recipe_bank.usage_ema,
+                                 self.config.training)
+
+    def _step_macro(self, batch, *, shortlist: bool, check_finite: bool):
+        """rte/training.py:1336-1476."""
+        tr = self.config.training
+        m = self.recursive_model
+        if shortlist and tr.debug_force_full_output:
+            raise RuntimeError("debug_force_full_output forbids recursive_macro_shortlist")
+        tokens, targets = self._move(batch)
+        with self._autocast():
+            hot = m.forward_macro(tokens, targets, return_states=True, return_loss_per_sample=True,
+                                  shortlist=shortlist, seed=tr.seed + self.global_step, fixed_recipe=tr.fixed_recipe,
+                                  fixed_depth=tr.fixed_depth)
+            audit = self.audit_engine.correction(m, tokens, targets, hot, seed=tr.seed + 10_000 + self.global_step)
+            aux = self._router_aux(hot)
+            scale = self._loss_scale(targets)
+            loss = audit.corrected_loss_per_sample.mean() / scale + sum(audit.macro_aux.values()) + sum(aux.values())
+        stepped = self._finish_step(loss, check_finite=check_finite)
+        m.recipe_bank.update_usage(hot.meta.recipe_ids, beta=tr.coverage_beta)
+        self.tokens_seen += tokens.numel()
+        metrics = {
+            "mode": "recursive_macro_shortlist" if shortlist else "recursive_macro",
+            "loss": loss.detach(),
+            "hot_lm_loss": hot.loss_per_sample.detach().mean() / scale,
+            "corrected_lm_loss": audit.corrected_loss_per_sample.detach().mean() / scale,
+            "nll_per_token": audit.corrected_loss_per_sample.detach().mean() / float(targets.shape[1]),
+            "avg_depth": hot.meta.depths.float().mean(),
+            "stepped": stepped,
+            **{f"audit_{k}": v for k, v in audit.metrics.items()},
+            **{f"macro_{k}": v.detach() for k, v in audit.macro_aux.items()},
+            **{f"aux_{k}": v.detach() for k, v in aux.items()},
+            **self.last_grad_metrics,
+        }
+        return TrainStepResult(loss, hot, metrics, audit)
+
+    # ------------------------------------------------------------------ checkpoint (rte/training.py:1656-1701)
+    def save_checkpoint(self, path) -> None:
+        model = self.recursive_model if self.recursive_model is not None else self.dense_model
+        torch.save({
+            "model": model.state_dict(),
+            "optimizer": self.optimizer.state_dict(),
+            "global_step": self.global_step,
+            "global_micro_step": self.global_micro_step,
+            "tokens_seen": self.tokens_seen,
+            "audit": self.audit_engine.state_dict(),
+            "torch_rng": torch.get_rng_state(),
+            "cuda_rng": torch.cuda.get_rng_state_all() if torch.cuda.is_available() else None,
+        }, path)
+
+    def load_checkpoint(self, path) -> None:
+        payload = torch.load(path, map_location=self.device, weights_only=False)
+        model = self.recursive_model if self.recursive_model is not None else self.dense_model
+        model.load_state_dict(payload["model"])
+        self.optimizer.load_state_dict(payload["optimizer"])
+        self.global_step = int(payload["global_step"])
+        self.global_micro_step = int(payload["global_micro_step"])
+        self.tokens_seen = int(payload["tokens_seen"])
+        self.audit_engine.load_state_dict(payload["audit"])
+        torch.set_rng_state(payload["torch_rng"].cpu())
+        if payload.get("cuda_rng") is not None and torch.cuda.is_available():
+            torch.cuda.set_rng_state_all([s.cpu() for s in payload["cuda_rng"]])
+
+
+def metrics_to_host(metrics: dict[str, Any]) -> dict[str, Any]:
+    """Copy every tensor metric to the host in one transfer."""
+    tens = {k: v for k, v in metrics.items() if isinstance(v, torch.Tensor)}
+    host = optimized.k_metrics_reduce(tens)
+    return {**{k: v for k, v in metrics.items() if not isinstance(v, torch.Tensor)}, **host}
