@@ -106,7 +106,7 @@ def kernel_candidates(B: int, S: int):
 
     def head():
         _lib.call("rte_gemm_bf16", x.data_ptr(), d, 0, None, w_head.data_ptr(), d, 0, None, head_out.data_ptr(), V,
-                  1, T, V, d, 1.0, 0.0, None, 0, s)
+                  1, T, V, d, 1.0, 0.0, None, 0, None, 0, s)
 
     def qkv():
         _lib.call("rte_qkv_rope_fwd", x.data_ptr(), wqkv.data_ptr(), cos.data_ptr(), sin.data_ptr(), B, S, 8, 64,

@@ -41,7 +41,12 @@ int rte_device_info(char* buf, int buf_len);
 int rte_gemm_bf16(const void* a, int64_t lda, int a_t, const int32_t* a_rows,
                   const void* b, int64_t ldb, int b_t, const int32_t* b_rows,
                   void* c, int64_t ldc, int c_f32, int M, int N, int K,
-                  float alpha, float beta, const float* resid, int64_t ld_resid, void* stream);
+                  float alpha, float beta, const float* resid, int64_t ld_resid,
+                  void* workspace, size_t workspace_bytes, void* stream);
+/* Workspace that lets a dense problem of this shape split its reduction along K
+ * (fp32 partials summed in a fixed order: deterministic).  A smaller or NULL
+ * workspace only disables the split. */
+size_t rte_gemm_workspace_bytes(int M, int N, int K);
 
 /* Same, with attention-layout operands: row r -> (r / rdiv)*rs_hi + (r % rdiv)*ld and
  * contiguous index c -> (c / cdiv)*cs_hi + c % cdiv  (rdiv/cdiv = 0: plain).
@@ -50,7 +55,8 @@ int rte_gemm_bf16(const void* a, int64_t lda, int a_t, const int32_t* a_rows,
 int rte_gemm_bf16_split(const void* a, const int64_t* a_layout, int a_t,
                         const void* b, const int64_t* b_layout, int b_t,
                         void* c, int64_t ldc, int c_f32, int M, int N, int K,
-                        float alpha, float beta, const float* resid, int64_t ld_resid, void* stream);
+                        float alpha, float beta, const float* resid, int64_t ld_resid,
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- routing (rte/kernels/cluster_pool_ffn.py:129-140 generalised to per-token top-k;
  *      rte/models.py:300-309 softmax-over-selected combine rule) ----
@@ -121,7 +127,7 @@ int rte_dense_swiglu_fwd(const void* x, int T, int d, int F, const void* wug, co
  * dwd f32 in the layout of wd (overwritten). */
 int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, const void* wug,
                          const void* wd, int wd_rows, const void* ug, const void* z, void* dug, void* dx,
-                         float* dwug, float* dwd, void* stream);
+                         float* dwug, float* dwd, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- fused QKV projection + interleaved RoPE (rte/layers.py:53-75, rte/kernels/reference.py:20-37) ----
  * x [B*S, d] bf16, wqkv [3d, d] bf16 (nn.Linear(d, 3d).weight), cos/sin [S, hd] f32.
@@ -133,7 +139,7 @@ int rte_qkv_rope_fwd(const void* x, const void* wqkv, const float* cos_t, const 
 int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const int64_t* sk, const void* dv,
                      const int64_t* sv, const void* x, const void* wqkv, const float* cos_t,
                      const float* sin_t, int B, int S, int H, int hd, void* dqkv, void* dx, float* dw,
-                     void* stream);
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- RMSNorm (rte/kernels/reference.py:9-17, rte/layers.py:26-33) ----
  * out bf16 = bf16(x * rsqrt(mean(x^2) + eps) * w), rstd [T] f32 saved for backward. */

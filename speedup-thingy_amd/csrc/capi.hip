@@ -84,9 +84,12 @@ int rte_device_info(char* buf, int buf_len) {
   return 0;
 }
 
+size_t rte_gemm_workspace_bytes(int M, int N, int K) { return gemm_splitk_bytes(M, N, K); }
+
 int rte_gemm_bf16(const void* a, int64_t lda, int a_t, const int32_t* a_rows, const void* b, int64_t ldb,
                   int b_t, const int32_t* b_rows, void* c, int64_t ldc, int c_f32, int M, int N, int K,
-                  float alpha, float beta, const float* resid, int64_t ld_resid, void* stream) {
+                  float alpha, float beta, const float* resid, int64_t ld_resid, void* workspace,
+                  size_t workspace_bytes, void* stream) {
   GemmArgs p;
   p.a = plain(a, lda);
   p.a.rows = a_rows;
@@ -104,12 +107,13 @@ int rte_gemm_bf16(const void* a, int64_t lda, int a_t, const int32_t* a_rows, co
   p.epi.beta = beta;
   p.epi.resid = resid;
   p.epi.ld_resid = ld_resid;
-  return gemm_launch(p, EPI_STORE, S(stream));
+  return gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes);
 }
 
 int rte_gemm_bf16_split(const void* a, const int64_t* a_layout, int a_t, const void* b, const int64_t* b_layout,
                         int b_t, void* c, int64_t ldc, int c_f32, int M, int N, int K, float alpha, float beta,
-                        const float* resid, int64_t ld_resid, void* stream) {
+                        const float* resid, int64_t ld_resid, void* workspace, size_t workspace_bytes,
+                        void* stream) {
   GemmArgs p;
   p.a = from_layout(a, a_layout);
   p.b = from_layout(b, b_layout);
@@ -128,7 +132,7 @@ int rte_gemm_bf16_split(const void* a, const int64_t* a_layout, int a_t, const v
   // split columns must keep 8-element vectors inside one segment
   if (p.a.cdiv) RTE_REQUIRE(p.a.cdiv % 8 == 0, "gemm_split: A cdiv must be a multiple of 8");
   if (p.b.cdiv) RTE_REQUIRE(p.b.cdiv % 8 == 0, "gemm_split: B cdiv must be a multiple of 8");
-  return gemm_launch(p, EPI_STORE, S(stream));
+  return gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes);
 }
 
 int rte_route_topk(const float* logits, int T, int C, int k, int32_t* ids, float* weights, void* stream) {
@@ -343,7 +347,7 @@ int rte_dense_swiglu_fwd(const void* x, int T, int d, int F, const void* wug, co
 
 int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, const void* wug, const void* wd,
                          int wd_rows, const void* ug, const void* z, void* dug, void* dx, float* dwug,
-                         float* dwd, void* stream) {
+                         float* dwd, void* workspace, size_t workspace_bytes, void* stream) {
   RTE_REQUIRE(F % 32 == 0 && d % 8 == 0, "dense_swiglu: F %% 32 and d %% 8 must be 0");
   {
     // dZ = dout @ W_down^T: B(n=f, k=dcol) = wd[dcol][f] (layout T) or wd[f][dcol] (layout N)
@@ -387,7 +391,7 @@ int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, c
     p.epi.ldc = d;
     p.epi.c_f32 = 1;
     p.epi.c_ilv = F;
-    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
   }
   {
     GemmArgs p;
@@ -411,7 +415,7 @@ int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, c
       p.b = plain(z, F);
       p.epi.ldc = F;
     }
-    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
   }
   return 0;
 }
@@ -440,7 +444,8 @@ int rte_qkv_rope_fwd(const void* x, const void* wqkv, const float* cos_t, const 
 
 int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const int64_t* sk, const void* dv,
                      const int64_t* sv, const void* x, const void* wqkv, const float* cos_t, const float* sin_t,
-                     int B, int S_, int H, int hd, void* dqkv, void* dx, float* dw, void* stream) {
+                     int B, int S_, int H, int hd, void* dqkv, void* dx, float* dw, void* workspace,
+                     size_t workspace_bytes, void* stream) {
   const int d = H * hd;
   const int T = B * S_;
   RTE_TRY(rope_bwd_pack(B16(dq), sq, B16(dk), sk, B16(dv), sv, cos_t, sin_t, B, H, S_, hd, B16(dqkv),
@@ -471,7 +476,7 @@ int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const in
     p.epi.c = dw;
     p.epi.ldc = d;
     p.epi.c_f32 = 1;
-    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
   }
   return 0;
 }

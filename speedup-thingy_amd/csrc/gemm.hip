@@ -4,9 +4,12 @@
 // walks k in steps of BK through double-buffered LDS.  Global tiles are fetched
 // into registers one step ahead (16-byte loads), then written to LDS in a
 // k-contiguous layout [row][BK+8] so every MFMA operand fetch is one 16-byte LDS
-// read per lane.  Operands whose output index is contiguous in memory (layout T)
-// are loaded as 4(k) x 8(i) blocks and transposed in registers before the LDS
-// write, so weight gradients (reduction over tokens) need no transposed copies.
+// read per lane (rows 36 dwords apart: 8 consecutive rows hit disjoint banks).
+// Operands whose output index is contiguous in memory (layout T) are loaded as
+// 4(k) x 8(i) blocks and transposed in registers before the LDS write; threads
+// walk k fastest there so each 8-byte LDS write wave touches every bank twice.
+// Row addresses of layout-N operands are resolved once per tile; the loop only
+// advances k.  Results leave through LDS so every global store is 16 bytes.
 //
 // MFMA lane layout used below (32x32x16): lane l supplies A row (l % 32) and
 // B column (l % 32) with 8 consecutive k values starting at 8*(l / 32); output
@@ -15,104 +18,232 @@
 // mapping has to match the hardware; the GPU parity tests pin it.
 #include "gemm.hpp"
 
-#include <stdarg.h>
 #include <stdio.h>
 
 namespace rte {
 
 namespace {
 
+constexpr int kThreads = 256;
+
 __device__ __forceinline__ int64_t ilv_row(int64_t r, int32_t half) {
   return ((r & 63) < 32 ? 0 : half) + (r >> 6) * 32 + (r & 31);
 }
 
+__device__ __forceinline__ int log2i(int v) { return 31 - __clz(v); }
+
 __device__ __forceinline__ int64_t row_off(const Operand& o, int64_t r) {
   if (o.ilv) r = ilv_row(r, o.ilv);
   if (o.rows) r = o.rows[r];
-  if (o.rdiv) return (r / o.rdiv) * o.rs_hi + (r % o.rdiv) * o.ld;
+  if (o.rdiv) return (r >> log2i(o.rdiv)) * o.rs_hi + (r & (o.rdiv - 1)) * o.ld;
   return r * o.ld;
 }
 
 __device__ __forceinline__ int64_t col_off(const Operand& o, int c) {
-  if (o.cdiv) return (int64_t)(c / o.cdiv) * o.cs_hi + (c % o.cdiv);
+  if (o.cdiv) return (int64_t)(c >> log2i(o.cdiv)) * o.cs_hi + (c & (o.cdiv - 1));
   return c;
 }
 
-template <int R, int BK, bool T>
-struct TileLoader {
-  static constexpr int LDP = BK + 8;
-  static constexpr int UNITS = T ? (R / 8) * (BK / 4) : R * (BK / 8);
-  static constexpr int PER = (UNITS + 255) / 256;
-  static constexpr int NREG = T ? PER * 4 : PER;
-  uint4 r[NREG];
+// ------------------------------------------------------------------ loaders
 
-  // i: output-index tile origin (m or n), ilim: its bound; k0/klim: reduction range.
-  __device__ __forceinline__ void load(const Operand& o, const bf16* base, int64_t rowshift, int i0,
-                                       int ilim, int k0, int klim, int tid) {
+template <int R, int BK>
+struct LoaderN {
+  static constexpr int LDP = BK + 8;
+  static constexpr int CPR = BK / 8;
+  static constexpr int UNITS = R * CPR;
+  static constexpr int PER = (UNITS + kThreads - 1) / kThreads;
+  const bf16* rowp[PER];
+  bool ok[PER];
+  uint4 r[PER];
+
+  __device__ __forceinline__ void init(const Operand& o, const bf16* base, int64_t rowshift, int i0, int ilim,
+                                       int tid) {
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
-      const int q = tid + u * 256;
-      if (T) {
-        const int mb = q % (R / 8), kb = q / (R / 8);
-        const int i = i0 + mb * 8;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int k = k0 + kb * 4 + j;
-          uint4 v = make_uint4(0u, 0u, 0u, 0u);
-          if (q < UNITS && i < ilim && k < klim)
-            v = *reinterpret_cast<const uint4*>(base + row_off(o, k + rowshift) + col_off(o, i));
-          r[u * 4 + j] = v;
-        }
-      } else {
-        const int rr = q / (BK / 8), kc = q % (BK / 8);
-        const int i = i0 + rr, k = k0 + kc * 8;
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (q < UNITS && i < ilim && k < klim)
-          v = *reinterpret_cast<const uint4*>(base + row_off(o, i + rowshift) + col_off(o, k));
-        r[u] = v;
-      }
+      const int q = tid + u * kThreads;
+      const int i = i0 + q / CPR;
+      ok[u] = q < UNITS && i < ilim;
+      rowp[u] = ok[u] ? base + row_off(o, i + rowshift) : base;
     }
   }
-
-  __device__ __forceinline__ static uint32_t lo2(uint32_t a, uint32_t b) {
-    return (a & 0xffffu) | (b << 16);
+  __device__ __forceinline__ void load(const Operand& o, int k0, int klim, int tid) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int q = tid + u * kThreads;
+      const int k = k0 + (q % CPR) * 8;
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (ok[u] && k < klim) v = *reinterpret_cast<const uint4*>(rowp[u] + col_off(o, k));
+      r[u] = v;
+    }
   }
-  __device__ __forceinline__ static uint32_t hi2(uint32_t a, uint32_t b) {
-    return (a >> 16) | (b & 0xffff0000u);
-  }
-
   __device__ __forceinline__ void store(bf16* lds, int tid) const {
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
-      const int q = tid + u * 256;
+      const int q = tid + u * kThreads;
       if (q >= UNITS) continue;
-      if (T) {
-        const int mb = q % (R / 8), kb = q / (R / 8);
-        const uint4 a = r[u * 4 + 0], b = r[u * 4 + 1], c = r[u * 4 + 2], d = r[u * 4 + 3];
-        const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
-        const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
-        const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
-        const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
+      *reinterpret_cast<uint4*>(lds + (q / CPR) * LDP + (q % CPR) * 8) = r[u];
+    }
+  }
+};
+
+template <int R, int BK>
+struct LoaderT {
+  static constexpr int LDP = BK + 8;
+  static constexpr int KB = BK / 4;
+  static constexpr int UNITS = (R / 8) * KB;
+  static constexpr int PER = (UNITS + kThreads - 1) / kThreads;
+  int64_t coff[PER];
+  bool ok[PER];
+  uint4 r[PER * 4];
+
+  __device__ __forceinline__ void init(const Operand& o, const bf16*, int64_t, int i0, int ilim, int tid) {
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          uint2 e, f;
-          e.x = lo2(aw[w], bw[w]);
-          e.y = lo2(cw[w], dw[w]);
-          f.x = hi2(aw[w], bw[w]);
-          f.y = hi2(cw[w], dw[w]);
-          *reinterpret_cast<uint2*>(lds + (mb * 8 + 2 * w) * LDP + kb * 4) = e;
-          *reinterpret_cast<uint2*>(lds + (mb * 8 + 2 * w + 1) * LDP + kb * 4) = f;
-        }
-      } else {
-        const int rr = q / (BK / 8), kc = q % (BK / 8);
-        *reinterpret_cast<uint4*>(lds + rr * LDP + kc * 8) = r[u];
+    for (int u = 0; u < PER; ++u) {
+      const int q = tid + u * kThreads;
+      const int i = i0 + (q / KB) * 8;
+      ok[u] = q < UNITS && i < ilim;
+      coff[u] = ok[u] ? col_off(o, i) : 0;
+    }
+  }
+  __device__ __forceinline__ void load(const Operand& o, const bf16* base, int64_t rowshift, int k0, int klim,
+                                       int tid) {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int q = tid + u * kThreads;
+      const int kb = q % KB;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k = k0 + kb * 4 + j;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (ok[u] && k < klim) v = *reinterpret_cast<const uint4*>(base + row_off(o, k + rowshift) + coff[u]);
+        r[u * 4 + j] = v;
+      }
+    }
+  }
+  __device__ __forceinline__ static uint32_t lo2(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }
+  __device__ __forceinline__ static uint32_t hi2(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xffff0000u); }
+  __device__ __forceinline__ void store(bf16* lds, int tid) const {
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+      const int q = tid + u * kThreads;
+      if (q >= UNITS) continue;
+      const int kb = q % KB, mb = q / KB;
+      const uint4 a = r[u * 4 + 0], b = r[u * 4 + 1], c = r[u * 4 + 2], d = r[u * 4 + 3];
+      const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
+      const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
+      const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+      const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        uint2 e, f;
+        e.x = lo2(aw[w], bw[w]);
+        e.y = lo2(cw[w], dw[w]);
+        f.x = hi2(aw[w], bw[w]);
+        f.y = hi2(cw[w], dw[w]);
+        *reinterpret_cast<uint2*>(lds + (mb * 8 + 2 * w) * LDP + kb * 4) = e;
+        *reinterpret_cast<uint2*>(lds + (mb * 8 + 2 * w + 1) * LDP + kb * 4) = f;
       }
     }
   }
 };
 
+// Uniform interface over the two loaders.
+template <int R, int BK, bool T>
+struct Loader;
+template <int R, int BK>
+struct Loader<R, BK, false> {
+  LoaderN<R, BK> l;
+  __device__ __forceinline__ void init(const Operand& o, const bf16* base, int64_t sh, int i0, int ilim, int tid) {
+    l.init(o, base, sh, i0, ilim, tid);
+  }
+  __device__ __forceinline__ void load(const Operand& o, const bf16*, int64_t, int k0, int klim, int tid) {
+    l.load(o, k0, klim, tid);
+  }
+  __device__ __forceinline__ void store(bf16* lds, int tid) const { l.store(lds, tid); }
+};
+template <int R, int BK>
+struct Loader<R, BK, true> {
+  LoaderT<R, BK> l;
+  __device__ __forceinline__ void init(const Operand& o, const bf16* base, int64_t sh, int i0, int ilim, int tid) {
+    l.init(o, base, sh, i0, ilim, tid);
+  }
+  __device__ __forceinline__ void load(const Operand& o, const bf16* base, int64_t sh, int k0, int klim, int tid) {
+    l.load(o, base, sh, k0, klim, tid);
+  }
+  __device__ __forceinline__ void store(bf16* lds, int tid) const { l.store(lds, tid); }
+};
+
+// ------------------------------------------------------------------ output chunks
+
+// Writes W consecutive outputs (row m of the tile space, columns n..n+W-1) applying
+// alpha, row_scale, output-row mapping, residual and beta.  vec: 16-byte path allowed.
+template <int W>
+__device__ __forceinline__ void store_chunk(const Epilogue& e, int g, int m, int n, int N, float* v, bool vec) {
+  const float rs = e.row_scale ? e.row_scale[m] : 1.0f;
+  int64_t orow = m + (int64_t)g * e.c_growstride;
+  if (e.c_ilv) orow = ilv_row(orow, e.c_ilv);
+  if (e.c_rows) orow = e.c_rows[orow];
+  const int nv = N - n < W ? N - n : W;
+#pragma unroll
+  for (int t = 0; t < W; ++t) v[t] *= e.alpha * rs;
+  if (e.resid) {
+    const float* rp = e.resid + orow * e.ld_resid + n;
+    if (vec && nv == W) {
+#pragma unroll
+      for (int t = 0; t < W; t += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(rp + t);
+        v[t] += x.x; v[t + 1] += x.y; v[t + 2] += x.z; v[t + 3] += x.w;
+      }
+    } else {
+      for (int t = 0; t < nv; ++t) v[t] += rp[t];
+    }
+  }
+  if (e.c_f32) {
+    float* cp = reinterpret_cast<float*>(e.c) + (int64_t)g * e.c_gstride + orow * e.ldc + n;
+    if (vec && nv == W) {
+#pragma unroll
+      for (int t = 0; t < W; t += 4) {
+        if (e.beta != 0.0f) {
+          const float4 o = *reinterpret_cast<const float4*>(cp + t);
+          v[t] += e.beta * o.x; v[t + 1] += e.beta * o.y; v[t + 2] += e.beta * o.z; v[t + 3] += e.beta * o.w;
+        }
+        *reinterpret_cast<float4*>(cp + t) = make_float4(v[t], v[t + 1], v[t + 2], v[t + 3]);
+      }
+    } else {
+      for (int t = 0; t < nv; ++t) cp[t] = v[t] + (e.beta != 0.0f ? e.beta * cp[t] : 0.0f);
+    }
+  } else {
+    bf16* cp = reinterpret_cast<bf16*>(e.c) + (int64_t)g * e.c_gstride + orow * e.ldc + n;
+    if (vec && nv == W && W == 8) {
+      if (e.beta != 0.0f) {
+        const uint4 o = *reinterpret_cast<const uint4*>(cp);
+        const uint32_t ow[4] = {o.x, o.y, o.z, o.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          v[2 * t] += e.beta * __uint_as_float(ow[t] << 16);
+          v[2 * t + 1] += e.beta * __uint_as_float(ow[t] & 0xffff0000u);
+        }
+      }
+      uint4 o;
+      o.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+      o.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+      o.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
+      o.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+      *reinterpret_cast<uint4*>(cp) = o;
+    } else {
+      for (int t = 0; t < nv; ++t) cp[t] = f2bf(v[t] + (e.beta != 0.0f ? e.beta * bf2f(cp[t]) : 0.0f));
+    }
+  }
+}
+
+struct EpiFlags {
+  int vec;  // 16-byte stores / residual loads are aligned
+};
+
+// ------------------------------------------------------------------ kernel
+
 template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI>
-__global__ void __launch_bounds__(256) gemm_kernel(GemmArgs p) {
+__global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
   constexpr int LDP = BK + 8;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -129,7 +260,7 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs p) {
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  int g = 0, m0 = 0, n0 = 0, mlim = p.M, kbeg = 0, kend = p.K;
+  int g = 0, m0 = 0, n0 = 0, mlim = p.M, kbeg = 0, kend = p.K, split = 0;
   if (p.mode == MODE_GROUP_M) {
     if (tid < 64) {
       if (tid == 0) s_tile[0] = -1;
@@ -156,9 +287,8 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs p) {
     __syncthreads();
     g = s_tile[0];
     if (g < 0) return;
-    const int gb = p.goff[g];
     mlim = p.goff[g + 1];
-    m0 = gb + s_tile[1] * BM;
+    m0 = p.goff[g] + s_tile[1] * BM;
     n0 = blockIdx.y * BN;
   } else if (p.mode == MODE_GROUP_K) {
     g = blockIdx.z;
@@ -174,6 +304,11 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs p) {
     if ((total & 7) == 0) lin = (lin & 7) * (total >> 3) + (lin >> 3);
     m0 = (lin / gy) * BM;
     n0 = (lin % gy) * BN;
+    if (p.splits > 1) {
+      split = blockIdx.z;
+      kbeg = split * p.k_chunk;
+      kend = kbeg + p.k_chunk < p.K ? kbeg + p.k_chunk : p.K;
+    }
   }
 
   const bf16* abase = p.a.ptr + (int64_t)g * p.a.gstride;
@@ -189,12 +324,14 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  TileLoader<BM, BK, AT> la;
-  TileLoader<BN, BK, BT> lb;
+  Loader<BM, BK, AT> la;
+  Loader<BN, BK, BT> lb;
+  la.init(p.a, abase, ashift, m0, mlim, tid);
+  lb.init(p.b, bbase, bshift, n0, p.N, tid);
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
   if (nk > 0) {
-    la.load(p.a, abase, ashift, m0, mlim, kbeg, kend, tid);
-    lb.load(p.b, bbase, bshift, n0, p.N, kbeg, kend, tid);
+    la.load(p.a, abase, ashift, kbeg, kend, tid);
+    lb.load(p.b, bbase, bshift, kbeg, kend, tid);
     la.store(As[0], tid);
     lb.store(Bs[0], tid);
   }
@@ -205,8 +342,8 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs p) {
     const bool more = kt + 1 < nk;
     if (more) {
       const int k0 = kbeg + (kt + 1) * BK;
-      la.load(p.a, abase, ashift, m0, mlim, k0, kend, tid);
-      lb.load(p.b, bbase, bshift, n0, p.N, k0, kend, tid);
+      la.load(p.a, abase, ashift, k0, kend, tid);
+      lb.load(p.b, bbase, bshift, k0, kend, tid);
     }
     const bf16* a_s = As[cur];
     const bf16* b_s = Bs[cur];
@@ -233,92 +370,146 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs p) {
     __syncthreads();
   }
 
-  // ---------------------------------------------------------------- epilogues
+  // ---------------------------------------------------------------- epilogues (LDS staged)
   const Epilogue& e = p.epi;
-  const int mw = m0 + wm * WTM + (lane >> 5) * 4;
-  const int nw = n0 + wn * WTN + (lane & 31);
+  const int rbase = wm * WTM + (lane >> 5) * 4;  // + i*32 + (r>>2)*8 + (r&3)
+  const int cbase = wn * WTN + (lane & 31);      // + j*32
 
   if constexpr (EPI == EPI_STORE) {
-    char* cbase = reinterpret_cast<char*>(e.c) +
-                  (int64_t)g * e.c_gstride * (e.c_f32 ? 4 : 2);
-    const int64_t crow_shift = (int64_t)g * e.c_growstride;
+    constexpr int CP = BN + 8;
+    float* Cs = reinterpret_cast<float*>(smem_raw);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = mw + i * 32 + (r >> 2) * 8 + (r & 3);
-        if (m >= mlim) continue;
-        const float rs = e.row_scale ? e.row_scale[m] : 1.0f;
-        int64_t orow = m + crow_shift;
-        if (e.c_ilv) orow = ilv_row(orow, e.c_ilv);
-        if (e.c_rows) orow = e.c_rows[orow];
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const int n = nw + j * 32;
-          if (n >= p.N) continue;
-          float v = acc[i][j][r] * e.alpha * rs;
-          if (e.resid) v += e.resid[orow * e.ld_resid + n];
-          if (e.c_f32) {
-            float* cp = reinterpret_cast<float*>(cbase) + orow * e.ldc + n;
-            if (e.beta != 0.0f) v += e.beta * *cp;
-            *cp = v;
-          } else {
-            bf16* cp = reinterpret_cast<bf16*>(cbase) + orow * e.ldc + n;
-            if (e.beta != 0.0f) v += e.beta * bf2f(*cp);
-            *cp = f2bf(v);
-          }
+        for (int r = 0; r < 16; ++r)
+          Cs[(rbase + i * 32 + (r >> 2) * 8 + (r & 3)) * CP + cbase + j * 32] = acc[i][j][r];
+    __syncthreads();
+    if (p.splits > 1) {
+      // fp32 partial of this k range, plain [M, N]
+      float* ws = p.splitk_ws + (int64_t)split * p.M * p.N;
+      constexpr int CH = BN / 4;
+      for (int c = tid; c < BM * CH; c += kThreads) {
+        const int row = c / CH, cc = (c % CH) * 4;
+        const int m = m0 + row, n = n0 + cc;
+        if (m >= mlim || n >= p.N) continue;
+        const float* src = Cs + row * CP + cc;
+        float* dst = ws + (int64_t)m * p.N + n;
+        if (fl.vec && n + 4 <= p.N) {
+          *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(src);
+        } else {
+          for (int t = 0; t < 4 && n + t < p.N; ++t) dst[t] = src[t];
         }
       }
+    } else if (e.c_f32) {
+      constexpr int CH = BN / 4;
+      for (int c = tid; c < BM * CH; c += kThreads) {
+        const int row = c / CH, cc = (c % CH) * 4;
+        const int m = m0 + row, n = n0 + cc;
+        if (m >= mlim || n >= p.N) continue;
+        float v[4];
+        const float4 x = *reinterpret_cast<const float4*>(Cs + row * CP + cc);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+        store_chunk<4>(e, g, m, n, p.N, v, fl.vec);
+      }
+    } else {
+      constexpr int CH = BN / 8;
+      for (int c = tid; c < BM * CH; c += kThreads) {
+        const int row = c / CH, cc = (c % CH) * 8;
+        const int m = m0 + row, n = n0 + cc;
+        if (m >= mlim || n >= p.N) continue;
+        float v[8];
+        const float4 x = *reinterpret_cast<const float4*>(Cs + row * CP + cc);
+        const float4 y = *reinterpret_cast<const float4*>(Cs + row * CP + cc + 4);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+        v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+        store_chunk<8>(e, g, m, n, p.N, v, fl.vec);
+      }
+    }
   } else if constexpr (EPI == EPI_SWIGLU_FWD) {
     // Column blocks of 32 alternate up / gate for the same 32 neurons, so the
     // up value and its gate sit in the same register of neighbouring blocks.
     static_assert(TN % 2 == 0, "SwiGLU epilogue pairs column blocks");
+    constexpr int HP = BN + 8, ZP = BN / 2 + 8;
+    bf16* Us = smem;
+    bf16* Zs = smem + BM * HP;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = mw + i * 32 + (r >> 2) * 8 + (r & 3);
-        if (m >= mlim) continue;
-        const float rs = e.row_scale ? e.row_scale[m] : 1.0f;
+        const int rl = rbase + i * 32 + (r >> 2) * 8 + (r & 3);
+        const int m = m0 + rl;
+        const float rs = (e.row_scale && m < mlim) ? e.row_scale[m] : 1.0f;
 #pragma unroll
         for (int jp = 0; jp < TN / 2; ++jp) {
-          const int ncol = nw + jp * 64;  // up column in the interleaved layout
-          if (ncol >= p.N) continue;
+          const int cl = cbase + jp * 64;  // up column (tile-local)
           const bf16 ub = f2bf(acc[i][2 * jp][r]);
           const bf16 gb = f2bf(acc[i][2 * jp + 1][r]);
           const float up = bf2f(ub), gt = bf2f(gb);
-          const float zval = up * gt * sigmoidf_(gt) * rs;
-          e.ug[(int64_t)m * e.ld_ug + ncol] = ub;
-          e.ug[(int64_t)m * e.ld_ug + ncol + 32] = gb;
-          const int neuron = (ncol >> 6) * 32 + (ncol & 31);
-          e.z[(int64_t)m * e.ld_z + neuron] = f2bf(zval);
+          Us[rl * HP + cl] = ub;
+          Us[rl * HP + cl + 32] = gb;
+          Zs[rl * ZP + (cl >> 6) * 32 + (cl & 31)] = f2bf(up * gt * sigmoidf_(gt) * rs);
         }
       }
+    __syncthreads();
+    {
+      constexpr int CH = BN / 8;
+      for (int c = tid; c < BM * CH; c += kThreads) {
+        const int row = c / CH, cc = (c % CH) * 8;
+        const int m = m0 + row, n = n0 + cc;
+        if (m >= mlim || n >= p.N) continue;
+        *reinterpret_cast<uint4*>(e.ug + (int64_t)m * e.ld_ug + n) = *reinterpret_cast<const uint4*>(Us + row * HP + cc);
+      }
+    }
+    {
+      constexpr int CH = BN / 16;
+      for (int c = tid; c < BM * CH; c += kThreads) {
+        const int row = c / CH, cc = (c % CH) * 8;
+        const int m = m0 + row, nz = n0 / 2 + cc;
+        if (m >= mlim || nz >= p.N / 2) continue;
+        *reinterpret_cast<uint4*>(e.z + (int64_t)m * e.ld_z + nz) = *reinterpret_cast<const uint4*>(Zs + row * ZP + cc);
+      }
+    }
   } else if constexpr (EPI == EPI_SWIGLU_BWD) {
     static_assert(WN == 1, "row reduction needs the whole N range in one wave");
+    // UG tile of this block: rows m0.., columns [(n0/32)*64, +2*BN) of the interleaved layout
+    constexpr int HP = 2 * BN + 8;
+    bf16* Us = smem;
+    const int64_t ucol0 = (int64_t)(n0 >> 5) * 64;
+    const int ucols = 2 * (p.N - n0 < BN ? p.N - n0 : BN);
+    {
+      constexpr int CH = 2 * BN / 8;
+      for (int c = tid; c < BM * CH; c += kThreads) {
+        const int row = c / CH, cc = (c % CH) * 8;
+        const int m = m0 + row;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (m < mlim && cc < ucols) v = *reinterpret_cast<const uint4*>(e.ug_in + (int64_t)m * e.ld_ug + ucol0 + cc);
+        *reinterpret_cast<uint4*>(Us + row * HP + cc) = v;
+      }
+    }
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = mw + i * 32 + (r >> 2) * 8 + (r & 3);
+        const int rl = rbase + i * 32 + (r >> 2) * 8 + (r & 3);
+        const int m = m0 + rl;
         const bool mok = m < mlim;
         const float rs = (mok && e.row_scale) ? e.row_scale[m] : 1.0f;
         float part = 0.0f;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          const int n = nw + j * 32;  // neuron index
-          if (!mok || n >= p.N) continue;
-          const int col = (n >> 5) * 64 + (n & 31);
-          const float up = bf2f(e.ug_in[(int64_t)m * e.ld_ug + col]);
-          const float gt = bf2f(e.ug_in[(int64_t)m * e.ld_ug + col + 32]);
+          const int nl = cbase + j * 32;  // tile-local neuron
+          const int cl = (nl >> 5) * 64 + (nl & 31);
+          const float up = bf2f(Us[rl * HP + cl]);
+          const float gt = bf2f(Us[rl * HP + cl + 32]);
           const float s = sigmoidf_(gt);
           const float silu = gt * s;
           const float draw = acc[i][j][r];
           const float dz = draw * rs;
-          const float dup = dz * silu;
-          const float dgt = dz * up * s * (1.0f + gt * (1.0f - s));
-          e.ug[(int64_t)m * e.ld_ug + col] = f2bf(dup);
-          e.ug[(int64_t)m * e.ld_ug + col + 32] = f2bf(dgt);
+          Us[rl * HP + cl] = f2bf(dz * silu);
+          Us[rl * HP + cl + 32] = f2bf(dz * up * s * (1.0f + gt * (1.0f - s)));
           part += up * silu * draw;
         }
         if (e.dw_row) {
@@ -327,41 +518,92 @@ __global__ void __launch_bounds__(256) gemm_kernel(GemmArgs p) {
           if ((lane & 31) == 0 && mok) e.dw_row[m] = part;
         }
       }
+    __syncthreads();
+    {
+      constexpr int CH = 2 * BN / 8;
+      for (int c = tid; c < BM * CH; c += kThreads) {
+        const int row = c / CH, cc = (c % CH) * 8;
+        const int m = m0 + row;
+        if (m >= mlim || cc >= ucols) continue;
+        *reinterpret_cast<uint4*>(e.ug + (int64_t)m * e.ld_ug + ucol0 + cc) =
+            *reinterpret_cast<const uint4*>(Us + row * HP + cc);
+      }
+    }
   } else if constexpr (EPI == EPI_ROPE_QKV) {
+    constexpr int HP = BN + 8;
+    bf16* Hs = smem;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = mw + i * 32 + (r >> 2) * 8 + (r & 3);
+        const int rl = rbase + i * 32 + (r >> 2) * 8 + (r & 3);
+        const int m = m0 + rl;
+        const int s = m % e.S;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          const int n = nw + j * 32;
+          const int n = n0 + cbase + j * 32;
           const float x = acc[i][j][r];
           const float partner = __shfl_xor(x, 1, 64);
-          if (m >= mlim || n >= p.N) continue;
-          const int part = n / e.dmodel;
-          const int within = n - part * e.dmodel;
-          const int h = within / e.hd;
-          const int dim = within - h * e.hd;
-          const int b = m / e.S;
-          const int s = m - b * e.S;
           float y = x;
-          if (part < 2) {
+          if (n < 2 * e.dmodel && m < mlim) {
+            const int dim = n % e.hd;
             const float c = e.cos_t[(int64_t)s * e.hd + dim];
             const float sn = e.sin_t[(int64_t)s * e.hd + dim];
             y = (dim & 1) ? (x * c + partner * sn) : (x * c - partner * sn);
           }
-          bf16* dst = part == 0 ? e.q : (part == 1 ? e.k : e.v);
-          dst[(((int64_t)b * e.H + h) * e.S + s) * e.hd + dim] = f2bf(y);
+          Hs[rl * HP + cbase + j * 32] = f2bf(y);
         }
       }
+    __syncthreads();
+    constexpr int CH = BN / 8;
+    for (int c = tid; c < BM * CH; c += kThreads) {
+      const int row = c / CH, cc = (c % CH) * 8;
+      const int m = m0 + row, n = n0 + cc;
+      if (m >= mlim || n >= p.N) continue;
+      const int part = n / e.dmodel;
+      const int within = n - part * e.dmodel;
+      const int h = within / e.hd, dim = within - h * e.hd;
+      const int b = m / e.S, s = m - b * e.S;
+      bf16* dst = part == 0 ? e.q : (part == 1 ? e.k : e.v);
+      *reinterpret_cast<uint4*>(dst + (((int64_t)b * e.H + h) * e.S + s) * e.hd + dim) =
+          *reinterpret_cast<const uint4*>(Hs + row * HP + cc);
+    }
   }
 }
 
+// Sums split-K partials in split order and applies the EPI_STORE epilogue.
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs p, EpiFlags fl) {
+  const int chunks = (p.N + 3) / 4;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)p.M * chunks) return;
+  const int m = (int)(idx / chunks), n = (int)(idx % chunks) * 4;
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t plane = (int64_t)p.M * p.N;
+  for (int s = 0; s < p.splits; ++s) {
+    const float* src = p.splitk_ws + s * plane + (int64_t)m * p.N + n;
+    if (fl.vec && n + 4 <= p.N) {
+      const float4 x = *reinterpret_cast<const float4*>(src);
+      v[0] += x.x; v[1] += x.y; v[2] += x.z; v[3] += x.w;
+    } else {
+      for (int t = 0; t < 4 && n + t < p.N; ++t) v[t] += src[t];
+    }
+  }
+  store_chunk<4>(p.epi, 0, m, n, p.N, v, fl.vec);
+}
+
+template <int BM, int BN, int BK, int EPI>
+constexpr size_t lds_bytes() {
+  constexpr size_t main_loop = (size_t)2 * (BM + BN) * (BK + 8) * 2;
+  constexpr size_t epi = EPI == EPI_STORE        ? (size_t)BM * (BN + 8) * 4
+                         : EPI == EPI_SWIGLU_FWD ? (size_t)BM * (BN + 8) * 2 + (size_t)BM * (BN / 2 + 8) * 2
+                         : EPI == EPI_SWIGLU_BWD ? (size_t)BM * (2 * BN + 8) * 2
+                                                 : (size_t)BM * (BN + 8) * 2;
+  return main_loop > epi ? main_loop : epi;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI>
-int launch_cfg(const GemmArgs& p, hipStream_t stream) {
-  constexpr int LDP = BK + 8;
-  constexpr size_t lds = (size_t)2 * (BM + BN) * LDP * sizeof(bf16);
+int launch_cfg(const GemmArgs& p0, hipStream_t stream, void* ws, size_t ws_bytes, int vec) {
+  constexpr size_t lds = lds_bytes<BM, BN, BK, EPI>();
   auto fn = gemm_kernel<BM, BN, BK, WM, WN, AT, BT, EPI>;
   static bool attr_done = false;
   if (!attr_done) {
@@ -375,6 +617,8 @@ int launch_cfg(const GemmArgs& p, hipStream_t stream) {
     }
     attr_done = true;
   }
+  GemmArgs p = p0;
+  EpiFlags fl{vec};
   dim3 grid;
   if (p.mode == MODE_GROUP_M) {
     grid = dim3(p.max_tiles_m, (p.N + BN - 1) / BN, 1);
@@ -382,23 +626,58 @@ int launch_cfg(const GemmArgs& p, hipStream_t stream) {
     grid = dim3((p.M + BM - 1) / BM, (p.N + BN - 1) / BN, p.G);
   } else {
     grid = dim3((p.M + BM - 1) / BM, (p.N + BN - 1) / BN, 1);
+    // split the reduction when the tile grid cannot fill the GPU
+    const int tiles = (int)(grid.x * grid.y);
+    p.splits = 1;
+    if (EPI == EPI_STORE && ws && tiles < 256 && p.K >= 1024) {
+      int splits = (512 + tiles - 1) / tiles;
+      const int max_by_k = p.K / 512;
+      if (splits > max_by_k) splits = max_by_k;
+      if (splits > 16) splits = 16;
+      while (splits > 1 && (size_t)splits * p.M * p.N * sizeof(float) > ws_bytes) --splits;
+      if (splits > 1) {
+        int kc = (p.K + splits - 1) / splits;
+        kc = (kc + BK - 1) / BK * BK;
+        p.k_chunk = kc;
+        p.splits = (p.K + kc - 1) / kc;
+        p.splitk_ws = static_cast<float*>(ws);
+        grid.z = p.splits;
+      }
+    }
   }
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return 0;
-  hipLaunchKernelGGL(fn, grid, dim3(256), lds, stream, p);
-  return check_launch("gemm");
+  hipLaunchKernelGGL(fn, grid, dim3(kThreads), lds, stream, p, fl);
+  RTE_TRY(check_launch("gemm"));
+  if (p.splits > 1) {
+    const int64_t n = (int64_t)p.M * ((p.N + 3) / 4);
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p, fl);
+    RTE_TRY(check_launch("gemm_splitk_reduce"));
+  }
+  return 0;
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int EPI>
-int launch_layouts(const GemmArgs& p, hipStream_t stream) {
-  if (!p.a_t && !p.b_t) return launch_cfg<BM, BN, BK, WM, WN, false, false, EPI>(p, stream);
-  if (!p.a_t && p.b_t) return launch_cfg<BM, BN, BK, WM, WN, false, true, EPI>(p, stream);
-  if (p.a_t && !p.b_t) return launch_cfg<BM, BN, BK, WM, WN, true, false, EPI>(p, stream);
-  return launch_cfg<BM, BN, BK, WM, WN, true, true, EPI>(p, stream);
+int launch_layouts(const GemmArgs& p, hipStream_t stream, void* ws, size_t ws_bytes, int vec) {
+  if (!p.a_t && !p.b_t) return launch_cfg<BM, BN, BK, WM, WN, false, false, EPI>(p, stream, ws, ws_bytes, vec);
+  if (!p.a_t && p.b_t) return launch_cfg<BM, BN, BK, WM, WN, false, true, EPI>(p, stream, ws, ws_bytes, vec);
+  if (p.a_t && !p.b_t) return launch_cfg<BM, BN, BK, WM, WN, true, false, EPI>(p, stream, ws, ws_bytes, vec);
+  return launch_cfg<BM, BN, BK, WM, WN, true, true, EPI>(p, stream, ws, ws_bytes, vec);
 }
+
+bool pow2_or_zero(int v) { return v == 0 || (v > 0 && (v & (v - 1)) == 0); }
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 }  // namespace
 
-int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream) {
+size_t gemm_splitk_bytes(int M, int N, int K) {
+  int splits = K / 512;
+  if (splits > 16) splits = 16;
+  if (splits < 2) return 0;
+  return (size_t)splits * M * N * sizeof(float);
+}
+
+int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream, void* ws, size_t ws_bytes) {
   RTE_REQUIRE(p.M >= 0 && p.N >= 0 && p.K >= 0, "gemm: negative size");
   RTE_REQUIRE(p.a.ptr && p.b.ptr, "gemm: null operand");
   // 16-byte vector loads: every contiguous run the kernel reads must hold whole
@@ -407,50 +686,69 @@ int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream) {
   if (!p.b_t) RTE_REQUIRE(p.K % 8 == 0 || p.mode == MODE_GROUP_K, "gemm: K %% 8 != 0 for layout-N B");
   if (p.a_t) RTE_REQUIRE(p.M % 8 == 0, "gemm: M %% 8 != 0 for layout-T A");
   if (p.b_t) RTE_REQUIRE(p.N % 8 == 0, "gemm: N %% 8 != 0 for layout-T B");
-  if (p.mode == MODE_GROUP_K)
-    RTE_REQUIRE(p.a_t && p.b_t, "gemm: GROUP_K needs both operands in layout T");
+  if (p.mode == MODE_GROUP_K) RTE_REQUIRE(p.a_t && p.b_t, "gemm: GROUP_K needs both operands in layout T");
   if (p.mode == MODE_GROUP_M) RTE_REQUIRE(!p.a_t, "gemm: GROUP_M needs layout-N A");
   if (p.mode != MODE_DENSE) RTE_REQUIRE(p.goff && p.G >= 1, "gemm: grouped mode needs offsets");
   for (const Operand* o : {&p.a, &p.b}) {
-    RTE_REQUIRE(((uintptr_t)o->ptr & 15) == 0, "gemm: operand pointer must be 16-byte aligned");
+    RTE_REQUIRE(aligned16(o->ptr), "gemm: operand pointer must be 16-byte aligned");
     RTE_REQUIRE(o->ld % 8 == 0 && o->gstride % 8 == 0 && o->rs_hi % 8 == 0 && o->cs_hi % 8 == 0,
                 "gemm: operand strides must be multiples of 8 elements");
     RTE_REQUIRE(o->cdiv % 8 == 0, "gemm: split column segments must be multiples of 8");
+    RTE_REQUIRE(pow2_or_zero(o->rdiv) && pow2_or_zero(o->cdiv), "gemm: split sizes must be powers of two");
+  }
+  const Epilogue& e = p.epi;
+  int vec = 1;
+  if (epi_kind == EPI_STORE) {
+    RTE_REQUIRE(e.c, "gemm: null output");
+    const int esz = e.c_f32 ? 4 : 2;
+    vec = aligned16(e.c) && (e.ldc * esz) % 16 == 0 && (e.c_gstride * esz) % 16 == 0;
+    if (e.resid) vec = vec && aligned16(e.resid) && e.ld_resid % 4 == 0;
+  } else if (epi_kind == EPI_SWIGLU_FWD) {
+    RTE_REQUIRE(aligned16(e.ug) && aligned16(e.z) && e.ld_ug % 8 == 0 && e.ld_z % 8 == 0,
+                "gemm: SwiGLU outputs must be 16-byte aligned with ld %% 8 == 0");
+  } else if (epi_kind == EPI_SWIGLU_BWD) {
+    RTE_REQUIRE(aligned16(e.ug) && aligned16(e.ug_in) && e.ld_ug % 8 == 0,
+                "gemm: SwiGLU buffers must be 16-byte aligned with ld %% 8 == 0");
+  } else if (epi_kind == EPI_ROPE_QKV) {
+    RTE_REQUIRE(aligned16(e.q) && aligned16(e.k) && aligned16(e.v) && e.hd % 8 == 0,
+                "gemm: QKV outputs must be 16-byte aligned with head_dim %% 8 == 0");
   }
 
   switch (epi_kind) {
     case EPI_STORE:
-      if (p.M <= 32) return launch_layouts<32, 128, 64, 1, 4, EPI_STORE>(p, stream);
-      if (p.M <= 64 && p.mode != MODE_GROUP_M) return launch_layouts<64, 128, 64, 2, 2, EPI_STORE>(p, stream);
-      if (p.N <= 64) return launch_layouts<128, 64, 64, 4, 1, EPI_STORE>(p, stream);
-      if (p.K <= 32 && p.mode != MODE_GROUP_K) return launch_layouts<128, 128, 32, 2, 2, EPI_STORE>(p, stream);
-      return launch_layouts<128, 128, 64, 2, 2, EPI_STORE>(p, stream);
+      if (p.M <= 32) return launch_layouts<32, 128, 64, 1, 4, EPI_STORE>(p, stream, ws, ws_bytes, vec);
+      if (p.M <= 64 && p.mode != MODE_GROUP_M)
+        return launch_layouts<64, 128, 64, 2, 2, EPI_STORE>(p, stream, ws, ws_bytes, vec);
+      if (p.N <= 64) return launch_layouts<128, 64, 64, 4, 1, EPI_STORE>(p, stream, ws, ws_bytes, vec);
+      if (p.K <= 32 && p.mode != MODE_GROUP_K)
+        return launch_layouts<128, 128, 32, 2, 2, EPI_STORE>(p, stream, ws, ws_bytes, vec);
+      return launch_layouts<128, 128, 64, 2, 2, EPI_STORE>(p, stream, ws, ws_bytes, vec);
     case EPI_SWIGLU_FWD:
       RTE_REQUIRE(!p.a_t && !p.b_t, "gemm: SwiGLU forward expects layout-N operands");
       RTE_REQUIRE(p.N % 64 == 0, "gemm: SwiGLU forward needs N %% 64 == 0");
       RTE_REQUIRE(p.epi.ug && p.epi.z, "gemm: SwiGLU forward needs UG and Z outputs");
-      if (p.N == 64) return launch_cfg<128, 64, 64, 4, 1, false, false, EPI_SWIGLU_FWD>(p, stream);
-      return launch_cfg<128, 128, 64, 2, 2, false, false, EPI_SWIGLU_FWD>(p, stream);
+      if (p.N == 64) return launch_cfg<128, 64, 64, 4, 1, false, false, EPI_SWIGLU_FWD>(p, stream, ws, ws_bytes, 1);
+      return launch_cfg<128, 128, 64, 2, 2, false, false, EPI_SWIGLU_FWD>(p, stream, ws, ws_bytes, 1);
     case EPI_SWIGLU_BWD:
       RTE_REQUIRE(!p.a_t, "gemm: SwiGLU backward expects layout-N dY");
       RTE_REQUIRE(p.epi.ug && p.epi.ug_in, "gemm: SwiGLU backward needs UG input and dUG output");
       RTE_REQUIRE(p.N % 32 == 0, "gemm: SwiGLU backward needs N %% 32 == 0");
       if (p.epi.dw_row) RTE_REQUIRE(p.N <= 128, "gemm: per-row reduction supports N <= 128");
       if (p.N <= 32) {
-        return p.b_t ? launch_cfg<128, 32, 64, 4, 1, false, true, EPI_SWIGLU_BWD>(p, stream)
-                     : launch_cfg<128, 32, 64, 4, 1, false, false, EPI_SWIGLU_BWD>(p, stream);
+        return p.b_t ? launch_cfg<128, 32, 64, 4, 1, false, true, EPI_SWIGLU_BWD>(p, stream, ws, ws_bytes, 1)
+                     : launch_cfg<128, 32, 64, 4, 1, false, false, EPI_SWIGLU_BWD>(p, stream, ws, ws_bytes, 1);
       }
       if (p.N <= 64) {
-        return p.b_t ? launch_cfg<128, 64, 64, 4, 1, false, true, EPI_SWIGLU_BWD>(p, stream)
-                     : launch_cfg<128, 64, 64, 4, 1, false, false, EPI_SWIGLU_BWD>(p, stream);
+        return p.b_t ? launch_cfg<128, 64, 64, 4, 1, false, true, EPI_SWIGLU_BWD>(p, stream, ws, ws_bytes, 1)
+                     : launch_cfg<128, 64, 64, 4, 1, false, false, EPI_SWIGLU_BWD>(p, stream, ws, ws_bytes, 1);
       }
-      return p.b_t ? launch_cfg<128, 128, 64, 4, 1, false, true, EPI_SWIGLU_BWD>(p, stream)
-                   : launch_cfg<128, 128, 64, 4, 1, false, false, EPI_SWIGLU_BWD>(p, stream);
+      return p.b_t ? launch_cfg<128, 128, 64, 4, 1, false, true, EPI_SWIGLU_BWD>(p, stream, ws, ws_bytes, 1)
+                   : launch_cfg<128, 128, 64, 4, 1, false, false, EPI_SWIGLU_BWD>(p, stream, ws, ws_bytes, 1);
     case EPI_ROPE_QKV:
       RTE_REQUIRE(!p.a_t && !p.b_t, "gemm: QKV epilogue expects layout-N operands");
       RTE_REQUIRE(p.epi.q && p.epi.k && p.epi.v && p.epi.cos_t && p.epi.sin_t, "gemm: QKV outputs");
       RTE_REQUIRE(p.epi.hd % 2 == 0 && p.epi.dmodel * 3 == p.N, "gemm: QKV shape");
-      return launch_cfg<128, 128, 64, 2, 2, false, false, EPI_ROPE_QKV>(p, stream);
+      return launch_cfg<128, 128, 64, 2, 2, false, false, EPI_ROPE_QKV>(p, stream, ws, ws_bytes, 1);
     default:
       set_error("gemm: unknown epilogue %d", epi_kind);
       return -1;

@@ -7,13 +7,15 @@
 //   layout T : the output index i (m or n) is contiguous elem(i, k) = row(k) + col(i)
 // "row(r)" applies, in order: a per-group row shift, the optional SwiGLU
 // interleave (see Operand::ilv), an optional int32 row indirection (gather), and
-// an optional two-level split (r / rdiv, r % rdiv) so
-// [B,H,S,hd]-strided attention tensors can be read as [B*S, H*hd] matrices.
-// "col(c)" optionally splits c into (c / cdiv, c % cdiv) with a second stride.
+// an optional two-level split (r / rdiv, r % rdiv) so [B,H,S,hd]-strided
+// attention tensors can be read as [B*S, H*hd] matrices.  "col(c)" optionally
+// splits c the same way with a second stride.  Split sizes are powers of two.
 //
 // Grouping (cluster pools): mode GROUP_M gives each group its own contiguous
-// range of m (slots of one cluster) with a device-side tile map; mode GROUP_K
+// range of m (slots of one cluster) with an in-kernel tile map; mode GROUP_K
 // gives each group its own range of k (the per-cluster weight-gradient reduction).
+// Dense problems with few output tiles and a long reduction are split along k
+// into fp32 partials that a second kernel sums in a fixed order (deterministic).
 #pragma once
 
 #include "common.hpp"
@@ -27,9 +29,9 @@ struct Operand {
   int64_t gstride = 0;            // element offset per group
   int64_t growstride = 0;         // row-index offset per group (before indirection)
   int32_t ilv = 0;                // >0: SwiGLU interleave, row r -> (r%64<32 ? 0 : ilv) + (r/64)*32 + r%32
-  int32_t rdiv = 0;               // 0: plain rows, else row r -> (r/rdiv)*rs_hi + (r%rdiv)*ld
+  int32_t rdiv = 0;               // 0: plain rows, else (power of 2) row r -> (r/rdiv)*rs_hi + (r%rdiv)*ld
   int64_t rs_hi = 0;
-  int32_t cdiv = 0;               // 0: plain cols, else col c -> (c/cdiv)*cs_hi + c%cdiv
+  int32_t cdiv = 0;               // 0: plain cols, else (power of 2) col c -> (c/cdiv)*cs_hi + c%cdiv
   int64_t cs_hi = 0;
 };
 
@@ -56,8 +58,8 @@ struct Epilogue {
   const float* resid = nullptr;      // fp32, indexed like C
   int64_t ld_resid = 0;
   // SwiGLU
-  bf16* ug = nullptr;                // fwd output / bwd input (UG layout == acc layout)
-  const bf16* ug_in = nullptr;
+  bf16* ug = nullptr;                // fwd output (UG) / bwd output (dUG); same interleaved layout
+  const bf16* ug_in = nullptr;       // bwd input (UG)
   int64_t ld_ug = 0;
   bf16* z = nullptr;                 // fwd: Z[m, neuron]
   int64_t ld_z = 0;
@@ -79,12 +81,21 @@ struct GemmArgs {
   const int32_t* goff = nullptr;   // [G+1] group offsets along m (GROUP_M) or k (GROUP_K)
   int G = 1;
   int max_tiles_m = 0;             // GROUP_M: grid bound on m-tiles, >= sum_g ceil(cnt_g / 128)
+  // split-K (dense EPI_STORE only): fp32 partials [splits, M, N] in `splitk_ws`
+  int splits = 1;
+  int k_chunk = 0;
+  float* splitk_ws = nullptr;
   Epilogue epi;
 };
 
 // Picks a tile configuration for the problem and launches it on `stream`.
+// `ws`/`ws_bytes` (optional) enable split-K for dense problems with few tiles.
 // Returns 0 or -1 with rte_last_error() set.
-int gemm_launch(const GemmArgs& args, int epi_kind, hipStream_t stream);
+int gemm_launch(const GemmArgs& args, int epi_kind, hipStream_t stream, void* ws = nullptr,
+                size_t ws_bytes = 0);
+
+// Workspace that lets gemm_launch split a dense problem of this shape along k.
+size_t gemm_splitk_bytes(int M, int N, int K);
 
 // Every GROUP_M configuration uses this tile height.
 constexpr int kGroupTileM = 128;

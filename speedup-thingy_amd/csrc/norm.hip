@@ -73,48 +73,109 @@ __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const float* __restric
 }
 
 // dx = rstd * (w*dy) - x * rstd^3 * mean(w*dy*x)  (+ dres);   partial dw per row block.
-constexpr int kNormRowsPerBlock = 64;
+// One wave per row, 8 columns per lane per step (16-byte dy loads, 32-byte x loads);
+// each lane keeps its columns' dw partial in registers across the block's rows, so
+// dw needs no atomics: per-block partials are summed in block order by colsum_kernel.
+constexpr int kNormRowsPerBlock = 32;
+constexpr int kNormMaxChunks = 4;  // d <= 64 lanes * 8 * 4 = 2048
+
+__device__ __forceinline__ void load8_bf16(const bf16* p, float* v) {
+  const uint4 u = *reinterpret_cast<const uint4*>(p);
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(w[i] << 16);
+    v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+
+__device__ __forceinline__ void load8_f32(const float* p, float* v) {
+  const float4 a = *reinterpret_cast<const float4*>(p);
+  const float4 b = *reinterpret_cast<const float4*>(p + 4);
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+__device__ __forceinline__ void store8_f32(float* p, const float* v) {
+  *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+  *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+}
 
 __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     const bf16* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ rstd, const float* __restrict__ dres, int T, int d,
     float* __restrict__ dx, float* __restrict__ dw_part) {
-  // each wave walks rows blockIdx.x*64 + wave, +4, ...; dw partial kept per lane column chunk
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   extern __shared__ float sdw[];  // [4][d]
-  for (int c = threadIdx.x; c < 4 * d; c += 256) sdw[c] = 0.0f;
-  __syncthreads();
+  const int nchunk = d / 8;
+  float wv[kNormMaxChunks][8];
+  float acc[kNormMaxChunks][8];
+#pragma unroll
+  for (int c = 0; c < kNormMaxChunks; ++c) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      acc[c][t] = 0.0f;
+      wv[c][t] = 0.0f;
+    }
+    if (lane + 64 * c < nchunk) load8_f32(w + (lane + 64 * c) * 8, wv[c]);
+  }
   const int r0 = blockIdx.x * kNormRowsPerBlock;
   for (int rr = wave; rr < kNormRowsPerBlock; rr += 4) {
     const int t = r0 + rr;
     if (t >= T) break;
     const float rs = rstd[t];
-    const bf16* dyr = dy + (int64_t)t * d;
-    const float* xr = x + (int64_t)t * d;
+    float g[kNormMaxChunks][8], xv[kNormMaxChunks][8];
     float dot = 0.0f;
-    for (int c = lane; c < d; c += 64) dot += w[c] * bf2f(dyr[c]) * xr[c];
+#pragma unroll
+    for (int c = 0; c < kNormMaxChunks; ++c) {
+      if (lane + 64 * c >= nchunk) continue;
+      const int col = (lane + 64 * c) * 8;
+      load8_bf16(dy + (int64_t)t * d + col, g[c]);
+      load8_f32(x + (int64_t)t * d + col, xv[c]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) dot += wv[c][i] * g[c][i] * xv[c][i];
+    }
     dot = wave_sum(dot);
     const float coef = rs * rs * rs * dot / (float)d;
-    for (int c = lane; c < d; c += 64) {
-      const float g = bf2f(dyr[c]);
-      float v = rs * w[c] * g - xr[c] * coef;
-      if (dres) v += dres[(int64_t)t * d + c];
-      dx[(int64_t)t * d + c] = v;
-      sdw[wave * d + c] += g * xr[c] * rs;
+#pragma unroll
+    for (int c = 0; c < kNormMaxChunks; ++c) {
+      if (lane + 64 * c >= nchunk) continue;
+      const int col = (lane + 64 * c) * 8;
+      float o[8];
+      if (dres) load8_f32(dres + (int64_t)t * d + col, o);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float v = rs * wv[c][i] * g[c][i] - xv[c][i] * coef;
+        o[i] = dres ? o[i] + v : v;
+        acc[c][i] += g[c][i] * xv[c][i] * rs;
+      }
+      store8_f32(dx + (int64_t)t * d + col, o);
     }
   }
+#pragma unroll
+  for (int c = 0; c < kNormMaxChunks; ++c)
+    if (lane + 64 * c < nchunk) store8_f32(sdw + wave * d + (lane + 64 * c) * 8, acc[c]);
   __syncthreads();
   for (int c = threadIdx.x; c < d; c += 256)
     dw_part[(int64_t)blockIdx.x * d + c] = ((sdw[c] + sdw[d + c]) + sdw[2 * d + c]) + sdw[3 * d + c];
 }
 
+// out[c] (+)= sum_r part[r, c]: 4 row phases per column, combined in fixed order.
 __global__ void __launch_bounds__(256) colsum_kernel(const float* __restrict__ part, int nrows, int d,
                                                      float* __restrict__ out, int accumulate) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= d) return;
+  __shared__ float sh[4][64];
+  const int l = threadIdx.x & 63;
+  const int col = blockIdx.x * 64 + l;
+  const int phase = threadIdx.x >> 6;
   float s = 0.0f;
-  for (int r = 0; r < nrows; ++r) s += part[(int64_t)r * d + c];
-  out[c] = accumulate ? out[c] + s : s;
+  if (col < d)
+    for (int r = phase; r < nrows; r += 4) s += part[(int64_t)r * d + col];
+  sh[phase][l] = s;
+  __syncthreads();
+  if (phase == 0 && col < d) {
+    const float tot = ((sh[0][l] + sh[1][l]) + sh[2][l]) + sh[3][l];
+    out[col] = accumulate ? out[col] + tot : tot;
+  }
 }
 
 // dq/dk/dv: [B,H,S,hd] with arbitrary element strides; dqkv: [B*S, 3*H*hd] bf16.
@@ -203,7 +264,7 @@ size_t rmsnorm_bwd_workspace_bytes(int T, int d) {
 int rmsnorm_bwd(const bf16* dy, const float* x, const float* w, const float* rstd, const float* dres, int T,
                 int d, float* dx, float* dw, int dw_accumulate, void* ws, size_t ws_bytes, hipStream_t s) {
   RTE_REQUIRE(ws_bytes >= rmsnorm_bwd_workspace_bytes(T, d), "rmsnorm_bwd: workspace too small");
-  RTE_REQUIRE((size_t)4 * d * sizeof(float) <= 65536, "rmsnorm_bwd: d too large");
+  RTE_REQUIRE(d % 8 == 0 && d <= 64 * 8 * kNormMaxChunks, "rmsnorm_bwd: d must be a multiple of 8 and <= 2048");
   const int nblk = (T + kNormRowsPerBlock - 1) / kNormRowsPerBlock;
   float* part = static_cast<float*>(ws);
   if (nblk > 0) {
@@ -213,7 +274,7 @@ int rmsnorm_bwd(const bf16* dy, const float* x, const float* w, const float* rst
   }
   if (dw) {
     if (nblk == 0) return dw_accumulate ? 0 : fill_f32(dw, 0.0f, d, s);
-    hipLaunchKernelGGL(colsum_kernel, dim3((d + 255) / 256), dim3(256), 0, s, part, nblk, d, dw, dw_accumulate);
+    hipLaunchKernelGGL(colsum_kernel, dim3((d + 63) / 64), dim3(256), 0, s, part, nblk, d, dw, dw_accumulate);
     RTE_TRY(check_launch("rmsnorm_dw"));
   }
   return 0;

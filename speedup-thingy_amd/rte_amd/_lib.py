@@ -26,8 +26,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_abi_version": (_I, []),
     "rte_last_error": (ctypes.c_char_p, []),
     "rte_device_info": (_I, [ctypes.c_char_p, _I]),
-    "rte_gemm_bf16": (_I, [_P, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _I, _I, _I, _I, _F, _F, _P, _I64, _P]),
-    "rte_gemm_bf16_split": (_I, [_P, _P, _I, _P, _P, _I, _P, _I64, _I, _I, _I, _I, _F, _F, _P, _I64, _P]),
+    "rte_gemm_bf16": (
+        _I, [_P, _I64, _I, _P, _P, _I64, _I, _P, _P, _I64, _I, _I, _I, _I, _F, _F, _P, _I64, _P, _SZ, _P]
+    ),
+    "rte_gemm_workspace_bytes": (_SZ, [_I, _I, _I]),
+    "rte_gemm_bf16_split": (_I, [_P, _P, _I, _P, _P, _I, _P, _I64, _I, _I, _I, _I, _F, _F, _P, _I64, _P, _SZ, _P]),
     "rte_route_topk": (_I, [_P, _I, _I, _I, _P, _P, _P]),
     "rte_pack_workspace_bytes": (_SZ, [_I, _I]),
     "rte_pack_index": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
@@ -42,11 +45,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _P, _I, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P],
     ),
     "rte_dense_swiglu_fwd": (_I, [_P, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P, _I, _P]),
-    "rte_dense_swiglu_bwd": (_I, [_P, _P, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P]),
+    "rte_dense_swiglu_bwd": (_I, [_P, _P, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "rte_qkv_rope_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P]),
     "rte_qkv_rope_bwd": (
         _I,
-        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P],
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _SZ, _P],
     ),
     "rte_rmsnorm_fwd": (_I, [_P, _P, _I, _I, _F, _P, _P, _P]),
     "rte_rmsnorm_bwd_workspace_bytes": (_SZ, [_I, _I]),

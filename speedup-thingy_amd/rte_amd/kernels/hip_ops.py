@@ -27,6 +27,29 @@ def _s() -> int:
     return _lib.stream_ptr()
 
 
+_WS: dict[int, torch.Tensor] = {}
+
+
+def workspace(nbytes: int, device: torch.device) -> tuple[int, int]:
+    """(pointer, bytes) of a cached per-device scratch buffer of at least nbytes.
+
+    Every operator here runs on the current stream, so launches that share the
+    buffer are ordered; callers that launch on several streams at once must not
+    share it."""
+    if nbytes <= 0:
+        return 0, 0
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    buf = _WS.get(idx)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(((nbytes + 255) // 256) * 256, dtype=torch.uint8, device=device)
+        _WS[idx] = buf
+    return buf.data_ptr(), buf.numel()
+
+
+def _gemm_ws(M: int, N: int, K: int, device) -> tuple[int, int]:
+    return workspace(_lib.load().rte_gemm_workspace_bytes(M, N, K), device)
+
+
 def cast_bf16(x: torch.Tensor) -> torch.Tensor:
     """fp32 -> bf16 (round to nearest even) with the HIP cast kernel."""
     if x.dtype == BF16:
@@ -72,12 +95,13 @@ def gemm(
         out = torch.empty((M, N), dtype=F32 if out_f32 else BF16, device=a.device)
     if resid is not None:
         resid = resid.contiguous().to(F32)
+    wsp, wsn = _gemm_ws(M, N, K, a.device)
     call(
         "rte_gemm_bf16",
         ptr(a), a.shape[1], int(a_t), None,
         ptr(b), b.shape[1], int(b_t), None,
         ptr(out), out.shape[1], int(out.dtype == F32), M, N, K,
-        float(alpha), float(beta), ptr(resid), 0 if resid is None else resid.shape[1], _s(),
+        float(alpha), float(beta), ptr(resid), 0 if resid is None else resid.shape[1], wsp, wsn, _s(),
     )
     return out
 
@@ -172,9 +196,10 @@ class QKVRopeFn(torch.autograd.Function):
         dqkv = torch.empty((B * S, 3 * d), dtype=BF16, device=xb.device)
         dx = torch.empty((B * S, d), dtype=BF16, device=xb.device)
         dw = torch.empty((3 * d, d), dtype=F32, device=xb.device)
+        wsp, wsn = _gemm_ws(3 * d, d, B * S, xb.device)
         call("rte_qkv_rope_bwd", ptr(grads[0]), strides[0].data_ptr(), ptr(grads[1]), strides[1].data_ptr(),
              ptr(grads[2]), strides[2].data_ptr(), ptr(xb), ptr(wb), ptr(cos), ptr(sin), B, S, H, hd,
-             ptr(dqkv), ptr(dx), ptr(dw), _s())
+             ptr(dqkv), ptr(dx), ptr(dw), wsp, wsn, _s())
         return dx.view(B, S, d), dw.to(ctx.w_dtype), None, None, None
 
 
@@ -201,7 +226,7 @@ class AttnOutProjFn(torch.autograd.Function):
         L = torch.tensor(layout, dtype=torch.int64)
         Lw = torch.tensor([K, 0, 0, 0, 0], dtype=torch.int64)
         call("rte_gemm_bf16_split", ptr(yb), L.data_ptr(), 0, ptr(wb), Lw.data_ptr(), 0, ptr(out), N, 1, T, N, K,
-             1.0, 0.0, ptr(r), 0 if r is None else N, _s())
+             1.0, 0.0, ptr(r), 0 if r is None else N, None, 0, _s())
         ctx.save_for_backward(yb, wb)
         ctx.has_resid = resid is not None
         ctx.w_dtype = w.dtype
@@ -221,8 +246,9 @@ class AttnOutProjFn(torch.autograd.Function):
         L = torch.tensor(layout, dtype=torch.int64)
         Ld = torch.tensor([N, 0, 0, 0, 0], dtype=torch.int64)
         dw = torch.empty((N, K), dtype=F32, device=yb.device)
+        wsp, wsn = _gemm_ws(N, K, T, yb.device)
         call("rte_gemm_bf16_split", ptr(db), Ld.data_ptr(), 1, ptr(yb), L.data_ptr(), 1, ptr(dw), K, 1, N, K, T,
-             1.0, 0.0, None, 0, _s())
+             1.0, 0.0, None, 0, wsp, wsn, _s())
         dy4 = dy.view(B, S, H, hd).transpose(1, 2)
         dres = dout if ctx.has_resid else None
         return dy4, dw.to(ctx.w_dtype), dres
@@ -271,8 +297,9 @@ class DenseSwiGLUFn(torch.autograd.Function):
         dx = torch.empty((T, d), dtype=BF16, device=xb.device)
         dwug = torch.empty((2 * F, d), dtype=F32, device=xb.device)
         dwd = torch.empty(wdb.shape, dtype=F32, device=xb.device)
+        wsp, wsn = _gemm_ws(2 * F, d, T, xb.device)
         call("rte_dense_swiglu_bwd", ptr(db), ptr(xb), T, d, F, ptr(wugb), ptr(wdb), int(wd_rows), ptr(ug), ptr(z),
-             ptr(dug), ptr(dx), ptr(dwug), ptr(dwd), _s())
+             ptr(dug), ptr(dx), ptr(dwug), ptr(dwd), wsp, wsn, _s())
         dres = dout if has_resid else None
         return dx.view(shape), dwug.to(wug_dtype), dwd.to(wd_dtype), dres, None, None
 

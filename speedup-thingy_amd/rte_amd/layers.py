@@ -19,6 +19,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from rte_amd.config import ModelConfig
+from rte_amd.gather import gather_cols, gather_rows
 from rte_amd.kernels import hip_ops
 from rte_amd.kernels import optimized as K
 from rte_amd.recipes import RecipeBank, RecipeSpec
@@ -173,12 +174,12 @@ class BankedAttention(nn.Module):
         heads = active_dim // hd
         out = x.new_zeros(b, s, d)
         for bank in spec.attention_banks:
-            qkv = x @ self.wqkv[bank][:, qkv_cols]
+            qkv = x @ gather_cols(self.wqkv[bank], qkv_cols)
             q, k, v = (t.view(b, s, heads, hd).transpose(1, 2) for t in qkv.split(active_dim, dim=-1))
             if self.rope is not None:
                 q, k = self.rope(q, k)
             y = K.k_flash_causal_grouped(q, k, v).transpose(1, 2).contiguous().view(b, s, active_dim)
-            out = out + K.k_out_proj_grouped(y, self.wo[bank], cols)
+            out = out + y @ gather_rows(self.wo[bank], cols)
         return out / max(len(spec.attention_banks), 1)
 
 
@@ -210,9 +211,9 @@ class BankedSwiGLU(nn.Module):
         gate_cols = self.recipe_gate_cols[spec.recipe_id, : 2 * active]
         out = x.new_zeros(*x.shape)
         for bank in spec.ffn_banks:
-            fused = x @ self.wug[bank][:, gate_cols]
+            fused = x @ gather_cols(self.wug[bank], gate_cols)
             up, gate = fused.split(active, dim=-1)
-            out = out + (up * F.silu(gate)) @ self.wd[bank][slabs, :]
+            out = out + (up * F.silu(gate)) @ gather_rows(self.wd[bank], slabs)
         return out / max(len(spec.ffn_banks), 1)
 
 
@@ -249,12 +250,22 @@ class BankedRecursiveCore(nn.Module):
         n2 = self.norm2(u) * (1.0 + self.pass_gamma2[pass_idx]) + self.pass_beta2[pass_idx]
         return u + self.pass_mlp_scale[pass_idx] * self.mlp(n2, spec)
 
-    def forward_step(self, h, h0, recipe_ids, active_mask=None, pass_idx: int = 0):
+    def forward_step(self, h, h0, recipe_ids, active_mask=None, pass_idx: int = 0, *, host_ids=None,
+                     host_active=None):
+        """One exact recursive pass, grouped by recipe (rte/layers.py:854-870).  host_ids /
+        host_active (python lists) let the caller read the routing decisions once per replay
+        instead of once per pass."""
+        if host_ids is None:
+            host_ids = recipe_ids.detach().cpu().tolist()
+            host_active = ([True] * len(host_ids) if active_mask is None
+                           else active_mask.detach().cpu().tolist())
         out = h.clone()
-        if active_mask is None:
-            active_mask = torch.ones(h.shape[0], dtype=torch.bool, device=h.device)
-        for rid in torch.unique(recipe_ids[active_mask]).detach().cpu().tolist():
-            mask = active_mask & (recipe_ids == int(rid))
+        for rid in sorted({r for r, a in zip(host_ids, host_active) if a}):
+            rows = [i for i, (r, a) in enumerate(zip(host_ids, host_active)) if a and r == rid]
             spec = self.recipe_bank.get_recipe(int(rid))
-            out[mask] = self.step_group(h[mask], h0[mask], spec, pass_idx=pass_idx).to(out.dtype)
+            if len(rows) == h.shape[0]:
+                return self.step_group(h, h0, spec, pass_idx=pass_idx).to(out.dtype)
+            idx = torch.tensor(rows, device=h.device, dtype=torch.long)
+            out = out.index_copy(0, idx, self.step_group(h.index_select(0, idx), h0.index_select(0, idx), spec,
+                                                         pass_idx=pass_idx).to(out.dtype))
         return out

@@ -15,6 +15,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from rte_amd.config import ModelConfig
+from rte_amd.gather import gather_rk, gather_rows
 
 
 def _rms(x, *, dim=-1, keepdim=False):
@@ -123,27 +124,28 @@ class MacroOperators(nn.Module):
 
     def _apply_bounded(self, h, h0, recipe_ids, stride_ids):
         """rte/macro.py:201-236."""
-        gain = self.d_gain[recipe_ids, stride_ids]
-        v = self.v[recipe_ids, stride_ids]
-        u = self.u[recipe_ids, stride_ids]
-        bias = self.bias[recipe_ids, stride_ids]
-        scale = self.update_scale[recipe_ids, stride_ids]
+        gain = gather_rk(self.d_gain, recipe_ids, stride_ids)
+        v = gather_rk(self.v, recipe_ids, stride_ids)
+        u = gather_rk(self.u, recipe_ids, stride_ids)
+        bias = gather_rk(self.bias, recipe_ids, stride_ids)
+        scale = gather_rk(self.update_scale, recipe_ids, stride_ids)
         normed = _rmsnorm(h)
         parts = [normed, normed.mean(dim=1, keepdim=True).expand_as(normed), h0]
         if self.config.macro_include_delta_to_h0:
             parts.append(normed - _rmsnorm(h0))
         if self.depth_embed is not None:
-            parts.append(self.depth_embed[stride_ids].unsqueeze(1).expand_as(normed))
+            parts.append(gather_rows(self.depth_embed, stride_ids).unsqueeze(1).expand_as(normed))
         z = torch.cat(parts, dim=-1)
         low = F.silu(torch.bmm(z, v))
         if self.v2 is not None:
-            low = F.silu(torch.bmm(low, self.v2[recipe_ids, stride_ids]))
+            low = F.silu(torch.bmm(low, gather_rk(self.v2, recipe_ids, stride_ids)))
         low = torch.bmm(low, u)
         update = gain.unsqueeze(1) * h + low + bias.unsqueeze(1)
         if self.gate_v is not None:
             gate = torch.sigmoid(
-                torch.bmm(F.silu(torch.bmm(z, self.gate_v[recipe_ids, stride_ids])), self.gate_u[recipe_ids, stride_ids])
-                + self.gate_bias[recipe_ids, stride_ids].unsqueeze(1)
+                torch.bmm(F.silu(torch.bmm(z, gather_rk(self.gate_v, recipe_ids, stride_ids))),
+                          gather_rk(self.gate_u, recipe_ids, stride_ids))
+                + gather_rk(self.gate_bias, recipe_ids, stride_ids).unsqueeze(1)
             )
         else:
             gate = 1.0
@@ -157,16 +159,17 @@ class MacroOperators(nn.Module):
         if self.config.macro_use_delta_to_h0 or self.config.macro_include_delta_to_h0:
             parts.append(normed - _rmsnorm(h0))
         if self.depth_embed is not None:
-            parts.append(self.depth_embed[stride_ids].unsqueeze(1).expand_as(normed))
+            parts.append(gather_rows(self.depth_embed, stride_ids).unsqueeze(1).expand_as(normed))
         if self.recipe_embed is not None:
-            parts.append(self.recipe_embed[recipe_ids].unsqueeze(1).expand_as(normed))
+            parts.append(gather_rows(self.recipe_embed, recipe_ids).unsqueeze(1).expand_as(normed))
         z = torch.cat(parts, dim=-1)
-        raw = torch.bmm(F.silu(torch.bmm(F.silu(torch.bmm(z, self.v[recipe_ids, stride_ids])),
-                                         self.v2[recipe_ids, stride_ids])), self.u[recipe_ids, stride_ids])
-        raw = raw + self.bias[recipe_ids, stride_ids].unsqueeze(1)
+        raw = torch.bmm(F.silu(torch.bmm(F.silu(torch.bmm(z, gather_rk(self.v, recipe_ids, stride_ids))),
+                                         gather_rk(self.v2, recipe_ids, stride_ids))),
+                        gather_rk(self.u, recipe_ids, stride_ids))
+        raw = raw + gather_rk(self.bias, recipe_ids, stride_ids).unsqueeze(1)
         direction = raw / _rms(raw, dim=(1, 2), keepdim=True).clamp_min(1e-6)
-        rho_head = torch.bmm(pooled.unsqueeze(1), self.rho_head[recipe_ids, stride_ids]).squeeze(-1).squeeze(-1)
-        rho = F.softplus(self.rho_base_raw[recipe_ids, stride_ids] + rho_head)
+        rho_head = torch.bmm(pooled.unsqueeze(1), gather_rk(self.rho_head, recipe_ids, stride_ids)).squeeze(-1).squeeze(-1)
+        rho = F.softplus(gather_rk(self.rho_base_raw, recipe_ids, stride_ids) + rho_head)
         teacher = self.teacher_delta_rms[recipe_ids, stride_ids].to(rho.device)
         if self.config.macro_radius_init_from_teacher:
             has = teacher > 0

@@ -142,3 +142,25 @@ def test_accelerated_modes_only():
     cfg = ExperimentConfig(model=ModelConfig(**_model()), training=TrainingConfig(mode="recursive_exact_route_em"))
     with pytest.raises(NotImplementedError):
         TrainEngine(cfg, device=torch.device("cpu"))
+
+
+def test_deterministic_gathers_match_indexing_gradients():
+    from rte_amd.gather import gather_cols, gather_rk, gather_rows
+
+    torch.manual_seed(0)
+    table = torch.randn(4, 3, 5, 2, dtype=torch.float64, requires_grad=True)
+    r = torch.tensor([1, 3, 1, 0, 1])
+    s = torch.tensor([2, 0, 2, 1, 0])
+    g = torch.randn(5, 5, 2, dtype=torch.float64)
+    (gather_rk(table, r, s) * g).sum().backward()
+    ref = torch.zeros_like(table).index_put_((r, s), g, accumulate=True)
+    assert torch.allclose(table.grad, ref)
+    mat = torch.randn(6, 7, requires_grad=True)
+    cols = torch.tensor([6, 1, 1, 3])
+    out = gather_cols(mat, cols)
+    assert torch.equal(out, mat[:, cols])
+    out.sum().backward()
+    assert torch.allclose(mat.grad, torch.zeros(6, 7).index_add_(1, cols, torch.ones(6, 4)))
+    w = torch.randn(5, 3, requires_grad=True)
+    gather_rows(w, torch.tensor([4, 4, 0])).sum().backward()
+    assert torch.allclose(w.grad[4], torch.full((3,), 2.0)) and torch.allclose(w.grad[1], torch.zeros(3))
