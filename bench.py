@@ -112,6 +112,16 @@ def kernel_candidates(B: int, S: int):
         _lib.call("rte_qkv_rope_fwd", x.data_ptr(), wqkv.data_ptr(), cos.data_ptr(), sin.data_ptr(), B, S, 8, 64,
                   q.data_ptr(), kk.data_ptr(), vv.data_ptr(), s)
 
+    dqkv = torch.randn(T, 3 * d, device=dev, generator=g).to(bf)
+    dw_qkv = torch.empty(3 * d, d, device=dev, dtype=torch.float32)
+    ws_bytes = _lib.load().rte_gemm_workspace_bytes(3 * d, d, T)
+    ws = torch.empty(max(ws_bytes, 16), device=dev, dtype=torch.uint8)
+
+    def wgrad():
+        # dW_qkv[c, :] = sum_t dqkv[t, c] x[t, :]  (both operands token-major: layout T, split-K)
+        _lib.call("rte_gemm_bf16", dqkv.data_ptr(), 3 * d, 1, None, x.data_ptr(), d, 1, None, dw_qkv.data_ptr(), d,
+                  1, 3 * d, d, T, 1.0, 0.0, None, 0, ws.data_ptr(), ws_bytes, s)
+
     def ffn_fwd():
         _lib.call("rte_grouped_swiglu_fwd", x.data_ptr(), T, d, pk.offsets.data_ptr(), C, n, P,
                   pk.tok_of_slot.data_ptr(), pk.pair_of_slot.data_ptr(), pk.w_of_slot.data_ptr(), wug.data_ptr(),
@@ -122,6 +132,7 @@ def kernel_candidates(B: int, S: int):
         ("gemm_qkv_rope_fwd", 2, 2.0 * T * 3 * d * d, qkv),
         # two grouped GEMM launches: x@[Wup|Wgate]^T with SwiGLU epilogue, then zw@Wdown
         ("grouped_swiglu_fwd", 2, 2.0 * P * d * 2 * n + 2.0 * P * n * d, ffn_fwd),
+        ("gemm_wgrad_qkv", 2, 2.0 * T * 3 * d * d, wgrad),
     ]
 
 

@@ -251,9 +251,10 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
   static_assert(TM >= 1 && TN >= 1, "wave tile must hold a 32x32 block");
 
   extern __shared__ __align__(16) unsigned char smem_raw[];
+  // LDS buffers are addressed as offsets from the shared base (a runtime-selected
+  // pointer would lose the LDS address space and turn every access into a flat op)
   bf16* smem = reinterpret_cast<bf16*>(smem_raw);
-  bf16* As[2] = {smem, smem + BM * LDP};
-  bf16* Bs[2] = {smem + 2 * BM * LDP, smem + 2 * BM * LDP + BN * LDP};
+  constexpr int A_STAGE = BM * LDP, B_STAGE = BN * LDP, B_BASE = 2 * BM * LDP;
   __shared__ int s_tile[2];
 
   const int tid = threadIdx.x;
@@ -332,8 +333,8 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
   if (nk > 0) {
     la.load(p.a, abase, ashift, kbeg, kend, tid);
     lb.load(p.b, bbase, bshift, kbeg, kend, tid);
-    la.store(As[0], tid);
-    lb.store(Bs[0], tid);
+    la.store(smem, tid);
+    lb.store(smem + B_BASE, tid);
   }
   __syncthreads();
 
@@ -345,8 +346,8 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
       la.load(p.a, abase, ashift, k0, kend, tid);
       lb.load(p.b, bbase, bshift, k0, kend, tid);
     }
-    const bf16* a_s = As[cur];
-    const bf16* b_s = Bs[cur];
+    const bf16* a_s = smem + cur * A_STAGE;
+    const bf16* b_s = smem + B_BASE + cur * B_STAGE;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8_v af[TM], bfr[TN];
@@ -364,8 +365,8 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
     if (more) {
-      la.store(As[cur ^ 1], tid);
-      lb.store(Bs[cur ^ 1], tid);
+      la.store(smem + (cur ^ 1) * A_STAGE, tid);
+      lb.store(smem + B_BASE + (cur ^ 1) * B_STAGE, tid);
     }
     __syncthreads();
   }
@@ -532,24 +533,32 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
   } else if constexpr (EPI == EPI_ROPE_QKV) {
     constexpr int HP = BN + 8;
     bf16* Hs = smem;
+    // per-column head position (hoisted), per-row sequence position
+    int dim_j[TN];
+    bool rot_j[TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + cbase + j * 32;
+      dim_j[j] = n % e.hd;
+      rot_j[j] = n < 2 * e.dmodel;
+    }
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int rl = rbase + i * 32 + (r >> 2) * 8 + (r & 3);
         const int m = m0 + rl;
-        const int s = m % e.S;
+        const int s = m < mlim ? m % e.S : 0;
+        const float* cs = e.cos_t + (int64_t)s * e.hd;
+        const float* sn = e.sin_t + (int64_t)s * e.hd;
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-          const int n = n0 + cbase + j * 32;
           const float x = acc[i][j][r];
           const float partner = __shfl_xor(x, 1, 64);
           float y = x;
-          if (n < 2 * e.dmodel && m < mlim) {
-            const int dim = n % e.hd;
-            const float c = e.cos_t[(int64_t)s * e.hd + dim];
-            const float sn = e.sin_t[(int64_t)s * e.hd + dim];
-            y = (dim & 1) ? (x * c + partner * sn) : (x * c - partner * sn);
+          if (rot_j[j]) {
+            const float c = cs[dim_j[j]], si = sn[dim_j[j]];
+            y = (dim_j[j] & 1) ? (x * c + partner * si) : (x * c - partner * si);
           }
           Hs[rl * HP + cbase + j * 32] = f2bf(y);
         }
