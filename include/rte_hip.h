@@ -141,6 +141,23 @@ int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const in
                      const float* sin_t, int B, int S, int H, int hd, void* dqkv, void* dx, float* dw,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- SVD low-rank SwiGLU FFN (rte/layers.py:342-643 SVDFactorSparseFFN factors
+ *      up_a = U S, up_b = V^T from refresh_svd :437-444) ----
+ * us_ug bf16 [d, 2r] = [U_up S_up | U_gate S_gate], v_ug bf16 [2F, r] = [V_up ; V_gate],
+ * v_dn bf16 [F, r], us_dn bf16 [d, r] = U_dn S_dn (W_down^T = U_dn S_dn V_dn^T).
+ * fwd: a_ug [T, 2r], ug [T, 2F] (interleaved per 64), z [T, F], b [T, r] (all bf16),
+ *      y [T, d] = resid + ((z V_dn) us_dn^T), f32 (y_f32=1) or bf16.  r % 8, F % 64, d % 8 == 0. */
+int rte_svd_ffn_fwd(const void* x, int T, int d, int F, int r, const void* us_ug, const void* v_ug,
+                    const void* v_dn, const void* us_dn, const float* resid, void* a_ug, void* ug, void* z,
+                    void* b, void* y, int y_f32, void* stream);
+/* bwd from dy bf16 [T, d]: scratch db [T, r], dug [T, 2F], da_ug [T, 2r] (bf16); dx [T, d] bf16;
+ * weight grads f32 (overwritten) dus_ug [d, 2r], dv_ug [2F, r], dv_dn [F, r], dus_dn [d, r]. */
+int rte_svd_ffn_bwd(const void* dy, const void* x, int T, int d, int F, int r, const void* us_ug,
+                    const void* v_ug, const void* v_dn, const void* us_dn, const void* a_ug, const void* ug,
+                    const void* z, const void* b, void* db, void* dug, void* da_ug, void* dx, float* dus_ug,
+                    float* dv_ug, float* dv_dn, float* dus_dn, void* workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* ---- RMSNorm (rte/kernels/reference.py:9-17, rte/layers.py:26-33) ----
  * out bf16 = bf16(x * rsqrt(mean(x^2) + eps) * w), rstd [T] f32 saved for backward. */
 int rte_rmsnorm_fwd(const float* x, const float* w, int T, int d, float eps, void* out, float* rstd,
@@ -150,6 +167,15 @@ size_t rte_rmsnorm_bwd_workspace_bytes(int T, int d);
 int rte_rmsnorm_bwd(const void* dy, const float* x, const float* w, const float* rstd, const float* dres,
                     int T, int d, float* dx, float* dw, int dw_accumulate, void* workspace,
                     size_t workspace_bytes, void* stream);
+
+/* ---- token cross-entropy on full logits (rte/models.py:73-75, rte/kernels/reference.py:146-147) ----
+ * logits f32 [T, ld] (first V columns used), targets int64 [T] (negative = ignored row).
+ * fwd: loss[t] = logsumexp(logits[t]) - logits[t, target], lse[t] saved.
+ * bwd: dlogits bf16 [T, V] = dloss[t] * (softmax - onehot(target)) + extra (f32 [T, V], optional). */
+int rte_ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, float* loss, float* lse,
+               void* stream);
+int rte_ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
+               const float* dloss, const float* extra, void* dlogits, void* stream);
 
 /* fp32 -> bf16 (round to nearest even) */
 int rte_cast_f32_bf16(const float* x, int64_t n, void* y, void* stream);

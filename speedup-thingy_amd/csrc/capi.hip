@@ -27,6 +27,10 @@ int rope_bwd_pack(const bf16* dq, const int64_t* sq, const bf16* dk, const int64
                   const int64_t* sv, const float* cos_t, const float* sin_t, int B, int H, int S, int hd,
                   bf16* dqkv, hipStream_t s);
 int cast_f32_bf16(const float* x, int64_t n, bf16* y, hipStream_t s);
+int ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, float* loss, float* lse,
+           hipStream_t s);
+int ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse, const float* g,
+           const float* extra, bf16* dlogits, hipStream_t s);
 }  // namespace rte
 
 using namespace rte;
@@ -481,6 +485,192 @@ int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const in
   return 0;
 }
 
+// ------------------------------------------------------------------ SVD low-rank SwiGLU FFN
+// Low-rank factors per projection: W_up = U_up diag(S_up) V_up^T (d x F), same for gate;
+// W_down^T = U_dn diag(S_dn) V_dn^T.  With us_* = U * S folded by the caller:
+//   a_ug = x @ [us_up | us_gate]            [T, 2r]
+//   ug   = [a_up V_up^T | a_gate V_gate^T]  [T, 2F] (interleaved per 64), z = up * silu(gate)
+//   b    = z @ V_dn                         [T, r]
+//   y    = resid + b @ us_dn^T              [T, d]
+
+int rte_svd_ffn_fwd(const void* x, int T, int d, int F, int r, const void* us_ug, const void* v_ug,
+                    const void* v_dn, const void* us_dn, const float* resid, void* a_ug, void* ug, void* z,
+                    void* b, void* y, int y_f32, void* stream) {
+  RTE_REQUIRE(r % 8 == 0 && F % 64 == 0 && d % 8 == 0, "svd_ffn: need r %% 8, F %% 64, d %% 8 == 0");
+  {
+    GemmArgs p;  // a_ug = x @ us_ug : B(n=j, k=dcol) = us_ug[dcol][j]
+    p.M = T;
+    p.N = 2 * r;
+    p.K = d;
+    p.a = plain(x, d);
+    p.b = plain(us_ug, 2 * r);
+    p.b_t = 1;
+    p.epi.c = a_ug;
+    p.epi.ldc = 2 * r;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  {
+    GemmArgs p;  // expand + SwiGLU: up blocks read a_ug[:, 0:r], gate blocks a_ug[:, r:2r]
+    p.M = T;
+    p.N = 2 * F;
+    p.K = r;
+    p.a = plain(a_ug, 2 * r);
+    p.a_koff2 = r;
+    p.b = plain(v_ug, r);
+    p.b.ilv = F;
+    p.epi.ug = B16(ug);
+    p.epi.ld_ug = 2 * F;
+    p.epi.z = B16(z);
+    p.epi.ld_z = F;
+    RTE_TRY(gemm_launch(p, EPI_SWIGLU_FWD, S(stream)));
+  }
+  {
+    GemmArgs p;  // b = z @ v_dn : B(n=j, k=f) = v_dn[f][j]
+    p.M = T;
+    p.N = r;
+    p.K = F;
+    p.a = plain(z, F);
+    p.b = plain(v_dn, r);
+    p.b_t = 1;
+    p.epi.c = b;
+    p.epi.ldc = r;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  {
+    GemmArgs p;  // y = resid + b @ us_dn^T : B(n=dcol, k=j) = us_dn[dcol][j]
+    p.M = T;
+    p.N = d;
+    p.K = r;
+    p.a = plain(b, r);
+    p.b = plain(us_dn, r);
+    p.epi.c = y;
+    p.epi.ldc = d;
+    p.epi.c_f32 = y_f32;
+    p.epi.resid = resid;
+    p.epi.ld_resid = d;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  return 0;
+}
+
+int rte_svd_ffn_bwd(const void* dy, const void* x, int T, int d, int F, int r, const void* us_ug, const void* v_ug,
+                    const void* v_dn, const void* us_dn, const void* a_ug, const void* ug, const void* z,
+                    const void* b, void* db, void* dug, void* da_ug, void* dx, float* dus_ug, float* dv_ug,
+                    float* dv_dn, float* dus_dn, void* workspace, size_t workspace_bytes, void* stream) {
+  RTE_REQUIRE(r % 8 == 0 && F % 64 == 0 && d % 8 == 0, "svd_ffn: need r %% 8, F %% 64, d %% 8 == 0");
+  hipStream_t st = S(stream);
+  {
+    GemmArgs p;  // db = dy @ us_dn : B(n=j, k=dcol) = us_dn[dcol][j]
+    p.M = T;
+    p.N = r;
+    p.K = d;
+    p.a = plain(dy, d);
+    p.b = plain(us_dn, r);
+    p.b_t = 1;
+    p.epi.c = db;
+    p.epi.ldc = r;
+    RTE_TRY(gemm_launch(p, EPI_STORE, st));
+  }
+  {
+    GemmArgs p;  // dus_dn[dcol, j] = sum_t dy[t, dcol] b[t, j]
+    p.M = d;
+    p.N = r;
+    p.K = T;
+    p.a = plain(dy, d);
+    p.a_t = 1;
+    p.b = plain(b, r);
+    p.b_t = 1;
+    p.epi.c = dus_dn;
+    p.epi.ldc = r;
+    p.epi.c_f32 = 1;
+    RTE_TRY(gemm_launch(p, EPI_STORE, st, workspace, workspace_bytes));
+  }
+  {
+    GemmArgs p;  // dZ = db @ v_dn^T with the SwiGLU backward epilogue -> dUG
+    p.M = T;
+    p.N = F;
+    p.K = r;
+    p.a = plain(db, r);
+    p.b = plain(v_dn, r);
+    p.epi.ug_in = B16(ug);
+    p.epi.ug = B16(dug);
+    p.epi.ld_ug = 2 * F;
+    RTE_TRY(gemm_launch(p, EPI_SWIGLU_BWD, st));
+  }
+  {
+    GemmArgs p;  // dv_dn[f, j] = sum_t z[t, f] db[t, j]
+    p.M = F;
+    p.N = r;
+    p.K = T;
+    p.a = plain(z, F);
+    p.a_t = 1;
+    p.b = plain(db, r);
+    p.b_t = 1;
+    p.epi.c = dv_dn;
+    p.epi.ldc = r;
+    p.epi.c_f32 = 1;
+    RTE_TRY(gemm_launch(p, EPI_STORE, st, workspace, workspace_bytes));
+  }
+  for (int half = 0; half < 2; ++half) {
+    // dUP / dGATE read from the interleaved dUG: column f -> (f/32)*64 + f%32 (+32 for gate)
+    Operand dsel = plain(static_cast<const bf16*>(dug) + 32 * half, 2 * F);
+    dsel.cdiv = 32;
+    dsel.cs_hi = 64;
+    {
+      GemmArgs p;  // da_half = dHALF @ V_half : B(n=j, k=f) = v_ug[half*F + f][j]
+      p.M = T;
+      p.N = r;
+      p.K = F;
+      p.a = dsel;
+      p.b = plain(static_cast<const bf16*>(v_ug) + (int64_t)half * F * r, r);
+      p.b_t = 1;
+      p.epi.c = static_cast<bf16*>(da_ug) + half * r;
+      p.epi.ldc = 2 * r;
+      RTE_TRY(gemm_launch(p, EPI_STORE, st));
+    }
+    {
+      GemmArgs p;  // dv_half[f, j] = sum_t dHALF[t, f] a_half[t, j]
+      p.M = F;
+      p.N = r;
+      p.K = T;
+      p.a = dsel;
+      p.a_t = 1;
+      p.b = plain(static_cast<const bf16*>(a_ug) + half * r, 2 * r);
+      p.b_t = 1;
+      p.epi.c = dv_ug + (int64_t)half * F * r;
+      p.epi.ldc = r;
+      p.epi.c_f32 = 1;
+      RTE_TRY(gemm_launch(p, EPI_STORE, st, workspace, workspace_bytes));
+    }
+  }
+  {
+    GemmArgs p;  // dx = da_ug @ us_ug^T : B(n=dcol, k=j) = us_ug[dcol][j]
+    p.M = T;
+    p.N = d;
+    p.K = 2 * r;
+    p.a = plain(da_ug, 2 * r);
+    p.b = plain(us_ug, 2 * r);
+    p.epi.c = dx;
+    p.epi.ldc = d;
+    RTE_TRY(gemm_launch(p, EPI_STORE, st));
+  }
+  {
+    GemmArgs p;  // dus_ug[dcol, j] = sum_t x[t, dcol] da_ug[t, j]
+    p.M = d;
+    p.N = 2 * r;
+    p.K = T;
+    p.a = plain(x, d);
+    p.a_t = 1;
+    p.b = plain(da_ug, 2 * r);
+    p.b_t = 1;
+    p.epi.c = dus_ug;
+    p.epi.ldc = 2 * r;
+    p.epi.c_f32 = 1;
+    RTE_TRY(gemm_launch(p, EPI_STORE, st, workspace, workspace_bytes));
+  }
+  return 0;
+}
+
 int rte_rmsnorm_fwd(const float* x, const float* w, int T, int d, float eps, void* out, float* rstd,
                     void* stream) {
   return rmsnorm_fwd(x, w, T, d, eps, B16(out), rstd, S(stream));
@@ -493,6 +683,16 @@ int rte_rmsnorm_bwd(const void* dy, const float* x, const float* w, const float*
                     void* stream) {
   return rmsnorm_bwd(B16(dy), x, w, rstd, dres, T, d, dx, dw, dw_accumulate, workspace, workspace_bytes,
                      S(stream));
+}
+
+int rte_ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, float* loss, float* lse,
+               void* stream) {
+  return ce_fwd(logits, ld, T, V, targets, loss, lse, S(stream));
+}
+
+int rte_ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
+               const float* dloss, const float* extra, void* dlogits, void* stream) {
+  return ce_bwd(logits, ld, T, V, targets, lse, dloss, extra, B16(dlogits), S(stream));
 }
 
 int rte_cast_f32_bf16(const float* x, int64_t n, void* y, void* stream) {

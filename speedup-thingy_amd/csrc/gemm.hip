@@ -242,8 +242,9 @@ struct EpiFlags {
 
 // ------------------------------------------------------------------ kernel
 
-template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI>
+template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI, bool DUALA = false>
 __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
+  static_assert(!DUALA || (EPI == EPI_SWIGLU_FWD && !AT), "dual-A is a SwiGLU-forward layout-N mode");
   constexpr int LDP = BK + 8;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -254,7 +255,8 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
   // LDS buffers are addressed as offsets from the shared base (a runtime-selected
   // pointer would lose the LDS address space and turn every access into a flat op)
   bf16* smem = reinterpret_cast<bf16*>(smem_raw);
-  constexpr int A_STAGE = BM * LDP, B_STAGE = BN * LDP, B_BASE = 2 * BM * LDP;
+  constexpr int A_TILE = BM * LDP;
+  constexpr int A_STAGE = (DUALA ? 2 : 1) * A_TILE, B_STAGE = BN * LDP, B_BASE = 2 * A_STAGE;
   __shared__ int s_tile[2];
 
   const int tid = threadIdx.x;
@@ -326,14 +328,19 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   Loader<BM, BK, AT> la;
+  Loader<BM, BK, AT> la2;  // DUALA: gate half of A
   Loader<BN, BK, BT> lb;
   la.init(p.a, abase, ashift, m0, mlim, tid);
+  if constexpr (DUALA) la2.init(p.a, abase, ashift, m0, mlim, tid);
   lb.init(p.b, bbase, bshift, n0, p.N, tid);
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+  const int ko2 = p.a_koff2;
   if (nk > 0) {
     la.load(p.a, abase, ashift, kbeg, kend, tid);
+    if constexpr (DUALA) la2.load(p.a, abase, ashift, kbeg + ko2, kend + ko2, tid);
     lb.load(p.b, bbase, bshift, kbeg, kend, tid);
     la.store(smem, tid);
+    if constexpr (DUALA) la2.store(smem + A_TILE, tid);
     lb.store(smem + B_BASE, tid);
   }
   __syncthreads();
@@ -344,28 +351,36 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
     if (more) {
       const int k0 = kbeg + (kt + 1) * BK;
       la.load(p.a, abase, ashift, k0, kend, tid);
+      if constexpr (DUALA) la2.load(p.a, abase, ashift, k0 + ko2, kend + ko2, tid);
       lb.load(p.b, bbase, bshift, k0, kend, tid);
     }
     const bf16* a_s = smem + cur * A_STAGE;
     const bf16* b_s = smem + B_BASE + cur * B_STAGE;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8_v af[TM], bfr[TN];
+      bf16x8_v af[TM], ag[DUALA ? TM : 1], bfr[TN];
       const int kof = ks * 16 + (lane >> 5) * 8;
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+      for (int i = 0; i < TM; ++i) {
         af[i] = *reinterpret_cast<const bf16x8_v*>(a_s + (wm * WTM + i * 32 + (lane & 31)) * LDP + kof);
+        if constexpr (DUALA)
+          ag[i] = *reinterpret_cast<const bf16x8_v*>(a_s + A_TILE + (wm * WTM + i * 32 + (lane & 31)) * LDP + kof);
+      }
 #pragma unroll
       for (int j = 0; j < TN; ++j)
         bfr[j] = *reinterpret_cast<const bf16x8_v*>(b_s + (wn * WTN + j * 32 + (lane & 31)) * LDP + kof);
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+        for (int j = 0; j < TN; ++j) {
+          // DUALA: odd column blocks are gate blocks and take the second A code
+          const bf16x8_v& a_op = (DUALA && (j & 1)) ? ag[DUALA ? i : 0] : af[i];
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_op, bfr[j], acc[i][j], 0, 0, 0);
+        }
     }
     if (more) {
       la.store(smem + (cur ^ 1) * A_STAGE, tid);
+      if constexpr (DUALA) la2.store(smem + (cur ^ 1) * A_STAGE + A_TILE, tid);
       lb.store(smem + B_BASE + (cur ^ 1) * B_STAGE, tid);
     }
     __syncthreads();
@@ -600,9 +615,9 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs p, EpiFlags
   store_chunk<4>(p.epi, 0, m, n, p.N, v, fl.vec);
 }
 
-template <int BM, int BN, int BK, int EPI>
+template <int BM, int BN, int BK, int EPI, bool DUALA = false>
 constexpr size_t lds_bytes() {
-  constexpr size_t main_loop = (size_t)2 * (BM + BN) * (BK + 8) * 2;
+  constexpr size_t main_loop = (size_t)2 * ((DUALA ? 2 : 1) * BM + BN) * (BK + 8) * 2;
   constexpr size_t epi = EPI == EPI_STORE        ? (size_t)BM * (BN + 8) * 4
                          : EPI == EPI_SWIGLU_FWD ? (size_t)BM * (BN + 8) * 2 + (size_t)BM * (BN / 2 + 8) * 2
                          : EPI == EPI_SWIGLU_BWD ? (size_t)BM * (2 * BN + 8) * 2
@@ -610,10 +625,10 @@ constexpr size_t lds_bytes() {
   return main_loop > epi ? main_loop : epi;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI>
+template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI, bool DUALA = false>
 int launch_cfg(const GemmArgs& p0, hipStream_t stream, void* ws, size_t ws_bytes, int vec) {
-  constexpr size_t lds = lds_bytes<BM, BN, BK, EPI>();
-  auto fn = gemm_kernel<BM, BN, BK, WM, WN, AT, BT, EPI>;
+  constexpr size_t lds = lds_bytes<BM, BN, BK, EPI, DUALA>();
+  auto fn = gemm_kernel<BM, BN, BK, WM, WN, AT, BT, EPI, DUALA>;
   static bool attr_done = false;
   if (!attr_done) {
     if (lds > 65536) {
@@ -736,6 +751,10 @@ int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream, void* ws, s
       RTE_REQUIRE(!p.a_t && !p.b_t, "gemm: SwiGLU forward expects layout-N operands");
       RTE_REQUIRE(p.N % 64 == 0, "gemm: SwiGLU forward needs N %% 64 == 0");
       RTE_REQUIRE(p.epi.ug && p.epi.z, "gemm: SwiGLU forward needs UG and Z outputs");
+      if (p.a_koff2) {
+        RTE_REQUIRE(p.mode == MODE_DENSE && p.N % 128 == 0, "gemm: dual-A SwiGLU needs dense mode and N %% 128 == 0");
+        return launch_cfg<128, 128, 32, 2, 2, false, false, EPI_SWIGLU_FWD, true>(p, stream, ws, ws_bytes, 1);
+      }
       if (p.N == 64) return launch_cfg<128, 64, 64, 4, 1, false, false, EPI_SWIGLU_FWD>(p, stream, ws, ws_bytes, 1);
       return launch_cfg<128, 128, 64, 2, 2, false, false, EPI_SWIGLU_FWD>(p, stream, ws, ws_bytes, 1);
     case EPI_SWIGLU_BWD:

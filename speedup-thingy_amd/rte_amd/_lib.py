@@ -51,9 +51,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _SZ, _P],
     ),
+    "rte_svd_ffn_fwd": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P]),
+    "rte_svd_ffn_bwd": (
+        _I,
+        [_P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+    ),
     "rte_rmsnorm_fwd": (_I, [_P, _P, _I, _I, _F, _P, _P, _P]),
     "rte_rmsnorm_bwd_workspace_bytes": (_SZ, [_I, _I]),
     "rte_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _P, _I, _P, _SZ, _P]),
+    "rte_ce_fwd": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P]),
+    "rte_ce_bwd": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P]),
     "rte_cast_f32_bf16": (_I, [_P, _I64, _P, _P]),
 }
 

@@ -471,3 +471,102 @@ class LinearFn(torch.autograd.Function):
 
 def linear(x, w, *, out_f32: bool = True):
     return LinearFn.apply(x, w, out_f32)
+
+
+# ----------------------------------------------------------------------------- LM head + cross-entropy
+
+class LMHeadCEFn(torch.autograd.Function):
+    """logits = hidden @ W^T (fp32) and per-token CE against targets in one operator.
+
+    Returns (logits, token_loss).  Both are differentiable: the backward fuses the CE
+    gradient, any gradient arriving on the logits themselves (e.g. a distillation KL term)
+    and the cast to bf16 into one kernel, then runs the two head GEMMs."""
+
+    @staticmethod
+    def forward(ctx, hidden, w, targets):
+        _lib.require_device_tensors("lm_head_ce", hidden, w, targets)
+        shape = hidden.shape
+        hb = hidden.reshape(-1, shape[-1]).contiguous().to(BF16)
+        wb = cast_bf16(w)
+        T, V = hb.shape[0], wb.shape[0]
+        logits = gemm(hb, wb, out_f32=True)
+        tg = targets.reshape(-1).contiguous().to(torch.int64)
+        loss = torch.empty((T,), dtype=F32, device=hb.device)
+        lse = torch.empty((T,), dtype=F32, device=hb.device)
+        call("rte_ce_fwd", ptr(logits), V, T, V, ptr(tg), ptr(loss), ptr(lse), _s())
+        ctx.save_for_backward(hb, wb, logits, tg, lse)
+        ctx.meta = (shape, hidden.dtype, w.dtype)
+        return logits.view(*shape[:-1], V), loss.view(shape[:-1])
+
+    @staticmethod
+    def backward(ctx, dlogits_ext, dloss):
+        hb, wb, logits, tg, lse = ctx.saved_tensors
+        shape, h_dt, w_dt = ctx.meta
+        T, V = logits.shape
+        ext = None if dlogits_ext is None else dlogits_ext.reshape(T, V).contiguous().to(F32)
+        g = None if dloss is None else dloss.reshape(T).contiguous().to(F32)
+        dl = torch.empty((T, V), dtype=BF16, device=hb.device)
+        call("rte_ce_bwd", ptr(logits), V, T, V, ptr(tg), ptr(lse), ptr(g), ptr(ext), ptr(dl), _s())
+        dh = gemm(dl, wb, b_t=True)                              # [T, d] = dlogits @ W
+        dw = gemm(dl, hb, a_t=True, b_t=True, out_f32=True)      # [V, d] = dlogits^T @ hidden
+        return dh.view(shape).to(h_dt), dw.to(w_dt), None
+
+
+def lm_head_ce(hidden, w, targets):
+    """(logits fp32, per-token cross-entropy) of hidden @ W^T against targets."""
+    return LMHeadCEFn.apply(hidden, w, targets)
+
+
+# ----------------------------------------------------------------------------- SVD low-rank SwiGLU FFN
+
+class SVDFFNFn(torch.autograd.Function):
+    """y = resid + SwiGLU FFN whose up / gate / down weights are rank-r factors.
+
+    us_ug [d, 2r] = [U_up S_up | U_gate S_gate], v_ug [2F, r] = [V_up ; V_gate],
+    v_dn [F, r], us_dn [d, r] = U_dn S_dn.  Four MFMA GEMMs forward (the expand GEMM
+    fuses SwiGLU and reads each half's low-rank code), eleven backward."""
+
+    @staticmethod
+    def forward(ctx, x, us_ug, v_ug, v_dn, us_dn, resid):
+        _lib.require_device_tensors("svd_ffn", x, us_ug, v_ug, v_dn, us_dn, resid)
+        shape = x.shape
+        d = shape[-1]
+        xb = x.reshape(-1, d).contiguous().to(BF16)
+        T = xb.shape[0]
+        r = us_dn.shape[1]
+        F = v_dn.shape[0]
+        w = [cast_bf16(t) for t in (us_ug, v_ug, v_dn, us_dn)]
+        dev = x.device
+        a_ug = torch.empty((T, 2 * r), dtype=BF16, device=dev)
+        ug = torch.empty((T, 2 * F), dtype=BF16, device=dev)
+        z = torch.empty((T, F), dtype=BF16, device=dev)
+        b = torch.empty((T, r), dtype=BF16, device=dev)
+        y = torch.empty((T, d), dtype=F32, device=dev)
+        rs = None if resid is None else resid.reshape(T, d).contiguous().to(F32)
+        call("rte_svd_ffn_fwd", ptr(xb), T, d, F, r, *[ptr(t) for t in w], ptr(rs), ptr(a_ug), ptr(ug), ptr(z),
+             ptr(b), ptr(y), 1, _s())
+        ctx.save_for_backward(xb, *w, a_ug, ug, z, b)
+        ctx.meta = (shape, r, F, resid is not None, [t.dtype for t in (us_ug, v_ug, v_dn, us_dn)])
+        return y.view(shape)
+
+    @staticmethod
+    def backward(ctx, dy):
+        xb, us_ug, v_ug, v_dn, us_dn, a_ug, ug, z, b = ctx.saved_tensors
+        shape, r, F, has_resid, dts = ctx.meta
+        T, d = xb.shape
+        dev = xb.device
+        dyb = cast_bf16(dy.reshape(T, d))
+        db = torch.empty((T, r), dtype=BF16, device=dev)
+        dug = torch.empty((T, 2 * F), dtype=BF16, device=dev)
+        da = torch.empty((T, 2 * r), dtype=BF16, device=dev)
+        dx = torch.empty((T, d), dtype=BF16, device=dev)
+        g = [torch.empty(t.shape, dtype=F32, device=dev) for t in (us_ug, v_ug, v_dn, us_dn)]
+        wsp, wsn = _gemm_ws(max(d, F), 2 * r, T, dev)
+        call("rte_svd_ffn_bwd", ptr(dyb), ptr(xb), T, d, F, r, ptr(us_ug), ptr(v_ug), ptr(v_dn), ptr(us_dn),
+             ptr(a_ug), ptr(ug), ptr(z), ptr(b), ptr(db), ptr(dug), ptr(da), ptr(dx), *[ptr(t) for t in g],
+             wsp, wsn, _s())
+        return (dx.view(shape), *[t.to(dt) for t, dt in zip(g, dts)], dy if has_resid else None)
+
+
+def svd_ffn(x, us_ug, v_ug, v_dn, us_dn, resid=None):
+    return SVDFFNFn.apply(x, us_ug, v_ug, v_dn, us_dn, resid)

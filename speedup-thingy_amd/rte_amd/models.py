@@ -15,6 +15,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from rte_amd.config import ModelConfig, OutputConfig
+from rte_amd.kernels import hip_ops
 from rte_amd.kernels import optimized as K
 from rte_amd.layers import BankedRecursiveCore, RMSNorm, TransformerBlock
 from rte_amd.macro import MacroOperators, MacroTrace
@@ -52,6 +53,14 @@ def lm_loss_per_sample(logits: torch.Tensor, targets: torch.Tensor) -> torch.Ten
     return tok.view_as(targets).sum(dim=-1)
 
 
+def head_logits_loss(hidden, vocab_weight, targets):
+    """(logits, per-sample CE) with the HIP LM-head GEMM + fused CE kernels; targets may be None."""
+    if targets is None:
+        return K.k_logits_full(hidden, vocab_weight), None
+    logits, tok = hip_ops.lm_head_ce(hidden, vocab_weight, targets)
+    return logits, tok.sum(dim=-1)
+
+
 class DenseModel(nn.Module):
     def __init__(self, config: ModelConfig):
         super().__init__()
@@ -72,8 +81,7 @@ class DenseModel(nn.Module):
         for block in self.blocks:
             x = block(x)
         hidden = self.final_norm(x)
-        logits = K.k_logits_full(hidden, self.vocab_weight)
-        lps = lm_loss_per_sample(logits, targets) if targets is not None else None
+        logits, lps = head_logits_loss(hidden, self.vocab_weight, targets)
         return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
                            ModelMeta(hidden=hidden, logits=logits))
 
@@ -132,8 +140,8 @@ class RecursiveModel(nn.Module):
             h = self.core.forward_step(h, h0, rid, active, pass_idx=t, host_ids=host_ids, host_active=host_active)
             if return_states and (t + 1) in self.config.depth_choices:
                 states[t + 1] = h.clone()
-        hidden, logits = self._coda_logits(h)
-        lps = lm_loss_per_sample(logits, targets) if targets is not None else None
+        hidden = self._coda_hidden(h)
+        logits, lps = head_logits_loss(hidden, self.vocab_weight, targets)
         meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
                          hidden=hidden, logits=logits, states=states if return_states else None,
                          active_touches=self.active_touch_table[route.recipe_id])
@@ -168,9 +176,9 @@ class RecursiveModel(nn.Module):
             sl = self.shortlist_head.loss(hidden, targets, self.vocab_weight, seed=seed)
             lps, logits = sl.loss_per_sample, sl.logits
         else:
-            hidden, full_logits = self._coda_logits(h)
+            hidden = self._coda_hidden(h)
+            full_logits, lps = head_logits_loss(hidden, self.vocab_weight, targets)
             logits = full_logits
-            lps = lm_loss_per_sample(full_logits, targets) if targets is not None else None
         meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
                          hidden=hidden, logits=full_logits, states=trace.states if return_states else None,
                          macro_trace=trace, shortlist=sl, active_touches=self.active_touch_table[route.recipe_id])

@@ -281,3 +281,64 @@ def test_attn_out_proj_strided_input():
     db = bf16_round(dout).reshape(B * S, d).astype(np.float64)
     assert_rel(_np(ty.grad.transpose(1, 2)).reshape(B * S, d), db @ bf16_round(w), BF16_RTOL, "oproj dy")
     assert_rel(_np(tw.grad), db.T @ y2, 1e-5, "oproj dw")
+
+
+# ---------------------------------------------------------------- SVD low-rank FFN
+
+@pytest.mark.parametrize("T,d,F,r", [(256, 128, 256, 32), (4096, 1024, 4096, 128)])
+def test_svd_ffn_fwd_bwd(T, d, F, r):
+    from oracle import svd_ffn as SV
+
+    H = _ops()
+    rng = np.random.default_rng(T + r)
+
+    def orth(n, k):
+        q, _ = np.linalg.qr(rng.standard_normal((n, k)))
+        return q
+
+    S = [10 ** rng.uniform(-2, 0, r) for _ in range(3)]
+    m = dict(us_up=orth(d, r) * S[0], us_gate=orth(d, r) * S[1], v_up=orth(F, r), v_gate=orth(F, r),
+             v_dn=orth(F, r), us_dn=orth(d, r) * S[2])
+    m = {k: bf16_round(v.astype(np.float32)) for k, v in m.items()}
+    x = bf16_round(rng.standard_normal((T, d)).astype(np.float32))
+    dy = bf16_round(rng.standard_normal((T, d)).astype(np.float32))
+    tw = {k: torch.from_numpy(v).to(DEV).requires_grad_() for k, v in m.items()}
+    tx = _bf(x).requires_grad_()
+    us_ug = torch.cat([tw["us_up"], tw["us_gate"]], 1)
+    v_ug = torch.cat([tw["v_up"], tw["v_gate"]], 0)
+    print(f"svd_ffn T={T} d={d} F={F} r={r}", flush=True)
+    y = H.svd_ffn(tx, us_ug, v_ug, tw["v_dn"], tw["us_dn"])
+    y.backward(torch.from_numpy(dy).to(DEV))
+    ref, c = SV.svd_ffn_fwd(x, **m)
+    assert_rel(_np(y), ref, BF16_RTOL, "svd y")
+    g = SV.svd_ffn_bwd(dy, x, **m, c=c)
+    assert_rel(_np(tx.grad), g["dx"], BF16_RTOL, "svd dx")
+    for k in m:
+        assert_rel(_np(tw[k].grad), g["d" + k], BF16_RTOL, f"svd d{k}")
+
+
+# ---------------------------------------------------------------- LM head + cross-entropy
+
+@pytest.mark.parametrize("T,d,V", [(64, 64, 128), (8192, 512, 2048)])
+def test_lm_head_ce_fwd_bwd(T, d, V):
+    from oracle import losses as L
+
+    H = _ops()
+    rng = np.random.default_rng(T + V)
+    h = bf16_round(rng.standard_normal((T, d)).astype(np.float32))
+    w = (rng.standard_normal((V, d)) * 0.05).astype(np.float32)
+    tg = rng.integers(0, V, T)
+    gl = rng.standard_normal(T).astype(np.float32)
+    ext = (rng.standard_normal((T, V)) * 1e-3).astype(np.float32)
+    th = _bf(h).requires_grad_()
+    tw = torch.from_numpy(w).to(DEV).requires_grad_()
+    logits, loss = H.lm_head_ce(th, tw, torch.from_numpy(tg).to(DEV))
+    torch.autograd.backward([loss, logits], [torch.from_numpy(gl).to(DEV), torch.from_numpy(ext).to(DEV)])
+    wb = bf16_round(w).astype(np.float64)
+    ref_logits = h.astype(np.float64) @ wb.T
+    assert_rel(_np(logits), ref_logits, FP32_RTOL, "logits")
+    rl, _, rg = L.cross_entropy(_np(logits), tg)
+    assert_rel(_np(loss), rl, FP32_RTOL, "ce loss")
+    dlog = gl[:, None] * rg + ext
+    assert_rel(_np(th.grad), dlog @ wb, BF16_RTOL, "head dhidden")
+    assert_rel(_np(tw.grad), dlog.T @ h, BF16_RTOL, "head dW")

@@ -280,3 +280,93 @@ def test_qkv_rope_backward_matches_torch():
     dx, dw = A.qkv_rope_bwd(dq, dk, dv, x, w, cos, sin)
     np.testing.assert_allclose(dx, tx.grad.numpy(), rtol=1e-10, atol=1e-12)
     np.testing.assert_allclose(dw, tw.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
+# ---------------------------------------------------------------- SVD low-rank FFN
+
+def _svd_problem(seed, T=6, d=8, F=12, r=3):
+    rng = _rng(seed)
+    x = rng.standard_normal((T, d))
+    mats = dict(us_up=rng.standard_normal((d, r)), us_gate=rng.standard_normal((d, r)),
+                v_up=rng.standard_normal((F, r)), v_gate=rng.standard_normal((F, r)),
+                v_dn=rng.standard_normal((F, r)), us_dn=rng.standard_normal((d, r)))
+    return x, {k: v * 0.3 for k, v in mats.items()}
+
+
+def test_svd_ffn_equals_dense_on_reconstructed_weights():
+    from oracle import svd_ffn as SV
+
+    x, m = _svd_problem(20)
+    y, _ = SV.svd_ffn_fwd(x, **m)
+    w_up = (m["us_up"] @ m["v_up"].T).T       # nn.Linear layout [F, d]
+    w_gate = (m["us_gate"] @ m["v_gate"].T).T
+    wd_rows = m["v_dn"] @ m["us_dn"].T          # [F, d]
+    dense, _ = SW.dense_swiglu_fwd(x, np.concatenate([w_up, w_gate]), wd_rows, wd_rows=True)
+    np.testing.assert_allclose(y, dense, rtol=1e-10, atol=1e-12)
+
+
+def test_svd_full_rank_factors_reproduce_dense_ffn():
+    # reference invariant (tests/test_models_and_training.py:54-67): full rank == dense
+    from oracle import svd_ffn as SV
+
+    rng = _rng(21)
+    d, F, T = 6, 10, 7
+    w_up, w_gate = rng.standard_normal((F, d)), rng.standard_normal((F, d))
+    wd = rng.standard_normal((d, F))
+    x = rng.standard_normal((T, d))
+
+    def factors(w_in_major):  # refresh_svd: A = U S, B = Vh (rte/layers.py:437-444)
+        u, s, vh = np.linalg.svd(w_in_major, full_matrices=False)
+        return u * s, vh.T
+
+    us_up, v_up = factors(w_up.T)
+    us_gate, v_gate = factors(w_gate.T)
+    vd, usd = factors(wd.T)  # W_down = wd^T (F x d) = (U S) Vh: v_dn = U S, us_dn = Vh^T
+    y, _ = SV.svd_ffn_fwd(x, us_up, us_gate, v_up, v_gate, vd, usd)
+    dense, _ = SW.dense_swiglu_fwd(x, np.concatenate([w_up, w_gate]), wd)
+    np.testing.assert_allclose(y, dense, rtol=1e-9, atol=1e-10)
+
+
+def test_svd_ffn_backward_matches_torch():
+    from oracle import svd_ffn as SV
+
+    x, m = _svd_problem(22)
+    dy = _rng(23).standard_normal((x.shape[0], x.shape[1]))
+    y, c = SV.svd_ffn_fwd(x, **m)
+    g = SV.svd_ffn_bwd(dy, x, **m, c=c)
+    t = {k: torch.tensor(v, requires_grad=True) for k, v in m.items()}
+    tx = torch.tensor(x, requires_grad=True)
+    up = (tx @ t["us_up"]) @ t["v_up"].t()
+    gate = (tx @ t["us_gate"]) @ t["v_gate"].t()
+    ty = ((up * torch.nn.functional.silu(gate)) @ t["v_dn"]) @ t["us_dn"].t()
+    ty.backward(torch.tensor(dy))
+    np.testing.assert_allclose(g["dx"], tx.grad.numpy(), rtol=1e-9, atol=1e-11)
+    for k in m:
+        np.testing.assert_allclose(g["d" + k], t[k].grad.numpy(), rtol=1e-9, atol=1e-11, err_msg=k)
+
+
+# ---------------------------------------------------------------- losses
+
+def test_cross_entropy_matches_torch():
+    from oracle import losses as L
+
+    rng = _rng(24)
+    lg = rng.standard_normal((9, 17)) * 3
+    tg = rng.integers(0, 17, 9)
+    loss, lse, grad = L.cross_entropy(lg, tg)
+    tl = torch.tensor(lg, requires_grad=True)
+    tt = torch.nn.functional.cross_entropy(tl, torch.tensor(tg), reduction="none")
+    tt.sum().backward()
+    np.testing.assert_allclose(loss, tt.detach().numpy(), rtol=1e-12)
+    np.testing.assert_allclose(grad, tl.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(lse, torch.logsumexp(tl, -1).detach().numpy(), rtol=1e-12)
+
+
+def test_audit_correction_p1_is_exact():
+    from oracle import losses as L
+
+    hot, exact = np.array([1.0, 2.0]), np.array([1.5, 1.0])
+    np.testing.assert_allclose(L.audit_corrected(hot, exact, np.ones(2)), exact)
+    # unbiased: E[hot + mask (exact-hot)/p] = exact for inclusion probability p
+    p = 0.25
+    np.testing.assert_allclose(hot + p * (exact - hot) / p, exact)
