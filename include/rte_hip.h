@@ -177,6 +177,31 @@ int rte_ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* tar
 int rte_ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
                const float* dloss, const float* extra, void* dlogits, void* stream);
 
+/* ---- shortlist output head (rte/output.py:46-136, rte/kernels/reference.py:141-147) ----
+ * build: replaces ShortlistHead.build_shortlist / _dedupe_preserve_first (rte/output.py:46-110).
+ *   Candidates per token t, in order: targets[t]; members[top_clusters[t, c], :] for c < tc
+ *   (members int64 [n_clusters, per_cluster], the padded table of rte/output.py:30-40);
+ *   arange(H) % V; random_negs[t, :R]; arange(L) % V; (targets[t] + arange(2L)) % V.
+ *   shortlist int32 [T, L] = the first L distinct ids in that order (target at 0);
+ *   dup_per_token int32 [T] = candidates - distinct candidates (sum = duplicate_count).
+ *   Requires 1 <= L <= V <= 65536. */
+int rte_shortlist_build(const int64_t* targets, const int32_t* top_clusters, int tc, const int64_t* members,
+                        int n_clusters, int per_cluster, const int64_t* random_negs, int R, int H, int L, int V,
+                        int T, int32_t* shortlist, int32_t* dup_per_token, void* stream);
+/* fwd: replaces k_logits_shortlist (rte/kernels/reference.py:141-143) + the CE at target position 0
+ * (rte/output.py:125-129).  hidden bf16 [T, d], W bf16 [V, d], d % 8 == 0, d <= 2048, L <= 4096.
+ * logits f32 [T, L] = hidden . W[shortlist]; lse f32 [T]; loss f32 [T] = lse - logits[:, 0]. */
+int rte_shortlist_fwd(const void* hidden, const void* W, int d, int V, const int32_t* shortlist, int L, int T,
+                      float* logits, float* lse, float* loss, void* stream);
+size_t rte_shortlist_bwd_workspace_bytes(int T, int L, int V, int d);
+/* bwd: g = dloss[t] (softmax - e_0) + dlogits (both optional); dhidden bf16 [T, d] (optional) =
+ * g . W[shortlist]; dW f32 [V, d] (optional, V <= 32768; overwritten unless dW_accumulate) gets
+ * the per-row sums of g * hidden in ascending (t, j) order (deterministic, no atomics). */
+int rte_shortlist_bwd(const float* dloss, const float* dlogits, const void* hidden, const void* W, int d, int V,
+                      const int32_t* shortlist, int L, int T, const float* logits, const float* lse,
+                      void* dhidden, float* dW, int dW_accumulate, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
 /* fp32 -> bf16 (round to nearest even) */
 int rte_cast_f32_bf16(const float* x, int64_t n, void* y, void* stream);
 

@@ -31,6 +31,15 @@ int ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets
            hipStream_t s);
 int ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse, const float* g,
            const float* extra, bf16* dlogits, hipStream_t s);
+int shortlist_build(const int64_t* targets, const int32_t* top_clusters, int tc, const int64_t* members,
+                    int n_clusters, int per_cluster, const int64_t* random_negs, int R, int H, int L, int V, int T,
+                    int32_t* shortlist, int32_t* dup_per_token, hipStream_t s);
+int shortlist_fwd(const bf16* hidden, const bf16* W, int d, int V, const int32_t* sl, int L, int T, float* logits,
+                  float* lse, float* loss, hipStream_t s);
+size_t shortlist_bwd_workspace_bytes(int T, int L, int V, int d);
+int shortlist_bwd(const float* dloss, const float* dlext, const bf16* hidden, const bf16* W, int d, int V,
+                  const int32_t* sl, int L, int T, const float* logits, const float* lse, bf16* dhidden, float* dW,
+                  int dW_accumulate, void* ws, size_t ws_bytes, hipStream_t s);
 }  // namespace rte
 
 using namespace rte;
@@ -697,6 +706,30 @@ int rte_ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* tar
 
 int rte_cast_f32_bf16(const float* x, int64_t n, void* y, void* stream) {
   return cast_f32_bf16(x, n, B16(y), S(stream));
+}
+
+int rte_shortlist_build(const int64_t* targets, const int32_t* top_clusters, int tc, const int64_t* members,
+                        int n_clusters, int per_cluster, const int64_t* random_negs, int R, int H, int L, int V,
+                        int T, int32_t* shortlist, int32_t* dup_per_token, void* stream) {
+  return shortlist_build(targets, top_clusters, tc, members, n_clusters, per_cluster, random_negs, R, H, L, V, T,
+                         shortlist, dup_per_token, S(stream));
+}
+
+int rte_shortlist_fwd(const void* hidden, const void* W, int d, int V, const int32_t* shortlist, int L, int T,
+                      float* logits, float* lse, float* loss, void* stream) {
+  return shortlist_fwd(B16(hidden), B16(W), d, V, shortlist, L, T, logits, lse, loss, S(stream));
+}
+
+size_t rte_shortlist_bwd_workspace_bytes(int T, int L, int V, int d) {
+  return shortlist_bwd_workspace_bytes(T, L, V, d);
+}
+
+int rte_shortlist_bwd(const float* dloss, const float* dlogits, const void* hidden, const void* W, int d, int V,
+                      const int32_t* shortlist, int L, int T, const float* logits, const float* lse,
+                      void* dhidden, float* dW, int dW_accumulate, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  return shortlist_bwd(dloss, dlogits, B16(hidden), B16(W), d, V, shortlist, L, T, logits, lse,
+                       static_cast<bf16*>(dhidden), dW, dW_accumulate, workspace, workspace_bytes, S(stream));
 }
 
 }  // extern "C"

@@ -517,6 +517,73 @@ def lm_head_ce(hidden, w, targets):
     return LMHeadCEFn.apply(hidden, w, targets)
 
 
+# ----------------------------------------------------------------------------- shortlist output head
+
+def shortlist_build(targets, top_clusters, members, hard_negatives: int, random_negs, max_tokens: int,
+                    vocab_size: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """First max_tokens distinct ids of [target | top-cluster members | hard | random | filler |
+    target filler] per token (rte/output.py:46-110).  Returns (shortlist int32 [..., L],
+    dup_per_token int32 [...]); the target sits at position 0."""
+    _lib.require_device_tensors("shortlist_build", targets, top_clusters, members, random_negs)
+    shape = targets.shape
+    tg = targets.reshape(-1).contiguous().to(torch.int64)
+    T = tg.shape[0]
+    top = top_clusters.reshape(T, top_clusters.shape[-1]).contiguous().to(torch.int32)
+    mem = members.contiguous().to(torch.int64)
+    rnd = random_negs.reshape(T, random_negs.shape[-1]).contiguous().to(torch.int64)
+    sl = torch.empty((T, max_tokens), dtype=torch.int32, device=tg.device)
+    dup = torch.empty((T,), dtype=torch.int32, device=tg.device)
+    call("rte_shortlist_build", ptr(tg), ptr(top), top.shape[1], ptr(mem), mem.shape[0], mem.shape[1], ptr(rnd),
+         rnd.shape[1], int(hard_negatives), int(max_tokens), int(vocab_size), T, ptr(sl), ptr(dup), _s())
+    return sl.view(*shape, max_tokens), dup.view(shape)
+
+
+class ShortlistCEFn(torch.autograd.Function):
+    """Shortlist logits hidden . W[shortlist] (fp32) and the per-token CE against position 0
+    in one kernel; the backward fuses the CE gradient with any gradient on the logits and
+    reduces the vocabulary-row gradient deterministically."""
+
+    @staticmethod
+    def forward(ctx, hidden, w, shortlist):
+        _lib.require_device_tensors("shortlist_ce", hidden, w, shortlist)
+        shape = hidden.shape
+        d = shape[-1]
+        hb = hidden.reshape(-1, d).contiguous().to(BF16)
+        wb = cast_bf16(w)
+        T, V = hb.shape[0], wb.shape[0]
+        sl = shortlist.reshape(T, -1).contiguous().to(torch.int32)
+        L = sl.shape[1]
+        logits = torch.empty((T, L), dtype=F32, device=hb.device)
+        lse = torch.empty((T,), dtype=F32, device=hb.device)
+        loss = torch.empty((T,), dtype=F32, device=hb.device)
+        call("rte_shortlist_fwd", ptr(hb), ptr(wb), d, V, ptr(sl), L, T, ptr(logits), ptr(lse), ptr(loss), _s())
+        ctx.save_for_backward(hb, wb, sl, logits, lse)
+        ctx.meta = (shape, hidden.dtype, w.dtype)
+        return logits.view(*shape[:-1], L), loss.view(shape[:-1])
+
+    @staticmethod
+    def backward(ctx, dlogits_ext, dloss):
+        hb, wb, sl, logits, lse = ctx.saved_tensors
+        shape, h_dt, w_dt = ctx.meta
+        T, L = logits.shape
+        V, d = wb.shape
+        ext = None if dlogits_ext is None else dlogits_ext.reshape(T, L).contiguous().to(F32)
+        g = None if dloss is None else dloss.reshape(T).contiguous().to(F32)
+        need_h, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dh = torch.empty((T, d), dtype=BF16, device=hb.device) if need_h else None
+        dw = torch.empty((V, d), dtype=F32, device=hb.device) if need_w else None
+        ws, nb = workspace(_lib.load().rte_shortlist_bwd_workspace_bytes(T, L, V, d), hb.device)
+        call("rte_shortlist_bwd", ptr(g), ptr(ext), ptr(hb), ptr(wb), d, V, ptr(sl), L, T, ptr(logits), ptr(lse),
+             ptr(dh), ptr(dw), 0, ws, nb, _s())
+        return (None if dh is None else dh.view(shape).to(h_dt),
+                None if dw is None else dw.to(w_dt), None)
+
+
+def shortlist_ce(hidden, w, shortlist):
+    """(shortlist logits fp32 [..., L], per-token CE against position 0 [...])."""
+    return ShortlistCEFn.apply(hidden, w, shortlist)
+
+
 # ----------------------------------------------------------------------------- SVD low-rank SwiGLU FFN
 
 class SVDFFNFn(torch.autograd.Function):

@@ -36,7 +36,7 @@ SYMBOLS: dict[str, str] = {
     "k_macro_phi": "torch",
     "k_recurrent_exact_loop": "python",
     "k_logits_full": "hip",
-    "k_logits_shortlist": "torch",
+    "k_logits_shortlist": "hip",
     "k_cross_entropy_unreduced": "torch",
     "k_sample_audit_mask": "torch",
     "k_metrics_reduce": "torch",
@@ -226,9 +226,10 @@ def k_recurrent_exact_loop(step_fn, h, h0, depth: int, boundaries: set[int]):
 
 
 def k_logits_shortlist(hidden, vocab_weight, shortlist):
+    """hidden . vocab_weight[shortlist] (rte/kernels/reference.py:141-143) on the shortlist kernel
+    (fp32 logits from bf16 operands; the kernel's CE at position 0 is discarded here)."""
     _require_cuda_tensor(hidden, vocab_weight, shortlist)
-    rows = vocab_weight[shortlist]
-    return (hidden.unsqueeze(-2) * rows).sum(dim=-1)
+    return hip_ops.shortlist_ce(hidden, vocab_weight, shortlist)[0]
 
 
 def k_cross_entropy_unreduced(logits, targets):

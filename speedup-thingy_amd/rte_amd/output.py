@@ -1,18 +1,21 @@
 """Shortlist output head (rte/output.py:13-136): per token, a fixed-width candidate list
 [target, members of the top vocab clusters, hard negatives, random negatives, fillers],
 first occurrences kept in order, logits only over the shortlist, target at position 0.
-Torch ops on the device for now."""
+
+The cluster router runs on the MFMA GEMM, the cluster top-k on the routing kernel, the
+candidate build + dedupe, the shortlist logits and their cross-entropy on the shortlist
+kernels.  The random negatives stay a torch draw from a device generator seeded with
+``seed`` (rte/output.py:86-94), so they follow the same RNG stream as the reference."""
 
 from __future__ import annotations
 
 from dataclasses import dataclass
 
 import torch
-import torch.nn.functional as F
 from torch import nn
 
 from rte_amd.config import OutputConfig
-from rte_amd.kernels import optimized as K
+from rte_amd.kernels import hip_ops
 
 
 @dataclass(slots=True)
@@ -46,36 +49,39 @@ class ShortlistHead(nn.Module):
         self.register_buffer("hard_negative_cache", torch.arange(config.hard_negatives) % vocab_size, persistent=False)
         self.register_buffer("shortlist_filler", torch.arange(config.shortlist_max_tokens) % vocab_size, persistent=False)
 
-    def _dedupe_preserve_first(self, candidates, max_tokens):
-        width = candidates.shape[-1]
-        flat = candidates.reshape(-1, width).long()
-        pos = torch.arange(width, device=candidates.device, dtype=torch.float32).view(1, -1)
-        first = torch.full((flat.shape[0], self.vocab_size), float(width + max_tokens), dtype=torch.float32,
-                           device=candidates.device)
-        first.scatter_reduce_(1, flat, pos.expand_as(flat), reduce="amin", include_self=True)
-        duplicate_count = (width - (first < width).sum(dim=-1)).float().sum()
-        _, shortlist = first.topk(k=max_tokens, dim=-1, largest=False, sorted=True)
-        return shortlist.view(*candidates.shape[:-1], max_tokens).contiguous(), duplicate_count
+    def cluster_logits(self, hidden: torch.Tensor) -> torch.Tensor:
+        """hidden @ W_router^T in fp32 on the MFMA GEMM (rte/output.py:81).  No loss reads the
+        cluster logits in the reference, so they carry no gradient here either."""
+        w = self.cluster_router.weight.detach()
+        C = w.shape[0]
+        pad = (-C) % 8
+        if pad:
+            w = torch.cat([w, w.new_zeros(pad, w.shape[1])])
+        with torch.no_grad():
+            lg = hip_ops.linear(hidden.detach(), w, out_f32=True)
+        return lg[..., :C].contiguous() if pad else lg
 
     def build_shortlist(self, hidden, targets, *, seed: int):
+        """(shortlist int64 [b, s, L], target positions (zeros), cluster logits, duplicate count)."""
+        sl, cl, dup = self._build(hidden, targets, seed)
+        return sl.long(), torch.zeros_like(targets, dtype=torch.long), cl, dup.sum().float()
+
+    def _build(self, hidden, targets, seed: int):
         b, s, _ = hidden.shape
         dev = hidden.device
-        cluster_logits = self.cluster_router(hidden)
-        top = cluster_logits.topk(k=min(self.config.shortlist_top_clusters, self.config.num_clusters), dim=-1).indices
-        L = self.config.shortlist_max_tokens
+        cl = self.cluster_logits(hidden)
+        k = min(self.config.shortlist_top_clusters, self.config.num_clusters)
+        top, _ = hip_ops.route_topk(cl.reshape(b * s, -1), k)
         gen = torch.Generator(device=dev)
         gen.manual_seed(seed)
         rnd = torch.randint(0, self.vocab_size, (b, s, self.config.random_negatives), device=dev, generator=gen)
-        members = self.cluster_members[top].flatten(start_dim=-2)
-        hard = self.hard_negative_cache.view(1, 1, -1).expand(b, s, -1)
-        filler = self.shortlist_filler.view(1, 1, -1).expand(b, s, -1)
-        tfill = (targets.unsqueeze(-1) + torch.arange(2 * L, device=dev).view(1, 1, -1)) % self.vocab_size
-        cand = torch.cat([targets.unsqueeze(-1), members, hard, rnd, filler, tfill], dim=-1)
-        shortlist, dup = self._dedupe_preserve_first(cand, L)
-        return shortlist, torch.zeros(b, s, dtype=torch.long, device=dev), cluster_logits, dup
+        sl, dup = hip_ops.shortlist_build(targets, top, self.cluster_members, self.config.hard_negatives, rnd,
+                                          self.config.shortlist_max_tokens, self.vocab_size)
+        return sl, cl, dup
 
     def loss(self, hidden, targets, vocab_weight, *, seed: int) -> ShortlistResult:
-        shortlist, tpos, cl, dup = self.build_shortlist(hidden, targets, seed=seed)
-        logits = K.k_logits_shortlist(hidden, vocab_weight, shortlist)
-        tok = F.cross_entropy(logits.float().flatten(0, -2), tpos.flatten(), reduction="none").view_as(targets)
-        return ShortlistResult(tok.sum(dim=-1), logits, shortlist, tpos, cl, dup)
+        """Per-sample CE over the shortlist logits (rte/output.py:112-136)."""
+        sl, cl, dup = self._build(hidden, targets, seed)
+        logits, tok = hip_ops.shortlist_ce(hidden, vocab_weight, sl)
+        return ShortlistResult(tok.sum(dim=-1), logits, sl.long(), torch.zeros_like(targets, dtype=torch.long), cl,
+                               dup.sum().float())

@@ -342,3 +342,135 @@ def test_lm_head_ce_fwd_bwd(T, d, V):
     dlog = gl[:, None] * rg + ext
     assert_rel(_np(th.grad), dlog @ wb, BF16_RTOL, "head dhidden")
     assert_rel(_np(tw.grad), dlog.T @ h, BF16_RTOL, "head dW")
+
+
+# ---------------------------------------------------------------- shortlist head
+
+def _sl_inputs(T, V, C, tc, H, R, L, seed, skew=False):
+    from oracle import shortlist as SLO
+
+    rng = np.random.default_rng(seed)
+    members, _ = SLO.cluster_member_table(V, C)
+    targets = rng.integers(0, V, T)
+    top = np.stack([rng.permutation(C)[:tc] for _ in range(T)]).astype(np.int32)
+    rnd = rng.integers(0, min(V, 8) if skew else V, (T, R))
+    return SLO, members, targets, top, rnd
+
+
+@pytest.mark.parametrize("T,V,C,tc,H,R,L", [
+    (300, 97, 7, 2, 9, 11, 16),          # small, many duplicates across segments
+    (257, 20, 3, 3, 40, 5, 15),          # V < 2L: the target filler wraps the vocabulary
+    (4096, 8192, 64, 2, 32, 32, 128),    # the scaled shortlist configuration's widths
+    (256, 65536, 64, 2, 32, 32, 128),    # largest vocabulary of the LDS bitmap
+    (130, 512, 16, 0, 0, 0, 100),        # no members / negatives: fillers only
+])
+def test_shortlist_build_bit_exact(T, V, C, tc, H, R, L):
+    H_ = _ops()
+    SLO, members, targets, top, rnd = _sl_inputs(T, V, C, tc, H, R, L, seed=T + V, skew=(V == 97))
+    print(f"shortlist_build T={T} V={V} C={C} tc={tc} H={H} R={R} L={L}", flush=True)
+    sl, dup = H_.shortlist_build(torch.from_numpy(targets).to(DEV), torch.from_numpy(top).to(DEV),
+                                 torch.from_numpy(members).to(DEV), H, torch.from_numpy(rnd).to(DEV), L, V)
+    want, want_dup = SLO.build_shortlist(targets, top, members, H, rnd, L, V)
+    np.testing.assert_array_equal(sl.cpu().numpy(), want)
+    np.testing.assert_array_equal(dup.cpu().numpy(), want_dup)
+
+
+@pytest.mark.parametrize("T,d,V,L", [(512, 256, 1000, 64), (333, 1024, 4096, 128), (200, 200, 300, 70),
+                                     (64, 2048, 600, 40)])
+def test_shortlist_ce_fwd_bwd(T, d, V, L):
+    from oracle import shortlist as SLO
+
+    H_ = _ops()
+    rng = np.random.default_rng(T + d)
+    h = bf16_round(rng.standard_normal((T, d)).astype(np.float32))
+    w = bf16_round((rng.standard_normal((V, d)) * 0.05).astype(np.float32))
+    sl = np.stack([rng.permutation(V)[:L] for _ in range(T)]).astype(np.int32)
+    gl = rng.standard_normal(T).astype(np.float32)
+    ext = (rng.standard_normal((T, L)) * 1e-2).astype(np.float32)
+    print(f"shortlist_ce T={T} d={d} V={V} L={L}", flush=True)
+    th = _bf(h).requires_grad_()
+    tw = torch.from_numpy(w).to(DEV).requires_grad_()
+    logits, loss = H_.shortlist_ce(th, tw, torch.from_numpy(sl).to(DEV))
+    torch.autograd.backward([loss, logits], [torch.from_numpy(gl).to(DEV), torch.from_numpy(ext).to(DEV)])
+    rl, rlse, rloss = SLO.shortlist_logits_ce(h, w, sl)
+    assert_rel(_np(logits), rl, FP32_RTOL, "shortlist logits")
+    assert_rel(_np(loss), rloss, FP32_RTOL, "shortlist loss")
+    _, rdh, rdw = SLO.shortlist_logits_ce_bwd(h, w, sl, rl, rlse, gl, ext)
+    assert_rel(_np(th.grad), rdh, BF16_RTOL, "shortlist dhidden")
+    assert_rel(_np(tw.grad), rdw, FP32_RTOL, "shortlist dW")
+
+
+def test_shortlist_bwd_skewed_rows_deterministic_and_accumulate():
+    """Every token shares most shortlist ids (multi-chunk rows of the vocabulary reduction);
+    dW is bitwise repeatable and dW_accumulate adds onto the existing gradient."""
+    from oracle import shortlist as SLO
+    from rte_amd import _lib
+
+    H_ = _ops()
+    rng = np.random.default_rng(77)
+    T, d, V, L = 3000, 512, 700, 96
+    h = bf16_round(rng.standard_normal((T, d)).astype(np.float32))
+    w = bf16_round((rng.standard_normal((V, d)) * 0.05).astype(np.float32))
+    base = rng.permutation(V)[:L]
+    sl = np.stack([np.concatenate([base[:80], rng.permutation(np.setdiff1d(np.arange(V), base[:80]))[:16]])
+                   for _ in range(T)]).astype(np.int32)
+    gl = rng.standard_normal(T).astype(np.float32)
+    hb, wb, slt = _bf(h), _bf(w), torch.from_numpy(sl).to(DEV)
+    logits = torch.empty((T, L), dtype=torch.float32, device=DEV)
+    lse = torch.empty((T,), dtype=torch.float32, device=DEV)
+    loss = torch.empty((T,), dtype=torch.float32, device=DEV)
+    _lib.call("rte_shortlist_fwd", _lib.ptr(hb), _lib.ptr(wb), d, V, _lib.ptr(slt), L, T, _lib.ptr(logits),
+              _lib.ptr(lse), _lib.ptr(loss), _lib.stream_ptr())
+    g = torch.from_numpy(gl).to(DEV)
+    nb = _lib.load().rte_shortlist_bwd_workspace_bytes(T, L, V, d)
+    ws = torch.empty((nb,), dtype=torch.uint8, device=DEV)
+    outs = []
+    for acc in (0, 0, 1):
+        dw = torch.ones((V, d), dtype=torch.float32, device=DEV)
+        dh = torch.empty((T, d), dtype=torch.bfloat16, device=DEV)
+        _lib.call("rte_shortlist_bwd", _lib.ptr(g), None, _lib.ptr(hb), _lib.ptr(wb), d, V, _lib.ptr(slt), L, T,
+                  _lib.ptr(logits), _lib.ptr(lse), _lib.ptr(dh), _lib.ptr(dw), acc, _lib.ptr(ws), nb,
+                  _lib.stream_ptr())
+        outs.append(dw.cpu().numpy())
+    assert np.array_equal(outs[0], outs[1]), "dW not bitwise repeatable"
+    _, _, rdw = SLO.shortlist_logits_ce_bwd(h, w, sl, _np(logits), _np(lse), gl)
+    assert_rel(outs[0], rdw, FP32_RTOL, "skewed dW")
+    assert_rel(outs[2], rdw + 1.0, FP32_RTOL, "accumulated dW")
+
+
+def test_shortlist_head_matches_oracle():
+    """ShortlistHead.loss end to end: router top-k, seeded random negatives, build, logits, CE."""
+    from oracle import losses as LO
+    from oracle import routing as RO
+    from oracle import shortlist as SLO
+    from rte_amd.config import OutputConfig
+    from rte_amd.output import ShortlistHead
+
+    torch.manual_seed(0)
+    b, s, d, V = 4, 64, 256, 2048
+    cfg = OutputConfig(mode="shortlist", num_clusters=64, shortlist_top_clusters=2, shortlist_max_tokens=128,
+                       hard_negatives=32, random_negatives=32)
+    head = ShortlistHead(d, V, cfg).to(DEV)
+    hidden = torch.randn(b, s, d, device=DEV).to(torch.bfloat16)
+    targets = torch.randint(0, V, (b, s), device=DEV)
+    vw = (torch.randn(V, d, device=DEV) * 0.05).requires_grad_()
+    res = head.loss(hidden, targets, vw, seed=11)
+    cl = _np(res.cluster_logits).reshape(b * s, -1)
+    top, _ = RO.route_topk(cl, 2)
+    gen = torch.Generator(device=DEV)
+    gen.manual_seed(11)
+    rnd = torch.randint(0, V, (b, s, 32), device=DEV, generator=gen).cpu().numpy()
+    tg = targets.cpu().numpy().reshape(-1)
+    want, want_dup = SLO.build_shortlist(tg, top, head.cluster_members.cpu().numpy(), 32, rnd, 128, V)
+    np.testing.assert_array_equal(res.shortlist.cpu().numpy().reshape(-1, 128), want)
+    assert float(res.duplicate_count) == float(want_dup.sum())
+    np.testing.assert_array_equal(res.target_positions.cpu().numpy(), 0)
+    hb = _np(hidden).reshape(b * s, d)
+    wb = bf16_round(_np(vw))
+    rl, rlse, rloss = SLO.shortlist_logits_ce(hb, wb, want)
+    assert_rel(_np(res.logits).reshape(b * s, -1), rl, FP32_RTOL, "head logits")
+    assert_rel(_np(res.loss_per_sample), rloss.reshape(b, s).sum(-1), FP32_RTOL, "head loss per sample")
+    res.loss_per_sample.sum().backward()
+    _, _, rdw = SLO.shortlist_logits_ce_bwd(hb, wb, want, rl, rlse, np.ones(b * s))
+    assert_rel(_np(vw.grad), rdw, FP32_RTOL, "head dW")
+    _ = LO

@@ -370,3 +370,101 @@ def test_audit_correction_p1_is_exact():
     # unbiased: E[hot + mask (exact-hot)/p] = exact for inclusion probability p
     p = 0.25
     np.testing.assert_allclose(hot + p * (exact - hot) / p, exact)
+
+
+# ---------------------------------------------------------------- shortlist
+
+def _brute_first_distinct(row, L):
+    seen, out = set(), []
+    for v in row:
+        if v not in seen:
+            seen.add(v)
+            out.append(v)
+    return out[:L], len(row) - len(seen)
+
+
+def _shortlist_case(seed, T=24, V=97, C=7, tc=2, H=9, R=11, L=16):
+    from oracle import shortlist as SL
+
+    rng = _rng(seed)
+    members, _ = SL.cluster_member_table(V, C)
+    targets = rng.integers(0, V, T)
+    top = np.stack([rng.permutation(C)[:tc] for _ in range(T)])
+    rnd = rng.integers(0, V, (T, R))
+    return SL, members, targets, top, rnd, H, L, V
+
+
+def test_shortlist_member_table_partitions_vocab():
+    from oracle import shortlist as SL
+
+    members, counts = SL.cluster_member_table(23, 5)
+    assert members.shape == (5, 5) and counts.tolist() == [5, 5, 5, 4, 4]
+    got = sorted(int(members[c, i]) for c in range(5) for i in range(counts[c]))
+    assert got == list(range(23))
+    assert all(int(members[c, i]) % 5 == c for c in range(5) for i in range(counts[c]))
+    assert members[3, 4] == 0 and members[4, 4] == 0          # padding id of short clusters
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_shortlist_dedupe_matches_brute_force(seed):
+    SL, members, targets, top, rnd, H, L, V = _shortlist_case(seed)
+    cand = SL.build_candidates(targets, top, members, H, rnd, L, V)
+    assert cand.shape[1] == 1 + top.shape[1] * members.shape[1] + H + rnd.shape[1] + 3 * L
+    sl, dup = SL.dedupe_preserve_first(cand, L)
+    for t in range(cand.shape[0]):
+        want, want_dup = _brute_first_distinct(cand[t].tolist(), L)
+        assert sl[t].tolist() == want
+        assert dup[t] == want_dup
+
+
+def test_shortlist_dedupe_matches_reference_formulation():
+    """The reference keeps first occurrences with scatter_reduce(amin) over [T, V] first
+    positions and topk(largest=False, sorted=True) (rte/output.py:52-69); run that
+    formulation with torch on the CPU."""
+    SL, members, targets, top, rnd, H, L, V = _shortlist_case(5, T=40, V=61, C=4, tc=3, H=70, R=30, L=20)
+    cand = SL.build_candidates(targets, top, members, H, rnd, L, V)
+    width = cand.shape[1]
+    flat = torch.tensor(cand)
+    pos = torch.arange(width, dtype=torch.float32).view(1, -1).expand_as(flat)
+    first = torch.full((flat.shape[0], V), float(width + L))
+    first.scatter_reduce_(1, flat, pos, reduce="amin", include_self=True)
+    dup_ref = (width - (first < width).sum(-1)).numpy()
+    _, ref = first.topk(k=L, dim=-1, largest=False, sorted=True)
+    sl, dup = SL.dedupe_preserve_first(cand, L)
+    np.testing.assert_array_equal(sl, ref.numpy())
+    np.testing.assert_array_equal(dup, dup_ref)
+
+
+def test_shortlist_reference_invariants():
+    """Target at position 0 and L distinct ids per token (tests/test_models_and_training.py:465-477),
+    also when V < 2L so that the target filler wraps around the vocabulary."""
+    for V, L in ((97, 16), (20, 15), (15, 15)):
+        SL, members, targets, top, rnd, H, _, _ = _shortlist_case(9, V=V, L=L, C=3)
+        sl, dup = SL.build_shortlist(targets, top, members, H, rnd, L, V)
+        np.testing.assert_array_equal(sl[:, 0], targets)
+        assert all(len(set(row.tolist())) == L for row in sl)
+        assert (dup >= 0).all()
+
+
+def test_shortlist_logits_ce_and_backward_match_torch_autograd():
+    from oracle import shortlist as SL
+
+    rng = _rng(31)
+    T, V, d, L = 12, 40, 8, 6
+    h = rng.standard_normal((T, d))
+    w = rng.standard_normal((V, d))
+    sl = np.stack([rng.permutation(V)[:L] for _ in range(T)])
+    sl[:3, 1] = sl[3:6, 2]                                   # shared rows across tokens
+    dloss = rng.standard_normal(T)
+    dlog = rng.standard_normal((T, L))
+    logits, lse, loss = SL.shortlist_logits_ce(h, w, sl)
+    g, dh, dw = SL.shortlist_logits_ce_bwd(h, w, sl, logits, lse, dloss, dlog)
+    th = torch.tensor(h, requires_grad=True)
+    tw = torch.tensor(w, requires_grad=True)
+    tl = (th.unsqueeze(-2) * tw[torch.tensor(sl)]).sum(-1)  # rte/kernels/reference.py:142-143
+    tloss = torch.nn.functional.cross_entropy(tl, torch.zeros(T, dtype=torch.long), reduction="none")
+    (tloss * torch.tensor(dloss)).sum().add((tl * torch.tensor(dlog)).sum()).backward()
+    np.testing.assert_allclose(logits, tl.detach().numpy(), rtol=1e-12)
+    np.testing.assert_allclose(loss, tloss.detach().numpy(), rtol=1e-12)
+    np.testing.assert_allclose(dh, th.grad.numpy(), rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(dw, tw.grad.numpy(), rtol=1e-10, atol=1e-12)
