@@ -78,9 +78,11 @@ int rte_pack_index(const int32_t* cl, int P, int C, int k, const float* w, int32
 
 /* out[t] = resid[t] + extra[t] + sum_{j<k} rows[t*k + j]  (j ascending; fp32 accumulation)
  * rows, extra: bf16; resid: f32 (optional); out: f32 (out_f32=1) or bf16.
+ * slot_of_pair (optional, from rte_pack_index): pairs whose slot is -1 (invalid cluster id,
+ * dropped by the pack) are skipped, so their rows are never read.
  * Replaces _gather_y_kernel (rte/kernels/cluster_pool_ffn.py:69-87) plus the top-k sum. */
-int rte_combine_rows(const void* rows, int T, int k, int d, const void* extra, const float* resid,
-                     void* out, int out_f32, void* stream);
+int rte_combine_rows(const void* rows, int T, int k, int d, const int32_t* slot_of_pair, const void* extra,
+                     const float* resid, void* out, int out_f32, void* stream);
 
 /* Routing-weight backward: dlogits[t, ids[t,j]] = w_j (dw_j - sum_i w_i dw_i), zero elsewhere.
  * dw_slot is indexed by slot (slot_of_pair maps pairs).  Either output may be NULL. */

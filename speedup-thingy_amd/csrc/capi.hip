@@ -14,7 +14,8 @@ size_t pack_workspace_bytes(int P, int C);
 int pack_pairs(const int32_t* cl, int P, int C, int k, const float* w, int32_t* offsets,
                int32_t* tok_of_slot, int32_t* pair_of_slot, int32_t* slot_of_pair, float* w_of_slot,
                int32_t* invalid, void* ws, size_t ws_bytes, hipStream_t s);
-int combine_rows(const bf16* rows, int T, int k, int d, const bf16* extra, const float* resid, void* out,
+int combine_rows(const bf16* rows, int T, int k, int d, const int32_t* slot_of_pair, const bf16* extra,
+                 const float* resid, void* out,
                  int out_f32, hipStream_t s);
 int route_bwd(const int32_t* ids, const float* w, const float* dw_slot, const int32_t* slot_of_pair, int T,
               int C, int k, bf16* dlogits, float* dlogits_f32, hipStream_t s);
@@ -161,9 +162,9 @@ int rte_pack_index(const int32_t* cl, int P, int C, int k, const float* w, int32
                     workspace, workspace_bytes, S(stream));
 }
 
-int rte_combine_rows(const void* rows, int T, int k, int d, const void* extra, const float* resid, void* out,
-                     int out_f32, void* stream) {
-  return combine_rows(B16(rows), T, k, d, B16(extra), resid, out, out_f32, S(stream));
+int rte_combine_rows(const void* rows, int T, int k, int d, const int32_t* slot_of_pair, const void* extra,
+                     const float* resid, void* out, int out_f32, void* stream) {
+  return combine_rows(B16(rows), T, k, d, slot_of_pair, B16(extra), resid, out, out_f32, S(stream));
 }
 
 int rte_route_bwd(const int32_t* ids, const float* w, const float* dw_slot, const int32_t* slot_of_pair, int T,

@@ -201,6 +201,7 @@ __device__ __forceinline__ void add8_bf16(float* acc, uint4 u) {
 // rows: [T*k, d] bf16 in pair order; extra: [T, d] bf16 or null; resid: [T, d] fp32 or null.
 template <typename OutT>
 __global__ void __launch_bounds__(256) combine_kernel(const bf16* __restrict__ rows, int T, int k, int d,
+                                                      const int32_t* __restrict__ slot_of_pair,
                                                       const bf16* __restrict__ extra,
                                                       const float* __restrict__ resid,
                                                       OutT* __restrict__ out) {
@@ -222,8 +223,10 @@ __global__ void __launch_bounds__(256) combine_kernel(const bf16* __restrict__ r
   float sum[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) sum[i] = 0.0f;
-  for (int j = 0; j < k; ++j)
+  for (int j = 0; j < k; ++j) {
+    if (slot_of_pair && slot_of_pair[(int64_t)t * k + j] < 0) continue;  // dropped (invalid) pair
     add8_bf16(sum, *reinterpret_cast<const uint4*>(rows + ((int64_t)t * k + j) * d + c));
+  }
   if (extra) add8_bf16(sum, *reinterpret_cast<const uint4*>(extra + (int64_t)t * d + c));
 #pragma unroll
   for (int i = 0; i < 8; ++i) acc[i] += sum[i];
@@ -298,7 +301,8 @@ int pack_pairs(const int32_t* cl, int P, int C, int k, const float* w, int32_t* 
   return 0;
 }
 
-int combine_rows(const bf16* rows, int T, int k, int d, const bf16* extra, const float* resid, void* out,
+int combine_rows(const bf16* rows, int T, int k, int d, const int32_t* slot_of_pair, const bf16* extra,
+                 const float* resid, void* out,
                  int out_f32, hipStream_t s) {
   RTE_REQUIRE(d % 8 == 0, "combine: d must be a multiple of 8");
   RTE_REQUIRE(k >= 0, "combine: k must be >= 0");
@@ -306,10 +310,10 @@ int combine_rows(const bf16* rows, int T, int k, int d, const bf16* extra, const
   if (n == 0) return 0;
   const dim3 grid((unsigned)((n + 255) / 256));
   if (out_f32)
-    hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(256), 0, s, rows, T, k, d, extra, resid,
+    hipLaunchKernelGGL(combine_kernel<float>, grid, dim3(256), 0, s, rows, T, k, d, slot_of_pair, extra, resid,
                        static_cast<float*>(out));
   else
-    hipLaunchKernelGGL(combine_kernel<bf16>, grid, dim3(256), 0, s, rows, T, k, d, extra, resid,
+    hipLaunchKernelGGL(combine_kernel<bf16>, grid, dim3(256), 0, s, rows, T, k, d, slot_of_pair, extra, resid,
                        static_cast<bf16*>(out));
   return check_launch("combine");
 }

@@ -357,17 +357,55 @@ def pack_index(ids: torch.Tensor, n_clusters: int, weights: torch.Tensor | None 
     return PackIndex(offsets, tok, pos, sop, wos, n_clusters, k)
 
 
-def combine_rows(rows: torch.Tensor, T: int, k: int, *, extra=None, resid=None, out_f32=True) -> torch.Tensor:
-    _lib.require_device_tensors("combine_rows", rows, extra, resid)
+def combine_rows(rows: torch.Tensor, T: int, k: int, *, extra=None, resid=None, out_f32=True,
+                 slot_of_pair=None) -> torch.Tensor:
+    """out[t] = resid[t] + extra[t] + sum_j rows[t*k + j]; pairs whose slot_of_pair is -1 are skipped."""
+    _lib.require_device_tensors("combine_rows", rows, extra, resid, slot_of_pair)
     d = rows.shape[-1]
     out = torch.empty((T, d), dtype=F32 if out_f32 else BF16, device=rows.device)
     r = None if resid is None else resid.reshape(T, d).contiguous().to(F32)
     e = None if extra is None else extra.reshape(T, d).contiguous().to(BF16)
-    call("rte_combine_rows", ptr(rows.contiguous()), T, k, d, ptr(e), ptr(r), ptr(out), int(out_f32), _s())
+    call("rte_combine_rows", ptr(rows.contiguous()), T, k, d, ptr(slot_of_pair), ptr(e), ptr(r), ptr(out),
+         int(out_f32), _s())
     return out
 
 
 # ----------------------------------------------------------------------------- routed cluster-pool SwiGLU
+
+def _pool_fwd(xb, ids, w, wugb, wdb, C: int, n: int, resid, masked: bool):
+    """Grouped pool forward over the (token, cluster) pairs of ids [T, k] (id -1 = no pair).
+    wugb [2F, d] rows [up F ; gate F], wdb [d, F]; cluster g owns neurons [g*n, (g+1)*n)."""
+    T, d = xb.shape
+    k = ids.shape[1]
+    F = C * n
+    pk = pack_index(ids, C, w)
+    P = T * k
+    ug = torch.empty((P, 2 * n), dtype=BF16, device=xb.device)
+    zw = torch.empty((P, n), dtype=BF16, device=xb.device)
+    yp = torch.empty((P, d), dtype=BF16, device=xb.device)
+    call("rte_grouped_swiglu_fwd", ptr(xb), T, d, ptr(pk.offsets), C, n, P, ptr(pk.tok_of_slot),
+         ptr(pk.pair_of_slot), ptr(pk.w_of_slot), ptr(wugb), ptr(wdb), F, ptr(ug), ptr(zw), ptr(yp), _s())
+    out = combine_rows(yp, T, k, resid=resid, out_f32=True, slot_of_pair=pk.slot_of_pair if masked else None)
+    return out, pk, ug, zw
+
+
+def _pool_bwd(db, xb, wugb, wdb, pk, ug, zw, C: int, n: int, k: int):
+    """Backward of _pool_fwd up to the combine: (dx_pairs bf16 [P, d] in pair order,
+    dwug f32 [2F, d], dwd f32 [d, F], dw_slot f32 [P] = per-slot <z, dz>)."""
+    T, d = xb.shape
+    F = C * n
+    P = T * k
+    dev = xb.device
+    dug = torch.empty((P, 2 * n), dtype=BF16, device=dev)
+    dw_slot = torch.empty((P,), dtype=F32, device=dev)
+    dxp = torch.empty((P, d), dtype=BF16, device=dev)
+    dwug = torch.empty((2 * F, d), dtype=F32, device=dev)
+    dwd = torch.empty((d, F), dtype=F32, device=dev)
+    call("rte_grouped_swiglu_bwd", ptr(db), ptr(xb), T, d, ptr(pk.offsets), C, n, P, ptr(pk.tok_of_slot),
+         ptr(pk.pair_of_slot), ptr(pk.w_of_slot), ptr(wugb), ptr(wdb), F, ptr(ug), ptr(zw), ptr(dug), ptr(dw_slot),
+         ptr(dxp), ptr(dwug), ptr(dwd), _s())
+    return dxp, dwug, dwd, dw_slot
+
 
 class RoutedClusterPoolFn(torch.autograd.Function):
     """Top-k routed cluster-pool SwiGLU FFN (cluster g owns neurons [g*n, (g+1)*n)).
@@ -383,7 +421,6 @@ class RoutedClusterPoolFn(torch.autograd.Function):
         shape = x.shape
         d = shape[-1]
         xb = x.reshape(-1, d).contiguous().to(BF16)
-        T = xb.shape[0]
         C = wr.shape[0]
         F = wug.shape[0] // 2
         if F % C != 0:
@@ -394,14 +431,7 @@ class RoutedClusterPoolFn(torch.autograd.Function):
         wdb = cast_bf16(wd)
         logits = gemm(xb, wrb, out_f32=True)
         ids, w = route_topk(logits, k)
-        pk = pack_index(ids, C, w)
-        P = T * k
-        ug = torch.empty((P, 2 * n), dtype=BF16, device=x.device)
-        zw = torch.empty((P, n), dtype=BF16, device=x.device)
-        yp = torch.empty((P, d), dtype=BF16, device=x.device)
-        call("rte_grouped_swiglu_fwd", ptr(xb), T, d, ptr(pk.offsets), C, n, P, ptr(pk.tok_of_slot),
-             ptr(pk.pair_of_slot), ptr(pk.w_of_slot), ptr(wugb), ptr(wdb), F, ptr(ug), ptr(zw), ptr(yp), _s())
-        out = combine_rows(yp, T, k, resid=resid, out_f32=True)
+        out, pk, ug, zw = _pool_fwd(xb, ids, w, wugb, wdb, C, n, resid, masked=False)
         ctx.save_for_backward(xb, wrb, wugb, wdb, ids, w, pk.offsets, pk.tok_of_slot, pk.pair_of_slot,
                               pk.slot_of_pair, pk.w_of_slot, ug, zw)
         ctx.meta = (shape, k, C, n, resid is not None, wr.dtype, wug.dtype, wd.dtype)
@@ -413,17 +443,10 @@ class RoutedClusterPoolFn(torch.autograd.Function):
         (xb, wrb, wugb, wdb, ids, w, offsets, tok, pos, sop, wos, ug, zw) = ctx.saved_tensors
         shape, k, C, n, has_resid, wr_dt, wug_dt, wd_dt = ctx.meta
         T, d = xb.shape
-        F = C * n
-        P = T * k
         dev = xb.device
         db = cast_bf16(dout.reshape(T, d))
-        dug = torch.empty((P, 2 * n), dtype=BF16, device=dev)
-        dw_slot = torch.empty((P,), dtype=F32, device=dev)
-        dxp = torch.empty((P, d), dtype=BF16, device=dev)
-        dwug = torch.empty((2 * F, d), dtype=F32, device=dev)
-        dwd = torch.empty((d, F), dtype=F32, device=dev)
-        call("rte_grouped_swiglu_bwd", ptr(db), ptr(xb), T, d, ptr(offsets), C, n, P, ptr(tok), ptr(pos), ptr(wos),
-             ptr(wugb), ptr(wdb), F, ptr(ug), ptr(zw), ptr(dug), ptr(dw_slot), ptr(dxp), ptr(dwug), ptr(dwd), _s())
+        pk = PackIndex(offsets, tok, pos, sop, wos, C, k)
+        dxp, dwug, dwd, dw_slot = _pool_bwd(db, xb, wugb, wdb, pk, ug, zw, C, n, k)
         dlog = torch.empty((T, C), dtype=BF16, device=dev)
         call("rte_route_bwd", ptr(ids), ptr(w), ptr(dw_slot), ptr(sop), T, C, k, ptr(dlog), None, _s())
         wr_k = wrb
@@ -441,6 +464,48 @@ class RoutedClusterPoolFn(torch.autograd.Function):
 def routed_cluster_pool_swiglu(x, wr, wug, wd, k: int, resid=None):
     """Returns (out, ids, weights); ids/weights are the routing decisions (no gradient)."""
     return RoutedClusterPoolFn.apply(x, wr, wug, wd, resid, k)
+
+
+class GroupedPoolFn(torch.autograd.Function):
+    """Grouped SwiGLU pool with routes given by the caller: out[t] = resid[t] +
+    sum_j w[t, j] * SwiGLU_{ids[t, j]}(x_t); ids == -1 marks an absent pair (dropped by
+    the pack, skipped by the combine).  ids / w carry no gradient.
+
+    wug_t bf16 [2F, d] (rows [up F ; gate F]) and wd_t bf16 [d, F] are differentiable
+    operands: their gradients come back in fp32."""
+
+    @staticmethod
+    def forward(ctx, x, ids, w, wug_t, wd_t, resid, n: int):
+        _lib.require_device_tensors("grouped_pool", x, ids, w, wug_t, wd_t, resid)
+        shape = x.shape
+        d = shape[-1]
+        xb = x.reshape(-1, d).contiguous().to(BF16)
+        T = xb.shape[0]
+        F = wug_t.shape[0] // 2
+        C = F // n
+        idc = ids.reshape(T, -1).contiguous().to(torch.int32)
+        wc = w.reshape(T, -1).contiguous().to(F32)
+        wugb, wdb = wug_t.contiguous().to(BF16), wd_t.contiguous().to(BF16)
+        rs = None if resid is None else resid.reshape(T, d)
+        out, pk, ug, zw = _pool_fwd(xb, idc, wc, wugb, wdb, C, n, rs, masked=True)
+        ctx.save_for_backward(xb, wugb, wdb, pk.offsets, pk.tok_of_slot, pk.pair_of_slot, pk.slot_of_pair,
+                              pk.w_of_slot, ug, zw)
+        ctx.meta = (shape, idc.shape[1], C, n, resid is not None, x.dtype)
+        return out.view(shape)
+
+    @staticmethod
+    def backward(ctx, dout):
+        xb, wugb, wdb, offsets, tok, pos, sop, wos, ug, zw = ctx.saved_tensors
+        shape, k, C, n, has_resid, x_dt = ctx.meta
+        T, d = xb.shape
+        pk = PackIndex(offsets, tok, pos, sop, wos, C, k)
+        dxp, dwug, dwd, _ = _pool_bwd(cast_bf16(dout.reshape(T, d)), xb, wugb, wdb, pk, ug, zw, C, n, k)
+        dx = combine_rows(dxp, T, k, out_f32=False, slot_of_pair=sop)
+        return dx.view(shape).to(x_dt), None, None, dwug, dwd, (dout if has_resid else None), None
+
+
+def grouped_pool_swiglu(x, ids, w, wug_t, wd_t, n: int, resid=None):
+    return GroupedPoolFn.apply(x, ids, w, wug_t, wd_t, resid, n)
 
 
 # ----------------------------------------------------------------------------- plain linear (LM head)

@@ -5,9 +5,10 @@ Hot modules run on the HIP kernels (rte_amd.kernels.hip_ops):
   DenseCausalSelfAttention  fused QKV GEMM + RoPE epilogue, SDPA core, O-proj GEMM + residual
   DenseSwiGLU             SwiGLU fused into the up/gate GEMM epilogue (fwd) and dZ GEMM (bwd)
   ClusterPoolSwiGLU       routed top-k cluster-pool SwiGLU (route, pack, grouped GEMMs, combine)
-The banked recursive core (exact-replay audit path, a few samples per step) is
-torch glue on the device for now; parameter names/shapes follow the reference so
-state dicts are interchangeable.
+  BankedAttention         per-bank QKV+RoPE / SDPA / O-proj with recipe head masks on V
+  BankedSwiGLU            grouped pool kernel over (bank, slab) clusters with recipe routes
+The banked recursive core keeps the reference's parameter names and shapes, so state
+dicts are interchangeable; its recipe selection is device-side table lookups.
 """
 
 from __future__ import annotations
@@ -19,7 +20,6 @@ import torch.nn.functional as F
 from torch import nn
 
 from rte_amd.config import ModelConfig
-from rte_amd.gather import gather_cols, gather_rows
 from rte_amd.kernels import hip_ops
 from rte_amd.kernels import optimized as K
 from rte_amd.recipes import RecipeBank, RecipeSpec
@@ -136,8 +136,31 @@ class TransformerBlock(nn.Module):
 
 # ----------------------------------------------------------------------------- banked recursive core
 
+def _head_scale(config: ModelConfig, spec: RecipeSpec) -> torch.Tensor:
+    """[attn_banks, n_heads]: 1/|banks| on the recipe's (bank, head) pairs, 0 elsewhere
+    (rte/layers.py:702-728: attention over the active head groups, mean over banks)."""
+    hpg = config.n_heads // config.head_groups
+    m = torch.zeros(config.attn_banks, config.n_heads)
+    for b in spec.attention_banks:
+        for g in spec.head_groups:
+            m[b, g * hpg:(g + 1) * hpg] = 1.0 / max(len(spec.attention_banks), 1)
+    return m
+
+
+def _ffn_route(config: ModelConfig, spec: RecipeSpec, kmax: int) -> tuple[torch.Tensor, float]:
+    """Pool clusters (bank * ffn_groups + slab group) a recipe's tokens visit, -1 padded to
+    kmax, and their weight 1/|banks| (rte/layers.py:744-779)."""
+    ids = [b * config.ffn_groups + g for b in spec.ffn_banks for g in spec.ffn_groups]
+    row = torch.full((kmax,), -1, dtype=torch.int32)
+    row[: len(ids)] = torch.tensor(ids, dtype=torch.int32)
+    return row, 1.0 / max(len(spec.ffn_banks), 1)
+
+
 class BankedAttention(nn.Module):
-    """rte/layers.py:659-728."""
+    """rte/layers.py:659-728.  Every sample runs the QKV+RoPE GEMM over all heads of each bank;
+    the recipe's head/bank selection (and the 1/|banks| mean) is a per-(sample, bank, head)
+    scale applied to V, which zeroes the unused heads' attention output exactly before the
+    O-projection.  No host read of the recipe ids is needed."""
 
     def __init__(self, config: ModelConfig, recipe_bank: RecipeBank):
         super().__init__()
@@ -155,6 +178,8 @@ class BankedAttention(nn.Module):
             qkv_cols[spec.recipe_id, : 3 * v.numel()] = torch.cat([v, v + d, v + 2 * d])
         self.register_buffer("recipe_cols", cols, persistent=False)
         self.register_buffer("recipe_qkv_cols", qkv_cols, persistent=False)
+        self.register_buffer("recipe_head_scale", torch.stack([_head_scale(config, s) for s in recipe_bank.recipes]),
+                             persistent=False)
 
     def _cols_for_groups(self, spec: RecipeSpec) -> list[int]:
         hpg = self.config.n_heads // self.config.head_groups
@@ -165,27 +190,36 @@ class BankedAttention(nn.Module):
                 out.extend(range(h * hd, (h + 1) * hd))
         return out
 
+    def _tables(self):
+        if self.rope is not None:
+            return self.rope.cos, self.rope.sin
+        hd = self.config.d_model // self.config.n_heads
+        cos = torch.ones(8192, hd, device=self.wqkv.device)
+        return cos, torch.zeros_like(cos)
+
+    def forward_scaled(self, x: torch.Tensor, head_scale: torch.Tensor) -> torch.Tensor:
+        """x [B, S, d], head_scale [B, attn_banks, n_heads] -> fp32 [B, S, d]."""
+        cos, sin = self._tables()
+        H = self.config.n_heads
+        out = None
+        for bank in range(self.config.attn_banks):
+            q, k, v = hip_ops.qkv_rope(x, self.wqkv[bank].t(), cos, sin, H)
+            v = v * head_scale[:, bank, :, None, None].to(v.dtype)
+            y = K.k_flash_causal_grouped(q, k, v)
+            out = hip_ops.attn_out_proj(y, self.wo[bank].t(), out)
+        return out
+
     def forward(self, x: torch.Tensor, spec: RecipeSpec) -> torch.Tensor:
-        b, s, d = x.shape
-        hd = d // self.config.n_heads
-        active_dim = len(spec.head_groups) * (self.config.n_heads // self.config.head_groups) * hd
-        cols = self.recipe_cols[spec.recipe_id, :active_dim]
-        qkv_cols = self.recipe_qkv_cols[spec.recipe_id, : 3 * active_dim]
-        heads = active_dim // hd
-        out = x.new_zeros(b, s, d)
-        for bank in spec.attention_banks:
-            qkv = x @ gather_cols(self.wqkv[bank], qkv_cols)
-            q, k, v = (t.view(b, s, heads, hd).transpose(1, 2) for t in qkv.split(active_dim, dim=-1))
-            if self.rope is not None:
-                q, k = self.rope(q, k)
-            y = K.k_flash_causal_grouped(q, k, v).transpose(1, 2).contiguous().view(b, s, active_dim)
-            out = out + y @ gather_rows(self.wo[bank], cols)
-        return out / max(len(spec.attention_banks), 1)
+        """Attention of one recipe for every sample of x (the reference's per-group call)."""
+        hs = _head_scale(self.config, spec).to(x.device)
+        return self.forward_scaled(x, hs.unsqueeze(0).expand(x.shape[0], -1, -1))
 
 
 class BankedSwiGLU(nn.Module):
-    """rte/layers.py:731-779: mean over the recipe's FFN banks of the SwiGLU restricted to
-    its active slabs."""
+    """rte/layers.py:731-779: mean over the recipe's FFN banks of the SwiGLU restricted to its
+    active slabs.  Runs as the grouped pool kernel: cluster (bank, slab group) owns the slab's
+    up/gate/down neurons of that bank, each token visits its recipe's clusters with weight
+    1/|banks| (absent pairs are -1 and cost nothing)."""
 
     def __init__(self, config: ModelConfig, recipe_bank: RecipeBank):
         super().__init__()
@@ -203,18 +237,44 @@ class BankedSwiGLU(nn.Module):
             gate_cols[spec.recipe_id, : 2 * v.numel()] = torch.cat([v, v + config.d_ff])
         self.register_buffer("recipe_slabs", slabs, persistent=False)
         self.register_buffer("recipe_gate_cols", gate_cols, persistent=False)
+        self.kmax = max(len(s.ffn_banks) * len(s.ffn_groups) for s in recipe_bank.recipes)
+        routes = [_ffn_route(config, s, self.kmax) for s in recipe_bank.recipes]
+        self.register_buffer("recipe_routes", torch.stack([r for r, _ in routes]), persistent=False)
+        self.register_buffer("recipe_route_w", torch.tensor([w for _, w in routes], dtype=torch.float32),
+                             persistent=False)
+
+    def pool_weights(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """Bank weights in the grouped kernel's layout: wug_t [2 * banks * F, d] with rows
+        [up of every bank ; gate of every bank], wd_t [d, banks * F] (differentiable copies)."""
+        A, d, F2 = self.wug.shape
+        F_ = F2 // 2
+        wug_t = self.wug.view(A, d, 2, F_).permute(2, 0, 3, 1).reshape(2 * A * F_, d)
+        wd_t = self.wd.permute(2, 0, 1).reshape(d, A * F_)
+        return wug_t, wd_t
+
+    def forward_routes(self, x: torch.Tensor, ids: torch.Tensor, w: torch.Tensor, weights=None) -> torch.Tensor:
+        """x [B, S, d]; ids [B*S, kmax] int32 (-1 = no pair); w [B*S, kmax] fp32 -> fp32 [B, S, d]."""
+        wug_t, wd_t = weights if weights is not None else self.pool_weights()
+        slab = self.config.d_ff // self.config.ffn_groups
+        return hip_ops.grouped_pool_swiglu(x, ids, w, wug_t, wd_t, slab)
+
+    def routes_for(self, recipe_ids: torch.Tensor, seq: int, active: torch.Tensor | None = None):
+        """Per-token routes of samples with recipe_ids [B] (inactive samples get none)."""
+        ids = self.recipe_routes[recipe_ids]                                   # [B, kmax]
+        if active is not None:
+            ids = torch.where(active[:, None], ids, torch.full_like(ids, -1))
+        w = self.recipe_route_w[recipe_ids][:, None].expand(-1, self.kmax)
+        B = recipe_ids.shape[0]
+        return (ids[:, None, :].expand(B, seq, self.kmax).reshape(B * seq, self.kmax),
+                w[:, None, :].expand(B, seq, self.kmax).reshape(B * seq, self.kmax))
 
     def forward(self, x: torch.Tensor, spec: RecipeSpec) -> torch.Tensor:
-        slab = self.config.d_ff // self.config.ffn_groups
-        active = len(spec.ffn_groups) * slab
-        slabs = self.recipe_slabs[spec.recipe_id, :active]
-        gate_cols = self.recipe_gate_cols[spec.recipe_id, : 2 * active]
-        out = x.new_zeros(*x.shape)
-        for bank in spec.ffn_banks:
-            fused = x @ gather_cols(self.wug[bank], gate_cols)
-            up, gate = fused.split(active, dim=-1)
-            out = out + (up * F.silu(gate)) @ gather_rows(self.wd[bank], slabs)
-        return out / max(len(spec.ffn_banks), 1)
+        """SwiGLU of one recipe for every token of x (the reference's per-group call)."""
+        row, wt = _ffn_route(self.config, spec, self.kmax)
+        T = x.shape[0] * x.shape[1]
+        ids = row.to(x.device)[None, :].expand(T, -1)
+        w = torch.full((T, self.kmax), wt, dtype=torch.float32, device=x.device)
+        return self.forward_routes(x, ids, w)
 
 
 class BankedRecursiveCore(nn.Module):
@@ -243,29 +303,35 @@ class BankedRecursiveCore(nn.Module):
         else:
             self.register_parameter("alpha_inj", None)
 
-    def step_group(self, h, h0, spec: RecipeSpec, pass_idx: int = 0):
+    def prepare(self):
+        """Per-forward weight layouts shared by every recursive pass."""
+        return self.mlp.pool_weights()
+
+    def _step(self, h, h0, head_scale, ids, w, pass_idx: int, weights=None):
         h_tilde = h if self.alpha_inj is None else h + self.alpha_inj * h0
         n1 = self.norm1(h_tilde) * (1.0 + self.pass_gamma1[pass_idx]) + self.pass_beta1[pass_idx]
-        u = h_tilde + self.pass_attn_scale[pass_idx] * self.attn(n1, spec)
+        u = h_tilde + self.pass_attn_scale[pass_idx] * self.attn.forward_scaled(n1, head_scale)
         n2 = self.norm2(u) * (1.0 + self.pass_gamma2[pass_idx]) + self.pass_beta2[pass_idx]
-        return u + self.pass_mlp_scale[pass_idx] * self.mlp(n2, spec)
+        return u + self.pass_mlp_scale[pass_idx] * self.mlp.forward_routes(n2, ids, w, weights)
 
-    def forward_step(self, h, h0, recipe_ids, active_mask=None, pass_idx: int = 0, *, host_ids=None,
-                     host_active=None):
-        """One exact recursive pass, grouped by recipe (rte/layers.py:854-870).  host_ids /
-        host_active (python lists) let the caller read the routing decisions once per replay
-        instead of once per pass."""
-        if host_ids is None:
-            host_ids = recipe_ids.detach().cpu().tolist()
-            host_active = ([True] * len(host_ids) if active_mask is None
-                           else active_mask.detach().cpu().tolist())
-        out = h.clone()
-        for rid in sorted({r for r, a in zip(host_ids, host_active) if a}):
-            rows = [i for i, (r, a) in enumerate(zip(host_ids, host_active)) if a and r == rid]
-            spec = self.recipe_bank.get_recipe(int(rid))
-            if len(rows) == h.shape[0]:
-                return self.step_group(h, h0, spec, pass_idx=pass_idx).to(out.dtype)
-            idx = torch.tensor(rows, device=h.device, dtype=torch.long)
-            out = out.index_copy(0, idx, self.step_group(h.index_select(0, idx), h0.index_select(0, idx), spec,
-                                                         pass_idx=pass_idx).to(out.dtype))
-        return out
+    def step_group(self, h, h0, spec: RecipeSpec, pass_idx: int = 0):
+        """One pass of a single recipe over every sample of h (rte/layers.py:826-845)."""
+        B, S, _ = h.shape
+        hs = _head_scale(self.config, spec).to(h.device).unsqueeze(0).expand(B, -1, -1)
+        row, wt = _ffn_route(self.config, spec, self.mlp.kmax)
+        ids = row.to(h.device)[None, :].expand(B * S, -1)
+        w = torch.full((B * S, self.mlp.kmax), wt, dtype=torch.float32, device=h.device)
+        return self._step(h, h0, hs, ids, w, pass_idx)
+
+    def forward_step(self, h, h0, recipe_ids, active_mask=None, pass_idx: int = 0, *, weights=None):
+        """One exact recursive pass (rte/layers.py:847-870): every sample runs its own recipe,
+        inactive samples keep h.  The recipe ids stay on the device: the head / slab selection
+        is table lookups and masks, so the pass needs no host synchronisation."""
+        B, S, _ = h.shape
+        rid = recipe_ids.long()
+        head_scale = self.attn.recipe_head_scale[rid]
+        ids, w = self.mlp.routes_for(rid, S, active_mask)
+        out = self._step(h, h0, head_scale, ids, w, pass_idx, weights).to(h.dtype)
+        if active_mask is None:
+            return out
+        return torch.where(active_mask[:, None, None], out, h)

@@ -129,15 +129,11 @@ class RecursiveModel(nn.Module):
         route = router_decisions or self.router(h0, fixed_recipe=fixed_recipe, fixed_depth=fixed_depth)
         h = h0
         states: dict[int, torch.Tensor] = {}
-        # routing decisions of the replayed samples, read to the host once per replay
-        by_pass = route.recipe_id_by_pass if route.recipe_id_by_pass is not None else route.recipe_id.unsqueeze(1)
-        host = torch.cat([by_pass.long(), route.depth.long().unsqueeze(1)], dim=1).cpu().tolist()
+        weights = self.core.prepare()
         for t in range(self.config.t_max):
             active = route.depth > t
             rid = route.recipe_id_by_pass[:, t] if route.recipe_id_by_pass is not None else route.recipe_id
-            host_ids = [row[t] if route.recipe_id_by_pass is not None else row[0] for row in host]
-            host_active = [row[-1] > t for row in host]
-            h = self.core.forward_step(h, h0, rid, active, pass_idx=t, host_ids=host_ids, host_active=host_active)
+            h = self.core.forward_step(h, h0, rid, active, pass_idx=t, weights=weights)
             if return_states and (t + 1) in self.config.depth_choices:
                 states[t + 1] = h.clone()
         hidden = self._coda_hidden(h)

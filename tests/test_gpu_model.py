@@ -160,3 +160,188 @@ def test_backend_status_reports_hip():
     assert st["mode"] == "rocm_hip_dispatch"
     assert st["uses_reference_fallback"] is False
     assert "gfx950" in st["device"]["arch"]
+
+
+# ---------------------------------------------------------------- banked recursive core
+
+def _banked_core(seed=0):
+    from rte_amd.config import ModelConfig
+    from rte_amd.layers import BankedRecursiveCore
+    from rte_amd.recipes import RecipeBank
+
+    cfg = ModelConfig(topology="recursive", vocab_size=64, d_model=128, n_heads=4, d_ff=256, n_dense_layers=2,
+                      n_prelude=1, n_coda=1, t_max=2, depth_choices=[1, 2], attn_banks=2, ffn_banks=2, head_groups=4,
+                      ffn_groups=8, active_head_groups=2, active_ffn_groups=2, recipe_count=7)
+    torch.manual_seed(seed)
+    core = BankedRecursiveCore(cfg, RecipeBank(cfg)).to("cuda")
+    with torch.no_grad():
+        for name in ("pass_gamma1", "pass_beta1", "pass_gamma2", "pass_beta2"):
+            getattr(core, name).normal_(0.0, 0.1)
+        core.pass_attn_scale.uniform_(0.5, 1.5)
+        core.pass_mlp_scale.uniform_(0.5, 1.5)
+        core.norm1.weight.uniform_(0.8, 1.2)
+        core.norm2.weight.uniform_(0.8, 1.2)
+    return cfg, core
+
+
+def _core_params_np(core):
+    p = {k: v.detach().double().cpu().numpy() for k, v in core.named_parameters()}
+    return dict(norm1=p["norm1.weight"], norm2=p["norm2.weight"], wqkv=p["attn.wqkv"], wo=p["attn.wo"],
+                wug=p["mlp.wug"], wd=p["mlp.wd"], pass_gamma1=p["pass_gamma1"], pass_beta1=p["pass_beta1"],
+                pass_gamma2=p["pass_gamma2"], pass_beta2=p["pass_beta2"], pass_attn_scale=p["pass_attn_scale"],
+                pass_mlp_scale=p["pass_mlp_scale"], alpha_inj=p.get("alpha_inj"))
+
+
+def _oracle_recipes(core):
+    return [dict(attention_banks=r.attention_banks, ffn_banks=r.ffn_banks, head_groups=r.head_groups,
+                 ffn_groups=r.ffn_groups) for r in core.recipe_bank.recipes]
+
+
+def test_banked_core_forward_step_matches_oracle():
+    """Mixed recipes (including the dense fallback, two banks each) and an inactive sample in
+    one device-side pass, against the per-sample reference restatement."""
+    from oracle import attention as AO
+    from oracle import banked as BK
+
+    cfg, core = _banked_core(1)
+    B, S, d = 5, 32, cfg.d_model
+    h = torch.randn(B, S, d, device="cuda")
+    h0 = torch.randn(B, S, d, device="cuda")
+    rid = torch.tensor([0, 3, 6, 1, 3], device="cuda")
+    active = torch.tensor([True, True, False, True, True], device="cuda")
+    print("banked forward_step B=5 S=32 d=128", flush=True)
+    out = core.forward_step(h, h0, rid, active, pass_idx=1)
+    cos, sin = AO.rope_tables(d // cfg.n_heads, S)
+    want = BK.core_forward_step(h.double().cpu().numpy(), h0.double().cpu().numpy(), rid.tolist(), active.tolist(),
+                                _oracle_recipes(core), _core_params_np(core), 1, n_heads=cfg.n_heads,
+                                head_groups=cfg.head_groups, ffn_groups=cfg.ffn_groups, cos=cos, sin=sin)
+    got = out.detach().double().cpu().numpy()
+    assert np.array_equal(got[2], h[2].double().cpu().numpy()), "inactive sample changed"
+    assert_rel(got - h.double().cpu().numpy(), want - h.double().cpu().numpy(), BF16_RTOL, "banked step delta")
+
+
+def _torch_core_step(h, h0, rid, active, recipes, p, pass_idx, cfg, cos, sin):
+    """fp64 CPU torch restatement of BankedRecursiveCore.forward_step (rte/layers.py:659-870),
+    per sample and per recipe; differentiable in every entry of p and in h, h0."""
+    d, H = cfg.d_model, cfg.n_heads
+    hd, hpg = d // H, H // cfg.head_groups
+    slab = cfg.d_ff // cfg.ffn_groups
+
+    def rms(v, w):
+        return v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + 1e-5) * w
+
+    def rot(t):
+        return torch.stack((-t[..., 1::2], t[..., ::2]), -1).flatten(-2)
+
+    outs = []
+    for i in range(h.shape[0]):
+        if not active[i]:
+            outs.append(h[i])
+            continue
+        r = recipes[rid[i]]
+        S = h.shape[1]
+        ht = h[i] + p["alpha_inj"] * h0[i] if "alpha_inj" in p else h[i]
+        n1 = rms(ht, p["norm1"]) * (1 + p["pass_gamma1"][pass_idx]) + p["pass_beta1"][pass_idx]
+        cols = torch.tensor([c for g in r["head_groups"] for hh in range(g * hpg, (g + 1) * hpg)
+                             for c in range(hh * hd, (hh + 1) * hd)])
+        a = cols.numel()
+        att = torch.zeros(S, d, dtype=torch.float64)
+        for b in r["attention_banks"]:
+            qkv = n1 @ p["wqkv"][b][:, torch.cat([cols, cols + d, cols + 2 * d])]
+            q, k, v = (qkv[:, j * a:(j + 1) * a].view(S, a // hd, hd).transpose(0, 1) for j in range(3))
+            q, k = q * cos + rot(q) * sin, k * cos + rot(k) * sin
+            y = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)
+            att = att + y.transpose(0, 1).reshape(S, a) @ p["wo"][b][cols, :]
+        u = ht + p["pass_attn_scale"][pass_idx] * att / len(r["attention_banks"])
+        n2 = rms(u, p["norm2"]) * (1 + p["pass_gamma2"][pass_idx]) + p["pass_beta2"][pass_idx]
+        slabs = torch.tensor([c for g in r["ffn_groups"] for c in range(g * slab, (g + 1) * slab)])
+        mlp = torch.zeros(S, d, dtype=torch.float64)
+        for b in r["ffn_banks"]:
+            fused = n2 @ p["wug"][b][:, torch.cat([slabs, slabs + cfg.d_ff])]
+            up, gate = fused.split(slabs.numel(), dim=-1)
+            mlp = mlp + (up * torch.nn.functional.silu(gate)) @ p["wd"][b][slabs, :]
+        outs.append(u + p["pass_mlp_scale"][pass_idx] * mlp / len(r["ffn_banks"]))
+    return torch.stack(outs)
+
+
+def test_banked_core_gradients_match_fp64_reference():
+    """Gradients of every core parameter and of h, h0 against fp64 autograd of a CPU torch
+    restatement whose forward is first checked against the numpy oracle."""
+    from oracle import attention as AO
+    from oracle import banked as BK
+    from helpers import rel_err
+
+    cfg, core = _banked_core(2)
+    B, S, d = 4, 16, cfg.d_model
+    gen = np.random.default_rng(2)
+    hn = gen.standard_normal((B, S, d))
+    h0n = gen.standard_normal((B, S, d))
+    G = gen.standard_normal((B, S, d))
+    rid, active = [0, 2, 5, 4], [True, True, True, False]
+    h = torch.tensor(hn, dtype=torch.float32, device="cuda", requires_grad=True)
+    h0 = torch.tensor(h0n, dtype=torch.float32, device="cuda", requires_grad=True)
+    print("banked core gradients B=4 S=16 d=128", flush=True)
+    out = core.forward_step(h, h0, torch.tensor(rid, device="cuda"), torch.tensor(active, device="cuda"),
+                            pass_idx=0, weights=core.prepare())
+    (out * torch.tensor(G, dtype=torch.float32, device="cuda")).sum().backward()
+    cos, sin = AO.rope_tables(d // cfg.n_heads, S)
+    recipes = _oracle_recipes(core)
+    base = _core_params_np(core)
+    tp = {k: torch.tensor(v, requires_grad=True) for k, v in base.items() if v is not None}
+    th, th0 = torch.tensor(hn, requires_grad=True), torch.tensor(h0n, requires_grad=True)
+    ref = _torch_core_step(th, th0, rid, active, recipes, tp, 0, cfg, torch.tensor(cos), torch.tensor(sin))
+    want = BK.core_forward_step(hn, h0n, rid, active, recipes, base, 0, n_heads=cfg.n_heads,
+                                head_groups=cfg.head_groups, ffn_groups=cfg.ffn_groups, cos=cos, sin=sin)
+    assert rel_err(ref.detach().numpy(), want) < 1e-12, "torch restatement disagrees with the oracle"
+    (ref * torch.tensor(G)).sum().backward()
+    mods = {"norm1": core.norm1.weight, "norm2": core.norm2.weight, "wqkv": core.attn.wqkv, "wo": core.attn.wo,
+            "wug": core.mlp.wug, "wd": core.mlp.wd, "pass_gamma1": core.pass_gamma1, "pass_beta1": core.pass_beta1,
+            "pass_gamma2": core.pass_gamma2, "pass_beta2": core.pass_beta2, "pass_attn_scale": core.pass_attn_scale,
+            "pass_mlp_scale": core.pass_mlp_scale}
+    if core.alpha_inj is not None:
+        mods["alpha_inj"] = core.alpha_inj
+    for name, param in mods.items():
+        assert_rel(param.grad.double().cpu().numpy(), tp[name].grad.numpy(), BF16_RTOL, f"d{name}")
+    assert_rel(h.grad.double().cpu().numpy(), th.grad.numpy(), BF16_RTOL, "dh")
+    if th0.grad is None:
+        assert h0.grad is None or not h0.grad.any()
+    else:
+        assert_rel(h0.grad.double().cpu().numpy(), th0.grad.numpy(), BF16_RTOL, "dh0")
+
+
+def test_banked_swiglu_weight_gradients_exact_layout():
+    """Element-wise FFN weight gradients of the banked SwiGLU (bank/slab layout of the grouped
+    kernel mapped back to [banks, d, 2F] / [banks, F, d]) against the dense-FFN oracle backward
+    applied to each sample's slabs."""
+    from oracle import swiglu as SWO
+
+    cfg, core = _banked_core(3)
+    B, S, d = 4, 16, cfg.d_model
+    gen = np.random.default_rng(3)
+    x = gen.standard_normal((B, S, d)).astype(np.float32)
+    xb = torch.tensor(x, device="cuda").to(torch.bfloat16)
+    rid = torch.tensor([0, 1, 4, 6], device="cuda")
+    ids, w = core.mlp.routes_for(rid, S)
+    out = core.mlp.forward_routes(xb, ids, w)
+    G = gen.standard_normal((B, S, d))
+    out.backward(torch.tensor(G, dtype=torch.float32, device="cuda"))
+    wug = core.mlp.wug.detach().to(torch.bfloat16).double().cpu().numpy()
+    wd = core.mlp.wd.detach().to(torch.bfloat16).double().cpu().numpy()
+    F_ = cfg.d_ff
+    slab = F_ // cfg.ffn_groups
+    dwug, dwd = np.zeros_like(wug), np.zeros_like(wd)
+    want = np.zeros((B, S, d))
+    xs = xb.double().cpu().numpy()
+    for i, r in enumerate(_oracle_recipes(core)[j] for j in rid.tolist()):
+        slabs = np.array([c for g in r["ffn_groups"] for c in range(g * slab, (g + 1) * slab)])
+        cols = np.concatenate([slabs, slabs + F_])
+        for b in r["ffn_banks"]:
+            sc = 1.0 / len(r["ffn_banks"])
+            y, cache = SWO.dense_swiglu_fwd(xs[i], wug[b][:, cols].T, wd[b][slabs, :], wd_rows=True)
+            want[i] += sc * y
+            _, gw, gd = SWO.dense_swiglu_bwd(sc * G[i], xs[i], wug[b][:, cols].T, wd[b][slabs, :], cache, wd_rows=True)
+            dwug[b][:, cols] += gw.T
+            dwd[b][slabs, :] += gd
+    assert_rel(out.detach().double().cpu().numpy(), want, BF16_RTOL, "banked ffn out")
+    assert_rel(core.mlp.wug.grad.double().cpu().numpy(), dwug, BF16_RTOL, "banked dwug")
+    assert_rel(core.mlp.wd.grad.double().cpu().numpy(), dwd, BF16_RTOL, "banked dwd")

@@ -468,3 +468,109 @@ def test_shortlist_logits_ce_and_backward_match_torch_autograd():
     np.testing.assert_allclose(loss, tloss.detach().numpy(), rtol=1e-12)
     np.testing.assert_allclose(dh, th.grad.numpy(), rtol=1e-10, atol=1e-12)
     np.testing.assert_allclose(dw, tw.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
+# ---------------------------------------------------------------- banked recursive core
+
+def _banked_case(seed, A=1, FB=1, H=4, HG=4, AHG=2, G=8, AG=2, d=32, F=64, R=7, S=12):
+    from oracle import banked as BK
+
+    rng = _rng(seed)
+    recipes = BK.recipe_templates(A, FB, HG, G, AHG, AG, R)
+    wqkv = rng.standard_normal((A, d, 3 * d)) / np.sqrt(d)
+    wo = rng.standard_normal((A, d, d)) / np.sqrt(d)
+    wug = rng.standard_normal((FB, d, 2 * F)) / np.sqrt(d)
+    wd = rng.standard_normal((FB, F, d)) / np.sqrt(F)
+    x = rng.standard_normal((S, d))
+    return BK, recipes, wqkv, wo, wug, wd, x
+
+
+def test_banked_recipe_templates_match_recipe_bank():
+    from oracle import banked as BK
+    from rte_amd.config import ModelConfig
+    from rte_amd.recipes import RecipeBank
+
+    cfg = ModelConfig(topology="recursive", vocab_size=64, d_model=32, n_heads=4, d_ff=64, n_dense_layers=2,
+                      n_prelude=1, n_coda=1, t_max=2, depth_choices=[1, 2], attn_banks=2, ffn_banks=3, head_groups=4,
+                      ffn_groups=8, active_head_groups=2, active_ffn_groups=2, recipe_count=11)
+    want = BK.recipe_templates(2, 3, 4, 8, 2, 2, 11)
+    got = [dict(attention_banks=r.attention_banks, ffn_banks=r.ffn_banks, head_groups=r.head_groups,
+                ffn_groups=r.ffn_groups) for r in RecipeBank(cfg).recipes]
+    assert got == want
+
+
+def test_banked_swiglu_dense_recipe_equals_dense_ffn():
+    """Recipe 0 (every slab) of a single bank is the dense SwiGLU of that bank."""
+    BK, recipes, _, _, wug, wd, x = _banked_case(40)
+    got = BK.banked_swiglu(x, recipes[0], wug, wd, 8)
+    want, _ = SW.dense_swiglu_fwd(x, wug[0].T, wd[0], wd_rows=True)
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def test_banked_swiglu_slab_partition_sums_to_dense():
+    """The recipes of one bank whose slab groups partition the FFN add up to recipe 0."""
+    BK, recipes, _, _, wug, wd, x = _banked_case(41)
+    parts = [r for r in recipes[1:] if r["ffn_banks"] == (0,)][:4]
+    assert sorted(g for r in parts for g in r["ffn_groups"]) == list(range(8))
+    total = sum(BK.banked_swiglu(x, r, wug, wd, 8) for r in parts)
+    np.testing.assert_allclose(total, BK.banked_swiglu(x, recipes[0], wug, wd, 8), rtol=1e-11, atol=1e-12)
+
+
+def test_banked_swiglu_bank_mean():
+    """A recipe over two banks is the mean of the single-bank outputs."""
+    BK, _, _, _, wug, wd, x = _banked_case(42, FB=2)
+    r2 = dict(attention_banks=(0,), ffn_banks=(0, 1), head_groups=(0,), ffn_groups=(1, 5))
+    r0 = dict(r2, ffn_banks=(0,))
+    r1 = dict(r2, ffn_banks=(1,))
+    np.testing.assert_allclose(BK.banked_swiglu(x, r2, wug, wd, 8),
+                               0.5 * (BK.banked_swiglu(x, r0, wug, wd, 8) + BK.banked_swiglu(x, r1, wug, wd, 8)),
+                               rtol=1e-12, atol=1e-12)
+
+
+def test_banked_attention_dense_recipe_matches_torch_sdpa():
+    """Recipe 0 of one bank is dense causal attention: torch SDPA on the CPU as the check."""
+    BK, recipes, wqkv, wo, _, _, x = _banked_case(43)
+    S, d = x.shape
+    H = 4
+    hd = d // H
+    cos, sin = A.rope_tables(hd, S)
+    got = BK.banked_attention(x, recipes[0], wqkv, wo, H, 4, cos, sin)
+    qkv = torch.tensor(x) @ torch.tensor(wqkv[0])
+    q, k, v = (qkv[:, i * d:(i + 1) * d].view(S, H, hd).transpose(0, 1) for i in range(3))
+    tc, ts = torch.tensor(cos), torch.tensor(sin)
+
+    def rope(t):
+        rot = torch.stack([-t[..., 1::2], t[..., 0::2]], dim=-1).flatten(-2)
+        return t * tc + rot * ts
+
+    y = torch.nn.functional.scaled_dot_product_attention(rope(q), rope(k), v, is_causal=True)
+    want = y.transpose(0, 1).reshape(S, d) @ torch.tensor(wo[0])
+    np.testing.assert_allclose(got, want.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_banked_attention_head_partition_sums_to_dense():
+    BK, recipes, wqkv, wo, _, _, x = _banked_case(44)
+    cos, sin = A.rope_tables(8, x.shape[0])
+    parts = [r for r in recipes[1:] if r["attention_banks"] == (0,)][:2]
+    assert sorted(g for r in parts for g in r["head_groups"]) == [0, 1, 2, 3]
+    total = sum(BK.banked_attention(x, r, wqkv, wo, 4, 4, cos, sin) for r in parts)
+    np.testing.assert_allclose(total, BK.banked_attention(x, recipes[0], wqkv, wo, 4, 4, cos, sin), rtol=1e-11,
+                               atol=1e-12)
+
+
+def test_banked_core_inactive_samples_keep_state():
+    BK, recipes, wqkv, wo, wug, wd, _ = _banked_case(45)
+    rng = _rng(45)
+    d, t = 32, 2
+    p = dict(norm1=np.ones(d), norm2=np.ones(d), wqkv=wqkv, wo=wo, wug=wug, wd=wd,
+             pass_gamma1=rng.standard_normal((t, d)) * 0.1, pass_beta1=rng.standard_normal((t, d)) * 0.1,
+             pass_gamma2=rng.standard_normal((t, d)) * 0.1, pass_beta2=rng.standard_normal((t, d)) * 0.1,
+             pass_attn_scale=np.ones(t), pass_mlp_scale=np.ones(t), alpha_inj=None)
+    h = rng.standard_normal((3, 12, d))
+    cos, sin = A.rope_tables(8, 12)
+    kw = dict(n_heads=4, head_groups=4, ffn_groups=8, cos=cos, sin=sin)
+    out = BK.core_forward_step(h, h, [0, 3, 5], [True, False, True], recipes, p, 1, **kw)
+    np.testing.assert_array_equal(out[1], h[1])
+    np.testing.assert_allclose(out[2], BK.core_step(h[2], h[2], recipes[5], p, 1, **kw), rtol=1e-12)
+    zero = dict(p, pass_attn_scale=np.zeros(t), pass_mlp_scale=np.zeros(t))
+    np.testing.assert_allclose(BK.core_step(h[0], h[0], recipes[0], zero, 0, **kw), h[0], rtol=0, atol=0)
