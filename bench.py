@@ -187,6 +187,8 @@ def main(argv=None) -> int:
     ap.add_argument("--seq", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every kernel from Python instead of replaying the captured step graph")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this build measures one GPU only; run bench.py with --gpus 1"}))
@@ -203,6 +205,11 @@ def main(argv=None) -> int:
     cfg = cfg3_config(args.batch, args.seq)
     dev = torch.device("cuda:0")
     engine = TrainEngine(cfg, device=dev)
+    if not args.eager:
+        # the whole step (forward, audit replay, backward, AdamW) replays as one HIP graph; the
+        # first two warm-up steps run eagerly and the third captures it
+        engine.enable_graph_capture(True)
+        args.warmup = max(args.warmup, 3)
     gen = torch.Generator()
     gen.manual_seed(cfg.training.seed)
     batches = [zipf_batch(gen, cfg.model.vocab_size, args.batch, args.seq, dev) for _ in range(4)]
@@ -237,6 +244,7 @@ def main(argv=None) -> int:
             "global_batch": args.batch,
             "seq_len": args.seq,
             "parallelism": "single GPU",
+            "launch": "eager" if args.eager else "captured step graph",
         },
     }
     if not args.no_roofline:

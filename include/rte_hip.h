@@ -179,6 +179,18 @@ int rte_ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* tar
 int rte_ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
                const float* dloss, const float* extra, void* dlogits, void* stream);
 
+/* ---- deterministic segmented row reduction (rte/kernels/cluster_pool_ffn.py:218-241 index_add_
+ * of pool gradients; the backward of every row gather / embedding lookup) ----
+ *   out[v] (+)= sum over p < P with keys[p] = v of w[p] * rows[p / row_div]
+ * keys int32 [P] (values outside [0, V) are skipped), w f32 [P] (NULL = 1), rows f32 (rows_f32=1)
+ * or bf16 [*, d]; out f32 [V, d], overwritten unless accumulate.  V <= 32768, d % 8 == 0, d <= 2048.
+ * Summation order is fixed (ascending p per key, 256-pair chunks added in order): bitwise
+ * repeatable, no atomics. */
+size_t rte_segment_reduce_workspace_bytes(int64_t P, int V, int d);
+int rte_segment_reduce_rows(const int32_t* keys, int64_t P, int V, int row_div, const float* w, const void* rows,
+                            int rows_f32, int d, float* out, int accumulate, void* workspace, size_t workspace_bytes,
+                            void* stream);
+
 /* ---- shortlist output head (rte/output.py:46-136, rte/kernels/reference.py:141-147) ----
  * build: replaces ShortlistHead.build_shortlist / _dedupe_preserve_first (rte/output.py:46-110).
  *   Candidates per token t, in order: targets[t]; members[top_clusters[t, c], :] for c < tc

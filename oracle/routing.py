@@ -81,3 +81,16 @@ def route_softmax_bwd(ids: np.ndarray, w: np.ndarray, dw: np.ndarray, n_clusters
     out = np.zeros((T, n_clusters), dtype=np.float64)
     np.put_along_axis(out, ids.astype(np.int64), g, axis=-1)
     return out
+
+
+def segment_reduce_rows(keys, n_keys, rows, w=None, row_div=1):
+    """out[v] = sum over p with keys[p] = v of w[p] * rows[p // row_div] (float64); keys outside
+    [0, n_keys) are skipped -- the index_add_ scatter of rte/kernels/cluster_pool_ffn.py:235-240."""
+    k = np.asarray(keys, np.int64).reshape(-1)
+    r = np.asarray(rows, np.float64)
+    wt = np.ones(k.shape[0]) if w is None else np.asarray(w, np.float64).reshape(-1)
+    out = np.zeros((n_keys, r.shape[-1]))
+    ok = (k >= 0) & (k < n_keys)
+    src = r[np.arange(k.shape[0]) // row_div]
+    np.add.at(out, k[ok], wt[ok, None] * src[ok])
+    return out

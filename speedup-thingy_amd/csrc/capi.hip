@@ -41,6 +41,9 @@ size_t shortlist_bwd_workspace_bytes(int T, int L, int V, int d);
 int shortlist_bwd(const float* dloss, const float* dlext, const bf16* hidden, const bf16* W, int d, int V,
                   const int32_t* sl, int L, int T, const float* logits, const float* lse, bf16* dhidden, float* dW,
                   int dW_accumulate, void* ws, size_t ws_bytes, hipStream_t s);
+size_t segreduce_workspace_bytes(int64_t P, int V, int d);
+int segreduce_rows(const int32_t* keys, int64_t P, int V, int row_div, const float* w, const void* rows, int rows_f32,
+                   int d, float* out, int accumulate, void* ws, size_t ws_bytes, hipStream_t s);
 }  // namespace rte
 
 using namespace rte;
@@ -731,6 +734,15 @@ int rte_shortlist_bwd(const float* dloss, const float* dlogits, const void* hidd
                       void* stream) {
   return shortlist_bwd(dloss, dlogits, B16(hidden), B16(W), d, V, shortlist, L, T, logits, lse,
                        static_cast<bf16*>(dhidden), dW, dW_accumulate, workspace, workspace_bytes, S(stream));
+}
+
+size_t rte_segment_reduce_workspace_bytes(int64_t P, int V, int d) { return segreduce_workspace_bytes(P, V, d); }
+
+int rte_segment_reduce_rows(const int32_t* keys, int64_t P, int V, int row_div, const float* w, const void* rows,
+                            int rows_f32, int d, float* out, int accumulate, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  return segreduce_rows(keys, P, V, row_div, w, rows, rows_f32, d, out, accumulate, workspace, workspace_bytes,
+                        S(stream));
 }
 
 }  // extern "C"

@@ -77,11 +77,19 @@ class AuditEngine:
              + self.config.audit_gamma * self._coverage_deficit(meta.recipe_ids, r.recipe_logits.shape[-1]))
         return p.clamp(self.config.audit_p_min, self.config.audit_p_max)
 
-    def sample_mask_with_prob(self, p: torch.Tensor, seed: int):
-        """rte/audit.py:99-132.  Returns (mask, inclusion_p, chosen_index or None, count or None);
-        the fixed-count sampler knows its count on the host, so it needs no device sync."""
-        gen = torch.Generator(device=p.device)
+    @staticmethod
+    def fixed_count_index(n: int, k: int, seed: int, device) -> torch.Tensor:
+        """The fixed-count sampler's audited rows: the first k of a seeded permutation of n
+        (rte/audit.py:102-115).  Depends only on (n, k, seed), so it can be drawn ahead of a
+        captured step."""
+        gen = torch.Generator(device=device)
         gen.manual_seed(seed)
+        return torch.randperm(n, device=device, generator=gen)[:k]
+
+    def sample_mask_with_prob(self, p: torch.Tensor, seed: int, chosen: torch.Tensor | None = None):
+        """rte/audit.py:99-132.  Returns (mask, inclusion_p, chosen_index or None, count or None);
+        the fixed-count sampler knows its count on the host, so it needs no device sync.
+        `chosen` supplies the fixed-count sampler's rows drawn ahead of time."""
         fixed = self.config.audit_fixed_count_per_batch
         if fixed is not None:
             n = p.numel()
@@ -89,12 +97,18 @@ class AuditEngine:
             mask = torch.zeros_like(p, dtype=torch.bool)
             incl = torch.zeros_like(p)
             self.last_sample_mode, self.last_candidate_count, self.last_capped_fraction = "fixed_count", k, 0.0
-            chosen = None
             if k > 0 and n > 0:
-                chosen = torch.randperm(n, device=p.device, generator=gen)[:k]
-                mask[chosen] = True
+                if chosen is None:
+                    chosen = self.fixed_count_index(n, k, seed, p.device)
+                mask.index_fill_(0, chosen, True)
                 incl.fill_(float(k) / float(n))
+            else:
+                chosen = None
             return mask, incl, chosen, k
+        if chosen is not None:
+            raise ValueError("precomputed audit rows need the fixed-count sampler")
+        gen = torch.Generator(device=p.device)
+        gen.manual_seed(seed)
         self.last_sample_mode = "bernoulli"
         mask = torch.bernoulli(p, generator=gen).bool()
         incl = p.clone()
@@ -111,14 +125,15 @@ class AuditEngine:
             mask = capped
         return mask, incl, None, None
 
-    def correction(self, model: RecursiveModel, tokens, targets, hot: ModelOutput, *, seed: int) -> AuditResult:
-        """rte/audit.py:245-387."""
+    def correction(self, model: RecursiveModel, tokens, targets, hot: ModelOutput, *, seed: int,
+                   chosen: torch.Tensor | None = None) -> AuditResult:
+        """rte/audit.py:245-387.  `chosen`: fixed-count audit rows drawn ahead (captured steps)."""
         if hot.loss_per_sample is None:
             raise ValueError("hot output must include per-sample losses")
         if self.config.audit_fixed_count_per_batch is None:
             self.flush_pending()  # the Bernoulli sampler's probability depends on the last residual
         req = self.compute_audit_prob(hot.meta)
-        mask, p, chosen, count = self.sample_mask_with_prob(req, seed=seed)
+        mask, p, chosen, count = self.sample_mask_with_prob(req, seed=seed, chosen=chosen)
         corrected = hot.loss_per_sample.clone()
         zero = hot.loss_per_sample.new_zeros(())
         aux = {k: zero for k in ("hid", "cos", "kl", "norm", "cons", "delta_dir", "delta_rms", "endpoint_normed",

@@ -582,6 +582,53 @@ def lm_head_ce(hidden, w, targets):
     return LMHeadCEFn.apply(hidden, w, targets)
 
 
+# ----------------------------------------------------------------------------- segmented row reduction
+
+def segment_reduce_rows(keys, n_keys: int, rows, *, w=None, row_div: int = 1, out=None,
+                        accumulate: bool = False) -> torch.Tensor:
+    """out[v] (+)= sum over p with keys[p] = v of w[p] * rows[p // row_div] (fp32 [n_keys, d]),
+    summed in a fixed order (deterministic, no atomics); keys outside [0, n_keys) are skipped."""
+    _lib.require_device_tensors("segment_reduce_rows", keys, rows, w, out)
+    k = keys.reshape(-1).contiguous().to(torch.int32)
+    d = rows.shape[-1]
+    r = rows.reshape(-1, d)
+    if r.dtype not in (F32, BF16):
+        r = r.to(F32)
+    r = r.contiguous()
+    if out is None:
+        out = torch.empty((n_keys, d), dtype=F32, device=r.device)
+        accumulate = False
+    wc = None if w is None else w.reshape(-1).contiguous().to(F32)
+    ws, nb = workspace(_lib.load().rte_segment_reduce_workspace_bytes(k.numel(), n_keys, d), r.device)
+    call("rte_segment_reduce_rows", ptr(k), k.numel(), n_keys, int(row_div), ptr(wc), ptr(r), int(r.dtype == F32), d,
+         ptr(out), int(accumulate), ws, nb, _s())
+    return out
+
+
+class EmbeddingFn(torch.autograd.Function):
+    """weight[ids] with a deterministic backward: dW[v] = sum of the output gradients of the
+    positions holding id v, reduced in a fixed order (replaces the embedding backward's
+    sort + atomic scatter)."""
+
+    @staticmethod
+    def forward(ctx, weight, ids):
+        _lib.require_device_tensors("embedding", weight, ids)
+        out = weight.index_select(0, ids.reshape(-1)).view(*ids.shape, weight.shape[1])
+        ctx.save_for_backward(ids)
+        ctx.n = weight.shape[0]
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        (ids,) = ctx.saved_tensors
+        dw = segment_reduce_rows(ids, ctx.n, dout.reshape(-1, dout.shape[-1]))
+        return dw, None
+
+
+def embedding(weight, ids):
+    return EmbeddingFn.apply(weight, ids)
+
+
 # ----------------------------------------------------------------------------- shortlist output head
 
 def shortlist_build(targets, top_clusters, members, hard_negatives: int, random_negs, max_tokens: int,

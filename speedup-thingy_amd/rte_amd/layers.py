@@ -35,6 +35,14 @@ class RMSNorm(nn.Module):
         return K.k_fused_rmsnorm(x, self.weight, eps=self.eps)[0]
 
 
+class Embedding(nn.Embedding):
+    """nn.Embedding (same parameter and state-dict key) whose backward is the deterministic
+    segmented row reduction instead of a sort + atomic scatter."""
+
+    def forward(self, ids: torch.Tensor) -> torch.Tensor:
+        return hip_ops.embedding(self.weight, ids)
+
+
 class RotaryEmbedding(nn.Module):
     """cos/sin tables [max_seq_len, dim] with frequencies repeated per interleaved pair
     (rte/layers.py:36-44)."""

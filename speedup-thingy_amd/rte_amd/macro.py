@@ -204,7 +204,8 @@ class MacroOperators(nn.Module):
         dst = self.cons_dst_idx.unsqueeze(1).expand(pc, b).reshape(-1)
         direct = self.apply_vectorized(h_rep, h0_rep, r_rep, dst)
         twice = self.apply_vectorized(self.apply_vectorized(h_rep, h0_rep, r_rep, src), h0_rep, r_rep, src)
-        return F.mse_loss(direct, twice)
+        # F.mse_loss (mean of squares) as staged means: per row, per sample, then over samples
+        return (direct - twice).square().mean(dim=-1).mean(dim=-1).mean()
 
 
 def macro_distill_loss(hot_hidden, exact_hidden, hot_logits, exact_logits, *, h0=None, lambda_hid=0.0,
@@ -237,8 +238,12 @@ def macro_distill_loss(hot_hidden, exact_hidden, hot_logits, exact_logits, *, h0
         delta_dir = delta_rms = endpoint_normed = endpoint_raw = rms_trust = zero
     if hot_logits is not None and exact_logits is not None and hot_logits.shape == exact_logits.shape:
         t = max(float(temperature), 1e-6)
-        kl = F.kl_div(F.log_softmax(hot_logits / t, dim=-1), F.softmax(exact_logits / t, dim=-1),
-                      reduction="batchmean") * (t**2)
+        # F.kl_div(log q, p, reduction="batchmean") = sum p (log p - log q) / batch, reduced row
+        # by row first (a per-row reduction keeps every partial sum inside one workgroup)
+        logq = F.log_softmax(hot_logits / t, dim=-1)
+        p = F.softmax(exact_logits / t, dim=-1)
+        rows = (torch.xlogy(p, p) - p * logq).sum(dim=-1)
+        kl = rows.reshape(rows.shape[0], -1).sum(dim=-1).sum() / hot_logits.shape[0] * (t**2)
     else:
         kl = zero
     return {

@@ -17,7 +17,7 @@ from torch import nn
 from rte_amd.config import ModelConfig, OutputConfig
 from rte_amd.kernels import hip_ops
 from rte_amd.kernels import optimized as K
-from rte_amd.layers import BankedRecursiveCore, RMSNorm, TransformerBlock
+from rte_amd.layers import BankedRecursiveCore, Embedding, RMSNorm, TransformerBlock
 from rte_amd.macro import MacroOperators, MacroTrace
 from rte_amd.output import ShortlistHead, ShortlistResult
 from rte_amd.recipes import RecipeBank
@@ -67,7 +67,7 @@ class DenseModel(nn.Module):
         if config.topology != "dense":
             raise ValueError("DenseModel requires topology='dense'")
         self.config = config
-        self.embed = nn.Embedding(config.vocab_size, config.d_model)
+        self.embed = Embedding(config.vocab_size, config.d_model)
         self.blocks = nn.Sequential(*[TransformerBlock(config) for _ in range(config.n_dense_layers)])
         self.final_norm = RMSNorm(config.d_model)
         self.lm_head = None if config.tie_embeddings else nn.Linear(config.d_model, config.vocab_size, bias=False)
@@ -95,7 +95,7 @@ class RecursiveModel(nn.Module):
         self.output_config = output_config or OutputConfig()
         self.recipe_bank = RecipeBank(config)
         self.register_buffer("active_touch_table", self.recipe_bank.active_touch_table, persistent=False)
-        self.embed = nn.Embedding(config.vocab_size, config.d_model)
+        self.embed = Embedding(config.vocab_size, config.d_model)
         self.prelude = nn.Sequential(*[TransformerBlock(config) for _ in range(config.n_prelude)])
         self.router = Router(config)
         self.core = BankedRecursiveCore(config, self.recipe_bank)
@@ -161,7 +161,8 @@ class RecursiveModel(nn.Module):
                                           router_decisions=route)
 
     def forward_macro(self, tokens, targets=None, return_states=False, return_loss_per_sample=False, *,
-                      shortlist=False, seed=0, fixed_recipe=None, fixed_depth=None) -> ModelOutput:
+                      shortlist=False, seed=0, fixed_recipe=None, fixed_depth=None,
+                      shortlist_random_negs=None) -> ModelOutput:
         h0 = self._prelude(tokens)
         route = self.router(h0, fixed_recipe=fixed_recipe, fixed_depth=fixed_depth)
         h, trace = self.macro(h0, h0, route.recipe_id, route.depth, return_states=return_states)
@@ -169,7 +170,8 @@ class RecursiveModel(nn.Module):
         if shortlist and targets is not None:
             hidden = self._coda_hidden(h)
             full_logits = None
-            sl = self.shortlist_head.loss(hidden, targets, self.vocab_weight, seed=seed)
+            sl = self.shortlist_head.loss(hidden, targets, self.vocab_weight, seed=seed,
+                                          random_negs=shortlist_random_negs)
             lps, logits = sl.loss_per_sample, sl.logits
         else:
             hidden = self._coda_hidden(h)

@@ -61,27 +61,30 @@ class ShortlistHead(nn.Module):
             lg = hip_ops.linear(hidden.detach(), w, out_f32=True)
         return lg[..., :C].contiguous() if pad else lg
 
-    def build_shortlist(self, hidden, targets, *, seed: int):
+    def build_shortlist(self, hidden, targets, *, seed: int, random_negs=None):
         """(shortlist int64 [b, s, L], target positions (zeros), cluster logits, duplicate count)."""
-        sl, cl, dup = self._build(hidden, targets, seed)
+        sl, cl, dup = self._build(hidden, targets, seed, random_negs)
         return sl.long(), torch.zeros_like(targets, dtype=torch.long), cl, dup.sum().float()
 
-    def _build(self, hidden, targets, seed: int):
+    def random_negatives(self, b: int, s: int, seed: int, device) -> torch.Tensor:
+        """The seeded random negatives of rte/output.py:86-94 (drawable ahead of a captured step)."""
+        gen = torch.Generator(device=device)
+        gen.manual_seed(seed)
+        return torch.randint(0, self.vocab_size, (b, s, self.config.random_negatives), device=device, generator=gen)
+
+    def _build(self, hidden, targets, seed: int, random_negs=None):
         b, s, _ = hidden.shape
-        dev = hidden.device
         cl = self.cluster_logits(hidden)
         k = min(self.config.shortlist_top_clusters, self.config.num_clusters)
         top, _ = hip_ops.route_topk(cl.reshape(b * s, -1), k)
-        gen = torch.Generator(device=dev)
-        gen.manual_seed(seed)
-        rnd = torch.randint(0, self.vocab_size, (b, s, self.config.random_negatives), device=dev, generator=gen)
+        rnd = random_negs if random_negs is not None else self.random_negatives(b, s, seed, hidden.device)
         sl, dup = hip_ops.shortlist_build(targets, top, self.cluster_members, self.config.hard_negatives, rnd,
                                           self.config.shortlist_max_tokens, self.vocab_size)
         return sl, cl, dup
 
-    def loss(self, hidden, targets, vocab_weight, *, seed: int) -> ShortlistResult:
+    def loss(self, hidden, targets, vocab_weight, *, seed: int, random_negs=None) -> ShortlistResult:
         """Per-sample CE over the shortlist logits (rte/output.py:112-136)."""
-        sl, cl, dup = self._build(hidden, targets, seed)
+        sl, cl, dup = self._build(hidden, targets, seed, random_negs)
         logits, tok = hip_ops.shortlist_ce(hidden, vocab_weight, sl)
         return ShortlistResult(tok.sum(dim=-1), logits, sl.long(), torch.zeros_like(targets, dtype=torch.long), cl,
                                dup.sum().float())

@@ -67,10 +67,11 @@ class RecipeBank:
         return self.recipes[int(recipe_id)]
 
     def update_usage(self, recipe_ids: torch.Tensor, beta: float = 0.98) -> None:
-        # kept on the ids' device; no host sync (the reference moves ids to the CPU here)
+        # kept on the ids' device with no host sync (the reference moves ids to the CPU and
+        # bincounts there); counts of ones are exact in fp32 whatever the summation order
         ids = recipe_ids.detach().long().flatten()
-        counts = torch.bincount(ids, minlength=self.config.recipe_count).float()
+        if self.usage_ema.device != ids.device:
+            self.usage_ema = self.usage_ema.to(ids.device)
+        counts = torch.zeros_like(self.usage_ema).index_add_(0, ids, torch.ones_like(ids, dtype=torch.float32))
         probs = counts / counts.sum().clamp_min(1.0)
-        if self.usage_ema.device != probs.device:
-            self.usage_ema = self.usage_ema.to(probs.device)
         self.usage_ema.mul_(beta).add_(probs, alpha=1.0 - beta)

@@ -87,6 +87,9 @@ class TrainEngine:
         self.global_micro_step = 0
         self.tokens_seen = 0
         self.last_grad_metrics: dict[str, Any] = {}
+        self._graph_enabled = False
+        self._graph_keep = False
+        self._gstate: dict[str, Any] | None = None
 
     # ------------------------------------------------------------------ optimizer
     def _param_groups(self) -> list[dict[str, Any]]:
@@ -210,25 +213,25 @@ class TrainEngine:
         return router_aux_losses(r.recipe_probs, r.expected_depth, self.recursive_model.recipe_bank.usage_ema,
                                  self.config.training)
 
-    def _step_macro(self, batch, *, shortlist: bool, check_finite: bool):
-        """rte/training.py:1336-1476."""
+    def _macro_loss(self, tokens, targets, *, shortlist: bool, chosen=None, random_negs=None):
+        """Forward of the recursive_macro step (rte/training.py:1336-1385): hot path, audit
+        correction, router aux; loss = corrected CE / S + macro aux + router aux."""
         tr = self.config.training
         m = self.recursive_model
-        if shortlist and tr.debug_force_full_output:
-            raise RuntimeError("debug_force_full_output forbids recursive_macro_shortlist")
-        tokens, targets = self._move(batch)
         with self._autocast():
             hot = m.forward_macro(tokens, targets, return_states=True, return_loss_per_sample=True,
                                   shortlist=shortlist, seed=tr.seed + self.global_step, fixed_recipe=tr.fixed_recipe,
-                                  fixed_depth=tr.fixed_depth)
-            audit = self.audit_engine.correction(m, tokens, targets, hot, seed=tr.seed + 10_000 + self.global_step)
+                                  fixed_depth=tr.fixed_depth, shortlist_random_negs=random_negs)
+            audit = self.audit_engine.correction(m, tokens, targets, hot, seed=tr.seed + 10_000 + self.global_step,
+                                                 chosen=chosen)
             aux = self._router_aux(hot)
             scale = self._loss_scale(targets)
             loss = audit.corrected_loss_per_sample.mean() / scale + sum(audit.macro_aux.values()) + sum(aux.values())
-        stepped = self._finish_step(loss, check_finite=check_finite)
-        m.recipe_bank.update_usage(hot.meta.recipe_ids, beta=tr.coverage_beta)
-        self.tokens_seen += tokens.numel()
-        metrics = {
+        return loss, hot, audit, aux, scale
+
+    def _macro_metrics(self, loss, hot, audit, aux, scale, targets, shortlist, stepped):
+        """rte/training.py:1412-1472 metric keys."""
+        return {
             "mode": "recursive_macro_shortlist" if shortlist else "recursive_macro",
             "loss": loss.detach(),
             "hot_lm_loss": hot.loss_per_sample.detach().mean() / scale,
@@ -241,7 +244,133 @@ class TrainEngine:
             **{f"aux_{k}": v.detach() for k, v in aux.items()},
             **self.last_grad_metrics,
         }
+
+    def _step_macro(self, batch, *, shortlist: bool, check_finite: bool):
+        """rte/training.py:1336-1476."""
+        tr = self.config.training
+        m = self.recursive_model
+        if shortlist and tr.debug_force_full_output:
+            raise RuntimeError("debug_force_full_output forbids recursive_macro_shortlist")
+        if self._graph_enabled:
+            return self._graph_macro_step(batch, shortlist, check_finite)
+        tokens, targets = self._move(batch)
+        loss, hot, audit, aux, scale = self._macro_loss(tokens, targets, shortlist=shortlist)
+        stepped = self._finish_step(loss, check_finite=check_finite)
+        m.recipe_bank.update_usage(hot.meta.recipe_ids, beta=tr.coverage_beta)
+        self.tokens_seen += tokens.numel()
+        metrics = self._macro_metrics(loss, hot, audit, aux, scale, targets, shortlist, stepped)
         return TrainStepResult(loss, hot, metrics, audit)
+
+    # ------------------------------------------------------------------ captured step
+    def enable_graph_capture(self, enabled: bool = True, *, keep_graph: bool = False) -> None:
+        """Run recursive_macro(_shortlist) steps as one captured HIP graph: forward, audit
+        replay, backward, gradient metrics and the fused AdamW update, replayed with one launch.
+
+        The first two steps run eagerly (on a side stream, through the same static input
+        buffers) to settle allocations and library state; the third is captured and every
+        later step replays the graph.  The step's randomness (the fixed-count audit rows and
+        the shortlist's random negatives) is drawn eagerly before each replay from the same
+        seeds as the eager step.  The non-finite-loss skip becomes a device-side flag that
+        the fused AdamW reads (found_inf): the update and its step count are skipped, and
+        ``metrics["stepped"]`` is a device bool.  Tensors inside the returned model output and
+        audit result are the graph's static buffers, overwritten by the next step; the loss
+        and metrics are copied out.  keep_graph keeps the captured graph's nodes inspectable
+        (``torch.cuda.CUDAGraph(keep_graph=True)``)."""
+        tr = self.config.training
+        if enabled:
+            if tr.mode not in ("recursive_macro", "recursive_macro_shortlist"):
+                raise ValueError("graph capture covers the recursive_macro modes")
+            if tr.grad_accum_steps != 1:
+                raise ValueError("graph capture needs grad_accum_steps == 1")
+            if self.audit_engine.config.audit_fixed_count_per_batch is None:
+                raise ValueError("graph capture needs the fixed-count audit sampler (its count is known on the host)")
+            if self.device.type != "cuda" or not isinstance(self.optimizer, torch.optim.AdamW):
+                raise ValueError("graph capture needs a ROCm device and the fused AdamW")
+            for g in self.optimizer.param_groups:
+                g["capturable"] = True
+        self._graph_enabled = enabled
+        self._graph_keep = keep_graph
+        self._gstate = None
+
+    def _graph_macro_step(self, batch, shortlist: bool, check_finite: bool):
+        tr = self.config.training
+        m = self.recursive_model
+        tokens, targets = self._move(batch)
+        key = (tuple(tokens.shape), tuple(targets.shape), shortlist, check_finite)
+        st = self._gstate
+        if st is None or st["key"] != key:
+            B, S = targets.shape
+            k = min(int(self.audit_engine.config.audit_fixed_count_per_batch), B)
+            st = self._gstate = {
+                "key": key, "graph": None, "warm": 0, "out": None,
+                "tokens": torch.empty_like(tokens), "targets": torch.empty_like(targets),
+                "chosen": torch.zeros((k,), dtype=torch.long, device=self.device),
+                "rnd": (torch.zeros((B, S, self.config.output.random_negatives), dtype=torch.long, device=self.device)
+                        if shortlist else None),
+            }
+        st["tokens"].copy_(tokens)
+        st["targets"].copy_(targets)
+        B, S = targets.shape
+        if st["chosen"].numel():
+            st["chosen"].copy_(self.audit_engine.fixed_count_index(B, st["chosen"].numel(),
+                                                                   tr.seed + 10_000 + self.global_step, self.device))
+        if shortlist:
+            st["rnd"].copy_(m.shortlist_head.random_negatives(B, S, tr.seed + self.global_step, self.device))
+        if st["graph"] is None and st["warm"] < 2:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                out = self._graph_body(st, shortlist, check_finite)
+            torch.cuda.current_stream().wait_stream(side)
+            st["warm"] += 1
+        else:
+            if st["graph"] is None:
+                self.optimizer.zero_grad(set_to_none=True)
+                graph = torch.cuda.CUDAGraph(keep_graph=self._graph_keep)
+                with torch.cuda.graph(graph):
+                    st["out"] = self._graph_body(st, shortlist, check_finite)
+                st["graph"] = graph
+            st["graph"].replay()
+            out = st["out"]
+        self.global_micro_step += 1
+        self.global_step += 1
+        self.tokens_seen += tokens.numel()
+        flat = out["flat"].clone()
+        metrics = dict(out["host_metrics"])
+        metrics.update({name: flat[i] for i, name in enumerate(out["names"])})
+        metrics["stepped"] = metrics["stepped"] > 0.5
+        self.last_grad_metrics = {k: metrics[k] for k in out["grad_names"]}
+        return TrainStepResult(flat[out["names"].index("loss")], out["hot"], metrics, out["audit"])
+
+    def _graph_body(self, st, shortlist: bool, check_finite: bool):
+        """Device work of one captured step; everything here is replayed as recorded."""
+        tr = self.config.training
+        m = self.recursive_model
+        loss, hot, audit, aux, scale = self._macro_loss(st["tokens"], st["targets"], shortlist=shortlist,
+                                                        chosen=st["chosen"] if st["chosen"].numel() else None,
+                                                        random_negs=st["rnd"])
+        bad = (~torch.isfinite(loss.detach())) if check_finite else torch.zeros((), dtype=torch.bool,
+                                                                                  device=loss.device)
+        loss.backward()
+        if tr.grad_clip_norm is not None:
+            params = [p for g in self.optimizer.param_groups for p in g["params"]]
+            torch.nn.utils.clip_grad_norm_(params, tr.grad_clip_norm, foreach=True)
+        self.last_grad_metrics = self._grad_metrics()
+        self.optimizer.found_inf = bad.float()
+        self.optimizer.grad_scale = None
+        try:
+            self.optimizer.step()
+        finally:
+            del self.optimizer.found_inf
+            del self.optimizer.grad_scale
+        self.optimizer.zero_grad(set_to_none=True)
+        m.recipe_bank.update_usage(hot.meta.recipe_ids, beta=tr.coverage_beta)
+        metrics = self._macro_metrics(loss, hot, audit, aux, scale, st["targets"], shortlist, ~bad)
+        names = [k for k, v in metrics.items() if isinstance(v, torch.Tensor)]
+        flat = torch.stack([metrics[k].detach().float().reshape(()) for k in names])
+        return {"flat": flat, "names": names, "hot": hot, "audit": audit,
+                "host_metrics": {k: v for k, v in metrics.items() if not isinstance(v, torch.Tensor)},
+                "grad_names": list(self.last_grad_metrics)}
 
     # ------------------------------------------------------------------ checkpoint (rte/training.py:1656-1701)
     def save_checkpoint(self, path) -> None:

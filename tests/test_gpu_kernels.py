@@ -474,3 +474,47 @@ def test_shortlist_head_matches_oracle():
     _, _, rdw = SLO.shortlist_logits_ce_bwd(hb, wb, want, rl, rlse, np.ones(b * s))
     assert_rel(_np(vw.grad), rdw, FP32_RTOL, "head dW")
     _ = LO
+
+
+# ---------------------------------------------------------------- segmented row reduction
+
+@pytest.mark.parametrize("P,V,d,div,f32", [(5000, 300, 128, 1, True), (20000, 64, 512, 4, False),
+                                         (70000, 2048, 64, 1, True), (3, 10, 8, 1, False), (0, 16, 32, 1, True)])
+def test_segment_reduce_rows(P, V, d, div, f32):
+    H = _ops()
+    rng = np.random.default_rng(P + V)
+    keys = rng.integers(-3, V + 3, P)
+    if P > 100:
+        keys[: P // 3] = 7 % V                      # one key with many chunks
+    rows = rng.standard_normal((max(P // div + 1, 1), d)).astype(np.float32)
+    if not f32:
+        rows = bf16_round(rows)
+    w = rng.standard_normal(P).astype(np.float32)
+    tk = torch.from_numpy(keys).to(DEV)
+    tr = torch.from_numpy(rows).to(DEV)
+    if not f32:
+        tr = tr.to(torch.bfloat16)
+    tw = torch.from_numpy(w).to(DEV)
+    print(f"segment_reduce P={P} V={V} d={d} div={div} f32={f32}", flush=True)
+    a = H.segment_reduce_rows(tk, V, tr, w=tw, row_div=div)
+    b = H.segment_reduce_rows(tk, V, tr, w=tw, row_div=div)
+    assert torch.equal(a, b), "segment reduce not bitwise repeatable"
+    want = R.segment_reduce_rows(keys, V, rows, w, row_div=div)
+    assert_rel(_np(a), want, FP32_RTOL, "segment reduce")
+    acc = torch.ones_like(a)
+    H.segment_reduce_rows(tk, V, tr, w=tw, row_div=div, out=acc, accumulate=True)
+    assert_rel(_np(acc), want + 1.0, FP32_RTOL, "segment reduce accumulate")
+
+
+def test_embedding_backward_deterministic():
+    H = _ops()
+    torch.manual_seed(0)
+    W = torch.randn(300, 64, device=DEV, requires_grad=True)
+    ids = torch.randint(0, 300, (8, 50), device=DEV)
+    ids[:, :10] = 3
+    g = torch.randn(8, 50, 64, device=DEV)
+    out = H.embedding(W, ids)
+    assert torch.equal(out, W.detach()[ids])
+    out.backward(g)
+    want = torch.zeros(300, 64, dtype=torch.float64).index_add_(0, ids.reshape(-1).cpu(), g.reshape(-1, 64).double().cpu())
+    assert_rel(W.grad.double().cpu().numpy(), want.numpy(), FP32_RTOL, "embedding dW")

@@ -345,3 +345,55 @@ def test_banked_swiglu_weight_gradients_exact_layout():
     assert_rel(out.detach().double().cpu().numpy(), want, BF16_RTOL, "banked ffn out")
     assert_rel(core.mlp.wug.grad.double().cpu().numpy(), dwug, BF16_RTOL, "banked dwug")
     assert_rel(core.mlp.wd.grad.double().cpu().numpy(), dwd, BF16_RTOL, "banked dwd")
+
+
+def _graph_node_kinds(graph) -> dict[str, int]:
+    """Node census of a captured graph through the HIP runtime API."""
+    import collections
+    import ctypes
+
+    hip = ctypes.CDLL("libamdhip64.so")
+    gp = ctypes.c_void_p(graph.raw_cuda_graph())
+    n = ctypes.c_size_t(0)
+    assert hip.hipGraphGetNodes(gp, None, ctypes.byref(n)) == 0
+    nodes = (ctypes.c_void_p * max(n.value, 1))()
+    assert hip.hipGraphGetNodes(gp, nodes, ctypes.byref(n)) == 0
+    names = {0: "kernel", 1: "memcpy", 2: "memset", 3: "host", 4: "graph", 5: "empty", 6: "wait_event",
+             7: "event_record"}
+    kinds = collections.Counter()
+    for i in range(n.value):
+        t = ctypes.c_int(-1)
+        hip.hipGraphNodeGetType(ctypes.c_void_p(nodes[i]), ctypes.byref(t))
+        kinds[names.get(t.value, str(t.value))] += 1
+    return dict(kinds)
+
+
+@pytest.mark.parametrize("mode", ["recursive_macro", "recursive_macro_shortlist"])
+def test_captured_step_matches_eager(mode):
+    """Eager and captured engines from the same seed on the same batches: every replay (with
+    eager work and synchronisation between replays) reproduces the eager step's loss and
+    metrics, the parameters agree afterwards, and the graph holds no memset node."""
+    a = _engine(mode)
+    b = _engine(mode)
+    b.enable_graph_capture(True, keep_graph=True)
+    g = torch.Generator().manual_seed(11)
+    batches = [torch.randint(0, 256, (4, 17), generator=g) for _ in range(3)]
+    for step in range(6):
+        tok = batches[step % 3]
+        print(f"captured-vs-eager {mode} step {step}", flush=True)
+        ra = a.train_step((tok[:, :-1], tok[:, 1:]))
+        rb = b.train_step((tok[:, :-1], tok[:, 1:]))
+        torch.cuda.synchronize()
+        la, lb = float(ra.loss.detach()), float(rb.loss)
+        assert abs(la - lb) <= 1e-5 * max(abs(la), 1.0), (step, la, lb)
+        for k, v in ra.metrics.items():
+            if isinstance(v, torch.Tensor) and v.numel() == 1 and v.dtype.is_floating_point:
+                x, y = float(v), float(rb.metrics[k])
+                assert abs(x - y) <= 1e-4 * max(abs(x), 1e-3) + 1e-6, (step, k, x, y)
+        assert bool(rb.metrics["stepped"])
+    for (na, pa), (nb, pb) in zip(a.recursive_model.named_parameters(), b.recursive_model.named_parameters()):
+        assert torch.allclose(pa, pb, rtol=1e-5, atol=1e-6), na
+    kinds = _graph_node_kinds(b._gstate["graph"])
+    print("graph nodes", kinds, flush=True)
+    assert kinds.get("memset", 0) == 0, kinds
+    assert kinds.get("kernel", 0) > 100

@@ -165,3 +165,20 @@ def test_deterministic_gathers_match_indexing_gradients():
     w = torch.randn(5, 3, requires_grad=True)
     gather_rows(w, torch.tensor([4, 4, 0])).sum().backward()
     assert torch.allclose(w.grad[4], torch.full((3,), 2.0)) and torch.allclose(w.grad[1], torch.zeros(3))
+
+
+def test_staged_reductions_equal_torch_losses():
+    """The per-row forms used for the distillation KL and the consistency MSE equal
+    F.kl_div(batchmean) and F.mse_loss."""
+    from rte_amd.macro import macro_distill_loss
+
+    torch.manual_seed(3)
+    hot, exact = torch.randn(2, 5, 11, dtype=torch.float64), torch.randn(2, 5, 11, dtype=torch.float64)
+    hh, eh = torch.randn(2, 5, 4, dtype=torch.float64), torch.randn(2, 5, 4, dtype=torch.float64)
+    t = 1.7
+    got = macro_distill_loss(hh, eh, hot, exact, lambda_kl=1.0, temperature=t)["kl"]
+    want = torch.nn.functional.kl_div(torch.log_softmax(hot / t, -1), torch.softmax(exact / t, -1),
+                                      reduction="batchmean") * t * t
+    assert torch.allclose(got, want, rtol=1e-12, atol=1e-12)
+    a, b = torch.randn(6, 7, 9, dtype=torch.float64), torch.randn(6, 7, 9, dtype=torch.float64)
+    assert torch.allclose((a - b).square().mean(dim=-1).mean(dim=-1).mean(), torch.nn.functional.mse_loss(a, b))

@@ -574,3 +574,23 @@ def test_banked_core_inactive_samples_keep_state():
     np.testing.assert_allclose(out[2], BK.core_step(h[2], h[2], recipes[5], p, 1, **kw), rtol=1e-12)
     zero = dict(p, pass_attn_scale=np.zeros(t), pass_mlp_scale=np.zeros(t))
     np.testing.assert_allclose(BK.core_step(h[0], h[0], recipes[0], zero, 0, **kw), h[0], rtol=0, atol=0)
+
+
+# ---------------------------------------------------------------- segmented row reduction
+
+def test_segment_reduce_matches_index_add_and_loop():
+    rng = _rng(60)
+    P, V, d, div = 300, 17, 6, 3
+    keys = rng.integers(-2, V + 2, P)
+    rows = rng.standard_normal((P // div + 1, d))
+    w = rng.standard_normal(P)
+    got = R.segment_reduce_rows(keys, V, rows, w, row_div=div)
+    want = np.zeros((V, d))
+    for p in range(P):
+        if 0 <= keys[p] < V:
+            want[keys[p]] += w[p] * rows[p // div]
+    np.testing.assert_allclose(got, want, rtol=1e-12, atol=1e-12)
+    ok = (keys >= 0) & (keys < V)
+    t = torch.zeros(V, d, dtype=torch.float64).index_add_(
+        0, torch.tensor(keys[ok]), torch.tensor(w[ok, None] * rows[np.arange(P)[ok] // div]))
+    np.testing.assert_allclose(got, t.numpy(), rtol=1e-12, atol=1e-12)
