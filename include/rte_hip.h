@@ -115,7 +115,11 @@ int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const 
                            int n, int P, const int32_t* tok_of_slot, const int32_t* pair_of_slot,
                            const float* w_of_slot, const void* wug, const void* wd, int64_t ld_wd,
                            const void* ug, const void* zw, void* dug, float* dw_slot, void* dx_pairs,
-                           float* dwug, float* dwd, void* stream);
+                           float* dwug, float* dwd, void* workspace, size_t workspace_bytes, void* stream);
+/* Workspace with which the per-cluster weight gradients of rte_grouped_swiglu_bwd are
+ * reduced by several workgroups per cluster when routing is skewed (fixed chunk order, so
+ * still deterministic).  NULL / too small: one workgroup column per cluster. */
+size_t rte_grouped_swiglu_bwd_workspace_bytes(int P, int G, int n, int d);
 
 /* ---- dense SwiGLU (rte/layers.py:78-116 DenseSwiGLU / PackedDenseSwiGLU;
  *      rte/kernels/active_swiglu_triton.py:62-102 fused activation fwd/bwd) ----
@@ -178,6 +182,26 @@ int rte_ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* tar
                void* stream);
 int rte_ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
                const float* dloss, const float* extra, void* dlogits, void* stream);
+
+/* ---- grouped linear: rows keyed to a group, one weight matrix per group ----
+ * Replaces the per-sample weight gather + bmm of the macro operators (rte/macro.py:201-236,
+ * gather of v / u by (recipe, stride) at :208-212) without materialising per-sample weights.
+ * Slots come from rte_pack_index over the rows' group keys (k = 1): offsets [G+1],
+ * row_of_slot (tok_of_slot) and out_row_of_slot (pair_of_slot).  w bf16 [G, K, Nout] row-major.
+ *   fwd: y[out_row(s)] = x[row(s)] @ W_g            x bf16 [N, K], y f32 (y_f32=1) or bf16 [N, Nout]
+ *   bwd: dx[row(s)] = dy[out_row(s)] @ W_g^T        (dx optional, f32 or bf16)
+ *        dW_g = sum_s x[row(s)]^T dy[out_row(s)]   (dw f32 [G, K, Nout], optional; fixed order)
+ * Rows of invalid keys are not written.  K % 8 == 0, Nout % 8 == 0. */
+int rte_grouped_linear_fwd(const void* x, int N, int K, const int32_t* offsets, int G, int P,
+                           const int32_t* row_of_slot, const int32_t* out_row_of_slot, const void* w, int Nout,
+                           void* y, int y_f32, void* stream);
+int rte_grouped_linear_bwd(const void* dy, const void* x, int N, int K, const int32_t* offsets, int G, int P,
+                           const int32_t* row_of_slot, const int32_t* out_row_of_slot, const void* w, int Nout,
+                           void* dx, int dx_f32, float* dw, void* workspace, size_t workspace_bytes,
+                           void* stream);
+/* Workspace that splits large groups of the dW reduction over several workgroups (same
+ * contract as rte_grouped_swiglu_bwd_workspace_bytes). */
+size_t rte_grouped_linear_bwd_workspace_bytes(int P, int G, int K, int Nout);
 
 /* ---- deterministic segmented row reduction (rte/kernels/cluster_pool_ffn.py:218-241 index_add_
  * of pool gradients; the backward of every row gather / embedding lookup) ----

@@ -233,7 +233,7 @@ int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const 
                            int P, const int32_t* tok_of_slot, const int32_t* pair_of_slot,
                            const float* w_of_slot, const void* wug, const void* wd, int64_t ld_wd, const void* ug,
                            const void* zw, void* dug, float* dw_slot, void* dx_pairs, float* dwug, float* dwd,
-                           void* stream) {
+                           void* workspace, size_t workspace_bytes, void* stream) {
   RTE_REQUIRE(n % 32 == 0 && n <= 128, "grouped_swiglu_bwd: n must be a multiple of 32 and <= 128");
   RTE_REQUIRE(d % 8 == 0, "grouped_swiglu_bwd: d_model must be a multiple of 8");
   const int dff = G * n;
@@ -299,7 +299,7 @@ int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const 
     p.epi.c_f32 = 1;
     p.epi.c_growstride = 2 * n;
     p.epi.c_ilv = dff;
-    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
   }
   {
     // dWd[:, g*n + j] = sum_slot dout[tok(slot), :] zw[slot, j]
@@ -319,11 +319,16 @@ int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const 
     p.epi.ldc = ld_wd;
     p.epi.c_f32 = 1;
     p.epi.c_gstride = n;
-    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
   }
   (void)T;
   (void)pair_of_slot;
   return 0;
+}
+
+size_t rte_grouped_swiglu_bwd_workspace_bytes(int P, int G, int n, int d) {
+  const size_t a = gemm_groupk_bytes(2 * n, d, P, G), b = gemm_groupk_bytes(d, n, P, G);
+  return a > b ? a : b;
 }
 
 int rte_dense_swiglu_fwd(const void* x, int T, int d, int F, const void* wug, const void* wd, int wd_rows,
@@ -743,6 +748,89 @@ int rte_segment_reduce_rows(const int32_t* keys, int64_t P, int V, int row_div, 
                             void* stream) {
   return segreduce_rows(keys, P, V, row_div, w, rows, rows_f32, d, out, accumulate, workspace, workspace_bytes,
                         S(stream));
+}
+
+int rte_grouped_linear_fwd(const void* x, int N, int K, const int32_t* offsets, int G, int P,
+                           const int32_t* row_of_slot, const int32_t* out_row_of_slot, const void* w, int Nout,
+                           void* y, int y_f32, void* stream) {
+  RTE_REQUIRE(K % 8 == 0 && Nout % 8 == 0, "grouped_linear: K and Nout must be multiples of 8");
+  RTE_REQUIRE(N >= 0 && P >= 0 && G >= 1, "grouped_linear: bad sizes");
+  if (P == 0) return 0;
+  // y[out_row(slot)] = x[row(slot)] @ W_g   with W_g [K, Nout] row-major (layout T for B)
+  GemmArgs p;
+  p.mode = MODE_GROUP_M;
+  p.goff = offsets;
+  p.G = G;
+  p.max_tiles_m = P / kGroupTileM + G + 1;
+  p.M = P;
+  p.N = Nout;
+  p.K = K;
+  p.a = plain(x, K);
+  p.a.rows = row_of_slot;
+  p.b = plain(w, Nout);
+  p.b.gstride = (int64_t)K * Nout;
+  p.b_t = 1;
+  p.epi.c = y;
+  p.epi.ldc = Nout;
+  p.epi.c_rows = out_row_of_slot;
+  p.epi.c_f32 = y_f32;
+  (void)N;
+  return gemm_launch(p, EPI_STORE, S(stream));
+}
+
+int rte_grouped_linear_bwd(const void* dy, const void* x, int N, int K, const int32_t* offsets, int G, int P,
+                           const int32_t* row_of_slot, const int32_t* out_row_of_slot, const void* w, int Nout,
+                           void* dx, int dx_f32, float* dw, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  RTE_REQUIRE(K % 8 == 0 && Nout % 8 == 0, "grouped_linear: K and Nout must be multiples of 8");
+  RTE_REQUIRE(N >= 0 && P >= 0 && G >= 1, "grouped_linear: bad sizes");
+  if (dx && P > 0) {
+    // dx[row(slot)] = dy[out_row(slot)] @ W_g^T   (B(n=kk, k=j) = W_g[kk, j]: layout N)
+    GemmArgs p;
+    p.mode = MODE_GROUP_M;
+    p.goff = offsets;
+    p.G = G;
+    p.max_tiles_m = P / kGroupTileM + G + 1;
+    p.M = P;
+    p.N = K;
+    p.K = Nout;
+    p.a = plain(dy, Nout);
+    p.a.rows = out_row_of_slot;
+    p.b = plain(w, Nout);
+    p.b.gstride = (int64_t)K * Nout;
+    p.epi.c = dx;
+    p.epi.ldc = K;
+    p.epi.c_rows = row_of_slot;
+    p.epi.c_f32 = dx_f32;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  if (dw) {
+    // dW_g[kk, j] = sum over the group's slots of x[row(slot), kk] dy[out_row(slot), j]
+    GemmArgs p;
+    p.mode = MODE_GROUP_K;
+    p.goff = offsets;
+    p.G = G;
+    p.M = K;
+    p.N = Nout;
+    p.K = P;
+    p.a = plain(x, K);
+    p.a.rows = row_of_slot;
+    p.a_t = 1;
+    p.b = plain(dy, Nout);
+    p.b.rows = out_row_of_slot;
+    p.b_t = 1;
+    p.epi.c = dw;
+    p.epi.ldc = Nout;
+    p.epi.c_f32 = 1;
+    p.epi.c_gstride = (int64_t)K * Nout;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
+  }
+  (void)N;
+  return 0;
+}
+
+size_t rte_grouped_linear_bwd_workspace_bytes(int P, int G, int K, int Nout) {
+  return gemm_groupk_bytes(K, Nout, P, G);
 }
 
 }  // extern "C"

@@ -263,7 +263,8 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
 
-  int g = 0, m0 = 0, n0 = 0, mlim = p.M, kbeg = 0, kend = p.K, split = 0;
+  int g = 0, m0 = 0, n0 = 0, mlim = p.M, kbeg = 0, kend = p.K;
+  float* partial_dst = nullptr;  // fp32 [M, N] partial of this work item (split-K / chunked group)
   if (p.mode == MODE_GROUP_M) {
     if (tid < 64) {
       if (tid == 0) s_tile[0] = -1;
@@ -294,9 +295,24 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
     m0 = p.goff[g] + s_tile[1] * BM;
     n0 = blockIdx.y * BN;
   } else if (p.mode == MODE_GROUP_K) {
-    g = blockIdx.z;
-    kbeg = p.goff[g];
-    kend = p.goff[g + 1];
+    if (p.gk_chunk > 0) {
+      const int item = blockIdx.z;
+      if (item >= p.gk_first[p.G]) return;  // uniform per workgroup
+      int lo = 0, hi = p.G;  // largest g with gk_first[g] <= item (skips empty groups)
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (p.gk_first[mid] <= item) lo = mid; else hi = mid;
+      }
+      g = lo;
+      const int c = item - p.gk_first[g];
+      kbeg = p.goff[g] + c * p.gk_chunk;
+      kend = kbeg + p.gk_chunk < p.goff[g + 1] ? kbeg + p.gk_chunk : p.goff[g + 1];
+      if (p.gk_first[g + 1] - p.gk_first[g] > 1) partial_dst = p.gk_part + (int64_t)item * p.M * p.N;
+    } else {
+      g = blockIdx.z;
+      kbeg = p.goff[g];
+      kend = p.goff[g + 1];
+    }
     m0 = blockIdx.x * BM;
     n0 = blockIdx.y * BN;
   } else {
@@ -308,9 +324,10 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
     m0 = (lin / gy) * BM;
     n0 = (lin % gy) * BN;
     if (p.splits > 1) {
-      split = blockIdx.z;
+      const int split = blockIdx.z;
       kbeg = split * p.k_chunk;
       kend = kbeg + p.k_chunk < p.K ? kbeg + p.k_chunk : p.K;
+      partial_dst = p.splitk_ws + (int64_t)split * p.M * p.N;
     }
   }
 
@@ -402,9 +419,9 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
         for (int r = 0; r < 16; ++r)
           Cs[(rbase + i * 32 + (r >> 2) * 8 + (r & 3)) * CP + cbase + j * 32] = acc[i][j][r];
     __syncthreads();
-    if (p.splits > 1) {
+    if (partial_dst) {
       // fp32 partial of this k range, plain [M, N]
-      float* ws = p.splitk_ws + (int64_t)split * p.M * p.N;
+      float* ws = partial_dst;
       constexpr int CH = BN / 4;
       for (int c = tid; c < BM * CH; c += kThreads) {
         const int row = c / CH, cc = (c % CH) * 4;
@@ -595,6 +612,52 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
   }
 }
 
+// gk_first[g] = sum over groups before g of ceil(rows_g / chunk)  (single workgroup)
+__global__ void __launch_bounds__(1024) groupk_prefix_kernel(const int32_t* __restrict__ goff, int G, int chunk,
+                                                             int32_t* __restrict__ first) {
+  __shared__ int32_t part[1024];
+  const int tid = threadIdx.x;
+  const int seg = (G + 1023) / 1024;
+  const int b0 = tid * seg, b1 = b0 + seg < G ? b0 + seg : G;
+  int32_t s = 0;
+  for (int g = b0; g < b1; ++g) s += (goff[g + 1] - goff[g] + chunk - 1) / chunk;
+  part[tid] = s;
+  __syncthreads();
+  for (int o = 1; o < 1024; o <<= 1) {
+    const int32_t y = tid >= o ? part[tid - o] : 0;
+    __syncthreads();
+    part[tid] += y;
+    __syncthreads();
+  }
+  int32_t run = part[tid] - s;
+  for (int g = b0; g < b1; ++g) {
+    first[g] = run;
+    run += (goff[g + 1] - goff[g] + chunk - 1) / chunk;
+  }
+  if (tid == 1023) first[G] = part[1023];
+}
+
+// Groups cut into several chunks (or none): add the chunk partials in chunk order and apply
+// the EPI_STORE epilogue.  One-chunk groups were stored by the GEMM itself.
+__global__ void __launch_bounds__(256) groupk_reduce_kernel(GemmArgs p, EpiFlags fl) {
+  const int chunks = (p.N + 3) / 4;
+  const int64_t per_g = (int64_t)p.M * chunks;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= per_g * p.G) return;
+  const int g = (int)(idx / per_g);
+  const int64_t r = idx % per_g;
+  const int m = (int)(r / chunks), n = (int)(r % chunks) * 4;
+  const int q0 = p.gk_first[g], q1 = p.gk_first[g + 1];
+  if (q1 - q0 == 1) return;
+  float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int64_t plane = (int64_t)p.M * p.N;
+  for (int q = q0; q < q1; ++q) {
+    const float* src = p.gk_part + q * plane + (int64_t)m * p.N + n;
+    for (int t = 0; t < 4 && n + t < p.N; ++t) v[t] += src[t];
+  }
+  store_chunk<4>(p.epi, g, m, n, p.N, v, fl.vec);
+}
+
 // Sums split-K partials in split order and applies the EPI_STORE epilogue.
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs p, EpiFlags fl) {
   const int chunks = (p.N + 3) / 4;
@@ -614,6 +677,16 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs p, EpiFlags
   }
   store_chunk<4>(p.epi, 0, m, n, p.N, v, fl.vec);
 }
+
+// Chunk of a GROUP_K group: about twice the mean group size, at least 256 rows, so balanced
+// groups stay whole and a dominant group is shared by many workgroups.
+int groupk_chunk(int K, int G) {
+  int64_t c = (2 * (int64_t)K + G - 1) / (G > 0 ? G : 1);
+  if (c < 256) c = 256;
+  return (int)((c + 63) / 64 * 64);
+}
+
+size_t groupk_first_bytes(int G) { return (((size_t)(G + 1) * 4 + 255) / 256) * 256; }
 
 template <int BM, int BN, int BK, int EPI, bool DUALA = false>
 constexpr size_t lds_bytes() {
@@ -648,6 +721,20 @@ int launch_cfg(const GemmArgs& p0, hipStream_t stream, void* ws, size_t ws_bytes
     grid = dim3(p.max_tiles_m, (p.N + BN - 1) / BN, 1);
   } else if (p.mode == MODE_GROUP_K) {
     grid = dim3((p.M + BM - 1) / BM, (p.N + BN - 1) / BN, p.G);
+    p.gk_chunk = 0;
+    if (EPI == EPI_STORE && ws && p.N % 4 == 0 && p.G >= 1) {
+      const size_t need = gemm_groupk_bytes(p.M, p.N, p.K, p.G);
+      if (need > 0 && ws_bytes >= need) {
+        const int chunk = groupk_chunk(p.K, p.G);
+        p.gk_chunk = chunk;
+        p.gk_first = static_cast<int32_t*>(ws);
+        p.gk_part = reinterpret_cast<float*>(static_cast<char*>(ws) + groupk_first_bytes(p.G));
+        grid.z = (unsigned)((p.K + chunk - 1) / chunk + p.G);
+        hipLaunchKernelGGL(groupk_prefix_kernel, dim3(1), dim3(1024), 0, stream, p.goff, p.G, chunk,
+                           const_cast<int32_t*>(p.gk_first));
+        RTE_TRY(check_launch("gemm_groupk_prefix"));
+      }
+    }
   } else {
     grid = dim3((p.M + BM - 1) / BM, (p.N + BN - 1) / BN, 1);
     // split the reduction when the tile grid cannot fill the GPU
@@ -677,6 +764,11 @@ int launch_cfg(const GemmArgs& p0, hipStream_t stream, void* ws, size_t ws_bytes
     hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p, fl);
     RTE_TRY(check_launch("gemm_splitk_reduce"));
   }
+  if (p.mode == MODE_GROUP_K && p.gk_chunk > 0) {
+    const int64_t n = (int64_t)p.G * p.M * ((p.N + 3) / 4);
+    hipLaunchKernelGGL(groupk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p, fl);
+    RTE_TRY(check_launch("gemm_groupk_reduce"));
+  }
   return 0;
 }
 
@@ -693,6 +785,13 @@ bool pow2_or_zero(int v) { return v == 0 || (v > 0 && (v & (v - 1)) == 0); }
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 }  // namespace
+
+size_t gemm_groupk_bytes(int M, int N, int K, int G) {
+  if (M <= 0 || N <= 0 || K <= 0 || G <= 0) return 0;
+  const int chunk = groupk_chunk(K, G);
+  const size_t items = (size_t)((K + chunk - 1) / chunk) + (size_t)G;
+  return groupk_first_bytes(G) + items * (size_t)M * N * sizeof(float);
+}
 
 size_t gemm_splitk_bytes(int M, int N, int K) {
   int splits = K / 512;

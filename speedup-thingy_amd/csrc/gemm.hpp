@@ -88,6 +88,13 @@ struct GemmArgs {
   // EPI_SWIGLU_FWD only: gate columns read A at k + a_koff2 (two low-rank codes side by
   // side in one A row, e.g. [x U_up | x U_gate]); 0 = both halves read the same A columns.
   int a_koff2 = 0;
+  // GROUP_K with chunked groups (set by gemm_launch when a workspace is given): group g's k
+  // range is cut into chunks of gk_chunk; work item i (grid z) is chunk i - gk_first[g] of the
+  // group g with gk_first[g] <= i < gk_first[g + 1].  A group of one chunk stores directly;
+  // larger groups store fp32 partials [item, M, N] that a second kernel adds in chunk order.
+  int gk_chunk = 0;
+  const int32_t* gk_first = nullptr;  // [G + 1]
+  float* gk_part = nullptr;
   Epilogue epi;
 };
 
@@ -99,6 +106,10 @@ int gemm_launch(const GemmArgs& args, int epi_kind, hipStream_t stream, void* ws
 
 // Workspace that lets gemm_launch split a dense problem of this shape along k.
 size_t gemm_splitk_bytes(int M, int N, int K);
+
+// Workspace that lets gemm_launch cut the groups of a GROUP_K problem (K = total rows of all
+// groups) into chunks, so one large group is reduced by many workgroups (deterministic).
+size_t gemm_groupk_bytes(int M, int N, int K, int G);
 
 // Every GROUP_M configuration uses this tile height.
 constexpr int kGroupTileM = 128;

@@ -140,6 +140,8 @@ __global__ void __launch_bounds__(1024) pack_scan_kernel(int32_t* __restrict__ h
   (void)P;
 }
 
+// One thread per pair: its slot is the block's base for its cluster plus the number of earlier
+// pairs of the block with the same cluster (stable: ascending pair order inside a cluster).
 __global__ void __launch_bounds__(256) pack_scatter_kernel(const int32_t* __restrict__ cl, int P, int C,
                                                            int k, const int32_t* __restrict__ hist,
                                                            int nblk, const float* __restrict__ w,
@@ -147,27 +149,32 @@ __global__ void __launch_bounds__(256) pack_scatter_kernel(const int32_t* __rest
                                                            int32_t* __restrict__ pair_of_slot,
                                                            int32_t* __restrict__ slot_of_pair,
                                                            float* __restrict__ w_of_slot) {
-  __shared__ int32_t sc[kPackChunk];
+  __shared__ __align__(16) int32_t sc[kPackChunk];
+  const int tid = threadIdx.x;
   const int p0 = blockIdx.x * kPackChunk;
   const int n = P - p0 < kPackChunk ? P - p0 : kPackChunk;
-  if (threadIdx.x < n) sc[threadIdx.x] = cl[p0 + threadIdx.x];
+  sc[tid] = tid < n ? cl[p0 + tid] : -1;
   __syncthreads();
-  if (slot_of_pair && threadIdx.x < n) {
-    const int c = sc[threadIdx.x];
-    if (c < 0 || c >= C) slot_of_pair[p0 + threadIdx.x] = -1;
+  if (tid >= n) return;
+  const int c = sc[tid];
+  const int p = p0 + tid;
+  if (c < 0 || c >= C) {
+    if (slot_of_pair) slot_of_pair[p] = -1;
+    return;
   }
-  for (int c = threadIdx.x; c < C; c += blockDim.x) {
-    int32_t slot = hist[(int64_t)c * nblk + blockIdx.x];
-    for (int i = 0; i < n; ++i) {
-      if (sc[i] != c) continue;
-      const int p = p0 + i;
-      if (tok_of_slot) tok_of_slot[slot] = p / k;
-      if (pair_of_slot) pair_of_slot[slot] = p;
-      if (slot_of_pair) slot_of_pair[p] = slot;
-      if (w_of_slot) w_of_slot[slot] = w ? w[p] : 1.0f;
-      ++slot;
-    }
+  int rank = 0;
+  const int4* s4 = reinterpret_cast<const int4*>(sc);
+  const int full = tid >> 2;
+  for (int j = 0; j < full; ++j) {
+    const int4 v = s4[j];
+    rank += (v.x == c) + (v.y == c) + (v.z == c) + (v.w == c);
   }
+  for (int j = full * 4; j < tid; ++j) rank += sc[j] == c;
+  const int slot = hist[(int64_t)c * nblk + blockIdx.x] + rank;
+  if (tok_of_slot) tok_of_slot[slot] = p / k;
+  if (pair_of_slot) pair_of_slot[slot] = p;
+  if (slot_of_pair) slot_of_pair[p] = slot;
+  if (w_of_slot) w_of_slot[slot] = w ? w[p] : 1.0f;
 }
 
 template <typename OutT>

@@ -42,8 +42,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "rte_grouped_swiglu_bwd": (
         _I,
-        [_P, _P, _I, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P],
+        [_P, _P, _I, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
     ),
+    "rte_grouped_swiglu_bwd_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "rte_dense_swiglu_fwd": (_I, [_P, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P, _I, _P]),
     "rte_dense_swiglu_bwd": (_I, [_P, _P, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "rte_qkv_rope_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P]),
@@ -62,6 +63,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_ce_fwd": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P]),
     "rte_ce_bwd": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P]),
     "rte_cast_f32_bf16": (_I, [_P, _I64, _P, _P]),
+    "rte_grouped_linear_fwd": (_I, [_P, _I, _I, _P, _I, _I, _P, _P, _P, _I, _P, _I, _P]),
+    "rte_grouped_linear_bwd": (_I, [_P, _P, _I, _I, _P, _I, _I, _P, _P, _P, _I, _P, _I, _P, _P, _SZ, _P]),
+    "rte_grouped_linear_bwd_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "rte_segment_reduce_workspace_bytes": (_SZ, [_I64, _I, _I]),
     "rte_segment_reduce_rows": (_I, [_P, _I64, _I, _I, _P, _P, _I, _I, _P, _I, _P, _SZ, _P]),
     "rte_shortlist_build": (_I, [_P, _P, _I, _P, _I, _I, _P, _I, _I, _I, _I, _I, _P, _P, _P]),

@@ -27,6 +27,16 @@ class AuditResult:
     metrics: dict[str, torch.Tensor]
 
 
+@dataclass(slots=True)
+class AuditLaunch:
+    """Work started right after routing on side streams: the exact replay of the audited rows
+    and the macro consistency loss.  correction() joins the streams before using them."""
+    chosen: torch.Tensor | None
+    exact: ModelOutput | None
+    cons: torch.Tensor | None
+    streams: list
+
+
 class AuditEngine:
     def __init__(self, config: TrainingConfig):
         self.config = config
@@ -77,6 +87,46 @@ class AuditEngine:
              + self.config.audit_gamma * self._coverage_deficit(meta.recipe_ids, r.recipe_logits.shape[-1]))
         return p.clamp(self.config.audit_p_min, self.config.audit_p_max)
 
+    def _side_stream(self, device, slot: int):
+        streams = self.__dict__.setdefault("_streams", {})
+        key = (device.index if device.index is not None else torch.cuda.current_device(), slot)
+        if key not in streams:
+            streams[key] = torch.cuda.Stream(device=device)  # default priority
+        return streams[key]
+
+    def begin(self, model: RecursiveModel, tokens, targets, h0, route, *, seed: int,
+              chosen: torch.Tensor | None = None) -> AuditLaunch | None:
+        """Start the fixed-count audit's exact replay and the macro consistency loss on their own
+        streams as soon as h0 and the routing decisions exist, so they (and their backward) run
+        beside the hot path.  Returns None when nothing can start early (Bernoulli sampler, no
+        device)."""
+        fixed = self.config.audit_fixed_count_per_batch
+        if fixed is None or h0.device.type != "cuda":
+            return None
+        n = h0.shape[0]
+        k = min(int(fixed), n)
+        main = torch.cuda.current_stream(h0.device)
+        launch = AuditLaunch(None, None, None, [])
+        if k > 0:
+            if chosen is None:
+                chosen = self.fixed_count_index(n, k, seed, h0.device)
+            side = self._side_stream(h0.device, 0)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                grad_corr = self.config.audit_mode == "gradient_corrected"
+                with (nullcontext() if grad_corr else torch.no_grad()):
+                    launch.exact = model.forward_exact_subset(tokens, targets, chosen, reuse_router_decisions=route,
+                                                              cached_h0=h0)
+            launch.chosen = chosen
+            launch.streams.append(side)
+        if self.config.lambda_cons != 0.0:
+            side = self._side_stream(h0.device, 1)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                launch.cons = model.macro.consistency_loss(h0, h0, route.recipe_id)
+            launch.streams.append(side)
+        return launch
+
     @staticmethod
     def fixed_count_index(n: int, k: int, seed: int, device) -> torch.Tensor:
         """The fixed-count sampler's audited rows: the first k of a seeded permutation of n
@@ -126,10 +176,19 @@ class AuditEngine:
         return mask, incl, None, None
 
     def correction(self, model: RecursiveModel, tokens, targets, hot: ModelOutput, *, seed: int,
-                   chosen: torch.Tensor | None = None) -> AuditResult:
-        """rte/audit.py:245-387.  `chosen`: fixed-count audit rows drawn ahead (captured steps)."""
+                   chosen: torch.Tensor | None = None, launch: AuditLaunch | None = None) -> AuditResult:
+        """rte/audit.py:245-387.  `chosen`: fixed-count audit rows drawn ahead (captured steps);
+        `launch`: the replay / consistency work begin() already started on side streams."""
         if hot.loss_per_sample is None:
             raise ValueError("hot output must include per-sample losses")
+        if launch is not None:
+            main = torch.cuda.current_stream(hot.loss_per_sample.device)
+            for st in launch.streams:
+                main.wait_stream(st)
+            if launch.chosen is not None:
+                chosen = launch.chosen
+            for t in _tensors_of(launch.exact) + ([launch.cons] if launch.cons is not None else []):
+                t.record_stream(main)
         if self.config.audit_fixed_count_per_batch is None:
             self.flush_pending()  # the Bernoulli sampler's probability depends on the last residual
         req = self.compute_audit_prob(hot.meta)
@@ -145,14 +204,20 @@ class AuditEngine:
             "audit_count": mask.float().sum(),
             "audit_inclusion_prob": p.mean(),
         }
-        idx = chosen if chosen is not None else mask.nonzero(as_tuple=False).flatten()
-        has_audit = (count > 0) if count is not None else idx.numel() > 0
+        if count is not None:  # fixed-count sampler: rows and count known without reading the mask
+            idx, has_audit = chosen, count > 0
+        else:
+            idx = mask.nonzero(as_tuple=False).flatten()
+            has_audit = idx.numel() > 0
         exact = None
         if has_audit:
             grad_corr = self.config.audit_mode == "gradient_corrected"
-            with (nullcontext() if grad_corr else torch.no_grad()):
-                exact = model.forward_exact_subset(tokens, targets, idx, reuse_router_decisions=hot.meta.router,
-                                                   cached_h0=hot.meta.h0)
+            if launch is not None and launch.exact is not None:
+                exact = launch.exact
+            else:
+                with (nullcontext() if grad_corr else torch.no_grad()):
+                    exact = model.forward_exact_subset(tokens, targets, idx, reuse_router_decisions=hot.meta.router,
+                                                       cached_h0=hot.meta.h0)
             hot_sub = hot.loss_per_sample.index_select(0, idx)
             residual = exact.loss_per_sample - hot_sub
             metrics["audit_residual_mean"] = residual.mean()
@@ -187,7 +252,9 @@ class AuditEngine:
             self._pending_residual = (1.0 - align["hidden_cosine_exact_macro"]).detach().clamp_min(0)
         if hot.meta.recipe_ids is not None:
             self._update_coverage(hot.meta.recipe_ids, mask)
-        if self.config.lambda_cons != 0.0 and hot.meta.h0 is not None and hot.meta.recipe_ids is not None:
+        if launch is not None and launch.cons is not None:
+            aux["cons"] = self.config.lambda_cons * launch.cons
+        elif self.config.lambda_cons != 0.0 and hot.meta.h0 is not None and hot.meta.recipe_ids is not None:
             aux["cons"] = self.config.lambda_cons * model.macro.consistency_loss(hot.meta.h0, hot.meta.h0,
                                                                                  hot.meta.recipe_ids)
         return AuditResult(mask, p, exact, corrected, aux, metrics)
@@ -198,3 +265,11 @@ class AuditEngine:
         if pend is not None:
             self.recent_residual = float(pend.item())
             self._pending_residual = None
+
+
+def _tensors_of(out: ModelOutput | None) -> list[torch.Tensor]:
+    """Tensors of a replay's output that the main stream reads."""
+    if out is None:
+        return []
+    ts = [out.loss_per_sample, out.meta.recurrent_hidden, out.meta.logits, out.meta.hidden]
+    return [t for t in ts if isinstance(t, torch.Tensor)]

@@ -27,22 +27,22 @@ def _s() -> int:
     return _lib.stream_ptr()
 
 
-_WS: dict[int, torch.Tensor] = {}
+_WS: dict[tuple[int, int], torch.Tensor] = {}
 
 
 def workspace(nbytes: int, device: torch.device) -> tuple[int, int]:
-    """(pointer, bytes) of a cached per-device scratch buffer of at least nbytes.
+    """(pointer, bytes) of a cached scratch buffer of at least nbytes, one per (device, stream).
 
-    Every operator here runs on the current stream, so launches that share the
-    buffer are ordered; callers that launch on several streams at once must not
-    share it."""
+    Launches on one stream are ordered, so they may share that stream's buffer; work issued
+    on another stream gets its own."""
     if nbytes <= 0:
         return 0, 0
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    buf = _WS.get(idx)
+    key = (idx, torch.cuda.current_stream(idx).cuda_stream)
+    buf = _WS.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(((nbytes + 255) // 256) * 256, dtype=torch.uint8, device=device)
-        _WS[idx] = buf
+        _WS[key] = buf
     return buf.data_ptr(), buf.numel()
 
 
@@ -401,9 +401,10 @@ def _pool_bwd(db, xb, wugb, wdb, pk, ug, zw, C: int, n: int, k: int):
     dxp = torch.empty((P, d), dtype=BF16, device=dev)
     dwug = torch.empty((2 * F, d), dtype=F32, device=dev)
     dwd = torch.empty((d, F), dtype=F32, device=dev)
+    ws, nb = workspace(_lib.load().rte_grouped_swiglu_bwd_workspace_bytes(P, C, n, d), dev)
     call("rte_grouped_swiglu_bwd", ptr(db), ptr(xb), T, d, ptr(pk.offsets), C, n, P, ptr(pk.tok_of_slot),
          ptr(pk.pair_of_slot), ptr(pk.w_of_slot), ptr(wugb), ptr(wdb), F, ptr(ug), ptr(zw), ptr(dug), ptr(dw_slot),
-         ptr(dxp), ptr(dwug), ptr(dwd), _s())
+         ptr(dxp), ptr(dwug), ptr(dwd), ws, nb, _s())
     return dxp, dwug, dwd, dw_slot
 
 
@@ -580,6 +581,60 @@ class LMHeadCEFn(torch.autograd.Function):
 def lm_head_ce(hidden, w, targets):
     """(logits fp32, per-token cross-entropy) of hidden @ W^T against targets."""
     return LMHeadCEFn.apply(hidden, w, targets)
+
+
+# ----------------------------------------------------------------------------- grouped linear
+
+def group_rows(keys: torch.Tensor, n_groups: int) -> PackIndex:
+    """Slot order of rows keyed to groups (ascending row inside a group; keys < 0 dropped)."""
+    return pack_index(keys.reshape(-1, 1), n_groups)
+
+
+class GroupedLinearFn(torch.autograd.Function):
+    """y[t] = x[t] @ W[key(t)] with W [G, K, Nout] (one matrix per group), rows grouped by the
+    pack of their keys: grouped MFMA GEMMs forward and backward, and the per-group weight
+    gradient is the deterministic grouped-K reduction (no per-row weight copies)."""
+
+    @staticmethod
+    def forward(ctx, x, w, pk: PackIndex, out_f32: bool = True):
+        _lib.require_device_tensors("grouped_linear", x, w)
+        shape = x.shape
+        K = shape[-1]
+        G, K2, Nout = w.shape
+        if K2 != K:
+            raise ValueError(f"grouped_linear: x has {K} columns, W groups are [{K2}, {Nout}]")
+        xb = x.reshape(-1, K).contiguous().to(BF16)
+        N = xb.shape[0]
+        wb = cast_bf16(w)
+        y = torch.empty((N, Nout), dtype=F32 if out_f32 else BF16, device=x.device)
+        P = pk.tok_of_slot.numel()
+        call("rte_grouped_linear_fwd", ptr(xb), N, K, ptr(pk.offsets), G, P, ptr(pk.tok_of_slot),
+             ptr(pk.pair_of_slot), ptr(wb), Nout, ptr(y), int(out_f32), _s())
+        ctx.save_for_backward(xb, wb, pk.offsets, pk.tok_of_slot, pk.pair_of_slot)
+        ctx.meta = (shape, x.dtype, w.dtype)
+        return y.view(*shape[:-1], Nout)
+
+    @staticmethod
+    def backward(ctx, dy):
+        xb, wb, offsets, tok, pos = ctx.saved_tensors
+        shape, x_dt, w_dt = ctx.meta
+        G, K, Nout = wb.shape
+        N = xb.shape[0]
+        dyb = cast_bf16(dy.reshape(N, Nout))
+        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        dx_f32 = x_dt != BF16
+        dx = torch.empty((N, K), dtype=F32 if dx_f32 else BF16, device=xb.device) if need_x else None
+        dw = torch.empty((G, K, Nout), dtype=F32, device=xb.device) if need_w else None
+        P = tok.numel()
+        ws, nb = workspace(_lib.load().rte_grouped_linear_bwd_workspace_bytes(P, G, K, Nout), xb.device)
+        call("rte_grouped_linear_bwd", ptr(dyb), ptr(xb), N, K, ptr(offsets), G, P, ptr(tok), ptr(pos),
+             ptr(wb), Nout, ptr(dx), int(dx_f32), ptr(dw), ws, nb, _s())
+        return (None if dx is None else dx.view(shape).to(x_dt), None if dw is None else dw.to(w_dt), None, None)
+
+
+def grouped_linear(x, w, pk: PackIndex, *, out_f32: bool = True):
+    """Rows of x keyed by pk's groups times their group's matrix; every key must be valid."""
+    return GroupedLinearFn.apply(x, w, pk, out_f32)
 
 
 # ----------------------------------------------------------------------------- segmented row reduction

@@ -3,7 +3,8 @@
 alignment metrics the audit uses (rte/macro.py:394-546).
 
 Parameter shapes and initialisation order follow the reference so state dicts load.
-Compute is torch on the device (a few small batched matmuls per step).
+The bounded operator's (recipe, stride)-indexed matrices run as grouped MFMA GEMMs over
+the rows of all samples sharing a key; the elementwise parts are torch on the device.
 """
 
 from __future__ import annotations
@@ -16,6 +17,7 @@ from torch import nn
 
 from rte_amd.config import ModelConfig
 from rte_amd.gather import gather_rk, gather_rows
+from rte_amd.kernels import hip_ops
 
 
 def _rms(x, *, dim=-1, keepdim=False):
@@ -122,31 +124,44 @@ class MacroOperators(nn.Module):
             return self._apply_v2(h, h0, recipe_ids, stride_ids)
         return self._apply_bounded(h, h0, recipe_ids, stride_ids)
 
+    def _rows(self, table: torch.Tensor, key: torch.Tensor) -> torch.Tensor:
+        """Per-sample rows of a [recipes, strides, d] table (deterministic backward)."""
+        flat = table.reshape(-1, table.shape[-1])
+        if isinstance(table, nn.Parameter) or table.requires_grad:
+            return hip_ops.embedding(flat, key)
+        return flat.index_select(0, key)
+
     def _apply_bounded(self, h, h0, recipe_ids, stride_ids):
-        """rte/macro.py:201-236."""
-        gain = gather_rk(self.d_gain, recipe_ids, stride_ids)
-        v = gather_rk(self.v, recipe_ids, stride_ids)
-        u = gather_rk(self.u, recipe_ids, stride_ids)
-        bias = gather_rk(self.bias, recipe_ids, stride_ids)
-        scale = gather_rk(self.update_scale, recipe_ids, stride_ids)
+        """rte/macro.py:201-236.  The (recipe, stride)-indexed low-rank matrices are applied as
+        grouped GEMMs over the rows of every sample sharing a key: no per-sample copies of
+        v / u are gathered, and their gradients are per-group reductions in a fixed order."""
+        B, S, d = h.shape
+        R, Kk = self.v.shape[0], self.v.shape[1]
+        key = recipe_ids.long() * Kk + stride_ids.long()
+        pk = hip_ops.group_rows(key[:, None].expand(B, S), R * Kk)
+        gain = self._rows(self.d_gain, key)
+        bias = self._rows(self.bias, key)
+        scale = self._rows(self.update_scale, key)
         normed = _rmsnorm(h)
         parts = [normed, normed.mean(dim=1, keepdim=True).expand_as(normed), h0]
         if self.config.macro_include_delta_to_h0:
             parts.append(normed - _rmsnorm(h0))
         if self.depth_embed is not None:
             parts.append(gather_rows(self.depth_embed, stride_ids).unsqueeze(1).expand_as(normed))
-        z = torch.cat(parts, dim=-1)
-        low = F.silu(torch.bmm(z, v))
+        # z is a GEMM operand only: build it in bf16 (the precision autocast gives the bmm)
+        z = torch.cat([t.to(torch.bfloat16) for t in parts], dim=-1).reshape(B * S, -1)
+
+        def lin(x, w, out_f32=False):
+            return hip_ops.grouped_linear(x, w.reshape(R * Kk, w.shape[-2], w.shape[-1]), pk, out_f32=out_f32)
+
+        low = F.silu(lin(z, self.v))
         if self.v2 is not None:
-            low = F.silu(torch.bmm(low, gather_rk(self.v2, recipe_ids, stride_ids)))
-        low = torch.bmm(low, u)
+            low = F.silu(lin(low, self.v2))
+        low = lin(low, self.u, out_f32=True).view(B, S, d)
         update = gain.unsqueeze(1) * h + low + bias.unsqueeze(1)
         if self.gate_v is not None:
-            gate = torch.sigmoid(
-                torch.bmm(F.silu(torch.bmm(z, gather_rk(self.gate_v, recipe_ids, stride_ids))),
-                          gather_rk(self.gate_u, recipe_ids, stride_ids))
-                + gather_rk(self.gate_bias, recipe_ids, stride_ids).unsqueeze(1)
-            )
+            gate = torch.sigmoid(lin(F.silu(lin(z, self.gate_v)), self.gate_u, out_f32=True).view(B, S, d)
+                                 + self._rows(self.gate_bias, key).unsqueeze(1))
         else:
             gate = 1.0
         return h + self.config.macro_update_scale * scale.unsqueeze(1) * gate * torch.tanh(update)

@@ -162,9 +162,13 @@ class RecursiveModel(nn.Module):
 
     def forward_macro(self, tokens, targets=None, return_states=False, return_loss_per_sample=False, *,
                       shortlist=False, seed=0, fixed_recipe=None, fixed_depth=None,
-                      shortlist_random_negs=None) -> ModelOutput:
+                      shortlist_random_negs=None, on_routed=None) -> ModelOutput:
+        """rte/models.py:681-723.  on_routed(h0, route), if given, runs right after routing: the
+        training step uses it to start the audit replay on its own stream while the hot path runs."""
         h0 = self._prelude(tokens)
         route = self.router(h0, fixed_recipe=fixed_recipe, fixed_depth=fixed_depth)
+        if on_routed is not None:
+            on_routed(h0, route)
         h, trace = self.macro(h0, h0, route.recipe_id, route.depth, return_states=return_states)
         sl = None
         if shortlist and targets is not None:

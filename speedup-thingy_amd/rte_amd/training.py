@@ -87,6 +87,8 @@ class TrainEngine:
         self.global_micro_step = 0
         self.tokens_seen = 0
         self.last_grad_metrics: dict[str, Any] = {}
+        # start the audit replay and the consistency loss on side streams right after routing
+        self.audit_streams = self.device.type == "cuda"
         self._graph_enabled = False
         self._graph_keep = False
         self._gstate: dict[str, Any] | None = None
@@ -218,12 +220,20 @@ class TrainEngine:
         correction, router aux; loss = corrected CE / S + macro aux + router aux."""
         tr = self.config.training
         m = self.recursive_model
+        launched = []
+        audit_seed = tr.seed + 10_000 + self.global_step
+
+        def on_routed(h0, route):
+            # the audit replay and the consistency loss need only h0 and the routing decisions
+            launched.append(self.audit_engine.begin(m, tokens, targets, h0, route, seed=audit_seed, chosen=chosen))
+
         with self._autocast():
             hot = m.forward_macro(tokens, targets, return_states=True, return_loss_per_sample=True,
                                   shortlist=shortlist, seed=tr.seed + self.global_step, fixed_recipe=tr.fixed_recipe,
-                                  fixed_depth=tr.fixed_depth, shortlist_random_negs=random_negs)
-            audit = self.audit_engine.correction(m, tokens, targets, hot, seed=tr.seed + 10_000 + self.global_step,
-                                                 chosen=chosen)
+                                  fixed_depth=tr.fixed_depth, shortlist_random_negs=random_negs,
+                                  on_routed=on_routed if self.audit_streams else None)
+            audit = self.audit_engine.correction(m, tokens, targets, hot, seed=audit_seed, chosen=chosen,
+                                                 launch=launched[0] if launched else None)
             aux = self._router_aux(hot)
             scale = self._loss_scale(targets)
             loss = audit.corrected_loss_per_sample.mean() / scale + sum(audit.macro_aux.values()) + sum(aux.values())

@@ -518,3 +518,39 @@ def test_embedding_backward_deterministic():
     out.backward(g)
     want = torch.zeros(300, 64, dtype=torch.float64).index_add_(0, ids.reshape(-1).cpu(), g.reshape(-1, 64).double().cpu())
     assert_rel(W.grad.double().cpu().numpy(), want.numpy(), FP32_RTOL, "embedding dW")
+
+
+# ---------------------------------------------------------------- grouped linear
+
+@pytest.mark.parametrize("N,K,Nout,G,skew", [(500, 96, 40, 7, False), (16384, 1536, 32, 48, False),
+                                              (4096, 32, 512, 48, False), (16384, 1536, 32, 48, True),
+                                              (8192, 32, 512, 48, True)])
+def test_grouped_linear_fwd_bwd(N, K, Nout, G, skew):
+    """Balanced and skewed groups (one group holding 90% of the rows: its weight-gradient
+    reduction is cut into chunks that are added in a fixed order)."""
+    from oracle import macro as MO
+
+    H = _ops()
+    rng = np.random.default_rng(N + K + skew)
+    x = bf16_round(rng.standard_normal((N, K)).astype(np.float32))
+    w = bf16_round((rng.standard_normal((G, K, Nout)) / np.sqrt(K)).astype(np.float32))
+    keys = rng.integers(0, G, N)
+    if skew:
+        keys[rng.random(N) < 0.9] = 5
+    keys[keys == 3] = 4                                   # group 3 empty
+    dy = bf16_round(rng.standard_normal((N, Nout)).astype(np.float32))
+    tx = _bf(x).float().requires_grad_()
+    tw = torch.from_numpy(w).to(DEV).requires_grad_()
+    pk = H.group_rows(torch.from_numpy(keys).to(DEV), G)
+    print(f"grouped_linear N={N} K={K} Nout={Nout} G={G} skew={skew}", flush=True)
+    y = H.grouped_linear(tx, tw, pk)
+    y.backward(torch.from_numpy(dy).to(DEV))
+    assert_rel(_np(y), MO.grouped_linear(x, w, keys), FP32_RTOL, "grouped linear y")
+    rdx, rdw = MO.grouped_linear_bwd(dy, x, w, keys)
+    assert_rel(_np(tx.grad), rdx, FP32_RTOL, "grouped linear dx")
+    assert_rel(_np(tw.grad), rdw, FP32_RTOL, "grouped linear dW")
+    assert not tw.grad[3].any(), "empty group must get a zero gradient"
+    first = tw.grad.clone()
+    tw.grad = None
+    H.grouped_linear(tx, tw, pk).backward(torch.from_numpy(dy).to(DEV))
+    assert torch.equal(first, tw.grad), "weight gradient not bitwise repeatable"

@@ -397,3 +397,60 @@ def test_captured_step_matches_eager(mode):
     print("graph nodes", kinds, flush=True)
     assert kinds.get("memset", 0) == 0, kinds
     assert kinds.get("kernel", 0) > 100
+
+
+# ---------------------------------------------------------------- macro operators
+
+def _torch_bounded(h, h0, rid, sid, p, c):
+    """fp64 CPU torch restatement of the bounded macro operator (rte/macro.py:201-236) with the
+    reference's per-sample weight gather and bmm."""
+    def rms(x):
+        return x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-5)
+
+    g = lambda t: t[rid, sid]  # noqa: E731
+    n = rms(h)
+    z = torch.cat([n, n.mean(dim=1, keepdim=True).expand_as(n), h0], -1)
+    low = torch.bmm(torch.nn.functional.silu(torch.bmm(z, g(p["v"]))), g(p["u"]))
+    upd = g(p["d_gain"]).unsqueeze(1) * h + low + g(p["bias"]).unsqueeze(1)
+    return h + c * g(p["update_scale"]).unsqueeze(1) * torch.tanh(upd)
+
+
+def test_macro_operator_grouped_matches_reference():
+    """MacroOperators (bounded) on the grouped GEMMs: forward against the numpy oracle, gradients
+    of every parameter and of h, h0 against fp64 autograd of the reference formula."""
+    from oracle import macro as MO
+    from helpers import rel_err
+    from rte_amd.macro import MacroOperators
+
+    cfg = _model_cfg(d_model=128, macro_rank=32, recipe_count=6, depth_choices=[1, 2, 4], t_max=4)
+    torch.manual_seed(4)
+    mac = MacroOperators(cfg).cuda()
+    with torch.no_grad():
+        mac.d_gain.normal_(0, 0.1)
+        mac.bias.normal_(0, 0.1)
+        mac.u.normal_(0, 0.05)
+    B, S, d = 10, 16, cfg.d_model
+    gen = np.random.default_rng(4)
+    hn, h0n = gen.standard_normal((B, S, d)), gen.standard_normal((B, S, d))
+    rid = torch.tensor(gen.integers(0, 6, B), device="cuda")
+    depths = torch.tensor(gen.choice([1, 2, 4], B), device="cuda")
+    h = torch.tensor(hn, dtype=torch.float32, device="cuda", requires_grad=True)
+    h0 = torch.tensor(h0n, dtype=torch.float32, device="cuda", requires_grad=True)
+    G = gen.standard_normal((B, S, d))
+    print("macro grouped B=10 S=16 d=128", flush=True)
+    out, _ = mac(h, h0, rid, depths)
+    (out * torch.tensor(G, dtype=torch.float32, device="cuda")).sum().backward()
+    sid = mac.stride_ids_for_depths(depths)
+    p = {k: getattr(mac, k).detach().double().cpu() for k in ("d_gain", "bias", "update_scale", "v", "u")}
+    want = MO.bounded_apply(hn, h0n, rid.cpu().numpy(), sid.cpu().numpy(), {k: v.numpy() for k, v in p.items()},
+                            cfg.macro_update_scale)
+    assert_rel(out.detach().double().cpu().numpy() - hn, want - hn, BF16_RTOL, "macro delta")
+    tp = {k: v.clone().requires_grad_(k != "update_scale") for k, v in p.items()}
+    th, th0 = torch.tensor(hn, requires_grad=True), torch.tensor(h0n, requires_grad=True)
+    ref = _torch_bounded(th, th0, rid.cpu(), sid.cpu(), tp, cfg.macro_update_scale)
+    assert rel_err(ref.detach().numpy(), want) < 1e-12
+    (ref * torch.tensor(G)).sum().backward()
+    for k in ("d_gain", "bias", "v", "u"):
+        assert_rel(getattr(mac, k).grad.double().cpu().numpy(), tp[k].grad.numpy(), BF16_RTOL, f"macro d{k}")
+    assert_rel(h.grad.double().cpu().numpy(), th.grad.numpy(), BF16_RTOL, "macro dh")
+    assert_rel(h0.grad.double().cpu().numpy(), th0.grad.numpy(), BF16_RTOL, "macro dh0")

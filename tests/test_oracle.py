@@ -594,3 +594,61 @@ def test_segment_reduce_matches_index_add_and_loop():
     t = torch.zeros(V, d, dtype=torch.float64).index_add_(
         0, torch.tensor(keys[ok]), torch.tensor(w[ok, None] * rows[np.arange(P)[ok] // div]))
     np.testing.assert_allclose(got, t.numpy(), rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------- macro operators
+
+def _macro_case(seed, B=6, S=5, d=8, m=3, R=4, K=3):
+    rng = _rng(seed)
+    p = dict(d_gain=rng.standard_normal((R, K, d)) * 0.1, bias=rng.standard_normal((R, K, d)) * 0.1,
+             update_scale=rng.uniform(0.5, 1.5, (R, K, d)), v=rng.standard_normal((R, K, 3 * d, m)) / 5,
+             u=rng.standard_normal((R, K, m, d)) / 3)
+    h = rng.standard_normal((B, S, d))
+    h0 = rng.standard_normal((B, S, d))
+    return p, h, h0, rng.integers(0, R, B), rng.integers(0, K, B)
+
+
+def test_macro_grouped_linear_matches_loop_and_backward():
+    from oracle import macro as MO
+
+    rng = _rng(70)
+    x, w, keys = rng.standard_normal((30, 7)), rng.standard_normal((5, 7, 4)), rng.integers(0, 5, 30)
+    y = MO.grouped_linear(x, w, keys)
+    for t in range(30):
+        np.testing.assert_allclose(y[t], x[t] @ w[keys[t]], rtol=1e-12)
+    dy = rng.standard_normal((30, 4))
+    dx, dw = MO.grouped_linear_bwd(dy, x, w, keys)
+    tx, tw = torch.tensor(x, requires_grad=True), torch.tensor(w, requires_grad=True)
+    (torch.bmm(tx.unsqueeze(1), tw[torch.tensor(keys)]).squeeze(1) * torch.tensor(dy)).sum().backward()
+    np.testing.assert_allclose(dx, tx.grad.numpy(), rtol=1e-12)
+    np.testing.assert_allclose(dw, tw.grad.numpy(), rtol=1e-12, atol=1e-14)
+
+
+def test_macro_closed_form_without_low_rank_path():
+    """u = 0 and gain = 0 leave Phi(h) = h + c * scale * tanh(bias)."""
+    from oracle import macro as MO
+
+    p, h, h0, r, k = _macro_case(71)
+    p["u"][:] = 0.0
+    p["d_gain"][:] = 0.0
+    out = MO.bounded_apply(h, h0, r, k, p, 0.05)
+    want = h + 0.05 * p["update_scale"][r, k][:, None, :] * np.tanh(p["bias"][r, k])[:, None, :]
+    np.testing.assert_allclose(out, want, rtol=1e-12)
+
+
+def test_macro_bounded_and_per_key():
+    """|Phi(h) - h| <= c * |scale| (tanh bound); a sample's output depends only on its own
+    (recipe, stride) parameters and on its own rows (equivariant under sample permutation)."""
+    from oracle import macro as MO
+
+    p, h, h0, r, k = _macro_case(72)
+    out = MO.bounded_apply(h, h0, r, k, p, 0.05)
+    assert (np.abs(out - h) <= 0.05 * p["update_scale"][r, k][:, None, :] + 1e-12).all()
+    other = {kk: v.copy() for kk, v in p.items()}
+    unused = [(a, b) for a in range(4) for b in range(3) if not ((r == a) & (k == b)).any()]
+    for a, b in unused:
+        for kk in other:
+            other[kk][a, b] = 7.0
+    np.testing.assert_allclose(MO.bounded_apply(h, h0, r, k, other, 0.05), out, rtol=1e-12)
+    perm = _rng(73).permutation(h.shape[0])
+    np.testing.assert_allclose(MO.bounded_apply(h[perm], h0[perm], r[perm], k[perm], p, 0.05), out[perm], rtol=1e-12)
