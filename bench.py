@@ -56,23 +56,10 @@ def zipf_batch(gen, vocab: int, batch: int, seq: int, device):
     return ids[:, :-1].contiguous(), ids[:, 1:].contiguous()
 
 
-def time_launches(fn, iters: int = 20) -> float:
-    """Average duration (s) of fn() on the current stream, bracketed by HIP events."""
-    import torch
-
-    fn()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(iters):
-        fn()
-    end.record()
-    end.synchronize()
-    return start.elapsed_time(end) / 1e3 / iters
-
-
 def kernel_candidates(B: int, S: int):
-    """Each hot kernel of the step at its cfg3 shape: (name, launches/step, flop, fn)."""
+    """Hot kernels of the step at their cfg3 shapes.  Each entry: name, launches per step,
+    kernels per call, algorithmic flop and HBM bytes per call (inputs read once, outputs
+    written once), and fn launching it on the current stream."""
     import torch
 
     from rte_amd import _lib
@@ -101,16 +88,16 @@ def kernel_candidates(B: int, S: int):
     ug = torch.empty(P, 2 * n, device=dev, dtype=bf)
     zw = torch.empty(P, n, device=dev, dtype=bf)
     yp = torch.empty(P, d, device=dev, dtype=bf)
-    s = _lib.stream_ptr()
     head_out = torch.empty(T, V, device=dev, dtype=torch.float32)
+    st = _lib.stream_ptr
 
     def head():
         _lib.call("rte_gemm_bf16", x.data_ptr(), d, 0, None, w_head.data_ptr(), d, 0, None, head_out.data_ptr(), V,
-                  1, T, V, d, 1.0, 0.0, None, 0, None, 0, s)
+                  1, T, V, d, 1.0, 0.0, None, 0, None, 0, st())
 
     def qkv():
         _lib.call("rte_qkv_rope_fwd", x.data_ptr(), wqkv.data_ptr(), cos.data_ptr(), sin.data_ptr(), B, S, 8, 64,
-                  q.data_ptr(), kk.data_ptr(), vv.data_ptr(), s)
+                  q.data_ptr(), kk.data_ptr(), vv.data_ptr(), st())
 
     dqkv = torch.randn(T, 3 * d, device=dev, generator=g).to(bf)
     dw_qkv = torch.empty(3 * d, d, device=dev, dtype=torch.float32)
@@ -120,20 +107,110 @@ def kernel_candidates(B: int, S: int):
     def wgrad():
         # dW_qkv[c, :] = sum_t dqkv[t, c] x[t, :]  (both operands token-major: layout T, split-K)
         _lib.call("rte_gemm_bf16", dqkv.data_ptr(), 3 * d, 1, None, x.data_ptr(), d, 1, None, dw_qkv.data_ptr(), d,
-                  1, 3 * d, d, T, 1.0, 0.0, None, 0, ws.data_ptr(), ws_bytes, s)
+                  1, 3 * d, d, T, 1.0, 0.0, None, 0, ws.data_ptr(), ws_bytes, st())
 
     def ffn_fwd():
         _lib.call("rte_grouped_swiglu_fwd", x.data_ptr(), T, d, pk.offsets.data_ptr(), C, n, P,
                   pk.tok_of_slot.data_ptr(), pk.pair_of_slot.data_ptr(), pk.w_of_slot.data_ptr(), wug.data_ptr(),
-                  wd.data_ptr(), F, ug.data_ptr(), zw.data_ptr(), yp.data_ptr(), s)
+                  wd.data_ptr(), F, ug.data_ptr(), zw.data_ptr(), yp.data_ptr(), st())
+
+    out_pool = torch.empty(T, d, device=dev, dtype=torch.float32)
+
+    def combine():
+        _lib.call("rte_combine_rows", yp.data_ptr(), T, k, d, None, None, None, out_pool.data_ptr(), 1, st())
 
     return [
-        ("gemm_lm_head_fwd", 1, 2.0 * T * V * d, head),
-        ("gemm_qkv_rope_fwd", 2, 2.0 * T * 3 * d * d, qkv),
-        # two grouped GEMM launches: x@[Wup|Wgate]^T with SwiGLU epilogue, then zw@Wdown
-        ("grouped_swiglu_fwd", 2, 2.0 * P * d * 2 * n + 2.0 * P * n * d, ffn_fwd),
-        ("gemm_wgrad_qkv", 2, 2.0 * T * 3 * d * d, wgrad),
+        dict(name="gemm_qkv_rope_fwd", per_step=2, kernels=1, flop=2.0 * T * 3 * d * d,
+             bytes=2.0 * T * d + 2.0 * 3 * d * d + 3 * 2.0 * T * d, fn=qkv),
+        dict(name="gemm_lm_head_fwd", per_step=1, kernels=1, flop=2.0 * T * V * d,
+             bytes=2.0 * T * d + 2.0 * V * d + 4.0 * T * V, fn=head),
+        # x@[Wup|Wgate]^T with the SwiGLU epilogue, then zw@Wdown into pair-major rows
+        dict(name="grouped_swiglu_fwd", per_step=2, kernels=2, flop=2.0 * P * d * 2 * n + 2.0 * P * n * d,
+             bytes=2.0 * T * d + 2.0 * 3 * F * d + 2.0 * P * 3 * n + 2.0 * P * d + 12.0 * P, fn=ffn_fwd),
+        # SURVEY combine unit: T*k*d*b + T*k*4 + T*d*b (bf16 rows in, fp32 rows out here)
+        dict(name="combine_rows", per_step=2, kernels=1, flop=1.0 * P * d,
+             bytes=2.0 * P * d + 4.0 * T * d, fn=combine),
+        dict(name="gemm_wgrad_qkv", per_step=2, kernels=2, flop=2.0 * T * 3 * d * d,
+             bytes=2.0 * T * 3 * d + 2.0 * T * d + 4.0 * 3 * d * d, fn=wgrad),
     ]
+
+
+def time_launches(fn, iters: int = 20) -> float:
+    """Average duration (s) of one fn() call: `iters` calls captured in a HIP graph and
+    replayed, timed with HIP events on the replaying stream (no host launch gaps)."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 5
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / 1e3 / (iters * reps)
+
+
+def roofline_rows(B: int, S: int) -> list[dict]:
+    rows = []
+    for c in kernel_candidates(B, S):
+        dt = time_launches(c["fn"])
+        t_mfma, t_hbm = c["flop"] / (PEAK_BF16_TFLOPS * 1e12), c["bytes"] / (PEAK_HBM_GBS * 1e9)
+        bound = "mfma" if t_mfma >= t_hbm else "hbm"
+        ach = c["flop"] / dt / 1e12 if bound == "mfma" else c["bytes"] / dt / 1e9
+        peak = PEAK_BF16_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
+        rows.append({"kernel": c["name"], "launches_per_step": c["per_step"], "kernels_per_call": c["kernels"],
+                     "avg_us": round(dt * 1e6, 2), "bound": bound, "achieved": round(ach, 1),
+                     "unit": "TFLOP/s" if bound == "mfma" else "GB/s", "peak": peak, "frac": round(ach / peak, 4),
+                     "flop": c["flop"], "bytes": c["bytes"],
+                     "tflops": round(c["flop"] / dt / 1e12, 1), "gbs": round(c["bytes"] / dt / 1e9, 1)})
+    return rows
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel), or None."""
+    path = ROOT / "profiles" / "traffic.json"
+    try:
+        data = json.loads(path.read_text())
+    except (OSError, ValueError):
+        return None
+    entry = data.get(kernel)
+    return None if entry is None else entry.get("bytes_per_launch")
+
+
+def profile_kernel(name: str, iters: int, B: int, S: int) -> int:
+    """Launch one candidate kernel `iters` times (the program rocprofv3 --pmc profiles)."""
+    import torch
+
+    if name == "copy":
+        # calibration: cast 64 Mi fp32 -> bf16 (reads 256 MiB, writes 128 MiB per launch)
+        from rte_amd import _lib
+
+        n = 64 << 20
+        src = torch.randn(n, device="cuda")
+        dst = torch.empty(n, device="cuda", dtype=torch.bfloat16)
+        for _ in range(iters):
+            _lib.call("rte_cast_f32_bf16", src.data_ptr(), n, dst.data_ptr(), _lib.stream_ptr())
+    else:
+        cands = {c["name"]: c for c in kernel_candidates(B, S)}
+        for _ in range(iters):
+            cands[name]["fn"]()
+    torch.cuda.synchronize()
+    print(json.dumps({"profiled": name, "iters": iters}))
+    return 0
 
 
 def cpu_baseline(budget_s: float = 15.0) -> dict:
@@ -187,6 +264,9 @@ def main(argv=None) -> int:
     ap.add_argument("--seq", type=int, default=64)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--profile-kernel", default=None,
+                    help="only launch this roofline candidate (or 'copy', the calibration kernel) --iters times")
+    ap.add_argument("--iters", type=int, default=50)
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from Python instead of replaying the captured step graph")
     args = ap.parse_args(argv)
@@ -202,6 +282,8 @@ def main(argv=None) -> int:
     if not _lib.device_ready():
         print(json.dumps({"error": "HIP backend unavailable (librte_hip.so not built or no gfx950 device)"}))
         return 1
+    if args.profile_kernel:
+        return profile_kernel(args.profile_kernel, args.iters, args.batch, args.seq)
     cfg = cfg3_config(args.batch, args.seq)
     dev = torch.device("cuda:0")
     engine = TrainEngine(cfg, device=dev)
@@ -248,23 +330,20 @@ def main(argv=None) -> int:
         },
     }
     if not args.no_roofline:
-        rows = []
-        for name, per_step, flop, fn in kernel_candidates(args.batch, args.seq):
-            dt = time_launches(fn)
-            rows.append({"kernel": name, "launches_per_step": per_step, "avg_us": round(dt * 1e6, 2),
-                         "tflops": round(flop / dt / 1e12, 1), "frac": round(flop / dt / 1e12 / PEAK_BF16_TFLOPS, 4),
-                         "flop": flop})
-        dom = max(rows, key=lambda r: r["avg_us"] * r["launches_per_step"])
+        rows = roofline_rows(args.batch, args.seq)
+        single = [r for r in rows if r["kernels_per_call"] == 1]
+        dom = max(single, key=lambda r: r["avg_us"] * r["launches_per_step"])
         out["roofline"] = {
             "kernel": dom["kernel"],
-            "bound": "mfma",
-            "achieved": dom["tflops"],
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
+            "bound": dom["bound"],
+            "achieved": dom["achieved"],
+            "peak": dom["peak"],
+            "unit": dom["unit"],
             "frac": dom["frac"],
-            "traffic": None,
+            "traffic": measured_traffic(dom["kernel"]),
             "avg_us": dom["avg_us"],
             "flop_per_launch": dom["flop"],
+            "algorithmic_bytes_per_launch": dom["bytes"],
         }
         out["kernels"] = rows
     if not args.no_cpu_baseline:
