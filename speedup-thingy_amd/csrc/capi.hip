@@ -445,7 +445,9 @@ int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, c
 int rte_qkv_rope_fwd(const void* x, const void* wqkv, const float* cos_t, const float* sin_t, int B, int S_,
                      int H, int hd, void* q, void* k, void* v, void* stream) {
   const int d = H * hd;
-  RTE_REQUIRE(d % 8 == 0 && hd % 2 == 0, "qkv_rope: bad head layout");
+  RTE_REQUIRE(d % 8 == 0 && hd % 8 == 0, "qkv_rope: head_dim must be a multiple of 8");
+  RTE_REQUIRE(((uintptr_t)cos_t & 15) == 0 && ((uintptr_t)sin_t & 15) == 0,
+              "qkv_rope: cos / sin tables must be 16-byte aligned");
   GemmArgs p;
   p.M = B * S_;
   p.N = 3 * d;

@@ -563,51 +563,52 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
       }
     }
   } else if constexpr (EPI == EPI_ROPE_QKV) {
-    constexpr int HP = BN + 8;
-    bf16* Hs = smem;
-    // per-column head position (hoisted), per-row sequence position
-    int dim_j[TN];
-    bool rot_j[TN];
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = n0 + cbase + j * 32;
-      dim_j[j] = n % e.hd;
-      rot_j[j] = n < 2 * e.dmodel;
-    }
+    // Stage the fp32 tile, then each thread rotates and writes 8 consecutive columns of one
+    // row: the RoPE pairs (2i, 2i+1) sit inside the chunk, and the chunk's cos / sin values
+    // are two 16-byte loads each.
+    constexpr int CP = BN + 4;
+    float* Cs = reinterpret_cast<float*>(smem_raw);
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int rl = rbase + i * 32 + (r >> 2) * 8 + (r & 3);
-        const int m = m0 + rl;
-        const int s = m < mlim ? m % e.S : 0;
-        const float* cs = e.cos_t + (int64_t)s * e.hd;
-        const float* sn = e.sin_t + (int64_t)s * e.hd;
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const float x = acc[i][j][r];
-          const float partner = __shfl_xor(x, 1, 64);
-          float y = x;
-          if (rot_j[j]) {
-            const float c = cs[dim_j[j]], si = sn[dim_j[j]];
-            y = (dim_j[j] & 1) ? (x * c + partner * si) : (x * c - partner * si);
-          }
-          Hs[rl * HP + cbase + j * 32] = f2bf(y);
-        }
-      }
+        for (int r = 0; r < 16; ++r)
+          Cs[(rbase + i * 32 + (r >> 2) * 8 + (r & 3)) * CP + cbase + j * 32] = acc[i][j][r];
     __syncthreads();
     constexpr int CH = BN / 8;
     for (int c = tid; c < BM * CH; c += kThreads) {
       const int row = c / CH, cc = (c % CH) * 8;
       const int m = m0 + row, n = n0 + cc;
       if (m >= mlim || n >= p.N) continue;
+      const float4 x0 = *reinterpret_cast<const float4*>(Cs + row * CP + cc);
+      const float4 x1 = *reinterpret_cast<const float4*>(Cs + row * CP + cc + 4);
+      float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
       const int part = n / e.dmodel;
       const int within = n - part * e.dmodel;
       const int h = within / e.hd, dim = within - h * e.hd;
       const int b = m / e.S, s = m - b * e.S;
+      if (part < 2) {
+        const float* cp = e.cos_t + (int64_t)s * e.hd + dim;
+        const float* sp = e.sin_t + (int64_t)s * e.hd + dim;
+        const float4 c0 = *reinterpret_cast<const float4*>(cp), c1 = *reinterpret_cast<const float4*>(cp + 4);
+        const float4 s0 = *reinterpret_cast<const float4*>(sp), s1 = *reinterpret_cast<const float4*>(sp + 4);
+        const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const float xe = v[2 * t], xo = v[2 * t + 1];
+          v[2 * t] = xe * cv[2 * t] - xo * sv[2 * t];
+          v[2 * t + 1] = xo * cv[2 * t + 1] + xe * sv[2 * t + 1];
+        }
+      }
+      uint4 o;
+      o.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+      o.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+      o.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
+      o.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
       bf16* dst = part == 0 ? e.q : (part == 1 ? e.k : e.v);
-      *reinterpret_cast<uint4*>(dst + (((int64_t)b * e.H + h) * e.S + s) * e.hd + dim) =
-          *reinterpret_cast<const uint4*>(Hs + row * HP + cc);
+      *reinterpret_cast<uint4*>(dst + (((int64_t)b * e.H + h) * e.S + s) * e.hd + dim) = o;
     }
   }
 }
@@ -694,7 +695,7 @@ constexpr size_t lds_bytes() {
   constexpr size_t epi = EPI == EPI_STORE        ? (size_t)BM * (BN + 8) * 4
                          : EPI == EPI_SWIGLU_FWD ? (size_t)BM * (BN + 8) * 2 + (size_t)BM * (BN / 2 + 8) * 2
                          : EPI == EPI_SWIGLU_BWD ? (size_t)BM * (2 * BN + 8) * 2
-                                                 : (size_t)BM * (BN + 8) * 2;
+                                                 : (size_t)BM * (BN + 4) * 4;  // EPI_ROPE_QKV: fp32 tile
   return main_loop > epi ? main_loop : epi;
 }
 
