@@ -20,6 +20,8 @@
 
 #include <stdio.h>
 
+#include <type_traits>
+
 namespace rte {
 
 namespace {
@@ -54,7 +56,7 @@ struct LoaderN {
   static constexpr int PER = (UNITS + kThreads - 1) / kThreads;
   const bf16* rowp[PER];
   bool ok[PER];
-  uint4 r[PER];
+  uint4 r[2][PER];  // two staged k tiles in flight
 
   __device__ __forceinline__ void init(const Operand& o, const bf16* base, int64_t rowshift, int i0, int ilim,
                                        int tid) {
@@ -66,22 +68,26 @@ struct LoaderN {
       rowp[u] = ok[u] ? base + row_off(o, i + rowshift) : base;
     }
   }
+  // Every lane issues its load (masked lanes read a valid address and keep zeros), so the
+  // number of loads in flight per stage is fixed and the wait for a stage is exact.
+  template <int S>
   __device__ __forceinline__ void load(const Operand& o, int k0, int klim, int tid) {
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
       const int q = tid + u * kThreads;
       const int k = k0 + (q % CPR) * 8;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (ok[u] && k < klim) v = *reinterpret_cast<const uint4*>(rowp[u] + col_off(o, k));
-      r[u] = v;
+      const bool valid = ok[u] && k < klim;
+      const uint4 v = *reinterpret_cast<const uint4*>(rowp[u] + (valid ? col_off(o, k) : 0));
+      r[S][u] = valid ? v : make_uint4(0u, 0u, 0u, 0u);
     }
   }
+  template <int S>
   __device__ __forceinline__ void store(bf16* lds, int tid) const {
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
       const int q = tid + u * kThreads;
       if (q >= UNITS) continue;
-      *reinterpret_cast<uint4*>(lds + (q / CPR) * LDP + (q % CPR) * 8) = r[u];
+      *reinterpret_cast<uint4*>(lds + (q / CPR) * LDP + (q % CPR) * 8) = r[S][u];
     }
   }
 };
@@ -94,7 +100,7 @@ struct LoaderT {
   static constexpr int PER = (UNITS + kThreads - 1) / kThreads;
   int64_t coff[PER];
   bool ok[PER];
-  uint4 r[PER * 4];
+  uint4 r[2][PER * 4];  // two staged k tiles in flight
 
   __device__ __forceinline__ void init(const Operand& o, const bf16*, int64_t, int i0, int ilim, int tid) {
 #pragma unroll
@@ -105,6 +111,9 @@ struct LoaderT {
       coff[u] = ok[u] ? col_off(o, i) : 0;
     }
   }
+  // Masked lanes read row min(k, klim - 1) (valid: the first tile starts below klim) and keep
+  // zeros, so every stage issues the same loads.
+  template <int S>
   __device__ __forceinline__ void load(const Operand& o, const bf16* base, int64_t rowshift, int k0, int klim,
                                        int tid) {
 #pragma unroll
@@ -114,21 +123,23 @@ struct LoaderT {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int k = k0 + kb * 4 + j;
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (ok[u] && k < klim) v = *reinterpret_cast<const uint4*>(base + row_off(o, k + rowshift) + coff[u]);
-        r[u * 4 + j] = v;
+        const bool valid = ok[u] && k < klim;
+        const int kk = k < klim ? k : klim - 1;
+        const uint4 v = *reinterpret_cast<const uint4*>(base + row_off(o, kk + rowshift) + coff[u]);
+        r[S][u * 4 + j] = valid ? v : make_uint4(0u, 0u, 0u, 0u);
       }
     }
   }
   __device__ __forceinline__ static uint32_t lo2(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }
   __device__ __forceinline__ static uint32_t hi2(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xffff0000u); }
+  template <int S>
   __device__ __forceinline__ void store(bf16* lds, int tid) const {
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
       const int q = tid + u * kThreads;
       if (q >= UNITS) continue;
       const int kb = q % KB, mb = q / KB;
-      const uint4 a = r[u * 4 + 0], b = r[u * 4 + 1], c = r[u * 4 + 2], d = r[u * 4 + 3];
+      const uint4 a = r[S][u * 4 + 0], b = r[S][u * 4 + 1], c = r[S][u * 4 + 2], d = r[S][u * 4 + 3];
       const uint32_t aw[4] = {a.x, a.y, a.z, a.w};
       const uint32_t bw[4] = {b.x, b.y, b.z, b.w};
       const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
@@ -156,10 +167,12 @@ struct Loader<R, BK, false> {
   __device__ __forceinline__ void init(const Operand& o, const bf16* base, int64_t sh, int i0, int ilim, int tid) {
     l.init(o, base, sh, i0, ilim, tid);
   }
+  template <int S>
   __device__ __forceinline__ void load(const Operand& o, const bf16*, int64_t, int k0, int klim, int tid) {
-    l.load(o, k0, klim, tid);
+    l.template load<S>(o, k0, klim, tid);
   }
-  __device__ __forceinline__ void store(bf16* lds, int tid) const { l.store(lds, tid); }
+  template <int S>
+  __device__ __forceinline__ void store(bf16* lds, int tid) const { l.template store<S>(lds, tid); }
 };
 template <int R, int BK>
 struct Loader<R, BK, true> {
@@ -167,10 +180,12 @@ struct Loader<R, BK, true> {
   __device__ __forceinline__ void init(const Operand& o, const bf16* base, int64_t sh, int i0, int ilim, int tid) {
     l.init(o, base, sh, i0, ilim, tid);
   }
+  template <int S>
   __device__ __forceinline__ void load(const Operand& o, const bf16* base, int64_t sh, int k0, int klim, int tid) {
-    l.load(o, base, sh, k0, klim, tid);
+    l.template load<S>(o, base, sh, k0, klim, tid);
   }
-  __device__ __forceinline__ void store(bf16* lds, int tid) const { l.store(lds, tid); }
+  template <int S>
+  __device__ __forceinline__ void store(bf16* lds, int tid) const { l.template store<S>(lds, tid); }
 };
 
 // ------------------------------------------------------------------ output chunks
@@ -242,8 +257,12 @@ struct EpiFlags {
 
 // ------------------------------------------------------------------ kernel
 
+// Tiles larger than 128x128 keep one workgroup per CU (their LDS and accumulators fill it).
+template <int BM, int BN>
+constexpr int wg_per_cu() { return BM * BN > 128 * 128 ? 1 : 2; }
+
 template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI, bool DUALA = false>
-__global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
+__global__ void __launch_bounds__(256, (wg_per_cu<BM, BN>())) gemm_kernel(GemmArgs p, EpiFlags fl) {
   static_assert(!DUALA || (EPI == EPI_SWIGLU_FWD && !AT), "dual-A is a SwiGLU-forward layout-N mode");
   constexpr int LDP = BK + 8;
   constexpr int WTM = BM / WM, WTN = BN / WN;
@@ -352,27 +371,28 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
   lb.init(p.b, bbase, bshift, n0, p.N, tid);
   const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
   const int ko2 = p.a_koff2;
-  if (nk > 0) {
-    la.load(p.a, abase, ashift, kbeg, kend, tid);
-    if constexpr (DUALA) la2.load(p.a, abase, ashift, kbeg + ko2, kend + ko2, tid);
-    lb.load(p.b, bbase, bshift, kbeg, kend, tid);
-    la.store(smem, tid);
-    if constexpr (DUALA) la2.store(smem + A_TILE, tid);
-    lb.store(smem + B_BASE, tid);
-  }
-  __syncthreads();
 
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    const bool more = kt + 1 < nk;
-    if (more) {
-      const int k0 = kbeg + (kt + 1) * BK;
-      la.load(p.a, abase, ashift, k0, kend, tid);
-      if constexpr (DUALA) la2.load(p.a, abase, ashift, k0 + ko2, kend + ko2, tid);
-      lb.load(p.b, bbase, bshift, k0, kend, tid);
-    }
-    const bf16* a_s = smem + cur * A_STAGE;
-    const bf16* b_s = smem + B_BASE + cur * B_STAGE;
+  // Pipeline: tile t's payload sits in register set t % 2 and LDS buffer t % 2.  While tile t
+  // is multiplied out of LDS, tile t + 2 is being fetched into the set tile t came through
+  // and tile t + 1 (fetched one step earlier) is written to the other LDS buffer, so global
+  // latency is covered by two compute steps.
+  auto load_tile = [&](auto stage, int t) {
+    constexpr int S = decltype(stage)::value;
+    const int k0 = kbeg + t * BK;
+    la.template load<S>(p.a, abase, ashift, k0, kend, tid);
+    if constexpr (DUALA) la2.template load<S>(p.a, abase, ashift, k0 + ko2, kend + ko2, tid);
+    lb.template load<S>(p.b, bbase, bshift, k0, kend, tid);
+  };
+  auto store_tile = [&](auto stage) {
+    constexpr int S = decltype(stage)::value;
+    la.template store<S>(smem + S * A_STAGE, tid);
+    if constexpr (DUALA) la2.template store<S>(smem + S * A_STAGE + A_TILE, tid);
+    lb.template store<S>(smem + B_BASE + S * B_STAGE, tid);
+  };
+  auto compute = [&](auto stage) {
+    constexpr int S = decltype(stage)::value;
+    const bf16* a_s = smem + S * A_STAGE;
+    const bf16* b_s = smem + B_BASE + S * B_STAGE;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8_v af[TM], ag[DUALA ? TM : 1], bfr[TN];
@@ -395,11 +415,24 @@ __global__ void __launch_bounds__(256, 2) gemm_kernel(GemmArgs p, EpiFlags fl) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_op, bfr[j], acc[i][j], 0, 0, 0);
         }
     }
-    if (more) {
-      la.store(smem + (cur ^ 1) * A_STAGE, tid);
-      if constexpr (DUALA) la2.store(smem + (cur ^ 1) * A_STAGE + A_TILE, tid);
-      lb.store(smem + B_BASE + (cur ^ 1) * B_STAGE, tid);
-    }
+  };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  if (nk > 0) {
+    load_tile(S0{}, 0);
+    load_tile(S1{}, 1);
+    store_tile(S0{});
+  }
+  __syncthreads();
+  for (int kt = 0; kt < nk; kt += 2) {
+    load_tile(S0{}, kt + 2);
+    compute(S0{});
+    if (kt + 1 < nk) store_tile(S1{});
+    __syncthreads();
+    if (kt + 1 >= nk) break;
+    load_tile(S1{}, kt + 3);
+    compute(S1{});
+    if (kt + 2 < nk) store_tile(S0{});
     __syncthreads();
   }
 
