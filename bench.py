@@ -28,6 +28,7 @@ for p in (ROOT, ROOT / "speedup-thingy_amd"):
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
+METRIC = "train tokens/sec, recursive_macro bf16 1\u00d7MI355X; FFN MFMA% + route HBM GB/s"
 
 
 def cfg3_config(batch: int = 128, seq: int = 64):
@@ -119,6 +120,23 @@ def kernel_candidates(B: int, S: int):
     def combine():
         _lib.call("rte_combine_rows", yp.data_ptr(), T, k, d, None, None, None, out_pool.data_ptr(), 1, st())
 
+    ids_out = torch.empty(T, k, device=dev, dtype=torch.int32)
+    w_out = torch.empty(T, k, device=dev, dtype=torch.float32)
+
+    def topk():
+        _lib.call("rte_route_topk", logits.data_ptr(), T, C, k, ids_out.data_ptr(), w_out.data_ptr(), st())
+
+    pk_ws_bytes = _lib.load().rte_pack_workspace_bytes(P, C)
+    pk_ws = torch.empty(max(pk_ws_bytes, 16), device=dev, dtype=torch.uint8)
+    pk_out = [torch.empty(P, device=dev, dtype=torch.int32) for _ in range(4)]
+    pk_off = torch.empty(C + 1, device=dev, dtype=torch.int32)
+    pk_w = torch.empty(P, device=dev, dtype=torch.float32)
+
+    def pack():
+        _lib.call("rte_pack_index", ids.data_ptr(), P, C, k, w.data_ptr(), pk_off.data_ptr(), pk_out[0].data_ptr(),
+                  pk_out[1].data_ptr(), pk_out[2].data_ptr(), pk_w.data_ptr(), None, pk_ws.data_ptr(), pk_ws_bytes,
+                  st())
+
     return [
         dict(name="gemm_qkv_rope_fwd", per_step=2, kernels=1, flop=2.0 * T * 3 * d * d,
              bytes=2.0 * T * d + 2.0 * 3 * d * d + 3 * 2.0 * T * d, fn=qkv),
@@ -130,6 +148,11 @@ def kernel_candidates(B: int, S: int):
         # SURVEY combine unit: T*k*d*b + T*k*4 + T*d*b (bf16 rows in, fp32 rows out here)
         dict(name="combine_rows", per_step=2, kernels=1, flop=1.0 * P * d,
              bytes=2.0 * P * d + 4.0 * T * d, fn=combine),
+        # route unit: T*C*4 logits in, T*k*(4+4) ids + weights out
+        dict(name="route_topk", per_step=1, kernels=1, flop=0.0, bytes=4.0 * T * C + 8.0 * T * k, fn=topk),
+        # pack unit: P*(4+4) ids + weights in, 4*P*4 + P*4 slot tables out, (C+1)*4 offsets
+        dict(name="pack_index", per_step=1, kernels=3, flop=0.0, bytes=8.0 * P + 20.0 * P + 4.0 * (C + 1),
+             fn=pack),
         dict(name="gemm_wgrad_qkv", per_step=2, kernels=2, flop=2.0 * T * 3 * d * d,
              bytes=2.0 * T * 3 * d + 2.0 * T * d + 4.0 * 3 * d * d, fn=wgrad),
     ]
@@ -307,7 +330,7 @@ def main(argv=None) -> int:
     value = tokens / elapsed
 
     out = {
-        "metric": "train tokens/sec, recursive_macro bf16 1xMI355X",
+        "metric": METRIC,
         "value": round(value, 1),
         "unit": "tokens/s",
         "n_gpus": 1,

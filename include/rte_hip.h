@@ -183,6 +183,25 @@ int rte_ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* tar
 int rte_ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
                const float* dloss, const float* extra, void* dlogits, void* stream);
 
+/* ---- control-variate audit correction (replaces AuditEngine.correction's loss arithmetic,
+ *      rte/audit.py:296-321, over lm_loss_per_sample rte/models.py:73-75) ----
+ * hot_tok f32 [B, seq] token losses of the hot (macro) pass; exact_tok f32 [A, seq] token losses
+ * of the exact replay of the audited rows idx int64 [A] (distinct, in [0, B)); p f32 [B]
+ * inclusion probabilities (clamped below at 1e-12); clip >= 0 (INFINITY for no clip).
+ * fwd, one workgroup, fixed reduction order:
+ *   hot[m] = sum_s hot_tok[m, s], exact_ps[a] = sum_s exact_tok[a, s], r_a = exact_ps[a] - hot[idx[a]]
+ *   corrected[m] = hot[m]; if grad_corrected: corrected[idx[a]] = hot[idx[a]] + clamp(r_a, +-clip) / p
+ *   coef f32 [B + A]: per-row and per-audited-row gradient coefficient (1/p inside the clip when
+ *   grad_corrected, else 0), kept for the backward
+ *   stats f32 [4] = mean r, std r, var r (population, unclipped), mean(hot + clamp(r)/p);
+ *   NaN if some idx lies outside [0, B).  B <= 8192.
+ * bwd: dhot_tok[m, s] = g[m] (1 - coef[m]), dexact_tok[a, s] = g[idx[a]] coef[B + a] (optional). */
+int rte_audit_correct_fwd(const float* hot_tok, const float* exact_tok, int B, int seq, const int64_t* idx, int A,
+                          const float* p, float clip, int grad_corrected, float* corrected, float* exact_ps,
+                          float* coef, float* stats, void* stream);
+int rte_audit_correct_bwd(const float* g, int B, int seq, const int64_t* idx, int A, const float* coef,
+                          float* dhot_tok, float* dexact_tok, void* stream);
+
 /* ---- grouped linear: rows keyed to a group, one weight matrix per group ----
  * Replaces the per-sample weight gather + bmm of the macro operators (rte/macro.py:201-236,
  * gather of v / u by (recipe, stride) at :208-212) without materialising per-sample weights.

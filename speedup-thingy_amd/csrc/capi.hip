@@ -32,6 +32,11 @@ int ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets
            hipStream_t s);
 int ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse, const float* g,
            const float* extra, bf16* dlogits, hipStream_t s);
+int audit_fwd(const float* hot_tok, const float* exact_tok, int B, int S, const int64_t* idx, int A, const float* p,
+              float clip, int grad_corrected, float* corrected, float* exact_ps, float* coef, float* stats,
+              hipStream_t s);
+int audit_bwd(const float* g, int B, int S, const int64_t* idx, int A, const float* coef, float* dhot_tok,
+              float* dexact_tok, hipStream_t s);
 int shortlist_build(const int64_t* targets, const int32_t* top_clusters, int tc, const int64_t* members,
                     int n_clusters, int per_cluster, const int64_t* random_negs, int R, int H, int L, int V, int T,
                     int32_t* shortlist, int32_t* dup_per_token, hipStream_t s);
@@ -713,6 +718,18 @@ int rte_ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* tar
 int rte_ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
                const float* dloss, const float* extra, void* dlogits, void* stream) {
   return ce_bwd(logits, ld, T, V, targets, lse, dloss, extra, B16(dlogits), S(stream));
+}
+
+int rte_audit_correct_fwd(const float* hot_tok, const float* exact_tok, int B, int seq, const int64_t* idx, int A,
+                          const float* p, float clip, int grad_corrected, float* corrected, float* exact_ps,
+                          float* coef, float* stats, void* stream) {
+  return audit_fwd(hot_tok, exact_tok, B, seq, idx, A, p, clip, grad_corrected, corrected, exact_ps, coef, stats,
+                   S(stream));
+}
+
+int rte_audit_correct_bwd(const float* g, int B, int seq, const int64_t* idx, int A, const float* coef,
+                          float* dhot_tok, float* dexact_tok, void* stream) {
+  return audit_bwd(g, B, seq, idx, A, coef, dhot_tok, dexact_tok, S(stream));
 }
 
 int rte_cast_f32_bf16(const float* x, int64_t n, void* y, void* stream) {

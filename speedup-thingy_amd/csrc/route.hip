@@ -1,6 +1,7 @@
 // Token -> cluster routing, deterministic packing and fixed-order combine.
 //
-//  route_topk  : one wave64 per token; k rounds of a wave arg-max over the C
+//  route_topk  : one wave64 per token; C <= 128: each logit ranked against the row
+//                (readlane broadcast), else k rounds of a wave arg-max over the C
 //                router logits (value descending, index ascending on ties,
 //                NaN above everything as torch.topk does), then softmax over
 //                the k selected logits.
@@ -88,6 +89,77 @@ __global__ void __launch_bounds__(256) route_topk_kernel(const float* __restrict
   }
 }
 
+// Small pools (C <= 64 * PER): the rank of element c is the number of elements better
+// than it, counted against every logit of the row broadcast with readlane (no LDS round
+// trips on the critical path); the k best land in LDS at their rank, then lanes j < k
+// finish exactly like route_topk_kernel (same selection values, same softmax order).
+template <int PER, bool kNaN>
+__device__ __forceinline__ void rank_row(const float (&v)[PER], int lane, int C, int (&rank)[PER]) {
+#pragma unroll
+  for (int q = 0; q < PER; ++q) {
+    const int nq = C - 64 * q < 64 ? C - 64 * q : 64;
+    for (int l = 0; l < nq; ++l) {
+      const float vj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[q]), l));
+      const int j = 64 * q + l;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int c = lane + 64 * i;
+        if (kNaN)
+          rank[i] += better(vj, j, v[i], c) ? 1 : 0;
+        else
+          rank[i] += (vj > v[i] || (vj == v[i] && j < c)) ? 1 : 0;
+      }
+    }
+  }
+}
+
+template <int PER>
+__global__ void __launch_bounds__(256) route_topk_rank_kernel(const float* __restrict__ logits, int T, int C, int k,
+                                                              int32_t* __restrict__ ids,
+                                                              float* __restrict__ weights) {
+  __shared__ float sel_v[4][16];
+  __shared__ int sel_i[4][16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = blockIdx.x * 4 + wave;
+  const bool live = t < T;  // no early exit: every wave reaches the barrier below
+  const float* row = logits + (int64_t)(live ? t : 0) * C;
+  float v[PER];
+  int rank[PER];
+  bool nan_here = false;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int c = lane + 64 * i;
+    v[i] = (live && c < C) ? row[c] : 0.0f;
+    rank[i] = 0;
+    nan_here |= v[i] != v[i];
+  }
+  if (__ballot(nan_here) != 0)
+    rank_row<PER, true>(v, lane, C, rank);
+  else
+    rank_row<PER, false>(v, lane, C, rank);
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int c = lane + 64 * i;
+    if (c < C && rank[i] < k) {
+      sel_v[wave][rank[i]] = v[i];
+      sel_i[wave][rank[i]] = c;
+    }
+  }
+  __syncthreads();
+  if (!live) return;
+  const float my_v = lane < k ? sel_v[wave][lane] : 0.0f;
+  const int my_i = lane < k ? sel_i[wave][lane] : 0;
+  const float mx = __shfl(my_v, 0, 64);
+  const float ex = lane < k ? expf(my_v - mx) : 0.0f;
+  float denom = ex;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) denom += __shfl_xor(denom, off, 64);
+  if (lane < k) {
+    ids[(int64_t)t * k + lane] = my_i;
+    weights[(int64_t)t * k + lane] = ex / denom;
+  }
+}
+
 constexpr int kPackChunk = 256;
 
 // hist layout: hist[c * nblk + b] = pairs of block b routed to cluster c.
@@ -110,33 +182,64 @@ __global__ void __launch_bounds__(256) pack_count_kernel(const int32_t* __restri
   for (int c = threadIdx.x; c < C; c += blockDim.x) hist[(int64_t)c * nblk + blockIdx.x] = sh[c];
 }
 
-// Exclusive scan of hist (length L = C * nblk) in place, single workgroup of 1024.
-__global__ void __launch_bounds__(1024) pack_scan_kernel(int32_t* __restrict__ hist, int C, int nblk,
-                                                         int32_t* __restrict__ offsets, int P) {
-  __shared__ int32_t part[1024];
+// Exclusive scan of hist (length L = C * nblk) in place, single workgroup of 1024, in tiles of
+// 8192 entries: coalesced loads into LDS, each thread scans 8 consecutive entries, a wave scan
+// of the thread totals (shuffles), the 16 wave totals in LDS, and a carry across tiles.
+constexpr int kScanThreads = 1024, kScanPer = 8, kScanTile = kScanThreads * kScanPer;
+
+__global__ void __launch_bounds__(kScanThreads) pack_scan_kernel(int32_t* __restrict__ hist, int C, int nblk,
+                                                                 int32_t* __restrict__ offsets, int P) {
+  __shared__ int32_t tile[kScanTile + kScanTile / 32];  // one pad word per 32 entries
+  __shared__ int32_t wsum[kScanThreads / 64];
+  __shared__ int32_t carry_sh;
   const int64_t L = (int64_t)C * nblk;
-  const int tid = threadIdx.x;
-  const int64_t seg = (L + 1023) / 1024;
-  const int64_t b0 = tid * seg, b1 = b0 + seg < L ? b0 + seg : L;
-  int32_t s = 0;
-  for (int64_t i = b0; i < b1; ++i) s += hist[i];
-  part[tid] = s;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int32_t y = tid >= off ? part[tid - off] : 0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  auto at = [](int i) { return i + (i >> 5); };
+  int32_t carry = 0;
+  for (int64_t base = 0; base < L; base += kScanTile) {
+    const int n = L - base < kScanTile ? (int)(L - base) : kScanTile;
+#pragma unroll
+    for (int r = 0; r < kScanPer; ++r) {
+      const int i = r * kScanThreads + tid;
+      tile[at(i)] = i < n ? hist[base + i] : 0;
+    }
     __syncthreads();
-    part[tid] += y;
+    int32_t v[kScanPer], sum = 0;
+#pragma unroll
+    for (int r = 0; r < kScanPer; ++r) {
+      v[r] = tile[at(tid * kScanPer + r)];
+      sum += v[r];
+    }
+    // inclusive wave scan of the thread totals
+    int32_t inc = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int32_t y = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += y;
+    }
+    if (lane == 63) wsum[wave] = inc;
+    __syncthreads();
+    int32_t before = carry;
+    for (int w2 = 0; w2 < wave; ++w2) before += wsum[w2];
+    int32_t run = before + inc - sum;
+#pragma unroll
+    for (int r = 0; r < kScanPer; ++r) {
+      tile[at(tid * kScanPer + r)] = run;
+      run += v[r];
+    }
+    if (tid == kScanThreads - 1) carry_sh = run;
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kScanPer; ++r) {
+      const int i = r * kScanThreads + tid;
+      if (i < n) hist[base + i] = tile[at(i)];
+    }
+    carry = carry_sh;
     __syncthreads();
   }
-  int32_t run = part[tid] - s;
-  for (int64_t i = b0; i < b1; ++i) {
-    const int32_t h = hist[i];
-    hist[i] = run;
-    run += h;
-  }
-  __syncthreads();
-  for (int c = tid; c < C; c += 1024) offsets[c] = hist[(int64_t)c * nblk];
-  if (tid == 0) offsets[C] = part[1023];
+  // every thread's last global write precedes this barrier; offsets read the scanned hist
+  for (int c = tid; c < C; c += kScanThreads) offsets[c] = hist[(int64_t)c * nblk];
+  if (tid == 0) offsets[C] = carry;
   (void)P;
 }
 
@@ -242,31 +345,38 @@ __global__ void __launch_bounds__(256) combine_kernel(const bf16* __restrict__ r
 
 // Routing-weight gradient: weights are softmax over the k selected logits, so
 // dlogit_j = w_j * (dw_j - sum_i w_i dw_i); everything else in the row is 0.
+// One thread per logit (t, c): the per-token sum s = sum_j w_j dw_j in j order, then the
+// gradient of the j that selected c (the last one, if an id repeats), zero elsewhere.  Rows
+// are written whole and coalesced.
 __global__ void __launch_bounds__(256) route_bwd_kernel(const int32_t* __restrict__ ids,
                                                         const float* __restrict__ w,
                                                         const float* __restrict__ dw_slot,
                                                         const int32_t* __restrict__ slot_of_pair, int T,
                                                         int C, int k, bf16* __restrict__ dlogits,
                                                         float* __restrict__ dlogits_f32) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= T) return;
-  float dw[16];
-  float s = 0.0f;
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (int64_t)T * C) return;
+  const int64_t t = e / C;
+  const int c = (int)(e - t * C);
+  const int32_t* it = ids + t * k;
+  const float* wt = w + t * k;
+  const int32_t* st = slot_of_pair + t * k;
+  float s = 0.0f, wsel = 0.0f, dsel = 0.0f;
+  bool hit = false;
   for (int j = 0; j < k; ++j) {
-    const int slot = slot_of_pair[(int64_t)t * k + j];
-    dw[j] = slot >= 0 ? dw_slot[slot] : 0.0f;
-    s += w[(int64_t)t * k + j] * dw[j];
+    const int slot = st[j];
+    const float dw = slot >= 0 ? dw_slot[slot] : 0.0f;
+    const float wj = wt[j];
+    s += wj * dw;
+    if (it[j] == c) {
+      hit = true;
+      wsel = wj;
+      dsel = dw;
+    }
   }
-  if (dlogits)
-    for (int c = 0; c < C; ++c) dlogits[(int64_t)t * C + c] = 0;
-  if (dlogits_f32)
-    for (int c = 0; c < C; ++c) dlogits_f32[(int64_t)t * C + c] = 0.0f;
-  for (int j = 0; j < k; ++j) {
-    const float g = w[(int64_t)t * k + j] * (dw[j] - s);
-    const int c = ids[(int64_t)t * k + j];
-    if (dlogits) dlogits[(int64_t)t * C + c] = f2bf(g);
-    if (dlogits_f32) dlogits_f32[(int64_t)t * C + c] = g;
-  }
+  const float g = hit ? wsel * (dsel - s) : 0.0f;
+  if (dlogits) dlogits[e] = f2bf(g);
+  if (dlogits_f32) dlogits_f32[e] = g;
 }
 
 }  // namespace
@@ -275,7 +385,13 @@ int route_topk(const float* logits, int T, int C, int k, int32_t* ids, float* we
   RTE_REQUIRE(T >= 0 && C >= 1 && C <= 64 * kMaxPerLane, "route_topk: C must be in [1, 1024]");
   RTE_REQUIRE(k >= 1 && k <= 16 && k <= C, "route_topk: k must be in [1, min(16, C)]");
   if (T == 0) return 0;
-  hipLaunchKernelGGL(route_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, C, k, ids, weights);
+  const dim3 grid((T + 3) / 4);
+  if (C <= 64)
+    hipLaunchKernelGGL(route_topk_rank_kernel<1>, grid, dim3(256), 0, s, logits, T, C, k, ids, weights);
+  else if (C <= 128)
+    hipLaunchKernelGGL(route_topk_rank_kernel<2>, grid, dim3(256), 0, s, logits, T, C, k, ids, weights);
+  else
+    hipLaunchKernelGGL(route_topk_kernel, grid, dim3(256), 0, s, logits, T, C, k, ids, weights);
   return check_launch("route_topk");
 }
 
@@ -329,8 +445,9 @@ int route_bwd(const int32_t* ids, const float* w, const float* dw_slot, const in
               int C, int k, bf16* dlogits, float* dlogits_f32, hipStream_t s) {
   RTE_REQUIRE(k >= 1 && k <= 16, "route_bwd: k must be in [1, 16]");
   if (T == 0) return 0;
-  hipLaunchKernelGGL(route_bwd_kernel, dim3((T + 255) / 256), dim3(256), 0, s, ids, w, dw_slot, slot_of_pair,
-                     T, C, k, dlogits, dlogits_f32);
+  const int64_t n = (int64_t)T * C;
+  hipLaunchKernelGGL(route_bwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ids, w, dw_slot,
+                     slot_of_pair, T, C, k, dlogits, dlogits_f32);
   return check_launch("route_bwd");
 }
 

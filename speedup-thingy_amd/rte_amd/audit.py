@@ -13,6 +13,7 @@ from dataclasses import dataclass
 import torch
 
 from rte_amd.config import TrainingConfig
+from rte_amd.kernels import hip_ops
 from rte_amd.macro import macro_alignment_metrics, macro_distill_loss
 from rte_amd.models import ModelMeta, ModelOutput, RecursiveModel
 
@@ -218,19 +219,19 @@ class AuditEngine:
                 with (nullcontext() if grad_corr else torch.no_grad()):
                     exact = model.forward_exact_subset(tokens, targets, idx, reuse_router_decisions=hot.meta.router,
                                                        cached_h0=hot.meta.h0)
-            hot_sub = hot.loss_per_sample.index_select(0, idx)
-            residual = exact.loss_per_sample - hot_sub
-            metrics["audit_residual_mean"] = residual.mean()
-            metrics["audit_residual_std"] = residual.float().std(unbiased=False)
-            metrics["audit_residual_var"] = residual.float().var(unbiased=False)
-            if self.config.audit_residual_clip is not None:
-                residual = residual.clamp(-self.config.audit_residual_clip, self.config.audit_residual_clip)
-            if not grad_corr:
-                residual = residual.detach()
-            p_sub = p.index_select(0, idx).clamp_min(1e-12)
-            metrics["corrected_metric_loss"] = (hot_sub + residual.detach() / p_sub).mean()
-            if grad_corr:
-                corrected = corrected.index_copy(0, idx, hot_sub + residual / p_sub)
+            hot_tok = hot.meta.token_loss
+            exact_tok = exact.meta.token_loss
+            if hot_tok is None or exact_tok is None:
+                raise ValueError("audit correction needs the token losses of the hot pass and of the replay")
+            # one kernel: per-sample sums, residual, clip, corrected rows and residual statistics
+            corrected, _, st = hip_ops.audit_correct(
+                hot_tok, exact_tok if grad_corr else exact_tok.detach(), idx, p,
+                clip=self.config.audit_residual_clip, grad_corrected=grad_corr)
+            metrics["audit_residual_mean"] = st[0]
+            metrics["audit_residual_std"] = st[1]
+            metrics["audit_residual_var"] = st[2]
+            metrics["corrected_metric_loss"] = st[3]
+            metrics["loss_residual"] = st[0]
             hot_end = hot.meta.recurrent_hidden.index_select(0, idx)
             h0_sub = hot.meta.h0.index_select(0, idx)
             hot_logits = hot.meta.logits.index_select(0, idx) if hot.meta.logits is not None else None
@@ -247,7 +248,6 @@ class AuditEngine:
                                             hot_logits=None if hot_logits is None else hot_logits.detach(),
                                             exact_logits=exact.meta.logits)
             metrics.update(align)
-            metrics["loss_residual"] = (exact.loss_per_sample - hot_sub).mean()
             # recent residual feeds the next step's audit probability; kept on device
             self._pending_residual = (1.0 - align["hidden_cosine_exact_macro"]).detach().clamp_min(0)
         if hot.meta.recipe_ids is not None:

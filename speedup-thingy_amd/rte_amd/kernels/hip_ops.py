@@ -583,6 +583,55 @@ def lm_head_ce(hidden, w, targets):
     return LMHeadCEFn.apply(hidden, w, targets)
 
 
+# ----------------------------------------------------------------------------- audit correction
+
+class AuditCorrectFn(torch.autograd.Function):
+    """Control-variate audit correction over token losses in one kernel (rte/audit.py:296-321):
+    per-sample sums of the hot and exact token losses, residual, clip, corrected losses and the
+    residual statistics; the backward broadcasts the per-sample gradient back to the tokens."""
+
+    @staticmethod
+    def forward(ctx, hot_tok, exact_tok, idx, p, clip, grad_corrected):
+        _lib.require_device_tensors("audit_correct", hot_tok, exact_tok, idx, p)
+        B, S = hot_tok.shape
+        A = int(idx.numel())
+        h = hot_tok.contiguous().to(F32)
+        e = None if exact_tok is None or A == 0 else exact_tok.reshape(A, S).contiguous().to(F32)
+        ix = idx.reshape(-1).contiguous().to(torch.int64)
+        pp = p.reshape(-1).contiguous().to(F32)
+        if pp.numel() != B:
+            raise ValueError(f"audit_correct: {pp.numel()} probabilities for {B} samples")
+        dev = h.device
+        corrected = torch.empty((B,), dtype=F32, device=dev)
+        exact_ps = torch.empty((A,), dtype=F32, device=dev)
+        coef = torch.empty((B + A,), dtype=F32, device=dev)
+        stats = torch.empty((4,), dtype=F32, device=dev)
+        c = float("inf") if clip is None else float(clip)
+        call("rte_audit_correct_fwd", ptr(h), ptr(e), B, S, ptr(ix), A, ptr(pp), c, int(bool(grad_corrected)),
+             ptr(corrected), ptr(exact_ps), ptr(coef), ptr(stats), _s())
+        ctx.save_for_backward(ix, coef)
+        ctx.meta = (B, S, A, hot_tok.dtype, None if exact_tok is None else exact_tok.dtype)
+        ctx.mark_non_differentiable(exact_ps, stats)
+        return corrected, exact_ps, stats
+
+    @staticmethod
+    def backward(ctx, g, _g_exact, _g_stats):
+        ix, coef = ctx.saved_tensors
+        B, S, A, h_dt, e_dt = ctx.meta
+        gg = g.contiguous().to(F32)
+        dh = torch.empty((B, S), dtype=F32, device=gg.device)
+        want_e = ctx.needs_input_grad[1] and A > 0
+        de = torch.empty((A, S), dtype=F32, device=gg.device) if want_e else None
+        call("rte_audit_correct_bwd", ptr(gg), B, S, ptr(ix), A, ptr(coef), ptr(dh), ptr(de), _s())
+        return dh.to(h_dt), (de.to(e_dt) if want_e else None), None, None, None, None
+
+
+def audit_correct(hot_tok, exact_tok, idx, p, *, clip=None, grad_corrected=True):
+    """(corrected per-sample loss [B], exact per-sample loss [A], stats [4] = residual mean, std,
+    var, corrected metric loss) from token losses hot_tok [B, S] and exact_tok [A, S]."""
+    return AuditCorrectFn.apply(hot_tok, exact_tok, idx, p, clip, grad_corrected)
+
+
 # ----------------------------------------------------------------------------- grouped linear
 
 def group_rows(keys: torch.Tensor, n_groups: int) -> PackIndex:

@@ -37,6 +37,7 @@ class ModelMeta:
     macro_trace: MacroTrace | None = None
     shortlist: ShortlistResult | None = None
     active_touches: torch.Tensor | None = None
+    token_loss: torch.Tensor | None = None
 
 
 @dataclass(slots=True)
@@ -54,11 +55,12 @@ def lm_loss_per_sample(logits: torch.Tensor, targets: torch.Tensor) -> torch.Ten
 
 
 def head_logits_loss(hidden, vocab_weight, targets):
-    """(logits, per-sample CE) with the HIP LM-head GEMM + fused CE kernels; targets may be None."""
+    """(logits, per-sample CE, token CE) with the HIP LM-head GEMM + fused CE kernels; targets
+    may be None."""
     if targets is None:
-        return K.k_logits_full(hidden, vocab_weight), None
+        return K.k_logits_full(hidden, vocab_weight), None, None
     logits, tok = hip_ops.lm_head_ce(hidden, vocab_weight, targets)
-    return logits, tok.sum(dim=-1)
+    return logits, tok.sum(dim=-1), tok
 
 
 class DenseModel(nn.Module):
@@ -81,9 +83,9 @@ class DenseModel(nn.Module):
         for block in self.blocks:
             x = block(x)
         hidden = self.final_norm(x)
-        logits, lps = head_logits_loss(hidden, self.vocab_weight, targets)
+        logits, lps, tok = head_logits_loss(hidden, self.vocab_weight, targets)
         return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
-                           ModelMeta(hidden=hidden, logits=logits))
+                           ModelMeta(hidden=hidden, logits=logits, token_loss=tok))
 
 
 class RecursiveModel(nn.Module):
@@ -137,10 +139,10 @@ class RecursiveModel(nn.Module):
             if return_states and (t + 1) in self.config.depth_choices:
                 states[t + 1] = h.clone()
         hidden = self._coda_hidden(h)
-        logits, lps = head_logits_loss(hidden, self.vocab_weight, targets)
+        logits, lps, tok = head_logits_loss(hidden, self.vocab_weight, targets)
         meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
                          hidden=hidden, logits=logits, states=states if return_states else None,
-                         active_touches=self.active_touch_table[route.recipe_id])
+                         active_touches=self.active_touch_table[route.recipe_id], token_loss=tok)
         return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
                            meta)
 
@@ -176,13 +178,14 @@ class RecursiveModel(nn.Module):
             full_logits = None
             sl = self.shortlist_head.loss(hidden, targets, self.vocab_weight, seed=seed,
                                           random_negs=shortlist_random_negs)
-            lps, logits = sl.loss_per_sample, sl.logits
+            lps, logits, tok = sl.loss_per_sample, sl.logits, sl.token_loss
         else:
             hidden = self._coda_hidden(h)
-            full_logits, lps = head_logits_loss(hidden, self.vocab_weight, targets)
+            full_logits, lps, tok = head_logits_loss(hidden, self.vocab_weight, targets)
             logits = full_logits
         meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
                          hidden=hidden, logits=full_logits, states=trace.states if return_states else None,
-                         macro_trace=trace, shortlist=sl, active_touches=self.active_touch_table[route.recipe_id])
+                         macro_trace=trace, shortlist=sl, active_touches=self.active_touch_table[route.recipe_id],
+                         token_loss=tok)
         return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
                            meta)

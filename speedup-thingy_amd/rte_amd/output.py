@@ -26,6 +26,7 @@ class ShortlistResult:
     target_positions: torch.Tensor
     cluster_logits: torch.Tensor
     duplicate_count: torch.Tensor
+    token_loss: torch.Tensor | None = None
 
 
 class ShortlistHead(nn.Module):
@@ -87,4 +88,4 @@ class ShortlistHead(nn.Module):
         sl, cl, dup = self._build(hidden, targets, seed, random_negs)
         logits, tok = hip_ops.shortlist_ce(hidden, vocab_weight, sl)
         return ShortlistResult(tok.sum(dim=-1), logits, sl.long(), torch.zeros_like(targets, dtype=torch.long), cl,
-                               dup.sum().float())
+                               dup.sum().float(), tok)

@@ -79,7 +79,8 @@ def test_gemm_bf16_out_resid_alpha():
 
 # ---------------------------------------------------------------- routing / packing
 
-@pytest.mark.parametrize("T,C,k", [(1, 4, 1), (513, 32, 4), (8192, 64, 8), (300, 256, 16), (77, 1000, 3)])
+@pytest.mark.parametrize("T,C,k", [(1, 4, 1), (513, 32, 4), (8192, 64, 8), (301, 100, 16), (64, 128, 16),
+                                   (300, 256, 16), (77, 1000, 3)])
 def test_route_topk_bit_exact(T, C, k):
     H = _ops()
     rng = np.random.default_rng(T + C)
@@ -95,7 +96,8 @@ def test_route_topk_bit_exact(T, C, k):
     np.testing.assert_allclose(w.cpu().numpy()[ok], rw[ok], rtol=FP32_RTOL, atol=1e-7)
 
 
-@pytest.mark.parametrize("T,k,C", [(1, 1, 1), (1000, 4, 32), (8192, 8, 64), (4096, 16, 256)])
+@pytest.mark.parametrize("T,k,C", [(1, 1, 1), (1000, 4, 32), (8192, 8, 64), (4096, 16, 256), (5000, 3, 77),
+                                   (20000, 8, 64)])
 def test_pack_index_bit_exact(T, k, C):
     H = _ops()
     rng = np.random.default_rng(T * k + C)
@@ -109,6 +111,31 @@ def test_pack_index_bit_exact(T, k, C):
     for name in ("offsets", "pair_of_slot", "tok_of_slot", "slot_of_pair"):
         np.testing.assert_array_equal(getattr(pk, name).cpu().numpy(), ref[name], err_msg=name)
     np.testing.assert_array_equal(pk.w_of_slot.cpu().numpy(), w.reshape(-1)[ref["pair_of_slot"]])
+
+
+@pytest.mark.parametrize("T,C,k", [(8192, 64, 8), (333, 100, 5)])
+def test_route_bwd_matches_oracle(T, C, k):
+    """dlogits of the top-k softmax: bf16 and fp32 outputs; pairs whose slot is -1 carry no
+    gradient (their dw counts as 0)."""
+    from rte_amd import _lib
+
+    H = _ops()
+    rng = np.random.default_rng(T + k)
+    lg = rng.standard_normal((T, C)).astype(np.float32)
+    ids, w = H.route_topk(torch.from_numpy(lg).to(DEV), k)
+    cl = ids.clone()
+    cl[::7, 0] = -1  # dropped pairs
+    pk = H.pack_index(cl, C, w)
+    dw_slot = torch.from_numpy(rng.standard_normal(T * k).astype(np.float32)).to(DEV)
+    d32 = torch.empty(T, C, device=DEV)
+    d16 = torch.empty(T, C, device=DEV, dtype=torch.bfloat16)
+    _lib.call("rte_route_bwd", ids.data_ptr(), w.data_ptr(), dw_slot.data_ptr(), pk.slot_of_pair.data_ptr(), T, C,
+              k, d16.data_ptr(), d32.data_ptr(), _lib.stream_ptr())
+    sop = pk.slot_of_pair.cpu().numpy().reshape(T, k)
+    dw = np.where(sop >= 0, dw_slot.cpu().numpy()[np.maximum(sop, 0)], 0.0)
+    ref = R.route_softmax_bwd(ids.cpu().numpy(), w.cpu().numpy(), dw, C)
+    np.testing.assert_allclose(d32.cpu().numpy(), ref, rtol=1e-5, atol=1e-6)
+    np.testing.assert_array_equal(d16.float().cpu().numpy(), d32.to(torch.bfloat16).float().cpu().numpy())
 
 
 def test_pack_index_counts_invalid_ids():
@@ -554,3 +581,43 @@ def test_grouped_linear_fwd_bwd(N, K, Nout, G, skew):
     tw.grad = None
     H.grouped_linear(tx, tw, pk).backward(torch.from_numpy(dy).to(DEV))
     assert torch.equal(first, tw.grad), "weight gradient not bitwise repeatable"
+
+
+# ---------------------------------------------------------------- audit correction
+
+@pytest.mark.parametrize("B,S,A,clip,grad_corrected", [
+    (128, 64, 1, None, True),      # the cfg3 step: one audited sample, p = 1/128
+    (32, 512, 4, 5.0, True),       # long rows, clipped and unclipped residuals
+    (9, 7, 9, None, True),         # p = 1 on every sample
+    (300, 33, 17, 1.0, False),     # not gradient-corrected: hot kept, no exact gradient
+    (5, 3, 0, None, True),         # nothing audited
+])
+def test_audit_correct_matches_oracle(B, S, A, clip, grad_corrected):
+    from oracle import audit as AU
+
+    rng = np.random.default_rng(B * 7 + A)
+    hot = rng.normal(size=(B, S)).astype(np.float32)
+    idx = rng.permutation(B)[:A].astype(np.int64)
+    exact = (hot[idx] + rng.normal(size=(A, S)) * 0.3).astype(np.float32)
+    p = (np.ones(B) if A == B else rng.uniform(0.01, 1.0, B)).astype(np.float32)
+    ops = _ops()
+    th = torch.from_numpy(hot).to(DEV).requires_grad_(True)
+    te = torch.from_numpy(exact).to(DEV).requires_grad_(grad_corrected)
+    corr, ex, st = ops.audit_correct(th, te, torch.from_numpy(idx).to(DEV), torch.from_numpy(p).to(DEV), clip=clip,
+                                     grad_corrected=grad_corrected)
+    o_corr, o_ex, o_st = AU.correction(hot, exact, idx, p, clip, grad_corrected)
+    np.testing.assert_allclose(corr.detach().cpu().numpy(), o_corr, rtol=1e-5, atol=1e-5 * np.abs(o_corr).max())
+    if A:
+        np.testing.assert_allclose(ex.cpu().numpy(), o_ex, rtol=1e-5, atol=1e-5 * np.abs(o_ex).max())
+        scale = np.abs(o_st).max()
+        np.testing.assert_allclose(st.cpu().numpy(), o_st, rtol=1e-5, atol=1e-5 * scale)
+    g = rng.normal(size=B).astype(np.float32)
+    corr.backward(torch.from_numpy(g).to(DEV))
+    o_dh, o_de = AU.correction_bwd(g, hot, exact, idx, p, clip, grad_corrected)
+    np.testing.assert_allclose(th.grad.cpu().numpy(), o_dh, rtol=1e-5, atol=1e-6 * np.abs(o_dh).max())
+    if grad_corrected and A:
+        np.testing.assert_allclose(te.grad.cpu().numpy(), o_de, rtol=1e-5, atol=1e-6 * np.abs(o_de).max())
+    # repeated calls give identical bits (fixed reduction order)
+    corr2, _, st2 = ops.audit_correct(th.detach(), te.detach(), torch.from_numpy(idx).to(DEV),
+                                      torch.from_numpy(p).to(DEV), clip=clip, grad_corrected=grad_corrected)
+    assert torch.equal(corr.detach(), corr2) and torch.equal(st, st2)

@@ -372,6 +372,89 @@ def test_audit_correction_p1_is_exact():
     np.testing.assert_allclose(hot + p * (exact - hot) / p, exact)
 
 
+def test_audit_oracle_p1_replaces_hot_with_exact():
+    """tests/test_audit.py:12-37 of the reference: with p = 1 on every sample the corrected
+    per-sample loss is the exact one."""
+    from oracle import audit as AU
+
+    rng = _rng(11)
+    hot, exact = rng.normal(size=(4, 6)), rng.normal(size=(4, 6))
+    corr, ex, st = AU.correction(hot, exact, np.arange(4), np.ones(4))
+    np.testing.assert_allclose(corr, exact.sum(-1), rtol=1e-12)
+    np.testing.assert_allclose(ex, exact.sum(-1), rtol=1e-12)
+    np.testing.assert_allclose(st[3], exact.sum(-1).mean(), rtol=1e-12)
+    # audit_mode other than gradient_corrected keeps the hot loss
+    corr2, _, _ = AU.correction(hot, exact, np.arange(4), np.ones(4), grad_corrected=False)
+    np.testing.assert_allclose(corr2, hot.sum(-1), rtol=1e-12)
+
+
+def test_audit_oracle_fixed_count_is_unbiased_by_enumeration():
+    """Every k-of-n subset drawn with equal probability (the fixed-count sampler,
+    p = k / n): the mean of corrected over all subsets is the exact loss, row by row."""
+    import itertools
+
+    from oracle import audit as AU
+
+    rng = _rng(12)
+    n, k, S = 6, 2, 5
+    hot, exact = rng.normal(size=(n, S)), rng.normal(size=(n, S))
+    p = np.full(n, k / n)
+    acc, cnt = np.zeros(n), 0
+    for sub in itertools.combinations(range(n), k):
+        corr, _, _ = AU.correction(hot, exact[list(sub)], np.array(sub), p)
+        acc += corr
+        cnt += 1
+    np.testing.assert_allclose(acc / cnt, exact.sum(-1), rtol=1e-12)
+
+
+def _torch_reference_correction(hot_tok, exact_tok, idx, p, clip, grad_corrected):
+    """The reference's boolean-mask formulation (rte/audit.py:305-321) in float64 torch."""
+    B = hot_tok.shape[0]
+    mask = torch.zeros(B, dtype=torch.bool)
+    mask[idx] = True
+    order = torch.argsort(idx)  # the mask visits audited rows in ascending order
+    hot = hot_tok.sum(-1)
+    exact = exact_tok[order].sum(-1)
+    corrected = hot.clone()
+    hot_subset = hot[mask]
+    residual = exact - hot_subset
+    stats = [residual.mean(), residual.std(unbiased=False), residual.var(unbiased=False)]
+    if clip is not None:
+        residual = residual.clamp(-clip, clip)
+    if not grad_corrected:
+        residual = residual.detach()
+    stats.append((hot_subset + residual.detach() / p[mask].clamp_min(1e-12)).mean())
+    if grad_corrected:
+        corrected[mask] = hot_subset + residual / p[mask].clamp_min(1e-12)
+    return corrected, torch.stack(stats)
+
+
+@pytest.mark.parametrize("clip,grad_corrected", [(None, True), (0.7, True), (0.7, False), (None, False)])
+def test_audit_oracle_matches_reference_formulation_and_autograd(clip, grad_corrected):
+    from oracle import audit as AU
+
+    rng = _rng(13)
+    B, S = 9, 7
+    hot = rng.normal(size=(B, S))
+    idx = np.array([7, 2, 4, 0])
+    exact = hot[idx] + rng.normal(size=(4, S)) * 0.4
+    p = rng.uniform(0.05, 1.0, B)
+    corr, _, st = AU.correction(hot, exact, idx, p, clip, grad_corrected)
+    th = torch.tensor(hot, requires_grad=True)
+    te = torch.tensor(exact, requires_grad=True)
+    tcorr, tst = _torch_reference_correction(th, te, torch.tensor(idx), torch.tensor(p), clip, grad_corrected)
+    np.testing.assert_allclose(corr, tcorr.detach().numpy(), rtol=1e-12)
+    np.testing.assert_allclose(st, tst.detach().numpy(), rtol=1e-12)
+    g = rng.normal(size=B)
+    tcorr.backward(torch.tensor(g))
+    dh, de = AU.correction_bwd(g, hot, exact, idx, p, clip, grad_corrected)
+    np.testing.assert_allclose(dh, th.grad.numpy(), rtol=1e-12)
+    np.testing.assert_allclose(de, te.grad.numpy() if te.grad is not None else np.zeros_like(de), rtol=1e-12)
+    if clip is not None:  # the case mixes clipped and unclipped rows
+        r = exact.sum(-1) - hot.sum(-1)[idx]
+        assert (np.abs(r) > clip).any() and (np.abs(r) <= clip).any()
+
+
 # ---------------------------------------------------------------- shortlist
 
 def _brute_first_distinct(row, L):
