@@ -183,6 +183,25 @@ int rte_ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* tar
 int rte_ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
                const float* dloss, const float* extra, void* dlogits, void* stream);
 
+/* ---- residual axpy + FiLM RMSNorm of a recursive pass (replaces the elementwise glue of
+ *      BankedRecursiveCore._step, rte/layers.py:826-845: h~ = h + alpha h0, rmsnorm * (1 + gamma)
+ *      + beta, u = h~ + s_attn attn, h' = u + s_mlp mlp, inactive samples keep h) ----
+ * fwd: x = a + c b (c: device fp32 scalar, NULL = 1; b optional); samples with mask[row / seq] == 0
+ *      (mask uint8 [T / seq], optional, needs keep) take keep's row; x_out f32 [T, d] optional;
+ *      n_out bf16 = x * rstd * w * (1 + gamma) + beta (gamma, beta optional), rstd f32 [T].
+ * bwd: g = dn (1 + gamma); dx = dx_ext + rstd w g - x rstd^3 mean(w g x) (dn, dx_ext optional);
+ *      da = active ? dx : 0; db = c da; dkeep = active ? 0 : dx (each output optional);
+ *      dparams f32 [3 d + 1] = (dw | dgamma | dbeta | dc), reduced in a fixed order.
+ * All arrays f32 [T, d] row-major, 16-byte aligned; d % 8 == 0, d <= 1024. */
+int rte_axpy_norm_fwd(const float* a, const float* b, const float* c, const float* keep, const uint8_t* mask,
+                      int seq, int T, int d, const float* w, const float* gamma, const float* beta, float eps,
+                      float* x_out, void* n_out, float* rstd_out, void* stream);
+size_t rte_axpy_norm_bwd_workspace_bytes(int T, int d);
+int rte_axpy_norm_bwd(const void* dn, const float* dx_ext, const float* x, const float* rstd, const float* w,
+                      const float* gamma, const float* b, const float* c, const uint8_t* mask, int seq, int T, int d,
+                      float* da, float* db, float* dkeep, float* dparams, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
 /* ---- control-variate audit correction (replaces AuditEngine.correction's loss arithmetic,
  *      rte/audit.py:296-321, over lm_loss_per_sample rte/models.py:73-75) ----
  * hot_tok f32 [B, seq] token losses of the hot (macro) pass; exact_tok f32 [A, seq] token losses

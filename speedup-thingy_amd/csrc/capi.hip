@@ -32,6 +32,13 @@ int ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets
            hipStream_t s);
 int ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse, const float* g,
            const float* extra, bf16* dlogits, hipStream_t s);
+int axpy_norm_fwd(const float* a, const float* b, const float* c, const float* keep, const uint8_t* mask, int S,
+                  int T, int d, const float* w, const float* gamma, const float* beta, float eps, float* x_out,
+                  bf16* n_out, float* rstd_out, hipStream_t s);
+size_t axpy_norm_bwd_workspace_bytes(int T, int d);
+int axpy_norm_bwd(const bf16* dn, const float* dx_ext, const float* x, const float* rstd, const float* w,
+                  const float* gamma, const float* b, const float* c, const uint8_t* mask, int S, int T, int d,
+                  float* da, float* db, float* dkeep, float* dparams, void* ws, size_t ws_bytes, hipStream_t s);
 int audit_fwd(const float* hot_tok, const float* exact_tok, int B, int S, const int64_t* idx, int A, const float* p,
               float clip, int grad_corrected, float* corrected, float* exact_ps, float* coef, float* stats,
               hipStream_t s);
@@ -718,6 +725,22 @@ int rte_ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* tar
 int rte_ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
                const float* dloss, const float* extra, void* dlogits, void* stream) {
   return ce_bwd(logits, ld, T, V, targets, lse, dloss, extra, B16(dlogits), S(stream));
+}
+
+int rte_axpy_norm_fwd(const float* a, const float* b, const float* c, const float* keep, const uint8_t* mask,
+                      int seq, int T, int d, const float* w, const float* gamma, const float* beta, float eps,
+                      float* x_out, void* n_out, float* rstd_out, void* stream) {
+  return axpy_norm_fwd(a, b, c, keep, mask, seq, T, d, w, gamma, beta, eps, x_out, B16(n_out), rstd_out, S(stream));
+}
+
+size_t rte_axpy_norm_bwd_workspace_bytes(int T, int d) { return axpy_norm_bwd_workspace_bytes(T, d); }
+
+int rte_axpy_norm_bwd(const void* dn, const float* dx_ext, const float* x, const float* rstd, const float* w,
+                      const float* gamma, const float* b, const float* c, const uint8_t* mask, int seq, int T, int d,
+                      float* da, float* db, float* dkeep, float* dparams, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+  return axpy_norm_bwd(reinterpret_cast<const bf16*>(dn), dx_ext, x, rstd, w, gamma, b, c, mask, seq, T, d, da, db,
+                       dkeep, dparams, workspace, workspace_bytes, S(stream));
 }
 
 int rte_audit_correct_fwd(const float* hot_tok, const float* exact_tok, int B, int seq, const int64_t* idx, int A,

@@ -19,6 +19,7 @@
 #include "gemm.hpp"
 
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <type_traits>
 
@@ -258,12 +259,53 @@ struct EpiFlags {
 // ------------------------------------------------------------------ kernel
 
 // Tiles larger than 128x128 keep one workgroup per CU (their LDS and accumulators fill it).
-template <int BM, int BN>
-constexpr int wg_per_cu() { return BM * BN > 128 * 128 ? 1 : 2; }
+template <int BM, int BN, int BK = 64, int DLS = 0>
+constexpr int wg_per_cu() {
+  if constexpr (DLS > 0) {
+    // direct-load kernels: as many workgroups as their LDS allows, at most 4
+    constexpr int lds = DLS * (BM + BN) * BK * 2 > (BM / 2) * (BN + 8) * 4 ? DLS * (BM + BN) * BK * 2
+                                                                          : (BM / 2) * (BN + 8) * 4;
+    constexpr int n = 163840 / lds;
+    return n < 1 ? 1 : (n > 4 ? 4 : n);
+  }
+  return BM * BN > 128 * 128 ? 1 : 2;
+}
 
-template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI, bool DUALA = false>
-__global__ void __launch_bounds__(256, (wg_per_cu<BM, BN>())) gemm_kernel(GemmArgs p, EpiFlags fl) {
+// Direct-to-LDS stage layout: a tile row holds BK k values = CPR chunks of 16 bytes, chunk c
+// stored at position c ^ swz(row), so that 32 lanes reading the same logical chunk of 32
+// consecutive rows (the MFMA operand reads) spread over all LDS banks.  Both swizzles were
+// chosen by measurement (SQ_LDS_BANK_CONFLICT of ds_read_b128 patterns on gfx950: zero
+// conflicts for these two, conflicts for the unswizzled rows and for (row & 7), (row >> 1) & 3).
+template <int CPR>
+__device__ __forceinline__ int dl_swz(int row) {
+  if constexpr (CPR == 8) return (row ^ (row >> 3)) & 7;  // 128-byte rows
+  else return (row >> 2) & 3;                             // 64-byte rows
+}
+
+// 16 bytes per lane from global memory straight into LDS at (LDS base + 16 * lane); the LDS
+// base must be wave-uniform.  The host pass of the compiler has no such builtin and never
+// runs kernel bodies, so it only sees the declaration.
+__device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
+#else
+  (void)src;
+  (void)lds_base;
+#endif
+}
+
+// s_waitcnt with vmcnt <= n and the other counters unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI, bool DUALA = false, int DLS = 0>
+__global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS>())) gemm_kernel(GemmArgs p, EpiFlags fl) {
   static_assert(!DUALA || (EPI == EPI_SWIGLU_FWD && !AT), "dual-A is a SwiGLU-forward layout-N mode");
+  static_assert(DLS == 0 || (!AT && !BT && !DUALA && (BK == 64 || BK == 32) && DLS >= 2 && DLS <= 4),
+                "direct-to-LDS loads: layout-N operands, BK 32 or 64, 2 to 4 stages");
   constexpr int LDP = BK + 8;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -363,77 +405,186 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN>())) gemm_kernel(GemmAr
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  Loader<BM, BK, AT> la;
-  Loader<BM, BK, AT> la2;  // DUALA: gate half of A
-  Loader<BN, BK, BT> lb;
-  la.init(p.a, abase, ashift, m0, mlim, tid);
-  if constexpr (DUALA) la2.init(p.a, abase, ashift, m0, mlim, tid);
-  lb.init(p.b, bbase, bshift, n0, p.N, tid);
-  const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
-  const int ko2 = p.a_koff2;
-
-  // Pipeline: tile t's payload sits in register set t % 2 and LDS buffer t % 2.  While tile t
-  // is multiplied out of LDS, tile t + 2 is being fetched into the set tile t came through
-  // and tile t + 1 (fetched one step earlier) is written to the other LDS buffer, so global
-  // latency is covered by two compute steps.
-  auto load_tile = [&](auto stage, int t) {
-    constexpr int S = decltype(stage)::value;
-    const int k0 = kbeg + t * BK;
-    la.template load<S>(p.a, abase, ashift, k0, kend, tid);
-    if constexpr (DUALA) la2.template load<S>(p.a, abase, ashift, k0 + ko2, kend + ko2, tid);
-    lb.template load<S>(p.b, bbase, bshift, k0, kend, tid);
-  };
-  auto store_tile = [&](auto stage) {
-    constexpr int S = decltype(stage)::value;
-    la.template store<S>(smem + S * A_STAGE, tid);
-    if constexpr (DUALA) la2.template store<S>(smem + S * A_STAGE + A_TILE, tid);
-    lb.template store<S>(smem + B_BASE + S * B_STAGE, tid);
-  };
-  auto compute = [&](auto stage) {
-    constexpr int S = decltype(stage)::value;
-    const bf16* a_s = smem + S * A_STAGE;
-    const bf16* b_s = smem + B_BASE + S * B_STAGE;
+  if constexpr (DLS > 0) {
+    // Global -> LDS without registers (global_load_lds_dwordx4): load u of thread tid fills
+    // 16-byte unit q = u * 256 + tid of the stage, i.e. row q / CPR at chunk position q % CPR,
+    // which holds logical chunk (q % CPR) ^ swz(row).  Rows past the tile's limit re-read the
+    // last valid row; their results are never stored.  The k range is a multiple of BK.
+    constexpr int CPR = BK / 8, ROWB = BK * 2;
+    constexpr int A_INS = BM * CPR / kThreads, B_INS = BN * CPR / kThreads;
+    constexpr int A_BYTES = BM * ROWB, STAGE = (BM + BN) * ROWB;
+    static_assert(A_INS >= 1 && B_INS >= 1, "tile too small for one load per thread");
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const bf16* ap[A_INS];
+    const bf16* bp[B_INS];
+    int ac[A_INS], bc[B_INS];
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8_v af[TM], ag[DUALA ? TM : 1], bfr[TN];
-      const int kof = ks * 16 + (lane >> 5) * 8;
-#pragma unroll
-      for (int i = 0; i < TM; ++i) {
-        af[i] = *reinterpret_cast<const bf16x8_v*>(a_s + (wm * WTM + i * 32 + (lane & 31)) * LDP + kof);
-        if constexpr (DUALA)
-          ag[i] = *reinterpret_cast<const bf16x8_v*>(a_s + A_TILE + (wm * WTM + i * 32 + (lane & 31)) * LDP + kof);
-      }
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bfr[j] = *reinterpret_cast<const bf16x8_v*>(b_s + (wn * WTN + j * 32 + (lane & 31)) * LDP + kof);
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          // DUALA: odd column blocks are gate blocks and take the second A code
-          const bf16x8_v& a_op = (DUALA && (j & 1)) ? ag[DUALA ? i : 0] : af[i];
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_op, bfr[j], acc[i][j], 0, 0, 0);
-        }
+    for (int u = 0; u < A_INS; ++u) {
+      const int q = u * kThreads + tid, row = q / CPR;
+      int i = m0 + row;
+      if (i >= mlim) i = mlim - 1;
+      ap[u] = abase + row_off(p.a, i + ashift);
+      ac[u] = ((q % CPR) ^ dl_swz<CPR>(row)) * 8;
     }
-  };
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
-  if (nk > 0) {
-    load_tile(S0{}, 0);
-    load_tile(S1{}, 1);
-    store_tile(S0{});
-  }
-  __syncthreads();
-  for (int kt = 0; kt < nk; kt += 2) {
-    load_tile(S0{}, kt + 2);
-    compute(S0{});
-    if (kt + 1 < nk) store_tile(S1{});
+#pragma unroll
+    for (int u = 0; u < B_INS; ++u) {
+      const int q = u * kThreads + tid, row = q / CPR;
+      int i = n0 + row;
+      if (i >= p.N) i = p.N - 1;
+      bp[u] = bbase + row_off(p.b, i + bshift);
+      bc[u] = ((q % CPR) ^ dl_swz<CPR>(row)) * 8;
+    }
+    const bool plain_cols = p.a.cdiv == 0 && p.b.cdiv == 0;  // uniform: k offsets are affine
+    auto issue = [&](int stage, int t) {
+      const int k0 = kbeg + t * BK;
+      unsigned char* dst = smem_raw + stage * STAGE + wv * 1024;
+      if (plain_cols) {
+#pragma unroll
+        for (int u = 0; u < A_INS; ++u)
+          lds_dma16(ap[u] + (k0 + ac[u]), dst + u * 4096);
+#pragma unroll
+        for (int u = 0; u < B_INS; ++u)
+          lds_dma16(bp[u] + (k0 + bc[u]), dst + A_BYTES + u * 4096);
+      } else {
+#pragma unroll
+        for (int u = 0; u < A_INS; ++u)
+          lds_dma16(ap[u] + col_off(p.a, k0 + ac[u]), dst + u * 4096);
+#pragma unroll
+        for (int u = 0; u < B_INS; ++u)
+          lds_dma16(bp[u] + col_off(p.b, k0 + bc[u]), dst + A_BYTES + u * 4096);
+      }
+    };
+    // operand rows of this lane and their swizzles
+    int aoff[TM], asw[TM], boff[TN], bsw[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm * WTM + i * 32 + (lane & 31);
+      aoff[i] = r * ROWB;
+      asw[i] = dl_swz<CPR>(r);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int r = wn * WTN + j * 32 + (lane & 31);
+      boff[j] = A_BYTES + r * ROWB;
+      bsw[j] = dl_swz<CPR>(r);
+    }
+    auto compute = [&](int stage) {
+      const unsigned char* st = smem_raw + stage * STAGE;
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        const int c = ks * 2 + (lane >> 5);
+        bf16x8_v af[TM], bfr[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const bf16x8_v*>(st + aoff[i] + ((c ^ asw[i]) << 4));
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bfr[j] = *reinterpret_cast<const bf16x8_v*>(st + boff[j] + ((c ^ bsw[j]) << 4));
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+      }
+    };
+    const int nk = (kend - kbeg) / BK;
+#pragma unroll
+    for (int t = 0; t < DLS - 1; ++t)
+      if (t < nk) issue(t, t);
+    int stage = 0;
+    for (int kt = 0; kt < nk; ++kt) {
+      // tile kt has landed once at most the (DLS - 2) younger tiles' loads are in flight
+      if constexpr (DLS == 4) {
+        if (kt + 2 < nk) wait_vmcnt<2 * (A_INS + B_INS)>();
+        else if (kt + 1 < nk) wait_vmcnt<A_INS + B_INS>();
+        else wait_vmcnt<0>();
+      } else if constexpr (DLS == 3) {
+        if (kt + 1 < nk) wait_vmcnt<A_INS + B_INS>(); else wait_vmcnt<0>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      __syncthreads();  // tile kt visible to all waves; every wave is done with tile kt - 1
+      if (kt + DLS - 1 < nk) {
+        int ns = stage + DLS - 1;
+        if (ns >= DLS) ns -= DLS;
+        issue(ns, kt + DLS - 1);
+      }
+      compute(stage);
+      stage = stage + 1 == DLS ? 0 : stage + 1;
+    }
+    __syncthreads();  // the epilogue reuses the stage buffers
+  } else {
+    Loader<BM, BK, AT> la;
+    Loader<BM, BK, AT> la2;  // DUALA: gate half of A
+    Loader<BN, BK, BT> lb;
+    la.init(p.a, abase, ashift, m0, mlim, tid);
+    if constexpr (DUALA) la2.init(p.a, abase, ashift, m0, mlim, tid);
+    lb.init(p.b, bbase, bshift, n0, p.N, tid);
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const int ko2 = p.a_koff2;
+
+    // Pipeline: tile t's payload sits in register set t % 2 and LDS buffer t % 2.  While tile t
+    // is multiplied out of LDS, tile t + 2 is being fetched into the set tile t came through
+    // and tile t + 1 (fetched one step earlier) is written to the other LDS buffer, so global
+    // latency is covered by two compute steps.
+    auto load_tile = [&](auto stage, int t) {
+      constexpr int S = decltype(stage)::value;
+      const int k0 = kbeg + t * BK;
+      la.template load<S>(p.a, abase, ashift, k0, kend, tid);
+      if constexpr (DUALA) la2.template load<S>(p.a, abase, ashift, k0 + ko2, kend + ko2, tid);
+      lb.template load<S>(p.b, bbase, bshift, k0, kend, tid);
+    };
+    auto store_tile = [&](auto stage) {
+      constexpr int S = decltype(stage)::value;
+      la.template store<S>(smem + S * A_STAGE, tid);
+      if constexpr (DUALA) la2.template store<S>(smem + S * A_STAGE + A_TILE, tid);
+      lb.template store<S>(smem + B_BASE + S * B_STAGE, tid);
+    };
+    auto compute = [&](auto stage) {
+      constexpr int S = decltype(stage)::value;
+      const bf16* a_s = smem + S * A_STAGE;
+      const bf16* b_s = smem + B_BASE + S * B_STAGE;
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        bf16x8_v af[TM], ag[DUALA ? TM : 1], bfr[TN];
+        const int kof = ks * 16 + (lane >> 5) * 8;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          af[i] = *reinterpret_cast<const bf16x8_v*>(a_s + (wm * WTM + i * 32 + (lane & 31)) * LDP + kof);
+          if constexpr (DUALA)
+            ag[i] = *reinterpret_cast<const bf16x8_v*>(a_s + A_TILE + (wm * WTM + i * 32 + (lane & 31)) * LDP + kof);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          bfr[j] = *reinterpret_cast<const bf16x8_v*>(b_s + (wn * WTN + j * 32 + (lane & 31)) * LDP + kof);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            // DUALA: odd column blocks are gate blocks and take the second A code
+            const bf16x8_v& a_op = (DUALA && (j & 1)) ? ag[DUALA ? i : 0] : af[i];
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a_op, bfr[j], acc[i][j], 0, 0, 0);
+          }
+      }
+    };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    if (nk > 0) {
+      load_tile(S0{}, 0);
+      load_tile(S1{}, 1);
+      store_tile(S0{});
+    }
     __syncthreads();
-    if (kt + 1 >= nk) break;
-    load_tile(S1{}, kt + 3);
-    compute(S1{});
-    if (kt + 2 < nk) store_tile(S0{});
-    __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+      load_tile(S0{}, kt + 2);
+      compute(S0{});
+      if (kt + 1 < nk) store_tile(S1{});
+      __syncthreads();
+      if (kt + 1 >= nk) break;
+      load_tile(S1{}, kt + 3);
+      compute(S1{});
+      if (kt + 2 < nk) store_tile(S0{});
+      __syncthreads();
+    }
+
   }
 
   // ---------------------------------------------------------------- epilogues (LDS staged)
@@ -442,55 +593,63 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN>())) gemm_kernel(GemmAr
   const int cbase = wn * WTN + (lane & 31);      // + j*32
 
   if constexpr (EPI == EPI_STORE) {
-    constexpr int CP = BN + 8;
+    // the direct-load kernels stage the tile in NH row slices so their LDS stays small
+    constexpr int CP = BN + 8, NH = DLS > 0 ? 2 : 1, HR = BM / NH;
+    static_assert(HR % WTM == 0, "a wave's rows lie in one slice");
     float* Cs = reinterpret_cast<float*>(smem_raw);
+    for (int h = 0; h < NH; ++h) {
+      if (h > 0) __syncthreads();  // the previous slice has been written out
+      if ((wm * WTM) / HR == h) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+          for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          Cs[(rbase + i * 32 + (r >> 2) * 8 + (r & 3)) * CP + cbase + j * 32] = acc[i][j][r];
-    __syncthreads();
-    if (partial_dst) {
-      // fp32 partial of this k range, plain [M, N]
-      float* ws = partial_dst;
-      constexpr int CH = BN / 4;
-      for (int c = tid; c < BM * CH; c += kThreads) {
-        const int row = c / CH, cc = (c % CH) * 4;
-        const int m = m0 + row, n = n0 + cc;
-        if (m >= mlim || n >= p.N) continue;
-        const float* src = Cs + row * CP + cc;
-        float* dst = ws + (int64_t)m * p.N + n;
-        if (fl.vec && n + 4 <= p.N) {
-          *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(src);
-        } else {
-          for (int t = 0; t < 4 && n + t < p.N; ++t) dst[t] = src[t];
+            for (int r = 0; r < 16; ++r)
+              Cs[(rbase - h * HR + i * 32 + (r >> 2) * 8 + (r & 3)) * CP + cbase + j * 32] = acc[i][j][r];
+      }
+      __syncthreads();
+      const int mh = m0 + h * HR;
+      if (partial_dst) {
+        // fp32 partial of this k range, plain [M, N]
+        float* ws = partial_dst;
+        constexpr int CH = BN / 4;
+        for (int c = tid; c < HR * CH; c += kThreads) {
+          const int row = c / CH, cc = (c % CH) * 4;
+          const int m = mh + row, n = n0 + cc;
+          if (m >= mlim || n >= p.N) continue;
+          const float* src = Cs + row * CP + cc;
+          float* dst = ws + (int64_t)m * p.N + n;
+          if (fl.vec && n + 4 <= p.N) {
+            *reinterpret_cast<float4*>(dst) = *reinterpret_cast<const float4*>(src);
+          } else {
+            for (int t = 0; t < 4 && n + t < p.N; ++t) dst[t] = src[t];
+          }
         }
-      }
-    } else if (e.c_f32) {
-      constexpr int CH = BN / 4;
-      for (int c = tid; c < BM * CH; c += kThreads) {
-        const int row = c / CH, cc = (c % CH) * 4;
-        const int m = m0 + row, n = n0 + cc;
-        if (m >= mlim || n >= p.N) continue;
-        float v[4];
-        const float4 x = *reinterpret_cast<const float4*>(Cs + row * CP + cc);
-        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-        store_chunk<4>(e, g, m, n, p.N, v, fl.vec);
-      }
-    } else {
-      constexpr int CH = BN / 8;
-      for (int c = tid; c < BM * CH; c += kThreads) {
-        const int row = c / CH, cc = (c % CH) * 8;
-        const int m = m0 + row, n = n0 + cc;
-        if (m >= mlim || n >= p.N) continue;
-        float v[8];
-        const float4 x = *reinterpret_cast<const float4*>(Cs + row * CP + cc);
-        const float4 y = *reinterpret_cast<const float4*>(Cs + row * CP + cc + 4);
-        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
-        v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
-        store_chunk<8>(e, g, m, n, p.N, v, fl.vec);
+      } else if (e.c_f32) {
+        constexpr int CH = BN / 4;
+        for (int c = tid; c < HR * CH; c += kThreads) {
+          const int row = c / CH, cc = (c % CH) * 4;
+          const int m = mh + row, n = n0 + cc;
+          if (m >= mlim || n >= p.N) continue;
+          float v[4];
+          const float4 x = *reinterpret_cast<const float4*>(Cs + row * CP + cc);
+          v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+          store_chunk<4>(e, g, m, n, p.N, v, fl.vec);
+        }
+      } else {
+        constexpr int CH = BN / 8;
+        for (int c = tid; c < HR * CH; c += kThreads) {
+          const int row = c / CH, cc = (c % CH) * 8;
+          const int m = mh + row, n = n0 + cc;
+          if (m >= mlim || n >= p.N) continue;
+          float v[8];
+          const float4 x = *reinterpret_cast<const float4*>(Cs + row * CP + cc);
+          const float4 y = *reinterpret_cast<const float4*>(Cs + row * CP + cc + 4);
+          v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+          v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+          store_chunk<8>(e, g, m, n, p.N, v, fl.vec);
+        }
       }
     }
   } else if constexpr (EPI == EPI_SWIGLU_FWD) {
@@ -599,49 +758,55 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN>())) gemm_kernel(GemmAr
     // Stage the fp32 tile, then each thread rotates and writes 8 consecutive columns of one
     // row: the RoPE pairs (2i, 2i+1) sit inside the chunk, and the chunk's cos / sin values
     // are two 16-byte loads each.
-    constexpr int CP = BN + 4;
+    constexpr int CP = BN + 4, NH = DLS > 0 ? 2 : 1, HR = BM / NH;
+    static_assert(HR % WTM == 0, "a wave's rows lie in one slice");
     float* Cs = reinterpret_cast<float*>(smem_raw);
+    for (int h = 0; h < NH; ++h) {
+      if (h > 0) __syncthreads();  // the previous slice has been written out
+      if ((wm * WTM) / HR == h) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j)
+          for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          Cs[(rbase + i * 32 + (r >> 2) * 8 + (r & 3)) * CP + cbase + j * 32] = acc[i][j][r];
-    __syncthreads();
-    constexpr int CH = BN / 8;
-    for (int c = tid; c < BM * CH; c += kThreads) {
-      const int row = c / CH, cc = (c % CH) * 8;
-      const int m = m0 + row, n = n0 + cc;
-      if (m >= mlim || n >= p.N) continue;
-      const float4 x0 = *reinterpret_cast<const float4*>(Cs + row * CP + cc);
-      const float4 x1 = *reinterpret_cast<const float4*>(Cs + row * CP + cc + 4);
-      float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-      const int part = n / e.dmodel;
-      const int within = n - part * e.dmodel;
-      const int h = within / e.hd, dim = within - h * e.hd;
-      const int b = m / e.S, s = m - b * e.S;
-      if (part < 2) {
-        const float* cp = e.cos_t + (int64_t)s * e.hd + dim;
-        const float* sp = e.sin_t + (int64_t)s * e.hd + dim;
-        const float4 c0 = *reinterpret_cast<const float4*>(cp), c1 = *reinterpret_cast<const float4*>(cp + 4);
-        const float4 s0 = *reinterpret_cast<const float4*>(sp), s1 = *reinterpret_cast<const float4*>(sp + 4);
-        const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-        const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          const float xe = v[2 * t], xo = v[2 * t + 1];
-          v[2 * t] = xe * cv[2 * t] - xo * sv[2 * t];
-          v[2 * t + 1] = xo * cv[2 * t + 1] + xe * sv[2 * t + 1];
-        }
+            for (int r = 0; r < 16; ++r)
+              Cs[(rbase - h * HR + i * 32 + (r >> 2) * 8 + (r & 3)) * CP + cbase + j * 32] = acc[i][j][r];
       }
-      uint4 o;
-      o.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
-      o.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-      o.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
-      o.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
-      bf16* dst = part == 0 ? e.q : (part == 1 ? e.k : e.v);
-      *reinterpret_cast<uint4*>(dst + (((int64_t)b * e.H + h) * e.S + s) * e.hd + dim) = o;
+      __syncthreads();
+      constexpr int CH = BN / 8;
+      for (int c = tid; c < HR * CH; c += kThreads) {
+        const int row = c / CH, cc = (c % CH) * 8;
+        const int m = m0 + h * HR + row, n = n0 + cc;
+        if (m >= mlim || n >= p.N) continue;
+        const float4 x0 = *reinterpret_cast<const float4*>(Cs + row * CP + cc);
+        const float4 x1 = *reinterpret_cast<const float4*>(Cs + row * CP + cc + 4);
+        float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const int part = n / e.dmodel;
+        const int within = n - part * e.dmodel;
+        const int hh = within / e.hd, dim = within - hh * e.hd;
+        const int b = m / e.S, s = m - b * e.S;
+        if (part < 2) {
+          const float* cp = e.cos_t + (int64_t)s * e.hd + dim;
+          const float* sp = e.sin_t + (int64_t)s * e.hd + dim;
+          const float4 c0 = *reinterpret_cast<const float4*>(cp), c1 = *reinterpret_cast<const float4*>(cp + 4);
+          const float4 s0 = *reinterpret_cast<const float4*>(sp), s1 = *reinterpret_cast<const float4*>(sp + 4);
+          const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+          const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const float xe = v[2 * t], xo = v[2 * t + 1];
+            v[2 * t] = xe * cv[2 * t] - xo * sv[2 * t];
+            v[2 * t + 1] = xo * cv[2 * t + 1] + xe * sv[2 * t + 1];
+          }
+        }
+        uint4 o;
+        o.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+        o.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+        o.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
+        o.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+        bf16* dst = part == 0 ? e.q : (part == 1 ? e.k : e.v);
+        *reinterpret_cast<uint4*>(dst + (((int64_t)b * e.H + hh) * e.S + s) * e.hd + dim) = o;
+      }
     }
   }
 }
@@ -722,20 +887,22 @@ int groupk_chunk(int K, int G) {
 
 size_t groupk_first_bytes(int G) { return (((size_t)(G + 1) * 4 + 255) / 256) * 256; }
 
-template <int BM, int BN, int BK, int EPI, bool DUALA = false>
+template <int BM, int BN, int BK, int EPI, bool DUALA = false, int DLS = 0>
 constexpr size_t lds_bytes() {
-  constexpr size_t main_loop = (size_t)2 * ((DUALA ? 2 : 1) * BM + BN) * (BK + 8) * 2;
-  constexpr size_t epi = EPI == EPI_STORE        ? (size_t)BM * (BN + 8) * 4
+  constexpr size_t main_loop = DLS > 0 ? (size_t)DLS * (BM + BN) * BK * 2
+                                       : (size_t)2 * ((DUALA ? 2 : 1) * BM + BN) * (BK + 8) * 2;
+  constexpr size_t rows = DLS > 0 ? BM / 2 : BM;  // direct-load kernels stage the output in two slices
+  constexpr size_t epi = EPI == EPI_STORE        ? rows * (BN + 8) * 4
                          : EPI == EPI_SWIGLU_FWD ? (size_t)BM * (BN + 8) * 2 + (size_t)BM * (BN / 2 + 8) * 2
                          : EPI == EPI_SWIGLU_BWD ? (size_t)BM * (2 * BN + 8) * 2
-                                                 : (size_t)BM * (BN + 4) * 4;  // EPI_ROPE_QKV: fp32 tile
+                                                 : rows * (BN + 4) * 4;  // EPI_ROPE_QKV: fp32 tile
   return main_loop > epi ? main_loop : epi;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI, bool DUALA = false>
+template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI, bool DUALA = false, int DLS = 0>
 int launch_cfg(const GemmArgs& p0, hipStream_t stream, void* ws, size_t ws_bytes, int vec) {
-  constexpr size_t lds = lds_bytes<BM, BN, BK, EPI, DUALA>();
-  auto fn = gemm_kernel<BM, BN, BK, WM, WN, AT, BT, EPI, DUALA>;
+  constexpr size_t lds = lds_bytes<BM, BN, BK, EPI, DUALA, DLS>();
+  auto fn = gemm_kernel<BM, BN, BK, WM, WN, AT, BT, EPI, DUALA, DLS>;
   static bool attr_done = false;
   if (!attr_done) {
     if (lds > 65536) {
@@ -814,6 +981,46 @@ int launch_layouts(const GemmArgs& p, hipStream_t stream, void* ws, size_t ws_by
   return launch_cfg<BM, BN, BK, WM, WN, true, true, EPI>(p, stream, ws, ws_bytes, vec);
 }
 
+// Direct-to-LDS mainloop selection.  Default: K <= 1024 -> BK 32, 2 stages (four workgroups
+// per CU: short reductions are latency-bound, occupancy hides it best); longer K -> BK 64,
+// 2 stages (fewer barriers per MFMA).  RTE_GEMM_DL overrides it for diagnostics: 0 keeps the
+// register-staged loop everywhere; otherwise 128x128 tiles with (BK, stages) = 2: (64, 2),
+// 3: (64, 3), 5: (32, 4), 6: (32, 3), 7: (32, 2); 4 = 256x128 tiles, (64, 2).
+int dl_env() {
+  static int mode = [] {
+    const char* v = getenv("RTE_GEMM_DL");
+    if (!v || !*v) return -1;
+    const int m = atoi(v);
+    return (m == 0 || (m >= 2 && m <= 7)) ? m : -1;
+  }();
+  return mode;
+}
+
+int dl_mode(const GemmArgs& p) {
+  const int env = dl_env();
+  if (env >= 0) return env;
+  const int klen = p.splits > 1 ? p.k_chunk : p.K;
+  return klen <= 1024 ? 7 : 2;
+}
+
+bool dl_ok(const GemmArgs& p) {
+  const int mode = dl_mode(p);
+  const int bk = mode >= 5 ? 32 : 64;
+  return mode != 0 && !p.a_t && !p.b_t && p.mode != MODE_GROUP_K && p.K % bk == 0 && p.K > 0 && !p.a_koff2;
+}
+
+template <int EPI>
+int launch_dl(const GemmArgs& p, hipStream_t stream, void* ws, size_t ws_bytes, int vec) {
+  switch (dl_mode(p)) {
+    case 3: return launch_cfg<128, 128, 64, 2, 2, false, false, EPI, false, 3>(p, stream, ws, ws_bytes, vec);
+    case 4: return launch_cfg<256, 128, 64, 2, 2, false, false, EPI, false, 2>(p, stream, ws, ws_bytes, vec);
+    case 5: return launch_cfg<128, 128, 32, 2, 2, false, false, EPI, false, 4>(p, stream, ws, ws_bytes, vec);
+    case 6: return launch_cfg<128, 128, 32, 2, 2, false, false, EPI, false, 3>(p, stream, ws, ws_bytes, vec);
+    case 7: return launch_cfg<128, 128, 32, 2, 2, false, false, EPI, false, 2>(p, stream, ws, ws_bytes, vec);
+    default: return launch_cfg<128, 128, 64, 2, 2, false, false, EPI, false, 2>(p, stream, ws, ws_bytes, vec);
+  }
+}
+
 bool pow2_or_zero(int v) { return v == 0 || (v > 0 && (v & (v - 1)) == 0); }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -879,6 +1086,7 @@ int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream, void* ws, s
       if (p.N <= 64) return launch_layouts<128, 64, 64, 4, 1, EPI_STORE>(p, stream, ws, ws_bytes, vec);
       if (p.K <= 32 && p.mode != MODE_GROUP_K)
         return launch_layouts<128, 128, 32, 2, 2, EPI_STORE>(p, stream, ws, ws_bytes, vec);
+      if (dl_ok(p)) return launch_dl<EPI_STORE>(p, stream, ws, ws_bytes, vec);
       return launch_layouts<128, 128, 64, 2, 2, EPI_STORE>(p, stream, ws, ws_bytes, vec);
     case EPI_SWIGLU_FWD:
       RTE_REQUIRE(!p.a_t && !p.b_t, "gemm: SwiGLU forward expects layout-N operands");
@@ -909,6 +1117,7 @@ int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream, void* ws, s
       RTE_REQUIRE(!p.a_t && !p.b_t, "gemm: QKV epilogue expects layout-N operands");
       RTE_REQUIRE(p.epi.q && p.epi.k && p.epi.v && p.epi.cos_t && p.epi.sin_t, "gemm: QKV outputs");
       RTE_REQUIRE(p.epi.hd % 2 == 0 && p.epi.dmodel * 3 == p.N, "gemm: QKV shape");
+      if (dl_ok(p)) return launch_dl<EPI_ROPE_QKV>(p, stream, ws, ws_bytes, 1);
       return launch_cfg<128, 128, 64, 2, 2, false, false, EPI_ROPE_QKV>(p, stream, ws, ws_bytes, 1);
     default:
       set_error("gemm: unknown epilogue %d", epi_kind);

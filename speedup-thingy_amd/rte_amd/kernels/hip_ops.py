@@ -153,6 +153,75 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5) -> torch.Tensor
     return RMSNormFn.apply(x, w, eps)
 
 
+class AxpyNormFn(torch.autograd.Function):
+    """x = a + c * b (c a scalar tensor, None = 1; b optional; samples whose mask is False keep
+    their `keep` rows) and, when w is given, n = bf16(rmsnorm(x) * w * (1 + gamma) + beta), in
+    one launch; the backward is one row kernel plus a fixed-order column sum that yields the
+    gradients of w, gamma, beta and c together (rte/layers.py:826-845)."""
+
+    @staticmethod
+    def forward(ctx, a, b, c, keep, mask, w, gamma, beta, eps):
+        _lib.require_device_tensors("axpy_norm", a, b, c, keep, mask, w, gamma, beta)
+        shape = a.shape
+        d = shape[-1]
+        T = a.numel() // d
+        S = 1
+        if mask is not None:
+            if keep is None or mask.numel() == 0 or T % mask.numel() != 0:
+                raise ValueError(f"axpy_norm: a mask of {mask.numel()} samples needs keep rows and divides {T} rows")
+            S = T // mask.numel()
+        a2 = a.reshape(T, d).contiguous().to(F32)
+        b2 = None if b is None else b.reshape(T, d).contiguous().to(F32)
+        k2 = None if keep is None else keep.reshape(T, d).contiguous().to(F32)
+        m = None if mask is None else mask.reshape(-1).contiguous().to(torch.bool)
+        cc = None if c is None else c.reshape(()).contiguous().to(F32)
+        vecs = [None if v is None else v.reshape(d).contiguous().to(F32) for v in (w, gamma, beta)]
+        dev = a.device
+        x = torch.empty((T, d), dtype=F32, device=dev)
+        n = torch.empty((T, d) if w is not None else (0,), dtype=BF16, device=dev)
+        rstd = torch.empty((T,) if w is not None else (0,), dtype=F32, device=dev)
+        call("rte_axpy_norm_fwd", ptr(a2), ptr(b2), ptr(cc), ptr(k2), ptr(m), S, T, d, ptr(vecs[0]), ptr(vecs[1]),
+             ptr(vecs[2]), float(eps), ptr(x), ptr(n) if w is not None else None,
+             ptr(rstd) if w is not None else None, _s())
+        ctx.save_for_backward(x, rstd, vecs[0], vecs[1], b2, cc, m)
+        ctx.meta = (shape, T, d, S, w is not None, c.shape if c is not None else None)
+        if w is None:
+            ctx.mark_non_differentiable(n)
+        return x.view(shape), (n.view(shape) if w is not None else n)
+
+    @staticmethod
+    def backward(ctx, dx_ext, dn):
+        x, rstd, w, gamma, b2, cc, m = ctx.saved_tensors
+        shape, T, d, S, has_norm, c_shape = ctx.meta
+        dev = x.device
+        dxe = None if dx_ext is None else dx_ext.reshape(T, d).contiguous().to(F32)
+        dnb = None if (dn is None or not has_norm) else dn.reshape(T, d).contiguous().to(BF16)
+        nia = ctx.needs_input_grad
+        da = torch.empty((T, d), dtype=F32, device=dev) if nia[0] else None
+        db = torch.empty((T, d), dtype=F32, device=dev) if nia[1] else None
+        dk = torch.empty((T, d), dtype=F32, device=dev) if nia[3] else None
+        dparams = torch.empty((3 * d + 1,), dtype=F32, device=dev)
+        ws, nb = workspace(_lib.load().rte_axpy_norm_bwd_workspace_bytes(T, d), dev)
+        call("rte_axpy_norm_bwd", ptr(dnb), ptr(dxe), ptr(x) if has_norm else None,
+             ptr(rstd) if has_norm else None, ptr(w), ptr(gamma), ptr(b2), ptr(cc), ptr(m), S, T, d, ptr(da),
+             ptr(db), ptr(dk), ptr(dparams), ws, nb, _s())
+        dc = dparams[3 * d].reshape(c_shape) if (nia[2] and c_shape is not None) else None
+        return (None if da is None else da.view(shape), None if db is None else db.view(shape), dc,
+                None if dk is None else dk.view(shape), None,
+                dparams[:d] if nia[5] else None, dparams[d:2 * d] if nia[6] else None,
+                dparams[2 * d:3 * d] if nia[7] else None, None)
+
+
+def axpy_norm(a, b, c, w, gamma=None, beta=None, eps: float = 1e-5, *, keep=None, mask=None):
+    """(x, n): x = a + c b (fp32), n = bf16(rmsnorm(x) w (1 + gamma) + beta)."""
+    return AxpyNormFn.apply(a, b, c, keep, mask, w, gamma, beta, eps)
+
+
+def axpy(a, b, c, *, keep=None, mask=None):
+    """x = a + c b (fp32); with mask [B], samples whose mask is False take keep's rows."""
+    return AxpyNormFn.apply(a, b, c, keep, mask, None, None, None, 0.0)[0]
+
+
 # ----------------------------------------------------------------------------- fused QKV + RoPE
 
 class QKVRopeFn(torch.autograd.Function):

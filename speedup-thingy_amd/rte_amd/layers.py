@@ -312,15 +312,26 @@ class BankedRecursiveCore(nn.Module):
             self.register_parameter("alpha_inj", None)
 
     def prepare(self):
-        """Per-forward weight layouts shared by every recursive pass."""
-        return self.mlp.pool_weights()
+        """Per-forward views shared by every recursive pass: the pool weight layouts and the
+        per-pass FiLM / scale parameters split once (one gradient stack per parameter in the
+        backward instead of a zero-fill and copy per pass)."""
+        per_pass = tuple(p.unbind(0) for p in (self.pass_gamma1, self.pass_beta1, self.pass_gamma2,
+                                                self.pass_beta2, self.pass_attn_scale, self.pass_mlp_scale))
+        return {"pool": self.mlp.pool_weights(), "pass": per_pass}
 
-    def _step(self, h, h0, head_scale, ids, w, pass_idx: int, weights=None):
-        h_tilde = h if self.alpha_inj is None else h + self.alpha_inj * h0
-        n1 = self.norm1(h_tilde) * (1.0 + self.pass_gamma1[pass_idx]) + self.pass_beta1[pass_idx]
-        u = h_tilde + self.pass_attn_scale[pass_idx] * self.attn.forward_scaled(n1, head_scale)
-        n2 = self.norm2(u) * (1.0 + self.pass_gamma2[pass_idx]) + self.pass_beta2[pass_idx]
-        return u + self.pass_mlp_scale[pass_idx] * self.mlp.forward_routes(n2, ids, w, weights)
+    def _step(self, h, h0, head_scale, ids, w, pass_idx: int, weights=None, active=None):
+        """One pass: three fused residual / FiLM-norm launches around attention and the pool
+        FFN; samples whose `active` entry is False keep h."""
+        if weights is None:
+            weights = self.prepare()
+        g1, b1, g2, b2, sa, sm = (p[pass_idx] for p in weights["pass"])
+        h = h.float()
+        h_tilde, n1 = hip_ops.axpy_norm(h, None if self.alpha_inj is None else h0.float(), self.alpha_inj,
+                                        self.norm1.weight, g1, b1, self.norm1.eps)
+        attn = self.attn.forward_scaled(n1, head_scale)
+        u, n2 = hip_ops.axpy_norm(h_tilde, attn, sa, self.norm2.weight, g2, b2, self.norm2.eps)
+        mlp = self.mlp.forward_routes(n2, ids, w, weights["pool"])
+        return hip_ops.axpy(u, mlp, sm, keep=h if active is not None else None, mask=active)
 
     def step_group(self, h, h0, spec: RecipeSpec, pass_idx: int = 0):
         """One pass of a single recipe over every sample of h (rte/layers.py:826-845)."""
@@ -339,7 +350,4 @@ class BankedRecursiveCore(nn.Module):
         rid = recipe_ids.long()
         head_scale = self.attn.recipe_head_scale[rid]
         ids, w = self.mlp.routes_for(rid, S, active_mask)
-        out = self._step(h, h0, head_scale, ids, w, pass_idx, weights).to(h.dtype)
-        if active_mask is None:
-            return out
-        return torch.where(active_mask[:, None, None], out, h)
+        return self._step(h, h0, head_scale, ids, w, pass_idx, weights, active_mask).to(h.dtype)

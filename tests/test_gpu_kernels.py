@@ -63,6 +63,24 @@ def test_gemm_layouts_fp32_out(a_t, b_t, M, N, K):
     assert_rel(_np(c), ref, FP32_RTOL, "gemm fp32")
 
 
+@pytest.mark.parametrize("M,N,K", [(129, 129, 64), (300, 200, 128), (1000, 520, 192), (2048, 1536, 512),
+                                   (4100, 260, 1024), (700, 300, 2112)])
+def test_gemm_layout_nn_k64_shapes(M, N, K):
+    """Both operands k-contiguous with K a multiple of 64 (the direct-to-LDS main loop):
+    ragged tile edges in M and N, one to sixteen k tiles, bf16 and fp32 outputs."""
+    H = _ops()
+    rng = np.random.default_rng(M + 3 * N + K)
+    A_ = bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    B_ = bf16_round(rng.standard_normal((N, K)).astype(np.float32))
+    ref = A_.astype(np.float64) @ B_.astype(np.float64).T
+    print(f"gemm nn M={M} N={N} K={K}", flush=True)
+    c = H.gemm(_bf(A_), _bf(B_), out_f32=True)
+    torch.cuda.synchronize()
+    assert_rel(_np(c), ref, FP32_RTOL, "gemm nn fp32")
+    cb = H.gemm(_bf(A_), _bf(B_))
+    assert_rel(_np(cb), ref, 5e-3, "gemm nn bf16")
+
+
 def test_gemm_bf16_out_resid_alpha():
     H = _ops()
     rng = np.random.default_rng(3)
@@ -621,3 +639,70 @@ def test_audit_correct_matches_oracle(B, S, A, clip, grad_corrected):
     corr2, _, st2 = ops.audit_correct(th.detach(), te.detach(), torch.from_numpy(idx).to(DEV),
                                       torch.from_numpy(p).to(DEV), clip=clip, grad_corrected=grad_corrected)
     assert torch.equal(corr.detach(), corr2) and torch.equal(st, st2)
+
+
+# ---------------------------------------------------------------- residual axpy + FiLM norm
+
+def _torch_axpy_norm(a, b, c, keep, mask, w, gamma, beta, eps, S):
+    """The recursive pass's glue in plain float64 torch (rte/layers.py:826-845)."""
+    x = a if b is None else a + (1.0 if c is None else c) * b
+    if mask is not None:
+        act = mask.repeat_interleave(S)[:, None]
+        x = torch.where(act, x, keep)
+    if w is None:
+        return x, None
+    n = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps) * w
+    if gamma is not None:
+        n = n * (1.0 + gamma)
+    if beta is not None:
+        n = n + beta
+    return x, n
+
+
+@pytest.mark.parametrize("B,S,d,norm,use_mask", [(2, 64, 512, True, False), (3, 17, 1024, True, True),
+                                                 (4, 8, 64, False, True), (1, 64, 512, True, False)])
+def test_axpy_norm_matches_float64(B, S, d, norm, use_mask):
+    H = _ops()
+    rng = np.random.default_rng(B * 100 + S + d)
+    T = B * S
+    f64 = torch.float64
+
+    def t(x, grad=True):
+        return torch.tensor(x, dtype=f64, requires_grad=grad)
+
+    a_, b_, k_ = (rng.standard_normal((T, d)) for _ in range(3))
+    c_ = np.array(rng.uniform(0.5, 1.5))
+    w_, g_, be_ = rng.uniform(0.5, 1.5, d), rng.standard_normal(d) * 0.1, rng.standard_normal(d) * 0.1
+    mask_ = rng.random(B) < 0.6 if use_mask else None
+    # reference in float64
+    ra, rb, rk, rc, rw, rg, rbe = t(a_), t(b_), t(k_), t(c_), t(w_), t(g_), t(be_)
+    rm = None if mask_ is None else torch.tensor(mask_)
+    rx, rn = _torch_axpy_norm(ra, rb, rc, rk if use_mask else None, rm, rw if norm else None, rg if norm else None,
+                              rbe if norm else None, 1e-5, S)
+    dx_ = rng.standard_normal((T, d))
+    dn_ = bf16_round(rng.standard_normal((T, d)).astype(np.float32)).astype(np.float64)
+    loss = (rx * t(dx_, False)).sum() + ((rn * t(dn_, False)).sum() if norm else 0.0)
+    loss.backward()
+    # device
+    dev = lambda x: torch.tensor(x, dtype=torch.float32, device=DEV, requires_grad=True)  # noqa: E731
+    da, db, dk, dc = dev(a_), dev(b_), dev(k_), dev(c_)
+    dw, dg, dbe = dev(w_), dev(g_), dev(be_)
+    dm = None if mask_ is None else torch.tensor(mask_, device=DEV)
+    print(f"axpy_norm B={B} S={S} d={d} norm={norm} mask={use_mask}", flush=True)
+    if norm:
+        x, n = H.axpy_norm(da, db, dc, dw, dg, dbe, 1e-5, keep=dk if use_mask else None, mask=dm)
+        assert_rel(_np(x), rx.detach().numpy(), FP32_RTOL, "x")
+        assert_rel(_np(n), rn.detach().numpy(), 8e-3, "n (bf16)")
+        ((x * torch.tensor(dx_, dtype=torch.float32, device=DEV)).sum()
+         + (n.float() * torch.tensor(dn_, dtype=torch.float32, device=DEV)).sum()).backward()
+        for got, ref, name in ((dw, rw, "dw"), (dg, rg, "dgamma"), (dbe, rbe, "dbeta")):
+            assert_rel(_np(got.grad), ref.grad.numpy(), FP32_RTOL, name)
+    else:
+        x = H.axpy(da, db, dc, keep=dk if use_mask else None, mask=dm)
+        assert_rel(_np(x), rx.detach().numpy(), FP32_RTOL, "x")
+        (x * torch.tensor(dx_, dtype=torch.float32, device=DEV)).sum().backward()
+    assert_rel(_np(da.grad), ra.grad.numpy(), FP32_RTOL, "da")
+    assert_rel(_np(db.grad), rb.grad.numpy(), FP32_RTOL, "db")
+    assert_rel(_np(dc.grad), rc.grad.numpy(), FP32_RTOL, "dc")
+    if use_mask:
+        assert_rel(_np(dk.grad), rk.grad.numpy(), FP32_RTOL, "dkeep")
