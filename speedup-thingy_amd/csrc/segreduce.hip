@@ -2,7 +2,8 @@
 // rte/kernels/cluster_pool_ffn.py:218-241 and of every index/gather backward):
 //   out[v] (+)= sum over pairs p with keys[p] = v of w[p] * rows[p / row_div]
 // The pairs are counting-sorted by key (stable: ascending p), each key's run is summed in
-// 256-pair chunks by one wave, and chunk partials are added in chunk order.  No
+// 256-pair chunks by one wave, and chunk partials are added in chunk order; up to 4096 pairs
+// over up to 1024 keys take a one-launch path (per-key pair lists, summed in ascending p).  No
 // floating-point atomics: the result is bitwise repeatable for a given input.
 #include "common.hpp"
 
@@ -277,6 +278,56 @@ SegCarve carve(void* base, int64_t P, int V, int d) {
   return c;
 }
 
+// Few pairs (P <= kSmallPairs) and few keys: one workgroup per key lists its pairs in
+// ascending order (ballot compaction into LDS), then each thread sums 8 columns over the list
+// in that order.  One launch instead of the sort pipeline; still deterministic.
+constexpr int kSmallPairs = 4096;
+constexpr int kSmallKeys = 1024;
+
+template <typename RowT>
+__global__ void __launch_bounds__(256) segsum_small_kernel(const int32_t* __restrict__ keys, int P, int row_div,
+                                                           const float* __restrict__ w,
+                                                           const RowT* __restrict__ rows, int d,
+                                                           float* __restrict__ out, int accumulate) {
+  __shared__ int32_t list[kSmallPairs];
+  __shared__ int32_t wcnt[4];
+  const int v = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int n = 0;
+  for (int base = 0; base < P; base += 256) {
+    const int p = base + tid;
+    const bool hit = p < P && keys[p] == v;
+    const unsigned long long m = __ballot(hit);
+    if (lane == 0) wcnt[wave] = __popcll(m);
+    __syncthreads();
+    int off = n;
+    for (int q = 0; q < wave; ++q) off += wcnt[q];
+    if (hit) list[off + __popcll(m & ((1ull << lane) - 1ull))] = p;
+    n += ((wcnt[0] + wcnt[1]) + wcnt[2]) + wcnt[3];
+    __syncthreads();
+  }
+  for (int col = tid * 8; col < d; col += 256 * 8) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int i = 0; i < n; ++i) {
+      const int p = list[i];
+      const float wp = w ? w[p] : 1.0f;
+      float r[8];
+      load8(rows + (int64_t)(p / row_div) * d + col, r);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[t] += wp * r[t];
+    }
+    float* o = out + (int64_t)v * d + col;
+    if (accumulate) {
+      float prev[8];
+      load8(o, prev);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[t] += prev[t];
+    }
+    *reinterpret_cast<float4*>(o) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *reinterpret_cast<float4*>(o + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  }
+}
+
 template <typename RowT>
 int launch_segsum(int nc2, dim3 grid, hipStream_t s, const SegCarve& c, int V, const RowT* rows, int d, float* out,
                   int accumulate) {
@@ -313,6 +364,15 @@ int segreduce_rows(const int32_t* keys, int64_t P, int V, int row_div, const flo
     return 0;
   }
   const int Pi = (int)P;
+  if (Pi <= kSmallPairs && V <= kSmallKeys) {
+    if (rows_f32)
+      hipLaunchKernelGGL(segsum_small_kernel<float>, dim3(V), dim3(256), 0, s, keys, Pi, row_div, w,
+                         static_cast<const float*>(rows), d, out, accumulate);
+    else
+      hipLaunchKernelGGL(segsum_small_kernel<bf16>, dim3(V), dim3(256), 0, s, keys, Pi, row_div, w,
+                         static_cast<const bf16*>(rows), d, out, accumulate);
+    return check_launch("segment_reduce_small");
+  }
   const int nblk = (Pi + kSortChunk - 1) / kSortChunk;
   const dim3 block(256);
   const size_t lds_hist = (size_t)V * sizeof(int32_t);

@@ -524,7 +524,10 @@ def test_shortlist_head_matches_oracle():
 # ---------------------------------------------------------------- segmented row reduction
 
 @pytest.mark.parametrize("P,V,d,div,f32", [(5000, 300, 128, 1, True), (20000, 64, 512, 4, False),
-                                         (70000, 2048, 64, 1, True), (3, 10, 8, 1, False), (0, 16, 32, 1, True)])
+                                         (70000, 2048, 64, 1, True), (3, 10, 8, 1, False), (0, 16, 32, 1, True),
+                                         # one-launch path: few pairs over few keys
+                                         (128, 16, 512, 1, True), (4096, 1024, 2048, 2, True),
+                                         (4000, 7, 264, 1, False)])
 def test_segment_reduce_rows(P, V, d, div, f32):
     H = _ops()
     rng = np.random.default_rng(P + V)
