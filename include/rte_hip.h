@@ -202,6 +202,26 @@ int rte_axpy_norm_bwd(const void* dn, const float* dx_ext, const float* x, const
                       float* da, float* db, float* dkeep, float* dparams, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/* ---- hot-vs-exact distillation losses + alignment metrics of the audit (replaces
+ *      macro_distill_loss rte/macro.py:394-471 and macro_alignment_metrics :499-546 on the
+ *      path with the residual origin h0; rte/audit.py:326-352 calls both) ----
+ * hot, exact, h0 f32 [A, seq, d]; hot_logits / exact_logits f32 [A, seq, V] (both optional).
+ * fwd: losses f32 [6] = delta_dir, delta_rms, endpoint_normed, endpoint_raw, rms_trust,
+ *      kl (temperature t, batchmean over A, times t^2; 0 without logits);
+ *      metrics f32 [10] = hidden_cosine, hidden_mse, macro_norm, exact_norm, macro_exact_norm_ratio,
+ *      delta_cosine, delta_rms_exact, delta_rms_pred, delta_rms_ratio, logit_kl (t = 1).
+ *      The workspace (rte_distill_workspace_bytes(A, rows = A * seq or 0)) keeps the per-sample
+ *      sums and logit lse's for the backward: keep it untouched until then.
+ * bwd: dhot f32 [A, seq, d] and dhot_logits f32 [A, seq, V] (each optional) for dlosses [6]. */
+size_t rte_distill_workspace_bytes(int A, int rows);
+int rte_distill_fwd(const float* hot, const float* exact, const float* h0, int A, int seq, int d,
+                    const float* hot_logits, const float* exact_logits, int V, float temperature, float eps,
+                    float* losses, float* metrics, void* workspace, size_t workspace_bytes, void* stream);
+int rte_distill_bwd(const float* hot, const float* exact, const float* h0, int A, int seq, int d,
+                    const float* hot_logits, const float* exact_logits, int V, float temperature, float eps,
+                    const float* dlosses, const void* workspace, size_t workspace_bytes, float* dhot,
+                    float* dhot_logits, void* stream);
+
 /* ---- control-variate audit correction (replaces AuditEngine.correction's loss arithmetic,
  *      rte/audit.py:296-321, over lm_loss_per_sample rte/models.py:73-75) ----
  * hot_tok f32 [B, seq] token losses of the hot (macro) pass; exact_tok f32 [A, seq] token losses

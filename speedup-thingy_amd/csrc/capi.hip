@@ -39,6 +39,13 @@ size_t axpy_norm_bwd_workspace_bytes(int T, int d);
 int axpy_norm_bwd(const bf16* dn, const float* dx_ext, const float* x, const float* rstd, const float* w,
                   const float* gamma, const float* b, const float* c, const uint8_t* mask, int S, int T, int d,
                   float* da, float* db, float* dkeep, float* dparams, void* ws, size_t ws_bytes, hipStream_t s);
+size_t distill_workspace_bytes(int A, int R);
+int distill_fwd(const float* hot, const float* exact, const float* h0, int A, int S, int d, const float* hot_logits,
+                const float* exact_logits, int V, float t, float eps, float* losses, float* metrics, void* ws,
+                size_t ws_bytes, hipStream_t s);
+int distill_bwd(const float* hot, const float* exact, const float* h0, int A, int S, int d, const float* hot_logits,
+                const float* exact_logits, int V, float t, float eps, const float* g, const void* ws,
+                size_t ws_bytes, float* dhot, float* dhot_logits, hipStream_t s);
 int audit_fwd(const float* hot_tok, const float* exact_tok, int B, int S, const int64_t* idx, int A, const float* p,
               float clip, int grad_corrected, float* corrected, float* exact_ps, float* coef, float* stats,
               hipStream_t s);
@@ -741,6 +748,23 @@ int rte_axpy_norm_bwd(const void* dn, const float* dx_ext, const float* x, const
                       void* stream) {
   return axpy_norm_bwd(reinterpret_cast<const bf16*>(dn), dx_ext, x, rstd, w, gamma, b, c, mask, seq, T, d, da, db,
                        dkeep, dparams, workspace, workspace_bytes, S(stream));
+}
+
+size_t rte_distill_workspace_bytes(int A, int rows) { return distill_workspace_bytes(A, rows); }
+
+int rte_distill_fwd(const float* hot, const float* exact, const float* h0, int A, int seq, int d,
+                    const float* hot_logits, const float* exact_logits, int V, float temperature, float eps,
+                    float* losses, float* metrics, void* workspace, size_t workspace_bytes, void* stream) {
+  return distill_fwd(hot, exact, h0, A, seq, d, hot_logits, exact_logits, V, temperature, eps, losses, metrics,
+                     workspace, workspace_bytes, S(stream));
+}
+
+int rte_distill_bwd(const float* hot, const float* exact, const float* h0, int A, int seq, int d,
+                    const float* hot_logits, const float* exact_logits, int V, float temperature, float eps,
+                    const float* dlosses, const void* workspace, size_t workspace_bytes, float* dhot,
+                    float* dhot_logits, void* stream) {
+  return distill_bwd(hot, exact, h0, A, seq, d, hot_logits, exact_logits, V, temperature, eps, dlosses, workspace,
+                     workspace_bytes, dhot, dhot_logits, S(stream));
 }
 
 int rte_audit_correct_fwd(const float* hot_tok, const float* exact_tok, int B, int seq, const int64_t* idx, int A,

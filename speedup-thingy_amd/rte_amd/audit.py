@@ -236,17 +236,35 @@ class AuditEngine:
             h0_sub = hot.meta.h0.index_select(0, idx)
             hot_logits = hot.meta.logits.index_select(0, idx) if hot.meta.logits is not None else None
             tr = self.config
-            aux.update(macro_distill_loss(
-                hot_end, exact.meta.recurrent_hidden, hot_logits, exact.meta.logits, h0=h0_sub,
-                lambda_hid=tr.effective_lambda_hid, lambda_cos=tr.effective_lambda_cos, lambda_kl=tr.effective_lambda_kl,
-                lambda_norm=tr.lambda_norm, lambda_delta_dir=tr.lambda_delta_dir, lambda_delta_rms=tr.lambda_delta_rms,
-                lambda_endpoint_normed=tr.lambda_endpoint_normed, lambda_endpoint_raw=tr.lambda_endpoint_raw,
-                lambda_macro_rms_trust=tr.lambda_macro_rms_trust if tr.macro_rms_trust_region else 0.0,
-                temperature=tr.distill_temperature,
-            ))
-            align = macro_alignment_metrics(hot_end.detach(), exact.meta.recurrent_hidden, h0=h0_sub,
-                                            hot_logits=None if hot_logits is None else hot_logits.detach(),
-                                            exact_logits=exact.meta.logits)
+            exact_end = exact.meta.recurrent_hidden
+            if h0_sub is not None and exact_end is not None:
+                # fused: every distillation term and alignment metric of rte/macro.py:394-546
+                losses, mets = hip_ops.distill(hot_end, exact_end, h0_sub, hot_logits, exact.meta.logits,
+                                               temperature=tr.distill_temperature)
+                lam = {"delta_dir": tr.lambda_delta_dir, "delta_rms": tr.lambda_delta_rms,
+                       "endpoint_normed": tr.lambda_endpoint_normed, "endpoint_raw": tr.lambda_endpoint_raw,
+                       "rms_trust": tr.lambda_macro_rms_trust if tr.macro_rms_trust_region else 0.0,
+                       "kl": tr.effective_lambda_kl}
+                for i, name in enumerate(hip_ops.DISTILL_LOSSES):
+                    aux[name] = lam[name] * losses[i]
+                align = {name: mets[i] for i, name in enumerate(hip_ops.DISTILL_METRICS)}
+                has_logits = (hot_logits is not None and exact.meta.logits is not None
+                              and hot_logits.shape == exact.meta.logits.shape)
+                if not has_logits:
+                    del align["logit_kl_exact_macro"]
+            else:
+                aux.update(macro_distill_loss(
+                    hot_end, exact_end, hot_logits, exact.meta.logits, h0=h0_sub,
+                    lambda_hid=tr.effective_lambda_hid, lambda_cos=tr.effective_lambda_cos,
+                    lambda_kl=tr.effective_lambda_kl, lambda_norm=tr.lambda_norm,
+                    lambda_delta_dir=tr.lambda_delta_dir, lambda_delta_rms=tr.lambda_delta_rms,
+                    lambda_endpoint_normed=tr.lambda_endpoint_normed, lambda_endpoint_raw=tr.lambda_endpoint_raw,
+                    lambda_macro_rms_trust=tr.lambda_macro_rms_trust if tr.macro_rms_trust_region else 0.0,
+                    temperature=tr.distill_temperature,
+                ))
+                align = macro_alignment_metrics(hot_end.detach(), exact_end, h0=h0_sub,
+                                                hot_logits=None if hot_logits is None else hot_logits.detach(),
+                                                exact_logits=exact.meta.logits)
             metrics.update(align)
             # recent residual feeds the next step's audit probability; kept on device
             self._pending_residual = (1.0 - align["hidden_cosine_exact_macro"]).detach().clamp_min(0)

@@ -652,6 +652,61 @@ def lm_head_ce(hidden, w, targets):
     return LMHeadCEFn.apply(hidden, w, targets)
 
 
+# ----------------------------------------------------------------------------- audit distillation
+
+DISTILL_LOSSES = ("delta_dir", "delta_rms", "endpoint_normed", "endpoint_raw", "rms_trust", "kl")
+DISTILL_METRICS = ("hidden_cosine_exact_macro", "hidden_mse_exact_macro", "macro_norm", "exact_norm",
+                   "macro_exact_norm_ratio", "delta_cosine_exact_macro", "delta_rms_exact", "delta_rms_pred",
+                   "delta_rms_ratio", "logit_kl_exact_macro")
+
+
+class DistillFn(torch.autograd.Function):
+    """Hot-vs-exact distillation losses (rte/macro.py:394-471, with h0) and alignment metrics
+    (:499-546) of the audited samples in three launches; the backward is one launch for the
+    hidden states and one for the logits.  exact, h0 and exact_logits carry no gradient."""
+
+    @staticmethod
+    def forward(ctx, hot, exact, h0, hot_logits, exact_logits, temperature, eps):
+        _lib.require_device_tensors("distill", hot, exact, h0, hot_logits, exact_logits)
+        A, S, d = hot.shape
+        dev = hot.device
+        hv = hot.contiguous().to(F32)
+        ev = exact.detach().contiguous().to(F32)
+        zv = h0.detach().contiguous().to(F32)
+        has_l = hot_logits is not None and exact_logits is not None and hot_logits.shape == exact_logits.shape
+        V = hot_logits.shape[-1] if has_l else 0
+        hl = hot_logits.reshape(A * S, V).contiguous().to(F32) if has_l else None
+        el = exact_logits.detach().reshape(A * S, V).contiguous().to(F32) if has_l else None
+        R = A * S if has_l else 0
+        nbytes = _lib.load().rte_distill_workspace_bytes(A, R)
+        ws = torch.empty(((nbytes + 3) // 4,), dtype=F32, device=dev)  # kept for the backward
+        losses = torch.empty((6,), dtype=F32, device=dev)
+        metrics = torch.empty((10,), dtype=F32, device=dev)
+        call("rte_distill_fwd", ptr(hv), ptr(ev), ptr(zv), A, S, d, ptr(hl), ptr(el), V, float(temperature),
+             float(eps), ptr(losses), ptr(metrics), ptr(ws), nbytes, _s())
+        ctx.save_for_backward(hv, ev, zv, hl, el, ws)
+        ctx.meta = (A, S, d, V, float(temperature), float(eps), nbytes, has_l,
+                    None if not has_l else hot_logits.shape)
+        ctx.mark_non_differentiable(metrics)
+        return losses, metrics
+
+    @staticmethod
+    def backward(ctx, g, _g_metrics):
+        hv, ev, zv, hl, el, ws = ctx.saved_tensors
+        A, S, d, V, t, eps, nbytes, has_l, lshape = ctx.meta
+        gg = g.contiguous().to(F32)
+        dh = torch.empty_like(hv) if ctx.needs_input_grad[0] else None
+        dl = torch.empty_like(hl) if (has_l and ctx.needs_input_grad[3]) else None
+        call("rte_distill_bwd", ptr(hv), ptr(ev), ptr(zv), A, S, d, ptr(hl), ptr(el), V, t, eps, ptr(gg), ptr(ws),
+             nbytes, ptr(dh), ptr(dl), _s())
+        return dh, None, None, (dl.view(lshape) if dl is not None else None), None, None, None
+
+
+def distill(hot, exact, h0, hot_logits=None, exact_logits=None, *, temperature: float = 1.0, eps: float = 1e-5):
+    """(losses [6], metrics [10]) in the orders DISTILL_LOSSES / DISTILL_METRICS."""
+    return DistillFn.apply(hot, exact, h0, hot_logits, exact_logits, temperature, eps)
+
+
 # ----------------------------------------------------------------------------- audit correction
 
 class AuditCorrectFn(torch.autograd.Function):

@@ -709,3 +709,37 @@ def test_axpy_norm_matches_float64(B, S, d, norm, use_mask):
     assert_rel(_np(dc.grad), rc.grad.numpy(), FP32_RTOL, "dc")
     if use_mask:
         assert_rel(_np(dk.grad), rk.grad.numpy(), FP32_RTOL, "dkeep")
+
+
+# ---------------------------------------------------------------- audit distillation
+
+@pytest.mark.parametrize("A,S,d,V", [(1, 64, 512, 2048), (3, 17, 96, 100), (2, 8, 64, 0)])
+def test_distill_matches_oracle(A, S, d, V):
+    from oracle import distill as DI
+
+    H = _ops()
+    rng = np.random.default_rng(A * 1000 + S + d + V)
+    h0 = rng.standard_normal((A, S, d))
+    exact = h0 + rng.standard_normal((A, S, d)) * 0.7
+    hot = exact + rng.standard_normal((A, S, d)) * 0.9
+    hl = rng.standard_normal((A, S, V)) * 2 if V else None
+    el = rng.standard_normal((A, S, V)) * 2 if V else None
+    t = 2.0
+    f = lambda x, g=False: None if x is None else torch.tensor(x, dtype=torch.float32, device=DEV,  # noqa: E731
+                                                               requires_grad=g)
+    hot32, exact32, h032 = (np.asarray(v, np.float32).astype(np.float64) for v in (hot, exact, h0))
+    hl32 = None if hl is None else np.asarray(hl, np.float32).astype(np.float64)
+    el32 = None if el is None else np.asarray(el, np.float32).astype(np.float64)
+    th, tl = f(hot, True), f(hl, True)
+    print(f"distill A={A} S={S} d={d} V={V}", flush=True)
+    losses, mets = H.distill(th, f(exact), f(h0), tl, f(el), temperature=t)
+    o_loss, o_met = DI.distill(hot32, exact32, h032, hl32, el32, t)
+    np.testing.assert_allclose(_np(losses), [o_loss[k] for k in H.DISTILL_LOSSES], rtol=1e-5, atol=1e-7)
+    want_m = [o_met.get(k, 0.0) for k in H.DISTILL_METRICS]
+    np.testing.assert_allclose(_np(mets), want_m, rtol=1e-5, atol=1e-7)
+    g = np.array([0.3, -1.1, 0.7, 1.9, 0.45, -0.8], np.float32)
+    (losses * torch.from_numpy(g).to(DEV)).sum().backward()
+    dh, dl = DI.distill_grad(hot32, exact32, h032, hl32, el32, t, g=g.astype(np.float64))
+    assert_rel(_np(th.grad), dh, FP32_RTOL, "d hot")
+    if V:
+        assert_rel(_np(tl.grad), dl, FP32_RTOL, "d hot logits")

@@ -455,6 +455,57 @@ def test_audit_oracle_matches_reference_formulation_and_autograd(clip, grad_corr
         assert (np.abs(r) > clip).any() and (np.abs(r) <= clip).any()
 
 
+def _distill_case(seed, A=2, S=5, d=12, V=9):
+    rng = _rng(seed)
+    h0 = rng.normal(size=(A, S, d))
+    exact = h0 + rng.normal(size=(A, S, d)) * 0.7
+    hot = exact + rng.normal(size=(A, S, d)) * 0.9       # mixes |z| < 1 and |z| > 1 smooth-L1 cases
+    hl, el = rng.normal(size=(A, S, V)) * 2, rng.normal(size=(A, S, V)) * 2
+    return hot, exact, h0, hl, el
+
+
+def test_distill_oracle_matches_reference_formulation():
+    """The oracle equals the reference's torch formulation (rte/macro.py:394-546, restated in
+    rte_amd.macro) evaluated on float64 inputs on the CPU, losses and metrics.  The reference's
+    _rms / _rmsnorm (rte/macro.py:12-18) reduce in float32 whatever the input dtype, hence
+    the 1e-6 tolerance."""
+    from oracle import distill as DI
+    from rte_amd.macro import macro_alignment_metrics, macro_distill_loss
+
+    hot, exact, h0, hl, el = _distill_case(21)
+    t = 2.0
+    o_loss, o_met = DI.distill(hot, exact, h0, hl, el, t)
+    T = lambda x: torch.tensor(x, dtype=torch.float64)  # noqa: E731
+    ref = macro_distill_loss(T(hot), T(exact), T(hl), T(el), h0=T(h0), lambda_kl=1.0, lambda_delta_dir=1.0,
+                             lambda_delta_rms=1.0, lambda_endpoint_normed=1.0, lambda_endpoint_raw=1.0,
+                             lambda_macro_rms_trust=1.0, temperature=t)
+    for k in DI.LOSSES:
+        np.testing.assert_allclose(o_loss[k], float(ref[k]), rtol=1e-6, err_msg=k)
+    met = macro_alignment_metrics(T(hot), T(exact), h0=T(h0), hot_logits=T(hl), exact_logits=T(el))
+    for k, v in o_met.items():
+        np.testing.assert_allclose(v, float(met[k]), rtol=1e-6, err_msg=k)
+
+
+def test_distill_oracle_gradient_matches_autograd():
+    from oracle import distill as DI
+    from rte_amd.macro import macro_distill_loss
+
+    hot, exact, h0, hl, el = _distill_case(22)
+    t = 2.0
+    g = np.array([0.3, -1.1, 0.7, 1.9, 0.45, -0.8])
+    th = torch.tensor(hot, requires_grad=True)
+    tl = torch.tensor(hl, requires_grad=True)
+    T = lambda x: torch.tensor(x, dtype=torch.float64)  # noqa: E731
+    ref = macro_distill_loss(th, T(exact), tl, T(el), h0=T(h0), lambda_kl=g[5], lambda_delta_dir=g[0],
+                             lambda_delta_rms=g[1], lambda_endpoint_normed=g[2], lambda_endpoint_raw=g[3],
+                             lambda_macro_rms_trust=g[4], temperature=t)
+    sum(ref.values()).backward()
+    dh, dl = DI.distill_grad(hot, exact, h0, hl, el, t, g=g)
+    # float32 reductions inside the reference's _rms / _rmsnorm: relative Frobenius 1e-6
+    assert np.linalg.norm(dh - th.grad.numpy()) <= 1e-6 * np.linalg.norm(dh)
+    assert np.linalg.norm(dl - tl.grad.numpy()) <= 1e-10 * np.linalg.norm(dl)
+
+
 # ---------------------------------------------------------------- shortlist
 
 def _brute_first_distinct(row, L):
