@@ -202,6 +202,28 @@ int rte_axpy_norm_bwd(const void* dn, const float* dx_ext, const float* x, const
                       float* da, float* db, float* dkeep, float* dparams, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/* ---- bounded-residual macro operator Phi, elementwise ends (rte/macro.py:201-236; the
+ *      (recipe, stride) low-rank matrices in between run as rte_grouped_linear_*) ----
+ * prologue fwd: z bf16 [B*seq, 3d] = [h * rstd | mean over the sample's rows of h * rstd | h0],
+ *               rstd f32 [B*seq] = rsqrt(mean(h^2) + eps) per row (h, h0 f32 [B, seq, d]).
+ * prologue bwd: dh = dh_extra (optional) + rmsnorm backward of dz[:, :d] + dz[:, d:2d] / seq
+ *               broadcast over the sample's rows; dh0 = dz[:, 2d:] (optional).
+ * epilogue fwd: out = h + c * scale[k] * tanh(gain[k] * h + low + bias[k]), k = key[b] (int64 [B]),
+ *               tables gain / bias / scale f32 [keys, d], low f32 [B*seq, d].
+ * epilogue bwd: dh = dout + dupd * gain[k], dlow bf16 = dupd, dupd = dout c scale[k] (1 - t^2);
+ *               part f32 [B, 3d] = per-sample sums (dupd h | dupd | dout c t) for the tables.
+ * seq <= 4096, d <= 4096. */
+int rte_macro_prologue_fwd(const float* h, const float* h0, int B, int seq, int d, float eps, void* z, float* rstd,
+                           void* stream);
+int rte_macro_prologue_bwd(const void* dz, const float* h, const float* rstd, const float* dh_extra, int B, int seq,
+                           int d, float* dh, float* dh0, void* stream);
+int rte_macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int seq, int d,
+                           const float* gain, const float* bias, const float* scale, float c, float* out,
+                           void* stream);
+int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int seq,
+                           int d, const float* gain, const float* bias, const float* scale, float c, float* dh,
+                           void* dlow, float* part, void* stream);
+
 /* ---- hot-vs-exact distillation losses + alignment metrics of the audit (replaces
  *      macro_distill_loss rte/macro.py:394-471 and macro_alignment_metrics :499-546 on the
  *      path with the residual origin h0; rte/audit.py:326-352 calls both) ----

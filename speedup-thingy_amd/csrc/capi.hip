@@ -39,6 +39,15 @@ size_t axpy_norm_bwd_workspace_bytes(int T, int d);
 int axpy_norm_bwd(const bf16* dn, const float* dx_ext, const float* x, const float* rstd, const float* w,
                   const float* gamma, const float* b, const float* c, const uint8_t* mask, int S, int T, int d,
                   float* da, float* db, float* dkeep, float* dparams, void* ws, size_t ws_bytes, hipStream_t s);
+int macro_prologue_fwd(const float* h, const float* h0, int B, int S, int d, float eps, bf16* z, float* rstd,
+                       hipStream_t s);
+int macro_prologue_bwd(const bf16* dz, const float* h, const float* rstd, const float* dh_extra, int B, int S, int d,
+                       float* dh, float* dh0, hipStream_t s);
+int macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int S, int d, const float* gain,
+                       const float* bias, const float* scale, float c, float* out, hipStream_t s);
+int macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int S, int d,
+                       const float* gain, const float* bias, const float* scale, float c, float* dh, bf16* dlow,
+                       float* part, hipStream_t s);
 size_t distill_workspace_bytes(int A, int R);
 int distill_fwd(const float* hot, const float* exact, const float* h0, int A, int S, int d, const float* hot_logits,
                 const float* exact_logits, int V, float t, float eps, float* losses, float* metrics, void* ws,
@@ -748,6 +757,28 @@ int rte_axpy_norm_bwd(const void* dn, const float* dx_ext, const float* x, const
                       void* stream) {
   return axpy_norm_bwd(reinterpret_cast<const bf16*>(dn), dx_ext, x, rstd, w, gamma, b, c, mask, seq, T, d, da, db,
                        dkeep, dparams, workspace, workspace_bytes, S(stream));
+}
+
+int rte_macro_prologue_fwd(const float* h, const float* h0, int B, int seq, int d, float eps, void* z, float* rstd,
+                           void* stream) {
+  return macro_prologue_fwd(h, h0, B, seq, d, eps, B16(z), rstd, S(stream));
+}
+
+int rte_macro_prologue_bwd(const void* dz, const float* h, const float* rstd, const float* dh_extra, int B, int seq,
+                           int d, float* dh, float* dh0, void* stream) {
+  return macro_prologue_bwd(reinterpret_cast<const bf16*>(dz), h, rstd, dh_extra, B, seq, d, dh, dh0, S(stream));
+}
+
+int rte_macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int seq, int d,
+                           const float* gain, const float* bias, const float* scale, float c, float* out,
+                           void* stream) {
+  return macro_epilogue_fwd(h, low, key, B, seq, d, gain, bias, scale, c, out, S(stream));
+}
+
+int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int seq,
+                           int d, const float* gain, const float* bias, const float* scale, float c, float* dh,
+                           void* dlow, float* part, void* stream) {
+  return macro_epilogue_bwd(dout, h, low, key, B, seq, d, gain, bias, scale, c, dh, B16(dlow), part, S(stream));
 }
 
 size_t rte_distill_workspace_bytes(int A, int rows) { return distill_workspace_bytes(A, rows); }

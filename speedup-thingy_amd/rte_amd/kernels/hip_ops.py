@@ -791,18 +791,102 @@ class GroupedLinearFn(torch.autograd.Function):
     def backward(ctx, dy):
         xb, wb, offsets, tok, pos = ctx.saved_tensors
         shape, x_dt, w_dt = ctx.meta
-        G, K, Nout = wb.shape
-        N = xb.shape[0]
-        dyb = cast_bf16(dy.reshape(N, Nout))
-        need_x, need_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-        dx_f32 = x_dt != BF16
-        dx = torch.empty((N, K), dtype=F32 if dx_f32 else BF16, device=xb.device) if need_x else None
-        dw = torch.empty((G, K, Nout), dtype=F32, device=xb.device) if need_w else None
-        P = tok.numel()
-        ws, nb = workspace(_lib.load().rte_grouped_linear_bwd_workspace_bytes(P, G, K, Nout), xb.device)
-        call("rte_grouped_linear_bwd", ptr(dyb), ptr(xb), N, K, ptr(offsets), G, P, ptr(tok), ptr(pos),
-             ptr(wb), Nout, ptr(dx), int(dx_f32), ptr(dw), ws, nb, _s())
+        N, Nout = xb.shape[0], wb.shape[2]
+        dx, dw = _grouped_linear_bwd(cast_bf16(dy.reshape(N, Nout)), xb, wb, offsets, tok, pos,
+                                     ctx.needs_input_grad[0], ctx.needs_input_grad[1], x_dt != BF16)
         return (None if dx is None else dx.view(shape).to(x_dt), None if dw is None else dw.to(w_dt), None, None)
+
+
+def _grouped_linear_fwd(xb, wb, pk: PackIndex, out_f32: bool):
+    N, K = xb.shape
+    G, _, Nout = wb.shape
+    y = torch.empty((N, Nout), dtype=F32 if out_f32 else BF16, device=xb.device)
+    call("rte_grouped_linear_fwd", ptr(xb), N, K, ptr(pk.offsets), G, pk.tok_of_slot.numel(), ptr(pk.tok_of_slot),
+         ptr(pk.pair_of_slot), ptr(wb), Nout, ptr(y), int(out_f32), _s())
+    return y
+
+
+def _grouped_linear_bwd(dyb, xb, wb, offsets, tok, pos, need_x: bool, need_w: bool, dx_f32: bool):
+    """(dx [N, K] (fp32 or bf16) or None, dW fp32 [G, K, Nout] or None) of y = x @ W[key]."""
+    G, K, Nout = wb.shape
+    N = xb.shape[0]
+    dx = torch.empty((N, K), dtype=F32 if dx_f32 else BF16, device=xb.device) if need_x else None
+    dw = torch.empty((G, K, Nout), dtype=F32, device=xb.device) if need_w else None
+    P = tok.numel()
+    ws, nb = workspace(_lib.load().rte_grouped_linear_bwd_workspace_bytes(P, G, K, Nout), xb.device)
+    call("rte_grouped_linear_bwd", ptr(dyb), ptr(xb), N, K, ptr(offsets), G, P, ptr(tok), ptr(pos),
+         ptr(wb), Nout, ptr(dx), int(dx_f32), ptr(dw), ws, nb, _s())
+    return dx, dw
+
+
+class MacroBoundedFn(torch.autograd.Function):
+    """The bounded-residual macro operator Phi (rte/macro.py:201-236) with the default options
+    (no gate, no second hidden layer, no extra input parts):
+
+        z   = [rmsnorm(h) | mean_s rmsnorm(h) | h0]                 (prologue kernel, bf16)
+        low = silu(z @ V[key]) @ U[key]                             (grouped MFMA GEMMs)
+        out = h + c * scale[key] * tanh(gain[key] * h + low + bias[key])   (epilogue kernel)
+
+    key = recipe * strides + stride per sample.  The backward reduces the per-key table and
+    matrix gradients in a fixed order (per-sample column sums, then the segmented reduction;
+    grouped-K GEMMs for V and U)."""
+
+    @staticmethod
+    def forward(ctx, h, h0, key, pk, v, u, gain, bias, scale, c, eps):
+        _lib.require_device_tensors("macro_bounded", h, h0, key, v, u, gain, bias, scale)
+        B, S, d = h.shape
+        G = v.shape[0] * v.shape[1]
+        hv = h.contiguous().to(F32)
+        h0v = h0.contiguous().to(F32)
+        kv = key.reshape(-1).contiguous().to(torch.int64)
+        dev = h.device
+        z = torch.empty((B * S, 3 * d), dtype=BF16, device=dev)
+        rstd = torch.empty((B * S,), dtype=F32, device=dev)
+        call("rte_macro_prologue_fwd", ptr(hv), ptr(h0v), B, S, d, float(eps), ptr(z), ptr(rstd), _s())
+        vb = cast_bf16(v.reshape(G, v.shape[-2], v.shape[-1]))
+        ub = cast_bf16(u.reshape(G, u.shape[-2], u.shape[-1]))
+        a = _grouped_linear_fwd(z, vb, pk, out_f32=False)
+        sa = torch.nn.functional.silu(a)
+        low = _grouped_linear_fwd(sa, ub, pk, out_f32=True)
+        tabs = [t.reshape(G, d).contiguous().to(F32) for t in (gain, bias, scale)]
+        out = torch.empty((B, S, d), dtype=F32, device=dev)
+        call("rte_macro_epilogue_fwd", ptr(hv), ptr(low), ptr(kv), B, S, d, ptr(tabs[0]), ptr(tabs[1]), ptr(tabs[2]),
+             float(c), ptr(out), _s())
+        ctx.save_for_backward(hv, kv, pk.offsets, pk.tok_of_slot, pk.pair_of_slot, vb, ub, z, rstd, a, sa, low,
+                              *tabs)
+        ctx.meta = (B, S, d, G, float(c), v.shape, u.shape, gain.shape, h.dtype, h0.dtype)
+        return out.to(h.dtype)
+
+    @staticmethod
+    def backward(ctx, dout):
+        hv, kv, offsets, tok, pos, vb, ub, z, rstd, a, sa, low, tg, tb, ts = ctx.saved_tensors
+        B, S, d, G, c, v_shape, u_shape, t_shape, h_dt, h0_dt = ctx.meta
+        nia = ctx.needs_input_grad
+        dev = hv.device
+        do = dout.contiguous().to(F32)
+        dh_epi = torch.empty((B, S, d), dtype=F32, device=dev)
+        dlow = torch.empty((B * S, d), dtype=BF16, device=dev)
+        part = torch.empty((B, 3 * d), dtype=F32, device=dev)
+        call("rte_macro_epilogue_bwd", ptr(do), ptr(hv), ptr(low), ptr(kv), B, S, d, ptr(tg), ptr(tb), ptr(ts),
+             c, ptr(dh_epi), ptr(dlow), ptr(part), _s())
+        dtab = segment_reduce_rows(kv, G, part) if (nia[6] or nia[7] or nia[8]) else None
+        dsa, du = _grouped_linear_bwd(dlow, sa, ub, offsets, tok, pos, True, nia[5], False)
+        da = torch.ops.aten.silu_backward(dsa, a)
+        dz, dv = _grouped_linear_bwd(da, z, vb, offsets, tok, pos, True, nia[4], False)
+        dh = torch.empty((B, S, d), dtype=F32, device=dev)
+        dh0 = torch.empty((B, S, d), dtype=F32, device=dev) if nia[1] else None
+        call("rte_macro_prologue_bwd", ptr(dz), ptr(hv), ptr(rstd), ptr(dh_epi), B, S, d, ptr(dh), ptr(dh0), _s())
+
+        def tab(i):
+            return None if (dtab is None or not nia[6 + i]) else dtab[:, i * d:(i + 1) * d].reshape(t_shape)
+
+        return (dh.to(h_dt), None if dh0 is None else dh0.to(h0_dt), None, None,
+                None if dv is None else dv.view(v_shape), None if du is None else du.view(u_shape),
+                tab(0), tab(1), tab(2), None, None)
+
+
+def macro_bounded(h, h0, key, pk, v, u, gain, bias, scale, c: float, eps: float = 1e-5):
+    return MacroBoundedFn.apply(h, h0, key, pk, v, u, gain, bias, scale, c, eps)
 
 
 def grouped_linear(x, w, pk: PackIndex, *, out_f32: bool = True):

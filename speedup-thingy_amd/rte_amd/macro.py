@@ -139,6 +139,11 @@ class MacroOperators(nn.Module):
         R, Kk = self.v.shape[0], self.v.shape[1]
         key = recipe_ids.long() * Kk + stride_ids.long()
         pk = hip_ops.group_rows(key[:, None].expand(B, S), R * Kk)
+        if (self.v2 is None and self.gate_v is None and not self.config.macro_include_delta_to_h0
+                and self.depth_embed is None):
+            # default options: fused prologue / epilogue kernels around the two grouped GEMMs
+            return hip_ops.macro_bounded(h, h0, key, pk, self.v, self.u, self.d_gain, self.bias, self.update_scale,
+                                         self.config.macro_update_scale)
         gain = self._rows(self.d_gain, key)
         bias = self._rows(self.bias, key)
         scale = self._rows(self.update_scale, key)

@@ -415,14 +415,17 @@ def _torch_bounded(h, h0, rid, sid, p, c):
     return h + c * g(p["update_scale"]).unsqueeze(1) * torch.tanh(upd)
 
 
-def test_macro_operator_grouped_matches_reference():
+@pytest.mark.parametrize("scale_init", [1.0, 0.5])
+def test_macro_operator_grouped_matches_reference(scale_init):
     """MacroOperators (bounded) on the grouped GEMMs: forward against the numpy oracle, gradients
-    of every parameter and of h, h0 against fp64 autograd of the reference formula."""
+    of every parameter and of h, h0 against fp64 autograd of the reference formula.  With
+    macro_update_scale_init != 1 the per-key update scale is a parameter too."""
     from oracle import macro as MO
     from helpers import rel_err
     from rte_amd.macro import MacroOperators
 
-    cfg = _model_cfg(d_model=128, macro_rank=32, recipe_count=6, depth_choices=[1, 2, 4], t_max=4)
+    cfg = _model_cfg(d_model=128, macro_rank=32, recipe_count=6, depth_choices=[1, 2, 4], t_max=4,
+                     macro_update_scale_init=scale_init)
     torch.manual_seed(4)
     mac = MacroOperators(cfg).cuda()
     with torch.no_grad():
@@ -445,12 +448,13 @@ def test_macro_operator_grouped_matches_reference():
     want = MO.bounded_apply(hn, h0n, rid.cpu().numpy(), sid.cpu().numpy(), {k: v.numpy() for k, v in p.items()},
                             cfg.macro_update_scale)
     assert_rel(out.detach().double().cpu().numpy() - hn, want - hn, BF16_RTOL, "macro delta")
-    tp = {k: v.clone().requires_grad_(k != "update_scale") for k, v in p.items()}
+    scale_param = isinstance(mac.update_scale, torch.nn.Parameter)
+    tp = {k: v.clone().requires_grad_(k != "update_scale" or scale_param) for k, v in p.items()}
     th, th0 = torch.tensor(hn, requires_grad=True), torch.tensor(h0n, requires_grad=True)
     ref = _torch_bounded(th, th0, rid.cpu(), sid.cpu(), tp, cfg.macro_update_scale)
     assert rel_err(ref.detach().numpy(), want) < 1e-12
     (ref * torch.tensor(G)).sum().backward()
-    for k in ("d_gain", "bias", "v", "u"):
+    for k in ("d_gain", "bias", "v", "u") + (("update_scale",) if scale_param else ()):
         assert_rel(getattr(mac, k).grad.double().cpu().numpy(), tp[k].grad.numpy(), BF16_RTOL, f"macro d{k}")
     assert_rel(h.grad.double().cpu().numpy(), th.grad.numpy(), BF16_RTOL, "macro dh")
     assert_rel(h0.grad.double().cpu().numpy(), th0.grad.numpy(), BF16_RTOL, "macro dh0")
