@@ -212,7 +212,7 @@ int rte_axpy_norm_bwd(const void* dn, const float* dx_ext, const float* x, const
  *               tables gain / bias / scale f32 [keys, d], low f32 [B*seq, d].
  * epilogue bwd: dh = dout + dupd * gain[k], dlow bf16 = dupd, dupd = dout c scale[k] (1 - t^2);
  *               part f32 [B, 3d] = per-sample sums (dupd h | dupd | dout c t) for the tables.
- * seq <= 4096, d <= 4096. */
+ * d % 8 == 0, d <= 1024, 16-byte aligned buffers. */
 int rte_macro_prologue_fwd(const float* h, const float* h0, int B, int seq, int d, float eps, void* z, float* rstd,
                            void* stream);
 int rte_macro_prologue_bwd(const void* dz, const float* h, const float* rstd, const float* dh_extra, int B, int seq,
