@@ -10,8 +10,9 @@
 //   kl              = sum_rows KL(softmax(exact / t) || softmax(hot / t)) / A * t^2
 // plus the alignment metrics (cosines, mse, rms norms and ratios, KL at t = 1).
 //
-// Forward: one workgroup per sample reduces its sums, one wave per logit row reduces the KL
-// rows, one lane finishes everything in double precision (3 launches, fixed order).
+// Forward: 16 workgroups per sample reduce partial sums, one wave per logit row reduces the KL
+// rows, one workgroup adds the partials in order and one lane finishes in double precision
+// (3 launches, fixed order).
 // Backward: one wave per hidden row and one per logit row.
 #include "common.hpp"
 
@@ -20,6 +21,7 @@ namespace rte {
 namespace {
 
 constexpr int kStats = 10;  // per-sample sums
+constexpr int kSplit = 16;  // workgroups per sample in the forward reduction
 // w12 = dp.de, w1 = |dp|^2, w2 = |de|^2, hh = |hot|^2, ee = |exact|^2, he = hot.exact,
 // sl1n = sum smooth_l1 of the row-normalised difference, sl1r = sum smooth_l1(hot - exact),
 // mse = sum (hot - exact)^2, (unused)
@@ -49,12 +51,13 @@ __global__ void __launch_bounds__(256) distill_sample_kernel(const float* __rest
                                                              const float* __restrict__ h0, int S, int d, float eps,
                                                              float* __restrict__ stats) {
   __shared__ float red[4][kStats];
-  const int a = blockIdx.x;
+  const int a = blockIdx.x, y = blockIdx.y;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   float acc[kStats];
 #pragma unroll
   for (int k = 0; k < kStats; ++k) acc[k] = 0.0f;
-  for (int s = wave; s < S; s += 4) {
+  // rows 4 * (y + kSplit * i) + wave of sample a
+  for (int s = 4 * y + wave; s < S; s += 4 * kSplit) {
     const int64_t rb = ((int64_t)a * S + s) * d;
     float rh = 0.0f, re = 0.0f;
     for (int c = lane; c < d; c += 64) {
@@ -86,7 +89,7 @@ __global__ void __launch_bounds__(256) distill_sample_kernel(const float* __rest
   __syncthreads();
   if (threadIdx.x < kStats) {
     const int k = threadIdx.x;
-    stats[(int64_t)a * kStats + k] = ((red[0][k] + red[1][k]) + red[2][k]) + red[3][k];
+    stats[((int64_t)a * kSplit + y) * kStats + k] = ((red[0][k] + red[1][k]) + red[2][k]) + red[3][k];
   }
 }
 
@@ -146,9 +149,17 @@ __global__ void __launch_bounds__(256) kl_rows_kernel(const float* __restrict__ 
 // metrics: [0] hidden_cosine, [1] hidden_mse, [2] macro_norm, [3] exact_norm,
 // [4] macro_exact_norm_ratio, [5] delta_cosine, [6] delta_rms_exact, [7] delta_rms_pred,
 // [8] delta_rms_ratio, [9] logit_kl_exact_macro
-__global__ void distill_final_kernel(const float* __restrict__ stats, int A, int S, int d,
-                                     const float* __restrict__ kl_row, const float* __restrict__ klm_row, int R,
-                                     float t, float* __restrict__ out, float* __restrict__ met) {
+__global__ void distill_final_kernel(const float* __restrict__ parts, float* __restrict__ stats, int A, int S,
+                                     int d, const float* __restrict__ kl_row, const float* __restrict__ klm_row,
+                                     int R, float t, float* __restrict__ out, float* __restrict__ met) {
+  // per-sample sums of the kSplit partials, in order (kept for the backward)
+  for (int q = threadIdx.x; q < A * kStats; q += blockDim.x) {
+    const int a = q / kStats, k = q - a * kStats;
+    float v = 0.0f;
+    for (int y = 0; y < kSplit; ++y) v += parts[((int64_t)a * kSplit + y) * kStats + k];
+    stats[q] = v;
+  }
+  __syncthreads();
   if (threadIdx.x != 0) return;
   const double N = (double)S * d;
   double cos_d = 0, cos_h = 0, lrms = 0, trust = 0, sl1n = 0, sl1r = 0, mse = 0, mn = 0, en = 0, pr = 0, er = 0;
@@ -258,8 +269,10 @@ __global__ void __launch_bounds__(256) kl_bwd_kernel(const float* __restrict__ h
 
 }  // namespace
 
+// workspace: per-sample sums [A][kStats] | KL rows [R] | metric KL rows [R] | lse [2R] |
+// forward partials [A][kSplit][kStats]
 size_t distill_workspace_bytes(int A, int R) {
-  return ((size_t)A * kStats + (size_t)R * 4 + 64) * sizeof(float);
+  return ((size_t)A * kStats * (1 + kSplit) + (size_t)R * 4 + 64) * sizeof(float);
 }
 
 int distill_fwd(const float* hot, const float* exact, const float* h0, int A, int S, int d, const float* hot_logits,
@@ -275,15 +288,16 @@ int distill_fwd(const float* hot, const float* exact, const float* h0, int A, in
   float* kl_row = stats + (size_t)A * kStats;
   float* klm_row = kl_row + R;
   float* lse = klm_row + R;
-  hipLaunchKernelGGL(distill_sample_kernel, dim3(A), dim3(256), 0, s, hot, exact, h0, S, d, eps, stats);
+  float* parts = lse + 2 * (size_t)R;
+  hipLaunchKernelGGL(distill_sample_kernel, dim3(A, kSplit), dim3(256), 0, s, hot, exact, h0, S, d, eps, parts);
   RTE_TRY(check_launch("distill_sample"));
   if (R > 0) {
     hipLaunchKernelGGL(kl_rows_kernel, dim3((R + 3) / 4), dim3(256), 0, s, hot_logits, exact_logits, R, V, 1.0f / t,
                        kl_row, klm_row, lse);
     RTE_TRY(check_launch("distill_kl_rows"));
   }
-  hipLaunchKernelGGL(distill_final_kernel, dim3(1), dim3(64), 0, s, stats, A, S, d, kl_row, klm_row, R, t, losses,
-                     metrics);
+  hipLaunchKernelGGL(distill_final_kernel, dim3(1), dim3(256), 0, s, parts, stats, A, S, d, kl_row, klm_row, R, t,
+                     losses, metrics);
   return check_launch("distill_final");
 }
 

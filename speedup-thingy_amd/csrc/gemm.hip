@@ -28,6 +28,8 @@ namespace rte {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kMaxSplits = 32;                      // split-K partials per output tile
+constexpr size_t kMaxSplitBytes = (size_t)64 << 20;  // split-K workspace ceiling
 
 __device__ __forceinline__ int64_t ilv_row(int64_t r, int32_t half) {
   return ((r & 63) < 32 ? 0 : half) + (r >> 6) * 32 + (r & 31);
@@ -938,14 +940,15 @@ int launch_cfg(const GemmArgs& p0, hipStream_t stream, void* ws, size_t ws_bytes
     }
   } else {
     grid = dim3((p.M + BM - 1) / BM, (p.N + BN - 1) / BN, 1);
-    // split the reduction when the tile grid cannot fill the GPU
+    // split the reduction when the tile grid cannot fill the GPU: about 512 workgroups,
+    // at least 128 k per split
     const int tiles = (int)(grid.x * grid.y);
     p.splits = 1;
-    if (EPI == EPI_STORE && ws && tiles < 256 && p.K >= 1024) {
+    if (EPI == EPI_STORE && ws && tiles < 256 && p.K >= 256) {
       int splits = (512 + tiles - 1) / tiles;
-      const int max_by_k = p.K / 512;
+      const int max_by_k = p.K / 128;
       if (splits > max_by_k) splits = max_by_k;
-      if (splits > 16) splits = 16;
+      if (splits > kMaxSplits) splits = kMaxSplits;
       while (splits > 1 && (size_t)splits * p.M * p.N * sizeof(float) > ws_bytes) --splits;
       if (splits > 1) {
         int kc = (p.K + splits - 1) / splits;
@@ -1035,10 +1038,11 @@ size_t gemm_groupk_bytes(int M, int N, int K, int G) {
 }
 
 size_t gemm_splitk_bytes(int M, int N, int K) {
-  int splits = K / 512;
-  if (splits > 16) splits = 16;
+  int splits = K / 128;
+  if (splits > kMaxSplits) splits = kMaxSplits;
   if (splits < 2) return 0;
-  return (size_t)splits * M * N * sizeof(float);
+  const size_t b = (size_t)splits * M * N * sizeof(float);
+  return b < kMaxSplitBytes ? b : kMaxSplitBytes;  // the launch uses fewer splits to fit
 }
 
 int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream, void* ws, size_t ws_bytes) {

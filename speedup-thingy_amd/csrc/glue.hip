@@ -20,7 +20,13 @@ namespace rte {
 
 namespace {
 
-constexpr int kGlueRows = 32;  // rows per backward workgroup
+constexpr int kGlueRows = 32;  // most rows per backward workgroup
+
+// Rows per backward workgroup: one per wave for small T, up to 32 once the grid is full.
+inline int glue_rows_per_block(int T) {
+  int r = ((T + 255) / 256 + 3) / 4 * 4;
+  return r < 4 ? 4 : (r > kGlueRows ? kGlueRows : r);
+}
 
 __device__ __forceinline__ float wave_sum_g(float v) {
 #pragma unroll
@@ -122,7 +128,8 @@ __global__ void __launch_bounds__(256) axpy_norm_bwd_kernel(
     const bf16* __restrict__ dn, const float* __restrict__ dx_ext, const float* __restrict__ x,
     const float* __restrict__ rstd, const float* __restrict__ w, const float* __restrict__ gamma,
     const float* __restrict__ b, const float* __restrict__ c, const uint8_t* __restrict__ mask, int S, int T,
-    int d, float* __restrict__ da, float* __restrict__ db, float* __restrict__ dkeep, float* __restrict__ part) {
+    int d, float* __restrict__ da, float* __restrict__ db, float* __restrict__ dkeep, float* __restrict__ part,
+    int rpb) {
   extern __shared__ float sh[];  // [4][3 d + 1]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nchunk = d / 8, W = 3 * d + 1;
@@ -148,8 +155,8 @@ __global__ void __launch_bounds__(256) axpy_norm_bwd_kernel(
     }
   }
   float pc = 0.0f;
-  const int r0 = blockIdx.x * kGlueRows;
-  for (int rr = wave; rr < kGlueRows; rr += 4) {
+  const int r0 = blockIdx.x * rpb;
+  for (int rr = wave; rr < rpb; rr += 4) {
     const int t = r0 + rr;
     if (t >= T) break;
     const int64_t rb = (int64_t)t * d;
@@ -230,18 +237,23 @@ __global__ void __launch_bounds__(256) axpy_norm_bwd_kernel(
     part[(int64_t)blockIdx.x * W + q] = ((sh[q] + sh[W + q]) + sh[2 * W + q]) + sh[3 * W + q];
 }
 
-// out[q] = sum_r part[r, q] in row order (4 row phases combined in fixed order).
+// out[q] = sum_r part[r, q]: 8 columns per workgroup, 32 row phases combined in phase order.
 __global__ void __launch_bounds__(256) glue_colsum_kernel(const float* __restrict__ part, int nrows, int W,
                                                           float* __restrict__ out) {
-  __shared__ float s4[4][64];
-  const int l = threadIdx.x & 63, phase = threadIdx.x >> 6;
-  const int q = blockIdx.x * 64 + l;
+  __shared__ float s32[32][8];
+  const int l = threadIdx.x & 7, phase = threadIdx.x >> 3;
+  const int q = blockIdx.x * 8 + l;
   float s = 0.0f;
   if (q < W)
-    for (int r = phase; r < nrows; r += 4) s += part[(int64_t)r * W + q];
-  s4[phase][l] = s;
+    for (int r = phase; r < nrows; r += 32) s += part[(int64_t)r * W + q];
+  s32[phase][l] = s;
   __syncthreads();
-  if (phase == 0 && q < W) out[q] = ((s4[0][l] + s4[1][l]) + s4[2][l]) + s4[3][l];
+  if (threadIdx.x < 8 && q < W) {
+    float tot = 0.0f;
+#pragma unroll
+    for (int p = 0; p < 32; ++p) tot += s32[p][l];
+    out[q] = tot;
+  }
 }
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -270,7 +282,8 @@ int axpy_norm_fwd(const float* a, const float* b, const float* c, const float* k
 }
 
 size_t axpy_norm_bwd_workspace_bytes(int T, int d) {
-  const int nblk = (T + kGlueRows - 1) / kGlueRows;
+  const int rpb = glue_rows_per_block(T);
+  const int nblk = (T + rpb - 1) / rpb;
   return (size_t)(nblk > 0 ? nblk : 1) * (size_t)(3 * d + 1) * sizeof(float);
 }
 
@@ -287,17 +300,18 @@ int axpy_norm_bwd(const bf16* dn, const float* dx_ext, const float* x, const flo
     RTE_REQUIRE(!p || al16(p), "axpy_norm_bwd: buffers must be 16-byte aligned");
   const int W = 3 * d + 1;
   if (T == 0) return fill_f32(dparams, 0.0f, W, s);
-  const int nblk = (T + kGlueRows - 1) / kGlueRows;
+  const int rpb = glue_rows_per_block(T);
+  const int nblk = (T + rpb - 1) / rpb;
   float* part = static_cast<float*>(ws);
   const size_t lds = (size_t)4 * W * sizeof(float);
   if (d <= 512)
     hipLaunchKernelGGL(axpy_norm_bwd_kernel<1>, dim3(nblk), dim3(256), lds, s, dn, dx_ext, x, rstd, w, gamma, b, c,
-                       mask, S, T, d, da, db, dkeep, part);
+                       mask, S, T, d, da, db, dkeep, part, rpb);
   else
     hipLaunchKernelGGL(axpy_norm_bwd_kernel<2>, dim3(nblk), dim3(256), lds, s, dn, dx_ext, x, rstd, w, gamma, b, c,
-                       mask, S, T, d, da, db, dkeep, part);
+                       mask, S, T, d, da, db, dkeep, part, rpb);
   RTE_TRY(check_launch("axpy_norm_bwd"));
-  hipLaunchKernelGGL(glue_colsum_kernel, dim3((W + 63) / 64), dim3(256), 0, s, part, nblk, W, dparams);
+  hipLaunchKernelGGL(glue_colsum_kernel, dim3((W + 7) / 8), dim3(256), 0, s, part, nblk, W, dparams);
   return check_launch("axpy_norm_colsum");
 }
 

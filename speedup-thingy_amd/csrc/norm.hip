@@ -76,7 +76,13 @@ __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const float* __restric
 // One wave per row, 8 columns per lane per step (16-byte dy loads, 32-byte x loads);
 // each lane keeps its columns' dw partial in registers across the block's rows, so
 // dw needs no atomics: per-block partials are summed in block order by colsum_kernel.
-constexpr int kNormRowsPerBlock = 32;
+constexpr int kNormRowsPerBlock = 32;  // upper bound; small T uses fewer rows per block
+
+// Rows per backward workgroup: 4 (one per wave) for small T, up to 32 once the grid is full.
+inline int norm_rows_per_block(int T) {
+  int r = ((T + 255) / 256 + 3) / 4 * 4;
+  return r < 4 ? 4 : (r > kNormRowsPerBlock ? kNormRowsPerBlock : r);
+}
 constexpr int kNormMaxChunks = 4;  // d <= 64 lanes * 8 * 4 = 2048
 
 __device__ __forceinline__ void load8_bf16(const bf16* p, float* v) {
@@ -104,7 +110,7 @@ __device__ __forceinline__ void store8_f32(float* p, const float* v) {
 __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     const bf16* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ rstd, const float* __restrict__ dres, int T, int d,
-    float* __restrict__ dx, float* __restrict__ dw_part) {
+    float* __restrict__ dx, float* __restrict__ dw_part, int rpb) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   extern __shared__ float sdw[];  // [4][d]
   const int nchunk = d / 8;
@@ -119,8 +125,8 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     }
     if (lane + 64 * c < nchunk) load8_f32(w + (lane + 64 * c) * 8, wv[c]);
   }
-  const int r0 = blockIdx.x * kNormRowsPerBlock;
-  for (int rr = wave; rr < kNormRowsPerBlock; rr += 4) {
+  const int r0 = blockIdx.x * rpb;
+  for (int rr = wave; rr < rpb; rr += 4) {
     const int t = r0 + rr;
     if (t >= T) break;
     const float rs = rstd[t];
@@ -160,20 +166,22 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     dw_part[(int64_t)blockIdx.x * d + c] = ((sdw[c] + sdw[d + c]) + sdw[2 * d + c]) + sdw[3 * d + c];
 }
 
-// out[c] (+)= sum_r part[r, c]: 4 row phases per column, combined in fixed order.
+// out[c] (+)= sum_r part[r, c]: 8 columns per workgroup, 32 row phases per column, the phase
+// sums combined in phase order (fixed order; 8x more workgroups than one column per lane).
 __global__ void __launch_bounds__(256) colsum_kernel(const float* __restrict__ part, int nrows, int d,
                                                      float* __restrict__ out, int accumulate) {
-  __shared__ float sh[4][64];
-  const int l = threadIdx.x & 63;
-  const int col = blockIdx.x * 64 + l;
-  const int phase = threadIdx.x >> 6;
+  __shared__ float sh[32][8];
+  const int l = threadIdx.x & 7, phase = threadIdx.x >> 3;
+  const int col = blockIdx.x * 8 + l;
   float s = 0.0f;
   if (col < d)
-    for (int r = phase; r < nrows; r += 4) s += part[(int64_t)r * d + col];
+    for (int r = phase; r < nrows; r += 32) s += part[(int64_t)r * d + col];
   sh[phase][l] = s;
   __syncthreads();
-  if (phase == 0 && col < d) {
-    const float tot = ((sh[0][l] + sh[1][l]) + sh[2][l]) + sh[3][l];
+  if (threadIdx.x < 8 && col < d) {
+    float tot = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 32; ++q) tot += sh[q][l];
     out[col] = accumulate ? out[col] + tot : tot;
   }
 }
@@ -257,7 +265,8 @@ int rmsnorm_fwd(const float* x, const float* w, int T, int d, float eps, bf16* o
 }
 
 size_t rmsnorm_bwd_workspace_bytes(int T, int d) {
-  const int nblk = (T + kNormRowsPerBlock - 1) / kNormRowsPerBlock;
+  const int rpb = norm_rows_per_block(T);
+  const int nblk = (T + rpb - 1) / rpb;
   return (size_t)(nblk > 0 ? nblk : 1) * d * sizeof(float);
 }
 
@@ -265,16 +274,17 @@ int rmsnorm_bwd(const bf16* dy, const float* x, const float* w, const float* rst
                 int d, float* dx, float* dw, int dw_accumulate, void* ws, size_t ws_bytes, hipStream_t s) {
   RTE_REQUIRE(ws_bytes >= rmsnorm_bwd_workspace_bytes(T, d), "rmsnorm_bwd: workspace too small");
   RTE_REQUIRE(d % 8 == 0 && d <= 64 * 8 * kNormMaxChunks, "rmsnorm_bwd: d must be a multiple of 8 and <= 2048");
-  const int nblk = (T + kNormRowsPerBlock - 1) / kNormRowsPerBlock;
+  const int rpb = norm_rows_per_block(T);
+  const int nblk = (T + rpb - 1) / rpb;
   float* part = static_cast<float*>(ws);
   if (nblk > 0) {
     hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3(nblk), dim3(256), 4 * d * sizeof(float), s, dy, x, w, rstd,
-                       dres, T, d, dx, part);
+                       dres, T, d, dx, part, rpb);
     RTE_TRY(check_launch("rmsnorm_bwd"));
   }
   if (dw) {
     if (nblk == 0) return dw_accumulate ? 0 : fill_f32(dw, 0.0f, d, s);
-    hipLaunchKernelGGL(colsum_kernel, dim3((d + 63) / 64), dim3(256), 0, s, part, nblk, d, dw, dw_accumulate);
+    hipLaunchKernelGGL(colsum_kernel, dim3((d + 7) / 8), dim3(256), 0, s, part, nblk, d, dw, dw_accumulate);
     RTE_TRY(check_launch("rmsnorm_dw"));
   }
   return 0;

@@ -50,14 +50,49 @@ def _gemm_ws(M: int, N: int, K: int, device) -> tuple[int, int]:
     return workspace(_lib.load().rte_gemm_workspace_bytes(M, N, K), device)
 
 
+_BF16_CACHE: dict = {}
+_BF16_CACHE_ON = [False]
+
+
+def bf16_cache_begin() -> None:
+    """Start of a training step: from here on the bf16 copy of a parameter (or of a view of one,
+    e.g. a transposed weight) is made once and shared by every use until the next call.  The
+    step's parameters must not change in place before the next call (the optimizer step comes
+    last); call it at the start of every step, eager or captured."""
+    _BF16_CACHE.clear()
+    _BF16_CACHE_ON[0] = True
+
+
+def bf16_cache_end() -> None:
+    _BF16_CACHE.clear()
+    _BF16_CACHE_ON[0] = False
+
+
+def _cache_key(x: torch.Tensor):
+    """Parameters (and views of them) only; keyed by the current stream as well, so a copy made
+    on one stream is never read unsynchronised from another."""
+    base = x._base if x._base is not None else x
+    if not isinstance(base, torch.nn.Parameter):
+        return None
+    return (x.data_ptr(), tuple(x.shape), tuple(x.stride()), x._version, _lib.stream_ptr())
+
+
 def cast_bf16(x: torch.Tensor) -> torch.Tensor:
-    """fp32 -> bf16 (round to nearest even) with the HIP cast kernel."""
+    """fp32 -> bf16 (round to nearest even) with the HIP cast kernel; parameters hit the
+    per-step cache while one is open (bf16_cache_begin)."""
     if x.dtype == BF16:
         return x.contiguous()
     _lib.require_device_tensors("cast_bf16", x)
-    x = x.contiguous().to(F32)
-    y = torch.empty(x.shape, dtype=BF16, device=x.device)
-    call("rte_cast_f32_bf16", ptr(x), x.numel(), ptr(y), _s())
+    key = _cache_key(x) if _BF16_CACHE_ON[0] else None
+    if key is not None:
+        hit = _BF16_CACHE.get(key)
+        if hit is not None:
+            return hit
+    xc = x.contiguous().to(F32)
+    y = torch.empty(xc.shape, dtype=BF16, device=xc.device)
+    call("rte_cast_f32_bf16", ptr(xc), xc.numel(), ptr(y), _s())
+    if key is not None:
+        _BF16_CACHE[key] = y
     return y
 
 

@@ -20,7 +20,7 @@ import torch
 
 from rte_amd.audit import AuditEngine, AuditResult
 from rte_amd.config import ExperimentConfig, TrainingConfig
-from rte_amd.kernels import optimized
+from rte_amd.kernels import hip_ops, optimized
 from rte_amd.models import DenseModel, ModelOutput, RecursiveModel
 
 ACCELERATED_MODES = {"dense_exact", "recursive_exact", "recursive_macro", "recursive_macro_shortlist"}
@@ -163,6 +163,7 @@ class TrainEngine:
         if step and tr.grad_clip_norm is not None:
             params = [p for g in self.optimizer.param_groups for p in g["params"]]
             torch.nn.utils.clip_grad_norm_(params, tr.grad_clip_norm, foreach=True)
+        hip_ops.bf16_cache_end()  # parameters change below
         if step:
             self.last_grad_metrics = self._grad_metrics()
             self.optimizer.step()
@@ -174,6 +175,7 @@ class TrainEngine:
         return batch[0].to(self.device, non_blocking=True), batch[1].to(self.device, non_blocking=True)
 
     def train_step(self, batch, *, check_finite: bool = True) -> TrainStepResult:
+        hip_ops.bf16_cache_begin()  # one bf16 copy per weight per step
         mode = self.config.training.mode
         if mode == "dense_exact":
             return self._step_dense(batch, check_finite)
@@ -354,6 +356,7 @@ class TrainEngine:
 
     def _graph_body(self, st, shortlist: bool, check_finite: bool):
         """Device work of one captured step; everything here is replayed as recorded."""
+        hip_ops.bf16_cache_begin()
         tr = self.config.training
         m = self.recursive_model
         loss, hot, audit, aux, scale = self._macro_loss(st["tokens"], st["targets"], shortlist=shortlist,
@@ -366,6 +369,7 @@ class TrainEngine:
             params = [p for g in self.optimizer.param_groups for p in g["params"]]
             torch.nn.utils.clip_grad_norm_(params, tr.grad_clip_norm, foreach=True)
         self.last_grad_metrics = self._grad_metrics()
+        hip_ops.bf16_cache_end()  # parameters change below
         self.optimizer.found_inf = bad.float()
         self.optimizer.grad_scale = None
         try:
