@@ -224,6 +224,23 @@ int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, 
                            int d, const float* gain, const float* bias, const float* scale, float c, float* dh,
                            void* dlow, float* part, void* stream);
 
+/* ---- fused AdamW step with the trainer's per-group norms (replaces torch.optim.AdamW.step,
+ *      clip_grad_norm_ and _optimizer_grad_metrics of rte/training.py:385-468) ----
+ * rows: device array of n_tensors records {p, g, exp_avg, exp_avg_sq, step (f32 scalar) pointers,
+ *       numel, optimizer group, metric-group bit mask} (8 int64 each); g == 0 leaves the tensor
+ *       (and its step) untouched.  blocks: int32 pairs (tensor, chunk of rte_adamw_chunk()
+ *       elements), tensors' chunks consecutive; first_block[n_tensors + 1] their starts.
+ * hyper f64 [n_groups][5] = lr, beta1, beta2, eps, weight_decay.  metric_lr_group int32
+ *       [n_metrics]: the group whose lr scales metric j's update ratio.  clip_max <= 0: no clip.
+ * found_inf (optional device f32): > 0 skips the update and the step counters.
+ * metrics f32 [n_metrics][2] = grad norm (after clipping), lr * grad norm / max(param norm, 1e-12),
+ *       both from the values before the update.  Three launches, fixed reduction order. */
+int rte_adamw_chunk(void);
+size_t rte_adamw_workspace_bytes(int n_tensors, int n_blocks, int n_groups);
+int rte_adamw_step(const void* rows, int n_tensors, const int32_t* blocks, const int32_t* first_block, int n_blocks,
+                   const double* hyper, int n_groups, const int32_t* metric_lr_group, int n_metrics, float clip_max,
+                   const float* found_inf, float* metrics, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- hot-vs-exact distillation losses + alignment metrics of the audit (replaces
  *      macro_distill_loss rte/macro.py:394-471 and macro_alignment_metrics :499-546 on the
  *      path with the residual origin h0; rte/audit.py:326-352 calls both) ----

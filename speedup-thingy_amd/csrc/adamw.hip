@@ -1,0 +1,201 @@
+// Fused AdamW step over every parameter of a model, with the per-group gradient / parameter
+// norms the trainer reports (rte/training.py:385-443) and optional gradient clipping
+// (torch.nn.utils.clip_grad_norm_, rte/training.py:456-462), in three launches:
+//
+//   norms    : one workgroup per chunk of a tensor: partial sum(g^2), sum(p^2)
+//   finalize : one workgroup: per-tensor sums (chunks in order), per-metric-group sums (tensors
+//              in order), clip coefficient, metrics, step counters and bias corrections
+//   update   : one workgroup per chunk: torch AdamW (decoupled decay p -= lr wd p, moments
+//              m = b1 m + (1 - b1) g, v = b2 v + (1 - b2) g^2, p -= lr / (1 - b1^t) m /
+//              (sqrt(v) / sqrt(1 - b2^t) + eps)), skipped entirely when found_inf is set
+//
+// Tensors are described by a device table (one row per parameter, pointers and sizes) and a
+// block table (tensor, chunk) built once per layout, so the same three launches serve any
+// parameter set and can be captured in a graph.
+#include "common.hpp"
+
+namespace rte {
+
+namespace {
+
+constexpr int kChunk = 4096;  // elements per workgroup chunk (256 threads x 16)
+
+struct AdamRow {
+  int64_t p, g, m, v, step;  // pointers (g == 0: no gradient this step -> untouched)
+  int64_t numel;
+  int64_t group;             // optimizer group
+  int64_t metric_mask;       // bit j: tensor belongs to metric group j
+};
+
+__device__ __forceinline__ float bsum(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.0f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) t += red[i];
+  return t;
+}
+
+__global__ void __launch_bounds__(256) adamw_norms_kernel(const AdamRow* __restrict__ rows,
+                                                          const int32_t* __restrict__ blk, float* __restrict__ part) {
+  __shared__ float red[4];
+  const int b = blockIdx.x;
+  const AdamRow r = rows[blk[2 * b]];
+  const int64_t off = (int64_t)blk[2 * b + 1] * kChunk;
+  const float* p = reinterpret_cast<const float*>(r.p);
+  const float* g = reinterpret_cast<const float*>(r.g);
+  float sg = 0.0f, sp = 0.0f;
+  for (int64_t i = off + threadIdx.x; i < off + kChunk && i < r.numel; i += 256) {
+    const float x = p[i];
+    sp += x * x;
+    if (g) {
+      const float y = g[i];
+      sg += y * y;
+    }
+  }
+  sg = bsum(sg, red);
+  sp = bsum(sp, red);
+  if (threadIdx.x == 0) {
+    part[2 * b] = sg;
+    part[2 * b + 1] = sp;
+  }
+}
+
+// hyper per optimizer group (float64): lr, beta1, beta2, eps, weight_decay.
+// scal (out): scal[4 * G] = clip coefficient, scal[4 * G + 1] = 1 when the update runs.
+// metrics (out): per metric group j: grad_norm (after clipping), update_ratio = lr_j gn / max(pn, 1e-12).
+__global__ void __launch_bounds__(1024) adamw_finalize_kernel(const AdamRow* __restrict__ rows, int nt,
+                                                              const int32_t* __restrict__ first_blk,
+                                                              const float* __restrict__ part,
+                                                              const double* __restrict__ hyper, int G,
+                                                              const int32_t* __restrict__ metric_lr_group, int M,
+                                                              float clip_max, const float* __restrict__ found_inf,
+                                                              float* __restrict__ tsum, float* __restrict__ scal,
+                                                              float* __restrict__ metrics) {
+  __shared__ double acc[64][2];
+  __shared__ double gtot;
+  // per-tensor sums of their chunks, in chunk order
+  for (int i = threadIdx.x; i < nt; i += blockDim.x) {
+    double sg = 0.0, sp = 0.0;
+    for (int b = first_blk[i]; b < first_blk[i + 1]; ++b) {
+      sg += part[2 * b];
+      sp += part[2 * b + 1];
+    }
+    tsum[2 * i] = (float)sg;
+    tsum[2 * i + 1] = (float)sp;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int j = 0; j < 64; ++j) acc[j][0] = acc[j][1] = 0.0;
+    double tot = 0.0;
+    for (int i = 0; i < nt; ++i) {
+      const double sg = tsum[2 * i], sp = tsum[2 * i + 1];
+      tot += sg;
+      const int64_t mask = rows[i].metric_mask;
+      for (int j = 0; j < M; ++j)
+        if ((mask >> j) & 1) {
+          acc[j][0] += sg;
+          acc[j][1] += sp;
+        }
+    }
+    gtot = tot;
+  }
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  const bool skip = found_inf && *found_inf > 0.0f;
+  // torch.nn.utils.clip_grad_norm_: coef = max_norm / (total_norm + 1e-6), clamped to 1
+  float coef = 1.0f;
+  if (clip_max > 0.0f) {
+    const float tn = (float)sqrt(gtot);
+    coef = fminf(clip_max / (tn + 1e-6f), 1.0f);
+  }
+  for (int j = 0; j < M; ++j) {
+    const float gn = (float)sqrt(acc[j][0]) * coef;
+    const float pn = (float)sqrt(acc[j][1]);
+    const float lr = (float)hyper[5 * metric_lr_group[j]];
+    metrics[2 * j] = gn;
+    metrics[2 * j + 1] = lr * gn / fmaxf(pn, 1e-12f);
+  }
+  scal[4 * G] = coef;
+  scal[4 * G + 1] = skip ? 0.0f : 1.0f;
+  // step counters advance once per tensor with a gradient; bias corrections per tensor are
+  // derived from its own counter in the update kernel
+  if (!skip)
+    for (int i = 0; i < nt; ++i)
+      if (rows[i].g) *reinterpret_cast<float*>(rows[i].step) += 1.0f;
+}
+
+__global__ void __launch_bounds__(256) adamw_update_kernel(const AdamRow* __restrict__ rows,
+                                                           const int32_t* __restrict__ blk,
+                                                           const double* __restrict__ hyper, int G,
+                                                           const float* __restrict__ scal) {
+  if (scal[4 * G + 1] == 0.0f) return;  // found_inf: no update
+  const int b = blockIdx.x;
+  const AdamRow r = rows[blk[2 * b]];
+  if (!r.g) return;
+  const int64_t off = (int64_t)blk[2 * b + 1] * kChunk;
+  const int gi = (int)r.group;
+  // scalar coefficients in double (the betas' complements and bias corrections lose about
+  // 1e-5 relative when formed from float betas), applied in float
+  const double lr_d = hyper[5 * gi], b1_d = hyper[5 * gi + 1], b2_d = hyper[5 * gi + 2];
+  const double step_d = (double)*reinterpret_cast<const float*>(r.step);
+  const float b1 = (float)b1_d, b2 = (float)b2_d, omb1 = (float)(1.0 - b1_d), omb2 = (float)(1.0 - b2_d);
+  const float eps = (float)hyper[5 * gi + 3];
+  const float lr_wd = (float)(lr_d * hyper[5 * gi + 4]);
+  const float step_size = (float)(lr_d / (1.0 - pow(b1_d, step_d)));
+  const float bc2_sqrt = (float)sqrt(1.0 - pow(b2_d, step_d));
+  const float coef = scal[4 * G];
+  float* p = reinterpret_cast<float*>(r.p);
+  const float* g = reinterpret_cast<const float*>(r.g);
+  float* m = reinterpret_cast<float*>(r.m);
+  float* v = reinterpret_cast<float*>(r.v);
+  for (int64_t i = off + threadIdx.x; i < off + kChunk && i < r.numel; i += 256) {
+    const float gr = g[i] * coef;
+    float x = p[i];
+    x -= lr_wd * x;
+    const float mi = b1 * m[i] + omb1 * gr;
+    const float vi = b2 * v[i] + omb2 * gr * gr;
+    const float denom = sqrtf(vi) / bc2_sqrt + eps;
+    x -= step_size * (mi / denom);
+    m[i] = mi;
+    v[i] = vi;
+    p[i] = x;
+  }
+}
+
+}  // namespace
+
+int adamw_chunk() { return kChunk; }
+
+size_t adamw_workspace_bytes(int nt, int nblk, int G) {
+  return ((size_t)2 * nblk + 2 * (size_t)nt + 4 * (size_t)G + 8) * sizeof(float);
+}
+
+int adamw_step(const void* rows, int nt, const int32_t* blk, const int32_t* first_blk, int nblk, const double* hyper,
+               int G, const int32_t* metric_lr_group, int M, float clip_max, const float* found_inf, float* metrics,
+               void* ws, size_t ws_bytes, hipStream_t s) {
+  RTE_REQUIRE(nt >= 0 && nblk >= 0 && G >= 1 && M >= 0 && M <= 64, "adamw: bad table sizes (at most 64 metric groups)");
+  RTE_REQUIRE(ws_bytes >= adamw_workspace_bytes(nt, nblk, G), "adamw: workspace too small");
+  if (nt == 0) return 0;
+  float* part = static_cast<float*>(ws);
+  float* tsum = part + 2 * (size_t)nblk;
+  float* scal = tsum + 2 * (size_t)nt;
+  const AdamRow* r = static_cast<const AdamRow*>(rows);
+  if (nblk > 0) {
+    hipLaunchKernelGGL(adamw_norms_kernel, dim3(nblk), dim3(256), 0, s, r, blk, part);
+    RTE_TRY(check_launch("adamw_norms"));
+  }
+  hipLaunchKernelGGL(adamw_finalize_kernel, dim3(1), dim3(1024), 0, s, r, nt, first_blk, part, hyper, G,
+                     metric_lr_group, M, clip_max, found_inf, tsum, scal, metrics);
+  RTE_TRY(check_launch("adamw_finalize"));
+  if (nblk > 0) {
+    hipLaunchKernelGGL(adamw_update_kernel, dim3(nblk), dim3(256), 0, s, r, blk, hyper, G, scal);
+    RTE_TRY(check_launch("adamw_update"));
+  }
+  return 0;
+}
+
+}  // namespace rte

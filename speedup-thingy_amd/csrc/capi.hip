@@ -48,6 +48,11 @@ int macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int
 int macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int S, int d,
                        const float* gain, const float* bias, const float* scale, float c, float* dh, bf16* dlow,
                        float* part, hipStream_t s);
+int adamw_chunk();
+size_t adamw_workspace_bytes(int nt, int nblk, int G);
+int adamw_step(const void* rows, int nt, const int32_t* blk, const int32_t* first_blk, int nblk, const double* hyper,
+               int G, const int32_t* metric_lr_group, int M, float clip_max, const float* found_inf, float* metrics,
+               void* ws, size_t ws_bytes, hipStream_t s);
 size_t distill_workspace_bytes(int A, int R);
 int distill_fwd(const float* hot, const float* exact, const float* h0, int A, int S, int d, const float* hot_logits,
                 const float* exact_logits, int V, float t, float eps, float* losses, float* metrics, void* ws,
@@ -779,6 +784,19 @@ int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, 
                            int d, const float* gain, const float* bias, const float* scale, float c, float* dh,
                            void* dlow, float* part, void* stream) {
   return macro_epilogue_bwd(dout, h, low, key, B, seq, d, gain, bias, scale, c, dh, B16(dlow), part, S(stream));
+}
+
+int rte_adamw_chunk(void) { return adamw_chunk(); }
+
+size_t rte_adamw_workspace_bytes(int n_tensors, int n_blocks, int n_groups) {
+  return adamw_workspace_bytes(n_tensors, n_blocks, n_groups);
+}
+
+int rte_adamw_step(const void* rows, int n_tensors, const int32_t* blocks, const int32_t* first_block, int n_blocks,
+                   const double* hyper, int n_groups, const int32_t* metric_lr_group, int n_metrics, float clip_max,
+                   const float* found_inf, float* metrics, void* workspace, size_t workspace_bytes, void* stream) {
+  return adamw_step(rows, n_tensors, blocks, first_block, n_blocks, hyper, n_groups, metric_lr_group, n_metrics,
+                    clip_max, found_inf, metrics, workspace, workspace_bytes, S(stream));
 }
 
 size_t rte_distill_workspace_bytes(int A, int rows) { return distill_workspace_bytes(A, rows); }

@@ -22,6 +22,7 @@ from rte_amd.audit import AuditEngine, AuditResult
 from rte_amd.config import ExperimentConfig, TrainingConfig
 from rte_amd.kernels import hip_ops, optimized
 from rte_amd.models import DenseModel, ModelOutput, RecursiveModel
+from rte_amd.optim import FusedAdamW
 
 ACCELERATED_MODES = {"dense_exact", "recursive_exact", "recursive_macro", "recursive_macro_shortlist"}
 
@@ -119,10 +120,18 @@ class TrainEngine:
         return groups
 
     def _build_optimizer(self, groups):
-        kw: dict[str, Any] = {"weight_decay": self.config.training.weight_decay}
-        if self.device.type == "cuda" and self.config.training.fused_optimizer:
-            kw["fused"] = True
-        elif self.config.training.foreach_optimizer:
+        tr = self.config.training
+        if self.device.type == "cuda" and tr.fused_optimizer:
+            # HIP AdamW: clipping, update and the per-group norm metrics in three launches
+            extra = []
+            if self.recursive_model is not None:
+                core = self.recursive_model.core
+                extra = [("pass_film", [core.pass_gamma1, core.pass_beta1, core.pass_gamma2, core.pass_beta2], "core"),
+                         ("pass_scale", [core.pass_attn_scale, core.pass_mlp_scale], "core")]
+            return FusedAdamW(groups, weight_decay=tr.weight_decay, extra_metrics=extra,
+                              clip_grad_norm=tr.grad_clip_norm)
+        kw: dict[str, Any] = {"weight_decay": tr.weight_decay}
+        if tr.foreach_optimizer:
             kw["foreach"] = True
         return torch.optim.AdamW(groups, **kw)
 
@@ -160,13 +169,18 @@ class TrainEngine:
         (loss / tr.grad_accum_steps).backward()
         self.global_micro_step += 1
         step = self.global_micro_step % tr.grad_accum_steps == 0
-        if step and tr.grad_clip_norm is not None:
+        fused = isinstance(self.optimizer, FusedAdamW)
+        if step and tr.grad_clip_norm is not None and not fused:
             params = [p for g in self.optimizer.param_groups for p in g["params"]]
             torch.nn.utils.clip_grad_norm_(params, tr.grad_clip_norm, foreach=True)
         hip_ops.bf16_cache_end()  # parameters change below
         if step:
-            self.last_grad_metrics = self._grad_metrics()
-            self.optimizer.step()
+            if fused:  # clipping and metrics happen inside the fused step
+                self.optimizer.step()
+                self.last_grad_metrics = self.optimizer.metrics_dict()
+            else:
+                self.last_grad_metrics = self._grad_metrics()
+                self.optimizer.step()
             self.optimizer.zero_grad(set_to_none=True)
             self.global_step += 1
         return step
@@ -296,10 +310,11 @@ class TrainEngine:
                 raise ValueError("graph capture needs grad_accum_steps == 1")
             if self.audit_engine.config.audit_fixed_count_per_batch is None:
                 raise ValueError("graph capture needs the fixed-count audit sampler (its count is known on the host)")
-            if self.device.type != "cuda" or not isinstance(self.optimizer, torch.optim.AdamW):
-                raise ValueError("graph capture needs a ROCm device and the fused AdamW")
-            for g in self.optimizer.param_groups:
-                g["capturable"] = True
+            if self.device.type != "cuda" or not isinstance(self.optimizer, (FusedAdamW, torch.optim.AdamW)):
+                raise ValueError("graph capture needs a ROCm device and AdamW")
+            if not isinstance(self.optimizer, FusedAdamW):
+                for g in self.optimizer.param_groups:
+                    g["capturable"] = True
         self._graph_enabled = enabled
         self._graph_keep = keep_graph
         self._gstate = None
@@ -365,18 +380,27 @@ class TrainEngine:
         bad = (~torch.isfinite(loss.detach())) if check_finite else torch.zeros((), dtype=torch.bool,
                                                                                   device=loss.device)
         loss.backward()
-        if tr.grad_clip_norm is not None:
-            params = [p for g in self.optimizer.param_groups for p in g["params"]]
-            torch.nn.utils.clip_grad_norm_(params, tr.grad_clip_norm, foreach=True)
-        self.last_grad_metrics = self._grad_metrics()
         hip_ops.bf16_cache_end()  # parameters change below
-        self.optimizer.found_inf = bad.float()
-        self.optimizer.grad_scale = None
-        try:
-            self.optimizer.step()
-        finally:
-            del self.optimizer.found_inf
-            del self.optimizer.grad_scale
+        if isinstance(self.optimizer, FusedAdamW):
+            # clipping, update (skipped on a non-finite loss) and metrics in three launches
+            self.optimizer.found_inf = bad.float()
+            try:
+                self.optimizer.step()
+            finally:
+                self.optimizer.found_inf = None
+            self.last_grad_metrics = self.optimizer.metrics_dict()
+        else:
+            if tr.grad_clip_norm is not None:
+                params = [p for g in self.optimizer.param_groups for p in g["params"]]
+                torch.nn.utils.clip_grad_norm_(params, tr.grad_clip_norm, foreach=True)
+            self.last_grad_metrics = self._grad_metrics()
+            self.optimizer.found_inf = bad.float()
+            self.optimizer.grad_scale = None
+            try:
+                self.optimizer.step()
+            finally:
+                del self.optimizer.found_inf
+                del self.optimizer.grad_scale
         self.optimizer.zero_grad(set_to_none=True)
         m.recipe_bank.update_usage(hot.meta.recipe_ids, beta=tr.coverage_beta)
         metrics = self._macro_metrics(loss, hot, audit, aux, scale, st["targets"], shortlist, ~bad)

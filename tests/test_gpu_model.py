@@ -458,3 +458,62 @@ def test_macro_operator_grouped_matches_reference(scale_init):
         assert_rel(getattr(mac, k).grad.double().cpu().numpy(), tp[k].grad.numpy(), BF16_RTOL, f"macro d{k}")
     assert_rel(h.grad.double().cpu().numpy(), th.grad.numpy(), BF16_RTOL, "macro dh")
     assert_rel(h0.grad.double().cpu().numpy(), th0.grad.numpy(), BF16_RTOL, "macro dh0")
+
+
+# ---------------------------------------------------------------- fused AdamW
+
+@pytest.mark.parametrize("clip", [None, 0.5])
+def test_fused_adamw_matches_torch_adamw(clip):
+    """FusedAdamW against torch.optim.AdamW (float64 on the CPU, after the same
+    clip_grad_norm_) over three steps: two groups with their own lr / weight decay, a
+    parameter without a gradient, the per-group metrics of rte/training.py:385-443 and the
+    found_inf skip (no update, no step count)."""
+    from rte_amd.optim import FusedAdamW
+
+    torch.manual_seed(0)
+    shapes = [(300, 17), (4097,), (64, 64), (5,)]
+    init = [torch.randn(s) for s in shapes]
+    dev = [torch.nn.Parameter(t.clone().cuda()) for t in init]
+    ref = [torch.nn.Parameter(t.clone().double()) for t in init]
+    mk = lambda ps: [{"params": ps[:2], "lr": 1e-2, "name": "a"},  # noqa: E731
+                     {"params": ps[2:], "lr": 3e-3, "weight_decay": 0.0, "name": "b"}]
+    opt = FusedAdamW(mk(dev), weight_decay=0.1, extra_metrics=[("first_two", dev[:2], "b")], clip_grad_norm=clip)
+    ropt = torch.optim.AdamW(mk(ref), weight_decay=0.1, foreach=False)
+    for step in range(4):
+        grads = [torch.randn(s) * (1 + step) for s in shapes]
+        for i, (p, q) in enumerate(zip(dev, ref)):
+            if i == 3 and step == 1:  # no gradient for this parameter this step
+                p.grad = q.grad = None
+                continue
+            p.grad = grads[i].cuda()
+            q.grad = grads[i].double()
+        if step == 2:  # non-finite step: nothing changes
+            opt.found_inf = torch.ones((), device="cuda")
+            before = [p.detach().clone() for p in dev]
+            opt.step()
+            opt.found_inf = None
+            for a, b in zip(before, dev):
+                assert torch.equal(a, b.detach())
+            continue
+        if clip is not None:
+            torch.nn.utils.clip_grad_norm_([q for q in ref if q.grad is not None], clip)
+        gsq = {n: sum(float(q.grad.pow(2).sum()) for q in qs if q.grad is not None)
+               for n, qs in (("a", ref[:2]), ("b", ref[2:]), ("first_two", ref[:2]))}
+        psq = {n: sum(float(q.detach().pow(2).sum()) for q in qs)
+               for n, qs in (("a", ref[:2]), ("b", ref[2:]), ("first_two", ref[:2]))}
+        lrs = {"a": 1e-2, "b": 3e-3, "first_two": 3e-3}
+        opt.step()
+        ropt.step()
+        m = opt.metrics_dict()
+        for n in ("a", "b", "first_two"):
+            gn = gsq[n] ** 0.5
+            np.testing.assert_allclose(float(m[f"grad_norm_{n}"]), gn, rtol=1e-5)
+            np.testing.assert_allclose(float(m[f"update_ratio_{n}"]), lrs[n] * gn / max(psq[n] ** 0.5, 1e-12),
+                                       rtol=1e-5)
+        for p, q in zip(dev, ref):
+            assert_rel(p.detach().double().cpu().numpy(), q.detach().numpy(), 1e-5, "param")
+            st, rst = opt.state[p], ropt.state[q]
+            if rst:
+                assert float(st["step"]) == float(rst["step"])
+                assert_rel(st["exp_avg"].double().cpu().numpy(), rst["exp_avg"].numpy(), 1e-5, "exp_avg")
+                assert_rel(st["exp_avg_sq"].double().cpu().numpy(), rst["exp_avg_sq"].numpy(), 1e-5, "exp_avg_sq")
