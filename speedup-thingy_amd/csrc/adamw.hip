@@ -77,33 +77,52 @@ __global__ void __launch_bounds__(1024) adamw_finalize_kernel(const AdamRow* __r
                                                               float* __restrict__ metrics) {
   __shared__ double acc[64][2];
   __shared__ double gtot;
-  // per-tensor sums of their chunks, in chunk order
-  for (int i = threadIdx.x; i < nt; i += blockDim.x) {
+  extern __shared__ double ts[];  // [nt][2] per-tensor sums, then [nt] metric masks
+  int64_t* tmask = reinterpret_cast<int64_t*>(ts + 2 * nt);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  // per-tensor sums: one wave per tensor, lanes stride its chunks, then a fixed xor tree
+  for (int i = wave; i < nt; i += nw) {
     double sg = 0.0, sp = 0.0;
-    for (int b = first_blk[i]; b < first_blk[i + 1]; ++b) {
+    for (int b = first_blk[i] + lane; b < first_blk[i + 1]; b += 64) {
       sg += part[2 * b];
       sp += part[2 * b + 1];
     }
-    tsum[2 * i] = (float)sg;
-    tsum[2 * i + 1] = (float)sp;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+      sg += __shfl_xor(sg, off, 64);
+      sp += __shfl_xor(sp, off, 64);
+    }
+    if (lane == 0) {
+      ts[2 * i] = sg;
+      ts[2 * i + 1] = sp;
+      tmask[i] = rows[i].metric_mask;
+      tsum[2 * i] = (float)sg;
+      tsum[2 * i + 1] = (float)sp;
+    }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    for (int j = 0; j < 64; ++j) acc[j][0] = acc[j][1] = 0.0;
+  // metric group j (thread j) and the global total (thread 64) sum the tensors in order
+  if (threadIdx.x < M) {
+    const int j = threadIdx.x;
+    double sg = 0.0, sp = 0.0;
+    for (int i = 0; i < nt; ++i)
+      if ((tmask[i] >> j) & 1) {
+        sg += ts[2 * i];
+        sp += ts[2 * i + 1];
+      }
+    acc[j][0] = sg;
+    acc[j][1] = sp;
+  } else if (threadIdx.x == 64) {
     double tot = 0.0;
-    for (int i = 0; i < nt; ++i) {
-      const double sg = tsum[2 * i], sp = tsum[2 * i + 1];
-      tot += sg;
-      const int64_t mask = rows[i].metric_mask;
-      for (int j = 0; j < M; ++j)
-        if ((mask >> j) & 1) {
-          acc[j][0] += sg;
-          acc[j][1] += sp;
-        }
-    }
+    for (int i = 0; i < nt; ++i) tot += ts[2 * i];
     gtot = tot;
   }
   __syncthreads();
+  const bool skip_all = found_inf && *found_inf > 0.0f;
+  // step counters advance once per tensor with a gradient (in parallel)
+  if (!skip_all)
+    for (int i = threadIdx.x; i < nt; i += blockDim.x)
+      if (rows[i].g) *reinterpret_cast<float*>(rows[i].step) += 1.0f;
   if (threadIdx.x != 0) return;
   const bool skip = found_inf && *found_inf > 0.0f;
   // torch.nn.utils.clip_grad_norm_: coef = max_norm / (total_norm + 1e-6), clamped to 1
@@ -121,11 +140,6 @@ __global__ void __launch_bounds__(1024) adamw_finalize_kernel(const AdamRow* __r
   }
   scal[4 * G] = coef;
   scal[4 * G + 1] = skip ? 0.0f : 1.0f;
-  // step counters advance once per tensor with a gradient; bias corrections per tensor are
-  // derived from its own counter in the update kernel
-  if (!skip)
-    for (int i = 0; i < nt; ++i)
-      if (rows[i].g) *reinterpret_cast<float*>(rows[i].step) += 1.0f;
 }
 
 __global__ void __launch_bounds__(256) adamw_update_kernel(const AdamRow* __restrict__ rows,
@@ -188,7 +202,9 @@ int adamw_step(const void* rows, int nt, const int32_t* blk, const int32_t* firs
     hipLaunchKernelGGL(adamw_norms_kernel, dim3(nblk), dim3(256), 0, s, r, blk, part);
     RTE_TRY(check_launch("adamw_norms"));
   }
-  hipLaunchKernelGGL(adamw_finalize_kernel, dim3(1), dim3(1024), 0, s, r, nt, first_blk, part, hyper, G,
+  const size_t lds = (size_t)3 * nt * sizeof(double);
+  RTE_REQUIRE(lds <= 60 * 1024, "adamw: at most 2560 tensors");
+  hipLaunchKernelGGL(adamw_finalize_kernel, dim3(1), dim3(1024), lds, s, r, nt, first_blk, part, hyper, G,
                      metric_lr_group, M, clip_max, found_inf, tsum, scal, metrics);
   RTE_TRY(check_launch("adamw_finalize"));
   if (nblk > 0) {
