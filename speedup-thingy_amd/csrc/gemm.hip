@@ -296,6 +296,109 @@ __device__ __forceinline__ void lds_dma16(const void* src, void* lds_base) {
 #endif
 }
 
+// Four bf16 of a k-major LDS tile, transposed across the 16 lanes of each lane group
+// (ds_read_b64_tr_b16, gfx950).  Measured lane layout: within a group of 16 lanes, lane i
+// receives element (i % 4) of the 8-byte rows that lanes 4j + i / 4 (j = 0..3) point at, in j
+// order.  So if lane s of the group points at k-row (kb + s / 4) and columns (cb + 4 (s % 4))..+3,
+// lane i gets column cb + i at k-rows kb..kb + 3: an MFMA operand fragment.
+typedef short short4_v __attribute__((ext_vector_type(4)));
+
+// 16 zero bytes in global memory: the source of direct loads past the end of a k range (a
+// layout-T tile's rows beyond the group of a grouped-K problem), so LDS gets exact zeros.
+__device__ __align__(16) unsigned int kDlZero[4] = {0u, 0u, 0u, 0u};  // never written
+__device__ __forceinline__ short4_v lds_read_tr4(const unsigned char* lds_byte_ptr) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_v*)lds_byte_ptr);
+#else
+  (void)lds_byte_ptr;
+  return short4_v{0, 0, 0, 0};
+#endif
+}
+
+// One operand of the direct-to-LDS main loop: R tile rows (the output index i) by BK k per
+// stage.  Layout N (k contiguous in memory): LDS rows are i, BK * 2 bytes each, chunk c (8 k)
+// at c ^ dl_swz(i).  Layout T (i contiguous): LDS rows are k, R * 2 bytes each, chunk c (8 i)
+// at c ^ tr_swz(k); the MFMA fragments then come out of ds_read_b64_tr_b16 pairs.
+template <int R, int BK, bool T>
+struct DlOperand {
+  static constexpr int ROWB = T ? R * 2 : BK * 2;  // bytes per LDS row
+  static constexpr int CPR = ROWB / 16;            // 16-byte chunks per LDS row
+  static constexpr int BYTES = R * BK * 2;
+  static constexpr int INS = BYTES / 16 / kThreads;  // loads per thread per stage
+  static_assert(INS >= 1, "tile too small for one load per thread");
+  static_assert(!T || CPR >= 4, "layout-T tiles need at least 32 columns");
+
+  // k-rows r, r+1, r+2, r+3 of a layout-T tile land in four distinct 64-byte windows of the
+  // row (XOR of the window index), so the 8 rows read by one ds_read_b64_tr_b16 spread over
+  // the banks.
+  __device__ __forceinline__ static int tr_swz(int krow) { return (krow % (CPR / 4)) * 4; }
+
+  const bf16* ptr[INS];
+  int off[INS];  // N: k offset of the chunk; T: k-row of the load within the stage
+
+  __device__ __forceinline__ void init(const Operand& o, const bf16* base, int64_t shift, int i0, int ilim,
+                                       int tid) {
+#pragma unroll
+    for (int u = 0; u < INS; ++u) {
+      const int q = u * kThreads + tid, row = q / CPR, pc = q % CPR;
+      if constexpr (!T) {
+        int i = i0 + row;
+        if (i >= ilim) i = ilim - 1;
+        ptr[u] = base + row_off(o, i + shift);
+        off[u] = (pc ^ dl_swz<CPR>(row)) * 8;
+      } else {
+        int i = i0 + (pc ^ tr_swz(row)) * 8;
+        if (i + 8 > ilim) i = ilim - 8;  // layout-T extents are multiples of 8
+        ptr[u] = base + col_off(o, i);
+        off[u] = row;
+      }
+    }
+  }
+  // global source of load u for the stage starting at k0 (k rows from klim on read zeros;
+  // layout-N k ranges are whole stages)
+  __device__ __forceinline__ const void* src(const Operand& o, int64_t shift, int k0, int klim, int u,
+                                             bool plain) const {
+    if constexpr (!T) {
+      return ptr[u] + (plain ? (int64_t)(k0 + off[u]) : col_off(o, k0 + off[u]));
+    } else {
+      const int k = k0 + off[u];
+      if (k >= klim) return kDlZero;
+      return ptr[u] + row_off(o, (int64_t)k + shift);
+    }
+  }
+  // per-lane fragment addresses of the 32-row blocks of this wave (rows rb + 32 b)
+  template <int NB>
+  __device__ __forceinline__ static void frag_offsets(int rb, int lane, int (&fo)[NB], int (&fs)[NB]) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if constexpr (!T) {
+        const int r = rb + 32 * b + (lane & 31);
+        fo[b] = r * ROWB;
+        fs[b] = dl_swz<CPR>(r);
+      } else {
+        const int g = lane >> 4, s = lane & 15;
+        const int kr = 8 * (g >> 1) + (s >> 2);           // k-row of this lane's 8-byte read
+        const int col = rb + 32 * b + 16 * (g & 1) + 4 * (s & 3);
+        fo[b] = kr * ROWB + (((col >> 3) ^ tr_swz(kr)) << 4) + (col & 7) * 2;
+        fs[b] = 0;
+      }
+    }
+  }
+  // MFMA operand of block b at k-step ks (16 k)
+  __device__ __forceinline__ static bf16x8_v frag(const unsigned char* st, int fo, int fs, int ks, int lane) {
+    if constexpr (!T) {
+      const int c = ks * 2 + (lane >> 5);
+      return *reinterpret_cast<const bf16x8_v*>(st + fo + ((c ^ fs) << 4));
+    } else {
+      const short4_v lo = lds_read_tr4(st + fo + (ks * 16) * ROWB);
+      const short4_v hi = lds_read_tr4(st + fo + (ks * 16 + 4) * ROWB);
+      typedef short short8_v __attribute__((ext_vector_type(8)));
+      const short8_v v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      return __builtin_bit_cast(bf16x8_v, v);
+    }
+  }
+};
+
 // s_waitcnt with vmcnt <= n and the other counters unconstrained (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -306,8 +409,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI, bool DUALA = false, int DLS = 0>
 __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS>())) gemm_kernel(GemmArgs p, EpiFlags fl) {
   static_assert(!DUALA || (EPI == EPI_SWIGLU_FWD && !AT), "dual-A is a SwiGLU-forward layout-N mode");
-  static_assert(DLS == 0 || (!AT && !BT && !DUALA && (BK == 64 || BK == 32) && DLS >= 2 && DLS <= 4),
-                "direct-to-LDS loads: layout-N operands, BK 32 or 64, 2 to 4 stages");
+  static_assert(DLS == 0 || (!DUALA && (BK == 64 || BK == 32) && DLS >= 2 && DLS <= 4),
+                "direct-to-LDS loads: BK 32 or 64, 2 to 4 stages");
   constexpr int LDP = BK + 8;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -409,77 +512,41 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS>())) gemm_kern
 
   if constexpr (DLS > 0) {
     // Global -> LDS without registers (global_load_lds_dwordx4): load u of thread tid fills
-    // 16-byte unit q = u * 256 + tid of the stage, i.e. row q / CPR at chunk position q % CPR,
-    // which holds logical chunk (q % CPR) ^ swz(row).  Rows past the tile's limit re-read the
-    // last valid row; their results are never stored.  The k range is a multiple of BK.
-    constexpr int CPR = BK / 8, ROWB = BK * 2;
-    constexpr int A_INS = BM * CPR / kThreads, B_INS = BN * CPR / kThreads;
-    constexpr int A_BYTES = BM * ROWB, STAGE = (BM + BN) * ROWB;
-    static_assert(A_INS >= 1 && B_INS >= 1, "tile too small for one load per thread");
+    // 16-byte unit q = u * 256 + tid of the operand's stage tile (see DlOperand for the row /
+    // chunk layouts).  Tile rows or columns past the operand's extent re-read the last valid
+    // ones; their results are never stored.  The k range is a multiple of BK.
+    using OpA = DlOperand<BM, BK, AT>;
+    using OpB = DlOperand<BN, BK, BT>;
+    constexpr int A_INS = OpA::INS, B_INS = OpB::INS;
+    constexpr int A_BYTES = OpA::BYTES, STAGE = OpA::BYTES + OpB::BYTES;
     const int wv = __builtin_amdgcn_readfirstlane(wave);
-    const bf16* ap[A_INS];
-    const bf16* bp[B_INS];
-    int ac[A_INS], bc[B_INS];
-#pragma unroll
-    for (int u = 0; u < A_INS; ++u) {
-      const int q = u * kThreads + tid, row = q / CPR;
-      int i = m0 + row;
-      if (i >= mlim) i = mlim - 1;
-      ap[u] = abase + row_off(p.a, i + ashift);
-      ac[u] = ((q % CPR) ^ dl_swz<CPR>(row)) * 8;
-    }
-#pragma unroll
-    for (int u = 0; u < B_INS; ++u) {
-      const int q = u * kThreads + tid, row = q / CPR;
-      int i = n0 + row;
-      if (i >= p.N) i = p.N - 1;
-      bp[u] = bbase + row_off(p.b, i + bshift);
-      bc[u] = ((q % CPR) ^ dl_swz<CPR>(row)) * 8;
-    }
-    const bool plain_cols = p.a.cdiv == 0 && p.b.cdiv == 0;  // uniform: k offsets are affine
+    OpA la;
+    OpB lb;
+    la.init(p.a, abase, ashift, m0, mlim, tid);
+    lb.init(p.b, bbase, bshift, n0, p.N, tid);
+    const bool plain_cols = p.a.cdiv == 0 && p.b.cdiv == 0;  // uniform: layout-N k offsets are affine
     auto issue = [&](int stage, int t) {
       const int k0 = kbeg + t * BK;
       unsigned char* dst = smem_raw + stage * STAGE + wv * 1024;
-      if (plain_cols) {
 #pragma unroll
-        for (int u = 0; u < A_INS; ++u)
-          lds_dma16(ap[u] + (k0 + ac[u]), dst + u * 4096);
+      for (int u = 0; u < A_INS; ++u) lds_dma16(la.src(p.a, ashift, k0, kend, u, plain_cols), dst + u * 4096);
 #pragma unroll
-        for (int u = 0; u < B_INS; ++u)
-          lds_dma16(bp[u] + (k0 + bc[u]), dst + A_BYTES + u * 4096);
-      } else {
-#pragma unroll
-        for (int u = 0; u < A_INS; ++u)
-          lds_dma16(ap[u] + col_off(p.a, k0 + ac[u]), dst + u * 4096);
-#pragma unroll
-        for (int u = 0; u < B_INS; ++u)
-          lds_dma16(bp[u] + col_off(p.b, k0 + bc[u]), dst + A_BYTES + u * 4096);
-      }
+      for (int u = 0; u < B_INS; ++u)
+        lds_dma16(lb.src(p.b, bshift, k0, kend, u, plain_cols), dst + A_BYTES + u * 4096);
     };
-    // operand rows of this lane and their swizzles
+    // fragment addresses of this lane
     int aoff[TM], asw[TM], boff[TN], bsw[TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int r = wm * WTM + i * 32 + (lane & 31);
-      aoff[i] = r * ROWB;
-      asw[i] = dl_swz<CPR>(r);
-    }
-#pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int r = wn * WTN + j * 32 + (lane & 31);
-      boff[j] = A_BYTES + r * ROWB;
-      bsw[j] = dl_swz<CPR>(r);
-    }
+    OpA::frag_offsets(wm * WTM, lane, aoff, asw);
+    OpB::frag_offsets(wn * WTN, lane, boff, bsw);
     auto compute = [&](int stage) {
       const unsigned char* st = smem_raw + stage * STAGE;
 #pragma unroll
       for (int ks = 0; ks < BK / 16; ++ks) {
-        const int c = ks * 2 + (lane >> 5);
         bf16x8_v af[TM], bfr[TN];
 #pragma unroll
-        for (int i = 0; i < TM; ++i) af[i] = *reinterpret_cast<const bf16x8_v*>(st + aoff[i] + ((c ^ asw[i]) << 4));
+        for (int i = 0; i < TM; ++i) af[i] = OpA::frag(st, aoff[i], asw[i], ks, lane);
 #pragma unroll
-        for (int j = 0; j < TN; ++j) bfr[j] = *reinterpret_cast<const bf16x8_v*>(st + boff[j] + ((c ^ bsw[j]) << 4));
+        for (int j = 0; j < TN; ++j) bfr[j] = OpB::frag(st + A_BYTES, boff[j], bsw[j], ks, lane);
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -487,7 +554,8 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS>())) gemm_kern
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
       }
     };
-    const int nk = (kend - kbeg) / BK;
+    // whole stages; a grouped-K tail (both operands layout T) reads zero rows past kend
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
 #pragma unroll
     for (int t = 0; t < DLS - 1; ++t)
       if (t < nk) issue(t, t);
@@ -1008,19 +1076,46 @@ int dl_mode(const GemmArgs& p) {
 
 bool dl_ok(const GemmArgs& p) {
   const int mode = dl_mode(p);
+  if (mode == 0 || p.a_koff2 || p.K <= 0) return false;
   const int bk = mode >= 5 ? 32 : 64;
-  return mode != 0 && !p.a_t && !p.b_t && p.mode != MODE_GROUP_K && p.K % bk == 0 && p.K > 0 && !p.a_koff2;
+  // dense / grouped-M: whole stages over K; grouped-K (both operands layout T): any group sizes
+  if (p.mode == MODE_GROUP_K) return p.a_t && p.b_t;
+  return p.K % bk == 0;
+}
+
+template <int BM, int BK, int DLS, int EPI>
+int launch_dl_layouts(const GemmArgs& p, hipStream_t stream, void* ws, size_t ws_bytes, int vec) {
+  if (!p.a_t && !p.b_t) return launch_cfg<BM, 128, BK, 2, 2, false, false, EPI, false, DLS>(p, stream, ws, ws_bytes, vec);
+  if constexpr (EPI == EPI_STORE) {
+    if (!p.a_t) return launch_cfg<BM, 128, BK, 2, 2, false, true, EPI, false, DLS>(p, stream, ws, ws_bytes, vec);
+    if (!p.b_t) return launch_cfg<BM, 128, BK, 2, 2, true, false, EPI, false, DLS>(p, stream, ws, ws_bytes, vec);
+    return launch_cfg<BM, 128, BK, 2, 2, true, true, EPI, false, DLS>(p, stream, ws, ws_bytes, vec);
+  }
+  set_error("gemm: direct-load layout-T operands need the plain store epilogue");
+  return -1;
+}
+
+// Tile height: 128 rows when that already gives two workgroups per CU or when the reduction
+// is long enough to split instead (K > 2048), else 64 (dense only: grouped modes keep their
+// 128-row tiles).
+template <int BK, int DLS, int EPI>
+int launch_dl_shape(const GemmArgs& p, hipStream_t stream, void* ws, size_t ws_bytes, int vec) {
+  const int64_t tiles128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
+  if (p.mode == MODE_DENSE && tiles128 < 512 && p.M > 64 && p.K <= 2048)
+    return launch_dl_layouts<64, BK, DLS, EPI>(p, stream, ws, ws_bytes, vec);
+  return launch_dl_layouts<128, BK, DLS, EPI>(p, stream, ws, ws_bytes, vec);
 }
 
 template <int EPI>
 int launch_dl(const GemmArgs& p, hipStream_t stream, void* ws, size_t ws_bytes, int vec) {
-  switch (dl_mode(p)) {
+  const bool nn = !p.a_t && !p.b_t;
+  switch (nn ? dl_mode(p) : (dl_mode(p) >= 5 ? 7 : 2)) {  // layout T: the two default shapes
     case 3: return launch_cfg<128, 128, 64, 2, 2, false, false, EPI, false, 3>(p, stream, ws, ws_bytes, vec);
     case 4: return launch_cfg<256, 128, 64, 2, 2, false, false, EPI, false, 2>(p, stream, ws, ws_bytes, vec);
     case 5: return launch_cfg<128, 128, 32, 2, 2, false, false, EPI, false, 4>(p, stream, ws, ws_bytes, vec);
     case 6: return launch_cfg<128, 128, 32, 2, 2, false, false, EPI, false, 3>(p, stream, ws, ws_bytes, vec);
-    case 7: return launch_cfg<128, 128, 32, 2, 2, false, false, EPI, false, 2>(p, stream, ws, ws_bytes, vec);
-    default: return launch_cfg<128, 128, 64, 2, 2, false, false, EPI, false, 2>(p, stream, ws, ws_bytes, vec);
+    case 7: return launch_dl_shape<32, 2, EPI>(p, stream, ws, ws_bytes, vec);
+    default: return launch_dl_shape<64, 2, EPI>(p, stream, ws, ws_bytes, vec);
   }
 }
 

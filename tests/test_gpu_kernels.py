@@ -81,6 +81,24 @@ def test_gemm_layout_nn_k64_shapes(M, N, K):
     assert_rel(_np(cb), ref, 5e-3, "gemm nn bf16")
 
 
+@pytest.mark.parametrize("a_t,b_t", [(False, True), (True, False), (True, True)])
+@pytest.mark.parametrize("M,N,K", [(136, 200, 64), (512, 384, 512), (1000, 520, 192), (2048, 1536, 2112)])
+def test_gemm_layout_t_k64_shapes(a_t, b_t, M, N, K):
+    """Layout-T operands on the direct-to-LDS main loop (k-major LDS tiles read through the
+    transposing LDS loads): ragged tile edges, one to 33 k stages, split-K on the small grids."""
+    H = _ops()
+    rng = np.random.default_rng(M + 5 * N + K + 2 * a_t + b_t)
+    A_ = bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    B_ = bf16_round(rng.standard_normal((N, K)).astype(np.float32))
+    ref = A_.astype(np.float64) @ B_.astype(np.float64).T
+    a = _bf(A_.T.copy() if a_t else A_)
+    b = _bf(B_.T.copy() if b_t else B_)
+    print(f"gemm T a_t={a_t} b_t={b_t} M={M} N={N} K={K}", flush=True)
+    c = H.gemm(a, b, a_t=a_t, b_t=b_t, out_f32=True)
+    torch.cuda.synchronize()
+    assert_rel(_np(c), ref, FP32_RTOL, "gemm layout T fp32")
+
+
 def test_gemm_bf16_out_resid_alpha():
     H = _ops()
     rng = np.random.default_rng(3)
