@@ -261,12 +261,19 @@ struct EpiFlags {
 // ------------------------------------------------------------------ kernel
 
 // Tiles larger than 128x128 keep one workgroup per CU (their LDS and accumulators fill it).
-template <int BM, int BN, int BK = 64, int DLS = 0>
+// Row slices of the direct-load kernels' staged epilogue: two when each wave's rows fit one half.
+template <int BM, int WM, int DLS>
+constexpr int dl_slices() {
+  return (DLS > 0 && BM >= 64 && ((BM / 2) % (BM / WM)) == 0) ? 2 : 1;
+}
+
+template <int BM, int BN, int BK = 64, int DLS = 0, int WM = 2>
 constexpr int wg_per_cu() {
   if constexpr (DLS > 0) {
     // direct-load kernels: as many workgroups as their LDS allows, at most 4
-    constexpr int lds = DLS * (BM + BN) * BK * 2 > (BM / 2) * (BN + 8) * 4 ? DLS * (BM + BN) * BK * 2
-                                                                          : (BM / 2) * (BN + 8) * 4;
+    constexpr int rows = BM / dl_slices<BM, WM, DLS>();
+    constexpr int lds = DLS * (BM + BN) * BK * 2 > rows * (BN + 8) * 4 ? DLS * (BM + BN) * BK * 2
+                                                                      : rows * (BN + 8) * 4;
     constexpr int n = 163840 / lds;
     return n < 1 ? 1 : (n > 4 ? 4 : n);
   }
@@ -407,7 +414,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI, bool DUALA = false, int DLS = 0>
-__global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS>())) gemm_kernel(GemmArgs p, EpiFlags fl) {
+__global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS, WM>())) gemm_kernel(GemmArgs p, EpiFlags fl) {
   static_assert(!DUALA || (EPI == EPI_SWIGLU_FWD && !AT), "dual-A is a SwiGLU-forward layout-N mode");
   static_assert(DLS == 0 || (!DUALA && (BK == 64 || BK == 32) && DLS >= 2 && DLS <= 4),
                 "direct-to-LDS loads: BK 32 or 64, 2 to 4 stages");
@@ -664,7 +671,7 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS>())) gemm_kern
 
   if constexpr (EPI == EPI_STORE) {
     // the direct-load kernels stage the tile in NH row slices so their LDS stays small
-    constexpr int CP = BN + 8, NH = DLS > 0 ? 2 : 1, HR = BM / NH;
+    constexpr int CP = BN + 8, NH = dl_slices<BM, WM, DLS>(), HR = BM / NH;
     static_assert(HR % WTM == 0, "a wave's rows lie in one slice");
     float* Cs = reinterpret_cast<float*>(smem_raw);
     for (int h = 0; h < NH; ++h) {
@@ -828,7 +835,7 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS>())) gemm_kern
     // Stage the fp32 tile, then each thread rotates and writes 8 consecutive columns of one
     // row: the RoPE pairs (2i, 2i+1) sit inside the chunk, and the chunk's cos / sin values
     // are two 16-byte loads each.
-    constexpr int CP = BN + 4, NH = DLS > 0 ? 2 : 1, HR = BM / NH;
+    constexpr int CP = BN + 4, NH = dl_slices<BM, WM, DLS>(), HR = BM / NH;
     static_assert(HR % WTM == 0, "a wave's rows lie in one slice");
     float* Cs = reinterpret_cast<float*>(smem_raw);
     for (int h = 0; h < NH; ++h) {
@@ -957,11 +964,11 @@ int groupk_chunk(int K, int G) {
 
 size_t groupk_first_bytes(int G) { return (((size_t)(G + 1) * 4 + 255) / 256) * 256; }
 
-template <int BM, int BN, int BK, int EPI, bool DUALA = false, int DLS = 0>
+template <int BM, int BN, int BK, int EPI, bool DUALA = false, int DLS = 0, int WM = 2>
 constexpr size_t lds_bytes() {
   constexpr size_t main_loop = DLS > 0 ? (size_t)DLS * (BM + BN) * BK * 2
                                        : (size_t)2 * ((DUALA ? 2 : 1) * BM + BN) * (BK + 8) * 2;
-  constexpr size_t rows = DLS > 0 ? BM / 2 : BM;  // direct-load kernels stage the output in two slices
+  constexpr size_t rows = BM / dl_slices<BM, WM, DLS>();  // direct-load kernels stage it in slices
   constexpr size_t epi = EPI == EPI_STORE        ? rows * (BN + 8) * 4
                          : EPI == EPI_SWIGLU_FWD ? (size_t)BM * (BN + 8) * 2 + (size_t)BM * (BN / 2 + 8) * 2
                          : EPI == EPI_SWIGLU_BWD ? (size_t)BM * (2 * BN + 8) * 2
@@ -971,7 +978,7 @@ constexpr size_t lds_bytes() {
 
 template <int BM, int BN, int BK, int WM, int WN, bool AT, bool BT, int EPI, bool DUALA = false, int DLS = 0>
 int launch_cfg(const GemmArgs& p0, hipStream_t stream, void* ws, size_t ws_bytes, int vec) {
-  constexpr size_t lds = lds_bytes<BM, BN, BK, EPI, DUALA, DLS>();
+  constexpr size_t lds = lds_bytes<BM, BN, BK, EPI, DUALA, DLS, WM>();
   auto fn = gemm_kernel<BM, BN, BK, WM, WN, AT, BT, EPI, DUALA, DLS>;
   static bool attr_done = false;
   if (!attr_done) {
@@ -1106,6 +1113,16 @@ int launch_dl_shape(const GemmArgs& p, hipStream_t stream, void* ws, size_t ws_b
   return launch_dl_layouts<128, BK, DLS, EPI>(p, stream, ws, ws_bytes, vec);
 }
 
+// Narrow tiles (a 32- or 64-wide side) on the direct-load loop, any operand layouts; BK 64
+// (a 32-row tile holds one 16-byte load per thread only at BK 64).
+template <int BM, int BN, int WM, int WN>
+int launch_dl_narrow(const GemmArgs& p, hipStream_t stream, void* ws, size_t ws_bytes, int vec) {
+  if (!p.a_t && !p.b_t) return launch_cfg<BM, BN, 64, WM, WN, false, false, EPI_STORE, false, 2>(p, stream, ws, ws_bytes, vec);
+  if (!p.a_t) return launch_cfg<BM, BN, 64, WM, WN, false, true, EPI_STORE, false, 2>(p, stream, ws, ws_bytes, vec);
+  if (!p.b_t) return launch_cfg<BM, BN, 64, WM, WN, true, false, EPI_STORE, false, 2>(p, stream, ws, ws_bytes, vec);
+  return launch_cfg<BM, BN, 64, WM, WN, true, true, EPI_STORE, false, 2>(p, stream, ws, ws_bytes, vec);
+}
+
 template <int EPI>
 int launch_dl(const GemmArgs& p, hipStream_t stream, void* ws, size_t ws_bytes, int vec) {
   const bool nn = !p.a_t && !p.b_t;
@@ -1178,15 +1195,25 @@ int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream, void* ws, s
   }
 
   switch (epi_kind) {
-    case EPI_STORE:
-      if (p.M <= 32) return launch_layouts<32, 128, 64, 1, 4, EPI_STORE>(p, stream, ws, ws_bytes, vec);
+    case EPI_STORE: {
+      // narrow problems: the direct-load loop when the reduction is whole 64-k stages (or
+      // grouped-K over layout-T operands), else the register-staged loop
+      const bool dl64 = dl_ok(p) && (p.mode == MODE_GROUP_K || p.K % 64 == 0);
+      if (p.M <= 32)
+        return dl64 ? launch_dl_narrow<32, 128, 1, 4>(p, stream, ws, ws_bytes, vec)
+                    : launch_layouts<32, 128, 64, 1, 4, EPI_STORE>(p, stream, ws, ws_bytes, vec);
       if (p.M <= 64 && p.mode != MODE_GROUP_M)
-        return launch_layouts<64, 128, 64, 2, 2, EPI_STORE>(p, stream, ws, ws_bytes, vec);
-      if (p.N <= 64) return launch_layouts<128, 64, 64, 4, 1, EPI_STORE>(p, stream, ws, ws_bytes, vec);
+        return dl64 ? launch_dl_narrow<64, 128, 2, 2>(p, stream, ws, ws_bytes, vec)
+                    : launch_layouts<64, 128, 64, 2, 2, EPI_STORE>(p, stream, ws, ws_bytes, vec);
+      if (p.N <= 32 && dl64) return launch_dl_narrow<128, 32, 4, 1>(p, stream, ws, ws_bytes, vec);
+      if (p.N <= 64)
+        return dl64 ? launch_dl_narrow<128, 64, 4, 1>(p, stream, ws, ws_bytes, vec)
+                    : launch_layouts<128, 64, 64, 4, 1, EPI_STORE>(p, stream, ws, ws_bytes, vec);
       if (p.K <= 32 && p.mode != MODE_GROUP_K)
         return launch_layouts<128, 128, 32, 2, 2, EPI_STORE>(p, stream, ws, ws_bytes, vec);
       if (dl_ok(p)) return launch_dl<EPI_STORE>(p, stream, ws, ws_bytes, vec);
       return launch_layouts<128, 128, 64, 2, 2, EPI_STORE>(p, stream, ws, ws_bytes, vec);
+    }
     case EPI_SWIGLU_FWD:
       RTE_REQUIRE(!p.a_t && !p.b_t, "gemm: SwiGLU forward expects layout-N operands");
       RTE_REQUIRE(p.N % 64 == 0, "gemm: SwiGLU forward needs N %% 64 == 0");

@@ -99,6 +99,24 @@ def test_gemm_layout_t_k64_shapes(a_t, b_t, M, N, K):
     assert_rel(_np(c), ref, FP32_RTOL, "gemm layout T fp32")
 
 
+@pytest.mark.parametrize("a_t", [False, True])
+@pytest.mark.parametrize("b_t", [False, True])
+@pytest.mark.parametrize("M,N,K", [(24, 304, 128), (64, 520, 192), (712, 56, 256), (1000, 32, 64), (96, 32, 2048)])
+def test_gemm_narrow_k64_shapes(a_t, b_t, M, N, K):
+    """Narrow tiles (32- or 64-wide sides) on the direct-load loop for every layout pair."""
+    H = _ops()
+    rng = np.random.default_rng(7 * M + N + K + 2 * a_t + b_t)
+    A_ = bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    B_ = bf16_round(rng.standard_normal((N, K)).astype(np.float32))
+    ref = A_.astype(np.float64) @ B_.astype(np.float64).T
+    a = _bf(A_.T.copy() if a_t else A_)
+    b = _bf(B_.T.copy() if b_t else B_)
+    print(f"gemm narrow a_t={a_t} b_t={b_t} M={M} N={N} K={K}", flush=True)
+    c = H.gemm(a, b, a_t=a_t, b_t=b_t, out_f32=True)
+    torch.cuda.synchronize()
+    assert_rel(_np(c), ref, FP32_RTOL, "gemm narrow fp32")
+
+
 def test_gemm_bf16_out_resid_alpha():
     H = _ops()
     rng = np.random.default_rng(3)
