@@ -212,6 +212,8 @@ int rte_axpy_norm_bwd(const void* dn, const float* dx_ext, const float* x, const
  *               tables gain / bias / scale f32 [keys, d], low f32 [B*seq, d].
  * epilogue bwd: dh = dout + dupd * gain[k], dlow bf16 = dupd, dupd = dout c scale[k] (1 - t^2);
  *               part f32 [B, 3d] = per-sample sums (dupd h | dupd | dout c t) for the tables.
+ * table grad: dgain / dbias / dscale f32 [n_keys, d] (each optional) = sums of part's three column
+ *               blocks over the samples with that key, in sample order (zero rows for unused keys).
  * d % 8 == 0, d <= 1024, 16-byte aligned buffers. */
 int rte_macro_prologue_fwd(const float* h, const float* h0, int B, int seq, int d, float eps, void* z, float* rstd,
                            void* stream);
@@ -223,6 +225,8 @@ int rte_macro_epilogue_fwd(const float* h, const float* low, const int64_t* key,
 int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int seq,
                            int d, const float* gain, const float* bias, const float* scale, float c, float* dh,
                            void* dlow, float* part, void* stream);
+int rte_macro_table_grad(const int64_t* key, int B, int n_keys, int d, const float* part, float* dgain, float* dbias,
+                         float* dscale, void* stream);
 
 /* ---- fused AdamW step with the trainer's per-group norms (replaces torch.optim.AdamW.step,
  *      clip_grad_norm_ and _optimizer_grad_metrics of rte/training.py:385-468) ----
@@ -245,21 +249,24 @@ int rte_adamw_step(const void* rows, int n_tensors, const int32_t* blocks, const
  *      macro_distill_loss rte/macro.py:394-471 and macro_alignment_metrics :499-546 on the
  *      path with the residual origin h0; rte/audit.py:326-352 calls both) ----
  * hot, exact, h0 f32 [A, seq, d]; hot_logits / exact_logits f32 [A, seq, V] (both optional).
- * fwd: losses f32 [6] = delta_dir, delta_rms, endpoint_normed, endpoint_raw, rms_trust,
- *      kl (temperature t, batchmean over A, times t^2; 0 without logits);
+ * fwd: losses f32 [6] = weights[i] (host array of 6 floats, NULL = all 1) times delta_dir, delta_rms,
+ *      endpoint_normed, endpoint_raw, rms_trust, kl (temperature t, batchmean over A, times t^2;
+ *      0 without logits);
  *      metrics f32 [10] = hidden_cosine, hidden_mse, macro_norm, exact_norm, macro_exact_norm_ratio,
  *      delta_cosine, delta_rms_exact, delta_rms_pred, delta_rms_ratio, logit_kl (t = 1).
  *      The workspace (rte_distill_workspace_bytes(A, rows = A * seq or 0)) keeps the per-sample
  *      sums and logit lse's for the backward: keep it untouched until then.
- * bwd: dhot f32 [A, seq, d] and dhot_logits f32 [A, seq, V] (each optional) for dlosses [6]. */
+ * bwd: dhot f32 [A, seq, d] and dhot_logits f32 [A, seq, V] (each optional) for dlosses [6] (device)
+ *      of the weighted losses (same weights). */
 size_t rte_distill_workspace_bytes(int A, int rows);
 int rte_distill_fwd(const float* hot, const float* exact, const float* h0, int A, int seq, int d,
                     const float* hot_logits, const float* exact_logits, int V, float temperature, float eps,
-                    float* losses, float* metrics, void* workspace, size_t workspace_bytes, void* stream);
+                    const float* weights, float* losses, float* metrics, void* workspace, size_t workspace_bytes,
+                    void* stream);
 int rte_distill_bwd(const float* hot, const float* exact, const float* h0, int A, int seq, int d,
                     const float* hot_logits, const float* exact_logits, int V, float temperature, float eps,
-                    const float* dlosses, const void* workspace, size_t workspace_bytes, float* dhot,
-                    float* dhot_logits, void* stream);
+                    const float* weights, const float* dlosses, const void* workspace, size_t workspace_bytes,
+                    float* dhot, float* dhot_logits, void* stream);
 
 /* ---- control-variate audit correction (replaces AuditEngine.correction's loss arithmetic,
  *      rte/audit.py:296-321, over lm_loss_per_sample rte/models.py:73-75) ----

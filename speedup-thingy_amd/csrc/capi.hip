@@ -53,13 +53,15 @@ size_t adamw_workspace_bytes(int nt, int nblk, int G);
 int adamw_step(const void* rows, int nt, const int32_t* blk, const int32_t* first_blk, int nblk, const double* hyper,
                int G, const int32_t* metric_lr_group, int M, float clip_max, const float* found_inf, float* metrics,
                void* ws, size_t ws_bytes, hipStream_t s);
+int macro_table_grad(const int64_t* key, int B, int G, int d, const float* part, float* dgain, float* dbias,
+                     float* dscale, hipStream_t s);
 size_t distill_workspace_bytes(int A, int R);
 int distill_fwd(const float* hot, const float* exact, const float* h0, int A, int S, int d, const float* hot_logits,
-                const float* exact_logits, int V, float t, float eps, float* losses, float* metrics, void* ws,
-                size_t ws_bytes, hipStream_t s);
+                const float* exact_logits, int V, float t, float eps, const float* weights, float* losses,
+                float* metrics, void* ws, size_t ws_bytes, hipStream_t s);
 int distill_bwd(const float* hot, const float* exact, const float* h0, int A, int S, int d, const float* hot_logits,
-                const float* exact_logits, int V, float t, float eps, const float* g, const void* ws,
-                size_t ws_bytes, float* dhot, float* dhot_logits, hipStream_t s);
+                const float* exact_logits, int V, float t, float eps, const float* weights, const float* g,
+                const void* ws, size_t ws_bytes, float* dhot, float* dhot_logits, hipStream_t s);
 int audit_fwd(const float* hot_tok, const float* exact_tok, int B, int S, const int64_t* idx, int A, const float* p,
               float clip, int grad_corrected, float* corrected, float* exact_ps, float* coef, float* stats,
               hipStream_t s);
@@ -786,6 +788,11 @@ int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, 
   return macro_epilogue_bwd(dout, h, low, key, B, seq, d, gain, bias, scale, c, dh, B16(dlow), part, S(stream));
 }
 
+int rte_macro_table_grad(const int64_t* key, int B, int n_keys, int d, const float* part, float* dgain, float* dbias,
+                         float* dscale, void* stream) {
+  return macro_table_grad(key, B, n_keys, d, part, dgain, dbias, dscale, S(stream));
+}
+
 int rte_adamw_chunk(void) { return adamw_chunk(); }
 
 size_t rte_adamw_workspace_bytes(int n_tensors, int n_blocks, int n_groups) {
@@ -803,17 +810,18 @@ size_t rte_distill_workspace_bytes(int A, int rows) { return distill_workspace_b
 
 int rte_distill_fwd(const float* hot, const float* exact, const float* h0, int A, int seq, int d,
                     const float* hot_logits, const float* exact_logits, int V, float temperature, float eps,
-                    float* losses, float* metrics, void* workspace, size_t workspace_bytes, void* stream) {
-  return distill_fwd(hot, exact, h0, A, seq, d, hot_logits, exact_logits, V, temperature, eps, losses, metrics,
-                     workspace, workspace_bytes, S(stream));
+                    const float* weights, float* losses, float* metrics, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  return distill_fwd(hot, exact, h0, A, seq, d, hot_logits, exact_logits, V, temperature, eps, weights, losses,
+                     metrics, workspace, workspace_bytes, S(stream));
 }
 
 int rte_distill_bwd(const float* hot, const float* exact, const float* h0, int A, int seq, int d,
                     const float* hot_logits, const float* exact_logits, int V, float temperature, float eps,
-                    const float* dlosses, const void* workspace, size_t workspace_bytes, float* dhot,
-                    float* dhot_logits, void* stream) {
-  return distill_bwd(hot, exact, h0, A, seq, d, hot_logits, exact_logits, V, temperature, eps, dlosses, workspace,
-                     workspace_bytes, dhot, dhot_logits, S(stream));
+                    const float* weights, const float* dlosses, const void* workspace, size_t workspace_bytes,
+                    float* dhot, float* dhot_logits, void* stream) {
+  return distill_bwd(hot, exact, h0, A, seq, d, hot_logits, exact_logits, V, temperature, eps, weights, dlosses,
+                     workspace, workspace_bytes, dhot, dhot_logits, S(stream));
 }
 
 int rte_audit_correct_fwd(const float* hot_tok, const float* exact_tok, int B, int seq, const int64_t* idx, int A,

@@ -149,9 +149,14 @@ __global__ void __launch_bounds__(256) kl_rows_kernel(const float* __restrict__ 
 // metrics: [0] hidden_cosine, [1] hidden_mse, [2] macro_norm, [3] exact_norm,
 // [4] macro_exact_norm_ratio, [5] delta_cosine, [6] delta_rms_exact, [7] delta_rms_pred,
 // [8] delta_rms_ratio, [9] logit_kl_exact_macro
+struct LossWeights {
+  float w[6];
+};
+
 __global__ void distill_final_kernel(const float* __restrict__ parts, float* __restrict__ stats, int A, int S,
                                      int d, const float* __restrict__ kl_row, const float* __restrict__ klm_row,
-                                     int R, float t, float* __restrict__ out, float* __restrict__ met) {
+                                     int R, float t, LossWeights lw, float* __restrict__ out,
+                                     float* __restrict__ met) {
   // per-sample sums of the kSplit partials, in order (kept for the backward)
   for (int q = threadIdx.x; q < A * kStats; q += blockDim.x) {
     const int a = q / kStats, k = q - a * kStats;
@@ -182,17 +187,17 @@ __global__ void distill_final_kernel(const float* __restrict__ parts, float* __r
     er += re_;
   }
   const double iA = A > 0 ? 1.0 / A : 0.0;
-  out[0] = (float)(1.0 - cos_d * iA);
-  out[1] = (float)(lrms * iA);
-  out[2] = (float)(sl1n * iA / N);
-  out[3] = (float)(sl1r * iA / N);
-  out[4] = (float)(trust * iA);
+  out[0] = lw.w[0] * (float)(1.0 - cos_d * iA);
+  out[1] = lw.w[1] * (float)(lrms * iA);
+  out[2] = lw.w[2] * (float)(sl1n * iA / N);
+  out[3] = lw.w[3] * (float)(sl1r * iA / N);
+  out[4] = lw.w[4] * (float)(trust * iA);
   double kl = 0, klm = 0;
   for (int r = 0; r < R; ++r) {
     kl += kl_row[r];
     klm += klm_row[r];
   }
-  out[5] = R > 0 ? (float)(kl * iA * (double)t * t) : 0.0f;
+  out[5] = R > 0 ? lw.w[5] * (float)(kl * iA * (double)t * t) : 0.0f;
   met[0] = (float)(cos_h * iA);
   met[1] = (float)(mse * iA / N);
   met[2] = (float)(mn * iA);
@@ -209,11 +214,14 @@ __global__ void distill_final_kernel(const float* __restrict__ parts, float* __r
 __global__ void __launch_bounds__(256) distill_bwd_kernel(const float* __restrict__ hot, const float* __restrict__ ex,
                                                           const float* __restrict__ h0,
                                                           const float* __restrict__ stats, int A, int S, int d,
-                                                          float eps, const float* __restrict__ g,
+                                                          float eps, const float* __restrict__ gin, LossWeights lw,
                                                           float* __restrict__ dhot) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= A * S) return;
+  float g[5];
+#pragma unroll
+  for (int q = 0; q < 5; ++q) g[q] = gin[q] * lw.w[q];
   const int a = row / S;
   const float* st = stats + (int64_t)a * kStats;
   const float N = (float)S * d, iA = 1.0f / (float)A;
@@ -260,7 +268,7 @@ __global__ void __launch_bounds__(256) kl_bwd_kernel(const float* __restrict__ h
   const int lane = threadIdx.x & 63;
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= R) return;
-  const float k = g[0] * scale;
+  const float k = g[0] * scale;  // scale includes the KL weight
   const float lq = lse[2 * r], lp = lse[2 * r + 1];
   const int64_t rb = (int64_t)r * V;
   for (int c = lane; c < V; c += 64)
@@ -276,8 +284,8 @@ size_t distill_workspace_bytes(int A, int R) {
 }
 
 int distill_fwd(const float* hot, const float* exact, const float* h0, int A, int S, int d, const float* hot_logits,
-                const float* exact_logits, int V, float t, float eps, float* losses, float* metrics, void* ws,
-                size_t ws_bytes, hipStream_t s) {
+                const float* exact_logits, int V, float t, float eps, const float* weights, float* losses,
+                float* metrics, void* ws, size_t ws_bytes, hipStream_t s) {
   RTE_REQUIRE(A >= 1 && S >= 1 && d >= 1, "distill: need at least one audited sample");
   RTE_REQUIRE(hot && exact && h0 && losses && metrics, "distill: hot, exact, h0 and the outputs are required");
   RTE_REQUIRE(t > 0.0f, "distill: temperature must be positive");
@@ -296,14 +304,16 @@ int distill_fwd(const float* hot, const float* exact, const float* h0, int A, in
                        kl_row, klm_row, lse);
     RTE_TRY(check_launch("distill_kl_rows"));
   }
-  hipLaunchKernelGGL(distill_final_kernel, dim3(1), dim3(256), 0, s, parts, stats, A, S, d, kl_row, klm_row, R, t,
+  LossWeights lw;
+  for (int q = 0; q < 6; ++q) lw.w[q] = weights ? weights[q] : 1.0f;
+  hipLaunchKernelGGL(distill_final_kernel, dim3(1), dim3(256), 0, s, parts, stats, A, S, d, kl_row, klm_row, R, t, lw,
                      losses, metrics);
   return check_launch("distill_final");
 }
 
 int distill_bwd(const float* hot, const float* exact, const float* h0, int A, int S, int d, const float* hot_logits,
-                const float* exact_logits, int V, float t, float eps, const float* g, const void* ws,
-                size_t ws_bytes, float* dhot, float* dhot_logits, hipStream_t s) {
+                const float* exact_logits, int V, float t, float eps, const float* weights, const float* g,
+                const void* ws, size_t ws_bytes, float* dhot, float* dhot_logits, hipStream_t s) {
   RTE_REQUIRE(A >= 1 && S >= 1 && d >= 1 && g, "distill_bwd: bad arguments");
   RTE_REQUIRE(ws_bytes >= distill_workspace_bytes(A, (hot_logits && exact_logits) ? A * S : 0),
               "distill_bwd: workspace too small");
@@ -311,13 +321,16 @@ int distill_bwd(const float* hot, const float* exact, const float* h0, int A, in
   const float* stats = static_cast<const float*>(ws);
   const float* lse = stats + (size_t)A * kStats + 2 * (size_t)R;
   if (dhot) {
+    LossWeights lw;
+    for (int q = 0; q < 6; ++q) lw.w[q] = weights ? weights[q] : 1.0f;
     hipLaunchKernelGGL(distill_bwd_kernel, dim3((A * S + 3) / 4), dim3(256), 0, s, hot, exact, h0, stats, A, S, d,
-                       eps, g, dhot);
+                       eps, g, lw, dhot);
     RTE_TRY(check_launch("distill_bwd"));
   }
   if (dhot_logits && R > 0) {
+    const float wkl = weights ? weights[5] : 1.0f;
     hipLaunchKernelGGL(kl_bwd_kernel, dim3((R + 3) / 4), dim3(256), 0, s, hot_logits, exact_logits, lse, R, V,
-                       1.0f / t, t / (float)A, g + 5, dhot_logits);
+                       1.0f / t, wkl * t / (float)A, g + 5, dhot_logits);
     RTE_TRY(check_launch("distill_kl_bwd"));
   }
   return 0;

@@ -316,6 +316,29 @@ __global__ void __launch_bounds__(512) macro_epilogue_bwd_kernel(const float* __
   }
 }
 
+// Table gradients: for key v (one workgroup each), the per-sample sums part[b] of the samples
+// with key[b] == v, added in sample order, written to the three tables (rows of keys no sample
+// uses come out zero).
+__global__ void __launch_bounds__(256) macro_table_grad_kernel(const int64_t* __restrict__ key, int B, int d,
+                                                               const float* __restrict__ part,
+                                                               float* __restrict__ dgain, float* __restrict__ dbias,
+                                                               float* __restrict__ dscale) {
+  const int v = blockIdx.x;
+  for (int col = threadIdx.x; col < d; col += 256) {
+    float g = 0.0f, bb = 0.0f, sc = 0.0f;
+    for (int b = 0; b < B; ++b) {
+      if (key[b] != v) continue;
+      const float* pr = part + (int64_t)b * 3 * d;
+      g += pr[col];
+      bb += pr[d + col];
+      sc += pr[2 * d + col];
+    }
+    if (dgain) dgain[(int64_t)v * d + col] = g;
+    if (dbias) dbias[(int64_t)v * d + col] = bb;
+    if (dscale) dscale[(int64_t)v * d + col] = sc;
+  }
+}
+
 bool al16m(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
@@ -365,6 +388,14 @@ int macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int
     hipLaunchKernelGGL(macro_epilogue_fwd_kernel<2>, grid, dim3(256), 0, s, h, low, key, S, R, d, gain, bias, scale, c,
                        out);
   return check_launch("macro_epilogue_fwd");
+}
+
+int macro_table_grad(const int64_t* key, int B, int G, int d, const float* part, float* dgain, float* dbias,
+                     float* dscale, hipStream_t s) {
+  RTE_REQUIRE(B >= 0 && G >= 1 && d >= 1, "macro_table_grad: bad sizes");
+  if (!dgain && !dbias && !dscale) return 0;
+  hipLaunchKernelGGL(macro_table_grad_kernel, dim3(G), dim3(256), 0, s, key, B, d, part, dgain, dbias, dscale);
+  return check_launch("macro_table_grad");
 }
 
 int macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int S, int d,

@@ -72,9 +72,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_adamw_chunk": (_I, []),
     "rte_adamw_workspace_bytes": (_SZ, [_I, _I, _I]),
     "rte_adamw_step": (_I, [_P, _I, _P, _P, _I, _P, _I, _P, _I, _F, _P, _P, _P, _SZ, _P]),
+    "rte_macro_table_grad": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P]),
     "rte_distill_workspace_bytes": (_SZ, [_I, _I]),
-    "rte_distill_fwd": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _I, _F, _F, _P, _P, _P, _SZ, _P]),
-    "rte_distill_bwd": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _I, _F, _F, _P, _P, _SZ, _P, _P, _P]),
+    "rte_distill_fwd": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P, _SZ, _P]),
+    "rte_distill_bwd": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _I, _F, _F, _P, _P, _P, _SZ, _P, _P, _P]),
     "rte_audit_correct_fwd": (_I, [_P, _P, _I, _I, _P, _I, _P, _F, _I, _P, _P, _P, _P, _P]),
     "rte_audit_correct_bwd": (_I, [_P, _I, _I, _P, _I, _P, _P, _P, _P]),
     "rte_cast_f32_bf16": (_I, [_P, _I64, _P, _P]),

@@ -239,14 +239,15 @@ class AuditEngine:
             exact_end = exact.meta.recurrent_hidden
             if h0_sub is not None and exact_end is not None:
                 # fused: every distillation term and alignment metric of rte/macro.py:394-546
-                losses, mets = hip_ops.distill(hot_end, exact_end, h0_sub, hot_logits, exact.meta.logits,
-                                               temperature=tr.distill_temperature)
                 lam = {"delta_dir": tr.lambda_delta_dir, "delta_rms": tr.lambda_delta_rms,
                        "endpoint_normed": tr.lambda_endpoint_normed, "endpoint_raw": tr.lambda_endpoint_raw,
                        "rms_trust": tr.lambda_macro_rms_trust if tr.macro_rms_trust_region else 0.0,
                        "kl": tr.effective_lambda_kl}
-                for i, name in enumerate(hip_ops.DISTILL_LOSSES):
-                    aux[name] = lam[name] * losses[i]
+                losses, mets = hip_ops.distill(hot_end, exact_end, h0_sub, hot_logits, exact.meta.logits,
+                                               temperature=tr.distill_temperature,
+                                               weights=[lam[n] for n in hip_ops.DISTILL_LOSSES])
+                for name, v in zip(hip_ops.DISTILL_LOSSES, losses):
+                    aux[name] = v
                 align = {name: mets[i] for i, name in enumerate(hip_ops.DISTILL_METRICS)}
                 has_logits = (hot_logits is not None and exact.meta.logits is not None
                               and hot_logits.shape == exact.meta.logits.shape)

@@ -12,6 +12,8 @@ their gradients are fp32, the residual stream is fp32.
 
 from __future__ import annotations
 
+import ctypes
+
 from dataclasses import dataclass
 
 import torch
@@ -696,12 +698,14 @@ DISTILL_METRICS = ("hidden_cosine_exact_macro", "hidden_mse_exact_macro", "macro
 
 
 class DistillFn(torch.autograd.Function):
-    """Hot-vs-exact distillation losses (rte/macro.py:394-471, with h0) and alignment metrics
-    (:499-546) of the audited samples in three launches; the backward is one launch for the
-    hidden states and one for the logits.  exact, h0 and exact_logits carry no gradient."""
+    """Hot-vs-exact distillation losses (rte/macro.py:394-471, with h0), each times its weight,
+    and the alignment metrics (:499-546) of the audited samples in three launches; the backward
+    is one launch for the hidden states and one for the logits.  The six weighted losses are six
+    outputs (their gradients arrive separately, no selects).  exact, h0 and exact_logits carry
+    no gradient."""
 
     @staticmethod
-    def forward(ctx, hot, exact, h0, hot_logits, exact_logits, temperature, eps):
+    def forward(ctx, hot, exact, h0, hot_logits, exact_logits, temperature, eps, weights):
         _lib.require_device_tensors("distill", hot, exact, h0, hot_logits, exact_logits)
         A, S, d = hot.shape
         dev = hot.device
@@ -717,29 +721,35 @@ class DistillFn(torch.autograd.Function):
         ws = torch.empty(((nbytes + 3) // 4,), dtype=F32, device=dev)  # kept for the backward
         losses = torch.empty((6,), dtype=F32, device=dev)
         metrics = torch.empty((10,), dtype=F32, device=dev)
+        w6 = (ctypes.c_float * 6)(*[float(x) for x in weights])
         call("rte_distill_fwd", ptr(hv), ptr(ev), ptr(zv), A, S, d, ptr(hl), ptr(el), V, float(temperature),
-             float(eps), ptr(losses), ptr(metrics), ptr(ws), nbytes, _s())
+             float(eps), ctypes.addressof(w6), ptr(losses), ptr(metrics), ptr(ws), nbytes, _s())
         ctx.save_for_backward(hv, ev, zv, hl, el, ws)
         ctx.meta = (A, S, d, V, float(temperature), float(eps), nbytes, has_l,
-                    None if not has_l else hot_logits.shape)
+                    None if not has_l else hot_logits.shape, tuple(float(x) for x in weights))
         ctx.mark_non_differentiable(metrics)
-        return losses, metrics
+        return (*losses.unbind(0), metrics)
 
     @staticmethod
-    def backward(ctx, g, _g_metrics):
+    def backward(ctx, *grads):
         hv, ev, zv, hl, el, ws = ctx.saved_tensors
-        A, S, d, V, t, eps, nbytes, has_l, lshape = ctx.meta
-        gg = g.contiguous().to(F32)
+        A, S, d, V, t, eps, nbytes, has_l, lshape, weights = ctx.meta
+        gs = [g if g is not None else torch.zeros((), dtype=F32, device=hv.device) for g in grads[:6]]
+        gg = torch.stack([g.reshape(()).to(F32) for g in gs])
         dh = torch.empty_like(hv) if ctx.needs_input_grad[0] else None
         dl = torch.empty_like(hl) if (has_l and ctx.needs_input_grad[3]) else None
-        call("rte_distill_bwd", ptr(hv), ptr(ev), ptr(zv), A, S, d, ptr(hl), ptr(el), V, t, eps, ptr(gg), ptr(ws),
-             nbytes, ptr(dh), ptr(dl), _s())
-        return dh, None, None, (dl.view(lshape) if dl is not None else None), None, None, None
+        w6 = (ctypes.c_float * 6)(*weights)
+        call("rte_distill_bwd", ptr(hv), ptr(ev), ptr(zv), A, S, d, ptr(hl), ptr(el), V, t, eps,
+             ctypes.addressof(w6), ptr(gg), ptr(ws), nbytes, ptr(dh), ptr(dl), _s())
+        return dh, None, None, (dl.view(lshape) if dl is not None else None), None, None, None, None
 
 
-def distill(hot, exact, h0, hot_logits=None, exact_logits=None, *, temperature: float = 1.0, eps: float = 1e-5):
-    """(losses [6], metrics [10]) in the orders DISTILL_LOSSES / DISTILL_METRICS."""
-    return DistillFn.apply(hot, exact, h0, hot_logits, exact_logits, temperature, eps)
+def distill(hot, exact, h0, hot_logits=None, exact_logits=None, *, temperature: float = 1.0, eps: float = 1e-5,
+            weights=(1.0, 1.0, 1.0, 1.0, 1.0, 1.0)):
+    """(weighted losses: 6 scalars in the order DISTILL_LOSSES, metrics [10] in the order
+    DISTILL_METRICS)."""
+    *losses, metrics = DistillFn.apply(hot, exact, h0, hot_logits, exact_logits, temperature, eps, tuple(weights))
+    return losses, metrics
 
 
 # ----------------------------------------------------------------------------- audit correction
@@ -904,7 +914,8 @@ class MacroBoundedFn(torch.autograd.Function):
         part = torch.empty((B, 3 * d), dtype=F32, device=dev)
         call("rte_macro_epilogue_bwd", ptr(do), ptr(hv), ptr(low), ptr(kv), B, S, d, ptr(tg), ptr(tb), ptr(ts),
              c, ptr(dh_epi), ptr(dlow), ptr(part), _s())
-        dtab = segment_reduce_rows(kv, G, part) if (nia[6] or nia[7] or nia[8]) else None
+        tabs_out = [torch.empty((G, d), dtype=F32, device=dev) if nia[6 + i] else None for i in range(3)]
+        call("rte_macro_table_grad", ptr(kv), B, G, d, ptr(part), *(ptr(t) for t in tabs_out), _s())
         dsa, du = _grouped_linear_bwd(dlow, sa, ub, offsets, tok, pos, True, nia[5], False)
         da = torch.ops.aten.silu_backward(dsa, a)
         dz, dv = _grouped_linear_bwd(da, z, vb, offsets, tok, pos, True, nia[4], False)
@@ -913,7 +924,7 @@ class MacroBoundedFn(torch.autograd.Function):
         call("rte_macro_prologue_bwd", ptr(dz), ptr(hv), ptr(rstd), ptr(dh_epi), B, S, d, ptr(dh), ptr(dh0), _s())
 
         def tab(i):
-            return None if (dtab is None or not nia[6 + i]) else dtab[:, i * d:(i + 1) * d].reshape(t_shape)
+            return None if tabs_out[i] is None else tabs_out[i].view(t_shape)
 
         return (dh.to(h_dt), None if dh0 is None else dh0.to(h0_dt), None, None,
                 None if dv is None else dv.view(v_shape), None if du is None else du.view(u_shape),

@@ -768,14 +768,17 @@ def test_distill_matches_oracle(A, S, d, V):
     el32 = None if el is None else np.asarray(el, np.float32).astype(np.float64)
     th, tl = f(hot, True), f(hl, True)
     print(f"distill A={A} S={S} d={d} V={V}", flush=True)
-    losses, mets = H.distill(th, f(exact), f(h0), tl, f(el), temperature=t)
+    wts = [0.5, 2.0, 1.0, 0.05, 2.0, 1e-2]
+    losses, mets = H.distill(th, f(exact), f(h0), tl, f(el), temperature=t, weights=wts)
+    losses = torch.stack(losses)
     o_loss, o_met = DI.distill(hot32, exact32, h032, hl32, el32, t)
-    np.testing.assert_allclose(_np(losses), [o_loss[k] for k in H.DISTILL_LOSSES], rtol=1e-5, atol=1e-7)
+    np.testing.assert_allclose(_np(losses), [w * o_loss[k] for w, k in zip(wts, H.DISTILL_LOSSES)], rtol=1e-5,
+                               atol=1e-7)
     want_m = [o_met.get(k, 0.0) for k in H.DISTILL_METRICS]
     np.testing.assert_allclose(_np(mets), want_m, rtol=1e-5, atol=1e-7)
     g = np.array([0.3, -1.1, 0.7, 1.9, 0.45, -0.8], np.float32)
     (losses * torch.from_numpy(g).to(DEV)).sum().backward()
-    dh, dl = DI.distill_grad(hot32, exact32, h032, hl32, el32, t, g=g.astype(np.float64))
+    dh, dl = DI.distill_grad(hot32, exact32, h032, hl32, el32, t, g=g.astype(np.float64) * np.array(wts))
     assert_rel(_np(th.grad), dh, FP32_RTOL, "d hot")
     if V:
         assert_rel(_np(tl.grad), dl, FP32_RTOL, "d hot logits")
