@@ -211,22 +211,26 @@ int rte_axpy_norm_bwd(const void* dn, const float* dx_ext, const float* x, const
  * epilogue fwd: out = h + c * scale[k] * tanh(gain[k] * h + low + bias[k]), k = key[b] (int64 [B]),
  *               tables gain / bias / scale f32 [keys, d], low f32 [B*seq, d].
  * epilogue bwd: dh = dout + dupd * gain[k], dlow bf16 = dupd, dupd = dout c scale[k] (1 - t^2);
- *               part f32 [B, 3d] = per-sample sums (dupd h | dupd | dout c t) for the tables.
+ *               part (rte_macro_workspace_bytes) = per-sample, per-row-slice sums (dupd h | dupd |
+ *               dout c t) for the tables.
  * table grad: dgain / dbias / dscale f32 [n_keys, d] (each optional) = sums of part's three column
- *               blocks over the samples with that key, in sample order (zero rows for unused keys).
- * d % 8 == 0, d <= 1024, 16-byte aligned buffers. */
+ *               blocks over the samples with that key, in sample order (zero rows for unused keys);
+ *               part as written by rte_macro_epilogue_bwd with the same B, seq, d.
+ * The prologues take a workspace of rte_macro_workspace_bytes(B, seq, d) for their per-slice sums.
+ * d % 8 == 0, d <= 1024, B <= 65535 (table grad: B <= 16384), 16-byte aligned buffers. */
+size_t rte_macro_workspace_bytes(int B, int seq, int d);
 int rte_macro_prologue_fwd(const float* h, const float* h0, int B, int seq, int d, float eps, void* z, float* rstd,
-                           void* stream);
+                           void* workspace, size_t workspace_bytes, void* stream);
 int rte_macro_prologue_bwd(const void* dz, const float* h, const float* rstd, const float* dh_extra, int B, int seq,
-                           int d, float* dh, float* dh0, void* stream);
+                           int d, float* dh, float* dh0, void* workspace, size_t workspace_bytes, void* stream);
 int rte_macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int seq, int d,
                            const float* gain, const float* bias, const float* scale, float c, float* out,
                            void* stream);
 int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int seq,
                            int d, const float* gain, const float* bias, const float* scale, float c, float* dh,
-                           void* dlow, float* part, void* stream);
-int rte_macro_table_grad(const int64_t* key, int B, int n_keys, int d, const float* part, float* dgain, float* dbias,
-                         float* dscale, void* stream);
+                           void* dlow, void* part, size_t part_bytes, void* stream);
+int rte_macro_table_grad(const int64_t* key, int B, int seq, int n_keys, int d, const void* part, float* dgain,
+                         float* dbias, float* dscale, void* stream);
 
 /* ---- fused AdamW step with the trainer's per-group norms (replaces torch.optim.AdamW.step,
  *      clip_grad_norm_ and _optimizer_grad_metrics of rte/training.py:385-468) ----

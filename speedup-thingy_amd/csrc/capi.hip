@@ -39,22 +39,24 @@ size_t axpy_norm_bwd_workspace_bytes(int T, int d);
 int axpy_norm_bwd(const bf16* dn, const float* dx_ext, const float* x, const float* rstd, const float* w,
                   const float* gamma, const float* b, const float* c, const uint8_t* mask, int S, int T, int d,
                   float* da, float* db, float* dkeep, float* dparams, void* ws, size_t ws_bytes, hipStream_t s);
-int macro_prologue_fwd(const float* h, const float* h0, int B, int S, int d, float eps, bf16* z, float* rstd,
-                       hipStream_t s);
+int macro_parts(int B, int S);
+size_t macro_workspace_bytes(int B, int S, int d);
+int macro_prologue_fwd(const float* h, const float* h0, int B, int S, int d, float eps, bf16* z, float* rstd, void* ws,
+                       size_t ws_bytes, hipStream_t s);
 int macro_prologue_bwd(const bf16* dz, const float* h, const float* rstd, const float* dh_extra, int B, int S, int d,
-                       float* dh, float* dh0, hipStream_t s);
+                       float* dh, float* dh0, void* ws, size_t ws_bytes, hipStream_t s);
 int macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int S, int d, const float* gain,
                        const float* bias, const float* scale, float c, float* out, hipStream_t s);
 int macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int S, int d,
                        const float* gain, const float* bias, const float* scale, float c, float* dh, bf16* dlow,
-                       float* part, hipStream_t s);
+                       void* part, size_t part_bytes, hipStream_t s);
+int macro_table_grad(const int64_t* key, int B, int S, int G, int d, const void* part, float* dgain, float* dbias,
+                     float* dscale, hipStream_t s);
 int adamw_chunk();
 size_t adamw_workspace_bytes(int nt, int nblk, int G);
 int adamw_step(const void* rows, int nt, const int32_t* blk, const int32_t* first_blk, int nblk, const double* hyper,
                int G, const int32_t* metric_lr_group, int M, float clip_max, const float* found_inf, float* metrics,
                void* ws, size_t ws_bytes, hipStream_t s);
-int macro_table_grad(const int64_t* key, int B, int G, int d, const float* part, float* dgain, float* dbias,
-                     float* dscale, hipStream_t s);
 size_t distill_workspace_bytes(int A, int R);
 int distill_fwd(const float* hot, const float* exact, const float* h0, int A, int S, int d, const float* hot_logits,
                 const float* exact_logits, int V, float t, float eps, const float* weights, float* losses,
@@ -766,14 +768,17 @@ int rte_axpy_norm_bwd(const void* dn, const float* dx_ext, const float* x, const
                        dkeep, dparams, workspace, workspace_bytes, S(stream));
 }
 
+size_t rte_macro_workspace_bytes(int B, int seq, int d) { return macro_workspace_bytes(B, seq, d); }
+
 int rte_macro_prologue_fwd(const float* h, const float* h0, int B, int seq, int d, float eps, void* z, float* rstd,
-                           void* stream) {
-  return macro_prologue_fwd(h, h0, B, seq, d, eps, B16(z), rstd, S(stream));
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  return macro_prologue_fwd(h, h0, B, seq, d, eps, B16(z), rstd, workspace, workspace_bytes, S(stream));
 }
 
 int rte_macro_prologue_bwd(const void* dz, const float* h, const float* rstd, const float* dh_extra, int B, int seq,
-                           int d, float* dh, float* dh0, void* stream) {
-  return macro_prologue_bwd(reinterpret_cast<const bf16*>(dz), h, rstd, dh_extra, B, seq, d, dh, dh0, S(stream));
+                           int d, float* dh, float* dh0, void* workspace, size_t workspace_bytes, void* stream) {
+  return macro_prologue_bwd(reinterpret_cast<const bf16*>(dz), h, rstd, dh_extra, B, seq, d, dh, dh0, workspace,
+                            workspace_bytes, S(stream));
 }
 
 int rte_macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int seq, int d,
@@ -784,13 +789,14 @@ int rte_macro_epilogue_fwd(const float* h, const float* low, const int64_t* key,
 
 int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int seq,
                            int d, const float* gain, const float* bias, const float* scale, float c, float* dh,
-                           void* dlow, float* part, void* stream) {
-  return macro_epilogue_bwd(dout, h, low, key, B, seq, d, gain, bias, scale, c, dh, B16(dlow), part, S(stream));
+                           void* dlow, void* part, size_t part_bytes, void* stream) {
+  return macro_epilogue_bwd(dout, h, low, key, B, seq, d, gain, bias, scale, c, dh, B16(dlow), part, part_bytes,
+                            S(stream));
 }
 
-int rte_macro_table_grad(const int64_t* key, int B, int n_keys, int d, const float* part, float* dgain, float* dbias,
-                         float* dscale, void* stream) {
-  return macro_table_grad(key, B, n_keys, d, part, dgain, dbias, dscale, S(stream));
+int rte_macro_table_grad(const int64_t* key, int B, int seq, int n_keys, int d, const void* part, float* dgain,
+                         float* dbias, float* dscale, void* stream) {
+  return macro_table_grad(key, B, seq, n_keys, d, part, dgain, dbias, dscale, S(stream));
 }
 
 int rte_adamw_chunk(void) { return adamw_chunk(); }

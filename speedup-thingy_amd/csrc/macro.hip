@@ -70,30 +70,85 @@ __device__ __forceinline__ void combine_waves(float* red, int d) {
   __syncthreads();
 }
 
+// Rows [s0, s1) of sample blockIdx.y: part blockIdx.x of the P equal slices of its seq rows.
+// Per-sample sums are formed per part (8 wave partials in wave order) and the P part sums are
+// added in part order by the consumer, so every sum keeps a fixed order.
+struct RowPart {
+  int64_t base;
+  int s0, s1;
+};
+
+__device__ __forceinline__ RowPart row_part(int S, int P) {
+  const int rb = (S + P - 1) / P;
+  RowPart rp;
+  rp.base = (int64_t)blockIdx.y * S;
+  rp.s0 = min(S, (int)blockIdx.x * rb);
+  rp.s1 = min(S, rp.s0 + rb);
+  return rp;
+}
+
+// Column sums of this block's 8 wave partials (vals per lane chunk) into dst[0, d).
+template <int NCH>
+__device__ __forceinline__ void store_part_sum(float* red, const float (&vals)[NCH][8], int d, float* dst) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int j = 0; j < NCH; ++j) {
+    const int ch = lane + 64 * j;
+    if (ch < d / 8) st8m(red + wave * d + ch * 8, vals[j]);
+  }
+  combine_waves(red, d);
+  for (int col = threadIdx.x; col < d; col += kMacroWaves * 64) dst[col] = red[col];
+}
+
+// mean[0, d) = (sum over the sample's P part sums, in part order) / S, in LDS.
+__device__ __forceinline__ void part_mean(const float* __restrict__ part, int S, int P, int d, float* mean) {
+  const float* pb = part + (int64_t)blockIdx.y * P * d;
+  const float invS = 1.0f / (float)S;
+  for (int col = threadIdx.x; col < d; col += kMacroWaves * 64) {
+    float s = 0.0f;
+    for (int q0 = 0; q0 < P; q0 += 8) {  // 8 independent loads in flight, added in part order
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = q0 + k < P ? pb[(int64_t)(q0 + k) * d + col] : 0.0f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) s += v[k];
+    }
+    mean[col] = s * invS;
+  }
+  __syncthreads();
+}
+
+// z[:, :d] = h * rstd, z[:, 2d:] = h0, rstd per row; part[b, p] = column sums of h * rstd.
 template <int NCH>
 __global__ void __launch_bounds__(512) macro_prologue_fwd_kernel(const float* __restrict__ h,
-                                                                 const float* __restrict__ h0, int S, int d,
+                                                                 const float* __restrict__ h0, int S, int P, int d,
                                                                  float eps, bf16* __restrict__ z,
-                                                                 float* __restrict__ rstd) {
+                                                                 float* __restrict__ rstd, float* __restrict__ part) {
   extern __shared__ float red[];  // [8][d]
-  const int b = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = d / 8, D3 = 3 * d;
-  const int64_t base = (int64_t)b * S;
+  const RowPart rp = row_part(S, P);
   float pool[NCH][8];
 #pragma unroll
   for (int j = 0; j < NCH; ++j)
 #pragma unroll
     for (int i = 0; i < 8; ++i) pool[j][i] = 0.0f;
-  for (int s = wave; s < S; s += kMacroWaves) {
-    const int64_t r = base + s;
-    float x[NCH][8];
+  for (int s = rp.s0 + wave; s < rp.s1; s += kMacroWaves) {
+    const int64_t r = rp.base + s;
+    float x[NCH][8], o[NCH][8];
     float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {  // both rows' loads issued before the reduction
+      const int ch = lane + 64 * j;
+      if (ch >= nch) continue;
+      ld8m(h + r * d + ch * 8, x[j]);
+      ld8m(h0 + r * d + ch * 8, o[j]);
+    }
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int ch = lane + 64 * j;
       if (ch >= nch) continue;
-      ld8m(h + r * d + ch * 8, x[j]);
+      st8m(z + r * D3 + 2 * d + ch * 8, o[j]);
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss += x[j][i] * x[j][i];
     }
@@ -104,58 +159,55 @@ __global__ void __launch_bounds__(512) macro_prologue_fwd_kernel(const float* __
     for (int j = 0; j < NCH; ++j) {
       const int ch = lane + 64 * j;
       if (ch >= nch) continue;
-      float y[8], o[8];
+      float y[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         y[i] = x[j][i] * rr;
         pool[j][i] += y[i];
       }
       st8m(z + r * D3 + ch * 8, y);
-      ld8m(h0 + r * d + ch * 8, o);
-      st8m(z + r * D3 + 2 * d + ch * 8, o);
     }
   }
-#pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    const int ch = lane + 64 * j;
-    if (ch < nch) st8m(red + wave * d + ch * 8, pool[j]);
-  }
-  combine_waves(red, d);
-  const float invS = 1.0f / (float)S;
-  for (int s = wave; s < S; s += kMacroWaves) {
-    const int64_t r = base + s;
+  store_part_sum<NCH>(red, pool, d, part + ((int64_t)blockIdx.y * P + blockIdx.x) * d);
+}
+
+// z[:, d:2d] of this part's rows = the sample's mean of h * rstd.
+template <int NCH>
+__global__ void __launch_bounds__(512) macro_prologue_mean_kernel(const float* __restrict__ part, int S, int P, int d,
+                                                                  bf16* __restrict__ z) {
+  __shared__ float mean[1024];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nch = d / 8, D3 = 3 * d;
+  const RowPart rp = row_part(S, P);
+  part_mean(part, S, P, d, mean);
+  for (int s = rp.s0 + wave; s < rp.s1; s += kMacroWaves) {
+    const int64_t r = rp.base + s;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int ch = lane + 64 * j;
       if (ch >= nch) continue;
-      float p[8];
-      ld8m(red + ch * 8, p);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) p[i] *= invS;
-      st8m(z + r * D3 + d + ch * 8, p);
+      float m[8];
+      ld8m(mean + ch * 8, m);
+      st8m(z + r * D3 + d + ch * 8, m);
     }
   }
 }
 
-// dh = dh_extra + rmsnorm backward of (dz[:, :d] + mean-broadcast of dz[:, d:2d]); dh0 = dz[:, 2d:]
+// part[b, p] = column sums of dz[:, d:2d] over this part's rows.
 template <int NCH>
-__global__ void __launch_bounds__(512) macro_prologue_bwd_kernel(const bf16* __restrict__ dz,
-                                                                 const float* __restrict__ h,
-                                                                 const float* __restrict__ rstd,
-                                                                 const float* __restrict__ dh_extra, int S, int d,
-                                                                 float* __restrict__ dh, float* __restrict__ dh0) {
+__global__ void __launch_bounds__(512) macro_prologue_bwd_sum_kernel(const bf16* __restrict__ dz, int S, int P,
+                                                                     int d, float* __restrict__ part) {
   extern __shared__ float red[];  // [8][d]
-  const int b = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = d / 8, D3 = 3 * d;
-  const int64_t base = (int64_t)b * S;
+  const RowPart rp = row_part(S, P);
   float gp[NCH][8];
 #pragma unroll
   for (int j = 0; j < NCH; ++j)
 #pragma unroll
     for (int i = 0; i < 8; ++i) gp[j][i] = 0.0f;
-  for (int s = wave; s < S; s += kMacroWaves) {
-    const int64_t r = base + s;
+  for (int s = rp.s0 + wave; s < rp.s1; s += kMacroWaves) {
+    const int64_t r = rp.base + s;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int ch = lane + 64 * j;
@@ -166,32 +218,55 @@ __global__ void __launch_bounds__(512) macro_prologue_bwd_kernel(const bf16* __r
       for (int i = 0; i < 8; ++i) gp[j][i] += g[i];
     }
   }
+  store_part_sum<NCH>(red, gp, d, part + ((int64_t)blockIdx.y * P + blockIdx.x) * d);
+}
+
+// dh = dh_extra + rmsnorm backward of (dz[:, :d] + mean-broadcast of dz[:, d:2d]); dh0 = dz[:, 2d:]
+template <int NCH>
+__global__ void __launch_bounds__(512) macro_prologue_bwd_kernel(const bf16* __restrict__ dz,
+                                                                 const float* __restrict__ h,
+                                                                 const float* __restrict__ rstd,
+                                                                 const float* __restrict__ dh_extra,
+                                                                 const float* __restrict__ part, int S, int P, int d,
+                                                                 float* __restrict__ dh, float* __restrict__ dh0) {
+  __shared__ float mean[1024];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nch = d / 8, D3 = 3 * d;
+  const RowPart rp = row_part(S, P);
+  part_mean(part, S, P, d, mean);
+  float gp[NCH][8];
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int ch = lane + 64 * j;
-    if (ch < nch) st8m(red + wave * d + ch * 8, gp[j]);
+    if (ch < nch) ld8m(mean + ch * 8, gp[j]);
   }
-  combine_waves(red, d);
-  const float invS = 1.0f / (float)S;
-#pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    const int ch = lane + 64 * j;
-    if (ch >= nch) continue;
-    ld8m(red + ch * 8, gp[j]);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) gp[j][i] *= invS;
-  }
-  for (int s = wave; s < S; s += kMacroWaves) {
-    const int64_t r = base + s;
+  for (int s = rp.s0 + wave; s < rp.s1; s += kMacroWaves) {
+    const int64_t r = rp.base + s;
     const float rr = rstd[r];
-    float g[NCH][8], x[NCH][8];
+    float g[NCH][8], x[NCH][8], e[NCH][8];
     float dot = 0.0f;
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {
+    for (int j = 0; j < NCH; ++j) {  // every load of the row issued before the reduction
       const int ch = lane + 64 * j;
       if (ch >= nch) continue;
       ld8m(dz + r * D3 + ch * 8, g[j]);
       ld8m(h + r * d + ch * 8, x[j]);
+      if (dh_extra) {
+        ld8m(dh_extra + r * d + ch * 8, e[j]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) e[j][i] = 0.0f;
+      }
+      if (dh0) {
+        float q[8];
+        ld8m(dz + r * D3 + 2 * d + ch * 8, q);
+        st8m(dh0 + r * d + ch * 8, q);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int ch = lane + 64 * j;
+      if (ch >= nch) continue;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         g[j][i] += gp[j][i];
@@ -204,16 +279,10 @@ __global__ void __launch_bounds__(512) macro_prologue_bwd_kernel(const bf16* __r
     for (int j = 0; j < NCH; ++j) {
       const int ch = lane + 64 * j;
       if (ch >= nch) continue;
-      float o[8], e[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (dh_extra) ld8m(dh_extra + r * d + ch * 8, e);
+      float o[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = rr * g[j][i] - x[j][i] * coef + e[i];
+      for (int i = 0; i < 8; ++i) o[i] = rr * g[j][i] - x[j][i] * coef + e[j][i];
       st8m(dh + r * d + ch * 8, o);
-      if (dh0) {
-        float q[8];
-        ld8m(dz + r * D3 + 2 * d + ch * 8, q);
-        st8m(dh0 + r * d + ch * 8, q);
-      }
     }
   }
 }
@@ -249,24 +318,24 @@ __global__ void __launch_bounds__(256) macro_epilogue_fwd_kernel(const float* __
   }
 }
 
-// Per sample: dh (= dout + dupd * gain), dlow (bf16) and the column sums of the table
-// gradients part[b] = (sum dupd * h | sum dupd | sum dout * c * tanh), dupd = dout c scale (1 - t^2).
+// Per part of a sample: dh (= dout + dupd * gain), dlow (bf16) and the column sums of the
+// table gradients part[b, p] = (sum dupd * h | sum dupd | sum dout * c * tanh),
+// dupd = dout c scale (1 - t^2).
 template <int NCH>
 __global__ void __launch_bounds__(512) macro_epilogue_bwd_kernel(const float* __restrict__ dout,
                                                                  const float* __restrict__ h,
                                                                  const float* __restrict__ low,
-                                                                 const int64_t* __restrict__ key, int S, int d,
-                                                                 const float* __restrict__ gain,
+                                                                 const int64_t* __restrict__ key, int S, int P,
+                                                                 int d, const float* __restrict__ gain,
                                                                  const float* __restrict__ bias,
                                                                  const float* __restrict__ scale, float c,
                                                                  float* __restrict__ dh, bf16* __restrict__ dlow,
                                                                  float* __restrict__ part) {
   extern __shared__ float red[];  // [8][d], reused for the three sums
-  const int b = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = d / 8;
-  const int64_t base = (int64_t)b * S;
-  const int64_t kb = key[b] * d;
+  const RowPart rp = row_part(S, P);
+  const int64_t kb = key[blockIdx.y] * d;
   float gn[NCH][8], bs[NCH][8], sc[NCH][8], pg[NCH][8], pb[NCH][8], ps[NCH][8];
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
@@ -278,8 +347,8 @@ __global__ void __launch_bounds__(512) macro_epilogue_bwd_kernel(const float* __
     ld8m(bias + kb + ch * 8, bs[j]);
     ld8m(scale + kb + ch * 8, sc[j]);
   }
-  for (int s = wave; s < S; s += kMacroWaves) {
-    const int64_t r = base + s;
+  for (int s = rp.s0 + wave; s < rp.s1; s += kMacroWaves) {
+    const int64_t r = rp.base + s;
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int ch = lane + 64 * j;
@@ -303,73 +372,126 @@ __global__ void __launch_bounds__(512) macro_epilogue_bwd_kernel(const float* __
       st8m(dlow + off, ol);
     }
   }
-  float* pr = part + (int64_t)b * 3 * d;
-  for (int q = 0; q < 3; ++q) {
-    if (q > 0) __syncthreads();  // the previous sum has been read out of red
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int ch = lane + 64 * j;
-      if (ch < nch) st8m(red + wave * d + ch * 8, q == 0 ? pg[j] : (q == 1 ? pb[j] : ps[j]));
-    }
-    combine_waves(red, d);
-    for (int col = threadIdx.x; col < d; col += kMacroWaves * 64) pr[q * d + col] = red[col];
-  }
+  float* pr = part + ((int64_t)blockIdx.y * P + blockIdx.x) * 3 * d;
+  store_part_sum<NCH>(red, pg, d, pr);
+  __syncthreads();  // red has been read out
+  store_part_sum<NCH>(red, pb, d, pr + d);
+  __syncthreads();
+  store_part_sum<NCH>(red, ps, d, pr + 2 * d);
 }
 
-// Table gradients: for key v (one workgroup each), the per-sample sums part[b] of the samples
-// with key[b] == v, added in sample order, written to the three tables (rows of keys no sample
-// uses come out zero).
-__global__ void __launch_bounds__(256) macro_table_grad_kernel(const int64_t* __restrict__ key, int B, int d,
+// Table gradients of key v = blockIdx.x for columns blockIdx.y * 64 + [0, 64) of the 3d part
+// columns: the part sums of the samples with key[b] == v, in (sample, part) order, written to
+// the three tables (rows of keys no sample uses come out zero).  The samples of v are first
+// listed in order in LDS (one ballot per 64 samples); the contributions j = (list index) * P +
+// part are then split over 4 thread groups by j mod 4, each summing its share in order with
+// 4 loads in flight, and the 4 group sums are added in group order.
+__global__ void __launch_bounds__(256) macro_table_grad_kernel(const int64_t* __restrict__ key, int B, int P, int d,
                                                                const float* __restrict__ part,
                                                                float* __restrict__ dgain, float* __restrict__ dbias,
                                                                float* __restrict__ dscale) {
+  extern __shared__ int list[];  // [B]
+  __shared__ int cnt;
+  __shared__ float gsum[4][64];
   const int v = blockIdx.x;
-  for (int col = threadIdx.x; col < d; col += 256) {
-    float g = 0.0f, bb = 0.0f, sc = 0.0f;
-    for (int b = 0; b < B; ++b) {
-      if (key[b] != v) continue;
-      const float* pr = part + (int64_t)b * 3 * d;
-      g += pr[col];
-      bb += pr[d + col];
-      sc += pr[2 * d + col];
+  const int lane = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  if (threadIdx.x < 64) {
+    int n = 0;
+    for (int b0 = 0; b0 < B; b0 += 64) {
+      const int b = b0 + lane;
+      const bool m = b < B && key[b] == v;
+      const unsigned long long bal = __ballot(m);
+      if (m) list[n + __popcll(bal & ((1ull << lane) - 1ull))] = b;
+      n += __popcll(bal);
     }
-    if (dgain) dgain[(int64_t)v * d + col] = g;
-    if (dbias) dbias[(int64_t)v * d + col] = bb;
-    if (dscale) dscale[(int64_t)v * d + col] = sc;
+    if (lane == 0) cnt = n;
   }
+  __syncthreads();
+  const int m = cnt * P, D3 = 3 * d;
+  const int col = blockIdx.y * 64 + lane;
+  float acc = 0.0f;
+  if (col < D3) {
+    for (int j0 = grp; j0 < m; j0 += 16) {
+      float x[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int j = j0 + 4 * k;
+        x[k] = 0.0f;
+        if (j < m) {
+          const int i = j / P, q = j - i * P;
+          x[k] = part[((int64_t)list[i] * P + q) * D3 + col];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) acc += x[k];
+    }
+  }
+  gsum[grp][lane] = acc;
+  __syncthreads();
+  if (grp != 0 || col >= D3) return;
+  const float tot = ((gsum[0][lane] + gsum[1][lane]) + gsum[2][lane]) + gsum[3][lane];
+  const int t = col / d, c = col - t * d;
+  float* dst = t == 0 ? dgain : (t == 1 ? dbias : dscale);
+  if (dst) dst[(int64_t)v * d + c] = tot;
 }
 
 bool al16m(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
 
-#define MACRO_SIZES(what)                                                                                  \
-  RTE_REQUIRE(B >= 0 && S >= 1 && d >= 8 && d % 8 == 0 && d <= 1024, what ": need d % 8 == 0, d <= 1024")
+#define MACRO_SIZES(what)                                                                                   \
+  RTE_REQUIRE(B >= 0 && B <= 65535 && S >= 1 && d >= 8 && d % 8 == 0 && d <= 1024,                          \
+              what ": need B <= 65535, d % 8 == 0, d <= 1024")
 
-int macro_prologue_fwd(const float* h, const float* h0, int B, int S, int d, float eps, bf16* z, float* rstd,
-                       hipStream_t s) {
+// Row parts per sample: slices of about 8 rows (one per wave), halved while the grid would
+// exceed 2048 workgroups.
+int macro_parts(int B, int S) {
+  int P = (S + kMacroWaves - 1) / kMacroWaves;
+  while (P > 1 && (int64_t)B * P > 2048) P = (P + 1) / 2;
+  return P;
+}
+
+size_t macro_workspace_bytes(int B, int S, int d) {
+  if (B <= 0 || S <= 0 || d <= 0) return 0;
+  return (size_t)B * macro_parts(B, S) * 3 * d * sizeof(float);
+}
+
+#define MACRO_LAUNCH(kern, lds, ...)                                                           \
+  do {                                                                                        \
+    if (d <= 512)                                                                             \
+      hipLaunchKernelGGL(kern<1>, dim3(P, B), dim3(kMacroWaves * 64), lds, s, __VA_ARGS__);   \
+    else                                                                                      \
+      hipLaunchKernelGGL(kern<2>, dim3(P, B), dim3(kMacroWaves * 64), lds, s, __VA_ARGS__);   \
+  } while (0)
+
+int macro_prologue_fwd(const float* h, const float* h0, int B, int S, int d, float eps, bf16* z, float* rstd, void* ws,
+                       size_t ws_bytes, hipStream_t s) {
   MACRO_SIZES("macro_prologue");
   RTE_REQUIRE(al16m(h) && al16m(h0) && al16m(z), "macro_prologue: 16-byte aligned buffers");
   if (B == 0) return 0;
+  RTE_REQUIRE(ws && ws_bytes >= macro_workspace_bytes(B, S, d), "macro_prologue: workspace too small");
+  const int P = macro_parts(B, S);
+  float* part = static_cast<float*>(ws);
   const size_t lds = (size_t)kMacroWaves * d * sizeof(float);
-  if (d <= 512)
-    hipLaunchKernelGGL(macro_prologue_fwd_kernel<1>, dim3(B), dim3(512), lds, s, h, h0, S, d, eps, z, rstd);
-  else
-    hipLaunchKernelGGL(macro_prologue_fwd_kernel<2>, dim3(B), dim3(512), lds, s, h, h0, S, d, eps, z, rstd);
-  return check_launch("macro_prologue_fwd");
+  MACRO_LAUNCH(macro_prologue_fwd_kernel, lds, h, h0, S, P, d, eps, z, rstd, part);
+  RTE_TRY(check_launch("macro_prologue_fwd"));
+  MACRO_LAUNCH(macro_prologue_mean_kernel, 0, part, S, P, d, z);
+  return check_launch("macro_prologue_mean");
 }
 
 int macro_prologue_bwd(const bf16* dz, const float* h, const float* rstd, const float* dh_extra, int B, int S, int d,
-                       float* dh, float* dh0, hipStream_t s) {
+                       float* dh, float* dh0, void* ws, size_t ws_bytes, hipStream_t s) {
   MACRO_SIZES("macro_prologue_bwd");
   RTE_REQUIRE(al16m(dz) && al16m(h) && al16m(dh_extra) && al16m(dh) && al16m(dh0),
               "macro_prologue_bwd: 16-byte aligned buffers");
   if (B == 0) return 0;
+  RTE_REQUIRE(ws && ws_bytes >= macro_workspace_bytes(B, S, d), "macro_prologue_bwd: workspace too small");
+  const int P = macro_parts(B, S);
+  float* part = static_cast<float*>(ws);
   const size_t lds = (size_t)kMacroWaves * d * sizeof(float);
-  if (d <= 512)
-    hipLaunchKernelGGL(macro_prologue_bwd_kernel<1>, dim3(B), dim3(512), lds, s, dz, h, rstd, dh_extra, S, d, dh, dh0);
-  else
-    hipLaunchKernelGGL(macro_prologue_bwd_kernel<2>, dim3(B), dim3(512), lds, s, dz, h, rstd, dh_extra, S, d, dh, dh0);
+  MACRO_LAUNCH(macro_prologue_bwd_sum_kernel, lds, dz, S, P, d, part);
+  RTE_TRY(check_launch("macro_prologue_bwd_sum"));
+  MACRO_LAUNCH(macro_prologue_bwd_kernel, 0, dz, h, rstd, dh_extra, part, S, P, d, dh, dh0);
   return check_launch("macro_prologue_bwd");
 }
 
@@ -390,30 +512,32 @@ int macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int
   return check_launch("macro_epilogue_fwd");
 }
 
-int macro_table_grad(const int64_t* key, int B, int G, int d, const float* part, float* dgain, float* dbias,
-                     float* dscale, hipStream_t s) {
-  RTE_REQUIRE(B >= 0 && G >= 1 && d >= 1, "macro_table_grad: bad sizes");
-  if (!dgain && !dbias && !dscale) return 0;
-  hipLaunchKernelGGL(macro_table_grad_kernel, dim3(G), dim3(256), 0, s, key, B, d, part, dgain, dbias, dscale);
-  return check_launch("macro_table_grad");
-}
-
 int macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int S, int d,
                        const float* gain, const float* bias, const float* scale, float c, float* dh, bf16* dlow,
-                       float* part, hipStream_t s) {
+                       void* part, size_t part_bytes, hipStream_t s) {
   MACRO_SIZES("macro_epilogue_bwd");
   RTE_REQUIRE(al16m(dout) && al16m(h) && al16m(low) && al16m(gain) && al16m(bias) && al16m(scale) && al16m(dh) &&
                   al16m(dlow),
               "macro_epilogue_bwd: 16-byte aligned buffers");
   if (B == 0) return 0;
+  RTE_REQUIRE(part && part_bytes >= macro_workspace_bytes(B, S, d), "macro_epilogue_bwd: part buffer too small");
+  const int P = macro_parts(B, S);
   const size_t lds = (size_t)kMacroWaves * d * sizeof(float);
-  if (d <= 512)
-    hipLaunchKernelGGL(macro_epilogue_bwd_kernel<1>, dim3(B), dim3(512), lds, s, dout, h, low, key, S, d, gain, bias,
-                       scale, c, dh, dlow, part);
-  else
-    hipLaunchKernelGGL(macro_epilogue_bwd_kernel<2>, dim3(B), dim3(512), lds, s, dout, h, low, key, S, d, gain, bias,
-                       scale, c, dh, dlow, part);
+  MACRO_LAUNCH(macro_epilogue_bwd_kernel, lds, dout, h, low, key, S, P, d, gain, bias, scale, c, dh, dlow,
+               static_cast<float*>(part));
   return check_launch("macro_epilogue_bwd");
+}
+
+int macro_table_grad(const int64_t* key, int B, int S, int G, int d, const void* part, float* dgain, float* dbias,
+                     float* dscale, hipStream_t s) {
+  RTE_REQUIRE(B >= 0 && B <= 16384 && S >= 1 && G >= 1 && G <= 65535 && d >= 1 && d <= 1024,
+              "macro_table_grad: need B <= 16384, n_keys <= 65535, d <= 1024");
+  if (!dgain && !dbias && !dscale) return 0;
+  const int P = B > 0 ? macro_parts(B, S) : 1;
+  const dim3 grid((unsigned)G, (unsigned)((3 * d + 63) / 64));
+  hipLaunchKernelGGL(macro_table_grad_kernel, grid, dim3(256), (size_t)(B > 0 ? B : 1) * sizeof(int), s, key, B, P, d,
+                     static_cast<const float*>(part), dgain, dbias, dscale);
+  return check_launch("macro_table_grad");
 }
 
 }  // namespace rte

@@ -887,7 +887,9 @@ class MacroBoundedFn(torch.autograd.Function):
         dev = h.device
         z = torch.empty((B * S, 3 * d), dtype=BF16, device=dev)
         rstd = torch.empty((B * S,), dtype=F32, device=dev)
-        call("rte_macro_prologue_fwd", ptr(hv), ptr(h0v), B, S, d, float(eps), ptr(z), ptr(rstd), _s())
+        wsb = _lib.load().rte_macro_workspace_bytes(B, S, d)
+        ws = torch.empty((max(wsb // 4, 1),), dtype=F32, device=dev)
+        call("rte_macro_prologue_fwd", ptr(hv), ptr(h0v), B, S, d, float(eps), ptr(z), ptr(rstd), ptr(ws), wsb, _s())
         vb = cast_bf16(v.reshape(G, v.shape[-2], v.shape[-1]))
         ub = cast_bf16(u.reshape(G, u.shape[-2], u.shape[-1]))
         a = _grouped_linear_fwd(z, vb, pk, out_f32=False)
@@ -911,17 +913,19 @@ class MacroBoundedFn(torch.autograd.Function):
         do = dout.contiguous().to(F32)
         dh_epi = torch.empty((B, S, d), dtype=F32, device=dev)
         dlow = torch.empty((B * S, d), dtype=BF16, device=dev)
-        part = torch.empty((B, 3 * d), dtype=F32, device=dev)
+        wsb = _lib.load().rte_macro_workspace_bytes(B, S, d)
+        ws = torch.empty((max(wsb // 4, 1),), dtype=F32, device=dev)
         call("rte_macro_epilogue_bwd", ptr(do), ptr(hv), ptr(low), ptr(kv), B, S, d, ptr(tg), ptr(tb), ptr(ts),
-             c, ptr(dh_epi), ptr(dlow), ptr(part), _s())
+             c, ptr(dh_epi), ptr(dlow), ptr(ws), wsb, _s())
         tabs_out = [torch.empty((G, d), dtype=F32, device=dev) if nia[6 + i] else None for i in range(3)]
-        call("rte_macro_table_grad", ptr(kv), B, G, d, ptr(part), *(ptr(t) for t in tabs_out), _s())
+        call("rte_macro_table_grad", ptr(kv), B, S, G, d, ptr(ws), *(ptr(t) for t in tabs_out), _s())
         dsa, du = _grouped_linear_bwd(dlow, sa, ub, offsets, tok, pos, True, nia[5], False)
         da = torch.ops.aten.silu_backward(dsa, a)
         dz, dv = _grouped_linear_bwd(da, z, vb, offsets, tok, pos, True, nia[4], False)
         dh = torch.empty((B, S, d), dtype=F32, device=dev)
         dh0 = torch.empty((B, S, d), dtype=F32, device=dev) if nia[1] else None
-        call("rte_macro_prologue_bwd", ptr(dz), ptr(hv), ptr(rstd), ptr(dh_epi), B, S, d, ptr(dh), ptr(dh0), _s())
+        call("rte_macro_prologue_bwd", ptr(dz), ptr(hv), ptr(rstd), ptr(dh_epi), B, S, d, ptr(dh), ptr(dh0),
+             ptr(ws), wsb, _s())
 
         def tab(i):
             return None if tabs_out[i] is None else tabs_out[i].view(t_shape)

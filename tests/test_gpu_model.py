@@ -415,11 +415,12 @@ def _torch_bounded(h, h0, rid, sid, p, c):
     return h + c * g(p["update_scale"]).unsqueeze(1) * torch.tanh(upd)
 
 
-@pytest.mark.parametrize("scale_init", [1.0, 0.5])
-def test_macro_operator_grouped_matches_reference(scale_init):
+@pytest.mark.parametrize("scale_init,B,S", [(1.0, 10, 16), (0.5, 10, 16), (1.0, 600, 37)])
+def test_macro_operator_grouped_matches_reference(scale_init, B, S):
     """MacroOperators (bounded) on the grouped GEMMs: forward against the numpy oracle, gradients
     of every parameter and of h, h0 against fp64 autograd of the reference formula.  With
-    macro_update_scale_init != 1 the per-key update scale is a parameter too."""
+    macro_update_scale_init != 1 the per-key update scale is a parameter too.  B=600, S=37 splits
+    each sample into uneven row slices (3 of 13, 13, 11 rows) and gives every key many samples."""
     from oracle import macro as MO
     from helpers import rel_err
     from rte_amd.macro import MacroOperators
@@ -432,7 +433,7 @@ def test_macro_operator_grouped_matches_reference(scale_init):
         mac.d_gain.normal_(0, 0.1)
         mac.bias.normal_(0, 0.1)
         mac.u.normal_(0, 0.05)
-    B, S, d = 10, 16, cfg.d_model
+    d = cfg.d_model
     gen = np.random.default_rng(4)
     hn, h0n = gen.standard_normal((B, S, d)), gen.standard_normal((B, S, d))
     rid = torch.tensor(gen.integers(0, 6, B), device="cuda")
@@ -440,7 +441,7 @@ def test_macro_operator_grouped_matches_reference(scale_init):
     h = torch.tensor(hn, dtype=torch.float32, device="cuda", requires_grad=True)
     h0 = torch.tensor(h0n, dtype=torch.float32, device="cuda", requires_grad=True)
     G = gen.standard_normal((B, S, d))
-    print("macro grouped B=10 S=16 d=128", flush=True)
+    print(f"macro grouped B={B} S={S} d={d}", flush=True)
     out, _ = mac(h, h0, rid, depths)
     (out * torch.tensor(G, dtype=torch.float32, device="cuda")).sum().backward()
     sid = mac.stride_ids_for_depths(depths)
