@@ -1059,6 +1059,149 @@ int launch_layouts(const GemmArgs& p, hipStream_t stream, void* ws, size_t ws_by
   return launch_cfg<BM, BN, BK, WM, WN, true, true, EPI>(p, stream, ws, ws_bytes, vec);
 }
 
+// ------------------------------------------------------------------ short reductions
+
+// K <= 64 with both operands k-contiguous and the plain store epilogue (low-rank and cluster
+// down-projections: K = rank or neurons per cluster).  Such products are bound by their output
+// writes, so the kernel drops the shared tile: one wave owns 32 output rows and a run of
+// 32-column blocks, loads its MFMA operands straight from global memory (16 bytes per lane per
+// 16 k; k past K reads zeros), and sends each 32x32 result block through a wave-private LDS
+// patch so every global store is 16 bytes of one row.  Waves never wait for each other; the
+// next block's B fragments are loaded before the current block is stored.
+constexpr int kSkPitch = 36;  // floats per patch row (144 bytes: 16-byte aligned rows)
+
+__device__ __forceinline__ bf16x8_v ld_frag16(const bf16* p) {
+  return __builtin_bit_cast(bf16x8_v, *reinterpret_cast<const uint4*>(p));
+}
+
+__device__ __forceinline__ void wave_lds_fence() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int KS>
+__global__ void __launch_bounds__(256) gemm_sk_kernel(GemmArgs p, EpiFlags fl, int nch, int cpt) {
+  __shared__ __align__(16) float patch[4][32 * kSkPitch];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, l32 = lane & 31;
+  const int task = blockIdx.x * 4 + wave;
+  const int rb = task / nch, ch = task - rb * nch;
+  int g = 0, m0 = 0, mlim = p.M;
+  if (p.mode == MODE_GROUP_M) {
+    // row block rb -> (group, block within the group): prefix sums of the groups' 32-row
+    // block counts, 64 groups per step
+    g = -1;
+    int local = 0, base = 0;
+    for (int c0 = 0; c0 < p.G; c0 += 64) {
+      const int gg = c0 + lane;
+      const int cnt = gg < p.G ? (p.goff[gg + 1] - p.goff[gg] + 31) / 32 : 0;
+      int incl = cnt;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+      }
+      const int excl = incl - cnt;
+      const unsigned long long hit = __ballot(cnt > 0 && rb >= base + excl && rb < base + incl);
+      if (hit) {
+        const int l = __ffsll((long long)hit) - 1;
+        g = c0 + l;
+        local = rb - base - __shfl(excl, l, 64);
+        break;
+      }
+      base += __shfl(incl, 63, 64);
+    }
+    if (g < 0) return;
+    mlim = p.goff[g + 1];
+    m0 = p.goff[g] + local * 32;
+  } else {
+    m0 = rb * 32;
+    if (m0 >= p.M) return;
+  }
+  const bf16* abase = p.a.ptr + (int64_t)g * p.a.gstride;
+  const bf16* bbase = p.b.ptr + (int64_t)g * p.b.gstride;
+  const int64_t ashift = (int64_t)g * p.a.growstride, bshift = (int64_t)g * p.b.growstride;
+  const bf16x8_v zero = __builtin_bit_cast(bf16x8_v, make_uint4(0u, 0u, 0u, 0u));
+
+  bf16x8_v af[KS];
+  {
+    int m = m0 + l32;
+    if (m >= mlim) m = mlim - 1;  // rows past the end re-read the last one; never stored
+    const bf16* ap = abase + row_off(p.a, m + ashift);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int k = ks * 16 + half * 8;
+      af[ks] = k < p.K ? ld_frag16(ap + col_off(p.a, k)) : zero;
+    }
+  }
+  const int CB = (p.N + 31) / 32;
+  const int cb0 = ch * cpt;
+  const int cb1 = cb0 + cpt < CB ? cb0 + cpt : CB;
+  auto load_b = [&](int cb, bf16x8_v(&bf)[KS]) {
+    int n = cb * 32 + l32;
+    if (n >= p.N) n = p.N - 1;
+    const bf16* bp = bbase + row_off(p.b, n + bshift);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int k = ks * 16 + half * 8;
+      bf[ks] = k < p.K ? ld_frag16(bp + col_off(p.b, k)) : zero;
+    }
+  };
+  float* pt = patch[wave];
+  bf16x8_v bcur[KS], bnext[KS];
+  if (cb0 < cb1) load_b(cb0, bcur);
+  for (int cb = cb0; cb < cb1; ++cb) {
+    if (cb + 1 < cb1) load_b(cb + 1, bnext);
+    f32x16_v acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks], bcur[ks], acc, 0, 0, 0);
+    wave_lds_fence();  // the previous block's patch reads are done
+#pragma unroll
+    for (int r = 0; r < 16; ++r) pt[(8 * (r >> 2) + 4 * half + (r & 3)) * kSkPitch + l32] = acc[r];
+    wave_lds_fence();
+#pragma unroll
+    for (int q = lane; q < 128; q += 64) {
+      const int row = q >> 2, cc = (q & 3) * 8;
+      const int m = m0 + row, n = cb * 32 + cc;
+      if (m >= mlim || n >= p.N) continue;
+      float v[8];
+      const float4 x = *reinterpret_cast<const float4*>(pt + row * kSkPitch + cc);
+      const float4 y = *reinterpret_cast<const float4*>(pt + row * kSkPitch + cc + 4);
+      v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+      v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+      store_chunk<8>(p.epi, g, m, n, p.N, v, fl.vec);
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) bcur[ks] = bnext[ks];
+  }
+}
+
+// Wave tasks: (32-row block, run of cpt column blocks), about 8192 of them (32 waves per CU)
+// when the problem has that many blocks.
+int launch_sk(const GemmArgs& p, hipStream_t stream, int vec) {
+  if (p.M == 0 || p.N == 0) return 0;
+  const int CB = (p.N + 31) / 32;
+  const int64_t rbound = p.mode == MODE_GROUP_M ? (int64_t)p.M / 32 + p.G + 1 : ((int64_t)p.M + 31) / 32;
+  int64_t c = rbound * CB / 8192;
+  if (c < 1) c = 1;
+  if (c > CB) c = CB;
+  const int cpt = (int)c, nch = (CB + cpt - 1) / cpt;
+  const int64_t tasks = rbound * nch;
+  RTE_REQUIRE(tasks / 4 < (int64_t)1 << 31, "gemm: problem too large for the short-K kernel");
+  const dim3 grid((unsigned)((tasks + 3) / 4));
+  EpiFlags fl{vec};
+  switch ((p.K + 15) / 16) {
+    case 1: hipLaunchKernelGGL(gemm_sk_kernel<1>, grid, dim3(256), 0, stream, p, fl, nch, cpt); break;
+    case 2: hipLaunchKernelGGL(gemm_sk_kernel<2>, grid, dim3(256), 0, stream, p, fl, nch, cpt); break;
+    case 3: hipLaunchKernelGGL(gemm_sk_kernel<3>, grid, dim3(256), 0, stream, p, fl, nch, cpt); break;
+    default: hipLaunchKernelGGL(gemm_sk_kernel<4>, grid, dim3(256), 0, stream, p, fl, nch, cpt); break;
+  }
+  return check_launch("gemm_short_k");
+}
+
 // Direct-to-LDS mainloop selection.  Default: K <= 1024 -> BK 32, 2 stages (four workgroups
 // per CU: short reductions are latency-bound, occupancy hides it best); longer K -> BK 64,
 // 2 stages (fewer barriers per MFMA).  RTE_GEMM_DL overrides it for diagnostics: 0 keeps the
@@ -1196,6 +1339,9 @@ int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream, void* ws, s
 
   switch (epi_kind) {
     case EPI_STORE: {
+      // short reductions over k-contiguous operands: output-bound, the barrier-free wave kernel
+      if (p.K <= 32 && !p.a_t && !p.b_t && p.mode != MODE_GROUP_K)
+        return launch_sk(p, stream, vec);
       // narrow problems: the direct-load loop when the reduction is whole 64-k stages (or
       // grouped-K over layout-T operands), else the register-staged loop
       const bool dl64 = dl_ok(p) && (p.mode == MODE_GROUP_K || p.K % 64 == 0);

@@ -117,6 +117,24 @@ def test_gemm_narrow_k64_shapes(a_t, b_t, M, N, K):
     assert_rel(_np(c), ref, FP32_RTOL, "gemm narrow fp32")
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 8, 8), (37, 40, 16), (1000, 520, 24), (4096, 512, 32), (70000, 64, 32)])
+def test_gemm_short_k(M, N, K):
+    """K <= 32 with k-contiguous operands (the barrier-free wave kernel): ragged 32-row and
+    32-column edges, K not a multiple of 16, fp32 with alpha + residual and bf16 outputs."""
+    H = _ops()
+    rng = np.random.default_rng(M + 11 * N + K)
+    A_ = bf16_round(rng.standard_normal((M, K)).astype(np.float32))
+    B_ = bf16_round(rng.standard_normal((N, K)).astype(np.float32))
+    r = rng.standard_normal((M, N)).astype(np.float32)
+    ref = A_.astype(np.float64) @ B_.astype(np.float64).T
+    print(f"gemm short-k M={M} N={N} K={K}", flush=True)
+    c = H.gemm(_bf(A_), _bf(B_), alpha=0.5, resid=torch.from_numpy(r).to(DEV), out_f32=True)
+    torch.cuda.synchronize()
+    assert_rel(_np(c), 0.5 * ref + r, FP32_RTOL, "gemm short-k fp32")
+    cb = H.gemm(_bf(A_), _bf(B_))
+    assert_rel(_np(cb), ref, 5e-3, "gemm short-k bf16")
+
+
 def test_gemm_bf16_out_resid_alpha():
     H = _ops()
     rng = np.random.default_rng(3)
