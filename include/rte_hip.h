@@ -147,6 +147,20 @@ int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const in
                      const float* sin_t, int B, int S, int H, int hd, void* dqkv, void* dx, float* dw,
                      void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- causal attention core, head_dim 32, 64 or 128 (the SDPA call of k_flash_causal_dense / _grouped,
+ *      rte/kernels/optimized.py:75-91, in rte/layers.py:53-75 and the banked attention :659-730) ----
+ * q, k, v bf16 [B, H, seq, hd] contiguous; out bf16 [B, seq, H, hd] (token-major rows of the
+ * O-projection input); lse f32 [B, H, seq] (log2 units: max + log2(sum 2^(s - max)) of
+ * s = q.k * scale * log2(e)), written by fwd and read by bwd.  head_scale f32 [B * H] (optional):
+ * out = head_scale[b, h] * softmax(q k^T * scale, causal) v.
+ * bwd: dout bf16 [B, seq, H, hd] (token-major); dq, dk, dv bf16 [B, H, seq, hd] (overwritten).
+ * Deterministic (fixed reduction order); 16-byte aligned buffers. */
+int rte_attention_fwd(const void* q, const void* k, const void* v, int B, int H, int seq, int head_dim, float scale,
+                      const float* head_scale, void* out, float* lse, void* stream);
+int rte_attention_bwd(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                      const float* lse, int B, int H, int seq, int head_dim, float scale, const float* head_scale,
+                      void* dq, void* dk, void* dv, void* stream);
+
 /* ---- SVD low-rank SwiGLU FFN (rte/layers.py:342-643 SVDFactorSparseFFN factors
  *      up_a = U S, up_b = V^T from refresh_svd :437-444) ----
  * us_ug bf16 [d, 2r] = [U_up S_up | U_gate S_gate], v_ug bf16 [2F, r] = [V_up ; V_gate],

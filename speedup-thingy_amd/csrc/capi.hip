@@ -57,6 +57,11 @@ size_t adamw_workspace_bytes(int nt, int nblk, int G);
 int adamw_step(const void* rows, int nt, const int32_t* blk, const int32_t* first_blk, int nblk, const double* hyper,
                int G, const int32_t* metric_lr_group, int M, float clip_max, const float* found_inf, float* metrics,
                void* ws, size_t ws_bytes, hipStream_t s);
+int attention_fwd(const bf16* q, const bf16* k, const bf16* v, int B, int H, int S, int head_dim, float scale,
+                  const float* hscale, bf16* out, float* lse, hipStream_t s);
+int attention_bwd(const bf16* q, const bf16* k, const bf16* v, const bf16* out, const bf16* dout, const float* lse,
+                  int B, int H, int S, int head_dim, float scale, const float* hscale, bf16* dq, bf16* dk, bf16* dv,
+                  hipStream_t s);
 size_t distill_workspace_bytes(int A, int R);
 int distill_fwd(const float* hot, const float* exact, const float* h0, int A, int S, int d, const float* hot_logits,
                 const float* exact_logits, int V, float t, float eps, const float* weights, float* losses,
@@ -797,6 +802,22 @@ int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, 
 int rte_macro_table_grad(const int64_t* key, int B, int seq, int n_keys, int d, const void* part, float* dgain,
                          float* dbias, float* dscale, void* stream) {
   return macro_table_grad(key, B, seq, n_keys, d, part, dgain, dbias, dscale, S(stream));
+}
+
+int rte_attention_fwd(const void* q, const void* k, const void* v, int B, int H, int seq, int head_dim, float scale,
+                      const float* head_scale, void* out, float* lse, void* stream) {
+  return attention_fwd(reinterpret_cast<const bf16*>(q), reinterpret_cast<const bf16*>(k),
+                       reinterpret_cast<const bf16*>(v), B, H, seq, head_dim, scale, head_scale, B16(out), lse,
+                       S(stream));
+}
+
+int rte_attention_bwd(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                      const float* lse, int B, int H, int seq, int head_dim, float scale, const float* head_scale,
+                      void* dq, void* dk, void* dv, void* stream) {
+  return attention_bwd(reinterpret_cast<const bf16*>(q), reinterpret_cast<const bf16*>(k),
+                       reinterpret_cast<const bf16*>(v), reinterpret_cast<const bf16*>(out),
+                       reinterpret_cast<const bf16*>(dout), lse, B, H, seq, head_dim, scale, head_scale, B16(dq),
+                       B16(dk), B16(dv), S(stream));
 }
 
 int rte_adamw_chunk(void) { return adamw_chunk(); }

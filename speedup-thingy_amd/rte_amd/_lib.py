@@ -74,6 +74,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_macro_epilogue_fwd": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _P, _F, _P, _P]),
     "rte_macro_epilogue_bwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _F, _P, _P, _P, _SZ, _P]),
     "rte_macro_table_grad": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
+    "rte_attention_fwd": (_I, [_P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P]),
+    "rte_attention_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P]),
     "rte_distill_workspace_bytes": (_SZ, [_I, _I]),
     "rte_distill_fwd": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P, _SZ, _P]),
     "rte_distill_bwd": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _I, _F, _F, _P, _P, _P, _SZ, _P, _P, _P]),

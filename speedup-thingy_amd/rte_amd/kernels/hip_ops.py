@@ -13,7 +13,7 @@ their gradients are fp32, the residual stream is fp32.
 from __future__ import annotations
 
 import ctypes
-
+import math
 from dataclasses import dataclass
 
 import torch
@@ -364,6 +364,50 @@ def attn_out_proj(y, w, resid=None):
     return AttnOutProjFn.apply(y, w, resid)
 
 
+# ----------------------------------------------------------------------------- attention core
+
+class AttentionFn(torch.autograd.Function):
+    """Causal softmax attention, head_dim 32 / 64 / 128, softmax scale 1/sqrt(head_dim) (torch
+    SDPA's default): out = head_scale[b, h] * softmax(q k^T scale, causal) v.  q, k, v [B, H, S, hd]
+    (bf16 on the kernel); the output is a [B, H, S, hd] view of token-major [B, S, H, hd] memory, which the
+    O-projection reads as plain rows.  head_scale (optional, [B, H], no gradient) is the banked
+    attention's recipe head mask applied to v (rte/layers.py:659-730)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, head_scale):
+        _lib.require_device_tensors("attention", q, k, v, head_scale)
+        B, H, S, hd = q.shape
+        if hd not in (32, 64, 128) or k.shape != q.shape or v.shape != q.shape:
+            raise ValueError("attention: q, k, v must share the shape [B, H, S, hd], hd 32, 64 or 128")
+        qb, kb, vb = (t.to(BF16).contiguous() for t in (q, k, v))
+        hs = None if head_scale is None else head_scale.reshape(B * H).to(F32).contiguous()
+        out = torch.empty((B, S, H, hd), dtype=BF16, device=q.device)
+        lse = torch.empty((B, H, S), dtype=F32, device=q.device)
+        scale = 1.0 / math.sqrt(hd)
+        call("rte_attention_fwd", ptr(qb), ptr(kb), ptr(vb), B, H, S, hd, scale, ptr(hs), ptr(out), ptr(lse), _s())
+        ctx.save_for_backward(qb, kb, vb, out, lse, hs)
+        ctx.scale = scale
+        ctx.dtypes = (q.dtype, k.dtype, v.dtype)
+        return out.transpose(1, 2)
+
+    @staticmethod
+    def backward(ctx, dout):
+        qb, kb, vb, out, lse, hs = ctx.saved_tensors
+        B, H, S, hd = qb.shape
+        dtok = dout.transpose(1, 2).to(BF16).contiguous()  # token-major [B, S, H, hd]
+        dq, dk, dv = (torch.empty_like(qb) for _ in range(3))
+        call("rte_attention_bwd", ptr(qb), ptr(kb), ptr(vb), ptr(out), ptr(dtok), ptr(lse), B, H, S, hd, ctx.scale,
+             ptr(hs), ptr(dq), ptr(dk), ptr(dv), _s())
+        qd, kd, vd = ctx.dtypes
+        return dq.to(qd), dk.to(kd), dv.to(vd), None
+
+
+def attention(q, k, v, head_scale=None):
+    if head_scale is not None and head_scale.requires_grad:
+        raise ValueError("attention: head_scale carries no gradient")
+    return AttentionFn.apply(q, k, v, head_scale)
+
+
 # ----------------------------------------------------------------------------- dense SwiGLU
 
 class DenseSwiGLUFn(torch.autograd.Function):
@@ -592,7 +636,7 @@ class GroupedPoolFn(torch.autograd.Function):
         C = F // n
         idc = ids.reshape(T, -1).contiguous().to(torch.int32)
         wc = w.reshape(T, -1).contiguous().to(F32)
-        wugb, wdb = wug_t.contiguous().to(BF16), wd_t.contiguous().to(BF16)
+        wugb, wdb = cast_bf16(wug_t), cast_bf16(wd_t)  # parameter views: once per step
         rs = None if resid is None else resid.reshape(T, d)
         out, pk, ug, zw = _pool_fwd(xb, idc, wc, wugb, wdb, C, n, rs, masked=True)
         ctx.save_for_backward(xb, wugb, wdb, pk.offsets, pk.tok_of_slot, pk.pair_of_slot, pk.slot_of_pair,

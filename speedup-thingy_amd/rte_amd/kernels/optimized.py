@@ -25,9 +25,9 @@ SYMBOLS: dict[str, str] = {
     "k_fused_rmsnorm": "hip",
     "k_rope_apply": "torch",
     "k_qkv_dense": "hip",
-    "k_flash_causal_dense": "torch_sdpa",
+    "k_flash_causal_dense": "hip",
     "k_qkv_grouped": "torch",
-    "k_flash_causal_grouped": "torch_sdpa",
+    "k_flash_causal_grouped": "hip",
     "k_out_proj_grouped": "torch",
     "k_swiglu_dense": "hip",
     "k_swiglu_grouped": "torch",
@@ -130,18 +130,10 @@ def k_logits_full(hidden, vocab_weight):
 # ----------------------------------------------------------------------------- attention core (SDPA)
 
 def _flash_attention(q, k, v):
-    _require_cuda_tensor(q, k, v)
-    if not q.is_cuda:
-        return F.scaled_dot_product_attention(q, k, v, is_causal=True)
-    try:
-        from torch.nn.attention import SDPBackend, sdpa_kernel
-
-        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
-            return F.scaled_dot_product_attention(q, k, v, is_causal=True)
-    except Exception:
-        if STRICT_CUDA and REQUIRE_FLASH:
-            raise
-        return F.scaled_dot_product_attention(q, k, v, is_causal=True)
+    """Causal attention with the softmax scale 1/sqrt(head_dim) (the reference's
+    F.scaled_dot_product_attention(q, k, v, is_causal=True)) on the HIP kernel; head_dim 32, 64 or 128."""
+    _hip_inputs("k_flash_causal", q, k, v)
+    return hip_ops.attention(q, k, v)
 
 
 def k_flash_causal_dense(q, k, v):

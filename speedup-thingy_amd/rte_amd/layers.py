@@ -212,8 +212,9 @@ class BankedAttention(nn.Module):
         out = None
         for bank in range(self.config.attn_banks):
             q, k, v = hip_ops.qkv_rope(x, self.wqkv[bank].t(), cos, sin, H)
-            v = v * head_scale[:, bank, :, None, None].to(v.dtype)
-            y = K.k_flash_causal_grouped(q, k, v)
+            # the recipe's head mask (1/|banks| on its heads, 0 elsewhere: rte/layers.py:702-730 runs
+            # only the active heads and averages the banks) scales each head's attention output
+            y = hip_ops.attention(q, k, v, head_scale[:, bank, :])
             out = hip_ops.attn_out_proj(y, self.wo[bank].t(), out)
         return out
 
