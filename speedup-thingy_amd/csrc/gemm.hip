@@ -954,10 +954,16 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs p, EpiFlags
   store_chunk<4>(p.epi, 0, m, n, p.N, v, fl.vec);
 }
 
-// Chunk of a GROUP_K group: about twice the mean group size, at least 256 rows, so balanced
-// groups stay whole and a dominant group is shared by many workgroups.
+// Chunk of a GROUP_K group: about half the mean group size, at least 256 rows, so a long
+// reduction is shared by a few workgroups (the fp32 partials cost less than the serial k
+// steps: measured on the cfg3 cluster-pool weight gradients) and a dominant group by many.
 int groupk_chunk(int K, int G) {
-  int64_t c = (2 * (int64_t)K + G - 1) / (G > 0 ? G : 1);
+  static const int env = [] {  // RTE_GK_CHUNK: fixed chunk for diagnostics
+    const char* v = getenv("RTE_GK_CHUNK");
+    return v && *v ? atoi(v) : 0;
+  }();
+  if (env >= 64) return (env + 63) / 64 * 64;
+  int64_t c = ((int64_t)K + G - 1) / (G > 0 ? G : 1) / 2;
   if (c < 256) c = 256;
   return (int)((c + 63) / 64 * 64);
 }
