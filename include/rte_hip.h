@@ -218,33 +218,50 @@ int rte_axpy_norm_bwd(const void* dn, const float* dx_ext, const float* x, const
 
 /* ---- bounded-residual macro operator Phi, elementwise ends (rte/macro.py:201-236; the
  *      (recipe, stride) low-rank matrices in between run as rte_grouped_linear_*) ----
- * prologue fwd: z bf16 [B*seq, 3d] = [h * rstd | mean over the sample's rows of h * rstd | h0],
- *               rstd f32 [B*seq] = rsqrt(mean(h^2) + eps) per row (h, h0 f32 [B, seq, d]).
- * prologue bwd: dh = dh_extra (optional) + rmsnorm backward of dz[:, :d] + dz[:, d:2d] / seq
- *               broadcast over the sample's rows; dh0 = dz[:, 2d:] (optional).
- * epilogue fwd: out = h + c * scale[k] * tanh(gain[k] * h + low + bias[k]), k = key[b] (int64 [B]),
+ * Samples b < B (key int64 [B]) read h rows of sample b % B_h and h0 rows of sample b % B_h0
+ * (B_h0 | B_h | B: one source batch evaluated under several keys, as the consistency loss does).
+ * prologue fwd (B = B_h samples): z bf16 [B_h*seq, 3d] = [h * rstd | mean over the sample's rows
+ *               of h * rstd | h0], rstd f32 [B_h*seq] = rsqrt(mean(h^2) + eps) per row
+ *               (h f32 [B_h, seq, d], h0 f32 [B_h0, seq, d]).
+ * prologue bwd: for each source sample b < B_h, over its repeats b + t B_h (B / B_h <= 4, in t
+ *               order): dh[b] = sum_t dh_extra[b + t B_h] (optional) + rmsnorm backward of
+ *               dz[b + t B_h, :d] + dz[b + t B_h, d:2d] / seq broadcast over the rows;
+ *               dh0[b] = sum_t dz[b + t B_h, 2d:] (optional; dh, dh0 f32 [B_h, seq, d], dz bf16
+ *               [B*seq, 3d]).
+ * epilogue fwd: out = h + c * scale[k] * tanh(gain[k] * h + low + bias[k]), k = key[b],
  *               tables gain / bias / scale f32 [keys, d], low f32 [B*seq, d].
- * epilogue bwd: dh = dout + dupd * gain[k], dlow bf16 = dupd, dupd = dout c scale[k] (1 - t^2);
- *               part (rte_macro_workspace_bytes) = per-sample, per-row-slice sums (dupd h | dupd |
- *               dout c t) for the tables.
+ * epilogue bwd: dh = dout + dupd * gain[k] (f32 [B, seq, d]), dlow bf16 = dupd,
+ *               dupd = dout c scale[k] (1 - t^2); part (rte_macro_workspace_bytes(B, ...)) =
+ *               per-sample, per-row-slice sums (dupd h | dupd | dout c t) for the tables.
  * table grad: dgain / dbias / dscale f32 [n_keys, d] (each optional) = sums of part's three column
  *               blocks over the samples with that key, in sample order (zero rows for unused keys);
  *               part as written by rte_macro_epilogue_bwd with the same B, seq, d.
- * The prologues take a workspace of rte_macro_workspace_bytes(B, seq, d) for their per-slice sums.
+ * The prologues take a workspace of rte_macro_workspace_bytes(B, seq, d) for their per-slice sums
+ * (B: the prologue's own batch, B_h for fwd and B for bwd).
  * d % 8 == 0, d <= 1024, B <= 65535 (table grad: B <= 16384), 16-byte aligned buffers. */
 size_t rte_macro_workspace_bytes(int B, int seq, int d);
-int rte_macro_prologue_fwd(const float* h, const float* h0, int B, int seq, int d, float eps, void* z, float* rstd,
-                           void* workspace, size_t workspace_bytes, void* stream);
-int rte_macro_prologue_bwd(const void* dz, const float* h, const float* rstd, const float* dh_extra, int B, int seq,
-                           int d, float* dh, float* dh0, void* workspace, size_t workspace_bytes, void* stream);
-int rte_macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int seq, int d,
+int rte_macro_prologue_fwd(const float* h, const float* h0, int B, int B_h0, int seq, int d, float eps, void* z,
+                           float* rstd, void* workspace, size_t workspace_bytes, void* stream);
+int rte_macro_prologue_bwd(const void* dz, const float* h, const float* rstd, const float* dh_extra, int B, int B_h,
+                           int seq, int d, float* dh, float* dh0, void* workspace, size_t workspace_bytes,
+                           void* stream);
+int rte_macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int B_h, int seq, int d,
                            const float* gain, const float* bias, const float* scale, float c, float* out,
                            void* stream);
-int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int seq,
-                           int d, const float* gain, const float* bias, const float* scale, float c, float* dh,
-                           void* dlow, void* part, size_t part_bytes, void* stream);
+int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int B_h,
+                           int seq, int d, const float* gain, const float* bias, const float* scale, float c,
+                           float* dh, void* dlow, void* part, size_t part_bytes, void* stream);
 int rte_macro_table_grad(const int64_t* key, int B, int seq, int n_keys, int d, const void* part, float* dgain,
                          float* dbias, float* dscale, void* stream);
+
+/* ---- mean squared difference (F.mse_loss of the macro consistency loss, rte/macro.py:342-359) ----
+ * fwd: out f32 [1] = mean((a - b)^2) over n f32 elements (fixed-order block sums, then one
+ * workgroup adds them in order); workspace rte_mse_workspace_bytes(n).
+ * bwd: da = dout[0] 2 (a - b) / n, db = -da (each optional).  16-byte aligned buffers. */
+size_t rte_mse_workspace_bytes(int64_t n);
+int rte_mse_fwd(const float* a, const float* b, int64_t n, float* out, void* workspace, size_t workspace_bytes,
+                void* stream);
+int rte_mse_bwd(const float* a, const float* b, int64_t n, const float* dout, float* da, float* db, void* stream);
 
 /* ---- fused AdamW step with the trainer's per-group norms (replaces torch.optim.AdamW.step,
  *      clip_grad_norm_ and _optimizer_grad_metrics of rte/training.py:385-468) ----

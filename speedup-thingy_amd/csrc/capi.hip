@@ -41,17 +41,20 @@ int axpy_norm_bwd(const bf16* dn, const float* dx_ext, const float* x, const flo
                   float* da, float* db, float* dkeep, float* dparams, void* ws, size_t ws_bytes, hipStream_t s);
 int macro_parts(int B, int S);
 size_t macro_workspace_bytes(int B, int S, int d);
-int macro_prologue_fwd(const float* h, const float* h0, int B, int S, int d, float eps, bf16* z, float* rstd, void* ws,
-                       size_t ws_bytes, hipStream_t s);
-int macro_prologue_bwd(const bf16* dz, const float* h, const float* rstd, const float* dh_extra, int B, int S, int d,
-                       float* dh, float* dh0, void* ws, size_t ws_bytes, hipStream_t s);
-int macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int S, int d, const float* gain,
-                       const float* bias, const float* scale, float c, float* out, hipStream_t s);
-int macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int S, int d,
-                       const float* gain, const float* bias, const float* scale, float c, float* dh, bf16* dlow,
+int macro_prologue_fwd(const float* h, const float* h0, int B, int Bh0, int S, int d, float eps, bf16* z, float* rstd,
+                       void* ws, size_t ws_bytes, hipStream_t s);
+int macro_prologue_bwd(const bf16* dz, const float* h, const float* rstd, const float* dh_extra, int Bt, int Bh, int S,
+                       int d, float* dh, float* dh0, void* ws, size_t ws_bytes, hipStream_t s);
+int macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int Bh, int S, int d,
+                       const float* gain, const float* bias, const float* scale, float c, float* out, hipStream_t s);
+int macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int Bh, int S,
+                       int d, const float* gain, const float* bias, const float* scale, float c, float* dh, bf16* dlow,
                        void* part, size_t part_bytes, hipStream_t s);
 int macro_table_grad(const int64_t* key, int B, int S, int G, int d, const void* part, float* dgain, float* dbias,
                      float* dscale, hipStream_t s);
+size_t mse_workspace_bytes(int64_t n);
+int mse_fwd(const float* a, const float* b, int64_t n, float* out, void* ws, size_t ws_bytes, hipStream_t s);
+int mse_bwd(const float* a, const float* b, int64_t n, const float* g, float* da, float* db, hipStream_t s);
 int adamw_chunk();
 size_t adamw_workspace_bytes(int nt, int nblk, int G);
 int adamw_step(const void* rows, int nt, const int32_t* blk, const int32_t* first_blk, int nblk, const double* hyper,
@@ -775,27 +778,28 @@ int rte_axpy_norm_bwd(const void* dn, const float* dx_ext, const float* x, const
 
 size_t rte_macro_workspace_bytes(int B, int seq, int d) { return macro_workspace_bytes(B, seq, d); }
 
-int rte_macro_prologue_fwd(const float* h, const float* h0, int B, int seq, int d, float eps, void* z, float* rstd,
-                           void* workspace, size_t workspace_bytes, void* stream) {
-  return macro_prologue_fwd(h, h0, B, seq, d, eps, B16(z), rstd, workspace, workspace_bytes, S(stream));
+int rte_macro_prologue_fwd(const float* h, const float* h0, int B, int B_h0, int seq, int d, float eps, void* z,
+                           float* rstd, void* workspace, size_t workspace_bytes, void* stream) {
+  return macro_prologue_fwd(h, h0, B, B_h0, seq, d, eps, B16(z), rstd, workspace, workspace_bytes, S(stream));
 }
 
-int rte_macro_prologue_bwd(const void* dz, const float* h, const float* rstd, const float* dh_extra, int B, int seq,
-                           int d, float* dh, float* dh0, void* workspace, size_t workspace_bytes, void* stream) {
-  return macro_prologue_bwd(reinterpret_cast<const bf16*>(dz), h, rstd, dh_extra, B, seq, d, dh, dh0, workspace,
+int rte_macro_prologue_bwd(const void* dz, const float* h, const float* rstd, const float* dh_extra, int B, int B_h,
+                           int seq, int d, float* dh, float* dh0, void* workspace, size_t workspace_bytes,
+                           void* stream) {
+  return macro_prologue_bwd(reinterpret_cast<const bf16*>(dz), h, rstd, dh_extra, B, B_h, seq, d, dh, dh0, workspace,
                             workspace_bytes, S(stream));
 }
 
-int rte_macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int seq, int d,
+int rte_macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int B_h, int seq, int d,
                            const float* gain, const float* bias, const float* scale, float c, float* out,
                            void* stream) {
-  return macro_epilogue_fwd(h, low, key, B, seq, d, gain, bias, scale, c, out, S(stream));
+  return macro_epilogue_fwd(h, low, key, B, B_h, seq, d, gain, bias, scale, c, out, S(stream));
 }
 
-int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int seq,
-                           int d, const float* gain, const float* bias, const float* scale, float c, float* dh,
-                           void* dlow, void* part, size_t part_bytes, void* stream) {
-  return macro_epilogue_bwd(dout, h, low, key, B, seq, d, gain, bias, scale, c, dh, B16(dlow), part, part_bytes,
+int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int B_h,
+                           int seq, int d, const float* gain, const float* bias, const float* scale, float c,
+                           float* dh, void* dlow, void* part, size_t part_bytes, void* stream) {
+  return macro_epilogue_bwd(dout, h, low, key, B, B_h, seq, d, gain, bias, scale, c, dh, B16(dlow), part, part_bytes,
                             S(stream));
 }
 
@@ -818,6 +822,17 @@ int rte_attention_bwd(const void* q, const void* k, const void* v, const void* o
                        reinterpret_cast<const bf16*>(v), reinterpret_cast<const bf16*>(out),
                        reinterpret_cast<const bf16*>(dout), lse, B, H, seq, head_dim, scale, head_scale, B16(dq),
                        B16(dk), B16(dv), S(stream));
+}
+
+size_t rte_mse_workspace_bytes(int64_t n) { return mse_workspace_bytes(n); }
+
+int rte_mse_fwd(const float* a, const float* b, int64_t n, float* out, void* workspace, size_t workspace_bytes,
+                void* stream) {
+  return mse_fwd(a, b, n, out, workspace, workspace_bytes, S(stream));
+}
+
+int rte_mse_bwd(const float* a, const float* b, int64_t n, const float* dout, float* da, float* db, void* stream) {
+  return mse_bwd(a, b, n, dout, da, db, S(stream));
 }
 
 int rte_adamw_chunk(void) { return adamw_chunk(); }

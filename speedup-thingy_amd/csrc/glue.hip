@@ -258,6 +258,83 @@ __global__ void __launch_bounds__(256) glue_colsum_kernel(const float* __restric
 
 bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
+// ---- mean squared difference (the macro consistency loss, rte/macro.py:342-359) ----
+// fwd: per-block sums of (a - b)^2 over fixed contiguous ranges (block-local tree in a fixed
+// order), then one workgroup adds the block sums in block order and scales by 1/n.
+constexpr int kMseThreads = 256, kMseMaxBlocks = 1024;
+
+__device__ __forceinline__ float block_sum_g(float v, float* red) {
+  v = wave_sum_g(v);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.0f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) t += red[i];
+  return t;
+}
+
+__global__ void __launch_bounds__(kMseThreads) mse_partial_kernel(const float* __restrict__ a, const float* __restrict__ b,
+                                                                  int64_t n, int64_t chunk, float* __restrict__ part) {
+  __shared__ float red[kMseThreads / 64];
+  const int64_t lo = (int64_t)blockIdx.x * chunk;
+  const int64_t hi = lo + chunk < n ? lo + chunk : n;
+  float s = 0.0f;
+  for (int64_t i = lo + 4 * threadIdx.x; i < hi; i += 4 * kMseThreads) {  // chunk is a multiple of 4
+    if (i + 4 <= hi) {
+      const float4 x = *reinterpret_cast<const float4*>(a + i), y = *reinterpret_cast<const float4*>(b + i);
+      const float d0 = x.x - y.x, d1 = x.y - y.y, d2 = x.z - y.z, d3 = x.w - y.w;
+      s += d0 * d0 + d1 * d1 + d2 * d2 + d3 * d3;
+    } else {
+      for (int64_t j = i; j < hi; ++j) {
+        const float dd = a[j] - b[j];
+        s += dd * dd;
+      }
+    }
+  }
+  s = block_sum_g(s, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = s;
+}
+
+__global__ void __launch_bounds__(kMseMaxBlocks) mse_final_kernel(const float* __restrict__ part, int nb, float inv_n,
+                                                                  float* __restrict__ out) {
+  __shared__ float red[kMseMaxBlocks / 64];
+  const float v = (int)threadIdx.x < nb ? part[threadIdx.x] : 0.0f;
+  const float t = block_sum_g(v, red);
+  if (threadIdx.x == 0) out[0] = t * inv_n;
+}
+
+// da = g 2 (a - b) / n, db = -da (each optional)
+__global__ void __launch_bounds__(256) mse_bwd_kernel(const float* __restrict__ a, const float* __restrict__ b, int64_t n,
+                                                      const float* __restrict__ g, float two_over_n,
+                                                      float* __restrict__ da, float* __restrict__ db) {
+  const float f = g[0] * two_over_n;
+  for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4; i < n; i += (int64_t)gridDim.x * 256 * 4) {
+    if (i + 4 <= n) {
+      const float4 x = *reinterpret_cast<const float4*>(a + i), y = *reinterpret_cast<const float4*>(b + i);
+      const float4 o = make_float4(f * (x.x - y.x), f * (x.y - y.y), f * (x.z - y.z), f * (x.w - y.w));
+      if (da) *reinterpret_cast<float4*>(da + i) = o;
+      if (db) *reinterpret_cast<float4*>(db + i) = make_float4(-o.x, -o.y, -o.z, -o.w);
+    } else {
+      for (int64_t j = i; j < n; ++j) {
+        const float o = f * (a[j] - b[j]);
+        if (da) da[j] = o;
+        if (db) db[j] = -o;
+      }
+    }
+  }
+}
+
+int mse_blocks(int64_t n, int64_t* chunk) {
+  int64_t nb = (n + 16383) / 16384;  // about 16 Ki elements per block
+  if (nb < 1) nb = 1;
+  if (nb > kMseMaxBlocks) nb = kMseMaxBlocks;
+  int64_t c = (n + nb - 1) / nb;
+  c = (c + 3) / 4 * 4;
+  *chunk = c;
+  return (int)((n + c - 1) / c > 0 ? (n + c - 1) / c : 1);
+}
+
 }  // namespace
 
 int axpy_norm_fwd(const float* a, const float* b, const float* c, const float* keep, const uint8_t* mask, int S,
@@ -313,6 +390,37 @@ int axpy_norm_bwd(const bf16* dn, const float* dx_ext, const float* x, const flo
   RTE_TRY(check_launch("axpy_norm_bwd"));
   hipLaunchKernelGGL(glue_colsum_kernel, dim3((W + 7) / 8), dim3(256), 0, s, part, nblk, W, dparams);
   return check_launch("axpy_norm_colsum");
+}
+
+size_t mse_workspace_bytes(int64_t n) {
+  int64_t chunk;
+  return (size_t)mse_blocks(n, &chunk) * sizeof(float);
+}
+
+int mse_fwd(const float* a, const float* b, int64_t n, float* out, void* ws, size_t ws_bytes, hipStream_t s) {
+  RTE_REQUIRE(n >= 1, "mse: need at least one element");
+  RTE_REQUIRE(((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0, "mse: 16-byte aligned inputs");
+  int64_t chunk;
+  const int nb = mse_blocks(n, &chunk);
+  RTE_REQUIRE(ws && ws_bytes >= (size_t)nb * sizeof(float), "mse: workspace too small");
+  float* part = static_cast<float*>(ws);
+  hipLaunchKernelGGL(mse_partial_kernel, dim3(nb), dim3(kMseThreads), 0, s, a, b, n, chunk, part);
+  RTE_TRY(check_launch("mse_partial"));
+  hipLaunchKernelGGL(mse_final_kernel, dim3(1), dim3(kMseMaxBlocks), 0, s, part, nb, (float)(1.0 / (double)n), out);
+  return check_launch("mse_final");
+}
+
+int mse_bwd(const float* a, const float* b, int64_t n, const float* g, float* da, float* db, hipStream_t s) {
+  RTE_REQUIRE(n >= 1, "mse: need at least one element");
+  RTE_REQUIRE(((uintptr_t)a & 15) == 0 && ((uintptr_t)b & 15) == 0 && ((uintptr_t)da & 15) == 0 &&
+                  ((uintptr_t)db & 15) == 0,
+              "mse: 16-byte aligned buffers");
+  if (!da && !db) return 0;
+  int64_t blocks = (n + 1023) / 1024;
+  if (blocks > 4096) blocks = 4096;
+  hipLaunchKernelGGL(mse_bwd_kernel, dim3((unsigned)blocks), dim3(256), 0, s, a, b, n, g, (float)(2.0 / (double)n), da,
+                     db);
+  return check_launch("mse_bwd");
 }
 
 }  // namespace rte

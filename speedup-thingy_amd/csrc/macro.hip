@@ -9,6 +9,12 @@
 // per-sample column sums of the table gradients; the prologue adds the rmsnorm / mean
 // backward to dh and gives dh0.
 //
+// Repeated sources: the operator may run on Bt samples whose h rows are those of sample b % Bh
+// and whose h0 rows are those of sample b % Bh0 (Bh0 | Bh | Bt), e.g. one source batch under
+// several (recipe, stride) keys.  z depends on (h, h0) only, so the prologue runs on the Bh
+// distinct samples and the grouped GEMMs gather its rows; the prologue backward adds the Bt / Bh
+// repeats of a sample in repeat order.
+//
 // Layout: one wave per row, each lane owning NCH chunks of 8 consecutive columns (16- and
 // 32-byte accesses; d % 8 == 0, d <= 512 * NCH).  Reductions over a sample's rows run in one
 // workgroup of 8 waves: per-lane partials, then the 8 wave partials in wave order, so every
@@ -101,8 +107,9 @@ __device__ __forceinline__ void store_part_sum(float* red, const float (&vals)[N
 }
 
 // mean[0, d) = (sum over the sample's P part sums, in part order) / S, in LDS.
-__device__ __forceinline__ void part_mean(const float* __restrict__ part, int S, int P, int d, float* mean) {
-  const float* pb = part + (int64_t)blockIdx.y * P * d;
+__device__ __forceinline__ void part_mean(const float* __restrict__ part, int S, int P, int d, float* mean,
+                                          int64_t sample) {
+  const float* pb = part + sample * P * d;
   const float invS = 1.0f / (float)S;
   for (int col = threadIdx.x; col < d; col += kMacroWaves * 64) {
     float s = 0.0f;
@@ -121,13 +128,14 @@ __device__ __forceinline__ void part_mean(const float* __restrict__ part, int S,
 // z[:, :d] = h * rstd, z[:, 2d:] = h0, rstd per row; part[b, p] = column sums of h * rstd.
 template <int NCH>
 __global__ void __launch_bounds__(512) macro_prologue_fwd_kernel(const float* __restrict__ h,
-                                                                 const float* __restrict__ h0, int S, int P, int d,
-                                                                 float eps, bf16* __restrict__ z,
+                                                                 const float* __restrict__ h0, int Bh0, int S, int P,
+                                                                 int d, float eps, bf16* __restrict__ z,
                                                                  float* __restrict__ rstd, float* __restrict__ part) {
   extern __shared__ float red[];  // [8][d]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = d / 8, D3 = 3 * d;
   const RowPart rp = row_part(S, P);
+  const int64_t base0 = (int64_t)(blockIdx.y % Bh0) * S;  // h0 rows of this sample
   float pool[NCH][8];
 #pragma unroll
   for (int j = 0; j < NCH; ++j)
@@ -142,7 +150,7 @@ __global__ void __launch_bounds__(512) macro_prologue_fwd_kernel(const float* __
       const int ch = lane + 64 * j;
       if (ch >= nch) continue;
       ld8m(h + r * d + ch * 8, x[j]);
-      ld8m(h0 + r * d + ch * 8, o[j]);
+      ld8m(h0 + (base0 + s) * d + ch * 8, o[j]);
     }
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
@@ -179,7 +187,7 @@ __global__ void __launch_bounds__(512) macro_prologue_mean_kernel(const float* _
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = d / 8, D3 = 3 * d;
   const RowPart rp = row_part(S, P);
-  part_mean(part, S, P, d, mean);
+  part_mean(part, S, P, d, mean, blockIdx.y);
   for (int s = rp.s0 + wave; s < rp.s1; s += kMacroWaves) {
     const int64_t r = rp.base + s;
 #pragma unroll
@@ -221,68 +229,86 @@ __global__ void __launch_bounds__(512) macro_prologue_bwd_sum_kernel(const bf16*
   store_part_sum<NCH>(red, gp, d, part + ((int64_t)blockIdx.y * P + blockIdx.x) * d);
 }
 
-// dh = dh_extra + rmsnorm backward of (dz[:, :d] + mean-broadcast of dz[:, d:2d]); dh0 = dz[:, 2d:]
+constexpr int kMaxRep = 4;  // repeats of a source sample the prologue backward adds
+
+// Per source sample b (grid y over Bh) and its repeats b + t Bh (t < rep):
+//   dh[b]  = sum_t dh_extra[b + t Bh] + rmsnorm backward of (dz[b + t Bh, :d] + mean-broadcast of
+//            dz[b + t Bh, d:2d])        (x and rstd are the source sample's)
+//   dh0[b] = sum_t dz[b + t Bh, 2d:]
 template <int NCH>
 __global__ void __launch_bounds__(512) macro_prologue_bwd_kernel(const bf16* __restrict__ dz,
                                                                  const float* __restrict__ h,
                                                                  const float* __restrict__ rstd,
                                                                  const float* __restrict__ dh_extra,
-                                                                 const float* __restrict__ part, int S, int P, int d,
-                                                                 float* __restrict__ dh, float* __restrict__ dh0) {
-  __shared__ float mean[1024];
+                                                                 const float* __restrict__ part, int Bh, int rep,
+                                                                 int S, int P, int d, float* __restrict__ dh,
+                                                                 float* __restrict__ dh0) {
+  __shared__ float mean[kMaxRep][1024];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nch = d / 8, D3 = 3 * d;
   const RowPart rp = row_part(S, P);
-  part_mean(part, S, P, d, mean);
-  float gp[NCH][8];
-#pragma unroll
-  for (int j = 0; j < NCH; ++j) {
-    const int ch = lane + 64 * j;
-    if (ch < nch) ld8m(mean + ch * 8, gp[j]);
-  }
+  for (int t = 0; t < rep; ++t) part_mean(part, S, P, d, mean[t], (int64_t)blockIdx.y + (int64_t)t * Bh);
   for (int s = rp.s0 + wave; s < rp.s1; s += kMacroWaves) {
-    const int64_t r = rp.base + s;
+    const int64_t r = rp.base + s;  // source row
     const float rr = rstd[r];
-    float g[NCH][8], x[NCH][8], e[NCH][8];
-    float dot = 0.0f;
+    float x[NCH][8], acc[NCH][8], acc0[NCH][8];
 #pragma unroll
-    for (int j = 0; j < NCH; ++j) {  // every load of the row issued before the reduction
+    for (int j = 0; j < NCH; ++j) {
       const int ch = lane + 64 * j;
-      if (ch >= nch) continue;
-      ld8m(dz + r * D3 + ch * 8, g[j]);
-      ld8m(h + r * d + ch * 8, x[j]);
-      if (dh_extra) {
-        ld8m(dh_extra + r * d + ch * 8, e[j]);
-      } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) e[j][i] = 0.0f;
+      for (int i = 0; i < 8; ++i) acc[j][i] = acc0[j][i] = 0.0f;
+      if (ch < nch) ld8m(h + r * d + ch * 8, x[j]);
+    }
+    for (int t = 0; t < rep; ++t) {
+      const int64_t rt = r + (int64_t)t * Bh * S;  // row of repeat t
+      float g[NCH][8], e[NCH][8];
+      float dot = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {  // every load of the row issued before the reduction
+        const int ch = lane + 64 * j;
+        if (ch >= nch) continue;
+        ld8m(dz + rt * D3 + ch * 8, g[j]);
+        if (dh_extra) {
+          ld8m(dh_extra + rt * d + ch * 8, e[j]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) e[j][i] = 0.0f;
+        }
+        if (dh0) {
+          float q[8];
+          ld8m(dz + rt * D3 + 2 * d + ch * 8, q);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc0[j][i] += q[i];
+        }
       }
-      if (dh0) {
-        float q[8];
-        ld8m(dz + r * D3 + 2 * d + ch * 8, q);
-        st8m(dh0 + r * d + ch * 8, q);
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int ch = lane + 64 * j;
+        if (ch >= nch) continue;
+        float m[8];
+        ld8m(mean[t] + ch * 8, m);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          g[j][i] += m[i];
+          dot += g[j][i] * x[j][i];
+        }
+      }
+      dot = wsum_m(dot);
+      const float coef = rr * rr * rr * dot / (float)d;
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+        const int ch = lane + 64 * j;
+        if (ch >= nch) continue;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[j][i] += rr * g[j][i] - x[j][i] * coef + e[j][i];
       }
     }
 #pragma unroll
     for (int j = 0; j < NCH; ++j) {
       const int ch = lane + 64 * j;
       if (ch >= nch) continue;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        g[j][i] += gp[j][i];
-        dot += g[j][i] * x[j][i];
-      }
-    }
-    dot = wsum_m(dot);
-    const float coef = rr * rr * rr * dot / (float)d;
-#pragma unroll
-    for (int j = 0; j < NCH; ++j) {
-      const int ch = lane + 64 * j;
-      if (ch >= nch) continue;
-      float o[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = rr * g[j][i] - x[j][i] * coef + e[j][i];
-      st8m(dh + r * d + ch * 8, o);
+      st8m(dh + r * d + ch * 8, acc[j]);
+      if (dh0) st8m(dh0 + r * d + ch * 8, acc0[j]);
     }
   }
 }
@@ -291,8 +317,8 @@ __global__ void __launch_bounds__(512) macro_prologue_bwd_kernel(const bf16* __r
 template <int NCH>
 __global__ void __launch_bounds__(256) macro_epilogue_fwd_kernel(const float* __restrict__ h,
                                                                  const float* __restrict__ low,
-                                                                 const int64_t* __restrict__ key, int S, int64_t R,
-                                                                 int d, const float* __restrict__ gain,
+                                                                 const int64_t* __restrict__ key, int Bh, int S,
+                                                                 int64_t R, int d, const float* __restrict__ gain,
                                                                  const float* __restrict__ bias,
                                                                  const float* __restrict__ scale, float c,
                                                                  float* __restrict__ out) {
@@ -301,13 +327,14 @@ __global__ void __launch_bounds__(256) macro_epilogue_fwd_kernel(const float* __
   if (r >= R) return;
   const int nch = d / 8;
   const int64_t kb = key[r / S] * d;
+  const int64_t hr = ((r / S) % Bh) * S + r % S;  // source row of h
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
     const int ch = lane + 64 * j;
     if (ch >= nch) continue;
     const int col = ch * 8;
     float x[8], l[8], gn[8], bs[8], sc[8], o[8];
-    ld8m(h + r * d + col, x);
+    ld8m(h + hr * d + col, x);
     ld8m(low + r * d + col, l);
     ld8m(gain + kb + col, gn);
     ld8m(bias + kb + col, bs);
@@ -325,8 +352,8 @@ template <int NCH>
 __global__ void __launch_bounds__(512) macro_epilogue_bwd_kernel(const float* __restrict__ dout,
                                                                  const float* __restrict__ h,
                                                                  const float* __restrict__ low,
-                                                                 const int64_t* __restrict__ key, int S, int P,
-                                                                 int d, const float* __restrict__ gain,
+                                                                 const int64_t* __restrict__ key, int Bh, int S,
+                                                                 int P, int d, const float* __restrict__ gain,
                                                                  const float* __restrict__ bias,
                                                                  const float* __restrict__ scale, float c,
                                                                  float* __restrict__ dh, bf16* __restrict__ dlow,
@@ -336,6 +363,7 @@ __global__ void __launch_bounds__(512) macro_epilogue_bwd_kernel(const float* __
   const int nch = d / 8;
   const RowPart rp = row_part(S, P);
   const int64_t kb = key[blockIdx.y] * d;
+  const int64_t hoff = (int64_t)(blockIdx.y % Bh) * S * d;  // source rows of h
   float gn[NCH][8], bs[NCH][8], sc[NCH][8], pg[NCH][8], pb[NCH][8], ps[NCH][8];
 #pragma unroll
   for (int j = 0; j < NCH; ++j) {
@@ -355,7 +383,7 @@ __global__ void __launch_bounds__(512) macro_epilogue_bwd_kernel(const float* __
       if (ch >= nch) continue;
       const int64_t off = r * d + ch * 8;
       float x[8], l[8], go[8], oh[8], ol[8];
-      ld8m(h + off, x);
+      ld8m(h + hoff + s * d + ch * 8, x);
       ld8m(low + off, l);
       ld8m(dout + off, go);
 #pragma unroll
@@ -464,58 +492,66 @@ size_t macro_workspace_bytes(int B, int S, int d) {
       hipLaunchKernelGGL(kern<2>, dim3(P, B), dim3(kMacroWaves * 64), lds, s, __VA_ARGS__);   \
   } while (0)
 
-int macro_prologue_fwd(const float* h, const float* h0, int B, int S, int d, float eps, bf16* z, float* rstd, void* ws,
-                       size_t ws_bytes, hipStream_t s) {
+int macro_prologue_fwd(const float* h, const float* h0, int B, int Bh0, int S, int d, float eps, bf16* z, float* rstd,
+                       void* ws, size_t ws_bytes, hipStream_t s) {
   MACRO_SIZES("macro_prologue");
+  RTE_REQUIRE(Bh0 >= 1 && B % Bh0 == 0, "macro_prologue: the h0 batch must divide the h batch");
   RTE_REQUIRE(al16m(h) && al16m(h0) && al16m(z), "macro_prologue: 16-byte aligned buffers");
   if (B == 0) return 0;
   RTE_REQUIRE(ws && ws_bytes >= macro_workspace_bytes(B, S, d), "macro_prologue: workspace too small");
   const int P = macro_parts(B, S);
   float* part = static_cast<float*>(ws);
   const size_t lds = (size_t)kMacroWaves * d * sizeof(float);
-  MACRO_LAUNCH(macro_prologue_fwd_kernel, lds, h, h0, S, P, d, eps, z, rstd, part);
+  MACRO_LAUNCH(macro_prologue_fwd_kernel, lds, h, h0, Bh0, S, P, d, eps, z, rstd, part);
   RTE_TRY(check_launch("macro_prologue_fwd"));
   MACRO_LAUNCH(macro_prologue_mean_kernel, 0, part, S, P, d, z);
   return check_launch("macro_prologue_mean");
 }
 
-int macro_prologue_bwd(const bf16* dz, const float* h, const float* rstd, const float* dh_extra, int B, int S, int d,
-                       float* dh, float* dh0, void* ws, size_t ws_bytes, hipStream_t s) {
+int macro_prologue_bwd(const bf16* dz, const float* h, const float* rstd, const float* dh_extra, int Bt, int Bh, int S,
+                       int d, float* dh, float* dh0, void* ws, size_t ws_bytes, hipStream_t s) {
+  const int B = Bt;
   MACRO_SIZES("macro_prologue_bwd");
+  RTE_REQUIRE(Bh >= 1 && Bt % Bh == 0 && Bt / Bh <= kMaxRep, "macro_prologue_bwd: Bt must be 1 to 4 times Bh");
   RTE_REQUIRE(al16m(dz) && al16m(h) && al16m(dh_extra) && al16m(dh) && al16m(dh0),
               "macro_prologue_bwd: 16-byte aligned buffers");
-  if (B == 0) return 0;
-  RTE_REQUIRE(ws && ws_bytes >= macro_workspace_bytes(B, S, d), "macro_prologue_bwd: workspace too small");
-  const int P = macro_parts(B, S);
+  if (Bt == 0) return 0;
+  RTE_REQUIRE(ws && ws_bytes >= macro_workspace_bytes(Bt, S, d), "macro_prologue_bwd: workspace too small");
+  const int P = macro_parts(Bt, S);
   float* part = static_cast<float*>(ws);
   const size_t lds = (size_t)kMacroWaves * d * sizeof(float);
   MACRO_LAUNCH(macro_prologue_bwd_sum_kernel, lds, dz, S, P, d, part);
   RTE_TRY(check_launch("macro_prologue_bwd_sum"));
-  MACRO_LAUNCH(macro_prologue_bwd_kernel, 0, dz, h, rstd, dh_extra, part, S, P, d, dh, dh0);
+  {
+    const int B = Bh;  // one workgroup per source sample and row slice
+    MACRO_LAUNCH(macro_prologue_bwd_kernel, 0, dz, h, rstd, dh_extra, part, Bh, Bt / Bh, S, P, d, dh, dh0);
+  }
   return check_launch("macro_prologue_bwd");
 }
 
-int macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int S, int d, const float* gain,
-                       const float* bias, const float* scale, float c, float* out, hipStream_t s) {
+int macro_epilogue_fwd(const float* h, const float* low, const int64_t* key, int B, int Bh, int S, int d,
+                       const float* gain, const float* bias, const float* scale, float c, float* out, hipStream_t s) {
   MACRO_SIZES("macro_epilogue");
+  RTE_REQUIRE(Bh >= 1 && B % Bh == 0, "macro_epilogue: the h batch must divide the batch");
   RTE_REQUIRE(al16m(h) && al16m(low) && al16m(gain) && al16m(bias) && al16m(scale) && al16m(out),
               "macro_epilogue: 16-byte aligned buffers");
   const int64_t R = (int64_t)B * S;
   if (R == 0) return 0;
   const dim3 grid((unsigned)((R + 3) / 4));
   if (d <= 512)
-    hipLaunchKernelGGL(macro_epilogue_fwd_kernel<1>, grid, dim3(256), 0, s, h, low, key, S, R, d, gain, bias, scale, c,
-                       out);
+    hipLaunchKernelGGL(macro_epilogue_fwd_kernel<1>, grid, dim3(256), 0, s, h, low, key, Bh, S, R, d, gain, bias, scale,
+                       c, out);
   else
-    hipLaunchKernelGGL(macro_epilogue_fwd_kernel<2>, grid, dim3(256), 0, s, h, low, key, S, R, d, gain, bias, scale, c,
-                       out);
+    hipLaunchKernelGGL(macro_epilogue_fwd_kernel<2>, grid, dim3(256), 0, s, h, low, key, Bh, S, R, d, gain, bias, scale,
+                       c, out);
   return check_launch("macro_epilogue_fwd");
 }
 
-int macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int S, int d,
-                       const float* gain, const float* bias, const float* scale, float c, float* dh, bf16* dlow,
+int macro_epilogue_bwd(const float* dout, const float* h, const float* low, const int64_t* key, int B, int Bh, int S,
+                       int d, const float* gain, const float* bias, const float* scale, float c, float* dh, bf16* dlow,
                        void* part, size_t part_bytes, hipStream_t s) {
   MACRO_SIZES("macro_epilogue_bwd");
+  RTE_REQUIRE(Bh >= 1 && B % Bh == 0, "macro_epilogue_bwd: the h batch must divide the batch");
   RTE_REQUIRE(al16m(dout) && al16m(h) && al16m(low) && al16m(gain) && al16m(bias) && al16m(scale) && al16m(dh) &&
                   al16m(dlow),
               "macro_epilogue_bwd: 16-byte aligned buffers");
@@ -523,7 +559,7 @@ int macro_epilogue_bwd(const float* dout, const float* h, const float* low, cons
   RTE_REQUIRE(part && part_bytes >= macro_workspace_bytes(B, S, d), "macro_epilogue_bwd: part buffer too small");
   const int P = macro_parts(B, S);
   const size_t lds = (size_t)kMacroWaves * d * sizeof(float);
-  MACRO_LAUNCH(macro_epilogue_bwd_kernel, lds, dout, h, low, key, S, P, d, gain, bias, scale, c, dh, dlow,
+  MACRO_LAUNCH(macro_epilogue_bwd_kernel, lds, dout, h, low, key, Bh, S, P, d, gain, bias, scale, c, dh, dlow,
                static_cast<float*>(part));
   return check_launch("macro_epilogue_bwd");
 }

@@ -69,13 +69,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_adamw_workspace_bytes": (_SZ, [_I, _I, _I]),
     "rte_adamw_step": (_I, [_P, _I, _P, _P, _I, _P, _I, _P, _I, _F, _P, _P, _P, _SZ, _P]),
     "rte_macro_workspace_bytes": (_SZ, [_I, _I, _I]),
-    "rte_macro_prologue_fwd": (_I, [_P, _P, _I, _I, _I, _F, _P, _P, _P, _SZ, _P]),
-    "rte_macro_prologue_bwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _SZ, _P]),
-    "rte_macro_epilogue_fwd": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _P, _F, _P, _P]),
-    "rte_macro_epilogue_bwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _F, _P, _P, _P, _SZ, _P]),
+    "rte_macro_prologue_fwd": (_I, [_P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _SZ, _P]),
+    "rte_macro_prologue_bwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _SZ, _P]),
+    "rte_macro_epilogue_fwd": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _F, _P, _P]),
+    "rte_macro_epilogue_bwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _F, _P, _P, _P, _SZ, _P]),
     "rte_macro_table_grad": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
     "rte_attention_fwd": (_I, [_P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P]),
     "rte_attention_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P]),
+    "rte_mse_workspace_bytes": (_SZ, [_I64]),
+    "rte_mse_fwd": (_I, [_P, _P, _I64, _P, _P, _SZ, _P]),
+    "rte_mse_bwd": (_I, [_P, _P, _I64, _P, _P, _P, _P]),
     "rte_distill_workspace_bytes": (_SZ, [_I, _I]),
     "rte_distill_fwd": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P, _SZ, _P]),
     "rte_distill_bwd": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _I, _F, _F, _P, _P, _P, _SZ, _P, _P, _P]),

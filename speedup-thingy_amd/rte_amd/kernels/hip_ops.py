@@ -886,19 +886,24 @@ class GroupedLinearFn(torch.autograd.Function):
         return (None if dx is None else dx.view(shape).to(x_dt), None if dw is None else dw.to(w_dt), None, None)
 
 
-def _grouped_linear_fwd(xb, wb, pk: PackIndex, out_f32: bool):
+def _grouped_linear_fwd(xb, wb, pk: PackIndex, out_f32: bool, tok=None, n_out: int | None = None):
+    """y[pair_of_slot] = x[tok] @ W[group] (tok defaults to pk.tok_of_slot; y has n_out rows,
+    default the rows of x)."""
     N, K = xb.shape
     G, _, Nout = wb.shape
-    y = torch.empty((N, Nout), dtype=F32 if out_f32 else BF16, device=xb.device)
-    call("rte_grouped_linear_fwd", ptr(xb), N, K, ptr(pk.offsets), G, pk.tok_of_slot.numel(), ptr(pk.tok_of_slot),
+    tok = pk.tok_of_slot if tok is None else tok
+    y = torch.empty((N if n_out is None else n_out, Nout), dtype=F32 if out_f32 else BF16, device=xb.device)
+    call("rte_grouped_linear_fwd", ptr(xb), N, K, ptr(pk.offsets), G, tok.numel(), ptr(tok),
          ptr(pk.pair_of_slot), ptr(wb), Nout, ptr(y), int(out_f32), _s())
     return y
 
 
-def _grouped_linear_bwd(dyb, xb, wb, offsets, tok, pos, need_x: bool, need_w: bool, dx_f32: bool):
-    """(dx [N, K] (fp32 or bf16) or None, dW fp32 [G, K, Nout] or None) of y = x @ W[key]."""
+def _grouped_linear_bwd(dyb, xb, wb, offsets, tok, pos, need_x: bool, need_w: bool, dx_f32: bool,
+                        n_x: int | None = None):
+    """(dx [N, K] (fp32 or bf16) or None, dW fp32 [G, K, Nout] or None) of y = x @ W[key]; dx is
+    scattered to the rows `tok` (n_x rows, default the rows of x)."""
     G, K, Nout = wb.shape
-    N = xb.shape[0]
+    N = xb.shape[0] if n_x is None else n_x
     dx = torch.empty((N, K), dtype=F32 if dx_f32 else BF16, device=xb.device) if need_x else None
     dw = torch.empty((G, K, Nout), dtype=F32, device=xb.device) if need_w else None
     P = tok.numel()
@@ -916,42 +921,51 @@ class MacroBoundedFn(torch.autograd.Function):
         low = silu(z @ V[key]) @ U[key]                             (grouped MFMA GEMMs)
         out = h + c * scale[key] * tanh(gain[key] * h + low + bias[key])   (epilogue kernel)
 
-    key = recipe * strides + stride per sample.  The backward reduces the per-key table and
-    matrix gradients in a fixed order (per-sample column sums, then the segmented reduction;
-    grouped-K GEMMs for V and U)."""
+    key = recipe * strides + stride per sample.  key may hold more samples than h and h0: sample
+    b uses h[b % len(h)] and h0[b % len(h0)] (len(h0) | len(h) | len(key), at most 4 repeats of
+    h), so one source batch runs under several keys without copies; z is formed once per source
+    sample and the grouped GEMM gathers its rows.  The backward reduces the per-key table and
+    matrix gradients in a fixed order and adds the repeats of a source sample in repeat order."""
 
     @staticmethod
     def forward(ctx, h, h0, key, pk, v, u, gain, bias, scale, c, eps):
         _lib.require_device_tensors("macro_bounded", h, h0, key, v, u, gain, bias, scale)
-        B, S, d = h.shape
+        Bh, S, d = h.shape
+        Bh0 = h0.shape[0]
+        kv = key.reshape(-1).contiguous().to(torch.int64)
+        B = kv.numel()
+        if Bh0 < 1 or Bh % Bh0 or B % Bh or B // Bh > 4 or h0.shape[1:] != h.shape[1:]:
+            raise ValueError("macro_bounded: need len(h0) | len(h) | len(key) with at most 4 repeats of h")
         G = v.shape[0] * v.shape[1]
         hv = h.contiguous().to(F32)
         h0v = h0.contiguous().to(F32)
-        kv = key.reshape(-1).contiguous().to(torch.int64)
         dev = h.device
-        z = torch.empty((B * S, 3 * d), dtype=BF16, device=dev)
-        rstd = torch.empty((B * S,), dtype=F32, device=dev)
-        wsb = _lib.load().rte_macro_workspace_bytes(B, S, d)
+        z = torch.empty((Bh * S, 3 * d), dtype=BF16, device=dev)
+        rstd = torch.empty((Bh * S,), dtype=F32, device=dev)
+        wsb = _lib.load().rte_macro_workspace_bytes(Bh, S, d)
         ws = torch.empty((max(wsb // 4, 1),), dtype=F32, device=dev)
-        call("rte_macro_prologue_fwd", ptr(hv), ptr(h0v), B, S, d, float(eps), ptr(z), ptr(rstd), ptr(ws), wsb, _s())
+        call("rte_macro_prologue_fwd", ptr(hv), ptr(h0v), Bh, Bh0, S, d, float(eps), ptr(z), ptr(rstd), ptr(ws), wsb,
+             _s())
+        # rows of z for the slots: pk's rows are b * S + s over all B samples
+        tok_z = pk.tok_of_slot if B == Bh else torch.remainder(pk.tok_of_slot, Bh * S)
         vb = cast_bf16(v.reshape(G, v.shape[-2], v.shape[-1]))
         ub = cast_bf16(u.reshape(G, u.shape[-2], u.shape[-1]))
-        a = _grouped_linear_fwd(z, vb, pk, out_f32=False)
+        a = _grouped_linear_fwd(z, vb, pk, out_f32=False, tok=tok_z, n_out=B * S)
         sa = torch.nn.functional.silu(a)
         low = _grouped_linear_fwd(sa, ub, pk, out_f32=True)
         tabs = [t.reshape(G, d).contiguous().to(F32) for t in (gain, bias, scale)]
         out = torch.empty((B, S, d), dtype=F32, device=dev)
-        call("rte_macro_epilogue_fwd", ptr(hv), ptr(low), ptr(kv), B, S, d, ptr(tabs[0]), ptr(tabs[1]), ptr(tabs[2]),
-             float(c), ptr(out), _s())
-        ctx.save_for_backward(hv, kv, pk.offsets, pk.tok_of_slot, pk.pair_of_slot, vb, ub, z, rstd, a, sa, low,
-                              *tabs)
-        ctx.meta = (B, S, d, G, float(c), v.shape, u.shape, gain.shape, h.dtype, h0.dtype)
+        call("rte_macro_epilogue_fwd", ptr(hv), ptr(low), ptr(kv), B, Bh, S, d, ptr(tabs[0]), ptr(tabs[1]),
+             ptr(tabs[2]), float(c), ptr(out), _s())
+        ctx.save_for_backward(hv, kv, pk.offsets, pk.tok_of_slot, pk.pair_of_slot, tok_z, vb, ub, z, rstd, a, sa,
+                              low, *tabs)
+        ctx.meta = (B, Bh, Bh0, S, d, G, float(c), v.shape, u.shape, gain.shape, h.dtype, h0.dtype)
         return out.to(h.dtype)
 
     @staticmethod
     def backward(ctx, dout):
-        hv, kv, offsets, tok, pos, vb, ub, z, rstd, a, sa, low, tg, tb, ts = ctx.saved_tensors
-        B, S, d, G, c, v_shape, u_shape, t_shape, h_dt, h0_dt = ctx.meta
+        hv, kv, offsets, tok, pos, tok_z, vb, ub, z, rstd, a, sa, low, tg, tb, ts = ctx.saved_tensors
+        B, Bh, Bh0, S, d, G, c, v_shape, u_shape, t_shape, h_dt, h0_dt = ctx.meta
         nia = ctx.needs_input_grad
         dev = hv.device
         do = dout.contiguous().to(F32)
@@ -959,17 +973,25 @@ class MacroBoundedFn(torch.autograd.Function):
         dlow = torch.empty((B * S, d), dtype=BF16, device=dev)
         wsb = _lib.load().rte_macro_workspace_bytes(B, S, d)
         ws = torch.empty((max(wsb // 4, 1),), dtype=F32, device=dev)
-        call("rte_macro_epilogue_bwd", ptr(do), ptr(hv), ptr(low), ptr(kv), B, S, d, ptr(tg), ptr(tb), ptr(ts),
+        call("rte_macro_epilogue_bwd", ptr(do), ptr(hv), ptr(low), ptr(kv), B, Bh, S, d, ptr(tg), ptr(tb), ptr(ts),
              c, ptr(dh_epi), ptr(dlow), ptr(ws), wsb, _s())
         tabs_out = [torch.empty((G, d), dtype=F32, device=dev) if nia[6 + i] else None for i in range(3)]
         call("rte_macro_table_grad", ptr(kv), B, S, G, d, ptr(ws), *(ptr(t) for t in tabs_out), _s())
         dsa, du = _grouped_linear_bwd(dlow, sa, ub, offsets, tok, pos, True, nia[5], False)
         da = torch.ops.aten.silu_backward(dsa, a)
-        dz, dv = _grouped_linear_bwd(da, z, vb, offsets, tok, pos, True, nia[4], False)
-        dh = torch.empty((B, S, d), dtype=F32, device=dev)
-        dh0 = torch.empty((B, S, d), dtype=F32, device=dev) if nia[1] else None
-        call("rte_macro_prologue_bwd", ptr(dz), ptr(hv), ptr(rstd), ptr(dh_epi), B, S, d, ptr(dh), ptr(dh0),
+        if B == Bh:
+            dz, dv = _grouped_linear_bwd(da, z, vb, offsets, tok, pos, True, nia[4], False)
+        else:
+            # dz per sample (its own rows, added over the repeats by the prologue backward);
+            # dV gathers the shared z rows
+            dz, _ = _grouped_linear_bwd(da, z, vb, offsets, pos, pos, True, False, False, n_x=B * S)
+            _, dv = _grouped_linear_bwd(da, z, vb, offsets, tok_z, pos, False, nia[4], False)
+        dh = torch.empty((Bh, S, d), dtype=F32, device=dev)
+        dh0 = torch.empty((Bh, S, d), dtype=F32, device=dev) if nia[1] else None
+        call("rte_macro_prologue_bwd", ptr(dz), ptr(hv), ptr(rstd), ptr(dh_epi), B, Bh, S, d, ptr(dh), ptr(dh0),
              ptr(ws), wsb, _s())
+        if dh0 is not None and Bh0 < Bh:
+            dh0 = dh0.view(Bh // Bh0, Bh0, S, d).sum(0)
 
         def tab(i):
             return None if tabs_out[i] is None else tabs_out[i].view(t_shape)
@@ -981,6 +1003,40 @@ class MacroBoundedFn(torch.autograd.Function):
 
 def macro_bounded(h, h0, key, pk, v, u, gain, bias, scale, c: float, eps: float = 1e-5):
     return MacroBoundedFn.apply(h, h0, key, pk, v, u, gain, bias, scale, c, eps)
+
+
+class MseFn(torch.autograd.Function):
+    """mean((a - b)^2) over all elements (F.mse_loss with mean reduction), fp32, in a fixed
+    reduction order."""
+
+    @staticmethod
+    def forward(ctx, a, b):
+        _lib.require_device_tensors("mse", a, b)
+        if a.shape != b.shape or a.numel() == 0:
+            raise ValueError("mse: a and b need the same non-empty shape")
+        av, bv = a.contiguous().to(F32), b.contiguous().to(F32)
+        n = av.numel()
+        out = torch.empty((), dtype=F32, device=a.device)
+        wsb = _lib.load().rte_mse_workspace_bytes(n)
+        ws = torch.empty((max(wsb // 4, 1),), dtype=F32, device=a.device)
+        call("rte_mse_fwd", ptr(av), ptr(bv), n, ptr(out), ptr(ws), wsb, _s())
+        ctx.save_for_backward(av, bv)
+        ctx.dtypes = (a.dtype, b.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        av, bv = ctx.saved_tensors
+        nia = ctx.needs_input_grad
+        gv = g.reshape(1).contiguous().to(F32)
+        da = torch.empty_like(av) if nia[0] else None
+        db = torch.empty_like(bv) if nia[1] else None
+        call("rte_mse_bwd", ptr(av), ptr(bv), av.numel(), ptr(gv), ptr(da), ptr(db), _s())
+        return (None if da is None else da.to(ctx.dtypes[0]), None if db is None else db.to(ctx.dtypes[1]))
+
+
+def mse(a, b):
+    return MseFn.apply(a, b)
 
 
 def grouped_linear(x, w, pk: PackIndex, *, out_f32: bool = True):

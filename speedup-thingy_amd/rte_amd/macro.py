@@ -131,16 +131,20 @@ class MacroOperators(nn.Module):
             return hip_ops.embedding(flat, key)
         return flat.index_select(0, key)
 
+    def _fused_bounded(self) -> bool:
+        return (self.config.macro_type != "v2_delta_radius" and self.v2 is None and self.gate_v is None
+                and not self.config.macro_include_delta_to_h0 and self.depth_embed is None)
+
     def _apply_bounded(self, h, h0, recipe_ids, stride_ids):
         """rte/macro.py:201-236.  The (recipe, stride)-indexed low-rank matrices are applied as
         grouped GEMMs over the rows of every sample sharing a key: no per-sample copies of
         v / u are gathered, and their gradients are per-group reductions in a fixed order."""
-        B, S, d = h.shape
+        _, S, d = h.shape
         R, Kk = self.v.shape[0], self.v.shape[1]
         key = recipe_ids.long() * Kk + stride_ids.long()
+        B = key.numel()  # may exceed h's samples on the fused path (repeated sources)
         pk = hip_ops.group_rows(key[:, None].expand(B, S), R * Kk)
-        if (self.v2 is None and self.gate_v is None and not self.config.macro_include_delta_to_h0
-                and self.depth_embed is None):
+        if self._fused_bounded():
             # default options: fused prologue / epilogue kernels around the two grouped GEMMs
             return hip_ops.macro_bounded(h, h0, key, pk, self.v, self.u, self.d_gain, self.bias, self.update_scale,
                                          self.config.macro_update_scale)
@@ -213,15 +217,23 @@ class MacroOperators(nn.Module):
         return out, trace
 
     def consistency_loss(self, h, h0, recipe_ids):
-        """rte/macro.py:342-359: Phi_{2s}(h) vs Phi_s(Phi_s(h))."""
+        """rte/macro.py:342-359: Phi_{2s}(h) vs Phi_s(Phi_s(h)) for every (s, 2s) stride pair."""
         if self.cons_src_idx.numel() == 0:
             return h.new_zeros(())
         pc, b = self.cons_src_idx.numel(), h.shape[0]
-        h_rep = h.unsqueeze(0).expand(pc, *h.shape).reshape(pc * b, *h.shape[1:])
-        h0_rep = h0.unsqueeze(0).expand(pc, *h0.shape).reshape(pc * b, *h0.shape[1:])
-        r_rep = recipe_ids.unsqueeze(0).expand(pc, b).reshape(-1)
-        src = self.cons_src_idx.unsqueeze(1).expand(pc, b).reshape(-1)
-        dst = self.cons_dst_idx.unsqueeze(1).expand(pc, b).reshape(-1)
+        r_rep = recipe_ids.repeat(pc)
+        src = self.cons_src_idx.repeat_interleave(b)
+        dst = self.cons_dst_idx.repeat_interleave(b)
+        if self._fused_bounded() and 2 * pc <= 4:
+            # Phi_{2s}(h) and the first Phi_s(h) read the same source batch: one operator call
+            # over the 2 pc b (sample, key) pairs; the second Phi_s reads its output with h0
+            # repeated.  No copies of h / h0 are made.
+            both = self._apply_bounded(h, h0, torch.cat([r_rep, r_rep]), torch.cat([dst, src]))
+            direct, first = both[:pc * b], both[pc * b:]
+            twice = self._apply_bounded(first, h0, r_rep, src)
+            return hip_ops.mse(direct, twice)
+        h_rep = h.repeat(pc, 1, 1)
+        h0_rep = h0.repeat(pc, 1, 1)
         direct = self.apply_vectorized(h_rep, h0_rep, r_rep, dst)
         twice = self.apply_vectorized(self.apply_vectorized(h_rep, h0_rep, r_rep, src), h0_rep, r_rep, src)
         # F.mse_loss (mean of squares) as staged means: per row, per sample, then over samples

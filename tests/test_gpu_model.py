@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
-
+from helpers import BF16_RTOL, FP32_RTOL, assert_rel
 from helpers import BF16_RTOL, assert_rel
 
 pytestmark = pytest.mark.gpu
@@ -459,6 +459,106 @@ def test_macro_operator_grouped_matches_reference(scale_init, B, S):
         assert_rel(getattr(mac, k).grad.double().cpu().numpy(), tp[k].grad.numpy(), BF16_RTOL, f"macro d{k}")
     assert_rel(h.grad.double().cpu().numpy(), th.grad.numpy(), BF16_RTOL, "macro dh")
     assert_rel(h0.grad.double().cpu().numpy(), th0.grad.numpy(), BF16_RTOL, "macro dh0")
+
+
+@pytest.mark.parametrize("Bh,Bh0,rep", [(6, 6, 4), (8, 4, 2), (5, 5, 1)])
+def test_macro_repeated_sources_match_copies(Bh, Bh0, rep):
+    """The bounded operator over Bt = rep * Bh samples reading h[b % Bh] and h0[b % Bh0] equals
+    the operator on explicit copies: outputs bitwise, gradients of h, h0 and every parameter
+    within the fp32 tolerance (repeats are added in the kernel instead of by autograd)."""
+    from helpers import rel_err
+    from rte_amd.kernels import hip_ops
+    from rte_amd.macro import MacroOperators
+
+    cfg = _model_cfg(d_model=128, macro_rank=32, recipe_count=6, depth_choices=[1, 2, 4], t_max=4,
+                     macro_update_scale_init=0.5)
+    torch.manual_seed(5)
+    mac = MacroOperators(cfg).cuda()
+    with torch.no_grad():
+        mac.d_gain.normal_(0, 0.1)
+        mac.bias.normal_(0, 0.1)
+        mac.u.normal_(0, 0.05)
+    S, d, Bt = 24, cfg.d_model, rep * Bh
+    gen = torch.Generator(device="cuda").manual_seed(6)
+    h = torch.randn(Bh, S, d, device="cuda", generator=gen, requires_grad=True)
+    h0 = torch.randn(Bh0, S, d, device="cuda", generator=gen, requires_grad=True)
+    rid = torch.randint(0, 6, (Bt,), device="cuda", generator=gen)
+    sid = torch.randint(0, 3, (Bt,), device="cuda", generator=gen)
+    g = torch.randn(Bt, S, d, device="cuda", generator=gen)
+    print(f"macro repeated sources Bh={Bh} Bh0={Bh0} rep={rep}", flush=True)
+    params = [mac.v, mac.u, mac.d_gain, mac.bias, mac.update_scale]
+
+    def run(hh, hh0):
+        for p in params + [h, h0]:
+            p.grad = None
+        out = mac._apply_bounded(hh, hh0, rid, sid)
+        out.backward(g)
+        return out.detach().clone(), [p.grad.clone() for p in params + [h, h0]]
+
+    out_r, grads_r = run(h, h0)
+    out_c, grads_c = run(h.repeat(rep, 1, 1), h0.repeat(Bt // Bh0, 1, 1))
+    assert torch.equal(out_r, out_c), "outputs differ"
+    for name, a, b in zip(["v", "u", "gain", "bias", "scale", "h", "h0"], grads_r, grads_c):
+        assert rel_err(a.double().cpu().numpy(), b.double().cpu().numpy()) < FP32_RTOL, name
+
+
+def test_consistency_loss_fused_matches_reference_formula():
+    """The consistency loss on one merged operator call (rte/macro.py:342-359 restated with
+    explicit copies of h and h0, three operator calls and torch's staged means) gives the same
+    loss and gradients within the bf16 tolerance."""
+    from helpers import rel_err
+    from rte_amd.macro import MacroOperators
+
+    cfg = _model_cfg(d_model=128, macro_rank=32, recipe_count=6, depth_choices=[1, 2, 4], t_max=4)
+    torch.manual_seed(7)
+    mac = MacroOperators(cfg).cuda()
+    with torch.no_grad():
+        mac.d_gain.normal_(0, 0.1)
+        mac.bias.normal_(0, 0.1)
+        mac.u.normal_(0, 0.05)
+    B, S, d = 12, 20, cfg.d_model
+    gen = torch.Generator(device="cuda").manual_seed(8)
+    h = torch.randn(B, S, d, device="cuda", generator=gen, requires_grad=True)
+    rid = torch.randint(0, 6, (B,), device="cuda", generator=gen)
+    params = [mac.v, mac.u, mac.d_gain, mac.bias, h]
+    print("consistency loss B=12 S=20 d=128", flush=True)
+    loss = mac.consistency_loss(h, h, rid)
+    loss.backward()
+    got = [p.grad.clone() for p in params]
+    for p in params:
+        p.grad = None
+    pc = mac.cons_src_idx.numel()
+    h_rep = h.unsqueeze(0).expand(pc, *h.shape).reshape(pc * B, S, d)
+    r_rep = rid.unsqueeze(0).expand(pc, B).reshape(-1)
+    src = mac.cons_src_idx.unsqueeze(1).expand(pc, B).reshape(-1)
+    dst = mac.cons_dst_idx.unsqueeze(1).expand(pc, B).reshape(-1)
+    direct = mac.apply_vectorized(h_rep, h_rep, r_rep, dst)
+    twice = mac.apply_vectorized(mac.apply_vectorized(h_rep, h_rep, r_rep, src), h_rep, r_rep, src)
+    ref = (direct - twice).square().mean(dim=-1).mean(dim=-1).mean()
+    ref.backward()
+    assert abs(loss.item() - ref.item()) <= 1e-5 * max(abs(ref.item()), 1e-12) + 1e-9
+    for name, a, p in zip(["v", "u", "gain", "bias", "h"], got, params):
+        assert rel_err(a.double().cpu().numpy(), p.grad.double().cpu().numpy()) < BF16_RTOL, name
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096, 100003, 256 * 64 * 512])
+def test_mse_matches_torch(n):
+    """Fused mean squared difference and its gradients against float64 torch; bitwise repeatable."""
+    from rte_amd.kernels import hip_ops
+
+    gen = torch.Generator(device="cuda").manual_seed(n % 1000)
+    a = torch.randn(n, device="cuda", generator=gen, requires_grad=True)
+    b = torch.randn(n, device="cuda", generator=gen, requires_grad=True)
+    print(f"mse n={n}", flush=True)
+    out = hip_ops.mse(a, b)
+    (out * 3.0).backward()
+    ad, bd = a.detach().double(), b.detach().double()
+    want = ((ad - bd) ** 2).mean()
+    assert abs(out.item() - want.item()) <= 1e-5 * want.item()
+    gw = 3.0 * 2.0 * (ad - bd) / n
+    assert_rel(a.grad.double().cpu().numpy(), gw.cpu().numpy(), FP32_RTOL, "mse da")
+    assert_rel(b.grad.double().cpu().numpy(), (-gw).cpu().numpy(), FP32_RTOL, "mse db")
+    assert torch.equal(hip_ops.mse(a, b), out), "mse not repeatable"
 
 
 # ---------------------------------------------------------------- fused AdamW
