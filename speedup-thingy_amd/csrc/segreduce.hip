@@ -11,10 +11,10 @@ namespace rte {
 
 namespace {
 
-constexpr int kSortChunk = 4096;      // pairs per counting-sort block
+constexpr int kSortChunk = 1024;      // pairs per counting-sort block
 constexpr int kSortSub = 256;         // pairs ranked together inside a sort block
 constexpr int kMaxSortKeys = 32768;   // LDS histogram of the sort: 128 KB
-constexpr int kSegChunk = 256;        // pairs per partial sum
+constexpr int kSegChunk = 64;         // pairs per partial sum (a long run is cut into many)
 
 // hist[v * nblk + b] = pairs of sort block b whose key is v.
 
@@ -104,20 +104,36 @@ __global__ void __launch_bounds__(256) sort_scatter_kernel(const int32_t* __rest
                                                            int32_t* __restrict__ tok_of_slot,
                                                            float* __restrict__ w_of_slot) {
   extern __shared__ int32_t cursor[];
-  __shared__ int32_t sk[kSortSub];
+  __shared__ __align__(16) int32_t sk[kSortSub];
   const int tid = threadIdx.x;
   for (int c = tid; c < V; c += 256) cursor[c] = offsets[c] + hist[(int64_t)c * nblk + blockIdx.x];
   const int64_t p0 = (int64_t)blockIdx.x * kSortChunk;
-  for (int q = 0; q < kSortChunk / kSortSub; ++q) {
+  constexpr int NQ = kSortChunk / kSortSub;
+  int kq[NQ];  // every key of the block loaded up front (one memory latency, not one per sub-chunk)
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
     const int64_t p = p0 + q * kSortSub + tid;
-    const int k = p < P ? keys[p] : -1;
+    kq[q] = p < P ? keys[p] : -1;
+  }
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int64_t p = p0 + q * kSortSub + tid;
+    const int k = kq[q];
     const bool valid = k >= 0 && k < V;
     __syncthreads();  // cursor ready / previous sub-chunk done with sk
     sk[tid] = valid ? k : -1;
     __syncthreads();
-    int rank = 0;
-    if (valid)
-      for (int i = 0; i < tid; ++i) rank += sk[i] == k;
+    int rank = 0;  // pairs of this sub-chunk before tid with the same key (16-byte LDS reads)
+    if (valid) {
+      const int4* s4 = reinterpret_cast<const int4*>(sk);
+#pragma unroll 4
+      for (int i4 = 0; 4 * i4 < tid; ++i4) {
+        const int4 v = s4[i4];
+        const int b = 4 * i4;
+        rank += (b < tid && v.x == k) + (b + 1 < tid && v.y == k) + (b + 2 < tid && v.z == k) +
+                (b + 3 < tid && v.w == k);
+      }
+    }
     const int slot = valid ? cursor[k] + rank : 0;
     __syncthreads();
     if (valid) {
@@ -144,7 +160,7 @@ __device__ __forceinline__ void load8(const float* p, float* v) {
   v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
 }
 
-// One wave per 256-pair chunk of one key's run: sum_s w[s] * rows[tok[s]].  A key with a
+// One wave per 64-pair chunk of one key's run: sum_s w[s] * rows[tok[s]].  A key with a
 // single chunk writes out directly; otherwise the chunk's partial goes to part[item].
 template <int NC2, typename RowT>
 __global__ void __launch_bounds__(256) sort_segsum_kernel(const int32_t* __restrict__ offsets,
@@ -185,11 +201,25 @@ __global__ void __launch_bounds__(256) sort_segsum_kernel(const int32_t* __restr
     }
   };
   int s = s0;
-  for (; s + 4 <= s1; s += 4) {
-    fma_row(s);
-    fma_row(s + 1);
-    fma_row(s + 2);
-    fma_row(s + 3);
+  for (; s + 8 <= s1; s += 8) {  // 8 rows in flight: indices and weights first, then the rows
+    int t8[8];
+    float g8[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      t8[j] = tok[s + j];
+      g8[j] = w[s + j];
+    }
+#pragma unroll
+    for (int c = 0; c < NC2; ++c) {
+      if (lane + 64 * c >= nch) continue;
+      float v[8][8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) load8(hidden + (int64_t)t8[j] * d + (lane + 64 * c) * 8, v[j]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[c][i] += g8[j] * v[j][i];
+    }
   }
   for (; s < s1; ++s) fma_row(s);
   float* dst = nq == 1 ? dW + (int64_t)v * d : part + (int64_t)item * d;
