@@ -430,7 +430,7 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS, WM>())) gemm_
   bf16* smem = reinterpret_cast<bf16*>(smem_raw);
   constexpr int A_TILE = BM * LDP;
   constexpr int A_STAGE = (DUALA ? 2 : 1) * A_TILE, B_STAGE = BN * LDP, B_BASE = 2 * A_STAGE;
-  __shared__ int s_tile[2];
+  __shared__ int s_tile[3];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -469,18 +469,41 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS, WM>())) gemm_
     n0 = blockIdx.y * BN;
   } else if (p.mode == MODE_GROUP_K) {
     if (p.gk_chunk > 0) {
+      // work item blockIdx.z -> (group, chunk): prefix sums of the groups' chunk counts, 64 groups
+      // per step; workgroup (0, 0, 0) also writes the chunk starts gk_first[0..G] for the
+      // partial-sum kernel that runs after this one
       const int item = blockIdx.z;
-      if (item >= p.gk_first[p.G]) return;  // uniform per workgroup
-      int lo = 0, hi = p.G;  // largest g with gk_first[g] <= item (skips empty groups)
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (p.gk_first[mid] <= item) lo = mid; else hi = mid;
+      const bool writer = blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0;
+      if (tid < 64) {
+        if (tid == 0) s_tile[0] = -1;
+        int base = 0;
+        for (int c0 = 0; c0 < p.G; c0 += 64) {
+          const int gg = c0 + tid;
+          const int cnt = gg < p.G ? (p.goff[gg + 1] - p.goff[gg] + p.gk_chunk - 1) / p.gk_chunk : 0;
+          int incl = cnt;
+#pragma unroll
+          for (int off = 1; off < 64; off <<= 1) {
+            const int y = __shfl_up(incl, off, 64);
+            if (tid >= off) incl += y;
+          }
+          const int excl = incl - cnt;
+          if (writer && gg < p.G) const_cast<int32_t*>(p.gk_first)[gg] = base + excl;
+          if (cnt > 0 && item >= base + excl && item < base + incl) {
+            s_tile[0] = gg;
+            s_tile[1] = item - base - excl;
+            s_tile[2] = cnt;
+          }
+          base += __shfl(incl, 63, 64);
+        }
+        if (writer && tid == 0) const_cast<int32_t*>(p.gk_first)[p.G] = base;
       }
-      g = lo;
-      const int c = item - p.gk_first[g];
+      __syncthreads();
+      g = s_tile[0];
+      if (g < 0) return;  // uniform per workgroup
+      const int c = s_tile[1];
       kbeg = p.goff[g] + c * p.gk_chunk;
       kend = kbeg + p.gk_chunk < p.goff[g + 1] ? kbeg + p.gk_chunk : p.goff[g + 1];
-      if (p.gk_first[g + 1] - p.gk_first[g] > 1) partial_dst = p.gk_part + (int64_t)item * p.M * p.N;
+      if (s_tile[2] > 1) partial_dst = p.gk_part + (int64_t)item * p.M * p.N;
     } else {
       g = blockIdx.z;
       kbeg = p.goff[g];
@@ -888,31 +911,6 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS, WM>())) gemm_
   }
 }
 
-// gk_first[g] = sum over groups before g of ceil(rows_g / chunk)  (single workgroup)
-__global__ void __launch_bounds__(1024) groupk_prefix_kernel(const int32_t* __restrict__ goff, int G, int chunk,
-                                                             int32_t* __restrict__ first) {
-  __shared__ int32_t part[1024];
-  const int tid = threadIdx.x;
-  const int seg = (G + 1023) / 1024;
-  const int b0 = tid * seg, b1 = b0 + seg < G ? b0 + seg : G;
-  int32_t s = 0;
-  for (int g = b0; g < b1; ++g) s += (goff[g + 1] - goff[g] + chunk - 1) / chunk;
-  part[tid] = s;
-  __syncthreads();
-  for (int o = 1; o < 1024; o <<= 1) {
-    const int32_t y = tid >= o ? part[tid - o] : 0;
-    __syncthreads();
-    part[tid] += y;
-    __syncthreads();
-  }
-  int32_t run = part[tid] - s;
-  for (int g = b0; g < b1; ++g) {
-    first[g] = run;
-    run += (goff[g + 1] - goff[g] + chunk - 1) / chunk;
-  }
-  if (tid == 1023) first[G] = part[1023];
-}
-
 // Groups cut into several chunks (or none): add the chunk partials in chunk order and apply
 // the EPI_STORE epilogue.  One-chunk groups were stored by the GEMM itself.
 __global__ void __launch_bounds__(256) groupk_reduce_kernel(GemmArgs p, EpiFlags fl) {
@@ -1014,9 +1012,6 @@ int launch_cfg(const GemmArgs& p0, hipStream_t stream, void* ws, size_t ws_bytes
         p.gk_first = static_cast<int32_t*>(ws);
         p.gk_part = reinterpret_cast<float*>(static_cast<char*>(ws) + groupk_first_bytes(p.G));
         grid.z = (unsigned)((p.K + chunk - 1) / chunk + p.G);
-        hipLaunchKernelGGL(groupk_prefix_kernel, dim3(1), dim3(1024), 0, stream, p.goff, p.G, chunk,
-                           const_cast<int32_t*>(p.gk_first));
-        RTE_TRY(check_launch("gemm_groupk_prefix"));
       }
     }
   } else {
