@@ -1280,6 +1280,11 @@ int launch_dl(const GemmArgs& p, hipStream_t stream, void* ws, size_t ws_bytes, 
   }
 }
 
+// The SwiGLU epilogue kernels' direct-load loop: whole 64-k stages of layout-N A.
+bool dl_whole64(const GemmArgs& p) {
+  return dl_mode(p) != 0 && !p.a_koff2 && !p.a_t && p.mode != MODE_GROUP_K && p.K > 0 && p.K % 64 == 0;
+}
+
 bool pow2_or_zero(int v) { return v == 0 || (v > 0 && (v & (v - 1)) == 0); }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -1369,6 +1374,11 @@ int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream, void* ws, s
         RTE_REQUIRE(p.mode == MODE_DENSE && p.N % 128 == 0, "gemm: dual-A SwiGLU needs dense mode and N %% 128 == 0");
         return launch_cfg<128, 128, 32, 2, 2, false, false, EPI_SWIGLU_FWD, true>(p, stream, ws, ws_bytes, 1);
       }
+      if (dl_whole64(p)) {
+        if (p.N == 64)
+          return launch_cfg<128, 64, 64, 4, 1, false, false, EPI_SWIGLU_FWD, false, 2>(p, stream, ws, ws_bytes, 1);
+        return launch_cfg<128, 128, 64, 2, 2, false, false, EPI_SWIGLU_FWD, false, 2>(p, stream, ws, ws_bytes, 1);
+      }
       if (p.N == 64) return launch_cfg<128, 64, 64, 4, 1, false, false, EPI_SWIGLU_FWD>(p, stream, ws, ws_bytes, 1);
       return launch_cfg<128, 128, 64, 2, 2, false, false, EPI_SWIGLU_FWD>(p, stream, ws, ws_bytes, 1);
     case EPI_SWIGLU_BWD:
@@ -1376,6 +1386,14 @@ int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream, void* ws, s
       RTE_REQUIRE(p.epi.ug && p.epi.ug_in, "gemm: SwiGLU backward needs UG input and dUG output");
       RTE_REQUIRE(p.N % 32 == 0, "gemm: SwiGLU backward needs N %% 32 == 0");
       if (p.epi.dw_row) RTE_REQUIRE(p.N <= 128, "gemm: per-row reduction supports N <= 128");
+      if (dl_whole64(p)) {
+        if (p.N <= 32)
+          return p.b_t ? launch_cfg<128, 32, 64, 4, 1, false, true, EPI_SWIGLU_BWD, false, 2>(p, stream, ws, ws_bytes, 1)
+                       : launch_cfg<128, 32, 64, 4, 1, false, false, EPI_SWIGLU_BWD, false, 2>(p, stream, ws, ws_bytes, 1);
+        if (p.N <= 64)
+          return p.b_t ? launch_cfg<128, 64, 64, 4, 1, false, true, EPI_SWIGLU_BWD, false, 2>(p, stream, ws, ws_bytes, 1)
+                       : launch_cfg<128, 64, 64, 4, 1, false, false, EPI_SWIGLU_BWD, false, 2>(p, stream, ws, ws_bytes, 1);
+      }
       if (p.N <= 32) {
         return p.b_t ? launch_cfg<128, 32, 64, 4, 1, false, true, EPI_SWIGLU_BWD>(p, stream, ws, ws_bytes, 1)
                      : launch_cfg<128, 32, 64, 4, 1, false, false, EPI_SWIGLU_BWD>(p, stream, ws, ws_bytes, 1);
