@@ -9,6 +9,10 @@
 //              m = b1 m + (1 - b1) g, v = b2 v + (1 - b2) g^2, p -= lr / (1 - b1^t) m /
 //              (sqrt(v) / sqrt(1 - b2^t) + eps)), skipped entirely when found_inf is set
 //
+// Without clipping the update does not depend on the norms, so the update kernel also forms
+// the per-chunk partial norms (of the gradient and of the parameter before it changes) and the
+// finish runs last: two launches and one pass over p and g.
+//
 // Tensors are described by a device table (one row per parameter, pointers and sizes) and a
 // block table (tensor, chunk) built once per layout, so the same three launches serve any
 // parameter set and can be captured in a graph.
@@ -142,26 +146,58 @@ __global__ void __launch_bounds__(1024) adamw_finalize_kernel(const AdamRow* __r
   scal[4 * G + 1] = skip ? 0.0f : 1.0f;
 }
 
+// NORMS: also write the chunk's partial sums of g^2 and p^2 (p before the update) to part, and
+// run whatever found_inf says (the finish kernel then skips the counters and the metrics use
+// the same values as without the update).  Otherwise the finish kernel ran first: scal holds the
+// clip coefficient and the skip flag, and the step counters are already advanced.
+template <bool NORMS>
 __global__ void __launch_bounds__(256) adamw_update_kernel(const AdamRow* __restrict__ rows,
                                                            const int32_t* __restrict__ blk,
                                                            const double* __restrict__ hyper, int G,
-                                                           const float* __restrict__ scal) {
-  if (scal[4 * G + 1] == 0.0f) return;  // found_inf: no update
+                                                           const float* __restrict__ scal,
+                                                           const float* __restrict__ found_inf,
+                                                           float* __restrict__ part) {
+  __shared__ float red[4];
   const int b = blockIdx.x;
   const AdamRow r = rows[blk[2 * b]];
-  if (!r.g) return;
   const int64_t off = (int64_t)blk[2 * b + 1] * kChunk;
+  bool skip;
+  if constexpr (NORMS) {
+    const float* p = reinterpret_cast<const float*>(r.p);
+    const float* g = reinterpret_cast<const float*>(r.g);
+    float sg = 0.0f, sp = 0.0f;
+    for (int64_t i = off + threadIdx.x; i < off + kChunk && i < r.numel; i += 256) {
+      const float x = p[i];
+      sp += x * x;
+      if (g) {
+        const float y = g[i];
+        sg += y * y;
+      }
+    }
+    sg = bsum(sg, red);
+    sp = bsum(sp, red);
+    if (threadIdx.x == 0) {
+      part[2 * b] = sg;
+      part[2 * b + 1] = sp;
+    }
+    __syncthreads();  // every thread has read p before any is updated
+    skip = found_inf && *found_inf > 0.0f;
+  } else {
+    skip = scal[4 * G + 1] == 0.0f;  // found_inf: no update
+  }
+  if (skip || !r.g) return;
   const int gi = (int)r.group;
   // scalar coefficients in double (the betas' complements and bias corrections lose about
   // 1e-5 relative when formed from float betas), applied in float
   const double lr_d = hyper[5 * gi], b1_d = hyper[5 * gi + 1], b2_d = hyper[5 * gi + 2];
-  const double step_d = (double)*reinterpret_cast<const float*>(r.step);
+  // the step this update is (the finish kernel advances the counter after it when NORMS)
+  const double step_d = (double)*reinterpret_cast<const float*>(r.step) + (NORMS ? 1.0 : 0.0);
   const float b1 = (float)b1_d, b2 = (float)b2_d, omb1 = (float)(1.0 - b1_d), omb2 = (float)(1.0 - b2_d);
   const float eps = (float)hyper[5 * gi + 3];
   const float lr_wd = (float)(lr_d * hyper[5 * gi + 4]);
   const float step_size = (float)(lr_d / (1.0 - pow(b1_d, step_d)));
   const float bc2_sqrt = (float)sqrt(1.0 - pow(b2_d, step_d));
-  const float coef = scal[4 * G];
+  const float coef = NORMS ? 1.0f : scal[4 * G];
   float* p = reinterpret_cast<float*>(r.p);
   const float* g = reinterpret_cast<const float*>(r.g);
   float* m = reinterpret_cast<float*>(r.m);
@@ -198,17 +234,29 @@ int adamw_step(const void* rows, int nt, const int32_t* blk, const int32_t* firs
   float* tsum = part + 2 * (size_t)nblk;
   float* scal = tsum + 2 * (size_t)nt;
   const AdamRow* r = static_cast<const AdamRow*>(rows);
+  const size_t lds = (size_t)3 * nt * sizeof(double);
+  RTE_REQUIRE(lds <= 60 * 1024, "adamw: at most 2560 tensors");
+  if (clip_max <= 0.0f) {
+    // no clipping: update with the partial norms, then the finish (metrics, step counters)
+    if (nblk > 0) {
+      hipLaunchKernelGGL(adamw_update_kernel<true>, dim3(nblk), dim3(256), 0, s, r, blk, hyper, G, scal, found_inf,
+                         part);
+      RTE_TRY(check_launch("adamw_update"));
+    }
+    hipLaunchKernelGGL(adamw_finalize_kernel, dim3(1), dim3(1024), lds, s, r, nt, first_blk, part, hyper, G,
+                       metric_lr_group, M, clip_max, found_inf, tsum, scal, metrics);
+    return check_launch("adamw_finalize");
+  }
   if (nblk > 0) {
     hipLaunchKernelGGL(adamw_norms_kernel, dim3(nblk), dim3(256), 0, s, r, blk, part);
     RTE_TRY(check_launch("adamw_norms"));
   }
-  const size_t lds = (size_t)3 * nt * sizeof(double);
-  RTE_REQUIRE(lds <= 60 * 1024, "adamw: at most 2560 tensors");
   hipLaunchKernelGGL(adamw_finalize_kernel, dim3(1), dim3(1024), lds, s, r, nt, first_blk, part, hyper, G,
                      metric_lr_group, M, clip_max, found_inf, tsum, scal, metrics);
   RTE_TRY(check_launch("adamw_finalize"));
   if (nblk > 0) {
-    hipLaunchKernelGGL(adamw_update_kernel, dim3(nblk), dim3(256), 0, s, r, blk, hyper, G, scal);
+    hipLaunchKernelGGL(adamw_update_kernel<false>, dim3(nblk), dim3(256), 0, s, r, blk, hyper, G, scal, found_inf,
+                       part);
     RTE_TRY(check_launch("adamw_update"));
   }
   return 0;

@@ -4,7 +4,9 @@
 //                (readlane broadcast), else k rounds of a wave arg-max over the C
 //                router logits (value descending, index ascending on ties,
 //                NaN above everything as torch.topk does), then softmax over
-//                the k selected logits.
+//                the k selected logits.  Many tokens (T >= 16384, C <= 128): one lane
+//                per token instead, rows staged through LDS and a sorted top-k kept in
+//                registers by insertion (same order, same softmax summation tree).
 //  pack        : stable counting sort of the T*k (token, cluster) pairs by
 //                cluster.  Slots inside a cluster follow ascending pair index,
 //                i.e. ascending token, like the nonzero()-based index build of
@@ -280,6 +282,99 @@ __global__ void __launch_bounds__(256) pack_scatter_kernel(const int32_t* __rest
   if (w_of_slot) w_of_slot[slot] = w ? w[p] : 1.0f;
 }
 
+// One lane per token: the wave's 64 rows are staged in LDS (row pitch C + 1: lanes reading
+// the same column hit distinct banks), each lane inserts its row's logits in index order into
+// a sorted top-K list (the element carried down by an insertion is compared with the full order,
+// index ascending on equal values), then the softmax over the k selected logits is summed with the xor tree the
+// wave-per-token kernel's butterfly forms, so both kernels give identical results.
+template <int K, bool kNaN>
+__device__ __forceinline__ void insert_row(const float* rowl, int C, float (&tv)[K], int (&ti)[K]) {
+  for (int c = 0; c < C; ++c) {
+    float v = rowl[c];
+    int i = c;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      bool take;
+      if (kNaN)
+        take = ti[j] < 0 || better(v, i, tv[j], ti[j]);
+      else  // a carried (displaced) element meets later equal values: index ascending
+        take = ti[j] < 0 || v > tv[j] || (v == tv[j] && i < ti[j]);
+      const float ov = tv[j];
+      const int oi = ti[j];
+      tv[j] = take ? v : ov;
+      ti[j] = take ? i : oi;
+      v = take ? ov : v;
+      i = take ? oi : i;
+    }
+  }
+}
+
+template <int K>
+__global__ void __launch_bounds__(64) route_topk_lanes_kernel(const float* __restrict__ logits, int T, int C, int k,
+                                                              int32_t* __restrict__ ids,
+                                                              float* __restrict__ weights) {
+  extern __shared__ float rows[];  // [64][C + 1]
+  const int lane = threadIdx.x;
+  const int t0 = blockIdx.x * 64;
+  const int nt = T - t0 < 64 ? T - t0 : 64;
+  const int P = C + 1;
+  const float* src = logits + (int64_t)t0 * C;
+  bool nan_here = false;
+  if ((C & 3) == 0) {  // 16-byte loads: consecutive lanes, consecutive logits
+    for (int e = 4 * lane; e < nt * C; e += 256) {
+      const float4 x = *reinterpret_cast<const float4*>(src + e);
+      nan_here |= x.x != x.x || x.y != x.y || x.z != x.z || x.w != x.w;
+      const int r = e / C, c = e - r * C;  // C % 4 == 0: the four stay in one row
+      float* d = rows + r * P + c;
+      d[0] = x.x;
+      d[1] = x.y;
+      d[2] = x.z;
+      d[3] = x.w;
+    }
+  } else {
+    for (int e = lane; e < nt * C; e += 64) {
+      const float x = src[e];
+      nan_here |= x != x;
+      const int r = e / C, c = e - r * C;
+      rows[r * P + c] = x;
+    }
+  }
+  __syncthreads();
+  if (lane >= nt) return;
+  float tv[K];
+  int ti[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    tv[j] = 0.0f;
+    ti[j] = -1;  // empty: below every logit
+  }
+  if (__ballot(nan_here) != 0)
+    insert_row<K, true>(rows + lane * P, C, tv, ti);
+  else
+    insert_row<K, false>(rows + lane * P, C, tv, ti);
+  float ex[K], sm[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    ex[j] = j < k ? expf(tv[j] - tv[0]) : 0.0f;
+    sm[j] = ex[j];
+  }
+#pragma unroll
+  for (int off = K / 2; off >= 1; off >>= 1) {
+    float nx[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) nx[j] = sm[j] + sm[j ^ off];
+#pragma unroll
+    for (int j = 0; j < K; ++j) sm[j] = nx[j];
+  }
+  const int64_t o = (int64_t)(t0 + lane) * k;
+#pragma unroll
+  for (int j = 0; j < K; ++j)
+    if (j < k) {
+      ids[o + j] = ti[j];
+      weights[o + j] = ex[j] / sm[0];
+    }
+}
+
 template <typename OutT>
 __device__ __forceinline__ void store8(OutT* dst, const float* v);
 
@@ -385,6 +480,16 @@ int route_topk(const float* logits, int T, int C, int k, int32_t* ids, float* we
   RTE_REQUIRE(T >= 0 && C >= 1 && C <= 64 * kMaxPerLane, "route_topk: C must be in [1, 1024]");
   RTE_REQUIRE(k >= 1 && k <= 16 && k <= C, "route_topk: k must be in [1, min(16, C)]");
   if (T == 0) return 0;
+  if (T >= 16384 && C <= 128) {
+    const size_t lds = (size_t)64 * (C + 1) * sizeof(float);
+    if (k <= 8)
+      hipLaunchKernelGGL(route_topk_lanes_kernel<8>, dim3((T + 63) / 64), dim3(64), lds, s, logits, T, C, k, ids,
+                         weights);
+    else
+      hipLaunchKernelGGL(route_topk_lanes_kernel<16>, dim3((T + 63) / 64), dim3(64), lds, s, logits, T, C, k, ids,
+                         weights);
+    return check_launch("route_topk");
+  }
   const dim3 grid((T + 3) / 4);
   if (C <= 64)
     hipLaunchKernelGGL(route_topk_rank_kernel<1>, grid, dim3(256), 0, s, logits, T, C, k, ids, weights);

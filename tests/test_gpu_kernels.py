@@ -199,7 +199,8 @@ def test_attention_matches_reference(B, H, S, scaled, hd):
 # ---------------------------------------------------------------- routing / packing
 
 @pytest.mark.parametrize("T,C,k", [(1, 4, 1), (513, 32, 4), (8192, 64, 8), (301, 100, 16), (64, 128, 16),
-                                   (300, 256, 16), (77, 1000, 3)])
+                                   (300, 256, 16), (77, 1000, 3), (20000, 64, 8), (17000, 100, 16),
+                                   (16384, 128, 3), (16385, 7, 5)])
 def test_route_topk_bit_exact(T, C, k):
     H = _ops()
     rng = np.random.default_rng(T + C)
@@ -213,6 +214,19 @@ def test_route_topk_bit_exact(T, C, k):
     np.testing.assert_array_equal(ids.cpu().numpy(), rids)
     ok = ~np.isnan(lg).any(-1)
     np.testing.assert_allclose(w.cpu().numpy()[ok], rw[ok], rtol=FP32_RTOL, atol=1e-7)
+
+
+@pytest.mark.parametrize("C,k", [(64, 8), (100, 16), (7, 5)])
+def test_route_topk_kernels_agree(C, k):
+    """The one-lane-per-token kernel (T >= 16384) and the wave-per-token kernel give identical ids
+    and weights on the same rows (same order, same softmax summation)."""
+    H = _ops()
+    rng = np.random.default_rng(C * 31 + k)
+    lg = (rng.integers(-3, 4, size=(16400, C)) + rng.standard_normal((16400, C)) * (rng.random((16400, C)) < 0.7))
+    lg = torch.from_numpy(lg.astype(np.float32)).to(DEV)
+    ids_l, w_l = H.route_topk(lg, k)
+    ids_w, w_w = H.route_topk(lg[:8000].contiguous(), k)
+    assert torch.equal(ids_l[:8000], ids_w) and torch.equal(w_l[:8000], w_w)
 
 
 @pytest.mark.parametrize("T,k,C", [(1, 1, 1), (1000, 4, 32), (8192, 8, 64), (4096, 16, 256), (5000, 3, 77),
