@@ -165,19 +165,24 @@ __global__ void __launch_bounds__(256) route_topk_rank_kernel(const float* __res
 constexpr int kPackChunk = 256;
 
 // hist layout: hist[c * nblk + b] = pairs of block b routed to cluster c.
-__global__ void __launch_bounds__(256) pack_count_kernel(const int32_t* __restrict__ cl, int P, int C,
+// A block covers nsub consecutive 256-pair sub-chunks (more for large P, so the histogram the
+// single-workgroup scan walks stays short).
+__global__ void __launch_bounds__(256) pack_count_kernel(const int32_t* __restrict__ cl, int P, int C, int nsub,
                                                          int32_t* __restrict__ hist, int nblk,
                                                          int32_t* __restrict__ invalid) {
   extern __shared__ int32_t sh[];
   for (int c = threadIdx.x; c < C; c += blockDim.x) sh[c] = 0;
   __syncthreads();
-  const int p = blockIdx.x * kPackChunk + threadIdx.x;
-  if (p < P) {
-    const int c = cl[p];
-    if (c >= 0 && c < C) {
-      atomicAdd(&sh[c], 1);
-    } else if (invalid) {
-      atomicAdd(invalid, 1);
+  const int64_t pb = (int64_t)blockIdx.x * nsub * kPackChunk;
+  for (int q = 0; q < nsub; ++q) {
+    const int64_t p = pb + (int64_t)q * kPackChunk + threadIdx.x;
+    if (p < P) {
+      const int c = cl[p];
+      if (c >= 0 && c < C) {
+        atomicAdd(&sh[c], 1);
+      } else if (invalid) {
+        atomicAdd(invalid, 1);
+      }
     }
   }
   __syncthreads();
@@ -245,41 +250,50 @@ __global__ void __launch_bounds__(kScanThreads) pack_scan_kernel(int32_t* __rest
   (void)P;
 }
 
-// One thread per pair: its slot is the block's base for its cluster plus the number of earlier
-// pairs of the block with the same cluster (stable: ascending pair order inside a cluster).
-__global__ void __launch_bounds__(256) pack_scatter_kernel(const int32_t* __restrict__ cl, int P, int C,
+// One thread per pair of each sub-chunk: its slot is the block's running base for its cluster
+// (the block's scanned histogram entry plus the cluster's pairs in earlier sub-chunks) plus the
+// number of earlier pairs of the sub-chunk with the same cluster (stable: ascending pair order
+// inside a cluster).
+__global__ void __launch_bounds__(256) pack_scatter_kernel(const int32_t* __restrict__ cl, int P, int C, int nsub,
                                                            int k, const int32_t* __restrict__ hist,
                                                            int nblk, const float* __restrict__ w,
                                                            int32_t* __restrict__ tok_of_slot,
                                                            int32_t* __restrict__ pair_of_slot,
                                                            int32_t* __restrict__ slot_of_pair,
                                                            float* __restrict__ w_of_slot) {
+  extern __shared__ int32_t cursor[];  // [C]
   __shared__ __align__(16) int32_t sc[kPackChunk];
   const int tid = threadIdx.x;
-  const int p0 = blockIdx.x * kPackChunk;
-  const int n = P - p0 < kPackChunk ? P - p0 : kPackChunk;
-  sc[tid] = tid < n ? cl[p0 + tid] : -1;
-  __syncthreads();
-  if (tid >= n) return;
-  const int c = sc[tid];
-  const int p = p0 + tid;
-  if (c < 0 || c >= C) {
-    if (slot_of_pair) slot_of_pair[p] = -1;
-    return;
+  for (int c = tid; c < C; c += kPackChunk) cursor[c] = hist[(int64_t)c * nblk + blockIdx.x];
+  const int64_t pb = (int64_t)blockIdx.x * nsub * kPackChunk;
+  for (int q = 0; q < nsub; ++q) {
+    const int64_t p = pb + (int64_t)q * kPackChunk + tid;
+    __syncthreads();  // cursor ready / the previous sub-chunk is done with sc and cursor
+    sc[tid] = p < P ? cl[p] : -1;
+    __syncthreads();
+    const int c = sc[tid];
+    const bool valid = p < P && c >= 0 && c < C;
+    int slot = -1;
+    if (valid) {
+      int rank = 0;
+      const int4* s4 = reinterpret_cast<const int4*>(sc);
+      const int full = tid >> 2;
+      for (int j = 0; j < full; ++j) {
+        const int4 v = s4[j];
+        rank += (v.x == c) + (v.y == c) + (v.z == c) + (v.w == c);
+      }
+      for (int j = full * 4; j < tid; ++j) rank += sc[j] == c;
+      slot = cursor[c] + rank;
+    }
+    __syncthreads();  // every slot read its cursor before the cursors advance
+    if (valid) {
+      atomicAdd(&cursor[c], 1);
+      if (tok_of_slot) tok_of_slot[slot] = (int32_t)(p / k);
+      if (pair_of_slot) pair_of_slot[slot] = (int32_t)p;
+      if (w_of_slot) w_of_slot[slot] = w ? w[p] : 1.0f;
+    }
+    if (p < P && slot_of_pair) slot_of_pair[p] = slot;
   }
-  int rank = 0;
-  const int4* s4 = reinterpret_cast<const int4*>(sc);
-  const int full = tid >> 2;
-  for (int j = 0; j < full; ++j) {
-    const int4 v = s4[j];
-    rank += (v.x == c) + (v.y == c) + (v.z == c) + (v.w == c);
-  }
-  for (int j = full * 4; j < tid; ++j) rank += sc[j] == c;
-  const int slot = hist[(int64_t)c * nblk + blockIdx.x] + rank;
-  if (tok_of_slot) tok_of_slot[slot] = p / k;
-  if (pair_of_slot) pair_of_slot[slot] = p;
-  if (slot_of_pair) slot_of_pair[p] = slot;
-  if (w_of_slot) w_of_slot[slot] = w ? w[p] : 1.0f;
 }
 
 // One lane per token: the wave's 64 rows are staged in LDS (row pitch C + 1: lanes reading
@@ -500,8 +514,21 @@ int route_topk(const float* logits, int T, int C, int k, int32_t* ids, float* we
   return check_launch("route_topk");
 }
 
+// 256-pair sub-chunks per pack block: one up to 64 Ki pairs, growing to 16 for large P
+int pack_nsub(int P) {
+  int64_t n = (int64_t)P / (kPackChunk * 256);
+  if (n < 1) n = 1;
+  if (n > 16) n = 16;
+  return (int)n;
+}
+
+int pack_blocks(int P) {
+  const int64_t per = (int64_t)pack_nsub(P) * kPackChunk;
+  return (int)(((int64_t)P + per - 1) / per);
+}
+
 size_t pack_workspace_bytes(int P, int C) {
-  const int nblk = (P + kPackChunk - 1) / kPackChunk;
+  const int nblk = pack_blocks(P);
   return (size_t)C * (size_t)(nblk > 0 ? nblk : 1) * sizeof(int32_t);
 }
 
@@ -511,19 +538,19 @@ int pack_pairs(const int32_t* cl, int P, int C, int k, const float* w, int32_t* 
   RTE_REQUIRE(P >= 0 && C >= 1 && k >= 1, "pack: bad sizes");
   RTE_REQUIRE(ws_bytes >= pack_workspace_bytes(P, C), "pack: workspace too small (%zu < %zu)", ws_bytes,
               pack_workspace_bytes(P, C));
-  const int nblk = (P + kPackChunk - 1) / kPackChunk;
+  const int nsub = pack_nsub(P), nblk = pack_blocks(P);
   int32_t* hist = static_cast<int32_t*>(ws);
   if (nblk == 0) return fill_i32(offsets, 0, C + 1, s);
   {
-    hipLaunchKernelGGL(pack_count_kernel, dim3(nblk), dim3(kPackChunk), C * sizeof(int32_t), s, cl, P, C,
+    hipLaunchKernelGGL(pack_count_kernel, dim3(nblk), dim3(kPackChunk), C * sizeof(int32_t), s, cl, P, C, nsub,
                        hist, nblk, invalid);
     RTE_TRY(check_launch("pack_count"));
   }
   hipLaunchKernelGGL(pack_scan_kernel, dim3(1), dim3(1024), 0, s, hist, C, nblk, offsets, P);
   RTE_TRY(check_launch("pack_scan"));
   {
-    hipLaunchKernelGGL(pack_scatter_kernel, dim3(nblk), dim3(256), 0, s, cl, P, C, k, hist, nblk, w,
-                       tok_of_slot, pair_of_slot, slot_of_pair, w_of_slot);
+    hipLaunchKernelGGL(pack_scatter_kernel, dim3(nblk), dim3(kPackChunk), C * sizeof(int32_t), s, cl, P, C, nsub,
+                       k, hist, nblk, w, tok_of_slot, pair_of_slot, slot_of_pair, w_of_slot);
     RTE_TRY(check_launch("pack_scatter"));
   }
   return 0;

@@ -230,7 +230,7 @@ def test_route_topk_kernels_agree(C, k):
 
 
 @pytest.mark.parametrize("T,k,C", [(1, 1, 1), (1000, 4, 32), (8192, 8, 64), (4096, 16, 256), (5000, 3, 77),
-                                   (20000, 8, 64)])
+                                   (20000, 8, 64), (70001, 8, 64)])
 def test_pack_index_bit_exact(T, k, C):
     H = _ops()
     rng = np.random.default_rng(T * k + C)
