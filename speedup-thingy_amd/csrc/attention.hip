@@ -44,10 +44,10 @@ __device__ __forceinline__ bf16x8_v ld16(const bf16* p) {
 template <int O>
 __device__ __forceinline__ bf16x8_v pack8(const float (&v)[16]) {
   uint4 u;
-  u.x = (uint32_t)f2bf(v[O]) | ((uint32_t)f2bf(v[O + 1]) << 16);
-  u.y = (uint32_t)f2bf(v[O + 2]) | ((uint32_t)f2bf(v[O + 3]) << 16);
-  u.z = (uint32_t)f2bf(v[O + 4]) | ((uint32_t)f2bf(v[O + 5]) << 16);
-  u.w = (uint32_t)f2bf(v[O + 6]) | ((uint32_t)f2bf(v[O + 7]) << 16);
+  u.x = pack_bf2(v[O], v[O + 1]);
+  u.y = pack_bf2(v[O + 2], v[O + 3]);
+  u.z = pack_bf2(v[O + 4], v[O + 5]);
+  u.w = pack_bf2(v[O + 6], v[O + 7]);
   return __builtin_bit_cast(bf16x8_v, u);
 }
 
@@ -124,8 +124,8 @@ __device__ __forceinline__ void store_rows(bf16* row, const f32x16_v (&acc)[NB],
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       uint2 w;
-      w.x = (uint32_t)f2bf(acc[db][4 * j] * f) | ((uint32_t)f2bf(acc[db][4 * j + 1] * f) << 16);
-      w.y = (uint32_t)f2bf(acc[db][4 * j + 2] * f) | ((uint32_t)f2bf(acc[db][4 * j + 3] * f) << 16);
+      w.x = pack_bf2(acc[db][4 * j] * f, acc[db][4 * j + 1] * f);
+      w.y = pack_bf2(acc[db][4 * j + 2] * f, acc[db][4 * j + 3] * f);
       *reinterpret_cast<uint2*>(row + 32 * db + 8 * j + 4 * hf) = w;
     }
 }

@@ -20,11 +20,16 @@ typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16_v;
 
 __device__ __forceinline__ float bf2f(bf16 h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-__device__ __forceinline__ bf16 f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (bf16)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16)(u >> 16);
+// fp32 -> bf16, round to nearest even: the hardware conversion (v_cvt_pk_bf16_f32 on gfx950)
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+typedef float f32x2_v __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ bf16 f2bf(float f) { return __builtin_bit_cast(bf16, (__bf16)f); }
+
+// two fp32 -> one word of two bf16 (a in the low half), one conversion instruction
+__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
+  const f32x2_v v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
 }
 
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }

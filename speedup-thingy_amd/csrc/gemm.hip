@@ -243,10 +243,10 @@ __device__ __forceinline__ void store_chunk(const Epilogue& e, int g, int m, int
         }
       }
       uint4 o;
-      o.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
-      o.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-      o.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
-      o.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+      o.x = pack_bf2(v[0], v[1]);
+      o.y = pack_bf2(v[2], v[3]);
+      o.z = pack_bf2(v[4], v[5]);
+      o.w = pack_bf2(v[6], v[7]);
       *reinterpret_cast<uint4*>(cp) = o;
     } else {
       for (int t = 0; t < nv; ++t) cp[t] = f2bf(v[t] + (e.beta != 0.0f ? e.beta * bf2f(cp[t]) : 0.0f));
@@ -900,10 +900,10 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS, WM>())) gemm_
           }
         }
         uint4 o;
-        o.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
-        o.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-        o.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
-        o.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+        o.x = pack_bf2(v[0], v[1]);
+        o.y = pack_bf2(v[2], v[3]);
+        o.z = pack_bf2(v[4], v[5]);
+        o.w = pack_bf2(v[6], v[7]);
         bf16* dst = part == 0 ? e.q : (part == 1 ? e.k : e.v);
         *reinterpret_cast<uint4*>(dst + (((int64_t)b * e.H + hh) * e.S + s) * e.hd + dim) = o;
       }

@@ -98,8 +98,8 @@ __global__ void __launch_bounds__(256) ce_bwd_kernel(const float* __restrict__ l
     }
     if (n == 4) {
       uint2 o;
-      o.x = (uint32_t)f2bf(d[0]) | ((uint32_t)f2bf(d[1]) << 16);
-      o.y = (uint32_t)f2bf(d[2]) | ((uint32_t)f2bf(d[3]) << 16);
+      o.x = pack_bf2(d[0], d[1]);
+      o.y = pack_bf2(d[2], d[3]);
       *reinterpret_cast<uint2*>(out + c) = o;
     } else {
       for (int i = 0; i < n; ++i) out[c + i] = f2bf(d[i]);

@@ -66,8 +66,8 @@ __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const float* __restric
     const float4 v = *reinterpret_cast<const float4*>(xr + c);
     const float4 g = *reinterpret_cast<const float4*>(w + c);
     uint2 o;
-    o.x = (uint32_t)f2bf(v.x * rstd * g.x) | ((uint32_t)f2bf(v.y * rstd * g.y) << 16);
-    o.y = (uint32_t)f2bf(v.z * rstd * g.z) | ((uint32_t)f2bf(v.w * rstd * g.w) << 16);
+    o.x = pack_bf2(v.x * rstd * g.x, v.y * rstd * g.y);
+    o.y = pack_bf2(v.z * rstd * g.z, v.w * rstd * g.w);
     *reinterpret_cast<uint2*>(orow + c) = o;
   }
 }
@@ -224,7 +224,7 @@ __global__ void __launch_bounds__(256) rope_bwd_pack_kernel(
     xe = ye * c0 + yo * s1;
     xo = yo * c1 - ye * s0;
   }
-  uint32_t packed = (uint32_t)f2bf(xe) | ((uint32_t)f2bf(xo) << 16);
+  uint32_t packed = pack_bf2(xe, xo);
   *reinterpret_cast<uint32_t*>(dqkv + t * 3 * d + col) = packed;
 }
 
@@ -234,8 +234,8 @@ __global__ void __launch_bounds__(256) cast_f32_bf16_kernel(const float* __restr
   if (i + 3 < n) {
     const float4 v = *reinterpret_cast<const float4*>(x + i);
     uint2 o;
-    o.x = (uint32_t)f2bf(v.x) | ((uint32_t)f2bf(v.y) << 16);
-    o.y = (uint32_t)f2bf(v.z) | ((uint32_t)f2bf(v.w) << 16);
+    o.x = pack_bf2(v.x, v.y);
+    o.y = pack_bf2(v.z, v.w);
     *reinterpret_cast<uint2*>(y + i) = o;
   } else {
     for (int64_t j = i; j < n; ++j) y[j] = f2bf(x[j]);

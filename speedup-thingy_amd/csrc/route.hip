@@ -401,10 +401,10 @@ __device__ __forceinline__ void store8<float>(float* dst, const float* v) {
 template <>
 __device__ __forceinline__ void store8<bf16>(bf16* dst, const float* v) {
   uint4 o;
-  o.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
-  o.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-  o.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
-  o.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+  o.x = pack_bf2(v[0], v[1]);
+  o.y = pack_bf2(v[2], v[3]);
+  o.z = pack_bf2(v[4], v[5]);
+  o.w = pack_bf2(v[6], v[7]);
   *reinterpret_cast<uint4*>(dst) = o;
 }
 

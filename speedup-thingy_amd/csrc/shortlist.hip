@@ -255,10 +255,10 @@ __global__ void __launch_bounds__(256) shortlist_bwd_dh_kernel(
   for (int c = 0; c < NC2; ++c) {
     if (lane + 64 * c >= nch) continue;
     uint4 o;
-    o.x = (uint32_t)f2bf(acc[c][0]) | ((uint32_t)f2bf(acc[c][1]) << 16);
-    o.y = (uint32_t)f2bf(acc[c][2]) | ((uint32_t)f2bf(acc[c][3]) << 16);
-    o.z = (uint32_t)f2bf(acc[c][4]) | ((uint32_t)f2bf(acc[c][5]) << 16);
-    o.w = (uint32_t)f2bf(acc[c][6]) | ((uint32_t)f2bf(acc[c][7]) << 16);
+    o.x = pack_bf2(acc[c][0], acc[c][1]);
+    o.y = pack_bf2(acc[c][2], acc[c][3]);
+    o.z = pack_bf2(acc[c][4], acc[c][5]);
+    o.w = pack_bf2(acc[c][6], acc[c][7]);
     *reinterpret_cast<uint4*>(dh + (int64_t)t * d + (lane + 64 * c) * 8) = o;
   }
 }
