@@ -873,18 +873,29 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS, WM>())) gemm_
               Cs[(rbase - h * HR + i * 32 + (r >> 2) * 8 + (r & 3)) * CP + cbase + j * 32] = acc[i][j][r];
       }
       __syncthreads();
-      constexpr int CH = BN / 8;
-      for (int c = tid; c < HR * CH; c += kThreads) {
-        const int row = c / CH, cc = (c % CH) * 8;
-        const int m = m0 + h * HR + row, n = n0 + cc;
+      // a thread keeps one 8-column chunk for the whole slice (kThreads % CH == 0), so the
+      // column's (part, head, dim) are divided out once and the row's (b, s) advance by steps
+      constexpr int CH = BN / 8, RSTEP = kThreads / CH;
+      static_assert(kThreads % CH == 0, "fixed column chunk per thread");
+      const int cc = (tid % CH) * 8, n = n0 + cc;
+      const int part = n / e.dmodel;
+      const int within = n - part * e.dmodel;
+      const int hh = within / e.hd, dim = within - hh * e.hd;
+      int row = tid / CH;
+      int m = m0 + h * HR + row;
+      int b = m / e.S, s = m - b * e.S;
+      for (; row < HR; row += RSTEP, m += RSTEP) {
+        if (row > tid / CH) {
+          s += RSTEP;
+          while (s >= e.S) {
+            s -= e.S;
+            ++b;
+          }
+        }
         if (m >= mlim || n >= p.N) continue;
         const float4 x0 = *reinterpret_cast<const float4*>(Cs + row * CP + cc);
         const float4 x1 = *reinterpret_cast<const float4*>(Cs + row * CP + cc + 4);
         float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-        const int part = n / e.dmodel;
-        const int within = n - part * e.dmodel;
-        const int hh = within / e.hd, dim = within - hh * e.hd;
-        const int b = m / e.S, s = m - b * e.S;
         if (part < 2) {
           const float* cp = e.cos_t + (int64_t)s * e.hd + dim;
           const float* sp = e.sin_t + (int64_t)s * e.hd + dim;
@@ -940,14 +951,25 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs p, EpiFlags
   const int m = (int)(idx / chunks), n = (int)(idx % chunks) * 4;
   float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   const int64_t plane = (int64_t)p.M * p.N;
-  for (int s = 0; s < p.splits; ++s) {
-    const float* src = p.splitk_ws + s * plane + (int64_t)m * p.N + n;
-    if (fl.vec && n + 4 <= p.N) {
-      const float4 x = *reinterpret_cast<const float4*>(src);
-      v[0] += x.x; v[1] += x.y; v[2] += x.z; v[3] += x.w;
-    } else {
-      for (int t = 0; t < 4 && n + t < p.N; ++t) v[t] += src[t];
+  const float* base = p.splitk_ws + (int64_t)m * p.N + n;
+  if (fl.vec && n + 4 <= p.N) {
+    int s = 0;
+    for (; s + 4 <= p.splits; s += 4) {  // four partials in flight, added in split order
+      float4 x[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) x[u] = *reinterpret_cast<const float4*>(base + (s + u) * plane);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        v[0] += x[u].x; v[1] += x[u].y; v[2] += x[u].z; v[3] += x[u].w;
+      }
     }
+    for (; s < p.splits; ++s) {
+      const float4 x = *reinterpret_cast<const float4*>(base + s * plane);
+      v[0] += x.x; v[1] += x.y; v[2] += x.z; v[3] += x.w;
+    }
+  } else {
+    for (int s = 0; s < p.splits; ++s)
+      for (int t = 0; t < 4 && n + t < p.N; ++t) v[t] += base[s * plane + t];
   }
   store_chunk<4>(p.epi, 0, m, n, p.N, v, fl.vec);
 }
