@@ -197,6 +197,7 @@ __global__ void __launch_bounds__(256) adamw_update_kernel(const AdamRow* __rest
   const float lr_wd = (float)(lr_d * hyper[5 * gi + 4]);
   const float step_size = (float)(lr_d / (1.0 - pow(b1_d, step_d)));
   const float bc2_sqrt = (float)sqrt(1.0 - pow(b2_d, step_d));
+  const float inv_bc2 = 1.0f / bc2_sqrt;  // once per workgroup; torch divides by bc2_sqrt
   const float coef = NORMS ? 1.0f : scal[4 * G];
   float* p = reinterpret_cast<float*>(r.p);
   const float* g = reinterpret_cast<const float*>(r.g);
@@ -208,8 +209,8 @@ __global__ void __launch_bounds__(256) adamw_update_kernel(const AdamRow* __rest
     x -= lr_wd * x;
     const float mi = b1 * m[i] + omb1 * gr;
     const float vi = b2 * v[i] + omb2 * gr * gr;
-    const float denom = sqrtf(vi) / bc2_sqrt + eps;
-    x -= step_size * (mi / denom);
+    const float denom = sqrtf(vi) * inv_bc2 + eps;
+    x -= step_size * (mi * __builtin_amdgcn_rcpf(denom));  // hardware reciprocal (1 ulp)
     m[i] = mi;
     v[i] = vi;
     p[i] = x;

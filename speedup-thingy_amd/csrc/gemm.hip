@@ -924,14 +924,14 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS, WM>())) gemm_
 
 // Groups cut into several chunks (or none): add the chunk partials in chunk order and apply
 // the EPI_STORE epilogue.  One-chunk groups were stored by the GEMM itself.
+// Grid (chunks of 256 column groups of 4 over M x N / 4, G): 32-bit index math only.
 __global__ void __launch_bounds__(256) groupk_reduce_kernel(GemmArgs p, EpiFlags fl) {
   const int chunks = (p.N + 3) / 4;
-  const int64_t per_g = (int64_t)p.M * chunks;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= per_g * p.G) return;
-  const int g = (int)(idx / per_g);
-  const int64_t r = idx % per_g;
-  const int m = (int)(r / chunks), n = (int)(r % chunks) * 4;
+  const int per_g = p.M * chunks;  // < 2^31, checked at launch
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= per_g) return;
+  const int g = blockIdx.y;
+  const int m = r / chunks, n = (r - m * chunks) * 4;
   const int q0 = p.gk_first[g], q1 = p.gk_first[g + 1];
   if (q1 - q0 == 1) return;
   float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1067,8 +1067,10 @@ int launch_cfg(const GemmArgs& p0, hipStream_t stream, void* ws, size_t ws_bytes
     RTE_TRY(check_launch("gemm_splitk_reduce"));
   }
   if (p.mode == MODE_GROUP_K && p.gk_chunk > 0) {
-    const int64_t n = (int64_t)p.G * p.M * ((p.N + 3) / 4);
-    hipLaunchKernelGGL(groupk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, p, fl);
+    const int64_t n = (int64_t)p.M * ((p.N + 3) / 4);
+    RTE_REQUIRE(n < ((int64_t)1 << 31) && p.G <= 65535, "gemm: grouped-K output too large");
+    hipLaunchKernelGGL(groupk_reduce_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)p.G), dim3(256), 0, stream, p,
+                       fl);
     RTE_TRY(check_launch("gemm_groupk_reduce"));
   }
   return 0;

@@ -27,6 +27,19 @@ namespace {
 
 constexpr int kMacroWaves = 8;  // waves per workgroup of the per-sample kernels
 
+// tanh in fp32 at a fraction of the library routine's cost: odd Taylor polynomial below 0.25
+// (truncation < 4e-9), else 1 - 2 / (e^(2|x|) + 1) with the sign of x (no cancellation there:
+// the result is at least 0.24).  About 2e-7 relative error.
+__device__ __forceinline__ float tanh_f(float x) {
+  const float a = fabsf(x);
+  if (a < 0.25f) {
+    const float x2 = x * x;
+    return x + x * x2 * (-0.333333333f + x2 * (0.133333333f + x2 * (-0.0539682540f + x2 * 0.0218694885f)));
+  }
+  const float e = __expf(2.0f * a);
+  return copysignf(1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f), x);
+}
+
 __device__ __forceinline__ float wsum_m(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -340,7 +353,7 @@ __global__ void __launch_bounds__(256) macro_epilogue_fwd_kernel(const float* __
     ld8m(bias + kb + col, bs);
     ld8m(scale + kb + col, sc);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = x[i] + c * sc[i] * tanhf(gn[i] * x[i] + l[i] + bs[i]);
+    for (int i = 0; i < 8; ++i) o[i] = x[i] + c * sc[i] * tanh_f(gn[i] * x[i] + l[i] + bs[i]);
     st8m(out + r * d + col, o);
   }
 }
@@ -388,7 +401,7 @@ __global__ void __launch_bounds__(512) macro_epilogue_bwd_kernel(const float* __
       ld8m(dout + off, go);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float t = tanhf(gn[j][i] * x[i] + l[i] + bs[j][i]);
+        const float t = tanh_f(gn[j][i] * x[i] + l[i] + bs[j][i]);
         const float du = go[i] * c * sc[j][i] * (1.0f - t * t);
         oh[i] = go[i] + du * gn[j][i];
         ol[i] = du;

@@ -186,46 +186,56 @@ __global__ void __launch_bounds__(256) colsum_kernel(const float* __restrict__ p
   }
 }
 
-// dq/dk/dv: [B,H,S,hd] with arbitrary element strides; dqkv: [B*S, 3*H*hd] bf16.
-// Inverse of the interleaved rotation y_e = x_e c - x_o s, y_o = x_o c + x_e s.
+// One workgroup per token row of dqkv [T, 3d]: each thread writes 8 consecutive columns (a
+// 16-byte store) from 8 consecutive dims of one head of dq / dk / dv (16-byte loads), with the
+// inverse interleaved rotation on the q and k parts.  Row (b, s) is divided out once per
+// workgroup, the column's (part, head, dim) once per chunk.
 __global__ void __launch_bounds__(256) rope_bwd_pack_kernel(
     const bf16* __restrict__ dq, const bf16* __restrict__ dk, const bf16* __restrict__ dv,
     int64_t sb, int64_t sh, int64_t ss, int64_t sbk, int64_t shk, int64_t ssk, int64_t sbv, int64_t shv,
     int64_t ssv, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int B, int H, int S,
     int hd, bf16* __restrict__ dqkv) {
-  const int d = H * hd;
-  const int64_t npairs = (int64_t)B * S * 3 * d / 2;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= npairs) return;
-  const int64_t e = idx * 2;  // even column of the output row
-  const int64_t t = e / (3 * d);
-  const int col = (int)(e % (3 * d));
-  const int part = col / d;
-  const int within = col % d;
-  const int h = within / hd, dim = within % hd;
-  const int b = (int)(t / S), s = (int)(t % S);
-  const bf16* src;
-  int64_t off;
-  if (part == 0) {
-    src = dq;
-    off = b * sb + h * sh + s * ss + dim;
-  } else if (part == 1) {
-    src = dk;
-    off = b * sbk + h * shk + s * ssk + dim;
-  } else {
-    src = dv;
-    off = b * sbv + h * shv + s * ssv + dim;
+  const int d = H * hd, nch = 3 * d / 8;
+  const int t = blockIdx.x;
+  const int b = t / S, sq = t - b * S;
+  bf16* orow = dqkv + (int64_t)t * 3 * d;
+  for (int c = threadIdx.x; c < nch; c += 256) {
+    const int col = c * 8;
+    const int part = col / d, within = col - part * d;
+    const int h = within / hd, dim = within - h * hd;
+    const bf16* src;
+    if (part == 0) src = dq + b * sb + h * sh + sq * ss + dim;
+    else if (part == 1) src = dk + b * sbk + h * shk + sq * ssk + dim;
+    else src = dv + b * sbv + h * shv + sq * ssv + dim;
+    const uint4 u = *reinterpret_cast<const uint4*>(src);
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      y[2 * i] = __uint_as_float(w[i] << 16);
+      y[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+    if (part < 2) {
+      const float* cp = cos_t + (int64_t)sq * hd + dim;
+      const float* sp = sin_t + (int64_t)sq * hd + dim;
+      const float4 c0 = *reinterpret_cast<const float4*>(cp), c1 = *reinterpret_cast<const float4*>(cp + 4);
+      const float4 s0 = *reinterpret_cast<const float4*>(sp), s1 = *reinterpret_cast<const float4*>(sp + 4);
+      const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ye = y[2 * i], yo = y[2 * i + 1];
+        y[2 * i] = ye * cv[2 * i] + yo * sv[2 * i + 1];
+        y[2 * i + 1] = yo * cv[2 * i + 1] - ye * sv[2 * i];
+      }
+    }
+    uint4 o;
+    o.x = pack_bf2(y[0], y[1]);
+    o.y = pack_bf2(y[2], y[3]);
+    o.z = pack_bf2(y[4], y[5]);
+    o.w = pack_bf2(y[6], y[7]);
+    *reinterpret_cast<uint4*>(orow + col) = o;
   }
-  float ye = bf2f(src[off]), yo = bf2f(src[off + 1]);
-  float xe = ye, xo = yo;
-  if (part < 2) {
-    const float c0 = cos_t[(int64_t)s * hd + dim], s0 = sin_t[(int64_t)s * hd + dim];
-    const float c1 = cos_t[(int64_t)s * hd + dim + 1], s1 = sin_t[(int64_t)s * hd + dim + 1];
-    xe = ye * c0 + yo * s1;
-    xo = yo * c1 - ye * s0;
-  }
-  uint32_t packed = pack_bf2(xe, xo);
-  *reinterpret_cast<uint32_t*>(dqkv + t * 3 * d + col) = packed;
 }
 
 __global__ void __launch_bounds__(256) cast_f32_bf16_kernel(const float* __restrict__ x, int64_t n,
@@ -293,16 +303,21 @@ int rmsnorm_bwd(const bf16* dy, const float* x, const float* w, const float* rst
 int rope_bwd_pack(const bf16* dq, const int64_t* sq, const bf16* dk, const int64_t* sk, const bf16* dv,
                   const int64_t* sv, const float* cos_t, const float* sin_t, int B, int H, int S, int hd,
                   bf16* dqkv, hipStream_t s) {
-  RTE_REQUIRE(hd % 2 == 0, "rope_bwd: head_dim must be even");
+  RTE_REQUIRE(hd % 8 == 0, "rope_bwd: head_dim must be a multiple of 8");
   for (int i = 0; i < 3; ++i) {
     const int64_t* st = i == 0 ? sq : (i == 1 ? sk : sv);
+    const bf16* base = i == 0 ? dq : (i == 1 ? dk : dv);
     RTE_REQUIRE(st[3] == 1, "rope_bwd: innermost stride must be 1");
+    RTE_REQUIRE(st[0] % 8 == 0 && st[1] % 8 == 0 && st[2] % 8 == 0 && ((uintptr_t)base & 15) == 0,
+                "rope_bwd: gradients need 16-byte aligned rows (strides multiples of 8)");
   }
-  const int64_t npairs = (int64_t)B * S * 3 * H * hd / 2;
-  if (npairs == 0) return 0;
-  hipLaunchKernelGGL(rope_bwd_pack_kernel, dim3((unsigned)((npairs + 255) / 256)), dim3(256), 0, s, dq, dk, dv,
-                     sq[0], sq[1], sq[2], sk[0], sk[1], sk[2], sv[0], sv[1], sv[2], cos_t, sin_t, B, H, S, hd,
-                     dqkv);
+  RTE_REQUIRE(((uintptr_t)dqkv & 15) == 0 && ((uintptr_t)cos_t & 15) == 0 && ((uintptr_t)sin_t & 15) == 0,
+              "rope_bwd: 16-byte aligned buffers");
+  const int64_t T = (int64_t)B * S;
+  if (T == 0 || H * hd == 0) return 0;
+  RTE_REQUIRE(T < ((int64_t)1 << 31), "rope_bwd: too many tokens");
+  hipLaunchKernelGGL(rope_bwd_pack_kernel, dim3((unsigned)T), dim3(256), 0, s, dq, dk, dv, sq[0], sq[1], sq[2],
+                     sk[0], sk[1], sk[2], sv[0], sv[1], sv[2], cos_t, sin_t, B, H, S, hd, dqkv);
   return check_launch("rope_bwd_pack");
 }
 
