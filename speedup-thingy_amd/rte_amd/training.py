@@ -252,7 +252,11 @@ class TrainEngine:
                                                  launch=launched[0] if launched else None)
             aux = self._router_aux(hot)
             scale = self._loss_scale(targets)
-            loss = audit.corrected_loss_per_sample.mean() / scale + sum(audit.macro_aux.values()) + sum(aux.values())
+            # the auxiliary terms as one stacked sum (two launches instead of one add per term)
+            terms = [audit.corrected_loss_per_sample.mean() / scale, *audit.macro_aux.values(), *aux.values()]
+            dev = terms[0].device
+            loss = torch.stack([(t if isinstance(t, torch.Tensor) else torch.tensor(float(t), device=dev))
+                                .reshape(()).float() for t in terms]).sum()
         return loss, hot, audit, aux, scale
 
     def _macro_metrics(self, loss, hot, audit, aux, scale, targets, shortlist, stepped):
