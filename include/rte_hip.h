@@ -89,6 +89,18 @@ int rte_combine_rows(const void* rows, int T, int k, int d, const int32_t* slot_
 int rte_route_bwd(const int32_t* ids, const float* w, const float* dw_slot, const int32_t* slot_of_pair,
                   int T, int C, int k, void* dlogits_bf16, float* dlogits_f32, void* stream);
 
+/* ---- pack of per-sample route lists (the banked FFN's recipe routing, rte/layers.py:744-779):
+ *      every token of sample b visits clusters routes[recipe_ids[b], j] (int32 [n_recipes, kmax],
+ *      -1 = none; recipe ids outside [0, n_recipes) route nowhere) with weight route_w[recipe_ids[b]] (f32 [R], NULL = 1); samples with active[b] == 0
+ *      (uint8 [B], optional) visit none.  Outputs as rte_pack_index for the B*seq*kmax expanded
+ *      (token, j) pairs (a route list must not repeat a cluster); two launches.
+ *      Workspace: rte_pack_routes_workspace_bytes(B, kmax). ---- */
+size_t rte_pack_routes_workspace_bytes(int B, int kmax);
+int rte_pack_routes(const int64_t* recipe_ids, const uint8_t* active, int B, int seq, const int32_t* routes,
+                    int n_recipes, int kmax,
+                    const float* route_w, int C, int32_t* offsets, int32_t* tok_of_slot, int32_t* pair_of_slot,
+                    int32_t* slot_of_pair, float* w_of_slot, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- routed cluster-pool SwiGLU (rte/kernels/cluster_pool_ffn.py:192-241,
  *      rte/layers.py:119-220 StaticClusterPoolSwiGLU, rte/layers.py:731-779 BankedSwiGLU) ----
  * Cluster g owns neurons [g*n, (g+1)*n) of a d_ff = G*n SwiGLU:

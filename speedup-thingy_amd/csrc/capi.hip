@@ -55,6 +55,10 @@ int macro_table_grad(const int64_t* key, int B, int S, int G, int d, const void*
 size_t mse_workspace_bytes(int64_t n);
 int mse_fwd(const float* a, const float* b, int64_t n, float* out, void* ws, size_t ws_bytes, hipStream_t s);
 int mse_bwd(const float* a, const float* b, int64_t n, const float* g, float* da, float* db, hipStream_t s);
+size_t pack_routes_workspace_bytes(int B, int kmax);
+int pack_routes(const int64_t* rid, const uint8_t* active, int B, int S, const int32_t* routes, int R, int kmax,
+                const float* route_w, int C, int32_t* offsets, int32_t* tok_of_slot, int32_t* pair_of_slot,
+                int32_t* slot_of_pair, float* w_of_slot, void* ws, size_t ws_bytes, hipStream_t s);
 int adamw_chunk();
 size_t adamw_workspace_bytes(int nt, int nblk, int G);
 int adamw_step(const void* rows, int nt, const int32_t* blk, const int32_t* first_blk, int nblk, const double* hyper,
@@ -833,6 +837,16 @@ int rte_mse_fwd(const float* a, const float* b, int64_t n, float* out, void* wor
 
 int rte_mse_bwd(const float* a, const float* b, int64_t n, const float* dout, float* da, float* db, void* stream) {
   return mse_bwd(a, b, n, dout, da, db, S(stream));
+}
+
+size_t rte_pack_routes_workspace_bytes(int B, int kmax) { return pack_routes_workspace_bytes(B, kmax); }
+
+int rte_pack_routes(const int64_t* recipe_ids, const uint8_t* active, int B, int seq, const int32_t* routes,
+                    int n_recipes, int kmax,
+                    const float* route_w, int C, int32_t* offsets, int32_t* tok_of_slot, int32_t* pair_of_slot,
+                    int32_t* slot_of_pair, float* w_of_slot, void* workspace, size_t workspace_bytes, void* stream) {
+  return pack_routes(recipe_ids, active, B, seq, routes, n_recipes, kmax, route_w, C, offsets, tok_of_slot, pair_of_slot,
+                     slot_of_pair, w_of_slot, workspace, workspace_bytes, S(stream));
 }
 
 int rte_adamw_chunk(void) { return adamw_chunk(); }

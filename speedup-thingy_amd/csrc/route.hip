@@ -389,6 +389,80 @@ __global__ void __launch_bounds__(64) route_topk_lanes_kernel(const float* __res
     }
 }
 
+// ---- pack of per-sample route lists (the banked FFN: every token of sample b visits the
+// clusters routes[rid[b], j], j < kmax, -1 = none, with weight route_w[rid[b]]; samples with
+// active[b] == 0 visit none).  Produces the slots pack_pairs gives for the expanded (token, j)
+// pairs: clusters in order, inside a cluster ascending token (sample, then position).
+// Plan (one workgroup): per-cluster sample counts, offsets, and for each (b, j) the number of
+// earlier samples routed to the same cluster; then one thread per pair writes its slot.
+__global__ void __launch_bounds__(256) pack_routes_plan_kernel(const int64_t* __restrict__ rid,
+                                                               const uint8_t* __restrict__ active, int B, int S,
+                                                               const int32_t* __restrict__ routes, int R, int kmax,
+                                                               int C, int32_t* __restrict__ offsets,
+                                                               int32_t* __restrict__ base) {
+  extern __shared__ int32_t cnt[];  // [C]
+  const int tid = threadIdx.x;
+  for (int c = tid; c < C; c += 256) cnt[c] = 0;
+  __syncthreads();
+  for (int b = tid; b < B; b += 256) {
+    if ((active && !active[b]) || rid[b] < 0 || rid[b] >= R) continue;
+    const int32_t* rr = routes + rid[b] * kmax;
+    for (int j = 0; j < kmax; ++j) {
+      const int c = rr[j];
+      if (c >= 0 && c < C) atomicAdd(&cnt[c], 1);  // integer counts: order-independent
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int run = 0;
+    for (int c = 0; c < C; ++c) {
+      const int v = cnt[c];
+      cnt[c] = run;
+      offsets[c] = run * S;
+      run += v;
+    }
+    offsets[C] = run * S;
+  }
+  __syncthreads();
+  for (int c = tid; c < C; c += 256) {  // samples in order: rank among the cluster's samples
+    int r = 0;
+    for (int b = 0; b < B; ++b) {
+      if ((active && !active[b]) || rid[b] < 0 || rid[b] >= R) continue;
+      const int32_t* rr = routes + rid[b] * kmax;
+      for (int j = 0; j < kmax; ++j)
+        if (rr[j] == c) base[b * kmax + j] = r++;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256) pack_routes_write_kernel(const int64_t* __restrict__ rid,
+                                                                const uint8_t* __restrict__ active, int B, int S,
+                                                                const int32_t* __restrict__ routes, int R, int kmax,
+                                                                const float* __restrict__ route_w, int C,
+                                                                const int32_t* __restrict__ offsets,
+                                                                const int32_t* __restrict__ base,
+                                                                int32_t* __restrict__ tok_of_slot,
+                                                                int32_t* __restrict__ pair_of_slot,
+                                                                int32_t* __restrict__ slot_of_pair,
+                                                                float* __restrict__ w_of_slot) {
+  const int P = B * S * kmax;
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  if (p >= P) return;
+  const int t = p / kmax, j = p - t * kmax;
+  const int b = t / S, s = t - b * S;
+  const bool on = !(active && !active[b]) && rid[b] >= 0 && rid[b] < R;  // unknown recipes route nowhere
+  const int c = on ? routes[rid[b] * kmax + j] : -1;
+  if (c < 0 || c >= C) {
+    if (slot_of_pair) slot_of_pair[p] = -1;
+    return;
+  }
+  const int slot = offsets[c] + base[b * kmax + j] * S + s;
+  if (tok_of_slot) tok_of_slot[slot] = t;
+  if (pair_of_slot) pair_of_slot[slot] = p;
+  if (slot_of_pair) slot_of_pair[p] = slot;
+  if (w_of_slot) w_of_slot[slot] = route_w ? route_w[rid[b]] : 1.0f;
+}
+
 template <typename OutT>
 __device__ __forceinline__ void store8(OutT* dst, const float* v);
 
@@ -581,6 +655,27 @@ int route_bwd(const int32_t* ids, const float* w, const float* dw_slot, const in
   hipLaunchKernelGGL(route_bwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, ids, w, dw_slot,
                      slot_of_pair, T, C, k, dlogits, dlogits_f32);
   return check_launch("route_bwd");
+}
+
+size_t pack_routes_workspace_bytes(int B, int kmax) {
+  return (size_t)(B > 0 ? B : 1) * (kmax > 0 ? kmax : 1) * sizeof(int32_t);
+}
+
+int pack_routes(const int64_t* rid, const uint8_t* active, int B, int S, const int32_t* routes, int R, int kmax,
+                const float* route_w, int C, int32_t* offsets, int32_t* tok_of_slot, int32_t* pair_of_slot,
+                int32_t* slot_of_pair, float* w_of_slot, void* ws, size_t ws_bytes, hipStream_t s) {
+  RTE_REQUIRE(B >= 0 && S >= 1 && R >= 1 && kmax >= 1 && C >= 1 && C <= 16384, "pack_routes: bad sizes");
+  RTE_REQUIRE((int64_t)B * S * kmax < ((int64_t)1 << 31), "pack_routes: too many pairs");
+  RTE_REQUIRE(ws && ws_bytes >= pack_routes_workspace_bytes(B, kmax), "pack_routes: workspace too small");
+  if (B == 0) return fill_i32(offsets, 0, C + 1, s);
+  int32_t* base = static_cast<int32_t*>(ws);
+  hipLaunchKernelGGL(pack_routes_plan_kernel, dim3(1), dim3(256), (size_t)C * sizeof(int32_t), s, rid, active, B, S,
+                     routes, R, kmax, C, offsets, base);
+  RTE_TRY(check_launch("pack_routes_plan"));
+  const int P = B * S * kmax;
+  hipLaunchKernelGGL(pack_routes_write_kernel, dim3((P + 255) / 256), dim3(256), 0, s, rid, active, B, S, routes, R,
+                     kmax, route_w, C, offsets, base, tok_of_slot, pair_of_slot, slot_of_pair, w_of_slot);
+  return check_launch("pack_routes_write");
 }
 
 }  // namespace rte

@@ -79,6 +79,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_mse_workspace_bytes": (_SZ, [_I64]),
     "rte_mse_fwd": (_I, [_P, _P, _I64, _P, _P, _SZ, _P]),
     "rte_mse_bwd": (_I, [_P, _P, _I64, _P, _P, _P, _P]),
+    "rte_pack_routes_workspace_bytes": (_SZ, [_I, _I]),
+    "rte_pack_routes": (_I, [_P, _P, _I, _I, _P, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "rte_distill_workspace_bytes": (_SZ, [_I, _I]),
     "rte_distill_fwd": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _I, _F, _F, _P, _P, _P, _P, _SZ, _P]),
     "rte_distill_bwd": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _I, _F, _F, _P, _P, _P, _SZ, _P, _P, _P]),

@@ -507,6 +507,33 @@ def pack_index(ids: torch.Tensor, n_clusters: int, weights: torch.Tensor | None 
     return PackIndex(offsets, tok, pos, sop, wos, n_clusters, k)
 
 
+def pack_routes(recipe_ids: torch.Tensor, routes: torch.Tensor, route_w: torch.Tensor | None, seq: int,
+                n_clusters: int, active: torch.Tensor | None = None) -> PackIndex:
+    """Pack of per-sample route lists: every token of sample b visits clusters
+    routes[recipe_ids[b]] (-1 = none) with weight route_w[recipe_ids[b]]; samples with active
+    False visit none.  The same slots as pack_index on the expanded [B*seq, kmax] ids, in two
+    launches instead of the expansion, copies and three counting-sort launches."""
+    _lib.require_device_tensors("pack_routes", recipe_ids, routes, route_w, active)
+    rid = recipe_ids.reshape(-1).contiguous().to(torch.int64)
+    rt = routes.contiguous().to(torch.int32)
+    R, kmax = rt.shape
+    B = rid.numel()
+    P = B * seq * kmax
+    dev = rid.device
+    offsets = torch.empty((n_clusters + 1,), dtype=torch.int32, device=dev)
+    tok = torch.empty((P,), dtype=torch.int32, device=dev)
+    pos = torch.empty((P,), dtype=torch.int32, device=dev)
+    sop = torch.empty((P,), dtype=torch.int32, device=dev)
+    wos = torch.empty((P,), dtype=F32, device=dev)
+    nbytes = _lib.load().rte_pack_routes_workspace_bytes(B, kmax)
+    ws = torch.empty((max(1, nbytes // 4),), dtype=torch.int32, device=dev)
+    act = None if active is None else active.reshape(-1).contiguous().to(torch.uint8)
+    rw = None if route_w is None else route_w.contiguous().to(F32)
+    call("rte_pack_routes", ptr(rid), ptr(act), B, seq, ptr(rt), R, kmax, ptr(rw), n_clusters, ptr(offsets), ptr(tok),
+         ptr(pos), ptr(sop), ptr(wos), ptr(ws), nbytes, _s())
+    return PackIndex(offsets, tok, pos, sop, wos, n_clusters, kmax)
+
+
 def combine_rows(rows: torch.Tensor, T: int, k: int, *, extra=None, resid=None, out_f32=True,
                  slot_of_pair=None) -> torch.Tensor:
     """out[t] = resid[t] + extra[t] + sum_j rows[t*k + j]; pairs whose slot_of_pair is -1 are skipped."""
@@ -522,13 +549,15 @@ def combine_rows(rows: torch.Tensor, T: int, k: int, *, extra=None, resid=None, 
 
 # ----------------------------------------------------------------------------- routed cluster-pool SwiGLU
 
-def _pool_fwd(xb, ids, w, wugb, wdb, C: int, n: int, resid, masked: bool):
-    """Grouped pool forward over the (token, cluster) pairs of ids [T, k] (id -1 = no pair).
-    wugb [2F, d] rows [up F ; gate F], wdb [d, F]; cluster g owns neurons [g*n, (g+1)*n)."""
+def _pool_fwd(xb, ids, w, wugb, wdb, C: int, n: int, resid, masked: bool, pk: PackIndex | None = None):
+    """Grouped pool forward over the (token, cluster) pairs of ids [T, k] (id -1 = no pair), or
+    of a prebuilt pack pk.  wugb [2F, d] rows [up F ; gate F], wdb [d, F]; cluster g owns
+    neurons [g*n, (g+1)*n)."""
     T, d = xb.shape
-    k = ids.shape[1]
+    k = ids.shape[1] if pk is None else pk.k
     F = C * n
-    pk = pack_index(ids, C, w)
+    if pk is None:
+        pk = pack_index(ids, C, w)
     P = T * k
     ug = torch.empty((P, 2 * n), dtype=BF16, device=xb.device)
     zw = torch.empty((P, n), dtype=BF16, device=xb.device)
@@ -626,7 +655,7 @@ class GroupedPoolFn(torch.autograd.Function):
     operands: their gradients come back in fp32."""
 
     @staticmethod
-    def forward(ctx, x, ids, w, wug_t, wd_t, resid, n: int):
+    def forward(ctx, x, ids, w, wug_t, wd_t, resid, n: int, pk=None):
         _lib.require_device_tensors("grouped_pool", x, ids, w, wug_t, wd_t, resid)
         shape = x.shape
         d = shape[-1]
@@ -634,14 +663,17 @@ class GroupedPoolFn(torch.autograd.Function):
         T = xb.shape[0]
         F = wug_t.shape[0] // 2
         C = F // n
-        idc = ids.reshape(T, -1).contiguous().to(torch.int32)
-        wc = w.reshape(T, -1).contiguous().to(F32)
+        if pk is None:
+            idc = ids.reshape(T, -1).contiguous().to(torch.int32)
+            wc = w.reshape(T, -1).contiguous().to(F32)
+        else:
+            idc = wc = None
         wugb, wdb = cast_bf16(wug_t), cast_bf16(wd_t)  # parameter views: once per step
         rs = None if resid is None else resid.reshape(T, d)
-        out, pk, ug, zw = _pool_fwd(xb, idc, wc, wugb, wdb, C, n, rs, masked=True)
+        out, pk, ug, zw = _pool_fwd(xb, idc, wc, wugb, wdb, C, n, rs, masked=True, pk=pk)
         ctx.save_for_backward(xb, wugb, wdb, pk.offsets, pk.tok_of_slot, pk.pair_of_slot, pk.slot_of_pair,
                               pk.w_of_slot, ug, zw)
-        ctx.meta = (shape, idc.shape[1], C, n, resid is not None, x.dtype)
+        ctx.meta = (shape, pk.k, C, n, resid is not None, x.dtype)
         return out.view(shape)
 
     @staticmethod
@@ -652,11 +684,13 @@ class GroupedPoolFn(torch.autograd.Function):
         pk = PackIndex(offsets, tok, pos, sop, wos, C, k)
         dxp, dwug, dwd, _ = _pool_bwd(cast_bf16(dout.reshape(T, d)), xb, wugb, wdb, pk, ug, zw, C, n, k)
         dx = combine_rows(dxp, T, k, out_f32=False, slot_of_pair=sop)
-        return dx.view(shape).to(x_dt), None, None, dwug, dwd, (dout if has_resid else None), None
+        return dx.view(shape).to(x_dt), None, None, dwug, dwd, (dout if has_resid else None), None, None
 
 
-def grouped_pool_swiglu(x, ids, w, wug_t, wd_t, n: int, resid=None):
-    return GroupedPoolFn.apply(x, ids, w, wug_t, wd_t, resid, n)
+def grouped_pool_swiglu(x, ids, w, wug_t, wd_t, n: int, resid=None, pk: PackIndex | None = None):
+    """Grouped pool SwiGLU over the routes ids / w [T, k], or over a prebuilt pack pk (then ids
+    and w are not read)."""
+    return GroupedPoolFn.apply(x, ids, w, wug_t, wd_t, resid, n, pk)
 
 
 # ----------------------------------------------------------------------------- plain linear (LM head)

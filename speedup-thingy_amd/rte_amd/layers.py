@@ -267,6 +267,16 @@ class BankedSwiGLU(nn.Module):
         slab = self.config.d_ff // self.config.ffn_groups
         return hip_ops.grouped_pool_swiglu(x, ids, w, wug_t, wd_t, slab)
 
+    def forward_recipes(self, x: torch.Tensor, recipe_ids: torch.Tensor, active: torch.Tensor | None = None,
+                        weights=None) -> torch.Tensor:
+        """Every sample's tokens through its recipe's clusters (inactive samples: none), packed
+        straight from the recipe ids (rte_pack_routes)."""
+        wug_t, wd_t = weights if weights is not None else self.pool_weights()
+        slab = self.config.d_ff // self.config.ffn_groups
+        pk = hip_ops.pack_routes(recipe_ids, self.recipe_routes, self.recipe_route_w, x.shape[1],
+                                 wug_t.shape[0] // 2 // slab, active)
+        return hip_ops.grouped_pool_swiglu(x, None, None, wug_t, wd_t, slab, pk=pk)
+
     def routes_for(self, recipe_ids: torch.Tensor, seq: int, active: torch.Tensor | None = None):
         """Per-token routes of samples with recipe_ids [B] (inactive samples get none)."""
         ids = self.recipe_routes[recipe_ids]                                   # [B, kmax]
@@ -320,7 +330,7 @@ class BankedRecursiveCore(nn.Module):
                                                 self.pass_beta2, self.pass_attn_scale, self.pass_mlp_scale))
         return {"pool": self.mlp.pool_weights(), "pass": per_pass}
 
-    def _step(self, h, h0, head_scale, ids, w, pass_idx: int, weights=None, active=None):
+    def _step(self, h, h0, head_scale, ids, w, pass_idx: int, weights=None, active=None, recipe_ids=None):
         """One pass: three fused residual / FiLM-norm launches around attention and the pool
         FFN; samples whose `active` entry is False keep h."""
         if weights is None:
@@ -331,7 +341,10 @@ class BankedRecursiveCore(nn.Module):
                                         self.norm1.weight, g1, b1, self.norm1.eps)
         attn = self.attn.forward_scaled(n1, head_scale)
         u, n2 = hip_ops.axpy_norm(h_tilde, attn, sa, self.norm2.weight, g2, b2, self.norm2.eps)
-        mlp = self.mlp.forward_routes(n2, ids, w, weights["pool"])
+        if recipe_ids is not None:  # per-sample recipes: pack the routes straight from the ids
+            mlp = self.mlp.forward_recipes(n2, recipe_ids, active, weights["pool"])
+        else:
+            mlp = self.mlp.forward_routes(n2, ids, w, weights["pool"])
         return hip_ops.axpy(u, mlp, sm, keep=h if active is not None else None, mask=active)
 
     def step_group(self, h, h0, spec: RecipeSpec, pass_idx: int = 0):
@@ -350,5 +363,4 @@ class BankedRecursiveCore(nn.Module):
         B, S, _ = h.shape
         rid = recipe_ids.long()
         head_scale = self.attn.recipe_head_scale[rid]
-        ids, w = self.mlp.routes_for(rid, S, active_mask)
-        return self._step(h, h0, head_scale, ids, w, pass_idx, weights, active_mask).to(h.dtype)
+        return self._step(h, h0, head_scale, None, None, pass_idx, weights, active_mask, rid).to(h.dtype)

@@ -229,6 +229,35 @@ def test_route_topk_kernels_agree(C, k):
     assert torch.equal(ids_l[:8000], ids_w) and torch.equal(w_l[:8000], w_w)
 
 
+@pytest.mark.parametrize("B,S,R,kmax,C", [(1, 64, 6, 8, 64), (128, 64, 16, 8, 64), (37, 5, 9, 4, 300)])
+def test_pack_routes_matches_expanded_pack(B, S, R, kmax, C):
+    """Route-list pack from recipe ids equals the counting-sort pack of the expanded per-token
+    routes (every field bit-exact), with -1 padding, inactive samples and an unknown recipe id."""
+    H = _ops()
+    rng = np.random.default_rng(B + R + C)
+    routes = np.full((R, kmax), -1, np.int32)
+    for r in range(R):
+        m = rng.integers(1, kmax + 1)
+        routes[r, :m] = rng.choice(C, size=m, replace=False)
+    rw = rng.random(R).astype(np.float32)
+    rid = rng.integers(0, R, B).astype(np.int64)
+    active = rng.random(B) < 0.8
+    if B > 2:
+        rid[2] = R + 3  # unknown recipe: no routes
+    exp_ids = np.where((active[:, None] & (rid[:, None] < R)), routes[np.minimum(rid, R - 1)], -1)
+    ids = np.repeat(exp_ids, S, axis=0)
+    w = np.repeat(np.where(rid < R, rw[np.minimum(rid, R - 1)], 0.0), S)[:, None].repeat(kmax, 1).astype(np.float32)
+    print(f"pack_routes B={B} S={S} R={R} kmax={kmax} C={C}", flush=True)
+    got = H.pack_routes(torch.from_numpy(rid).to(DEV), torch.from_numpy(routes).to(DEV),
+                        torch.from_numpy(rw).to(DEV), S, C, torch.from_numpy(active).to(DEV))
+    want = H.pack_index(torch.from_numpy(ids).to(DEV), C, torch.from_numpy(w).to(DEV))
+    n = int(want.offsets[-1].item())
+    assert torch.equal(got.offsets, want.offsets)
+    for name in ("tok_of_slot", "pair_of_slot", "w_of_slot"):
+        assert torch.equal(getattr(got, name)[:n], getattr(want, name)[:n]), name
+    assert torch.equal(got.slot_of_pair, want.slot_of_pair)
+
+
 @pytest.mark.parametrize("T,k,C", [(1, 1, 1), (1000, 4, 32), (8192, 8, 64), (4096, 16, 256), (5000, 3, 77),
                                    (20000, 8, 64), (70001, 8, 64)])
 def test_pack_index_bit_exact(T, k, C):
