@@ -222,6 +222,7 @@ class AxpyNormFn(torch.autograd.Function):
              ptr(rstd) if w is not None else None, _s())
         ctx.save_for_backward(x, rstd, vecs[0], vecs[1], b2, cc, m)
         ctx.meta = (shape, T, d, S, w is not None, c.shape if c is not None else None)
+        ctx.set_materialize_grads(False)  # an unused output's gradient stays None (no zero fill)
         if w is None:
             ctx.mark_non_differentiable(n)
         return x.view(shape), (n.view(shape) if w is not None else n)
@@ -230,6 +231,8 @@ class AxpyNormFn(torch.autograd.Function):
     def backward(ctx, dx_ext, dn):
         x, rstd, w, gamma, b2, cc, m = ctx.saved_tensors
         shape, T, d, S, has_norm, c_shape = ctx.meta
+        if dx_ext is None and (dn is None or not has_norm):
+            return (None,) * 9
         dev = x.device
         dxe = None if dx_ext is None else dx_ext.reshape(T, d).contiguous().to(F32)
         dnb = None if (dn is None or not has_norm) else dn.reshape(T, d).contiguous().to(BF16)
@@ -616,10 +619,13 @@ class RoutedClusterPoolFn(torch.autograd.Function):
                               pk.slot_of_pair, pk.w_of_slot, ug, zw)
         ctx.meta = (shape, k, C, n, resid is not None, wr.dtype, wug.dtype, wd.dtype)
         ctx.mark_non_differentiable(ids, w)
+        ctx.set_materialize_grads(False)  # no zero fills for the routing outputs
         return out.view(shape), ids, w
 
     @staticmethod
     def backward(ctx, dout, _dids, _dw):
+        if dout is None:
+            return (None,) * 6
         (xb, wrb, wugb, wdb, ids, w, offsets, tok, pos, sop, wos, ug, zw) = ctx.saved_tensors
         shape, k, C, n, has_resid, wr_dt, wug_dt, wd_dt = ctx.meta
         T, d = xb.shape
@@ -806,10 +812,13 @@ class DistillFn(torch.autograd.Function):
         ctx.meta = (A, S, d, V, float(temperature), float(eps), nbytes, has_l,
                     None if not has_l else hot_logits.shape, tuple(float(x) for x in weights))
         ctx.mark_non_differentiable(metrics)
+        ctx.set_materialize_grads(False)
         return (*losses.unbind(0), metrics)
 
     @staticmethod
     def backward(ctx, *grads):
+        if all(g is None for g in grads[:6]):
+            return (None,) * 8
         hv, ev, zv, hl, el, ws = ctx.saved_tensors
         A, S, d, V, t, eps, nbytes, has_l, lshape, weights = ctx.meta
         gs = [g if g is not None else torch.zeros((), dtype=F32, device=hv.device) for g in grads[:6]]
@@ -859,10 +868,13 @@ class AuditCorrectFn(torch.autograd.Function):
         ctx.save_for_backward(ix, coef)
         ctx.meta = (B, S, A, hot_tok.dtype, None if exact_tok is None else exact_tok.dtype)
         ctx.mark_non_differentiable(exact_ps, stats)
+        ctx.set_materialize_grads(False)
         return corrected, exact_ps, stats
 
     @staticmethod
     def backward(ctx, g, _g_exact, _g_stats):
+        if g is None:
+            return (None,) * 6
         ix, coef = ctx.saved_tensors
         B, S, A, h_dt, e_dt = ctx.meta
         gg = g.contiguous().to(F32)

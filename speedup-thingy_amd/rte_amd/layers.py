@@ -205,17 +205,23 @@ class BankedAttention(nn.Module):
         cos = torch.ones(8192, hd, device=self.wqkv.device)
         return cos, torch.zeros_like(cos)
 
-    def forward_scaled(self, x: torch.Tensor, head_scale: torch.Tensor) -> torch.Tensor:
+    def bank_weights(self):
+        """Per-bank (Wqkv^T, Wo^T) views, split once per forward: every recursive pass then shares
+        one gradient stack per parameter instead of a zero-fill and copy per use."""
+        return tuple(w.t() for w in self.wqkv.unbind(0)), tuple(w.t() for w in self.wo.unbind(0))
+
+    def forward_scaled(self, x: torch.Tensor, head_scale: torch.Tensor, banks=None) -> torch.Tensor:
         """x [B, S, d], head_scale [B, attn_banks, n_heads] -> fp32 [B, S, d]."""
         cos, sin = self._tables()
         H = self.config.n_heads
+        wqkv_t, wo_t = banks if banks is not None else self.bank_weights()
         out = None
         for bank in range(self.config.attn_banks):
-            q, k, v = hip_ops.qkv_rope(x, self.wqkv[bank].t(), cos, sin, H)
+            q, k, v = hip_ops.qkv_rope(x, wqkv_t[bank], cos, sin, H)
             # the recipe's head mask (1/|banks| on its heads, 0 elsewhere: rte/layers.py:702-730 runs
             # only the active heads and averages the banks) scales each head's attention output
             y = hip_ops.attention(q, k, v, head_scale[:, bank, :])
-            out = hip_ops.attn_out_proj(y, self.wo[bank].t(), out)
+            out = hip_ops.attn_out_proj(y, wo_t[bank], out)
         return out
 
     def forward(self, x: torch.Tensor, spec: RecipeSpec) -> torch.Tensor:
@@ -328,7 +334,7 @@ class BankedRecursiveCore(nn.Module):
         backward instead of a zero-fill and copy per pass)."""
         per_pass = tuple(p.unbind(0) for p in (self.pass_gamma1, self.pass_beta1, self.pass_gamma2,
                                                 self.pass_beta2, self.pass_attn_scale, self.pass_mlp_scale))
-        return {"pool": self.mlp.pool_weights(), "pass": per_pass}
+        return {"pool": self.mlp.pool_weights(), "pass": per_pass, "attn": self.attn.bank_weights()}
 
     def _step(self, h, h0, head_scale, ids, w, pass_idx: int, weights=None, active=None, recipe_ids=None):
         """One pass: three fused residual / FiLM-norm launches around attention and the pool
@@ -339,7 +345,7 @@ class BankedRecursiveCore(nn.Module):
         h = h.float()
         h_tilde, n1 = hip_ops.axpy_norm(h, None if self.alpha_inj is None else h0.float(), self.alpha_inj,
                                         self.norm1.weight, g1, b1, self.norm1.eps)
-        attn = self.attn.forward_scaled(n1, head_scale)
+        attn = self.attn.forward_scaled(n1, head_scale, weights.get("attn"))
         u, n2 = hip_ops.axpy_norm(h_tilde, attn, sa, self.norm2.weight, g2, b2, self.norm2.eps)
         if recipe_ids is not None:  # per-sample recipes: pack the routes straight from the ids
             mlp = self.mlp.forward_recipes(n2, recipe_ids, active, weights["pool"])
