@@ -142,7 +142,9 @@ size_t rte_grouped_swiglu_bwd_workspace_bytes(int P, int G, int n, int d);
 int rte_dense_swiglu_fwd(const void* x, int T, int d, int F, const void* wug, const void* wd, int wd_rows,
                          const float* resid, void* ug, void* z, void* out, int out_f32, void* stream);
 /* dout bf16 [T, d]; writes dug [T, 2F] bf16, dx [T, d] bf16, dwug [2F, d] f32,
- * dwd f32 in the layout of wd (overwritten). */
+ * dwd f32 in the layout of wd (overwritten).  workspace: split-K partials of the dx and weight
+ * gradients, max of rte_gemm_workspace_bytes(T, d, 2F), (2F, d, T) and (d, F, T) bytes (fewer
+ * bytes: fewer splits). */
 int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, const void* wug,
                          const void* wd, int wd_rows, const void* ug, const void* z, void* dug, void* dx,
                          float* dwug, float* dwd, void* workspace, size_t workspace_bytes, void* stream);
@@ -153,7 +155,9 @@ int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, c
 int rte_qkv_rope_fwd(const void* x, const void* wqkv, const float* cos_t, const float* sin_t, int B, int S,
                      int H, int hd, void* q, void* k, void* v, void* stream);
 /* dq/dk/dv: [B,H,S,hd] bf16 with element strides s*[4] (innermost must be 1).
- * dqkv: [B*S, 3d] bf16 workspace; dx [B*S, d] bf16; dw [3d, d] f32 (overwritten). */
+ * dqkv: [B*S, 3d] bf16 workspace; dx [B*S, d] bf16; dw [3d, d] f32 (overwritten).
+ * workspace: split-K partials of dx and dw, max of rte_gemm_workspace_bytes(B*S, d, 3d) and
+ * (3d, d, B*S) bytes (fewer bytes: fewer splits). */
 int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const int64_t* sk, const void* dv,
                      const int64_t* sv, const void* x, const void* wqkv, const float* cos_t,
                      const float* sin_t, int B, int S, int H, int hd, void* dqkv, void* dx, float* dw,

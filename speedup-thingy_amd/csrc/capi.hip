@@ -446,7 +446,8 @@ int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, c
     p.b_t = 1;
     p.epi.c = dx;
     p.epi.ldc = d;
-    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+    // few row tiles (short T): split the reduction in the workspace, as the weight gradients do
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
   }
   {
     // dW_ug[ilv(c), :] = sum_t dUG[t, c] x[t, :]
@@ -534,7 +535,8 @@ int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const in
     p.b_t = 1;
     p.epi.c = dx;
     p.epi.ldc = d;
-    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+    // few row tiles (short T): split the reduction in the workspace, as dW does after it
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
   }
   {
     // dW[c, :] = sum_t dqkv[t, c] x[t, :]

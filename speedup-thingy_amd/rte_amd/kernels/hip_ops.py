@@ -52,6 +52,12 @@ def _gemm_ws(M: int, N: int, K: int, device) -> tuple[int, int]:
     return workspace(_lib.load().rte_gemm_workspace_bytes(M, N, K), device)
 
 
+def _gemm_ws_max(device, *shapes) -> tuple[int, int]:
+    """One split-K workspace for several GEMMs run in turn on one stream."""
+    lib = _lib.load()
+    return workspace(max(lib.rte_gemm_workspace_bytes(M, N, K) for M, N, K in shapes), device)
+
+
 _BF16_CACHE: dict = {}
 _BF16_CACHE_ON = [False]
 
@@ -305,7 +311,7 @@ class QKVRopeFn(torch.autograd.Function):
         dqkv = torch.empty((B * S, 3 * d), dtype=BF16, device=xb.device)
         dx = torch.empty((B * S, d), dtype=BF16, device=xb.device)
         dw = torch.empty((3 * d, d), dtype=F32, device=xb.device)
-        wsp, wsn = _gemm_ws(3 * d, d, B * S, xb.device)
+        wsp, wsn = _gemm_ws_max(xb.device, (3 * d, d, B * S), (B * S, d, 3 * d))
         call("rte_qkv_rope_bwd", ptr(grads[0]), strides[0].data_ptr(), ptr(grads[1]), strides[1].data_ptr(),
              ptr(grads[2]), strides[2].data_ptr(), ptr(xb), ptr(wb), ptr(cos), ptr(sin), B, S, H, hd,
              ptr(dqkv), ptr(dx), ptr(dw), wsp, wsn, _s())
@@ -450,7 +456,7 @@ class DenseSwiGLUFn(torch.autograd.Function):
         dx = torch.empty((T, d), dtype=BF16, device=xb.device)
         dwug = torch.empty((2 * F, d), dtype=F32, device=xb.device)
         dwd = torch.empty(wdb.shape, dtype=F32, device=xb.device)
-        wsp, wsn = _gemm_ws(2 * F, d, T, xb.device)
+        wsp, wsn = _gemm_ws_max(xb.device, (2 * F, d, T), (T, d, 2 * F), (d, F, T))
         call("rte_dense_swiglu_bwd", ptr(db), ptr(xb), T, d, F, ptr(wugb), ptr(wdb), int(wd_rows), ptr(ug), ptr(z),
              ptr(dug), ptr(dx), ptr(dwug), ptr(dwd), wsp, wsn, _s())
         dres = dout if has_resid else None
