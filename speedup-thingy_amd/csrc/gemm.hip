@@ -479,7 +479,13 @@ __global__ void __launch_bounds__(256, (wg_per_cu<BM, BN, BK, DLS, WM>())) gemm_
         int base = 0;
         for (int c0 = 0; c0 < p.G; c0 += 64) {
           const int gg = c0 + tid;
-          const int cnt = gg < p.G ? (p.goff[gg + 1] - p.goff[gg] + p.gk_chunk - 1) / p.gk_chunk : 0;
+          // an empty group still takes one work item: its empty k range stores the epilogue of
+          // a zero sum, so every group's output is written by this kernel
+          int cnt = 0;
+          if (gg < p.G) {
+            cnt = (p.goff[gg + 1] - p.goff[gg] + p.gk_chunk - 1) / p.gk_chunk;
+            if (cnt < 1) cnt = 1;
+          }
           int incl = cnt;
 #pragma unroll
           for (int off = 1; off < 64; off <<= 1) {

@@ -90,8 +90,9 @@ struct GemmArgs {
   int a_koff2 = 0;
   // GROUP_K with chunked groups (set by gemm_launch when a workspace is given): group g's k
   // range is cut into chunks of gk_chunk; work item i (grid z) is chunk i - gk_first[g] of the
-  // group g with gk_first[g] <= i < gk_first[g + 1].  A group of one chunk stores directly;
-  // larger groups store fp32 partials [item, M, N] that a second kernel adds in chunk order.
+  // group g with gk_first[g] <= i < gk_first[g + 1] (an empty group has one, with an empty
+  // k range).  A group of one chunk stores directly; larger groups store fp32 partials
+  // [item, M, N] that a second kernel adds in chunk order.
   int gk_chunk = 0;
   const int32_t* gk_first = nullptr;  // [G + 1]
   float* gk_part = nullptr;

@@ -395,42 +395,92 @@ __global__ void __launch_bounds__(64) route_topk_lanes_kernel(const float* __res
 // pairs: clusters in order, inside a cluster ascending token (sample, then position).
 // Plan (one workgroup): per-cluster sample counts, offsets, and for each (b, j) the number of
 // earlier samples routed to the same cluster; then one thread per pair writes its slot.
+// With `fast` (the host checked that the tables fit in LDS) the plan keeps each sample's
+// recipe (-1: routes nowhere) and an inverse table inv[r][c] = the j with routes[r][j] == c in
+// LDS, so the counts run over all (b, j) at once and each cluster's ranks over the samples
+// alone; a recipe that lists a cluster twice drops back to the (b, j) scan of the general
+// plan.
 __global__ void __launch_bounds__(256) pack_routes_plan_kernel(const int64_t* __restrict__ rid,
                                                                const uint8_t* __restrict__ active, int B, int S,
                                                                const int32_t* __restrict__ routes, int R, int kmax,
                                                                int C, int32_t* __restrict__ offsets,
-                                                               int32_t* __restrict__ base) {
-  extern __shared__ int32_t cnt[];  // [C]
-  const int tid = threadIdx.x;
+                                                               int32_t* __restrict__ base, int fast) {
+  extern __shared__ int32_t sh[];  // cnt [C]; fast: inv [R * C], recipe [B]
+  __shared__ int dup;
+  int32_t* cnt = sh;
+  int32_t* inv = sh + C;
+  int32_t* rec = inv + (fast ? R * C : 0);
+  const int tid = threadIdx.x, lane = tid & 63;
+  auto recipe_of = [&](int b) -> int {  // recipe of sample b, -1 when it routes nowhere
+    const int64_t r = rid[b];
+    return ((active && !active[b]) || r < 0 || r >= R) ? -1 : (int)r;
+  };
   for (int c = tid; c < C; c += 256) cnt[c] = 0;
+  if (fast) {
+    for (int i = tid; i < R * C; i += 256) inv[i] = -1;
+    for (int b = tid; b < B; b += 256) rec[b] = recipe_of(b);
+    if (tid == 0) dup = 0;
+  }
   __syncthreads();
-  for (int b = tid; b < B; b += 256) {
-    if ((active && !active[b]) || rid[b] < 0 || rid[b] >= R) continue;
-    const int32_t* rr = routes + rid[b] * kmax;
-    for (int j = 0; j < kmax; ++j) {
-      const int c = rr[j];
+  if (fast) {
+    for (int i = tid; i < R * kmax; i += 256) {
+      const int r = i / kmax, c = routes[i];
+      if (c >= 0 && c < C && atomicExch(&inv[r * C + c], i - r * kmax) != -1) dup = 1;
+    }
+    for (int i = tid; i < B * kmax; i += 256) {
+      const int b = i / kmax, r = rec[b];
+      if (r < 0) continue;
+      const int c = routes[r * kmax + (i - b * kmax)];
       if (c >= 0 && c < C) atomicAdd(&cnt[c], 1);  // integer counts: order-independent
     }
-  }
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int c = 0; c < C; ++c) {
-      const int v = cnt[c];
-      cnt[c] = run;
-      offsets[c] = run * S;
-      run += v;
+  } else {
+    for (int b = tid; b < B; b += 256) {
+      const int r = recipe_of(b);
+      if (r < 0) continue;
+      const int32_t* rr = routes + (int64_t)r * kmax;
+      for (int j = 0; j < kmax; ++j) {
+        const int c = rr[j];
+        if (c >= 0 && c < C) atomicAdd(&cnt[c], 1);
+      }
     }
-    offsets[C] = run * S;
   }
   __syncthreads();
-  for (int c = tid; c < C; c += 256) {  // samples in order: rank among the cluster's samples
-    int r = 0;
-    for (int b = 0; b < B; ++b) {
-      if ((active && !active[b]) || rid[b] < 0 || rid[b] >= R) continue;
-      const int32_t* rr = routes + rid[b] * kmax;
-      for (int j = 0; j < kmax; ++j)
-        if (rr[j] == c) base[b * kmax + j] = r++;
+  if (tid < 64) {  // exclusive prefix over the clusters, 64 at a time
+    int carry = 0;
+    for (int c0 = 0; c0 < C; c0 += 64) {
+      const int c = c0 + lane;
+      const int v = c < C ? cnt[c] : 0;
+      int incl = v;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(incl, off, 64);
+        if (lane >= off) incl += y;
+      }
+      if (c < C) offsets[c] = (carry + incl - v) * S;
+      carry += __shfl(incl, 63, 64);
+    }
+    if (lane == 0) offsets[C] = carry * S;
+  }
+  if (fast && !dup) {  // dup was settled before the barrier above
+    for (int c = tid; c < C; c += 256) {  // samples in order: rank among the cluster's samples
+      int r = 0;
+      for (int b = 0; b < B; ++b) {
+        const int rc = rec[b];
+        if (rc < 0) continue;
+        const int j = inv[rc * C + c];
+        if (j >= 0) base[b * kmax + j] = r++;
+      }
+    }
+  } else {
+    for (int c = tid; c < C; c += 256) {
+      int r = 0;
+      for (int b = 0; b < B; ++b) {
+        const int rc = recipe_of(b);
+        if (rc < 0) continue;
+        const int32_t* rr = routes + (int64_t)rc * kmax;
+        for (int j = 0; j < kmax; ++j)
+          if (rr[j] == c) base[b * kmax + j] = r++;
+      }
     }
   }
 }
@@ -669,8 +719,10 @@ int pack_routes(const int64_t* rid, const uint8_t* active, int B, int S, const i
   RTE_REQUIRE(ws && ws_bytes >= pack_routes_workspace_bytes(B, kmax), "pack_routes: workspace too small");
   if (B == 0) return fill_i32(offsets, 0, C + 1, s);
   int32_t* base = static_cast<int32_t*>(ws);
-  hipLaunchKernelGGL(pack_routes_plan_kernel, dim3(1), dim3(256), (size_t)C * sizeof(int32_t), s, rid, active, B, S,
-                     routes, R, kmax, C, offsets, base);
+  const size_t fast_lds = ((size_t)C + (size_t)R * C + (size_t)B) * sizeof(int32_t);
+  const int fast = fast_lds <= 65536 ? 1 : 0;
+  hipLaunchKernelGGL(pack_routes_plan_kernel, dim3(1), dim3(256), fast ? fast_lds : (size_t)C * sizeof(int32_t), s,
+                     rid, active, B, S, routes, R, kmax, C, offsets, base, fast);
   RTE_TRY(check_launch("pack_routes_plan"));
   const int P = B * S * kmax;
   hipLaunchKernelGGL(pack_routes_write_kernel, dim3((P + 255) / 256), dim3(256), 0, s, rid, active, B, S, routes, R,

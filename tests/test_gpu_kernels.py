@@ -229,10 +229,12 @@ def test_route_topk_kernels_agree(C, k):
     assert torch.equal(ids_l[:8000], ids_w) and torch.equal(w_l[:8000], w_w)
 
 
-@pytest.mark.parametrize("B,S,R,kmax,C", [(1, 64, 6, 8, 64), (128, 64, 16, 8, 64), (37, 5, 9, 4, 300)])
+@pytest.mark.parametrize("B,S,R,kmax,C", [(1, 64, 6, 8, 64), (128, 64, 16, 8, 64), (37, 5, 9, 4, 300),
+                                          (1, 64, 16, 64, 64), (64, 8, 60, 8, 300)])
 def test_pack_routes_matches_expanded_pack(B, S, R, kmax, C):
     """Route-list pack from recipe ids equals the counting-sort pack of the expanded per-token
-    routes (every field bit-exact), with -1 padding, inactive samples and an unknown recipe id."""
+    routes (every field bit-exact), with -1 padding, inactive samples and an unknown recipe id.
+    The last case's recipe table is too large for the plan's LDS tables (the scanning plan)."""
     H = _ops()
     rng = np.random.default_rng(B + R + C)
     routes = np.full((R, kmax), -1, np.int32)
