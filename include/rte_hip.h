@@ -398,6 +398,16 @@ int rte_shortlist_bwd(const float* dloss, const float* dlogits, const void* hidd
 /* fp32 -> bf16 (round to nearest even) */
 int rte_cast_f32_bf16(const float* x, int64_t n, void* y, void* stream);
 
+/* Several fp32 -> bf16 casts in one launch: a training step's bf16 weight copies (the
+ * per-step cast of every nn.Linear / bank weight behind the autocast matmuls of
+ * rte/layers.py:53-87, 659-779).  jobs (device, int64 [njobs, 8]): {src, dst, rows, cols, ld,
+ * kind, first_blk, 0}; dst contiguous bf16 [rows, cols]; kind 0: src the same matrix
+ * contiguous; kind 1: src column by column, (r, c) at src[c * ld + r] (a transposed view).
+ * Job j owns workgroups first_blk .. first_blk + rte_cast_many_blocks(kind, rows, cols) - 1;
+ * blk (device, int32 [nblk]) holds each workgroup's job.  Bit-identical to rte_cast_f32_bf16. */
+int rte_cast_many_blocks(int kind, int64_t rows, int64_t cols);
+int rte_cast_many(const int64_t* jobs, const int32_t* blk, int nblk, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -28,6 +28,8 @@ int rope_bwd_pack(const bf16* dq, const int64_t* sq, const bf16* dk, const int64
                   const int64_t* sv, const float* cos_t, const float* sin_t, int B, int H, int S, int hd,
                   bf16* dqkv, hipStream_t s);
 int cast_f32_bf16(const float* x, int64_t n, bf16* y, hipStream_t s);
+int cast_many_blocks(int kind, int64_t rows, int64_t cols);
+int cast_many(const int64_t* jobs, const int32_t* blk, int nblk, hipStream_t s);
 int ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, float* loss, float* lse,
            hipStream_t s);
 int ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse, const float* g,
@@ -896,6 +898,16 @@ int rte_audit_correct_bwd(const float* g, int B, int seq, const int64_t* idx, in
 
 int rte_cast_f32_bf16(const float* x, int64_t n, void* y, void* stream) {
   return cast_f32_bf16(x, n, B16(y), S(stream));
+}
+
+int rte_cast_many_blocks(int kind, int64_t rows, int64_t cols) {
+  if (kind != 0 && kind != 1) return -1;
+  return cast_many_blocks(kind, rows, cols);
+}
+
+int rte_cast_many(const int64_t* jobs, const int32_t* blk, int nblk, void* stream) {
+  RTE_REQUIRE(nblk >= 0 && (nblk == 0 || (jobs && blk)), "cast_many: bad tables");
+  return cast_many(jobs, blk, nblk, S(stream));
 }
 
 int rte_shortlist_build(const int64_t* targets, const int32_t* top_clusters, int tc, const int64_t* members,

@@ -252,7 +252,66 @@ __global__ void __launch_bounds__(256) cast_f32_bf16_kernel(const float* __restr
   }
 }
 
+// Several fp32 -> bf16 casts in one launch.  Job row (int64 x 8): {src, dst, rows, cols, ld,
+// kind, first_blk, 0}; dst is a contiguous [rows, cols] bf16 matrix.  kind 0: src is the same
+// matrix contiguous, cast in runs of kCastRun elements per workgroup; kind 1: src holds the
+// matrix column by column (element (r, c) at src[c * ld + r], a transposed view), cast in
+// 64 x 64 tiles staged through LDS so reads and writes both run along memory.  blk[b] is the
+// job of workgroup b.  Rounding as cast_f32_bf16_kernel (nearest even, the same conversion).
+constexpr int kCastRun = 4096;
+
+__global__ void __launch_bounds__(256) cast_many_kernel(const int64_t* __restrict__ jobs,
+                                                        const int32_t* __restrict__ blk) {
+  __shared__ float tile[64][65];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int64_t* jr = jobs + 8 * blk[b];
+  const float* src = reinterpret_cast<const float*>(jr[0]);
+  bf16* dst = reinterpret_cast<bf16*>(jr[1]);
+  const int64_t rows = jr[2], cols = jr[3], ld = jr[4];
+  const int64_t t = b - jr[6];
+  if (jr[5] == 0) {
+    const int64_t n = rows * cols;
+    const int64_t i0 = t * kCastRun, i1 = i0 + kCastRun < n ? i0 + kCastRun : n;
+    const bool vec = ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) & 15) == 0;
+    for (int64_t i = i0 + 4 * tid; i < i1; i += 4 * 256) {
+      if (vec && i + 4 <= i1) {
+        const float4 v = *reinterpret_cast<const float4*>(src + i);
+        uint2 o;
+        o.x = pack_bf2(v.x, v.y);
+        o.y = pack_bf2(v.z, v.w);
+        *reinterpret_cast<uint2*>(dst + i) = o;
+      } else {
+        for (int64_t j = i; j < i + 4 && j < i1; ++j) dst[j] = f2bf(src[j]);
+      }
+    }
+  } else {
+    const int64_t tiles_c = (cols + 63) / 64;
+    const int64_t r0 = (t / tiles_c) * 64, c0 = (t % tiles_c) * 64;
+    for (int e = tid; e < 64 * 64; e += 256) {  // read along r (contiguous in src)
+      const int r = e & 63, c = e >> 6;
+      if (r0 + r < rows && c0 + c < cols) tile[c][r] = src[(c0 + c) * ld + r0 + r];
+    }
+    __syncthreads();
+    for (int e = tid; e < 64 * 64; e += 256) {  // write along c (contiguous in dst)
+      const int c = e & 63, r = e >> 6;
+      if (r0 + r < rows && c0 + c < cols) dst[(r0 + r) * cols + c0 + c] = f2bf(tile[c][r]);
+    }
+  }
+}
+
 }  // namespace
+
+int cast_many_blocks(int kind, int64_t rows, int64_t cols) {
+  if (rows <= 0 || cols <= 0) return 0;
+  if (kind == 0) return (int)((rows * cols + kCastRun - 1) / kCastRun);
+  return (int)(((rows + 63) / 64) * ((cols + 63) / 64));
+}
+
+int cast_many(const int64_t* jobs, const int32_t* blk, int nblk, hipStream_t s) {
+  if (nblk <= 0) return 0;
+  hipLaunchKernelGGL(cast_many_kernel, dim3((unsigned)nblk), dim3(256), 0, s, jobs, blk);
+  return check_launch("cast_many");
+}
 
 int fill_i32(int32_t* p, int32_t value, int64_t n, hipStream_t s) {
   if (n <= 0) return 0;

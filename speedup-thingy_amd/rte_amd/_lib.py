@@ -87,6 +87,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_audit_correct_fwd": (_I, [_P, _P, _I, _I, _P, _I, _P, _F, _I, _P, _P, _P, _P, _P]),
     "rte_audit_correct_bwd": (_I, [_P, _I, _I, _P, _I, _P, _P, _P, _P]),
     "rte_cast_f32_bf16": (_I, [_P, _I64, _P, _P]),
+    "rte_cast_many_blocks": (_I, [_I, _I64, _I64]),
+    "rte_cast_many": (_I, [_P, _P, _I, _P]),
     "rte_grouped_linear_fwd": (_I, [_P, _I, _I, _P, _I, _I, _P, _P, _P, _I, _P, _I, _P]),
     "rte_grouped_linear_bwd": (_I, [_P, _P, _I, _I, _P, _I, _I, _P, _P, _P, _I, _P, _I, _P, _P, _SZ, _P]),
     "rte_grouped_linear_bwd_workspace_bytes": (_SZ, [_I, _I, _I, _I]),

@@ -76,6 +76,93 @@ def bf16_cache_end() -> None:
     _BF16_CACHE_ON[0] = False
 
 
+_BF16_REC: list = [None]  # Bf16Prefetch recording the step's parameter casts
+
+
+class Bf16Prefetch:
+    """A training step's bf16 weight copies in one launch (rte_cast_many) instead of one cast
+    per weight at first use.  The first step (eager) runs with the per-use casts and records
+    which parameter views they cast on which stream; every later step makes all of them at
+    begin(), into buffers kept for the session, and files them in the per-step cache under
+    the keys the uses look up.  Views other than contiguous ones and 2-D transposes are left to
+    the per-use path.  Use begin() / end() in place of bf16_cache_begin / bf16_cache_end."""
+
+    def __init__(self, enabled: bool = True):
+        self.enabled = enabled
+        self.entries = None   # [(param, shape, stride, offset, stream or None = the step's stream)]
+        self.tables = None
+
+    def begin(self) -> None:
+        bf16_cache_begin()
+        _BF16_REC[0] = None
+        if not self.enabled:
+            return
+        if self.entries is None:
+            self._main = _lib.stream_ptr()
+            self._rec = []
+            _BF16_REC[0] = self
+        elif self.entries:
+            self._run()
+
+    def end(self) -> None:
+        if _BF16_REC[0] is self:
+            _BF16_REC[0] = None
+            if not torch.cuda.is_current_stream_capturing():
+                self._build(self._rec)
+            self._rec = []
+        bf16_cache_end()
+
+    def record(self, x: torch.Tensor) -> None:
+        base = x._base if x._base is not None else x
+        st = _lib.stream_ptr()
+        self._rec.append((base, tuple(x.shape), tuple(x.stride()), x.storage_offset(),
+                          None if st == self._main else torch.cuda.current_stream()))
+
+    def _build(self, rec) -> None:
+        seen, jobs, entries, outs = {}, [], [], []
+        nblk = 0
+        lib = _lib.load()
+        for base, shape, stride, off, stream in rec:
+            ident = (id(base), shape, stride, off)
+            if ident not in seen:
+                view = base.as_strided(shape, stride, off)
+                if view.is_contiguous():
+                    kind, rows, cols, ld = 0, 1, view.numel(), 0
+                elif len(shape) == 2 and stride == (1, shape[0]):
+                    kind, rows, cols, ld = 1, shape[0], shape[1], shape[0]
+                else:
+                    continue
+                if view.numel() == 0:
+                    continue
+                dst = torch.empty(shape, dtype=BF16, device=base.device)
+                nb = lib.rte_cast_many_blocks(kind, rows, cols)
+                seen[ident] = len(outs)
+                jobs.append([view.data_ptr(), dst.data_ptr(), rows, cols, ld, kind, nblk, 0])
+                outs.append(dst)
+                nblk += nb
+            entries.append((base, shape, stride, off, stream, seen[ident]))
+        self.entries = entries
+        if not jobs:
+            return
+        dev = outs[0].device
+        blk = torch.cat([torch.full((lib.rte_cast_many_blocks(j[5], j[2], j[3]),), i, dtype=torch.int32)
+                         for i, j in enumerate(jobs)])
+        self.tables = (torch.tensor(jobs, dtype=torch.int64).to(dev), blk.to(dev), nblk, outs,
+                       [(e[0], e[0].data_ptr()) for e in entries])
+
+    def _run(self) -> None:
+        jobs, blk, nblk, outs, ptrs = self.tables
+        if any(b.data_ptr() != pv for b, pv in ptrs):  # parameters moved: record again next step
+            self.entries, self.tables = None, None
+            return
+        call("rte_cast_many", ptr(jobs), ptr(blk), nblk, _s())
+        main = _lib.stream_ptr()
+        for base, shape, stride, off, stream, j in self.entries:
+            view = base.as_strided(shape, stride, off)
+            st = main if stream is None else stream.cuda_stream
+            _BF16_CACHE[(view.data_ptr(), shape, stride, view._version, st)] = outs[j]
+
+
 def _cache_key(x: torch.Tensor):
     """Parameters (and views of them) only; keyed by the current stream as well, so a copy made
     on one stream is never read unsynchronised from another."""
@@ -96,6 +183,8 @@ def cast_bf16(x: torch.Tensor) -> torch.Tensor:
         hit = _BF16_CACHE.get(key)
         if hit is not None:
             return hit
+        if _BF16_REC[0] is not None:
+            _BF16_REC[0].record(x)
     xc = x.contiguous().to(F32)
     y = torch.empty(xc.shape, dtype=BF16, device=xc.device)
     call("rte_cast_f32_bf16", ptr(xc), xc.numel(), ptr(y), _s())

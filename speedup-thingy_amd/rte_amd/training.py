@@ -90,6 +90,7 @@ class TrainEngine:
         self.last_grad_metrics: dict[str, Any] = {}
         # start the audit replay and the consistency loss on side streams right after routing
         self.audit_streams = self.device.type == "cuda"
+        self._bf16 = hip_ops.Bf16Prefetch(enabled=self.device.type == "cuda")
         self._graph_enabled = False
         self._graph_keep = False
         self._gstate: dict[str, Any] | None = None
@@ -173,7 +174,7 @@ class TrainEngine:
         if step and tr.grad_clip_norm is not None and not fused:
             params = [p for g in self.optimizer.param_groups for p in g["params"]]
             torch.nn.utils.clip_grad_norm_(params, tr.grad_clip_norm, foreach=True)
-        hip_ops.bf16_cache_end()  # parameters change below
+        self._bf16.end()  # parameters change below
         if step:
             if fused:  # clipping and metrics happen inside the fused step
                 self.optimizer.step()
@@ -189,7 +190,7 @@ class TrainEngine:
         return batch[0].to(self.device, non_blocking=True), batch[1].to(self.device, non_blocking=True)
 
     def train_step(self, batch, *, check_finite: bool = True) -> TrainStepResult:
-        hip_ops.bf16_cache_begin()  # one bf16 copy per weight per step
+        self._bf16.begin()  # one bf16 copy per weight per step
         mode = self.config.training.mode
         if mode == "dense_exact":
             return self._step_dense(batch, check_finite)
@@ -375,7 +376,7 @@ class TrainEngine:
 
     def _graph_body(self, st, shortlist: bool, check_finite: bool):
         """Device work of one captured step; everything here is replayed as recorded."""
-        hip_ops.bf16_cache_begin()
+        self._bf16.begin()
         tr = self.config.training
         m = self.recursive_model
         loss, hot, audit, aux, scale = self._macro_loss(st["tokens"], st["targets"], shortlist=shortlist,
@@ -384,7 +385,7 @@ class TrainEngine:
         bad = (~torch.isfinite(loss.detach())) if check_finite else torch.zeros((), dtype=torch.bool,
                                                                                   device=loss.device)
         loss.backward()
-        hip_ops.bf16_cache_end()  # parameters change below
+        self._bf16.end()  # parameters change below
         if isinstance(self.optimizer, FusedAdamW):
             # clipping, update (skipped on a non-finite loss) and metrics in three launches
             self.optimizer.found_inf = bad.float()

@@ -892,3 +892,39 @@ def test_distill_matches_oracle(A, S, d, V):
     assert_rel(_np(th.grad), dh, FP32_RTOL, "d hot")
     if V:
         assert_rel(_np(tl.grad), dl, FP32_RTOL, "d hot logits")
+
+
+@pytest.mark.parametrize("shape,transposed", [((1536, 512), True), ((300, 77), True), ((64, 1), True),
+                                              ((4096, 512), False), ((7, 13), False), ((1,), False)])
+def test_cast_many_bit_exact(shape, transposed):
+    """One-launch weight casts (contiguous and transposed views, ragged tile edges, an offset
+    view) equal the per-tensor cast bit for bit, with NaN / inf / rounding-tie inputs."""
+    H = _ops()
+    from rte_amd import _lib
+
+    lib = _lib.load()
+    g = torch.Generator().manual_seed(sum(shape))
+    n = int(np.prod(shape))
+    x = torch.randn(n + 3, generator=g)
+    x[:3] = torch.tensor([float("nan"), float("inf"), 1.0 + 2.0 ** -8])  # tie: rounds to even
+    base = x.to(DEV)
+    if transposed:
+        src = base[3:].view(shape[1], shape[0]).t()  # element (r, c) at c * rows + r
+    else:
+        src = base[3:].view(shape)
+    print(f"cast_many shape={shape} transposed={transposed}", flush=True)
+    want = H.cast_bf16(src)
+    rows, cols = (shape[0], shape[1]) if len(shape) == 2 else (1, shape[0])
+    kind = 1 if transposed else 0
+    out = torch.empty(shape, dtype=torch.bfloat16, device=DEV)
+    other = torch.randn(5000, device=DEV)
+    out2 = torch.empty(5000, dtype=torch.bfloat16, device=DEV)
+    nb1 = lib.rte_cast_many_blocks(kind, rows, cols)
+    nb2 = lib.rte_cast_many_blocks(0, 1, 5000)
+    jobs = torch.tensor([[src.data_ptr(), out.data_ptr(), rows, cols, rows if transposed else 0, kind, 0, 0],
+                         [other.data_ptr(), out2.data_ptr(), 1, 5000, 0, 0, nb1, 0]], dtype=torch.int64).to(DEV)
+    blk = torch.tensor([0] * nb1 + [1] * nb2, dtype=torch.int32).to(DEV)
+    H.call("rte_cast_many", jobs.data_ptr(), blk.data_ptr(), nb1 + nb2, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(out2.view(torch.int16), H.cast_bf16(other).view(torch.int16))

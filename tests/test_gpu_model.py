@@ -399,6 +399,25 @@ def test_captured_step_matches_eager(mode):
     assert kinds.get("kernel", 0) > 100
 
 
+def test_bf16_prefetch_matches_per_use_casts():
+    """Engines with and without the one-launch weight cast (recorded on the first step, run
+    from the second) take bit-identical steps: same losses, same parameters."""
+    a = _engine("recursive_macro")
+    b = _engine("recursive_macro")
+    b._bf16.enabled = False
+    g = torch.Generator().manual_seed(5)
+    for step in range(4):
+        tok = torch.randint(0, 256, (4, 17), generator=g)
+        print(f"bf16 prefetch step {step}", flush=True)
+        ra = a.train_step((tok[:, :-1], tok[:, 1:]))
+        rb = b.train_step((tok[:, :-1], tok[:, 1:]))
+        torch.cuda.synchronize()
+        assert float(ra.loss.detach()) == float(rb.loss.detach()), step
+    assert a._bf16.entries and a._bf16.tables is not None
+    for (na, pa), (_, pb) in zip(a.recursive_model.named_parameters(), b.recursive_model.named_parameters()):
+        assert torch.equal(pa, pb), na
+
+
 # ---------------------------------------------------------------- macro operators
 
 def _torch_bounded(h, h0, rid, sid, p, c):
