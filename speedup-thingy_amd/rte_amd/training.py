@@ -190,8 +190,9 @@ class TrainEngine:
         return batch[0].to(self.device, non_blocking=True), batch[1].to(self.device, non_blocking=True)
 
     def train_step(self, batch, *, check_finite: bool = True) -> TrainStepResult:
-        self._bf16.begin()  # one bf16 copy per weight per step
         mode = self.config.training.mode
+        if not (self._graph_enabled and mode in ("recursive_macro", "recursive_macro_shortlist")):
+            self._bf16.begin()  # one bf16 copy per weight per step (the captured body opens its own)
         if mode == "dense_exact":
             return self._step_dense(batch, check_finite)
         if mode == "recursive_exact":
