@@ -285,6 +285,50 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5) -> torch.Tensor
     return RMSNormFn.apply(x, w, eps)
 
 
+class RMSNormResidFn(torch.autograd.Function):
+    """(rmsnorm(x) * w, x): the norm together with its input passed on as the residual branch,
+    so the backward adds the residual's gradient inside the norm-backward kernel (its dres
+    input) instead of autograd adding two [T, d] gradients of x."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, w: torch.Tensor, eps: float):
+        _lib.require_device_tensors("rmsnorm", x, w)
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1]).contiguous().to(F32)
+        w32 = w.contiguous().to(F32)
+        T, d = x2.shape
+        out = torch.empty((T, d), dtype=BF16, device=x.device)
+        rstd = torch.empty((T,), dtype=F32, device=x.device)
+        call("rte_rmsnorm_fwd", ptr(x2), ptr(w32), T, d, float(eps), ptr(out), ptr(rstd), _s())
+        ctx.save_for_backward(x2, w32, rstd)
+        ctx.shape = shape
+        ctx.w_dtype = w.dtype
+        ctx.x_dtype = x.dtype
+        ctx.set_materialize_grads(False)
+        return out.view(*shape[:-1], d), x2.view(shape)
+
+    @staticmethod
+    def backward(ctx, dy: torch.Tensor | None, dres: torch.Tensor | None):
+        x2, w32, rstd = ctx.saved_tensors
+        T, d = x2.shape
+        if dy is None:
+            return (None if dres is None else dres.to(ctx.x_dtype)), None, None
+        dy = dy.reshape(T, d).contiguous().to(BF16)
+        r = None if dres is None else dres.reshape(T, d).contiguous().to(F32)
+        dx = torch.empty((T, d), dtype=F32, device=x2.device)
+        dw = torch.empty((d,), dtype=F32, device=x2.device)
+        nbytes = _lib.load().rte_rmsnorm_bwd_workspace_bytes(T, d)
+        ws = torch.empty((max(1, nbytes // 4),), dtype=F32, device=x2.device)
+        call("rte_rmsnorm_bwd", ptr(dy), ptr(x2), ptr(w32), ptr(rstd), ptr(r), T, d, ptr(dx), ptr(dw), 0,
+             ptr(ws), nbytes, _s())
+        return dx.view(ctx.shape).to(ctx.x_dtype), dw.to(ctx.w_dtype), None
+
+
+def rmsnorm_resid(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5) -> tuple[torch.Tensor, torch.Tensor]:
+    """(bf16 rmsnorm(x) * w, fp32 x for the residual add): one gradient for x."""
+    return RMSNormResidFn.apply(x, w, eps)
+
+
 class AxpyNormFn(torch.autograd.Function):
     """x = a + c * b (c a scalar tensor, None = 1; b optional; samples whose mask is False keep
     their `keep` rows) and, when w is given, n = bf16(rmsnorm(x) * w * (1 + gamma) + beta), in

@@ -137,9 +137,11 @@ class TransformerBlock(nn.Module):
         self.mlp = make_ffn(config)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        x = x.float()
-        u = self.attn(self.norm1(x), resid=x)
-        return self.mlp(self.norm2(u), resid=u)
+        # each norm hands its input on as the residual branch: one gradient per stream tensor
+        n1, x = hip_ops.rmsnorm_resid(x.float(), self.norm1.weight, self.norm1.eps)
+        u = self.attn(n1, resid=x)
+        n2, u = hip_ops.rmsnorm_resid(u, self.norm2.weight, self.norm2.eps)
+        return self.mlp(n2, resid=u)
 
 
 # ----------------------------------------------------------------------------- banked recursive core
