@@ -34,12 +34,31 @@ class RouterOutput:
     recipe_probs_by_pass: torch.Tensor | None = None
     recipe_id_by_pass: torch.Tensor | None = None
 
-    def subset(self, mask: torch.Tensor) -> "RouterOutput":
-        vals = {}
-        for name in self.__dataclass_fields__:
-            v = getattr(self, name)
-            vals[name] = v[mask] if isinstance(v, torch.Tensor) else v
-        return RouterOutput(**vals)
+    def subset(self, mask: torch.Tensor) -> "RouterSubset":
+        """The decisions of rows `mask` (bool mask or indices); each field is indexed when first
+        read, so an exact replay that reads only the recipe ids and depths launches no index
+        kernels for the other fields."""
+        return RouterSubset(self, mask)
+
+
+class RouterSubset:
+    """Rows of a RouterOutput with the same field names, each indexed at its first read."""
+
+    def __init__(self, parent, mask: torch.Tensor):
+        object.__setattr__(self, "_parent", parent)
+        object.__setattr__(self, "_mask", mask)
+
+    def __getattr__(self, name: str):
+        if name.startswith("_"):
+            raise AttributeError(name)
+        v = getattr(self._parent, name)
+        if isinstance(v, torch.Tensor):
+            v = v[self._mask]
+        object.__setattr__(self, name, v)
+        return v
+
+    def subset(self, mask: torch.Tensor) -> "RouterSubset":
+        return RouterSubset(self, mask)
 
 
 def _entropy(p: torch.Tensor) -> torch.Tensor:
