@@ -137,7 +137,7 @@ class RecursiveModel(nn.Module):
             rid = route.recipe_id_by_pass[:, t] if route.recipe_id_by_pass is not None else route.recipe_id
             h = self.core.forward_step(h, h0, rid, active, pass_idx=t, weights=weights)
             if return_states and (t + 1) in self.config.depth_choices:
-                states[t + 1] = h.clone()
+                states[t + 1] = h  # every pass returns a new tensor; nothing writes h in place
         hidden = self._coda_hidden(h)
         logits, lps, tok = head_logits_loss(hidden, self.vocab_weight, targets)
         meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,

@@ -399,6 +399,35 @@ def test_captured_step_matches_eager(mode):
     assert kinds.get("kernel", 0) > 100
 
 
+def test_rmsnorm_resid_matches_separate_residual():
+    """The norm that hands its input on as the residual branch gives the gradients of the plain
+    norm plus a separate residual use (the residual gradient added inside the norm backward)."""
+    from rte_amd.kernels import hip_ops
+
+    g = torch.Generator().manual_seed(4)
+    x0 = torch.randn(3, 37, 256, generator=g).to("cuda")
+    w0 = (1.0 + 0.1 * torch.randn(256, generator=g)).to("cuda")
+    g1 = torch.randn(3, 37, 256, generator=g).to("cuda")
+    g2 = torch.randn(3, 37, 256, generator=g).to("cuda")
+    print("rmsnorm_resid 3x37x256", flush=True)
+    x, w = x0.clone().requires_grad_(), w0.clone().requires_grad_()
+    n, xr = hip_ops.rmsnorm_resid(x, w)
+    ((n.float() * g1).sum() + (xr * g2).sum()).backward()
+    xa, wa = x0.clone().requires_grad_(), w0.clone().requires_grad_()
+    na = hip_ops.rmsnorm(xa, wa)
+    ((na.float() * g1).sum() + (xa * g2).sum()).backward()
+    assert torch.equal(n, na) and torch.equal(xr, x0)
+    assert_rel(x.grad.cpu().numpy(), xa.grad.cpu().numpy(), 1e-6, "dx")
+    assert_rel(w.grad.cpu().numpy(), wa.grad.cpu().numpy(), 1e-6, "dw")
+    # only the norm output used: the residual branch's gradient is absent
+    x, w = x0.clone().requires_grad_(), w0.clone().requires_grad_()
+    n, _ = hip_ops.rmsnorm_resid(x, w)
+    (n.float() * g1).sum().backward()
+    xa, wa = x0.clone().requires_grad_(), w0.clone().requires_grad_()
+    (hip_ops.rmsnorm(xa, wa).float() * g1).sum().backward()
+    assert torch.equal(x.grad, xa.grad) and torch.equal(w.grad, wa.grad)
+
+
 def test_bf16_prefetch_matches_per_use_casts():
     """Engines with and without the one-launch weight cast (recorded on the first step, run
     from the second) take bit-identical steps: same losses, same parameters."""
