@@ -146,15 +146,15 @@ class AuditEngine:
             n = p.numel()
             k = min(int(fixed), n)
             mask = torch.zeros_like(p, dtype=torch.bool)
-            incl = torch.zeros_like(p)
             self.last_sample_mode, self.last_candidate_count, self.last_capped_fraction = "fixed_count", k, 0.0
             if k > 0 and n > 0:
                 if chosen is None:
                     chosen = self.fixed_count_index(n, k, seed, p.device)
                 mask.index_fill_(0, chosen, True)
-                incl.fill_(float(k) / float(n))
+                incl = torch.full_like(p, float(k) / float(n))
             else:
                 chosen = None
+                incl = torch.zeros_like(p)
             return mask, incl, chosen, k
         if chosen is not None:
             raise ValueError("precomputed audit rows need the fixed-count sampler")
@@ -198,12 +198,14 @@ class AuditEngine:
         zero = hot.loss_per_sample.new_zeros(())
         aux = {k: zero for k in ("hid", "cos", "kl", "norm", "cons", "delta_dir", "delta_rms", "endpoint_normed",
                                  "endpoint_raw", "rms_trust")}
+        p_mean = p.mean()
+        mask_f = mask.float()
         metrics: dict[str, torch.Tensor] = {
-            "audit_probability": p.mean(),
+            "audit_probability": p_mean,
             "audit_requested_probability": req.mean(),
-            "audit_rate": mask.float().mean(),
-            "audit_count": mask.float().sum(),
-            "audit_inclusion_prob": p.mean(),
+            "audit_rate": mask_f.mean(),
+            "audit_count": mask_f.sum(),
+            "audit_inclusion_prob": p_mean,
         }
         if count is not None:  # fixed-count sampler: rows and count known without reading the mask
             idx, has_audit = chosen, count > 0
