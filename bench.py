@@ -145,7 +145,7 @@ def kernel_candidates(B: int, S: int):
         # x@[Wup|Wgate]^T with the SwiGLU epilogue, then zw@Wdown into pair-major rows
         dict(name="grouped_swiglu_fwd", per_step=2, kernels=2, flop=2.0 * P * d * 2 * n + 2.0 * P * n * d,
              bytes=2.0 * T * d + 2.0 * 3 * F * d + 2.0 * P * 3 * n + 2.0 * P * d + 12.0 * P, fn=ffn_fwd),
-        # SURVEY combine unit: T*k*d*b + T*k*4 + T*d*b (bf16 rows in, fp32 rows out here)
+        # combine unit: T*k*d*b + T*k*4 + T*d*b (bf16 rows in, fp32 rows out here)
         dict(name="combine_rows", per_step=2, kernels=1, flop=1.0 * P * d,
              bytes=2.0 * P * d + 4.0 * T * d, fn=combine),
         # route unit: T*C*4 logits in, T*k*(4+4) ids + weights out
