@@ -1048,8 +1048,12 @@ int launch_cfg(const GemmArgs& p0, hipStream_t stream, void* ws, size_t ws_bytes
     // at least 128 k per split
     const int tiles = (int)(grid.x * grid.y);
     p.splits = 1;
+    static const int target = [] {  // RTE_SPLIT_WG: workgroup target of the split, for diagnostics
+      const char* v = getenv("RTE_SPLIT_WG");
+      return v && *v && atoi(v) >= 64 ? atoi(v) : 512;
+    }();
     if (EPI == EPI_STORE && ws && tiles < 256 && p.K >= 256) {
-      int splits = (512 + tiles - 1) / tiles;
+      int splits = (target + tiles - 1) / tiles;
       const int max_by_k = p.K / 128;
       if (splits > max_by_k) splits = max_by_k;
       if (splits > kMaxSplits) splits = kMaxSplits;
