@@ -210,6 +210,8 @@ class BankedAttention(nn.Module):
     def bank_weights(self):
         """Per-bank (Wqkv^T, Wo^T) views, split once per forward: every recursive pass then shares
         one gradient stack per parameter instead of a zero-fill and copy per use."""
+        if self.wqkv.shape[0] == 1:  # one bank: plain views (no gradient stack)
+            return (self.wqkv.squeeze(0).t(),), (self.wo.squeeze(0).t(),)
         return tuple(w.t() for w in self.wqkv.unbind(0)), tuple(w.t() for w in self.wo.unbind(0))
 
     def forward_scaled(self, x: torch.Tensor, head_scale: torch.Tensor, banks=None) -> torch.Tensor:
