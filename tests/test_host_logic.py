@@ -182,3 +182,40 @@ def test_staged_reductions_equal_torch_losses():
     assert torch.allclose(got, want, rtol=1e-12, atol=1e-12)
     a, b = torch.randn(6, 7, 9, dtype=torch.float64), torch.randn(6, 7, 9, dtype=torch.float64)
     assert torch.allclose((a - b).square().mean(dim=-1).mean(dim=-1).mean(), torch.nn.functional.mse_loss(a, b))
+
+
+def test_router_subset_indexes_each_field_on_first_read():
+    """The audited rows' routing decisions equal direct indexing of every field, and a field
+    that is never read is never indexed (nested subsets compose)."""
+    from rte_amd.config import ModelConfig
+    from rte_amd.routing import Router
+
+    cfg = ModelConfig(**_model(d_model=32, n_heads=4, d_ff=64))
+    torch.manual_seed(0)
+    route = Router(cfg)(torch.randn(6, 5, 32))
+    idx = torch.tensor([4, 1, 3])
+    sub = route.subset(idx)
+    assert "recipe_probs" not in vars(sub)
+    for name in route.__dataclass_fields__:
+        v = getattr(route, name)
+        got = getattr(sub, name)
+        if isinstance(v, torch.Tensor):
+            assert torch.equal(got, v[idx]), name
+        else:
+            assert got == v, name
+    assert "recipe_probs" in vars(sub)
+    mask = torch.tensor([True, False, True])
+    assert torch.equal(sub.subset(mask).depth, route.depth[idx][mask])
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N with N > 1 prints a message and exits nonzero (one GPU per box)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       cwd=root, timeout=300)
+    assert r.returncode != 0
+    assert "one GPU" in r.stdout
