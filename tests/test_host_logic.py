@@ -219,3 +219,31 @@ def test_bench_refuses_more_than_one_gpu():
                        cwd=root, timeout=300)
     assert r.returncode != 0
     assert "one GPU" in r.stdout
+
+
+def test_bf16_prefetch_tables():
+    """The one-launch weight-cast plan: contiguous views cast flat, 2-D transposed views by
+    tiles, other strides left to the per-use cast; repeated views share one job and buffer."""
+    from rte_amd import _lib
+    from rte_amd.kernels import hip_ops
+
+    lib = _lib.load()
+    w = torch.nn.Parameter(torch.randn(2, 48, 80))
+    v = torch.nn.Parameter(torch.randn(1000))
+    t = w[1].t()                 # [80, 48], stride (1, 80): transposed view
+    odd = v[::2]                 # stride 2: not planned
+    rec = [(w, tuple(w.shape), tuple(w.stride()), 0, None),
+           (w, tuple(t.shape), tuple(t.stride()), t.storage_offset(), None),
+           (v, tuple(odd.shape), tuple(odd.stride()), 0, None),
+           (w, tuple(t.shape), tuple(t.stride()), t.storage_offset(), "side")]
+    plan = hip_ops.Bf16Prefetch(enabled=False)
+    plan._build(rec)
+    jobs, blk, nblk, outs, _ = plan.tables
+    jobs = jobs.tolist()
+    assert len(jobs) == 2 and len(outs) == 2 and len(plan.entries) == 3
+    assert jobs[0][2:7] == [1, w.numel(), 0, 0, 0]
+    assert jobs[1][2:7] == [80, 48, 80, 1, lib.rte_cast_many_blocks(0, 1, w.numel())]
+    assert jobs[1][0] == t.data_ptr() and tuple(outs[1].shape) == (80, 48)
+    assert nblk == lib.rte_cast_many_blocks(0, 1, w.numel()) + lib.rte_cast_many_blocks(1, 80, 48)
+    assert blk.tolist() == [0] * jobs[1][6] + [1] * (nblk - jobs[1][6])
+    assert plan.entries[1][5] == plan.entries[2][5] == 1  # same view on two streams: one buffer
