@@ -155,7 +155,8 @@ int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, c
 int rte_qkv_rope_fwd(const void* x, const void* wqkv, const float* cos_t, const float* sin_t, int B, int S,
                      int H, int hd, void* q, void* k, void* v, void* stream);
 /* dq/dk/dv: [B,H,S,hd] bf16 with element strides s*[4] (innermost must be 1).
- * dqkv: [B*S, 3d] bf16 workspace; dx [B*S, d] bf16; dw [3d, d] f32 (overwritten).
+ * dqkv: [B*S, 3d] bf16 workspace (dq = NULL: dqkv is the input, already packed and rotated back
+ * by rte_attention_bwd_qkv); dx [B*S, d] bf16; dw [3d, d] f32 (overwritten).
  * workspace: split-K partials of dx and dw, max of rte_gemm_workspace_bytes(B*S, d, 3d) and
  * (3d, d, B*S) bytes (fewer bytes: fewer splits). */
 int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const int64_t* sk, const void* dv,
@@ -176,6 +177,14 @@ int rte_attention_fwd(const void* q, const void* k, const void* v, int B, int H,
 int rte_attention_bwd(const void* q, const void* k, const void* v, const void* out, const void* dout,
                       const float* lse, int B, int H, int seq, int head_dim, float scale, const float* head_scale,
                       void* dq, void* dk, void* dv, void* stream);
+/* The same backward writing the fused QKV projection's input gradient directly: dqkv bf16
+ * [B*seq, 3 H hd] rows [dq | dk | dv] with dq and dk rotated back by the RoPE angle of their
+ * position (cos / sin f32 [seq, hd] as in rte_qkv_rope_fwd), bit-identical to rte_attention_bwd
+ * followed by the packing step of rte_qkv_rope_bwd; pass dqkv to rte_qkv_rope_bwd with dq,
+ * dk, dv = NULL. */
+int rte_attention_bwd_qkv(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                          const float* lse, int B, int H, int seq, int head_dim, float scale,
+                          const float* head_scale, const float* cos_t, const float* sin_t, void* dqkv, void* stream);
 
 /* ---- SVD low-rank SwiGLU FFN (rte/layers.py:342-643 SVDFactorSparseFFN factors
  *      up_a = U S, up_b = V^T from refresh_svd :437-444) ----

@@ -117,6 +117,38 @@ __device__ __forceinline__ void store_block(bf16* blk, int lane, const u32x4_v (
 
 // Lane l holds row (its query or key) l % 32 and, in block db, columns 32 db + 8 j + 4 (l / 32)
 // + {0..3} of acc[db][4 j .. 4 j + 3]: written as 8-byte runs, times f.
+// Backward outputs: row (b, h, s) of dq / dk / dv starts at p + b sb + h sh + s ss (the same
+// strides for the three).  cs / sn (cos, sin [S, HD], optional): dq and dk rows leave rotated
+// back by their position's RoPE angle, exactly as rope_bwd_pack does it (bf16 value first,
+// then the rotation in fp32 with the same fma order), so the QKV backward reads them directly.
+struct BwdOut {
+  bf16 *dq, *dk, *dv;
+  int64_t sb, sh, ss;
+  const float *cs, *sn;
+};
+
+template <int NB>
+__device__ __forceinline__ void store_rows_rot(bf16* row, const f32x16_v (&acc)[NB], float f, int hf,
+                                               const float* cs, const float* sn) {
+#pragma unroll
+  for (int db = 0; db < NB; ++db)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int col = 32 * db + 8 * j + 4 * hf;
+      float y[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) y[i] = bf2f(f2bf(acc[db][4 * j + i] * f));
+      const float4 c = *reinterpret_cast<const float4*>(cs + col);
+      const float4 sv = *reinterpret_cast<const float4*>(sn + col);
+      const float r0 = fmaf(y[0], c.x, y[1] * sv.y), r1 = fmaf(y[1], c.y, -(y[0] * sv.x));
+      const float r2 = fmaf(y[2], c.z, y[3] * sv.w), r3 = fmaf(y[3], c.w, -(y[2] * sv.z));
+      uint2 w;
+      w.x = pack_bf2(r0, r1);
+      w.y = pack_bf2(r2, r3);
+      *reinterpret_cast<uint2*>(row + col) = w;
+    }
+}
+
 template <int NB>
 __device__ __forceinline__ void store_rows(bf16* row, const f32x16_v (&acc)[NB], float f, int hf) {
 #pragma unroll
@@ -223,7 +255,7 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_kernel(const bf16* __restrict
                                                           const bf16* __restrict__ dout,
                                                           const float* __restrict__ lse, int BH, int H, int S,
                                                           float c2, float scale, const float* __restrict__ hscale,
-                                                          bf16* __restrict__ dq) {
+                                                          BwdOut o) {
   constexpr int KS = HD / 16, NB = HD / 32, P = pitch<HD>();
   __shared__ __align__(16) bf16 ksm[4][32 * P];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l32 = lane & 31, hf = lane >> 5;
@@ -294,7 +326,11 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_kernel(const bf16* __restrict
         acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(tr_frag<HD>(blk, 16 * t + 4 * hf, 32 * db + 16 * g1, lane),
                                                           db8[t], acc[db], 0, 0, 0);
   }
-  if (qi < S) store_rows(dq + base + (int64_t)qi * HD, acc, scale, hf);
+  if (qi < S) {
+    bf16* row = o.dq + b * o.sb + h * o.sh + qi * o.ss;
+    if (o.cs) store_rows_rot(row, acc, scale, hf, o.cs + (int64_t)qi * HD, o.sn + (int64_t)qi * HD);
+    else store_rows(row, acc, scale, hf);
+  }
 }
 
 // dK, dV of one 32-key block: loop over the query blocks from the diagonal on.
@@ -305,7 +341,7 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_kernel(const bf16* __restri
                                                             const bf16* __restrict__ dout,
                                                             const float* __restrict__ lse, int BH, int H, int S,
                                                             float c2, float scale, const float* __restrict__ hscale,
-                                                            bf16* __restrict__ dk, bf16* __restrict__ dv) {
+                                                            BwdOut o) {
   constexpr int KS = HD / 16, NB = HD / 32, P = pitch<HD>();
   __shared__ __align__(16) bf16 qsm[4][32 * P];
   __shared__ __align__(16) bf16 dsm[4][32 * P];
@@ -387,8 +423,10 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_kernel(const bf16* __restri
       }
   }
   if (ki < S) {
-    store_rows(dv + base + (int64_t)ki * HD, dva, hs, hf);
-    store_rows(dk + base + (int64_t)ki * HD, dka, scale, hf);
+    const int64_t off = b * o.sb + h * o.sh + ki * o.ss;
+    store_rows(o.dv + off, dva, hs, hf);
+    if (o.cs) store_rows_rot(o.dk + off, dka, scale, hf, o.cs + (int64_t)ki * HD, o.sn + (int64_t)ki * HD);
+    else store_rows(o.dk + off, dka, scale, hf);
   }
 }
 
@@ -413,16 +451,25 @@ void launch_attn_fwd(const bf16* q, const bf16* k, const bf16* v, int BH, int H,
 
 template <int HD>
 int launch_attn_bwd(const bf16* q, const bf16* k, const bf16* v, const bf16* out, const bf16* dout,
-                    const float* lse, int BH, int H, int S, float scale, const float* hscale, bf16* dq, bf16* dk,
-                    bf16* dv, hipStream_t s) {
+                    const float* lse, int BH, int H, int S, float scale, const float* hscale, const BwdOut& o,
+                    hipStream_t s) {
   const int64_t tasks = (int64_t)BH * ((S + 31) / 32);
   const dim3 grid((unsigned)((tasks + 3) / 4));
   hipLaunchKernelGGL(attn_bwd_dkdv_kernel<HD>, grid, dim3(256), 0, s, q, k, v, out, dout, lse, BH, H, S,
-                     scale * kLog2e, scale, hscale, dk, dv);
+                     scale * kLog2e, scale, hscale, o);
   RTE_TRY(check_launch("attention_bwd_dkdv"));
   hipLaunchKernelGGL(attn_bwd_dq_kernel<HD>, grid, dim3(256), 0, s, q, k, v, out, dout, lse, BH, H, S,
-                     scale * kLog2e, scale, hscale, dq);
+                     scale * kLog2e, scale, hscale, o);
   return check_launch("attention_bwd_dq");
+}
+
+int attn_bwd_dispatch(const bf16* q, const bf16* k, const bf16* v, const bf16* out, const bf16* dout,
+                      const float* lse, int B, int H, int S, int head_dim, float scale, const float* hscale,
+                      const BwdOut& o, hipStream_t s) {
+  if (B == 0) return 0;
+  if (head_dim == 32) return launch_attn_bwd<32>(q, k, v, out, dout, lse, B * H, H, S, scale, hscale, o, s);
+  if (head_dim == 64) return launch_attn_bwd<64>(q, k, v, out, dout, lse, B * H, H, S, scale, hscale, o, s);
+  return launch_attn_bwd<128>(q, k, v, out, dout, lse, B * H, H, S, scale, hscale, o, s);
 }
 
 }  // namespace
@@ -444,10 +491,20 @@ int attention_bwd(const bf16* q, const bf16* k, const bf16* v, const bf16* out, 
   ATTN_CHECK("attention_bwd");
   RTE_REQUIRE(al16a(q) && al16a(k) && al16a(v) && al16a(out) && al16a(dout) && al16a(dq) && al16a(dk) && al16a(dv),
               "attention_bwd: 16-byte aligned buffers");
-  if (B == 0) return 0;
-  if (head_dim == 32) return launch_attn_bwd<32>(q, k, v, out, dout, lse, B * H, H, S, scale, hscale, dq, dk, dv, s);
-  if (head_dim == 64) return launch_attn_bwd<64>(q, k, v, out, dout, lse, B * H, H, S, scale, hscale, dq, dk, dv, s);
-  return launch_attn_bwd<128>(q, k, v, out, dout, lse, B * H, H, S, scale, hscale, dq, dk, dv, s);
+  const BwdOut o{dq, dk, dv, (int64_t)H * S * head_dim, (int64_t)S * head_dim, head_dim, nullptr, nullptr};
+  return attn_bwd_dispatch(q, k, v, out, dout, lse, B, H, S, head_dim, scale, hscale, o, s);
+}
+
+int attention_bwd_qkv(const bf16* q, const bf16* k, const bf16* v, const bf16* out, const bf16* dout,
+                      const float* lse, int B, int H, int S, int head_dim, float scale, const float* hscale,
+                      const float* cos_t, const float* sin_t, bf16* dqkv, hipStream_t s) {
+  ATTN_CHECK("attention_bwd_qkv");
+  RTE_REQUIRE(al16a(q) && al16a(k) && al16a(v) && al16a(out) && al16a(dout) && al16a(dqkv) && al16a(cos_t) &&
+                  al16a(sin_t),
+              "attention_bwd_qkv: 16-byte aligned buffers");
+  const int64_t d = (int64_t)H * head_dim;
+  const BwdOut o{dqkv, dqkv + d, dqkv + 2 * d, (int64_t)S * 3 * d, head_dim, 3 * d, cos_t, sin_t};
+  return attn_bwd_dispatch(q, k, v, out, dout, lse, B, H, S, head_dim, scale, hscale, o, s);
 }
 
 }  // namespace rte

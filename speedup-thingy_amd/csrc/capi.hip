@@ -71,6 +71,9 @@ int attention_fwd(const bf16* q, const bf16* k, const bf16* v, int B, int H, int
 int attention_bwd(const bf16* q, const bf16* k, const bf16* v, const bf16* out, const bf16* dout, const float* lse,
                   int B, int H, int S, int head_dim, float scale, const float* hscale, bf16* dq, bf16* dk, bf16* dv,
                   hipStream_t s);
+int attention_bwd_qkv(const bf16* q, const bf16* k, const bf16* v, const bf16* out, const bf16* dout,
+                      const float* lse, int B, int H, int S, int head_dim, float scale, const float* hscale,
+                      const float* cos_t, const float* sin_t, bf16* dqkv, hipStream_t s);
 size_t distill_workspace_bytes(int A, int R);
 int distill_fwd(const float* hot, const float* exact, const float* h0, int A, int S, int d, const float* hot_logits,
                 const float* exact_logits, int V, float t, float eps, const float* weights, float* losses,
@@ -524,8 +527,9 @@ int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const in
                      size_t workspace_bytes, void* stream) {
   const int d = H * hd;
   const int T = B * S_;
-  RTE_TRY(rope_bwd_pack(B16(dq), sq, B16(dk), sk, B16(dv), sv, cos_t, sin_t, B, H, S_, hd, B16(dqkv),
-                        S(stream)));
+  if (dq)  // else dqkv already holds the packed, rotated-back gradient (rte_attention_bwd_qkv)
+    RTE_TRY(rope_bwd_pack(B16(dq), sq, B16(dk), sk, B16(dv), sv, cos_t, sin_t, B, H, S_, hd, B16(dqkv),
+                          S(stream)));
   {
     // dx = dqkv @ Wqkv   (B(n=dcol, k=c) = wqkv[c][dcol] -> layout T)
     GemmArgs p;
@@ -830,6 +834,16 @@ int rte_attention_bwd(const void* q, const void* k, const void* v, const void* o
                        reinterpret_cast<const bf16*>(v), reinterpret_cast<const bf16*>(out),
                        reinterpret_cast<const bf16*>(dout), lse, B, H, seq, head_dim, scale, head_scale, B16(dq),
                        B16(dk), B16(dv), S(stream));
+}
+
+int rte_attention_bwd_qkv(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                          const float* lse, int B, int H, int seq, int head_dim, float scale, const float* head_scale,
+                          const float* cos_t, const float* sin_t, void* dqkv, void* stream) {
+  RTE_REQUIRE(cos_t && sin_t && dqkv, "attention_bwd_qkv: cos, sin and dqkv are required");
+  return attention_bwd_qkv(reinterpret_cast<const bf16*>(q), reinterpret_cast<const bf16*>(k),
+                           reinterpret_cast<const bf16*>(v), reinterpret_cast<const bf16*>(out),
+                           reinterpret_cast<const bf16*>(dout), lse, B, H, seq, head_dim, scale, head_scale, cos_t,
+                           sin_t, B16(dqkv), S(stream));
 }
 
 size_t rte_mse_workspace_bytes(int64_t n) { return mse_workspace_bytes(n); }

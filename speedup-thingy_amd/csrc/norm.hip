@@ -224,9 +224,9 @@ __global__ void __launch_bounds__(256) rope_bwd_pack_kernel(
       const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float ye = y[2 * i], yo = y[2 * i + 1];
-        y[2 * i] = ye * cv[2 * i] + yo * sv[2 * i + 1];
-        y[2 * i + 1] = yo * cv[2 * i + 1] - ye * sv[2 * i];
+        const float ye = y[2 * i], yo = y[2 * i + 1];  // fma order shared with the attention backward
+        y[2 * i] = fmaf(ye, cv[2 * i], yo * sv[2 * i + 1]);
+        y[2 * i + 1] = fmaf(yo, cv[2 * i + 1], -(ye * sv[2 * i]));
       }
     }
     uint4 o;

@@ -76,6 +76,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_macro_table_grad": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
     "rte_attention_fwd": (_I, [_P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P]),
     "rte_attention_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P]),
+    "rte_attention_bwd_qkv": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P]),
     "rte_mse_workspace_bytes": (_SZ, [_I64]),
     "rte_mse_fwd": (_I, [_P, _P, _I64, _P, _P, _SZ, _P]),
     "rte_mse_bwd": (_I, [_P, _P, _I64, _P, _P, _P, _P]),

@@ -550,6 +550,64 @@ def attention(q, k, v, head_scale=None):
     return AttentionFn.apply(q, k, v, head_scale)
 
 
+class QKVRopeAttentionFn(torch.autograd.Function):
+    """attention(qkv_rope(x, w)) as one autograd node: the attention backward writes the QKV
+    projection's input gradient straight in its packed, RoPE-rotated-back layout
+    (rte_attention_bwd_qkv), so the separate packing pass of the QKV backward is skipped.
+    Values and gradients equal QKVRopeFn followed by AttentionFn bit for bit."""
+
+    @staticmethod
+    def forward(ctx, x, w, cos, sin, n_heads: int, head_scale):
+        _lib.require_device_tensors("qkv_rope_attention", x, w, cos, sin, head_scale)
+        B, S, d = x.shape
+        hd = d // n_heads
+        if w.shape != (3 * d, d) or hd not in (32, 64, 128) or hd * n_heads != d:
+            raise ValueError("qkv_rope_attention: wqkv [3d, d] and head_dim 32, 64 or 128 required")
+        xb = x.contiguous().to(BF16)
+        wb = cast_bf16(w)
+        cs = cos[:S].contiguous().to(F32)
+        sn = sin[:S].contiguous().to(F32)
+        q = torch.empty((B, n_heads, S, hd), dtype=BF16, device=x.device)
+        k = torch.empty_like(q)
+        v = torch.empty_like(q)
+        call("rte_qkv_rope_fwd", ptr(xb), ptr(wb), ptr(cs), ptr(sn), B, S, n_heads, hd, ptr(q), ptr(k), ptr(v), _s())
+        hs = None if head_scale is None else head_scale.reshape(B * n_heads).to(F32).contiguous()
+        out = torch.empty((B, S, n_heads, hd), dtype=BF16, device=x.device)
+        lse = torch.empty((B, n_heads, S), dtype=F32, device=x.device)
+        scale = 1.0 / math.sqrt(hd)
+        call("rte_attention_fwd", ptr(q), ptr(k), ptr(v), B, n_heads, S, hd, scale, ptr(hs), ptr(out), ptr(lse),
+             _s())
+        ctx.save_for_backward(xb, wb, cs, sn, q, k, v, out, lse, hs)
+        ctx.meta = (B, S, n_heads, hd, scale, x.dtype, w.dtype)
+        ctx.set_materialize_grads(False)
+        return out.transpose(1, 2)
+
+    @staticmethod
+    def backward(ctx, dout):
+        if dout is None:
+            return (None,) * 6
+        xb, wb, cs, sn, q, k, v, out, lse, hs = ctx.saved_tensors
+        B, S, H, hd, scale, x_dt, w_dt = ctx.meta
+        d = H * hd
+        dtok = dout.transpose(1, 2).to(BF16).contiguous()  # token-major [B, S, H, hd]
+        dqkv = torch.empty((B * S, 3 * d), dtype=BF16, device=xb.device)
+        call("rte_attention_bwd_qkv", ptr(q), ptr(k), ptr(v), ptr(out), ptr(dtok), ptr(lse), B, H, S, hd, scale,
+             ptr(hs), ptr(cs), ptr(sn), ptr(dqkv), _s())
+        dx = torch.empty((B * S, d), dtype=BF16, device=xb.device)
+        dw = torch.empty((3 * d, d), dtype=F32, device=xb.device)
+        wsp, wsn = _gemm_ws_max(xb.device, (3 * d, d, B * S), (B * S, d, 3 * d))
+        call("rte_qkv_rope_bwd", None, None, None, None, None, None, ptr(xb), ptr(wb), ptr(cs), ptr(sn), B, S, H, hd,
+             ptr(dqkv), ptr(dx), ptr(dw), wsp, wsn, _s())
+        return dx.view(B, S, d).to(x_dt), dw.to(w_dt), None, None, None, None
+
+
+def qkv_rope_attention(x, w, cos, sin, n_heads, head_scale=None):
+    """[B, H, S, hd] view of the token-major attention output of x's fused QKV + RoPE."""
+    if head_scale is not None and head_scale.requires_grad:
+        raise ValueError("qkv_rope_attention: head_scale carries no gradient")
+    return QKVRopeAttentionFn.apply(x, w, cos, sin, n_heads, head_scale)
+
+
 # ----------------------------------------------------------------------------- dense SwiGLU
 
 class DenseSwiGLUFn(torch.autograd.Function):

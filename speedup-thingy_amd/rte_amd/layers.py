@@ -78,8 +78,9 @@ class DenseCausalSelfAttention(nn.Module):
         else:
             cos = torch.ones_like(self.wqkv.weight[:1, : self.head_dim].float()).expand(x.shape[1], -1)
             sin = torch.zeros_like(cos)
-        q, k, v = hip_ops.qkv_rope(x, self.wqkv.weight, cos, sin, self.n_heads)
-        y = K.k_flash_causal_dense(q, k, v)
+        # QKV + RoPE + causal attention as one node: its backward hands the QKV GEMMs their
+        # packed, rotated-back input gradient directly (k_flash_causal_dense's math)
+        y = hip_ops.qkv_rope_attention(x, self.wqkv.weight, cos, sin, self.n_heads)
         return hip_ops.attn_out_proj(y, self.wo.weight, resid)
 
 
@@ -221,10 +222,9 @@ class BankedAttention(nn.Module):
         wqkv_t, wo_t = banks if banks is not None else self.bank_weights()
         out = None
         for bank in range(self.config.attn_banks):
-            q, k, v = hip_ops.qkv_rope(x, wqkv_t[bank], cos, sin, H)
             # the recipe's head mask (1/|banks| on its heads, 0 elsewhere: rte/layers.py:702-730 runs
             # only the active heads and averages the banks) scales each head's attention output
-            y = hip_ops.attention(q, k, v, head_scale[:, bank, :])
+            y = hip_ops.qkv_rope_attention(x, wqkv_t[bank], cos, sin, H, head_scale[:, bank, :])
             out = hip_ops.attn_out_proj(y, wo_t[bank], out)
         return out
 

@@ -928,3 +928,31 @@ def test_cast_many_bit_exact(shape, transposed):
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), want.view(torch.int16))
     assert torch.equal(out2.view(torch.int16), H.cast_bf16(other).view(torch.int16))
+
+
+@pytest.mark.parametrize("B,S,H,hd,scaled", [(2, 64, 8, 64, False), (3, 37, 4, 32, True), (1, 100, 2, 128, True)])
+def test_qkv_rope_attention_fused_matches_two_nodes(B, S, H, hd, scaled):
+    """QKV + RoPE + attention as one node (backward writes the packed, rotated-back dqkv in the
+    attention kernels) equals qkv_rope followed by attention, outputs and gradients bit for bit."""
+    H_ = _ops()
+    d = H * hd
+    g = torch.Generator().manual_seed(B * 100 + S)
+    x0 = torch.randn(B, S, d, generator=g).to(DEV)
+    w0 = (torch.randn(3 * d, d, generator=g) / d ** 0.5).to(DEV)
+    pos = torch.arange(S, dtype=torch.float32)[:, None]
+    inv = 10000.0 ** (-torch.arange(0, hd, 2, dtype=torch.float32) / hd)
+    ang = (pos * inv).repeat_interleave(2, dim=1)
+    cos, sin = ang.cos().to(DEV), ang.sin().to(DEV)
+    hs = (torch.rand(B, H, generator=g) * (torch.rand(B, H, generator=g) < 0.7)).to(DEV) if scaled else None
+    gy = torch.randn(B, H, S, hd, generator=g).to(DEV)
+    print(f"qkv_rope_attention B={B} S={S} H={H} hd={hd} scaled={scaled}", flush=True)
+    x1, w1 = x0.clone().requires_grad_(), w0.clone().requires_grad_()
+    y1 = H_.qkv_rope_attention(x1, w1, cos, sin, H, hs)
+    (y1.float() * gy).sum().backward()
+    x2, w2 = x0.clone().requires_grad_(), w0.clone().requires_grad_()
+    q, k, v = H_.qkv_rope(x2, w2, cos, sin, H)
+    y2 = H_.attention(q, k, v, hs)
+    (y2.float() * gy).sum().backward()
+    assert torch.equal(y1, y2)
+    assert torch.equal(x1.grad, x2.grad)
+    assert torch.equal(w1.grad, w2.grad)
