@@ -17,4 +17,16 @@ How each function is pinned (tests/test_oracle.py):
                              k = 1 equals the reference per-cluster loop; finite differences
   attention.rope / rmsnorm   complex-rotation closed form, norm preservation, manual formula
   losses.*                   closed forms; p = 1 correction == exact loss
+  distill.distill            closed forms: hot == exact (all losses 0, cosines / ratios 1);
+                             hot - h0 = 2 (exact - h0) (delta_dir 0, delta_rms (ln 2)^2);
+                             hot = 3 exact (rms_trust (ln 3)^2); smooth-L1 of constant offsets
+                             0.5 / 1 / 2; the two-class KL in closed form at t = 1 and 2
+  distill.distill_grad       torch autograd (fp64) of the reference formulation
+  macro.bounded_apply        hand-worked values: one-hot v / u expose rmsnorm(h)[s, j],
+                             mean_s rmsnorm(h)[j] and h0[s, j] separately on a 2x3x4 input with
+                             round rms values; u = gain = 0 closed form; tanh bound; per-key
+                             locality and permutation equivariance
+  macro.grouped_linear*      explicit loop + torch autograd
+  banked.recipe_templates    two hand-enumerated recipe tables (every recipe's banks and
+                             groups) with zero balance spread; recipe 0 == dense bank
 """

@@ -786,3 +786,180 @@ def test_macro_bounded_and_per_key():
     np.testing.assert_allclose(MO.bounded_apply(h, h0, r, k, other, 0.05), out, rtol=1e-12)
     perm = _rng(73).permutation(h.shape[0])
     np.testing.assert_allclose(MO.bounded_apply(h[perm], h0[perm], r[perm], k[perm], p, 0.05), out[perm], rtol=1e-12)
+
+
+# ---------------------------------------------------------------- pins by closed form / hand values
+
+def _distill_rows(A=2, S=3, d=8, seed=90):
+    rng = _rng(seed)
+    return rng.normal(size=(A, S, d)), rng.normal(size=(A, S, d))
+
+
+def test_distill_closed_form_identical_states():
+    """hot == exact (and equal logits): every loss is 0, cosines 1, norm ratios 1, mse 0."""
+    from oracle import distill as DI
+
+    exact, h0 = _distill_rows()
+    lg = _rng(91).normal(size=(2, 3, 5))
+    loss, met = DI.distill(exact.copy(), exact, h0, lg.copy(), lg)
+    for k in DI.LOSSES:
+        assert abs(loss[k]) < 1e-12, k
+    assert abs(met["hidden_cosine_exact_macro"] - 1.0) < 1e-12
+    assert abs(met["delta_cosine_exact_macro"] - 1.0) < 1e-12
+    assert met["hidden_mse_exact_macro"] == 0.0
+    assert abs(met["macro_exact_norm_ratio"] - 1.0) < 1e-12
+    assert abs(met["delta_rms_ratio"] - 1.0) < 1e-12
+    assert abs(met["logit_kl_exact_macro"]) < 1e-12
+
+
+def test_distill_closed_form_doubled_delta():
+    """hot - h0 = 2 (exact - h0): delta_dir = 0, delta_rms = (ln 2)^2, delta_rms ratio 2."""
+    from oracle import distill as DI
+
+    exact, h0 = _distill_rows(seed=92)
+    hot = h0 + 2.0 * (exact - h0)
+    loss, met = DI.distill(hot, exact, h0)
+    assert abs(loss["delta_dir"]) < 1e-12
+    assert abs(loss["delta_rms"] - np.log(2.0) ** 2) < 1e-12
+    assert abs(met["delta_rms_ratio"] - 2.0) < 1e-12
+    assert abs(met["delta_cosine_exact_macro"] - 1.0) < 1e-12
+    # hot - h0 = -(exact - h0): opposite direction, equal size
+    loss, _ = DI.distill(h0 - (exact - h0), exact, h0)
+    assert abs(loss["delta_dir"] - 2.0) < 1e-12 and abs(loss["delta_rms"]) < 1e-12
+
+
+def test_distill_closed_form_scaled_endpoint():
+    """hot = 3 exact: rms_trust = (ln 3)^2, norm ratio 3, hidden cosine 1, and the
+    rms-normalised endpoint loss vanishes up to the norm's eps."""
+    from oracle import distill as DI
+
+    exact, h0 = _distill_rows(seed=93)
+    loss, met = DI.distill(3.0 * exact, exact, h0)
+    assert abs(loss["rms_trust"] - np.log(3.0) ** 2) < 1e-12
+    assert abs(met["macro_exact_norm_ratio"] - 3.0) < 1e-12
+    assert abs(met["hidden_cosine_exact_macro"] - 1.0) < 1e-12
+    assert loss["endpoint_normed"] < 1e-9
+
+
+@pytest.mark.parametrize("offset,want", [(0.5, 0.125), (-0.5, 0.125), (2.0, 1.5), (-2.0, 1.5), (1.0, 0.5)])
+def test_distill_smooth_l1_constant_offset(offset, want):
+    """smooth_l1 (beta 1) of a constant offset o: o^2 / 2 for |o| < 1, |o| - 1/2 otherwise."""
+    from oracle import distill as DI
+
+    exact, h0 = _distill_rows(seed=94)
+    loss, met = DI.distill(exact + offset, exact, h0)
+    assert abs(loss["endpoint_raw"] - want) < 1e-12
+    assert abs(met["hidden_mse_exact_macro"] - offset * offset) < 1e-12
+
+
+@pytest.mark.parametrize("t", [1.0, 2.0])
+def test_distill_two_class_kl_closed_form(t):
+    """Two classes with logits (0, a) exact and (0, b) hot: per row
+    KL = p ln(p / q) + (1 - p) ln((1 - p) / (1 - q)), p = sigmoid(a / t), q = sigmoid(b / t);
+    batchmean divides the sum over rows by the batch size A, times t^2."""
+    from oracle import distill as DI
+
+    A, S = 2, 3
+    a = np.array([[0.3, -1.2, 2.0], [0.0, 1.5, -0.4]])
+    b = np.array([[1.1, 0.2, -0.7], [0.9, -2.0, 0.4]])
+    el = np.stack([np.zeros_like(a), a], -1)
+    hl = np.stack([np.zeros_like(b), b], -1)
+    exact, h0 = _distill_rows(A, S, 4, seed=95)
+    loss, met = DI.distill(exact, exact, h0, hl, el, t)
+    sig = lambda x: 1.0 / (1.0 + np.exp(-x))  # noqa: E731
+
+    def kl_rows(tt):
+        p, q = sig(a / tt), sig(b / tt)
+        return p * np.log(p / q) + (1 - p) * np.log((1 - p) / (1 - q))
+
+    assert abs(loss["kl"] - kl_rows(t).sum() / A * t * t) < 1e-12
+    assert abs(met["logit_kl_exact_macro"] - kl_rows(1.0).mean()) < 1e-12
+
+
+def test_macro_low_rank_path_hand_values():
+    """One-hot v columns pick single coordinates of each block of
+    z = [rmsnorm(h) | mean_s rmsnorm(h) | h0] and one-hot u rows route them to distinct output
+    coordinates, so with gain = bias = 0 and scale = 1, atanh((Phi(h) - h) / c) exposes
+    silu(rmsnorm(h)[s, 1]), silu(mean_s rmsnorm(h)[0]) and silu(h0[s, 2]).  The expected
+    numbers are worked by hand (rows chosen with round rms values), so pooling h instead of
+    rmsnorm(h), swapping blocks or transposing v / u fails (rte/macro.py:201-236)."""
+    from oracle import macro as MO
+
+    d, c = 4, 0.5
+    h = np.array([[[3, 4, 0, 0], [1, 1, 1, 1], [2, 0, 0, 0]],           # rms 2.5, 1, 1
+                  [[0, 0, 0, -2], [1, -1, 1, -1], [0, 6, 0, 8]]], float)  # rms 1, 1, 5
+    h0 = np.array([[[0.1, 0.2, 0.7, 0.4], [0.5, 0.6, -0.3, 0.8], [0.9, 1.0, 1.1, 1.2]],
+                   [[-0.1, -0.2, 0.25, -0.4], [0.3, 0.1, -1.5, 0.2], [0.0, 0.0, 2.0, 0.0]]])
+    v = np.zeros((1, 1, 3 * d, 3))
+    v[0, 0, 1, 0] = 1.0          # rmsnorm(h)[s, 1]
+    v[0, 0, d + 0, 1] = 1.0      # mean_s rmsnorm(h)[0]
+    v[0, 0, 2 * d + 2, 2] = 1.0  # h0[s, 2]
+    u = np.zeros((1, 1, 3, d))
+    u[0, 0, 0, 3] = u[0, 0, 1, 0] = u[0, 0, 2, 1] = 1.0
+    p = dict(d_gain=np.zeros((1, 1, d)), bias=np.zeros((1, 1, d)), update_scale=np.ones((1, 1, d)), v=v, u=u)
+    zero = np.zeros(2, int)
+    out = MO.bounded_apply(h, h0, zero, zero, p, c)
+    low = np.arctanh((out - h) / c)
+    silu = lambda x: x / (1.0 + np.exp(-np.asarray(x, float)))  # noqa: E731
+    normed_col1 = np.array([[1.6, 1.0, 0.0], [0.0, -1.0, 1.2]])        # h[b, s, 1] / rms
+    pooled_col0 = np.array([(1.2 + 1.0 + 2.0) / 3, (0.0 + 1.0 + 0.0) / 3])
+    np.testing.assert_allclose(low[..., 3], silu(normed_col1), rtol=1e-4, atol=1e-9)
+    np.testing.assert_allclose(low[..., 0], silu(np.repeat(pooled_col0[:, None], 3, 1)), rtol=1e-4)
+    np.testing.assert_allclose(low[..., 1], silu(h0[..., 2]), rtol=1e-9)
+    np.testing.assert_allclose(low[..., 2], 0.0, atol=1e-12)
+    # gain multiplies h itself, bias adds per coordinate, scale multiplies the tanh
+    p2 = dict(p, d_gain=np.full((1, 1, d), 0.25), bias=np.array([[[0.1, -0.2, 0.3, 0.0]]]),
+              update_scale=np.array([[[1.0, 0.5, 2.0, 1.0]]]))
+    out2 = MO.bounded_apply(h, h0, zero, zero, p2, c)
+    arg = np.arctanh((out2 - h) / (c * p2["update_scale"][0, 0]))
+    np.testing.assert_allclose(arg - 0.25 * h - p2["bias"][0, 0], low, rtol=1e-9, atol=1e-9)
+
+
+# Recipe tables enumerated by hand from the template rule of rte/recipes.py:65-100: recipe 0 is
+# dense; sparse recipe idx + 1 takes head slot idx % head_slots, ffn slot idx % ffn_slots,
+# attention bank (idx // head_slots) % attn_banks, ffn bank (idx // ffn_slots) % ffn_banks.
+_RECIPE_TABLES = [
+    (dict(attn_banks=2, ffn_banks=2, head_groups=4, ffn_groups=4, active_head_groups=2, active_ffn_groups=1,
+          recipe_count=9),
+     [((0,), (0,), (0, 1), (0,)), ((0,), (0,), (2, 3), (1,)), ((1,), (0,), (0, 1), (2,)),
+      ((1,), (0,), (2, 3), (3,)), ((0,), (1,), (0, 1), (0,)), ((0,), (1,), (2, 3), (1,)),
+      ((1,), (1,), (0, 1), (2,)), ((1,), (1,), (2, 3), (3,))]),
+    (dict(attn_banks=3, ffn_banks=1, head_groups=4, ffn_groups=6, active_head_groups=1, active_ffn_groups=2,
+          recipe_count=13),
+     [((0,), (0,), (0,), (0, 1)), ((0,), (0,), (1,), (2, 3)), ((0,), (0,), (2,), (4, 5)),
+      ((0,), (0,), (3,), (0, 1)), ((1,), (0,), (0,), (2, 3)), ((1,), (0,), (1,), (4, 5)),
+      ((1,), (0,), (2,), (0, 1)), ((1,), (0,), (3,), (2, 3)), ((2,), (0,), (0,), (4, 5)),
+      ((2,), (0,), (1,), (0, 1)), ((2,), (0,), (2,), (2, 3)), ((2,), (0,), (3,), (4, 5))]),
+]
+
+
+@pytest.mark.parametrize("case", range(len(_RECIPE_TABLES)))
+def test_recipe_templates_enumerated_and_balanced(case):
+    """The oracle's and the package's recipe tables equal the hand-enumerated ones, and every
+    bank / group is used equally often (validate_balance spreads of rte/recipes.py:141-159 are 0)."""
+    from oracle import banked as BK
+    from rte_amd.config import ModelConfig
+    from rte_amd.recipes import RecipeBank
+
+    kw, sparse = _RECIPE_TABLES[case]
+    want = [dict(attention_banks=tuple(range(kw["attn_banks"])), ffn_banks=tuple(range(kw["ffn_banks"])),
+                 head_groups=tuple(range(kw["head_groups"])), ffn_groups=tuple(range(kw["ffn_groups"])))]
+    want += [dict(attention_banks=a, ffn_banks=f, head_groups=h, ffn_groups=s) for a, f, h, s in sparse]
+    got = BK.recipe_templates(kw["attn_banks"], kw["ffn_banks"], kw["head_groups"], kw["ffn_groups"],
+                              kw["active_head_groups"], kw["active_ffn_groups"], kw["recipe_count"])
+    assert got == want
+    cfg = ModelConfig(topology="recursive", vocab_size=64, d_model=48, n_heads=12, d_ff=96, n_dense_layers=2,
+                      n_prelude=1, n_coda=1, t_max=2, depth_choices=[1, 2], **kw)
+    bank = RecipeBank(cfg)
+    assert [dict(attention_banks=r.attention_banks, ffn_banks=r.ffn_banks, head_groups=r.head_groups,
+                 ffn_groups=r.ffn_groups) for r in bank.recipes] == want
+    counts = {key: np.zeros(n, int) for key, n in (("attention_banks", kw["attn_banks"]),
+                                                    ("ffn_banks", kw["ffn_banks"]),
+                                                    ("head_groups", kw["head_groups"]),
+                                                    ("ffn_groups", kw["ffn_groups"]))}
+    for r in want[1:]:
+        for key, arr in counts.items():
+            arr[list(r[key])] += 1
+    assert all(a.max() - a.min() == 0 for a in counts.values())
+    if hasattr(bank, "validate_balance"):
+        assert all(v == 0 for v in bank.validate_balance().values())
