@@ -315,6 +315,16 @@ class DataConfig:
     eval_tokens: int = 20_000
     synthetic_tokens: int = 20_000
 
+    def __post_init__(self) -> None:
+        # rte/config.py:364-369: the projection lane defaults to the vocab projection and must
+        # agree with it; train_tokens, when given, is the token budget
+        if self.projection_lane is None:
+            self.projection_lane = self.vocab_projection
+        elif self.projection_lane != self.vocab_projection:
+            raise ValueError("data.projection_lane and data.vocab_projection must match")
+        if self.train_tokens is not None:
+            self.max_tokens = self.train_tokens
+
 
 @dataclass(slots=True)
 class ExperimentConfig:
@@ -324,28 +334,40 @@ class ExperimentConfig:
     data: DataConfig = field(default_factory=DataConfig)
     run_name: str = "rte-run"
     output_dir: str = "runs"
+    allow_unknown_config_keys: bool = False
 
 
-def _build(cls, raw: dict[str, Any], where: str):
+_ROOT_KEYS = ("model", "training", "output", "data", "run_name", "output_dir", "allow_unknown_config_keys")
+
+
+def _known_keys(cls, raw: dict[str, Any], section: str, allow_unknown: bool) -> dict[str, Any]:
+    """The keys of `raw` that are fields of `cls`; unknown keys raise unless allow_unknown, in
+    which case they are dropped (rte/config.py:385-397)."""
     known = {f.name for f in fields(cls)}
     unknown = sorted(set(raw) - known)
-    if unknown:
-        raise ValueError(f"unknown {where} config keys: {unknown}")
-    return cls(**raw)
+    if unknown and not allow_unknown:
+        raise ValueError("unknown config key(s): " + ", ".join(f"{section}.{k}" for k in unknown))
+    return {k: v for k, v in raw.items() if k in known}
 
 
 def config_from_dict(raw: dict[str, Any]) -> ExperimentConfig:
-    top = {"model", "training", "output", "data", "run_name", "output_dir"}
-    unknown = sorted(set(raw) - top)
-    if unknown:
-        raise ValueError(f"unknown top-level config keys: {unknown}")
+    """ExperimentConfig of a parsed YAML mapping.  With allow_unknown_config_keys: true at the
+    top level, keys this build does not know are ignored instead of rejected (rte/config.py:400-449)."""
+    allow = bool(raw.get("allow_unknown_config_keys", False))
+    unknown = sorted(set(raw) - set(_ROOT_KEYS))
+    if unknown and not allow:
+        raise ValueError("unknown config key(s): " + ", ".join(unknown))
+    sections = {name: _known_keys(cls, raw.get(name) or {}, name, allow)
+                for name, cls in (("model", ModelConfig), ("training", TrainingConfig), ("output", OutputConfig),
+                                  ("data", DataConfig))}
     return ExperimentConfig(
-        model=_build(ModelConfig, raw.get("model", {}), "model"),
-        training=_build(TrainingConfig, raw.get("training", {}), "training"),
-        output=_build(OutputConfig, raw.get("output") or {}, "output"),
-        data=_build(DataConfig, raw.get("data") or {}, "data"),
+        model=ModelConfig(**sections["model"]),
+        training=TrainingConfig(**sections["training"]),
+        output=OutputConfig(**sections["output"]),
+        data=DataConfig(**sections["data"]),
         run_name=raw.get("run_name", "rte-run"),
         output_dir=raw.get("output_dir", "runs"),
+        allow_unknown_config_keys=allow,
     )
 
 

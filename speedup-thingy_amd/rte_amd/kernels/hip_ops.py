@@ -401,6 +401,14 @@ def axpy(a, b, c, *, keep=None, mask=None):
     return AxpyNormFn.apply(a, b, c, keep, mask, None, None, None, 0.0)[0]
 
 
+def _check_rope_tables(cos: torch.Tensor, sin: torch.Tensor, S: int, hd: int) -> None:
+    """The kernels read cos / sin rows 0..S-1 of width hd: refuse shorter tables (a sequence
+    longer than the rotary table) before any launch, as the reference's broadcast fails."""
+    if cos.ndim != 2 or cos.shape[0] < S or cos.shape[1] != hd or sin.shape != cos.shape:
+        raise ValueError(f"RoPE tables of shape {tuple(cos.shape)} / {tuple(sin.shape)} do not cover "
+                         f"seq_len {S} x head_dim {hd}")
+
+
 # ----------------------------------------------------------------------------- fused QKV + RoPE
 
 class QKVRopeFn(torch.autograd.Function):
@@ -408,9 +416,10 @@ class QKVRopeFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x: torch.Tensor, w: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, n_heads: int):
-        _lib.require_device_tensors("qkv_rope", x, w, cos, sin)
         B, S, d = x.shape
         hd = d // n_heads
+        _check_rope_tables(cos, sin, S, hd)
+        _lib.require_device_tensors("qkv_rope", x, w, cos, sin)
         if w.shape != (3 * d, d):
             raise ValueError(f"wqkv must be [3d, d], got {tuple(w.shape)}")
         xb = x.contiguous().to(BF16)
@@ -558,9 +567,10 @@ class QKVRopeAttentionFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x, w, cos, sin, n_heads: int, head_scale):
-        _lib.require_device_tensors("qkv_rope_attention", x, w, cos, sin, head_scale)
         B, S, d = x.shape
         hd = d // n_heads
+        _check_rope_tables(cos, sin, S, hd)
+        _lib.require_device_tensors("qkv_rope_attention", x, w, cos, sin, head_scale)
         if w.shape != (3 * d, d) or hd not in (32, 64, 128) or hd * n_heads != d:
             raise ValueError("qkv_rope_attention: wqkv [3d, d] and head_dim 32, 64 or 128 required")
         xb = x.contiguous().to(BF16)

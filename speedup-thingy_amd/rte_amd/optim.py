@@ -150,9 +150,12 @@ class FusedAdamW(torch.optim.Optimizer):
             self._build_layout(dev)
             self._layout["static_rows"] = self._static_rows(params)
             self._layout["spares"] = [self._new_host_pair() for _ in range(4)]
+            self._layout["hyper_ring"] = [(torch.empty(self._layout["hyper"].shape, dtype=torch.float64,
+                                                       pin_memory=True), None) for _ in range(4)]
+            self._layout["ring_i"] = 0
         lay = self._layout
         nt = len(params)
-        rows_h, hyper_h = self._host_tables()
+        rows_h, _ = self._host_tables()
         rows = lay["static_rows"].copy()
         for i, p in enumerate(params):
             g = p.grad
@@ -161,11 +164,11 @@ class FusedAdamW(torch.optim.Optimizer):
                 p.grad = g
             rows[i, 1] = 0 if g is None else g.data_ptr()
         rows_h.numpy()[:] = rows
-        hyper_h.numpy()[:] = np.array([[g["lr"], g["betas"][0], g["betas"][1], g["eps"], g["weight_decay"]]
-                                       for g in self.param_groups], dtype=np.float64)
         lay["rows"].copy_(rows_h, non_blocking=True)
-        lay["hyper"].copy_(hyper_h, non_blocking=True)
         if not torch.cuda.is_current_stream_capturing():
+            # a captured step reads the hyper-parameters the caller stages before each replay
+            # (stage_hyper), so a learning-rate schedule reaches every replay
+            self.stage_hyper()
             self._eager_event = torch.cuda.Event()
             self._eager_event.record()
         fi = self.found_inf
@@ -178,8 +181,45 @@ class FusedAdamW(torch.optim.Optimizer):
         self.last_metrics = lay["metrics"]
         return loss
 
+    def stage_hyper(self) -> None:
+        """Copy the groups' current (lr, betas, eps, weight_decay) to the device table the update
+        kernel reads, on the current stream.  Eager steps call it themselves; before replaying a
+        captured step, call it so the replay uses this step's learning rates.  The pinned
+        sources rotate over a ring whose entries are reused only after their copy finished."""
+        lay = self._layout
+        if lay is None:
+            return
+        ring = lay["hyper_ring"]
+        i = lay["ring_i"]
+        buf, ev = ring[i]
+        if ev is not None:
+            ev.synchronize()
+        buf.numpy()[:] = np.array([[g["lr"], g["betas"][0], g["betas"][1], g["eps"], g["weight_decay"]]
+                                   for g in self.param_groups], dtype=np.float64)
+        lay["hyper"].copy_(buf, non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        ring[i] = (buf, ev)
+        lay["ring_i"] = (i + 1) % len(ring)
+
     def load_state_dict(self, state_dict):
         super().load_state_dict(state_dict)
+        # the update kernel dereferences every state tensor on the device: a state loaded from a
+        # CPU map_location or from torch.optim.AdamW (CPU 'step') is moved next to its parameter
+        for p in self._params():
+            st = self.state.get(p)
+            if not st:
+                continue
+            if "step" in st:
+                st["step"] = torch.as_tensor(st["step"]).detach().to(device=p.device, dtype=torch.float32).reshape(())
+                st["step"] = st["step"].clone()
+            for key in ("exp_avg", "exp_avg_sq"):
+                if key not in st:
+                    raise ValueError(f"FusedAdamW: optimizer state lacks {key!r}")
+                t = st[key]
+                if t.shape != p.shape:
+                    raise ValueError(f"FusedAdamW: state {key!r} has shape {tuple(t.shape)}, parameter {tuple(p.shape)}")
+                st[key] = t.detach().to(device=p.device, dtype=torch.float32).contiguous()
         self._layout = None  # state tensors were replaced: rebuild the pointer tables
 
     def metrics_dict(self) -> dict[str, torch.Tensor]:

@@ -21,6 +21,7 @@ import torch
 from rte_amd.audit import AuditEngine, AuditResult
 from rte_amd.config import ExperimentConfig, TrainingConfig
 from rte_amd.kernels import hip_ops, optimized
+from rte_amd.metrics import hot_budget
 from rte_amd.models import DenseModel, ModelOutput, RecursiveModel
 from rte_amd.optim import FusedAdamW
 
@@ -65,6 +66,13 @@ class TrainEngine:
         tr = config.training
         if tr.mode not in ACCELERATED_MODES:
             raise NotImplementedError(f"mode {tr.mode!r} is outside the accelerated path ({sorted(ACCELERATED_MODES)})")
+        if tr.precision != "bf16":
+            # the HIP GEMMs take bf16 operands with fp32 accumulation (the reference's bf16
+            # autocast numerics); fp32 matmuls are not implemented, so refuse rather than
+            # silently train at bf16
+            raise NotImplementedError(
+                f"precision={tr.precision!r}: the MI355X kernels compute matmuls with bf16 operands "
+                "(fp32 accumulation, fp32 master weights); set training.precision: bf16")
         self.device = device or torch.device("cuda")
         set_seed(tr.seed)
         if tr.strict_cuda and self.device.type != "cuda":
@@ -88,6 +96,8 @@ class TrainEngine:
         self.global_micro_step = 0
         self.tokens_seen = 0
         self.last_grad_metrics: dict[str, Any] = {}
+        self.aligned_lm_phase = "A"  # the lm_aligned mode's phase (rte/training.py:128); kept for checkpoints
+        self._current_lr = tr.lr
         # start the audit replay and the consistency loss on side streams right after routing
         self.audit_streams = self.device.type == "cuda"
         self._bf16 = hip_ops.Bf16Prefetch(enabled=self.device.type == "cuda")
@@ -141,6 +151,36 @@ class TrainEngine:
             return nullcontext()
         return torch.autocast(device_type=self.device.type, dtype=torch.bfloat16)
 
+    def _lr_scale(self) -> float:
+        """rte/training.py:470-484: constant, or linear from 1 to lr_final_scale between
+        lr_decay_start_tokens and lr_decay_end_tokens of tokens seen."""
+        tr = self.config.training
+        if tr.lr_schedule == "constant":
+            return 1.0
+        if tr.lr_schedule == "linear_decay_after":
+            if self.tokens_seen <= tr.lr_decay_start_tokens:
+                return 1.0
+            if self.tokens_seen >= tr.lr_decay_end_tokens:
+                return tr.lr_final_scale
+            progress = (self.tokens_seen - tr.lr_decay_start_tokens) / (
+                tr.lr_decay_end_tokens - tr.lr_decay_start_tokens)
+            return 1.0 + progress * (tr.lr_final_scale - 1.0)
+        raise ValueError(tr.lr_schedule)
+
+    def _apply_lr_schedule(self) -> float:
+        """Scale every group's base learning rate (rte/training.py:486-490); returns the scaled
+        global lr.  Runs at the start of every step, before the optimizer reads the rates."""
+        scale = self._lr_scale()
+        for group in self.optimizer.param_groups:
+            group["lr"] = float(group.get("base_lr", self.config.training.lr)) * scale
+        return self.config.training.lr * scale
+
+    def _hot_budget(self, shortlist: bool) -> dict[str, Any]:
+        """Refuse a step whose hot path exceeds the configured budget (rte/training.py:707-740,
+        applied at :1389-1392); host arithmetic on the config only."""
+        size = self.config.output.shortlist_max_tokens if shortlist else None
+        return hot_budget(self.config.model, self.config.training, shortlist_size=size, include_output=True)
+
     def _loss_scale(self, targets) -> float:
         return float(targets.shape[1]) if self.config.training.loss_normalization == "token_mean" else 1.0
 
@@ -191,6 +231,7 @@ class TrainEngine:
 
     def train_step(self, batch, *, check_finite: bool = True) -> TrainStepResult:
         mode = self.config.training.mode
+        self._current_lr = self._apply_lr_schedule()
         if not (self._graph_enabled and mode in ("recursive_macro", "recursive_macro_shortlist")):
             self._bf16.begin()  # one bf16 copy per weight per step (the captured body opens its own)
         if mode == "dense_exact":
@@ -208,7 +249,8 @@ class TrainEngine:
         stepped = self._finish_step(loss, check_finite=check_finite)
         self.tokens_seen += tokens.numel()
         return TrainStepResult(loss, out, {"mode": "dense_exact", "loss": loss, "stepped": stepped,
-                                           "host_time": time.perf_counter() - t0, **self.last_grad_metrics})
+                                           "lr": self._current_lr, "host_time": time.perf_counter() - t0,
+                                           **self.last_grad_metrics})
 
     def _step_recursive_exact(self, batch, check_finite):
         tr = self.config.training
@@ -223,7 +265,7 @@ class TrainEngine:
         m.recipe_bank.update_usage(out.meta.recipe_ids, beta=tr.coverage_beta)
         self.tokens_seen += tokens.numel()
         return TrainStepResult(loss, out, {"mode": "recursive_exact", "loss": loss, "stepped": stepped,
-                                           **self.last_grad_metrics})
+                                           "lr": self._current_lr, **self.last_grad_metrics})
 
     def _router_aux(self, out: ModelOutput) -> dict[str, torch.Tensor]:
         r = out.meta.router
@@ -283,14 +325,18 @@ class TrainEngine:
         m = self.recursive_model
         if shortlist and tr.debug_force_full_output:
             raise RuntimeError("debug_force_full_output forbids recursive_macro_shortlist")
+        budget = self._hot_budget(shortlist)
         if self._graph_enabled:
-            return self._graph_macro_step(batch, shortlist, check_finite)
+            res = self._graph_macro_step(batch, shortlist, check_finite)
+            res.metrics.update(budget, lr=self._current_lr)
+            return res
         tokens, targets = self._move(batch)
         loss, hot, audit, aux, scale = self._macro_loss(tokens, targets, shortlist=shortlist)
         stepped = self._finish_step(loss, check_finite=check_finite)
         m.recipe_bank.update_usage(hot.meta.recipe_ids, beta=tr.coverage_beta)
         self.tokens_seen += tokens.numel()
         metrics = self._macro_metrics(loss, hot, audit, aux, scale, targets, shortlist, stepped)
+        metrics.update(budget, lr=self._current_lr)
         return TrainStepResult(loss, hot, metrics, audit)
 
     # ------------------------------------------------------------------ captured step
@@ -319,6 +365,9 @@ class TrainEngine:
             if self.device.type != "cuda" or not isinstance(self.optimizer, (FusedAdamW, torch.optim.AdamW)):
                 raise ValueError("graph capture needs a ROCm device and AdamW")
             if not isinstance(self.optimizer, FusedAdamW):
+                if tr.lr_schedule != "constant":
+                    raise ValueError("graph capture with torch AdamW bakes the learning rate into the graph: "
+                                     "use the fused optimizer for a learning-rate schedule")
                 for g in self.optimizer.param_groups:
                     g["capturable"] = True
         self._graph_enabled = enabled
@@ -363,6 +412,8 @@ class TrainEngine:
                 with torch.cuda.graph(graph):
                     st["out"] = self._graph_body(st, shortlist, check_finite)
                 st["graph"] = graph
+            if isinstance(self.optimizer, FusedAdamW):
+                self.optimizer.stage_hyper()  # this step's learning rates, read by the replay
             st["graph"].replay()
             out = st["out"]
         self.global_micro_step += 1
@@ -416,32 +467,59 @@ class TrainEngine:
                 "host_metrics": {k: v for k, v in metrics.items() if not isinstance(v, torch.Tensor)},
                 "grad_names": list(self.last_grad_metrics)}
 
-    # ------------------------------------------------------------------ checkpoint (rte/training.py:1656-1701)
-    def save_checkpoint(self, path) -> None:
-        model = self.recursive_model if self.recursive_model is not None else self.dense_model
-        torch.save({
-            "model": model.state_dict(),
+    # ------------------------------------------------------------------ checkpoint
+    def save_checkpoint(self, path, *, data_cursor: int | None = None) -> None:
+        """The payload of rte/training.py:1656-1676 (same keys).  The config is stored as a plain
+        dict, so checkpoints written here load with torch.load(weights_only=True)."""
+        from pathlib import Path
+
+        from rte_amd.config import config_to_dict
+
+        model = self.dense_model if self.dense_model is not None else self.recursive_model
+        payload = {
+            "config": config_to_dict(self.config),
+            "model": model.state_dict() if model is not None else None,
             "optimizer": self.optimizer.state_dict(),
             "global_step": self.global_step,
             "global_micro_step": self.global_micro_step,
             "tokens_seen": self.tokens_seen,
             "audit": self.audit_engine.state_dict(),
-            "torch_rng": torch.get_rng_state(),
-            "cuda_rng": torch.cuda.get_rng_state_all() if torch.cuda.is_available() else None,
-        }, path)
+            "aligned_lm_phase": self.aligned_lm_phase,
+            "data_cursor": data_cursor,
+            "torch_rng_state": torch.get_rng_state(),
+        }
+        if torch.cuda.is_available():
+            payload["cuda_rng_state_all"] = torch.cuda.get_rng_state_all()
+        p = Path(path)
+        p.parent.mkdir(parents=True, exist_ok=True)
+        torch.save(payload, p)
 
-    def load_checkpoint(self, path) -> None:
-        payload = torch.load(path, map_location=self.device, weights_only=False)
-        model = self.recursive_model if self.recursive_model is not None else self.dense_model
-        model.load_state_dict(payload["model"])
-        self.optimizer.load_state_dict(payload["optimizer"])
-        self.global_step = int(payload["global_step"])
-        self.global_micro_step = int(payload["global_micro_step"])
-        self.tokens_seen = int(payload["tokens_seen"])
-        self.audit_engine.load_state_dict(payload["audit"])
-        torch.set_rng_state(payload["torch_rng"].cpu())
-        if payload.get("cuda_rng") is not None and torch.cuda.is_available():
-            torch.cuda.set_rng_state_all([s.cpu() for s in payload["cuda_rng"]])
+    def load_checkpoint(self, path, *, trusted: bool = False) -> int | None:
+        """Restore a payload with the keys of rte/training.py:1678-1701 (every key optional, as
+        there); returns its data_cursor.  By default the file is read with
+        torch.load(weights_only=True); a reference checkpoint, whose config is a pickled
+        dataclass, needs trusted=True (full unpickling: only for files you trust)."""
+        payload = torch.load(path, map_location=self.device, weights_only=not trusted)
+        model = self.dense_model if self.dense_model is not None else self.recursive_model
+        if model is not None and payload.get("model") is not None:
+            model.load_state_dict(payload["model"])
+        if payload.get("optimizer") is not None:
+            try:
+                self.optimizer.load_state_dict(payload["optimizer"])
+            except ValueError:
+                # a checkpoint of another parameter grouping: weights load, the optimizer starts fresh
+                pass
+        self.global_step = int(payload.get("global_step", 0))
+        self.global_micro_step = int(payload.get("global_micro_step", 0))
+        self.tokens_seen = int(payload.get("tokens_seen", 0))
+        self.audit_engine.load_state_dict(payload.get("audit", {}))
+        self.aligned_lm_phase = str(payload.get("aligned_lm_phase", self.aligned_lm_phase))
+        if "torch_rng_state" in payload:
+            torch.set_rng_state(payload["torch_rng_state"].detach().cpu())
+        if torch.cuda.is_available() and "cuda_rng_state_all" in payload:
+            torch.cuda.set_rng_state_all([t.detach().cpu().to(torch.uint8) for t in payload["cuda_rng_state_all"]])
+        self._gstate = None  # a captured step holds the old state's buffers
+        return payload.get("data_cursor")
 
 
 def metrics_to_host(metrics: dict[str, Any]) -> dict[str, Any]:

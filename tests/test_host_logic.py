@@ -247,3 +247,179 @@ def test_bf16_prefetch_tables():
     assert nblk == lib.rte_cast_many_blocks(0, 1, w.numel()) + lib.rte_cast_many_blocks(1, 80, 48)
     assert blk.tolist() == [0] * jobs[1][6] + [1] * (nblk - jobs[1][6])
     assert plan.entries[1][5] == plan.entries[2][5] == 1  # same view on two streams: one buffer
+
+
+# ---------------------------------------------------------------- config loader, precision, budget, lr, checkpoint
+
+def test_allow_unknown_config_keys_drops_them():
+    """allow_unknown_config_keys: true ignores unknown keys at every level (rte/config.py:385-449)."""
+    raw = {"allow_unknown_config_keys": True, "extra_top": 1, "model": {**_model(), "bogus": 1},
+           "training": {"mode": "recursive_macro", "nope": 2}, "data": {"future_key": 3}}
+    cfg = config_from_dict(raw)
+    assert cfg.allow_unknown_config_keys and cfg.model.d_model == 16
+    with pytest.raises(ValueError, match="unknown config key"):
+        config_from_dict({**raw, "allow_unknown_config_keys": False})
+
+
+def test_data_config_post_init():
+    """rte/config.py:364-369: projection_lane defaults to vocab_projection and must equal it;
+    train_tokens sets max_tokens."""
+    from rte_amd.config import DataConfig
+
+    assert DataConfig(vocab_projection="modulo").projection_lane == "modulo"
+    with pytest.raises(ValueError, match="projection_lane"):
+        DataConfig(vocab_projection="filter", projection_lane="modulo")
+    assert DataConfig(train_tokens=1234).max_tokens == 1234
+    assert DataConfig().max_tokens == 200_000
+
+
+def _tiny_engine_cfg(**train):
+    from rte_amd.config import OutputConfig
+
+    tr = dict(mode="recursive_macro", precision="bf16", batch_size=2, seq_len=8, audit_fixed_count=1)
+    tr.update(train)
+    return ExperimentConfig(model=ModelConfig(**_model()), training=TrainingConfig(**tr), output=OutputConfig())
+
+
+def test_fp32_precision_is_refused():
+    from rte_amd.training import TrainEngine
+
+    with pytest.raises(NotImplementedError, match="bf16"):
+        TrainEngine(_tiny_engine_cfg(precision="fp32"), device=torch.device("cpu"))
+
+
+def test_parameter_counts_closed_form():
+    """The fairness formulas of rte/metrics.py:12-94 on a config small enough to count by hand."""
+    from rte_amd import metrics as M
+
+    cfg = ModelConfig(**_model(topology="dense", vocab_size=10, d_model=8, n_heads=2, d_ff=16, n_dense_layers=2,
+                               head_groups=2, ffn_groups=2, macro_rank=2, router_hidden=4))
+    assert M.dense_block_param_count(cfg) == 4 * 64 + 3 * 8 * 16 + 4 * 8 == 672
+    assert M.dense_param_count(cfg) == 10 * 8 + 2 * 672 + 8
+    rec = ModelConfig(**{**_model(vocab_size=10, d_model=8, n_heads=2, d_ff=16, head_groups=2, ffn_groups=2,
+                                  macro_rank=2, router_hidden=4), "attn_banks": 2, "ffn_banks": 3})
+    macro = 8 + 3 * 8 * 2 + 2 * 8 + 8
+    assert M.macro_operator_param_count(rec) == macro == 80
+    want = 80 + 2 * 672 + (2 * 4 * 64 + 3 * 3 * 8 * 16) + 2 * (8 * 4 + 4) + 4 * 3 * macro + 8
+    assert M.recursive_param_count(rec) == want
+    assert M.estimate_hot_active_param_equiv_per_token(rec, include_output=True) == 2 * 672 + 80 + 10 * 8
+    assert M.estimate_hot_active_param_equiv_per_token(rec, shortlist_size=4, include_output=True) == 2 * 672 + 80 + 32
+    # routed pool blocks: k of C pools plus the router
+    pool = ModelConfig(**_model(d_model=16, d_ff=256, ffn_groups=4, ffn_kind="cluster_pool", ffn_clusters=4,
+                                ffn_top_k=2))
+    assert M.active_block_param_count(pool) == 4 * 256 + 3 * 16 * 128 + 4 * 16 + 16 * 4
+    rep = M.build_fairness_report(cfg, rec, tolerance=0.5)
+    assert rep.dense_params == M.dense_param_count(cfg) and rep.recursive_params == want
+    assert rep.passed == (abs(want - rep.dense_params) / rep.dense_params <= 0.5)
+
+
+def test_solve_banks_matches_brute_force():
+    from dataclasses import asdict
+
+    from rte_amd import metrics as M
+
+    cfg = ModelConfig(**_model(d_model=16, d_ff=64, n_dense_layers=7))
+    best = None
+    for a in range(1, 21):
+        for f in range(1, 21):
+            c = ModelConfig(**{**asdict(cfg), "attn_banks": a, "ffn_banks": f})
+            rel = abs(M.recursive_param_count(c) - M.dense_param_count(cfg)) / M.dense_param_count(cfg)
+            if best is None or rel < best[2]:
+                best = (a, f, rel)
+    got = M.solve_banks_for_fairness(cfg, max_banks=20)
+    assert got[:2] == best[:2] and abs(got[2] - best[2]) < 1e-15
+
+
+def test_active_budget_is_enforced_before_device_work():
+    """A budget the hot path exceeds refuses the step (rte/training.py:707-740; the reference's
+    tests/test_training_fixes.py:78-99) before any kernel runs, so this runs on the CPU."""
+    from rte_amd.training import TrainEngine
+
+    eng = TrainEngine(_tiny_engine_cfg(max_active_param_equiv_per_token=1.0), device=torch.device("cpu"))
+    batch = (torch.zeros(2, 8, dtype=torch.long), torch.zeros(2, 8, dtype=torch.long))
+    with pytest.raises(RuntimeError, match="active parameter budget"):
+        eng.train_step(batch)
+    eng = TrainEngine(_tiny_engine_cfg(max_hotpath_flops_per_token=10.0), device=torch.device("cpu"))
+    with pytest.raises(RuntimeError, match="FLOPs/token budget"):
+        eng.train_step(batch)
+    eng = TrainEngine(_tiny_engine_cfg(target_speedup_vs_dense=1000.0), device=torch.device("cpu"))
+    with pytest.raises(RuntimeError, match="active parameter budget"):
+        eng.train_step(batch)
+    eng = TrainEngine(_tiny_engine_cfg(max_active_param_equiv_per_token=1e12), device=torch.device("cpu"))
+    assert eng._hot_budget(False)["active_param_budget"] == 1e12
+
+
+def test_linear_lr_schedule_by_tokens():
+    """rte/training.py:470-490 (the reference's test_linear_lr_schedule_updates_by_tokens): lr is
+    the base lr until lr_decay_start_tokens, then linear to lr_final_scale at lr_decay_end_tokens."""
+    from rte_amd.training import TrainEngine
+
+    eng = TrainEngine(_tiny_engine_cfg(lr=0.01, lr_schedule="linear_decay_after", lr_decay_start_tokens=16,
+                                       lr_decay_end_tokens=48, lr_final_scale=0.25), device=torch.device("cpu"))
+    seen = []
+    for tokens in (0, 16, 24, 32, 48, 100):
+        eng.tokens_seen = tokens
+        seen.append(eng._apply_lr_schedule())
+        assert all(abs(g["lr"] - g["base_lr"] * seen[-1] / 0.01) < 1e-15 for g in eng.optimizer.param_groups)
+    assert seen == pytest.approx([0.01, 0.01, 0.01 * (1 - 0.75 * 0.25), 0.01 * (1 - 0.75 * 0.5), 0.0025, 0.0025])
+
+
+def test_checkpoint_payload_keys_and_round_trip(tmp_path):
+    """The payload keys of rte/training.py:1656-1701; a reference-shaped payload (keys only, no
+    pickled objects) loads, and the engine's own checkpoint round-trips with weights_only loading."""
+    from rte_amd.training import TrainEngine
+
+    eng = TrainEngine(_tiny_engine_cfg(), device=torch.device("cpu"))
+    eng.global_step, eng.global_micro_step, eng.tokens_seen = 3, 4, 48
+    path = tmp_path / "ck.pt"
+    eng.save_checkpoint(path, data_cursor=17)
+    payload = torch.load(path, weights_only=True)
+    assert {"config", "model", "optimizer", "global_step", "global_micro_step", "tokens_seen", "audit",
+            "aligned_lm_phase", "data_cursor", "torch_rng_state"} <= set(payload)
+    other = TrainEngine(_tiny_engine_cfg(), device=torch.device("cpu"))
+    assert other.load_checkpoint(path) == 17
+    assert (other.global_step, other.global_micro_step, other.tokens_seen) == (3, 4, 48)
+    for (k, a), (_, b) in zip(eng.recursive_model.state_dict().items(), other.recursive_model.state_dict().items()):
+        assert torch.equal(a, b), k
+    # a payload with only some of the reference's keys: the rest default as in the reference
+    ref_like = {"model": eng.recursive_model.state_dict(), "global_step": 9, "torch_rng_state": torch.get_rng_state()}
+    torch.save(ref_like, tmp_path / "ref.pt")
+    third = TrainEngine(_tiny_engine_cfg(), device=torch.device("cpu"))
+    assert third.load_checkpoint(tmp_path / "ref.pt") is None
+    assert (third.global_step, third.tokens_seen, third.aligned_lm_phase) == (9, 0, "A")
+
+
+def test_fused_adamw_state_dict_is_normalised():
+    """A state dict from torch.optim.AdamW (CPU 'step' tensors) loads into FusedAdamW with every
+    state tensor as float32 next to its parameter; a mis-shaped moment is refused."""
+    from rte_amd.optim import FusedAdamW
+
+    p = torch.nn.Parameter(torch.randn(4, 3))
+    ref = torch.optim.AdamW([p], lr=0.1)
+    p.grad = torch.randn(4, 3)
+    ref.step()
+    sd = ref.state_dict()
+    sd["state"][0]["step"] = torch.tensor(5.0, dtype=torch.float64)
+    opt = FusedAdamW([p], lr=0.1)
+    opt.load_state_dict(sd)
+    st = opt.state[p]
+    assert st["step"].dtype == torch.float32 and st["step"].shape == () and float(st["step"]) == 5.0
+    assert st["exp_avg"].dtype == torch.float32 and st["exp_avg"].is_contiguous()
+    bad = ref.state_dict()
+    bad["state"][0]["exp_avg"] = torch.zeros(2)
+    with pytest.raises(ValueError, match="exp_avg"):
+        FusedAdamW([p], lr=0.1).load_state_dict(bad)
+
+
+def test_rope_tables_shorter_than_sequence_are_refused():
+    """A sequence longer than the rotary table is a ValueError before any kernel launch."""
+    from rte_amd.kernels import hip_ops
+
+    d, H = 16, 2
+    x = torch.zeros(1, 9, d)
+    w = torch.zeros(3 * d, d)
+    cos = torch.zeros(8, d // H)
+    with pytest.raises(ValueError, match="do not cover"):
+        hip_ops.qkv_rope(x, w, cos, cos, H)
+    with pytest.raises(ValueError, match="do not cover"):
+        hip_ops.qkv_rope_attention(x, w, cos, cos, H)
