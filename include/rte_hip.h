@@ -76,6 +76,18 @@ int rte_pack_index(const int32_t* cl, int P, int C, int k, const float* w, int32
                    float* w_of_slot, int32_t* invalid, void* workspace, size_t workspace_bytes,
                    void* stream);
 
+/* rte_pack_index without a workspace argument: no counterpart in the reference.  For callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same outputs as rte_pack_index (bit-identical); its histogram lives in a
+ * static device array of rte_pack_index_noalloc_max_bytes() bytes (1 MiB) per device, so sizes whose
+ * rte_pack_workspace_bytes(P, C) exceeds that are rejected with an error.  The library allocates
+ * nothing in this call.  Every call on one device shares that device's array: calls that overlap
+ * on one device (other streams or host threads) race. */
+size_t rte_pack_index_noalloc_max_bytes(void);
+int rte_pack_index_noalloc(const int32_t* cl, int P, int C, int k, const float* w, int32_t* offsets,
+                           int32_t* tok_of_slot, int32_t* pair_of_slot, int32_t* slot_of_pair, float* w_of_slot,
+                           int32_t* invalid, void* stream);
+
 /* out[t] = resid[t] + extra[t] + sum_{j<k} rows[t*k + j]  (j ascending; fp32 accumulation)
  * rows, extra: bf16; resid: f32 (optional); out: f32 (out_f32=1) or bf16.
  * slot_of_pair (optional, from rte_pack_index): pairs whose slot is -1 (invalid cluster id,

@@ -34,6 +34,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_route_topk": (_I, [_P, _I, _I, _I, _P, _P, _P]),
     "rte_pack_workspace_bytes": (_SZ, [_I, _I]),
     "rte_pack_index": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "rte_pack_index_noalloc_max_bytes": (_SZ, []),
+    "rte_pack_index_noalloc": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P]),
     "rte_combine_rows": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _I, _P]),
     "rte_route_bwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _P, _P, _P]),
     "rte_grouped_swiglu_fwd": (
