@@ -47,6 +47,26 @@ def cfg3_config(batch: int = 128, seq: int = 64):
     return ExperimentConfig(model=model, training=training, output=OutputConfig(), run_name="bench_cfg3")
 
 
+def cfg5_config(batch: int = 32, seq: int = 512):
+    """scaled recursive_macro_shortlist step, d1024, 16 heads, depth 8,
+    routed pool 256 clusters x 64 neurons (top-16) in the prelude / coda blocks and 256 slabs x 64
+    (16 active) in the banked core, V8192 with the default shortlist head, B32 x S512."""
+    from rte_amd.config import ExperimentConfig, ModelConfig, OutputConfig, TrainingConfig
+
+    model = ModelConfig(
+        topology="recursive", vocab_size=8192, d_model=1024, n_heads=16, d_ff=16384, n_dense_layers=2,
+        n_prelude=1, n_coda=1, t_max=8, depth_choices=[1, 2, 4, 8], attn_banks=1, ffn_banks=1, head_groups=16,
+        ffn_groups=256, active_head_groups=4, active_ffn_groups=16, recipe_count=16, macro_rank=32,
+        ffn_kind="cluster_pool", ffn_clusters=256, ffn_top_k=16,
+    )
+    training = TrainingConfig(
+        mode="recursive_macro_shortlist", precision="bf16", lr=3e-4, weight_decay=0.1, batch_size=batch,
+        seq_len=seq, audit_sampler="fixed_count", audit_fixed_count=1, fixed_depth=8, seed=1337,
+    )
+    return ExperimentConfig(model=model, training=training, output=OutputConfig(mode="shortlist"),
+                            run_name="bench_cfg5")
+
+
 def zipf_batch(gen, vocab: int, batch: int, seq: int, device):
     import torch
 

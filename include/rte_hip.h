@@ -225,6 +225,34 @@ int rte_rmsnorm_bwd(const void* dy, const float* x, const float* w, const float*
                     int T, int d, float* dx, float* dw, int dw_accumulate, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* ---- elementwise dispatch symbols in the caller's dtype ----
+ * Fused RMSNorm (replaces k_fused_rmsnorm, rte/kernels/reference.py:9-17): y = x + residual
+ * (residual optional; y written when both y and residual are given), rstd f32 [T] =
+ * rsqrt(mean(y^2) + eps), out = (y * rstd) * w.  x, residual, y: f32 (io_f32 = 1) or bf16 [T, d];
+ * w f32 [d]; out f32 (out_f32 = 1) or bf16.  bf16 inputs are rounded where torch's bf16 ops round
+ * (the sum, the rsqrt factor, the normalised row).  d % 8 == 0, d <= 4096.
+ * bwd: g (f32 if g_f32 else bf16) = dL/d(out); dy (io dtype) = dL/dy = rstd w g - y rstd^3
+ * mean(w g y) (+ dy_extra, io dtype, optional: the gradient of the returned y); dw f32 [d] = sum
+ * over rows of g y rstd, in a fixed order.  d <= 2048; workspace
+ * rte_fused_rmsnorm_bwd_workspace_bytes(T, d). */
+int rte_fused_rmsnorm_fwd(const void* x, const void* residual, int io_f32, const float* w, int T, int d, float eps,
+                          void* y, void* out, int out_f32, float* rstd, void* stream);
+size_t rte_fused_rmsnorm_bwd_workspace_bytes(int T, int d);
+int rte_fused_rmsnorm_bwd(const void* g, int g_f32, const void* dy_extra, const void* y, int io_f32, const float* w,
+                          const float* rstd, int T, int d, void* dy, float* dw, void* workspace, size_t workspace_bytes,
+                          void* stream);
+/* Interleaved RoPE (replaces k_rope_apply, rte/kernels/reference.py:20-28): q, k contiguous
+ * [rows, S, hd] (f32 if in_f32 else bf16), cos / sin f32 [S, hd];
+ *   out[2i] = x[2i] cos[2i] - x[2i+1] sin[2i], out[2i+1] = x[2i+1] cos[2i+1] + x[2i] sin[2i+1];
+ * inverse = 1 applies the transpose (the backward).  Outputs f32 (out_f32 = 1) or bf16; hd % 8 == 0. */
+int rte_rope_apply(const void* q, const void* k, int in_f32, int64_t rows, int S, int hd, const float* cos_t,
+                   const float* sin_t, void* q_out, void* k_out, int out_f32, int inverse, void* stream);
+/* Static-centre routing (replaces route_to_static_centers, rte/kernels/cluster_pool_ffn.py:129-140):
+ * q f32 [T, R2] = [x A_up | x A_gate]; out int32 [T] = argmax_c normalize(q[t]) . centers[c]
+ * (centers f32 [C, R2]; F.normalize's 1e-12 clamp; first index of the maximum, NaN counts as
+ * the maximum).  R2 <= 8192. */
+int rte_route_centers(const float* q, int T, int R2, const float* centers, int C, int32_t* out, void* stream);
+
 /* ---- token cross-entropy on full logits (rte/models.py:73-75, rte/kernels/reference.py:146-147) ----
  * logits f32 [T, ld] (first V columns used), targets int64 [T] (negative = ignored row).
  * fwd: loss[t] = logsumexp(logits[t]) - logits[t, target], lse[t] saved.

@@ -12,6 +12,9 @@ How each function is pinned (tests/test_oracle.py):
                              k = 1 equals the reference argmax routing
   routing.pack_index         brute-force per-cluster ascending lists; permutation round trip
   routing.static_pack_gather the padded pack_index / flat_gather of the reference builder
+  routing.static_centers     brute-force per-token loop over the centres; invariance of the
+                             choice under positive scaling of a token's features; k = 1 of
+                             route_topk on the centre scores
   swiglu.*                   finite differences (fp64) + torch autograd on CPU
   cluster_pool.*             all clusters with uniform weights == dense SwiGLU / C;
                              k = 1 equals the reference per-cluster loop; finite differences

@@ -94,3 +94,14 @@ def segment_reduce_rows(keys, n_keys, rows, w=None, row_div=1):
     src = r[np.arange(k.shape[0]) // row_div]
     np.add.at(out, k[ok], wt[ok, None] * src[ok])
     return out
+
+
+def static_centers(q, centers):
+    """route_to_static_centers (rte/kernels/cluster_pool_ffn.py:129-140) on precomputed selector
+    features q = [x A_up | x A_gate]: argmax_c of normalize(q) . centers[c], normalize dividing
+    by max(||q||, 1e-12) as F.normalize; the first maximal index wins (torch.argmax)."""
+    q = np.asarray(q, np.float64)
+    nrm = np.maximum(np.sqrt((q * q).sum(-1, keepdims=True)), 1e-12)
+    scores = (q / nrm) @ np.asarray(centers, np.float64).T
+    return np.argmax(scores, axis=-1).astype(np.int64), scores
+

@@ -62,6 +62,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_rmsnorm_fwd": (_I, [_P, _P, _I, _I, _F, _P, _P, _P]),
     "rte_rmsnorm_bwd_workspace_bytes": (_SZ, [_I, _I]),
     "rte_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _P, _I, _P, _SZ, _P]),
+    "rte_fused_rmsnorm_fwd": (_I, [_P, _P, _I, _P, _I, _I, _F, _P, _P, _I, _P, _P]),
+    "rte_fused_rmsnorm_bwd_workspace_bytes": (_SZ, [_I, _I]),
+    "rte_fused_rmsnorm_bwd": (_I, [_P, _I, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _SZ, _P]),
+    "rte_rope_apply": (_I, [_P, _P, _I, _I64, _I, _I, _P, _P, _P, _P, _I, _I, _P]),
+    "rte_route_centers": (_I, [_P, _I, _I, _P, _I, _P, _P]),
     "rte_ce_fwd": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P]),
     "rte_ce_bwd": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P]),
     "rte_axpy_norm_fwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _F, _P, _P, _P, _P]),

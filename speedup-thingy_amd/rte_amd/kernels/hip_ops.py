@@ -206,13 +206,15 @@ def gemm(
     resid: torch.Tensor | None = None,
     out: torch.Tensor | None = None,
     beta: float = 0.0,
+    b_rows: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """C[m, n] = alpha * sum_k A(m, k) B(n, k) (+ beta C) (+ resid).
 
     a: [M, K] (a_t False) or [K, M] (a_t True); b: [N, K] (b_t False) or [K, N] (b_t True).
-    bf16 operands, fp32 accumulation.
+    b_rows (int32, optional): B's memory rows are b_rows[n] (b_t False) or b_rows[k] (b_t True),
+    so b may hold more rows than the problem reads.  bf16 operands, fp32 accumulation.
     """
-    _lib.require_device_tensors("gemm", a, b, resid, out)
+    _lib.require_device_tensors("gemm", a, b, resid, out, b_rows)
     if a.dtype != BF16 or b.dtype != BF16:
         raise TypeError("gemm operands must be bfloat16")
     a = a.contiguous()
@@ -221,6 +223,12 @@ def gemm(
     K = a.shape[0] if a_t else a.shape[1]
     N = b.shape[1] if b_t else b.shape[0]
     Kb = b.shape[0] if b_t else b.shape[1]
+    if b_rows is not None:
+        b_rows = b_rows.reshape(-1).contiguous().to(torch.int32)
+        if b_t:
+            Kb = b_rows.numel()
+        else:
+            N = b_rows.numel()
     if K != Kb:
         raise ValueError(f"gemm: reduction sizes differ ({K} vs {Kb})")
     if out is None:
@@ -231,7 +239,7 @@ def gemm(
     call(
         "rte_gemm_bf16",
         ptr(a), a.shape[1], int(a_t), None,
-        ptr(b), b.shape[1], int(b_t), None,
+        ptr(b), b.shape[1], int(b_t), ptr(b_rows),
         ptr(out), out.shape[1], int(out.dtype == F32), M, N, K,
         float(alpha), float(beta), ptr(resid), 0 if resid is None else resid.shape[1], wsp, wsn, _s(),
     )
@@ -665,6 +673,15 @@ class DenseSwiGLUFn(torch.autograd.Function):
 
 
 def dense_swiglu(x, wug, wd, resid=None, *, wd_rows: bool = False, out_f32: bool = True):
+    """resid + (up * silu(gate)) @ W_down; a width F that is not a multiple of 32 (the kernels'
+    column block) is padded with zero neurons, which contribute nothing and get no gradient."""
+    F = wug.shape[0] // 2
+    pad = (-F) % 32
+    if pad:
+        up, gate = wug[:F], wug[F:]
+        zr = wug.new_zeros(pad, wug.shape[1])
+        wug = torch.cat([up, zr, gate, zr])
+        wd = torch.cat([wd, wd.new_zeros(pad, wd.shape[1])]) if wd_rows else torch.cat([wd, wd.new_zeros(wd.shape[0], pad)], 1)
     return DenseSwiGLUFn.apply(x, wug, wd, resid, wd_rows, out_f32)
 
 
@@ -1464,3 +1481,211 @@ class SVDFFNFn(torch.autograd.Function):
 
 def svd_ffn(x, us_ug, v_ug, v_dn, us_dn, resid=None):
     return SVDFFNFn.apply(x, us_ug, v_ug, v_dn, us_dn, resid)
+
+
+# ----------------------------------------------------------------------------- dispatch-symbol kernels
+
+def _io_flag(t: torch.Tensor, op: str) -> int:
+    if t.dtype == F32:
+        return 1
+    if t.dtype == BF16:
+        return 0
+    raise TypeError(f"{op}: float32 or bfloat16 tensors expected, got {t.dtype}")
+
+
+class FusedRMSNormFn(torch.autograd.Function):
+    """(y * rsqrt(mean(y^2) + eps) * w, y) with y = x + residual, in the dtype torch gives the
+    reference's k_fused_rmsnorm (rte/kernels/reference.py:9-17): the output is
+    promote(y.dtype, w.dtype), y keeps x's dtype."""
+
+    @staticmethod
+    def forward(ctx, x, w, residual, eps: float):
+        _lib.require_device_tensors("k_fused_rmsnorm", x, w, residual)
+        io = _io_flag(x, "k_fused_rmsnorm")
+        if residual is not None and residual.dtype != x.dtype:
+            raise TypeError("k_fused_rmsnorm: x and residual must share a dtype")
+        shape = x.shape
+        d = shape[-1]
+        x2 = x.reshape(-1, d).contiguous()
+        T = x2.shape[0]
+        r2 = None if residual is None else residual.reshape(T, d).contiguous()
+        w32 = w.detach().reshape(d).contiguous().to(F32)
+        out_dt = torch.promote_types(x.dtype, w.dtype)
+        if out_dt not in (F32, BF16):
+            raise TypeError(f"k_fused_rmsnorm: output dtype {out_dt} unsupported")
+        out = torch.empty((T, d), dtype=out_dt, device=x.device)
+        y = torch.empty_like(x2) if r2 is not None else None
+        rstd = torch.empty((T,), dtype=F32, device=x.device)
+        call("rte_fused_rmsnorm_fwd", ptr(x2), ptr(r2), io, ptr(w32), T, d, float(eps), ptr(y), ptr(out),
+             int(out_dt == F32), ptr(rstd), _s())
+        ysave = y if y is not None else x2
+        ctx.save_for_backward(ysave, w32, rstd)
+        ctx.meta = (shape, io, residual is not None, w.dtype)
+        ctx.set_materialize_grads(False)
+        if y is None:
+            return out.view(shape), None
+        return out.view(shape), y.view(shape)
+
+    @staticmethod
+    def backward(ctx, g, gy):
+        y, w32, rstd = ctx.saved_tensors
+        shape, io, has_res, w_dt = ctx.meta
+        T, d = y.shape
+        if g is None:
+            gx = None if gy is None else gy
+            return gx, None, gx if has_res else None, None
+        gc = g.reshape(T, d).contiguous()
+        if gc.dtype not in (F32, BF16):
+            gc = gc.to(F32)
+        ey = None if gy is None else gy.reshape(T, d).contiguous().to(y.dtype)
+        dy = torch.empty_like(y)
+        dw = torch.empty((d,), dtype=F32, device=y.device)
+        ws, nb = workspace(_lib.load().rte_fused_rmsnorm_bwd_workspace_bytes(T, d), y.device)
+        call("rte_fused_rmsnorm_bwd", ptr(gc), int(gc.dtype == F32), ptr(ey), ptr(y), io, ptr(w32), ptr(rstd), T, d,
+             ptr(dy), ptr(dw), ws, nb, _s())
+        dyv = dy.view(shape)
+        return dyv, dw.to(w_dt), (dyv if has_res else None), None
+
+
+def fused_rmsnorm(x, w, residual=None, eps: float = 1e-5):
+    return FusedRMSNormFn.apply(x, w, residual, eps)
+
+
+class RopeApplyFn(torch.autograd.Function):
+    """Interleaved RoPE of q and k (rte/kernels/reference.py:20-28) on the HIP kernel; q, k
+    [..., S, hd] in float32 or bfloat16, cos / sin broadcastable [S, hd]; the output dtype is
+    promote(q.dtype, cos.dtype) as in the reference.  cos / sin carry no gradient."""
+
+    @staticmethod
+    def forward(ctx, q, k, cos, sin):
+        _lib.require_device_tensors("k_rope_apply", q, k, cos, sin)
+        if q.shape != k.shape or q.dtype != k.dtype:
+            raise ValueError("k_rope_apply: q and k must share shape and dtype")
+        S, hd = q.shape[-2], q.shape[-1]
+        c2 = cos.reshape(-1, cos.shape[-1])
+        s2 = sin.reshape(-1, sin.shape[-1])
+        if c2.shape != (S, hd) or s2.shape != (S, hd):
+            raise ValueError(f"k_rope_apply: cos / sin must be [{S}, {hd}] (got {tuple(cos.shape)})")
+        io = _io_flag(q, "k_rope_apply")
+        out_dt = torch.promote_types(q.dtype, cos.dtype)
+        if out_dt not in (F32, BF16):
+            raise TypeError(f"k_rope_apply: output dtype {out_dt} unsupported")
+        cf, sf = c2.contiguous().to(F32), s2.contiguous().to(F32)
+        qc, kc = q.contiguous(), k.contiguous()
+        qo = torch.empty(q.shape, dtype=out_dt, device=q.device)
+        ko = torch.empty(k.shape, dtype=out_dt, device=k.device)
+        rows = q.numel() // hd
+        call("rte_rope_apply", ptr(qc), ptr(kc), io, rows, S, hd, ptr(cf), ptr(sf), ptr(qo), ptr(ko),
+             int(out_dt == F32), 0, _s())
+        ctx.save_for_backward(cf, sf)
+        ctx.meta = (q.dtype, S, hd)
+        ctx.set_materialize_grads(False)
+        return qo, ko
+
+    @staticmethod
+    def backward(ctx, gq, gk):
+        cf, sf = ctx.saved_tensors
+        q_dt, S, hd = ctx.meta
+        ref = gq if gq is not None else gk
+        if ref is None:
+            return None, None, None, None
+        gq = torch.zeros_like(ref) if gq is None else gq
+        gk = torch.zeros_like(ref) if gk is None else gk
+        gin = torch.promote_types(gq.dtype, gk.dtype)
+        if gin not in (F32, BF16):
+            gin = F32
+        gqc, gkc = gq.contiguous().to(gin), gk.contiguous().to(gin)
+        dq = torch.empty(gq.shape, dtype=q_dt, device=gq.device)
+        dk = torch.empty(gk.shape, dtype=q_dt, device=gk.device)
+        call("rte_rope_apply", ptr(gqc), ptr(gkc), int(gin == F32), gq.numel() // hd, S, hd, ptr(cf), ptr(sf), ptr(dq),
+             ptr(dk), int(q_dt == F32), 1, _s())
+        return dq, dk, None, None
+
+
+def rope_apply(q, k, cos, sin):
+    return RopeApplyFn.apply(q, k, cos, sin)
+
+
+class RowsLinearFn(torch.autograd.Function):
+    """x @ W[rows, :] (the reference's k_out_proj_grouped, rte/kernels/reference.py:58-59): the GEMM
+    reads W's rows through an index table (no gathered weight copy); dW's selected rows are
+    reduced into W's rows in a fixed order (repeated indices add up)."""
+
+    @staticmethod
+    def forward(ctx, x, w, rows, out_dtype):
+        _lib.require_device_tensors("k_out_proj_grouped", x, w, rows)
+        shape = x.shape
+        K = shape[-1]
+        rid = rows.reshape(-1).contiguous().to(torch.int32)
+        if rid.numel() != K:
+            raise ValueError(f"k_out_proj_grouped: {rid.numel()} row indices for x of width {K}")
+        xb = x.reshape(-1, K).contiguous().to(BF16)
+        wb = cast_bf16(w)
+        out = gemm(xb, wb, b_t=True, b_rows=rid, out_f32=out_dtype == F32)
+        ctx.save_for_backward(xb, wb, rid)
+        ctx.meta = (shape, x.dtype, w.dtype, w.shape[0])
+        return out.view(*shape[:-1], wb.shape[1]).to(out_dtype)
+
+    @staticmethod
+    def backward(ctx, dout):
+        xb, wb, rid = ctx.saved_tensors
+        shape, x_dt, w_dt, n_rows = ctx.meta
+        N = wb.shape[1]
+        db = dout.reshape(-1, N).contiguous().to(BF16)
+        dx = gemm(db, wb, b_rows=rid)                                  # [T, K] = dout @ W[rows]^T
+        dsel = gemm(xb, db, a_t=True, b_t=True, out_f32=True)          # [K, N] = x^T dout
+        dw = segment_reduce_rows(rid, n_rows, dsel)
+        return dx.view(shape).to(x_dt), dw.to(w_dt), None, None
+
+
+def rows_linear(x, w, rows, out_dtype=BF16):
+    return RowsLinearFn.apply(x, w, rows, out_dtype)
+
+
+def route_centers(q: torch.Tensor, centers: torch.Tensor) -> torch.Tensor:
+    """argmax_c normalize(q[t]) . centers[c] (fp32, int32 ids) on the HIP kernel."""
+    _lib.require_device_tensors("route_to_static_centers", q, centers)
+    qf = q.reshape(-1, q.shape[-1]).contiguous().to(F32)
+    cf = centers.contiguous().to(F32)
+    if cf.ndim != 2 or cf.shape[1] != qf.shape[1]:
+        raise ValueError(f"route_to_static_centers: centers {tuple(cf.shape)} do not match features {qf.shape[1]}")
+    out = torch.empty((qf.shape[0],), dtype=torch.int32, device=qf.device)
+    call("rte_route_centers", ptr(qf), qf.shape[0], qf.shape[1], ptr(cf), cf.shape[0], ptr(out), _s())
+    return out.view(q.shape[:-1])
+
+
+class CrossEntropyFn(torch.autograd.Function):
+    """Per-token cross-entropy of fp32 logits [..., V] against int64 targets (negative targets,
+    such as F.cross_entropy's ignore_index -100, give 0) on the fused CE kernel; the backward is
+    (softmax - onehot) * dloss in fp32 from the saved log-sum-exp."""
+
+    @staticmethod
+    def forward(ctx, logits, targets):
+        _lib.require_device_tensors("cross_entropy", logits, targets)
+        V = logits.shape[-1]
+        lg = logits.reshape(-1, V).contiguous().to(F32)
+        T = lg.shape[0]
+        tg = targets.reshape(-1).contiguous().to(torch.int64)
+        if tg.numel() != T:
+            raise ValueError(f"cross_entropy: {tg.numel()} targets for {T} rows")
+        loss = torch.empty((T,), dtype=F32, device=lg.device)
+        lse = torch.empty((T,), dtype=F32, device=lg.device)
+        call("rte_ce_fwd", ptr(lg), V, T, V, ptr(tg), ptr(loss), ptr(lse), _s())
+        ctx.save_for_backward(lg, tg, lse)
+        ctx.meta = (logits.shape, logits.dtype)
+        return loss.view(targets.shape)
+
+    @staticmethod
+    def backward(ctx, g):
+        lg, tg, lse = ctx.saved_tensors
+        shape, dt = ctx.meta
+        valid = tg >= 0
+        p = torch.exp(lg - lse[:, None])
+        p[valid, tg[valid]] -= 1.0
+        p *= (g.reshape(-1).to(F32) * valid.to(F32))[:, None]
+        return p.view(shape).to(dt), None
+
+
+def cross_entropy(logits, targets):
+    return CrossEntropyFn.apply(logits, targets)
+

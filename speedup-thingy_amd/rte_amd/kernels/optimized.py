@@ -20,24 +20,27 @@ from rte_amd.kernels import hip_ops
 STRICT_CUDA = False
 REQUIRE_FLASH = True
 
-# symbol -> implementation ("hip": librte_hip kernels, "torch": tensor ops on the device)
+# symbol -> implementation ("hip": librte_hip kernels, "torch": tensor ops on the device,
+# "python": a host loop).  The torch / python ones are the symbols the reference's own optimized
+# module also leaves as plain tensor code (stable sort by recipe key, its inverse, the seeded
+# Bernoulli draw, the metric copy, the recurrent loop driver).
 SYMBOLS: dict[str, str] = {
     "k_fused_rmsnorm": "hip",
-    "k_rope_apply": "torch",
+    "k_rope_apply": "hip",
     "k_qkv_dense": "hip",
     "k_flash_causal_dense": "hip",
-    "k_qkv_grouped": "torch",
+    "k_qkv_grouped": "hip",
     "k_flash_causal_grouped": "hip",
-    "k_out_proj_grouped": "torch",
+    "k_out_proj_grouped": "hip",
     "k_swiglu_dense": "hip",
-    "k_swiglu_grouped": "torch",
+    "k_swiglu_grouped": "hip",
     "k_pack_by_recipe": "torch",
     "k_unpack_from_recipe": "torch",
-    "k_macro_phi": "torch",
+    "k_macro_phi": "hip",
     "k_recurrent_exact_loop": "python",
     "k_logits_full": "hip",
     "k_logits_shortlist": "hip",
-    "k_cross_entropy_unreduced": "torch",
+    "k_cross_entropy_unreduced": "hip",
     "k_sample_audit_mask": "torch",
     "k_metrics_reduce": "torch",
 }
@@ -72,6 +75,7 @@ def backend_status() -> dict[str, object]:
         # no symbol ever substitutes reference math for a HIP kernel; unavailable -> error
         "uses_reference_fallback": False,
         "symbols": dict(SYMBOLS),
+        "torch_symbols": sorted(k for k, v in SYMBOLS.items() if v != "hip"),
     }
     if ready:
         try:
@@ -100,32 +104,116 @@ def _hip_inputs(op: str, *tensors) -> None:
 
 # ----------------------------------------------------------------------------- hot-path symbols (HIP)
 
+def _mm_dtype(op: str, *tensors) -> torch.dtype:
+    """The matmul symbols compute with bf16 operands and fp32 accumulation, which is what the
+    reference computes under bf16 autocast (its training precision "bf16"); their result is
+    bf16 as there.  Float32 operands outside a bf16 autocast region would ask for fp32 matmuls,
+    which this build does not implement: refuse instead of returning bf16-accurate numbers."""
+    if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+        return torch.bfloat16
+    floats = [t for t in tensors if isinstance(t, torch.Tensor) and t.is_floating_point()]
+    if all(t.dtype == torch.bfloat16 for t in floats):
+        return torch.bfloat16
+    raise RuntimeError(f"{op}: the HIP matmul kernels take bf16 operands; call it under "
+                       "torch.autocast('cuda', dtype=torch.bfloat16) or pass bfloat16 tensors "
+                       "(fp32 matmuls are not implemented)")
+
+
 def k_fused_rmsnorm(x, weight, residual=None, eps: float = 1e-5):
-    """(normed * weight, x + residual or None), normed in bf16 (rte/kernels/reference.py:9-17)."""
+    """(y * rsqrt(mean(y^2) + eps) * weight, y or None) with y = x + residual
+    (rte/kernels/reference.py:9-17), in the dtypes the reference returns: the normed output is
+    promote(x.dtype, weight.dtype), y keeps x's dtype."""
     _hip_inputs("k_fused_rmsnorm", x, weight, residual)
-    y = x if residual is None else x + residual
-    return hip_ops.rmsnorm(y, weight, eps), (y if residual is not None else None)
+    return hip_ops.fused_rmsnorm(x, weight, residual, eps)
+
+
+def k_rope_apply(q, k, cos, sin):
+    """Interleaved rotary embedding of q and k (rte/kernels/reference.py:20-28)."""
+    _hip_inputs("k_rope_apply", q, k, cos, sin)
+    return hip_ops.rope_apply(q, k, cos, sin)
 
 
 def k_qkv_dense(x, wq, wk, wv):
-    """x @ wq, x @ wk, x @ wv with [in, out] weights (rte/kernels/reference.py:31-37)."""
+    """x @ wq, x @ wk, x @ wv with [in, out] weights (rte/kernels/reference.py:31-37): one GEMM
+    over the concatenated weights."""
     _hip_inputs("k_qkv_dense", x, wq, wk, wv)
+    _mm_dtype("k_qkv_dense", x, wq, wk, wv)
     w = torch.cat([wq.t(), wk.t(), wv.t()], dim=0)  # nn.Linear layout [3*out, in]
     out = hip_ops.linear(x, w, out_f32=False)
     return out.split(wq.shape[1], dim=-1)
 
 
+def k_qkv_grouped(x, wq, wk, wv, column_indices):
+    """x @ w[:, columns] for w in (wq, wk, wv) (rte/kernels/reference.py:44-51): the selected
+    columns of the three weights feed one GEMM."""
+    _hip_inputs("k_qkv_grouped", x, wq, wk, wv, column_indices)
+    _mm_dtype("k_qkv_grouped", x, wq, wk, wv)
+    cols = column_indices.to(device=wq.device, dtype=torch.long)
+    w = torch.cat([wq.index_select(1, cols), wk.index_select(1, cols), wv.index_select(1, cols)], dim=1).t()
+    out = hip_ops.linear(x, w, out_f32=False)
+    return out.split(cols.numel(), dim=-1)
+
+
+def k_out_proj_grouped(x, wo, row_indices):
+    """x @ wo[rows, :] (rte/kernels/reference.py:58-59): the GEMM reads wo's rows through the index
+    table; the weight gradient of repeated rows adds up in a fixed order."""
+    _hip_inputs("k_out_proj_grouped", x, wo, row_indices)
+    _mm_dtype("k_out_proj_grouped", x, wo)
+    return hip_ops.rows_linear(x, wo, row_indices, torch.bfloat16)
+
+
 def k_swiglu_dense(x, wu, wg, wd):
     """(x @ wu) * silu(x @ wg) @ wd with [in, out] weights (rte/kernels/reference.py:62-68)."""
     _hip_inputs("k_swiglu_dense", x, wu, wg, wd)
+    _mm_dtype("k_swiglu_dense", x, wu, wg, wd)
     wug = torch.cat([wu.t(), wg.t()], dim=0)
-    return hip_ops.dense_swiglu(x, wug, wd, None, wd_rows=True, out_f32=True)
+    return hip_ops.dense_swiglu(x, wug, wd, None, wd_rows=True, out_f32=False)
+
+
+def k_swiglu_grouped(x, wu, wg, wd, slab_indices):
+    """The SwiGLU of the selected slabs, (x @ wu[:, s]) * silu(x @ wg[:, s]) @ wd[s, :]
+    (rte/kernels/reference.py:71-78), on the fused SwiGLU GEMMs."""
+    _hip_inputs("k_swiglu_grouped", x, wu, wg, wd, slab_indices)
+    _mm_dtype("k_swiglu_grouped", x, wu, wg, wd)
+    sl = slab_indices.to(device=wu.device, dtype=torch.long)
+    wug = torch.cat([wu.index_select(1, sl).t(), wg.index_select(1, sl).t()], dim=0)
+    return hip_ops.dense_swiglu(x, wug, wd.index_select(0, sl), None, wd_rows=True, out_f32=False)
+
+
+def k_macro_phi(h, h0, d_gain, v, u, bias, eps: float = 1e-5):
+    """h + d_gain h + silu(z v) u + bias with z = [rmsnorm(h) | mean_s rmsnorm(h) | h0]
+    (rte/kernels/reference.py:111-124).  v [3d, m] and u [m, d] shared by all samples, or per
+    sample [B, 3d, m] / [B, m, d] (a grouped GEMM keyed by sample)."""
+    _hip_inputs("k_macro_phi", h, h0, v, u)
+    _mm_dtype("k_macro_phi", v, u)
+    ones = torch.ones(h.shape[-1], device=h.device, dtype=h.dtype)
+    normed, _ = hip_ops.fused_rmsnorm(h, ones, None, eps)
+    pooled = normed.mean(dim=1, keepdim=True).expand_as(normed)
+    z = torch.cat([normed, pooled, h0.to(normed.dtype)], dim=-1)
+    B, S, _ = h.shape
+    if v.ndim == 2:
+        a = hip_ops.linear(z, v.t(), out_f32=False)
+        low = hip_ops.linear(F.silu(a), u.t(), out_f32=True)
+    else:
+        keys = torch.arange(B, device=h.device, dtype=torch.int32).repeat_interleave(S)
+        pk = hip_ops.group_rows(keys, B)
+        a = hip_ops.grouped_linear(z, v, pk, out_f32=False)
+        low = hip_ops.grouped_linear(F.silu(a), u, pk, out_f32=True)
+    return h + d_gain * h + low.view_as(h).to(h.dtype) + bias
 
 
 def k_logits_full(hidden, vocab_weight):
+    """hidden @ vocab_weight^T (rte/kernels/reference.py:131-132), bf16 as under autocast."""
     _hip_inputs("k_logits_full", hidden, vocab_weight)
-    return hip_ops.linear(hidden, vocab_weight, out_f32=True)
+    _mm_dtype("k_logits_full", hidden, vocab_weight)
+    return hip_ops.linear(hidden, vocab_weight, out_f32=False)
 
+
+def k_cross_entropy_unreduced(logits, targets):
+    """Per-token cross-entropy (rte/kernels/reference.py:146-147; ignore_index -100 rows give 0)
+    on the fused CE kernels, fp32 as F.cross_entropy computes it."""
+    _hip_inputs("k_cross_entropy_unreduced", logits, targets)
+    return hip_ops.cross_entropy(logits, targets)
 
 # ----------------------------------------------------------------------------- attention core (SDPA)
 
@@ -145,32 +233,6 @@ def k_flash_causal_grouped(q, k, v):
 
 
 # ----------------------------------------------------------------------------- glue symbols (torch)
-
-def k_rope_apply(q, k, cos, sin):
-    _require_cuda_tensor(q, k)
-
-    def rotate_half(x):
-        return torch.stack((-x[..., 1::2], x[..., ::2]), dim=-1).flatten(-2)
-
-    while cos.ndim < q.ndim:
-        cos, sin = cos.unsqueeze(0), sin.unsqueeze(0)
-    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
-
-
-def k_qkv_grouped(x, wq, wk, wv, column_indices):
-    _require_cuda_tensor(x)
-    return x @ wq[:, column_indices], x @ wk[:, column_indices], x @ wv[:, column_indices]
-
-
-def k_out_proj_grouped(x, wo, row_indices):
-    _require_cuda_tensor(x)
-    return x @ wo[row_indices, :]
-
-
-def k_swiglu_grouped(x, wu, wg, wd, slab_indices):
-    _require_cuda_tensor(x)
-    return (x @ wu[:, slab_indices]) * F.silu(x @ wg[:, slab_indices]) @ wd[slab_indices, :]
-
 
 class PackedByRecipe:
     __slots__ = ("packed", "permutation", "inverse_permutation", "keys", "offsets", "unique_keys")
@@ -200,14 +262,6 @@ def k_unpack_from_recipe(packed, inverse_permutation):
     return packed[inverse_permutation]
 
 
-def k_macro_phi(h, h0, d_gain, v, u, bias, eps: float = 1e-5):
-    _require_cuda_tensor(h, h0)
-    normed = h * torch.rsqrt(h.float().pow(2).mean(dim=-1, keepdim=True) + eps).to(h.dtype)
-    pooled = normed.mean(dim=1, keepdim=True).expand_as(normed)
-    low = F.silu(torch.cat([normed, pooled, h0], dim=-1) @ v) @ u
-    return h + d_gain * h + low + bias
-
-
 def k_recurrent_exact_loop(step_fn, h, h0, depth: int, boundaries: set[int]):
     states: dict[int, torch.Tensor] = {}
     for t in range(depth):
@@ -222,10 +276,6 @@ def k_logits_shortlist(hidden, vocab_weight, shortlist):
     (fp32 logits from bf16 operands; the kernel's CE at position 0 is discarded here)."""
     _require_cuda_tensor(hidden, vocab_weight, shortlist)
     return hip_ops.shortlist_ce(hidden, vocab_weight, shortlist)[0]
-
-
-def k_cross_entropy_unreduced(logits, targets):
-    return F.cross_entropy(logits.flatten(0, -2), targets.flatten(), reduction="none").view_as(targets)
 
 
 def k_sample_audit_mask(p, seed: int):

@@ -32,7 +32,9 @@ class RMSNorm(nn.Module):
         self.eps = eps
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return K.k_fused_rmsnorm(x, self.weight, eps=self.eps)[0]
+        # bf16 output for the bf16 GEMMs that consume it (the reference's autocast casts there);
+        # the dtype-preserving boundary symbol is K.k_fused_rmsnorm
+        return hip_ops.rmsnorm(x, self.weight, self.eps)
 
 
 class Embedding(nn.Embedding):
@@ -120,6 +122,155 @@ class ClusterPoolSwiGLU(nn.Module):
         )
         self.last_ids, self.last_weights = ids, w
         return out
+
+
+class PackedDenseSwiGLU(nn.Module):
+    """Dense SwiGLU with row-oriented W_down (rte/layers.py:90-116): wug [2F, d], wdown_rows [F, d];
+    the flag use_triton_swiglu_backward is kept for API parity (both settings run the fused
+    HIP SwiGLU)."""
+
+    def __init__(self, dense: DenseSwiGLU):
+        super().__init__()
+        d_model, d_ff = dense.wug.in_features, dense.wd.in_features
+        self.wug = nn.Linear(d_model, 2 * d_ff, bias=False)
+        self.wdown_rows = nn.Parameter(torch.empty(d_ff, d_model))
+        self.use_triton_swiglu_backward = False
+        with torch.no_grad():
+            self.wug.weight.copy_(dense.wug.weight.detach())
+            self.wdown_rows.copy_(dense.wd.weight.detach().t().contiguous())
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        flat = x.reshape(-1, x.shape[-1])
+        out = hip_ops.dense_swiglu(flat, self.wug.weight, self.wdown_rows, None, wd_rows=True, out_f32=False)
+        return out.view(*x.shape[:-1], -1)
+
+
+class StaticClusterPoolSwiGLU(nn.Module):
+    """Static cluster-pool SwiGLU (rte/layers.py:119-220): tokens routed to fixed centres of their
+    SVD selector features, each cluster running its candidate pool of neurons gathered from the
+    dense weights every forward (the dense weights stay the source of truth).  Pools may overlap;
+    their gradients reach the dense rows through the deterministic segmented reduction."""
+
+    def __init__(self, dense: DenseSwiGLU, factors: dict, codebook: dict, *, rank: int, sparse_enabled: bool = True):
+        super().__init__()
+        self.wug = nn.Linear(dense.wug.in_features, dense.wug.out_features, bias=False)
+        self.wd = nn.Linear(dense.wd.in_features, dense.wd.out_features, bias=False)
+        self.wug.load_state_dict(dense.wug.state_dict())
+        self.wd.load_state_dict(dense.wd.state_dict())
+        self.rank = int(rank)
+        self.sparse_enabled = bool(sparse_enabled)
+        d_model = dense.wug.in_features
+        self.register_buffer("up_a", torch.empty(d_model, 0), persistent=False)
+        self.register_buffer("gate_a", torch.empty(d_model, 0), persistent=False)
+        self.register_buffer("centers", torch.empty(0, 0), persistent=False)
+        self.register_buffer("candidate_ids", torch.empty(0, 0, dtype=torch.long), persistent=False)
+        self.update_codebook(factors, codebook, rank=rank)
+
+    @torch.no_grad()
+    def update_codebook(self, factors: dict, codebook: dict, *, rank: int | None = None) -> None:
+        """rte/layers.py:150-181: selector factors truncated to the rank, centres, candidate ids."""
+        if rank is not None:
+            self.rank = int(rank)
+        rank = min(max(1, self.rank), int(factors["up_a"].shape[1]), int(factors["gate_a"].shape[1]))
+        self.rank = rank
+        dev, dt = self.wug.weight.device, self.wug.weight.dtype
+        self.up_a = factors["up_a"][:, :rank].detach().to(device=dev, dtype=dt)
+        self.gate_a = factors["gate_a"][:, :rank].detach().to(device=dev, dtype=dt)
+        self.centers = codebook["centers"].detach().to(device=dev, dtype=dt)
+        self.candidate_ids = codebook["candidate_ids"].detach().to(device=dev, dtype=torch.long)
+
+    def dense_forward(self, x: torch.Tensor) -> torch.Tensor:
+        flat = x.reshape(-1, x.shape[-1])
+        return hip_ops.dense_swiglu(flat, self.wug.weight, self.wd.weight, None, out_f32=False).view(
+            *x.shape[:-1], -1)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        from rte_amd.kernels import cluster_pool_ffn as CPF
+
+        if not self.sparse_enabled:
+            return self.dense_forward(x)
+        if self.candidate_ids.numel() == 0:
+            raise RuntimeError("StaticClusterPoolSwiGLU has no candidate pool")
+        flat = x.reshape(-1, x.shape[-1])
+        assignments = CPF.route_to_static_centers(flat, self.up_a[:, : self.rank], self.gate_a[:, : self.rank],
+                                                  self.centers)
+        up_w, gate_w = self.wug.weight.chunk(2, dim=0)
+        pools = CPF.prepare_cluster_pool_weights(up_w, gate_w, self.wd.weight.t(), self.candidate_ids)
+        out = CPF._run(flat, assignments, *pools)
+        return out.view(*x.shape[:-1], -1)
+
+
+class ActiveUnionSwiGLU(nn.Module):
+    """SwiGLU over the union of candidate neurons (rte/layers.py:223-281): the active rows of the
+    dense weights (sorted unique ids) gathered per forward, one fused SwiGLU over them."""
+
+    def __init__(self, dense: DenseSwiGLU, active_ids: torch.Tensor, *, sparse_enabled: bool = True):
+        super().__init__()
+        self.wug = nn.Linear(dense.wug.in_features, dense.wug.out_features, bias=False)
+        self.wd = nn.Linear(dense.wd.in_features, dense.wd.out_features, bias=False)
+        self.wug.load_state_dict(dense.wug.state_dict())
+        self.wd.load_state_dict(dense.wd.state_dict())
+        self.sparse_enabled = bool(sparse_enabled)
+        self.register_buffer("active_ids", torch.empty(0, dtype=torch.long), persistent=False)
+        self.update_active_ids(active_ids)
+
+    @torch.no_grad()
+    def update_active_ids(self, active_ids: torch.Tensor) -> None:
+        active_ids = active_ids.reshape(-1)
+        if active_ids.numel() == 0:
+            raise ValueError("active union must contain at least one neuron")
+        self.active_ids = torch.unique(active_ids.detach().to(device=self.wug.weight.device, dtype=torch.long),
+                                       sorted=True)
+
+    def dense_forward(self, x: torch.Tensor) -> torch.Tensor:
+        flat = x.reshape(-1, x.shape[-1])
+        return hip_ops.dense_swiglu(flat, self.wug.weight, self.wd.weight, None, out_f32=False).view(
+            *x.shape[:-1], -1)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if not self.sparse_enabled:
+            return self.dense_forward(x)
+        if self.active_ids.numel() == 0:
+            raise RuntimeError("ActiveUnionSwiGLU has no active neurons")
+        flat = x.reshape(-1, x.shape[-1])
+        ids = self.active_ids.to(flat.device)
+        d_ff = self.wd.in_features
+        wug = hip_ops.embedding(self.wug.weight, torch.cat([ids, ids + d_ff]))
+        down_rows = hip_ops.embedding(self.wd.weight.t(), ids)
+        out = hip_ops.dense_swiglu(flat, wug, down_rows, None, wd_rows=True, out_f32=False)
+        return out.view(*x.shape[:-1], -1)
+
+
+class PackedActiveUnionSwiGLU(nn.Module):
+    """Trainable packed active-union SwiGLU (rte/layers.py:284-339): the selected up/gate rows as
+    one parameter wug_active [2M, d], the selected down rows as wdown_active_rows [M, d]."""
+
+    def __init__(self, dense: DenseSwiGLU, active_ids: torch.Tensor):
+        super().__init__()
+        active_ids = active_ids.reshape(-1)
+        if active_ids.numel() == 0:
+            raise ValueError("packed active union must contain at least one neuron")
+        ids = torch.unique(active_ids.detach().to(device=dense.wug.weight.device, dtype=torch.long), sorted=True)
+        d_model, m = dense.wug.in_features, int(ids.numel())
+        self.d_ff_total = int(dense.wd.in_features)
+        self.wug_active = nn.Linear(d_model, 2 * m, bias=False)
+        self.wdown_active_rows = nn.Parameter(torch.empty(m, d_model))
+        self.use_triton_swiglu_backward = False
+        self.register_buffer("active_ids", ids, persistent=True)
+        with torch.no_grad():
+            up_w, gate_w = dense.wug.weight.detach().chunk(2, dim=0)
+            self.wug_active.weight.copy_(torch.cat([up_w.index_select(0, ids), gate_w.index_select(0, ids)]))
+            self.wdown_active_rows.copy_(dense.wd.weight.detach().t().index_select(0, ids).contiguous())
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        flat = x.reshape(-1, x.shape[-1])
+        out = hip_ops.dense_swiglu(flat, self.wug_active.weight, self.wdown_active_rows, None, wd_rows=True,
+                                   out_f32=False)
+        return out.view(*x.shape[:-1], -1)
+
+    @property
+    def active_m(self) -> int:
+        return int(self.active_ids.numel())
 
 
 def make_ffn(config: ModelConfig) -> nn.Module:

@@ -58,7 +58,7 @@ def head_logits_loss(hidden, vocab_weight, targets):
     """(logits, per-sample CE, token CE) with the HIP LM-head GEMM + fused CE kernels; targets
     may be None."""
     if targets is None:
-        return K.k_logits_full(hidden, vocab_weight), None, None
+        return hip_ops.linear(hidden, vocab_weight, out_f32=True), None, None
     logits, tok = hip_ops.lm_head_ce(hidden, vocab_weight, targets)
     return logits, tok.sum(dim=-1), tok
 
@@ -124,7 +124,7 @@ class RecursiveModel(nn.Module):
 
     def _coda_logits(self, h):
         hidden = self._coda_hidden(h)
-        return hidden, K.k_logits_full(hidden, self.vocab_weight)
+        return hidden, hip_ops.linear(hidden, self.vocab_weight, out_f32=True)
 
     def forward_exact_from_h0(self, h0, targets=None, return_states=False, return_loss_per_sample=False, *,
                               router_decisions: RouterOutput | None = None, fixed_recipe=None, fixed_depth=None):

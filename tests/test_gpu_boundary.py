@@ -1,0 +1,420 @@
+"""The reference's dispatch symbols and module backends on the HIP kernels, against the oracle
+or an fp32/fp64 restatement of the reference formula (rte/kernels/reference.py,
+rte/kernels/cluster_pool_ffn.py, rte/kernels/active_swiglu_triton.py, rte/layers.py:90-339).
+
+Tolerances: fp32 paths 1e-5 relative; bf16 paths 2e-2 relative (Frobenius); indices bit-exact."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import BF16_RTOL, FP32_RTOL, assert_rel, bf16_round
+from oracle import cluster_pool as CP
+from oracle import routing as R
+from oracle import swiglu as SW
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _hip():
+    from rte_amd import _lib
+
+    if not _lib.device_ready():
+        pytest.fail("HIP backend not ready on this GPU box (library or gfx950 device missing)")
+    yield
+
+
+def _np(t):
+    return t.detach().double().cpu().numpy()
+
+
+def _K():
+    from rte_amd.kernels import optimized
+
+    return optimized
+
+
+def _autocast():
+    return torch.autocast("cuda", dtype=torch.bfloat16)
+
+
+# ---------------------------------------------------------------- elementwise symbols, caller dtype
+
+@pytest.mark.parametrize("with_res", [False, True])
+def test_fused_rmsnorm_fp32_matches_reference_formula(with_res):
+    """k_fused_rmsnorm in fp32 (rte/kernels/reference.py:9-17): output dtype and values within
+    1e-5 of the fp64 formula, y returned only with a residual, gradients of x, residual, weight."""
+    K = _K()
+    g = torch.Generator().manual_seed(3)
+    x0 = torch.randn(5, 37, 256, generator=g, dtype=torch.float64)
+    r0 = torch.randn(5, 37, 256, generator=g, dtype=torch.float64)
+    w0 = 1 + 0.1 * torch.randn(256, generator=g, dtype=torch.float64)
+    gy = torch.randn(5, 37, 256, generator=g, dtype=torch.float64)
+    gr = torch.randn(5, 37, 256, generator=g, dtype=torch.float64)
+    x, w = x0.float().to(DEV).requires_grad_(), w0.float().to(DEV).requires_grad_()
+    r = r0.float().to(DEV).requires_grad_() if with_res else None
+    print(f"k_fused_rmsnorm fp32 residual={with_res}", flush=True)
+    out, y = K.k_fused_rmsnorm(x, w, r, eps=1e-5)
+    assert out.dtype == torch.float32 and (y is None) == (not with_res)
+    loss = (out.double() * gy.to(DEV)).sum() + ((y.double() * gr.to(DEV)).sum() if with_res else 0)
+    loss.backward()
+    xr, wr = x0.clone().requires_grad_(), w0.clone().requires_grad_()
+    rr = r0.clone().requires_grad_() if with_res else None
+    yr = xr if rr is None else xr + rr
+    ref = yr * torch.rsqrt(yr.pow(2).mean(-1, keepdim=True) + 1e-5) * wr
+    (ref * gy).sum().add((yr * gr).sum() if with_res else 0).backward()
+    assert_rel(_np(out), ref.detach().numpy(), FP32_RTOL, "rmsnorm out")
+    assert_rel(_np(x.grad), xr.grad.numpy(), FP32_RTOL, "rmsnorm dx")
+    assert_rel(_np(w.grad), wr.grad.numpy(), FP32_RTOL, "rmsnorm dw")
+    if with_res:
+        assert_rel(_np(y), yr.detach().numpy(), FP32_RTOL, "rmsnorm y")
+        assert_rel(_np(r.grad), rr.grad.numpy(), FP32_RTOL, "rmsnorm dres")
+
+
+def test_fused_rmsnorm_bf16_input():
+    """bf16 x with an fp32 weight returns fp32 (promote), bf16 rounding points as torch's."""
+    K = _K()
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(64, 512, generator=g).to(torch.bfloat16).to(DEV)
+    w = (1 + 0.1 * torch.randn(512, generator=g)).to(DEV)
+    out, y = K.k_fused_rmsnorm(x, w)
+    ref = (x * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-5).to(x.dtype)) * w
+    assert out.dtype == ref.dtype == torch.float32 and y is None
+    assert_rel(_np(out), _np(ref), 1e-2, "rmsnorm bf16")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rope_apply_matches_reference_formula(dtype):
+    """k_rope_apply (rte/kernels/reference.py:20-28) against the rotate_half formula, forward and
+    backward (the transpose rotation)."""
+    from oracle import attention as A
+
+    K = _K()
+    B, H, S, hd = 2, 4, 33, 64
+    g = torch.Generator().manual_seed(5)
+    q0 = torch.randn(B, H, S, hd, generator=g)
+    k0 = torch.randn(B, H, S, hd, generator=g)
+    inv = 1.0 / (10000.0 ** (torch.arange(0, hd, 2).float() / hd))
+    ang = torch.repeat_interleave(torch.outer(torch.arange(S).float(), inv), 2, -1)
+    cos, sin = ang.cos(), ang.sin()
+    gq, gk = torch.randn(B, H, S, hd, generator=g), torch.randn(B, H, S, hd, generator=g)
+    q = q0.to(dtype).to(DEV).requires_grad_()
+    k = k0.to(dtype).to(DEV).requires_grad_()
+    print(f"k_rope_apply {dtype}", flush=True)
+    qo, ko = K.k_rope_apply(q, k, cos.to(DEV).to(dtype), sin.to(DEV).to(dtype))
+    assert qo.dtype == dtype
+    ((qo.float() * gq.to(DEV)).sum() + (ko.float() * gk.to(DEV)).sum()).backward()
+    tol = FP32_RTOL if dtype == torch.float32 else BF16_RTOL
+    qr = torch.tensor(np.asarray(q0.to(dtype).double()), requires_grad=True)
+    kr = torch.tensor(np.asarray(k0.to(dtype).double()), requires_grad=True)
+
+    def rot(x):
+        return torch.stack((-x[..., 1::2], x[..., ::2]), dim=-1).flatten(-2)
+
+    c, s = cos.to(dtype).double(), sin.to(dtype).double()
+    qref, kref = qr * c + rot(qr) * s, kr * c + rot(kr) * s
+    ((qref * gq.double()).sum() + (kref * gk.double()).sum()).backward()
+    assert_rel(_np(qo), qref.detach().numpy(), tol, "rope q")
+    assert_rel(_np(ko), kref.detach().numpy(), tol, "rope k")
+    assert_rel(_np(q.grad), qr.grad.numpy(), tol, "rope dq")
+    assert_rel(_np(k.grad), kr.grad.numpy(), tol, "rope dk")
+    # the oracle's rotation agrees with the reference formula
+    np.testing.assert_allclose(A.rope_apply(q0.numpy(), cos.numpy(), sin.numpy()),
+                               (q0.double() * cos.double() + rot(q0.double()) * sin.double()).numpy(),
+                               rtol=1e-6, atol=1e-6)
+
+
+def test_cross_entropy_unreduced_matches_torch():
+    K = _K()
+    g = torch.Generator().manual_seed(6)
+    logits = (torch.randn(4, 9, 300, generator=g) * 3).to(DEV).requires_grad_()
+    tgt = torch.randint(0, 300, (4, 9), generator=g).to(DEV)
+    tgt[0, 0] = -100  # ignore_index
+    loss = K.k_cross_entropy_unreduced(logits, tgt)
+    gl = torch.randn(4, 9, generator=g).to(DEV)
+    (loss * gl).sum().backward()
+    lr = logits.detach().double().cpu().requires_grad_()
+    ref = torch.nn.functional.cross_entropy(lr.flatten(0, -2), tgt.cpu().flatten(), reduction="none").view(4, 9)
+    (ref * gl.cpu().double()).sum().backward()
+    assert_rel(_np(loss), ref.detach().numpy(), FP32_RTOL, "ce")
+    assert_rel(_np(logits.grad), lr.grad.numpy(), FP32_RTOL, "ce grad")
+
+
+# ---------------------------------------------------------------- matmul symbols (bf16 under autocast)
+
+def _bfr(t):
+    return torch.from_numpy(bf16_round(t.numpy().astype(np.float32))).double()
+
+
+def test_out_proj_grouped_reads_weight_rows_through_indices():
+    """k_out_proj_grouped(x, wo, rows) = x @ wo[rows, :] (rte/kernels/reference.py:58-59) with
+    repeated rows; the weight gradient of repeated rows adds up."""
+    K = _K()
+    g = torch.Generator().manual_seed(7)
+    T, d, n = 300, 256, 128
+    x0 = torch.randn(T, n, generator=g)
+    wo0 = torch.randn(d, d, generator=g) * 0.05
+    rows = torch.randint(0, d, (n,), generator=g)
+    rows[5] = rows[9]
+    gy = torch.randn(T, d, generator=g)
+    x = x0.to(DEV).requires_grad_()
+    wo = wo0.to(DEV).requires_grad_()
+    with _autocast():
+        y = K.k_out_proj_grouped(x, wo, rows.to(DEV))
+    assert y.dtype == torch.bfloat16
+    (y.float() * gy.to(DEV)).sum().backward()
+    xr, wr = _bfr(x0).requires_grad_(), _bfr(wo0).requires_grad_()
+    yr = xr @ wr[rows]
+    (yr * gy.double()).sum().backward()
+    assert_rel(_np(y), yr.detach().numpy(), BF16_RTOL, "out_proj y")
+    assert_rel(_np(x.grad), xr.grad.numpy(), BF16_RTOL, "out_proj dx")
+    assert_rel(_np(wo.grad), wr.grad.numpy(), BF16_RTOL, "out_proj dwo")
+
+
+def test_qkv_and_swiglu_symbols():
+    """k_qkv_dense / k_qkv_grouped / k_swiglu_dense / k_swiglu_grouped against fp64 of the
+    bf16-rounded operands (rte/kernels/reference.py:31-78), bf16 results under autocast; fp32
+    operands outside autocast are refused."""
+    K = _K()
+    g = torch.Generator().manual_seed(8)
+    T, d, m = 256, 128, 96
+    x0 = torch.randn(T, d, generator=g)
+    wq0, wk0, wv0 = (torch.randn(d, d, generator=g) * 0.05 for _ in range(3))
+    wu0, wg0 = (torch.randn(d, 4 * m, generator=g) * 0.05 for _ in range(2))
+    wd0 = torch.randn(4 * m, d, generator=g) * 0.05
+    cols = torch.randperm(d, generator=g)[:64]
+    slabs = torch.randperm(4 * m, generator=g)[:m]
+    x = x0.to(DEV)
+    with _autocast():
+        q, k, v = K.k_qkv_dense(x, wq0.to(DEV), wk0.to(DEV), wv0.to(DEV))
+        qg, kg, vg = K.k_qkv_grouped(x, wq0.to(DEV), wk0.to(DEV), wv0.to(DEV), cols.to(DEV))
+        sd = K.k_swiglu_dense(x, wu0.to(DEV), wg0.to(DEV), wd0.to(DEV))
+        sg = K.k_swiglu_grouped(x, wu0.to(DEV), wg0.to(DEV), wd0.to(DEV), slabs.to(DEV))
+    xb = _bfr(x0)
+    for got, w in ((q, wq0), (k, wk0), (v, wv0)):
+        assert got.dtype == torch.bfloat16
+        assert_rel(_np(got), (xb @ _bfr(w)).numpy(), BF16_RTOL, "qkv_dense")
+    for got, w in ((qg, wq0), (kg, wk0), (vg, wv0)):
+        assert_rel(_np(got), (xb @ _bfr(w)[:, cols]).numpy(), BF16_RTOL, "qkv_grouped")
+    silu = torch.nn.functional.silu
+    ref = (xb @ _bfr(wu0)) * silu(xb @ _bfr(wg0)) @ _bfr(wd0)
+    assert_rel(_np(sd), ref.numpy(), BF16_RTOL, "swiglu_dense")
+    refg = (xb @ _bfr(wu0)[:, slabs]) * silu(xb @ _bfr(wg0)[:, slabs]) @ _bfr(wd0)[slabs]
+    assert_rel(_np(sg), refg.numpy(), BF16_RTOL, "swiglu_grouped")
+    with pytest.raises(RuntimeError, match="bf16"):
+        K.k_qkv_dense(x, wq0.to(DEV), wk0.to(DEV), wv0.to(DEV))
+
+
+@pytest.mark.parametrize("per_sample", [False, True])
+def test_macro_phi_symbol(per_sample):
+    """k_macro_phi (rte/kernels/reference.py:111-124) with shared [3d, m] or per-sample [B, 3d, m]
+    factors, against an fp64 restatement with bf16-rounded GEMM operands."""
+    K = _K()
+    g = torch.Generator().manual_seed(9)
+    B, S, d, m = 3, 16, 64, 32
+    h = torch.randn(B, S, d, generator=g)
+    h0 = torch.randn(B, S, d, generator=g)
+    vs = (B, 3 * d, m) if per_sample else (3 * d, m)
+    us = (B, m, d) if per_sample else (m, d)
+    v = torch.randn(*vs, generator=g) * 0.1
+    u = torch.randn(*us, generator=g) * 0.1
+    dg, bias = torch.randn(d, generator=g) * 0.1, torch.randn(d, generator=g) * 0.1
+    with _autocast():
+        out = K.k_macro_phi(h.to(DEV), h0.to(DEV), dg.to(DEV), v.to(DEV), u.to(DEV), bias.to(DEV))
+    hd = h.double()
+    normed = hd * torch.rsqrt(hd.pow(2).mean(-1, keepdim=True) + 1e-5)
+    z = torch.cat([normed, normed.mean(1, keepdim=True).expand_as(normed), h0.double()], -1)
+    z = _bfr(z.float())
+    a = z @ _bfr(v)
+    low = _bfr(torch.nn.functional.silu(_bfr(a.float()).float())) @ _bfr(u)
+    ref = hd + dg.double() * hd + low + bias.double()
+    assert_rel(_np(out) - h.double().numpy(), (ref - hd).numpy(), BF16_RTOL, "macro_phi")
+
+
+# ---------------------------------------------------------------- module backends
+
+def _pool_case(seed, T=512, d=128, F=256, C=6, M=64):
+    rng = np.random.default_rng(seed)
+    x = bf16_round(rng.standard_normal((T, d)).astype(np.float32))
+    w_up = bf16_round((rng.standard_normal((F, d)) * 0.05).astype(np.float32))
+    w_gate = bf16_round((rng.standard_normal((F, d)) * 0.05).astype(np.float32))
+    w_down_rows = bf16_round((rng.standard_normal((F, d)) * 0.05).astype(np.float32))
+    cand = np.stack([rng.choice(F, M, replace=False) for _ in range(C)])  # overlapping pools
+    assign = rng.integers(0, C, T)
+    return rng, x, w_up, w_gate, w_down_rows, cand, assign
+
+
+def test_static_pack_gather_indices_bit_exact():
+    from rte_amd.kernels import cluster_pool_ffn as CPF
+
+    rng = np.random.default_rng(10)
+    a = rng.integers(0, 7, 1000)
+    a[a == 3] = 4  # an empty cluster
+    pack, flat, counts, mc = CPF.build_static_pack_gather_indices(torch.from_numpy(a).to(DEV), cluster_count=7)
+    rp, rf, rc, rmc = R.static_pack_gather(a, 7)
+    assert mc == rmc
+    np.testing.assert_array_equal(pack.cpu().numpy(), rp)
+    np.testing.assert_array_equal(flat.cpu().numpy(), rf)
+    np.testing.assert_array_equal(counts.cpu().numpy(), rc)
+
+
+def test_preindexed_pool_ffn_and_grad_scatter():
+    """prepare_cluster_pool_weights (overlapping candidate pools) + cluster_pool_ffn_forward_preindexed
+    against the reference's per-cluster loop oracle; the pool gradients against fp64 autograd of
+    that loop; scatter_cluster_pool_grads against np.add.at (fp32, 1e-5)."""
+    from rte_amd.kernels import cluster_pool_ffn as CPF
+
+    rng, x, w_up, w_gate, w_down_rows, cand, assign = _pool_case(11)
+    F, d = w_up.shape
+    dy = rng.standard_normal(x.shape)
+    tw = [torch.from_numpy(a).to(DEV).requires_grad_() for a in (w_up, w_gate, w_down_rows)]
+    pools = CPF.prepare_cluster_pool_weights(*tw, torch.from_numpy(cand).to(DEV))
+    pk, fg, _, _ = CPF.build_static_pack_gather_indices(torch.from_numpy(assign).to(DEV), cluster_count=cand.shape[0])
+    tx = torch.from_numpy(x).to(DEV).requires_grad_()
+    with _autocast():
+        out = CPF.cluster_pool_ffn_forward_preindexed(tx, pk, fg, *pools)
+    assert out.dtype == torch.bfloat16
+    out.float().backward(torch.from_numpy(dy).float().to(DEV))
+    ref_pools = CP.prepare_pools(w_up, w_gate, w_down_rows, cand)
+    assert_rel(_np(out), CP.cluster_pool_reference_loop(x, assign, *ref_pools), BF16_RTOL, "preindexed y")
+    # fp64 autograd of the reference loop through the row gathers
+    tr = [torch.tensor(a, dtype=torch.float64, requires_grad=True) for a in (w_up, w_gate, w_down_rows)]
+    txr = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    ids = torch.from_numpy(cand)
+    outr = torch.zeros(x.shape, dtype=torch.float64)
+    for c in range(cand.shape[0]):
+        tok = torch.from_numpy(np.nonzero(assign == c)[0])
+        up = txr[tok] @ tr[0][ids[c]].T
+        gate = txr[tok] @ tr[1][ids[c]].T
+        outr = outr.index_add(0, tok, (up * torch.nn.functional.silu(gate)) @ tr[2][ids[c]])
+    (outr * torch.from_numpy(dy)).sum().backward()
+    assert_rel(_np(tx.grad), txr.grad.numpy(), BF16_RTOL, "preindexed dx")
+    for name, a, b in zip(("dup", "dgate", "ddown"), tw, tr):
+        assert_rel(_np(a.grad), b.grad.numpy(), BF16_RTOL, f"preindexed {name}")
+    # scatter of pool gradients into dense rows
+    C, M = cand.shape
+    gp = [rng.standard_normal(s).astype(np.float32) for s in ((C, d, M), (C, d, M), (C, M, d))]
+    got = CPF.scatter_cluster_pool_grads(torch.from_numpy(cand).to(DEV), *(torch.from_numpy(a).to(DEV) for a in gp),
+                                         d_ff=F)
+    for i, (gg, arr) in enumerate(zip(got, (np.transpose(gp[0], (0, 2, 1)), np.transpose(gp[1], (0, 2, 1)), gp[2]))):
+        want = np.zeros((F, d))
+        np.add.at(want, cand.reshape(-1), arr.reshape(-1, d).astype(np.float64))
+        assert_rel(_np(gg), want, FP32_RTOL, f"scatter {i}")
+
+
+def test_forward_from_assignments_capacity_and_errors():
+    """Inference path with a capacity: the tokens of a cluster beyond its first cap (ascending
+    token order) give zero rows and set the overflow flag; grads are refused."""
+    from rte_amd.kernels import cluster_pool_ffn as CPF
+
+    rng, x, w_up, w_gate, w_down_rows, cand, assign = _pool_case(12)
+    pools = [torch.from_numpy(p.copy()).to(DEV) for p in CP.prepare_pools(w_up, w_gate, w_down_rows, cand)]
+    tx = torch.from_numpy(x).to(DEV)
+    ta = torch.from_numpy(assign).to(DEV)
+    cap = int(np.bincount(assign).min())
+    with torch.no_grad():
+        out, of = CPF.cluster_pool_ffn_forward_from_assignments(tx, ta, *pools, max_tokens_per_cluster=cap,
+                                                                return_overflow=True)
+    full = CP.cluster_pool_reference_loop(x, assign, *[p.cpu().numpy() for p in pools])
+    keep = np.zeros(len(assign), bool)
+    for c in range(cand.shape[0]):
+        keep[np.nonzero(assign == c)[0][:cap]] = True
+    assert int(of) == 1
+    assert np.all(_np(out)[~keep] == 0)
+    assert_rel(_np(out)[keep], full[keep], BF16_RTOL, "capacity y")
+    with pytest.raises(RuntimeError, match="inference/eval only"):
+        CPF.cluster_pool_ffn_forward_from_assignments(tx, ta, pools[0].requires_grad_(), pools[1], pools[2])
+
+
+def test_route_to_static_centers_bit_exact():
+    """route_to_static_centers on the kernel's selector features against the oracle's argmax."""
+    from rte_amd.kernels import cluster_pool_ffn as CPF
+    from rte_amd.kernels import hip_ops as H
+
+    rng = np.random.default_rng(13)
+    T, d, r, C = 4096, 256, 16, 64
+    x = torch.from_numpy(rng.standard_normal((T, d)).astype(np.float32)).to(DEV)
+    up_a = torch.from_numpy((rng.standard_normal((d, r)) * 0.1).astype(np.float32)).to(DEV)
+    gate_a = torch.from_numpy((rng.standard_normal((d, r)) * 0.1).astype(np.float32)).to(DEV)
+    centers = rng.standard_normal((C, 2 * r)).astype(np.float32)
+    centers[9] = centers[4]
+    got = CPF.route_to_static_centers(x, up_a, gate_a, torch.from_numpy(centers).to(DEV))
+    assert got.dtype == torch.long
+    q = H.gemm(x.to(torch.bfloat16), H.cast_bf16(torch.cat([up_a, gate_a], 1).t().contiguous()), out_f32=True)
+    want, scores = R.static_centers(q.cpu().numpy(), centers)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
+    assert 9 not in got.cpu().numpy()
+
+
+def test_triton_packed_swiglu_mirror_with_padding():
+    """triton_packed_swiglu_ffn (rte/kernels/active_swiglu_triton.py:105-118) with a width that is not
+    a multiple of 32 (zero-padded inside), forward and backward against the oracle."""
+    from rte_amd.kernels import active_swiglu_triton as AS
+
+    rng = np.random.default_rng(14)
+    T, d, M = 384, 128, 72
+    x = bf16_round(rng.standard_normal((T, d)).astype(np.float32))
+    wug = bf16_round((rng.standard_normal((2 * M, d)) * 0.05).astype(np.float32))
+    wdr = bf16_round((rng.standard_normal((M, d)) * 0.05).astype(np.float32))
+    dy = bf16_round(rng.standard_normal((T, d)).astype(np.float32))
+    tx, tw, td = (torch.from_numpy(a).to(DEV).requires_grad_() for a in (x, wug, wdr))
+    with _autocast():
+        y = AS.triton_packed_swiglu_ffn(tx, tw, td)
+    y.float().backward(torch.from_numpy(dy).to(DEV))
+    ref, cache = SW.dense_swiglu_fwd(x, wug, wdr, wd_rows=True)
+    assert_rel(_np(y), ref, BF16_RTOL, "packed y")
+    dx, dwug, dwd = SW.dense_swiglu_bwd(dy, x, wug, wdr, cache, wd_rows=True)
+    assert_rel(_np(tx.grad), dx, BF16_RTOL, "packed dx")
+    assert_rel(_np(tw.grad), dwug, BF16_RTOL, "packed dwug")
+    assert_rel(_np(td.grad), dwd, BF16_RTOL, "packed dwd")
+
+
+def test_static_cluster_pool_layer_overlapping_pools():
+    """StaticClusterPoolSwiGLU (rte/layers.py:119-220) end to end with overlapping candidate pools:
+    output against the loop oracle on the kernel's routing, dense-weight gradients against fp64
+    autograd of the gathered-pool formulation (duplicated rows summed)."""
+    from rte_amd.config import ModelConfig
+    from rte_amd.kernels import cluster_pool_ffn as CPF
+    from rte_amd.layers import DenseSwiGLU, StaticClusterPoolSwiGLU
+
+    cfg = ModelConfig(topology="dense", vocab_size=64, d_model=128, n_heads=4, d_ff=256, n_dense_layers=1,
+                      n_prelude=1, n_coda=1, t_max=1, depth_choices=[1], attn_banks=1, ffn_banks=1, head_groups=4,
+                      ffn_groups=4, active_head_groups=1, active_ffn_groups=1, recipe_count=2)
+    torch.manual_seed(15)
+    dense = DenseSwiGLU(cfg)
+    with torch.no_grad():
+        dense.wug.weight.copy_(torch.from_numpy(bf16_round(dense.wug.weight.numpy())))
+        dense.wd.weight.copy_(torch.from_numpy(bf16_round(dense.wd.weight.numpy())))
+    rng = np.random.default_rng(15)
+    C, M, r = 5, 64, 8
+    cand = np.stack([rng.choice(256, M, replace=False) for _ in range(C)])
+    factors = {"up_a": torch.randn(128, r) * 0.1, "gate_a": torch.randn(128, r) * 0.1}
+    codebook = {"centers": torch.randn(C, 2 * r), "candidate_ids": torch.from_numpy(cand)}
+    layer = StaticClusterPoolSwiGLU(dense, factors, codebook, rank=r).to(DEV)
+    x = bf16_round(rng.standard_normal((2, 150, 128)).astype(np.float32))
+    dy = rng.standard_normal((2, 150, 128))
+    tx = torch.from_numpy(x).to(DEV)
+    out = layer(tx)
+    out.float().backward(torch.from_numpy(dy).float().to(DEV))
+    assign = CPF.route_to_static_centers(tx.reshape(-1, 128), layer.up_a, layer.gate_a, layer.centers).cpu().numpy()
+    wug = dense.wug.weight.detach().double()
+    wd = dense.wd.weight.detach().double()
+    tw = wug.clone().requires_grad_()
+    td = wd.clone().requires_grad_()
+    xf = torch.from_numpy(x.reshape(-1, 128)).double()
+    outr = torch.zeros_like(xf)
+    ids = torch.from_numpy(cand)
+    for c in range(C):
+        tok = torch.from_numpy(np.nonzero(assign == c)[0])
+        up = xf[tok] @ tw[:256][ids[c]].T
+        gate = xf[tok] @ tw[256:][ids[c]].T
+        outr = outr.index_add(0, tok, (up * torch.nn.functional.silu(gate)) @ td.t()[ids[c]])
+    (outr * torch.from_numpy(dy.reshape(-1, 128))).sum().backward()
+    assert_rel(_np(out).reshape(-1, 128), outr.detach().numpy(), BF16_RTOL, "static pool y")
+    assert_rel(_np(layer.wug.weight.grad), tw.grad.numpy(), BF16_RTOL, "static pool dwug")
+    assert_rel(_np(layer.wd.weight.grad), td.grad.numpy(), BF16_RTOL, "static pool dwd")

@@ -423,3 +423,43 @@ def test_rope_tables_shorter_than_sequence_are_refused():
         hip_ops.qkv_rope(x, w, cos, cos, H)
     with pytest.raises(ValueError, match="do not cover"):
         hip_ops.qkv_rope_attention(x, w, cos, cos, H)
+
+
+def test_matmul_symbols_refuse_fp32_outside_autocast():
+    """The matmul dispatch symbols compute with bf16 operands: fp32 operands outside a bf16
+    autocast region are refused (no silent bf16 numerics for an fp32 caller)."""
+    from rte_amd.kernels import optimized
+
+    a, b = torch.zeros(2, 2), torch.zeros(2, 2)
+    with pytest.raises(RuntimeError, match="bf16"):
+        optimized._mm_dtype("k_qkv_dense", a, b)
+    assert optimized._mm_dtype("k_qkv_dense", a.bfloat16(), b.bfloat16()) == torch.bfloat16
+    with torch.autocast("cpu", dtype=torch.bfloat16):
+        with pytest.raises(RuntimeError, match="bf16"):  # only a ROCm bf16 autocast region counts
+            optimized._mm_dtype("k_qkv_dense", a, b)
+
+
+def test_backend_modules_fail_loudly_without_device():
+    """The module backends mirror the reference's names and raise without the HIP backend (no CPU
+    fallback path)."""
+    from rte_amd import _lib
+    from rte_amd.kernels import active_swiglu_triton as AS
+    from rte_amd.kernels import cluster_pool_ffn as CPF
+    from rte_amd.kernels import optimized
+
+    if _lib.device_ready():
+        pytest.skip("a ROCm device is present")
+    assert not CPF.available() and not AS.available()
+    x = torch.zeros(8, 16)
+    with pytest.raises(RuntimeError):
+        CPF.cluster_pool_ffn_forward_from_assignments(x, torch.zeros(8, dtype=torch.long), torch.zeros(2, 16, 32),
+                                                      torch.zeros(2, 16, 32), torch.zeros(2, 32, 16))
+    with pytest.raises(RuntimeError, match="HIP"):
+        AS.triton_packed_swiglu_ffn(x, torch.zeros(64, 16), torch.zeros(32, 16))
+    with pytest.raises(RuntimeError, match="HIP backend is required"):
+        optimized.k_rope_apply(torch.zeros(1, 2, 4, 8), torch.zeros(1, 2, 4, 8), torch.zeros(4, 8), torch.zeros(4, 8))
+    with pytest.raises(ValueError):
+        CPF.build_static_pack_gather_indices(torch.zeros(2, 2, dtype=torch.long), cluster_count=2)
+    st = optimized.backend_status()
+    assert st["torch_symbols"] == ["k_metrics_reduce", "k_pack_by_recipe", "k_recurrent_exact_loop",
+                                   "k_sample_audit_mask", "k_unpack_from_recipe"]

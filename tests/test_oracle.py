@@ -963,3 +963,28 @@ def test_recipe_templates_enumerated_and_balanced(case):
     assert all(a.max() - a.min() == 0 for a in counts.values())
     if hasattr(bank, "validate_balance"):
         assert all(v == 0 for v in bank.validate_balance().values())
+
+
+def test_static_centers_brute_force_and_invariants():
+    """route_to_static_centers (rte/kernels/cluster_pool_ffn.py:129-140) restated: a per-token
+    loop with math.sqrt gives the same choice; scaling a token's features by a positive factor
+    changes nothing (the features are normalised); equal centres go to the lower index; k = 1
+    top-k of the scores agrees."""
+    import math
+
+    rng = _rng(80)
+    q = rng.standard_normal((200, 12))
+    centers = rng.standard_normal((9, 12))
+    centers[7] = centers[2]  # a tie: index 2 wins
+    ids, scores = R.static_centers(q, centers)
+    for t in range(q.shape[0]):
+        n = math.sqrt(sum(v * v for v in q[t]))
+        best, bi = -math.inf, -1
+        for c in range(centers.shape[0]):
+            sc = sum(q[t, j] / n * centers[c, j] for j in range(12))
+            if sc > best:
+                best, bi = sc, c
+        assert ids[t] == bi
+    np.testing.assert_array_equal(R.static_centers(q * rng.uniform(0.1, 10.0, (200, 1)), centers)[0], ids)
+    assert 7 not in ids
+    np.testing.assert_array_equal(R.route_topk(scores.astype(np.float32), 1)[0][:, 0], ids)
