@@ -215,6 +215,32 @@ int rte_svd_ffn_bwd(const void* dy, const void* x, int T, int d, int F, int r, c
                     float* dv_ug, float* dv_dn, float* dus_dn, void* workspace, size_t workspace_bytes,
                     void* stream);
 
+/* ---- SVD-factor sparse SwiGLU FFN, per-token candidates (SVDFactorSparseFFN, rte/layers.py:342-643,
+ *      modes mask / slots; the device driver rte/kernels/svd_sparse_ffn_triton.py:480-714) ----
+ * Selector: a_ug [T, 2r] = x @ us_ug (us_ug bf16 [d, 2r] = [A_up | A_gate], the rank-r factors
+ * U S of refresh_svd), ug [T, 2F] = [a_up B_up | a_gate B_gate] (v_ug bf16 [2F, r] = [B_up^T ;
+ * B_gate^T], interleaved per 64 as rte_svd_ffn_fwd), z_hat [T, F] (workspaces, bf16).
+ * Per token: the top up_m of |up_hat| w, top gate_m of |silu(gate_hat)| w and top product_m of
+ * |up_hat silu(gate_hat)| w (w = wd_norm f32 [F] = ||W_down row||) united; fewer than top_k
+ * candidates: the top top_k of the product scores are added; activations u = <x, W_up[c]>,
+ * g = <x, W_gate[c]> (exact = 1) or the selector's (exact = 0); the top top_k of |u silu(g)| w
+ * are selected; out [T, d] (f32 if out_f32 else bf16) = sum of u silu(g) W_down[c] over them.
+ * product_only = 1: the selected are the top top_k of the product scores (approximate activations).
+ * Every top-m takes the larger scores first, then ties by lower neuron id (NaN ranks first).
+ * sel_ids int32 / sel_u / sel_g f32 [T, top_k] (ascending id; -1 / 0 pads), n_cand int32 [T]
+ * (optional).  w_up, w_gate, w_down bf16 [F, d] (rows = neurons).  F % 64, d % 8, r % 8 == 0.
+ * bwd: dout bf16 [T, d] -> dx bf16 [T, d], z = u silu(g), du = dz silu(g), dg = dz u silu'(g)
+ * (f32 [T, top_k], dz = <dout, W_down[c]>); the weight gradients are rte_segment_reduce_rows
+ * keyed by sel_ids: dW_down rows (w = z, rows = dout), dW_up (w = du, rows = x), dW_gate (w = dg). */
+int rte_svd_sparse_fwd(const void* x, int T, int d, int F, int r, const void* us_ug, const void* v_ug,
+                       const void* w_up, const void* w_gate, const void* w_down, const float* wd_norm, int up_m,
+                       int gate_m, int product_m, int top_k, int exact, int product_only, void* a_ug, void* ug,
+                       void* z_hat, void* out, int out_f32, int32_t* sel_ids, float* sel_u, float* sel_g,
+                       int32_t* n_cand, void* stream);
+int rte_svd_sparse_bwd(const void* dout, int T, int d, int top_k, const void* w_up, const void* w_gate,
+                       const void* w_down, const int32_t* sel_ids, const float* sel_u, const float* sel_g, void* dx,
+                       float* z, float* du, float* dg, void* stream);
+
 /* ---- RMSNorm (rte/kernels/reference.py:9-17, rte/layers.py:26-33) ----
  * out bf16 = bf16(x * rsqrt(mean(x^2) + eps) * w), rstd [T] f32 saved for backward. */
 int rte_rmsnorm_fwd(const float* x, const float* w, int T, int d, float eps, void* out, float* rstd,

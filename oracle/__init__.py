@@ -30,6 +30,10 @@ How each function is pinned (tests/test_oracle.py):
                              round rms values; u = gain = 0 closed form; tanh bound; per-key
                              locality and permutation equivariance
   macro.grouped_linear*      explicit loop + torch autograd
+  router.router              torch autograd-free restatement checked against nn.Linear / softmax /
+                             argmax run with torch on the CPU (same weights), entropies and
+                             expected depth by hand on a 2-class case
+  router.factorized_topk     brute-force enumeration of the (bank, bank, slot, slot) tuples
   banked.recipe_templates    two hand-enumerated recipe tables (every recipe's banks and
                              groups) with zero balance spread; recipe 0 == dense bank
 """

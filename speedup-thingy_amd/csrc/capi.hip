@@ -9,6 +9,13 @@
 
 namespace rte {
 const char* last_error();
+int svd_sparse_select(const bf16* x, const bf16* ug, const bf16* w_up, const bf16* w_gate, const bf16* w_down,
+                      const float* wdn, int T, int d, int F, int up_m, int gate_m, int product_m, int top_k,
+                      int exact, int product_only, void* out, int out_f32, int32_t* sel_ids, float* sel_u,
+                      float* sel_g, int32_t* n_cand, hipStream_t s);
+int svd_sparse_bwd(const bf16* dout, const bf16* w_up, const bf16* w_gate, const bf16* w_down, const int32_t* sel_ids,
+                   const float* sel_u, const float* sel_g, int T, int d, int top_k, bf16* dx, float* z, float* du,
+                   float* dg, hipStream_t s);
 int route_topk(const float* logits, int T, int C, int k, int32_t* ids, float* weights, hipStream_t s);
 size_t pack_workspace_bytes(int P, int C);
 int pack_pairs(const int32_t* cl, int P, int C, int k, const float* w, int32_t* offsets,
@@ -569,6 +576,52 @@ int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const in
 //   ug   = [a_up V_up^T | a_gate V_gate^T]  [T, 2F] (interleaved per 64), z = up * silu(gate)
 //   b    = z @ V_dn                         [T, r]
 //   y    = resid + b @ us_dn^T              [T, d]
+
+int rte_svd_sparse_fwd(const void* x, int T, int d, int F, int r, const void* us_ug, const void* v_ug,
+                       const void* w_up, const void* w_gate, const void* w_down, const float* wd_norm, int up_m,
+                       int gate_m, int product_m, int top_k, int exact, int product_only, void* a_ug, void* ug,
+                       void* z_hat, void* out, int out_f32, int32_t* sel_ids, float* sel_u, float* sel_g,
+                       int32_t* n_cand, void* stream) {
+  RTE_REQUIRE(r % 8 == 0 && F % 64 == 0 && d % 8 == 0, "svd_sparse: need r %% 8, F %% 64, d %% 8 == 0");
+  if (T == 0) return 0;
+  {
+    GemmArgs p;  // selector codes a_ug = x @ [A_up | A_gate]
+    p.M = T;
+    p.N = 2 * r;
+    p.K = d;
+    p.a = plain(x, d);
+    p.b = plain(us_ug, 2 * r);
+    p.b_t = 1;
+    p.epi.c = a_ug;
+    p.epi.ldc = 2 * r;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
+  }
+  {
+    GemmArgs p;  // approximate activations up_hat | gate_hat (interleaved) and z_hat
+    p.M = T;
+    p.N = 2 * F;
+    p.K = r;
+    p.a = plain(a_ug, 2 * r);
+    p.a_koff2 = r;
+    p.b = plain(v_ug, r);
+    p.b.ilv = F;
+    p.epi.ug = B16(ug);
+    p.epi.ld_ug = 2 * F;
+    p.epi.z = B16(z_hat);
+    p.epi.ld_z = F;
+    RTE_TRY(gemm_launch(p, EPI_SWIGLU_FWD, S(stream)));
+  }
+  return svd_sparse_select(B16(x), B16(ug), B16(w_up), B16(w_gate), B16(w_down), wd_norm, T, d, F, up_m, gate_m,
+                           product_m, top_k, exact, product_only, out, out_f32, sel_ids, sel_u, sel_g, n_cand,
+                           S(stream));
+}
+
+int rte_svd_sparse_bwd(const void* dout, int T, int d, int top_k, const void* w_up, const void* w_gate,
+                       const void* w_down, const int32_t* sel_ids, const float* sel_u, const float* sel_g, void* dx,
+                       float* z, float* du, float* dg, void* stream) {
+  return svd_sparse_bwd(B16(dout), B16(w_up), B16(w_gate), B16(w_down), sel_ids, sel_u, sel_g, T, d, top_k, B16(dx),
+                        z, du, dg, S(stream));
+}
 
 int rte_svd_ffn_fwd(const void* x, int T, int d, int F, int r, const void* us_ug, const void* v_ug,
                     const void* v_dn, const void* us_dn, const float* resid, void* a_ug, void* ug, void* z,

@@ -943,14 +943,60 @@ class LinearFn(torch.autograd.Function):
     def backward(ctx, dout):
         xb, wb = ctx.saved_tensors
         shape, x_dt, w_dt = ctx.meta
-        db = cast_bf16(dout.reshape(-1, wb.shape[0]))
+        N = wb.shape[0]
+        db = cast_bf16(dout.reshape(-1, N))
+        n8 = (N + 7) // 8 * 8  # both backward GEMMs reduce over or read N in 8-element vectors
+        if n8 != N:
+            db = torch.nn.functional.pad(db, (0, n8 - N))
+            wb = torch.nn.functional.pad(wb, (0, 0, 0, n8 - N))
         dx = gemm(db, wb, b_t=True)                              # [T, K]
-        dw = gemm(db, xb, a_t=True, b_t=True, out_f32=True)      # [N, K]
+        dw = gemm(db, xb, a_t=True, b_t=True, out_f32=True)[:N]  # [N, K]
         return dx.view(shape).to(x_dt), dw.to(w_dt), None
 
 
 def linear(x, w, *, out_f32: bool = True):
     return LinearFn.apply(x, w, out_f32)
+
+
+class LinearBiasFn(torch.autograd.Function):
+    """out = x @ W^T + b (nn.Linear with bias) on the MFMA GEMM: the bias is added in the GEMM
+    epilogue as a broadcast residual row (fp32); the backward is two GEMMs and a column sum."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, out_f32: bool):
+        _lib.require_device_tensors("linear_bias", x, w, b)
+        shape = x.shape
+        xb = x.reshape(-1, shape[-1]).contiguous().to(BF16)
+        wb = cast_bf16(w)
+        M, N, K = xb.shape[0], wb.shape[0], xb.shape[1]
+        bias = b.detach().reshape(N).contiguous().to(F32)
+        out = torch.empty((M, N), dtype=F32 if out_f32 else BF16, device=x.device)
+        wsp, wsn = _gemm_ws(M, N, K, x.device)
+        call("rte_gemm_bf16", ptr(xb), K, 0, None, ptr(wb), K, 0, None, ptr(out), N, int(out_f32), M, N, K, 1.0, 0.0,
+             ptr(bias), 0, wsp, wsn, _s())
+        ctx.save_for_backward(xb, wb)
+        ctx.meta = (shape, x.dtype, w.dtype, b.dtype)
+        return out.view(*shape[:-1], N)
+
+    @staticmethod
+    def backward(ctx, dout):
+        xb, wb = ctx.saved_tensors
+        shape, x_dt, w_dt, b_dt = ctx.meta
+        N = wb.shape[0]
+        d2 = dout.reshape(-1, N)
+        db = cast_bf16(d2)
+        n8 = (N + 7) // 8 * 8  # both backward GEMMs reduce over or read N in 8-element vectors
+        if n8 != N:
+            db = torch.nn.functional.pad(db, (0, n8 - N))
+            wb = torch.nn.functional.pad(wb, (0, 0, 0, n8 - N))
+        dx = gemm(db, wb, b_t=True)                              # [M, K] = dout @ W
+        dw = gemm(db, xb, a_t=True, b_t=True, out_f32=True)[:N]  # [N, K] = dout^T @ x
+        dbias = d2.float().sum(0)
+        return dx.view(shape).to(x_dt), dw.to(w_dt), dbias.to(b_dt), None
+
+
+def linear_bias(x, w, b, *, out_f32: bool = True):
+    return LinearBiasFn.apply(x, w, b, out_f32)
 
 
 # ----------------------------------------------------------------------------- LM head + cross-entropy
@@ -1688,4 +1734,86 @@ class CrossEntropyFn(torch.autograd.Function):
 
 def cross_entropy(logits, targets):
     return CrossEntropyFn.apply(logits, targets)
+
+
+# ----------------------------------------------------------------------------- SVD-factor sparse FFN
+
+class SVDSparseFn(torch.autograd.Function):
+    """Per-token sparse SwiGLU with SVD-factor candidate retrieval and exact rerank
+    (rte/layers.py:446-643): the selector GEMMs, one workgroup per token for the candidate union,
+    activations, rerank and down-sum; the backward is one workgroup per token for dx and the
+    selected activations' gradients, and three fixed-order segmented reductions keyed by the
+    selected neuron ids for the weight rows."""
+
+    @staticmethod
+    def forward(ctx, x, w_up, w_gate, w_down, us_ug, v_ug, wd_norm, up_m: int, gate_m: int, product_m: int,
+                top_k: int, exact: bool, product_only: bool, out_dtype):
+        _lib.require_device_tensors("svd_sparse_ffn", x, w_up, w_gate, w_down, us_ug, v_ug, wd_norm)
+        shape = x.shape
+        d = shape[-1]
+        xb = x.reshape(-1, d).contiguous().to(BF16)
+        T = xb.shape[0]
+        F = w_up.shape[0]
+        r2 = us_ug.shape[1]
+        wub, wgb, wdb = cast_bf16(w_up), cast_bf16(w_gate), cast_bf16(w_down)
+        usb, vb = cast_bf16(us_ug), cast_bf16(v_ug)
+        dev = x.device
+        a_ug = torch.empty((T, r2), dtype=BF16, device=dev)
+        ug = torch.empty((T, 2 * F), dtype=BF16, device=dev)
+        zh = torch.empty((T, F), dtype=BF16, device=dev)
+        out = torch.empty((T, d), dtype=out_dtype, device=dev)
+        sel = torch.empty((T, top_k), dtype=torch.int32, device=dev)
+        su = torch.empty((T, top_k), dtype=F32, device=dev)
+        sg = torch.empty((T, top_k), dtype=F32, device=dev)
+        nc = torch.empty((T,), dtype=torch.int32, device=dev)
+        call("rte_svd_sparse_fwd", ptr(xb), T, d, F, r2 // 2, ptr(usb), ptr(vb), ptr(wub), ptr(wgb), ptr(wdb),
+             ptr(wd_norm.contiguous().to(F32)), int(up_m), int(gate_m), int(product_m), int(top_k), int(exact),
+             int(product_only), ptr(a_ug), ptr(ug), ptr(zh), ptr(out), int(out_dtype == F32), ptr(sel), ptr(su),
+             ptr(sg), ptr(nc), _s())
+        ctx.save_for_backward(xb, wub, wgb, wdb, sel, su, sg)
+        ctx.meta = (shape, F, top_k, x.dtype, [t.dtype for t in (w_up, w_gate, w_down)])
+        ctx.mark_non_differentiable(sel, nc)
+        ctx.set_materialize_grads(False)
+        return out.view(shape), sel.view(*shape[:-1], top_k), nc.view(shape[:-1])
+
+    @staticmethod
+    def backward(ctx, dout, _dsel, _dnc):
+        if dout is None:
+            return (None,) * 14
+        xb, wub, wgb, wdb, sel, su, sg = ctx.saved_tensors
+        shape, F, K, x_dt, w_dts = ctx.meta
+        T, d = xb.shape
+        dev = xb.device
+        db = dout.reshape(T, d).contiguous().to(BF16)
+        dx = torch.empty((T, d), dtype=BF16, device=dev)
+        z = torch.empty((T, K), dtype=F32, device=dev)
+        du = torch.empty((T, K), dtype=F32, device=dev)
+        dg = torch.empty((T, K), dtype=F32, device=dev)
+        call("rte_svd_sparse_bwd", ptr(db), T, d, K, ptr(wub), ptr(wgb), ptr(wdb), ptr(sel), ptr(su), ptr(sg),
+             ptr(dx), ptr(z), ptr(du), ptr(dg), _s())
+        keys = sel.reshape(-1)
+        nia = ctx.needs_input_grad
+        dwu = segment_reduce_rows(keys, F, xb, w=du, row_div=K) if nia[1] else None
+        dwg = segment_reduce_rows(keys, F, xb, w=dg, row_div=K) if nia[2] else None
+        dwd = segment_reduce_rows(keys, F, db, w=z, row_div=K) if nia[3] else None
+        return (dx.view(shape).to(x_dt), None if dwu is None else dwu.to(w_dts[0]),
+                None if dwg is None else dwg.to(w_dts[1]), None if dwd is None else dwd.to(w_dts[2]),
+                None, None, None, None, None, None, None, None, None, None)
+
+
+def svd_sparse_ffn(x, w_up, w_gate, w_down, up_a, up_b, gate_a, gate_b, *, up_m: int, gate_m: int, product_m: int,
+                   top_k: int, exact: bool = True, product_only: bool = False, wd_norm=None, out_dtype=None):
+    """(out, selected ids, candidate counts) of the SVD-factor sparse FFN.  up_a / gate_a [d, r],
+    up_b / gate_b [r, F] (refresh_svd's factors); w_* [F, d].  The rank is zero-padded to a multiple
+    of 8 (zero factor columns change no score)."""
+    r = up_a.shape[1]
+    pad = (-r) % 8
+    us_ug = torch.cat([up_a, up_a.new_zeros(up_a.shape[0], pad), gate_a, gate_a.new_zeros(gate_a.shape[0], pad)], 1)
+    v_ug = torch.cat([torch.cat([up_b.t(), up_b.new_zeros(up_b.shape[1], pad)], 1),
+                      torch.cat([gate_b.t(), gate_b.new_zeros(gate_b.shape[1], pad)], 1)], 0)
+    if wd_norm is None:
+        wd_norm = w_down.detach().float().norm(dim=-1)
+    out_dtype = out_dtype or (BF16 if x.dtype == BF16 else F32)
+    return SVDSparseFn.apply(x, w_up, w_gate, w_down, us_ug.detach(), v_ug.detach(), wd_norm, up_m, gate_m,
+                             product_m, top_k, exact, product_only, out_dtype)
 

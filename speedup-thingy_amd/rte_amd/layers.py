@@ -14,6 +14,7 @@ dicts are interchangeable; its recipe selection is device-side table lookups.
 from __future__ import annotations
 
 import math
+import time
 
 import torch
 import torch.nn.functional as F
@@ -271,6 +272,113 @@ class PackedActiveUnionSwiGLU(nn.Module):
     @property
     def active_m(self) -> int:
         return int(self.active_ids.numel())
+
+
+class SVDFactorSparseFFN(nn.Module):
+    """Token-level sparse SwiGLU FFN with SVD factor candidate retrieval (rte/layers.py:342-643).
+
+    The low-rank factors of W_up and W_gate (refresh_svd) give approximate activations for every
+    neuron; each token's candidates are the top up_m / gate_m / product_m neurons by |up|, |silu(gate)|
+    and |up silu(gate)| times ||W_down row||, evaluated exactly, reranked to top_k and summed through
+    W_down.  candidate_mode "mask" and "slots" differ in the reference only in how the candidate
+    list is stored (a boolean mask or concatenated slots); both select the same set, which is what
+    the HIP kernel computes (a per-token bitmap), and both train.  "triton" is the inference-only
+    device driver (rte/kernels/svd_sparse_ffn_triton.py:480-714): the "product" strategy takes the
+    top top_k of the approximate product scores, "union" reranks the union with exact or
+    approximate activations."""
+
+    def __init__(self, d_model: int, d_ff: int, *, rank: int, top_k: int, up_m: int, gate_m: int | None = None,
+                 product_m: int = 0, candidate_mode: str = "mask", triton_exact_activation: bool = False,
+                 triton_candidate_strategy: str = "product", refresh_on_init: bool = True):
+        super().__init__()
+        self.d_model = int(d_model)
+        self.d_ff = int(d_ff)
+        self.rank = min(max(1, int(rank)), self.d_model, self.d_ff)
+        self.top_k = min(max(1, int(top_k)), self.d_ff)
+        self.up_m = min(max(0, int(up_m)), self.d_ff)
+        self.gate_m = self.up_m if gate_m is None else min(max(0, int(gate_m)), self.d_ff)
+        self.product_m = min(max(0, int(product_m)), self.d_ff)
+        if candidate_mode not in {"mask", "slots", "triton"}:
+            raise ValueError("candidate_mode must be 'mask', 'slots', or 'triton'")
+        self.candidate_mode = candidate_mode
+        self.triton_exact_activation = bool(triton_exact_activation)
+        if triton_candidate_strategy not in {"union", "product"}:
+            raise ValueError("triton_candidate_strategy must be 'union' or 'product'")
+        self.triton_candidate_strategy = triton_candidate_strategy
+        self.refresh_on_init = bool(refresh_on_init)
+        self.w_up = nn.Parameter(torch.empty(self.d_ff, self.d_model))
+        self.w_gate = nn.Parameter(torch.empty(self.d_ff, self.d_model))
+        self.w_down = nn.Parameter(torch.empty(self.d_ff, self.d_model))
+        self.register_buffer("up_a", torch.empty(self.d_model, self.rank), persistent=False)
+        self.register_buffer("up_b", torch.empty(self.rank, self.d_ff), persistent=False)
+        self.register_buffer("gate_a", torch.empty(self.d_model, self.rank), persistent=False)
+        self.register_buffer("gate_b", torch.empty(self.rank, self.d_ff), persistent=False)
+        self.reset_parameters()
+
+    def reset_parameters(self) -> None:
+        scale = 1.0 / math.sqrt(self.d_model)
+        for w in (self.w_up, self.w_gate, self.w_down):
+            nn.init.normal_(w, std=scale)
+        if self.refresh_on_init:
+            self.refresh_svd()
+        else:
+            for b in (self.up_a, self.up_b, self.gate_a, self.gate_b):
+                nn.init.normal_(b, std=scale)
+
+    @classmethod
+    def from_dense(cls, mlp: DenseSwiGLU, *, rank: int, top_k: int, up_m: int, gate_m: int | None = None,
+                   product_m: int = 0, candidate_mode: str = "mask", triton_exact_activation: bool = False,
+                   triton_candidate_strategy: str = "product") -> "SVDFactorSparseFFN":
+        module = cls(mlp.wug.in_features, mlp.wd.in_features, rank=rank, top_k=top_k, up_m=up_m, gate_m=gate_m,
+                     product_m=product_m, candidate_mode=candidate_mode,
+                     triton_exact_activation=triton_exact_activation,
+                     triton_candidate_strategy=triton_candidate_strategy).to(
+            device=mlp.wug.weight.device, dtype=mlp.wug.weight.dtype)
+        with torch.no_grad():
+            up, gate = mlp.wug.weight.detach().chunk(2, dim=0)
+            module.w_up.copy_(up)
+            module.w_gate.copy_(gate)
+            module.w_down.copy_(mlp.wd.weight.detach().t())
+            module.refresh_svd()
+        return module
+
+    @torch.no_grad()
+    def refresh_svd(self) -> None:
+        """Rank-r factors of W_up^T and W_gate^T: a = U[:, :r] S[:r], b = Vh[:r] (an fp32 SVD on the
+        host, rte/layers.py:437-444)."""
+        for prefix, weight in (("up", self.w_up), ("gate", self.w_gate)):
+            mat = weight.detach().float().t().cpu().contiguous()
+            u, s, vh = torch.linalg.svd(mat, full_matrices=False)
+            r = self.rank
+            getattr(self, f"{prefix}_a").copy_((u[:, :r] * s[:r]).to(weight.device, weight.dtype))
+            getattr(self, f"{prefix}_b").copy_(vh[:r, :].to(weight.device, weight.dtype))
+
+    def forward(self, x: torch.Tensor, *, return_aux: bool = False, profile: bool = False):
+        flat = x.reshape(-1, self.d_model)
+        exact, product_only = True, False
+        if self.candidate_mode == "triton":
+            if self.training:
+                raise RuntimeError("SVDFactorSparseFFN Triton mode is inference/eval only; call .eval() first")
+            product_only = self.triton_candidate_strategy == "product"
+            exact = self.triton_exact_activation and not product_only
+        t0 = time.perf_counter() if profile else 0.0
+        out, sel, ncand = hip_ops.svd_sparse_ffn(flat, self.w_up, self.w_gate, self.w_down, self.up_a, self.up_b,
+                                                 self.gate_a, self.gate_b, up_m=self.up_m, gate_m=self.gate_m,
+                                                 product_m=self.product_m, top_k=self.top_k, exact=exact,
+                                                 product_only=product_only)
+        out = out.view(*x.shape[:-1], self.d_model)
+        if not return_aux:
+            return out
+        aux = {"selected_ids": sel, "avg_candidate_size": float(ncand.float().mean().detach().cpu()),
+               "candidate_slots": float(self.top_k if product_only else self.up_m + self.gate_m + self.product_m),
+               "candidate_mode": self.candidate_mode}
+        if self.candidate_mode == "triton":
+            aux.update(triton_exact_activation=self.triton_exact_activation,
+                       triton_candidate_strategy=self.triton_candidate_strategy)
+        if profile:
+            torch.cuda.synchronize()
+            aux["sparse_ffn_time"] = time.perf_counter() - t0
+        return out, aux
 
 
 def make_ffn(config: ModelConfig) -> nn.Module:

@@ -126,6 +126,30 @@ class RecursiveModel(nn.Module):
         hidden = self._coda_hidden(h)
         return hidden, hip_ops.linear(hidden, self.vocab_weight, out_f32=True)
 
+    def _factorized_topk_routes(self, route: RouterOutput, *, pass_idx: int, top_k: int):
+        """(factors [B, k, 4] long = (attn bank, ffn bank, head slot, ffn slot), weights [B, k]) of
+        the k best factor tuples of one pass by summed factor logits (rte/models.py:273-310): the
+        outer-sum scores go through the HIP top-k (value desc, flat index asc, softmax over the
+        selected)."""
+        req = [route.attn_bank_logits_by_pass, route.ffn_bank_logits_by_pass, route.head_slot_logits_by_pass,
+               route.ffn_slot_logits_by_pass]
+        if any(v is None for v in req):
+            raise RuntimeError("factorized routing requires factor logits from the router")
+        a, b, c, e = (v[:, pass_idx, :] for v in req)
+        scores = (a[:, :, None, None, None] + b[:, None, :, None, None] + c[:, None, None, :, None]
+                  + e[:, None, None, None, :]).flatten(1).float()
+        k = min(max(1, int(top_k)), scores.shape[-1])
+        ids, weights = hip_ops.route_topk(scores, k)
+        head_slots, ffn_slots = self.router.head_slots, self.router.ffn_slots
+        flat = ids.long()
+        ffn_slot = flat % ffn_slots
+        flat = flat // ffn_slots
+        head_slot = flat % head_slots
+        flat = flat // head_slots
+        ffn_bank = flat % self.config.ffn_banks
+        attn_bank = flat // self.config.ffn_banks
+        return torch.stack([attn_bank, ffn_bank, head_slot, ffn_slot], dim=-1), weights
+
     def forward_exact_from_h0(self, h0, targets=None, return_states=False, return_loss_per_sample=False, *,
                               router_decisions: RouterOutput | None = None, fixed_recipe=None, fixed_depth=None):
         route = router_decisions or self.router(h0, fixed_recipe=fixed_recipe, fixed_depth=fixed_depth)

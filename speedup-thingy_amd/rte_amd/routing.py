@@ -1,6 +1,9 @@
 """Per-sample recipe / depth router on the pooled prelude state (rte/routing.py:47-188).
 
-Tiny MLPs on [B, d]; kept as torch ops on the device (it is glue, not a hot kernel).
+Every Linear runs on the MFMA GEMM with its bias added in the GEMM epilogue; the four factor
+heads (attention bank, FFN bank, head slot, FFN slot per recursive pass, rte/routing.py:94-101)
+are evaluated when one of their fields is first read, since the accelerated modes' losses
+never read them (their values are the reference's whenever they are read).
 """
 
 from __future__ import annotations
@@ -12,10 +15,11 @@ import torch.nn.functional as F
 from torch import nn
 
 from rte_amd.config import ModelConfig
+from rte_amd.kernels import hip_ops
 from rte_amd.recipes import factor_slot_counts
 
 
-@dataclass(slots=True)
+@dataclass
 class RouterOutput:
     recipe_logits: torch.Tensor
     recipe_probs: torch.Tensor
@@ -33,6 +37,29 @@ class RouterOutput:
     recipe_logits_by_pass: torch.Tensor | None = None
     recipe_probs_by_pass: torch.Tensor | None = None
     recipe_id_by_pass: torch.Tensor | None = None
+    recipe_onehot_st_by_pass: torch.Tensor | None = None
+    _factor_fn: object = None
+    _factor: dict | None = None
+
+    def factor(self, name: str):
+        """A factor-head field (computed once, on first use)."""
+        if self._factor is None:
+            self._factor = self._factor_fn() if self._factor_fn is not None else {}
+        return self._factor.get(name)
+
+    attn_bank_logits_by_pass = property(lambda self: self.factor("attn_bank_logits_by_pass"))
+    attn_bank_probs_by_pass = property(lambda self: self.factor("attn_bank_probs_by_pass"))
+    attn_bank_id_by_pass = property(lambda self: self.factor("attn_bank_id_by_pass"))
+    ffn_bank_logits_by_pass = property(lambda self: self.factor("ffn_bank_logits_by_pass"))
+    ffn_bank_probs_by_pass = property(lambda self: self.factor("ffn_bank_probs_by_pass"))
+    ffn_bank_id_by_pass = property(lambda self: self.factor("ffn_bank_id_by_pass"))
+    head_slot_logits_by_pass = property(lambda self: self.factor("head_slot_logits_by_pass"))
+    head_slot_probs_by_pass = property(lambda self: self.factor("head_slot_probs_by_pass"))
+    head_slot_id_by_pass = property(lambda self: self.factor("head_slot_id_by_pass"))
+    ffn_slot_logits_by_pass = property(lambda self: self.factor("ffn_slot_logits_by_pass"))
+    ffn_slot_probs_by_pass = property(lambda self: self.factor("ffn_slot_probs_by_pass"))
+    ffn_slot_id_by_pass = property(lambda self: self.factor("ffn_slot_id_by_pass"))
+    factor_entropy = property(lambda self: self.factor("factor_entropy"))
 
     def subset(self, mask: torch.Tensor) -> "RouterSubset":
         """The decisions of rows `mask` (bool mask or indices); each field is indexed when first
@@ -65,6 +92,12 @@ def _entropy(p: torch.Tensor) -> torch.Tensor:
     return -(p.clamp_min(1e-9).log() * p).sum(dim=-1)
 
 
+def _mlp(seq: nn.Sequential, x: torch.Tensor) -> torch.Tensor:
+    """Linear -> SiLU -> Linear on the bias-fused HIP GEMM (fp32 output)."""
+    a = F.silu(hip_ops.linear_bias(x, seq[0].weight, seq[0].bias))
+    return hip_ops.linear_bias(a, seq[2].weight, seq[2].bias)
+
+
 class Router(nn.Module):
     def __init__(self, config: ModelConfig):
         super().__init__()
@@ -73,6 +106,7 @@ class Router(nn.Module):
         self.recipe_mlp = nn.Sequential(nn.Linear(config.d_model, hidden), nn.SiLU(), nn.Linear(hidden, config.recipe_count))
         self.pass_recipe_bias = nn.Parameter(torch.zeros(config.t_max, config.recipe_count))
         head_slots, ffn_slots = factor_slot_counts(config)
+        self.head_slots, self.ffn_slots = head_slots, ffn_slots
         self.factor_mlp = nn.Sequential(nn.Linear(config.d_model, hidden), nn.SiLU(), nn.Linear(hidden, hidden))
         self.pass_factor_bias = nn.Parameter(torch.zeros(config.t_max, hidden))
         self.attn_bank_head = nn.Linear(hidden, config.attn_banks)
@@ -82,12 +116,29 @@ class Router(nn.Module):
         self.depth_mlp = nn.Sequential(nn.Linear(config.d_model, hidden), nn.SiLU(), nn.Linear(hidden, len(config.depth_choices)))
         self.register_buffer("depth_values", torch.tensor(config.depth_choices, dtype=torch.long), persistent=False)
 
+    def _factor_heads(self, pooled: torch.Tensor, inv_t: float) -> dict[str, torch.Tensor]:
+        """Per-pass factor logits / probs / argmax and the mean factor entropy (rte/routing.py:94-101,
+        :114-175)."""
+        fh = F.silu(_mlp(self.factor_mlp, pooled).unsqueeze(1) + self.pass_factor_bias.unsqueeze(0))
+        out: dict[str, torch.Tensor] = {}
+        ent = 0.0
+        for name, head in (("attn_bank", self.attn_bank_head), ("ffn_bank", self.ffn_bank_head),
+                           ("head_slot", self.head_slot_head), ("ffn_slot", self.ffn_slot_head)):
+            logits = hip_ops.linear_bias(fh, head.weight, head.bias) * inv_t
+            probs = F.softmax(logits, dim=-1)
+            out[f"{name}_logits_by_pass"] = logits
+            out[f"{name}_probs_by_pass"] = probs
+            out[f"{name}_id_by_pass"] = probs.argmax(dim=-1)
+            ent = ent + _entropy(probs)
+        out["factor_entropy"] = ent.mean(dim=-1)
+        return out
+
     def forward(self, h0: torch.Tensor, *, fixed_recipe: int | None = None, fixed_depth: int | None = None,
                 temperature: float = 1.0) -> RouterOutput:
         pooled = h0.mean(dim=1)
         inv_t = 1.0 / max(temperature, 1e-6)
-        recipe_logits = self.recipe_mlp(pooled) * inv_t
-        depth_logits = self.depth_mlp(pooled) * inv_t
+        recipe_logits = _mlp(self.recipe_mlp, pooled) * inv_t
+        depth_logits = _mlp(self.depth_mlp, pooled) * inv_t
         recipe_logits_by_pass = recipe_logits.unsqueeze(1) + self.pass_recipe_bias.unsqueeze(0) * inv_t
         recipe_probs = F.softmax(recipe_logits, dim=-1)
         recipe_probs_by_pass = F.softmax(recipe_logits_by_pass, dim=-1)
@@ -106,6 +157,7 @@ class Router(nn.Module):
                 raise ValueError(f"fixed_depth={fixed_depth} is not in depth_choices")
             depth_id = torch.full((B,), self.config.depth_choices.index(fixed_depth), device=h0.device, dtype=torch.long)
         recipe_hard = F.one_hot(recipe_id, recipe_probs.shape[-1]).to(recipe_probs.dtype)
+        recipe_hard_by_pass = F.one_hot(recipe_id_by_pass, recipe_probs.shape[-1]).to(recipe_probs.dtype)
         depth_hard = F.one_hot(depth_id, depth_probs.shape[-1]).to(depth_probs.dtype)
         depth_values = self.depth_values.to(depth_probs.dtype)
         recipe_entropy = _entropy(recipe_probs)
@@ -127,4 +179,6 @@ class Router(nn.Module):
             recipe_logits_by_pass=recipe_logits_by_pass,
             recipe_probs_by_pass=recipe_probs_by_pass,
             recipe_id_by_pass=recipe_id_by_pass,
+            recipe_onehot_st_by_pass=recipe_hard_by_pass + recipe_probs_by_pass - recipe_probs_by_pass.detach(),
+            _factor_fn=lambda: self._factor_heads(pooled, inv_t),
         )

@@ -418,3 +418,79 @@ def test_static_cluster_pool_layer_overlapping_pools():
     assert_rel(_np(out).reshape(-1, 128), outr.detach().numpy(), BF16_RTOL, "static pool y")
     assert_rel(_np(layer.wug.weight.grad), tw.grad.numpy(), BF16_RTOL, "static pool dwug")
     assert_rel(_np(layer.wd.weight.grad), td.grad.numpy(), BF16_RTOL, "static pool dwd")
+
+
+# ---------------------------------------------------------------- router
+
+def test_router_matches_oracle_and_factor_heads():
+    """Router (rte/routing.py:80-188) on the bias-fused HIP GEMMs against the oracle with
+    bf16-rounded GEMM operands: logits within 2e-2; ids, probabilities and entropies are exactly
+    the softmax / argmax of the kernel's own logits; factor fields appear when read; the
+    factorized top-k (rte/models.py:273-310) is bit-exact against the oracle on those logits."""
+    from oracle import router as RO
+    from rte_amd.config import ModelConfig
+    from rte_amd.models import RecursiveModel
+
+    cfg = ModelConfig(topology="recursive", vocab_size=64, d_model=128, n_heads=4, d_ff=256, n_dense_layers=1,
+                      n_prelude=1, n_coda=1, t_max=4, depth_choices=[1, 2, 4], attn_banks=2, ffn_banks=3,
+                      head_groups=4, ffn_groups=8, active_head_groups=2, active_ffn_groups=2, recipe_count=9)
+    torch.manual_seed(16)
+    model = RecursiveModel(cfg).to(DEV)
+    with torch.no_grad():
+        for prm in model.router.parameters():
+            prm.add_(torch.randn_like(prm) * 0.05)
+    h0 = torch.randn(6, 20, 128, device=DEV)
+    route = model.router(h0, temperature=0.8)
+    p = {k: v.detach().double().cpu().numpy() for k, v in model.router.state_dict().items()}
+    for k in p:
+        if k.endswith(".weight"):
+            p[k] = bf16_round(p[k].astype(np.float32)).astype(np.float64)
+    ref = RO.router(h0.cpu().numpy(), p, [1, 2, 4], temperature=0.8)
+    assert_rel(_np(route.recipe_logits), ref["recipe_logits"], BF16_RTOL, "recipe logits")
+    assert_rel(_np(route.depth_logits), ref["depth_logits"], BF16_RTOL, "depth logits")
+    own = RO._softmax(_np(route.recipe_logits_by_pass))
+    np.testing.assert_array_equal(route.recipe_id_by_pass.cpu().numpy(), own.argmax(-1))
+    np.testing.assert_allclose(_np(route.recipe_probs_by_pass), own, rtol=1e-5, atol=1e-7)
+    np.testing.assert_array_equal(route.depth_id.cpu().numpy(), _np(route.depth_logits).argmax(-1))
+    assert route._factor is None  # nothing read the factor heads yet
+    for name in ("attn_bank", "ffn_bank", "head_slot", "ffn_slot"):
+        lg = getattr(route, name + "_logits_by_pass")
+        assert_rel(_np(lg), ref[name + "_logits_by_pass"], BF16_RTOL, name)
+        np.testing.assert_array_equal(getattr(route, name + "_id_by_pass").cpu().numpy(), _np(lg).argmax(-1))
+    assert route.factor_entropy.shape == (6,)
+    factors, w = model._factorized_topk_routes(route, pass_idx=2, top_k=7)
+    rf, rw = RO.factorized_topk(*(_np(getattr(route, n + "_logits_by_pass"))[:, 2, :]
+                                  for n in ("attn_bank", "ffn_bank", "head_slot", "ffn_slot")), 7)
+    np.testing.assert_array_equal(factors.cpu().numpy(), rf)
+    np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
+
+
+def test_router_backward_small_heads():
+    """Gradients through the router's Linear layers (the depth head has 3 outputs, not a multiple
+    of the GEMM's 8-element vectors) against fp64 autograd of the same modules on the CPU."""
+    from rte_amd.config import ModelConfig
+    from rte_amd.routing import Router
+
+    cfg = ModelConfig(topology="recursive", vocab_size=64, d_model=64, n_heads=4, d_ff=128, n_dense_layers=1,
+                      n_prelude=1, n_coda=1, t_max=4, depth_choices=[1, 2, 4], attn_banks=1, ffn_banks=1,
+                      head_groups=4, ffn_groups=4, active_head_groups=1, active_ffn_groups=1, recipe_count=5)
+    torch.manual_seed(17)
+    r = Router(cfg).to(DEV)
+    with torch.no_grad():
+        for prm in r.parameters():
+            prm.copy_(torch.from_numpy(bf16_round(prm.detach().cpu().numpy())).to(DEV))
+    h0 = torch.from_numpy(bf16_round(np.random.default_rng(17).standard_normal((4, 9, 64)).astype(np.float32)))
+    out = r(h0.to(DEV))
+    loss = (out.recipe_probs * torch.arange(5, device=DEV)).sum() + out.expected_depth.sum()
+    loss.backward()
+    ref = Router(cfg).double()
+    ref.load_state_dict({k: v.detach().double().cpu() for k, v in r.state_dict().items()})
+    F_ = torch.nn.functional
+    pooled = h0.double().mean(1)
+    rl = ref.recipe_mlp(pooled)
+    dl = ref.depth_mlp(pooled)
+    lref = (F_.softmax(rl, -1) * torch.arange(5)).sum() + (F_.softmax(dl, -1) * torch.tensor([1.0, 2.0, 4.0])).sum()
+    lref.backward()
+    for (n, a), (_, b) in zip(r.named_parameters(), ref.named_parameters()):
+        if b.grad is not None:
+            assert_rel(_np(a.grad), b.grad.numpy(), 5e-2, n)

@@ -187,16 +187,16 @@ def test_staged_reductions_equal_torch_losses():
 def test_router_subset_indexes_each_field_on_first_read():
     """The audited rows' routing decisions equal direct indexing of every field, and a field
     that is never read is never indexed (nested subsets compose)."""
-    from rte_amd.config import ModelConfig
-    from rte_amd.routing import Router
+    from rte_amd.routing import RouterOutput
 
-    cfg = ModelConfig(**_model(d_model=32, n_heads=4, d_ff=64))
     torch.manual_seed(0)
-    route = Router(cfg)(torch.randn(6, 5, 32))
+    fields = [f for f in RouterOutput.__dataclass_fields__ if not f.startswith("_")]
+    route = RouterOutput(**{f: torch.randn(6, 3) for f in fields},
+                         _factor_fn=lambda: {"factor_entropy": torch.randn(6), "attn_bank_id_by_pass": torch.ones(6, 2)})
     idx = torch.tensor([4, 1, 3])
     sub = route.subset(idx)
     assert "recipe_probs" not in vars(sub)
-    for name in route.__dataclass_fields__:
+    for name in fields + ["factor_entropy", "attn_bank_id_by_pass", "ffn_slot_id_by_pass"]:
         v = getattr(route, name)
         got = getattr(sub, name)
         if isinstance(v, torch.Tensor):

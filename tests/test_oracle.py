@@ -988,3 +988,140 @@ def test_static_centers_brute_force_and_invariants():
     np.testing.assert_array_equal(R.static_centers(q * rng.uniform(0.1, 10.0, (200, 1)), centers)[0], ids)
     assert 7 not in ids
     np.testing.assert_array_equal(R.route_topk(scores.astype(np.float32), 1)[0][:, 0], ids)
+
+
+def _router_params(rng, d=16, H=12, R=5, D=3, t=4, A=2, Fb=3, Hs=2, Fs=4):
+    def lin(o, i):
+        return rng.standard_normal((o, i)) * 0.3, rng.standard_normal(o) * 0.1
+
+    p = {}
+    for name, o, i in (("recipe_mlp.0", H, d), ("recipe_mlp.2", R, H), ("depth_mlp.0", H, d), ("depth_mlp.2", D, H),
+                       ("factor_mlp.0", H, d), ("factor_mlp.2", H, H), ("attn_bank_head", A, H),
+                       ("ffn_bank_head", Fb, H), ("head_slot_head", Hs, H), ("ffn_slot_head", Fs, H)):
+        p[name + ".weight"], p[name + ".bias"] = lin(o, i)
+    p["pass_recipe_bias"] = rng.standard_normal((t, R)) * 0.2
+    p["pass_factor_bias"] = rng.standard_normal((t, H)) * 0.2
+    return p
+
+
+def test_router_oracle_matches_torch_modules():
+    """The router oracle against the same computation by torch modules (nn.Linear, F.silu,
+    F.softmax, argmax) on the CPU in float64, for every output field (rte/routing.py:80-188)."""
+    from oracle import router as RO
+
+    rng = _rng(81)
+    p = _router_params(rng)
+    h0 = rng.standard_normal((6, 7, 16))
+    o = RO.router(h0, p, [1, 2, 4], temperature=0.7)
+    T = lambda k: torch.tensor(p[k])  # noqa: E731
+    F = torch.nn.functional
+    lin = lambda x, n: F.linear(x, T(n + ".weight"), T(n + ".bias"))  # noqa: E731
+    pooled = torch.tensor(h0).mean(1)
+    mlp = lambda n: lin(F.silu(lin(pooled, n + ".0")), n + ".2")  # noqa: E731
+    rl = mlp("recipe_mlp") / 0.7
+    np.testing.assert_allclose(o["recipe_logits"], rl.numpy(), rtol=1e-12)
+    np.testing.assert_allclose(o["recipe_logits_by_pass"], (rl[:, None] + T("pass_recipe_bias") / 0.7).numpy(),
+                               rtol=1e-12)
+    dp = F.softmax(mlp("depth_mlp") / 0.7, -1)
+    np.testing.assert_allclose(o["depth_probs"], dp.numpy(), rtol=1e-12)
+    np.testing.assert_array_equal(o["depth_id"], dp.argmax(-1).numpy())
+    np.testing.assert_allclose(o["expected_depth"], (dp * torch.tensor([1.0, 2.0, 4.0])).sum(-1).numpy(), rtol=1e-12)
+    fh = F.silu(mlp("factor_mlp")[:, None] + T("pass_factor_bias"))
+    ent = 0
+    for name in ("attn_bank", "ffn_bank", "head_slot", "ffn_slot"):
+        pr = F.softmax(lin(fh, name + "_head") / 0.7, -1)
+        np.testing.assert_array_equal(o[name + "_id_by_pass"], pr.argmax(-1).numpy())
+        ent = ent - (pr.clamp_min(1e-9).log() * pr).sum(-1)
+    np.testing.assert_allclose(o["factor_entropy"], ent.mean(-1).numpy(), rtol=1e-12)
+
+
+def test_router_entropy_and_depth_closed_form():
+    """Two equal logits give entropy ln 2 and expected depth the mean of the two choices."""
+    from oracle import router as RO
+
+    assert abs(RO._entropy(RO._softmax(np.array([[0.3, 0.3]])))[0] - np.log(2.0)) < 1e-12
+    pr = RO._softmax(np.array([[1.0, 1.0]]))
+    assert abs((pr * np.array([2.0, 4.0])).sum() - 3.0) < 1e-12
+
+
+def test_factorized_topk_brute_force():
+    """_factorized_topk_routes (rte/models.py:273-310): enumerate every (attn bank, ffn bank, head
+    slot, ffn slot) tuple, sort by summed logit (value desc, flat index asc), softmax the top k."""
+    import itertools
+
+    from oracle import router as RO
+
+    rng = _rng(82)
+    A, Fb, Hs, Fs = 2, 3, 2, 4
+    a, b, c, e = (rng.standard_normal((5, n)) for n in (A, Fb, Hs, Fs))
+    factors, w = RO.factorized_topk(a, b, c, e, 6)
+    for t in range(5):
+        tuples = list(itertools.product(range(A), range(Fb), range(Hs), range(Fs)))
+        sc = [np.float32(a[t, i] + b[t, j] + c[t, k] + e[t, m]) for i, j, k, m in tuples]
+        order = sorted(range(len(tuples)), key=lambda q: (-sc[q], q))[:6]
+        assert [tuple(x) for x in factors[t]] == [tuples[q] for q in order]
+        sel = np.array([sc[q] for q in order], np.float64)
+        np.testing.assert_allclose(w[t], np.exp(sel - sel.max()) / np.exp(sel - sel.max()).sum(), rtol=1e-6)
+
+
+def _svd_sparse_case(seed, T=6, d=8, F=16):
+    rng = _rng(seed)
+    x = rng.standard_normal((T, d))
+    wu, wg, wd = (rng.standard_normal((F, d)) * 0.5 for _ in range(3))
+    uh = (x @ wu.T + rng.standard_normal((T, F)) * 0.3).astype(np.float32)
+    gh = (x @ wg.T + rng.standard_normal((T, F)) * 0.3).astype(np.float32)
+    return x, wu, wg, wd, uh, gh
+
+
+def test_svd_sparse_all_neurons_is_dense_swiglu():
+    """Every neuron a candidate and selected (top_k = d_ff): the sparse FFN is the dense SwiGLU
+    (rte/layers.py:620-643 with the full candidate set)."""
+    from oracle import svd_sparse as SS
+
+    x, wu, wg, wd, uh, gh = _svd_sparse_case(83)
+    out, sel, _, _ = SS.forward(x, wu, wg, wd, uh, gh, up_m=16, gate_m=0, product_m=0, top_k=16)
+    dense, _ = SW.dense_swiglu_fwd(x, np.concatenate([wu, wg]), wd, wd_rows=True)
+    np.testing.assert_allclose(out, dense, rtol=1e-12, atol=1e-12)
+    assert (sel == np.arange(16)).all()
+
+
+def test_svd_sparse_brute_force_selection():
+    """Candidate union, fill and rerank against explicit sorts with (score desc, id asc) keys."""
+    import math
+
+    from oracle import svd_sparse as SS
+
+    x, wu, wg, wd, uh, gh = _svd_sparse_case(84)
+    w = np.sqrt((wd * wd).sum(-1)).astype(np.float32)
+    for up_m, gate_m, product_m, top_k in ((3, 2, 2, 4), (1, 0, 0, 5), (4, 4, 4, 3)):
+        _, sel, _, _ = SS.forward(x, wu, wg, wd, uh, gh, up_m=up_m, gate_m=gate_m, product_m=product_m, top_k=top_k)
+        for t in range(x.shape[0]):
+            def top(sc, m):
+                return [j for _, j in sorted((-float(sc[j]), j) for j in range(16))[:m]]
+
+            gs = [float(gh[t, j]) / (1 + math.exp(-float(gh[t, j]))) for j in range(16)]
+            cand = set(top([abs(uh[t, j]) * w[j] for j in range(16)], up_m))
+            cand |= set(top([abs(gs[j]) * w[j] for j in range(16)], gate_m))
+            prod = [abs(uh[t, j] * np.float32(gs[j])) * w[j] for j in range(16)]
+            cand |= set(top(prod, product_m))
+            if len(cand) < top_k:
+                cand |= set(top(prod, top_k))
+            ex = {c: abs((x[t] @ wu[c]) * (x[t] @ wg[c]) / (1 + math.exp(-(x[t] @ wg[c])))) * w[c] for c in cand}
+            want = sorted(c for _, c in sorted((-ex[c], c) for c in cand)[:top_k])
+            assert sel[t].tolist() == want
+
+
+def test_svd_sparse_backward_matches_autograd():
+    from oracle import svd_sparse as SS
+
+    x, wu, wg, wd, uh, gh = _svd_sparse_case(85)
+    out, sel, u, g = SS.forward(x, wu, wg, wd, uh, gh, up_m=3, gate_m=3, product_m=2, top_k=4)
+    dy = _rng(86).standard_normal(out.shape)
+    dx, dwu, dwg, dwd = SS.backward(dy, x, wu, wg, wd, sel, u, g)
+    tx, twu, twg, twd = (torch.tensor(a, requires_grad=True) for a in (x, wu, wg, wd))
+    s = torch.from_numpy(sel)
+    uu = (tx[:, None, :] * twu[s]).sum(-1)
+    gg = (tx[:, None, :] * twg[s]).sum(-1)
+    ((uu * torch.nn.functional.silu(gg))[:, :, None] * twd[s]).sum(1).mul(torch.tensor(dy)).sum().backward()
+    for a, b in ((dx, tx), (dwu, twu), (dwg, twg), (dwd, twd)):
+        np.testing.assert_allclose(a, b.grad.numpy(), rtol=1e-10, atol=1e-12)
