@@ -463,3 +463,30 @@ def test_backend_modules_fail_loudly_without_device():
     st = optimized.backend_status()
     assert st["torch_symbols"] == ["k_metrics_reduce", "k_pack_by_recipe", "k_recurrent_exact_loop",
                                    "k_sample_audit_mask", "k_unpack_from_recipe"]
+
+
+def test_manifest_and_metrics_formats(tmp_path):
+    """manifest.json with config hash / backend status (rte/artifacts.py:63-79) and metrics.jsonl
+    rows (rte/reporting.py:10-29) round-trip; the speed-proof check reads the backend status
+    (benchmarks/speed_audit.py:49-53)."""
+    import json
+
+    from rte_amd import artifacts as AR
+
+    cfg = ExperimentConfig(model=ModelConfig(**_model()), training=TrainingConfig(mode="recursive_macro"))
+    man = AR.build_manifest(cfg, command=["train"], extra={"run": 1})
+    assert {"config_hash", "config", "git", "hardware", "backend", "command", "run"} <= set(man)
+    assert man["config_hash"] == AR.config_hash(cfg) and len(man["config_hash"]) == 64
+    assert man["backend"]["uses_reference_fallback"] is False and AR.speed_proof_allowed(man)
+    assert not AR.speed_proof_allowed({"uses_reference_fallback": True})
+    AR.write_json(tmp_path / "run" / "manifest.json", man)
+    log = AR.JsonlLogger(tmp_path / "run" / "metrics.jsonl")
+    log.write({"step": 1, "loss": torch.tensor([2.0, 4.0]), "mode": "recursive_macro"})
+    log.write({"step": 2, "loss": torch.tensor(1.5), "val_loss": 1.2, "elapsed_train_time": 9.0})
+    log.close()
+    rows = AR.read_jsonl(tmp_path / "run" / "metrics.jsonl")
+    assert rows[0] == {"loss": 3.0, "mode": "recursive_macro", "step": 1}
+    summ = AR.summarize_metrics(tmp_path / "run")
+    assert summ["rows"] == 2 and summ["means"]["mean_loss"] == 2.25 and summ["manifest"]["run"] == 1
+    assert AR.summarize_time_to_target(rows, 1.3)["time_to_target_loss"] == 9.0
+    assert json.loads((tmp_path / "run" / "manifest.json").read_text())["config"]["model"]["d_model"] == 16
