@@ -345,6 +345,58 @@ int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, 
 int rte_macro_table_grad(const int64_t* key, int B, int seq, int n_keys, int d, const void* part, float* dgain,
                          float* dbias, float* dscale, void* stream);
 
+/* Fused bounded macro operator Phi at hidden rank 32 (rte/macro.py:201-236, the path of
+ * MacroOperators._apply_vectorized_bounded and consistency_loss at rte/macro.py:342-359 with
+ * the default options).  z = [rmsnorm(h) | mean_s rmsnorm(h) | h0] of the reference is split by
+ * the rows of V = [V1; V2; V3]: a = x2 @ [V1; V3][k] + pooled @ V2[k] with x2 = [bf16(h rstd) |
+ * bf16(h0)] per source row and pooled = bf16(mean_s h rstd) per source sample; low = silu(a) @
+ * U[k]; out = h + c scale[k] tanh(gain[k] h + low + bias[k]).  Sample b of B reads h row block
+ * b % B_h and h0 row block b % B_h0 (B_h0 | B_h | B, B / B_h <= 8); k = key[b] in [0, n_keys).
+ * prep  : bf16 weight layouts from v f32 [n_keys, 3d, 32] and u f32 [n_keys, 32, d]: v_b (same
+ *         layout), vc_t [n_keys, 32, 2d] (V1 | V3 transposed), v2_t [n_keys, 32, d], u_b (same),
+ *         u_t [n_keys, d, 32].
+ * fwd   : x2 bf16 [B_h*seq, 2d], rstd f32 [B_h*seq], pooled bf16 [B_h, d], p f32 [B, 32], a f32
+ *         [B*seq, 32], sa = bf16(silu(a)) [B*seq, 32], out f32 [B, seq, d]; with mse_ref (f32
+ *         [B, seq, d]) also mse_part f32 [B * tiles] = per-tile sums of (out - mse_ref)^2, tiles =
+ *         rte_macro_fused_tiles(seq); workspace rte_macro_fused_fwd_workspace_bytes(B_h, seq, d).
+ * sum   : out[0] = inv_n * sum of part[0, n) in a fixed order.
+ * bwd   : upstream gradient: samples b < nsplit take mul * g[0] * (dout_p - dout_q)[b], the others
+ *         dout[b - nsplit].  Writes du bf16 [B*seq, d], da bf16 [B*seq, 32], part_tab f32
+ *         [B, tiles, 3, d] (du h | du | dout c tanh column sums), part_da f32 [B, tiles, 32], da_sum bf16
+ *         [B, 32] (sum over the sample's rows of da), dh f32
+ *         [B_h, seq, d] (all repeats added in repeat order; with dh0_into_dh the h0 gradient too;
+ *         plus n_extra blocks of extra f32 [n_extra * B_h, seq, d]) and dh0 f32 [B_h, seq, d]
+ *         (optional, per h source sample).  Workspace rte_macro_fused_bwd_workspace_bytes(B, seq).
+ * wgrad : weight gradients of one call (B1 = 0) or of two calls listed together (call 1's
+ *         samples follow call 0's in key / du / da / part buffers, its x2 and pooled rows follow
+ *         call 0's B_h0 source blocks): du_w f32 [n_keys, 32, d], dv_w f32 [n_keys, 3d, 32],
+ *         dgain / dbias / dscale f32 [n_keys, d] (each optional), every sum in a fixed order.
+ *         Workspace rte_macro_fused_wgrad_workspace_bytes(B0 + B1, seq, d, n_keys).
+ * d % 128 == 0, d <= 1024, seq <= 65536, B <= 65535 (wgrad: B0 + B1 <= 16384). */
+int rte_macro_fused_tiles(int seq);
+size_t rte_macro_fused_fwd_workspace_bytes(int B_h, int seq, int d);
+size_t rte_macro_fused_bwd_workspace_bytes(int B, int seq);
+size_t rte_macro_fused_wgrad_workspace_bytes(int B_total, int seq, int d, int n_keys);
+int rte_macro_fused_prep(const float* v, const float* u, int n_keys, int d, void* v_b, void* vc_t, void* v2_t,
+                         void* u_b, void* u_t, void* stream);
+int rte_macro_fused_fwd(const float* h, const float* h0, int B_h, int B_h0, const int64_t* key, int B, int seq, int d,
+                        int n_keys, float eps, const void* v_b, const void* vc_t, const void* u_t, const float* gain,
+                        const float* bias, const float* scale, float c, void* x2, float* rstd, void* pooled, float* p,
+                        float* a, void* sa, float* out, const float* mse_ref, float* mse_part, void* workspace,
+                        size_t workspace_bytes, void* stream);
+int rte_macro_fused_sum(const float* part, int n, float inv_n, float* out, void* stream);
+int rte_macro_fused_bwd(const float* dout_p, const float* dout_q, const float* g, float mul, int nsplit,
+                        const float* dout, const float* h, const float* rstd, const void* x2, int B_h,
+                        const int64_t* key, int B, int seq, int d, int n_keys, const float* a, const void* sa,
+                        const void* v_b, const void* v2_t, const void* u_b, const void* u_t, const float* gain,
+                        const float* bias, const float* scale, float c, void* du, void* da, float* part_tab,
+                        float* part_da, float* dh, float* dh0, int dh0_into_dh, const float* extra, int n_extra,
+                        void* da_sum, void* workspace, size_t workspace_bytes, void* stream);
+int rte_macro_fused_wgrad(const int64_t* key, int B0, int B_h0, int B1, int B_h1, int seq, int d, int n_keys,
+                          const void* x2, const void* sa, const void* du, const void* da, const void* pooled,
+                          const void* da_sum, const float* part_tab, float* du_w, float* dv_w, float* dgain,
+                          float* dbias, float* dscale, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- mean squared difference (F.mse_loss of the macro consistency loss, rte/macro.py:342-359) ----
  * fwd: out f32 [1] = mean((a - b)^2) over n f32 elements (fixed-order block sums, then one
  * workgroup adds them in order); workspace rte_mse_workspace_bytes(n).

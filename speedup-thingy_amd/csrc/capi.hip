@@ -61,6 +61,27 @@ int macro_epilogue_bwd(const float* dout, const float* h, const float* low, cons
                        void* part, size_t part_bytes, hipStream_t s);
 int macro_table_grad(const int64_t* key, int B, int S, int G, int d, const void* part, float* dgain, float* dbias,
                      float* dscale, hipStream_t s);
+int macro_fused_tiles(int S);
+size_t macro_fused_fwd_workspace_bytes(int Bh, int S, int d);
+size_t macro_fused_wgrad_workspace_bytes(int Bt, int S, int d, int G);
+int macro_fused_prep(const float* V, const float* U, int G, int d, bf16* Vb, bf16* VcT, bf16* V2T, bf16* Ub, bf16* UT,
+                     hipStream_t s);
+size_t macro_fused_bwd_workspace_bytes(int B, int S);
+int macro_fused_fwd(const float* h, const float* h0, int Bh, int Bh0, const int64_t* key, int B, int S, int d, int G,
+                    float eps, const bf16* Vb, const bf16* VcT, const bf16* UT, const float* gain, const float* bias,
+                    const float* scale, float c, bf16* x2, float* rstd, bf16* pooled, float* P, float* a, bf16* sa,
+                    float* out, const float* mse_ref, float* mse_part, void* ws, size_t ws_bytes, hipStream_t s);
+int macro_fused_sum(const float* part, int n, float inv_n, float* out, hipStream_t s);
+int macro_fused_bwd(const float* dp, const float* dq, const float* g, float mul, int nsplit, const float* dbuf,
+                    const float* h, const float* rstd, const bf16* x2, int Bh, const int64_t* key, int B, int S, int d,
+                    int G, const float* a, const bf16* sa, const bf16* Vb, const bf16* V2T, const bf16* Ub,
+                    const bf16* UT, const float* gain, const float* bias, const float* scale, float c, bf16* du,
+                    bf16* da, float* part_tab, float* part_da, float* dh, float* dh0, int dh0_into_dh,
+                    const float* extra, int n_extra, bf16* dsum, void* ws, size_t ws_bytes, hipStream_t s);
+int macro_fused_wgrad(const int64_t* key, int B0, int Bh0, int B1, int Bh1, int S, int d, int G, const bf16* x2,
+                      const bf16* sa, const bf16* du, const bf16* da, const bf16* pooled, const bf16* dsum,
+                      const float* part_tab, float* dU, float* dV, float* dgain, float* dbias, float* dscale,
+                      void* ws, size_t ws_bytes, hipStream_t s);
 size_t mse_workspace_bytes(int64_t n);
 int mse_fwd(const float* a, const float* b, int64_t n, float* out, void* ws, size_t ws_bytes, hipStream_t s);
 int mse_bwd(const float* a, const float* b, int64_t n, const float* g, float* da, float* db, hipStream_t s);
@@ -871,6 +892,62 @@ int rte_macro_epilogue_bwd(const float* dout, const float* h, const float* low, 
 int rte_macro_table_grad(const int64_t* key, int B, int seq, int n_keys, int d, const void* part, float* dgain,
                          float* dbias, float* dscale, void* stream) {
   return macro_table_grad(key, B, seq, n_keys, d, part, dgain, dbias, dscale, S(stream));
+}
+
+int rte_macro_fused_tiles(int seq) { return seq >= 1 ? macro_fused_tiles(seq) : 0; }
+
+size_t rte_macro_fused_fwd_workspace_bytes(int B_h, int seq, int d) {
+  return macro_fused_fwd_workspace_bytes(B_h, seq, d);
+}
+
+size_t rte_macro_fused_wgrad_workspace_bytes(int B_total, int seq, int d, int n_keys) {
+  return macro_fused_wgrad_workspace_bytes(B_total, seq, d, n_keys);
+}
+
+int rte_macro_fused_prep(const float* v, const float* u, int n_keys, int d, void* v_b, void* vc_t, void* v2_t,
+                         void* u_b, void* u_t, void* stream) {
+  return macro_fused_prep(v, u, n_keys, d, B16(v_b), B16(vc_t), B16(v2_t), B16(u_b), B16(u_t), S(stream));
+}
+
+size_t rte_macro_fused_bwd_workspace_bytes(int B, int seq) { return macro_fused_bwd_workspace_bytes(B, seq); }
+
+int rte_macro_fused_fwd(const float* h, const float* h0, int B_h, int B_h0, const int64_t* key, int B, int seq, int d,
+                        int n_keys, float eps, const void* v_b, const void* vc_t, const void* u_t, const float* gain,
+                        const float* bias, const float* scale, float c, void* x2, float* rstd, void* pooled, float* p,
+                        float* a, void* sa, float* out, const float* mse_ref, float* mse_part, void* workspace,
+                        size_t workspace_bytes, void* stream) {
+  return macro_fused_fwd(h, h0, B_h, B_h0, key, B, seq, d, n_keys, eps, reinterpret_cast<const bf16*>(v_b),
+                         reinterpret_cast<const bf16*>(vc_t), reinterpret_cast<const bf16*>(u_t), gain, bias, scale, c,
+                         B16(x2), rstd, B16(pooled), p, a, B16(sa), out, mse_ref, mse_part, workspace, workspace_bytes,
+                         S(stream));
+}
+
+int rte_macro_fused_sum(const float* part, int n, float inv_n, float* out, void* stream) {
+  return macro_fused_sum(part, n, inv_n, out, S(stream));
+}
+
+int rte_macro_fused_bwd(const float* dout_p, const float* dout_q, const float* g, float mul, int nsplit,
+                        const float* dout, const float* h, const float* rstd, const void* x2, int B_h,
+                        const int64_t* key, int B, int seq, int d, int n_keys, const float* a, const void* sa,
+                        const void* v_b, const void* v2_t, const void* u_b, const void* u_t, const float* gain,
+                        const float* bias, const float* scale, float c, void* du, void* da, float* part_tab,
+                        float* part_da, float* dh, float* dh0, int dh0_into_dh, const float* extra, int n_extra,
+                        void* da_sum, void* workspace, size_t workspace_bytes, void* stream) {
+  auto cb = [](const void* p) { return reinterpret_cast<const bf16*>(p); };
+  return macro_fused_bwd(dout_p, dout_q, g, mul, nsplit, dout, h, rstd, cb(x2), B_h, key, B, seq, d, n_keys, a, cb(sa),
+                         cb(v_b), cb(v2_t), cb(u_b), cb(u_t), gain, bias, scale, c, B16(du), B16(da), part_tab,
+                         part_da, dh, dh0, dh0_into_dh, extra, n_extra, B16(da_sum), workspace, workspace_bytes,
+                         S(stream));
+}
+
+int rte_macro_fused_wgrad(const int64_t* key, int B0, int B_h0, int B1, int B_h1, int seq, int d, int n_keys,
+                          const void* x2, const void* sa, const void* du, const void* da, const void* pooled,
+                          const void* da_sum, const float* part_tab, float* du_w, float* dv_w, float* dgain,
+                          float* dbias, float* dscale, void* workspace, size_t workspace_bytes, void* stream) {
+  auto cb = [](const void* p) { return reinterpret_cast<const bf16*>(p); };
+  return macro_fused_wgrad(key, B0, B_h0, B1, B_h1, seq, d, n_keys, cb(x2), cb(sa), cb(du), cb(da), cb(pooled),
+                           cb(da_sum), part_tab, du_w, dv_w, dgain, dbias, dscale, workspace, workspace_bytes,
+                           S(stream));
 }
 
 int rte_attention_fwd(const void* q, const void* k, const void* v, int B, int H, int seq, int head_dim, float scale,

@@ -426,7 +426,7 @@ __global__ void __launch_bounds__(512) macro_epilogue_bwd_kernel(const float* __
 // the three tables (rows of keys no sample uses come out zero).  The samples of v are first
 // listed in order in LDS (one ballot per 64 samples); the contributions j = (list index) * P +
 // part are then split over 4 thread groups by j mod 4, each summing its share in order with
-// 4 loads in flight, and the 4 group sums are added in group order.
+// 16 loads in flight, and the 4 group sums are added in group order.
 __global__ void __launch_bounds__(256) macro_table_grad_kernel(const int64_t* __restrict__ key, int B, int P, int d,
                                                                const float* __restrict__ part,
                                                                float* __restrict__ dgain, float* __restrict__ dbias,
@@ -452,19 +452,17 @@ __global__ void __launch_bounds__(256) macro_table_grad_kernel(const int64_t* __
   const int col = blockIdx.y * 64 + lane;
   float acc = 0.0f;
   if (col < D3) {
-    for (int j0 = grp; j0 < m; j0 += 16) {
-      float x[4];
+    for (int j0 = grp; j0 < m; j0 += 64) {  // 16 loads in flight per thread
+      float x[16];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
+      for (int k = 0; k < 16; ++k) {
         const int j = j0 + 4 * k;
-        x[k] = 0.0f;
-        if (j < m) {
-          const int i = j / P, q = j - i * P;
-          x[k] = part[((int64_t)list[i] * P + q) * D3 + col];
-        }
+        const int jj = j < m ? j : grp;  // past the end: re-read a valid entry, weight 0
+        const int i = jj / P, q = jj - i * P;
+        x[k] = part[((int64_t)list[i] * P + q) * D3 + col];
       }
 #pragma unroll
-      for (int k = 0; k < 4; ++k) acc += x[k];
+      for (int k = 0; k < 16; ++k) acc += j0 + 4 * k < m ? x[k] : 0.0f;
     }
   }
   gsum[grp][lane] = acc;
@@ -590,6 +588,18 @@ int macro_table_grad(const int64_t* key, int B, int S, int G, int d, const void*
               "macro_table_grad: need B <= 16384, n_keys <= 65535, d <= 1024");
   if (!dgain && !dbias && !dscale) return 0;
   const int P = B > 0 ? macro_parts(B, S) : 1;
+  const dim3 grid((unsigned)G, (unsigned)((3 * d + 63) / 64));
+  hipLaunchKernelGGL(macro_table_grad_kernel, grid, dim3(256), (size_t)(B > 0 ? B : 1) * sizeof(int), s, key, B, P, d,
+                     static_cast<const float*>(part), dgain, dbias, dscale);
+  return check_launch("macro_table_grad");
+}
+
+// As macro_table_grad with the number of part rows per sample given (part [B][P][3d]).
+int macro_table_grad_parts(const int64_t* key, int B, int P, int G, int d, const void* part, float* dgain,
+                           float* dbias, float* dscale, hipStream_t s) {
+  RTE_REQUIRE(B >= 0 && B <= 16384 && P >= 1 && G >= 1 && G <= 65535 && d >= 1 && d <= 1024,
+              "macro_table_grad: need B <= 16384, n_keys <= 65535, d <= 1024");
+  if (!dgain && !dbias && !dscale) return 0;
   const dim3 grid((unsigned)G, (unsigned)((3 * d + 63) / 64));
   hipLaunchKernelGGL(macro_table_grad_kernel, grid, dim3(256), (size_t)(B > 0 ? B : 1) * sizeof(int), s, key, B, P, d,
                      static_cast<const float*>(part), dgain, dbias, dscale);

@@ -84,6 +84,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_macro_epilogue_fwd": (_I, [_P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _F, _P, _P]),
     "rte_macro_epilogue_bwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _F, _P, _P, _P, _SZ, _P]),
     "rte_macro_table_grad": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P]),
+    "rte_macro_fused_tiles": (_I, [_I]),
+    "rte_macro_fused_fwd_workspace_bytes": (_SZ, [_I, _I, _I]),
+    "rte_macro_fused_wgrad_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "rte_macro_fused_prep": (_I, [_P, _P, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "rte_macro_fused_bwd_workspace_bytes": (_SZ, [_I, _I]),
+    "rte_macro_fused_fwd": (_I, [_P, _P, _I, _I, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P,
+                                 _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
+    "rte_macro_fused_sum": (_I, [_P, _I, _F, _P, _P]),
+    "rte_macro_fused_bwd": (_I, [_P, _P, _P, _F, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P,
+                                 _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _P, _I, _P, _P, _SZ, _P]),
+    "rte_macro_fused_wgrad": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                   _P, _P, _SZ, _P]),
     "rte_attention_fwd": (_I, [_P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P]),
     "rte_attention_bwd": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P]),
     "rte_attention_bwd_qkv": (_I, [_P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P]),

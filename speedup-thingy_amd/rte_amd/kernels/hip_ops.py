@@ -1321,6 +1321,270 @@ def macro_bounded(h, h0, key, pk, v, u, gain, bias, scale, c: float, eps: float 
     return MacroBoundedFn.apply(h, h0, key, pk, v, u, gain, bias, scale, c, eps)
 
 
+# ----------------------------------------------------------------------------- fused macro operator
+
+MACRO_FUSED_RANK = 32
+
+
+def macro_fused_supported(v: torch.Tensor, u: torch.Tensor, repeats: int = 1) -> bool:
+    """Shapes the fused operator kernels take: hidden rank 32, d a multiple of 128 up to 1024,
+    at most 8 repeats of a source sample."""
+    d = u.shape[-1]
+    return (v.shape[-1] == MACRO_FUSED_RANK and u.shape[-2] == MACRO_FUSED_RANK and v.shape[-2] == 3 * d
+            and d % 128 == 0 and 128 <= d <= 1024 and 1 <= repeats <= 8)
+
+
+def macro_fused_weights(v: torch.Tensor, u: torch.Tensor):
+    """bf16 (V, [V1; V3]^T, V2^T, U, U^T) of V [R, K, 3d, 32] and U [R, K, 32, d] in the layouts the fused
+    kernels read, made in one launch; while a per-step cache is open (bf16_cache_begin) they are
+    made once per step and stream."""
+    _lib.require_device_tensors("macro_fused_weights", v, u)
+    G = v.shape[0] * v.shape[1]
+    d = u.shape[-1]
+    key = None
+    if _BF16_CACHE_ON[0] and isinstance(v, torch.nn.Parameter) and isinstance(u, torch.nn.Parameter):
+        key = ("macro_fused", v.data_ptr(), v._version, u.data_ptr(), u._version, _lib.stream_ptr())
+        hit = _BF16_CACHE.get(key)
+        if hit is not None:
+            return hit
+    vf = v.detach().reshape(G, 3 * d, MACRO_FUSED_RANK).contiguous().to(F32)
+    uf = u.detach().reshape(G, MACRO_FUSED_RANK, d).contiguous().to(F32)
+    dev = v.device
+    vb = torch.empty((G, 3 * d, MACRO_FUSED_RANK), dtype=BF16, device=dev)
+    vct = torch.empty((G, MACRO_FUSED_RANK, 2 * d), dtype=BF16, device=dev)
+    v2t = torch.empty((G, MACRO_FUSED_RANK, d), dtype=BF16, device=dev)
+    ub = torch.empty((G, MACRO_FUSED_RANK, d), dtype=BF16, device=dev)
+    ut = torch.empty((G, d, MACRO_FUSED_RANK), dtype=BF16, device=dev)
+    call("rte_macro_fused_prep", ptr(vf), ptr(uf), G, d, ptr(vb), ptr(vct), ptr(v2t), ptr(ub), ptr(ut), _s())
+    out = (vb, vct, v2t, ub, ut)
+    if key is not None:
+        _BF16_CACHE[key] = out
+    return out
+
+
+class _MacroCall:
+    """Buffers of one fused operator application (forward outputs saved for the backward).
+    Per-sample buffers may be views into larger ones shared by two applications."""
+
+    def __init__(self, h, h0, key, x2, pooled, a, sa, S, d):
+        self.h, self.h0, self.key = h, h0, key
+        self.Bh, self.Bh0, self.B = h.shape[0], h0.shape[0], key.numel()
+        self.S, self.d = S, d
+        self.x2, self.pooled, self.a, self.sa = x2, pooled, a, sa
+        dev = h.device
+        self.rstd = torch.empty((self.Bh * S,), dtype=F32, device=dev)
+        self.P = torch.empty((self.B, MACRO_FUSED_RANK), dtype=F32, device=dev)
+        self.out = torch.empty((self.B, S, d), dtype=F32, device=dev)
+
+    def forward(self, G, eps, w, tabs, c, mse_ref=None, mse_part=None):
+        vb, vct, v2t, ub, ut = w
+        nb = _lib.load().rte_macro_fused_fwd_workspace_bytes(self.Bh, self.S, self.d)
+        ws, nbytes = workspace(nb, self.h.device)
+        call("rte_macro_fused_fwd", ptr(self.h), ptr(self.h0), self.Bh, self.Bh0, ptr(self.key), self.B, self.S,
+             self.d, G, float(eps), ptr(vb), ptr(vct), ptr(ut), ptr(tabs[0]), ptr(tabs[1]), ptr(tabs[2]), float(c),
+             ptr(self.x2), ptr(self.rstd), ptr(self.pooled), ptr(self.P), ptr(self.a), ptr(self.sa), ptr(self.out),
+             ptr(mse_ref), ptr(mse_part), ws, nbytes, _s())
+
+    def backward(self, G, w, tabs, c, du, da, part_tab, part_da, dsum, dh, *, dout=None, diff=None, nsplit=0,
+                 dh0=None, dh0_into_dh=False, extra=None, n_extra=0):
+        """diff = (p, q, g, mul): samples b < nsplit take mul g (p - q) as their upstream gradient,
+        the others dout's row block b - nsplit."""
+        vb, vct, v2t, ub, ut = w
+        p, q, g, mul = diff if diff is not None else (None, None, None, 0.0)
+        nb = _lib.load().rte_macro_fused_bwd_workspace_bytes(self.B, self.S)
+        ws, nbytes = workspace(nb, self.h.device)
+        call("rte_macro_fused_bwd", ptr(p), ptr(q), ptr(g), float(mul), int(nsplit), ptr(dout), ptr(self.h),
+             ptr(self.rstd), ptr(self.x2), self.Bh, ptr(self.key), self.B, self.S, self.d, G, ptr(self.a),
+             ptr(self.sa), ptr(vb), ptr(v2t), ptr(ub), ptr(ut), ptr(tabs[0]), ptr(tabs[1]), ptr(tabs[2]), float(c),
+             ptr(du), ptr(da), ptr(part_tab), ptr(part_da), ptr(dh), ptr(dh0), int(dh0_into_dh), ptr(extra),
+             int(n_extra), ptr(dsum), ws, nbytes, _s())
+
+
+def _macro_tabs(gain, bias, scale, G, d):
+    return [t.detach().reshape(G, d).contiguous().to(F32) for t in (gain, bias, scale)]
+
+
+def _macro_wgrad(keys, B0, Bh0, B1, Bh1, S, d, G, x2, sa, du, da, pooled, dsum, part_tab, need, v_shape, u_shape,
+                 t_shape, dev):
+    """(dV, dU, dgain, dbias, dscale) of one or two operator applications listed together."""
+    dU = torch.empty((G, MACRO_FUSED_RANK, d), dtype=F32, device=dev) if need[1] else None
+    dV = torch.empty((G, 3 * d, MACRO_FUSED_RANK), dtype=F32, device=dev) if need[0] else None
+    tabs = [torch.empty((G, d), dtype=F32, device=dev) if need[2 + i] else None for i in range(3)]
+    nb = _lib.load().rte_macro_fused_wgrad_workspace_bytes(B0 + B1, S, d, G)
+    ws, nbytes = workspace(nb, dev)
+    call("rte_macro_fused_wgrad", ptr(keys), B0, Bh0, B1, Bh1, S, d, G, ptr(x2), ptr(sa), ptr(du), ptr(da),
+         ptr(pooled), ptr(dsum), ptr(part_tab), ptr(dU), ptr(dV), ptr(tabs[0]), ptr(tabs[1]), ptr(tabs[2]), ws,
+         nbytes, _s())
+    return (None if dV is None else dV.view(v_shape), None if dU is None else dU.view(u_shape),
+            *(None if t is None else t.view(t_shape) for t in tabs))
+
+
+class MacroFusedFn(torch.autograd.Function):
+    """The bounded-residual macro operator Phi (rte/macro.py:201-236, default options) at hidden
+    rank 32 on the fused kernels:
+
+        a   = [rmsnorm(h) | h0] @ [V1; V3][key] + mean_s(rmsnorm(h)) @ V2[key]
+        out = h + c * scale[key] * tanh(gain[key] * h + silu(a) @ U[key] + bias[key])
+
+    (the reference's z = [rmsnorm(h) | mean | h0] @ V, split by rows of V).  Sample b reads
+    h[b % len(h)] and h0[b % len(h0)] (len(h0) | len(h) | len(key), at most 8 repeats).  One
+    workgroup owns 64 rows of one sample, so its products use a single key's matrices; weight
+    gradients are grouped-K reductions over each key's rows in a fixed order."""
+
+    @staticmethod
+    def forward(ctx, h, h0, key, v, u, gain, bias, scale, c, eps):
+        _lib.require_device_tensors("macro_fused", h, h0, key, v, u, gain, bias, scale)
+        Bh, S, d = h.shape
+        Bh0 = h0.shape[0]
+        kv = key.reshape(-1).contiguous().to(torch.int64)
+        B = kv.numel()
+        if Bh0 < 1 or Bh % Bh0 or B % Bh or B // Bh > 8 or h0.shape[1:] != h.shape[1:]:
+            raise ValueError("macro_fused: need len(h0) | len(h) | len(key) with at most 8 repeats of h")
+        if not macro_fused_supported(v, u, B // Bh):
+            raise ValueError("macro_fused: needs hidden rank 32 and d a multiple of 128 up to 1024")
+        G = v.shape[0] * v.shape[1]
+        same = h is h0
+        hv = h.detach().contiguous().to(F32)
+        h0v = hv if same else h0.detach().contiguous().to(F32)
+        dev = h.device
+        w = macro_fused_weights(v, u)
+        tabs = _macro_tabs(gain, bias, scale, G, d)
+        x2 = torch.empty((Bh * S, 2 * d), dtype=BF16, device=dev)
+        pooled = torch.empty((Bh, d), dtype=BF16, device=dev)
+        a = torch.empty((B * S, MACRO_FUSED_RANK), dtype=F32, device=dev)
+        sa = torch.empty((B * S, MACRO_FUSED_RANK), dtype=BF16, device=dev)
+        mc = _MacroCall(hv, h0v, kv, x2, pooled, a, sa, S, d)
+        mc.forward(G, eps, w, tabs, c)
+        out, mc.out = mc.out, None  # the output is not needed by the backward
+        mc.h = mc.h0 = None         # saved below (version-checked)
+        ctx.save_for_backward(hv)
+        ctx.mc, ctx.w, ctx.tabs = mc, w, tabs
+        ctx.meta = (G, float(c), same, v.shape, u.shape, gain.shape, h.dtype, h0.dtype)
+        return out.to(h.dtype)
+
+    @staticmethod
+    def backward(ctx, dout):
+        mc, w, tabs = ctx.mc, ctx.w, ctx.tabs
+        (mc.h,) = ctx.saved_tensors
+        G, c, same, v_shape, u_shape, t_shape, h_dt, h0_dt = ctx.meta
+        nia = ctx.needs_input_grad
+        B, Bh, Bh0, S, d = mc.B, mc.Bh, mc.Bh0, mc.S, mc.d
+        dev = mc.h.device
+        T = (S + 31) // 32
+        do = dout.contiguous().to(F32)
+        du = torch.empty((B * S, d), dtype=BF16, device=dev)
+        da = torch.empty((B * S, MACRO_FUSED_RANK), dtype=BF16, device=dev)
+        part_tab = torch.empty((B * T * 3 * d,), dtype=F32, device=dev)
+        part_da = torch.empty((B * T * MACRO_FUSED_RANK,), dtype=F32, device=dev)
+        dsum = torch.empty((B, MACRO_FUSED_RANK), dtype=BF16, device=dev)
+        dh = torch.empty((Bh, S, d), dtype=F32, device=dev)
+        want_h0 = nia[1] and not same
+        dh0 = torch.empty((Bh, S, d), dtype=F32, device=dev) if want_h0 else None
+        mc.backward(G, w, tabs, c, du, da, part_tab, part_da, dsum, dh, dout=do, dh0=dh0, dh0_into_dh=same)
+        grads = _macro_wgrad(mc.key, B, Bh, 0, 0, S, d, G, mc.x2, mc.sa, du, da, mc.pooled, dsum, part_tab,
+                             nia[3:8], v_shape, u_shape, t_shape, dev)
+        if dh0 is not None and Bh0 < Bh:
+            dh0 = dh0.view(Bh // Bh0, Bh0, S, d).sum(0)
+        ctx.mc = ctx.w = ctx.tabs = None
+        return (dh.to(h_dt), None if dh0 is None else dh0.to(h0_dt), None, *grads, None, None)
+
+
+def macro_fused(h, h0, key, v, u, gain, bias, scale, c: float, eps: float = 1e-5):
+    return MacroFusedFn.apply(h, h0, key, v, u, gain, bias, scale, c, eps)
+
+
+class MacroConsistencyFn(torch.autograd.Function):
+    """The macro consistency loss (rte/macro.py:342-359) on the fused operator:
+    mse(Phi_{dst}(h), Phi_{src}(Phi_{src}(h))) over every (s, 2s) stride pair and sample.
+
+    The first application runs the 2 pc b (sample, key) pairs [dst keys; src keys] of the b
+    source samples of h (one h row block per source, 2 pc <= 8 repeats); the second reads the
+    src half of its output with h0 = h.  The MSE is summed inside the second application's
+    forward kernel (per-tile partial sums, fixed order).  The backward takes the MSE gradient
+    inside the operator kernels (no difference tensors), feeds the second application's dh
+    straight into the first one's upstream gradient, adds every path to h in the kernels, and
+    reduces the weight gradients of both applications in one grouped pass."""
+
+    @staticmethod
+    def forward(ctx, h, key_both, key_src, v, u, gain, bias, scale, c, eps):
+        _lib.require_device_tensors("macro_consistency", h, key_both, key_src, v, u, gain, bias, scale)
+        b, S, d = h.shape
+        kb = key_both.reshape(-1).contiguous().to(torch.int64)
+        ks = key_src.reshape(-1).contiguous().to(torch.int64)
+        pcb = ks.numel()
+        if pcb == 0 or pcb % b or kb.numel() != 2 * pcb or 2 * pcb // b > 8:
+            raise ValueError("macro_consistency: need 2 pc b first keys and pc b second keys, 2 pc <= 8")
+        if not macro_fused_supported(v, u, 2 * pcb // b):
+            raise ValueError("macro_consistency: needs hidden rank 32 and d a multiple of 128 up to 1024")
+        G = v.shape[0] * v.shape[1]
+        dev = h.device
+        hv = h.detach().contiguous().to(F32)
+        w = macro_fused_weights(v, u)
+        tabs = _macro_tabs(gain, bias, scale, G, d)
+        R = MACRO_FUSED_RANK
+        x2 = torch.empty(((b + pcb) * S, 2 * d), dtype=BF16, device=dev)
+        pooled = torch.empty((b + pcb, d), dtype=BF16, device=dev)
+        a = torch.empty((3 * pcb * S, R), dtype=F32, device=dev)
+        sa = torch.empty((3 * pcb * S, R), dtype=BF16, device=dev)
+        n0 = 2 * pcb * S
+        both = _MacroCall(hv, hv, kb, x2[:b * S], pooled[:b], a[:n0], sa[:n0], S, d)
+        both.forward(G, eps, w, tabs, c)
+        direct, first = both.out[:pcb], both.out[pcb:]
+        T = (S + 31) // 32
+        mse_part = torch.empty((pcb * T,), dtype=F32, device=dev)
+        twice = _MacroCall(first, hv, ks, x2[b * S:], pooled[b:], a[n0:], sa[n0:], S, d)
+        twice.forward(G, eps, w, tabs, c, mse_ref=direct, mse_part=mse_part)
+        n = pcb * S * d
+        loss = torch.empty((), dtype=F32, device=dev)
+        call("rte_macro_fused_sum", ptr(mse_part), mse_part.numel(), float(1.0 / n), ptr(loss), _s())
+        ctx.calls = (both, twice)
+        ctx.bufs = (x2, pooled, a, sa, torch.cat([kb, ks]))
+        ctx.w, ctx.tabs = w, tabs
+        ctx.meta = (G, float(c), b, pcb, S, d, n, v.shape, u.shape, gain.shape, h.dtype)
+        return loss
+
+    @staticmethod
+    def backward(ctx, g):
+        both, twice = ctx.calls
+        x2, pooled, a, sa, keys = ctx.bufs
+        w, tabs = ctx.w, ctx.tabs
+        G, c, b, pcb, S, d, n, v_shape, u_shape, t_shape, h_dt = ctx.meta
+        nia = ctx.needs_input_grad
+        dev = a.device
+        R = MACRO_FUSED_RANK
+        T = (S + 31) // 32
+        gv = g.reshape(1).contiguous().to(F32)
+        mul = 2.0 / n
+        rows = 3 * pcb * S
+        du = torch.empty((rows, d), dtype=BF16, device=dev)
+        da = torch.empty((rows, R), dtype=BF16, device=dev)
+        part_tab = torch.empty((3 * pcb * T * 3 * d,), dtype=F32, device=dev)
+        part_da = torch.empty((3 * pcb * T * R,), dtype=F32, device=dev)
+        dsum = torch.empty((3 * pcb, R), dtype=BF16, device=dev)
+        n0 = 2 * pcb * S
+        t0, r0 = 2 * pcb * T * 3 * d, 2 * pcb * T * R
+        direct = both.out[:pcb]
+        # second application: d loss / d twice = mul g (twice - direct); its dh is the upstream
+        # gradient of the first application's src half, its dh0 goes to h
+        d_first = torch.empty((pcb, S, d), dtype=F32, device=dev)
+        dh0_tw = torch.empty((pcb, S, d), dtype=F32, device=dev)
+        twice.backward(G, w, tabs, c, du[n0:], da[n0:], part_tab[t0:], part_da[r0:], dsum[2 * pcb:], d_first,
+                       diff=(twice.out, direct, gv, mul), nsplit=pcb, dh0=dh0_tw)
+        # first application: dst half mul g (direct - twice), src half d_first; h = h0 = h
+        dh = torch.empty((b, S, d), dtype=F32, device=dev)
+        both.backward(G, w, tabs, c, du[:n0], da[:n0], part_tab[:t0], part_da[:r0], dsum[:2 * pcb], dh, dout=d_first,
+                      diff=(direct, twice.out, gv, mul), nsplit=pcb, dh0_into_dh=True, extra=dh0_tw,
+                      n_extra=pcb // b)
+        grads = _macro_wgrad(keys, 2 * pcb, b, pcb, pcb, S, d, G, x2, sa, du, da, pooled, dsum, part_tab,
+                             nia[3:8], v_shape, u_shape, t_shape, dev)
+        ctx.calls = ctx.bufs = ctx.w = ctx.tabs = None
+        return (dh.to(h_dt) if nia[0] else None, None, None, *grads, None, None)
+
+
+def macro_consistency(h, key_both, key_src, v, u, gain, bias, scale, c: float, eps: float = 1e-5):
+    return MacroConsistencyFn.apply(h, key_both, key_src, v, u, gain, bias, scale, c, eps)
+
+
 class MseFn(torch.autograd.Function):
     """mean((a - b)^2) over all elements (F.mse_loss with mean reduction), fp32, in a fixed
     reduction order."""

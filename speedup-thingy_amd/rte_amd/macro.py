@@ -143,6 +143,11 @@ class MacroOperators(nn.Module):
         R, Kk = self.v.shape[0], self.v.shape[1]
         key = recipe_ids.long() * Kk + stride_ids.long()
         B = key.numel()  # may exceed h's samples on the fused path (repeated sources)
+        if (self._fused_bounded() and B % h.shape[0] == 0
+                and hip_ops.macro_fused_supported(self.v, self.u, B // h.shape[0])):
+            # rank 32: one fused kernel chain per direction, no row grouping needed
+            return hip_ops.macro_fused(h, h0, key, self.v, self.u, self.d_gain, self.bias, self.update_scale,
+                                       self.config.macro_update_scale)
         pk = hip_ops.group_rows(key[:, None].expand(B, S), R * Kk)
         if self._fused_bounded():
             # default options: fused prologue / epilogue kernels around the two grouped GEMMs
@@ -224,6 +229,13 @@ class MacroOperators(nn.Module):
         r_rep = recipe_ids.repeat(pc)
         src = self.cons_src_idx.repeat_interleave(b)
         dst = self.cons_dst_idx.repeat_interleave(b)
+        if h is h0 and self._fused_bounded() and hip_ops.macro_fused_supported(self.v, self.u, 2 * pc):
+            # both operator applications, the MSE and every backward path in the fused kernels
+            Kk = self.v.shape[1]
+            rk = r_rep.long() * Kk
+            return hip_ops.macro_consistency(h, torch.cat([rk + dst, rk + src]), rk + src, self.v, self.u,
+                                             self.d_gain, self.bias, self.update_scale,
+                                             self.config.macro_update_scale)
         if self._fused_bounded() and 2 * pc <= 4:
             # Phi_{2s}(h) and the first Phi_s(h) read the same source batch: one operator call
             # over the 2 pc b (sample, key) pairs; the second Phi_s reads its output with h0

@@ -589,6 +589,97 @@ def test_consistency_loss_fused_matches_reference_formula():
         assert rel_err(a.double().cpu().numpy(), p.grad.double().cpu().numpy()) < BF16_RTOL, name
 
 
+@pytest.mark.parametrize("d,B,S,depths", [(256, 7, 150, [1, 2, 4]), (1024, 3, 70, [1, 2, 4, 8]), (512, 40, 64, [1, 2, 4])])
+def test_macro_fused_operator_matches_reference(d, B, S, depths):
+    """The fused rank-32 operator (several 64-row tiles per sample with a ragged last one, d up to
+    1024): forward and every gradient against fp64 autograd of the reference formula."""
+    from helpers import rel_err
+    from rte_amd.kernels import hip_ops
+    from rte_amd.macro import MacroOperators
+
+    cfg = _model_cfg(d_model=d, n_heads=d // 64, macro_rank=32, recipe_count=6, depth_choices=depths,
+                     t_max=max(depths), macro_update_scale_init=0.5)
+    torch.manual_seed(11)
+    mac = MacroOperators(cfg).cuda()
+    assert hip_ops.macro_fused_supported(mac.v, mac.u)
+    with torch.no_grad():
+        mac.d_gain.normal_(0, 0.1)
+        mac.bias.normal_(0, 0.1)
+        mac.u.normal_(0, 0.05)
+    gen = torch.Generator(device="cuda").manual_seed(12)
+    h = torch.randn(B, S, d, device="cuda", generator=gen, requires_grad=True)
+    h0 = torch.randn(B, S, d, device="cuda", generator=gen, requires_grad=True)
+    rid = torch.randint(0, 6, (B,), device="cuda", generator=gen)
+    sid = torch.randint(0, len(depths), (B,), device="cuda", generator=gen)
+    g = torch.randn(B, S, d, device="cuda", generator=gen)
+    print(f"macro fused d={d} B={B} S={S}", flush=True)
+    out = mac._apply_bounded(h, h0, rid, sid)
+    out.backward(g)
+    names = ("d_gain", "bias", "update_scale", "v", "u")
+    tp = {k: getattr(mac, k).detach().double().cpu().requires_grad_(True) for k in names}
+    th = h.detach().double().cpu().requires_grad_(True)
+    th0 = h0.detach().double().cpu().requires_grad_(True)
+    ref = _torch_bounded(th, th0, rid.cpu(), sid.cpu(), tp, cfg.macro_update_scale)
+    (ref * g.double().cpu()).sum().backward()
+    assert_rel(out.detach().double().cpu().numpy() - th.detach().numpy(), (ref - th).detach().numpy(), BF16_RTOL,
+               "delta")
+    for k in names:
+        assert_rel(getattr(mac, k).grad.double().cpu().numpy(), tp[k].grad.numpy(), BF16_RTOL, f"d{k}")
+    assert_rel(h.grad.double().cpu().numpy(), th.grad.numpy(), BF16_RTOL, "dh")
+    assert_rel(h0.grad.double().cpu().numpy(), th0.grad.numpy(), BF16_RTOL, "dh0")
+    # same tensor as h and h0 (the hot path's call): one gradient, equal to the sum of both paths
+    for p in names:
+        getattr(mac, p).grad = None
+    hh = h.detach().clone().requires_grad_(True)
+    mac._apply_bounded(hh, hh, rid, sid).backward(g)
+    th2 = th.detach().clone().requires_grad_(True)
+    _torch_bounded(th2, th2, rid.cpu(), sid.cpu(), {k: v.detach() for k, v in tp.items()},
+                   cfg.macro_update_scale).mul(g.double().cpu()).sum().backward()
+    assert_rel(hh.grad.double().cpu().numpy(), th2.grad.numpy(), BF16_RTOL, "dh (h is h0)")
+    assert rel_err(out.detach().double().cpu().numpy(), ref.detach().numpy()) < 1e-3
+
+
+@pytest.mark.parametrize("d,B,S,depths", [(256, 5, 80, [1, 2, 4, 8]), (512, 16, 64, [1, 2, 4])])
+def test_macro_fused_consistency_matches_reference(d, B, S, depths):
+    """The fused consistency loss (both operator applications, the MSE and the backward in the
+    fused kernels, 2 pc up to 6 repeats) against fp64 autograd of rte/macro.py:342-359 restated
+    with explicit copies."""
+    from rte_amd.macro import MacroOperators
+
+    cfg = _model_cfg(d_model=d, n_heads=d // 64, macro_rank=32, recipe_count=6, depth_choices=depths,
+                     t_max=max(depths))
+    torch.manual_seed(13)
+    mac = MacroOperators(cfg).cuda()
+    with torch.no_grad():
+        mac.d_gain.normal_(0, 0.1)
+        mac.bias.normal_(0, 0.1)
+        mac.u.normal_(0, 0.05)
+    gen = torch.Generator(device="cuda").manual_seed(14)
+    h = torch.randn(B, S, d, device="cuda", generator=gen, requires_grad=True)
+    rid = torch.randint(0, 6, (B,), device="cuda", generator=gen)
+    print(f"fused consistency d={d} B={B} S={S} pairs={mac.cons_src_idx.numel()}", flush=True)
+    loss = mac.consistency_loss(h, h, rid)
+    loss.backward()
+    names = ("d_gain", "bias", "v", "u")
+    tp = {k: getattr(mac, k).detach().double().cpu().requires_grad_(k != "update_scale")
+          for k in names + ("update_scale",)}
+    th = h.detach().double().cpu().requires_grad_(True)
+    pc = mac.cons_src_idx.numel()
+    r_rep = rid.cpu().repeat(pc)
+    src = mac.cons_src_idx.cpu().repeat_interleave(B)
+    dst = mac.cons_dst_idx.cpu().repeat_interleave(B)
+    h_rep = th.repeat(pc, 1, 1)
+    c = cfg.macro_update_scale
+    direct = _torch_bounded(h_rep, h_rep, r_rep, dst, tp, c)
+    twice = _torch_bounded(_torch_bounded(h_rep, h_rep, r_rep, src, tp, c), h_rep, r_rep, src, tp, c)
+    ref = (direct - twice).square().mean()
+    ref.backward()
+    assert abs(loss.item() - ref.item()) <= 2e-2 * abs(ref.item()) + 1e-9
+    for k in names:
+        assert_rel(getattr(mac, k).grad.double().cpu().numpy(), tp[k].grad.numpy(), BF16_RTOL, f"d{k}")
+    assert_rel(h.grad.double().cpu().numpy(), th.grad.numpy(), BF16_RTOL, "dh")
+
+
 @pytest.mark.parametrize("n", [1, 7, 4096, 100003, 256 * 64 * 512])
 def test_mse_matches_torch(n):
     """Fused mean squared difference and its gradients against float64 torch; bitwise repeatable."""
