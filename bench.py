@@ -7,9 +7,10 @@ seq 64, token ids Zipf(1.1), fixed-count audit of 1 sample (p = 1/128), AdamW.  
 seeded data, random-init weights.  One step = forward_macro + audit correction + backward
 + AdamW, exactly TrainEngine.train_step.
 
-Prints ONE JSON line.  Also reports the roofline of the dominant kernel (timed live with
-HIP events on the launch stream) and a CPU baseline (the numpy oracle of the cluster-pool
-SwiGLU layer, BASELINE.json configs[0], on a bounded token sample, this host's cores).
+Prints ONE JSON line.  Also reports the roofline of the operation that takes the most time per
+step (every candidate timed live with HIP events on the launch stream, its HBM traffic from two
+rocprofv3 --pmc runs of this script calibrated against a copy kernel) and a CPU baseline (the
+cfg3 step ported to torch on this host's cores, float32, on a bounded batch sample).
 """
 
 from __future__ import annotations
@@ -78,9 +79,10 @@ def zipf_batch(gen, vocab: int, batch: int, seq: int, device):
 
 
 def kernel_candidates(B: int, S: int):
-    """Hot kernels of the step at their cfg3 shapes.  Each entry: name, launches per step,
-    kernels per call, algorithmic flop and HBM bytes per call (inputs read once, outputs
-    written once), and fn launching it on the current stream."""
+    """Hot operations of the step at their cfg3 shapes, each one call of a C-ABI entry point (one
+    or several kernels).  Entry: name, calls per step, kernels per call, algorithmic flop and HBM
+    bytes per call (every input read once, every output written once), fn launching it on the
+    current stream."""
     import torch
 
     from rte_amd import _lib
@@ -111,29 +113,63 @@ def kernel_candidates(B: int, S: int):
     yp = torch.empty(P, d, device=dev, dtype=bf)
     head_out = torch.empty(T, V, device=dev, dtype=torch.float32)
     st = _lib.stream_ptr
+    lib = _lib.load()
+
+    def gemm(a, lda, a_t, b, ldb, b_t, c, ldc, M, N, K, ws=None, wsb=0):
+        _lib.call("rte_gemm_bf16", a.data_ptr(), lda, a_t, None, b.data_ptr(), ldb, b_t, None, c.data_ptr(), ldc, 1, M,
+                  N, K, 1.0, 0.0, None, 0, None if ws is None else ws.data_ptr(), wsb, st())
 
     def head():
-        _lib.call("rte_gemm_bf16", x.data_ptr(), d, 0, None, w_head.data_ptr(), d, 0, None, head_out.data_ptr(), V,
-                  1, T, V, d, 1.0, 0.0, None, 0, None, 0, st())
+        gemm(x, d, 0, w_head, d, 0, head_out, V, T, V, d)
 
     def qkv():
         _lib.call("rte_qkv_rope_fwd", x.data_ptr(), wqkv.data_ptr(), cos.data_ptr(), sin.data_ptr(), B, S, 8, 64,
                   q.data_ptr(), kk.data_ptr(), vv.data_ptr(), st())
 
+    def split_ws(M, N, K):
+        nb = lib.rte_gemm_workspace_bytes(M, N, K)
+        return torch.empty(max(nb, 16), device=dev, dtype=torch.uint8), nb
+
     dqkv = torch.randn(T, 3 * d, device=dev, generator=g).to(bf)
     dw_qkv = torch.empty(3 * d, d, device=dev, dtype=torch.float32)
-    ws_bytes = _lib.load().rte_gemm_workspace_bytes(3 * d, d, T)
-    ws = torch.empty(max(ws_bytes, 16), device=dev, dtype=torch.uint8)
+    ws_q, wsb_q = split_ws(3 * d, d, T)
 
-    def wgrad():
+    def wgrad_qkv():
         # dW_qkv[c, :] = sum_t dqkv[t, c] x[t, :]  (both operands token-major: layout T, split-K)
-        _lib.call("rte_gemm_bf16", dqkv.data_ptr(), 3 * d, 1, None, x.data_ptr(), d, 1, None, dw_qkv.data_ptr(), d,
-                  1, 3 * d, d, T, 1.0, 0.0, None, 0, ws.data_ptr(), ws_bytes, st())
+        gemm(dqkv, 3 * d, 1, x, d, 1, dw_qkv, d, 3 * d, d, T, ws_q, wsb_q)
+
+    dlog = (torch.randn(T, V, device=dev, generator=g) * 0.01).to(bf)
+    dx_head = torch.empty(T, d, device=dev, dtype=torch.float32)
+    dw_head = torch.empty(V, d, device=dev, dtype=torch.float32)
+    ws_h, wsb_h = split_ws(V, d, T)
+
+    def head_dx():
+        # dX = dlogits @ W  (W [V, d]: column index contiguous, layout T)
+        gemm(dlog, V, 0, w_head, d, 1, dx_head, d, T, d, V)
+
+    def head_wgrad():
+        gemm(dlog, V, 1, x, d, 1, dw_head, d, V, d, T, ws_h, wsb_h)
 
     def ffn_fwd():
         _lib.call("rte_grouped_swiglu_fwd", x.data_ptr(), T, d, pk.offsets.data_ptr(), C, n, P,
                   pk.tok_of_slot.data_ptr(), pk.pair_of_slot.data_ptr(), pk.w_of_slot.data_ptr(), wug.data_ptr(),
                   wd.data_ptr(), F, ug.data_ptr(), zw.data_ptr(), yp.data_ptr(), st())
+
+    ffn_fwd()
+    dpool = (torch.randn(T, d, device=dev, generator=g) * 0.01).to(bf)
+    dug = torch.empty(P, 2 * n, device=dev, dtype=bf)
+    dw_slot = torch.empty(P, device=dev, dtype=torch.float32)
+    dx_pairs = torch.empty(P, d, device=dev, dtype=bf)
+    dwug = torch.empty(2 * F, d, device=dev, dtype=torch.float32)
+    dwd = torch.empty(d, F, device=dev, dtype=torch.float32)
+    gsb = lib.rte_grouped_swiglu_bwd_workspace_bytes(P, C, n, d)
+    gs_ws = torch.empty(max(gsb, 16), device=dev, dtype=torch.uint8)
+
+    def ffn_bwd():
+        _lib.call("rte_grouped_swiglu_bwd", dpool.data_ptr(), x.data_ptr(), T, d, pk.offsets.data_ptr(), C, n, P,
+                  pk.tok_of_slot.data_ptr(), pk.pair_of_slot.data_ptr(), pk.w_of_slot.data_ptr(), wug.data_ptr(),
+                  wd.data_ptr(), F, ug.data_ptr(), zw.data_ptr(), dug.data_ptr(), dw_slot.data_ptr(),
+                  dx_pairs.data_ptr(), dwug.data_ptr(), dwd.data_ptr(), gs_ws.data_ptr(), gsb, st())
 
     out_pool = torch.empty(T, d, device=dev, dtype=torch.float32)
 
@@ -146,7 +182,7 @@ def kernel_candidates(B: int, S: int):
     def topk():
         _lib.call("rte_route_topk", logits.data_ptr(), T, C, k, ids_out.data_ptr(), w_out.data_ptr(), st())
 
-    pk_ws_bytes = _lib.load().rte_pack_workspace_bytes(P, C)
+    pk_ws_bytes = lib.rte_pack_workspace_bytes(P, C)
     pk_ws = torch.empty(max(pk_ws_bytes, 16), device=dev, dtype=torch.uint8)
     pk_out = [torch.empty(P, device=dev, dtype=torch.int32) for _ in range(4)]
     pk_off = torch.empty(C + 1, device=dev, dtype=torch.int32)
@@ -157,14 +193,56 @@ def kernel_candidates(B: int, S: int):
                   pk_out[1].data_ptr(), pk_out[2].data_ptr(), pk_w.data_ptr(), None, pk_ws.data_ptr(), pk_ws_bytes,
                   st())
 
+    # macro consistency loss (both operator applications, MSE, backward, weight gradients): the
+    # cfg3 operator tables (16 recipes x 3 strides, rank 32) over the whole batch's h0
+    R3, K3, r = 16, 3, 32
+    mv = (torch.randn(R3, K3, 3 * d, r, device=dev, generator=g) / (3 * d) ** 0.5).requires_grad_()
+    mu = (torch.randn(R3, K3, r, d, device=dev, generator=g) * 0.05).requires_grad_()
+    mg = (torch.randn(R3, K3, d, device=dev, generator=g) * 0.1).requires_grad_()
+    mb = (torch.randn(R3, K3, d, device=dev, generator=g) * 0.1).requires_grad_()
+    ms = torch.ones(R3, K3, d, device=dev)
+    mh = torch.randn(B, S, d, device=dev, generator=g).requires_grad_()
+    rid = torch.randint(0, R3, (B,), device=dev, generator=g)
+    src_i, dst_i = torch.tensor([0, 1], device=dev), torch.tensor([1, 2], device=dev)
+    rk = rid.repeat(2) * K3
+    kb = torch.cat([rk + dst_i.repeat_interleave(B), rk + src_i.repeat_interleave(B)])
+    ks = rk + src_i.repeat_interleave(B)
+
+    def macro_cons():
+        loss = hip_ops.macro_consistency(mh, kb, ks, mv, mu, mg, mb, ms, 0.1)
+        torch.autograd.grad(loss, [mh, mv, mu, mg, mb])
+
+    # bytes of the macro consistency: forward reads h (2 reads), writes x2 (bf16 2d per source
+    # row, 1 + pc sources) and both outputs, reads the first output and the MSE reference; the
+    # backward reads h / first twice, the MSE operands twice per application, writes du (bf16)
+    # and dh / dh0 / d_first, the weight reductions read x2, du and da once per (sample, row)
+    rows_src, rows_both, rows_tw = T, 4 * T, 2 * T
+    f4, b2 = 4.0 * d, 2.0 * d
+    macro_bytes = (rows_src * (2 * f4 + 2 * b2) + rows_both * f4
+                   + rows_tw * (f4 + 2 * b2 + f4 + f4)
+                   + rows_tw * (2 * f4 + 4 * f4 + b2 + 2 * f4) + rows_both * (2 * f4 + b2) + rows_src * f4
+                   + (rows_both + rows_tw) * (2 * b2 + b2))
+    macro_flop = (rows_both + rows_tw) * 2.0 * (2 * d * r + r * d) * 3
+
     return [
         dict(name="gemm_qkv_rope_fwd", per_step=2, kernels=1, flop=2.0 * T * 3 * d * d,
              bytes=2.0 * T * d + 2.0 * 3 * d * d + 3 * 2.0 * T * d, fn=qkv),
         dict(name="gemm_lm_head_fwd", per_step=1, kernels=1, flop=2.0 * T * V * d,
              bytes=2.0 * T * d + 2.0 * V * d + 4.0 * T * V, fn=head),
+        dict(name="gemm_lm_head_dx", per_step=1, kernels=1, flop=2.0 * T * V * d,
+             bytes=2.0 * T * V + 2.0 * V * d + 4.0 * T * d, fn=head_dx),
+        dict(name="gemm_lm_head_wgrad", per_step=1, kernels=2, flop=2.0 * T * V * d,
+             bytes=2.0 * T * V + 2.0 * T * d + 4.0 * V * d, fn=head_wgrad),
+        dict(name="gemm_wgrad_qkv", per_step=2, kernels=2, flop=2.0 * T * 3 * d * d,
+             bytes=2.0 * T * 3 * d + 2.0 * T * d + 4.0 * 3 * d * d, fn=wgrad_qkv),
         # x@[Wup|Wgate]^T with the SwiGLU epilogue, then zw@Wdown into pair-major rows
         dict(name="grouped_swiglu_fwd", per_step=2, kernels=2, flop=2.0 * P * d * 2 * n + 2.0 * P * n * d,
              bytes=2.0 * T * d + 2.0 * 3 * F * d + 2.0 * P * 3 * n + 2.0 * P * d + 12.0 * P, fn=ffn_fwd),
+        # backward: dZ / dW_down, SwiGLU derivative, dX-pairs / dW_up|gate; reads x, dout, weights,
+        # ug, zw, slot tables; writes dug, dw_slot, dx_pairs and the fp32 weight gradients
+        dict(name="grouped_swiglu_bwd", per_step=2, kernels=None, flop=2.0 * (2.0 * P * d * 2 * n + 2.0 * P * n * d),
+             bytes=2.0 * T * d * 2 + 2.0 * 3 * F * d + 2.0 * P * 3 * n + 12.0 * P + 2.0 * P * 2 * n + 4.0 * P
+             + 2.0 * P * d + 4.0 * 3 * F * d, fn=ffn_bwd),
         # combine unit: T*k*d*b + T*k*4 + T*d*b (bf16 rows in, fp32 rows out here)
         dict(name="combine_rows", per_step=2, kernels=1, flop=1.0 * P * d,
              bytes=2.0 * P * d + 4.0 * T * d, fn=combine),
@@ -173,8 +251,8 @@ def kernel_candidates(B: int, S: int):
         # pack unit: P*(4+4) ids + weights in, 4*P*4 + P*4 slot tables out, (C+1)*4 offsets
         dict(name="pack_index", per_step=1, kernels=3, flop=0.0, bytes=8.0 * P + 20.0 * P + 4.0 * (C + 1),
              fn=pack),
-        dict(name="gemm_wgrad_qkv", per_step=2, kernels=2, flop=2.0 * T * 3 * d * d,
-             bytes=2.0 * T * 3 * d + 2.0 * T * d + 4.0 * 3 * d * d, fn=wgrad),
+        dict(name="macro_consistency_fwd_bwd", per_step=1, kernels=None, flop=macro_flop, bytes=macro_bytes,
+             fn=macro_cons),
     ]
 
 
@@ -215,86 +293,143 @@ def roofline_rows(B: int, S: int) -> list[dict]:
         ach = c["flop"] / dt / 1e12 if bound == "mfma" else c["bytes"] / dt / 1e9
         peak = PEAK_BF16_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
         rows.append({"kernel": c["name"], "launches_per_step": c["per_step"], "kernels_per_call": c["kernels"],
-                     "avg_us": round(dt * 1e6, 2), "bound": bound, "achieved": round(ach, 1),
+                     "avg_us": round(dt * 1e6, 2), "us_per_step": round(dt * 1e6 * c["per_step"], 1),
+                     "bound": bound, "achieved": round(ach, 1),
                      "unit": "TFLOP/s" if bound == "mfma" else "GB/s", "peak": peak, "frac": round(ach / peak, 4),
                      "flop": c["flop"], "bytes": c["bytes"],
                      "tflops": round(c["flop"] / dt / 1e12, 1), "gbs": round(c["bytes"] / dt / 1e9, 1)})
+    rows.sort(key=lambda r: -r["us_per_step"])
     return rows
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel), or None."""
-    path = ROOT / "profiles" / "traffic.json"
-    try:
-        data = json.loads(path.read_text())
-    except (OSError, ValueError):
+def _pmc_per_call(csv_dir: Path, counter: str, calls: int, only=None):
+    """Sum of `counter` over the profiled calls' dispatches / calls, in bytes (KiB counters), read
+    from rocprofv3's counter_collection.csv; `only` filters kernel names."""
+    import csv
+
+    files = sorted(csv_dir.rglob("*counter_collection.csv"))
+    if not files:
         return None
-    entry = data.get(kernel)
-    return None if entry is None else entry.get("bytes_per_launch")
+    tot = 0.0
+    with open(files[0]) as fh:
+        for r in csv.DictReader(fh):
+            if r.get("Counter_Name") != counter:
+                continue
+            if only is not None and not only(r.get("Kernel_Name", "")):
+                continue
+            tot += float(r["Counter_Value"])
+    return tot * 1024.0 / calls
 
 
-def profile_kernel(name: str, iters: int, B: int, S: int) -> int:
-    """Launch one candidate kernel `iters` times (the program rocprofv3 --pmc profiles)."""
+COPY_ELEMS = 64 << 20  # calibration: rte_cast_f32_bf16 over 64 Mi elements (reads 256 MiB, writes 128 MiB)
+
+
+def measure_traffic(name: str, B: int, S: int, iters: int = 20, timeout_s: int = 120) -> dict:
+    """HBM bytes per call of candidate `name`, from two rocprofv3 --pmc runs of this script in
+    --profile-kernel mode (FETCH_SIZE, then WRITE_SIZE), each scaled by what the same counter
+    reads for the calibration copy kernel of known size.  Returns {"bytes": ..., ...} or
+    {"bytes": None, "note": why}."""
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not Path(prof).exists():
+        return {"bytes": None, "note": "rocprofv3 not found"}
+    out = {}
+    tmp = Path(tempfile.mkdtemp(prefix="rte_pmc_"))
+    try:
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            d = tmp / counter
+            cmd = [prof, "--pmc", counter, "-d", str(d), "-o", "p", "--output-format", "csv", "--",
+                   sys.executable, str(ROOT / "bench.py"), "--profile-kernel", name, "--with-copy", "--iters",
+                   str(iters), "--batch", str(B), "--seq", str(S)]
+            r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s, cwd=str(ROOT))
+            if r.returncode != 0:
+                return {"bytes": None, "note": f"rocprofv3 --pmc {counter} exited {r.returncode}"}
+            op = _pmc_per_call(d, counter, iters, lambda k: "cast_f32_bf16" not in k)
+            cp = _pmc_per_call(d, counter, iters, lambda k: "cast_f32_bf16" in k)
+            known = COPY_ELEMS * (4.0 if counter == "FETCH_SIZE" else 2.0)
+            if not op or not cp:
+                return {"bytes": None, "note": f"no {counter} rows in the rocprofv3 output"}
+            out[counter] = (op, known / cp)
+    except subprocess.TimeoutExpired:
+        return {"bytes": None, "note": "rocprofv3 --pmc run timed out"}
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    fetch = out["FETCH_SIZE"][0] * out["FETCH_SIZE"][1]
+    write = out["WRITE_SIZE"][0] * out["WRITE_SIZE"][1]
+    return {"bytes": round(fetch + write), "fetch": round(fetch), "write": round(write),
+            "fetch_scale": round(out["FETCH_SIZE"][1], 4), "write_scale": round(out["WRITE_SIZE"][1], 4)}
+
+
+def profile_kernel(name: str, iters: int, B: int, S: int, with_copy: bool = False) -> int:
+    """Launch one candidate `iters` times (the program rocprofv3 --pmc profiles); with_copy (or
+    name 'copy') also launches the calibration copy kernel `iters` times."""
     import torch
 
-    if name == "copy":
-        # calibration: cast 64 Mi fp32 -> bf16 (reads 256 MiB, writes 128 MiB per launch)
-        from rte_amd import _lib
+    from rte_amd import _lib
 
-        n = 64 << 20
-        src = torch.randn(n, device="cuda")
-        dst = torch.empty(n, device="cuda", dtype=torch.bfloat16)
-        for _ in range(iters):
-            _lib.call("rte_cast_f32_bf16", src.data_ptr(), n, dst.data_ptr(), _lib.stream_ptr())
-    else:
+    if name != "copy":
         cands = {c["name"]: c for c in kernel_candidates(B, S)}
+        torch.cuda.synchronize()
         for _ in range(iters):
             cands[name]["fn"]()
+    if with_copy or name == "copy":
+        src = torch.randn(COPY_ELEMS, device="cuda")
+        dst = torch.empty(COPY_ELEMS, device="cuda", dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        for _ in range(iters):
+            _lib.call("rte_cast_f32_bf16", src.data_ptr(), COPY_ELEMS, dst.data_ptr(), _lib.stream_ptr())
     torch.cuda.synchronize()
     print(json.dumps({"profiled": name, "iters": iters}))
     return 0
 
 
-def cpu_baseline(budget_s: float = 15.0) -> dict:
-    """numpy oracle of one cluster-pool SwiGLU layer fwd+bwd at BASELINE configs[0]
-    (d 256, 32 clusters x 32, top-4, fp64 math), on a token sample sized to ~budget_s."""
-    import numpy as np
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    from oracle import cluster_pool as CP
-    from oracle import routing as R
 
-    rng = np.random.default_rng(0)
-    d, C, n, k = 256, 32, 32, 4
-    F = C * n
-    wr = rng.standard_normal((C, d)) * 0.02
-    wug = rng.standard_normal((2 * F, d)) * 0.02
-    wd = rng.standard_normal((d, F)) * 0.02
+def cpu_baseline(budget_s: float = 20.0) -> dict:
+    """The cfg3 recursive_macro train step ported to torch on the host CPU in float32 (the CPU
+    path of the same workload: forward, audit replay, consistency and distillation terms,
+    backward, AdamW), on a batch sample sized so the timed steps take about budget_s."""
+    import torch
 
-    def run(T):
-        x = rng.standard_normal((T, d))
-        ids, w = R.route_topk((x @ wr.T).astype(np.float32), k)
-        out = CP.routed_fwd(x, wug, wd, ids, w, C)
-        CP.routed_bwd(np.ones_like(out) / out.size, x, wr, wug, wd, ids, w, C)
+    from oracle import step_port as SP
 
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    S = 64
+    p = SP.make_params(0)
+    opt = SP.make_optimizer(p)
+    tok, tgt = SP.zipf_tokens(8, S, 1)
+    SP.train_step(p, opt, tok, tgt)  # warm-up
     t0 = time.perf_counter()
-    run(256)
-    per_tok = (time.perf_counter() - t0) / 256
-    T = int(max(256, min(8192, budget_s / 3 / max(per_tok, 1e-9))))
+    SP.train_step(p, opt, tok, tgt)
+    per_sample = (time.perf_counter() - t0) / 8
+    B = int(max(8, min(128, budget_s / 2 / max(per_sample, 1e-9))))
+    tok, tgt = SP.zipf_tokens(B, S, 2)
     times = []
-    for _ in range(3):
+    for _ in range(2):
         t0 = time.perf_counter()
-        run(T)
+        SP.train_step(p, opt, tok, tgt)
         times.append(time.perf_counter() - t0)
-    med = sorted(times)[1]
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or os.cpu_count()
+    best = min(times)
     return {
-        "value": T / med,
+        "value": round(B * S / best, 1),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"numpy oracle, cluster-pool SwiGLU layer fwd+bwd (configs[0] shape: d256, 32x32, top-4), "
-                  f"{T} of 8192 tokens x 3 runs, median; BLAS threads={threads}",
+        "cpu": _cpu_model(),
+        "sample": f"fp32 torch-CPU port of the cfg3 recursive_macro step (oracle/step_port.py), batch {B} of 128 "
+                  f"x seq {S} (rows independent), faster of 2 timed steps after a warm-up; {threads} threads",
     }
 
 
@@ -310,6 +445,8 @@ def main(argv=None) -> int:
     ap.add_argument("--profile-kernel", default=None,
                     help="only launch this roofline candidate (or 'copy', the calibration kernel) --iters times")
     ap.add_argument("--iters", type=int, default=50)
+    ap.add_argument("--with-copy", action="store_true", help="--profile-kernel: also launch the calibration copy")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from Python instead of replaying the captured step graph")
     args = ap.parse_args(argv)
@@ -326,7 +463,7 @@ def main(argv=None) -> int:
         print(json.dumps({"error": "HIP backend unavailable (librte_hip.so not built or no gfx950 device)"}))
         return 1
     if args.profile_kernel:
-        return profile_kernel(args.profile_kernel, args.iters, args.batch, args.seq)
+        return profile_kernel(args.profile_kernel, args.iters, args.batch, args.seq, args.with_copy)
     cfg = cfg3_config(args.batch, args.seq)
     dev = torch.device("cuda:0")
     engine = TrainEngine(cfg, device=dev)
@@ -373,9 +510,10 @@ def main(argv=None) -> int:
         },
     }
     if not args.no_roofline:
-        rows = roofline_rows(args.batch, args.seq)
-        single = [r for r in rows if r["kernels_per_call"] == 1]
-        dom = max(single, key=lambda r: r["avg_us"] * r["launches_per_step"])
+        rows = roofline_rows(args.batch, args.seq)  # sorted by time per step
+        dom = rows[0]
+        traffic = measure_traffic(dom["kernel"], args.batch, args.seq) if not args.no_traffic else {
+            "bytes": None, "note": "--no-traffic"}
         out["roofline"] = {
             "kernel": dom["kernel"],
             "bound": dom["bound"],
@@ -383,8 +521,10 @@ def main(argv=None) -> int:
             "peak": dom["peak"],
             "unit": dom["unit"],
             "frac": dom["frac"],
-            "traffic": measured_traffic(dom["kernel"]),
+            "traffic": traffic["bytes"],
+            "traffic_detail": traffic,
             "avg_us": dom["avg_us"],
+            "us_per_step": dom["us_per_step"],
             "flop_per_launch": dom["flop"],
             "algorithmic_bytes_per_launch": dom["bytes"],
         }

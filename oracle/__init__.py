@@ -36,4 +36,8 @@ How each function is pinned (tests/test_oracle.py):
   router.factorized_topk     brute-force enumeration of the (bank, bank, slot, slot) tuples
   banked.recipe_templates    two hand-enumerated recipe tables (every recipe's banks and
                              groups) with zero balance spread; recipe 0 == dense bank
+
+step_port is not a checker: it is the CPU path of the benchmark's workload (the cfg3 train step
+in float32 torch on the host) that bench.py's cpu_baseline leg times; its test only checks that it
+runs and updates the parameters (parity unpinned: it is never compared with the GPU step).
 """

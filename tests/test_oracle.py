@@ -1125,3 +1125,21 @@ def test_svd_sparse_backward_matches_autograd():
     ((uu * torch.nn.functional.silu(gg))[:, :, None] * twd[s]).sum(1).mul(torch.tensor(dy)).sum().backward()
     for a, b in ((dx, tx), (dwu, twu), (dwg, twg), (dwd, twd)):
         np.testing.assert_allclose(a, b.grad.numpy(), rtol=1e-10, atol=1e-12)
+
+
+def test_step_port_runs_and_updates():
+    """The CPU step port that bench.py times as its baseline: one step on 2 samples gives a
+    finite loss and moves the parameters the step reaches (Phi, core, coda, embedding)."""
+    import torch
+
+    from oracle import step_port as SP
+
+    torch.manual_seed(0)
+    p = SP.make_params(0)
+    before = {k: v.detach().clone() for k, v in p.items()}
+    opt = SP.make_optimizer(p)
+    tok, tgt = SP.zipf_tokens(2, 16, 1)
+    loss = SP.train_step(p, opt, tok, tgt)
+    assert np.isfinite(loss)
+    for k in ("m.v", "core.wqkv", "coda.wug", "embed", "pre.wqkv"):
+        assert not torch.equal(before[k], p[k].detach()), k
