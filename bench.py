@@ -124,7 +124,7 @@ def kernel_candidates(B: int, S: int):
 
     def qkv():
         _lib.call("rte_qkv_rope_fwd", x.data_ptr(), wqkv.data_ptr(), cos.data_ptr(), sin.data_ptr(), B, S, 8, 64,
-                  q.data_ptr(), kk.data_ptr(), vv.data_ptr(), st())
+                  q.data_ptr(), kk.data_ptr(), vv.data_ptr(), None, 0, st())
 
     def split_ws(M, N, K):
         nb = lib.rte_gemm_workspace_bytes(M, N, K)

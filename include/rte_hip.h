@@ -163,9 +163,12 @@ int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, c
 
 /* ---- fused QKV projection + interleaved RoPE (rte/layers.py:53-75, rte/kernels/reference.py:20-37) ----
  * x [B*S, d] bf16, wqkv [3d, d] bf16 (nn.Linear(d, 3d).weight), cos/sin [S, hd] f32.
- * q, k, v written as contiguous [B, H, S, hd] bf16. */
+ * q, k, v written as contiguous [B, H, S, hd] bf16.  workspace (optional, see
+ * rte_gemm_workspace_bytes(B*S, 3d, d)): with few output tiles (short batches) the reduction is
+ * split, the partials added in split order and rotated by the split-K reduce. */
 int rte_qkv_rope_fwd(const void* x, const void* wqkv, const float* cos_t, const float* sin_t, int B, int S,
-                     int H, int hd, void* q, void* k, void* v, void* stream);
+                     int H, int hd, void* q, void* k, void* v, void* workspace, size_t workspace_bytes,
+                     void* stream);
 /* dq/dk/dv: [B,H,S,hd] bf16 with element strides s*[4] (innermost must be 1).
  * dqkv: [B*S, 3d] bf16 workspace (dq = NULL: dqkv is the input, already packed and rotated back
  * by rte_attention_bwd_qkv); dx [B*S, d] bf16; dw [3d, d] f32 (overwritten).

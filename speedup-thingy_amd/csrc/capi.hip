@@ -526,7 +526,8 @@ int rte_dense_swiglu_bwd(const void* dout, const void* x, int T, int d, int F, c
 }
 
 int rte_qkv_rope_fwd(const void* x, const void* wqkv, const float* cos_t, const float* sin_t, int B, int S_,
-                     int H, int hd, void* q, void* k, void* v, void* stream) {
+                     int H, int hd, void* q, void* k, void* v, void* workspace, size_t workspace_bytes,
+                     void* stream) {
   const int d = H * hd;
   RTE_REQUIRE(d % 8 == 0 && hd % 8 == 0, "qkv_rope: head_dim must be a multiple of 8");
   RTE_REQUIRE(((uintptr_t)cos_t & 15) == 0 && ((uintptr_t)sin_t & 15) == 0,
@@ -546,7 +547,7 @@ int rte_qkv_rope_fwd(const void* x, const void* wqkv, const float* cos_t, const 
   p.epi.H = H;
   p.epi.hd = hd;
   p.epi.dmodel = d;
-  return gemm_launch(p, EPI_ROPE_QKV, S(stream));
+  return gemm_launch(p, EPI_ROPE_QKV, S(stream), workspace, workspace_bytes);
 }
 
 int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const int64_t* sk, const void* dv,

@@ -965,7 +965,30 @@ __global__ void __launch_bounds__(256) groupk_reduce_kernel(GemmArgs p, EpiFlags
   store_chunk<4>(p.epi, g, m, n, p.N, v, fl.vec);
 }
 
-// Sums split-K partials in split order and applies the EPI_STORE epilogue.
+// Columns n .. n + 3 of row m of the fused QKV product: RoPE on the q / k parts (pairs (2i, 2i+1)
+// inside the 4 columns, cos / sin of the row's position), bf16 into q / k / v [B, H, S, hd].
+__device__ __forceinline__ void rope_store4(const Epilogue& e, int m, int n, const float* v) {
+  const int part = n / e.dmodel;
+  const int within = n - part * e.dmodel;
+  const int hh = within / e.hd, dim = within - hh * e.hd;
+  const int b = m / e.S, s = m - b * e.S;
+  float o[4] = {v[0], v[1], v[2], v[3]};
+  if (part < 2) {
+    const float4 c = *reinterpret_cast<const float4*>(e.cos_t + (int64_t)s * e.hd + dim);
+    const float4 sn = *reinterpret_cast<const float4*>(e.sin_t + (int64_t)s * e.hd + dim);
+    o[0] = v[0] * c.x - v[1] * sn.x;
+    o[1] = v[1] * c.y + v[0] * sn.y;
+    o[2] = v[2] * c.z - v[3] * sn.z;
+    o[3] = v[3] * c.w + v[2] * sn.w;
+  }
+  bf16* dst = part == 0 ? e.q : (part == 1 ? e.k : e.v);
+  uint2 w;
+  w.x = pack_bf2(o[0], o[1]);
+  w.y = pack_bf2(o[2], o[3]);
+  *reinterpret_cast<uint2*>(dst + (((int64_t)b * e.H + hh) * e.S + s) * e.hd + dim) = w;
+}
+
+// Sums split-K partials in split order and applies the EPI_STORE epilogue (or the QKV RoPE store).
 __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs p, EpiFlags fl) {
   const int chunks = (p.N + 3) / 4;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -992,6 +1015,10 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(GemmArgs p, EpiFlags
   } else {
     for (int s = 0; s < p.splits; ++s)
       for (int t = 0; t < 4 && n + t < p.N; ++t) v[t] += base[s * plane + t];
+  }
+  if (p.epi.q) {  // QKV with RoPE: the split-K path of small-M projections
+    rope_store4(p.epi, m, n, v);
+    return;
   }
   store_chunk<4>(p.epi, 0, m, n, p.N, v, fl.vec);
 }
@@ -1073,6 +1100,7 @@ int launch_cfg(const GemmArgs& p0, hipStream_t stream, void* ws, size_t ws_bytes
       const int max_by_k = p.K / 128;
       if (splits > max_by_k) splits = max_by_k;
       if (splits > kMaxSplits) splits = kMaxSplits;
+      if (p.splits_forced && splits < 2) splits = 2;
       while (splits > 1 && (size_t)splits * p.M * p.N * sizeof(float) > ws_bytes) --splits;
       if (splits > 1) {
         int kc = (p.K + splits - 1) / splits;
@@ -1085,6 +1113,7 @@ int launch_cfg(const GemmArgs& p0, hipStream_t stream, void* ws, size_t ws_bytes
     }
   }
   if (grid.x == 0 || grid.y == 0 || grid.z == 0) return 0;
+  RTE_REQUIRE(EPI != EPI_STORE || p.epi.c || p.splits > 1, "gemm: the QKV split-K path needs at least two splits");
   hipLaunchKernelGGL(fn, grid, dim3(kThreads), lds, stream, p, fl);
   RTE_TRY(check_launch("gemm"));
   if (p.splits > 1) {
@@ -1378,7 +1407,8 @@ int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream, void* ws, s
   const Epilogue& e = p.epi;
   int vec = 1;
   if (epi_kind == EPI_STORE) {
-    RTE_REQUIRE(e.c, "gemm: null output");
+    // no C with the RoPE outputs set: the split-K partials are stored as QKV by the reduce
+    RTE_REQUIRE(e.c || (e.q && p.splits_forced), "gemm: null output");
     const int esz = e.c_f32 ? 4 : 2;
     vec = aligned16(e.c) && (e.ldc * esz) % 16 == 0 && (e.c_gstride * esz) % 16 == 0;
     if (e.resid) vec = vec && aligned16(e.resid) && e.ld_resid % 4 == 0;
@@ -1458,6 +1488,17 @@ int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream, void* ws, s
       RTE_REQUIRE(!p.a_t && !p.b_t, "gemm: QKV epilogue expects layout-N operands");
       RTE_REQUIRE(p.epi.q && p.epi.k && p.epi.v && p.epi.cos_t && p.epi.sin_t, "gemm: QKV outputs");
       RTE_REQUIRE(p.epi.hd % 2 == 0 && p.epi.dmodel * 3 == p.N, "gemm: QKV shape");
+      if (ws && p.mode == MODE_DENSE && p.K >= 256 && p.N % 4 == 0 &&
+          (int64_t)((p.M + 31) / 32) * ((p.N + 127) / 128) < 256 &&
+          ws_bytes >= (size_t)2 * p.M * p.N * sizeof(float)) {
+        // few output tiles (a short sequence batch): split the reduction, the split-K reduce
+        // applies RoPE and the head split (tiles < 256, K >= 256 and room for two partial
+        // planes always give at least two splits)
+        GemmArgs ps = p;
+        ps.epi.c = nullptr;
+        ps.splits_forced = 1;
+        return gemm_launch(ps, EPI_STORE, stream, ws, ws_bytes);
+      }
       if (dl_ok(p)) return launch_dl<EPI_ROPE_QKV>(p, stream, ws, ws_bytes, 1);
       return launch_cfg<128, 128, 64, 2, 2, false, false, EPI_ROPE_QKV>(p, stream, ws, ws_bytes, 1);
     default:

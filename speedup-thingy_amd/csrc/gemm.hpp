@@ -85,6 +85,7 @@ struct GemmArgs {
   int splits = 1;
   int k_chunk = 0;
   float* splitk_ws = nullptr;
+  int splits_forced = 0;           // set: the launch must split (the reduce stores the output)
   // EPI_SWIGLU_FWD only: gate columns read A at k + a_koff2 (two low-rank codes side by
   // side in one A row, e.g. [x U_up | x U_gate]); 0 = both halves read the same A columns.
   int a_koff2 = 0;

@@ -437,8 +437,9 @@ class QKVRopeFn(torch.autograd.Function):
         q = torch.empty((B, n_heads, S, hd), dtype=BF16, device=x.device)
         k = torch.empty_like(q)
         v = torch.empty_like(q)
+        wsp, wsn = _gemm_ws(B * S, 3 * n_heads * hd, n_heads * hd, x.device)
         call("rte_qkv_rope_fwd", ptr(xb), ptr(wb), ptr(cos), ptr(sin), B, S, n_heads, hd, ptr(q), ptr(k),
-             ptr(v), _s())
+             ptr(v), wsp, wsn, _s())
         ctx.save_for_backward(xb, wb, cos, sin)
         ctx.dims = (B, S, n_heads, hd)
         ctx.w_dtype = w.dtype
@@ -490,8 +491,9 @@ class AttnOutProjFn(torch.autograd.Function):
         r = None if resid is None else resid.reshape(T, N).contiguous().to(F32)
         L = torch.tensor(layout, dtype=torch.int64)
         Lw = torch.tensor([K, 0, 0, 0, 0], dtype=torch.int64)
+        wsp, wsn = _gemm_ws(T, N, K, yb.device)
         call("rte_gemm_bf16_split", ptr(yb), L.data_ptr(), 0, ptr(wb), Lw.data_ptr(), 0, ptr(out), N, 1, T, N, K,
-             1.0, 0.0, ptr(r), 0 if r is None else N, None, 0, _s())
+             1.0, 0.0, ptr(r), 0 if r is None else N, wsp, wsn, _s())
         ctx.save_for_backward(yb, wb)
         ctx.has_resid = resid is not None
         ctx.w_dtype = w.dtype
@@ -588,7 +590,9 @@ class QKVRopeAttentionFn(torch.autograd.Function):
         q = torch.empty((B, n_heads, S, hd), dtype=BF16, device=x.device)
         k = torch.empty_like(q)
         v = torch.empty_like(q)
-        call("rte_qkv_rope_fwd", ptr(xb), ptr(wb), ptr(cs), ptr(sn), B, S, n_heads, hd, ptr(q), ptr(k), ptr(v), _s())
+        wsp, wsn = _gemm_ws(B * S, 3 * n_heads * hd, n_heads * hd, x.device)
+        call("rte_qkv_rope_fwd", ptr(xb), ptr(wb), ptr(cs), ptr(sn), B, S, n_heads, hd, ptr(q), ptr(k), ptr(v), wsp,
+             wsn, _s())
         hs = None if head_scale is None else head_scale.reshape(B * n_heads).to(F32).contiguous()
         out = torch.empty((B, S, n_heads, hd), dtype=BF16, device=x.device)
         lse = torch.empty((B, n_heads, S), dtype=F32, device=x.device)

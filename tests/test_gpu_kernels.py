@@ -427,8 +427,10 @@ def test_rmsnorm_fwd_bwd(T, d):
     assert_rel(_np(tw.grad), dw, 1e-5, "rmsnorm dw")
 
 
-@pytest.mark.parametrize("B,S,H_,hd", [(2, 16, 2, 64), (128, 64, 8, 64)])
+@pytest.mark.parametrize("B,S,H_,hd", [(2, 16, 2, 64), (128, 64, 8, 64), (1, 64, 8, 64), (3, 40, 4, 64)])
 def test_qkv_rope_fwd_bwd(B, S, H_, hd):
+    """QKV + RoPE forward / backward against the oracle; (1, 64, 8, 64) and (3, 40, 4, 64) have
+    few output tiles and run the split-K path whose reduce applies RoPE."""
     H = _ops()
     d = H_ * hd
     rng = np.random.default_rng(B + S)
