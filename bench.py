@@ -304,21 +304,25 @@ def roofline_rows(B: int, S: int) -> list[dict]:
 
 def _pmc_per_call(csv_dir: Path, counter: str, calls: int, only=None):
     """Sum of `counter` over the profiled calls' dispatches / calls, in bytes (KiB counters), read
-    from rocprofv3's counter_collection.csv; `only` filters kernel names."""
+    from rocprofv3's counter_collection.csv; `only` filters kernel names, and kernels dispatched
+    fewer than `calls` times (the candidates' set-up work) are left out."""
     import csv
+    from collections import defaultdict
 
     files = sorted(csv_dir.rglob("*counter_collection.csv"))
     if not files:
         return None
-    tot = 0.0
+    tot, n = defaultdict(float), defaultdict(int)
     with open(files[0]) as fh:
         for r in csv.DictReader(fh):
             if r.get("Counter_Name") != counter:
                 continue
-            if only is not None and not only(r.get("Kernel_Name", "")):
+            k = r.get("Kernel_Name", "")
+            if only is not None and not only(k):
                 continue
-            tot += float(r["Counter_Value"])
-    return tot * 1024.0 / calls
+            tot[k] += float(r["Counter_Value"])
+            n[k] += 1
+    return sum(v for k, v in tot.items() if n[k] >= calls) * 1024.0 / calls
 
 
 COPY_ELEMS = 64 << 20  # calibration: rte_cast_f32_bf16 over 64 Mi elements (reads 256 MiB, writes 128 MiB)
@@ -386,6 +390,112 @@ def profile_kernel(name: str, iters: int, B: int, S: int, with_copy: bool = Fals
     return 0
 
 
+def _kernel_family(name: str) -> str:
+    base = name[5:] if name.startswith("void ") else name
+    if base.startswith("rte::"):
+        return "rte (HIP, this library)"
+    if "Cijk_" in base:
+        return "hipBLASLt / rocBLAS"
+    if base.startswith("at::"):
+        return "torch"
+    return "other"
+
+
+def _short_kernel(name: str, width: int = 110) -> str:
+    base = name[5:] if name.startswith("void ") else name
+    base = base.replace("(anonymous namespace)::", "")
+    if base.startswith("rte::"):
+        base = base.split("(", 1)[0]
+    return base if len(base) <= width else base[: width - 3] + "..."
+
+
+def trace_summary(csv_path: str, steps: int, top: int = 40) -> str:
+    """Markdown report of a rocprofv3 --kernel-trace CSV of a bench.py run whose last dispatches
+    are `steps` identical step replays: the dispatches of one step (found as the shortest period
+    that repeats `steps` times at the end of the trace), their time by kernel family and the
+    kernels that take the most time per step."""
+    import csv
+    from collections import defaultdict
+
+    with open(csv_path) as fh:
+        rows = [(int(r["Dispatch_Id"]), int(r["Start_Timestamp"]), int(r["End_Timestamp"]), r["Kernel_Name"])
+                for r in csv.DictReader(fh)]
+    rows.sort()  # dispatch order: fixed within a graph replay, whatever order parallel branches run in
+    names = [r[3] for r in rows]
+    n = len(names)
+    period = None
+    for p in range(1, n // max(steps, 1) + 1):
+        tail = names[n - p * steps:]
+        if all(tail[i] == tail[i % p] for i in range(len(tail))):
+            period = p
+            break
+    if period is None:
+        raise ValueError(f"no period repeating {steps} times at the end of {csv_path}")
+    step_rows = rows[n - period * steps:]
+    fam_us, fam_n, k_us, k_n = defaultdict(float), defaultdict(int), defaultdict(float), defaultdict(int)
+    for _, s, e, k in step_rows:
+        us = (e - s) / 1e3 / steps
+        fam_us[_kernel_family(k)] += us
+        fam_n[_kernel_family(k)] += 1
+        k_us[k] += us
+        k_n[k] += 1
+    busy = sum(fam_us.values())
+    wall = (max(r[2] for r in step_rows) - min(r[1] for r in step_rows)) / 1e3 / steps
+    out = [f"Dispatches per step: {period}; kernel time per step {busy:.1f} us (sum of kernel durations, mean "
+           f"over the last {steps} replays; first-start to last-end span under the tracer {wall:.1f} us per step).",
+           "",
+           "| family | dispatches / step | us / step | % of kernel time |", "|---|---:|---:|---:|"]
+    for f in sorted(fam_us, key=lambda f: -fam_us[f]):
+        out.append(f"| {f} | {fam_n[f] // steps} | {fam_us[f]:.1f} | {100 * fam_us[f] / busy:.1f} |")
+    out += ["", f"Top {top} kernels by time per step:", "",
+            "| us / step | dispatches / step | avg us | kernel |", "|---:|---:|---:|---|"]
+    for k in sorted(k_us, key=lambda k: -k_us[k])[:top]:
+        c = k_n[k] // steps
+        out.append(f"| {k_us[k]:.1f} | {c} | {k_us[k] / max(c, 1):.1f} | `{_short_kernel(k)}` |")
+    return "\n".join(out)
+
+
+def pmc_summary(csv_dir: str, calls: int) -> str:
+    """Markdown table of every counter in a rocprofv3 --pmc run's counter_collection.csv, summed
+    per kernel over its dispatches and divided by `calls` (the --iters of a --profile-kernel run)."""
+    import csv
+    from collections import defaultdict
+
+    files = sorted(Path(csv_dir).rglob("*counter_collection.csv"))
+    if not files:
+        raise FileNotFoundError(f"no counter_collection.csv under {csv_dir}")
+    tot, disp = defaultdict(float), defaultdict(set)
+    for f in files:
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                key = (r["Kernel_Name"], r["Counter_Name"])
+                tot[key] += float(r["Counter_Value"])
+                disp[r["Kernel_Name"]].add((str(f), r.get("Dispatch_Id", r.get("Correlation_Id", ""))))
+    out = [f"Per call (raw counters: sums over a kernel's dispatches / {calls} calls; derived ratios: mean per "
+           "dispatch; kernels dispatched less than once per call, i.e. set-up work, are left out):", "",
+           "| kernel | dispatches / call | counter | value / call |", "|---|---:|---|---:|"]
+    for (k, c) in sorted(tot):
+        if len(disp[k]) < calls:
+            continue
+        # raw counters (upper case) add up over a call's dispatches; derived ratios (MfmaUtil, ...)
+        # are averaged over the dispatches
+        v = tot[(k, c)] / calls if c.upper() == c else tot[(k, c)] / len(disp[k])
+        out.append(f"| `{_short_kernel(k, 80)}` | {len(disp[k]) / calls:g} | {c} | {v:.6g} |")
+    for c, per_elem in (("FETCH_SIZE", 4.0), ("WRITE_SIZE", 2.0)):
+        keys = [k for (k, cc) in tot if cc == c and len(disp[k]) >= calls]
+        if not keys:
+            continue
+        op = sum(tot[(k, c)] for k in keys if "cast_f32_bf16" not in k) * 1024.0 / calls
+        cp = sum(tot[(k, c)] for k in keys if "cast_f32_bf16" in k) * 1024.0 / calls
+        line = f"{c}: operation kernels {op:.4g} B per call (counter KiB x 1024)"
+        if cp:
+            scale = COPY_ELEMS * per_elem / cp
+            line += (f"; calibration copy counted {cp:.4g} B for a known {COPY_ELEMS * per_elem:.4g} B -> scale "
+                     f"{scale:.4f}; operation {op * scale:.4g} B per call")
+        out += ["", line]
+    return "\n".join(out)
+
+
 def _cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -449,7 +559,19 @@ def main(argv=None) -> int:
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 --pmc traffic runs")
     ap.add_argument("--eager", action="store_true",
                     help="launch every kernel from Python instead of replaying the captured step graph")
+    ap.add_argument("--trace-summary", default=None, metavar="CSV",
+                    help="print the per-step breakdown of a rocprofv3 kernel-trace CSV of a bench.py run whose "
+                         "last --steps dispatch groups are the timed steps, then exit (no GPU)")
+    ap.add_argument("--pmc-summary", default=None, metavar="DIR",
+                    help="print the counters of a rocprofv3 --pmc run of --profile-kernel per call (--iters "
+                         "calls), then exit (no GPU)")
     args = ap.parse_args(argv)
+    if args.trace_summary:
+        print(trace_summary(args.trace_summary, args.steps))
+        return 0
+    if args.pmc_summary:
+        print(pmc_summary(args.pmc_summary, args.iters))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this build measures one GPU only; run bench.py with --gpus 1"}))
         return 2

@@ -417,6 +417,10 @@ class TrainEngine:
             st["graph"].replay()
             out = st["out"]
         self.global_micro_step += 1
+        # Counted on the host without reading the device: a replay whose update was skipped (a
+        # non-finite gradient, metrics["stepped"] False) still advances global_step, unlike the
+        # eager path, which knows the outcome before counting.  Reading it here would put a
+        # device synchronisation into every captured step.
         self.global_step += 1
         self.tokens_seen += tokens.numel()
         flat = out["flat"].clone()

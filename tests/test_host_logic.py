@@ -221,6 +221,45 @@ def test_bench_refuses_more_than_one_gpu():
     assert "one GPU" in r.stdout
 
 
+def test_bench_trace_and_pmc_summaries(tmp_path):
+    """The profile summarizers: one step is the shortest dispatch period repeating --steps times
+    at the end of the trace; counters are summed per kernel and divided by the call count."""
+    import bench
+
+    hdr = "Dispatch_Id,Kernel_Name,Start_Timestamp,End_Timestamp\n"
+    lines, did, t = [], 0, 0
+    for name in ["void at::native::setup", "rte::warm(int)"]:  # warm-up dispatches before the steps
+        did += 1
+        lines.append(f'{did},"{name}",{t},{t + 500}\n')
+        t += 1000
+    step = [("rte::gemm_kernel<1>(int)", 3000), ("rte::gemm_kernel<1>(int)", 1000),
+            ("void at::native::vectorized_elementwise_kernel<add>(int)", 500), ("Cijk_Alik_Bljk", 1500)]
+    for _ in range(3):
+        for name, dur in step:
+            did += 1
+            lines.append(f'{did},"{name}",{t},{t + dur}\n')
+            t += dur + 100
+    f = tmp_path / "k_kernel_trace.csv"
+    f.write_text(hdr + "".join(lines))
+    rep = bench.trace_summary(str(f), steps=3)
+    assert "Dispatches per step: 4;" in rep
+    assert "kernel time per step 6.0 us" in rep
+    assert "| rte (HIP, this library) | 2 | 4.0 | 66.7 |" in rep
+    assert "| torch | 1 | 0.5 | 8.3 |" in rep
+    assert "| hipBLASLt / rocBLAS | 1 | 1.5 | 25.0 |" in rep
+    assert "| 4.0 | 2 | 2.0 | `rte::gemm_kernel<1>` |" in rep
+
+    d = tmp_path / "pmc" / "run"
+    d.mkdir(parents=True)
+    (d / "p_counter_collection.csv").write_text(
+        "Dispatch_Id,Kernel_Name,Counter_Name,Counter_Value\n"
+        '1,"rte::k(int)",FETCH_SIZE,10\n2,"rte::k(int)",FETCH_SIZE,30\n'
+        '1,"rte::k(int)",WRITE_SIZE,4\n2,"rte::k(int)",WRITE_SIZE,6\n')
+    rep = bench.pmc_summary(str(tmp_path / "pmc"), calls=2)
+    assert "| `rte::k` | 1 | FETCH_SIZE | 20 |" in rep
+    assert "| `rte::k` | 1 | WRITE_SIZE | 5 |" in rep
+
+
 def test_bf16_prefetch_tables():
     """The one-launch weight-cast plan: contiguous views cast flat, 2-D transposed views by
     tiles, other strides left to the per-use cast; repeated views share one job and buffer."""
