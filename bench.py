@@ -256,6 +256,56 @@ def kernel_candidates(B: int, S: int):
     ]
 
 
+def svd_cfg4_candidate(T: int = 32768):
+    """the SVD low-rank FFN forward + backward (d 1024, F 4096, rank 128
+    factors U diag(S) V^T for up / gate / down, S log-uniform in [1e-2, 1], U and V orthonormal from
+    a seeded QR) over T tokens, as one autograd call of hip_ops.svd_ffn plus its backward."""
+    import torch
+
+    from rte_amd.kernels import hip_ops
+
+    dev = "cuda"
+    d, F, r = 1024, 4096, 128
+    g = torch.Generator()
+    g.manual_seed(3)
+
+    def orth(a, b):
+        return torch.linalg.qr(torch.randn(a, b, generator=g))[0]
+
+    def svals():
+        return 10.0 ** (torch.rand(r, generator=g) * 2.0 - 2.0)
+
+    us_ug = torch.cat([orth(d, r) * svals(), orth(d, r) * svals()], 1).to(dev).requires_grad_()
+    v_ug = torch.cat([orth(F, r), orth(F, r)], 0).to(dev).requires_grad_()
+    v_dn = orth(F, r).to(dev).requires_grad_()
+    us_dn = (orth(d, r) * svals()).to(dev).requires_grad_()
+    x = torch.randn(T, d, generator=g).to(dev).to(torch.bfloat16).requires_grad_()
+    dy = torch.randn(T, d, generator=g).to(dev)
+    params = [x, us_ug, v_ug, v_dn, us_dn]
+
+    def fn():
+        y = hip_ops.svd_ffn(x, us_ug, v_ug, v_dn, us_dn)
+        torch.autograd.grad(y, params, dy)
+
+    # fwd 2T(d 2r + 2F r + F r + r d) FLOP, backward twice that; bytes: x, dy, dx (bf16), y (fp32),
+    # the four factors read (fp32) and their gradients written (fp32)
+    fwd = 2.0 * T * (d * 2 * r + 2 * F * r + F * r + r * d)
+    wbytes = 4.0 * (d * 2 * r + 2 * F * r + F * r + d * r)
+    return dict(name="svd_ffn_cfg4_fwd_bwd", per_step=0, kernels=None, flop=3.0 * fwd,
+                bytes=2.0 * T * d * 3 + 4.0 * T * d + 2.0 * wbytes, fn=fn, T=T, d=d, F=F, r=r)
+
+
+def svd_cfg4_row(iters: int = 5) -> dict:
+    """Roofline line of the cfg4 SVD FFN forward + backward (not part of the cfg3 step)."""
+    c = svd_cfg4_candidate()
+    dt = time_launches(c["fn"], iters)
+    tf = c["flop"] / dt / 1e12
+    return {"workload": "SVD low-rank FFN fwd+bwd (BASELINE configs[3]): T 32768, d 1024, F 4096, rank 128",
+            "avg_us": round(dt * 1e6, 1), "bound": "mfma", "achieved": round(tf, 1), "unit": "TFLOP/s",
+            "peak": PEAK_BF16_TFLOPS, "frac": round(tf / PEAK_BF16_TFLOPS, 4), "flop": c["flop"],
+            "algorithmic_bytes": c["bytes"], "tokens_per_s": round(c["T"] / dt, 1)}
+
+
 def time_launches(fn, iters: int = 20) -> float:
     """Average duration (s) of one fn() call: `iters` calls captured in a HIP graph and
     replayed, timed with HIP events on the replaying stream (no host launch gaps)."""
@@ -375,7 +425,8 @@ def profile_kernel(name: str, iters: int, B: int, S: int, with_copy: bool = Fals
     from rte_amd import _lib
 
     if name != "copy":
-        cands = {c["name"]: c for c in kernel_candidates(B, S)}
+        cands = {c["name"]: c for c in
+                 ([svd_cfg4_candidate()] if name == "svd_ffn_cfg4_fwd_bwd" else kernel_candidates(B, S))}
         torch.cuda.synchronize()
         for _ in range(iters):
             cands[name]["fn"]()
@@ -651,6 +702,7 @@ def main(argv=None) -> int:
             "algorithmic_bytes_per_launch": dom["bytes"],
         }
         out["kernels"] = rows
+        out["svd_ffn_cfg4"] = svd_cfg4_row()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

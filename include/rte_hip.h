@@ -217,6 +217,22 @@ int rte_svd_ffn_bwd(const void* dy, const void* x, int T, int d, int F, int r, c
                     const void* z, const void* b, void* db, void* dug, void* da_ug, void* dx, float* dus_ug,
                     float* dv_ug, float* dv_dn, float* dus_dn, void* workspace, size_t workspace_bytes,
                     void* stream);
+/* The same FFN with the wide activations kept on chip (the fused "x A -> B -> SwiGLU -> V_d ->
+ * U_d^T" path; same factor layouts, results within bf16 rounding of rte_svd_ffn_fwd / _bwd):
+ * the [T, 2F] up / gate pre-activations and the [T, F] SwiGLU output are never written; the
+ * backward recomputes them per (token, neuron) block.  fwd writes a_ug [T, 2r], b [T, r] (bf16)
+ * and y; bwd writes db [T, r], da_ug [T, 2r] (bf16 scratch), dx and the four fp32 weight
+ * gradients (overwritten).  r in {64, 128}, F % 128 == 0, d % 8 == 0, T % 8 == 0; both calls take
+ * rte_svd_ffn_fused_workspace_bytes(T, d, F, r) bytes of workspace.  Sums over neuron / token
+ * ranges are fp32 partials added in a fixed order: bitwise repeatable. */
+size_t rte_svd_ffn_fused_workspace_bytes(int T, int d, int F, int r);
+int rte_svd_ffn_fused_fwd(const void* x, int T, int d, int F, int r, const void* us_ug, const void* v_ug,
+                          const void* v_dn, const void* us_dn, const float* resid, void* a_ug, void* b, void* y,
+                          int y_f32, void* workspace, size_t workspace_bytes, void* stream);
+int rte_svd_ffn_fused_bwd(const void* dy, const void* x, int T, int d, int F, int r, const void* us_ug,
+                          const void* v_ug, const void* v_dn, const void* us_dn, const void* a_ug, const void* b,
+                          void* db, void* da_ug, void* dx, float* dus_ug, float* dv_ug, float* dv_dn,
+                          float* dus_dn, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- SVD-factor sparse SwiGLU FFN, per-token candidates (SVDFactorSparseFFN, rte/layers.py:342-643,
  *      modes mask / slots; the device driver rte/kernels/svd_sparse_ffn_triton.py:480-714) ----

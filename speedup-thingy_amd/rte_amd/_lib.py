@@ -59,6 +59,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
     ),
+    "rte_svd_ffn_fused_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "rte_svd_ffn_fused_fwd": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _SZ, _P]),
+    "rte_svd_ffn_fused_bwd": (
+        _I,
+        [_P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+    ),
     "rte_svd_sparse_fwd": (_I, [_P, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P,
                                 _I, _P, _P, _P, _P, _P]),
     "rte_svd_sparse_bwd": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),

@@ -1744,12 +1744,19 @@ def shortlist_ce(hidden, w, shortlist):
 
 # ----------------------------------------------------------------------------- SVD low-rank SwiGLU FFN
 
+def svd_ffn_fused_supported(T: int, d: int, F: int, r: int) -> bool:
+    """Shapes the on-chip SVD FFN path takes (rte_svd_ffn_fused_*); others use the four-GEMM path."""
+    return r in (64, 128) and F % 128 == 0 and d % 8 == 0 and T % 8 == 0
+
+
 class SVDFFNFn(torch.autograd.Function):
     """y = resid + SwiGLU FFN whose up / gate / down weights are rank-r factors.
 
     us_ug [d, 2r] = [U_up S_up | U_gate S_gate], v_ug [2F, r] = [V_up ; V_gate],
-    v_dn [F, r], us_dn [d, r] = U_dn S_dn.  Four MFMA GEMMs forward (the expand GEMM
-    fuses SwiGLU and reads each half's low-rank code), eleven backward."""
+    v_dn [F, r], us_dn [d, r] = U_dn S_dn.  For rank 64 / 128 the [T, 2F] activations and the
+    [T, F] SwiGLU output stay on chip (rte_svd_ffn_fused_*: the backward recomputes them);
+    otherwise four MFMA GEMMs forward (the expand GEMM fuses SwiGLU and reads each half's
+    low-rank code), eleven backward."""
 
     @staticmethod
     def forward(ctx, x, us_ug, v_ug, v_dn, us_dn, resid):
@@ -1762,34 +1769,47 @@ class SVDFFNFn(torch.autograd.Function):
         F = v_dn.shape[0]
         w = [cast_bf16(t) for t in (us_ug, v_ug, v_dn, us_dn)]
         dev = x.device
+        fused = svd_ffn_fused_supported(T, d, F, r)
         a_ug = torch.empty((T, 2 * r), dtype=BF16, device=dev)
-        ug = torch.empty((T, 2 * F), dtype=BF16, device=dev)
-        z = torch.empty((T, F), dtype=BF16, device=dev)
         b = torch.empty((T, r), dtype=BF16, device=dev)
         y = torch.empty((T, d), dtype=F32, device=dev)
         rs = None if resid is None else resid.reshape(T, d).contiguous().to(F32)
-        call("rte_svd_ffn_fwd", ptr(xb), T, d, F, r, *[ptr(t) for t in w], ptr(rs), ptr(a_ug), ptr(ug), ptr(z),
-             ptr(b), ptr(y), 1, _s())
-        ctx.save_for_backward(xb, *w, a_ug, ug, z, b)
-        ctx.meta = (shape, r, F, resid is not None, [t.dtype for t in (us_ug, v_ug, v_dn, us_dn)])
+        if fused:
+            wsp, wsn = workspace(_lib.load().rte_svd_ffn_fused_workspace_bytes(T, d, F, r), dev)
+            call("rte_svd_ffn_fused_fwd", ptr(xb), T, d, F, r, *[ptr(t) for t in w], ptr(rs), ptr(a_ug), ptr(b),
+                 ptr(y), 1, wsp, wsn, _s())
+            ctx.save_for_backward(xb, *w, a_ug, b)
+        else:
+            ug = torch.empty((T, 2 * F), dtype=BF16, device=dev)
+            z = torch.empty((T, F), dtype=BF16, device=dev)
+            call("rte_svd_ffn_fwd", ptr(xb), T, d, F, r, *[ptr(t) for t in w], ptr(rs), ptr(a_ug), ptr(ug),
+                 ptr(z), ptr(b), ptr(y), 1, _s())
+            ctx.save_for_backward(xb, *w, a_ug, b, ug, z)
+        ctx.meta = (shape, r, F, fused, resid is not None, [t.dtype for t in (us_ug, v_ug, v_dn, us_dn)])
         return y.view(shape)
 
     @staticmethod
     def backward(ctx, dy):
-        xb, us_ug, v_ug, v_dn, us_dn, a_ug, ug, z, b = ctx.saved_tensors
-        shape, r, F, has_resid, dts = ctx.meta
+        xb, us_ug, v_ug, v_dn, us_dn, a_ug, b, *wide = ctx.saved_tensors
+        shape, r, F, fused, has_resid, dts = ctx.meta
         T, d = xb.shape
         dev = xb.device
         dyb = cast_bf16(dy.reshape(T, d))
         db = torch.empty((T, r), dtype=BF16, device=dev)
-        dug = torch.empty((T, 2 * F), dtype=BF16, device=dev)
         da = torch.empty((T, 2 * r), dtype=BF16, device=dev)
         dx = torch.empty((T, d), dtype=BF16, device=dev)
         g = [torch.empty(t.shape, dtype=F32, device=dev) for t in (us_ug, v_ug, v_dn, us_dn)]
-        wsp, wsn = _gemm_ws(max(d, F), 2 * r, T, dev)
-        call("rte_svd_ffn_bwd", ptr(dyb), ptr(xb), T, d, F, r, ptr(us_ug), ptr(v_ug), ptr(v_dn), ptr(us_dn),
-             ptr(a_ug), ptr(ug), ptr(z), ptr(b), ptr(db), ptr(dug), ptr(da), ptr(dx), *[ptr(t) for t in g],
-             wsp, wsn, _s())
+        if fused:
+            wsp, wsn = workspace(_lib.load().rte_svd_ffn_fused_workspace_bytes(T, d, F, r), dev)
+            call("rte_svd_ffn_fused_bwd", ptr(dyb), ptr(xb), T, d, F, r, ptr(us_ug), ptr(v_ug), ptr(v_dn),
+                 ptr(us_dn), ptr(a_ug), ptr(b), ptr(db), ptr(da), ptr(dx), *[ptr(t) for t in g], wsp, wsn, _s())
+        else:
+            ug, z = wide
+            dug = torch.empty((T, 2 * F), dtype=BF16, device=dev)
+            wsp, wsn = _gemm_ws(max(d, F), 2 * r, T, dev)
+            call("rte_svd_ffn_bwd", ptr(dyb), ptr(xb), T, d, F, r, ptr(us_ug), ptr(v_ug), ptr(v_dn), ptr(us_dn),
+                 ptr(a_ug), ptr(ug), ptr(z), ptr(b), ptr(db), ptr(dug), ptr(da), ptr(dx), *[ptr(t) for t in g],
+                 wsp, wsn, _s())
         return (dx.view(shape), *[t.to(dt) for t, dt in zip(g, dts)], dy if has_resid else None)
 
 

@@ -478,8 +478,11 @@ def test_attn_out_proj_strided_input():
 
 # ---------------------------------------------------------------- SVD low-rank FFN
 
-@pytest.mark.parametrize("T,d,F,r", [(256, 128, 256, 32), (4096, 1024, 4096, 128)])
+@pytest.mark.parametrize("T,d,F,r", [(256, 128, 256, 32), (4096, 1024, 4096, 128), (1000, 256, 512, 64),
+                                     (200, 128, 384, 128), (8, 64, 128, 64)])
 def test_svd_ffn_fwd_bwd(T, d, F, r):
+    """SVD FFN forward and backward against the oracle: rank 32 on the four-GEMM path, ranks 64 /
+    128 on the on-chip path (token counts that fill no whole 128-token tile, one neuron tile)."""
     from oracle import svd_ffn as SV
 
     H = _ops()
@@ -508,6 +511,67 @@ def test_svd_ffn_fwd_bwd(T, d, F, r):
     assert_rel(_np(tx.grad), g["dx"], BF16_RTOL, "svd dx")
     for k in m:
         assert_rel(_np(tw[k].grad), g["d" + k], BF16_RTOL, f"svd d{k}")
+
+
+@pytest.mark.parametrize("T,d,F,r", [(2048, 512, 1024, 128), (1016, 256, 512, 64)])
+def test_svd_ffn_fused_matches_unfused_and_repeats(T, d, F, r):
+    """rte_svd_ffn_fused_* against rte_svd_ffn_* through the C-ABI on the same inputs (bf16
+    rounding apart: the unfused path rounds the activations to bf16 in HBM), and the fused call
+    twice bitwise."""
+    from rte_amd import _lib
+
+    lib = _lib.load()
+    g = torch.Generator(device=DEV)
+    g.manual_seed(T + r)
+    bf = torch.bfloat16
+
+    def rnd(*shape, scale=1.0):
+        return (torch.randn(*shape, device=DEV, generator=g) * scale).to(bf)
+
+    x, dy = rnd(T, d), rnd(T, d)
+    us_ug, v_ug = rnd(d, 2 * r, scale=d ** -0.5), rnd(2 * F, r, scale=r ** -0.5)
+    v_dn, us_dn = rnd(F, r, scale=F ** -0.5), rnd(d, r, scale=r ** -0.5)
+    st = _lib.stream_ptr()
+    print(f"svd fused vs unfused T={T} d={d} F={F} r={r}", flush=True)
+
+    def unfused():
+        a, b = torch.empty(T, 2 * r, device=DEV, dtype=bf), torch.empty(T, r, device=DEV, dtype=bf)
+        ug, z = torch.empty(T, 2 * F, device=DEV, dtype=bf), torch.empty(T, F, device=DEV, dtype=bf)
+        y = torch.empty(T, d, device=DEV)
+        _lib.call("rte_svd_ffn_fwd", x.data_ptr(), T, d, F, r, us_ug.data_ptr(), v_ug.data_ptr(), v_dn.data_ptr(),
+                  us_dn.data_ptr(), None, a.data_ptr(), ug.data_ptr(), z.data_ptr(), b.data_ptr(), y.data_ptr(), 1, st)
+        db, da = torch.empty(T, r, device=DEV, dtype=bf), torch.empty(T, 2 * r, device=DEV, dtype=bf)
+        dug, dx = torch.empty(T, 2 * F, device=DEV, dtype=bf), torch.empty(T, d, device=DEV, dtype=bf)
+        gr = [torch.empty(s, device=DEV) for s in ((d, 2 * r), (2 * F, r), (F, r), (d, r))]
+        nb = lib.rte_gemm_workspace_bytes(max(d, F), 2 * r, T)
+        ws = torch.empty(max(nb, 16), device=DEV, dtype=torch.uint8)
+        _lib.call("rte_svd_ffn_bwd", dy.data_ptr(), x.data_ptr(), T, d, F, r, us_ug.data_ptr(), v_ug.data_ptr(),
+                  v_dn.data_ptr(), us_dn.data_ptr(), a.data_ptr(), ug.data_ptr(), z.data_ptr(), b.data_ptr(),
+                  db.data_ptr(), dug.data_ptr(), da.data_ptr(), dx.data_ptr(), *[t.data_ptr() for t in gr],
+                  ws.data_ptr(), nb, st)
+        return [y, dx, *gr]
+
+    def fused():
+        a, b = torch.empty(T, 2 * r, device=DEV, dtype=bf), torch.empty(T, r, device=DEV, dtype=bf)
+        y = torch.empty(T, d, device=DEV)
+        nb = lib.rte_svd_ffn_fused_workspace_bytes(T, d, F, r)
+        ws = torch.empty(nb, device=DEV, dtype=torch.uint8)
+        _lib.call("rte_svd_ffn_fused_fwd", x.data_ptr(), T, d, F, r, us_ug.data_ptr(), v_ug.data_ptr(),
+                  v_dn.data_ptr(), us_dn.data_ptr(), None, a.data_ptr(), b.data_ptr(), y.data_ptr(), 1,
+                  ws.data_ptr(), nb, st)
+        db, da = torch.empty(T, r, device=DEV, dtype=bf), torch.empty(T, 2 * r, device=DEV, dtype=bf)
+        dx = torch.empty(T, d, device=DEV, dtype=bf)
+        gr = [torch.empty(s, device=DEV) for s in ((d, 2 * r), (2 * F, r), (F, r), (d, r))]
+        _lib.call("rte_svd_ffn_fused_bwd", dy.data_ptr(), x.data_ptr(), T, d, F, r, us_ug.data_ptr(),
+                  v_ug.data_ptr(), v_dn.data_ptr(), us_dn.data_ptr(), a.data_ptr(), b.data_ptr(), db.data_ptr(),
+                  da.data_ptr(), dx.data_ptr(), *[t.data_ptr() for t in gr], ws.data_ptr(), nb, st)
+        return [y, dx, *gr]
+
+    ref, got, again = unfused(), fused(), fused()
+    torch.cuda.synchronize()
+    for name, a, b, c in zip(["y", "dx", "dus_ug", "dv_ug", "dv_dn", "dus_dn"], ref, got, again):
+        assert_rel(_np(b), _np(a).astype(np.float64), BF16_RTOL, f"fused {name}")
+        assert torch.equal(b, c), f"fused {name} not bitwise repeatable"
 
 
 # ---------------------------------------------------------------- LM head + cross-entropy
