@@ -847,6 +847,117 @@ __global__ void __launch_bounds__(1024) mf_pack_kernel(const int64_t* __restrict
   }
 }
 
+// The same lists for up to 256 keys and 4096 samples without per-key scans over all samples:
+// each thread holds one sample's key, each wave ranks its 64 samples per key with one ballot per
+// key, and a per-key prefix over the waves (in wave order) places them, so a key's samples keep
+// ascending sample order (the lists are identical to mf_pack_kernel's).
+constexpr int kPackFastKeys = 256, kPackFastSamples = 4096;
+
+__global__ void __launch_bounds__(1024) mf_pack_fast_kernel(const int64_t* __restrict__ key, int B0, int Bh0, int B1,
+                                                            int Bh1, int S, int G, int32_t* __restrict__ offsets,
+                                                            int32_t* __restrict__ tok, int32_t* __restrict__ pos,
+                                                            int32_t* __restrict__ soff, int32_t* __restrict__ slist,
+                                                            int32_t* __restrict__ psrc) {
+  __shared__ int cw[16][kPackFastKeys];  // per wave, per key: counts, then slot bases
+  __shared__ int run[kPackFastKeys];     // per key: totals, then the running slot base
+  __shared__ int sl[kPackFastSamples];   // listed sample of each slot
+  __shared__ int sp[kPackFastSamples];   // its source row block
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, Bt = B0 + B1;
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  for (int g = tid; g < G; g += 1024) run[g] = 0;
+  __syncthreads();
+  for (int j0 = 0; j0 < Bt; j0 += 1024) {
+    const int j = j0 + tid;
+    const int k = j < Bt ? (int)clamp_key(key[j], G) : -1;
+    for (int g = 0; g < G; ++g) {
+      const unsigned long long m = __ballot(k == g);
+      if (lane == 0 && m != 0ull) atomicAdd(&run[g], __popcll(m));  // integer totals: order-free
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {  // exclusive scan of the per-key totals: lane l owns keys [4 l, 4 l + 4)
+    int v[4], sum = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int g = 4 * lane + q;
+      v[q] = g < G ? run[g] : 0;
+      sum += v[q];
+    }
+    int inc = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += y;
+    }
+    int s = inc - sum;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int g = 4 * lane + q;
+      if (g < G) {
+        soff[g] = s;
+        offsets[g] = s * S;
+        run[g] = s;
+      }
+      s += v[q];
+    }
+    if (lane == 63) {
+      soff[G] = s;
+      offsets[G] = s * S;
+    }
+  }
+  __syncthreads();
+  for (int j0 = 0; j0 < Bt; j0 += 1024) {
+    const int j = j0 + tid;
+    const int k = j < Bt ? (int)clamp_key(key[j], G) : -1;
+    int rank = 0;
+    for (int g = 0; g < G; ++g) {
+      const unsigned long long m = __ballot(k == g);
+      if (k == g) rank = __popcll(m & lt);
+      if (lane == 0) cw[wave][g] = __popcll(m);
+    }
+    __syncthreads();
+    for (int g = tid; g < G; g += 1024) {
+      int s = run[g];
+      for (int w = 0; w < 16; ++w) {
+        const int c = cw[w][g];
+        cw[w][g] = s;
+        s += c;
+      }
+      run[g] = s;
+    }
+    __syncthreads();
+    if (k >= 0) {
+      const int slot = cw[wave][k] + rank;
+      const int src = j < B0 ? j % Bh0 : Bh0 + (j - B0) % Bh1;
+      slist[slot] = j;
+      psrc[slot] = src;
+      sl[slot] = j;
+      sp[slot] = src;
+    }
+    __syncthreads();
+  }
+  // one wave per listed sample (S rows), four samples in flight per wave
+  for (int slot0 = wave; slot0 < Bt; slot0 += 64) {
+    int js[4], xs[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int slot = slot0 + 16 * u;
+      js[u] = slot < Bt ? sl[slot] : 0;
+      xs[u] = slot < Bt ? sp[slot] * S : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int slot = slot0 + 16 * u;
+      if (slot < Bt) {
+        for (int s = lane; s < S; s += 64) {
+          tok[slot * S + s] = xs[u] + s;
+          pos[slot * S + s] = js[u] * S + s;
+        }
+      }
+    }
+  }
+}
+
 // dV [G][3d][32] = [dVc[:, :d]; dV2; dVc[:, d:]]
 __global__ void __launch_bounds__(256) mf_vassemble_kernel(const float4* __restrict__ dVc, const float4* __restrict__ dV2,
                                                            int G, int d, float4* __restrict__ dV) {
@@ -1003,10 +1114,15 @@ int macro_fused_wgrad(const int64_t* key, int B0, int Bh0, int B1, int Bh1, int 
   float* dVc = reinterpret_cast<float*>(take((size_t)G * 2 * d * kRank * 4));
   float* dV2 = reinterpret_cast<float*>(take((size_t)G * d * kRank * 4));
   const size_t gk_bytes = ws_bytes - (size_t)(w - static_cast<char*>(ws));
-  const size_t lds = (size_t)(G + 2 * Bt) * sizeof(int);
-  RTE_REQUIRE(lds <= 64 * 1024, "macro_fused_wgrad: too many keys and samples for one pack workgroup");
-  hipLaunchKernelGGL(mf_pack_kernel, dim3(1), dim3(1024), lds, s, key, B0, Bh0, B1, Bh1 > 0 ? Bh1 : 1, S, G, offsets,
-                     tok, pos, soff, slist, psrc);
+  if (G <= kPackFastKeys && Bt <= kPackFastSamples) {
+    hipLaunchKernelGGL(mf_pack_fast_kernel, dim3(1), dim3(1024), 0, s, key, B0, Bh0, B1, Bh1 > 0 ? Bh1 : 1, S, G,
+                       offsets, tok, pos, soff, slist, psrc);
+  } else {
+    const size_t lds = (size_t)(G + 2 * Bt) * sizeof(int);
+    RTE_REQUIRE(lds <= 64 * 1024, "macro_fused_wgrad: too many keys and samples for one pack workgroup");
+    hipLaunchKernelGGL(mf_pack_kernel, dim3(1), dim3(1024), lds, s, key, B0, Bh0, B1, Bh1 > 0 ? Bh1 : 1, S, G,
+                       offsets, tok, pos, soff, slist, psrc);
+  }
   RTE_TRY(check_launch("macro_fused_pack"));
   if (dU)
     RTE_TRY(rte_grouped_linear_bwd(du, sa, P, kRank, offsets, G, P, pos, pos, nullptr, d, nullptr, 0, dU, w,
