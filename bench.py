@@ -182,6 +182,19 @@ def kernel_candidates(B: int, S: int):
     def topk():
         _lib.call("rte_route_topk", logits.data_ptr(), T, C, k, ids_out.data_ptr(), w_out.data_ptr(), st())
 
+    rp_ws_bytes = lib.rte_route_pack_workspace_bytes(T, C)
+    rp_ws = torch.empty(max(rp_ws_bytes, 16), device=dev, dtype=torch.uint8)
+    rp_ids = torch.empty(T, k, device=dev, dtype=torch.int32)
+    rp_w = torch.empty(T, k, device=dev, dtype=torch.float32)
+    rp_out = [torch.empty(P, device=dev, dtype=torch.int32) for _ in range(3)]
+    rp_off = torch.empty(C + 1, device=dev, dtype=torch.int32)
+    rp_wos = torch.empty(P, device=dev, dtype=torch.float32)
+
+    def route_pack():
+        _lib.call("rte_route_pack", x.data_ptr(), T, d, wr.data_ptr(), C, k, rp_ids.data_ptr(), rp_w.data_ptr(),
+                  rp_off.data_ptr(), rp_out[0].data_ptr(), rp_out[1].data_ptr(), rp_out[2].data_ptr(),
+                  rp_wos.data_ptr(), None, rp_ws.data_ptr(), rp_ws_bytes, st())
+
     pk_ws_bytes = lib.rte_pack_workspace_bytes(P, C)
     pk_ws = torch.empty(max(pk_ws_bytes, 16), device=dev, dtype=torch.uint8)
     pk_out = [torch.empty(P, device=dev, dtype=torch.int32) for _ in range(4)]
@@ -246,10 +259,17 @@ def kernel_candidates(B: int, S: int):
         # combine unit: T*k*d*b + T*k*4 + T*d*b (bf16 rows in, fp32 rows out here)
         dict(name="combine_rows", per_step=2, kernels=1, flop=1.0 * P * d,
              bytes=2.0 * P * d + 4.0 * T * d, fn=combine),
+        # router GEMM + top-k + pack (the step's routing): x and Wr in, ids + weights (8 B per pair)
+        # and the slot tables (4 int32 + 1 fp32 per pair) out; the per-block cluster counts (T / 32 x C
+        # int32) written and read once
+        dict(name="route_pack", per_step=1, kernels=2, flop=2.0 * T * C * d,
+             bytes=2.0 * T * d + 2.0 * C * d + 8.0 * P + 20.0 * P + 4.0 * (C + 1) + 8.0 * (T // 32) * C,
+             fn=route_pack),
+        # the standalone entry points (not in the cfg3 step, which routes through route_pack):
         # route unit: T*C*4 logits in, T*k*(4+4) ids + weights out
-        dict(name="route_topk", per_step=1, kernels=1, flop=0.0, bytes=4.0 * T * C + 8.0 * T * k, fn=topk),
+        dict(name="route_topk", per_step=0, kernels=1, flop=0.0, bytes=4.0 * T * C + 8.0 * T * k, fn=topk),
         # pack unit: P*(4+4) ids + weights in, 4*P*4 + P*4 slot tables out, (C+1)*4 offsets
-        dict(name="pack_index", per_step=1, kernels=3, flop=0.0, bytes=8.0 * P + 20.0 * P + 4.0 * (C + 1),
+        dict(name="pack_index", per_step=0, kernels=3, flop=0.0, bytes=8.0 * P + 20.0 * P + 4.0 * (C + 1),
              fn=pack),
         dict(name="macro_consistency_fwd_bwd", per_step=1, kernels=None, flop=macro_flop, bytes=macro_bytes,
              fn=macro_cons),

@@ -64,6 +64,20 @@ int rte_gemm_bf16_split(const void* a, const int64_t* a_layout, int a_t,
  * weights: softmax over the k selected logits.  C <= 1024, k <= 16. */
 int rte_route_topk(const float* logits, int T, int C, int k, int32_t* ids, float* weights, void* stream);
 
+/* ---- router GEMM, top-k and pack in two launches (replaces the router linear + top-k routing of
+ *      rte/kernels/cluster_pool_ffn.py:129-140 / rte/models.py:300-309 and the pack index build
+ *      :165-189 for the routed cluster pool) ----
+ * x bf16 [T, d], wr bf16 [C, d]: logits = x wr^T (fp32 accumulation; written to logits [T, C] fp32
+ * when it is not NULL), ids int32 [T, k] / weights fp32 [T, k] = route_topk of those logits (the
+ * same selection order and softmax, bitwise), and the pack outputs of rte_pack_index for cl = ids
+ * (offsets [C+1], tok_of_slot, pair_of_slot, slot_of_pair, w_of_slot [T*k], all written).
+ * C in {32, 64, 128}, 1 <= k <= min(16, C), d % 64 == 0; workspace
+ * rte_route_pack_workspace_bytes(T, C) bytes (per-block cluster counts). */
+size_t rte_route_pack_workspace_bytes(int T, int C);
+int rte_route_pack(const void* x, int T, int d, const void* wr, int C, int k, int32_t* ids, float* weights,
+                   int32_t* offsets, int32_t* tok_of_slot, int32_t* pair_of_slot, int32_t* slot_of_pair,
+                   float* w_of_slot, float* logits, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- deterministic pack index (replaces build_static_pack_gather_indices
  *      rte/kernels/cluster_pool_ffn.py:165-189 and _assign_slots_kernel :32-45) ----
  * cl[p] = cluster of pair p (p = t*k + j).  Stable counting sort by cluster:

@@ -17,6 +17,10 @@ int svd_sparse_bwd(const bf16* dout, const bf16* w_up, const bf16* w_gate, const
                    const float* sel_u, const float* sel_g, int T, int d, int top_k, bf16* dx, float* z, float* du,
                    float* dg, hipStream_t s);
 int route_topk(const float* logits, int T, int C, int k, int32_t* ids, float* weights, hipStream_t s);
+size_t route_pack_workspace_bytes(int T, int C);
+int route_pack(const bf16* x, int T, int d, const bf16* wr, int C, int k, int32_t* ids, float* weights,
+               int32_t* offsets, int32_t* tok_of_slot, int32_t* pair_of_slot, int32_t* slot_of_pair,
+               float* w_of_slot, float* logits, void* ws, size_t ws_bytes, hipStream_t s);
 size_t pack_workspace_bytes(int P, int C);
 int pack_pairs(const int32_t* cl, int P, int C, int k, const float* w, int32_t* offsets,
                int32_t* tok_of_slot, int32_t* pair_of_slot, int32_t* slot_of_pair, float* w_of_slot,
@@ -239,6 +243,15 @@ int rte_route_topk(const float* logits, int T, int C, int k, int32_t* ids, float
 }
 
 size_t rte_pack_workspace_bytes(int P, int C) { return pack_workspace_bytes(P, C); }
+
+size_t rte_route_pack_workspace_bytes(int T, int C) { return route_pack_workspace_bytes(T, C); }
+
+int rte_route_pack(const void* x, int T, int d, const void* wr, int C, int k, int32_t* ids, float* weights,
+                   int32_t* offsets, int32_t* tok_of_slot, int32_t* pair_of_slot, int32_t* slot_of_pair,
+                   float* w_of_slot, float* logits, void* workspace, size_t workspace_bytes, void* stream) {
+  return route_pack(B16(x), T, d, B16(wr), C, k, ids, weights, offsets, tok_of_slot, pair_of_slot, slot_of_pair,
+                    w_of_slot, logits, workspace, workspace_bytes, S(stream));
+}
 
 int rte_pack_index(const int32_t* cl, int P, int C, int k, const float* w, int32_t* offsets,
                    int32_t* tok_of_slot, int32_t* pair_of_slot, int32_t* slot_of_pair, float* w_of_slot,

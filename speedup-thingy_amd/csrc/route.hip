@@ -323,6 +323,33 @@ __device__ __forceinline__ void insert_row(const float* rowl, int C, float (&tv)
   }
 }
 
+// softmax over the k selected logits (sorted, tv[0] the largest) summed with the xor tree the
+// wave-per-token kernel's butterfly forms, then the k ids and weights stored
+template <int K>
+__device__ __forceinline__ void topk_softmax_store(const float (&tv)[K], const int (&ti)[K], int k, int32_t* ids,
+                                                   float* weights) {
+  float ex[K], sm[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    ex[j] = j < k ? expf(tv[j] - tv[0]) : 0.0f;
+    sm[j] = ex[j];
+  }
+#pragma unroll
+  for (int off = K / 2; off >= 1; off >>= 1) {
+    float nx[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) nx[j] = sm[j] + sm[j ^ off];
+#pragma unroll
+    for (int j = 0; j < K; ++j) sm[j] = nx[j];
+  }
+#pragma unroll
+  for (int j = 0; j < K; ++j)
+    if (j < k) {
+      ids[j] = ti[j];
+      weights[j] = ex[j] / sm[0];
+    }
+}
+
 template <int K>
 __global__ void __launch_bounds__(64) route_topk_lanes_kernel(const float* __restrict__ logits, int T, int C, int k,
                                                               int32_t* __restrict__ ids,
@@ -366,27 +393,7 @@ __global__ void __launch_bounds__(64) route_topk_lanes_kernel(const float* __res
     insert_row<K, true>(rows + lane * P, C, tv, ti);
   else
     insert_row<K, false>(rows + lane * P, C, tv, ti);
-  float ex[K], sm[K];
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    ex[j] = j < k ? expf(tv[j] - tv[0]) : 0.0f;
-    sm[j] = ex[j];
-  }
-#pragma unroll
-  for (int off = K / 2; off >= 1; off >>= 1) {
-    float nx[K];
-#pragma unroll
-    for (int j = 0; j < K; ++j) nx[j] = sm[j] + sm[j ^ off];
-#pragma unroll
-    for (int j = 0; j < K; ++j) sm[j] = nx[j];
-  }
-  const int64_t o = (int64_t)(t0 + lane) * k;
-#pragma unroll
-  for (int j = 0; j < K; ++j)
-    if (j < k) {
-      ids[o + j] = ti[j];
-      weights[o + j] = ex[j] / sm[0];
-    }
+  topk_softmax_store<K>(tv, ti, k, ids + (int64_t)(t0 + lane) * k, weights + (int64_t)(t0 + lane) * k);
 }
 
 // ---- pack of per-sample route lists (the banked FFN: every token of sample b visits the
@@ -612,6 +619,292 @@ __global__ void __launch_bounds__(256) route_bwd_kernel(const int32_t* __restric
   if (dlogits_f32) dlogits_f32[e] = g;
 }
 
+// ---- router GEMM + top-k + pack in two launches (C % 32 == 0, C <= 128, d % 64 == 0) ----
+//
+// route_gemm_topk: one workgroup per 32 tokens.  logits^T [C][32] = Wr x^T on
+// v_mfma_f32_32x32x16_bf16 (cluster index as the row dimension: the accumulators hold a token
+// per lane), the four waves each reduce a quarter of d and their partials are added in wave
+// order through LDS; then one lane per token runs the insertion top-k and softmax of
+// route_topk_lanes_kernel on the LDS row (same selections, same weights as route_topk applied
+// to these logits), and the block's cluster counts go to hist[block][C].
+// pack_place: one workgroup per 128 tokens (four route blocks): cluster offsets and the block's
+// base per cluster from the histograms (integer sums), then per 256-pair chunk one ballot per
+// cluster and wave ranks the pairs; slots follow cluster, then ascending pair index, as
+// rte_pack_index.
+constexpr int kRouteTok = 32;     // tokens per route_gemm_topk block
+constexpr int kPlaceTok = 128;    // tokens per pack_place block
+
+__device__ __forceinline__ f32x16_v rt_mfma(bf16x8_v a, bf16x8_v b, f32x16_v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// NaN-aware order with empty entries (index < 0) last
+__device__ __forceinline__ bool rt_first(float a, int ia, float b, int ib) {
+  if (ib < 0) return ia >= 0;
+  if (ia < 0) return false;
+  return better(a, ia, b, ib);
+}
+
+// the best K of a lane's 16 CB accumulator logits, inserted in ascending index as insert_row
+template <int CB, int K, bool kNaN>
+__device__ __forceinline__ void rt_insert(const f32x16_v (&acc)[CB], int h, float (&tv)[K], int (&ti)[K]) {
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      float v = acc[cb][r];
+      int i = cb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+#pragma unroll
+      for (int j = 0; j < K; ++j) {
+        bool take;
+        if (kNaN)
+          take = ti[j] < 0 || better(v, i, tv[j], ti[j]);
+        else
+          take = ti[j] < 0 || v > tv[j] || (v == tv[j] && i < ti[j]);
+        const float ov = tv[j];
+        const int oi = ti[j];
+        tv[j] = take ? v : ov;
+        ti[j] = take ? i : oi;
+        v = take ? ov : v;
+        i = take ? oi : i;
+      }
+    }
+}
+
+template <int CB, int K>
+__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) route_gemm_topk_kernel(
+    const bf16* __restrict__ x, int T, int d, const bf16* __restrict__ wr, int k, int32_t* __restrict__ ids,
+    float* __restrict__ weights, int32_t* __restrict__ hist, float* __restrict__ logits) {
+  constexpr int C = 32 * CB;
+  __shared__ int hs[C];
+  const int lane = threadIdx.x, h = lane >> 5, l32 = lane & 31;
+  const int t0 = blockIdx.x * kRouteTok;
+  const int t = t0 + l32;
+  const int tl = t < T ? t : T - 1;
+  for (int c = lane; c < C; c += 64) hs[c] = 0;
+  f32x16_v acc[CB];
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[cb][r] = 0.0f;
+  // eight 16-wide k steps per round with the loads first (a step past d re-reads step 0 and is
+  // skipped: wave-uniform)
+  const bf16* xr = x + (int64_t)tl * d + 8 * h;
+  const bf16* wrow = wr + (int64_t)l32 * d + 8 * h;
+  for (int k0 = 0; k0 < d; k0 += 128) {
+    bf16x8_v b[8], a[8][CB];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int kk = k0 + 16 * j < d ? k0 + 16 * j : 0;
+      b[j] = __builtin_bit_cast(bf16x8_v, *reinterpret_cast<const uint4*>(xr + kk));
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb)
+        a[j][cb] = __builtin_bit_cast(bf16x8_v, *reinterpret_cast<const uint4*>(wrow + (int64_t)cb * 32 * d + kk));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (k0 + 16 * j < d) {
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) acc[cb] = rt_mfma(a[j][cb], b[j], acc[cb]);
+      }
+  }
+  {
+  // lane (token l32, half h) holds logits c = 32 cb + 8 q + 4 h + i of register 4 q + i
+  bool nan_here = false;
+#pragma unroll
+  for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) nan_here |= acc[cb][r] != acc[cb][r];
+  if (logits != nullptr && t < T) {
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float4*>(logits + (int64_t)t * C + cb * 32 + 8 * q + 4 * h) =
+            make_float4(acc[cb][4 * q], acc[cb][4 * q + 1], acc[cb][4 * q + 2], acc[cb][4 * q + 3]);
+  }
+  const bool any_nan = __ballot(nan_here) != 0;
+  // the best K of this lane's 16 CB logits (inserted in ascending index), as insert_row
+  float tv[K];
+  int ti[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    tv[j] = 0.0f;
+    ti[j] = -1;
+  }
+  if (any_nan)
+    rt_insert<CB, K, true>(acc, h, tv, ti);
+  else
+    rt_insert<CB, K, false>(acc, h, tv, ti);
+  // merge with the other half of the token's logits (lane ^ 32): the best of A[j] and B[K-1-j]
+  // form a bitonic sequence holding the top K, sorted by a bitonic merge
+  float mv[K];
+  int mi[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const float pv = __shfl_xor(tv[K - 1 - j], 32, 64);
+    const int pi = __shfl_xor(ti[K - 1 - j], 32, 64);
+    const bool mine = rt_first(tv[j], ti[j], pv, pi);
+    mv[j] = mine ? tv[j] : pv;
+    mi[j] = mine ? ti[j] : pi;
+  }
+#pragma unroll
+  for (int off = K / 2; off >= 1; off >>= 1)
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+      if ((j & off) == 0 && rt_first(mv[j + off], mi[j + off], mv[j], mi[j])) {
+        const float fv = mv[j];
+        const int fi = mi[j];
+        mv[j] = mv[j + off];
+        mi[j] = mi[j + off];
+        mv[j + off] = fv;
+        mi[j + off] = fi;
+      }
+  if (h == 0 && t < T) {
+    topk_softmax_store<K>(mv, mi, k, ids + (int64_t)t * k, weights + (int64_t)t * k);
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+      if (j < k) atomicAdd(&hs[mi[j]], 1);  // integer counts: order-free
+  }
+  }
+  __syncthreads();
+  for (int c = lane; c < C; c += 64) hist[(int64_t)blockIdx.x * C + c] = hs[c];
+}
+
+template <int C, int K>
+__global__ void __launch_bounds__(256) pack_place_kernel(const int32_t* __restrict__ ids, const float* __restrict__ w,
+                                                         int T, int k, const int32_t* __restrict__ hist, int nblk,
+                                                         int32_t* __restrict__ offsets,
+                                                         int32_t* __restrict__ tok_of_slot,
+                                                         int32_t* __restrict__ pair_of_slot,
+                                                         int32_t* __restrict__ slot_of_pair,
+                                                         float* __restrict__ w_of_slot) {
+  constexpr int VPR = C / 4;          // 16-byte vectors per histogram row
+  constexpr int RPP = 256 / VPR;      // histogram rows per pass of the 256 threads
+  constexpr int MW = C / 64 > 0 ? C / 64 : 1;  // 64-bit route-mask words per token
+  constexpr int SEG = kPlaceTok / 4;  // tokens per wave in the per-cluster token prefix
+  __shared__ int sb[RPP][C], st[RPP][C];
+  __shared__ int base[C];
+  __shared__ unsigned long long mask[kPlaceTok][MW];
+  __shared__ unsigned short pre[kPlaceTok][C];  // earlier tokens of the wave's segment routed to c
+  __shared__ int segtot[4][C];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t0 = blockIdx.x * kPlaceTok;
+  const int first = blockIdx.x * (kPlaceTok / kRouteTok);  // this block's first route block
+  {
+    // thread: clusters 4 (tid % VPR) .. +3 of rows tid / VPR + RPP i, 16-byte loads all in flight
+    const int c0 = 4 * (tid % VPR), r0 = tid / VPR;
+    int4 bef = make_int4(0, 0, 0, 0), tot = make_int4(0, 0, 0, 0);
+#pragma unroll 8
+    for (int b = r0; b < nblk; b += RPP) {
+      const int4 v = *reinterpret_cast<const int4*>(hist + (int64_t)b * C + c0);
+      tot.x += v.x;
+      tot.y += v.y;
+      tot.z += v.z;
+      tot.w += v.w;
+      if (b < first) {
+        bef.x += v.x;
+        bef.y += v.y;
+        bef.z += v.z;
+        bef.w += v.w;
+      }
+    }
+    *reinterpret_cast<int4*>(&sb[r0][c0]) = bef;
+    *reinterpret_cast<int4*>(&st[r0][c0]) = tot;
+  }
+  // the route mask of each of the block's tokens (its k clusters are distinct: a top-k)
+  if (tid < kPlaceTok) {
+    unsigned long long m[MW];
+#pragma unroll
+    for (int q = 0; q < MW; ++q) m[q] = 0ull;
+    const int t = t0 + tid;
+    if (t < T) {
+      int cs[K];  // all k loads in flight
+#pragma unroll
+      for (int j = 0; j < K; ++j) cs[j] = j < k ? ids[(int64_t)t * k + j] : -1;
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+        if (cs[j] >= 0) {
+#pragma unroll
+          for (int q = 0; q < MW; ++q)
+            if ((cs[j] >> 6) == q) m[q] |= 1ull << (cs[j] & 63);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < MW; ++q) mask[tid][q] = m[q];
+  }
+  __syncthreads();
+  if (wave == 0) {  // exclusive scan of the cluster totals: lane l owns clusters [2 l, 2 l + 2)
+    int v[2], b[2], sum = 0;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = 2 * lane + u;
+      v[u] = 0;
+      b[u] = 0;
+      if (c < C) {
+#pragma unroll
+        for (int q = 0; q < RPP; ++q) {
+          v[u] += st[q][c];
+          b[u] += sb[q][c];
+        }
+      }
+      sum += v[u];
+    }
+    int inc = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int y = __shfl_up(inc, off, 64);
+      if (lane >= off) inc += y;
+    }
+    int s = inc - sum;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int c = 2 * lane + u;
+      if (c < C) {
+        base[c] = s + b[u];
+        if (blockIdx.x == 0) offsets[c] = s;
+      }
+      s += v[u];
+    }
+    if (blockIdx.x == 0 && lane == 63) offsets[C] = s;
+  }
+  // per cluster, the earlier tokens of this wave's 32-token segment routed to it
+  for (int c = lane; c < C; c += 64) {
+    int run = 0;
+    for (int r = 0; r < SEG; ++r) {
+      const int t = wave * SEG + r;
+      pre[t][c] = (unsigned short)run;
+      run += (int)((mask[t][c >> 6] >> (c & 63)) & 1ull);
+    }
+    segtot[wave][c] = run;
+  }
+  __syncthreads();
+  // one thread per token writes its k slots: cluster base + earlier segments + earlier tokens
+  if (tid < kPlaceTok && t0 + tid < T) {
+    const int t = t0 + tid, sg = tid / SEG;
+    int cs[K];
+    float ws[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      cs[j] = j < k ? ids[(int64_t)t * k + j] : 0;
+      ws[j] = j < k ? w[(int64_t)t * k + j] : 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+      if (j < k) {
+        const int64_t p = (int64_t)t * k + j;
+        const int c = cs[j];
+        int slot = base[c] + pre[tid][c];
+        for (int q = 0; q < sg; ++q) slot += segtot[q][c];
+        tok_of_slot[slot] = t;
+        pair_of_slot[slot] = (int32_t)p;
+        slot_of_pair[p] = slot;
+        w_of_slot[slot] = ws[j];
+      }
+  }
+}
+
+
 }  // namespace
 
 int route_topk(const float* logits, int T, int C, int k, int32_t* ids, float* weights, hipStream_t s) {
@@ -678,6 +971,51 @@ int pack_pairs(const int32_t* cl, int P, int C, int k, const float* w, int32_t* 
     RTE_TRY(check_launch("pack_scatter"));
   }
   return 0;
+}
+
+size_t route_pack_workspace_bytes(int T, int C) {
+  const int nblk = (T + kRouteTok - 1) / kRouteTok;
+  return (size_t)(nblk > 0 ? nblk : 1) * (size_t)(C > 0 ? C : 1) * sizeof(int32_t);
+}
+
+int route_pack(const bf16* x, int T, int d, const bf16* wr, int C, int k, int32_t* ids, float* weights,
+               int32_t* offsets, int32_t* tok_of_slot, int32_t* pair_of_slot, int32_t* slot_of_pair,
+               float* w_of_slot, float* logits, void* ws, size_t ws_bytes, hipStream_t s) {
+  RTE_REQUIRE(C == 32 || C == 64 || C == 128, "route_pack: C must be 32, 64 or 128 (got %d)", C);
+  RTE_REQUIRE(k >= 1 && k <= 16 && k <= C, "route_pack: k must be in [1, min(16, C)]");
+  RTE_REQUIRE(d >= 64 && d % 64 == 0, "route_pack: d must be a positive multiple of 64");
+  RTE_REQUIRE(T >= 0 && (int64_t)T * k < ((int64_t)1 << 31), "route_pack: too many pairs");
+  if (T == 0) return fill_i32(offsets, 0, C + 1, s);
+  RTE_REQUIRE(ws != nullptr && ws_bytes >= route_pack_workspace_bytes(T, C), "route_pack: workspace too small");
+  const int nblk = (T + kRouteTok - 1) / kRouteTok;
+  int32_t* hist = static_cast<int32_t*>(ws);
+#define RTE_ROUTE_GEMM(CB, K)                                                                                 \
+  hipLaunchKernelGGL((route_gemm_topk_kernel<CB, K>), dim3(nblk), dim3(64), 0, s, x, T, d, wr, k, ids, weights, \
+                     hist, logits)
+#define RTE_PACK_PLACE(C, K)                                                                                     \
+  hipLaunchKernelGGL((pack_place_kernel<C, K>), grid, dim3(256), 0, s, ids, weights, T, k, hist, nblk, offsets, \
+                     tok_of_slot, pair_of_slot, slot_of_pair, w_of_slot)
+  const dim3 grid((T + kPlaceTok - 1) / kPlaceTok);
+  if (k <= 8) {
+    if (C == 32) RTE_ROUTE_GEMM(1, 8);
+    else if (C == 64) RTE_ROUTE_GEMM(2, 8);
+    else RTE_ROUTE_GEMM(4, 8);
+    RTE_TRY(check_launch("route_gemm_topk"));
+    if (C == 32) RTE_PACK_PLACE(32, 8);
+    else if (C == 64) RTE_PACK_PLACE(64, 8);
+    else RTE_PACK_PLACE(128, 8);
+  } else {
+    if (C == 32) RTE_ROUTE_GEMM(1, 16);
+    else if (C == 64) RTE_ROUTE_GEMM(2, 16);
+    else RTE_ROUTE_GEMM(4, 16);
+    RTE_TRY(check_launch("route_gemm_topk"));
+    if (C == 32) RTE_PACK_PLACE(32, 16);
+    else if (C == 64) RTE_PACK_PLACE(64, 16);
+    else RTE_PACK_PLACE(128, 16);
+  }
+#undef RTE_ROUTE_GEMM
+#undef RTE_PACK_PLACE
+  return check_launch("pack_place");
 }
 
 int combine_rows(const bf16* rows, int T, int k, int d, const int32_t* slot_of_pair, const bf16* extra,

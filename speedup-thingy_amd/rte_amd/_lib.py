@@ -32,6 +32,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_gemm_workspace_bytes": (_SZ, [_I, _I, _I]),
     "rte_gemm_bf16_split": (_I, [_P, _P, _I, _P, _P, _I, _P, _I64, _I, _I, _I, _I, _F, _F, _P, _I64, _P, _SZ, _P]),
     "rte_route_topk": (_I, [_P, _I, _I, _I, _P, _P, _P]),
+    "rte_route_pack_workspace_bytes": (_SZ, [_I, _I]),
+    "rte_route_pack": (_I, [_P, _I, _I, _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "rte_pack_workspace_bytes": (_SZ, [_I, _I]),
     "rte_pack_index": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "rte_pack_index_noalloc_max_bytes": (_SZ, []),

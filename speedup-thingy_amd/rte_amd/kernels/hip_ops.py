@@ -718,6 +718,33 @@ def route_topk(logits: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor
     return ids, w
 
 
+def route_pack_supported(C: int, k: int, d: int) -> bool:
+    """Shapes rte_route_pack takes: the router GEMM, top-k and pack in two launches."""
+    return C in (32, 64, 128) and 1 <= k <= min(16, C) and d % 64 == 0
+
+
+def route_pack(xb: torch.Tensor, wrb: torch.Tensor, k: int, *, with_logits: bool = False):
+    """logits = xb wrb^T, ids / weights = route_topk(logits, k) and their pack, from
+    rte_route_pack: (ids int32 [T, k], weights fp32 [T, k], PackIndex, logits fp32 [T, C] or None)."""
+    _lib.require_device_tensors("route_pack", xb, wrb)
+    T, d = xb.shape
+    C = wrb.shape[0]
+    dev = xb.device
+    P = T * k
+    ids = torch.empty((T, k), dtype=torch.int32, device=dev)
+    w = torch.empty((T, k), dtype=F32, device=dev)
+    offsets = torch.empty((C + 1,), dtype=torch.int32, device=dev)
+    tok = torch.empty((P,), dtype=torch.int32, device=dev)
+    pos = torch.empty((P,), dtype=torch.int32, device=dev)
+    sop = torch.empty((P,), dtype=torch.int32, device=dev)
+    wos = torch.empty((P,), dtype=F32, device=dev)
+    logits = torch.empty((T, C), dtype=F32, device=dev) if with_logits else None
+    wsp, wsn = workspace(_lib.load().rte_route_pack_workspace_bytes(T, C), dev)
+    call("rte_route_pack", ptr(xb), T, d, ptr(wrb), C, k, ptr(ids), ptr(w), ptr(offsets), ptr(tok), ptr(pos),
+         ptr(sop), ptr(wos), ptr(logits), wsp, wsn, _s())
+    return ids, w, PackIndex(offsets, tok, pos, sop, wos, C, k), logits
+
+
 def pack_index(ids: torch.Tensor, n_clusters: int, weights: torch.Tensor | None = None,
                invalid: torch.Tensor | None = None) -> PackIndex:
     _lib.require_device_tensors("pack_index", ids, weights, invalid)
@@ -840,9 +867,13 @@ class RoutedClusterPoolFn(torch.autograd.Function):
         wrb = cast_bf16(wr)
         wugb = cast_bf16(wug)
         wdb = cast_bf16(wd)
-        logits = gemm(xb, wrb, out_f32=True)
-        ids, w = route_topk(logits, k)
-        out, pk, ug, zw = _pool_fwd(xb, ids, w, wugb, wdb, C, n, resid, masked=False)
+        if route_pack_supported(C, k, d):
+            ids, w, pk, _ = route_pack(xb, wrb, k)
+        else:
+            logits = gemm(xb, wrb, out_f32=True)
+            ids, w = route_topk(logits, k)
+            pk = None
+        out, pk, ug, zw = _pool_fwd(xb, ids, w, wugb, wdb, C, n, resid, masked=False, pk=pk)
         ctx.save_for_backward(xb, wrb, wugb, wdb, ids, w, pk.offsets, pk.tok_of_slot, pk.pair_of_slot,
                               pk.slot_of_pair, pk.w_of_slot, ug, zw)
         ctx.meta = (shape, k, C, n, resid is not None, wr.dtype, wug.dtype, wd.dtype)

@@ -277,6 +277,30 @@ def test_pack_index_bit_exact(T, k, C):
     np.testing.assert_array_equal(pk.w_of_slot.cpu().numpy(), w.reshape(-1)[ref["pair_of_slot"]])
 
 
+@pytest.mark.parametrize("T,d,C,k", [(8192, 512, 64, 8), (1000, 256, 32, 1), (777, 128, 128, 16),
+                                     (4096, 1024, 128, 8), (31, 64, 64, 8)])
+def test_route_pack_matches_gemm_topk_pack(T, d, C, k):
+    """rte_route_pack (router GEMM + top-k + pack in two launches): its logits within fp32
+    rounding of the oracle's x wr^T, its ids / weights bitwise route_topk of its own logits (and
+    the oracle's top-k rule), its pack bitwise rte_pack_index of those ids; skewed router rows."""
+    H = _ops()
+    rng = np.random.default_rng(T + 7 * C + k)
+    x = bf16_round(rng.standard_normal((T, d)).astype(np.float32))
+    # Zipf-like load: cluster c's router row grows with its popularity
+    wr = bf16_round((rng.standard_normal((C, d)) * 0.05 + 0.02 * (1.0 / np.arange(1, C + 1))[:, None]).astype(np.float32))
+    print(f"route_pack T={T} d={d} C={C} k={k}", flush=True)
+    ids, w, pk, logits = H.route_pack(_bf(x), _bf(wr), k, with_logits=True)
+    ref_logits = x.astype(np.float64) @ wr.astype(np.float64).T
+    assert_rel(_np(logits), ref_logits, FP32_RTOL, "route_pack logits")
+    ids2, w2 = H.route_topk(logits, k)
+    assert torch.equal(ids, ids2) and torch.equal(w, w2), "route_pack top-k differs from route_topk"
+    ref_ids, _ = R.route_topk(_np(logits).astype(np.float32), k)
+    np.testing.assert_array_equal(ids.cpu().numpy(), ref_ids)
+    pk2 = H.pack_index(ids, C, w)
+    for name in ("offsets", "tok_of_slot", "pair_of_slot", "slot_of_pair", "w_of_slot"):
+        assert torch.equal(getattr(pk, name), getattr(pk2, name)), name
+
+
 @pytest.mark.parametrize("T,C,k", [(8192, 64, 8), (333, 100, 5)])
 def test_route_bwd_matches_oracle(T, C, k):
     """dlogits of the top-k softmax: bf16 and fp32 outputs; pairs whose slot is -1 carry no
