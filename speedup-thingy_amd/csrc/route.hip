@@ -573,9 +573,23 @@ __global__ void __launch_bounds__(256) combine_kernel(const bf16* __restrict__ r
   float sum[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) sum[i] = 0.0f;
-  for (int j = 0; j < k; ++j) {
-    if (slot_of_pair && slot_of_pair[(int64_t)t * k + j] < 0) continue;  // dropped (invalid) pair
-    add8_bf16(sum, *reinterpret_cast<const uint4*>(rows + ((int64_t)t * k + j) * d + c));
+  if (k <= 16) {
+    // every pair's slot flag and row loaded before the (ascending j) sum: one memory latency
+    uint4 v[16];
+    bool use[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      use[j] = j < k && (!slot_of_pair || slot_of_pair[(int64_t)t * k + j] >= 0);  // dropped pairs skip
+      v[j] = j < k ? *reinterpret_cast<const uint4*>(rows + ((int64_t)t * k + j) * d + c) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (use[j]) add8_bf16(sum, v[j]);
+  } else {
+    for (int j = 0; j < k; ++j) {
+      if (slot_of_pair && slot_of_pair[(int64_t)t * k + j] < 0) continue;  // dropped (invalid) pair
+      add8_bf16(sum, *reinterpret_cast<const uint4*>(rows + ((int64_t)t * k + j) * d + c));
+    }
   }
   if (extra) add8_bf16(sum, *reinterpret_cast<const uint4*>(extra + (int64_t)t * d + c));
 #pragma unroll
@@ -603,15 +617,39 @@ __global__ void __launch_bounds__(256) route_bwd_kernel(const int32_t* __restric
   const int32_t* st = slot_of_pair + t * k;
   float s = 0.0f, wsel = 0.0f, dsel = 0.0f;
   bool hit = false;
-  for (int j = 0; j < k; ++j) {
-    const int slot = st[j];
-    const float dw = slot >= 0 ? dw_slot[slot] : 0.0f;
-    const float wj = wt[j];
-    s += wj * dw;
-    if (it[j] == c) {
-      hit = true;
-      wsel = wj;
-      dsel = dw;
+  if (k <= 16) {
+    // the row's slots, weights and ids first, then the slot gradients: two memory latencies
+    int sl[16], id[16];
+    float wv[16], dv[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      sl[j] = j < k ? st[j] : -1;
+      wv[j] = j < k ? wt[j] : 0.0f;
+      id[j] = j < k ? it[j] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) dv[j] = sl[j] >= 0 ? dw_slot[sl[j]] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (j < k) {
+        s += wv[j] * dv[j];
+        if (id[j] == c) {
+          hit = true;
+          wsel = wv[j];
+          dsel = dv[j];
+        }
+      }
+  } else {
+    for (int j = 0; j < k; ++j) {
+      const int slot = st[j];
+      const float dw = slot >= 0 ? dw_slot[slot] : 0.0f;
+      const float wj = wt[j];
+      s += wj * dw;
+      if (it[j] == c) {
+        hit = true;
+        wsel = wj;
+        dsel = dw;
+      }
     }
   }
   const float g = hit ? wsel * (dsel - s) : 0.0f;
