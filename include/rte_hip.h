@@ -439,6 +439,51 @@ int rte_mse_fwd(const float* a, const float* b, int64_t n, float* out, void* wor
                 void* stream);
 int rte_mse_bwd(const float* a, const float* b, int64_t n, const float* dout, float* da, float* db, void* stream);
 
+/* ---- per-sample recipe / depth router (replaces Router.forward's recipe and depth heads,
+ *      rte/routing.py:80-188, and router_aux_losses, rte/metrics.py:97-112) ----
+ * pool: pooled f32 / bf16 [B, d] = mean over S of h0 f32 [B, S, d].
+ * Layer 1 of both MLPs (z1 = pooled W1^T + b1, f32 [B, hid]) runs on rte_gemm_bf16.
+ * heads_fwd (one wave per row): raw = silu(z1) W2^T + b2 (w2 f32 [N, hid]); logits = raw inv_t;
+ *   probs = softmax; id = first argmax of probs (NaN counts as maximal) or fixed_* when >= 0
+ *   (fixed_depth indexes depth_values); onehot_st = (onehot(id) + p) - p; entropy =
+ *   -sum log(max(p, 1e-9)) p; per pass t < P: logits + pass_bias[t] inv_t -> softmax / argmax /
+ *   one-hot; expected_depth = sum p_j depth_values[j]; depth = depth_values[depth id];
+ *   router entropy = recipe + depth entropy.  Outputs in this order: recipe logits, probs, id (i64),
+ *   onehot [B, R]; depth logits, probs, id (i64), depth (i64), onehot [B, D]; recipe / depth /
+ *   router entropy, expected depth [B]; per-pass logits, probs [B, P, R], ids (i64) [B, P],
+ *   onehot [B, P, R].  hid <= 4096, R and D <= 64, P <= 16.
+ * heads_bwd: gradients of those outputs (each optional, null = zero; same order without the ids
+ *   and depth) -> d raw logits draw_r [B, R], draw_d [B, D] and per-pass logit gradients dlbp
+ *   [B, P, R].
+ * mlp_bwd: dW2 [N, hid], db2 [N], dz1 bf16 [B, hid] (= (draw W2) silu'(z1)), db1 [hid] for both
+ *   MLPs and d pass_bias [P, R] = inv_t sum_rows dlbp; dW1 and d pooled then run on rte_gemm_bf16.
+ * aux_fwd: out f32 [3] = lambda_load (R sum_r mean_b(p)^2 - 1), lambda_cover sum_r
+ *   relu(coverage_min - ema_r)^2, lambda_depth mean_b(expected_depth); mean_prob [R] for the
+ *   backward.  aux_bwd: grad_out [3] -> dprobs [B, R], d expected_depth [B].
+ * Every sum runs in a fixed order. */
+int rte_router_pool(const float* h0, int B, int S, int d, float* pooled, void* pooled_bf16, void* stream);
+int rte_router_heads_fwd(const float* z1r, const float* z1d, int B, int hid, const float* w2r, const float* b2r,
+                         int R, const float* w2d, const float* b2d, int D, const float* pass_bias, int P,
+                         const int64_t* depth_values, float inv_t, int fixed_recipe, int fixed_depth, float* rlog,
+                         float* rprob, int64_t* rid, float* ronehot, float* dlog, float* dprob, int64_t* did,
+                         int64_t* depth, float* donehot, float* rent, float* dent, float* ent, float* edepth,
+                         float* rlog_bp, float* rprob_bp, int64_t* rid_bp, float* ronehot_bp, void* stream);
+int rte_router_heads_bwd(const float* rprob, const float* rprob_bp, const float* dprob, const int64_t* depth_values,
+                         int B, int R, int D, int P, float inv_t, const float* g_rlog, const float* g_rprob,
+                         const float* g_ronehot, const float* g_dlog, const float* g_dprob, const float* g_donehot,
+                         const float* g_rent, const float* g_dent, const float* g_ent, const float* g_edepth,
+                         const float* g_rlog_bp, const float* g_rprob_bp, const float* g_ronehot_bp, float* draw_r,
+                         float* draw_d, float* dlbp, void* stream);
+int rte_router_mlp_bwd(const float* draw_r, const float* draw_d, const float* z1r, const float* z1d,
+                       const float* w2r, const float* w2d, int B, int hid, int R, int D, const float* dlbp, int P,
+                       float inv_t, void* dz1r, void* dz1d, float* db1r, float* db1d, float* dw2r, float* dw2d,
+                       float* db2r, float* db2d, float* dpass, void* stream);
+int rte_router_aux_fwd(const float* probs, const float* edepth, const float* ema, int B, int R, float coverage_min,
+                       float lambda_load, float lambda_cover, float lambda_depth, float* mean_prob, float* out,
+                       void* stream);
+int rte_router_aux_bwd(const float* mean_prob, const float* grad_out, int B, int R, float lambda_load,
+                       float lambda_depth, float* dprobs, float* dedepth, void* stream);
+
 /* ---- fused AdamW step with the trainer's per-group norms (replaces torch.optim.AdamW.step,
  *      clip_grad_norm_ and _optimizer_grad_metrics of rte/training.py:385-468) ----
  * rows: device array of n_tensors records {p, g, exp_avg, exp_avg_sq, step (f32 scalar) pointers,

@@ -1034,6 +1034,159 @@ def linear_bias(x, w, b, *, out_f32: bool = True):
     return LinearBiasFn.apply(x, w, b, out_f32)
 
 
+# ----------------------------------------------------------------------------- recipe / depth router
+
+ROUTER_FIELDS = ("recipe_logits", "recipe_probs", "recipe_id", "recipe_onehot_st", "depth_logits", "depth_probs",
+                 "depth_id", "depth", "depth_onehot_st", "recipe_entropy", "depth_entropy", "router_entropy",
+                 "expected_depth", "recipe_logits_by_pass", "recipe_probs_by_pass", "recipe_id_by_pass",
+                 "recipe_onehot_st_by_pass")
+
+
+def router_supported(hid: int, R: int, D: int, P: int, d: int) -> bool:
+    return 1 <= hid <= 4096 and 1 <= R <= 64 and 1 <= D <= 64 and 0 <= P <= 16 and d % 8 == 0
+
+
+class RouterFn(torch.autograd.Function):
+    """Router.forward (rte/routing.py:80-188) for the recipe and depth heads: pooled mean of h0,
+    the two Linear -> SiLU -> Linear MLPs (layer 1 on the MFMA GEMM with the bias in its epilogue,
+    layer 2 and every head field in one launch with a wave per sample), per-pass recipe logits,
+    softmax / argmax / straight-through one-hot / entropies / expected depth.  The backward is two
+    small launches (heads, then layer 2 + SiLU + biases + pass bias) and the GEMMs of layer 1.
+    Outputs are ROUTER_FIELDS in order; ids and depth are int64."""
+
+    @staticmethod
+    def forward(ctx, h0, w1r, b1r, w2r, b2r, w1d, b1d, w2d, b2d, pass_bias, depth_values, inv_t: float,
+                fixed_recipe: int, fixed_depth: int):
+        _lib.require_device_tensors("router", h0, w1r, b1r, w2r, b2r, w1d, b1d, w2d, b2d, pass_bias, depth_values)
+        B, S, d = h0.shape
+        hid, R, D, P = w1r.shape[0], w2r.shape[0], w2d.shape[0], pass_bias.shape[0]
+        if not router_supported(hid, R, D, P, d) or w1d.shape[0] != hid:
+            raise ValueError(f"router: unsupported sizes (hidden {hid}, recipes {R}, depths {D}, passes {P}, d {d})")
+        dev = h0.device
+        h0c = h0.detach().contiguous().to(F32)
+        pooled = torch.empty((B, d), dtype=F32, device=dev)
+        pooled_b = torch.empty((B, d), dtype=BF16, device=dev)
+        call("rte_router_pool", ptr(h0c), B, S, d, ptr(pooled), ptr(pooled_b), _s())
+        w1rb, w1db = cast_bf16(w1r), cast_bf16(w1d)
+        z1 = torch.empty((2, B, hid), dtype=F32, device=dev)
+        wsp, wsn = _gemm_ws(B, hid, d, dev)
+        for i, (wb, bias) in enumerate(((w1rb, b1r), (w1db, b1d))):
+            bias = bias.detach().reshape(hid).contiguous().to(F32)
+            call("rte_gemm_bf16", ptr(pooled_b), d, 0, None, ptr(wb), d, 0, None, ptr(z1[i]), hid, 1, B, hid, d,
+                 1.0, 0.0, ptr(bias), 0, wsp, wsn, _s())
+        f32 = [w.detach().contiguous().to(F32) for w in (w2r, b2r, w2d, b2d, pass_bias)]
+        dv = depth_values.detach().contiguous().to(torch.int64)
+
+        def e(*shape, dt=F32):
+            return torch.empty(shape, dtype=dt, device=dev)
+
+        I64 = torch.int64
+        out = (e(B, R), e(B, R), e(B, dt=I64), e(B, R), e(B, D), e(B, D), e(B, dt=I64), e(B, dt=I64), e(B, D),
+               e(B), e(B), e(B), e(B), e(B, P, R), e(B, P, R), e(B, P, dt=I64), e(B, P, R))
+        rlog, rprob, rid, roh, dlog, dprob, did, depth, doh, rent, dent, ent, edep, rlbp, rpbp, ridbp, rohbp = out
+        call("rte_router_heads_fwd", ptr(z1[0]), ptr(z1[1]), B, hid, ptr(f32[0]), ptr(f32[1]), R, ptr(f32[2]),
+             ptr(f32[3]), D, ptr(f32[4]), P, ptr(dv), float(inv_t), int(fixed_recipe), int(fixed_depth),
+             *(ptr(t) for t in out), _s())
+        ctx.save_for_backward(pooled_b, z1, w1rb, w1db, f32[0], f32[2], rprob, rpbp, dprob, dv)
+        ctx.meta = (B, S, d, hid, R, D, P, float(inv_t), h0.dtype, [t.dtype for t in (w1r, b1r, w2r, b2r, w1d, b1d,
+                                                                                      w2d, b2d, pass_bias)])
+        ctx.mark_non_differentiable(rid, did, depth, ridbp)
+        ctx.set_materialize_grads(False)
+        return out
+
+    @staticmethod
+    def backward(ctx, *g):
+        pooled_b, z1, w1rb, w1db, w2r, w2d, rprob, rpbp, dprob, dv = ctx.saved_tensors
+        B, S, d, hid, R, D, P, inv_t, h0_dt, w_dts = ctx.meta
+        dev = z1.device
+        gi = {n: (None if t is None else t.detach().contiguous().to(F32)) for n, t in zip(ROUTER_FIELDS, g)}
+
+        def gp(n):
+            return ptr(gi[n])
+
+        draw_r = torch.empty((B, R), dtype=F32, device=dev)
+        draw_d = torch.empty((B, D), dtype=F32, device=dev)
+        dlbp = torch.empty((B, P, R), dtype=F32, device=dev)
+        call("rte_router_heads_bwd", ptr(rprob), ptr(rpbp), ptr(dprob), ptr(dv), B, R, D, P, inv_t,
+             gp("recipe_logits"), gp("recipe_probs"), gp("recipe_onehot_st"), gp("depth_logits"), gp("depth_probs"),
+             gp("depth_onehot_st"), gp("recipe_entropy"), gp("depth_entropy"), gp("router_entropy"),
+             gp("expected_depth"), gp("recipe_logits_by_pass"), gp("recipe_probs_by_pass"),
+             gp("recipe_onehot_st_by_pass"), ptr(draw_r), ptr(draw_d), ptr(dlbp), _s())
+        dz1 = torch.empty((2, B, hid), dtype=BF16, device=dev)
+        db1 = torch.empty((2, hid), dtype=F32, device=dev)
+        dw2r = torch.empty((R, hid), dtype=F32, device=dev)
+        dw2d = torch.empty((D, hid), dtype=F32, device=dev)
+        db2r = torch.empty((R,), dtype=F32, device=dev)
+        db2d = torch.empty((D,), dtype=F32, device=dev)
+        dpass = torch.empty((P, R), dtype=F32, device=dev)
+        call("rte_router_mlp_bwd", ptr(draw_r), ptr(draw_d), ptr(z1[0]), ptr(z1[1]), ptr(w2r), ptr(w2d), B, hid, R, D,
+             ptr(dlbp), P, inv_t, ptr(dz1[0]), ptr(dz1[1]), ptr(db1[0]), ptr(db1[1]), ptr(dw2r), ptr(dw2d), ptr(db2r),
+             ptr(db2d), ptr(dpass), _s())
+        need = ctx.needs_input_grad
+        dw1r = gemm(dz1[0], pooled_b, a_t=True, b_t=True, out_f32=True) if need[1] else None
+        dw1d = gemm(dz1[1], pooled_b, a_t=True, b_t=True, out_f32=True) if need[5] else None
+        dh0 = None
+        if need[0]:
+            # d pooled / S, broadcast over the sequence as a view
+            dp = gemm(dz1[0], w1rb, b_t=True, out_f32=True, alpha=1.0 / S)
+            dp = gemm(dz1[1], w1db, b_t=True, out_f32=True, alpha=1.0 / S, resid=dp)
+            dh0 = dp.to(h0_dt).unsqueeze(1).expand(B, S, d)
+        grads = [dw1r, db1[0], dw2r, db2r, dw1d, db1[1], dw2d, db2d, dpass]
+        grads = [None if (t is None or not need[i + 1]) else t.to(dt) for i, (t, dt) in enumerate(zip(grads, w_dts))]
+        return (dh0, *grads, None, None, None, None)
+
+
+def router(h0, w1r, b1r, w2r, b2r, w1d, b1d, w2d, b2d, pass_bias, depth_values, *, inv_t: float = 1.0,
+           fixed_recipe: int | None = None, fixed_depth: int | None = None) -> dict[str, torch.Tensor]:
+    """The router's recipe / depth fields (ROUTER_FIELDS) from h0 [B, S, d]; fixed_depth is an
+    index into depth_values."""
+    out = RouterFn.apply(h0, w1r, b1r, w2r, b2r, w1d, b1d, w2d, b2d, pass_bias, depth_values, float(inv_t),
+                         -1 if fixed_recipe is None else int(fixed_recipe),
+                         -1 if fixed_depth is None else int(fixed_depth))
+    return dict(zip(ROUTER_FIELDS, out))
+
+
+class RouterAuxFn(torch.autograd.Function):
+    """router_aux_losses (rte/metrics.py:97-112) in one launch: load = lambda_load (R sum_r
+    mean_b(p)^2 - 1), cover = lambda_cover sum_r relu(coverage_min - usage_ema)^2, depth =
+    lambda_depth mean_b(expected_depth); the backward is one launch (cover has no gradient)."""
+
+    @staticmethod
+    def forward(ctx, probs, expected_depth, usage_ema, coverage_min: float, l_load: float, l_cover: float,
+                l_depth: float):
+        usage_ema = usage_ema.to(probs.device)
+        _lib.require_device_tensors("router_aux", probs, expected_depth, usage_ema)
+        B, R = probs.shape
+        if not (B >= 1 and 1 <= R <= 64):
+            raise ValueError(f"router_aux: unsupported sizes ({B} rows, {R} recipes)")
+        pc = probs.detach().contiguous().to(F32)
+        ec = expected_depth.detach().contiguous().to(F32)
+        ema = usage_ema.detach().contiguous().to(F32)
+        mp = torch.empty((R,), dtype=F32, device=probs.device)
+        out = torch.empty((3,), dtype=F32, device=probs.device)
+        call("rte_router_aux_fwd", ptr(pc), ptr(ec), ptr(ema), B, R, float(coverage_min), float(l_load),
+             float(l_cover), float(l_depth), ptr(mp), ptr(out), _s())
+        ctx.save_for_backward(mp)
+        ctx.meta = (B, R, float(l_load), float(l_depth), probs.dtype, expected_depth.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        (mp,) = ctx.saved_tensors
+        B, R, l_load, l_depth, p_dt, e_dt = ctx.meta
+        gc = g.detach().contiguous().to(F32)
+        dp = torch.empty((B, R), dtype=F32, device=g.device)
+        de = torch.empty((B,), dtype=F32, device=g.device)
+        call("rte_router_aux_bwd", ptr(mp), ptr(gc), B, R, l_load, l_depth, ptr(dp), ptr(de), _s())
+        return dp.to(p_dt), de.to(e_dt), None, None, None, None, None
+
+
+def router_aux(probs, expected_depth, usage_ema, *, coverage_min: float, lambda_load: float, lambda_cover: float,
+               lambda_depth: float) -> dict[str, torch.Tensor]:
+    out = RouterAuxFn.apply(probs, expected_depth, usage_ema, coverage_min, lambda_load, lambda_cover, lambda_depth)
+    return {"load": out[0], "cover": out[1], "depth": out[2]}
+
+
 # ----------------------------------------------------------------------------- LM head + cross-entropy
 
 class LMHeadCEFn(torch.autograd.Function):

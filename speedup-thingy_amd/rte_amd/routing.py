@@ -1,9 +1,11 @@
 """Per-sample recipe / depth router on the pooled prelude state (rte/routing.py:47-188).
 
-Every Linear runs on the MFMA GEMM with its bias added in the GEMM epilogue; the four factor
-heads (attention bank, FFN bank, head slot, FFN slot per recursive pass, rte/routing.py:94-101)
-are evaluated when one of their fields is first read, since the accelerated modes' losses
-never read them (their values are the reference's whenever they are read).
+The recipe and depth heads run as one HIP operator (hip_ops.router: a pooling launch, the two
+layer-1 GEMMs with the bias in their epilogue and one launch for layer 2 and every head field;
+backward in two launches plus the layer-1 GEMMs).  The four factor heads (attention bank, FFN
+bank, head slot, FFN slot per recursive pass, rte/routing.py:94-101) run on the bias-fused GEMM
+when one of their fields is first read, since the accelerated modes' losses never read them
+(their values are the reference's whenever they are read).
 """
 
 from __future__ import annotations
@@ -135,50 +137,16 @@ class Router(nn.Module):
 
     def forward(self, h0: torch.Tensor, *, fixed_recipe: int | None = None, fixed_depth: int | None = None,
                 temperature: float = 1.0) -> RouterOutput:
-        pooled = h0.mean(dim=1)
+        """The recipe and depth heads in one HIP operator (hip_ops.router: pooled mean, both MLPs,
+        per-pass logits, softmax / argmax / straight-through one-hot / entropies / expected depth)."""
         inv_t = 1.0 / max(temperature, 1e-6)
-        recipe_logits = _mlp(self.recipe_mlp, pooled) * inv_t
-        depth_logits = _mlp(self.depth_mlp, pooled) * inv_t
-        recipe_logits_by_pass = recipe_logits.unsqueeze(1) + self.pass_recipe_bias.unsqueeze(0) * inv_t
-        recipe_probs = F.softmax(recipe_logits, dim=-1)
-        recipe_probs_by_pass = F.softmax(recipe_logits_by_pass, dim=-1)
-        depth_probs = F.softmax(depth_logits, dim=-1)
-        B = h0.shape[0]
-        if fixed_recipe is None:
-            recipe_id = recipe_probs.argmax(dim=-1)
-            recipe_id_by_pass = recipe_probs_by_pass.argmax(dim=-1)
-        else:
-            recipe_id = torch.full((B,), fixed_recipe, device=h0.device, dtype=torch.long)
-            recipe_id_by_pass = torch.full((B, self.config.t_max), fixed_recipe, device=h0.device, dtype=torch.long)
-        if fixed_depth is None:
-            depth_id = depth_probs.argmax(dim=-1)
-        else:
+        depth_idx = None
+        if fixed_depth is not None:
             if fixed_depth not in self.config.depth_choices:
                 raise ValueError(f"fixed_depth={fixed_depth} is not in depth_choices")
-            depth_id = torch.full((B,), self.config.depth_choices.index(fixed_depth), device=h0.device, dtype=torch.long)
-        recipe_hard = F.one_hot(recipe_id, recipe_probs.shape[-1]).to(recipe_probs.dtype)
-        recipe_hard_by_pass = F.one_hot(recipe_id_by_pass, recipe_probs.shape[-1]).to(recipe_probs.dtype)
-        depth_hard = F.one_hot(depth_id, depth_probs.shape[-1]).to(depth_probs.dtype)
-        depth_values = self.depth_values.to(depth_probs.dtype)
-        recipe_entropy = _entropy(recipe_probs)
-        depth_entropy = _entropy(depth_probs)
-        return RouterOutput(
-            recipe_logits=recipe_logits,
-            recipe_probs=recipe_probs,
-            recipe_id=recipe_id,
-            recipe_onehot_st=recipe_hard + recipe_probs - recipe_probs.detach(),
-            depth_logits=depth_logits,
-            depth_probs=depth_probs,
-            depth_id=depth_id,
-            depth=self.depth_values[depth_id],
-            depth_onehot_st=depth_hard + depth_probs - depth_probs.detach(),
-            router_entropy=recipe_entropy + depth_entropy,
-            recipe_entropy=recipe_entropy,
-            depth_entropy=depth_entropy,
-            expected_depth=(depth_probs * depth_values).sum(dim=-1),
-            recipe_logits_by_pass=recipe_logits_by_pass,
-            recipe_probs_by_pass=recipe_probs_by_pass,
-            recipe_id_by_pass=recipe_id_by_pass,
-            recipe_onehot_st_by_pass=recipe_hard_by_pass + recipe_probs_by_pass - recipe_probs_by_pass.detach(),
-            _factor_fn=lambda: self._factor_heads(pooled, inv_t),
-        )
+            depth_idx = self.config.depth_choices.index(fixed_depth)
+        rm, dm = self.recipe_mlp, self.depth_mlp
+        f = hip_ops.router(h0, rm[0].weight, rm[0].bias, rm[2].weight, rm[2].bias, dm[0].weight, dm[0].bias,
+                           dm[2].weight, dm[2].bias, self.pass_recipe_bias, self.depth_values, inv_t=inv_t,
+                           fixed_recipe=fixed_recipe, fixed_depth=depth_idx)
+        return RouterOutput(**f, _factor_fn=lambda: self._factor_heads(h0.mean(dim=1), inv_t))

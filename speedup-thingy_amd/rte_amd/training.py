@@ -39,7 +39,8 @@ def set_seed(seed: int) -> None:
 
 
 def router_aux_losses(recipe_probs, expected_depth, usage_ema, tr: TrainingConfig) -> dict[str, torch.Tensor]:
-    """rte/metrics.py:97-112."""
+    """rte/metrics.py:97-112 in torch ops (the training step runs the same formula as one HIP
+    launch, hip_ops.router_aux)."""
     r = recipe_probs.shape[-1]
     mean_prob = recipe_probs.float().mean(dim=0)
     load = r * mean_prob.square().sum() - 1.0
@@ -272,8 +273,10 @@ class TrainEngine:
         if self.config.training.disable_router_aux:
             z = r.recipe_probs.new_zeros(())
             return {"load": z, "cover": z, "depth": z}
-        return router_aux_losses(r.recipe_probs, r.expected_depth, self.recursive_model.recipe_bank.usage_ema,
-                                 self.config.training)
+        tr = self.config.training
+        return hip_ops.router_aux(r.recipe_probs, r.expected_depth, self.recursive_model.recipe_bank.usage_ema,
+                                  coverage_min=tr.coverage_min, lambda_load=tr.lambda_load,
+                                  lambda_cover=tr.lambda_cover, lambda_depth=tr.lambda_depth)
 
     def _macro_loss(self, tokens, targets, *, shortlist: bool, chosen=None, random_negs=None):
         """Forward of the recursive_macro step (rte/training.py:1336-1385): hot path, audit

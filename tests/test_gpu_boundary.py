@@ -465,6 +465,148 @@ def test_router_matches_oracle_and_factor_heads():
     np.testing.assert_allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=1e-7)
 
 
+def _router_ref(h0, p, ids, inv_t):
+    """fp64 torch restatement of Router.forward's recipe / depth heads (rte/routing.py:80-188)
+    with the layer-1 GEMM operands (pooled state, W1) rounded to bf16 in the forward only; the
+    one-hot rows come from the kernel's ids."""
+    F_ = torch.nn.functional
+
+    def rb(t):
+        r = torch.from_numpy(bf16_round(t.detach().float().numpy())).double()
+        return t + (r - t).detach()
+
+    pooled = h0.mean(1)
+    out = {}
+    for head, (w1, b1, w2, b2) in (("recipe", p["r"]), ("depth", p["d"])):
+        z1 = rb(pooled) @ rb(w1).T + b1
+        out[head + "_logits"] = (F_.silu(z1) @ w2.T + b2) * inv_t
+
+    def heads(lg, idv):
+        pr = F_.softmax(lg, -1)
+        hard = F_.one_hot(idv, pr.shape[-1]).double()
+        return pr, hard + pr - pr.detach(), -(pr.clamp_min(1e-9).log() * pr).sum(-1)
+
+    rl, dl = out["recipe_logits"], out["depth_logits"]
+    out["recipe_probs"], out["recipe_onehot_st"], out["recipe_entropy"] = heads(rl, ids["recipe_id"])
+    out["depth_probs"], out["depth_onehot_st"], out["depth_entropy"] = heads(dl, ids["depth_id"])
+    out["router_entropy"] = out["recipe_entropy"] + out["depth_entropy"]
+    out["expected_depth"] = (out["depth_probs"] * p["dv"]).sum(-1)
+    lbp = rl.unsqueeze(1) + p["pass"].unsqueeze(0) * inv_t
+    out["recipe_logits_by_pass"] = lbp
+    out["recipe_probs_by_pass"], out["recipe_onehot_st_by_pass"], _ = heads(lbp, ids["recipe_id_by_pass"])
+    return out
+
+
+@pytest.mark.parametrize("fixed", [(None, None), (4, 1)])
+def test_router_operator_fields_and_gradients(fixed):
+    """hip_ops.router (pool + layer-1 GEMMs + one heads launch; backward in two launches + GEMMs)
+    against the fp64 restatement: logits within 1e-4 (fp32 sums of bf16-exact layer-1 operands),
+    ids the first argmax of the kernel's own probabilities (a tied pair of recipe rows picks the
+    lower index), probabilities / entropies / expected depth within 1e-5 of the formulas on the
+    kernel's logits, one-hot rows exactly (onehot + p) - p; gradients of h0 and every router
+    parameter for upstream gradients on all differentiable fields within 2e-2."""
+    from rte_amd.kernels import hip_ops
+
+    g = torch.Generator().manual_seed(41)
+    B, S, d, hid, R, D, P = 6, 20, 128, 128, 9, 3, 4
+    inv_t = 1.0 / 0.7
+
+    def rnd(*s, sc=1.0):
+        return (torch.randn(*s, generator=g, dtype=torch.float64) * sc)
+
+    w2r = rnd(R, hid, sc=0.2)
+    b2r = rnd(R, sc=0.1)
+    w2r[5] = w2r[2]
+    b2r[5] = b2r[2] = 4.0  # recipes 2 and 5 tie for the maximum on every row
+    cpu = {"r": [rnd(hid, d, sc=0.1), rnd(hid, sc=0.1), w2r, b2r],
+           "d": [rnd(hid, d, sc=0.1), rnd(hid, sc=0.1), rnd(D, hid, sc=0.2), rnd(D, sc=0.1)],
+           "pass": rnd(P, R, sc=0.5), "dv": torch.tensor([1.0, 2.0, 4.0], dtype=torch.float64)}
+    h0c = rnd(B, S, d)
+    dev = [t.float().to(DEV).requires_grad_() for t in (*cpu["r"], *cpu["d"], cpu["pass"])]
+    h0 = h0c.float().to(DEV).requires_grad_()
+    dvals = torch.tensor([1, 2, 4], dtype=torch.long, device=DEV)
+    fr, fd = fixed
+    f = hip_ops.router(h0, *dev[:8], dev[8], dvals, inv_t=inv_t, fixed_recipe=fr, fixed_depth=fd)
+    rp = _np(f["recipe_probs"])
+    if fr is None:
+        assert (f["recipe_id"].cpu().numpy() == 2).all()
+        np.testing.assert_array_equal(f["recipe_id"].cpu().numpy(), rp.argmax(-1))
+        np.testing.assert_array_equal(f["recipe_id_by_pass"].cpu().numpy(), _np(f["recipe_probs_by_pass"]).argmax(-1))
+        np.testing.assert_array_equal(f["depth_id"].cpu().numpy(), _np(f["depth_probs"]).argmax(-1))
+    else:
+        assert (f["recipe_id"].cpu().numpy() == fr).all() and (f["recipe_id_by_pass"].cpu().numpy() == fr).all()
+        assert (f["depth_id"].cpu().numpy() == fd).all()
+    np.testing.assert_array_equal(f["depth"].cpu().numpy(), np.array([1, 2, 4])[f["depth_id"].cpu().numpy()])
+    for name in ("recipe", "depth"):
+        lg = f[name + "_logits"].detach().cpu().numpy()
+        own = RO_softmax(lg.astype(np.float64))
+        np.testing.assert_allclose(_np(f[name + "_probs"]), own, rtol=1e-5, atol=1e-7)
+        pf = f[name + "_probs"].detach().cpu().numpy()
+        hard = np.eye(pf.shape[-1], dtype=np.float32)[f[name + "_id"].cpu().numpy()]
+        np.testing.assert_array_equal(f[name + "_onehot_st"].detach().cpu().numpy(), (hard + pf) - pf)
+        ent = -(np.log(np.maximum(own, 1e-9)) * own).sum(-1)
+        np.testing.assert_allclose(_np(f[name + "_entropy"]), ent, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(_np(f["router_entropy"]), _np(f["recipe_entropy"]) + _np(f["depth_entropy"]),
+                               rtol=1e-6)
+    np.testing.assert_allclose(_np(f["expected_depth"]), (_np(f["depth_probs"]) * [1.0, 2.0, 4.0]).sum(-1), rtol=1e-5)
+
+    h0r = h0c.clone().requires_grad_()
+    prm = {"r": [t.clone().requires_grad_() for t in cpu["r"]], "d": [t.clone().requires_grad_() for t in cpu["d"]],
+           "pass": cpu["pass"].clone().requires_grad_(), "dv": cpu["dv"]}
+    ids = {k: f[k].cpu() for k in ("recipe_id", "depth_id", "recipe_id_by_pass")}
+    ref = _router_ref(h0r, prm, ids, inv_t)
+    for k in ("recipe_logits", "depth_logits", "recipe_logits_by_pass"):
+        assert_rel(_np(f[k]), ref[k].detach().numpy(), 1e-4, k)
+    loss_k, loss_r = 0.0, 0.0
+    for k, v in ref.items():
+        gk = torch.randn(v.shape, generator=g, dtype=torch.float64)
+        loss_r = loss_r + (v * gk).sum()
+        loss_k = loss_k + (f[k] * gk.float().to(DEV)).sum()
+    loss_k.backward()
+    loss_r.backward()
+    assert_rel(_np(h0.grad), h0r.grad.numpy(), BF16_RTOL, "d h0")
+    refs = [*prm["r"], *prm["d"], prm["pass"]]
+    names = ["w1r", "b1r", "w2r", "b2r", "w1d", "b1d", "w2d", "b2d", "pass_bias"]
+    for n, a, b in zip(names, dev, refs):
+        assert_rel(_np(a.grad), b.grad.numpy(), BF16_RTOL, n)
+
+
+def RO_softmax(x):
+    e = np.exp(x - x.max(-1, keepdims=True))
+    return e / e.sum(-1, keepdims=True)
+
+
+def test_router_aux_operator_matches_torch_formula():
+    """hip_ops.router_aux (one launch forward, one backward) against router_aux_losses
+    (rte/metrics.py:97-112 in torch ops) on the same device tensors: values and the gradients of
+    the recipe probabilities and expected depth within 1e-5."""
+    from types import SimpleNamespace
+
+    from rte_amd.kernels import hip_ops
+    from rte_amd.training import router_aux_losses
+
+    tr = SimpleNamespace(lambda_load=0.3, lambda_cover=0.7, lambda_depth=0.05, coverage_min=0.2)
+    g = torch.Generator().manual_seed(43)
+    probs0 = torch.softmax(torch.randn(37, 16, generator=g), -1)
+    ed0 = torch.rand(37, generator=g) * 4
+    ema = torch.rand(16, generator=g) * 0.4
+    outs, grads = [], []
+    for fn in ("hip", "torch"):
+        p = probs0.to(DEV).requires_grad_()
+        e = ed0.to(DEV).requires_grad_()
+        if fn == "hip":
+            o = hip_ops.router_aux(p, e, ema.to(DEV), coverage_min=tr.coverage_min, lambda_load=tr.lambda_load,
+                                   lambda_cover=tr.lambda_cover, lambda_depth=tr.lambda_depth)
+        else:
+            o = router_aux_losses(p, e, ema.to(DEV), tr)
+        (2.0 * o["load"] + 3.0 * o["cover"] - 1.5 * o["depth"]).backward()
+        outs.append([o[k].item() for k in ("load", "cover", "depth")])
+        grads.append((_np(p.grad), _np(e.grad)))
+    np.testing.assert_allclose(outs[0], outs[1], rtol=1e-5)
+    np.testing.assert_allclose(grads[0][0], grads[1][0], rtol=1e-5, atol=1e-9)
+    np.testing.assert_allclose(grads[0][1], grads[1][1], rtol=1e-5, atol=1e-9)
+
+
 def test_router_backward_small_heads():
     """Gradients through the router's Linear layers (the depth head has 3 outputs, not a multiple
     of the GEMM's 8-element vectors) against fp64 autograd of the same modules on the CPU."""
