@@ -484,6 +484,21 @@ int rte_router_aux_fwd(const float* probs, const float* edepth, const float* ema
 int rte_router_aux_bwd(const float* mean_prob, const float* grad_out, int B, int R, float lambda_load,
                        float lambda_depth, float* dprobs, float* dedepth, void* stream);
 
+/* ---- audit sampler and usage statistics (replaces AuditEngine.compute_audit_prob and the
+ *      fixed-count branch of sample_mask_with_prob, rte/audit.py:79-132, and the bincount EMAs of
+ *      RecipeBank.update_usage / the audit coverage update) ----
+ * audit_sample_fixed (one workgroup): req[b] = clamp(p_min + alpha entropy[b] / denom + beta
+ *   residual + gamma max(coverage_min - coverage_ema[recipe_ids[b]], 0) / max(coverage_min,
+ *   1e-12), p_min, p_max); incl[b] = k / B; mask (bool bytes) [b] = b in chosen[0..k); stats f32
+ *   [5] = mean incl, mean req, count / B, count, mean incl.
+ * count_ema (one workgroup, bins R <= 4096): counts[r] = #{i < n : ids[i] == r and (mask null or
+ *   mask[i])}; ema[r] = ema[r] beta + (1 - beta) counts[r] / max(sum counts, 1), in place. */
+int rte_audit_sample_fixed(const float* entropy, const int64_t* recipe_ids, const float* coverage_ema,
+                           const int64_t* chosen, int B, int k, int R, float denom, float p_min, float p_max,
+                           float alpha, float beta, float gamma, float residual, float coverage_min, float* req,
+                           float* incl, void* mask, float* stats, void* stream);
+int rte_count_ema(const int64_t* ids, const void* mask, int n, float* ema, int R, float beta, void* stream);
+
 /* ---- fused AdamW step with the trainer's per-group norms (replaces torch.optim.AdamW.step,
  *      clip_grad_norm_ and _optimizer_grad_metrics of rte/training.py:385-468) ----
  * rows: device array of n_tensors records {p, g, exp_avg, exp_avg_sq, step (f32 scalar) pointers,

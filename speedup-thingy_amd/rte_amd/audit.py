@@ -128,6 +128,30 @@ class AuditEngine:
             launch.streams.append(side)
         return launch
 
+    def _fixed_count_sample(self, meta: ModelMeta, seed: int, chosen: torch.Tensor | None):
+        """compute_audit_prob followed by the fixed-count branch of sample_mask_with_prob and the
+        sampler's means, as one HIP launch.  Returns (mask, inclusion p, chosen, count, stats [5])."""
+        r = meta.router
+        R, D = r.recipe_logits.shape[-1], r.depth_logits.shape[-1]
+        ids = meta.recipe_ids
+        dev = ids.device
+        if self.recipe_audit_ema is None or self.recipe_audit_ema.numel() != R:
+            self.recipe_audit_ema = torch.zeros(R, dtype=torch.float32, device=dev)
+        self.recipe_audit_ema = self.recipe_audit_ema.to(dev).float().contiguous()
+        n = ids.numel()
+        k = min(int(self.config.audit_fixed_count_per_batch), n)
+        self.last_sample_mode, self.last_candidate_count, self.last_capped_fraction = "fixed_count", k, 0.0
+        if k > 0 and chosen is None:
+            chosen = self.fixed_count_index(n, k, seed, dev)
+        if k == 0:
+            chosen = None
+        c = self.config
+        _, incl, mask, st = hip_ops.audit_sample_fixed(
+            r.router_entropy, ids, self.recipe_audit_ema, chosen, denom=float(R + D), p_min=c.audit_p_min,
+            p_max=c.audit_p_max, alpha=c.audit_alpha, beta=c.audit_beta, gamma=c.audit_gamma,
+            residual=self.recent_residual, coverage_min=c.coverage_min)
+        return mask, incl, chosen, k, st
+
     @staticmethod
     def fixed_count_index(n: int, k: int, seed: int, device) -> torch.Tensor:
         """The fixed-count sampler's audited rows: the first k of a seeded permutation of n
@@ -192,21 +216,29 @@ class AuditEngine:
                 t.record_stream(main)
         if self.config.audit_fixed_count_per_batch is None:
             self.flush_pending()  # the Bernoulli sampler's probability depends on the last residual
-        req = self.compute_audit_prob(hot.meta)
-        mask, p, chosen, count = self.sample_mask_with_prob(req, seed=seed, chosen=chosen)
-        corrected = hot.loss_per_sample.clone()
+        fused = self.config.audit_fixed_count_per_batch is not None and hot.loss_per_sample.is_cuda
+        if fused:
+            # requested probability, fixed-count mask, inclusion probability and their means: one launch
+            mask, p, chosen, count, st = self._fixed_count_sample(hot.meta, seed, chosen)
+            metrics: dict[str, torch.Tensor] = {
+                name: st[i] for i, name in enumerate(("audit_probability", "audit_requested_probability",
+                                                      "audit_rate", "audit_count", "audit_inclusion_prob"))}
+        else:
+            req = self.compute_audit_prob(hot.meta)
+            mask, p, chosen, count = self.sample_mask_with_prob(req, seed=seed, chosen=chosen)
+            p_mean = p.mean()
+            mask_f = mask.float()
+            metrics = {
+                "audit_probability": p_mean,
+                "audit_requested_probability": req.mean(),
+                "audit_rate": mask_f.mean(),
+                "audit_count": mask_f.sum(),
+                "audit_inclusion_prob": p_mean,
+            }
+        corrected = None
         zero = hot.loss_per_sample.new_zeros(())
         aux = {k: zero for k in ("hid", "cos", "kl", "norm", "cons", "delta_dir", "delta_rms", "endpoint_normed",
                                  "endpoint_raw", "rms_trust")}
-        p_mean = p.mean()
-        mask_f = mask.float()
-        metrics: dict[str, torch.Tensor] = {
-            "audit_probability": p_mean,
-            "audit_requested_probability": req.mean(),
-            "audit_rate": mask_f.mean(),
-            "audit_count": mask_f.sum(),
-            "audit_inclusion_prob": p_mean,
-        }
         if count is not None:  # fixed-count sampler: rows and count known without reading the mask
             idx, has_audit = chosen, count > 0
         else:
@@ -271,8 +303,13 @@ class AuditEngine:
             metrics.update(align)
             # recent residual feeds the next step's audit probability; kept on device
             self._pending_residual = (1.0 - align["hidden_cosine_exact_macro"]).detach().clamp_min(0)
+        if corrected is None:
+            corrected = hot.loss_per_sample.clone()
         if hot.meta.recipe_ids is not None:
-            self._update_coverage(hot.meta.recipe_ids, mask)
+            if fused:
+                hip_ops.count_ema(hot.meta.recipe_ids, mask, self.recipe_audit_ema, self.config.coverage_beta)
+            else:
+                self._update_coverage(hot.meta.recipe_ids, mask)
         if launch is not None and launch.cons is not None:
             aux["cons"] = self.config.lambda_cons * launch.cons
         elif self.config.lambda_cons != 0.0 and hot.meta.h0 is not None and hot.meta.recipe_ids is not None:

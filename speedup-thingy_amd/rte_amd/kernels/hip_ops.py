@@ -1343,6 +1343,40 @@ class AuditCorrectFn(torch.autograd.Function):
         return dh.to(h_dt), (de.to(e_dt) if want_e else None), None, None, None, None
 
 
+def audit_sample_fixed(entropy, recipe_ids, coverage_ema, chosen, *, denom: float, p_min: float, p_max: float,
+                       alpha: float, beta: float, gamma: float, residual: float, coverage_min: float):
+    """The audit's requested probability (rte/audit.py:79-97) and the fixed-count sampler's mask
+    and inclusion probability (rte/audit.py:99-132) in one launch.  Returns (req [B], incl [B],
+    mask bool [B], stats [5] = mean incl, mean req, rate, count, mean incl)."""
+    _lib.require_device_tensors("audit_sample_fixed", entropy, recipe_ids, coverage_ema, chosen)
+    B = entropy.numel()
+    k = 0 if chosen is None else chosen.numel()
+    dev = entropy.device
+    ent = entropy.detach().reshape(B).contiguous().to(F32)
+    ids = recipe_ids.detach().reshape(B).contiguous().to(torch.int64)
+    ema = coverage_ema.detach().contiguous().to(F32)
+    ch = None if chosen is None else chosen.reshape(k).contiguous().to(torch.int64)
+    req = torch.empty((B,), dtype=F32, device=dev)
+    incl = torch.empty((B,), dtype=F32, device=dev)
+    mask = torch.empty((B,), dtype=torch.bool, device=dev)
+    stats = torch.empty((5,), dtype=F32, device=dev)
+    call("rte_audit_sample_fixed", ptr(ent), ptr(ids), ptr(ema), ptr(ch), B, k, ema.numel(), float(denom),
+         float(p_min), float(p_max), float(alpha), float(beta), float(gamma), float(residual), float(coverage_min),
+         ptr(req), ptr(incl), ptr(mask), ptr(stats), _s())
+    return req, incl, mask, stats
+
+
+def count_ema(ids, mask, ema, beta: float) -> None:
+    """In place: ema = beta ema + (1 - beta) counts / max(sum counts, 1), counts[r] the rows of
+    ids equal to r (where mask, if given, is set); ema is a contiguous fp32 device tensor."""
+    _lib.require_device_tensors("count_ema", ids, mask, ema)
+    if ema.dtype != F32 or not ema.is_contiguous():
+        raise TypeError("count_ema: ema must be a contiguous float32 tensor")
+    i = ids.detach().reshape(-1).contiguous().to(torch.int64)
+    m = None if mask is None else mask.detach().reshape(-1).contiguous().to(torch.bool)
+    call("rte_count_ema", ptr(i), ptr(m), i.numel(), ptr(ema), ema.numel(), float(beta), _s())
+
+
 def audit_correct(hot_tok, exact_tok, idx, p, *, clip=None, grad_corrected=True):
     """(corrected per-sample loss [B], exact per-sample loss [A], stats [4] = residual mean, std,
     var, corrected metric loss) from token losses hot_tok [B, S] and exact_tok [A, S]."""

@@ -10,6 +10,7 @@ from dataclasses import dataclass
 import torch
 
 from rte_amd.config import ModelConfig
+from rte_amd.kernels import hip_ops
 
 
 @dataclass(frozen=True, slots=True)
@@ -67,11 +68,10 @@ class RecipeBank:
         return self.recipes[int(recipe_id)]
 
     def update_usage(self, recipe_ids: torch.Tensor, beta: float = 0.98) -> None:
-        # kept on the ids' device with no host sync (the reference moves ids to the CPU and
-        # bincounts there); counts of ones are exact in fp32 whatever the summation order
+        """usage_ema = beta usage_ema + (1 - beta) bincount(ids) / max(#ids, 1) as one HIP launch
+        on the ids' device with no host sync (the reference moves ids to the CPU and bincounts
+        there); counts are exact integers."""
         ids = recipe_ids.detach().long().flatten()
-        if self.usage_ema.device != ids.device:
-            self.usage_ema = self.usage_ema.to(ids.device)
-        counts = torch.zeros_like(self.usage_ema).index_add_(0, ids, torch.ones_like(ids, dtype=torch.float32))
-        probs = counts / counts.sum().clamp_min(1.0)
-        self.usage_ema.mul_(beta).add_(probs, alpha=1.0 - beta)
+        if self.usage_ema.device != ids.device or not self.usage_ema.is_contiguous():
+            self.usage_ema = self.usage_ema.to(ids.device).contiguous()
+        hip_ops.count_ema(ids, None, self.usage_ema, beta)

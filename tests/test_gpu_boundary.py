@@ -607,6 +607,49 @@ def test_router_aux_operator_matches_torch_formula():
     np.testing.assert_allclose(grads[0][1], grads[1][1], rtol=1e-5, atol=1e-9)
 
 
+def test_audit_fixed_sampler_and_usage_ema_match_torch_formulas():
+    """hip_ops.audit_sample_fixed against AuditEngine.compute_audit_prob + the fixed-count branch of
+    sample_mask_with_prob (rte/audit.py:79-132, torch ops on the same device tensors): requested
+    probability within 1e-6, mask and inclusion probability exact, the five means; hip_ops.count_ema
+    against the bincount EMA (rte/recipes.py update_usage, the audit coverage update) with and
+    without a mask, within 1e-6."""
+    from types import SimpleNamespace
+
+    from rte_amd.audit import AuditEngine
+    from rte_amd.kernels import hip_ops
+
+    cfg = SimpleNamespace(audit_fixed_count_per_batch=5, audit_p_min=0.02, audit_p_max=0.6, audit_alpha=0.7,
+                          audit_beta=0.3, audit_gamma=0.9, coverage_min=0.15, coverage_beta=0.9)
+    eng = AuditEngine(cfg)
+    eng.recent_residual = 0.37
+    g = torch.Generator().manual_seed(44)
+    B, R, D = 300, 16, 3
+    ids = torch.randint(0, R, (B,), generator=g).to(DEV)
+    ent = (torch.rand(B, generator=g) * 3).to(DEV)
+    eng.recipe_audit_ema = (torch.rand(R, generator=g) * 0.3).to(DEV)
+    meta = SimpleNamespace(router=SimpleNamespace(router_entropy=ent, recipe_logits=torch.empty(1, R),
+                                                  depth_logits=torch.empty(1, D)), recipe_ids=ids)
+    chosen = torch.randperm(B, generator=g)[:5].to(DEV)
+    req_t = eng.compute_audit_prob(meta)
+    mask_t, incl_t, _, _ = eng.sample_mask_with_prob(req_t, seed=0, chosen=chosen)
+    req, incl, mask, st = hip_ops.audit_sample_fixed(ent, ids, eng.recipe_audit_ema, chosen, denom=float(R + D),
+                                                     p_min=0.02, p_max=0.6, alpha=0.7, beta=0.3, gamma=0.9,
+                                                     residual=0.37, coverage_min=0.15)
+    np.testing.assert_allclose(_np(req), _np(req_t), rtol=1e-6)
+    np.testing.assert_array_equal(mask.cpu().numpy(), mask_t.cpu().numpy())
+    np.testing.assert_array_equal(incl.cpu().numpy(), incl_t.cpu().numpy())
+    ref = [incl_t.mean(), req_t.mean(), mask_t.float().mean(), mask_t.float().sum(), incl_t.mean()]
+    np.testing.assert_allclose(_np(st), [float(v) for v in ref], rtol=1e-6)
+    for m in (None, mask_t):
+        ema0 = (torch.rand(R, generator=g) * 0.2).to(DEV)
+        w = torch.ones(B, device=DEV) if m is None else m.float()
+        counts = torch.zeros(R, device=DEV).index_add_(0, ids, w)
+        ref_e = ema0 * 0.9 + (counts / counts.sum().clamp_min(1.0)) * 0.1
+        e = ema0.clone()
+        hip_ops.count_ema(ids, m, e, 0.9)
+        np.testing.assert_allclose(_np(e), _np(ref_e), rtol=1e-6, atol=1e-8)
+
+
 def test_router_backward_small_heads():
     """Gradients through the router's Linear layers (the depth head has 3 outputs, not a multiple
     of the GEMM's 8-element vectors) against fp64 autograd of the same modules on the CPU."""
