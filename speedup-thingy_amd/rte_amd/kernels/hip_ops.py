@@ -785,7 +785,10 @@ def pack_routes(recipe_ids: torch.Tensor, routes: torch.Tensor, route_w: torch.T
     wos = torch.empty((P,), dtype=F32, device=dev)
     nbytes = _lib.load().rte_pack_routes_workspace_bytes(B, kmax)
     ws = torch.empty((max(1, nbytes // 4),), dtype=torch.int32, device=dev)
-    act = None if active is None else active.reshape(-1).contiguous().to(torch.uint8)
+    act = None
+    if active is not None:  # a bool mask is read as bytes in place
+        act = active.reshape(-1).contiguous()
+        act = act.view(torch.uint8) if act.dtype == torch.bool else act.to(torch.uint8)
     rw = None if route_w is None else route_w.contiguous().to(F32)
     call("rte_pack_routes", ptr(rid), ptr(act), B, seq, ptr(rt), R, kmax, ptr(rw), n_clusters, ptr(offsets), ptr(tok),
          ptr(pos), ptr(sop), ptr(wos), ptr(ws), nbytes, _s())

@@ -625,11 +625,13 @@ class BankedRecursiveCore(nn.Module):
         w = torch.full((B * S, self.mlp.kmax), wt, dtype=torch.float32, device=h.device)
         return self._step(h, h0, hs, ids, w, pass_idx)
 
-    def forward_step(self, h, h0, recipe_ids, active_mask=None, pass_idx: int = 0, *, weights=None):
+    def forward_step(self, h, h0, recipe_ids, active_mask=None, pass_idx: int = 0, *, weights=None,
+                     head_scale=None):
         """One exact recursive pass (rte/layers.py:847-870): every sample runs its own recipe,
         inactive samples keep h.  The recipe ids stay on the device: the head / slab selection
-        is table lookups and masks, so the pass needs no host synchronisation."""
-        B, S, _ = h.shape
+        is table lookups and masks, so the pass needs no host synchronisation.  head_scale
+        (optional): the recipes' rows of attn.recipe_head_scale, looked up ahead."""
         rid = recipe_ids.long()
-        head_scale = self.attn.recipe_head_scale[rid]
+        if head_scale is None:
+            head_scale = self.attn.recipe_head_scale[rid]
         return self._step(h, h0, head_scale, None, None, pass_idx, weights, active_mask, rid).to(h.dtype)

@@ -97,6 +97,7 @@ class RecursiveModel(nn.Module):
         self.output_config = output_config or OutputConfig()
         self.recipe_bank = RecipeBank(config)
         self.register_buffer("active_touch_table", self.recipe_bank.active_touch_table, persistent=False)
+        self.register_buffer("pass_index", torch.arange(config.t_max), persistent=False)
         self.embed = Embedding(config.vocab_size, config.d_model)
         self.prelude = nn.Sequential(*[TransformerBlock(config) for _ in range(config.n_prelude)])
         self.router = Router(config)
@@ -156,10 +157,15 @@ class RecursiveModel(nn.Module):
         h = h0
         states: dict[int, torch.Tensor] = {}
         weights = self.core.prepare()
-        for t in range(self.config.t_max):
-            active = route.depth > t
-            rid = route.recipe_id_by_pass[:, t] if route.recipe_id_by_pass is not None else route.recipe_id
-            h = self.core.forward_step(h, h0, rid, active, pass_idx=t, weights=weights)
+        T = self.config.t_max
+        # every pass's recipe ids, active masks and head scales in one launch each
+        rid_bp = route.recipe_id_by_pass
+        rids = (rid_bp.t() if rid_bp is not None else route.recipe_id.reshape(1, -1).expand(T, -1)).contiguous()
+        actives = self.pass_index[:T, None] < route.depth.reshape(1, -1)
+        head_scales = self.core.attn.recipe_head_scale[rids.long()]
+        for t in range(T):
+            h = self.core.forward_step(h, h0, rids[t], actives[t], pass_idx=t, weights=weights,
+                                       head_scale=head_scales[t])
             if return_states and (t + 1) in self.config.depth_choices:
                 states[t + 1] = h  # every pass returns a new tensor; nothing writes h in place
         hidden = self._coda_hidden(h)
