@@ -5,7 +5,7 @@
 //   z1      = pooled W1^T + b1        (recipe and depth MLPs)      (the MFMA GEMM, bias epilogue)
 //   raw     = silu(z1) W2^T + b2                                   \
 //   logits  = raw * inv_t; probs = softmax; id = argmax(probs)      |  rtr_heads_fwd: one wave per
-//   by pass: logits + pass_bias[t] * inv_t -> softmax, argmax       |  sample row
+//   by pass: logits + pass_bias[t] * inv_t -> softmax, argmax       |  sample row, W2 through LDS
 //   onehot_st = (onehot(id) + p) - p; entropy = -sum log(max(p, 1e-9)) p
 //   expected_depth = sum_j p_j depth_values[j]                     /
 //
@@ -23,7 +23,7 @@ namespace {
 constexpr float kEntEps = 1e-9f;
 constexpr int kRtrMaxOut = 64;    // recipes or depth choices per head
 constexpr int kRtrMaxPass = 16;   // recursive passes with their own recipe bias
-constexpr int kRtrMaxHid = 4096;  // hidden width of the router MLPs
+constexpr int kRtrMaxHid = 4096;  // hidden width of the router MLPs (a launch-size bound only)
 constexpr int kRtrRowChunk = 64;  // rows of d raw logits staged per LDS pass in rtr_mlp_bwd
 
 __device__ __forceinline__ float rtr_wsum(float v) {
@@ -101,26 +101,53 @@ struct RtrFwd {
   float* rlog_bp;  float* rprob_bp;  int64_t* rid_bp;  float* ronehot_bp;  // [B, P, R] / [B, P]
 };
 
-__global__ void __launch_bounds__(64) rtr_heads_fwd_kernel(RtrFwd a) {
-  __shared__ float act[2][kRtrMaxHid];
-  __shared__ float raw[2 * kRtrMaxOut];
-  const int b = blockIdx.x, lane = threadIdx.x;
-  for (int j = lane; j < a.hid; j += 64) {
-    act[0][j] = rtr_silu(a.z1r[(int64_t)b * a.hid + j]);
-    act[1][j] = rtr_silu(a.z1d[(int64_t)b * a.hid + j]);
+constexpr int kRtrRows = 4;     // sample rows per workgroup (one wave each)
+constexpr int kRtrHidChunk = 128;  // hidden columns of W2 staged per LDS pass
+
+// raw[w][o] for the workgroup's rows: W2 (both heads, [R + D] rows) and the rows' silu(z1) are
+// staged through LDS kHidChunk columns at a time with coalesced loads; lane o of wave w then
+// sums its output over the columns in order (lanes o and o + 64 when R + D > 64).
+__global__ void __launch_bounds__(256) rtr_heads_fwd_kernel(RtrFwd a) {
+  __shared__ float ws[2 * kRtrMaxOut][kRtrHidChunk + 1];
+  __shared__ float act[kRtrRows][2][kRtrHidChunk];
+  __shared__ float raws[kRtrRows][2 * kRtrMaxOut];
+  const int t = threadIdx.x, w = t >> 6, lane = t & 63;
+  const int b0 = blockIdx.x * kRtrRows, NO = a.R + a.D;
+  float acc0 = 0.0f, acc1 = 0.0f;
+  for (int j0 = 0; j0 < a.hid; j0 += kRtrHidChunk) {
+    const int nc = a.hid - j0 < kRtrHidChunk ? a.hid - j0 : kRtrHidChunk;
+    __syncthreads();
+#pragma unroll 4
+    for (int i = t; i < NO * kRtrHidChunk; i += 256) {
+      const int o = i / kRtrHidChunk, c = i % kRtrHidChunk;
+      float v = 0.0f;
+      if (c < nc) v = o < a.R ? a.w2r[(int64_t)o * a.hid + j0 + c] : a.w2d[(int64_t)(o - a.R) * a.hid + j0 + c];
+      ws[o][c] = v;
+    }
+#pragma unroll 4
+    for (int i = t; i < kRtrRows * 2 * kRtrHidChunk; i += 256) {
+      const int r = i / (2 * kRtrHidChunk), m = (i / kRtrHidChunk) & 1, c = i % kRtrHidChunk;
+      const int row = b0 + r;
+      float v = 0.0f;
+      if (c < nc && row < a.B) v = rtr_silu((m ? a.z1d : a.z1r)[(int64_t)row * a.hid + j0 + c]);
+      act[r][m][c] = v;
+    }
+    __syncthreads();
+    if (lane < NO) {
+      const float* x = act[w][lane < a.R ? 0 : 1];
+      for (int c = 0; c < nc; ++c) acc0 += x[c] * ws[lane][c];
+    }
+    if (lane + 64 < NO) {
+      const float* x = act[w][lane + 64 < a.R ? 0 : 1];
+      for (int c = 0; c < nc; ++c) acc1 += x[c] * ws[lane + 64][c];
+    }
   }
+  if (lane < NO) raws[w][lane] = acc0 + (lane < a.R ? a.b2r[lane] : a.b2d[lane - a.R]);
+  if (lane + 64 < NO) raws[w][lane + 64] = acc1 + (lane + 64 < a.R ? a.b2r[lane + 64] : a.b2d[lane + 64 - a.R]);
   __syncthreads();
-  // layer 2: each output a wave-wide dot product over the hidden units (fixed xor tree)
-  for (int o = 0; o < a.R + a.D; ++o) {
-    const bool isr = o < a.R;
-    const float* w = isr ? a.w2r + (int64_t)o * a.hid : a.w2d + (int64_t)(o - a.R) * a.hid;
-    const float* x = act[isr ? 0 : 1];
-    float acc = 0.0f;
-    for (int j = lane; j < a.hid; j += 64) acc += x[j] * w[j];
-    acc = rtr_wsum(acc);
-    if (lane == 0) raw[o] = acc + (isr ? a.b2r[o] : a.b2d[o - a.R]);
-  }
-  __syncthreads();
+  const int b = b0 + w;
+  if (b >= a.B) return;  // whole wave: the heads below use only wave-level reductions
+  const float* raw = raws[w];
   const int R = a.R, D = a.D;
   const int64_t rb = (int64_t)b * R, db = (int64_t)b * D;
   // recipe head
@@ -129,11 +156,11 @@ __global__ void __launch_bounds__(64) rtr_heads_fwd_kernel(RtrFwd a) {
   float re = 0.0f;
   rtr_head_row(lg, lane, R, a.fixed_recipe, a.rprob + rb, a.rid + b, a.ronehot + rb, &re);
   // per-pass recipe heads
-  for (int t = 0; t < a.P; ++t) {
-    const int64_t o = ((int64_t)b * a.P + t) * R;
-    const float l2 = lane < R ? lg + a.pass_bias[t * R + lane] * a.inv_t : 0.0f;
+  for (int tp = 0; tp < a.P; ++tp) {
+    const int64_t o = ((int64_t)b * a.P + tp) * R;
+    const float l2 = lane < R ? lg + a.pass_bias[tp * R + lane] * a.inv_t : 0.0f;
     if (lane < R) a.rlog_bp[o + lane] = l2;
-    rtr_head_row(l2, lane, R, a.fixed_recipe, a.rprob_bp + o, a.rid_bp + (int64_t)b * a.P + t, a.ronehot_bp + o,
+    rtr_head_row(l2, lane, R, a.fixed_recipe, a.rprob_bp + o, a.rid_bp + (int64_t)b * a.P + tp, a.ronehot_bp + o,
                  nullptr);
   }
   // depth head
@@ -226,19 +253,65 @@ struct RtrMlpBwd {
   float* dpass;   // [P, R]
 };
 
-// grid (hid / 64, 2 MLPs), 256 threads: thread column j = 64 blockIdx.x + lane; the four waves
-// take interleaved row chunks of 16 and their partial sums meet in LDS in wave order.
+constexpr int kRtrStage = 4096;  // fp32 values per LDS staging pass
+
+// out[c] = (mul sum_{r < rows} src[r cols + c]) / div for c < cols <= 1024, by one workgroup of
+// 256 threads: rows are staged through LDS with coalesced loads, each column summed in row order.
+__device__ void rtr_colsum_block(const float* src, int rows, int cols, float mul, float div, float* out,
+                                 float* stage) {
+  const int t = threadIdx.x;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int chunk = kRtrStage / cols;
+  for (int r0 = 0; r0 < rows; r0 += chunk) {
+    const int nr = rows - r0 < chunk ? rows - r0 : chunk;
+    const int n = nr * cols;
+    __syncthreads();
+#pragma unroll 8
+    for (int i = t; i < n; i += 256) stage[i] = src[(int64_t)r0 * cols + i];
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = t + 256 * q;
+      if (c < cols) {
+        float s = acc[q];
+#pragma unroll 8
+        for (int r = 0; r < nr; ++r) s += stage[r * cols + c];
+        acc[q] = s;
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int c = t + 256 * q;
+    if (c < cols) out[c] = (acc[q] * mul) / div;
+  }
+}
+
+// grid (max(hid / 64, 3), 3), 256 threads.  y = 0, 1 (recipe, depth MLP): thread column
+// j = 64 blockIdx.x + lane; each 64-row chunk of d raw logits and z1[:, block columns] is staged
+// in LDS, wave w takes rows 16w .. 16w + 15 and the waves' partial sums meet in LDS in wave order.
+// y = 2: x = 0, 1 the layer-2 bias gradients, x = 2 the pass-bias gradient (column sums).
+template <int NB>
 __global__ void __launch_bounds__(256) rtr_mlp_bwd_kernel(RtrMlpBwd a) {
-  __shared__ float sd[kRtrRowChunk * kRtrMaxOut];
-  __shared__ float part[4][kRtrMaxOut + 1][64];
-  const int m = blockIdx.y, lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int N = a.N[m], hid = a.hid, B = a.B;
+  __shared__ float sd[kRtrRowChunk * NB];
+  __shared__ float zs[kRtrRowChunk][64];
+  __shared__ float part[4][NB + 1][64];
+  __shared__ float stage[kRtrStage];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int B = a.B, hid = a.hid;
+  if (blockIdx.y == 2) {
+    if (blockIdx.x < 2) rtr_colsum_block(a.draw[blockIdx.x], B, a.N[blockIdx.x], 1.0f, 1.0f, a.db2[blockIdx.x], stage);
+    else if (blockIdx.x == 2 && a.dpass) rtr_colsum_block(a.dlbp, B, a.P * a.R, a.inv_t, 1.0f, a.dpass, stage);
+    return;
+  }
+  if (blockIdx.x * 64 >= hid) return;
+  const int m = blockIdx.y, N = a.N[m];
   const int j = blockIdx.x * 64 + lane;
   const bool onj = j < hid;
-  float w2c[kRtrMaxOut];
-  float dw2[kRtrMaxOut];
+  float w2c[NB];
+  float dw2[NB];
 #pragma unroll
-  for (int n = 0; n < kRtrMaxOut; ++n) {
+  for (int n = 0; n < NB; ++n) {
     w2c[n] = (n < N && onj) ? a.w2[m][(int64_t)n * hid + j] : 0.0f;
     dw2[n] = 0.0f;
   }
@@ -246,69 +319,74 @@ __global__ void __launch_bounds__(256) rtr_mlp_bwd_kernel(RtrMlpBwd a) {
   for (int r0 = 0; r0 < B; r0 += kRtrRowChunk) {
     const int rows = B - r0 < kRtrRowChunk ? B - r0 : kRtrRowChunk;
     __syncthreads();
-    for (int i = threadIdx.x; i < rows * N; i += 256) sd[i] = a.draw[m][(int64_t)r0 * N + i];
+#pragma unroll 4
+    for (int i = t; i < rows * N; i += 256) sd[i] = a.draw[m][(int64_t)r0 * N + i];
+#pragma unroll 8
+    for (int i = t; i < kRtrRowChunk * 64; i += 256) {
+      const int rr = i >> 6, c = i & 63, jj = blockIdx.x * 64 + c;
+      zs[rr][c] = (rr < rows && jj < hid) ? a.z1[m][(int64_t)(r0 + rr) * hid + jj] : 0.0f;
+    }
     __syncthreads();
-    // wave w takes rows 16w .. 16w + 15 of the chunk
     for (int rr = 16 * w; rr < rows && rr < 16 * w + 16; ++rr) {
-      const int64_t row = r0 + rr;
-      const float z = onj ? a.z1[m][row * hid + j] : 0.0f;
+      const float z = zs[rr][lane];
       const float sg = 1.0f / (1.0f + expf(-z));
       const float act = rtr_silu(z);
       float da = 0.0f;
 #pragma unroll
-      for (int n = 0; n < kRtrMaxOut; ++n)
+      for (int n = 0; n < NB; ++n)
         if (n < N) {
           const float g = sd[rr * N + n];
           da += g * w2c[n];
           dw2[n] += g * act;
         }
       const float dz = da * (sg * (1.0f + z * (1.0f - sg)));
-      if (onj) a.dz1[m][row * hid + j] = f2bf(dz);
+      if (onj) a.dz1[m][(int64_t)(r0 + rr) * hid + j] = f2bf(dz);
       db1 += dz;
     }
   }
-  // the waves' partials in wave order
 #pragma unroll
-  for (int n = 0; n < kRtrMaxOut; ++n)
+  for (int n = 0; n < NB; ++n)
     if (n < N) part[w][n][lane] = dw2[n];
-  part[w][kRtrMaxOut][lane] = db1;
+  part[w][NB][lane] = db1;
   __syncthreads();
-  for (int i = threadIdx.x; i < (N + 1) * 64; i += 256) {
-    const int n = i / 64 < N ? i / 64 : kRtrMaxOut, l = i % 64;
+  for (int i = t; i < (N + 1) * 64; i += 256) {
+    const int n = i / 64 < N ? i / 64 : NB, l = i % 64;
     const int jj = blockIdx.x * 64 + l;
     const float s = ((part[0][n][l] + part[1][n][l]) + part[2][n][l]) + part[3][n][l];
     if (jj < hid) {
-      if (n < kRtrMaxOut) a.dw2[m][(int64_t)n * hid + jj] = s;
+      if (n < NB) a.dw2[m][(int64_t)n * hid + jj] = s;
       else a.db1[m][jj] = s;
-    }
-  }
-  if (blockIdx.x == 0) {
-    // bias of layer 2: rows in order
-    for (int n = threadIdx.x; n < N; n += 256) {
-      float s = 0.0f;
-      for (int r = 0; r < B; ++r) s += a.draw[m][(int64_t)r * N + n];
-      a.db2[m][n] = s;
-    }
-    if (m == 0 && a.dpass) {
-      for (int i = threadIdx.x; i < a.P * a.R; i += 256) {
-        float s = 0.0f;
-        for (int r = 0; r < B; ++r) s += a.dlbp[(int64_t)r * a.P * a.R + i];
-        a.dpass[i] = s * a.inv_t;
-      }
     }
   }
 }
 
-// pooled[b, c] = (sum_s h0[b, s, c]) / S, fp32 and bf16
+// pooled[b, c] = (sum_s h0[b, s, c]) / S, fp32 and bf16.  Block: 64 columns x 4 sequence
+// quarters (16 loads in flight per thread), quarters added in order.
 __global__ void __launch_bounds__(256) rtr_pool_kernel(const float* h0, int S, int d, float* pooled, bf16* pooled_b) {
-  const int c = blockIdx.x * 256 + threadIdx.x, b = blockIdx.y;
-  if (c >= d) return;
-  const float* p = h0 + (int64_t)b * S * d + c;
+  __shared__ float part[4][64];
+  const int lane = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane, b = blockIdx.y;
+  const int per = (S + 3) / 4, s0 = q * per < S ? q * per : S, s1 = s0 + per < S ? s0 + per : S;
   float s = 0.0f;
-  for (int i = 0; i < S; ++i) s += p[(int64_t)i * d];
-  const float v = s / (float)S;
-  pooled[(int64_t)b * d + c] = v;
-  pooled_b[(int64_t)b * d + c] = f2bf(v);
+  if (c < d) {
+    const float* p = h0 + (int64_t)b * S * d + c;
+    int i = s0;
+    for (; i + 16 <= s1; i += 16) {
+      float v[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) v[u] = p[(int64_t)(i + u) * d];
+#pragma unroll
+      for (int u = 0; u < 16; ++u) s += v[u];
+    }
+    for (; i < s1; ++i) s += p[(int64_t)i * d];
+  }
+  part[q][lane] = s;
+  __syncthreads();
+  if (q == 0 && c < d) {
+    const float v = (((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane]) / (float)S;
+    pooled[(int64_t)b * d + c] = v;
+    pooled_b[(int64_t)b * d + c] = f2bf(v);
+  }
 }
 
 // load = lambda_load (R sum_r mean_b(p)^2 - 1), cover = lambda_cover sum_r relu(cmin - ema_r)^2,
@@ -316,15 +394,14 @@ __global__ void __launch_bounds__(256) rtr_pool_kernel(const float* h0, int S, i
 __global__ void __launch_bounds__(256) rtr_aux_fwd_kernel(const float* probs, const float* edepth, const float* ema,
                                                           int B, int R, float cmin, float l_load, float l_cover,
                                                           float l_depth, float* mean_prob, float* out) {
+  __shared__ float stage[kRtrStage];
   __shared__ float mp[kRtrMaxOut];
-  const int t = threadIdx.x;
-  if (t < R) {
-    float s = 0.0f;
-    for (int b = 0; b < B; ++b) s += probs[(int64_t)b * R + t];
-    mp[t] = s / (float)B;
-    mean_prob[t] = mp[t];
-  }
+  __shared__ float em[1];
+  rtr_colsum_block(probs, B, R, 1.0f, (float)B, mp, stage);
+  rtr_colsum_block(edepth, B, 1, 1.0f, (float)B, em, stage);
   __syncthreads();
+  const int t = threadIdx.x;
+  if (t < R) mean_prob[t] = mp[t];
   if (t == 0) {
     float sq = 0.0f, cv = 0.0f;
     for (int r = 0; r < R; ++r) {
@@ -333,11 +410,9 @@ __global__ void __launch_bounds__(256) rtr_aux_fwd_kernel(const float* probs, co
       const float rl = g > 0.0f ? g : 0.0f;
       cv += rl * rl;
     }
-    float e = 0.0f;
-    for (int b = 0; b < B; ++b) e += edepth[b];
     out[0] = l_load * ((float)R * sq - 1.0f);
     out[1] = l_cover * cv;
-    out[2] = l_depth * (e / (float)B);
+    out[2] = l_depth * em[0];
   }
 }
 
@@ -363,7 +438,7 @@ int rte_router_pool(const float* h0, int B, int S, int d, float* pooled, void* p
   RTE_REQUIRE(B >= 0 && S >= 1 && d >= 1, "router_pool: bad sizes");
   RTE_REQUIRE(h0 && pooled && pooled_bf16, "router_pool: null argument");
   if (B == 0) return 0;
-  hipLaunchKernelGGL(rtr_pool_kernel, dim3((d + 255) / 256, B), dim3(256), 0, static_cast<hipStream_t>(stream), h0,
+  hipLaunchKernelGGL(rtr_pool_kernel, dim3((d + 63) / 64, B), dim3(256), 0, static_cast<hipStream_t>(stream), h0,
                      S, d, pooled, static_cast<bf16*>(pooled_bf16));
   return check_launch("router_pool");
 }
@@ -386,7 +461,8 @@ int rte_router_heads_fwd(const float* z1r, const float* z1d, int B, int hid, con
   RtrFwd a{z1r, z1d, w2r, b2r, w2d, b2d, pass_bias, depth_values, B, hid, R, D, P, inv_t, fixed_recipe, fixed_depth,
            rlog, rprob, rid, ronehot, dlog, dprob, did, depth, donehot, rent, dent, ent, edepth, rlog_bp, rprob_bp,
            rid_bp, ronehot_bp};
-  hipLaunchKernelGGL(rtr_heads_fwd_kernel, dim3(B), dim3(64), 0, static_cast<hipStream_t>(stream), a);
+  hipLaunchKernelGGL(rtr_heads_fwd_kernel, dim3((B + kRtrRows - 1) / kRtrRows), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), a);
   return check_launch("router_heads_fwd");
 }
 
@@ -422,8 +498,13 @@ int rte_router_mlp_bwd(const float* draw_r, const float* draw_d, const float* z1
   RtrMlpBwd a{{draw_r, draw_d}, {z1r, z1d}, {w2r, w2d}, {R, D}, B, hid, P, R, dlbp, inv_t,
               {static_cast<bf16*>(dz1r), static_cast<bf16*>(dz1d)}, {db1r, db1d}, {dw2r, dw2d}, {db2r, db2d},
               P > 0 ? dpass : nullptr};
-  hipLaunchKernelGGL(rtr_mlp_bwd_kernel, dim3((hid + 63) / 64, 2), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     a);
+  const int nbx = (hid + 63) / 64 > 3 ? (hid + 63) / 64 : 3;
+  const int nmax = R > D ? R : D;
+  const dim3 grid(nbx, 3);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (nmax <= 16) hipLaunchKernelGGL(rtr_mlp_bwd_kernel<16>, grid, dim3(256), 0, st, a);
+  else if (nmax <= 32) hipLaunchKernelGGL(rtr_mlp_bwd_kernel<32>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(rtr_mlp_bwd_kernel<64>, grid, dim3(256), 0, st, a);
   return check_launch("router_mlp_bwd");
 }
 
