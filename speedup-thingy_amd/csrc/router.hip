@@ -24,7 +24,6 @@ constexpr float kEntEps = 1e-9f;
 constexpr int kRtrMaxOut = 64;    // recipes or depth choices per head
 constexpr int kRtrMaxPass = 16;   // recursive passes with their own recipe bias
 constexpr int kRtrMaxHid = 4096;  // hidden width of the router MLPs (a launch-size bound only)
-constexpr int kRtrRowChunk = 64;  // rows of d raw logits staged per LDS pass in rtr_mlp_bwd
 
 __device__ __forceinline__ float rtr_wsum(float v) {
 #pragma unroll
@@ -101,45 +100,82 @@ struct RtrFwd {
   float* rlog_bp;  float* rprob_bp;  int64_t* rid_bp;  float* ronehot_bp;  // [B, P, R] / [B, P]
 };
 
-constexpr int kRtrRows = 4;     // sample rows per workgroup (one wave each)
-constexpr int kRtrHidChunk = 128;  // hidden columns of W2 staged per LDS pass
+constexpr int kRtrRows = 4;           // sample rows per workgroup (one wave each)
+constexpr int kRtrWsFloats = 12288;   // LDS for W2 columns (both heads)
+constexpr int kRtrMaxChunk = 512;     // hidden columns per staging pass
 
-// raw[w][o] for the workgroup's rows: W2 (both heads, [R + D] rows) and the rows' silu(z1) are
-// staged through LDS kHidChunk columns at a time with coalesced loads; lane o of wave w then
-// sums its output over the columns in order (lanes o and o + 64 when R + D > 64).
+// Loads n float4 (n <= 256 * U) from src rows into registers in one batch, then hands each to
+// put(i, value): every load of the batch is in flight before the first use.
+template <int U, typename Src, typename Put>
+__device__ __forceinline__ void rtr_stage4(int n, Src src, Put put) {
+  float4 v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = threadIdx.x + 256 * u;
+    if (i < n) v[u] = src(i);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = threadIdx.x + 256 * u;
+    if (i < n) put(i, v[u]);
+  }
+}
+
+// raw[w][o] for the workgroup's rows: W2 of both heads ([R + D] rows, column-major in LDS) and the
+// rows' silu(z1) are staged in one batch of 16-byte loads per pass (every pass when hid fits:
+// ch = min(hid, 512, 12288 / (R + D)) columns); lane o of wave w sums output o over the columns in
+// order (lanes o and o + 64 when R + D > 64).
 __global__ void __launch_bounds__(256) rtr_heads_fwd_kernel(RtrFwd a) {
-  __shared__ float ws[2 * kRtrMaxOut][kRtrHidChunk + 1];
-  __shared__ float act[kRtrRows][2][kRtrHidChunk];
+  __shared__ float ws[kRtrWsFloats];
+  __shared__ float act[kRtrRows][2][kRtrMaxChunk];
   __shared__ float raws[kRtrRows][2 * kRtrMaxOut];
   const int t = threadIdx.x, w = t >> 6, lane = t & 63;
-  const int b0 = blockIdx.x * kRtrRows, NO = a.R + a.D;
+  const int b0 = blockIdx.x * kRtrRows, NO = a.R + a.D, hid = a.hid;
+  int ch = kRtrWsFloats / NO;
+  ch = (ch < kRtrMaxChunk ? ch : kRtrMaxChunk) & ~3;
   float acc0 = 0.0f, acc1 = 0.0f;
-  for (int j0 = 0; j0 < a.hid; j0 += kRtrHidChunk) {
-    const int nc = a.hid - j0 < kRtrHidChunk ? a.hid - j0 : kRtrHidChunk;
+  for (int j0 = 0; j0 < hid; j0 += ch) {
+    const int nc = hid - j0 < ch ? hid - j0 : ch;  // a multiple of 4
+    const int q4 = nc / 4;
     __syncthreads();
-#pragma unroll 4
-    for (int i = t; i < NO * kRtrHidChunk; i += 256) {
-      const int o = i / kRtrHidChunk, c = i % kRtrHidChunk;
-      float v = 0.0f;
-      if (c < nc) v = o < a.R ? a.w2r[(int64_t)o * a.hid + j0 + c] : a.w2d[(int64_t)(o - a.R) * a.hid + j0 + c];
-      ws[o][c] = v;
-    }
-#pragma unroll 4
-    for (int i = t; i < kRtrRows * 2 * kRtrHidChunk; i += 256) {
-      const int r = i / (2 * kRtrHidChunk), m = (i / kRtrHidChunk) & 1, c = i % kRtrHidChunk;
-      const int row = b0 + r;
-      float v = 0.0f;
-      if (c < nc && row < a.B) v = rtr_silu((m ? a.z1d : a.z1r)[(int64_t)row * a.hid + j0 + c]);
-      act[r][m][c] = v;
-    }
+    rtr_stage4<12>(
+        NO * q4,
+        [&](int i) {
+          const int o = i / q4, c = 4 * (i % q4);
+          const float* src = o < a.R ? a.w2r + (int64_t)o * hid : a.w2d + (int64_t)(o - a.R) * hid;
+          return *reinterpret_cast<const float4*>(src + j0 + c);
+        },
+        [&](int i, float4 v) {
+          const int o = i / q4, c = 4 * (i % q4);
+          ws[(c + 0) * NO + o] = v.x;
+          ws[(c + 1) * NO + o] = v.y;
+          ws[(c + 2) * NO + o] = v.z;
+          ws[(c + 3) * NO + o] = v.w;
+        });
+    rtr_stage4<4>(
+        kRtrRows * 2 * q4,
+        [&](int i) {
+          const int r = i / (2 * q4), m = (i / q4) & 1, c = 4 * (i % q4);
+          const int row = b0 + r < a.B ? b0 + r : a.B - 1;
+          return *reinterpret_cast<const float4*>((m ? a.z1d : a.z1r) + (int64_t)row * hid + j0 + c);
+        },
+        [&](int i, float4 v) {
+          const int r = i / (2 * q4), m = (i / q4) & 1, c = 4 * (i % q4);
+          act[r][m][c + 0] = rtr_silu(v.x);
+          act[r][m][c + 1] = rtr_silu(v.y);
+          act[r][m][c + 2] = rtr_silu(v.z);
+          act[r][m][c + 3] = rtr_silu(v.w);
+        });
     __syncthreads();
     if (lane < NO) {
       const float* x = act[w][lane < a.R ? 0 : 1];
-      for (int c = 0; c < nc; ++c) acc0 += x[c] * ws[lane][c];
+#pragma unroll 16
+      for (int c = 0; c < nc; ++c) acc0 += x[c] * ws[c * NO + lane];
     }
     if (lane + 64 < NO) {
       const float* x = act[w][lane + 64 < a.R ? 0 : 1];
-      for (int c = 0; c < nc; ++c) acc1 += x[c] * ws[lane + 64][c];
+#pragma unroll 16
+      for (int c = 0; c < nc; ++c) acc1 += x[c] * ws[c * NO + lane + 64];
     }
   }
   if (lane < NO) raws[w][lane] = acc0 + (lane < a.R ? a.b2r[lane] : a.b2d[lane - a.R]);
@@ -253,10 +289,11 @@ struct RtrMlpBwd {
   float* dpass;   // [P, R]
 };
 
-constexpr int kRtrStage = 4096;  // fp32 values per LDS staging pass
+constexpr int kRtrStage = 8192;  // fp32 values per LDS staging pass of a column sum
 
 // out[c] = (mul sum_{r < rows} src[r cols + c]) / div for c < cols <= 1024, by one workgroup of
-// 256 threads: rows are staged through LDS with coalesced loads, each column summed in row order.
+// 256 threads: rows are staged through LDS (16-byte loads when cols % 4 == 0), each column summed
+// in row order.
 __device__ void rtr_colsum_block(const float* src, int rows, int cols, float mul, float div, float* out,
                                  float* stage) {
   const int t = threadIdx.x;
@@ -265,9 +302,16 @@ __device__ void rtr_colsum_block(const float* src, int rows, int cols, float mul
   for (int r0 = 0; r0 < rows; r0 += chunk) {
     const int nr = rows - r0 < chunk ? rows - r0 : chunk;
     const int n = nr * cols;
+    const float* s0 = src + (int64_t)r0 * cols;
     __syncthreads();
+    if (cols % 4 == 0) {
+      rtr_stage4<8>(
+          n / 4, [&](int i) { return *reinterpret_cast<const float4*>(s0 + 4 * i); },
+          [&](int i, float4 v) { *reinterpret_cast<float4*>(stage + 4 * i) = v; });
+    } else {
 #pragma unroll 8
-    for (int i = t; i < n; i += 256) stage[i] = src[(int64_t)r0 * cols + i];
+      for (int i = t; i < n; i += 256) stage[i] = s0[i];
+    }
     __syncthreads();
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -288,20 +332,22 @@ __device__ void rtr_colsum_block(const float* src, int rows, int cols, float mul
 }
 
 // grid (max(hid / 64, 3), 3), 256 threads.  y = 0, 1 (recipe, depth MLP): thread column
-// j = 64 blockIdx.x + lane; each 64-row chunk of d raw logits and z1[:, block columns] is staged
-// in LDS, wave w takes rows 16w .. 16w + 15 and the waves' partial sums meet in LDS in wave order.
-// y = 2: x = 0, 1 the layer-2 bias gradients, x = 2 the pass-bias gradient (column sums).
-template <int NB>
+// j = 64 blockIdx.x + lane; each RC-row chunk of d raw logits and z1[:, block columns] is staged
+// in LDS in one batch of loads, wave w takes rows w RC/4 .. (w + 1) RC/4 - 1 and the waves'
+// partial sums meet in LDS in wave order.  y = 2: x = 0, 1 the layer-2 bias gradients, x = 2 the
+// pass-bias gradient (column sums).
+template <int NB, int RC>
 __global__ void __launch_bounds__(256) rtr_mlp_bwd_kernel(RtrMlpBwd a) {
-  __shared__ float sd[kRtrRowChunk * NB];
-  __shared__ float zs[kRtrRowChunk][64];
-  __shared__ float part[4][NB + 1][64];
-  __shared__ float stage[kRtrStage];
+  constexpr int kMain = RC * NB + RC * 64 + 4 * (NB + 1) * 64;
+  __shared__ __align__(16) float lds[kMain > kRtrStage ? kMain : kRtrStage];
+  float* sd = lds;                                              // [RC][N]
+  float (*zs)[64] = reinterpret_cast<float (*)[64]>(lds + RC * NB);  // [RC][64]
+  float (*part)[NB + 1][64] = reinterpret_cast<float (*)[NB + 1][64]>(lds + RC * NB + RC * 64);
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int B = a.B, hid = a.hid;
   if (blockIdx.y == 2) {
-    if (blockIdx.x < 2) rtr_colsum_block(a.draw[blockIdx.x], B, a.N[blockIdx.x], 1.0f, 1.0f, a.db2[blockIdx.x], stage);
-    else if (blockIdx.x == 2 && a.dpass) rtr_colsum_block(a.dlbp, B, a.P * a.R, a.inv_t, 1.0f, a.dpass, stage);
+    if (blockIdx.x < 2) rtr_colsum_block(a.draw[blockIdx.x], B, a.N[blockIdx.x], 1.0f, 1.0f, a.db2[blockIdx.x], lds);
+    else if (blockIdx.x == 2 && a.dpass) rtr_colsum_block(a.dlbp, B, a.P * a.R, a.inv_t, 1.0f, a.dpass, lds);
     return;
   }
   if (blockIdx.x * 64 >= hid) return;
@@ -316,18 +362,25 @@ __global__ void __launch_bounds__(256) rtr_mlp_bwd_kernel(RtrMlpBwd a) {
     dw2[n] = 0.0f;
   }
   float db1 = 0.0f;
-  for (int r0 = 0; r0 < B; r0 += kRtrRowChunk) {
-    const int rows = B - r0 < kRtrRowChunk ? B - r0 : kRtrRowChunk;
+  const int c0 = blockIdx.x * 64;
+  const int ncol = hid - c0 < 64 ? hid - c0 : 64;  // a multiple of 4
+  for (int r0 = 0; r0 < B; r0 += RC) {
+    const int rows = B - r0 < RC ? B - r0 : RC;
+    const float* dr = a.draw[m] + (int64_t)r0 * N;
+    const float* zr = a.z1[m] + (int64_t)r0 * hid + c0;
     __syncthreads();
-#pragma unroll 4
-    for (int i = t; i < rows * N; i += 256) sd[i] = a.draw[m][(int64_t)r0 * N + i];
+    rtr_stage4<RC / 16>(
+        rows * 16, [&](int i) {
+          const int rr = i >> 4, c = 4 * (i & 15);
+          return c < ncol ? *reinterpret_cast<const float4*>(zr + (int64_t)rr * hid + c) : make_float4(0, 0, 0, 0);
+        },
+        [&](int i, float4 v) { *reinterpret_cast<float4*>(&zs[i >> 4][4 * (i & 15)]) = v; });
 #pragma unroll 8
-    for (int i = t; i < kRtrRowChunk * 64; i += 256) {
-      const int rr = i >> 6, c = i & 63, jj = blockIdx.x * 64 + c;
-      zs[rr][c] = (rr < rows && jj < hid) ? a.z1[m][(int64_t)(r0 + rr) * hid + jj] : 0.0f;
-    }
+    for (int i = t; i < rows * N; i += 256) sd[i] = dr[i];
     __syncthreads();
-    for (int rr = 16 * w; rr < rows && rr < 16 * w + 16; ++rr) {
+    const int rlo = w * (RC / 4), rhi = rlo + RC / 4 < rows ? rlo + RC / 4 : rows;
+#pragma unroll 4
+    for (int rr = rlo; rr < rhi; ++rr) {
       const float z = zs[rr][lane];
       const float sg = 1.0f / (1.0f + expf(-z));
       const float act = rtr_silu(z);
@@ -344,6 +397,7 @@ __global__ void __launch_bounds__(256) rtr_mlp_bwd_kernel(RtrMlpBwd a) {
       db1 += dz;
     }
   }
+  __syncthreads();
 #pragma unroll
   for (int n = 0; n < NB; ++n)
     if (n < N) part[w][n][lane] = dw2[n];
@@ -351,7 +405,7 @@ __global__ void __launch_bounds__(256) rtr_mlp_bwd_kernel(RtrMlpBwd a) {
   __syncthreads();
   for (int i = t; i < (N + 1) * 64; i += 256) {
     const int n = i / 64 < N ? i / 64 : NB, l = i % 64;
-    const int jj = blockIdx.x * 64 + l;
+    const int jj = c0 + l;
     const float s = ((part[0][n][l] + part[1][n][l]) + part[2][n][l]) + part[3][n][l];
     if (jj < hid) {
       if (n < NB) a.dw2[m][(int64_t)n * hid + jj] = s;
@@ -394,7 +448,7 @@ __global__ void __launch_bounds__(256) rtr_pool_kernel(const float* h0, int S, i
 __global__ void __launch_bounds__(256) rtr_aux_fwd_kernel(const float* probs, const float* edepth, const float* ema,
                                                           int B, int R, float cmin, float l_load, float l_cover,
                                                           float l_depth, float* mean_prob, float* out) {
-  __shared__ float stage[kRtrStage];
+  __shared__ __align__(16) float stage[kRtrStage];
   __shared__ float mp[kRtrMaxOut];
   __shared__ float em[1];
   rtr_colsum_block(probs, B, R, 1.0f, (float)B, mp, stage);
@@ -452,6 +506,7 @@ int rte_router_heads_fwd(const float* z1r, const float* z1d, int B, int hid, con
   RTE_REQUIRE(B >= 0 && hid >= 1 && hid <= kRtrMaxHid && R >= 1 && R <= kRtrMaxOut && D >= 1 && D <= kRtrMaxOut &&
                   P >= 0 && P <= kRtrMaxPass,
               "router_heads_fwd: sizes out of range (hid <= 4096, R, D <= 64, passes <= 16)");
+  RTE_REQUIRE(hid % 4 == 0, "router_heads_fwd: hidden width must be a multiple of 4");
   RTE_REQUIRE(fixed_recipe < R && fixed_depth < D, "router_heads_fwd: fixed id out of range");
   RTE_REQUIRE(z1r && z1d && w2r && b2r && w2d && b2d && depth_values && rlog && rprob && rid && ronehot && dlog &&
                   dprob && did && depth && donehot && rent && dent && ent && edepth,
@@ -490,6 +545,7 @@ int rte_router_mlp_bwd(const float* draw_r, const float* draw_d, const float* z1
   RTE_REQUIRE(B >= 0 && hid >= 1 && R >= 1 && R <= kRtrMaxOut && D >= 1 && D <= kRtrMaxOut && P >= 0 &&
                   P <= kRtrMaxPass,
               "router_mlp_bwd: sizes out of range");
+  RTE_REQUIRE(hid % 4 == 0, "router_mlp_bwd: hidden width must be a multiple of 4");
   RTE_REQUIRE(draw_r && draw_d && z1r && z1d && w2r && w2d && dz1r && dz1d && db1r && db1d && dw2r && dw2d && db2r &&
                   db2d,
               "router_mlp_bwd: null argument");
@@ -502,9 +558,9 @@ int rte_router_mlp_bwd(const float* draw_r, const float* draw_d, const float* z1
   const int nmax = R > D ? R : D;
   const dim3 grid(nbx, 3);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (nmax <= 16) hipLaunchKernelGGL(rtr_mlp_bwd_kernel<16>, grid, dim3(256), 0, st, a);
-  else if (nmax <= 32) hipLaunchKernelGGL(rtr_mlp_bwd_kernel<32>, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(rtr_mlp_bwd_kernel<64>, grid, dim3(256), 0, st, a);
+  if (nmax <= 16) hipLaunchKernelGGL((rtr_mlp_bwd_kernel<16, 128>), grid, dim3(256), 0, st, a);
+  else if (nmax <= 32) hipLaunchKernelGGL((rtr_mlp_bwd_kernel<32, 128>), grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL((rtr_mlp_bwd_kernel<64, 64>), grid, dim3(256), 0, st, a);
   return check_launch("router_mlp_bwd");
 }
 
