@@ -459,7 +459,8 @@ int rte_mse_bwd(const float* a, const float* b, int64_t n, const float* dout, fl
  *   MLPs and d pass_bias [P, R] = inv_t sum_rows dlbp; dW1 and d pooled then run on rte_gemm_bf16.
  * aux_fwd: out f32 [3] = lambda_load (R sum_r mean_b(p)^2 - 1), lambda_cover sum_r
  *   relu(coverage_min - ema_r)^2, lambda_depth mean_b(expected_depth); mean_prob [R] for the
- *   backward.  aux_bwd: grad_out [3] -> dprobs [B, R], d expected_depth [B].
+ *   backward.  aux_bwd: gradients of the load and depth terms (scalars, null = zero) -> dprobs
+ *   [B, R], d expected_depth [B].
  * Every sum runs in a fixed order. */
 int rte_router_pool(const float* h0, int B, int S, int d, float* pooled, void* pooled_bf16, void* stream);
 int rte_router_heads_fwd(const float* z1r, const float* z1d, int B, int hid, const float* w2r, const float* b2r,
@@ -481,8 +482,8 @@ int rte_router_mlp_bwd(const float* draw_r, const float* draw_d, const float* z1
 int rte_router_aux_fwd(const float* probs, const float* edepth, const float* ema, int B, int R, float coverage_min,
                        float lambda_load, float lambda_cover, float lambda_depth, float* mean_prob, float* out,
                        void* stream);
-int rte_router_aux_bwd(const float* mean_prob, const float* grad_out, int B, int R, float lambda_load,
-                       float lambda_depth, float* dprobs, float* dedepth, void* stream);
+int rte_router_aux_bwd(const float* mean_prob, const float* g_load, const float* g_depth, int B, int R,
+                       float lambda_load, float lambda_depth, float* dprobs, float* dedepth, void* stream);
 
 /* ---- audit sampler and usage statistics (replaces AuditEngine.compute_audit_prob and the
  *      fixed-count branch of sample_mask_with_prob, rte/audit.py:79-132, and the bincount EMAs of

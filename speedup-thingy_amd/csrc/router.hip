@@ -471,11 +471,12 @@ __global__ void __launch_bounds__(256) rtr_aux_fwd_kernel(const float* probs, co
 }
 
 // d probs[b, r] = g_load lambda_load R 2 mean_prob[r] / B;  d expected_depth[b] = g_depth lambda_depth / B
-__global__ void __launch_bounds__(256) rtr_aux_bwd_kernel(const float* mean_prob, const float* g, int B, int R,
-                                                          float l_load, float l_depth, float* dprobs,
-                                                          float* dedepth) {
+// (a null gradient is zero)
+__global__ void __launch_bounds__(256) rtr_aux_bwd_kernel(const float* mean_prob, const float* g_load,
+                                                          const float* g_depth, int B, int R, float l_load,
+                                                          float l_depth, float* dprobs, float* dedepth) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const float gl = g[0], gd = g[2];
+  const float gl = g_load ? g_load[0] : 0.0f, gd = g_depth ? g_depth[0] : 0.0f;
   if (i < (int64_t)B * R) dprobs[i] = gl * l_load * (float)R * (2.0f * mean_prob[i % R]) / (float)B;
   if (i < B) dedepth[i] = gd * l_depth / (float)B;
 }
@@ -574,14 +575,14 @@ int rte_router_aux_fwd(const float* probs, const float* edepth, const float* ema
   return check_launch("router_aux_fwd");
 }
 
-int rte_router_aux_bwd(const float* mean_prob, const float* grad_out, int B, int R, float lambda_load,
-                       float lambda_depth, float* dprobs, float* dedepth, void* stream) {
+int rte_router_aux_bwd(const float* mean_prob, const float* g_load, const float* g_depth, int B, int R,
+                       float lambda_load, float lambda_depth, float* dprobs, float* dedepth, void* stream) {
   RTE_REQUIRE(B >= 1 && R >= 1 && R <= kRtrMaxOut, "router_aux_bwd: sizes out of range");
-  RTE_REQUIRE(mean_prob && grad_out && dprobs && dedepth, "router_aux_bwd: null argument");
+  RTE_REQUIRE(mean_prob && dprobs && dedepth, "router_aux_bwd: null argument");
   const int64_t n = (int64_t)B * R > B ? (int64_t)B * R : B;
   hipLaunchKernelGGL(rtr_aux_bwd_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), mean_prob, grad_out, B, R, lambda_load, lambda_depth, dprobs,
-                     dedepth);
+                     static_cast<hipStream_t>(stream), mean_prob, g_load, g_depth, B, R, lambda_load, lambda_depth,
+                     dprobs, dedepth);
   return check_launch("router_aux_bwd");
 }
 

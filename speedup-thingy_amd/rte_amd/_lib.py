@@ -112,7 +112,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_router_heads_bwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _F] + [_P] * 13 + [_P, _P, _P, _P]),
     "rte_router_mlp_bwd": (_I, [_P] * 6 + [_I, _I, _I, _I, _P, _I, _F] + [_P] * 9 + [_P]),
     "rte_router_aux_fwd": (_I, [_P, _P, _P, _I, _I, _F, _F, _F, _F, _P, _P, _P]),
-    "rte_router_aux_bwd": (_I, [_P, _P, _I, _I, _F, _F, _P, _P, _P]),
+    "rte_router_aux_bwd": (_I, [_P, _P, _P, _I, _I, _F, _F, _P, _P, _P]),
     "rte_audit_sample_fixed": (_I, [_P, _P, _P, _P, _I, _I, _I] + [_F] * 8 + [_P, _P, _P, _P, _P]),
     "rte_count_ema": (_I, [_P, _P, _I, _P, _I, _F, _P]),
     "rte_mse_workspace_bytes": (_SZ, [_I64]),

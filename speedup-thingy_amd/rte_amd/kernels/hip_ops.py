@@ -1152,7 +1152,8 @@ def router(h0, w1r, b1r, w2r, b2r, w1d, b1d, w2d, b2d, pass_bias, depth_values, 
 class RouterAuxFn(torch.autograd.Function):
     """router_aux_losses (rte/metrics.py:97-112) in one launch: load = lambda_load (R sum_r
     mean_b(p)^2 - 1), cover = lambda_cover sum_r relu(coverage_min - usage_ema)^2, depth =
-    lambda_depth mean_b(expected_depth); the backward is one launch (cover has no gradient)."""
+    lambda_depth mean_b(expected_depth) as three scalar outputs; the backward is one launch (cover
+    has no gradient)."""
 
     @staticmethod
     def forward(ctx, probs, expected_depth, usage_ema, coverage_min: float, l_load: float, l_cover: float,
@@ -1171,23 +1172,28 @@ class RouterAuxFn(torch.autograd.Function):
              float(l_cover), float(l_depth), ptr(mp), ptr(out), _s())
         ctx.save_for_backward(mp)
         ctx.meta = (B, R, float(l_load), float(l_depth), probs.dtype, expected_depth.dtype)
-        return out
+        ctx.set_materialize_grads(False)
+        # three scalar outputs, so each loss term's gradient arrives without a select backward
+        return out[0], out[1], out[2]
 
     @staticmethod
-    def backward(ctx, g):
+    def backward(ctx, g_load, g_cover, g_depth):
         (mp,) = ctx.saved_tensors
         B, R, l_load, l_depth, p_dt, e_dt = ctx.meta
-        gc = g.detach().contiguous().to(F32)
-        dp = torch.empty((B, R), dtype=F32, device=g.device)
-        de = torch.empty((B,), dtype=F32, device=g.device)
-        call("rte_router_aux_bwd", ptr(mp), ptr(gc), B, R, l_load, l_depth, ptr(dp), ptr(de), _s())
+        dev = mp.device
+        gl = None if g_load is None else g_load.detach().reshape(1).contiguous().to(F32)
+        gd = None if g_depth is None else g_depth.detach().reshape(1).contiguous().to(F32)
+        dp = torch.empty((B, R), dtype=F32, device=dev)
+        de = torch.empty((B,), dtype=F32, device=dev)
+        call("rte_router_aux_bwd", ptr(mp), ptr(gl), ptr(gd), B, R, l_load, l_depth, ptr(dp), ptr(de), _s())
         return dp.to(p_dt), de.to(e_dt), None, None, None, None, None
 
 
 def router_aux(probs, expected_depth, usage_ema, *, coverage_min: float, lambda_load: float, lambda_cover: float,
                lambda_depth: float) -> dict[str, torch.Tensor]:
-    out = RouterAuxFn.apply(probs, expected_depth, usage_ema, coverage_min, lambda_load, lambda_cover, lambda_depth)
-    return {"load": out[0], "cover": out[1], "depth": out[2]}
+    load, cover, depth = RouterAuxFn.apply(probs, expected_depth, usage_ema, coverage_min, lambda_load, lambda_cover,
+                                           lambda_depth)
+    return {"load": load, "cover": cover, "depth": depth}
 
 
 # ----------------------------------------------------------------------------- LM head + cross-entropy

@@ -114,6 +114,9 @@ class MacroOperators(nn.Module):
         pairs = [(i, self.stride_to_idx[s * 2]) for i, s in enumerate(self.strides) if s * 2 in self.stride_to_idx]
         self.register_buffer("cons_src_idx", torch.tensor([p[0] for p in pairs], dtype=torch.long), persistent=False)
         self.register_buffer("cons_dst_idx", torch.tensor([p[1] for p in pairs], dtype=torch.long), persistent=False)
+        # [dst strides ; src strides]: the key offsets of the consistency loss's two operator calls
+        self.register_buffer("cons_key_idx", torch.tensor([p[1] for p in pairs] + [p[0] for p in pairs],
+                                                          dtype=torch.long), persistent=False)
 
     def stride_ids_for_depths(self, depths: torch.Tensor) -> torch.Tensor:
         matches = depths.unsqueeze(-1) == self.depth_values.to(depths.device).unsqueeze(0)
@@ -207,11 +210,13 @@ class MacroOperators(nn.Module):
             rho = torch.where(has, clamped, rho)
         return h0 + rho.view(-1, 1, 1).to(direction.dtype) * direction
 
-    def forward(self, h, h0, recipe_ids, depths, *, return_states: bool = False):
+    def forward(self, h, h0, recipe_ids, depths, *, return_states: bool = False, stride_ids=None):
+        """stride_ids (optional): stride_ids_for_depths(depths) when the caller already has it."""
         del return_states
         if self.config.macro_decomposition != "direct":
             raise NotImplementedError("only macro_decomposition='direct' is on the accelerated path")
-        stride_ids = self.stride_ids_for_depths(depths)
+        if stride_ids is None:
+            stride_ids = self.stride_ids_for_depths(depths)
         out = self.apply_vectorized(h, h0, recipe_ids, stride_ids)
         trace = MacroTrace(
             states={},
@@ -226,16 +231,16 @@ class MacroOperators(nn.Module):
         if self.cons_src_idx.numel() == 0:
             return h.new_zeros(())
         pc, b = self.cons_src_idx.numel(), h.shape[0]
+        if h is h0 and self._fused_bounded() and hip_ops.macro_fused_supported(self.v, self.u, 2 * pc):
+            # both operator applications, the MSE and every backward path in the fused kernels;
+            # keys[p, i] = recipe_ids[i] Kk + [dst ; src][p] in one launch
+            Kk = self.v.shape[1]
+            keys = torch.add(self.cons_key_idx.unsqueeze(1), recipe_ids.long().unsqueeze(0), alpha=Kk).reshape(-1)
+            return hip_ops.macro_consistency(h, keys, keys[pc * b:], self.v, self.u, self.d_gain, self.bias,
+                                             self.update_scale, self.config.macro_update_scale)
         r_rep = recipe_ids.repeat(pc)
         src = self.cons_src_idx.repeat_interleave(b)
         dst = self.cons_dst_idx.repeat_interleave(b)
-        if h is h0 and self._fused_bounded() and hip_ops.macro_fused_supported(self.v, self.u, 2 * pc):
-            # both operator applications, the MSE and every backward path in the fused kernels
-            Kk = self.v.shape[1]
-            rk = r_rep.long() * Kk
-            return hip_ops.macro_consistency(h, torch.cat([rk + dst, rk + src]), rk + src, self.v, self.u,
-                                             self.d_gain, self.bias, self.update_scale,
-                                             self.config.macro_update_scale)
         if self._fused_bounded() and 2 * pc <= 4:
             # Phi_{2s}(h) and the first Phi_s(h) read the same source batch: one operator call
             # over the 2 pc b (sample, key) pairs; the second Phi_s reads its output with h0

@@ -36,8 +36,15 @@ class ModelMeta:
     states: dict[int, torch.Tensor] | None = None
     macro_trace: MacroTrace | None = None
     shortlist: ShortlistResult | None = None
-    active_touches: torch.Tensor | None = None
+    touch_table: torch.Tensor | None = None
     token_loss: torch.Tensor | None = None
+
+    @property
+    def active_touches(self) -> torch.Tensor | None:
+        """Per-sample active touches of the chosen recipes (looked up when read)."""
+        if self.touch_table is None or self.recipe_ids is None:
+            return None
+        return self.touch_table[self.recipe_ids]
 
 
 @dataclass(slots=True)
@@ -172,7 +179,7 @@ class RecursiveModel(nn.Module):
         logits, lps, tok = head_logits_loss(hidden, self.vocab_weight, targets)
         meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
                          hidden=hidden, logits=logits, states=states if return_states else None,
-                         active_touches=self.active_touch_table[route.recipe_id], token_loss=tok)
+                         touch_table=self.active_touch_table, token_loss=tok)
         return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
                            meta)
 
@@ -201,7 +208,10 @@ class RecursiveModel(nn.Module):
         route = self.router(h0, fixed_recipe=fixed_recipe, fixed_depth=fixed_depth)
         if on_routed is not None:
             on_routed(h0, route)
-        h, trace = self.macro(h0, h0, route.recipe_id, route.depth, return_states=return_states)
+        # the macro strides are the depth choices: with distinct choices a depth's stride id is its
+        # depth id (stride_ids_for_depths: first stride equal to the depth)
+        sid = route.depth_id if len(set(self.config.depth_choices)) == len(self.config.depth_choices) else None
+        h, trace = self.macro(h0, h0, route.recipe_id, route.depth, return_states=return_states, stride_ids=sid)
         sl = None
         if shortlist and targets is not None:
             hidden = self._coda_hidden(h)
@@ -215,7 +225,7 @@ class RecursiveModel(nn.Module):
             logits = full_logits
         meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
                          hidden=hidden, logits=full_logits, states=trace.states if return_states else None,
-                         macro_trace=trace, shortlist=sl, active_touches=self.active_touch_table[route.recipe_id],
+                         macro_trace=trace, shortlist=sl, touch_table=self.active_touch_table,
                          token_loss=tok)
         return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
                            meta)
