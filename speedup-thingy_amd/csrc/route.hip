@@ -659,12 +659,9 @@ __global__ void __launch_bounds__(256) route_bwd_kernel(const int32_t* __restric
 
 // ---- router GEMM + top-k + pack in two launches (C % 32 == 0, C <= 128, d % 64 == 0) ----
 //
-// route_gemm_topk: one workgroup per 32 tokens.  logits^T [C][32] = Wr x^T on
-// v_mfma_f32_32x32x16_bf16 (cluster index as the row dimension: the accumulators hold a token
-// per lane), the four waves each reduce a quarter of d and their partials are added in wave
-// order through LDS; then one lane per token runs the insertion top-k and softmax of
-// route_topk_lanes_kernel on the LDS row (same selections, same weights as route_topk applied
-// to these logits), and the block's cluster counts go to hist[block][C].
+// route_gemm_topk: one workgroup per 32 tokens: router logits on MFMA, the top-k and softmax of
+// route_topk (same selections and weights on the same logits), and the block's cluster counts
+// to hist[block][C].
 // pack_place: one workgroup per 128 tokens (four route blocks): cluster offsets and the block's
 // base per cluster from the histograms (integer sums), then per 256-pair chunk one ballot per
 // cluster and wave ranks the pairs; slots follow cluster, then ascending pair index, as
@@ -676,137 +673,148 @@ __device__ __forceinline__ f32x16_v rt_mfma(bf16x8_v a, bf16x8_v b, f32x16_v c) 
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
-// NaN-aware order with empty entries (index < 0) last
-__device__ __forceinline__ bool rt_first(float a, int ia, float b, int ib) {
-  if (ib < 0) return ia >= 0;
-  if (ia < 0) return false;
-  return better(a, ia, b, ib);
+// 64-bit selection keys whose unsigned order is better(): high word the float's order-preserving
+// bit pattern (every NaN maximal, -0 as +0), low word ~index (ties: lower index first); an empty
+// entry is key 0, below every logit.
+__device__ __forceinline__ uint64_t rt_key(float v, int i) {
+  const uint32_t u = __float_as_uint(v == 0.0f ? 0.0f : v);
+  const uint32_t hi = v != v ? 0xffffffffu : ((u & 0x80000000u) ? ~u : (u | 0x80000000u));
+  return ((uint64_t)hi << 32) | (uint64_t)(~(uint32_t)i);
 }
 
-// the best K of a lane's 16 CB accumulator logits, inserted in ascending index as insert_row
-template <int CB, int K, bool kNaN>
-__device__ __forceinline__ void rt_insert(const f32x16_v (&acc)[CB], int h, float (&tv)[K], int (&ti)[K]) {
+__device__ __forceinline__ float rt_key_val(uint64_t key) {
+  const uint32_t hi = (uint32_t)(key >> 32);
+  if (hi == 0xffffffffu) return __uint_as_float(0x7fc00000u);
+  return __uint_as_float((hi & 0x80000000u) ? (hi & 0x7fffffffu) : ~hi);
+}
+
+__device__ __forceinline__ int rt_key_idx(uint64_t key) { return (int)~(uint32_t)key; }
+
+__device__ __forceinline__ uint64_t rt_shfl_xor(uint64_t v, int off) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, off, 64), hi = __shfl_xor((uint32_t)(v >> 32), off, 64);
+  return ((uint64_t)hi << 32) | lo;
+}
+
+// keys sorted descending by a bitonic network (N a power of two)
+template <int N>
+__device__ __forceinline__ void rt_sort(uint64_t (&key)[N]) {
 #pragma unroll
-  for (int cb = 0; cb < CB; ++cb)
+  for (int size = 2; size <= N; size <<= 1)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float v = acc[cb][r];
-      int i = cb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+    for (int stride = size / 2; stride > 0; stride >>= 1)
 #pragma unroll
-      for (int j = 0; j < K; ++j) {
-        bool take;
-        if (kNaN)
-          take = ti[j] < 0 || better(v, i, tv[j], ti[j]);
-        else
-          take = ti[j] < 0 || v > tv[j] || (v == tv[j] && i < ti[j]);
-        const float ov = tv[j];
-        const int oi = ti[j];
-        tv[j] = take ? v : ov;
-        ti[j] = take ? i : oi;
-        v = take ? ov : v;
-        i = take ? oi : i;
+      for (int i = 0; i < N; ++i) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const uint64_t x = key[i], y = key[j];
+          const bool sw = ((i & size) == 0) ? (y > x) : (x > y);
+          key[i] = sw ? y : x;
+          key[j] = sw ? x : y;
+        }
       }
-    }
 }
 
 template <int CB, int K>
-__global__ void __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(1, 2))) route_gemm_topk_kernel(
-    const bf16* __restrict__ x, int T, int d, const bf16* __restrict__ wr, int k, int32_t* __restrict__ ids,
-    float* __restrict__ weights, int32_t* __restrict__ hist, float* __restrict__ logits) {
+__global__ void __launch_bounds__(256) route_gemm_topk_kernel(const bf16* __restrict__ x, int T, int d,
+                                                              const bf16* __restrict__ wr, int k,
+                                                              int32_t* __restrict__ ids, float* __restrict__ weights,
+                                                              int32_t* __restrict__ hist, float* __restrict__ logits) {
   constexpr int C = 32 * CB;
+  constexpr int PER = C / 8;  // logits per lane in the top-k
+  __shared__ float part[4][C][kRouteTok + 1];
   __shared__ int hs[C];
-  const int lane = threadIdx.x, h = lane >> 5, l32 = lane & 31;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int t0 = blockIdx.x * kRouteTok;
-  const int t = t0 + l32;
-  const int tl = t < T ? t : T - 1;
-  for (int c = lane; c < C; c += 64) hs[c] = 0;
-  f32x16_v acc[CB];
-#pragma unroll
-  for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[cb][r] = 0.0f;
-  // eight 16-wide k steps per round with the loads first (a step past d re-reads step 0 and is
-  // skipped: wave-uniform)
-  const bf16* xr = x + (int64_t)tl * d + 8 * h;
-  const bf16* wrow = wr + (int64_t)l32 * d + 8 * h;
-  for (int k0 = 0; k0 < d; k0 += 128) {
-    bf16x8_v b[8], a[8][CB];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int kk = k0 + 16 * j < d ? k0 + 16 * j : 0;
-      b[j] = __builtin_bit_cast(bf16x8_v, *reinterpret_cast<const uint4*>(xr + kk));
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
-        a[j][cb] = __builtin_bit_cast(bf16x8_v, *reinterpret_cast<const uint4*>(wrow + (int64_t)cb * 32 * d + kk));
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (k0 + 16 * j < d) {
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) acc[cb] = rt_mfma(a[j][cb], b[j], acc[cb]);
-      }
-  }
+  for (int c = tid; c < C; c += 256) hs[c] = 0;
   {
-  // lane (token l32, half h) holds logits c = 32 cb + 8 q + 4 h + i of register 4 q + i
-  bool nan_here = false;
-#pragma unroll
-  for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) nan_here |= acc[cb][r] != acc[cb][r];
-  if (logits != nullptr && t < T) {
+    f32x16_v acc[CB];
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        *reinterpret_cast<float4*>(logits + (int64_t)t * C + cb * 32 + 8 * q + 4 * h) =
-            make_float4(acc[cb][4 * q], acc[cb][4 * q + 1], acc[cb][4 * q + 2], acc[cb][4 * q + 3]);
+      for (int r = 0; r < 16; ++r) acc[cb][r] = 0.0f;
+    const int tl = t0 + l32 < T ? t0 + l32 : T - 1;
+    const int kq = d / 4;  // a multiple of 16
+    const bf16* xr = x + (int64_t)tl * d + w * kq + 8 * h;
+    const bf16* wrow = wr + (int64_t)l32 * d + w * kq + 8 * h;
+    for (int k0 = 0; k0 < kq; k0 += 128) {
+      bf16x8_v b[8], a[8][CB];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int kk = k0 + 16 * j < kq ? k0 + 16 * j : 0;  // a step past the quarter re-reads step 0, skipped
+        b[j] = __builtin_bit_cast(bf16x8_v, *reinterpret_cast<const uint4*>(xr + kk));
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+          a[j][cb] = __builtin_bit_cast(bf16x8_v, *reinterpret_cast<const uint4*>(wrow + (int64_t)cb * 32 * d + kk));
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (k0 + 16 * j < kq) {
+#pragma unroll
+          for (int cb = 0; cb < CB; ++cb) acc[cb] = rt_mfma(a[j][cb], b[j], acc[cb]);
+        }
+    }
+    // register r of lane: cluster 32 cb + 8 (r / 4) + 4 h + r % 4, token l32
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) part[w][cb * 32 + 8 * (r >> 2) + 4 * h + (r & 3)][l32] = acc[cb][r];
   }
-  const bool any_nan = __ballot(nan_here) != 0;
-  // the best K of this lane's 16 CB logits (inserted in ascending index), as insert_row
+  __syncthreads();
+  const int tt = tid >> 3, s = tid & 7, t = t0 + tt;
+  float v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int c = s + 8 * i;
+    v[i] = ((part[0][c][tt] + part[1][c][tt]) + part[2][c][tt]) + part[3][c][tt];
+  }
+  if (logits != nullptr && t < T) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) logits[(int64_t)t * C + s + 8 * i] = v[i];
+  }
+  // the lane's PER logits sorted, its best K kept (empty keys past PER), then the eight lanes'
+  // lists merged pairwise
+  uint64_t key[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) key[i] = rt_key(v[i], s + 8 * i);
+  rt_sort<PER>(key);
+  uint64_t top[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) top[j] = j < PER ? key[j < PER ? j : 0] : 0ull;
+#pragma unroll
+  for (int off = 1; off < 8; off <<= 1) {
+    uint64_t m[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+      const uint64_t o = rt_shfl_xor(top[K - 1 - j], off);
+      m[j] = top[j] > o ? top[j] : o;
+    }
+#pragma unroll
+    for (int o2 = K / 2; o2 >= 1; o2 >>= 1)
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+        if ((j & o2) == 0) {
+          const uint64_t x = m[j], y = m[j + o2];
+          m[j] = x > y ? x : y;
+          m[j + o2] = x > y ? y : x;
+        }
+#pragma unroll
+    for (int j = 0; j < K; ++j) top[j] = m[j];
+  }
   float tv[K];
   int ti[K];
 #pragma unroll
   for (int j = 0; j < K; ++j) {
-    tv[j] = 0.0f;
-    ti[j] = -1;
+    tv[j] = rt_key_val(top[j]);
+    ti[j] = rt_key_idx(top[j]);
   }
-  if (any_nan)
-    rt_insert<CB, K, true>(acc, h, tv, ti);
-  else
-    rt_insert<CB, K, false>(acc, h, tv, ti);
-  // merge with the other half of the token's logits (lane ^ 32): the best of A[j] and B[K-1-j]
-  // form a bitonic sequence holding the top K, sorted by a bitonic merge
-  float mv[K];
-  int mi[K];
-#pragma unroll
-  for (int j = 0; j < K; ++j) {
-    const float pv = __shfl_xor(tv[K - 1 - j], 32, 64);
-    const int pi = __shfl_xor(ti[K - 1 - j], 32, 64);
-    const bool mine = rt_first(tv[j], ti[j], pv, pi);
-    mv[j] = mine ? tv[j] : pv;
-    mi[j] = mine ? ti[j] : pi;
-  }
-#pragma unroll
-  for (int off = K / 2; off >= 1; off >>= 1)
+  if (s == 0 && t < T) {
+    topk_softmax_store<K>(tv, ti, k, ids + (int64_t)t * k, weights + (int64_t)t * k);
 #pragma unroll
     for (int j = 0; j < K; ++j)
-      if ((j & off) == 0 && rt_first(mv[j + off], mi[j + off], mv[j], mi[j])) {
-        const float fv = mv[j];
-        const int fi = mi[j];
-        mv[j] = mv[j + off];
-        mi[j] = mi[j + off];
-        mv[j + off] = fv;
-        mi[j + off] = fi;
-      }
-  if (h == 0 && t < T) {
-    topk_softmax_store<K>(mv, mi, k, ids + (int64_t)t * k, weights + (int64_t)t * k);
-#pragma unroll
-    for (int j = 0; j < K; ++j)
-      if (j < k) atomicAdd(&hs[mi[j]], 1);  // integer counts: order-free
-  }
+      if (j < k) atomicAdd(&hs[ti[j]], 1);  // integer counts: order-free
   }
   __syncthreads();
-  for (int c = lane; c < C; c += 64) hist[(int64_t)blockIdx.x * C + c] = hs[c];
+  for (int c = tid; c < C; c += 256) hist[(int64_t)blockIdx.x * C + c] = hs[c];
 }
 
 template <int C, int K>
@@ -1028,7 +1036,7 @@ int route_pack(const bf16* x, int T, int d, const bf16* wr, int C, int k, int32_
   const int nblk = (T + kRouteTok - 1) / kRouteTok;
   int32_t* hist = static_cast<int32_t*>(ws);
 #define RTE_ROUTE_GEMM(CB, K)                                                                                 \
-  hipLaunchKernelGGL((route_gemm_topk_kernel<CB, K>), dim3(nblk), dim3(64), 0, s, x, T, d, wr, k, ids, weights, \
+  hipLaunchKernelGGL((route_gemm_topk_kernel<CB, K>), dim3(nblk), dim3(256), 0, s, x, T, d, wr, k, ids, weights, \
                      hist, logits)
 #define RTE_PACK_PLACE(C, K)                                                                                     \
   hipLaunchKernelGGL((pack_place_kernel<C, K>), grid, dim3(256), 0, s, ids, weights, T, k, hist, nblk, offsets, \
