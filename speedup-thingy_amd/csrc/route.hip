@@ -828,20 +828,29 @@ __global__ void __launch_bounds__(256) pack_place_kernel(const int32_t* __restri
   constexpr int VPR = C / 4;          // 16-byte vectors per histogram row
   constexpr int RPP = 256 / VPR;      // histogram rows per pass of the 256 threads
   constexpr int MW = C / 64 > 0 ? C / 64 : 1;  // 64-bit route-mask words per token
-  constexpr int SEG = kPlaceTok / 4;  // tokens per wave in the per-cluster token prefix
+  constexpr int SEG = kPlaceTok / 4;  // tokens per 32-bit segment mask (32)
   __shared__ int sb[RPP][C], st[RPP][C];
   __shared__ int base[C];
   __shared__ unsigned long long mask[kPlaceTok][MW];
-  __shared__ unsigned short pre[kPlaceTok][C];  // earlier tokens of the wave's segment routed to c
-  __shared__ int segtot[4][C];
+  __shared__ uint32_t segbits[4][C];  // per cluster, which tokens of each 32-token segment route to it
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int t0 = blockIdx.x * kPlaceTok;
   const int first = blockIdx.x * (kPlaceTok / kRouteTok);  // this block's first route block
+  // every global load first: the token's ids and weights (threads < kPlaceTok), the histograms
+  const int tok = t0 + tid;
+  const bool own = tid < kPlaceTok && tok < T;
+  int cs[K];
+  float ws[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    cs[j] = (own && j < k) ? ids[(int64_t)tok * k + j] : -1;
+    ws[j] = (own && j < k) ? w[(int64_t)tok * k + j] : 0.0f;
+  }
   {
-    // thread: clusters 4 (tid % VPR) .. +3 of rows tid / VPR + RPP i, 16-byte loads all in flight
+    // thread: clusters 4 (tid % VPR) .. +3 of rows tid / VPR + RPP i
     const int c0 = 4 * (tid % VPR), r0 = tid / VPR;
     int4 bef = make_int4(0, 0, 0, 0), tot = make_int4(0, 0, 0, 0);
-#pragma unroll 8
+#pragma unroll 16
     for (int b = r0; b < nblk; b += RPP) {
       const int4 v = *reinterpret_cast<const int4*>(hist + (int64_t)b * C + c0);
       tot.x += v.x;
@@ -863,19 +872,13 @@ __global__ void __launch_bounds__(256) pack_place_kernel(const int32_t* __restri
     unsigned long long m[MW];
 #pragma unroll
     for (int q = 0; q < MW; ++q) m[q] = 0ull;
-    const int t = t0 + tid;
-    if (t < T) {
-      int cs[K];  // all k loads in flight
 #pragma unroll
-      for (int j = 0; j < K; ++j) cs[j] = j < k ? ids[(int64_t)t * k + j] : -1;
+    for (int j = 0; j < K; ++j)
+      if (cs[j] >= 0) {
 #pragma unroll
-      for (int j = 0; j < K; ++j)
-        if (cs[j] >= 0) {
-#pragma unroll
-          for (int q = 0; q < MW; ++q)
-            if ((cs[j] >> 6) == q) m[q] |= 1ull << (cs[j] & 63);
-        }
-    }
+        for (int q = 0; q < MW; ++q)
+          if ((cs[j] >> 6) == q) m[q] |= 1ull << (cs[j] & 63);
+      }
 #pragma unroll
     for (int q = 0; q < MW; ++q) mask[tid][q] = m[q];
   }
@@ -914,35 +917,27 @@ __global__ void __launch_bounds__(256) pack_place_kernel(const int32_t* __restri
     }
     if (blockIdx.x == 0 && lane == 63) offsets[C] = s;
   }
-  // per cluster, the earlier tokens of this wave's 32-token segment routed to it
+  // wave w: per cluster, the bit mask of the tokens of segment w routed to it (independent
+  // broadcast reads of the route masks)
   for (int c = lane; c < C; c += 64) {
-    int run = 0;
-    for (int r = 0; r < SEG; ++r) {
-      const int t = wave * SEG + r;
-      pre[t][c] = (unsigned short)run;
-      run += (int)((mask[t][c >> 6] >> (c & 63)) & 1ull);
-    }
-    segtot[wave][c] = run;
+    uint32_t bits = 0u;
+#pragma unroll
+    for (int r = 0; r < SEG; ++r) bits |= (uint32_t)((mask[wave * SEG + r][c >> 6] >> (c & 63)) & 1ull) << r;
+    segbits[wave][c] = bits;
   }
   __syncthreads();
   // one thread per token writes its k slots: cluster base + earlier segments + earlier tokens
-  if (tid < kPlaceTok && t0 + tid < T) {
-    const int t = t0 + tid, sg = tid / SEG;
-    int cs[K];
-    float ws[K];
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
-      cs[j] = j < k ? ids[(int64_t)t * k + j] : 0;
-      ws[j] = j < k ? w[(int64_t)t * k + j] : 0.0f;
-    }
+  if (own) {
+    const int sg = tid / SEG, r = tid % SEG;
+    const uint32_t below = (1u << r) - 1u;
 #pragma unroll
     for (int j = 0; j < K; ++j)
       if (j < k) {
-        const int64_t p = (int64_t)t * k + j;
+        const int64_t p = (int64_t)tok * k + j;
         const int c = cs[j];
-        int slot = base[c] + pre[tid][c];
-        for (int q = 0; q < sg; ++q) slot += segtot[q][c];
-        tok_of_slot[slot] = t;
+        int slot = base[c] + __popc(segbits[sg][c] & below);
+        for (int q = 0; q < sg; ++q) slot += __popc(segbits[q][c]);
+        tok_of_slot[slot] = tok;
         pair_of_slot[slot] = (int32_t)p;
         slot_of_pair[p] = slot;
         w_of_slot[slot] = ws[j];
