@@ -499,6 +499,14 @@ int rte_audit_sample_fixed(const float* entropy, const int64_t* recipe_ids, cons
                            float alpha, float beta, float gamma, float residual, float coverage_min, float* req,
                            float* incl, void* mask, float* stats, void* stream);
 int rte_count_ema(const int64_t* ids, const void* mask, int n, float* ema, int R, float beta, void* stream);
+/* nonfinite: bad[0] = 1 when x[0] is inf or NaN, else 0; ok[0] = 1 - bad[0] (the optimizer's
+ * skip flag and the "stepped" metric of rte/training.py:445-468 without a host read).
+ * step_metrics (one workgroup): out f32 [4] = mean(hot) / scale, mean(corr) / scale,
+ * mean(corr) / seq, mean(depth) over B samples (the metric keys hot_lm_loss, corrected_lm_loss,
+ * nll_per_token, avg_depth of rte/training.py:1412-1472). */
+int rte_nonfinite(const float* x, float* bad, float* ok, void* stream);
+int rte_step_metrics(const float* hot, const float* corr, const int64_t* depth, int B, float scale, float seq,
+                     float* out, void* stream);
 
 /* ---- fused AdamW step with the trainer's per-group norms (replaces torch.optim.AdamW.step,
  *      clip_grad_norm_ and _optimizer_grad_metrics of rte/training.py:385-468) ----

@@ -8,6 +8,8 @@
 //     stats   = mean(incl), mean(req), count / B, count, mean(incl)
 //   count_ema (rte/recipes.py update_usage, rte/audit.py coverage update):
 //     counts[r] = #{i : ids[i] == r and mask[i]};  ema = ema beta + (1 - beta) counts / max(sum counts, 1)
+//   nonfinite (the step's skip test on the loss, rte/training.py:445-468) and step_metrics (the
+//     per-sample means of rte/training.py:1412-1472: hot / corrected loss, nll per token, depth)
 //
 // Row sums run in a fixed order (per-thread row strides, then an LDS tree); the counts are
 // integer LDS atomics, exact in any order.
@@ -97,6 +99,38 @@ __global__ void __launch_bounds__(kBkThreads)
   for (int r = t; r < R; r += kBkThreads) ema[r] = ema[r] * beta + (1.0f - beta) * ((float)cnt[r] / den);
 }
 
+// bad = 1 when x[0] is not finite (inf or NaN), else 0; ok = 1 - bad
+__global__ void nonfinite_kernel(const float* x, float* bad, float* ok) {
+  if (threadIdx.x == 0) {
+    const float v = x[0];
+    const float b = (v - v) != 0.0f || v != v ? 1.0f : 0.0f;  // inf - inf and NaN are NaN
+    bad[0] = b;
+    ok[0] = 1.0f - b;
+  }
+}
+
+// out = mean(hot) / scale, mean(corr) / scale, mean(corr) / seq, mean(depth)
+__global__ void __launch_bounds__(kBkThreads)
+    step_metrics_kernel(const float* hot, const float* corr, const int64_t* depth, int B, float scale, float seq,
+                        float* out) {
+  __shared__ float red[kBkThreads];
+  const int t = threadIdx.x;
+  float sh = 0.0f, sc = 0.0f, sd = 0.0f;
+  for (int b = t; b < B; b += kBkThreads) {
+    sh += hot[b];
+    sc += corr[b];
+    sd += (float)depth[b];
+  }
+  const float th = bk_block_sum(sh, red), tc = bk_block_sum(sc, red), td = bk_block_sum(sd, red);
+  if (t == 0) {
+    const float mh = th / (float)B, mc = tc / (float)B;
+    out[0] = mh / scale;
+    out[1] = mc / scale;
+    out[2] = mc / seq;
+    out[3] = td / (float)B;
+  }
+}
+
 }  // namespace
 
 }  // namespace rte
@@ -125,6 +159,20 @@ int rte_count_ema(const int64_t* ids, const void* mask, int n, float* ema, int R
   hipLaunchKernelGGL(count_ema_kernel, dim3(1), dim3(kBkThreads), 0, static_cast<hipStream_t>(stream), ids,
                      static_cast<const uint8_t*>(mask), n, ema, R, beta);
   return check_launch("count_ema");
+}
+
+int rte_nonfinite(const float* x, float* bad, float* ok, void* stream) {
+  RTE_REQUIRE(x && bad && ok, "nonfinite: null argument");
+  hipLaunchKernelGGL(nonfinite_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), x, bad, ok);
+  return check_launch("nonfinite");
+}
+
+int rte_step_metrics(const float* hot, const float* corr, const int64_t* depth, int B, float scale, float seq,
+                     float* out, void* stream) {
+  RTE_REQUIRE(B >= 1 && hot && corr && depth && out, "step_metrics: bad arguments");
+  hipLaunchKernelGGL(step_metrics_kernel, dim3(1), dim3(kBkThreads), 0, static_cast<hipStream_t>(stream), hot, corr,
+                     depth, B, scale, seq, out);
+  return check_launch("step_metrics");
 }
 
 }  // extern "C"

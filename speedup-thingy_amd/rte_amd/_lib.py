@@ -115,6 +115,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_router_aux_bwd": (_I, [_P, _P, _P, _I, _I, _F, _F, _P, _P, _P]),
     "rte_audit_sample_fixed": (_I, [_P, _P, _P, _P, _I, _I, _I] + [_F] * 8 + [_P, _P, _P, _P, _P]),
     "rte_count_ema": (_I, [_P, _P, _I, _P, _I, _F, _P]),
+    "rte_nonfinite": (_I, [_P, _P, _P, _P]),
+    "rte_step_metrics": (_I, [_P, _P, _P, _I, _F, _F, _P, _P]),
     "rte_mse_workspace_bytes": (_SZ, [_I64]),
     "rte_mse_fwd": (_I, [_P, _P, _I64, _P, _P, _SZ, _P]),
     "rte_mse_bwd": (_I, [_P, _P, _I64, _P, _P, _P, _P]),

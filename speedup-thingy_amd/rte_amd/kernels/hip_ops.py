@@ -1386,6 +1386,27 @@ def count_ema(ids, mask, ema, beta: float) -> None:
     call("rte_count_ema", ptr(i), ptr(m), i.numel(), ptr(ema), ema.numel(), float(beta), _s())
 
 
+def nonfinite_flags(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(bad, ok) fp32 scalars: bad = 1 when the scalar x is inf or NaN, else 0; ok = 1 - bad."""
+    _lib.require_device_tensors("nonfinite", x)
+    xc = x.detach().reshape(1).contiguous().to(F32)
+    out = torch.empty((2,), dtype=F32, device=x.device)
+    call("rte_nonfinite", ptr(xc), ptr(out), ptr(out[1:]), _s())
+    return out[0], out[1]
+
+
+def step_metrics(hot_lps, corr_lps, depths, *, scale: float, seq: float) -> torch.Tensor:
+    """fp32 [4] = mean(hot) / scale, mean(corr) / scale, mean(corr) / seq, mean(depth)."""
+    _lib.require_device_tensors("step_metrics", hot_lps, corr_lps, depths)
+    B = hot_lps.numel()
+    h = hot_lps.detach().reshape(B).contiguous().to(F32)
+    c = corr_lps.detach().reshape(B).contiguous().to(F32)
+    d = depths.detach().reshape(B).contiguous().to(torch.int64)
+    out = torch.empty((4,), dtype=F32, device=h.device)
+    call("rte_step_metrics", ptr(h), ptr(c), ptr(d), B, float(scale), float(seq), ptr(out), _s())
+    return out
+
+
 def audit_correct(hot_tok, exact_tok, idx, p, *, clip=None, grad_corrected=True):
     """(corrected per-sample loss [B], exact per-sample loss [A], stats [4] = residual mean, std,
     var, corrected metric loss) from token losses hot_tok [B, S] and exact_tok [A, S]."""

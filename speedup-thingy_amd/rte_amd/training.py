@@ -308,13 +308,15 @@ class TrainEngine:
 
     def _macro_metrics(self, loss, hot, audit, aux, scale, targets, shortlist, stepped):
         """rte/training.py:1412-1472 metric keys."""
+        m = hip_ops.step_metrics(hot.loss_per_sample, audit.corrected_loss_per_sample, hot.meta.depths, scale=scale,
+                                 seq=float(targets.shape[1]))
         return {
             "mode": "recursive_macro_shortlist" if shortlist else "recursive_macro",
             "loss": loss.detach(),
-            "hot_lm_loss": hot.loss_per_sample.detach().mean() / scale,
-            "corrected_lm_loss": audit.corrected_loss_per_sample.detach().mean() / scale,
-            "nll_per_token": audit.corrected_loss_per_sample.detach().mean() / float(targets.shape[1]),
-            "avg_depth": hot.meta.depths.float().mean(),
+            "hot_lm_loss": m[0],
+            "corrected_lm_loss": m[1],
+            "nll_per_token": m[2],
+            "avg_depth": m[3],
             "stepped": stepped,
             **{f"audit_{k}": v for k, v in audit.metrics.items()},
             **{f"macro_{k}": v.detach() for k, v in audit.macro_aux.items()},
@@ -441,13 +443,15 @@ class TrainEngine:
         loss, hot, audit, aux, scale = self._macro_loss(st["tokens"], st["targets"], shortlist=shortlist,
                                                         chosen=st["chosen"] if st["chosen"].numel() else None,
                                                         random_negs=st["rnd"])
-        bad = (~torch.isfinite(loss.detach())) if check_finite else torch.zeros((), dtype=torch.bool,
-                                                                                  device=loss.device)
+        if check_finite:  # skip flag and "stepped" metric in one launch, no host read
+            bad, ok = hip_ops.nonfinite_flags(loss)
+        else:
+            bad, ok = torch.zeros((), device=loss.device), torch.ones((), device=loss.device)
         loss.backward()
         self._bf16.end()  # parameters change below
         if isinstance(self.optimizer, FusedAdamW):
             # clipping, update (skipped on a non-finite loss) and metrics in three launches
-            self.optimizer.found_inf = bad.float()
+            self.optimizer.found_inf = bad
             try:
                 self.optimizer.step()
             finally:
@@ -458,7 +462,7 @@ class TrainEngine:
                 params = [p for g in self.optimizer.param_groups for p in g["params"]]
                 torch.nn.utils.clip_grad_norm_(params, tr.grad_clip_norm, foreach=True)
             self.last_grad_metrics = self._grad_metrics()
-            self.optimizer.found_inf = bad.float()
+            self.optimizer.found_inf = bad
             self.optimizer.grad_scale = None
             try:
                 self.optimizer.step()
@@ -467,7 +471,7 @@ class TrainEngine:
                 del self.optimizer.grad_scale
         self.optimizer.zero_grad(set_to_none=True)
         m.recipe_bank.update_usage(hot.meta.recipe_ids, beta=tr.coverage_beta)
-        metrics = self._macro_metrics(loss, hot, audit, aux, scale, st["targets"], shortlist, ~bad)
+        metrics = self._macro_metrics(loss, hot, audit, aux, scale, st["targets"], shortlist, ok)
         names = [k for k, v in metrics.items() if isinstance(v, torch.Tensor)]
         flat = torch.stack([metrics[k].detach().float().reshape(()) for k in names])
         return {"flat": flat, "names": names, "hot": hot, "audit": audit,

@@ -650,6 +650,23 @@ def test_audit_fixed_sampler_and_usage_ema_match_torch_formulas():
         np.testing.assert_allclose(_np(e), _np(ref_e), rtol=1e-6, atol=1e-8)
 
 
+def test_step_flags_and_metrics_match_torch():
+    """hip_ops.nonfinite_flags (the step's skip flag) on finite, inf, -inf and NaN losses, and
+    hip_ops.step_metrics against the torch means of the metric keys (rte/training.py:1412-1472)."""
+    from rte_amd.kernels import hip_ops
+
+    for v, want in ((1.5, 0.0), (float("inf"), 1.0), (float("-inf"), 1.0), (float("nan"), 1.0), (0.0, 0.0)):
+        bad, ok = hip_ops.nonfinite_flags(torch.tensor(v, device=DEV))
+        assert (bad.item(), ok.item()) == (want, 1.0 - want), v
+    g = torch.Generator().manual_seed(45)
+    hot = (torch.rand(300, generator=g) * 50).to(DEV)
+    corr = (torch.rand(300, generator=g) * 50).to(DEV)
+    depth = torch.randint(1, 5, (300,), generator=g).to(DEV)
+    m = hip_ops.step_metrics(hot, corr, depth, scale=64.0, seq=64.0)
+    ref = [hot.mean() / 64.0, corr.mean() / 64.0, corr.mean() / 64.0, depth.float().mean()]
+    np.testing.assert_allclose(_np(m), [float(r) for r in ref], rtol=1e-6)
+
+
 def test_router_backward_small_heads():
     """Gradients through the router's Linear layers (the depth head has 3 outputs, not a multiple
     of the GEMM's 8-element vectors) against fp64 autograd of the same modules on the CPU."""
