@@ -185,7 +185,8 @@ int rte_qkv_rope_fwd(const void* x, const void* wqkv, const float* cos_t, const 
                      void* stream);
 /* dq/dk/dv: [B,H,S,hd] bf16 with element strides s*[4] (innermost must be 1).
  * dqkv: [B*S, 3d] bf16 workspace (dq = NULL: dqkv is the input, already packed and rotated back
- * by rte_attention_bwd_qkv); dx [B*S, d] bf16; dw [3d, d] f32 (overwritten).
+ * by rte_attention_bwd_qkv); dx [B*S, d] bf16; dw [3d, d] f32 (overwritten; NULL: no weight
+ * gradient, for callers that form it in another layout).
  * workspace: split-K partials of dx and dw, max of rte_gemm_workspace_bytes(B*S, d, 3d) and
  * (3d, d, B*S) bytes (fewer bytes: fewer splits). */
 int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const int64_t* sk, const void* dv,

@@ -586,7 +586,7 @@ int rte_qkv_rope_bwd(const void* dq, const int64_t* sq, const void* dk, const in
     // few row tiles (short T): split the reduction in the workspace, as dW does after it
     RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
   }
-  {
+  if (dw) {
     // dW[c, :] = sum_t dqkv[t, c] x[t, :]
     GemmArgs p;
     p.M = 3 * d;

@@ -475,6 +475,11 @@ def qkv_rope(x, w, cos, sin, n_heads):
 
 # ----------------------------------------------------------------------------- attention output projection
 
+def _is_t_view(w: torch.Tensor) -> bool:
+    """w is a 2-D transposed view of contiguous memory (its gradient is formed in that layout)."""
+    return w.dim() == 2 and not w.is_contiguous() and w.t().is_contiguous()
+
+
 class AttnOutProjFn(torch.autograd.Function):
     """out = resid + y @ Wo^T where y is the [B, H, S, hd] attention output (any strides)."""
 
@@ -497,6 +502,7 @@ class AttnOutProjFn(torch.autograd.Function):
         ctx.save_for_backward(yb, wb)
         ctx.has_resid = resid is not None
         ctx.w_dtype = w.dtype
+        ctx.w_t = _is_t_view(w)
         B, H, S, hd = y.shape
         return out.view(B, S, N)
 
@@ -512,10 +518,17 @@ class AttnOutProjFn(torch.autograd.Function):
         layout, _, _ = _attn_layout(yb)
         L = torch.tensor(layout, dtype=torch.int64)
         Ld = torch.tensor([N, 0, 0, 0, 0], dtype=torch.int64)
-        dw = torch.empty((N, K), dtype=F32, device=yb.device)
-        wsp, wsn = _gemm_ws(N, K, T, yb.device)
-        call("rte_gemm_bf16_split", ptr(db), Ld.data_ptr(), 1, ptr(yb), L.data_ptr(), 1, ptr(dw), K, 1, N, K, T,
-             1.0, 0.0, None, 0, wsp, wsn, _s())
+        if ctx.w_t:  # w is a transposed view: dW^T [K, N] = y^T dout, returned as its transpose
+            dwt = torch.empty((K, N), dtype=F32, device=yb.device)
+            wsp, wsn = _gemm_ws(K, N, T, yb.device)
+            call("rte_gemm_bf16_split", ptr(yb), L.data_ptr(), 1, ptr(db), Ld.data_ptr(), 1, ptr(dwt), N, 1, K, N, T,
+                 1.0, 0.0, None, 0, wsp, wsn, _s())
+            dw = dwt.t()
+        else:
+            dw = torch.empty((N, K), dtype=F32, device=yb.device)
+            wsp, wsn = _gemm_ws(N, K, T, yb.device)
+            call("rte_gemm_bf16_split", ptr(db), Ld.data_ptr(), 1, ptr(yb), L.data_ptr(), 1, ptr(dw), K, 1, N, K, T,
+                 1.0, 0.0, None, 0, wsp, wsn, _s())
         dy4 = dy.view(B, S, H, hd).transpose(1, 2)
         dres = dout if ctx.has_resid else None
         return dy4, dw.to(ctx.w_dtype), dres
@@ -600,7 +613,7 @@ class QKVRopeAttentionFn(torch.autograd.Function):
         call("rte_attention_fwd", ptr(q), ptr(k), ptr(v), B, n_heads, S, hd, scale, ptr(hs), ptr(out), ptr(lse),
              _s())
         ctx.save_for_backward(xb, wb, cs, sn, q, k, v, out, lse, hs)
-        ctx.meta = (B, S, n_heads, hd, scale, x.dtype, w.dtype)
+        ctx.meta = (B, S, n_heads, hd, scale, x.dtype, w.dtype, _is_t_view(w))
         ctx.set_materialize_grads(False)
         return out.transpose(1, 2)
 
@@ -609,17 +622,19 @@ class QKVRopeAttentionFn(torch.autograd.Function):
         if dout is None:
             return (None,) * 6
         xb, wb, cs, sn, q, k, v, out, lse, hs = ctx.saved_tensors
-        B, S, H, hd, scale, x_dt, w_dt = ctx.meta
+        B, S, H, hd, scale, x_dt, w_dt, w_t = ctx.meta
         d = H * hd
         dtok = dout.transpose(1, 2).to(BF16).contiguous()  # token-major [B, S, H, hd]
         dqkv = torch.empty((B * S, 3 * d), dtype=BF16, device=xb.device)
         call("rte_attention_bwd_qkv", ptr(q), ptr(k), ptr(v), ptr(out), ptr(dtok), ptr(lse), B, H, S, hd, scale,
              ptr(hs), ptr(cs), ptr(sn), ptr(dqkv), _s())
         dx = torch.empty((B * S, d), dtype=BF16, device=xb.device)
-        dw = torch.empty((3 * d, d), dtype=F32, device=xb.device)
+        dw = None if w_t else torch.empty((3 * d, d), dtype=F32, device=xb.device)
         wsp, wsn = _gemm_ws_max(xb.device, (3 * d, d, B * S), (B * S, d, 3 * d))
         call("rte_qkv_rope_bwd", None, None, None, None, None, None, ptr(xb), ptr(wb), ptr(cs), ptr(sn), B, S, H, hd,
              ptr(dqkv), ptr(dx), ptr(dw), wsp, wsn, _s())
+        if w_t:  # w is a transposed view: dW^T [d, 3d] = x^T dqkv, returned as its transpose
+            dw = gemm(xb.reshape(B * S, d), dqkv, a_t=True, b_t=True, out_f32=True).t()
         return dx.view(B, S, d).to(x_dt), dw.to(w_dt), None, None, None, None
 
 
