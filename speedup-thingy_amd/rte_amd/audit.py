@@ -122,6 +122,11 @@ class AuditEngine:
             launch.streams.append(side)
         if self.config.lambda_cons != 0.0:
             side = self._side_stream(h0.device, 1)
+            mac = model.macro
+            if (getattr(mac, "v", None) is not None and mac._fused_bounded()
+                    and hip_ops.macro_fused_supported(mac.v, mac.u)):
+                # one bf16 copy of the operator tables per step, shared with the hot path
+                hip_ops.macro_fused_weights_share(mac.v, mac.u, side)
             side.wait_stream(main)
             with torch.cuda.stream(side):
                 launch.cons = model.macro.consistency_loss(h0, h0, route.recipe_id)

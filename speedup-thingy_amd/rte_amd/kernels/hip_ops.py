@@ -1629,6 +1629,18 @@ def macro_fused_weights(v: torch.Tensor, u: torch.Tensor):
     return out
 
 
+def macro_fused_weights_share(v, u, stream) -> None:
+    """Make this step's fused-operator weight copies (macro_fused_weights) on the current stream
+    and let `stream` read the same copies; `stream` must wait on the current stream before it
+    uses them.  Outside a per-step cache it does nothing."""
+    if not (_BF16_CACHE_ON[0] and isinstance(v, torch.nn.Parameter) and isinstance(u, torch.nn.Parameter)):
+        return
+    out = macro_fused_weights(v, u)
+    _BF16_CACHE[("macro_fused", v.data_ptr(), v._version, u.data_ptr(), u._version, stream.cuda_stream)] = out
+    for t in out:
+        t.record_stream(stream)
+
+
 class _MacroCall:
     """Buffers of one fused operator application (forward outputs saved for the backward).
     Per-sample buffers may be views into larger ones shared by two applications."""
