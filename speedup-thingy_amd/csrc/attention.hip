@@ -14,6 +14,7 @@
 //   forward  S^T = K Q^T, O^T += V^T P^T      (lane = query: row max / sum are one xor-32 step)
 //   dQ       S^T = K Q^T, dP^T = V dO^T, dQ^T += K^T dS^T            (lane = query)
 //   dK, dV   S = Q K^T, dP = dO V^T, dV^T += dO^T P, dK^T += Q^T dS   (lane = key)
+// The backward is one launch: each wave forms dK, dV of its key block, then dQ of its query block.
 // The score registers of a lane are fed back as the MFMA operand of the second product
 // directly: a 32x32 MFMA output register r of lane l holds row 8(r/4) + 4(l/32) + r%4, so the
 // 8 registers 8t..8t+7 of half h hold rows 16t + 4h + {0..3, 8..11}; the other operand reads
@@ -248,19 +249,18 @@ __global__ void __launch_bounds__(256) attn_fwd_kernel(const bf16* __restrict__ 
   }
 }
 
-// dQ of one 32-query block: loop over the key blocks up to the diagonal.
+// dQ of one 32-query block (wave task `task`): loop over the key blocks up to the diagonal.
+// blk: the wave's [32][pitch] LDS block.
 template <int HD>
-__global__ void __launch_bounds__(256) attn_bwd_dq_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
-                                                          const bf16* __restrict__ v, const bf16* __restrict__ out,
-                                                          const bf16* __restrict__ dout,
-                                                          const float* __restrict__ lse, int BH, int H, int S,
-                                                          float c2, float scale, const float* __restrict__ hscale,
-                                                          BwdOut o) {
-  constexpr int KS = HD / 16, NB = HD / 32, P = pitch<HD>();
-  __shared__ __align__(16) bf16 ksm[4][32 * P];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l32 = lane & 31, hf = lane >> 5;
+__device__ __forceinline__ void attn_bwd_dq_task(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                 const bf16* __restrict__ v, const bf16* __restrict__ out,
+                                                 const bf16* __restrict__ dout, const float* __restrict__ lse,
+                                                 int BH, int H, int S, float c2, float scale,
+                                                 const float* __restrict__ hscale, const BwdOut& o, int task,
+                                                 bf16* blk) {
+  constexpr int KS = HD / 16, NB = HD / 32;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, hf = lane >> 5;
   const int nqb = (S + 31) / 32;
-  const int task = blockIdx.x * 4 + wave;
   const int bh = task / nqb, qb = task - bh * nqb;
   if (bh >= BH) return;
   const int b = bh / H, h = bh - b * H;
@@ -285,7 +285,6 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_kernel(const bf16* __restrict
   for (int r = 0; r < 16; ++r)
 #pragma unroll
     for (int db = 0; db < NB; ++db) acc[db][r] = 0.0f;
-  bf16* blk = ksm[wave];
   const int g1 = (lane >> 4) & 1;
   const int kend = S < q0 + 32 ? S : q0 + 32;
   for (int kb0 = 0; kb0 < kend; kb0 += 32) {
@@ -333,21 +332,18 @@ __global__ void __launch_bounds__(256) attn_bwd_dq_kernel(const bf16* __restrict
   }
 }
 
-// dK, dV of one 32-key block: loop over the query blocks from the diagonal on.
+// dK, dV of one 32-key block (wave task `task`): loop over the query blocks from the diagonal on.
+// qblk, dblk: the wave's two [32][pitch] LDS blocks.
 template <int HD>
-__global__ void __launch_bounds__(256) attn_bwd_dkdv_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
-                                                            const bf16* __restrict__ v,
-                                                            const bf16* __restrict__ out,
-                                                            const bf16* __restrict__ dout,
-                                                            const float* __restrict__ lse, int BH, int H, int S,
-                                                            float c2, float scale, const float* __restrict__ hscale,
-                                                            BwdOut o) {
+__device__ __forceinline__ void attn_bwd_dkdv_task(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                   const bf16* __restrict__ v, const bf16* __restrict__ out,
+                                                   const bf16* __restrict__ dout, const float* __restrict__ lse,
+                                                   int BH, int H, int S, float c2, float scale,
+                                                   const float* __restrict__ hscale, const BwdOut& o, int task,
+                                                   bf16* qblk, bf16* dblk) {
   constexpr int KS = HD / 16, NB = HD / 32, P = pitch<HD>();
-  __shared__ __align__(16) bf16 qsm[4][32 * P];
-  __shared__ __align__(16) bf16 dsm[4][32 * P];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, l32 = lane & 31, hf = lane >> 5;
+  const int lane = threadIdx.x & 63, l32 = lane & 31, hf = lane >> 5;
   const int nkb = (S + 31) / 32;
-  const int task = blockIdx.x * 4 + wave;
   const int bh = task / nkb, kb = task - bh * nkb;
   if (bh >= BH) return;
   const int b = bh / H, h = bh - b * H;
@@ -368,8 +364,6 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_kernel(const bf16* __restri
   for (int r = 0; r < 16; ++r)
 #pragma unroll
     for (int db = 0; db < NB; ++db) dva[db][r] = dka[db][r] = 0.0f;
-  bf16* qblk = qsm[wave];
-  bf16* dblk = dsm[wave];
   const int g1 = (lane >> 4) & 1;
   for (int qb = kb; qb < nkb; ++qb) {
     const int q0 = qb * 32;
@@ -430,6 +424,25 @@ __global__ void __launch_bounds__(256) attn_bwd_dkdv_kernel(const bf16* __restri
   }
 }
 
+// The whole backward in one launch: wave task t (a (b, h) and a 32-row block) first forms dK, dV
+// of key block t, then dQ of query block t (the dQ pass reuses the first LDS block).  A wave's
+// two loops together visit nb + 1 score blocks for every block index, so long sequences balance.
+template <int HD>
+__global__ void __launch_bounds__(256) attn_bwd_kernel(const bf16* __restrict__ q, const bf16* __restrict__ k,
+                                                       const bf16* __restrict__ v, const bf16* __restrict__ out,
+                                                       const bf16* __restrict__ dout, const float* __restrict__ lse,
+                                                       int BH, int H, int S, float c2, float scale,
+                                                       const float* __restrict__ hscale, BwdOut o) {
+  constexpr int P = pitch<HD>();
+  __shared__ __align__(16) bf16 qsm[4][32 * P];
+  __shared__ __align__(16) bf16 dsm[4][32 * P];
+  const int wave = threadIdx.x >> 6;
+  const int task = blockIdx.x * 4 + wave;
+  attn_bwd_dkdv_task<HD>(q, k, v, out, dout, lse, BH, H, S, c2, scale, hscale, o, task, qsm[wave], dsm[wave]);
+  wave_lds_fence();  // the dQ pass overwrites the wave's first block
+  attn_bwd_dq_task<HD>(q, k, v, out, dout, lse, BH, H, S, c2, scale, hscale, o, task, qsm[wave]);
+}
+
 bool al16a(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace
@@ -455,12 +468,9 @@ int launch_attn_bwd(const bf16* q, const bf16* k, const bf16* v, const bf16* out
                     hipStream_t s) {
   const int64_t tasks = (int64_t)BH * ((S + 31) / 32);
   const dim3 grid((unsigned)((tasks + 3) / 4));
-  hipLaunchKernelGGL(attn_bwd_dkdv_kernel<HD>, grid, dim3(256), 0, s, q, k, v, out, dout, lse, BH, H, S,
-                     scale * kLog2e, scale, hscale, o);
-  RTE_TRY(check_launch("attention_bwd_dkdv"));
-  hipLaunchKernelGGL(attn_bwd_dq_kernel<HD>, grid, dim3(256), 0, s, q, k, v, out, dout, lse, BH, H, S,
-                     scale * kLog2e, scale, hscale, o);
-  return check_launch("attention_bwd_dq");
+  hipLaunchKernelGGL(attn_bwd_kernel<HD>, grid, dim3(256), 0, s, q, k, v, out, dout, lse, BH, H, S, scale * kLog2e,
+                     scale, hscale, o);
+  return check_launch("attention_bwd");
 }
 
 int attn_bwd_dispatch(const bf16* q, const bf16* k, const bf16* v, const bf16* out, const bf16* dout,
