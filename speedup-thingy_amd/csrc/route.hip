@@ -407,16 +407,26 @@ __global__ void __launch_bounds__(64) route_topk_lanes_kernel(const float* __res
 // LDS, so the counts run over all (b, j) at once and each cluster's ranks over the samples
 // alone; a recipe that lists a cluster twice drops back to the (b, j) scan of the general
 // plan.
+// With `fused` (few pairs: the host checked that offsets and ranks fit in LDS beside the tables)
+// the same workgroup then writes every pair's slot, as pack_routes_write_kernel does.
 __global__ void __launch_bounds__(256) pack_routes_plan_kernel(const int64_t* __restrict__ rid,
                                                                const uint8_t* __restrict__ active, int B, int S,
                                                                const int32_t* __restrict__ routes, int R, int kmax,
                                                                int C, int32_t* __restrict__ offsets,
-                                                               int32_t* __restrict__ base, int fast) {
-  extern __shared__ int32_t sh[];  // cnt [C]; fast: inv [R * C], recipe [B]
+                                                               int32_t* __restrict__ base, int fast, int fused,
+                                                               const float* __restrict__ route_w,
+                                                               int32_t* __restrict__ tok_of_slot,
+                                                               int32_t* __restrict__ pair_of_slot,
+                                                               int32_t* __restrict__ slot_of_pair,
+                                                               float* __restrict__ w_of_slot) {
+  // cnt [C]; fast: inv [R * C], recipe [B]; fused: offsets [C + 1], ranks [B * kmax]
+  extern __shared__ int32_t sh[];
   __shared__ int dup;
   int32_t* cnt = sh;
   int32_t* inv = sh + C;
   int32_t* rec = inv + (fast ? R * C : 0);
+  int32_t* offs = rec + (fast ? B : 0);
+  int32_t* ranks = offs + (C + 1);
   const int tid = threadIdx.x, lane = tid & 63;
   auto recipe_of = [&](int b) -> int {  // recipe of sample b, -1 when it routes nowhere
     const int64_t r = rid[b];
@@ -463,10 +473,16 @@ __global__ void __launch_bounds__(256) pack_routes_plan_kernel(const int64_t* __
         const int y = __shfl_up(incl, off, 64);
         if (lane >= off) incl += y;
       }
-      if (c < C) offsets[c] = (carry + incl - v) * S;
+      if (c < C) {
+        offsets[c] = (carry + incl - v) * S;
+        if (fused) offs[c] = (carry + incl - v) * S;
+      }
       carry += __shfl(incl, 63, 64);
     }
-    if (lane == 0) offsets[C] = carry * S;
+    if (lane == 0) {
+      offsets[C] = carry * S;
+      if (fused) offs[C] = carry * S;
+    }
   }
   if (fast && !dup) {  // dup was settled before the barrier above
     for (int c = tid; c < C; c += 256) {  // samples in order: rank among the cluster's samples
@@ -475,7 +491,10 @@ __global__ void __launch_bounds__(256) pack_routes_plan_kernel(const int64_t* __
         const int rc = rec[b];
         if (rc < 0) continue;
         const int j = inv[rc * C + c];
-        if (j >= 0) base[b * kmax + j] = r++;
+        if (j >= 0) {
+          if (fused) ranks[b * kmax + j] = r;
+          base[b * kmax + j] = r++;
+        }
       }
     }
   } else {
@@ -486,9 +505,30 @@ __global__ void __launch_bounds__(256) pack_routes_plan_kernel(const int64_t* __
         if (rc < 0) continue;
         const int32_t* rr = routes + (int64_t)rc * kmax;
         for (int j = 0; j < kmax; ++j)
-          if (rr[j] == c) base[b * kmax + j] = r++;
+          if (rr[j] == c) {
+            if (fused) ranks[b * kmax + j] = r;
+            base[b * kmax + j] = r++;
+          }
       }
     }
+  }
+  if (!fused) return;
+  __syncthreads();
+  const int P = B * S * kmax;
+  for (int p = tid; p < P; p += 256) {
+    const int t = p / kmax, j = p - t * kmax;
+    const int b = t / S, s = t - b * S;
+    const int rc = recipe_of(b);
+    const int c = rc >= 0 ? routes[rc * kmax + j] : -1;
+    if (c < 0 || c >= C) {
+      if (slot_of_pair) slot_of_pair[p] = -1;
+      continue;
+    }
+    const int slot = offs[c] + ranks[b * kmax + j] * S + s;
+    if (tok_of_slot) tok_of_slot[slot] = t;
+    if (pair_of_slot) pair_of_slot[slot] = p;
+    if (slot_of_pair) slot_of_pair[p] = slot;
+    if (w_of_slot) w_of_slot[slot] = route_w ? route_w[rc] : 1.0f;
   }
 }
 
@@ -1100,10 +1140,16 @@ int pack_routes(const int64_t* rid, const uint8_t* active, int B, int S, const i
   int32_t* base = static_cast<int32_t*>(ws);
   const size_t fast_lds = ((size_t)C + (size_t)R * C + (size_t)B) * sizeof(int32_t);
   const int fast = fast_lds <= 65536 ? 1 : 0;
-  hipLaunchKernelGGL(pack_routes_plan_kernel, dim3(1), dim3(256), fast ? fast_lds : (size_t)C * sizeof(int32_t), s,
-                     rid, active, B, S, routes, R, kmax, C, offsets, base, fast);
-  RTE_TRY(check_launch("pack_routes_plan"));
+  const size_t plan_lds = fast ? fast_lds : (size_t)C * sizeof(int32_t);
   const int P = B * S * kmax;
+  // few pairs: the plan's workgroup writes the slots too (one launch)
+  const size_t fused_lds = plan_lds + ((size_t)C + 1 + (size_t)B * kmax) * sizeof(int32_t);
+  const int fused = (P <= 16384 && fused_lds <= 65536) ? 1 : 0;
+  hipLaunchKernelGGL(pack_routes_plan_kernel, dim3(1), dim3(256), fused ? fused_lds : plan_lds, s, rid, active, B, S,
+                     routes, R, kmax, C, offsets, base, fast, fused, route_w, tok_of_slot, pair_of_slot, slot_of_pair,
+                     w_of_slot);
+  RTE_TRY(check_launch("pack_routes_plan"));
+  if (fused) return 0;
   hipLaunchKernelGGL(pack_routes_write_kernel, dim3((P + 255) / 256), dim3(256), 0, s, rid, active, B, S, routes, R,
                      kmax, route_w, C, offsets, base, tok_of_slot, pair_of_slot, slot_of_pair, w_of_slot);
   return check_launch("pack_routes_write");
