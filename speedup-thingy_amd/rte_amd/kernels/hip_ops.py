@@ -475,6 +475,49 @@ def qkv_rope(x, w, cos, sin, n_heads):
 
 # ----------------------------------------------------------------------------- attention output projection
 
+class SharedWGrad:
+    """Gradient of one weight used by several calls of one forward (the recursive passes of a
+    banked core): every call's backward hands over its input rows X_t and output-gradient rows
+    dY_t, and the last one to arrive forms sum_t dY_t^T X_t as one GEMM over the concatenated
+    rows (instead of one GEMM per call and autograd's adds); the other calls return no weight
+    gradient.  The order of the rows is the order the backward calls arrive in, fixed for a
+    given graph, so results repeat bitwise.  Every registered call must run its backward."""
+
+    def __init__(self):
+        self.uses = 0
+        self.arrived = 0
+        self.items: list[tuple[torch.Tensor, torch.Tensor]] = []
+
+    def register(self) -> None:
+        self.uses += 1
+
+    def add(self, x2d: torch.Tensor | None, dy2d: torch.Tensor | None, transposed: bool):
+        """Stores (x2d [T, K], dy2d [T, N]) (bf16; None for a call whose output got no gradient);
+        returns the weight gradient fp32 ([N, K], or a transposed view of a contiguous [K, N] when
+        `transposed`) once every call is in, else None."""
+        self.arrived += 1
+        if x2d is not None:
+            self.items.append((x2d, dy2d))
+        if self.arrived < self.uses:
+            if self.arrived == 1:  # a backward that leaves some calls out would lose their part
+                torch.autograd.Variable._execution_engine.queue_callback(self._check_drained)
+            return None
+        items, self.items, self.arrived = self.items, [], 0  # a second backward over the graph starts again
+        if not items:
+            return None
+        xs = torch.cat([x for x, _ in items]) if len(items) > 1 else items[0][0]
+        dys = torch.cat([dy for _, dy in items]) if len(items) > 1 else items[0][1]
+        if transposed:
+            return gemm(xs, dys, a_t=True, b_t=True, out_f32=True).t()
+        return gemm(dys, xs, a_t=True, b_t=True, out_f32=True)
+
+    def _check_drained(self) -> None:
+        if self.arrived:
+            n, self.arrived, self.items = self.arrived, 0, []
+            raise RuntimeError(f"SharedWGrad: the backward reached {n} of the {self.uses} calls sharing a weight; "
+                               "differentiate through every call of the forward")
+
+
 def _is_t_view(w: torch.Tensor) -> bool:
     """w is a 2-D transposed view of contiguous memory (its gradient is formed in that layout)."""
     return w.dim() == 2 and not w.is_contiguous() and w.t().is_contiguous()
@@ -484,7 +527,7 @@ class AttnOutProjFn(torch.autograd.Function):
     """out = resid + y @ Wo^T where y is the [B, H, S, hd] attention output (any strides)."""
 
     @staticmethod
-    def forward(ctx, y: torch.Tensor, w: torch.Tensor, resid: torch.Tensor | None):
+    def forward(ctx, y: torch.Tensor, w: torch.Tensor, resid: torch.Tensor | None, wgrad: SharedWGrad | None = None):
         _lib.require_device_tensors("attn_out_proj", y, w, resid)
         yb = y.to(BF16)
         if yb.stride(-1) != 1:
@@ -503,6 +546,9 @@ class AttnOutProjFn(torch.autograd.Function):
         ctx.has_resid = resid is not None
         ctx.w_dtype = w.dtype
         ctx.w_t = _is_t_view(w)
+        ctx.wgrad = wgrad if (wgrad is not None and ctx.needs_input_grad[1]) else None
+        if ctx.wgrad is not None:
+            ctx.wgrad.register()
         B, H, S, hd = y.shape
         return out.view(B, S, N)
 
@@ -518,6 +564,11 @@ class AttnOutProjFn(torch.autograd.Function):
         layout, _, _ = _attn_layout(yb)
         L = torch.tensor(layout, dtype=torch.int64)
         Ld = torch.tensor([N, 0, 0, 0, 0], dtype=torch.int64)
+        dy4 = dy.view(B, S, H, hd).transpose(1, 2)
+        dres = dout if ctx.has_resid else None
+        if ctx.wgrad is not None:  # token-major rows of y (its memory order) for the shared gradient
+            dw = ctx.wgrad.add(yb.transpose(1, 2).reshape(T, K), db, ctx.w_t)
+            return dy4, (None if dw is None else dw.to(ctx.w_dtype)), dres, None
         if ctx.w_t:  # w is a transposed view: dW^T [K, N] = y^T dout, returned as its transpose
             dwt = torch.empty((K, N), dtype=F32, device=yb.device)
             wsp, wsn = _gemm_ws(K, N, T, yb.device)
@@ -529,13 +580,11 @@ class AttnOutProjFn(torch.autograd.Function):
             wsp, wsn = _gemm_ws(N, K, T, yb.device)
             call("rte_gemm_bf16_split", ptr(db), Ld.data_ptr(), 1, ptr(yb), L.data_ptr(), 1, ptr(dw), K, 1, N, K, T,
                  1.0, 0.0, None, 0, wsp, wsn, _s())
-        dy4 = dy.view(B, S, H, hd).transpose(1, 2)
-        dres = dout if ctx.has_resid else None
-        return dy4, dw.to(ctx.w_dtype), dres
+        return dy4, dw.to(ctx.w_dtype), dres, None
 
 
-def attn_out_proj(y, w, resid=None):
-    return AttnOutProjFn.apply(y, w, resid)
+def attn_out_proj(y, w, resid=None, wgrad: SharedWGrad | None = None):
+    return AttnOutProjFn.apply(y, w, resid, wgrad)
 
 
 # ----------------------------------------------------------------------------- attention core
@@ -589,7 +638,7 @@ class QKVRopeAttentionFn(torch.autograd.Function):
     Values and gradients equal QKVRopeFn followed by AttentionFn bit for bit."""
 
     @staticmethod
-    def forward(ctx, x, w, cos, sin, n_heads: int, head_scale):
+    def forward(ctx, x, w, cos, sin, n_heads: int, head_scale, wgrad: SharedWGrad | None = None):
         B, S, d = x.shape
         hd = d // n_heads
         _check_rope_tables(cos, sin, S, hd)
@@ -614,13 +663,17 @@ class QKVRopeAttentionFn(torch.autograd.Function):
              _s())
         ctx.save_for_backward(xb, wb, cs, sn, q, k, v, out, lse, hs)
         ctx.meta = (B, S, n_heads, hd, scale, x.dtype, w.dtype, _is_t_view(w))
+        ctx.wgrad = wgrad if (wgrad is not None and ctx.needs_input_grad[1]) else None
+        if ctx.wgrad is not None:
+            ctx.wgrad.register()
         ctx.set_materialize_grads(False)
         return out.transpose(1, 2)
 
     @staticmethod
     def backward(ctx, dout):
         if dout is None:
-            return (None,) * 6
+            dw = ctx.wgrad.add(None, None, ctx.meta[7]) if ctx.wgrad is not None else None
+            return None, (None if dw is None else dw.to(ctx.meta[6])), None, None, None, None, None
         xb, wb, cs, sn, q, k, v, out, lse, hs = ctx.saved_tensors
         B, S, H, hd, scale, x_dt, w_dt, w_t = ctx.meta
         d = H * hd
@@ -629,20 +682,24 @@ class QKVRopeAttentionFn(torch.autograd.Function):
         call("rte_attention_bwd_qkv", ptr(q), ptr(k), ptr(v), ptr(out), ptr(dtok), ptr(lse), B, H, S, hd, scale,
              ptr(hs), ptr(cs), ptr(sn), ptr(dqkv), _s())
         dx = torch.empty((B * S, d), dtype=BF16, device=xb.device)
-        dw = None if w_t else torch.empty((3 * d, d), dtype=F32, device=xb.device)
+        shared = ctx.wgrad is not None
+        dw = None if (w_t or shared) else torch.empty((3 * d, d), dtype=F32, device=xb.device)
         wsp, wsn = _gemm_ws_max(xb.device, (3 * d, d, B * S), (B * S, d, 3 * d))
         call("rte_qkv_rope_bwd", None, None, None, None, None, None, ptr(xb), ptr(wb), ptr(cs), ptr(sn), B, S, H, hd,
              ptr(dqkv), ptr(dx), ptr(dw), wsp, wsn, _s())
-        if w_t:  # w is a transposed view: dW^T [d, 3d] = x^T dqkv, returned as its transpose
+        if shared:
+            dw = ctx.wgrad.add(xb.reshape(B * S, d), dqkv, w_t)
+        elif w_t:  # w is a transposed view: dW^T [d, 3d] = x^T dqkv, returned as its transpose
             dw = gemm(xb.reshape(B * S, d), dqkv, a_t=True, b_t=True, out_f32=True).t()
-        return dx.view(B, S, d).to(x_dt), dw.to(w_dt), None, None, None, None
+        return dx.view(B, S, d).to(x_dt), (None if dw is None else dw.to(w_dt)), None, None, None, None, None
 
 
-def qkv_rope_attention(x, w, cos, sin, n_heads, head_scale=None):
-    """[B, H, S, hd] view of the token-major attention output of x's fused QKV + RoPE."""
+def qkv_rope_attention(x, w, cos, sin, n_heads, head_scale=None, wgrad: SharedWGrad | None = None):
+    """[B, H, S, hd] view of the token-major attention output of x's fused QKV + RoPE; wgrad (optional)
+    shares one weight-gradient GEMM among the calls of a forward that use w."""
     if head_scale is not None and head_scale.requires_grad:
         raise ValueError("qkv_rope_attention: head_scale carries no gradient")
-    return QKVRopeAttentionFn.apply(x, w, cos, sin, n_heads, head_scale)
+    return QKVRopeAttentionFn.apply(x, w, cos, sin, n_heads, head_scale, wgrad)
 
 
 # ----------------------------------------------------------------------------- dense SwiGLU

@@ -474,17 +474,19 @@ class BankedAttention(nn.Module):
             return (self.wqkv.squeeze(0).t(),), (self.wo.squeeze(0).t(),)
         return tuple(w.t() for w in self.wqkv.unbind(0)), tuple(w.t() for w in self.wo.unbind(0))
 
-    def forward_scaled(self, x: torch.Tensor, head_scale: torch.Tensor, banks=None) -> torch.Tensor:
-        """x [B, S, d], head_scale [B, attn_banks, n_heads] -> fp32 [B, S, d]."""
+    def forward_scaled(self, x: torch.Tensor, head_scale: torch.Tensor, banks=None, wgrads=None) -> torch.Tensor:
+        """x [B, S, d], head_scale [B, attn_banks, n_heads] -> fp32 [B, S, d].  wgrads (optional):
+        per bank (qkv, out) hip_ops.SharedWGrad of the passes sharing these weights."""
         cos, sin = self._tables()
         H = self.config.n_heads
         wqkv_t, wo_t = banks if banks is not None else self.bank_weights()
         out = None
         for bank in range(self.config.attn_banks):
+            gq, go = wgrads[bank] if wgrads is not None else (None, None)
             # the recipe's head mask (1/|banks| on its heads, 0 elsewhere: rte/layers.py:702-730 runs
             # only the active heads and averages the banks) scales each head's attention output
-            y = hip_ops.qkv_rope_attention(x, wqkv_t[bank], cos, sin, H, head_scale[:, bank, :])
-            out = hip_ops.attn_out_proj(y, wo_t[bank], out)
+            y = hip_ops.qkv_rope_attention(x, wqkv_t[bank], cos, sin, H, head_scale[:, bank, :], wgrad=gq)
+            out = hip_ops.attn_out_proj(y, wo_t[bank], out, wgrad=go)
         return out
 
     def forward(self, x: torch.Tensor, spec: RecipeSpec) -> torch.Tensor:
@@ -597,7 +599,10 @@ class BankedRecursiveCore(nn.Module):
         backward instead of a zero-fill and copy per pass)."""
         per_pass = tuple(p.unbind(0) for p in (self.pass_gamma1, self.pass_beta1, self.pass_gamma2,
                                                 self.pass_beta2, self.pass_attn_scale, self.pass_mlp_scale))
-        return {"pool": self.mlp.pool_weights(), "pass": per_pass, "attn": self.attn.bank_weights()}
+        # one shared weight-gradient GEMM per attention weight over every pass of this forward
+        wgrads = [(hip_ops.SharedWGrad(), hip_ops.SharedWGrad()) for _ in range(self.config.attn_banks)]
+        return {"pool": self.mlp.pool_weights(), "pass": per_pass, "attn": self.attn.bank_weights(),
+                "attn_wgrad": wgrads}
 
     def _step(self, h, h0, head_scale, ids, w, pass_idx: int, weights=None, active=None, recipe_ids=None):
         """One pass: three fused residual / FiLM-norm launches around attention and the pool
@@ -608,7 +613,7 @@ class BankedRecursiveCore(nn.Module):
         h = h.float()
         h_tilde, n1 = hip_ops.axpy_norm(h, None if self.alpha_inj is None else h0.float(), self.alpha_inj,
                                         self.norm1.weight, g1, b1, self.norm1.eps)
-        attn = self.attn.forward_scaled(n1, head_scale, weights.get("attn"))
+        attn = self.attn.forward_scaled(n1, head_scale, weights.get("attn"), weights.get("attn_wgrad"))
         u, n2 = hip_ops.axpy_norm(h_tilde, attn, sa, self.norm2.weight, g2, b2, self.norm2.eps)
         if recipe_ids is not None:  # per-sample recipes: pack the routes straight from the ids
             mlp = self.mlp.forward_recipes(n2, recipe_ids, active, weights["pool"])

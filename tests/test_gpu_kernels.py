@@ -1046,3 +1046,50 @@ def test_qkv_rope_attention_fused_matches_two_nodes(B, S, H, hd, scaled):
     assert torch.equal(y1, y2)
     assert torch.equal(x1.grad, x2.grad)
     assert torch.equal(w1.grad, w2.grad)
+
+
+@pytest.mark.parametrize("transposed", [False, True])
+def test_shared_weight_gradient_over_passes(transposed):
+    """Three recursive passes through one attention weight pair: the shared weight gradient (one
+    GEMM over every pass's rows, formed by the last backward call) equals the per-pass gradients
+    summed by autograd (fp32 accumulation in another order: tolerance 1e-5 relative), inputs'
+    gradients bit for bit, and a backward that reaches only some of the passes raises."""
+    H_ = _ops()
+    B, S, Hn, hd, T = 2, 64, 4, 32, 3  # the strided out-proj reads need power-of-two S
+    d = Hn * hd
+    g = torch.Generator().manual_seed(7 + transposed)
+    x0 = torch.randn(B, S, d, generator=g).to(DEV)
+    wq0 = (torch.randn(3 * d, d, generator=g) / d ** 0.5).to(DEV)
+    wo0 = (torch.randn(d, d, generator=g) / d ** 0.5).to(DEV)
+    pos = torch.arange(S, dtype=torch.float32)[:, None]
+    inv = 10000.0 ** (-torch.arange(0, hd, 2, dtype=torch.float32) / hd)
+    ang = (pos * inv).repeat_interleave(2, dim=1)
+    cos, sin = ang.cos().to(DEV), ang.sin().to(DEV)
+    gy = torch.randn(B, S, d, generator=g).to(DEV)
+    print(f"shared weight gradient transposed={transposed}", flush=True)
+
+    def run(shared, upto=T):
+        x = x0.clone().requires_grad_()
+        pq = (wq0.t().contiguous() if transposed else wq0.clone()).requires_grad_()
+        po = (wo0.t().contiguous() if transposed else wo0.clone()).requires_grad_()
+        wq, wo = (pq.t(), po.t()) if transposed else (pq, po)
+        gq, go = (H_.SharedWGrad(), H_.SharedWGrad()) if shared else (None, None)
+        h, hs = x, []
+        for _ in range(T):
+            y = H_.qkv_rope_attention(h, wq, cos, sin, Hn, None, wgrad=gq)
+            h = H_.attn_out_proj(y, wo, h, wgrad=go)
+            hs.append(h)
+        (hs[upto - 1] * gy).sum().backward()
+        return hs[-1], x.grad, pq.grad, po.grad
+
+    h1, dx1, dq1, do1 = run(False)
+    h2, dx2, dq2, do2 = run(True)
+    assert torch.equal(h1, h2)
+    assert torch.equal(dx1, dx2)
+    assert dq2.is_contiguous() and do2.is_contiguous()
+    assert_rel(_np(dq2), _np(dq1), FP32_RTOL, "dWqkv")
+    assert_rel(_np(do2), _np(do1), FP32_RTOL, "dWo")
+    h3, dx3, dq3, do3 = run(True)  # repeats bit for bit
+    assert torch.equal(dq2, dq3) and torch.equal(do2, do3)
+    with pytest.raises(RuntimeError, match="SharedWGrad"):
+        run(True, upto=1)
