@@ -422,10 +422,10 @@ int rte_macro_fused_sum(const float* part, int n, float inv_n, float* out, void*
 int rte_macro_fused_bwd(const float* dout_p, const float* dout_q, const float* g, float mul, int nsplit,
                         const float* dout, const float* h, const float* rstd, const void* x2, int B_h,
                         const int64_t* key, int B, int seq, int d, int n_keys, const float* a, const void* sa,
-                        const void* v_b, const void* v2_t, const void* u_b, const void* u_t, const float* gain,
-                        const float* bias, const float* scale, float c, void* du, void* da, float* part_tab,
-                        float* part_da, float* dh, float* dh0, int dh0_into_dh, const float* extra, int n_extra,
-                        void* da_sum, void* workspace, size_t workspace_bytes, void* stream);
+                        const void* v_b, const void* vc_t, const void* v2_t, const void* u_b, const void* u_t,
+                        const float* gain, const float* bias, const float* scale, float c, void* du, void* da,
+                        float* part_tab, float* part_da, float* dh, float* dh0, int dh0_into_dh, const float* extra,
+                        int n_extra, void* da_sum, void* workspace, size_t workspace_bytes, void* stream);
 int rte_macro_fused_wgrad(const int64_t* key, int B0, int B_h0, int B1, int B_h1, int seq, int d, int n_keys,
                           const void* x2, const void* sa, const void* du, const void* da, const void* pooled,
                           const void* da_sum, const float* part_tab, float* du_w, float* dv_w, float* dgain,

@@ -453,12 +453,13 @@ __global__ void __launch_bounds__(256) mf_sum_kernel(const float* __restrict__ p
 // Tile blockIdx.x (32 rows) of sample blockIdx.y:
 //   du (bf16), table column sums part_tab[b][tile][3][d] = (du h | du | dout c tanh),
 //   da = (du @ U^T) silu'(a) (bf16) and its column sums part_da[b][tile],
-//   rd[row]  = <da @ V1^T, h_row>            (the row-local part of the rmsnorm dot)
+//   rd[row]  = <da @ V1^T, h_row> = da_row . (x2[:, :d] @ V1) / rstd   (the row-local part of the
+//              rmsnorm dot, from the bf16 normalised rows as the pooled part below)
 //   xv2[row] = h_row @ V2 = (x2[:, :d] @ V2) / rstd   (the pooled part's per-row factor)
 __global__ void __launch_bounds__(256) mf_bwd_a_kernel(DoutDesc dd, const float* __restrict__ h,
                                                        const float* __restrict__ rstd, const bf16* __restrict__ x2,
                                                        int Bh, int S, int d, const int64_t* __restrict__ key, int G,
-                                                       const float* __restrict__ a_buf, const bf16* __restrict__ Vb,
+                                                       const float* __restrict__ a_buf, const bf16* __restrict__ VcT,
                                                        const bf16* __restrict__ V2T, const bf16* __restrict__ UT,
                                                        const bf16* __restrict__ Ub, const float* __restrict__ gain,
                                                        const float* __restrict__ bias, const float* __restrict__ scale,
@@ -468,7 +469,6 @@ __global__ void __launch_bounds__(256) mf_bwd_a_kernel(DoutDesc dd, const float*
   __shared__ float al[kTile][kRank + 1];
   __shared__ __align__(16) bf16 sal[kTile][kPitch];
   __shared__ __align__(16) bf16 dul[4][kTile][kPitch];
-  __shared__ __align__(16) bf16 dal[kTile][kPitch];
   __shared__ float red[4][kTile][kRank + 1];
   __shared__ float rdw[4][kTile];
   __shared__ float rs[kTile];
@@ -555,7 +555,6 @@ __global__ void __launch_bounds__(256) mf_bwd_a_kernel(DoutDesc dd, const float*
     const float dav = row < nrow ? v * sg * (1.0f + av * (1.0f - sg)) : 0.0f;
     const bf16 db = f2bf(dav);
     if (row < nrow) da_buf[(b * S + s0 + row) * kRank + n] = db;
-    dal[row][n] = db;
     al[row][n] = dav;  // only this thread reads or writes element (row, n) here
   }
   __syncthreads();
@@ -564,38 +563,27 @@ __global__ void __launch_bounds__(256) mf_bwd_a_kernel(DoutDesc dd, const float*
     for (int row = 0; row < kTile; ++row) s += al[row][tid];
     part_da[(b * T + tile) * kRank + tid] = s;
   }
-  // rd: <da @ V1^T, h> per row over the wave's column blocks, then the 4 waves in order
-  {
-    const bf16* lp = &dal[lane & 31][8 * (lane >> 5)];
-    const bf16x8_v d0 = ld8b(lp), d1 = ld8b(lp + 16);
-    float rp[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) rp[r] = 0.0f;
-    for (int cb = wave; cb < d / 32; cb += 4) {
-      const int col = cb * 32 + (lane & 31);
-      const bf16* vp = Vb + (k * 3 * d + col) * kRank + 8 * (lane >> 5);
-      float xv[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) xv[r] = hs[acc_row_ld(r, lane, 0, nrow) * d + col];
-      f32x16_v acc = zero16();
-      acc = mfma16(d0, ld8b(vp), acc);
-      acc = mfma16(d1, ld8b(vp + 16), acc);
-#pragma unroll
-      for (int r = 0; r < 16; ++r) rp[r] += acc[r] * xv[r];
-    }
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const float v = half_sum(rp[r]);
-      if ((lane & 31) == 0) rdw[wave][acc_row(r, lane)] = v;
-    }
-  }
-  // xv2 = x2[:, :d] @ V2 (wave w: quarter w of the d-long products)
+  // xv2 = x2[:, :d] @ V2 and xv1 = x2[:, :d] @ V1 (wave w: quarter w of the d-long products);
+  // the wave's rd part is da_row . xv1 over its quarter (the 4 quarters are added in order)
   {
     int rl = lane & 31;
     if (rl >= nrow) rl = nrow - 1;
     const int kq = wave * (d / 4);
     const bf16* ap = x2 + (src * S + s0 + rl) * 2 * d + kq + 8 * (lane >> 5);
     const bf16* bp = V2T + (k * kRank + (lane & 31)) * d + kq + 8 * (lane >> 5);
+    const bf16* cp = VcT + (k * kRank + (lane & 31)) * 2 * d + kq + 8 * (lane >> 5);
+    {  // one accumulator at a time (register budget)
+      f32x16_v acc1 = zero16();
+      for (int kk = 0; kk < d / 4; kk += 32) {
+        acc1 = mfma16(ld8b(ap + kk), ld8b(cp + kk), acc1);
+        acc1 = mfma16(ld8b(ap + kk + 16), ld8b(cp + kk + 16), acc1);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {  // rows past the tile have da = 0
+        const float v = half_sum(acc1[r] * al[acc_row(r, lane)][lane & 31]);
+        if ((lane & 31) == 0) rdw[wave][acc_row(r, lane)] = v;
+      }
+    }
     f32x16_v acc = zero16();
     for (int kk = 0; kk < d / 4; kk += 32) {
       const bf16x8_v a0 = ld8b(ap + kk), a1 = ld8b(ap + kk + 16);
@@ -614,7 +602,7 @@ __global__ void __launch_bounds__(256) mf_bwd_a_kernel(DoutDesc dd, const float*
     const float v = ((red[0][row][n] + red[1][row][n]) + red[2][row][n]) + red[3][row][n];
     xv2_out[(b * S + s0 + row) * kRank + n] = v / rs[row];
   }
-  if (tid < nrow) rd_out[b * S + s0 + tid] = ((rdw[0][tid] + rdw[1][tid]) + rdw[2][tid]) + rdw[3][tid];
+  if (tid < nrow) rd_out[b * S + s0 + tid] = (((rdw[0][tid] + rdw[1][tid]) + rdw[2][tid]) + rdw[3][tid]) / rs[tid];
 }
 
 // LDS of mf_bwd_b_kernel for rep repeats
@@ -1039,8 +1027,9 @@ size_t macro_fused_bwd_workspace_bytes(int B, int S) {
 
 int macro_fused_bwd(const float* dp, const float* dq, const float* g, float mul, int nsplit, const float* dbuf,
                     const float* h, const float* rstd, const bf16* x2, int Bh, const int64_t* key, int B, int S, int d,
-                    int G, const float* a, const bf16* sa, const bf16* Vb, const bf16* V2T, const bf16* Ub,
-                    const bf16* UT, const float* gain, const float* bias, const float* scale, float c, bf16* du,
+                    int G, const float* a, const bf16* sa, const bf16* Vb, const bf16* VcT, const bf16* V2T,
+                    const bf16* Ub, const bf16* UT, const float* gain, const float* bias, const float* scale, float c,
+                    bf16* du,
                     bf16* da, float* part_tab, float* part_da, float* dh, float* dh0, int dh0_into_dh,
                     const float* extra, int n_extra, bf16* dsum, void* ws, size_t ws_bytes, hipStream_t s) {
   MF_SHAPES("macro_fused_bwd");
@@ -1055,7 +1044,7 @@ int macro_fused_bwd(const float* dp, const float* dq, const float* g, float mul,
   float* xv2 = static_cast<float*>(ws);
   float* rd = xv2 + (size_t)B * S * kRank;
   DoutDesc dd{dp, dq, g, mul, nsplit, dbuf};
-  hipLaunchKernelGGL(mf_bwd_a_kernel, dim3(T, B), dim3(256), 0, s, dd, h, rstd, x2, Bh, S, d, key, G, a, Vb, V2T, UT,
+  hipLaunchKernelGGL(mf_bwd_a_kernel, dim3(T, B), dim3(256), 0, s, dd, h, rstd, x2, Bh, S, d, key, G, a, VcT, V2T, UT,
                      Ub, gain, bias, scale, c, du, da, part_tab, part_da, rd, xv2);
   RTE_TRY(check_launch("macro_fused_bwd_a"));
   const size_t lds = bwd_b_lds(rep);

@@ -101,7 +101,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                  _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "rte_macro_fused_sum": (_I, [_P, _I, _F, _P, _P]),
     "rte_macro_fused_bwd": (_I, [_P, _P, _P, _F, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P,
-                                 _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _P, _I, _P, _P, _SZ, _P]),
+                                 _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _P, _I, _P, _P, _SZ, _P]),
     "rte_macro_fused_wgrad": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                    _P, _P, _SZ, _P]),
     "rte_attention_fwd": (_I, [_P, _P, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P]),

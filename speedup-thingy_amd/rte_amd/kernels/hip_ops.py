@@ -1731,8 +1731,8 @@ class _MacroCall:
         ws, nbytes = workspace(nb, self.h.device)
         call("rte_macro_fused_bwd", ptr(p), ptr(q), ptr(g), float(mul), int(nsplit), ptr(dout), ptr(self.h),
              ptr(self.rstd), ptr(self.x2), self.Bh, ptr(self.key), self.B, self.S, self.d, G, ptr(self.a),
-             ptr(self.sa), ptr(vb), ptr(v2t), ptr(ub), ptr(ut), ptr(tabs[0]), ptr(tabs[1]), ptr(tabs[2]), float(c),
-             ptr(du), ptr(da), ptr(part_tab), ptr(part_da), ptr(dh), ptr(dh0), int(dh0_into_dh), ptr(extra),
+             ptr(self.sa), ptr(vb), ptr(vct), ptr(v2t), ptr(ub), ptr(ut), ptr(tabs[0]), ptr(tabs[1]), ptr(tabs[2]),
+             float(c), ptr(du), ptr(da), ptr(part_tab), ptr(part_da), ptr(dh), ptr(dh0), int(dh0_into_dh), ptr(extra),
              int(n_extra), ptr(dsum), ws, nbytes, _s())
 
 
