@@ -169,7 +169,7 @@ def kernel_candidates(B: int, S: int):
         _lib.call("rte_grouped_swiglu_bwd", dpool.data_ptr(), x.data_ptr(), T, d, pk.offsets.data_ptr(), C, n, P,
                   pk.tok_of_slot.data_ptr(), pk.pair_of_slot.data_ptr(), pk.w_of_slot.data_ptr(), wug.data_ptr(),
                   wd.data_ptr(), F, ug.data_ptr(), zw.data_ptr(), dug.data_ptr(), dw_slot.data_ptr(),
-                  dx_pairs.data_ptr(), dwug.data_ptr(), dwd.data_ptr(), gs_ws.data_ptr(), gsb, st())
+                  dx_pairs.data_ptr(), dwug.data_ptr(), dwd.data_ptr(), 0, 0.0, gs_ws.data_ptr(), gsb, st())
 
     out_pool = torch.empty(T, d, device=dev, dtype=torch.float32)
 

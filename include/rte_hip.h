@@ -147,13 +147,18 @@ int rte_grouped_swiglu_fwd(const void* x, int T, int d, const int32_t* offsets, 
  *   dug     [P, 2n] bf16 (workspace-like output),
  *   dw_slot [P] f32    = <dout[t], y_unweighted>  (routing-weight gradient per slot),
  *   dx_pairs[T*k, d] bf16 in pair order (combine them for dx),
- *   dwug    [2*d_ff, d] f32 and dwd [d, ld_wd] f32 (overwritten; every neuron row is
- *           owned by exactly one cluster, so no reduction across clusters is needed). */
+ *   dwug    [2*d_ff, d] f32 and dwd [d, ld_wd] f32 (every neuron row is owned by exactly one
+ *           cluster, so no reduction across clusters is needed); with w_t = 1 their transposes
+ *           instead: dwug [d, 2*d_ff] (columns [up | gate]) and dwd [d_ff, d], the layouts of
+ *           weights whose transposes the kernel reads.  beta = 0 overwrites dwug / dwd, beta = 1
+ *           adds the gradients to what they hold (several uses of one weight summed in the
+ *           order of the calls, no separate adds). */
 int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const int32_t* offsets, int G,
                            int n, int P, const int32_t* tok_of_slot, const int32_t* pair_of_slot,
                            const float* w_of_slot, const void* wug, const void* wd, int64_t ld_wd,
                            const void* ug, const void* zw, void* dug, float* dw_slot, void* dx_pairs,
-                           float* dwug, float* dwd, void* workspace, size_t workspace_bytes, void* stream);
+                           float* dwug, float* dwd, int w_t, float beta, void* workspace, size_t workspace_bytes,
+                           void* stream);
 /* Workspace with which the per-cluster weight gradients of rte_grouped_swiglu_bwd are
  * reduced by several workgroups per cluster when routing is skewed (fixed chunk order, so
  * still deterministic).  NULL / too small: one workgroup column per cluster. */

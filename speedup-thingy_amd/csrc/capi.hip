@@ -328,8 +328,9 @@ int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const 
                            int P, const int32_t* tok_of_slot, const int32_t* pair_of_slot,
                            const float* w_of_slot, const void* wug, const void* wd, int64_t ld_wd, const void* ug,
                            const void* zw, void* dug, float* dw_slot, void* dx_pairs, float* dwug, float* dwd,
-                           void* workspace, size_t workspace_bytes, void* stream) {
+                           int w_t, float beta, void* workspace, size_t workspace_bytes, void* stream) {
   RTE_REQUIRE(n % 32 == 0 && n <= 128, "grouped_swiglu_bwd: n must be a multiple of 32 and <= 128");
+  RTE_REQUIRE(w_t == 0 || w_t == 1, "grouped_swiglu_bwd: w_t must be 0 or 1");
   RTE_REQUIRE(d % 8 == 0, "grouped_swiglu_bwd: d_model must be a multiple of 8");
   const int dff = G * n;
   const int tiles = P / kGroupTileM + G + 1;
@@ -375,7 +376,28 @@ int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const 
     p.epi.c_rows = pair_of_slot;
     RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
   }
-  {
+  if (w_t) {
+    // dWug^T[:, ilv(g*2n + c)] = sum_slot x[tok(slot), :] dUG[slot, c]   ([d, 2F]: columns [up F | gate F])
+    GemmArgs p;
+    p.mode = MODE_GROUP_K;
+    p.goff = offsets;
+    p.G = G;
+    p.M = d;
+    p.N = 2 * n;
+    p.K = P;
+    p.a = plain(x, d);
+    p.a.rows = tok_of_slot;
+    p.a_t = 1;
+    p.b = plain(dug, 2 * n);
+    p.b_t = 1;
+    p.epi.c = dwug;
+    p.epi.ldc = 2 * (int64_t)dff;
+    p.epi.c_f32 = 1;
+    p.epi.c_gstride = 2 * n;
+    p.epi.c_col_ilv = dff;
+    p.epi.beta = beta;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
+  } else {
     // dWug_g[c, :] = sum_slot dUG[slot, c] x[tok(slot), :]
     GemmArgs p;
     p.mode = MODE_GROUP_K;
@@ -394,9 +416,30 @@ int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const 
     p.epi.c_f32 = 1;
     p.epi.c_growstride = 2 * n;
     p.epi.c_ilv = dff;
+    p.epi.beta = beta;
     RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
   }
-  {
+  if (w_t) {
+    // dWd^T[g*n + j, :] = sum_slot zw[slot, j] dout[tok(slot), :]   ([F, d])
+    GemmArgs p;
+    p.mode = MODE_GROUP_K;
+    p.goff = offsets;
+    p.G = G;
+    p.M = n;
+    p.N = d;
+    p.K = P;
+    p.a = plain(zw, n);
+    p.a_t = 1;
+    p.b = plain(dout, d);
+    p.b.rows = tok_of_slot;
+    p.b_t = 1;
+    p.epi.c = dwd;
+    p.epi.ldc = d;
+    p.epi.c_f32 = 1;
+    p.epi.c_growstride = n;
+    p.epi.beta = beta;
+    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
+  } else {
     // dWd[:, g*n + j] = sum_slot dout[tok(slot), :] zw[slot, j]
     GemmArgs p;
     p.mode = MODE_GROUP_K;
@@ -414,6 +457,7 @@ int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const 
     p.epi.ldc = ld_wd;
     p.epi.c_f32 = 1;
     p.epi.c_gstride = n;
+    p.epi.beta = beta;
     RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
   }
   (void)T;

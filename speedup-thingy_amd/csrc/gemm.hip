@@ -216,8 +216,10 @@ __device__ __forceinline__ void store_chunk(const Epilogue& e, int g, int m, int
       for (int t = 0; t < nv; ++t) v[t] += rp[t];
     }
   }
+  // W-column chunks start at multiples of W and never cross a 32-column run of the interleave
+  const int64_t ocol = e.c_col_ilv ? ilv_row((int64_t)g * e.c_gstride + n, e.c_col_ilv) : (int64_t)g * e.c_gstride + n;
   if (e.c_f32) {
-    float* cp = reinterpret_cast<float*>(e.c) + (int64_t)g * e.c_gstride + orow * e.ldc + n;
+    float* cp = reinterpret_cast<float*>(e.c) + orow * e.ldc + ocol;
     if (vec && nv == W) {
 #pragma unroll
       for (int t = 0; t < W; t += 4) {
@@ -231,7 +233,7 @@ __device__ __forceinline__ void store_chunk(const Epilogue& e, int g, int m, int
       for (int t = 0; t < nv; ++t) cp[t] = v[t] + (e.beta != 0.0f ? e.beta * cp[t] : 0.0f);
     }
   } else {
-    bf16* cp = reinterpret_cast<bf16*>(e.c) + (int64_t)g * e.c_gstride + orow * e.ldc + n;
+    bf16* cp = reinterpret_cast<bf16*>(e.c) + orow * e.ldc + ocol;
     if (vec && nv == W && W == 8) {
       if (e.beta != 0.0f) {
         const uint4 o = *reinterpret_cast<const uint4*>(cp);
@@ -1410,7 +1412,9 @@ int gemm_launch(const GemmArgs& p, int epi_kind, hipStream_t stream, void* ws, s
     // no C with the RoPE outputs set: the split-K partials are stored as QKV by the reduce
     RTE_REQUIRE(e.c || (e.q && p.splits_forced), "gemm: null output");
     const int esz = e.c_f32 ? 4 : 2;
-    vec = aligned16(e.c) && (e.ldc * esz) % 16 == 0 && (e.c_gstride * esz) % 16 == 0;
+    vec = aligned16(e.c) && (e.ldc * esz) % 16 == 0 && (e.c_gstride * esz) % 16 == 0 &&
+          ((int64_t)e.c_col_ilv * esz) % 16 == 0;
+    RTE_REQUIRE(!e.c_col_ilv || (e.c_gstride % 32 == 0 && !e.c_ilv), "gemm: column interleave needs 32-column groups");
     if (e.resid) vec = vec && aligned16(e.resid) && e.ld_resid % 4 == 0;
   } else if (epi_kind == EPI_SWIGLU_FWD) {
     RTE_REQUIRE(aligned16(e.ug) && aligned16(e.z) && e.ld_ug % 8 == 0 && e.ld_z % 8 == 0,

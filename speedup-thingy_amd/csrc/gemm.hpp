@@ -51,6 +51,8 @@ struct Epilogue {
   int64_t c_growstride = 0;
   const int32_t* c_rows = nullptr;
   int32_t c_ilv = 0;                 // SwiGLU interleave of output rows (see Operand::ilv)
+  int32_t c_col_ilv = 0;             // SwiGLU interleave of output columns g * c_gstride + n (then
+                                     // c_gstride is a column offset per group, a multiple of 32)
   int c_f32 = 0;
   float alpha = 1.0f;
   float beta = 0.0f;

@@ -518,6 +518,41 @@ class SharedWGrad:
                                "differentiate through every call of the forward")
 
 
+class SharedGradAccum:
+    """Weight gradients of several calls of one forward summed in place: the first backward call
+    to arrive writes fresh buffers, every later one adds to them in its GEMM epilogue (in arrival
+    order, fixed for a given graph), and the last returns them (the others return no weight
+    gradient).  Every registered call must run its backward."""
+
+    def __init__(self):
+        self.uses = 0
+        self.arrived = 0
+        self.bufs = None
+
+    def register(self) -> None:
+        self.uses += 1
+
+    def arrive(self, make):
+        """-> (buffers, beta, last): make() allocates the buffers on the first arrival."""
+        first = self.arrived == 0
+        if first:
+            self.bufs = make()
+            if self.uses > 1:  # a backward that leaves some calls out would lose their part
+                torch.autograd.Variable._execution_engine.queue_callback(self._check_drained)
+        self.arrived += 1
+        bufs = self.bufs
+        last = self.arrived >= self.uses
+        if last:
+            self.arrived, self.bufs = 0, None  # a second backward over the graph starts again
+        return bufs, (0.0 if first else 1.0), last
+
+    def _check_drained(self) -> None:
+        if self.arrived:
+            n, self.arrived, self.bufs = self.arrived, 0, None
+            raise RuntimeError(f"SharedGradAccum: the backward reached {n} of the {self.uses} calls sharing a "
+                               "weight; differentiate through every call of the forward")
+
+
 def _is_t_view(w: torch.Tensor) -> bool:
     """w is a 2-D transposed view of contiguous memory (its gradient is formed in that layout)."""
     return w.dim() == 2 and not w.is_contiguous() and w.t().is_contiguous()
@@ -901,9 +936,12 @@ def _pool_fwd(xb, ids, w, wugb, wdb, C: int, n: int, resid, masked: bool, pk: Pa
     return out, pk, ug, zw
 
 
-def _pool_bwd(db, xb, wugb, wdb, pk, ug, zw, C: int, n: int, k: int):
+def _pool_bwd(db, xb, wugb, wdb, pk, ug, zw, C: int, n: int, k: int, dwug=None, dwd=None, w_t: bool = False,
+              beta: float = 0.0):
     """Backward of _pool_fwd up to the combine: (dx_pairs bf16 [P, d] in pair order,
-    dwug f32 [2F, d], dwd f32 [d, F], dw_slot f32 [P] = per-slot <z, dz>)."""
+    dwug f32 [2F, d], dwd f32 [d, F], dw_slot f32 [P] = per-slot <z, dz>).  w_t: the weight
+    gradients in the transposed layouts ([d, 2F], [F, d]); dwug / dwd given: written there
+    (beta = 1: added to what they hold)."""
     T, d = xb.shape
     F = C * n
     P = T * k
@@ -911,12 +949,14 @@ def _pool_bwd(db, xb, wugb, wdb, pk, ug, zw, C: int, n: int, k: int):
     dug = torch.empty((P, 2 * n), dtype=BF16, device=dev)
     dw_slot = torch.empty((P,), dtype=F32, device=dev)
     dxp = torch.empty((P, d), dtype=BF16, device=dev)
-    dwug = torch.empty((2 * F, d), dtype=F32, device=dev)
-    dwd = torch.empty((d, F), dtype=F32, device=dev)
+    if dwug is None:
+        dwug = torch.empty((d, 2 * F) if w_t else (2 * F, d), dtype=F32, device=dev)
+    if dwd is None:
+        dwd = torch.empty((F, d) if w_t else (d, F), dtype=F32, device=dev)
     ws, nb = workspace(_lib.load().rte_grouped_swiglu_bwd_workspace_bytes(P, C, n, d), dev)
     call("rte_grouped_swiglu_bwd", ptr(db), ptr(xb), T, d, ptr(pk.offsets), C, n, P, ptr(pk.tok_of_slot),
          ptr(pk.pair_of_slot), ptr(pk.w_of_slot), ptr(wugb), ptr(wdb), F, ptr(ug), ptr(zw), ptr(dug), ptr(dw_slot),
-         ptr(dxp), ptr(dwug), ptr(dwd), ws, nb, _s())
+         ptr(dxp), ptr(dwug), ptr(dwd), int(w_t), float(beta), ws, nb, _s())
     return dxp, dwug, dwd, dw_slot
 
 
@@ -995,7 +1035,7 @@ class GroupedPoolFn(torch.autograd.Function):
     operands: their gradients come back in fp32."""
 
     @staticmethod
-    def forward(ctx, x, ids, w, wug_t, wd_t, resid, n: int, pk=None):
+    def forward(ctx, x, ids, w, wug_t, wd_t, resid, n: int, pk=None, acc: "SharedGradAccum | None" = None):
         _lib.require_device_tensors("grouped_pool", x, ids, w, wug_t, wd_t, resid)
         shape = x.shape
         d = shape[-1]
@@ -1013,6 +1053,11 @@ class GroupedPoolFn(torch.autograd.Function):
         out, pk, ug, zw = _pool_fwd(xb, idc, wc, wugb, wdb, C, n, rs, masked=True, pk=pk)
         ctx.save_for_backward(xb, wugb, wdb, pk.offsets, pk.tok_of_slot, pk.pair_of_slot, pk.slot_of_pair,
                               pk.w_of_slot, ug, zw)
+        # weights that are transposed views get their gradients formed in their own layout
+        ctx.w_t = _is_t_view(wug_t) and _is_t_view(wd_t)
+        ctx.acc = acc if (acc is not None and ctx.needs_input_grad[3] and ctx.needs_input_grad[4]) else None
+        if ctx.acc is not None:
+            ctx.acc.register()
         ctx.meta = (shape, pk.k, C, n, resid is not None, x.dtype)
         return out.view(shape)
 
@@ -1021,16 +1066,29 @@ class GroupedPoolFn(torch.autograd.Function):
         xb, wugb, wdb, offsets, tok, pos, sop, wos, ug, zw = ctx.saved_tensors
         shape, k, C, n, has_resid, x_dt = ctx.meta
         T, d = xb.shape
+        F = C * n
         pk = PackIndex(offsets, tok, pos, sop, wos, C, k)
-        dxp, dwug, dwd, _ = _pool_bwd(cast_bf16(dout.reshape(T, d)), xb, wugb, wdb, pk, ug, zw, C, n, k)
+        w_t, dev = ctx.w_t, xb.device
+        bufs, beta, last = (None, None), 0.0, True
+        if ctx.acc is not None:
+            shapes = ((d, 2 * F), (F, d)) if w_t else ((2 * F, d), (d, F))
+            bufs, beta, last = ctx.acc.arrive(lambda: tuple(torch.empty(s_, dtype=F32, device=dev) for s_ in shapes))
+        dxp, dwug, dwd, _ = _pool_bwd(cast_bf16(dout.reshape(T, d)), xb, wugb, wdb, pk, ug, zw, C, n, k,
+                                      dwug=bufs[0], dwd=bufs[1], w_t=w_t, beta=beta)
         dx = combine_rows(dxp, T, k, out_f32=False, slot_of_pair=sop)
-        return dx.view(shape).to(x_dt), None, None, dwug, dwd, (dout if has_resid else None), None, None
+        if not last:
+            dwug = dwd = None
+        elif w_t:
+            dwug, dwd = dwug.t(), dwd.t()
+        return dx.view(shape).to(x_dt), None, None, dwug, dwd, (dout if has_resid else None), None, None, None
 
 
-def grouped_pool_swiglu(x, ids, w, wug_t, wd_t, n: int, resid=None, pk: PackIndex | None = None):
+def grouped_pool_swiglu(x, ids, w, wug_t, wd_t, n: int, resid=None, pk: PackIndex | None = None,
+                        acc: "SharedGradAccum | None" = None):
     """Grouped pool SwiGLU over the routes ids / w [T, k], or over a prebuilt pack pk (then ids
-    and w are not read)."""
-    return GroupedPoolFn.apply(x, ids, w, wug_t, wd_t, resid, n, pk)
+    and w are not read).  acc (optional): the calls of a forward that share these weights sum
+    their weight gradients in one pair of buffers."""
+    return GroupedPoolFn.apply(x, ids, w, wug_t, wd_t, resid, n, pk, acc)
 
 
 # ----------------------------------------------------------------------------- plain linear (LM head)

@@ -532,21 +532,23 @@ class BankedSwiGLU(nn.Module):
         wd_t = self.wd.permute(2, 0, 1).reshape(d, A * F_)
         return wug_t, wd_t
 
-    def forward_routes(self, x: torch.Tensor, ids: torch.Tensor, w: torch.Tensor, weights=None) -> torch.Tensor:
-        """x [B, S, d]; ids [B*S, kmax] int32 (-1 = no pair); w [B*S, kmax] fp32 -> fp32 [B, S, d]."""
+    def forward_routes(self, x: torch.Tensor, ids: torch.Tensor, w: torch.Tensor, weights=None,
+                       acc=None) -> torch.Tensor:
+        """x [B, S, d]; ids [B*S, kmax] int32 (-1 = no pair); w [B*S, kmax] fp32 -> fp32 [B, S, d].
+        acc: hip_ops.SharedGradAccum of the passes sharing the weights (optional)."""
         wug_t, wd_t = weights if weights is not None else self.pool_weights()
         slab = self.config.d_ff // self.config.ffn_groups
-        return hip_ops.grouped_pool_swiglu(x, ids, w, wug_t, wd_t, slab)
+        return hip_ops.grouped_pool_swiglu(x, ids, w, wug_t, wd_t, slab, acc=acc)
 
     def forward_recipes(self, x: torch.Tensor, recipe_ids: torch.Tensor, active: torch.Tensor | None = None,
-                        weights=None) -> torch.Tensor:
+                        weights=None, acc=None) -> torch.Tensor:
         """Every sample's tokens through its recipe's clusters (inactive samples: none), packed
         straight from the recipe ids (rte_pack_routes)."""
         wug_t, wd_t = weights if weights is not None else self.pool_weights()
         slab = self.config.d_ff // self.config.ffn_groups
         pk = hip_ops.pack_routes(recipe_ids, self.recipe_routes, self.recipe_route_w, x.shape[1],
                                  wug_t.shape[0] // 2 // slab, active)
-        return hip_ops.grouped_pool_swiglu(x, None, None, wug_t, wd_t, slab, pk=pk)
+        return hip_ops.grouped_pool_swiglu(x, None, None, wug_t, wd_t, slab, pk=pk, acc=acc)
 
     def routes_for(self, recipe_ids: torch.Tensor, seq: int, active: torch.Tensor | None = None):
         """Per-token routes of samples with recipe_ids [B] (inactive samples get none)."""
@@ -601,8 +603,9 @@ class BankedRecursiveCore(nn.Module):
                                                 self.pass_beta2, self.pass_attn_scale, self.pass_mlp_scale))
         # one shared weight-gradient GEMM per attention weight over every pass of this forward
         wgrads = [(hip_ops.SharedWGrad(), hip_ops.SharedWGrad()) for _ in range(self.config.attn_banks)]
+        # and one pair of pool weight-gradient buffers that every pass adds into
         return {"pool": self.mlp.pool_weights(), "pass": per_pass, "attn": self.attn.bank_weights(),
-                "attn_wgrad": wgrads}
+                "attn_wgrad": wgrads, "pool_wgrad": hip_ops.SharedGradAccum()}
 
     def _step(self, h, h0, head_scale, ids, w, pass_idx: int, weights=None, active=None, recipe_ids=None):
         """One pass: three fused residual / FiLM-norm launches around attention and the pool
@@ -616,9 +619,9 @@ class BankedRecursiveCore(nn.Module):
         attn = self.attn.forward_scaled(n1, head_scale, weights.get("attn"), weights.get("attn_wgrad"))
         u, n2 = hip_ops.axpy_norm(h_tilde, attn, sa, self.norm2.weight, g2, b2, self.norm2.eps)
         if recipe_ids is not None:  # per-sample recipes: pack the routes straight from the ids
-            mlp = self.mlp.forward_recipes(n2, recipe_ids, active, weights["pool"])
+            mlp = self.mlp.forward_recipes(n2, recipe_ids, active, weights["pool"], weights.get("pool_wgrad"))
         else:
-            mlp = self.mlp.forward_routes(n2, ids, w, weights["pool"])
+            mlp = self.mlp.forward_routes(n2, ids, w, weights["pool"], weights.get("pool_wgrad"))
         return hip_ops.axpy(u, mlp, sm, keep=h if active is not None else None, mask=active)
 
     def step_group(self, h, h0, spec: RecipeSpec, pass_idx: int = 0):

@@ -1093,3 +1093,47 @@ def test_shared_weight_gradient_over_passes(transposed):
     assert torch.equal(dq2, dq3) and torch.equal(do2, do3)
     with pytest.raises(RuntimeError, match="SharedWGrad"):
         run(True, upto=1)
+
+
+def test_grouped_pool_transposed_and_accumulated_weight_grads():
+    """Grouped pool SwiGLU used by three passes: weight gradients formed in the layout of
+    transposed-view weights (rte_grouped_swiglu_bwd w_t = 1) and summed in place across the
+    passes (beta = 1) equal the plain-layout per-pass gradients summed by autograd (fp32 sums in
+    another order: 1e-5 relative); inputs' gradients bit for bit; repeat runs bit for bit; a
+    backward that misses a pass raises."""
+    H = _ops()
+    rng = np.random.default_rng(5)
+    T, d, C, n, k, P_ = 512, 256, 16, 32, 4, 3
+    F = C * n
+    xs0 = [torch.from_numpy(rng.standard_normal((T, d)).astype(np.float32)).to(DEV) for _ in range(P_)]
+    ids = torch.from_numpy(np.stack([rng.permutation(C)[:k] for _ in range(T)]).astype(np.int32)).to(DEV)
+    ids[::7, -1] = -1  # absent pairs
+    w = torch.from_numpy(rng.random((T, k)).astype(np.float32)).to(DEV)
+    wug0 = (torch.from_numpy(rng.standard_normal((d, 2 * F)).astype(np.float32)) * 0.05).to(DEV)  # [d, 2F]
+    wd0 = (torch.from_numpy(rng.standard_normal((F, d)).astype(np.float32)) * 0.05).to(DEV)       # [F, d]
+    dys = [torch.from_numpy(rng.standard_normal((T, d)).astype(np.float32)).to(DEV) for _ in range(P_)]
+    print(f"grouped pool shared grads T={T} d={d} C={C} n={n} k={k}", flush=True)
+
+    def run(view, acc_on, upto=P_):
+        xs = [x.clone().requires_grad_() for x in xs0]
+        pu, pd = wug0.clone().requires_grad_(), wd0.clone().requires_grad_()
+        # view: transposed views of the parameters; else contiguous copies in the kernel layout
+        wug_t, wd_t = (pu.t(), pd.t()) if view else (pu.t().contiguous(), pd.t().contiguous())
+        acc = H.SharedGradAccum() if acc_on else None
+        outs = [H.grouped_pool_swiglu(x, ids, w, wug_t, wd_t, n, acc=acc) for x in xs]
+        sum((o * g).sum() for o, g in zip(outs[:upto], dys[:upto])).backward()
+        return [x.grad for x in xs], pu.grad, pd.grad
+
+    dx_ref, du_ref, dd_ref = run(False, False)
+    for view, acc_on in ((True, False), (True, True), (False, True)):
+        dx, du, dd = run(view, acc_on)
+        for a, b in zip(dx, dx_ref):
+            assert torch.equal(a, b)
+        assert du.is_contiguous() and dd.is_contiguous()
+        assert_rel(_np(du), _np(du_ref), FP32_RTOL, f"dwug view={view} acc={acc_on}")
+        assert_rel(_np(dd), _np(dd_ref), FP32_RTOL, f"dwd view={view} acc={acc_on}")
+    _, du1, dd1 = run(True, True)
+    _, du2, dd2 = run(True, True)
+    assert torch.equal(du1, du2) and torch.equal(dd1, dd2)
+    with pytest.raises(RuntimeError, match="SharedGradAccum"):
+        run(True, True, upto=2)
