@@ -621,7 +621,8 @@ __host__ __device__ constexpr size_t bwd_b_lds(int rep) {
 //   dh0 = sum_t da @ V3^T
 // With dh0_into_dh (h and h0 are one tensor) dh0 is added to dh; `extra` adds n_extra further
 // [Bh, S, d] blocks to dh (in block order).
-__global__ void __launch_bounds__(256) mf_bwd_b_kernel(DoutDesc dd, const float* __restrict__ h,
+template <bool INTO>
+__global__ void __launch_bounds__(256, INTO ? 3 : 2) mf_bwd_b_kernel(DoutDesc dd, const float* __restrict__ h,
                                                        const float* __restrict__ rstd, int Bh, int rep, int S, int d,
                                                        const int64_t* __restrict__ key, int G,
                                                        const bf16* __restrict__ da_buf, const bf16* __restrict__ sa_buf,
@@ -630,7 +631,7 @@ __global__ void __launch_bounds__(256) mf_bwd_b_kernel(DoutDesc dd, const float*
                                                        const bf16* __restrict__ Vb, const bf16* __restrict__ UT,
                                                        const float* __restrict__ gain, const float* __restrict__ bias,
                                                        const float* __restrict__ scale, float c, float* __restrict__ dh,
-                                                       float* __restrict__ dh0, int dh0_into_dh,
+                                                       float* __restrict__ dh0,
                                                        const float* __restrict__ extra, int n_extra,
                                                        bf16* __restrict__ dsum_out) {
   extern __shared__ __align__(16) unsigned char smem[];
@@ -648,13 +649,18 @@ __global__ void __launch_bounds__(256) mf_bwd_b_kernel(DoutDesc dd, const float*
   const float coef = dout_coef(dd);
   const float invS = 1.0f / (float)S;
   const float* hs = h + src * sd + (int64_t)s0 * d;
-  for (int e = tid; e < rep * kTile * kRank; e += 256) {
-    const int t = e / (kTile * kRank), row = (e >> 5) & (kTile - 1), n = e & 31;
+  // da / silu(a) tiles of every repeat: 16-byte pieces (8 of the 32 rank values; rows past the
+  // tile read the last valid row and store zeros)
+  for (int e = tid; e < rep * kTile * 4; e += 256) {
+    const int t = e / (kTile * 4), row = (e >> 2) & (kTile - 1), q = e & 3;
     const int64_t b = src + (int64_t)t * Bh;
-    const int64_t g = (b * S + s0 + (row < nrow ? row : nrow - 1)) * kRank + n;
-    const bf16 zb = 0;
-    dal[((size_t)t * kTile + row) * kPitch + n] = row < nrow ? da_buf[g] : zb;
-    sal[((size_t)t * kTile + row) * kPitch + n] = row < nrow ? sa_buf[g] : zb;
+    const int64_t g = (b * S + s0 + (row < nrow ? row : nrow - 1)) * kRank + 8 * q;
+    uint4 dv = *reinterpret_cast<const uint4*>(da_buf + g);
+    uint4 sv = *reinterpret_cast<const uint4*>(sa_buf + g);
+    if (row >= nrow) dv = sv = make_uint4(0u, 0u, 0u, 0u);
+    const size_t l = ((size_t)t * kTile + row) * kPitch + 8 * q;
+    *reinterpret_cast<uint4*>(dal + l) = dv;
+    *reinterpret_cast<uint4*>(sal + l) = sv;
   }
   for (int e = tid; e < rep * kRank; e += 256) {
     const int t = e >> 5, n = e & 31;
@@ -708,12 +714,12 @@ __global__ void __launch_bounds__(256) mf_bwd_b_kernel(DoutDesc dd, const float*
   __syncthreads();
   const int cl = wave * 32 + (lane & 31), col = c0 + cl;
   if (c0 + wave * 32 >= d) return;  // no barrier follows
-  float x[16], ah[16], ah0[16];
+  float x[16], ah[16], ah0[INTO ? 1 : 16];  // INTO: the h0 gradient goes straight into ah
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     x[r] = hs[acc_row_ld(r, lane, 0, nrow) * d + col];
     ah[r] = 0.0f;
-    ah0[r] = 0.0f;
+    if constexpr (!INTO) ah0[r] = 0.0f;
   }
   for (int t = 0; t < rep; ++t) {
     const int64_t b = src + (int64_t)t * Bh;
@@ -754,7 +760,13 @@ __global__ void __launch_bounds__(256) mf_bwd_b_kernel(DoutDesc dd, const float*
       dq = mfma16(a0, ld8b(wp), dq);
       dq = mfma16(a1, ld8b(wp + 16), dq);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ah0[r] += dq[r];
+      for (int r = 0; r < 16; ++r) {
+        if constexpr (INTO) {
+          ah[r] += dq[r];
+        } else {
+          ah0[r] += dq[r];
+        }
+      }
     }
   }
 #pragma unroll
@@ -763,10 +775,11 @@ __global__ void __launch_bounds__(256) mf_bwd_b_kernel(DoutDesc dd, const float*
     if (row >= nrow) continue;
     const int64_t off = src * sd + (int64_t)(s0 + row) * d + col;
     float v = ah[r];
-    if (dh0_into_dh) v += ah0[r];
     for (int e = 0; e < n_extra; ++e) v += extra[(int64_t)e * Bh * sd + off];
     dh[off] = v;
-    if (!dh0_into_dh && dh0) dh0[off] = ah0[r];
+    if constexpr (!INTO) {
+      if (dh0) dh0[off] = ah0[r];
+    }
   }
 }
 
@@ -1039,6 +1052,7 @@ int macro_fused_bwd(const float* dp, const float* dq, const float* g, float mul,
               "macro_fused_bwd: bad upstream-gradient description");
   RTE_REQUIRE(n_extra >= 0 && (n_extra == 0 || extra), "macro_fused_bwd: missing extra gradient blocks");
   RTE_REQUIRE(dh && dsum, "macro_fused_bwd: dh and dsum are required");
+  RTE_REQUIRE(al16(da) && al16(sa), "macro_fused_bwd: da and silu(a) must be 16-byte aligned");
   RTE_REQUIRE(ws && ws_bytes >= macro_fused_bwd_workspace_bytes(B, S), "macro_fused_bwd: workspace too small");
   const int T = macro_fused_tiles(S), rep = B / Bh;
   float* xv2 = static_cast<float*>(ws);
@@ -1048,9 +1062,13 @@ int macro_fused_bwd(const float* dp, const float* dq, const float* g, float mul,
                      Ub, gain, bias, scale, c, du, da, part_tab, part_da, rd, xv2);
   RTE_TRY(check_launch("macro_fused_bwd_a"));
   const size_t lds = bwd_b_lds(rep);
-  hipLaunchKernelGGL(mf_bwd_b_kernel, dim3(T, Bh, d / 128), dim3(256), lds, s, dd, h, rstd, Bh, rep, S, d, key, G, da,
-                     sa, part_da, T, rd, xv2, Vb, UT, gain, bias, scale, c, dh, dh0, dh0_into_dh, extra, n_extra,
-                     dsum);
+  if (dh0_into_dh)
+    hipLaunchKernelGGL(mf_bwd_b_kernel<true>, dim3(T, Bh, d / 128), dim3(256), lds, s, dd, h, rstd, Bh, rep, S, d, key,
+                       G, da, sa, part_da, T, rd, xv2, Vb, UT, gain, bias, scale, c, dh, dh0, extra, n_extra, dsum);
+  else
+    hipLaunchKernelGGL(mf_bwd_b_kernel<false>, dim3(T, Bh, d / 128), dim3(256), lds, s, dd, h, rstd, Bh, rep, S, d,
+                       key, G, da, sa, part_da, T, rd, xv2, Vb, UT, gain, bias, scale, c, dh, dh0, extra, n_extra,
+                       dsum);
   return check_launch("macro_fused_bwd_b");
 }
 
