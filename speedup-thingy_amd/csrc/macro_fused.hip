@@ -150,7 +150,6 @@ struct DoutRows {
   const float* p;
   const float* q;
   bool diff;
-  __device__ __forceinline__ float at(float coef, int off) const { return diff ? coef * (p[off] - q[off]) : p[off]; }
 };
 
 __device__ __forceinline__ DoutRows dout_rows(const DoutDesc& dd, int64_t b, int64_t sd, int64_t start) {
@@ -159,6 +158,30 @@ __device__ __forceinline__ DoutRows dout_rows(const DoutDesc& dd, int64_t b, int
   r.p = r.diff ? dd.p + b * sd + start : dd.buf + (b - dd.nsplit) * sd + start;
   r.q = r.diff ? dd.q + b * sd + start : nullptr;
   return r;
+}
+
+// base[off] with a 32-bit byte offset (offsets inside one sample's row block), so the load can
+// take the uniform base in scalar registers
+__device__ __forceinline__ float ldf(const float* base, uint32_t off) {
+  return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + (off << 2));
+}
+
+// The upstream gradient at the 16 offsets: every load of the branch is issued before any is
+// used (one memory round trip; a select over a conditional load would wait per row).
+__device__ __forceinline__ void dout16(const DoutRows& gr, float coef, const uint32_t* off, float* gv) {
+  if (gr.diff) {
+    float a[16], b[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      a[r] = ldf(gr.p, off[r]);
+      b[r] = ldf(gr.q, off[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) gv[r] = coef * (a[r] - b[r]);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) gv[r] = ldf(gr.p, off[r]);
+  }
 }
 
 __device__ __forceinline__ float dout_coef(const DoutDesc& dd) { return dd.nsplit > 0 ? dd.mul * (dd.g ? dd.g[0] : 1.0f) : 0.0f; }
@@ -504,12 +527,13 @@ __global__ void __launch_bounds__(256) mf_bwd_a_kernel(DoutDesc dd, const float*
       const bf16* ubp = Ub + (k * kRank + (lane & 31)) * d + cb * 32 + 8 * (lane >> 5);
       const float gn = gk[col], bs = bk[col], sc = sk[col];
       float xv[16], gv[16];
+      uint32_t off[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int off = acc_row_ld(r, lane, 0, nrow) * d + col;
-        xv[r] = hs[off];
-        gv[r] = gr.at(coef, off);
+        off[r] = (uint32_t)(acc_row_ld(r, lane, 0, nrow) * d + col);
+        xv[r] = ldf(hs, off[r]);
       }
+      dout16(gr, coef, off, gv);
       f32x16_v acc = zero16();
       acc = mfma16(s0v, ld8b(up), acc);
       acc = mfma16(s1v, ld8b(up + 16), acc);
@@ -726,8 +750,10 @@ __global__ void __launch_bounds__(256, INTO ? 3 : 2) mf_bwd_b_kernel(DoutDesc dd
     const int64_t k = clamp_key(key[b], G);
     const DoutRows gr = dout_rows(dd, b, sd, (int64_t)s0 * d);
     float gv[16];
+    uint32_t off[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) gv[r] = gr.at(coef, acc_row_ld(r, lane, 0, nrow) * d + col);
+    for (int r = 0; r < 16; ++r) off[r] = (uint32_t)(acc_row_ld(r, lane, 0, nrow) * d + col);
+    dout16(gr, coef, off, gv);
     const bf16* vp = Vb + (k * 3 * d + col) * kRank + 8 * (lane >> 5);
     const bf16* wp = Vb + (k * 3 * d + 2 * d + col) * kRank + 8 * (lane >> 5);
     const bf16* up = UT + (k * d + col) * kRank + 8 * (lane >> 5);
