@@ -877,7 +877,9 @@ __global__ void __launch_bounds__(1024) mf_pack_kernel(const int64_t* __restrict
 // The same lists for up to 256 keys and 4096 samples without per-key scans over all samples:
 // each thread holds one sample's key, each wave ranks its 64 samples per key with one ballot per
 // key, and a per-key prefix over the waves (in wave order) places them, so a key's samples keep
-// ascending sample order (the lists are identical to mf_pack_kernel's).
+// ascending sample order (the lists are identical to mf_pack_kernel's).  Every workgroup builds
+// the sample lists in its LDS (a few microseconds); workgroup 0 writes them, and the row lists
+// (S rows per listed sample) are written by all workgroups, a slice of the slots each.
 constexpr int kPackFastKeys = 256, kPackFastSamples = 4096;
 
 __global__ void __launch_bounds__(1024) mf_pack_fast_kernel(const int64_t* __restrict__ key, int B0, int Bh0, int B1,
@@ -921,13 +923,15 @@ __global__ void __launch_bounds__(1024) mf_pack_fast_kernel(const int64_t* __res
     for (int q = 0; q < 4; ++q) {
       const int g = 4 * lane + q;
       if (g < G) {
-        soff[g] = s;
-        offsets[g] = s * S;
+        if (blockIdx.x == 0) {
+          soff[g] = s;
+          offsets[g] = s * S;
+        }
         run[g] = s;
       }
       s += v[q];
     }
-    if (lane == 63) {
+    if (lane == 63 && blockIdx.x == 0) {
       soff[G] = s;
       offsets[G] = s * S;
     }
@@ -956,25 +960,29 @@ __global__ void __launch_bounds__(1024) mf_pack_fast_kernel(const int64_t* __res
     if (k >= 0) {
       const int slot = cw[wave][k] + rank;
       const int src = j < B0 ? j % Bh0 : Bh0 + (j - B0) % Bh1;
-      slist[slot] = j;
-      psrc[slot] = src;
+      if (blockIdx.x == 0) {
+        slist[slot] = j;
+        psrc[slot] = src;
+      }
       sl[slot] = j;
       sp[slot] = src;
     }
     __syncthreads();
   }
-  // one wave per listed sample (S rows), four samples in flight per wave
-  for (int slot0 = wave; slot0 < Bt; slot0 += 64) {
+  // one wave per listed sample (S rows), four samples in flight per wave, the waves of all
+  // workgroups striding over the slots
+  const int gw = blockIdx.x * 16 + wave, nw = gridDim.x * 16;
+  for (int slot0 = gw; slot0 < Bt; slot0 += 4 * nw) {
     int js[4], xs[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int slot = slot0 + 16 * u;
+      const int slot = slot0 + nw * u;
       js[u] = slot < Bt ? sl[slot] : 0;
       xs[u] = slot < Bt ? sp[slot] * S : 0;
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int slot = slot0 + 16 * u;
+      const int slot = slot0 + nw * u;
       if (slot < Bt) {
         for (int s = lane; s < S; s += 64) {
           tok[slot * S + s] = xs[u] + s;
@@ -1148,7 +1156,8 @@ int macro_fused_wgrad(const int64_t* key, int B0, int Bh0, int B1, int Bh1, int 
   float* dV2 = reinterpret_cast<float*>(take((size_t)G * d * kRank * 4));
   const size_t gk_bytes = ws_bytes - (size_t)(w - static_cast<char*>(ws));
   if (G <= kPackFastKeys && Bt <= kPackFastSamples) {
-    hipLaunchKernelGGL(mf_pack_fast_kernel, dim3(1), dim3(1024), 0, s, key, B0, Bh0, B1, Bh1 > 0 ? Bh1 : 1, S, G,
+    const int nwg = std::max(1, std::min(32, (Bt + 63) / 64));  // about 64 listed samples per workgroup
+    hipLaunchKernelGGL(mf_pack_fast_kernel, dim3(nwg), dim3(1024), 0, s, key, B0, Bh0, B1, Bh1 > 0 ? Bh1 : 1, S, G,
                        offsets, tok, pos, soff, slist, psrc);
   } else {
     const size_t lds = (size_t)(G + 2 * Bt) * sizeof(int);
