@@ -78,12 +78,19 @@ __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const float* __restric
 // dw needs no atomics: per-block partials are summed in block order by colsum_kernel.
 constexpr int kNormRowsPerBlock = 32;  // upper bound; small T uses fewer rows per block
 
+constexpr int kNormMaxChunks = 4;  // d <= 64 lanes * 8 * 4 = 2048
+
+// 8-column chunks per lane of the backward kernel instantiated for d
+inline int norm_chunks(int d) { return (d / 8 + 63) / 64; }
+
 // Rows per backward workgroup: 4 (one per wave) for small T, up to 32 once the grid is full.
-inline int norm_rows_per_block(int T) {
-  int r = ((T + 255) / 256 + 3) / 4 * 4;
+// With one chunk per lane (d <= 512) the kernel is small enough for 8 waves per SIMD, so the
+// grid aims at 1024 workgroups (two rows per wave at T = 8192) instead of 256.
+inline int norm_rows_per_block(int T, int d) {
+  const int target = norm_chunks(d) == 1 ? 1024 : 256;
+  int r = ((T + target - 1) / target + 3) / 4 * 4;
   return r < 4 ? 4 : (r > kNormRowsPerBlock ? kNormRowsPerBlock : r);
 }
-constexpr int kNormMaxChunks = 4;  // d <= 64 lanes * 8 * 4 = 2048
 
 __device__ __forceinline__ void load8_bf16(const bf16* p, float* v) {
   const uint4 u = *reinterpret_cast<const uint4*>(p);
@@ -107,6 +114,7 @@ __device__ __forceinline__ void store8_f32(float* p, const float* v) {
   *reinterpret_cast<float4*>(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
 }
 
+template <int NCH>
 __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     const bf16* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ rstd, const float* __restrict__ dres, int T, int d,
@@ -114,10 +122,10 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   extern __shared__ float sdw[];  // [4][d]
   const int nchunk = d / 8;
-  float wv[kNormMaxChunks][8];
-  float acc[kNormMaxChunks][8];
+  float wv[NCH][8];
+  float acc[NCH][8];
 #pragma unroll
-  for (int c = 0; c < kNormMaxChunks; ++c) {
+  for (int c = 0; c < NCH; ++c) {
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       acc[c][t] = 0.0f;
@@ -130,10 +138,10 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     const int t = r0 + rr;
     if (t >= T) break;
     const float rs = rstd[t];
-    float g[kNormMaxChunks][8], xv[kNormMaxChunks][8];
+    float g[NCH][8], xv[NCH][8];
     float dot = 0.0f;
 #pragma unroll
-    for (int c = 0; c < kNormMaxChunks; ++c) {
+    for (int c = 0; c < NCH; ++c) {
       if (lane + 64 * c >= nchunk) continue;
       const int col = (lane + 64 * c) * 8;
       load8_bf16(dy + (int64_t)t * d + col, g[c]);
@@ -144,7 +152,7 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     dot = wave_sum(dot);
     const float coef = rs * rs * rs * dot / (float)d;
 #pragma unroll
-    for (int c = 0; c < kNormMaxChunks; ++c) {
+    for (int c = 0; c < NCH; ++c) {
       if (lane + 64 * c >= nchunk) continue;
       const int col = (lane + 64 * c) * 8;
       float o[8];
@@ -159,7 +167,7 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     }
   }
 #pragma unroll
-  for (int c = 0; c < kNormMaxChunks; ++c)
+  for (int c = 0; c < NCH; ++c)
     if (lane + 64 * c < nchunk) store8_f32(sdw + wave * d + (lane + 64 * c) * 8, acc[c]);
   __syncthreads();
   for (int c = threadIdx.x; c < d; c += 256)
@@ -334,7 +342,7 @@ int rmsnorm_fwd(const float* x, const float* w, int T, int d, float eps, bf16* o
 }
 
 size_t rmsnorm_bwd_workspace_bytes(int T, int d) {
-  const int rpb = norm_rows_per_block(T);
+  const int rpb = norm_rows_per_block(T, d);
   const int nblk = (T + rpb - 1) / rpb;
   return (size_t)(nblk > 0 ? nblk : 1) * d * sizeof(float);
 }
@@ -343,12 +351,24 @@ int rmsnorm_bwd(const bf16* dy, const float* x, const float* w, const float* rst
                 int d, float* dx, float* dw, int dw_accumulate, void* ws, size_t ws_bytes, hipStream_t s) {
   RTE_REQUIRE(ws_bytes >= rmsnorm_bwd_workspace_bytes(T, d), "rmsnorm_bwd: workspace too small");
   RTE_REQUIRE(d % 8 == 0 && d <= 64 * 8 * kNormMaxChunks, "rmsnorm_bwd: d must be a multiple of 8 and <= 2048");
-  const int rpb = norm_rows_per_block(T);
+  const int rpb = norm_rows_per_block(T, d);
   const int nblk = (T + rpb - 1) / rpb;
   float* part = static_cast<float*>(ws);
   if (nblk > 0) {
-    hipLaunchKernelGGL(rmsnorm_bwd_kernel, dim3(nblk), dim3(256), 4 * d * sizeof(float), s, dy, x, w, rstd,
-                       dres, T, d, dx, part, rpb);
+    const size_t lds = 4 * d * sizeof(float);
+    switch (norm_chunks(d)) {
+      case 1:
+        hipLaunchKernelGGL(rmsnorm_bwd_kernel<1>, dim3(nblk), dim3(256), lds, s, dy, x, w, rstd, dres, T, d, dx,
+                           part, rpb);
+        break;
+      case 2:
+        hipLaunchKernelGGL(rmsnorm_bwd_kernel<2>, dim3(nblk), dim3(256), lds, s, dy, x, w, rstd, dres, T, d, dx,
+                           part, rpb);
+        break;
+      default:
+        hipLaunchKernelGGL(rmsnorm_bwd_kernel<kNormMaxChunks>, dim3(nblk), dim3(256), lds, s, dy, x, w, rstd, dres,
+                           T, d, dx, part, rpb);
+    }
     RTE_TRY(check_launch("rmsnorm_bwd"));
   }
   if (dw) {
