@@ -540,14 +540,20 @@ class BankedSwiGLU(nn.Module):
         slab = self.config.d_ff // self.config.ffn_groups
         return hip_ops.grouped_pool_swiglu(x, ids, w, wug_t, wd_t, slab, acc=acc)
 
+    def pack_recipes(self, recipe_ids: torch.Tensor, seq: int, active: torch.Tensor | None = None):
+        """The pool pack of samples with recipe_ids [B] (inactive samples get no pairs)."""
+        slab = self.config.d_ff // self.config.ffn_groups
+        clusters = self.config.ffn_banks * self.config.d_ff // slab
+        return hip_ops.pack_routes(recipe_ids, self.recipe_routes, self.recipe_route_w, seq, clusters, active)
+
     def forward_recipes(self, x: torch.Tensor, recipe_ids: torch.Tensor, active: torch.Tensor | None = None,
-                        weights=None, acc=None) -> torch.Tensor:
+                        weights=None, acc=None, pk=None) -> torch.Tensor:
         """Every sample's tokens through its recipe's clusters (inactive samples: none), packed
-        straight from the recipe ids (rte_pack_routes)."""
+        straight from the recipe ids (rte_pack_routes); pk: that pack, made ahead (optional)."""
         wug_t, wd_t = weights if weights is not None else self.pool_weights()
         slab = self.config.d_ff // self.config.ffn_groups
-        pk = hip_ops.pack_routes(recipe_ids, self.recipe_routes, self.recipe_route_w, x.shape[1],
-                                 wug_t.shape[0] // 2 // slab, active)
+        if pk is None:
+            pk = self.pack_recipes(recipe_ids, x.shape[1], active)
         return hip_ops.grouped_pool_swiglu(x, None, None, wug_t, wd_t, slab, pk=pk, acc=acc)
 
     def routes_for(self, recipe_ids: torch.Tensor, seq: int, active: torch.Tensor | None = None):
@@ -619,7 +625,8 @@ class BankedRecursiveCore(nn.Module):
         attn = self.attn.forward_scaled(n1, head_scale, weights.get("attn"), weights.get("attn_wgrad"))
         u, n2 = hip_ops.axpy_norm(h_tilde, attn, sa, self.norm2.weight, g2, b2, self.norm2.eps)
         if recipe_ids is not None:  # per-sample recipes: pack the routes straight from the ids
-            mlp = self.mlp.forward_recipes(n2, recipe_ids, active, weights["pool"], weights.get("pool_wgrad"))
+            mlp = self.mlp.forward_recipes(n2, recipe_ids, active, weights["pool"], weights.get("pool_wgrad"),
+                                           weights.get("pool_pack"))
         else:
             mlp = self.mlp.forward_routes(n2, ids, w, weights["pool"], weights.get("pool_wgrad"))
         return hip_ops.axpy(u, mlp, sm, keep=h if active is not None else None, mask=active)

@@ -168,11 +168,17 @@ class RecursiveModel(nn.Module):
         # every pass's recipe ids, active masks and head scales in one launch each
         rid_bp = route.recipe_id_by_pass
         rids = (rid_bp.t() if rid_bp is not None else route.recipe_id.reshape(1, -1).expand(T, -1)).contiguous()
-        actives = self.pass_index[:T, None] < route.depth.reshape(1, -1)
+        # a fixed depth of at least T (known on the host) keeps every sample active in every pass:
+        # no pass masks, and with one recipe per sample every pass shares one pool pack
+        fixed = getattr(route, "fixed_depth_value", None)
+        all_active = fixed is not None and fixed >= T
+        actives = None if all_active else self.pass_index[:T, None] < route.depth.reshape(1, -1)
+        if all_active and rid_bp is None:
+            weights["pool_pack"] = self.core.mlp.pack_recipes(rids[0], h0.shape[1])
         head_scales = self.core.attn.recipe_head_scale[rids.long()]
         for t in range(T):
-            h = self.core.forward_step(h, h0, rids[t], actives[t], pass_idx=t, weights=weights,
-                                       head_scale=head_scales[t])
+            h = self.core.forward_step(h, h0, rids[t], None if actives is None else actives[t], pass_idx=t,
+                                       weights=weights, head_scale=head_scales[t])
             if return_states and (t + 1) in self.config.depth_choices:
                 states[t + 1] = h  # every pass returns a new tensor; nothing writes h in place
         hidden = self._coda_hidden(h)

@@ -40,6 +40,7 @@ class RouterOutput:
     recipe_probs_by_pass: torch.Tensor | None = None
     recipe_id_by_pass: torch.Tensor | None = None
     recipe_onehot_st_by_pass: torch.Tensor | None = None
+    fixed_depth_value: int | None = None  # every sample's depth when the router ran with a fixed depth
     _factor_fn: object = None
     _factor: dict | None = None
 
@@ -149,4 +150,5 @@ class Router(nn.Module):
         f = hip_ops.router(h0, rm[0].weight, rm[0].bias, rm[2].weight, rm[2].bias, dm[0].weight, dm[0].bias,
                            dm[2].weight, dm[2].bias, self.pass_recipe_bias, self.depth_values, inv_t=inv_t,
                            fixed_recipe=fixed_recipe, fixed_depth=depth_idx)
-        return RouterOutput(**f, _factor_fn=lambda: self._factor_heads(h0.mean(dim=1), inv_t))
+        return RouterOutput(**f, fixed_depth_value=fixed_depth,
+                            _factor_fn=lambda: self._factor_heads(h0.mean(dim=1), inv_t))

@@ -29,7 +29,8 @@ def test_library_loads_and_exports_every_symbol():
     assert lib.rte_abi_version() == 1
     # pure host helpers work without a device
     assert lib.rte_pack_workspace_bytes(65536, 64) == 64 * 256 * 4
-    assert lib.rte_rmsnorm_bwd_workspace_bytes(8192, 512) == 256 * 512 * 4  # 32-row blocks
+    assert lib.rte_rmsnorm_bwd_workspace_bytes(8192, 512) == 1024 * 512 * 4  # 8-row blocks (d <= 512)
+    assert lib.rte_rmsnorm_bwd_workspace_bytes(8192, 1024) == 256 * 1024 * 4  # 32-row blocks
 
 
 def test_ops_fail_loudly_without_device():
