@@ -271,11 +271,11 @@ class AuditEngine:
             metrics["audit_residual_var"] = st[2]
             metrics["corrected_metric_loss"] = st[3]
             metrics["loss_residual"] = st[0]
-            hot_end = hot.meta.recurrent_hidden.index_select(0, idx)
+            hot_end = hip_ops.select_rows(hot.meta.recurrent_hidden, idx)
             # the replay already selected these h0 rows (with their gradient path when it ran with
             # gradients): reuse them instead of a second full-size selection and its backward
             h0_sub = (exact.meta.h0 if grad_corr and exact.meta.h0 is not None and exact.meta.h0.requires_grad
-                      else hot.meta.h0.index_select(0, idx))
+                      else hip_ops.select_rows(hot.meta.h0, idx))
             hot_logits = hot.meta.logits.index_select(0, idx) if hot.meta.logits is not None else None
             tr = self.config
             exact_end = exact.meta.recurrent_hidden

@@ -1436,6 +1436,73 @@ def distill(hot, exact, h0, hot_logits=None, exact_logits=None, *, temperature: 
     return losses, metrics
 
 
+# ----------------------------------------------------------------------------- audited-row selection
+
+class _RowSink:
+    """Gradients of one select_rows call, waiting for the hook on the source tensor."""
+
+    def __init__(self, idx: torch.Tensor):
+        self.idx = idx
+        self.grads: list[torch.Tensor] = []
+        self.pending = False
+
+    def check_drained(self) -> None:
+        if self.grads:
+            self.grads.clear()
+            raise RuntimeError("select_rows: the selected rows received a gradient but the hook on the source "
+                               "tensor that adds them never ran")
+        self.pending = False
+
+
+class SelectRowsFn(torch.autograd.Function):
+    """x.index_select(0, idx) whose backward hands its gradient to a hook on x instead of returning a
+    full-size gradient: the hook adds the rows into x's accumulated gradient (one index_add_ over
+    the selected rows) in place of a zero fill, a scatter and a full-size add."""
+
+    @staticmethod
+    def forward(ctx, x, idx, sink):
+        ctx.sink = sink
+        ctx.set_materialize_grads(False)
+        return x.index_select(0, idx)
+
+    @staticmethod
+    def backward(ctx, g):
+        sink = ctx.sink
+        if g is not None:
+            sink.grads.append(g)
+            if not sink.pending:  # a backward in which x gets no other gradient must fail loudly
+                sink.pending = True
+                torch.autograd.Variable._execution_engine.queue_callback(sink.check_drained)
+        return None, None, None
+
+
+def select_rows(x: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """Rows idx of x (dim 0) with the gradient added into x's own accumulated gradient.  x must be
+    a non-leaf whose other consumers' backward hands x a gradient buffer of its own (every
+    operator of this package allocates its input gradients; autograd's sum of several
+    contributions is its own buffer too): the hook adds the rows in place.  x must also receive a
+    gradient from those consumers (autograd lets no hook replace a missing gradient): otherwise the
+    backward raises.  Leaves and no-grad inputs use index_select."""
+    if not (torch.is_grad_enabled() and x.requires_grad and x.grad_fn is not None):
+        return x.index_select(0, idx)
+    sink = _RowSink(idx)
+
+    def add_rows(gx):
+        if not sink.grads:
+            return gx
+        if gx is None:
+            sink.grads.clear()
+            raise RuntimeError("select_rows: the source tensor received no gradient besides the selected rows'; "
+                               "select with index_select there")
+        for g in sink.grads:  # in arrival order
+            gx.index_add_(0, sink.idx, g.to(gx.dtype))
+        sink.grads.clear()
+        return gx
+
+    x.register_hook(add_rows)
+    return SelectRowsFn.apply(x, idx, sink)
+
+
 # ----------------------------------------------------------------------------- audit correction
 
 class AuditCorrectFn(torch.autograd.Function):

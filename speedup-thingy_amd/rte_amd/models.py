@@ -199,7 +199,7 @@ class RecursiveModel(nn.Module):
         idx = audit_index.nonzero(as_tuple=False).flatten() if audit_index.dtype == torch.bool else audit_index
         route = reuse_router_decisions.subset(idx)
         if cached_h0 is not None:
-            h0 = cached_h0.index_select(0, idx)
+            h0 = hip_ops.select_rows(cached_h0, idx)
         else:
             h0 = self._prelude(tokens.index_select(0, idx))
         return self.forward_exact_from_h0(h0, targets.index_select(0, idx), return_states, return_loss_per_sample,
