@@ -326,6 +326,14 @@ int rte_ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* tar
                void* stream);
 int rte_ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
                const float* dloss, const float* extra, void* dlogits, void* stream);
+/* rte_ce_bwd with the extra logit gradient given only for whole samples: extra_rows f32
+ * [n_samples * seq, V] holds the rows of samples sample_ids[0, n_samples) (seq tokens each; token t
+ * belongs to sample t / seq), every other token has none.  Replaces the zero-filled [T, V] gradient
+ * of the audited-sample selection of the hot logits (hot.meta.logits[mask], rte/audit.py:336, fed to
+ * macro_distill_loss, rte/macro.py:394); a sample listed twice adds its rows in list order. */
+int rte_ce_bwd_rows(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
+                    const float* dloss, const float* extra_rows, const int64_t* sample_ids, int n_samples, int seq,
+                    void* dlogits, void* stream);
 
 /* ---- residual axpy + FiLM RMSNorm of a recursive pass (replaces the elementwise glue of
  *      BankedRecursiveCore._step, rte/layers.py:826-845: h~ = h + alpha h0, rmsnorm * (1 + gamma)

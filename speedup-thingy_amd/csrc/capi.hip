@@ -44,7 +44,7 @@ int cast_many(const int64_t* jobs, const int32_t* blk, int nblk, hipStream_t s);
 int ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, float* loss, float* lse,
            hipStream_t s);
 int ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse, const float* g,
-           const float* extra, bf16* dlogits, hipStream_t s);
+           const float* extra, const int64_t* ext_ids, int ext_k, int ext_S, bf16* dlogits, hipStream_t s);
 int axpy_norm_fwd(const float* a, const float* b, const float* c, const float* keep, const uint8_t* mask, int S,
                   int T, int d, const float* w, const float* gamma, const float* beta, float eps, float* x_out,
                   bf16* n_out, float* rstd_out, hipStream_t s);
@@ -901,7 +901,16 @@ int rte_ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* tar
 
 int rte_ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
                const float* dloss, const float* extra, void* dlogits, void* stream) {
-  return ce_bwd(logits, ld, T, V, targets, lse, dloss, extra, B16(dlogits), S(stream));
+  return ce_bwd(logits, ld, T, V, targets, lse, dloss, extra, nullptr, 0, 1, B16(dlogits), S(stream));
+}
+
+int rte_ce_bwd_rows(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse,
+                    const float* dloss, const float* extra_rows, const int64_t* sample_ids, int n_samples, int seq,
+                    void* dlogits, void* stream) {
+  RTE_REQUIRE(extra_rows && sample_ids && n_samples >= 1 && seq >= 1 && T % seq == 0,
+              "ce_bwd_rows: need the rows, their sample ids, and T a multiple of the tokens per sample");
+  return ce_bwd(logits, ld, T, V, targets, lse, dloss, extra_rows, sample_ids, n_samples, seq, B16(dlogits),
+                S(stream));
 }
 
 int rte_axpy_norm_fwd(const float* a, const float* b, const float* c, const float* keep, const uint8_t* mask,

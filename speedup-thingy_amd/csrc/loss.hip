@@ -68,12 +68,23 @@ __global__ void __launch_bounds__(256) ce_fwd_kernel(const float* __restrict__ l
 __global__ void __launch_bounds__(256) ce_bwd_kernel(const float* __restrict__ logits, int64_t ld, int T, int V,
                                                      const int64_t* __restrict__ targets,
                                                      const float* __restrict__ lse, const float* __restrict__ g,
-                                                     const float* __restrict__ extra, bf16* __restrict__ dlogits) {
+                                                     const float* __restrict__ extra,
+                                                     const int64_t* __restrict__ ext_ids, int ext_k, int ext_S,
+                                                     bf16* __restrict__ dlogits) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= T) return;
   const float* row = logits + (int64_t)t * ld;
-  const float* ex = extra ? extra + (int64_t)t * V : nullptr;
+  const float* ex = nullptr;
+  int j0 = 0;
+  if (extra && !ext_ids) {
+    ex = extra + (int64_t)t * V;
+  } else if (extra) {  // rows of the samples ext_ids (ext_S tokens each): the first match, more below
+    const int64_t smp = t / ext_S;
+    for (; j0 < ext_k && ext_ids[j0] != smp; ++j0) {
+    }
+    if (j0 < ext_k) ex = extra + ((int64_t)j0 * ext_S + t % ext_S) * V;
+  }
   bf16* out = dlogits + (int64_t)t * V;
   const int64_t tg = targets[t];
   const bool valid = tg >= 0 && tg < V;
@@ -86,7 +97,18 @@ __global__ void __launch_bounds__(256) ce_bwd_kernel(const float* __restrict__ l
       const float4 x = *reinterpret_cast<const float4*>(row + c);
       const float xs[4] = {x.x, x.y, x.z, x.w};
       float4 e4 = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (ex) e4 = *reinterpret_cast<const float4*>(ex + c);
+      if (ex) {
+        e4 = *reinterpret_cast<const float4*>(ex + c);
+        if (ext_ids) {  // a sample listed again adds its rows in list order (index_add_ order)
+          const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+          e4 = make_float4(z.x + e4.x, z.y + e4.y, z.z + e4.z, z.w + e4.w);
+          for (int j = j0 + 1; j < ext_k; ++j) {
+            if (ext_ids[j] != t / ext_S) continue;
+            const float4 f = *reinterpret_cast<const float4*>(extra + ((int64_t)j * ext_S + t % ext_S) * V + c);
+            e4.x += f.x; e4.y += f.y; e4.z += f.z; e4.w += f.w;
+          }
+        }
+      }
       const float es[4] = {e4.x, e4.y, e4.z, e4.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i) d[i] = gt * (__expf(xs[i] - l) - (c + i == tg ? 1.0f : 0.0f)) + es[i];
@@ -254,13 +276,15 @@ int ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets
 }
 
 int ce_bwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, const float* lse, const float* g,
-           const float* extra, bf16* dlogits, hipStream_t s) {
+           const float* extra, const int64_t* ext_ids, int ext_k, int ext_S, bf16* dlogits, hipStream_t s) {
   RTE_REQUIRE(V % 4 == 0 && ld % 4 == 0, "ce_bwd: V and the row stride must be multiples of 4");
+  RTE_REQUIRE(!ext_ids || (extra && ext_k >= 1 && ext_S >= 1),
+              "ce_bwd: extra rows by sample need the rows, a sample count and tokens per sample");
   RTE_REQUIRE(((uintptr_t)logits & 15) == 0 && ((uintptr_t)extra & 15) == 0 && ((uintptr_t)dlogits & 7) == 0,
               "ce_bwd: misaligned buffers");
   if (T == 0) return 0;
   hipLaunchKernelGGL(ce_bwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, ld, T, V, targets, lse, g, extra,
-                     dlogits);
+                     ext_ids, ext_ids ? ext_k : 0, ext_ids ? ext_S : 1, dlogits);
   return check_launch("ce_bwd");
 }
 

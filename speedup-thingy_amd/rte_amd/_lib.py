@@ -81,6 +81,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_route_centers": (_I, [_P, _I, _I, _P, _I, _P, _P]),
     "rte_ce_fwd": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P]),
     "rte_ce_bwd": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _P]),
+    "rte_ce_bwd_rows": (_I, [_P, _I64, _I, _I, _P, _P, _P, _P, _P, _I, _I, _P, _P]),
     "rte_axpy_norm_fwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _F, _P, _P, _P, _P]),
     "rte_axpy_norm_bwd_workspace_bytes": (_SZ, [_I, _I]),
     "rte_axpy_norm_bwd": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P, _P, _P, _P, _SZ, _P]),

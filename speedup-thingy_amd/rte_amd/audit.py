@@ -276,7 +276,7 @@ class AuditEngine:
             # gradients): reuse them instead of a second full-size selection and its backward
             h0_sub = (exact.meta.h0 if grad_corr and exact.meta.h0 is not None and exact.meta.h0.requires_grad
                       else hip_ops.select_rows(hot.meta.h0, idx))
-            hot_logits = hot.meta.logits.index_select(0, idx) if hot.meta.logits is not None else None
+            hot_logits = hip_ops.select_logit_rows(hot.meta.logits, idx) if hot.meta.logits is not None else None
             tr = self.config
             exact_end = exact.meta.recurrent_hidden
             if h0_sub is not None and exact_end is not None:

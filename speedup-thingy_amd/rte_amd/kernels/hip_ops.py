@@ -1349,6 +1349,7 @@ class LMHeadCEFn(torch.autograd.Function):
         call("rte_ce_fwd", ptr(logits), V, T, V, ptr(tg), ptr(loss), ptr(lse), _s())
         ctx.save_for_backward(hb, wb, logits, tg, lse)
         ctx.meta = (shape, hidden.dtype, w.dtype)
+        ctx.set_materialize_grads(False)  # no zero-filled [T, V] when only the loss has a gradient
         return logits.view(*shape[:-1], V), loss.view(shape[:-1])
 
     @staticmethod
@@ -1358,8 +1359,28 @@ class LMHeadCEFn(torch.autograd.Function):
         T, V = logits.shape
         ext = None if dlogits_ext is None else dlogits_ext.reshape(T, V).contiguous().to(F32)
         g = None if dloss is None else dloss.reshape(T).contiguous().to(F32)
+        # gradients of whole-sample logit rows selected by select_logit_rows, in arrival order
+        parts = [(sk.idx, gr) for sk in getattr(ctx, "row_sinks", ()) for gr in sk.grads]
+        for sk in getattr(ctx, "row_sinks", ()):
+            sk.grads.clear()
         dl = torch.empty((T, V), dtype=BF16, device=hb.device)
-        call("rte_ce_bwd", ptr(logits), V, T, V, ptr(tg), ptr(lse), ptr(g), ptr(ext), ptr(dl), _s())
+        if parts and ext is None:
+            S = shape[-2]
+            if len(parts) == 1:
+                ids, rows = parts[0][0], parts[0][1].reshape(-1, V)
+            else:
+                ids, rows = torch.cat([p[0] for p in parts]), torch.cat([p[1].reshape(-1, V) for p in parts])
+            ids = ids.to(torch.int64).contiguous()
+            rows = rows.contiguous().to(F32)
+            call("rte_ce_bwd_rows", ptr(logits), V, T, V, ptr(tg), ptr(lse), ptr(g), ptr(rows), ptr(ids),
+                 ids.numel(), S, ptr(dl), _s())
+        else:
+            if parts:  # a dense logit gradient as well: add the rows to it
+                ext = ext.view(-1, shape[-2], V).clone()
+                for ids, gr in parts:
+                    ext.index_add_(0, ids, gr.to(F32))
+                ext = ext.view(T, V)
+            call("rte_ce_bwd", ptr(logits), V, T, V, ptr(tg), ptr(lse), ptr(g), ptr(ext), ptr(dl), _s())
         dh = gemm(dl, wb, b_t=True)                              # [T, d] = dlogits @ W
         dw = gemm(dl, hb, a_t=True, b_t=True, out_f32=True)      # [V, d] = dlogits^T @ hidden
         return dh.view(shape).to(h_dt), dw.to(w_dt), None
@@ -1368,6 +1389,19 @@ class LMHeadCEFn(torch.autograd.Function):
 def lm_head_ce(hidden, w, targets):
     """(logits fp32, per-token cross-entropy) of hidden @ W^T against targets."""
     return LMHeadCEFn.apply(hidden, w, targets)
+
+
+def select_logit_rows(logits: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
+    """Samples idx of [B, S, V] logits made by lm_head_ce (rte/audit.py:336, hot.meta.logits[mask]).
+    Their gradient goes to the head's backward, whose CE kernel adds the rows of those samples
+    only (rte_ce_bwd_rows): no zero-filled [B, S, V] gradient.  Other logits use index_select."""
+    node = logits.grad_fn
+    if not (torch.is_grad_enabled() and logits.requires_grad and logits.dim() == 3 and node is not None
+            and type(node).__name__ == "LMHeadCEFnBackward"):
+        return logits.index_select(0, idx)
+    sink = _RowSink(idx)
+    node.row_sinks = getattr(node, "row_sinks", []) + [sink]
+    return SelectRowsFn.apply(logits, idx, sink)
 
 
 # ----------------------------------------------------------------------------- audit distillation

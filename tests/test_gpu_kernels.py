@@ -625,6 +625,60 @@ def test_lm_head_ce_fwd_bwd(T, d, V):
     assert_rel(_np(tw.grad), dlog.T @ h, BF16_RTOL, "head dW")
 
 
+@pytest.mark.parametrize("ids", [[3], [0, 6], [5, 2, 5]])
+def test_ce_bwd_rows_matches_dense(ids):
+    """rte_ce_bwd_rows (extra logit gradient for whole samples only) against rte_ce_bwd with the
+    same rows scattered into a zero [T, V] gradient by index_add_ (a repeated sample adds its rows
+    in list order): bitwise equal."""
+    from rte_amd import _lib
+
+    B, S, V = 8, 16, 256
+    T = B * S
+    print(f"ce_bwd_rows B={B} S={S} V={V} ids={ids}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    logits = torch.randn(T, V, device=DEV, generator=g) * 3
+    tg = torch.randint(0, V, (T,), device=DEV, generator=g)
+    tg[5] = -1  # an ignored target
+    lse = torch.logsumexp(logits, dim=1).contiguous()
+    dloss = torch.randn(T, device=DEV, generator=g)
+    ix = torch.tensor(ids, dtype=torch.int64, device=DEV)
+    rows = torch.randn(len(ids), S, V, device=DEV, generator=g) * 1e-2
+    dense = torch.zeros(B, S, V, device=DEV).index_add_(0, ix, rows).reshape(T, V).contiguous()
+    p = _lib.ptr
+    st = _lib.stream_ptr()
+    want = torch.empty(T, V, dtype=torch.bfloat16, device=DEV)
+    got = torch.empty_like(want)
+    rows = rows.contiguous()
+    _lib.call("rte_ce_bwd", p(logits), V, T, V, p(tg), p(lse), p(dloss), p(dense), p(want), st)
+    _lib.call("rte_ce_bwd_rows", p(logits), V, T, V, p(tg), p(lse), p(dloss), p(rows), p(ix), len(ids), S, p(got), st)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
+def test_select_logit_rows_grads_match_index_select():
+    """The audited-sample selection of lm_head_ce logits (gradient rows handed to the head's CE
+    backward) against index_select of the same logits: same values, bitwise-equal gradients."""
+    H = _ops()
+    B, S, d, V = 4, 32, 64, 256
+    print(f"select_logit_rows B={B} S={S} d={d} V={V}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    h0 = torch.randn(B, S, d, device=DEV, generator=gen).to(torch.bfloat16)
+    w0 = torch.randn(V, d, device=DEV, generator=gen) * 0.05
+    tg = torch.randint(0, V, (B, S), device=DEV, generator=gen)
+    ix = torch.tensor([2, 0], dtype=torch.int64, device=DEV)
+    c = torch.randn(2, S, V, device=DEV, generator=gen)
+    res = []
+    for select in (lambda x, i: x.index_select(0, i), H.select_logit_rows):
+        h = h0.clone().requires_grad_()
+        w = w0.clone().requires_grad_()
+        logits, tok = H.lm_head_ce(h, w, tg)
+        sel = select(logits, ix)
+        (tok.sum() + (sel * c).sum()).backward()
+        res.append((sel.detach(), h.grad, w.grad))
+    for a, b in zip(res[0], res[1]):
+        assert torch.equal(a, b)
+
+
 # ---------------------------------------------------------------- shortlist head
 
 def _sl_inputs(T, V, C, tc, H, R, L, seed, skew=False):
