@@ -7,7 +7,7 @@ the loss estimate unbiased for inclusion probability p.
 
 from __future__ import annotations
 
-from contextlib import nullcontext
+from contextlib import contextmanager, nullcontext
 from dataclasses import dataclass
 
 import torch
@@ -26,6 +26,37 @@ class AuditResult:
     corrected_loss_per_sample: torch.Tensor
     macro_aux: dict[str, torch.Tensor]
     metrics: dict[str, torch.Tensor]
+
+
+@contextmanager
+def main_stream_aliases(*modules):
+    """Inside the block every trainable parameter of `modules` reads as a view of itself made on
+    the stream current at entry (one view per parameter, shared by every module holding it).
+
+    Work issued on a side stream inside the block then differentiates into those views, whose
+    backward runs on the entry stream, so each parameter's gradient accumulator is fed from that
+    one stream (autograd warns, and synchronises, when a leaf's accumulator receives gradients
+    produced on another stream than its own)."""
+    if not torch.is_grad_enabled():
+        yield
+        return
+    alias: dict[int, torch.Tensor] = {}
+    swaps = []
+    for mod in modules:
+        for m in mod.modules():
+            for name, p in list(m._parameters.items()):
+                if p is None or not p.requires_grad:
+                    continue
+                a = alias.get(id(p))
+                if a is None:
+                    a = alias[id(p)] = p.view_as(p)
+                m._parameters[name] = a
+                swaps.append((m, name, p))
+    try:
+        yield
+    finally:
+        for m, name, p in swaps:
+            m._parameters[name] = p
 
 
 @dataclass(slots=True)
@@ -113,9 +144,9 @@ class AuditEngine:
                 chosen = self.fixed_count_index(n, k, seed, h0.device)
             side = self._side_stream(h0.device, 0)
             side.wait_stream(main)
-            with torch.cuda.stream(side):
-                grad_corr = self.config.audit_mode == "gradient_corrected"
-                with (nullcontext() if grad_corr else torch.no_grad()):
+            grad_corr = self.config.audit_mode == "gradient_corrected"
+            with (nullcontext() if grad_corr else torch.no_grad()), main_stream_aliases(model):
+                with torch.cuda.stream(side):
                     launch.exact = model.forward_exact_subset(tokens, targets, chosen, reuse_router_decisions=route,
                                                               cached_h0=h0)
             launch.chosen = chosen
@@ -128,7 +159,7 @@ class AuditEngine:
                 # one bf16 copy of the operator tables per step, shared with the hot path
                 hip_ops.macro_fused_weights_share(mac.v, mac.u, side)
             side.wait_stream(main)
-            with torch.cuda.stream(side):
+            with main_stream_aliases(model.macro), torch.cuda.stream(side):
                 launch.cons = model.macro.consistency_loss(h0, h0, route.recipe_id)
             launch.streams.append(side)
         return launch

@@ -1360,9 +1360,7 @@ class LMHeadCEFn(torch.autograd.Function):
         ext = None if dlogits_ext is None else dlogits_ext.reshape(T, V).contiguous().to(F32)
         g = None if dloss is None else dloss.reshape(T).contiguous().to(F32)
         # gradients of whole-sample logit rows selected by select_logit_rows, in arrival order
-        parts = [(sk.idx, gr) for sk in getattr(ctx, "row_sinks", ()) for gr in sk.grads]
-        for sk in getattr(ctx, "row_sinks", ()):
-            sk.grads.clear()
+        parts = [(sk.idx, gr) for sk in getattr(ctx, "row_sinks", ()) for gr in sk.take()]
         dl = torch.empty((T, V), dtype=BF16, device=hb.device)
         if parts and ext is None:
             S = shape[-2]
@@ -1473,12 +1471,38 @@ def distill(hot, exact, h0, hot_logits=None, exact_logits=None, *, temperature: 
 # ----------------------------------------------------------------------------- audited-row selection
 
 class _RowSink:
-    """Gradients of one select_rows call, waiting for the hook on the source tensor."""
+    """Gradients of one select_rows call, waiting for the hook on the source tensor.
+
+    The selection's backward may run on another stream than the consumer of the gradient (the
+    audit replay selects h0 rows on a side stream; h0's producer runs its backward on the main
+    stream), and autograd inserts no stream wait for a gradient handed over outside its graph.
+    Each gradient therefore travels with an event recorded on its producing stream; take()
+    makes the consuming stream wait on it and marks the tensor as used there, so the caching
+    allocator does not hand its memory to the producing stream's next allocation too early."""
 
     def __init__(self, idx: torch.Tensor):
         self.idx = idx
-        self.grads: list[torch.Tensor] = []
+        self.grads: list[tuple[torch.Tensor, object]] = []
         self.pending = False
+
+    def put(self, g: torch.Tensor) -> None:
+        ev = None
+        if g.is_cuda:
+            ev = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(g.device))
+        self.grads.append((g, ev))
+
+    def take(self) -> list[torch.Tensor]:
+        """The stored gradients in arrival order, ordered before the current stream's next work."""
+        out = []
+        for g, ev in self.grads:
+            if ev is not None:
+                cur = torch.cuda.current_stream(g.device)
+                cur.wait_event(ev)
+                g.record_stream(cur)
+            out.append(g)
+        self.grads.clear()
+        return out
 
     def check_drained(self) -> None:
         if self.grads:
@@ -1490,7 +1514,7 @@ class _RowSink:
 
 class SelectRowsFn(torch.autograd.Function):
     """x.index_select(0, idx) whose backward hands its gradient to a hook on x instead of returning a
-    full-size gradient: the hook adds the rows into x's accumulated gradient (one index_add_ over
+    full-size gradient: the hook adds the rows into x's accumulated gradient (one index_add over
     the selected rows) in place of a zero fill, a scatter and a full-size add."""
 
     @staticmethod
@@ -1503,7 +1527,7 @@ class SelectRowsFn(torch.autograd.Function):
     def backward(ctx, g):
         sink = ctx.sink
         if g is not None:
-            sink.grads.append(g)
+            sink.put(g)
             if not sink.pending:  # a backward in which x gets no other gradient must fail loudly
                 sink.pending = True
                 torch.autograd.Variable._execution_engine.queue_callback(sink.check_drained)
@@ -1511,12 +1535,12 @@ class SelectRowsFn(torch.autograd.Function):
 
 
 def select_rows(x: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
-    """Rows idx of x (dim 0) with the gradient added into x's own accumulated gradient.  x must be
-    a non-leaf whose other consumers' backward hands x a gradient buffer of its own (every
-    operator of this package allocates its input gradients; autograd's sum of several
-    contributions is its own buffer too): the hook adds the rows in place.  x must also receive a
-    gradient from those consumers (autograd lets no hook replace a missing gradient): otherwise the
-    backward raises.  Leaves and no-grad inputs use index_select."""
+    """Rows idx of x (dim 0) with the gradient added into x's accumulated gradient by a hook on x.
+    The hook returns a new tensor (gx with the rows added; the incoming gradient is never written,
+    since a pending node may still hold it) on the stream x's backward runs on, after the
+    selection's backward stream has produced the rows.  x must also receive a gradient from its
+    other consumers (autograd lets no hook replace a missing gradient): otherwise the backward
+    raises.  Leaves and no-grad inputs use index_select."""
     if not (torch.is_grad_enabled() and x.requires_grad and x.grad_fn is not None):
         return x.index_select(0, idx)
     sink = _RowSink(idx)
@@ -1528,9 +1552,8 @@ def select_rows(x: torch.Tensor, idx: torch.Tensor) -> torch.Tensor:
             sink.grads.clear()
             raise RuntimeError("select_rows: the source tensor received no gradient besides the selected rows'; "
                                "select with index_select there")
-        for g in sink.grads:  # in arrival order
-            gx.index_add_(0, sink.idx, g.to(gx.dtype))
-        sink.grads.clear()
+        for g in sink.take():  # in arrival order
+            gx = gx.index_add(0, sink.idx, g.to(gx.dtype))
         return gx
 
     x.register_hook(add_rows)
@@ -1809,6 +1832,15 @@ def macro_bounded(h, h0, key, pk, v, u, gain, bias, scale, c: float, eps: float 
 MACRO_FUSED_RANK = 32
 
 
+def _whole_param(t: torch.Tensor) -> bool:
+    """t is a parameter, or a view covering exactly a parameter's memory (a per-step alias)."""
+    if isinstance(t, torch.nn.Parameter):
+        return True
+    b = t._base
+    return (isinstance(b, torch.nn.Parameter) and t.shape == b.shape and t.stride() == b.stride()
+            and t.storage_offset() == b.storage_offset())
+
+
 def macro_fused_supported(v: torch.Tensor, u: torch.Tensor, repeats: int = 1) -> bool:
     """Shapes the fused operator kernels take: hidden rank 32, d a multiple of 128 up to 1024,
     at most 8 repeats of a source sample."""
@@ -1825,7 +1857,7 @@ def macro_fused_weights(v: torch.Tensor, u: torch.Tensor):
     G = v.shape[0] * v.shape[1]
     d = u.shape[-1]
     key = None
-    if _BF16_CACHE_ON[0] and isinstance(v, torch.nn.Parameter) and isinstance(u, torch.nn.Parameter):
+    if _BF16_CACHE_ON[0] and _whole_param(v) and _whole_param(u):
         key = ("macro_fused", v.data_ptr(), v._version, u.data_ptr(), u._version, _lib.stream_ptr())
         hit = _BF16_CACHE.get(key)
         if hit is not None:
@@ -1849,7 +1881,7 @@ def macro_fused_weights_share(v, u, stream) -> None:
     """Make this step's fused-operator weight copies (macro_fused_weights) on the current stream
     and let `stream` read the same copies; `stream` must wait on the current stream before it
     uses them.  Outside a per-step cache it does nothing."""
-    if not (_BF16_CACHE_ON[0] and isinstance(v, torch.nn.Parameter) and isinstance(u, torch.nn.Parameter)):
+    if not (_BF16_CACHE_ON[0] and _whole_param(v) and _whole_param(u)):
         return
     out = macro_fused_weights(v, u)
     _BF16_CACHE[("macro_fused", v.data_ptr(), v._version, u.data_ptr(), u._version, stream.cuda_stream)] = out

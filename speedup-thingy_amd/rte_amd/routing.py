@@ -43,11 +43,16 @@ class RouterOutput:
     fixed_depth_value: int | None = None  # every sample's depth when the router ran with a fixed depth
     _factor_fn: object = None
     _factor: dict | None = None
+    _factor_src: tuple | None = None  # (router, h0, inv_t): the factor heads' inputs
 
     def factor(self, name: str):
         """A factor-head field (computed once, on first use)."""
         if self._factor is None:
-            self._factor = self._factor_fn() if self._factor_fn is not None else {}
+            if self._factor_src is not None:
+                router, h0, inv_t = self._factor_src
+                self._factor = router._factor_heads(h0.mean(dim=1), inv_t)
+            else:
+                self._factor = self._factor_fn() if self._factor_fn is not None else {}
         return self._factor.get(name)
 
     attn_bank_logits_by_pass = property(lambda self: self.factor("attn_bank_logits_by_pass"))
@@ -150,5 +155,4 @@ class Router(nn.Module):
         f = hip_ops.router(h0, rm[0].weight, rm[0].bias, rm[2].weight, rm[2].bias, dm[0].weight, dm[0].bias,
                            dm[2].weight, dm[2].bias, self.pass_recipe_bias, self.depth_values, inv_t=inv_t,
                            fixed_recipe=fixed_recipe, fixed_depth=depth_idx)
-        return RouterOutput(**f, fixed_depth_value=fixed_depth,
-                            _factor_fn=lambda: self._factor_heads(h0.mean(dim=1), inv_t))
+        return RouterOutput(**f, fixed_depth_value=fixed_depth, _factor_src=(self, h0, inv_t))

@@ -11,6 +11,7 @@ torch._foreach_norm.
 
 from __future__ import annotations
 
+import dataclasses
 import time
 from contextlib import nullcontext
 from dataclasses import dataclass
@@ -50,6 +51,34 @@ def router_aux_losses(recipe_probs, expected_depth, usage_ema, tr: TrainingConfi
         "cover": tr.lambda_cover * cover,
         "depth": tr.lambda_depth * expected_depth.float().mean(),
     }
+
+
+def _detached(obj, memo: dict | None = None):
+    """obj with every tensor detached: dataclasses rebuilt field by field, containers copied,
+    router subsets re-rooted, anything else (modules, numbers) kept.  A step's returned outputs
+    then keep no autograd graph alive into the next step, whose leaves' gradient accumulators
+    would otherwise still belong to the old graph and its streams."""
+    from rte_amd.routing import RouterSubset
+
+    memo = {} if memo is None else memo
+    key = id(obj)
+    if key in memo:
+        return memo[key]
+    if isinstance(obj, torch.Tensor):
+        out = obj.detach()
+    elif isinstance(obj, dict):
+        out = {k: _detached(v, memo) for k, v in obj.items()}
+    elif isinstance(obj, (list, tuple)):
+        out = type(obj)(_detached(v, memo) for v in obj)
+    elif isinstance(obj, RouterSubset):
+        out = RouterSubset(_detached(obj._parent, memo), obj._mask)
+    elif dataclasses.is_dataclass(obj) and not isinstance(obj, type):
+        out = dataclasses.replace(obj, **{f.name: _detached(getattr(obj, f.name), memo)
+                                          for f in dataclasses.fields(obj) if f.init})
+    else:
+        out = obj
+    memo[key] = out
+    return out
 
 
 @dataclass
@@ -249,9 +278,10 @@ class TrainEngine:
         loss = out.loss_per_sample.mean() / self._loss_scale(targets)
         stepped = self._finish_step(loss, check_finite=check_finite)
         self.tokens_seen += tokens.numel()
-        return TrainStepResult(loss, out, {"mode": "dense_exact", "loss": loss, "stepped": stepped,
-                                           "lr": self._current_lr, "host_time": time.perf_counter() - t0,
-                                           **self.last_grad_metrics})
+        loss = loss.detach()
+        return TrainStepResult(loss, _detached(out), {"mode": "dense_exact", "loss": loss, "stepped": stepped,
+                                                      "lr": self._current_lr, "host_time": time.perf_counter() - t0,
+                                                      **self.last_grad_metrics})
 
     def _step_recursive_exact(self, batch, check_finite):
         tr = self.config.training
@@ -265,8 +295,9 @@ class TrainEngine:
         stepped = self._finish_step(loss, check_finite=check_finite)
         m.recipe_bank.update_usage(out.meta.recipe_ids, beta=tr.coverage_beta)
         self.tokens_seen += tokens.numel()
-        return TrainStepResult(loss, out, {"mode": "recursive_exact", "loss": loss, "stepped": stepped,
-                                           "lr": self._current_lr, **self.last_grad_metrics})
+        loss = loss.detach()
+        return TrainStepResult(loss, _detached(out), {"mode": "recursive_exact", "loss": loss, "stepped": stepped,
+                                                      "lr": self._current_lr, **self.last_grad_metrics})
 
     def _router_aux(self, out: ModelOutput) -> dict[str, torch.Tensor]:
         r = out.meta.router
@@ -342,7 +373,8 @@ class TrainEngine:
         self.tokens_seen += tokens.numel()
         metrics = self._macro_metrics(loss, hot, audit, aux, scale, targets, shortlist, stepped)
         metrics.update(budget, lr=self._current_lr)
-        return TrainStepResult(loss, hot, metrics, audit)
+        memo: dict = {}
+        return TrainStepResult(loss.detach(), _detached(hot, memo), metrics, _detached(audit, memo))
 
     # ------------------------------------------------------------------ captured step
     def enable_graph_capture(self, enabled: bool = True, *, keep_graph: bool = False) -> None:
@@ -474,7 +506,8 @@ class TrainEngine:
         metrics = self._macro_metrics(loss, hot, audit, aux, scale, st["targets"], shortlist, ok)
         names = [k for k, v in metrics.items() if isinstance(v, torch.Tensor)]
         flat = torch.stack([metrics[k].detach().float().reshape(()) for k in names])
-        return {"flat": flat, "names": names, "hot": hot, "audit": audit,
+        memo: dict = {}
+        return {"flat": flat, "names": names, "hot": _detached(hot, memo), "audit": _detached(audit, memo),
                 "host_metrics": {k: v for k, v in metrics.items() if not isinstance(v, torch.Tensor)},
                 "grad_names": list(self.last_grad_metrics)}
 

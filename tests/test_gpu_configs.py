@@ -11,6 +11,7 @@ Tolerances: routing ids bit-exact, bf16 paths 2e-2 relative (Frobenius)."""
 from __future__ import annotations
 
 import math
+import warnings
 
 import numpy as np
 import pytest
@@ -202,8 +203,12 @@ def test_cfg3_step_eager_vs_captured():
     before = {n_: p.detach().clone() for n_, p in a.recursive_model.named_parameters()}
     for step, batch in enumerate(batches):
         print(f"cfg3 step {step}", flush=True)
-        ra, rb = a.train_step(batch), b.train_step(batch)
-        torch.cuda.synchronize()
+        with warnings.catch_warnings(record=True) as caught:
+            warnings.simplefilter("always")
+            ra, rb = a.train_step(batch), b.train_step(batch)
+            torch.cuda.synchronize()
+        # the step results hold no autograd graph, so no gradient accumulator outlives its step
+        assert not [w for w in caught if "AccumulateGrad" in str(w.message)], step
         la, lb = float(ra.loss.detach()), float(rb.loss)
         assert math.isfinite(la) and abs(la - lb) <= 1e-4 * max(abs(la), 1.0), (step, la, lb)
         assert bool(ra.metrics["stepped"]) and bool(rb.metrics["stepped"])
@@ -249,3 +254,36 @@ def test_cfg5_shortlist_step():
     assert losses[-1] < losses[0], losses
     sl = res.model_output.meta.shortlist
     assert sl is not None and sl.shortlist.shape[-1] == cfg.output.shortlist_max_tokens
+
+
+def test_cfg3_side_stream_audit_gradients_match_main_stream():
+    """gradient_corrected audit whose exact replay runs on a side stream (the replay selects h0 rows
+    there, and their gradient is added into h0's on the main stream by a hook): every parameter
+    gradient of one step equals, to fp32 summation order, the same step with the replay on the
+    main stream.  Guards the cross-stream hand-over of the selected rows' gradient."""
+    import bench
+
+    cfg = bench.cfg3_config(batch=16)
+    assert cfg.training.audit_mode == "gradient_corrected"
+    eng = _engine_from(cfg)
+    gen = torch.Generator().manual_seed(7)
+    tok, tgt = bench.zipf_batch(gen, cfg.model.vocab_size, 16, 64, DEV)
+    grads = []
+    for streams in (True, False, True):
+        print(f"side-stream audit step, audit_streams={streams}", flush=True)
+        eng.audit_streams = streams
+        eng._bf16.begin()
+        loss, *_ = eng._macro_loss(tok, tgt, shortlist=False)
+        loss.backward()
+        eng._bf16.end()
+        torch.cuda.synchronize()
+        grads.append({n_: p.grad.detach().clone() for n_, p in eng.recursive_model.named_parameters()
+                      if p.grad is not None})
+        eng.optimizer.zero_grad(set_to_none=True)
+    side, main, side2 = grads
+    assert set(side) == set(main) and any(n_.startswith("embed") for n_ in side)
+    for n_ in main:
+        ref = main[n_]
+        err = float((side[n_] - ref).norm() / ref.norm().clamp_min(1e-30))
+        assert err <= 1e-5, (n_, err)
+        assert torch.equal(side[n_], side2[n_]), n_

@@ -53,3 +53,32 @@ def test_select_rows_no_grad_and_leaf_fall_back():
     assert hip_ops.select_rows(w, ix).grad_fn.name().startswith("IndexSelect")
     with torch.no_grad():
         assert hip_ops.select_rows(w * 2, ix).grad_fn is None
+
+
+@pytest.mark.parametrize("a_first", [True, False])
+def test_select_rows_pass_through_gradient_not_written(a_first):
+    """The source's other consumer is a residual add, whose backward hands the same gradient
+    tensor to both of its inputs: adding the selected rows must not write into it, or the other
+    input's gradient would carry them too (it does when the sibling's backward runs after the
+    hook, i.e. when the source is created last)."""
+    def run(select):
+        torch.manual_seed(1)
+        wa = torch.randn(5, 4, requires_grad=True)
+        wb = torch.randn(5, 4, requires_grad=True)
+        if a_first:  # non-leaf sources, in both creation orders
+            a = wa * 2.0
+            b = wb * 3.0
+        else:
+            b = wb * 3.0
+            a = wa * 2.0
+        z = a + b                   # AddBackward passes one gradient to a and b
+        loss = (z * torch.randn(5, 4)).sum()
+        sel = select(a, torch.tensor([1, 3]))
+        loss = loss + (sel * sel).sum()
+        loss.backward()
+        return wa.grad.clone(), wb.grad.clone()
+
+    ga_ref, gb_ref = run(lambda x, i: x.index_select(0, i))
+    ga, gb = run(hip_ops.select_rows)
+    assert torch.allclose(ga, ga_ref, rtol=1e-6, atol=1e-6)
+    assert torch.equal(gb, gb_ref)
