@@ -10,7 +10,8 @@ seeded data, random-init weights.  One step = forward_macro + audit correction +
 Prints ONE JSON line.  Also reports the roofline of the operation that takes the most time per
 step (every candidate timed live with HIP events on the launch stream, its HBM traffic from two
 rocprofv3 --pmc runs of this script calibrated against a copy kernel) and a CPU baseline (the
-cfg3 step ported to torch on this host's cores, float32, on a bounded batch sample).
+reference's cfg3 step restated in float32 torch on this host's cores, on a bounded batch sample,
+and the cfg1 cluster-pool layer in the reference's two CPU forms).
 """
 
 from __future__ import annotations
@@ -18,6 +19,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -577,40 +579,84 @@ def _cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(budget_s: float = 20.0) -> dict:
-    """The cfg3 recursive_macro train step ported to torch on the host CPU in float32 (the CPU
-    path of the same workload: forward, audit replay, consistency and distillation terms,
-    backward, AdamW), on a batch sample sized so the timed steps take about budget_s."""
+def _cpu_threads() -> tuple[int, int]:
+    """(threads used, os.cpu_count()): the host cores this process may use -- its CPU affinity,
+    capped by OMP_NUM_THREADS when the box sets it to this job's share of the host."""
+    total = os.cpu_count() or 1
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except AttributeError:
+        avail = total
+    omp = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    return (min(avail, omp) if omp > 0 else avail), total
+
+
+def _median_time(fn, warmup: int, iters: int) -> float:
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(iters):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def cpu_baseline(step_budget_s: float = 16.0, warmup: int = 2, iters: int = 10) -> dict:
+    """The reference's CPU path, timed on the host cores (median of `iters` timed runs after
+    `warmup` untimed ones, rte/cli.py:7755-7760): the cfg3 recursive_macro train step restated in
+    float32 torch (oracle/step_port.py: forward, exact replay of the audited sample with the
+    control-variate correction, consistency and distillation terms, backward, AdamW) on a batch
+    sample sized so the timed steps take about step_budget_s (rows are independent), and the
+    cfg1 cluster-pool layer forward + backward in both of the reference's forms
+    (oracle/pool_port.py: per-cluster loop and preindexed bmm) at its full size."""
     import torch
 
+    import rte_amd.models as RM
+    from oracle import pool_port as PP
     from oracle import step_port as SP
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(os.cpu_count() or 1, 16)
+    threads, total = _cpu_threads()
     torch.set_num_threads(threads)
     S = 64
-    p = SP.make_params(0)
-    opt = SP.make_optimizer(p)
-    tok, tgt = SP.zipf_tokens(8, S, 1)
-    SP.train_step(p, opt, tok, tgt)  # warm-up
+
+    def make(B):
+        cfg = cfg3_config(batch=B, seq=S)
+        torch.manual_seed(cfg.training.seed)
+        m = RM.RecursiveModel(cfg.model, cfg.output)
+        port = SP.StepPort(cfg, dict(m.named_parameters()), dict(m.named_buffers()))
+        opt = SP.make_optimizer(port)
+        tok, tgt = SP.zipf_tokens(cfg.model.vocab_size, B, S, seed=1)
+        usage = torch.zeros(cfg.model.recipe_count)
+        chosen = torch.zeros(1, dtype=torch.long)
+        return lambda: SP.train_step(port, opt, tok, tgt, chosen=chosen, usage_ema=usage)
+
+    probe = make(8)
+    probe()
     t0 = time.perf_counter()
-    SP.train_step(p, opt, tok, tgt)
+    probe()
     per_sample = (time.perf_counter() - t0) / 8
-    B = int(max(8, min(128, budget_s / 2 / max(per_sample, 1e-9))))
-    tok, tgt = SP.zipf_tokens(B, S, 2)
-    times = []
-    for _ in range(2):
-        t0 = time.perf_counter()
-        SP.train_step(p, opt, tok, tgt)
-        times.append(time.perf_counter() - t0)
-    best = min(times)
+    B = int(max(8, min(128, step_budget_s / iters / max(per_sample, 1e-9))))
+    step_s = _median_time(make(B), warmup, iters)
+    x, wr, wup, wgate, wdown = PP.make_cfg1()
+    dy = torch.randn(x.shape, generator=torch.Generator().manual_seed(1))
+    layer = {}
+    for name, form in (("loop", PP.layer_loop), ("preindexed", PP.layer_preindexed)):
+        t = _median_time(lambda: PP.fwd_bwd(form, x, wr, wup, wgate, wdown, dy, 4, 32), warmup, iters)
+        layer[name] = {"tokens_per_s": round(x.shape[0] / t, 1), "ms": round(t * 1e3, 2)}
     return {
-        "value": round(B * S / best, 1),
+        "value": round(B * S / step_s, 1),
         "unit": "tokens/s",
         "cores": threads,
         "kind": "port",
         "cpu": _cpu_model(),
-        "sample": f"fp32 torch-CPU port of the cfg3 recursive_macro step (oracle/step_port.py), batch {B} of 128 "
-                  f"x seq {S} (rows independent), faster of 2 timed steps after a warm-up; {threads} threads",
+        "host_cpu_count": total,
+        "sample": (f"fp32 torch-CPU restatement of the cfg3 recursive_macro step (oracle/step_port.py), batch {B} of "
+                   f"128 x seq {S} (rows independent), median of {iters} timed steps after {warmup} warm-ups; "
+                   f"{threads} threads (this job's share of the host's {total})"),
+        "cfg1_layer": {"workload": "BASELINE configs[0]: cluster-pool SwiGLU layer fwd+bwd, T 8192, d 256, "
+                                  "32 x 32 neurons, top-4, fp32 (oracle/pool_port.py)",
+                       "median_of": iters, **layer},
     }
 
 

@@ -37,7 +37,19 @@ How each function is pinned (tests/test_oracle.py):
   banked.recipe_templates    two hand-enumerated recipe tables (every recipe's banks and
                              groups) with zero balance spread; recipe 0 == dense bank
 
-step_port is not a checker: it is the CPU path of the benchmark's workload (the cfg3 train step
-in float32 torch on the host) that bench.py's cpu_baseline leg times; its test only checks that it
-runs and updates the parameters (parity unpinned: it is never compared with the GPU step).
+  step_port.StepPort         the whole recursive_macro step (tests/test_step_port.py): its loss,
+                             term by term (corrected CE, every distillation term, consistency,
+                             router load / cover / depth), equals a composition of the functions
+                             above (attention, routed pool, router, bounded_apply, banked core,
+                             cross_entropy, audit.correction, distill.distill) on a small model
+                             with per-sample depths, to 1e-6; its gradients equal central
+                             finite differences of its own loss (float64) on 40 entries of 20
+                             parameters of every kind, with the step's decisions and the
+                             distillation's detached operands held fixed.  It is the checker of
+                             the GPU step (tests/test_gpu_step_parity.py) and the cfg3 CPU
+                             baseline bench.py times.
+  pool_port.layer_*          the cfg1 layer's two CPU forms (per-cluster loop, preindexed bmm):
+                             outputs equal cluster_pool.routed_fwd on the same routing; the two
+                             forms' gradients agree and match finite differences
+                             (tests/test_pool_port.py).  Timed as the cfg1 CPU baseline.
 """

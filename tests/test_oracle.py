@@ -1128,18 +1128,30 @@ def test_svd_sparse_backward_matches_autograd():
 
 
 def test_step_port_runs_and_updates():
-    """The CPU step port that bench.py times as its baseline: one step on 2 samples gives a
-    finite loss and moves the parameters the step reaches (Phi, core, coda, embedding)."""
+    """The CPU step that bench.py times as its baseline: one AdamW step at a small cfg3-shaped
+    model gives a finite loss and moves the parameters the step reaches (Phi, core, coda,
+    embedding, prelude)."""
     import torch
 
     from oracle import step_port as SP
+    from rte_amd.config import ExperimentConfig, ModelConfig, OutputConfig, TrainingConfig
+    from rte_amd.models import RecursiveModel
 
+    mc = ModelConfig(topology="recursive", vocab_size=64, d_model=64, n_heads=2, d_ff=256, n_dense_layers=2,
+                     n_prelude=1, n_coda=1, t_max=4, depth_choices=[1, 2, 4], attn_banks=1, ffn_banks=1,
+                     head_groups=2, ffn_groups=8, active_head_groups=1, active_ffn_groups=2, recipe_count=4,
+                     macro_rank=8, ffn_kind="cluster_pool", ffn_clusters=8, ffn_top_k=2)
+    tc = TrainingConfig(mode="recursive_macro", batch_size=2, seq_len=16, audit_sampler="fixed_count",
+                        audit_fixed_count=1, fixed_depth=4)
+    cfg = ExperimentConfig(model=mc, training=tc, output=OutputConfig())
     torch.manual_seed(0)
-    p = SP.make_params(0)
-    before = {k: v.detach().clone() for k, v in p.items()}
-    opt = SP.make_optimizer(p)
-    tok, tgt = SP.zipf_tokens(2, 16, 1)
-    loss = SP.train_step(p, opt, tok, tgt)
+    m = RecursiveModel(mc, cfg.output)
+    port = SP.StepPort(cfg, dict(m.named_parameters()), dict(m.named_buffers()))
+    before = {k: v.detach().clone() for k, v in port.params(False).items()}
+    opt = SP.make_optimizer(port)
+    tok, tgt = SP.zipf_tokens(64, 2, 16, seed=1)
+    loss = SP.train_step(port, opt, tok, tgt, chosen=torch.tensor([1]), usage_ema=torch.zeros(4))
     assert np.isfinite(loss)
-    for k in ("m.v", "core.wqkv", "coda.wug", "embed", "pre.wqkv"):
-        assert not torch.equal(before[k], p[k].detach()), k
+    after = port.params(False)
+    for k in ("macro.v", "core.attn.wqkv", "coda.0.mlp.wug.weight", "embed.weight", "prelude.0.attn.wqkv.weight"):
+        assert not torch.equal(before[k], after[k]), k
