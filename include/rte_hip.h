@@ -651,6 +651,54 @@ int rte_cast_f32_bf16(const float* x, int64_t n, void* y, void* stream);
 int rte_cast_many_blocks(int kind, int64_t rows, int64_t cols);
 int rte_cast_many(const int64_t* jobs, const int32_t* blk, int nblk, void* stream);
 
+/* ---- fp32 arithmetic: training.precision = "fp32", the reference default (rte/config.py:118),
+ * where every matmul of rte/layers.py, rte/macro.py and rte/models.py runs in float32 outside
+ * autocast (rte/training.py:356-363).  All buffers f32, fp32 accumulation. ---- */
+/* C(m,n) = alpha sum_k A(m,k) B(n,k) + beta C(m,n) on v_mfma_f32_32x32x2_f32.
+ * a_t == 0: A(m,k) = A[row(m)*lda + k]   a_t == 1: A(m,k) = A[row(k)*lda + m]   (same for B with n)
+ * row(i) = a_rows ? a_rows[i] : i; a_scale (optional) multiplies A's memory row i by a_scale[i]
+ * (same for B); c_rows (optional) scatters output row m to c_rows[m].
+ * Batch z in [0, Z1*Z2): operand X starts at X + (z / Z2) sX1 + (z % Z2) sX2 (at most 65535).
+ * Replaces torch's fp32 matmuls: nn.Linear (rte/layers.py:53-87), the SDPA products
+ * (rte/kernels/optimized.py:75-91), k_qkv_dense / k_swiglu_dense / k_logits_* (rte/kernels/reference.py). */
+int rte_gemm_f32(const float* A, int64_t lda, int a_t, const int32_t* a_rows, const float* a_scale, const float* B,
+                 int64_t ldb, int b_t, const int32_t* b_rows, const float* b_scale, float* C, int64_t ldc,
+                 const int32_t* c_rows, int M, int N, int K, float alpha, float beta, int Z1, int Z2, int64_t sA1,
+                 int64_t sA2, int64_t sB1, int64_t sB2, int64_t sC1, int64_t sC2, void* stream);
+/* Grouped form over device offsets goff[G+1] (int32).  mode 1 (rows): group g computes output rows
+ * [goff[g], goff[g+1]) of the M total with B at b_goff[g] (int64, optional) or g*b_gstride and
+ * b_rows shifted by g*b_rows_gstride: the routed / banked pools' per-cluster products and the macro
+ * operator's per-(recipe, stride) products (replacing the bmm over gathered per-sample weights of
+ * rte/macro.py:208-221 and the pooled bmm of rte/kernels/cluster_pool_ffn.py:192-215).  mode 2
+ * (reduction): group g sums k over [goff[g], goff[g+1]) into C at c_goff[g] or g*c_gstride, rows
+ * through c_rows shifted by g*c_rows_gstride: their weight gradients, one workgroup per output tile
+ * summing its group's rows in order (replacing index_add_ scatter, :218-241; deterministic). */
+int rte_gemm_f32_grouped(int mode, const int32_t* goff, int G, const float* A, int64_t lda, int a_t,
+                         const int32_t* a_rows, const float* a_scale, const float* B, int64_t ldb, int b_t,
+                         const int32_t* b_rows, const float* b_scale, const int64_t* b_goff, int64_t b_gstride,
+                         int64_t b_rows_gstride, float* C, int64_t ldc, const int32_t* c_rows, const int64_t* c_goff,
+                         int64_t c_gstride, int64_t c_rows_gstride, int M, int N, int K, float alpha, float beta,
+                         void* stream);
+/* Causal softmax of score rows s [Z, S, S] (F.scaled_dot_product_attention(is_causal=True)'s
+ * softmax, rte/kernels/optimized.py:75-91): p = softmax(scale s) over keys <= query, y = oscale[z] p
+ * (oscale optional: the banked recipe's head mask, rte/layers.py:702-728).  rows = Z*S. */
+int rte_softmax_causal_f32_fwd(const float* s, int64_t rows, int S, float scale, const float* oscale, float* p,
+                               float* y, void* stream);
+/* ds = scale p (g - sum p g) with g = oscale[z] dy */
+int rte_softmax_causal_f32_bwd(const float* p, const float* dy, int64_t rows, int S, float scale,
+                               const float* oscale, float* ds, void* stream);
+/* z = up silu(gate) over rows [up (n) | gate (n)] of width ld (rte/layers.py:78-87), and its
+ * backward (rte/kernels/active_swiglu_triton.py:87-102) into dug with the same layout. */
+int rte_swiglu_f32_fwd(const float* ug, int64_t rows, int n, int64_t ld, float* z, void* stream);
+int rte_swiglu_f32_bwd(const float* ug, const float* dz, int64_t rows, int n, int64_t ld, float* dug, void* stream);
+/* out[t] = resid[t] + sum_j w[t,j] rows[slot[t k + j]] in j order (slot < 0: no pair; w, resid
+ * optional): the pooled FFN's gather back to tokens (rte/kernels/cluster_pool_ffn.py:215). */
+int rte_combine_f32(const float* rows, const int32_t* slot, const float* w, int T, int k, int d, const float* resid,
+                    float* out, void* stream);
+/* dw[p] = dout[p / k] . rows[slot[p]] (0 for slot < 0): the routing weights' gradient. */
+int rte_pair_dot_f32(const float* dout, const float* rows, const int32_t* slot, int64_t pairs, int k, int d, float* dw,
+                     void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -71,7 +71,7 @@ def causal_attention(q, k, v):
     """softmax(q k^T / sqrt(hd), causal) v  (F.scaled_dot_product_attention(is_causal=True))."""
     S = q.shape[-2]
     s = q @ k.transpose(-1, -2) / math.sqrt(q.shape[-1])
-    s = s.masked_fill(~torch.ones(S, S, dtype=torch.bool).tril(), float("-inf"))
+    s = s.masked_fill(~torch.ones(S, S, dtype=torch.bool, device=q.device).tril(), float("-inf"))
     return s.softmax(dim=-1) @ v
 
 

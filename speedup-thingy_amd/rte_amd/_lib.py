@@ -121,6 +121,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_step_metrics": (_I, [_P, _P, _P, _I, _F, _F, _P, _P]),
     "rte_mse_workspace_bytes": (_SZ, [_I64]),
     "rte_mse_fwd": (_I, [_P, _P, _I64, _P, _P, _SZ, _P]),
+    "rte_gemm_f32": (_I, [_P, _I64, _I, _P, _P, _P, _I64, _I, _P, _P, _P, _I64, _P, _I, _I, _I, _F, _F, _I, _I,
+                          _I64, _I64, _I64, _I64, _I64, _I64, _P]),
+    "rte_gemm_f32_grouped": (_I, [_I, _P, _I, _P, _I64, _I, _P, _P, _P, _I64, _I, _P, _P, _P, _I64, _I64, _P, _I64,
+                                  _P, _P, _I64, _I64, _I, _I, _I, _F, _F, _P]),
+    "rte_softmax_causal_f32_fwd": (_I, [_P, _I64, _I, _F, _P, _P, _P, _P]),
+    "rte_softmax_causal_f32_bwd": (_I, [_P, _P, _I64, _I, _F, _P, _P, _P]),
+    "rte_swiglu_f32_fwd": (_I, [_P, _I64, _I, _I64, _P, _P]),
+    "rte_swiglu_f32_bwd": (_I, [_P, _P, _I64, _I, _I64, _P, _P]),
+    "rte_combine_f32": (_I, [_P, _P, _P, _I, _I, _I, _P, _P, _P]),
+    "rte_pair_dot_f32": (_I, [_P, _P, _P, _I64, _I, _I, _P, _P]),
     "rte_mse_bwd": (_I, [_P, _P, _I64, _P, _P, _P, _P]),
     "rte_pack_routes_workspace_bytes": (_SZ, [_I, _I]),
     "rte_pack_routes": (_I, [_P, _P, _I, _I, _P, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P, _SZ, _P]),

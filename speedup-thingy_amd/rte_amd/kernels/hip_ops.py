@@ -14,6 +14,8 @@ from __future__ import annotations
 
 import ctypes
 import math
+import threading
+from contextlib import contextmanager
 from dataclasses import dataclass
 
 import torch
@@ -23,6 +25,32 @@ from rte_amd._lib import call, ptr
 
 BF16 = torch.bfloat16
 F32 = torch.float32
+
+_PRECISION = threading.local()
+
+
+def fp32_active() -> bool:
+    """True inside a fp32_precision() block: the model's operators then compute in fp32 on the
+    fp32 kernels (rte_amd.kernels.f32_ops) instead of taking bf16 GEMM operands."""
+    return getattr(_PRECISION, "fp32", False)
+
+
+@contextmanager
+def fp32_precision(enabled: bool = True):
+    """training.precision = "fp32" (the reference's default, rte/config.py:118): every operator
+    called inside runs its products with fp32 operands and accumulation."""
+    prev = fp32_active()
+    _PRECISION.fp32 = bool(enabled)
+    try:
+        yield
+    finally:
+        _PRECISION.fp32 = prev
+
+
+def _f32():
+    from rte_amd.kernels import f32_ops
+
+    return f32_ops
 
 
 def _s() -> int:
@@ -290,6 +318,8 @@ class RMSNormFn(torch.autograd.Function):
 
 
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    if fp32_active():
+        return FusedRMSNormFn.apply(x.float(), w, None, eps)[0]
     return RMSNormFn.apply(x, w, eps)
 
 
@@ -334,6 +364,9 @@ class RMSNormResidFn(torch.autograd.Function):
 
 def rmsnorm_resid(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5) -> tuple[torch.Tensor, torch.Tensor]:
     """(bf16 rmsnorm(x) * w, fp32 x for the residual add): one gradient for x."""
+    if fp32_active():
+        x = x.float()
+        return FusedRMSNormFn.apply(x, w, None, eps)[0], x
     return RMSNormResidFn.apply(x, w, eps)
 
 
@@ -399,13 +432,36 @@ class AxpyNormFn(torch.autograd.Function):
                 dparams[2 * d:3 * d] if nia[7] else None, None)
 
 
+def _axpy_norm_f32(a, b, c, w, gamma, beta, eps, keep, mask):
+    """fp32 composite of axpy_norm: x = a + c b (masked samples keep `keep`), n = rmsnorm(x) w
+    (1 + gamma) + beta on the fp32 norm kernel."""
+    x = a.float()
+    if b is not None:
+        x = x + (b.float() if c is None else c.float() * b.float())
+    if mask is not None:
+        m = mask.reshape(-1, *([1] * (x.dim() - 1))).to(torch.bool)
+        x = torch.where(m, x, keep.float())
+    if w is None:
+        return x, None
+    n = FusedRMSNormFn.apply(x, w, None, eps)[0]
+    if gamma is not None:
+        n = n * (1.0 + gamma.float())
+    if beta is not None:
+        n = n + beta.float()
+    return x, n
+
+
 def axpy_norm(a, b, c, w, gamma=None, beta=None, eps: float = 1e-5, *, keep=None, mask=None):
     """(x, n): x = a + c b (fp32), n = bf16(rmsnorm(x) w (1 + gamma) + beta)."""
+    if fp32_active():
+        return _axpy_norm_f32(a, b, c, w, gamma, beta, eps, keep, mask)
     return AxpyNormFn.apply(a, b, c, keep, mask, w, gamma, beta, eps)
 
 
 def axpy(a, b, c, *, keep=None, mask=None):
     """x = a + c b (fp32); with mask [B], samples whose mask is False take keep's rows."""
+    if fp32_active():
+        return _axpy_norm_f32(a, b, c, None, None, None, 0.0, keep, mask)[0]
     return AxpyNormFn.apply(a, b, c, keep, mask, None, None, None, 0.0)[0]
 
 
@@ -619,6 +675,8 @@ class AttnOutProjFn(torch.autograd.Function):
 
 
 def attn_out_proj(y, w, resid=None, wgrad: SharedWGrad | None = None):
+    if fp32_active():
+        return _f32().attn_out_proj(y, w, resid)
     return AttnOutProjFn.apply(y, w, resid, wgrad)
 
 
@@ -661,6 +719,9 @@ class AttentionFn(torch.autograd.Function):
 
 
 def attention(q, k, v, head_scale=None):
+    if fp32_active():  # [B, H, S, hd] view of the token-major fp32 attention output
+        B, Hh, S, hd = q.shape
+        return _f32().AttentionFn.apply(q, k, v, head_scale).view(B, S, Hh, hd).transpose(1, 2)
     if head_scale is not None and head_scale.requires_grad:
         raise ValueError("attention: head_scale carries no gradient")
     return AttentionFn.apply(q, k, v, head_scale)
@@ -732,6 +793,8 @@ class QKVRopeAttentionFn(torch.autograd.Function):
 def qkv_rope_attention(x, w, cos, sin, n_heads, head_scale=None, wgrad: SharedWGrad | None = None):
     """[B, H, S, hd] view of the token-major attention output of x's fused QKV + RoPE; wgrad (optional)
     shares one weight-gradient GEMM among the calls of a forward that use w."""
+    if fp32_active():
+        return _f32().qkv_rope_attention(x, w, cos, sin, n_heads, head_scale)
     if head_scale is not None and head_scale.requires_grad:
         raise ValueError("qkv_rope_attention: head_scale carries no gradient")
     return QKVRopeAttentionFn.apply(x, w, cos, sin, n_heads, head_scale, wgrad)
@@ -786,6 +849,8 @@ class DenseSwiGLUFn(torch.autograd.Function):
 def dense_swiglu(x, wug, wd, resid=None, *, wd_rows: bool = False, out_f32: bool = True):
     """resid + (up * silu(gate)) @ W_down; a width F that is not a multiple of 32 (the kernels'
     column block) is padded with zero neurons, which contribute nothing and get no gradient."""
+    if fp32_active():
+        return _f32().dense_swiglu(x, wug, wd, resid, wd_rows=wd_rows)
     F = wug.shape[0] // 2
     pad = (-F) % 32
     if pad:
@@ -1023,6 +1088,8 @@ class RoutedClusterPoolFn(torch.autograd.Function):
 
 def routed_cluster_pool_swiglu(x, wr, wug, wd, k: int, resid=None):
     """Returns (out, ids, weights); ids/weights are the routing decisions (no gradient)."""
+    if fp32_active():
+        return _f32().routed_cluster_pool_swiglu(x, wr, wug, wd, k, resid)
     return RoutedClusterPoolFn.apply(x, wr, wug, wd, resid, k)
 
 
@@ -1088,6 +1155,8 @@ def grouped_pool_swiglu(x, ids, w, wug_t, wd_t, n: int, resid=None, pk: PackInde
     """Grouped pool SwiGLU over the routes ids / w [T, k], or over a prebuilt pack pk (then ids
     and w are not read).  acc (optional): the calls of a forward that share these weights sum
     their weight gradients in one pair of buffers."""
+    if fp32_active():
+        return _f32().grouped_pool_swiglu(x, ids, w, wug_t, wd_t, n, resid, pk)
     return GroupedPoolFn.apply(x, ids, w, wug_t, wd_t, resid, n, pk, acc)
 
 
@@ -1123,6 +1192,8 @@ class LinearFn(torch.autograd.Function):
 
 
 def linear(x, w, *, out_f32: bool = True):
+    if fp32_active():
+        return _f32().linear(x, w)
     return LinearFn.apply(x, w, out_f32)
 
 
@@ -1164,6 +1235,8 @@ class LinearBiasFn(torch.autograd.Function):
 
 
 def linear_bias(x, w, b, *, out_f32: bool = True):
+    if fp32_active():
+        return _f32().linear(x, w, b)
     return LinearBiasFn.apply(x, w, b, out_f32)
 
 
@@ -1273,6 +1346,9 @@ def router(h0, w1r, b1r, w2r, b2r, w1d, b1d, w2d, b2d, pass_bias, depth_values, 
            fixed_recipe: int | None = None, fixed_depth: int | None = None) -> dict[str, torch.Tensor]:
     """The router's recipe / depth fields (ROUTER_FIELDS) from h0 [B, S, d]; fixed_depth is an
     index into depth_values."""
+    if fp32_active():
+        return _f32().router(h0, w1r, b1r, w2r, b2r, w1d, b1d, w2d, b2d, pass_bias, depth_values,
+                             inv_t=inv_t, fixed_recipe=fixed_recipe, fixed_depth=fixed_depth)
     out = RouterFn.apply(h0, w1r, b1r, w2r, b2r, w1d, b1d, w2d, b2d, pass_bias, depth_values, float(inv_t),
                          -1 if fixed_recipe is None else int(fixed_recipe),
                          -1 if fixed_depth is None else int(fixed_depth))
@@ -1386,6 +1462,8 @@ class LMHeadCEFn(torch.autograd.Function):
 
 def lm_head_ce(hidden, w, targets):
     """(logits fp32, per-token cross-entropy) of hidden @ W^T against targets."""
+    if fp32_active():
+        return _f32().lm_head_ce(hidden, w, targets)
     return LMHeadCEFn.apply(hidden, w, targets)
 
 
@@ -1844,6 +1922,8 @@ def _whole_param(t: torch.Tensor) -> bool:
 def macro_fused_supported(v: torch.Tensor, u: torch.Tensor, repeats: int = 1) -> bool:
     """Shapes the fused operator kernels take: hidden rank 32, d a multiple of 128 up to 1024,
     at most 8 repeats of a source sample."""
+    if fp32_active():
+        return False
     d = u.shape[-1]
     return (v.shape[-1] == MACRO_FUSED_RANK and u.shape[-2] == MACRO_FUSED_RANK and v.shape[-2] == 3 * d
             and d % 128 == 0 and 128 <= d <= 1024 and 1 <= repeats <= 8)
@@ -2148,6 +2228,8 @@ def mse(a, b):
 
 def grouped_linear(x, w, pk: PackIndex, *, out_f32: bool = True):
     """Rows of x keyed by pk's groups times their group's matrix; every key must be valid."""
+    if fp32_active():
+        return _f32().grouped_linear(x, w, pk)
     return GroupedLinearFn.apply(x, w, pk, out_f32)
 
 
@@ -2262,6 +2344,8 @@ class ShortlistCEFn(torch.autograd.Function):
 
 def shortlist_ce(hidden, w, shortlist):
     """(shortlist logits fp32 [..., L], per-token CE against position 0 [...])."""
+    if fp32_active():
+        return _f32().shortlist_ce(hidden, w, shortlist)
     return ShortlistCEFn.apply(hidden, w, shortlist)
 
 
@@ -2496,6 +2580,8 @@ class RowsLinearFn(torch.autograd.Function):
 
 
 def rows_linear(x, w, rows, out_dtype=BF16):
+    if fp32_active():  # x @ w[rows, :] on the fp32 GEMM
+        return _f32().linear(x, w.index_select(0, rows.to(device=w.device, dtype=torch.long)).t())
     return RowsLinearFn.apply(x, w, rows, out_dtype)
 
 

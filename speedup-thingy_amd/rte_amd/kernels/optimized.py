@@ -108,9 +108,13 @@ def _mm_dtype(op: str, *tensors) -> torch.dtype:
     """The matmul symbols compute with bf16 operands and fp32 accumulation, which is what the
     reference computes under bf16 autocast (its training precision "bf16"); their result is
     bf16 as there.  Float32 operands outside a bf16 autocast region would ask for fp32 matmuls,
-    which this build does not implement: refuse instead of returning bf16-accurate numbers."""
+    which this build does not implement: refuse instead of returning bf16-accurate numbers.  Inside
+    hip_ops.fp32_precision() (training.precision fp32) they compute with fp32 operands on the
+    fp32 GEMM and return fp32."""
     if torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
         return torch.bfloat16
+    if hip_ops.fp32_active():
+        return torch.float32
     floats = [t for t in tensors if isinstance(t, torch.Tensor) and t.is_floating_point()]
     if all(t.dtype == torch.bfloat16 for t in floats):
         return torch.bfloat16

@@ -16,7 +16,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from rte_amd.config import ModelConfig
-from rte_amd.gather import gather_rk, gather_rows
+from rte_amd.gather import gather_rows
 from rte_amd.kernels import hip_ops
 
 
@@ -131,7 +131,9 @@ class MacroOperators(nn.Module):
         """Per-sample rows of a [recipes, strides, d] table (deterministic backward)."""
         flat = table.reshape(-1, table.shape[-1])
         if isinstance(table, nn.Parameter) or table.requires_grad:
-            return hip_ops.embedding(flat, key)
+            if flat.shape[1] % 8 == 0 and flat.shape[1] <= 2048:  # the segmented-reduction backward
+                return hip_ops.embedding(flat, key)
+            return gather_rows(flat, key)  # narrow tables (the v2 radius): one-hot product backward
         return flat.index_select(0, key)
 
     def _fused_bounded(self) -> bool:
@@ -152,10 +154,15 @@ class MacroOperators(nn.Module):
             return hip_ops.macro_fused(h, h0, key, self.v, self.u, self.d_gain, self.bias, self.update_scale,
                                        self.config.macro_update_scale)
         pk = hip_ops.group_rows(key[:, None].expand(B, S), R * Kk)
-        if self._fused_bounded():
+        f32 = hip_ops.fp32_active()
+        if self._fused_bounded() and not f32:
             # default options: fused prologue / epilogue kernels around the two grouped GEMMs
             return hip_ops.macro_bounded(h, h0, key, pk, self.v, self.u, self.d_gain, self.bias, self.update_scale,
                                          self.config.macro_update_scale)
+        if h.shape[0] != B:  # repeated source batches: sample b reads h[b % B_h]
+            h = h.repeat(B // h.shape[0], 1, 1)
+        if h0.shape[0] != B:
+            h0 = h0.repeat(B // h0.shape[0], 1, 1)
         gain = self._rows(self.d_gain, key)
         bias = self._rows(self.bias, key)
         scale = self._rows(self.update_scale, key)
@@ -165,8 +172,10 @@ class MacroOperators(nn.Module):
             parts.append(normed - _rmsnorm(h0))
         if self.depth_embed is not None:
             parts.append(gather_rows(self.depth_embed, stride_ids).unsqueeze(1).expand_as(normed))
-        # z is a GEMM operand only: build it in bf16 (the precision autocast gives the bmm)
-        z = torch.cat([t.to(torch.bfloat16) for t in parts], dim=-1).reshape(B * S, -1)
+        # z is a GEMM operand only: build it in bf16 (the precision autocast gives the bmm), or
+        # fp32 under precision fp32
+        zdt = torch.float32 if f32 else torch.bfloat16
+        z = torch.cat([t.to(zdt) for t in parts], dim=-1).reshape(B * S, -1)
 
         def lin(x, w, out_f32=False):
             return hip_ops.grouped_linear(x, w.reshape(R * Kk, w.shape[-2], w.shape[-1]), pk, out_f32=out_f32)
@@ -184,7 +193,14 @@ class MacroOperators(nn.Module):
         return h + self.config.macro_update_scale * scale.unsqueeze(1) * gate * torch.tanh(update)
 
     def _apply_v2(self, h, h0, recipe_ids, stride_ids):
-        """rte/macro.py:238-279."""
+        """rte/macro.py:238-279.  The three (recipe, stride)-indexed products run as grouped GEMMs
+        over the rows of every sample sharing a key (no per-sample [B, in, hidden] copies of v /
+        v2 / u), their weight gradients as per-key reductions in a fixed order; rho_head's
+        per-sample dot and the normalisation are device glue."""
+        B, S, d = h0.shape
+        R, Kk = self.v.shape[0], self.v.shape[1]
+        key = recipe_ids.long() * Kk + stride_ids.long()
+        f32 = hip_ops.fp32_active()
         normed = _rmsnorm(h0)
         pooled = normed.mean(dim=1)
         parts = [normed, pooled.unsqueeze(1).expand_as(normed), h0]
@@ -194,15 +210,20 @@ class MacroOperators(nn.Module):
             parts.append(gather_rows(self.depth_embed, stride_ids).unsqueeze(1).expand_as(normed))
         if self.recipe_embed is not None:
             parts.append(gather_rows(self.recipe_embed, recipe_ids).unsqueeze(1).expand_as(normed))
-        z = torch.cat(parts, dim=-1)
-        raw = torch.bmm(F.silu(torch.bmm(F.silu(torch.bmm(z, gather_rk(self.v, recipe_ids, stride_ids))),
-                                         gather_rk(self.v2, recipe_ids, stride_ids))),
-                        gather_rk(self.u, recipe_ids, stride_ids))
-        raw = raw + gather_rk(self.bias, recipe_ids, stride_ids).unsqueeze(1)
+        zdt = torch.float32 if f32 else torch.bfloat16
+        z = torch.cat([t.to(zdt) for t in parts], dim=-1).reshape(B * S, -1)
+        pk = hip_ops.group_rows(key[:, None].expand(B, S), R * Kk)
+
+        def lin(x, w, out_f32=False):
+            return hip_ops.grouped_linear(x.to(zdt), w.reshape(R * Kk, w.shape[-2], w.shape[-1]), pk, out_f32=out_f32)
+
+        raw = lin(F.silu(lin(F.silu(lin(z, self.v)), self.v2)), self.u, out_f32=True).view(B, S, d).float()
+        raw = raw + self._rows(self.bias, key).unsqueeze(1)
         direction = raw / _rms(raw, dim=(1, 2), keepdim=True).clamp_min(1e-6)
-        rho_head = torch.bmm(pooled.unsqueeze(1), gather_rk(self.rho_head, recipe_ids, stride_ids)).squeeze(-1).squeeze(-1)
-        rho = F.softplus(gather_rk(self.rho_base_raw, recipe_ids, stride_ids) + rho_head)
-        teacher = self.teacher_delta_rms[recipe_ids, stride_ids].to(rho.device)
+        # rho_head [R, K, d, 1]: the sample's row dotted with its pooled features
+        rho_head = (pooled.float() * self._rows(self.rho_head.squeeze(-1), key)).sum(dim=-1)
+        rho = F.softplus(self._rows(self.rho_base_raw.unsqueeze(-1), key).squeeze(-1) + rho_head)
+        teacher = self.teacher_delta_rms.reshape(-1).index_select(0, key).to(rho.device)
         if self.config.macro_radius_init_from_teacher:
             has = teacher > 0
             clamped = torch.clamp(rho, min=teacher * self.config.macro_radius_clamp_mult_min,

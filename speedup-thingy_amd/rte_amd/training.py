@@ -96,13 +96,8 @@ class TrainEngine:
         tr = config.training
         if tr.mode not in ACCELERATED_MODES:
             raise NotImplementedError(f"mode {tr.mode!r} is outside the accelerated path ({sorted(ACCELERATED_MODES)})")
-        if tr.precision != "bf16":
-            # the HIP GEMMs take bf16 operands with fp32 accumulation (the reference's bf16
-            # autocast numerics); fp32 matmuls are not implemented, so refuse rather than
-            # silently train at bf16
-            raise NotImplementedError(
-                f"precision={tr.precision!r}: the MI355X kernels compute matmuls with bf16 operands "
-                "(fp32 accumulation, fp32 master weights); set training.precision: bf16")
+        if tr.precision not in ("bf16", "fp32"):
+            raise ValueError(f"precision={tr.precision!r}: expected 'fp32' or 'bf16'")
         self.device = device or torch.device("cuda")
         set_seed(tr.seed)
         if tr.strict_cuda and self.device.type != "cuda":
@@ -130,7 +125,7 @@ class TrainEngine:
         self._current_lr = tr.lr
         # start the audit replay and the consistency loss on side streams right after routing
         self.audit_streams = self.device.type == "cuda"
-        self._bf16 = hip_ops.Bf16Prefetch(enabled=self.device.type == "cuda")
+        self._bf16 = hip_ops.Bf16Prefetch(enabled=self.device.type == "cuda" and tr.precision == "bf16")
         self._graph_enabled = False
         self._graph_keep = False
         self._gstate: dict[str, Any] | None = None
@@ -177,8 +172,10 @@ class TrainEngine:
         return torch.optim.AdamW(groups, **kw)
 
     def _autocast(self):
+        """rte/training.py:356-363: bf16 autocast for precision bf16; for precision fp32 (the
+        reference default) every operator computes with fp32 operands (hip_ops.fp32_precision)."""
         if self.config.training.precision != "bf16":
-            return nullcontext()
+            return hip_ops.fp32_precision() if self.device.type == "cuda" else nullcontext()
         return torch.autocast(device_type=self.device.type, dtype=torch.bfloat16)
 
     def _lr_scale(self) -> float:
