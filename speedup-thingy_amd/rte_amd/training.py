@@ -129,6 +129,8 @@ class TrainEngine:
         self._graph_enabled = False
         self._graph_keep = False
         self._gstate: dict[str, Any] | None = None
+        # captured steps' "stepped" flags not yet read back (see reconcile_global_step)
+        self._stepped_pending: list[torch.Tensor] = []
 
     # ------------------------------------------------------------------ optimizer
     def _param_groups(self) -> list[dict[str, Any]]:
@@ -451,16 +453,20 @@ class TrainEngine:
             st["graph"].replay()
             out = st["out"]
         self.global_micro_step += 1
-        # Counted on the host without reading the device: a replay whose update was skipped (a
-        # non-finite gradient, metrics["stepped"] False) still advances global_step, unlike the
-        # eager path, which knows the outcome before counting.  Reading it here would put a
-        # device synchronisation into every captured step.
+        # Counted on the host without reading the device: reading whether the update was skipped
+        # (a non-finite loss) would synchronise every captured step.  The device flag is kept and
+        # reconcile_global_step() takes the skipped replays off the count (checkpoints call it, so
+        # a saved global_step counts applied updates as the reference's _finish_step does); until
+        # then the seeds of the following steps use the attempted-step count.
         self.global_step += 1
         self.tokens_seen += tokens.numel()
         flat = out["flat"].clone()
         metrics = dict(out["host_metrics"])
         metrics.update({name: flat[i] for i, name in enumerate(out["names"])})
         metrics["stepped"] = metrics["stepped"] > 0.5
+        self._stepped_pending.append(metrics["stepped"])
+        if len(self._stepped_pending) >= 1024:
+            self.reconcile_global_step()
         self.last_grad_metrics = {k: metrics[k] for k in out["grad_names"]}
         return TrainStepResult(flat[out["names"].index("loss")], out["hot"], metrics, out["audit"])
 
@@ -508,12 +514,23 @@ class TrainEngine:
                 "host_metrics": {k: v for k, v in metrics.items() if not isinstance(v, torch.Tensor)},
                 "grad_names": list(self.last_grad_metrics)}
 
+    def reconcile_global_step(self) -> int:
+        """Take the captured replays whose update was skipped (their "stepped" flag False) off
+        global_step, with one device read for every flag since the last call; returns the count
+        of applied updates (rte/training.py:445-468 counts only those)."""
+        if self._stepped_pending:
+            flags = torch.stack([f.reshape(()) for f in self._stepped_pending]).cpu()
+            self._stepped_pending.clear()
+            self.global_step -= int((~flags).sum())
+        return self.global_step
+
     # ------------------------------------------------------------------ checkpoint
     def save_checkpoint(self, path, *, data_cursor: int | None = None) -> None:
         """The payload of rte/training.py:1656-1676 (same keys).  The config is stored as a plain
         dict, so checkpoints written here load with torch.load(weights_only=True)."""
         from pathlib import Path
 
+        self.reconcile_global_step()
         from rte_amd.config import config_to_dict
 
         model = self.dense_model if self.dense_model is not None else self.recursive_model
@@ -550,6 +567,7 @@ class TrainEngine:
             except ValueError:
                 # a checkpoint of another parameter grouping: weights load, the optimizer starts fresh
                 pass
+        self._stepped_pending.clear()
         self.global_step = int(payload.get("global_step", 0))
         self.global_micro_step = int(payload.get("global_micro_step", 0))
         self.tokens_seen = int(payload.get("tokens_seen", 0))

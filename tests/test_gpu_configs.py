@@ -287,3 +287,37 @@ def test_cfg3_side_stream_audit_gradients_match_main_stream():
         err = float((side[n_] - ref).norm() / ref.norm().clamp_min(1e-30))
         assert err <= 1e-5, (n_, err)
         assert torch.equal(side[n_], side2[n_]), n_
+
+
+def test_captured_step_skips_nonfinite_and_reconciles_global_step(tmp_path):
+    """A captured replay whose loss is non-finite (a weight set to NaN from the host) skips the
+    update (parameters unchanged, stepped False); reconcile_global_step() and the checkpoint then
+    count applied updates only, as the eager path (rte/training.py:445-468) does."""
+    import bench
+
+    cfg = bench.cfg3_config(batch=8)
+    eng = _engine_from(cfg)
+    eng.enable_graph_capture(True)
+    m = eng.recursive_model
+    gen = torch.Generator().manual_seed(3)
+    batch = bench.zipf_batch(gen, cfg.model.vocab_size, 8, 64, DEV)
+    for step in range(4):  # two eager warm-ups, the capture, a replay
+        print(f"captured step {step}", flush=True)
+        assert bool(eng.train_step(batch).metrics["stepped"])
+    saved = m.final_norm.weight.detach().clone()
+    with torch.no_grad():
+        m.final_norm.weight.fill_(float("nan"))
+    before = {n_: p.detach().clone() for n_, p in m.named_parameters() if n_ != "final_norm.weight"}
+    res = eng.train_step(batch)
+    torch.cuda.synchronize()
+    assert not bool(res.metrics["stepped"])
+    for n_, p in m.named_parameters():
+        if n_ != "final_norm.weight":
+            assert torch.equal(before[n_], p.detach()), n_
+    with torch.no_grad():
+        m.final_norm.weight.copy_(saved)
+    assert bool(eng.train_step(batch).metrics["stepped"])
+    assert eng.global_step == 6  # attempted replays, counted without a device read
+    assert eng.reconcile_global_step() == 5
+    eng.save_checkpoint(tmp_path / "ck.pt")
+    assert torch.load(tmp_path / "ck.pt", weights_only=True)["global_step"] == 5
