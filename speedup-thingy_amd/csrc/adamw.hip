@@ -150,6 +150,10 @@ __global__ void __launch_bounds__(1024) adamw_finalize_kernel(const AdamRow* __r
 // run whatever found_inf says (the finish kernel then skips the counters and the metrics use
 // the same values as without the update).  Otherwise the finish kernel ran first: scal holds the
 // clip coefficient and the skip flag, and the step counters are already advanced.
+//
+// One pass over the chunk: each thread loads its 16 elements of p, g, m, v into registers (four
+// 16-byte loads per tensor when the chunk is whole and aligned: elements 4 t + 1024 j + 0..3),
+// forms the norm partials from the loaded p and g, updates and stores them; p and g are read once.
 template <bool NORMS>
 __global__ void __launch_bounds__(256) adamw_update_kernel(const AdamRow* __restrict__ rows,
                                                            const int32_t* __restrict__ blk,
@@ -158,34 +162,71 @@ __global__ void __launch_bounds__(256) adamw_update_kernel(const AdamRow* __rest
                                                            const float* __restrict__ found_inf,
                                                            float* __restrict__ part) {
   __shared__ float red[4];
-  const int b = blockIdx.x;
+  constexpr int kPer = kChunk / 256;  // 16 elements per thread
+  const int b = blockIdx.x, tid = threadIdx.x;
   const AdamRow r = rows[blk[2 * b]];
   const int64_t off = (int64_t)blk[2 * b + 1] * kChunk;
+  float* p = reinterpret_cast<float*>(r.p);
+  const float* g = reinterpret_cast<const float*>(r.g);
+  float* m = reinterpret_cast<float*>(r.m);
+  float* v = reinterpret_cast<float*>(r.v);
+  const bool vec = off + kChunk <= r.numel &&
+                   ((r.p | r.g | r.m | r.v) & 15) == 0;  // whole chunk, 16-byte aligned tensors
+  // element e of this thread: vec ? off + 4 (t + 256 (e / 4)) + e % 4 : off + t + 256 e
+  auto idx = [&](int e) -> int64_t {
+    return vec ? off + 4 * (tid + 256 * (e >> 2)) + (e & 3) : off + tid + 256 * e;
+  };
   bool skip;
   if constexpr (NORMS) {
-    const float* p = reinterpret_cast<const float*>(r.p);
-    const float* g = reinterpret_cast<const float*>(r.g);
-    float sg = 0.0f, sp = 0.0f;
-    for (int64_t i = off + threadIdx.x; i < off + kChunk && i < r.numel; i += 256) {
-      const float x = p[i];
-      sp += x * x;
-      if (g) {
-        const float y = g[i];
-        sg += y * y;
-      }
-    }
-    sg = bsum(sg, red);
-    sp = bsum(sp, red);
-    if (threadIdx.x == 0) {
-      part[2 * b] = sg;
-      part[2 * b + 1] = sp;
-    }
-    __syncthreads();  // every thread has read p before any is updated
     skip = found_inf && *found_inf > 0.0f;
   } else {
     skip = scal[4 * G + 1] == 0.0f;  // found_inf: no update
   }
-  if (skip || !r.g) return;
+  const bool upd = !skip && g != nullptr;
+  float pv[kPer], gv[kPer], mv[kPer], vv[kPer];
+  if (vec) {
+#pragma unroll
+    for (int j = 0; j < kPer / 4; ++j) {
+      const int64_t i = off + 4 * (tid + 256 * j);
+      const float4 a = *reinterpret_cast<const float4*>(p + i);
+      pv[4 * j] = a.x; pv[4 * j + 1] = a.y; pv[4 * j + 2] = a.z; pv[4 * j + 3] = a.w;
+      if (g) {
+        const float4 c = *reinterpret_cast<const float4*>(g + i);
+        gv[4 * j] = c.x; gv[4 * j + 1] = c.y; gv[4 * j + 2] = c.z; gv[4 * j + 3] = c.w;
+      }
+      if (upd) {
+        const float4 e = *reinterpret_cast<const float4*>(m + i);
+        const float4 f = *reinterpret_cast<const float4*>(v + i);
+        mv[4 * j] = e.x; mv[4 * j + 1] = e.y; mv[4 * j + 2] = e.z; mv[4 * j + 3] = e.w;
+        vv[4 * j] = f.x; vv[4 * j + 1] = f.y; vv[4 * j + 2] = f.z; vv[4 * j + 3] = f.w;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int64_t i = idx(e);
+      const bool in = i < r.numel;
+      pv[e] = in ? p[i] : 0.0f;
+      gv[e] = (in && g) ? g[i] : 0.0f;
+      mv[e] = (in && upd) ? m[i] : 0.0f;
+      vv[e] = (in && upd) ? v[i] : 0.0f;
+    }
+  }
+  if constexpr (NORMS) {
+    float sg = 0.0f, sp = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      sp += pv[e] * pv[e];
+      if (g) sg += gv[e] * gv[e];
+    }
+    sg = bsum(sg, red);
+    sp = bsum(sp, red);
+    if (tid == 0) {
+      part[2 * b] = sg;
+      part[2 * b + 1] = sp;
+    }
+  }
+  if (!upd) return;
   const int gi = (int)r.group;
   // scalar coefficients in double (the betas' complements and bias corrections lose about
   // 1e-5 relative when formed from float betas), applied in float
@@ -199,21 +240,37 @@ __global__ void __launch_bounds__(256) adamw_update_kernel(const AdamRow* __rest
   const float bc2_sqrt = (float)sqrt(1.0 - pow(b2_d, step_d));
   const float inv_bc2 = 1.0f / bc2_sqrt;  // once per workgroup; torch divides by bc2_sqrt
   const float coef = NORMS ? 1.0f : scal[4 * G];
-  float* p = reinterpret_cast<float*>(r.p);
-  const float* g = reinterpret_cast<const float*>(r.g);
-  float* m = reinterpret_cast<float*>(r.m);
-  float* v = reinterpret_cast<float*>(r.v);
-  for (int64_t i = off + threadIdx.x; i < off + kChunk && i < r.numel; i += 256) {
-    const float gr = g[i] * coef;
-    float x = p[i];
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const float gr = gv[e] * coef;
+    float x = pv[e];
     x -= lr_wd * x;
-    const float mi = b1 * m[i] + omb1 * gr;
-    const float vi = b2 * v[i] + omb2 * gr * gr;
+    const float mi = b1 * mv[e] + omb1 * gr;
+    const float vi = b2 * vv[e] + omb2 * gr * gr;
     const float denom = sqrtf(vi) * inv_bc2 + eps;
     x -= step_size * (mi * __builtin_amdgcn_rcpf(denom));  // hardware reciprocal (1 ulp)
-    m[i] = mi;
-    v[i] = vi;
-    p[i] = x;
+    pv[e] = x;
+    mv[e] = mi;
+    vv[e] = vi;
+  }
+  if (vec) {
+#pragma unroll
+    for (int j = 0; j < kPer / 4; ++j) {
+      const int64_t i = off + 4 * (tid + 256 * j);
+      *reinterpret_cast<float4*>(p + i) = make_float4(pv[4 * j], pv[4 * j + 1], pv[4 * j + 2], pv[4 * j + 3]);
+      *reinterpret_cast<float4*>(m + i) = make_float4(mv[4 * j], mv[4 * j + 1], mv[4 * j + 2], mv[4 * j + 3]);
+      *reinterpret_cast<float4*>(v + i) = make_float4(vv[4 * j], vv[4 * j + 1], vv[4 * j + 2], vv[4 * j + 3]);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int64_t i = idx(e);
+      if (i < r.numel) {
+        p[i] = pv[e];
+        m[i] = mv[e];
+        v[i] = vv[e];
+      }
+    }
   }
 }
 
