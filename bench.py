@@ -218,20 +218,19 @@ def kernel_candidates(B: int, S: int):
     ms = torch.ones(R3, K3, d, device=dev)
     mh = torch.randn(B, S, d, device=dev, generator=g).requires_grad_()
     rid = torch.randint(0, R3, (B,), device=dev, generator=g)
-    src_i, dst_i = torch.tensor([0, 1], device=dev), torch.tensor([1, 2], device=dev)
-    rk = rid.repeat(2) * K3
-    kb = torch.cat([rk + dst_i.repeat_interleave(B), rk + src_i.repeat_interleave(B)])
-    ks = rk + src_i.repeat_interleave(B)
+    # the first application's keys: the union of the strides, src = blocks [0, 2), dst = [1, 3)
+    kf = (rid * K3).repeat(3) + torch.arange(3, device=dev).repeat_interleave(B)
+    ks = kf[:2 * B]
 
     def macro_cons():
-        loss = hip_ops.macro_consistency(mh, kb, ks, mv, mu, mg, mb, ms, 0.1)
+        loss = hip_ops.macro_consistency(mh, kf, ks, mv, mu, mg, mb, ms, 0.1, src_lo=0, dst_lo=1)
         torch.autograd.grad(loss, [mh, mv, mu, mg, mb])
 
     # bytes of the macro consistency: forward reads h (2 reads), writes x2 (bf16 2d per source
     # row, 1 + pc sources) and both outputs, reads the first output and the MSE reference; the
     # backward reads h / first twice, the MSE operands twice per application, writes du (bf16)
     # and dh / dh0 / d_first, the weight reductions read x2, du and da once per (sample, row)
-    rows_src, rows_both, rows_tw = T, 4 * T, 2 * T
+    rows_src, rows_both, rows_tw = T, 3 * T, 2 * T
     f4, b2 = 4.0 * d, 2.0 * d
     macro_bytes = (rows_src * (2 * f4 + 2 * b2) + rows_both * f4
                    + rows_tw * (f4 + 2 * b2 + f4 + f4)

@@ -407,8 +407,9 @@ int rte_macro_table_grad(const int64_t* key, int B, int seq, int n_keys, int d, 
  *         [B, seq, d]) also mse_part f32 [B * tiles] = per-tile sums of (out - mse_ref)^2, tiles =
  *         rte_macro_fused_tiles(seq); workspace rte_macro_fused_fwd_workspace_bytes(B_h, seq, d).
  * sum   : out[0] = inv_n * sum of part[0, n) in a fixed order.
- * bwd   : upstream gradient: samples b < nsplit take mul * g[0] * (dout_p - dout_q)[b], the others
- *         dout[b - nsplit].  Writes du bf16 [B*seq, d], da bf16 [B*seq, 32], part_tab f32
+ * bwd   : upstream gradient of sample b: mul * g[0] * (dout_p - dout_q)[b - diff_lo] for b in
+ *         [diff_lo, diff_lo + n_diff), plus dout[b - dout_lo] for b in [dout_lo, dout_lo + n_dout)
+ *         (the ranges may overlap; a sample in neither has gradient 0).  Writes du bf16 [B*seq, d], da bf16 [B*seq, 32], part_tab f32
  *         [B, tiles, 3, d] (du h | du | dout c tanh column sums), part_da f32 [B, tiles, 32], da_sum bf16
  *         [B, 32] (sum over the sample's rows of da), dh f32
  *         [B_h, seq, d] (all repeats added in repeat order; with dh0_into_dh the h0 gradient too;
@@ -432,8 +433,8 @@ int rte_macro_fused_fwd(const float* h, const float* h0, int B_h, int B_h0, cons
                         float* a, void* sa, float* out, const float* mse_ref, float* mse_part, void* workspace,
                         size_t workspace_bytes, void* stream);
 int rte_macro_fused_sum(const float* part, int n, float inv_n, float* out, void* stream);
-int rte_macro_fused_bwd(const float* dout_p, const float* dout_q, const float* g, float mul, int nsplit,
-                        const float* dout, const float* h, const float* rstd, const void* x2, int B_h,
+int rte_macro_fused_bwd(const float* dout_p, const float* dout_q, const float* g, float mul, int diff_lo,
+                        int n_diff, const float* dout, int dout_lo, int n_dout, const float* h, const float* rstd, const void* x2, int B_h,
                         const int64_t* key, int B, int seq, int d, int n_keys, const float* a, const void* sa,
                         const void* v_b, const void* vc_t, const void* v2_t, const void* u_b, const void* u_t,
                         const float* gain, const float* bias, const float* scale, float c, void* du, void* da,

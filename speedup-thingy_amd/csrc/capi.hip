@@ -76,7 +76,8 @@ int macro_fused_fwd(const float* h, const float* h0, int Bh, int Bh0, const int6
                     const float* scale, float c, bf16* x2, float* rstd, bf16* pooled, float* P, float* a, bf16* sa,
                     float* out, const float* mse_ref, float* mse_part, void* ws, size_t ws_bytes, hipStream_t s);
 int macro_fused_sum(const float* part, int n, float inv_n, float* out, hipStream_t s);
-int macro_fused_bwd(const float* dp, const float* dq, const float* g, float mul, int nsplit, const float* dbuf,
+int macro_fused_bwd(const float* dp, const float* dq, const float* g, float mul, int diff_lo, int n_diff,
+                    const float* dbuf, int buf_lo, int n_buf,
                     const float* h, const float* rstd, const bf16* x2, int Bh, const int64_t* key, int B, int S, int d,
                     int G, const float* a, const bf16* sa, const bf16* Vb, const bf16* VcT, const bf16* V2T,
                     const bf16* Ub, const bf16* UT, const float* gain, const float* bias, const float* scale, float c,
@@ -993,15 +994,15 @@ int rte_macro_fused_sum(const float* part, int n, float inv_n, float* out, void*
   return macro_fused_sum(part, n, inv_n, out, S(stream));
 }
 
-int rte_macro_fused_bwd(const float* dout_p, const float* dout_q, const float* g, float mul, int nsplit,
-                        const float* dout, const float* h, const float* rstd, const void* x2, int B_h,
+int rte_macro_fused_bwd(const float* dout_p, const float* dout_q, const float* g, float mul, int diff_lo,
+                        int n_diff, const float* dout, int dout_lo, int n_dout, const float* h, const float* rstd, const void* x2, int B_h,
                         const int64_t* key, int B, int seq, int d, int n_keys, const float* a, const void* sa,
                         const void* v_b, const void* vc_t, const void* v2_t, const void* u_b, const void* u_t,
                         const float* gain, const float* bias, const float* scale, float c, void* du, void* da,
                         float* part_tab, float* part_da, float* dh, float* dh0, int dh0_into_dh, const float* extra,
                         int n_extra, void* da_sum, void* workspace, size_t workspace_bytes, void* stream) {
   auto cb = [](const void* p) { return reinterpret_cast<const bf16*>(p); };
-  return macro_fused_bwd(dout_p, dout_q, g, mul, nsplit, dout, h, rstd, cb(x2), B_h, key, B, seq, d, n_keys, a, cb(sa),
+  return macro_fused_bwd(dout_p, dout_q, g, mul, diff_lo, n_diff, dout, dout_lo, n_dout, h, rstd, cb(x2), B_h, key, B, seq, d, n_keys, a, cb(sa),
                          cb(v_b), cb(vc_t), cb(v2_t), cb(u_b), cb(u_t), gain, bias, scale, c, B16(du), B16(da), part_tab,
                          part_da, dh, dh0, dh0_into_dh, extra, n_extra, B16(da_sum), workspace, workspace_bytes,
                          S(stream));

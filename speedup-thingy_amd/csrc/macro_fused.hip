@@ -133,30 +133,36 @@ __device__ __forceinline__ void st8b(bf16* p, const float* v) {
 
 __device__ __forceinline__ int64_t clamp_key(int64_t k, int G) { return k < 0 ? 0 : (k >= G ? G - 1 : k); }
 
-// Upstream gradient of the operator's output: plain (buf), or for samples b < nsplit the
-// scaled difference coef (p - q) of two saved tensors (the MSE of the consistency loss, coef =
-// mul * g[0] read on the device).  Sample b >= nsplit reads buf row block b - nsplit.
+// Upstream gradient of the operator's output, per sample b: coef (p - q) row block b - diff_lo
+// of two saved tensors when b lies in [diff_lo, diff_lo + n_diff) (the MSE of the consistency
+// loss, coef = mul * g[0] read on the device), plus buf row block b - buf_lo when b lies in
+// [buf_lo, buf_lo + n_buf); 0 for a sample in neither range.  The ranges may overlap (an
+// operator application shared by both roles of the consistency loss).
 struct DoutDesc {
   const float* p;
   const float* q;
   const float* g;
   float mul;
-  int nsplit;
+  int diff_lo, n_diff;
   const float* buf;
+  int buf_lo, n_buf;
 };
 
-// The upstream gradient rows of sample b from row s0 on: g(off) = diff ? coef (p[off] - q[off]) : p[off]
+// The upstream gradient rows of sample b from row s0 on
 struct DoutRows {
   const float* p;
   const float* q;
-  bool diff;
+  const float* buf;
+  bool diff, has_buf;
 };
 
 __device__ __forceinline__ DoutRows dout_rows(const DoutDesc& dd, int64_t b, int64_t sd, int64_t start) {
   DoutRows r;
-  r.diff = b < dd.nsplit;
-  r.p = r.diff ? dd.p + b * sd + start : dd.buf + (b - dd.nsplit) * sd + start;
-  r.q = r.diff ? dd.q + b * sd + start : nullptr;
+  r.diff = b >= dd.diff_lo && b < dd.diff_lo + dd.n_diff;
+  r.has_buf = b >= dd.buf_lo && b < dd.buf_lo + dd.n_buf;
+  r.p = r.diff ? dd.p + (b - dd.diff_lo) * sd + start : nullptr;
+  r.q = r.diff ? dd.q + (b - dd.diff_lo) * sd + start : nullptr;
+  r.buf = r.has_buf ? dd.buf + (b - dd.buf_lo) * sd + start : nullptr;
   return r;
 }
 
@@ -169,7 +175,17 @@ __device__ __forceinline__ float ldf(const float* base, uint32_t off) {
 // The upstream gradient at the 16 offsets: every load of the branch is issued before any is
 // used (one memory round trip; a select over a conditional load would wait per row).
 __device__ __forceinline__ void dout16(const DoutRows& gr, float coef, const uint32_t* off, float* gv) {
-  if (gr.diff) {
+  if (gr.diff && gr.has_buf) {
+    float a[16], b[16], e[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      a[r] = ldf(gr.p, off[r]);
+      b[r] = ldf(gr.q, off[r]);
+      e[r] = ldf(gr.buf, off[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) gv[r] = coef * (a[r] - b[r]) + e[r];
+  } else if (gr.diff) {
     float a[16], b[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -178,13 +194,16 @@ __device__ __forceinline__ void dout16(const DoutRows& gr, float coef, const uin
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) gv[r] = coef * (a[r] - b[r]);
+  } else if (gr.has_buf) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) gv[r] = ldf(gr.buf, off[r]);
   } else {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) gv[r] = ldf(gr.p, off[r]);
+    for (int r = 0; r < 16; ++r) gv[r] = 0.0f;
   }
 }
 
-__device__ __forceinline__ float dout_coef(const DoutDesc& dd) { return dd.nsplit > 0 ? dd.mul * (dd.g ? dd.g[0] : 1.0f) : 0.0f; }
+__device__ __forceinline__ float dout_coef(const DoutDesc& dd) { return dd.n_diff > 0 ? dd.mul * (dd.g ? dd.g[0] : 1.0f) : 0.0f; }
 
 // ------------------------------------------------------------------ weights
 
@@ -1072,7 +1091,8 @@ size_t macro_fused_bwd_workspace_bytes(int B, int S) {
   return (size_t)(B > 0 ? B : 1) * (S > 0 ? S : 1) * (kRank + 1) * sizeof(float) + 256;
 }
 
-int macro_fused_bwd(const float* dp, const float* dq, const float* g, float mul, int nsplit, const float* dbuf,
+int macro_fused_bwd(const float* dp, const float* dq, const float* g, float mul, int diff_lo, int n_diff,
+                    const float* dbuf, int buf_lo, int n_buf,
                     const float* h, const float* rstd, const bf16* x2, int Bh, const int64_t* key, int B, int S, int d,
                     int G, const float* a, const bf16* sa, const bf16* Vb, const bf16* VcT, const bf16* V2T,
                     const bf16* Ub, const bf16* UT, const float* gain, const float* bias, const float* scale, float c,
@@ -1082,7 +1102,8 @@ int macro_fused_bwd(const float* dp, const float* dq, const float* g, float mul,
   MF_SHAPES("macro_fused_bwd");
   RTE_REQUIRE(Bh >= 1 && B % Bh == 0 && B / Bh <= kMaxRepeats && B <= 65535,
               "macro_fused_bwd: need len(h) | len(key), at most 8 repeats");
-  RTE_REQUIRE(nsplit >= 0 && nsplit <= B && (nsplit == 0 || (dp && dq)) && (nsplit == B || dbuf),
+  RTE_REQUIRE(diff_lo >= 0 && n_diff >= 0 && diff_lo + n_diff <= B && (n_diff == 0 || (dp && dq)) && buf_lo >= 0 &&
+                  n_buf >= 0 && buf_lo + n_buf <= B && (n_buf == 0 || dbuf),
               "macro_fused_bwd: bad upstream-gradient description");
   RTE_REQUIRE(n_extra >= 0 && (n_extra == 0 || extra), "macro_fused_bwd: missing extra gradient blocks");
   RTE_REQUIRE(dh && dsum, "macro_fused_bwd: dh and dsum are required");
@@ -1091,7 +1112,7 @@ int macro_fused_bwd(const float* dp, const float* dq, const float* g, float mul,
   const int T = macro_fused_tiles(S), rep = B / Bh;
   float* xv2 = static_cast<float*>(ws);
   float* rd = xv2 + (size_t)B * S * kRank;
-  DoutDesc dd{dp, dq, g, mul, nsplit, dbuf};
+  DoutDesc dd{dp, dq, g, mul, diff_lo, n_diff, dbuf, buf_lo, n_buf};
   hipLaunchKernelGGL(mf_bwd_a_kernel, dim3(T, B), dim3(256), 0, s, dd, h, rstd, x2, Bh, S, d, key, G, a, VcT, V2T, UT,
                      Ub, gain, bias, scale, c, du, da, part_tab, part_da, rd, xv2);
   RTE_TRY(check_launch("macro_fused_bwd_a"));

@@ -102,7 +102,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_macro_fused_fwd": (_I, [_P, _P, _I, _I, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P,
                                  _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "rte_macro_fused_sum": (_I, [_P, _I, _F, _P, _P]),
-    "rte_macro_fused_bwd": (_I, [_P, _P, _P, _F, _I, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P,
+    "rte_macro_fused_bwd": (_I, [_P, _P, _P, _F, _I, _I, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P,
                                  _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _P, _I, _P, _P, _SZ, _P]),
     "rte_macro_fused_wgrad": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                    _P, _P, _SZ, _P]),

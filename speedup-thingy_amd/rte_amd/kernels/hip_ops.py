@@ -1992,15 +1992,19 @@ class _MacroCall:
              ptr(self.x2), ptr(self.rstd), ptr(self.pooled), ptr(self.P), ptr(self.a), ptr(self.sa), ptr(self.out),
              ptr(mse_ref), ptr(mse_part), ws, nbytes, _s())
 
-    def backward(self, G, w, tabs, c, du, da, part_tab, part_da, dsum, dh, *, dout=None, diff=None, nsplit=0,
-                 dh0=None, dh0_into_dh=False, extra=None, n_extra=0):
-        """diff = (p, q, g, mul): samples b < nsplit take mul g (p - q) as their upstream gradient,
-        the others dout's row block b - nsplit."""
+    def backward(self, G, w, tabs, c, du, da, part_tab, part_da, dsum, dh, *, dout=None, dout_lo=0, diff=None,
+                 diff_lo=0, dh0=None, dh0_into_dh=False, extra=None, n_extra=0):
+        """The upstream gradient of sample b: mul g (p - q)[b - diff_lo] for the len(p) samples from
+        diff_lo on (diff = (p, q, g, mul)), plus dout[b - dout_lo] for the len(dout) samples from
+        dout_lo on; the two ranges may overlap."""
         vb, vct, v2t, ub, ut = w
         p, q, g, mul = diff if diff is not None else (None, None, None, 0.0)
+        n_diff = 0 if p is None else p.shape[0]
+        n_dout = 0 if dout is None else dout.shape[0]
         nb = _lib.load().rte_macro_fused_bwd_workspace_bytes(self.B, self.S)
         ws, nbytes = workspace(nb, self.h.device)
-        call("rte_macro_fused_bwd", ptr(p), ptr(q), ptr(g), float(mul), int(nsplit), ptr(dout), ptr(self.h),
+        call("rte_macro_fused_bwd", ptr(p), ptr(q), ptr(g), float(mul), int(diff_lo), n_diff, ptr(dout),
+             int(dout_lo), n_dout, ptr(self.h),
              ptr(self.rstd), ptr(self.x2), self.Bh, ptr(self.key), self.B, self.S, self.d, G, ptr(self.a),
              ptr(self.sa), ptr(vb), ptr(vct), ptr(v2t), ptr(ub), ptr(ut), ptr(tabs[0]), ptr(tabs[1]), ptr(tabs[2]),
              float(c), ptr(du), ptr(da), ptr(part_tab), ptr(part_da), ptr(dh), ptr(dh0), int(dh0_into_dh), ptr(extra),
@@ -2104,24 +2108,30 @@ class MacroConsistencyFn(torch.autograd.Function):
     """The macro consistency loss (rte/macro.py:342-359) on the fused operator:
     mse(Phi_{dst}(h), Phi_{src}(Phi_{src}(h))) over every (s, 2s) stride pair and sample.
 
-    The first application runs the 2 pc b (sample, key) pairs [dst keys; src keys] of the b
-    source samples of h (one h row block per source, 2 pc <= 8 repeats); the second reads the
-    src half of its output with h0 = h.  The MSE is summed inside the second application's
-    forward kernel (per-tile partial sums, fixed order).  The backward takes the MSE gradient
-    inside the operator kernels (no difference tensors), feeds the second application's dh
-    straight into the first one's upstream gradient, adds every path to h in the kernels, and
-    reduces the weight gradients of both applications in one grouped pass."""
+    The first application runs nf key blocks of the b source samples of h (key_first, one h row
+    block per source, nf <= 8): the pc src blocks from block src_lo on and the pc dst blocks from
+    block dst_lo on.  When the stride pairs chain ((1, 2), (2, 4)) the src and dst ranges overlap
+    and a shared key block is computed once.  The second application reads the src blocks of the
+    first one's output with h0 = h.  The MSE is summed inside the second application's forward
+    kernel (per-tile partial sums, fixed order).  The backward takes the MSE gradient inside the
+    operator kernels (no difference tensors), feeds the second application's dh straight into
+    the first one's src blocks (added to the MSE gradient of a block that is also a dst block),
+    adds every path to h in the kernels, and reduces the weight gradients of both applications
+    in one grouped pass."""
 
     @staticmethod
-    def forward(ctx, h, key_both, key_src, v, u, gain, bias, scale, c, eps):
-        _lib.require_device_tensors("macro_consistency", h, key_both, key_src, v, u, gain, bias, scale)
+    def forward(ctx, h, key_first, key_src, src_lo, dst_lo, v, u, gain, bias, scale, c, eps):
+        _lib.require_device_tensors("macro_consistency", h, key_first, key_src, v, u, gain, bias, scale)
         b, S, d = h.shape
-        kb = key_both.reshape(-1).contiguous().to(torch.int64)
+        kf = key_first.reshape(-1).contiguous().to(torch.int64)
         ks = key_src.reshape(-1).contiguous().to(torch.int64)
-        pcb = ks.numel()
-        if pcb == 0 or pcb % b or kb.numel() != 2 * pcb or 2 * pcb // b > 8:
-            raise ValueError("macro_consistency: need 2 pc b first keys and pc b second keys, 2 pc <= 8")
-        if not macro_fused_supported(v, u, 2 * pcb // b):
+        pcb, B0 = ks.numel(), kf.numel()
+        if pcb == 0 or pcb % b or B0 % b or B0 // b > 8:
+            raise ValueError("macro_consistency: need nf b first keys (nf <= 8) and pc b second keys")
+        nf, pc = B0 // b, pcb // b
+        if not (0 <= src_lo <= nf - pc and 0 <= dst_lo <= nf - pc):
+            raise ValueError("macro_consistency: src / dst key blocks outside the first application")
+        if not macro_fused_supported(v, u, nf):
             raise ValueError("macro_consistency: needs hidden rank 32 and d a multiple of 128 up to 1024")
         G = v.shape[0] * v.shape[1]
         dev = h.device
@@ -2131,12 +2141,13 @@ class MacroConsistencyFn(torch.autograd.Function):
         R = MACRO_FUSED_RANK
         x2 = torch.empty(((b + pcb) * S, 2 * d), dtype=BF16, device=dev)
         pooled = torch.empty((b + pcb, d), dtype=BF16, device=dev)
-        a = torch.empty((3 * pcb * S, R), dtype=F32, device=dev)
-        sa = torch.empty((3 * pcb * S, R), dtype=BF16, device=dev)
-        n0 = 2 * pcb * S
-        both = _MacroCall(hv, hv, kb, x2[:b * S], pooled[:b], a[:n0], sa[:n0], S, d)
-        both.forward(G, eps, w, tabs, c)
-        direct, first = both.out[:pcb], both.out[pcb:]
+        a = torch.empty(((B0 + pcb) * S, R), dtype=F32, device=dev)
+        sa = torch.empty(((B0 + pcb) * S, R), dtype=BF16, device=dev)
+        n0 = B0 * S
+        first_call = _MacroCall(hv, hv, kf, x2[:b * S], pooled[:b], a[:n0], sa[:n0], S, d)
+        first_call.forward(G, eps, w, tabs, c)
+        s0, d0 = src_lo * b, dst_lo * b
+        first, direct = first_call.out[s0:s0 + pcb], first_call.out[d0:d0 + pcb]
         T = (S + 31) // 32
         mse_part = torch.empty((pcb * T,), dtype=F32, device=dev)
         twice = _MacroCall(first, hv, ks, x2[b * S:], pooled[b:], a[n0:], sa[n0:], S, d)
@@ -2144,52 +2155,60 @@ class MacroConsistencyFn(torch.autograd.Function):
         n = pcb * S * d
         loss = torch.empty((), dtype=F32, device=dev)
         call("rte_macro_fused_sum", ptr(mse_part), mse_part.numel(), float(1.0 / n), ptr(loss), _s())
-        ctx.calls = (both, twice)
-        ctx.bufs = (x2, pooled, a, sa, torch.cat([kb, ks]))
+        ctx.calls = (first_call, twice)
+        ctx.bufs = (x2, pooled, a, sa, torch.cat([kf, ks]))
         ctx.w, ctx.tabs = w, tabs
-        ctx.meta = (G, float(c), b, pcb, S, d, n, v.shape, u.shape, gain.shape, h.dtype)
+        ctx.meta = (G, float(c), b, B0, pcb, s0, d0, S, d, n, v.shape, u.shape, gain.shape, h.dtype)
         return loss
 
     @staticmethod
     def backward(ctx, g):
-        both, twice = ctx.calls
+        first_call, twice = ctx.calls
         x2, pooled, a, sa, keys = ctx.bufs
         w, tabs = ctx.w, ctx.tabs
-        G, c, b, pcb, S, d, n, v_shape, u_shape, t_shape, h_dt = ctx.meta
+        G, c, b, B0, pcb, s0, d0, S, d, n, v_shape, u_shape, t_shape, h_dt = ctx.meta
         nia = ctx.needs_input_grad
         dev = a.device
         R = MACRO_FUSED_RANK
         T = (S + 31) // 32
         gv = g.reshape(1).contiguous().to(F32)
         mul = 2.0 / n
-        rows = 3 * pcb * S
-        du = torch.empty((rows, d), dtype=BF16, device=dev)
-        da = torch.empty((rows, R), dtype=BF16, device=dev)
-        part_tab = torch.empty((3 * pcb * T * 3 * d,), dtype=F32, device=dev)
-        part_da = torch.empty((3 * pcb * T * R,), dtype=F32, device=dev)
-        dsum = torch.empty((3 * pcb, R), dtype=BF16, device=dev)
-        n0 = 2 * pcb * S
-        t0, r0 = 2 * pcb * T * 3 * d, 2 * pcb * T * R
-        direct = both.out[:pcb]
+        nb = B0 + pcb
+        du = torch.empty((nb * S, d), dtype=BF16, device=dev)
+        da = torch.empty((nb * S, R), dtype=BF16, device=dev)
+        part_tab = torch.empty((nb * T * 3 * d,), dtype=F32, device=dev)
+        part_da = torch.empty((nb * T * R,), dtype=F32, device=dev)
+        dsum = torch.empty((nb, R), dtype=BF16, device=dev)
+        n0 = B0 * S
+        t0, r0 = B0 * T * 3 * d, B0 * T * R
+        direct = first_call.out[d0:d0 + pcb]
         # second application: d loss / d twice = mul g (twice - direct); its dh is the upstream
-        # gradient of the first application's src half, its dh0 goes to h
+        # gradient of the first application's src blocks, its dh0 goes to h
         d_first = torch.empty((pcb, S, d), dtype=F32, device=dev)
         dh0_tw = torch.empty((pcb, S, d), dtype=F32, device=dev)
-        twice.backward(G, w, tabs, c, du[n0:], da[n0:], part_tab[t0:], part_da[r0:], dsum[2 * pcb:], d_first,
-                       diff=(twice.out, direct, gv, mul), nsplit=pcb, dh0=dh0_tw)
-        # first application: dst half mul g (direct - twice), src half d_first; h = h0 = h
+        twice.backward(G, w, tabs, c, du[n0:], da[n0:], part_tab[t0:], part_da[r0:], dsum[B0:], d_first,
+                       diff=(twice.out, direct, gv, mul), dh0=dh0_tw)
+        # first application: dst blocks mul g (direct - twice), src blocks d_first (both where
+        # they overlap), other blocks 0; h = h0 = h
         dh = torch.empty((b, S, d), dtype=F32, device=dev)
-        both.backward(G, w, tabs, c, du[:n0], da[:n0], part_tab[:t0], part_da[:r0], dsum[:2 * pcb], dh, dout=d_first,
-                      diff=(direct, twice.out, gv, mul), nsplit=pcb, dh0_into_dh=True, extra=dh0_tw,
-                      n_extra=pcb // b)
-        grads = _macro_wgrad(keys, 2 * pcb, b, pcb, pcb, S, d, G, x2, sa, du, da, pooled, dsum, part_tab,
-                             nia[3:8], v_shape, u_shape, t_shape, dev)
+        first_call.backward(G, w, tabs, c, du[:n0], da[:n0], part_tab[:t0], part_da[:r0], dsum[:B0], dh,
+                            dout=d_first, dout_lo=s0, diff=(direct, twice.out, gv, mul), diff_lo=d0,
+                            dh0_into_dh=True, extra=dh0_tw, n_extra=pcb // b)
+        grads = _macro_wgrad(keys, B0, b, pcb, pcb, S, d, G, x2, sa, du, da, pooled, dsum, part_tab,
+                             nia[5:10], v_shape, u_shape, t_shape, dev)
         ctx.calls = ctx.bufs = ctx.w = ctx.tabs = None
-        return (dh.to(h_dt) if nia[0] else None, None, None, *grads, None, None)
+        return (dh.to(h_dt) if nia[0] else None, None, None, None, None, *grads, None, None)
 
 
-def macro_consistency(h, key_both, key_src, v, u, gain, bias, scale, c: float, eps: float = 1e-5):
-    return MacroConsistencyFn.apply(h, key_both, key_src, v, u, gain, bias, scale, c, eps)
+def macro_consistency(h, key_first, key_src, v, u, gain, bias, scale, c: float, eps: float = 1e-5, *,
+                      src_lo: int | None = None, dst_lo: int = 0):
+    """key_first: the first application's nf key blocks of len(h) samples; key_src: the pc src
+    blocks, which sit from block src_lo on in key_first (default nf - pc: the [dst; src] layout),
+    the dst blocks from block dst_lo on."""
+    b = h.shape[0]
+    nf, pc = key_first.numel() // b, key_src.numel() // b
+    return MacroConsistencyFn.apply(h, key_first, key_src, nf - pc if src_lo is None else int(src_lo), int(dst_lo),
+                                    v, u, gain, bias, scale, c, eps)
 
 
 class MseFn(torch.autograd.Function):

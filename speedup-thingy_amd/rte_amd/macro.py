@@ -114,9 +114,18 @@ class MacroOperators(nn.Module):
         pairs = [(i, self.stride_to_idx[s * 2]) for i, s in enumerate(self.strides) if s * 2 in self.stride_to_idx]
         self.register_buffer("cons_src_idx", torch.tensor([p[0] for p in pairs], dtype=torch.long), persistent=False)
         self.register_buffer("cons_dst_idx", torch.tensor([p[1] for p in pairs], dtype=torch.long), persistent=False)
-        # [dst strides ; src strides]: the key offsets of the consistency loss's two operator calls
-        self.register_buffer("cons_key_idx", torch.tensor([p[1] for p in pairs] + [p[0] for p in pairs],
-                                                          dtype=torch.long), persistent=False)
+        # key offsets of the consistency loss's first operator call: the sorted union of the src
+        # and dst strides when each role is a run of it (chained pairs such as (1, 2), (2, 4): a
+        # shared stride is applied once), else [dst strides ; src strides]
+        src, dst = [p[0] for p in pairs], [p[1] for p in pairs]
+        union = sorted(set(src) | set(dst))
+        pos_s, pos_d = [union.index(i) for i in src], [union.index(i) for i in dst]
+        run = lambda pos: pos == list(range(pos[0], pos[0] + len(pos)))  # noqa: E731
+        if pairs and run(pos_s) and run(pos_d) and len(union) < 2 * len(pairs):
+            first, self.cons_src_lo, self.cons_dst_lo = union, pos_s[0], pos_d[0]
+        else:
+            first, self.cons_src_lo, self.cons_dst_lo = dst + src, len(pairs), 0
+        self.register_buffer("cons_key_idx", torch.tensor(first, dtype=torch.long), persistent=False)
 
     def stride_ids_for_depths(self, depths: torch.Tensor) -> torch.Tensor:
         matches = depths.unsqueeze(-1) == self.depth_values.to(depths.device).unsqueeze(0)
@@ -252,13 +261,16 @@ class MacroOperators(nn.Module):
         if self.cons_src_idx.numel() == 0:
             return h.new_zeros(())
         pc, b = self.cons_src_idx.numel(), h.shape[0]
-        if h is h0 and self._fused_bounded() and hip_ops.macro_fused_supported(self.v, self.u, 2 * pc):
+        nf = self.cons_key_idx.numel()
+        if h is h0 and self._fused_bounded() and hip_ops.macro_fused_supported(self.v, self.u, nf):
             # both operator applications, the MSE and every backward path in the fused kernels;
-            # keys[p, i] = recipe_ids[i] Kk + [dst ; src][p] in one launch
+            # keys[p, i] = recipe_ids[i] Kk + cons_key_idx[p] in one launch
             Kk = self.v.shape[1]
             keys = torch.add(self.cons_key_idx.unsqueeze(1), recipe_ids.long().unsqueeze(0), alpha=Kk).reshape(-1)
-            return hip_ops.macro_consistency(h, keys, keys[pc * b:], self.v, self.u, self.d_gain, self.bias,
-                                             self.update_scale, self.config.macro_update_scale)
+            s0 = self.cons_src_lo * b
+            return hip_ops.macro_consistency(h, keys, keys[s0:s0 + pc * b], self.v, self.u, self.d_gain, self.bias,
+                                             self.update_scale, self.config.macro_update_scale,
+                                             src_lo=self.cons_src_lo, dst_lo=self.cons_dst_lo)
         r_rep = recipe_ids.repeat(pc)
         src = self.cons_src_idx.repeat_interleave(b)
         dst = self.cons_dst_idx.repeat_interleave(b)

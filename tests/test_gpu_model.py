@@ -639,11 +639,13 @@ def test_macro_fused_operator_matches_reference(d, B, S, depths):
     assert rel_err(out.detach().double().cpu().numpy(), ref.detach().numpy()) < 1e-3
 
 
-@pytest.mark.parametrize("d,B,S,depths", [(256, 5, 80, [1, 2, 4, 8]), (512, 16, 64, [1, 2, 4])])
+@pytest.mark.parametrize("d,B,S,depths", [(256, 5, 80, [1, 2, 4, 8]), (512, 16, 64, [1, 2, 4]),
+                                          (256, 6, 40, [1, 2, 3, 6])])
 def test_macro_fused_consistency_matches_reference(d, B, S, depths):
     """The fused consistency loss (both operator applications, the MSE and the backward in the
-    fused kernels, 2 pc up to 6 repeats) against fp64 autograd of rte/macro.py:342-359 restated
-    with explicit copies."""
+    fused kernels) against fp64 autograd of rte/macro.py:342-359 restated with explicit copies:
+    chained stride pairs sharing first-application key blocks (strides 1, 2, 4 (, 8): src and dst
+    blocks overlap), and unchained pairs in the [dst; src] layout (strides 1, 2, 3, 6)."""
     from rte_amd.macro import MacroOperators
 
     cfg = _model_cfg(d_model=d, n_heads=d // 64, macro_rank=32, recipe_count=6, depth_choices=depths,

@@ -337,6 +337,30 @@ def test_fp32_precision_is_accepted():
     assert not hip_ops.fp32_active()
 
 
+@pytest.mark.parametrize("depths,first,src_lo,dst_lo", [
+    ([1, 2, 4], [0, 1, 2], 0, 1),
+    ([1, 2, 4, 8], [0, 1, 2, 3], 0, 1),
+    ([1, 2, 3, 6], [1, 3, 0, 2], 2, 0),
+    ([2, 4], [1, 0], 1, 0),
+])
+def test_consistency_first_call_key_layout(depths, first, src_lo, dst_lo):
+    """The consistency loss's first operator call: chained (s, 2s) pairs share key blocks (the
+    sorted stride union, src and dst runs inside it), other pair sets use [dst; src]; either way
+    block src_lo + i holds pair i's src stride and block dst_lo + i its dst stride."""
+    from rte_amd.config import ModelConfig
+    from rte_amd.macro import MacroOperators
+
+    cfg = ModelConfig(**_model(depth_choices=depths, t_max=max(depths), d_model=128, n_heads=4, macro_rank=32))
+    mac = MacroOperators(cfg)
+    assert mac.cons_key_idx.tolist() == first
+    assert (mac.cons_src_lo, mac.cons_dst_lo) == (src_lo, dst_lo)
+    pc = mac.cons_src_idx.numel()
+    assert mac.cons_key_idx[src_lo:src_lo + pc].tolist() == mac.cons_src_idx.tolist()
+    assert mac.cons_key_idx[dst_lo:dst_lo + pc].tolist() == mac.cons_dst_idx.tolist()
+    strides = mac.depth_values.tolist()
+    assert all(strides[d] == 2 * strides[s] for s, d in zip(mac.cons_src_idx.tolist(), mac.cons_dst_idx.tolist()))
+
+
 def test_parameter_counts_closed_form():
     """The fairness formulas of rte/metrics.py:12-94 on a config small enough to count by hand."""
     from rte_amd import metrics as M
