@@ -700,6 +700,54 @@ int rte_combine_f32(const float* rows, const int32_t* slot, const float* w, int 
 int rte_pair_dot_f32(const float* dout, const float* rows, const int32_t* slot, int64_t pairs, int k, int d, float* dw,
                      void* stream);
 
+/* ---------------------------------------------------------------- exact replay of the banked core
+ * One exact recursive pass of BankedRecursiveCore.forward_step (rte/layers.py:806-870, one bank of
+ * heads and of FFN slabs) for the few samples of the audit's exact replay, which forward_exact runs
+ * pass by pass (rte/models.py:416-512, called from rte/audit.py:245-387 on the audited rows):
+ *   h~ = h + alpha h0; n1 = rmsnorm(h~) w1 (1 + g1) + b1; attention over the recipe's heads (RoPE,
+ *   causal, scale 1/8); u = h~ + s_attn attn; n2 = rmsnorm(u) w2 (1 + g2) + b2; SwiGLU over the
+ *   recipe's slabs (route weight route_w); h' = act ? u + s_mlp mlp : h.
+ * Shapes: B samples x S positions (M = B S rows), d <= 512 (d % 128 == 0), H heads of width 64
+ * (H 64 = d), F = n_blk 32 FFN neurons.  info int32 [B, W] (W = 4 + 2 H + 2 n_blk), one record per
+ * sample for this pass: act | nh | nb | 0 | heads[H] (the recipe's heads, ascending) | ihead[H]
+ * (slot of each head or -1) | blks[n_blk] (its 32-neuron slab blocks, ascending) | iblk[n_blk];
+ * h_max / nb_max = the largest nh / nb.  Weights bf16: wqkv_t [3d, d], wo_t [d, d], wug_t [2F, d]
+ * (rows up F then gate F), wd_t [d, F] for the forward; wqkv [d, 3d], wo [d, d], wug [d, 2F], wd
+ * [F, d] for the backward.  cos / sin f32 [S, 64].  Scalars s_attn, s_mlp, alpha: device f32.
+ * fwd outputs: ht, attn, u, mlp, h_out f32 [M, d]; n1, n2 bf16 [M, d]; rstd1, rstd2 f32 [M]; q, k, v
+ * bf16 [B, h_max, S, 64] (compact heads); y bf16 [M, h_max 64]; lse f32 [B, h_max, S]; ug bf16
+ * [M, nb_max 64] ([up 32 | gate 32] per slot); z bf16 [M, nb_max 32]; y_full bf16 [M, d], z_full
+ * bf16 [M, F] (zeros outside the recipe's heads / blocks).
+ * bwd (dh f32 [M, d] = gradient of h_out): dh_in f32 [M, d], dh0 f32 [M, d] (alpha dh~, added to
+ * its contents when accumulate), the weight-gradient operands d_mlp, d_attn bf16 [M, d],
+ * dug_full bf16 [M, 2F], dqkv_full bf16 [M, 3d] (dW = operand^T pair summed over passes:
+ * dWqkv = n1^T dqkv_full, dWo = y_full^T d_attn, dWug = n2^T dug_full, dWd = z_full^T d_mlp),
+ * and per-tile partials (nt = B ceil(S / 64) tiles, nct = d / 64): p_film1, p_film2 f32 [nt, 3d]
+ * (dw | dg | db), p_sa, p_alpha f32 [nt, nct], p_sm f32 [nt].  Scratch: dug bf16 [M, nb_max 64],
+ * dn2, dn1, du f32 [M, d], dy bf16 [M, h_max 64], dqkv bf16 [M, 3 h_max 64].
+ * param_reduce: out f32 [T, 6d] (per pass dw1 | dg1 | db1 | dw2 | dg2 | db2), then dw1 [d], dw2 [d]
+ * over the T passes, ds_attn [T], ds_mlp [T], dalpha [1]; partials stacked pass-major. */
+int rte_replay_fwd_pass(int B, int S, int d, int H, int F, int n_blk, int h_max, int nb_max, const int32_t* info,
+                        const float* h, const float* h0, const float* alpha, const float* w1, const float* g1,
+                        const float* b1, float eps1, const float* w2, const float* g2, const float* b2, float eps2,
+                        const float* s_attn, const float* s_mlp, float route_w, const void* wqkv_t, const void* wo_t,
+                        const void* wug_t, const void* wd_t, const float* cos_t, const float* sin_t, float* ht,
+                        void* n1, float* rstd1, void* q, void* k, void* v, void* y, float* lse, float* attn, float* u,
+                        void* y_full, void* n2, float* rstd2, void* ug, void* z, float* mlp, float* h_out,
+                        void* z_full, void* stream);
+int rte_replay_bwd_pass(int B, int S, int d, int H, int F, int n_blk, int h_max, int nb_max, const int32_t* info,
+                        const float* dh, const float* mlp, const float* s_mlp, const void* wd, const void* ug, float route_w,
+                        void* dug, void* d_mlp, float* p_sm, const void* wug, float* dn2, void* dug_full,
+                        const float* u, const float* rstd2, const float* w2, const float* g2, const float* attn,
+                        const float* s_attn, const void* wo, float* du, void* d_attn, void* dy, float* p_film2,
+                        float* p_sa, const void* q, const void* k, const void* v, const void* y, const float* lse,
+                        const float* cos_t, const float* sin_t, void* dqkv, const void* wqkv, float* dn1,
+                        void* dqkv_full, const float* ht, const float* rstd1, const float* w1, const float* g1,
+                        const float* h0, const float* alpha, int accumulate, float* dh_in, float* dh0,
+                        float* p_film1, float* p_alpha, void* stream);
+int rte_replay_param_reduce(int T, int B, int S, int d, const float* p_film1, const float* p_film2,
+                            const float* p_sa, const float* p_sm, const float* p_alpha, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -274,12 +274,22 @@ def gemm(
     return out
 
 
+def _token_major(y: torch.Tensor) -> bool:
+    """y [B, H, S, hd] is a view of token-major [B, S, H, hd] rows (what the attention writes)."""
+    B, H, S, hd = y.shape
+    sb, sh, ss, sd = y.stride()
+    return sd == 1 and sh == hd and ss == H * hd and (B == 1 or sb == S * ss)
+
+
 def _attn_layout(y: torch.Tensor) -> tuple[list[int], int, int]:
-    """Layout descriptor reading a [B, H, S, hd] tensor as rows t = b*S + s, cols c = h*hd + dim."""
+    """Layout descriptor reading a [B, H, S, hd] tensor as rows t = b*S + s, cols c = h*hd + dim:
+    plain rows for token-major memory, else a split of rows by S and columns by hd (powers of two)."""
     B, H, S, hd = y.shape
     sb, sh, ss, sd = y.stride()
     if sd != 1:
         raise ValueError("attention tensor needs a unit innermost stride")
+    if _token_major(y):
+        return [H * hd, 0, 0, 0, 0], B * S, H * hd
     return [ss, S, sb, hd, sh], B * S, H * hd
 
 
@@ -623,6 +633,9 @@ class AttnOutProjFn(torch.autograd.Function):
         yb = y.to(BF16)
         if yb.stride(-1) != 1:
             yb = yb.contiguous()
+        B_, H_, S_, hd_ = yb.shape
+        if not _token_major(yb) and (S_ & (S_ - 1) or hd_ & (hd_ - 1)):
+            yb = yb.transpose(1, 2).contiguous().transpose(1, 2)  # the split layout needs powers of two
         layout, T, K = _attn_layout(yb)
         wb = cast_bf16(w)
         N = wb.shape[0]

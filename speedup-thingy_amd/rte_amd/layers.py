@@ -576,7 +576,15 @@ class BankedSwiGLU(nn.Module):
 
 
 class BankedRecursiveCore(nn.Module):
-    """rte/layers.py:806-870 (global low-rank corrector not supported: off by default)."""
+    """rte/layers.py:806-870 (global low-rank corrector not supported: off by default).
+
+    The exact replay of a few samples (forward_replay) runs all passes as one node on the replay
+    kernels when the shape allows (one bank of heads and of slabs, head width 64, d <= 512,
+    slabs of whole 32-neuron blocks, RoPE); fused_replay = False keeps it on the per-operator
+    path."""
+
+    fused_replay = True
+    replay_max_rows = 2048  # the replay's few samples; larger exact batches keep the wide GEMMs
 
     def __init__(self, config: ModelConfig, recipe_bank: RecipeBank):
         super().__init__()
@@ -600,6 +608,54 @@ class BankedRecursiveCore(nn.Module):
             self.alpha_inj = nn.Parameter(torch.tensor(0.1))
         else:
             self.register_parameter("alpha_inj", None)
+        self._init_replay_tables(config, recipe_bank)
+
+    def _init_replay_tables(self, config: ModelConfig, recipe_bank: RecipeBank) -> None:
+        """Per recipe: its heads and 32-neuron slab blocks, the replay kernels' selection tables
+        (rte/layers.py:702-779: the recipe's head groups and FFN groups of its single bank)."""
+        from rte_amd.kernels import replay_core as RC
+
+        H, d = config.n_heads, config.d_model
+        hpg = H // config.head_groups
+        slab = config.d_ff // config.ffn_groups
+        self._replay_shape_ok = (config.attn_banks == 1 and config.ffn_banks == 1 and config.use_rope
+                                 and d // H == RC.HEAD_DIM and d % 128 == 0 and d <= RC.MAX_D
+                                 and slab % RC.BLOCK == 0)
+        self._replay_meta = None
+        if not self._replay_shape_ok:
+            return
+        bps = slab // RC.BLOCK
+        heads = [[g * hpg + i for g in s.head_groups for i in range(hpg)] for s in recipe_bank.recipes]
+        blocks = [[g * bps + j for g in s.ffn_groups for j in range(bps)] for s in recipe_bank.recipes]
+        rec = RC.build_records(heads, blocks, H, config.d_ff // RC.BLOCK)
+        self.register_buffer("replay_records", rec, persistent=False)
+        self._replay_meta = (H, config.d_ff // RC.BLOCK, int(rec[:, 1].max()), int(rec[:, 2].max()))
+
+    def replay_tables(self):
+        from rte_amd.kernels import replay_core as RC
+
+        H, NB, hm, nbm = self._replay_meta
+        return RC.ReplayTables(self.replay_records, H, NB, hm, nbm)
+
+    def replay_fused_ok(self, h0: torch.Tensor) -> bool:
+        """The fused replay applies: shape supported, a ROCm device, bf16 operators (not the fp32
+        precision path), sequence within the rotary table."""
+        return (type(self).fused_replay and self._replay_shape_ok and h0.is_cuda and not hip_ops.fp32_active()
+                and h0.dim() == 3 and h0.shape[1] <= self.attn.rope.cos.shape[0]
+                and h0.shape[0] * h0.shape[1] <= self.replay_max_rows)
+
+    def forward_replay(self, h0, recipe_ids_by_pass, active_by_pass=None, keep=()):
+        """All T exact passes from h0 (rte/layers.py:847-870 for t = 0 .. T-1): recipe_ids_by_pass
+        [T, B], active_by_pass [T, B] bool or None.  Returns (h_T, *states of the passes in keep)."""
+        from rte_amd.kernels import replay_core as RC
+
+        cos, sin = self.attn._tables()
+        outs = RC.replay_core(h0, self.pass_gamma1, self.pass_beta1, self.pass_gamma2, self.pass_beta2,
+                              self.pass_attn_scale, self.pass_mlp_scale, self.alpha_inj, self.norm1.weight,
+                              self.norm2.weight, self.attn.wqkv, self.attn.wo, self.mlp.wug, self.mlp.wd,
+                              recipe_ids_by_pass, active_by_pass, self.replay_tables(), cos, sin, self.norm1.eps,
+                              self.norm2.eps, 1.0, keep)
+        return outs
 
     def prepare(self):
         """Per-forward views shared by every recursive pass: the pool weight layouts and the

@@ -163,7 +163,6 @@ class RecursiveModel(nn.Module):
         route = router_decisions or self.router(h0, fixed_recipe=fixed_recipe, fixed_depth=fixed_depth)
         h = h0
         states: dict[int, torch.Tensor] = {}
-        weights = self.core.prepare()
         T = self.config.t_max
         # every pass's recipe ids, active masks and head scales in one launch each
         rid_bp = route.recipe_id_by_pass
@@ -173,14 +172,24 @@ class RecursiveModel(nn.Module):
         fixed = getattr(route, "fixed_depth_value", None)
         all_active = fixed is not None and fixed >= T
         actives = None if all_active else self.pass_index[:T, None] < route.depth.reshape(1, -1)
-        if all_active and rid_bp is None:
-            weights["pool_pack"] = self.core.mlp.pack_recipes(rids[0], h0.shape[1])
-        head_scales = self.core.attn.recipe_head_scale[rids.long()]
-        for t in range(T):
-            h = self.core.forward_step(h, h0, rids[t], None if actives is None else actives[t], pass_idx=t,
-                                       weights=weights, head_scale=head_scales[t])
-            if return_states and (t + 1) in self.config.depth_choices:
-                states[t + 1] = h  # every pass returns a new tensor; nothing writes h in place
+        if self.core.replay_fused_ok(h0):
+            # every pass as one node on the replay kernels (the few audited rows of the exact replay)
+            keep = [t for t in range(T - 1) if return_states and (t + 1) in self.config.depth_choices]
+            h, *kept = self.core.forward_replay(h0, rids.long(), actives, keep)
+            h = h.to(h0.dtype)
+            states = {t + 1: s.to(h0.dtype) for t, s in zip(keep, kept)}
+            if return_states and T in self.config.depth_choices:
+                states[T] = h
+        else:
+            weights = self.core.prepare()
+            if all_active and rid_bp is None:
+                weights["pool_pack"] = self.core.mlp.pack_recipes(rids[0], h0.shape[1])
+            head_scales = self.core.attn.recipe_head_scale[rids.long()]
+            for t in range(T):
+                h = self.core.forward_step(h, h0, rids[t], None if actives is None else actives[t], pass_idx=t,
+                                           weights=weights, head_scale=head_scales[t])
+                if return_states and (t + 1) in self.config.depth_choices:
+                    states[t + 1] = h  # every pass returns a new tensor; nothing writes h in place
         hidden = self._coda_hidden(h)
         logits, lps, tok = head_logits_loss(hidden, self.vocab_weight, targets)
         meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
