@@ -718,15 +718,20 @@ int rte_pair_dot_f32(const float* dout, const float* rows, const int32_t* slot, 
  * bf16 [B, h_max, S, 64] (compact heads); y bf16 [M, h_max 64]; lse f32 [B, h_max, S]; ug bf16
  * [M, nb_max 64] ([up 32 | gate 32] per slot); z bf16 [M, nb_max 32]; y_full bf16 [M, d], z_full
  * bf16 [M, F] (zeros outside the recipe's heads / blocks).
- * bwd (dh f32 [M, d] = gradient of h_out): dh_in f32 [M, d], dh0 f32 [M, d] (alpha dh~, added to
- * its contents when accumulate), the weight-gradient operands d_mlp, d_attn bf16 [M, d],
- * dug_full bf16 [M, 2F], dqkv_full bf16 [M, 3d] (dW = operand^T pair summed over passes:
- * dWqkv = n1^T dqkv_full, dWo = y_full^T d_attn, dWug = n2^T dug_full, dWd = z_full^T d_mlp),
- * and per-tile partials (nt = B ceil(S / 64) tiles, nct = d / 64): p_film1, p_film2 f32 [nt, 3d]
- * (dw | dg | db), p_sa, p_alpha f32 [nt, nct], p_sm f32 [nt].  Scratch: dug bf16 [M, nb_max 64],
- * dn2, dn1, du f32 [M, d], dy bf16 [M, h_max 64], dqkv bf16 [M, 3 h_max 64].
+ * bwd_prep (once, for the first pass the backward visits): a_mlp = bf16(s_mlp dh) bf16 [M, d] and
+ * p_sm f32 [nt] (per row-workgroup sums of dh mlp), nt = rte_replay_row_tiles(B, S) = ceil(M / 4).
+ * bwd (dh f32 [M, d] = gradient of h_out, a_mlp from bwd_prep or the previous bwd call):
+ * dh_in f32 [M, d], dh0 f32 [M, d] (alpha dh~, added to its contents when accumulate), the
+ * weight-gradient operands d_attn bf16 [M, d], dug_full bf16 [M, 2F], dqkv_full bf16 [M, 3d]
+ * (dW = operand^T pair summed over passes: dWqkv = n1^T dqkv_full, dWo = y_full^T d_attn,
+ * dWug = n2^T dug_full, dWd = z_full^T a_mlp), and per-row-workgroup partials: p_film1, p_film2
+ * f32 [nt, 3d] (dw | dg | db), p_sa, p_alpha f32 [nt].  With a_next (the pass before this one):
+ * its down operand a_next = bf16(s_mlp_next dh_in) [M, d] and p_sm_next f32 [nt] from mlp_next.
+ * Scratch: dug bf16 [M, nb_max 64], dn2, dn1, du f32 [M, d], dy bf16 [M, h_max 64], dqkv bf16
+ * [M, 3 h_max 64].
  * param_reduce: out f32 [T, 6d] (per pass dw1 | dg1 | db1 | dw2 | dg2 | db2), then dw1 [d], dw2 [d]
  * over the T passes, ds_attn [T], ds_mlp [T], dalpha [1]; partials stacked pass-major. */
+int rte_replay_row_tiles(int B, int S);
 int rte_replay_fwd_pass(int B, int S, int d, int H, int F, int n_blk, int h_max, int nb_max, const int32_t* info,
                         const float* h, const float* h0, const float* alpha, const float* w1, const float* g1,
                         const float* b1, float eps1, const float* w2, const float* g2, const float* b2, float eps2,
@@ -735,16 +740,18 @@ int rte_replay_fwd_pass(int B, int S, int d, int H, int F, int n_blk, int h_max,
                         void* n1, float* rstd1, void* q, void* k, void* v, void* y, float* lse, float* attn, float* u,
                         void* y_full, void* n2, float* rstd2, void* ug, void* z, float* mlp, float* h_out,
                         void* z_full, void* stream);
+int rte_replay_bwd_prep(int B, int S, int d, const float* dh, const float* mlp, const float* s_mlp, void* a_mlp,
+                        float* p_sm, void* stream);
 int rte_replay_bwd_pass(int B, int S, int d, int H, int F, int n_blk, int h_max, int nb_max, const int32_t* info,
-                        const float* dh, const float* mlp, const float* s_mlp, const void* wd, const void* ug, float route_w,
-                        void* dug, void* d_mlp, float* p_sm, const void* wug, float* dn2, void* dug_full,
-                        const float* u, const float* rstd2, const float* w2, const float* g2, const float* attn,
-                        const float* s_attn, const void* wo, float* du, void* d_attn, void* dy, float* p_film2,
-                        float* p_sa, const void* q, const void* k, const void* v, const void* y, const float* lse,
-                        const float* cos_t, const float* sin_t, void* dqkv, const void* wqkv, float* dn1,
-                        void* dqkv_full, const float* ht, const float* rstd1, const float* w1, const float* g1,
-                        const float* h0, const float* alpha, int accumulate, float* dh_in, float* dh0,
-                        float* p_film1, float* p_alpha, void* stream);
+                        const float* dh, const void* a_mlp, const void* wd, const void* ug, float route_w, void* dug,
+                        const void* wug, float* dn2, void* dug_full, const float* u, const float* rstd2,
+                        const float* w2, const float* g2, const float* attn, const float* s_attn, float* du,
+                        void* d_attn, float* p_film2, float* p_sa, const void* wo, void* dy, const void* q,
+                        const void* k, const void* v, const void* y, const float* lse, const float* cos_t,
+                        const float* sin_t, void* dqkv, const void* wqkv, float* dn1, void* dqkv_full,
+                        const float* ht, const float* rstd1, const float* w1, const float* g1, const float* h0,
+                        const float* alpha, int accumulate, float* dh_in, float* dh0, float* p_film1, float* p_alpha,
+                        const float* mlp_next, const float* s_mlp_next, void* a_next, float* p_sm_next, void* stream);
 int rte_replay_param_reduce(int T, int B, int S, int d, const float* p_film1, const float* p_film2,
                             const float* p_sa, const float* p_sm, const float* p_alpha, float* out, void* stream);
 

@@ -10,33 +10,33 @@
 //   mlp = z Wd (recipe slabs' rows)         h' = active ? u + s_mlp mlp : h
 //
 // The replay runs a handful of samples (64 rows each at the bench shape).  There every launch is
-// bound by memory latency, not work: a dependent global access costs about as much as the whole
-// tile's arithmetic.  So every kernel owns a 64-row tile of one sample and a 64-column output
-// tile, issues all the loads that do not depend on the recipe together with the sample's recipe
-// record (one round trip), then the recipe-dependent weight panel (a second round trip, overlapped
-// with the row arithmetic), and runs its MFMAs from LDS.  Only the recipe's heads (64 columns
-// each) and 32-neuron slab blocks take part.  The record of each (pass, sample), gathered once per
-// replay, is int32 [W], W = 4 + 2 H + 2 NB:
+// bound by memory latency and by how much one CU can pull, not by arithmetic.  So the products run
+// as tile kernels that read only bf16 panels: each owns a 64-row tile of one sample and a 64-column
+// output tile, loads its A panel together with the sample's recipe record (one round trip), then
+// the recipe's weight rows (a second), and runs its MFMAs from LDS.  The RMSNorm forward and
+// backward, whose row statistics need whole rows, run as row kernels spread over many workgroups
+// (one wave per row).  Only the recipe's heads (64 columns each) and 32-neuron slab blocks take
+// part.  The record of each (pass, sample), gathered once per replay, is int32 [W],
+// W = 4 + 2 H + 2 NB:
 //   act | nh | nb | 0 | heads[H] (ascending) | ihead[H] (slot or -1) | blks[NB] | iblk[NB]
 //
-//   forward per pass : qkv (norm1 + QKV + RoPE, compact heads) -> attention (attention.hip) ->
-//                      oproj (O-projection + residual) -> upgate (norm2 + up/gate + SwiGLU) ->
-//                      down (down-projection + residual)
-//   backward per pass: down_bwd (dz + SwiGLU backward) -> upgate_bwd (dn2) -> oproj_bwd (norm2
-//                      backward, residual, dy) -> attention backward (dqkv, RoPE undone) ->
-//                      qkv_bwd (dn1) -> norm_bwd (norm1 backward, residual, dh, dh0 and every
-//                      FiLM / scale / skip partial)
+//   forward per pass : axpy_norm (h~, n1) -> qkv (QKV + RoPE, compact heads) -> attention
+//                      (attention.hip) -> oproj (O-projection) -> axpy_norm (u, n2) -> upgate
+//                      (up/gate + SwiGLU) -> down (down-projection + residual)
+//   backward per pass: down_bwd (dz + SwiGLU backward) -> upgate_bwd (dn2) -> norm2_bwd (du,
+//                      d_attn, FiLM2 / s_attn partials) -> dy (O-projection backward) ->
+//                      attention backward (dqkv, RoPE undone) -> qkv_bwd (dn1) -> norm1_bwd (dh,
+//                      dh0, FiLM1 / alpha partials, and the next pass's down operand)
 //
 // Weight gradients are not formed here: the kernels write each pass's product operands at full
 // width (zeros outside the recipe's heads / slabs), so one plain GEMM per weight over all passes'
-// rows forms them afterwards.  FiLM, scale and skip gradients leave as per-(tile, column)
-// partials, summed by param_reduce in a fixed order.  No atomics: results repeat bitwise.
+// rows forms them afterwards.  FiLM, scale and skip gradients leave as per-workgroup partials,
+// summed by param_reduce in a fixed order.  No atomics: results repeat bitwise.
 //
 // MFMA lane layout (32x32x16 bf16): lane l supplies A row l % 32 and B column l % 32 with k values
 // 8 (l / 32) .. +7 of each 16-step; output register r of lane l holds row 8 (r / 4) + 4 (l / 32)
-// + r % 4, column l % 32.  Eight waves (512 threads) per workgroup: waves w and w + 4 take the two
-// halves of K on quadrant w % 4 of the 64 x 64 tile.  Row work maps thread t to row t / 8 and the
-// 64-column segment t % 8 of that row.
+// + r % 4, column l % 32.  Eight waves (512 threads) per tile workgroup: waves w and w + 4 take the
+// two halves of K on quadrant w % 4 of the 64 x 64 tile.
 #include "common.hpp"
 
 namespace rte {
@@ -51,7 +51,6 @@ constexpr int kLda = kKC + 8;             // panel pitch in bf16 (16 bytes of pa
 constexpr int kPanel = kRows * kLda;      // bf16 elements per panel
 constexpr int kCp = kCols + 4;            // epilogue staging pitch (fp32)
 constexpr int kMaxD = 512;
-constexpr int kSeg = 64;                  // columns of a row per thread (d <= 8 kSeg)
 constexpr int kHd = 64;                   // head width
 constexpr int kBlk = 32;                  // neurons per slab block
 constexpr int kInfoMax = 1024;            // record words
@@ -94,23 +93,6 @@ __device__ __forceinline__ Tile tile_of(const Meta& M) {
   return t;
 }
 
-// Row work: thread -> (row, segment of kSeg columns)
-struct RowPos {
-  int row, seg, cb;
-  bool ok;        // row inside the sample and segment inside d
-  int64_t base;   // offset of the segment in a [M, d] matrix
-};
-
-__device__ __forceinline__ RowPos row_pos(const Tile& T, int d) {
-  RowPos p;
-  p.row = threadIdx.x >> 3;
-  p.seg = threadIdx.x & 7;
-  p.cb = p.seg * kSeg;
-  p.ok = p.row < T.nrows && p.cb < d;
-  p.base = (T.row0 + p.row) * d + p.cb;
-  return p;
-}
-
 struct Smem {
   bf16* A;
   bf16* B;
@@ -145,30 +127,6 @@ struct InfoLoad {
   }
 };
 
-// Norm vectors into LDS: vec[j d + c] = p_j[c] for up to four vectors (null: zeros)
-struct VecLoad {
-  float v[4];
-  int n;
-  __device__ __forceinline__ void issue(const float* p0, const float* p1, const float* p2, const float* p3, int nv,
-                                        int d) {
-    n = nv * d;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = threadIdx.x + kThreads * k;
-      const int j = i / d, c = i - j * d;
-      const float* p = j == 0 ? p0 : (j == 1 ? p1 : (j == 2 ? p2 : p3));
-      v[k] = (i < n && p) ? p[c] : 0.0f;
-    }
-  }
-  __device__ __forceinline__ void commit(float* dst) const {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int i = threadIdx.x + kThreads * k;
-      if (i < n) dst[i] = v[k];
-    }
-  }
-};
-
 __device__ __forceinline__ f32x16_v zero16() {
   f32x16_v z;
 #pragma unroll
@@ -180,23 +138,6 @@ __device__ __forceinline__ float wsum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
-}
-
-// Sum of v over the row's 8 segment threads (adjacent lanes)
-__device__ __forceinline__ float row_sum(float v) {
-  v += __shfl_xor(v, 1, 64);
-  v += __shfl_xor(v, 2, 64);
-  v += __shfl_xor(v, 4, 64);
-  return v;
-}
-
-// Sum of v over the workgroup (red: 8 floats of LDS); every thread gets it, in a fixed order.
-__device__ __forceinline__ float block_sum(float v, float* red) {
-  v = wsum(v);
-  __syncthreads();
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-  __syncthreads();
-  return ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
 }
 
 __device__ __forceinline__ void to_f8(uint4 u, float* v) {
@@ -236,16 +177,6 @@ __device__ __forceinline__ void ldn(const float* p, bool ok, float* v) {
     } else {
       v[j] = v[j + 1] = v[j + 2] = v[j + 3] = 0.0f;
     }
-  }
-}
-
-// N consecutive floats of an LDS vector (16-byte aligned)
-template <int N>
-__device__ __forceinline__ void lds_n(const float* p, float* v) {
-#pragma unroll
-  for (int j = 0; j < N; j += 4) {
-    const float4 a = *reinterpret_cast<const float4*>(p + j);
-    v[j] = a.x; v[j + 1] = a.y; v[j + 2] = a.z; v[j + 3] = a.w;
   }
 }
 
@@ -334,37 +265,6 @@ __device__ __forceinline__ void stage_acc(float* C, const f32x16_v& acc) {
   __syncthreads();
 }
 
-// rstd of the row from the thread's kSeg columns
-__device__ __forceinline__ float norm_rstd(const float* x, int d, float eps) {
-  float ss = 0.0f;
-#pragma unroll
-  for (int i = 0; i < kSeg; ++i) ss += x[i] * x[i];
-  return rsqrtf(row_sum(ss) / (float)d + eps);
-}
-
-// n = bf16(x rstd w (1 + g) + beta) of the thread's segment into the A panel, vec = w | g | beta
-// (length d each, LDS); the writer stores x and n.
-__device__ __forceinline__ void norm_to_panel(bf16* Ap, const float* vec, const float* x, float rstd, int d,
-                                              const RowPos& P, bool writer, float* x_out, bf16* n_out) {
-  if (P.cb >= d) return;
-  if (writer && P.ok && x_out) {
-#pragma unroll
-    for (int j = 0; j < kSeg; j += 4) st4f(x_out + P.base + j, x + j);
-  }
-#pragma unroll
-  for (int g = 0; g < kSeg / 8; ++g) {
-    float w8[8], g8[8], b8[8], o[8];
-    lds_n<8>(vec + P.cb + 8 * g, w8);
-    lds_n<8>(vec + d + P.cb + 8 * g, g8);
-    lds_n<8>(vec + 2 * d + P.cb + 8 * g, b8);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = P.ok ? x[8 * g + j] * rstd * w8[j] * (1.0f + g8[j]) + b8[j] : 0.0f;
-    const uint4 u = from_f8(o);
-    *reinterpret_cast<uint4*>(Ap + P.row * kLda + P.cb + 8 * g) = u;
-    if (writer && P.ok && n_out) *reinterpret_cast<uint4*>(n_out + P.base + 8 * g) = u;
-  }
-}
-
 // Zero rows [row0, row0 + nrows) x columns [c0, c0 + nc) of a bf16 matrix (nc % 8 == 0)
 __device__ __forceinline__ void zero_bf16(bf16* p, int64_t ld, int64_t row0, int nrows, int c0, int nc) {
   const int upr = nc >> 3;
@@ -406,40 +306,30 @@ __device__ __forceinline__ int epi_col() { return (threadIdx.x & 7) * 8; }
 
 // ============================================================================ forward
 
-// grid (3 Hmax, B rts): column tile c = (part, slot) of the compact q | k | v heads.
+// grid (3 Hmax, B rts): column tile c = (part, slot) of the compact q | k | v heads from the bf16
+// norm rows n1 (A panel), RoPE on q and k.
 __global__ void __launch_bounds__(kThreads) rp_qkv_fwd_kernel(Meta M, const int32_t* __restrict__ info,
-                                                               const float* __restrict__ h,
-                                                               const float* __restrict__ h0,
-                                                               const float* __restrict__ alpha, const float* w1,
-                                                               const float* g1, const float* b1, float eps,
+                                                               const bf16* __restrict__ n1,
                                                                const bf16* __restrict__ wqkv_t,
                                                                const float* __restrict__ cs,
-                                                               const float* __restrict__ sn, float* __restrict__ ht,
-                                                               bf16* __restrict__ n1, float* __restrict__ rstd1,
-                                                               bf16* __restrict__ q, bf16* __restrict__ k,
-                                                               bf16* __restrict__ v) {
+                                                               const float* __restrict__ sn, bf16* __restrict__ q,
+                                                               bf16* __restrict__ k, bf16* __restrict__ v) {
   extern __shared__ __align__(16) char smem[];
   const Smem L = smem_of(smem);
   const Tile T = tile_of(M);
   const int d = M.d;
-  const RowPos P = row_pos(T, d);
   const int c = blockIdx.x, part = c / M.Hmax, slot = c - part * M.Hmax;
-  const bool writer = c == 0;
-  // round trip 1: the record, the rows, the norm vectors, this thread's RoPE factors
+  // round trip 1: the record, the A panel, this thread's RoPE factors
   InfoLoad il;
   il.issue(info, M, T.b);
-  float x[kSeg], y[kSeg];
-  ldn<kSeg>(h + P.base, P.ok, x);
-  if (alpha) ldn<kSeg>(h0 + P.base, P.ok, y);
-  const float al = alpha ? *alpha : 0.0f;
-  VecLoad vl;
-  vl.issue(w1, g1, b1, nullptr, 3, d);
+  PanelLoad la;
+  la.issue(0, d, [&](int r, int kk) -> const bf16* { return r < T.nrows ? n1 + (T.row0 + r) * d + kk : nullptr; });
   const int er = epi_row(), ec = epi_col(), s = T.s0 + er;
   float cv[8], sv[8];
   ldn<8>(cs + (int64_t)s * kHd + ec, part < 2 && er < T.nrows, cv);
   ldn<8>(sn + (int64_t)s * kHd + ec, part < 2 && er < T.nrows, sv);
   il.commit(L.inf, M);
-  vl.commit(L.vec);
+  la.commit(L.A);
   __syncthreads();
   const Info I{L.inf, M.H, M.NB};
   bf16* dst = part == 0 ? q : (part == 1 ? k : v);
@@ -447,20 +337,12 @@ __global__ void __launch_bounds__(kThreads) rp_qkv_fwd_kernel(Meta M, const int3
   if (!I.act() || slot >= I.nh()) {
     // an inactive sample or an unused head slot: zeros (the attention reads every slot)
     zero_bf16(dst, kHd, head_base + T.s0, T.nrows, 0, kHd);
-    if (!I.act() && writer) zero_bf16(n1, d, T.row0, T.nrows, 0, d);
     return;
   }
-  // round trip 2: the head's weight rows, overlapped with the norm
+  // round trip 2: the head's weight rows
   const bf16* wrow = wqkv_t + ((int64_t)part * d + (int64_t)I.head(slot) * kHd) * d;
   PanelLoad lb;
   lb.issue(0, d, [&](int r, int kk) -> const bf16* { return wrow + (int64_t)r * d + kk; });
-  if (alpha) {
-#pragma unroll
-    for (int i = 0; i < kSeg; ++i) x[i] += al * y[i];
-  }
-  const float rstd = norm_rstd(x, d, eps);
-  if (writer && P.ok && P.seg == 0) rstd1[T.row0 + P.row] = rstd;
-  norm_to_panel(L.A, L.vec, x, rstd, d, P, writer, ht, n1);
   lb.commit(L.B);
   __syncthreads();
   f32x16_v acc = zero16();
@@ -482,14 +364,12 @@ __global__ void __launch_bounds__(kThreads) rp_qkv_fwd_kernel(Meta M, const int3
   *reinterpret_cast<uint4*>(dst + (head_base + s) * kHd + ec) = from_f8(o);
 }
 
-// grid (d / 64, B rts): attn = y Wo over the recipe's heads, u = h~ + s_attn attn; y_full (the
-// O-projection weight gradient's operand) gets head c's 64 columns or zeros.
+// grid (d / 64, B rts): attn = y Wo over the recipe's heads; y_full (the O-projection weight
+// gradient's operand) gets head c's 64 columns or zeros.
 __global__ void __launch_bounds__(kThreads) rp_oproj_fwd_kernel(Meta M, const int32_t* __restrict__ info,
                                                                  const bf16* __restrict__ y,
                                                                  const bf16* __restrict__ wo_t,
-                                                                 const float* __restrict__ ht,
-                                                                 const float* __restrict__ s_attn,
-                                                                 float* __restrict__ attn, float* __restrict__ u,
+                                                                 float* __restrict__ attn,
                                                                  bf16* __restrict__ y_full) {
   extern __shared__ __align__(16) char smem[];
   const Smem L = smem_of(smem);
@@ -504,9 +384,6 @@ __global__ void __launch_bounds__(kThreads) rp_oproj_fwd_kernel(Meta M, const in
   la.issue(0, ldy, [&](int r, int kk) -> const bf16* {
     return r < T.nrows ? y + (T.row0 + r) * ldy + kk : nullptr;
   });
-  float hv[8];
-  ldn<8>(ht + off, rok, hv);
-  const float sa = *s_attn;
   il.commit(L.inf, M);
   la.commit(L.A);
   __syncthreads();
@@ -527,51 +404,33 @@ __global__ void __launch_bounds__(kThreads) rp_oproj_fwd_kernel(Meta M, const in
   float* C = reinterpret_cast<float*>(L.B);
   stage_acc(C, acc);
   if (!rok) return;
-  float a8[8], u8[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    a8[j] = C[er * kCp + ec + j];
-    u8[j] = hv[j] + sa * a8[j];
-  }
-  st4f(attn + off, a8);
-  st4f(attn + off + 4, a8 + 4);
-  st4f(u + off, u8);
-  st4f(u + off + 4, u8 + 4);
+  st4f(attn + off, C + er * kCp + ec);
+  st4f(attn + off + 4, C + er * kCp + ec + 4);
   const int sl = I.ihead(c);  // head c's slot in the compact row (still in the A panel)
   uint4 v0 = make_uint4(0u, 0u, 0u, 0u);
   if (sl >= 0) v0 = *reinterpret_cast<const uint4*>(L.A + er * kLda + sl * kHd + ec);
   *reinterpret_cast<uint4*>(y_full + off) = v0;
 }
 
-// grid (NBmax, B rts): slot c's 32 neurons: [up | gate] = n2 [Wup | Wgate] rows, SwiGLU; ug keeps the
-// bf16 pre-activations ([up 32 | gate 32] per slot), z = w up silu(gate).
+// grid (NBmax, B rts): slot c's 32 neurons: [up | gate] = n2 [Wup | Wgate] rows from the bf16 norm
+// rows n2, SwiGLU; ug keeps the bf16 pre-activations ([up 32 | gate 32] per slot), z = w up silu(gate).
 __global__ void __launch_bounds__(kThreads) rp_upgate_fwd_kernel(Meta M, const int32_t* __restrict__ info,
-                                                                  const float* __restrict__ u, const float* w2,
-                                                                  const float* g2, const float* b2, float eps,
+                                                                  const bf16* __restrict__ n2,
                                                                   const bf16* __restrict__ wug_t, float route_w,
-                                                                  bf16* __restrict__ n2, float* __restrict__ rstd2,
                                                                   bf16* __restrict__ ug, bf16* __restrict__ z) {
   extern __shared__ __align__(16) char smem[];
   const Smem L = smem_of(smem);
   const Tile T = tile_of(M);
   const int c = blockIdx.x, d = M.d;
-  const RowPos P = row_pos(T, d);
-  const bool writer = c == 0;
   InfoLoad il;
   il.issue(info, M, T.b);
-  float x[kSeg];
-  ldn<kSeg>(u + P.base, P.ok, x);
-  VecLoad vl;
-  vl.issue(w2, g2, b2, nullptr, 3, d);
+  PanelLoad la;
+  la.issue(0, d, [&](int r, int kk) -> const bf16* { return r < T.nrows ? n2 + (T.row0 + r) * d + kk : nullptr; });
   il.commit(L.inf, M);
-  vl.commit(L.vec);
+  la.commit(L.A);
   __syncthreads();
   const Info I{L.inf, M.H, M.NB};
-  if (!I.act()) {
-    if (writer) zero_bf16(n2, d, T.row0, T.nrows, 0, d);
-    return;
-  }
-  if (c >= I.nb()) return;
+  if (!I.act() || c >= I.nb()) return;
   const int blk = I.blk(c);
   const int64_t F = M.F;
   PanelLoad lb;
@@ -579,9 +438,6 @@ __global__ void __launch_bounds__(kThreads) rp_upgate_fwd_kernel(Meta M, const i
     const int64_t nrow = r < kBlk ? (int64_t)blk * kBlk + r : F + (int64_t)blk * kBlk + (r - kBlk);
     return wug_t + nrow * d + kk;
   });
-  const float rstd = norm_rstd(x, d, eps);
-  if (writer && P.ok && P.seg == 0) rstd2[T.row0 + P.row] = rstd;
-  norm_to_panel(L.A, L.vec, x, rstd, d, P, writer, nullptr, n2);
   lb.commit(L.B);
   __syncthreads();
   f32x16_v acc = zero16();
@@ -684,33 +540,25 @@ __global__ void __launch_bounds__(kThreads) rp_down_fwd_kernel(Meta M, const int
 
 // ============================================================================ backward
 
-// grid (ceil(NBmax / 2), B rts): dz = s_mlp dh Wd^T over two slots (64 neurons), SwiGLU backward
-// into dug ([d up 32 | d gate 32] per slot).  The writer (c = 0) stores d_mlp = bf16(s_mlp dh) (the
-// down weight gradient's operand) and the tile's sum of dh mlp (the s_mlp gradient).
+// grid (ceil(NBmax / 2), B rts): dz = a_mlp Wd^T over two slots (64 neurons) with a_mlp =
+// bf16(s_mlp dh) (row kernels make it), SwiGLU backward into dug ([d up 32 | d gate 32] per slot).
 __global__ void __launch_bounds__(kThreads) rp_down_bwd_kernel(Meta M, const int32_t* __restrict__ info,
-                                                                const float* __restrict__ dh,
-                                                                const float* __restrict__ mlp,
-                                                                const float* __restrict__ s_mlp,
+                                                                const bf16* __restrict__ a_mlp,
                                                                 const bf16* __restrict__ wd,
                                                                 const bf16* __restrict__ ug, float route_w,
-                                                                bf16* __restrict__ dug, bf16* __restrict__ d_mlp,
-                                                                float* __restrict__ p_sm) {
+                                                                bf16* __restrict__ dug) {
   extern __shared__ __align__(16) char smem[];
   const Smem L = smem_of(smem);
   const Tile T = tile_of(M);
-  const int c = blockIdx.x, d = M.d, tid = threadIdx.x;
-  const RowPos P = row_pos(T, d);
-  const bool writer = c == 0;
+  const int c = blockIdx.x, d = M.d;
   const int64_t ldu = (int64_t)M.NBmax * 2 * kBlk;
-  const int er = epi_row(), e = tid & 7;
+  const int er = epi_row(), e = threadIdx.x & 7;
   const int sl = 2 * c + (e >> 2), n0 = (e & 3) * 8;  // epilogue: 8 neurons of one slot
   const bool eok = er < T.nrows && sl < M.NBmax;
   InfoLoad il;
   il.issue(info, M, T.b);
-  float x[kSeg], mv[kSeg];
-  ldn<kSeg>(dh + P.base, P.ok, x);
-  if (writer) ldn<kSeg>(mlp + P.base, P.ok, mv);
-  const float sm = *s_mlp;
+  PanelLoad la;
+  la.issue(0, d, [&](int r, int kk) -> const bf16* { return r < T.nrows ? a_mlp + (T.row0 + r) * d + kk : nullptr; });
   uint4 uq[2] = {};
   if (eok) {
     const bf16* ugr = ug + (T.row0 + er) * ldu + sl * 2 * kBlk;
@@ -718,41 +566,16 @@ __global__ void __launch_bounds__(kThreads) rp_down_bwd_kernel(Meta M, const int
     uq[1] = *reinterpret_cast<const uint4*>(ugr + kBlk + n0);
   }
   il.commit(L.inf, M);
+  la.commit(L.A);
   __syncthreads();
   const Info I{L.inf, M.H, M.NB};
-  if (!I.act()) {
-    if (writer) {
-      zero_bf16(d_mlp, d, T.row0, T.nrows, 0, d);
-      if (tid == 0) p_sm[blockIdx.y] = 0.0f;
-    }
-    return;
-  }
   const int nbv = I.nb();
-  if (2 * c >= nbv) return;
+  if (!I.act() || 2 * c >= nbv) return;
   PanelLoad lb;
   lb.issue(0, d, [&](int r, int kk) -> const bf16* {
     const int s_ = 2 * c + r / kBlk;
     return s_ < nbv ? wd + ((int64_t)I.blk(s_) * kBlk + (r % kBlk)) * d + kk : nullptr;
   });
-  float dsum = 0.0f;
-  if (P.cb < d) {
-#pragma unroll
-    for (int g = 0; g < kSeg / 8; ++g) {
-      float o[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        o[j] = x[8 * g + j] * sm;
-        if (writer) dsum += x[8 * g + j] * mv[8 * g + j];
-      }
-      const uint4 uv = from_f8(o);
-      *reinterpret_cast<uint4*>(L.A + P.row * kLda + P.cb + 8 * g) = uv;
-      if (writer && P.ok) *reinterpret_cast<uint4*>(d_mlp + P.base + 8 * g) = uv;
-    }
-  }
-  if (writer) {
-    const float tot = block_sum(dsum, L.red);
-    if (tid == 0) p_sm[blockIdx.y] = tot;
-  }
   lb.commit(L.B);
   __syncthreads();
   f32x16_v acc = zero16();
@@ -832,98 +655,35 @@ __global__ void __launch_bounds__(kThreads) rp_upgate_bwd_kernel(Meta M, const i
   });
 }
 
-// grid (d / 64, B rts).  Every tile: du = dh + the rmsnorm-FiLM backward of dn2 (the row dot over the
-// whole row), A = bf16(s_attn du).  Tile c stores du and d_attn = A (the O weight gradient's operand)
-// on its 64 columns, and for c < Hmax forms head slot c of dy = A Wo^T (zeros for an unused slot).
-__global__ void __launch_bounds__(kThreads) rp_oproj_bwd_kernel(Meta M, const int32_t* __restrict__ info,
-                                                                 const float* __restrict__ dh,
-                                                                 const float* __restrict__ dn2,
-                                                                 const float* __restrict__ u,
-                                                                 const float* __restrict__ rstd2, const float* w2,
-                                                                 const float* g2, const float* __restrict__ s_attn,
-                                                                 const bf16* __restrict__ wo, float* __restrict__ du,
-                                                                 bf16* __restrict__ d_attn, bf16* __restrict__ dy) {
+// grid (Hmax, B rts): head slot c of dy = d_attn Wo^T (d_attn = bf16(s_attn du), the row kernel's
+// output), zeros for an unused slot or an inactive sample (the attention backward reads every slot).
+__global__ void __launch_bounds__(kThreads) rp_dy_kernel(Meta M, const int32_t* __restrict__ info,
+                                                          const bf16* __restrict__ d_attn,
+                                                          const bf16* __restrict__ wo, bf16* __restrict__ dy) {
   extern __shared__ __align__(16) char smem[];
   const Smem L = smem_of(smem);
   const Tile T = tile_of(M);
-  const int c = blockIdx.x, d = M.d, tid = threadIdx.x;
-  const RowPos P = row_pos(T, d);
+  const int c = blockIdx.x, d = M.d;
   const int64_t ldy = (int64_t)M.Hmax * kHd;
   InfoLoad il;
   il.issue(info, M, T.b);
-  float a[kSeg], x[kSeg], g[kSeg];
-  ldn<kSeg>(dn2 + P.base, P.ok, a);
-  ldn<kSeg>(u + P.base, P.ok, x);
-  ldn<kSeg>(dh + P.base, P.ok, g);
-  const float rs = P.row < T.nrows ? rstd2[T.row0 + P.row] : 0.0f;
-  const float sa = *s_attn;
-  VecLoad vl;
-  vl.issue(w2, g2, nullptr, nullptr, 2, d);
+  PanelLoad la;
+  la.issue(0, d, [&](int r, int kk) -> const bf16* { return r < T.nrows ? d_attn + (T.row0 + r) * d + kk : nullptr; });
   il.commit(L.inf, M);
-  vl.commit(L.vec);
+  la.commit(L.A);
   __syncthreads();
   const Info I{L.inf, M.H, M.NB};
-  auto zero_dy = [&]() {
+  if (!I.act() || c >= I.nh()) {
     const int upr = kHd / 8;
-    for (int uu = tid; uu < T.nrows * upr; uu += kThreads) {
+    for (int uu = threadIdx.x; uu < T.nrows * upr; uu += kThreads) {
       const int r = uu / upr;
       *reinterpret_cast<uint4*>(dy + (T.row0 + r) * ldy + c * kHd + (uu - r * upr) * 8) = make_uint4(0u, 0u, 0u, 0u);
     }
-  };
-  if (!I.act()) {
-    if (c < M.Hmax) zero_dy();
-    zero_bf16(d_attn, d, T.row0, T.nrows, c * kCols, kCols);
     return;
   }
-  float dot = 0.0f;
-  if (P.cb < d) {
-#pragma unroll
-    for (int gg = 0; gg < kSeg / 8; ++gg) {
-      float w8[8], g8[8];
-      lds_n<8>(L.vec + P.cb + 8 * gg, w8);
-      lds_n<8>(L.vec + d + P.cb + 8 * gg, g8);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        a[8 * gg + j] *= w8[j] * (1.0f + g8[j]);  // dn^
-        dot += a[8 * gg + j] * x[8 * gg + j];
-      }
-    }
-  }
-  const float mean = row_sum(dot) * rs / (float)d;
-#pragma unroll
-  for (int i = 0; i < kSeg; ++i) a[i] = rs * (a[i] - x[i] * rs * mean);  // the norm term; x is done
-  // round trip 2: the head's weight rows, overlapped with du and the A panel
-  const bool mm = c < M.Hmax && c < I.nh();
+  const int head = I.head(c);
   PanelLoad lb;
-  if (mm) {
-    const int head = I.head(c);
-    lb.issue(0, d, [&](int r, int kk) -> const bf16* { return wo + ((int64_t)head * kHd + r) * d + kk; });
-  }
-  // du = dh + norm term; A panel and (from segment c of the row) tile c's du / d_attn columns
-  if (P.cb < d) {
-#pragma unroll
-    for (int gg = 0; gg < kSeg / 8; ++gg) {
-      float o[8], dv[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int i = 8 * gg + j;
-        dv[j] = P.ok ? g[i] + a[i] : 0.0f;
-        o[j] = sa * dv[j];
-      }
-      const uint4 av = from_f8(o);
-      *reinterpret_cast<uint4*>(L.A + P.row * kLda + P.cb + 8 * gg) = av;
-      if (P.ok && P.seg == c) {
-        st4f(du + P.base + 8 * gg, dv);
-        st4f(du + P.base + 8 * gg + 4, dv + 4);
-        *reinterpret_cast<uint4*>(d_attn + P.base + 8 * gg) = av;
-      }
-    }
-  }
-  if (c >= M.Hmax) return;
-  if (!mm) {
-    zero_dy();
-    return;
-  }
+  lb.issue(0, d, [&](int r, int kk) -> const bf16* { return wo + ((int64_t)head * kHd + r) * d + kk; });
   lb.commit(L.B);
   __syncthreads();
   f32x16_v acc = zero16();
@@ -990,157 +750,212 @@ __global__ void __launch_bounds__(kThreads) rp_qkv_bwd_kernel(Meta M, const int3
   });
 }
 
-// grid (d / 64, B rts): dh~ = du + the rmsnorm-FiLM backward of dn1 (the row dot over the whole row,
-// every tile), then tile c's columns: dh_in = dh~ (inactive samples: dh_in = dh), dh0 (+)= alpha dh~,
-// and the tile's partials: dw1 | dg1 | db1 and dw2 | dg2 | db2 per column, sum du attn (s_attn)
-// and sum dh~ h0 (alpha).
-__global__ void __launch_bounds__(kThreads) rp_norm_bwd_kernel(Meta M, const int32_t* __restrict__ info,
-                                                                const float* __restrict__ dn1,
-                                                                const float* __restrict__ du,
-                                                                const float* __restrict__ dh,
-                                                                const float* __restrict__ ht,
-                                                                const float* __restrict__ rstd1, const float* w1,
-                                                                const float* g1, const float* __restrict__ h0,
-                                                                const float* __restrict__ alpha,
-                                                                const float* __restrict__ dn2,
-                                                                const float* __restrict__ u,
-                                                                const float* __restrict__ rstd2, const float* w2,
-                                                                const float* g2, const float* __restrict__ attn,
-                                                                int accumulate, float* __restrict__ dh_in,
-                                                                float* __restrict__ dh0, float* __restrict__ p_film1,
-                                                                float* __restrict__ p_film2, float* __restrict__ p_sa,
-                                                                float* __restrict__ p_alpha) {
-  extern __shared__ __align__(16) char smem[];
-  const Smem L = smem_of(smem);
-  float* Pw = reinterpret_cast<float*>(smem);  // 6 x [64][kCols] partial terms (panel area)
-  const Tile T = tile_of(M);
-  const int c = blockIdx.x, d = M.d, tid = threadIdx.x;
-  const RowPos P = row_pos(T, d);
-  const int nct = gridDim.x;
-  const int er = epi_row(), ec = epi_col();
-  const bool rok = er < T.nrows;
-  const int own0 = c * kCols;
-  const int64_t off = (T.row0 + er) * d + own0 + ec;
-  InfoLoad il;
-  il.issue(info, M, T.b);
-  float a[kSeg], x[kSeg];
-  ldn<kSeg>(dn1 + P.base, P.ok, a);
-  ldn<kSeg>(ht + P.base, P.ok, x);
-  const float rs1r = P.row < T.nrows ? rstd1[T.row0 + P.row] : 0.0f;
-  const float rs1 = rok ? rstd1[T.row0 + er] : 0.0f;
-  const float rs2 = rok ? rstd2[T.row0 + er] : 0.0f;
-  const float al = alpha ? *alpha : 0.0f;
-  VecLoad vl;
-  vl.issue(w1, g1, w2, g2, 4, d);
-  // this thread's 8 columns of tile c
-  float a1[8], x1[8], uu[8], zz[8], dd[8], a2[8], x2[8], at[8];
-  ldn<8>(dn1 + off, rok, a1);
-  ldn<8>(ht + off, rok, x1);
-  ldn<8>(du + off, rok, uu);
-  ldn<8>(h0 + off, rok && h0, zz);
-  ldn<8>(dh + off, rok, dd);
-  ldn<8>(dn2 + off, rok, a2);
-  ldn<8>(u + off, rok, x2);
-  ldn<8>(attn + off, rok, at);
-  il.commit(L.inf, M);
-  vl.commit(L.vec);
-  __syncthreads();
-  const Info I{L.inf, M.H, M.NB};
-  float* pf1 = p_film1 + (int64_t)blockIdx.y * 3 * d;
-  float* pf2 = p_film2 + (int64_t)blockIdx.y * 3 * d;
-  if (!I.act()) {
-    if (rok) {
-      st4f(dh_in + off, dd);
-      st4f(dh_in + off + 4, dd + 4);
-      if (dh0 && !accumulate) {
-        const float zf[4] = {0.f, 0.f, 0.f, 0.f};
-        st4f(dh0 + off, zf);
-        st4f(dh0 + off + 4, zf);
-      }
-    }
-    for (int i = tid; i < 3 * kCols; i += kThreads) {
-      pf1[(i / kCols) * d + own0 + (i % kCols)] = 0.0f;
-      pf2[(i / kCols) * d + own0 + (i % kCols)] = 0.0f;
-    }
-    if (tid == 0) {
-      p_sa[(int64_t)blockIdx.y * nct + c] = 0.0f;
-      p_alpha[(int64_t)blockIdx.y * nct + c] = 0.0f;
-    }
-    return;
-  }
-  const float* v1 = L.vec;           // w1 | g1
-  const float* v2 = L.vec + 2 * d;   // w2 | g2
-  float dot = 0.0f;
-  if (P.cb < d) {
+// ---------------------------------------------------------------------------- row kernels
+// One wave per row (four rows per workgroup), lane l on columns [8 l, 8 l + 8) (d <= 512): the
+// norm backwards, whose row dots need whole rows.  Per-workgroup partials of the parameter
+// gradients (sums over the workgroup's rows, fixed order) go to param_reduce.
+
+constexpr int kRowWG = 4;
+
+struct RowCtx {
+  int64_t m;      // global row
+  int c0;         // first column of the lane
+  bool ok, act;   // row exists, lane inside d; sample takes this pass
+};
+
+__device__ __forceinline__ RowCtx row_ctx(const Meta& M, const int32_t* info) {
+  RowCtx r;
+  r.m = (int64_t)blockIdx.x * kRowWG + (threadIdx.x >> 6);
+  r.c0 = (threadIdx.x & 63) * 8;
+  const bool row_ok = r.m < (int64_t)M.B * M.S;
+  r.ok = row_ok && r.c0 < M.d;
+  r.act = row_ok && info[(r.m / M.S) * M.W] != 0;
+  return r;
+}
+
+__device__ __forceinline__ void ld8(const float* p, bool ok, float* v) { ldn<8>(p, ok, v); }
+
+__device__ __forceinline__ void st8(float* p, const float* v) {
+  st4f(p, v);
+  st4f(p + 4, v + 4);
+}
+
+// Column partials of NT terms [kRowWG waves][NT][d] in LDS summed over the waves into out[t d + c]
+template <int NT>
+__device__ __forceinline__ void wave_col_partials(float* lds, const float (&terms)[NT][8], int d, int c0,
+                                                  float* out) {
+  const int wave = threadIdx.x >> 6;
+  if (c0 < d) {
 #pragma unroll
-    for (int gg = 0; gg < kSeg / 8; ++gg) {
-      float w8[8], g8[8];
-      lds_n<8>(v1 + P.cb + 8 * gg, w8);
-      lds_n<8>(v1 + d + P.cb + 8 * gg, g8);
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) dot += a[8 * gg + j] * w8[j] * (1.0f + g8[j]) * x[8 * gg + j];
-    }
-  }
-  // the row mapping and the tile-column mapping both put thread t on row t / 8
-  const float mean = row_sum(dot) * rs1r / (float)d;
-  float w1v[8], g1v[8], w2v[8], g2v[8];
-  lds_n<8>(v1 + own0 + ec, w1v);
-  lds_n<8>(v1 + d + own0 + ec, g1v);
-  lds_n<8>(v2 + own0 + ec, w2v);
-  lds_n<8>(v2 + d + own0 + ec, g2v);
-  __syncthreads();  // the vectors are read; the panel area becomes the partial terms
-  float osa = 0.0f, oal = 0.0f;
-  float o[8], s0[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float xh1 = x1[j] * rs1, xh2 = x2[j] * rs2;
-    const float dnh = a1[j] * w1v[j] * (1.0f + g1v[j]);
-    o[j] = uu[j] + rs1 * (dnh - xh1 * mean);
-    osa += uu[j] * at[j];
-    oal += o[j] * zz[j];
-    Pw[(0 * kRows + er) * kCols + ec + j] = rok ? a1[j] * (1.0f + g1v[j]) * xh1 : 0.0f;  // dw1
-    Pw[(1 * kRows + er) * kCols + ec + j] = rok ? a1[j] * w1v[j] * xh1 : 0.0f;            // dg1
-    Pw[(2 * kRows + er) * kCols + ec + j] = rok ? a1[j] : 0.0f;                           // db1
-    Pw[(3 * kRows + er) * kCols + ec + j] = rok ? a2[j] * (1.0f + g2v[j]) * xh2 : 0.0f;  // dw2
-    Pw[(4 * kRows + er) * kCols + ec + j] = rok ? a2[j] * w2v[j] * xh2 : 0.0f;            // dg2
-    Pw[(5 * kRows + er) * kCols + ec + j] = rok ? a2[j] : 0.0f;                           // db2
-  }
-  if (rok) {
-    st4f(dh_in + off, o);
-    st4f(dh_in + off + 4, o + 4);
-    if (dh0) {
-      float p8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      if (accumulate) {
-        ld4f(dh0 + off, p8);
-        ld4f(dh0 + off + 4, p8 + 4);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) s0[j] = p8[j] + al * o[j];
-      st4f(dh0 + off, s0);
-      st4f(dh0 + off + 4, s0 + 4);
-    }
-  } else {
-    osa = oal = 0.0f;
+      for (int j = 0; j < 8; ++j) lds[(wave * NT + t) * kMaxD + c0 + j] = terms[t][j];
   }
   __syncthreads();
-  for (int i = tid; i < 6 * kCols; i += kThreads) {
-    const int term = i / kCols, col = i - term * kCols;
+  for (int i = threadIdx.x; i < NT * d; i += 256) {
+    const int t = i / d, c = i - t * d;
     float s = 0.0f;
-    for (int r = 0; r < kRows; ++r) s += Pw[(term * kRows + r) * kCols + col];
-    float* pf = term < 3 ? pf1 : pf2;
-    pf[(term % 3) * d + own0 + col] = s;
-  }
-  const float tsa = block_sum(osa, L.red);
-  const float tal = block_sum(oal, L.red);
-  if (tid == 0) {
-    p_sa[(int64_t)blockIdx.y * nct + c] = tsa;
-    p_alpha[(int64_t)blockIdx.y * nct + c] = tal;
+    for (int w = 0; w < kRowWG; ++w) s += lds[(w * NT + t) * kMaxD + c];
+    out[t * d + c] = s;
   }
 }
 
-// Fixed-order sums of the per-tile partials of T passes: out [T, 6d] = (dw1 | dg1 | db1 | dw2 | dg2 |
-// db2) of each pass, then dw1 [d] and dw2 [d] over all passes, ds_attn [T], ds_mlp [T], dalpha.
-__global__ void __launch_bounds__(256) rp_param_reduce_kernel(int T, int nt, int nct, int d, const float* __restrict__ p1,
+__device__ __forceinline__ float wg_sum(float v, float* red) {
+  v = wsum(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// a_mlp = bf16(s_mlp dh) and the workgroup's sum of dh mlp (the s_mlp gradient): the down
+// backward's operand for the first pass the backward visits (later passes get it from norm1_bwd).
+__global__ void __launch_bounds__(256) rp_dh_prep_kernel(Meta M, const float* __restrict__ dh,
+                                                          const float* __restrict__ mlp,
+                                                          const float* __restrict__ s_mlp, bf16* __restrict__ a_mlp,
+                                                          float* __restrict__ p_sm) {
+  __shared__ float red[4];
+  const int64_t m = (int64_t)blockIdx.x * kRowWG + (threadIdx.x >> 6);
+  const int c0 = (threadIdx.x & 63) * 8, d = M.d;
+  const bool ok = m < (int64_t)M.B * M.S && c0 < d;
+  float x[8], mv[8];
+  ld8(dh + m * d + c0, ok, x);
+  ld8(mlp + m * d + c0, ok, mv);
+  const float sm = *s_mlp;
+  float s = 0.0f, o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    s += x[j] * mv[j];
+    o[j] = sm * x[j];
+  }
+  if (ok) *reinterpret_cast<uint4*>(a_mlp + m * d + c0) = from_f8(o);
+  const float tot = wg_sum(s, red);
+  if (threadIdx.x == 0) p_sm[blockIdx.x] = tot;
+}
+
+// du = dh + rmsnorm-FiLM backward of dn2 (w2, g2, rstd2, u), d_attn = bf16(s_attn du) (zeros for an
+// inactive sample), partials dw2 | dg2 | db2 [nt, 3d] and sum du attn (the s_attn gradient) [nt].
+__global__ void __launch_bounds__(256) rp_norm2_bwd_kernel(Meta M, const int32_t* __restrict__ info,
+                                                            const float* __restrict__ dh, const float* __restrict__ dn2,
+                                                            const float* __restrict__ u, const float* __restrict__ rstd2,
+                                                            const float* __restrict__ w2, const float* __restrict__ g2,
+                                                            const float* __restrict__ attn,
+                                                            const float* __restrict__ s_attn, float* __restrict__ du,
+                                                            bf16* __restrict__ d_attn, float* __restrict__ p_film2,
+                                                            float* __restrict__ p_sa) {
+  __shared__ float lds[kRowWG * 3 * kMaxD];
+  __shared__ float red[4];
+  const RowCtx R = row_ctx(M, info);
+  const int d = M.d;
+  const int64_t off = R.m * d + R.c0;
+  float a[8], x[8], g[8], at[8], w8[8], g8[8];
+  ld8(dn2 + off, R.ok, a);
+  ld8(u + off, R.ok, x);
+  ld8(dh + off, R.ok, g);
+  ld8(attn + off, R.ok, at);
+  ld8(w2 + R.c0, R.c0 < d, w8);
+  ld8(g2 + R.c0, R.c0 < d, g8);
+  const float rs = R.ok ? rstd2[R.m] : 0.0f;
+  const float sa = *s_attn;
+  float dot = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) dot += a[j] * w8[j] * (1.0f + g8[j]) * x[j];
+  const float mean = wsum(dot) * rs / (float)d;
+  float terms[3][8], dv[8], o[8], sat = 0.0f;
+  const bool act = R.act && R.ok;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float xh = x[j] * rs, dnh = a[j] * w8[j] * (1.0f + g8[j]);
+    dv[j] = g[j] + rs * (dnh - xh * mean);
+    o[j] = act ? sa * dv[j] : 0.0f;
+    terms[0][j] = act ? a[j] * (1.0f + g8[j]) * xh : 0.0f;
+    terms[1][j] = act ? a[j] * w8[j] * xh : 0.0f;
+    terms[2][j] = act ? a[j] : 0.0f;
+    sat += act ? dv[j] * at[j] : 0.0f;
+  }
+  if (R.ok) {
+    if (R.act) st8(du + off, dv);
+    *reinterpret_cast<uint4*>(d_attn + off) = from_f8(o);
+  }
+  wave_col_partials<3>(lds, terms, d, R.c0, p_film2 + (int64_t)blockIdx.x * 3 * d);
+  const float tot = wg_sum(sat, red);
+  if (threadIdx.x == 0) p_sa[blockIdx.x] = tot;
+}
+
+// dh~ = du + rmsnorm-FiLM backward of dn1 (w1, g1, rstd1, h~); dh_in = dh~ (inactive: dh_in = dh),
+// dh0 (+)= alpha dh~; partials dw1 | dg1 | db1 [nt, 3d] and sum dh~ h0 (the alpha gradient) [nt].
+// With a_next: the next pass's down operand bf16(s_mlp_next dh_in) and its sum dh_in mlp_next.
+__global__ void __launch_bounds__(256) rp_norm1_bwd_kernel(Meta M, const int32_t* __restrict__ info,
+                                                            const float* __restrict__ dn1, const float* __restrict__ du,
+                                                            const float* __restrict__ dh, const float* __restrict__ ht,
+                                                            const float* __restrict__ rstd1,
+                                                            const float* __restrict__ w1, const float* __restrict__ g1,
+                                                            const float* __restrict__ h0,
+                                                            const float* __restrict__ alpha, int accumulate,
+                                                            float* __restrict__ dh_in, float* __restrict__ dh0,
+                                                            float* __restrict__ p_film1, float* __restrict__ p_alpha,
+                                                            const float* __restrict__ mlp_next,
+                                                            const float* __restrict__ s_mlp_next,
+                                                            bf16* __restrict__ a_next, float* __restrict__ p_sm_next) {
+  __shared__ float lds[kRowWG * 3 * kMaxD];
+  __shared__ float red[4];
+  const RowCtx R = row_ctx(M, info);
+  const int d = M.d;
+  const int64_t off = R.m * d + R.c0;
+  const bool act = R.act && R.ok;
+  float a[8], x[8], uu[8], g[8], z8[8], w8[8], g8[8], mv[8];
+  ld8(dn1 + off, R.ok, a);
+  ld8(ht + off, R.ok, x);
+  ld8(du + off, act, uu);
+  ld8(dh + off, R.ok, g);
+  ld8(h0 + off, R.ok && h0, z8);
+  ld8(w1 + R.c0, R.c0 < d, w8);
+  ld8(g1 + R.c0, R.c0 < d, g8);
+  ld8(mlp_next + off, R.ok && a_next, mv);
+  const float rs = R.ok ? rstd1[R.m] : 0.0f;
+  const float al = alpha ? *alpha : 0.0f;
+  const float smn = a_next ? *s_mlp_next : 0.0f;
+  float dot = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) dot += a[j] * w8[j] * (1.0f + g8[j]) * x[j];
+  const float mean = wsum(dot) * rs / (float)d;
+  float terms[3][8], o[8], s0[8], nx[8], sal = 0.0f, ssm = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float xh = x[j] * rs, dnh = a[j] * w8[j] * (1.0f + g8[j]);
+    const float dht = uu[j] + rs * (dnh - xh * mean);
+    o[j] = act ? dht : g[j];
+    terms[0][j] = act ? a[j] * (1.0f + g8[j]) * xh : 0.0f;
+    terms[1][j] = act ? a[j] * w8[j] * xh : 0.0f;
+    terms[2][j] = act ? a[j] : 0.0f;
+    sal += act ? dht * z8[j] : 0.0f;
+    nx[j] = smn * o[j];
+    ssm += o[j] * mv[j];
+  }
+  if (R.ok) {
+    st8(dh_in + off, o);
+    if (dh0) {
+      float p8[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (accumulate) ld8(dh0 + off, true, p8);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s0[j] = p8[j] + (act ? al * o[j] : 0.0f);
+      st8(dh0 + off, s0);
+    }
+    if (a_next) *reinterpret_cast<uint4*>(a_next + off) = from_f8(nx);
+  }
+  wave_col_partials<3>(lds, terms, d, R.c0, p_film1 + (int64_t)blockIdx.x * 3 * d);
+  const float tal = wg_sum(sal, red);
+  if (threadIdx.x == 0) p_alpha[blockIdx.x] = tal;
+  if (a_next) {
+    const float tsm = wg_sum(ssm, red);
+    if (threadIdx.x == 0) p_sm_next[blockIdx.x] = tsm;
+  }
+}
+
+// Fixed-order sums of the per-workgroup partials of T passes (nt row workgroups each): out [T, 6d] =
+// (dw1 | dg1 | db1 | dw2 | dg2 | db2) of each pass, then dw1 [d] and dw2 [d] over all passes,
+// ds_attn [T], ds_mlp [T], dalpha.
+__global__ void __launch_bounds__(256) rp_param_reduce_kernel(int T, int nt, int d, const float* __restrict__ p1,
                                                                const float* __restrict__ p2, const float* __restrict__ psa,
                                                                const float* __restrict__ psm, const float* __restrict__ pal,
                                                                float* __restrict__ out) {
@@ -1168,7 +983,7 @@ __global__ void __launch_bounds__(256) rp_param_reduce_kernel(int T, int nt, int
   const int64_t k = j - 2 * d;
   if (k < T) {
     float s = 0.0f;
-    for (int r = 0; r < nt * nct; ++r) s += psa[(int64_t)k * nt * nct + r];
+    for (int r = 0; r < nt; ++r) s += psa[(int64_t)k * nt + r];
     out[n_pass + 2 * d + k] = s;
   } else if (k < 2 * T) {
     float s = 0.0f;
@@ -1176,7 +991,7 @@ __global__ void __launch_bounds__(256) rp_param_reduce_kernel(int T, int nt, int
     out[n_pass + 2 * d + k] = s;
   } else if (k == 2 * T) {
     float s = 0.0f;
-    for (int r = 0; r < T * nt * nct; ++r) s += pal[r];
+    for (int r = 0; r < T * nt; ++r) s += pal[r];
     out[n_pass + 2 * d + k] = s;
   }
 }
@@ -1189,11 +1004,10 @@ bool g_lds_set = false;
 
 int replay_prepare() {
   if (g_lds_set) return 0;
-  const void* fns[] = {(const void*)rp_qkv_fwd_kernel,   (const void*)rp_oproj_fwd_kernel,
+  const void* fns[] = {(const void*)rp_qkv_fwd_kernel,  (const void*)rp_oproj_fwd_kernel,
                        (const void*)rp_upgate_fwd_kernel, (const void*)rp_down_fwd_kernel,
-                       (const void*)rp_down_bwd_kernel,   (const void*)rp_upgate_bwd_kernel,
-                       (const void*)rp_oproj_bwd_kernel,  (const void*)rp_qkv_bwd_kernel,
-                       (const void*)rp_norm_bwd_kernel};
+                       (const void*)rp_down_bwd_kernel,  (const void*)rp_upgate_bwd_kernel,
+                       (const void*)rp_dy_kernel,         (const void*)rp_qkv_bwd_kernel};
   for (const void* f : fns) RTE_REQUIRE(set_lds(f, kLds), "replay: cannot raise the LDS limit to %zu bytes", kLds);
   g_lds_set = true;
   return 0;
@@ -1220,6 +1034,11 @@ int attention_fwd(const bf16* q, const bf16* k, const bf16* v, int B, int H, int
 int attention_bwd_qkv(const bf16* q, const bf16* k, const bf16* v, const bf16* out, const bf16* dout,
                       const float* lse, int B, int H, int S, int head_dim, float scale, const float* hscale,
                       const float* cos_t, const float* sin_t, bf16* dqkv, hipStream_t s);
+int axpy_norm_fwd(const float* a, const float* b, const float* c, const float* keep, const uint8_t* mask, int S,
+                  int T, int d, const float* w, const float* gamma, const float* beta, float eps, float* x_out,
+                  bf16* n_out, float* rstd_out, hipStream_t s);
+
+int replay_row_tiles(int B, int S) { return (B * S + kRowWG - 1) / kRowWG; }
 
 int replay_fwd_pass(int B, int S, int d, int H, int F, int NB, int h_max, int nb_max, const int32_t* info,
                     const float* h, const float* h0, const float* alpha, const float* w1, const float* g1,
@@ -1234,64 +1053,82 @@ int replay_fwd_pass(int B, int S, int d, int H, int F, int NB, int h_max, int nb
   RTE_REQUIRE(info && h && h0 && w1 && w2 && s_attn && s_mlp && wqkv_t && wo_t && wug_t && wd_t && cs && sn,
               "replay_fwd: missing input");
   const unsigned rt = (unsigned)(B * M.rts);
-  hipLaunchKernelGGL(rp_qkv_fwd_kernel, dim3(3 * h_max, rt), dim3(kThreads), kLds, s, M, info, h, h0, alpha, w1, g1, b1,
-                     eps1, wqkv_t, cs, sn, ht, n1, rstd1, q, k, v);
+  const int Mrows = B * S;
+  // h~ = h + alpha h0 and its FiLM norm (the axpy / norm row kernel of the per-operator pass)
+  RTE_TRY(axpy_norm_fwd(h, alpha ? h0 : nullptr, alpha, nullptr, nullptr, S, Mrows, d, w1, g1, b1, eps1, ht, n1,
+                        rstd1, s));
+  hipLaunchKernelGGL(rp_qkv_fwd_kernel, dim3(3 * h_max, rt), dim3(kThreads), kLds, s, M, info, n1, wqkv_t, cs, sn, q,
+                     k, v);
   RTE_TRY(check_launch("replay_qkv_fwd"));
   RTE_TRY(attention_fwd(q, k, v, B, h_max, S, kHd, 0.125f, nullptr, y, lse, s));
-  hipLaunchKernelGGL(rp_oproj_fwd_kernel, dim3(d / kCols, rt), dim3(kThreads), kLds, s, M, info, y, wo_t, ht, s_attn, attn,
-                     u, y_full);
+  hipLaunchKernelGGL(rp_oproj_fwd_kernel, dim3(d / kCols, rt), dim3(kThreads), kLds, s, M, info, y, wo_t, attn,
+                     y_full);
   RTE_TRY(check_launch("replay_oproj_fwd"));
-  hipLaunchKernelGGL(rp_upgate_fwd_kernel, dim3(nb_max, rt), dim3(kThreads), kLds, s, M, info, u, w2, g2, b2, eps2, wug_t,
-                     route_w, n2, rstd2, ug, z);
+  // u = h~ + s_attn attn and its FiLM norm
+  RTE_TRY(axpy_norm_fwd(ht, attn, s_attn, nullptr, nullptr, S, Mrows, d, w2, g2, b2, eps2, u, n2, rstd2, s));
+  hipLaunchKernelGGL(rp_upgate_fwd_kernel, dim3(nb_max, rt), dim3(kThreads), kLds, s, M, info, n2, wug_t, route_w, ug,
+                     z);
   RTE_TRY(check_launch("replay_upgate_fwd"));
-  hipLaunchKernelGGL(rp_down_fwd_kernel, dim3(d / kCols, rt), dim3(kThreads), kLds, s, M, info, z, wd_t, u, h, s_mlp, mlp,
-                     h_out, z_full);
+  hipLaunchKernelGGL(rp_down_fwd_kernel, dim3(d / kCols, rt), dim3(kThreads), kLds, s, M, info, z, wd_t, u, h, s_mlp,
+                     mlp, h_out, z_full);
   return check_launch("replay_down_fwd");
 }
 
+int replay_bwd_prep(int B, int S, int d, const float* dh, const float* mlp, const float* s_mlp, bf16* a_mlp,
+                    float* p_sm, hipStream_t s) {
+  RTE_REQUIRE(B >= 1 && S >= 1 && d % 128 == 0 && d <= kMaxD && dh && mlp && s_mlp && a_mlp && p_sm,
+              "replay_bwd_prep: bad arguments");
+  Meta M{B, S, d, 0, 0, 0, 0, 0, 0, 0};
+  hipLaunchKernelGGL(rp_dh_prep_kernel, dim3(replay_row_tiles(B, S)), dim3(256), 0, s, M, dh, mlp, s_mlp, a_mlp, p_sm);
+  return check_launch("replay_bwd_prep");
+}
+
 int replay_bwd_pass(int B, int S, int d, int H, int F, int NB, int h_max, int nb_max, const int32_t* info,
-                    const float* dh, const float* mlp, const float* s_mlp, const bf16* wd, const bf16* ug,
-                    float route_w, bf16* dug, bf16* d_mlp, float* p_sm, const bf16* wug, float* dn2, bf16* dug_full,
-                    const float* u, const float* rstd2, const float* w2, const float* g2, const float* attn,
-                    const float* s_attn, const bf16* wo, float* du, bf16* d_attn, bf16* dy, float* p_film2,
-                    float* p_sa, const bf16* q, const bf16* k, const bf16* v, const bf16* y, const float* lse,
-                    const float* cs, const float* sn, bf16* dqkv, const bf16* wqkv, float* dn1, bf16* dqkv_full,
-                    const float* ht, const float* rstd1, const float* w1, const float* g1, const float* h0,
-                    const float* alpha, int accumulate, float* dh_in, float* dh0, float* p_film1, float* p_alpha,
-                    hipStream_t s) {
+                    const float* dh, const bf16* a_mlp, const bf16* wd, const bf16* ug, float route_w, bf16* dug,
+                    const bf16* wug, float* dn2, bf16* dug_full, const float* u, const float* rstd2,
+                    const float* w2, const float* g2, const float* attn, const float* s_attn, float* du,
+                    bf16* d_attn, float* p_film2, float* p_sa, const bf16* wo, bf16* dy, const bf16* q, const bf16* k,
+                    const bf16* v, const bf16* y, const float* lse, const float* cs, const float* sn, bf16* dqkv,
+                    const bf16* wqkv, float* dn1, bf16* dqkv_full, const float* ht, const float* rstd1,
+                    const float* w1, const float* g1, const float* h0, const float* alpha, int accumulate,
+                    float* dh_in, float* dh0, float* p_film1, float* p_alpha, const float* mlp_next,
+                    const float* s_mlp_next, bf16* a_next, float* p_sm_next, hipStream_t s) {
   Meta M;
   RTE_TRY(make_meta(B, S, d, H, F, NB, h_max, nb_max, &M));
-  RTE_REQUIRE(info && dh && mlp && s_mlp && wd && ug && dug && d_mlp && p_sm && wug && dn2 && dug_full && u &&
-                  rstd2 && w2 && attn && s_attn && wo && du && d_attn && dy && p_film2 && p_sa && q && k && v && y &&
-                  lse && cs && sn && dqkv && wqkv && dn1 && dqkv_full && ht && rstd1 && w1 && dh_in && p_film1 &&
-                  p_alpha,
+  RTE_REQUIRE(info && dh && a_mlp && wd && ug && dug && wug && dn2 && dug_full && u && rstd2 && w2 && attn && s_attn &&
+                  du && d_attn && p_film2 && p_sa && wo && dy && q && k && v && y && lse && cs && sn && dqkv &&
+                  wqkv && dn1 && dqkv_full && ht && rstd1 && w1 && dh_in && p_film1 && p_alpha,
               "replay_bwd: missing buffer");
   RTE_REQUIRE(!alpha || (h0 && dh0), "replay_bwd: the input skip needs h0 and dh0");
-  const unsigned rt = (unsigned)(B * M.rts);
-  hipLaunchKernelGGL(rp_down_bwd_kernel, dim3((nb_max + 1) / 2, rt), dim3(kThreads), kLds, s, M, info, dh, mlp, s_mlp, wd,
-                     ug, route_w, dug, d_mlp, p_sm);
+  RTE_REQUIRE(!a_next || (mlp_next && s_mlp_next && p_sm_next), "replay_bwd: the next pass's operand needs mlp");
+  const unsigned rt = (unsigned)(B * M.rts), nrow = (unsigned)replay_row_tiles(B, S);
+  hipLaunchKernelGGL(rp_down_bwd_kernel, dim3((nb_max + 1) / 2, rt), dim3(kThreads), kLds, s, M, info, a_mlp, wd, ug,
+                     route_w, dug);
   RTE_TRY(check_launch("replay_down_bwd"));
-  hipLaunchKernelGGL(rp_upgate_bwd_kernel, dim3(d / kCols, rt), dim3(kThreads), kLds, s, M, info, dug, wug, dn2, dug_full);
+  hipLaunchKernelGGL(rp_upgate_bwd_kernel, dim3(d / kCols, rt), dim3(kThreads), kLds, s, M, info, dug, wug, dn2,
+                     dug_full);
   RTE_TRY(check_launch("replay_upgate_bwd"));
-  hipLaunchKernelGGL(rp_oproj_bwd_kernel, dim3(d / kCols, rt), dim3(kThreads), kLds, s, M, info, dh, dn2, u, rstd2, w2, g2,
-                     s_attn, wo, du, d_attn, dy);
-  RTE_TRY(check_launch("replay_oproj_bwd"));
+  hipLaunchKernelGGL(rp_norm2_bwd_kernel, dim3(nrow), dim3(256), 0, s, M, info, dh, dn2, u, rstd2, w2, g2, attn, s_attn,
+                     du, d_attn, p_film2, p_sa);
+  RTE_TRY(check_launch("replay_norm2_bwd"));
+  hipLaunchKernelGGL(rp_dy_kernel, dim3(h_max, rt), dim3(kThreads), kLds, s, M, info, d_attn, wo, dy);
+  RTE_TRY(check_launch("replay_dy"));
   RTE_TRY(attention_bwd_qkv(q, k, v, y, dy, lse, B, h_max, S, kHd, 0.125f, nullptr, cs, sn, dqkv, s));
-  hipLaunchKernelGGL(rp_qkv_bwd_kernel, dim3(d / kCols, rt), dim3(kThreads), kLds, s, M, info, dqkv, wqkv, dn1, dqkv_full);
+  hipLaunchKernelGGL(rp_qkv_bwd_kernel, dim3(d / kCols, rt), dim3(kThreads), kLds, s, M, info, dqkv, wqkv, dn1,
+                     dqkv_full);
   RTE_TRY(check_launch("replay_qkv_bwd"));
-  hipLaunchKernelGGL(rp_norm_bwd_kernel, dim3(d / kCols, rt), dim3(kThreads), kLds, s, M, info, dn1, du, dh, ht, rstd1, w1,
-                     g1, h0, alpha, dn2, u, rstd2, w2, g2, attn, accumulate, dh_in, dh0, p_film1, p_film2, p_sa,
-                     p_alpha);
-  return check_launch("replay_norm_bwd");
+  hipLaunchKernelGGL(rp_norm1_bwd_kernel, dim3(nrow), dim3(256), 0, s, M, info, dn1, du, dh, ht, rstd1, w1, g1, h0,
+                     alpha, accumulate, dh_in, dh0, p_film1, p_alpha, mlp_next, s_mlp_next, a_next, p_sm_next);
+  return check_launch("replay_norm1_bwd");
 }
 
 int replay_param_reduce(int T, int B, int S, int d, const float* p1, const float* p2, const float* psa,
                         const float* psm, const float* pal, float* out, hipStream_t s) {
   RTE_REQUIRE(T >= 1 && B >= 1 && S >= 1 && d % 128 == 0 && d <= kMaxD, "replay_param_reduce: bad shape");
-  const int nt = B * ((S + kRows - 1) / kRows), nct = d / kCols;
+  const int nt = replay_row_tiles(B, S);
   const int64_t n = (int64_t)T * 6 * d + 2 * d + 2 * T + 1;
-  hipLaunchKernelGGL(rp_param_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, T, nt, nct, d, p1,
-                     p2, psa, psm, pal, out);
+  hipLaunchKernelGGL(rp_param_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, T, nt, d, p1, p2,
+                     psa, psm, pal, out);
   return check_launch("replay_param_reduce");
 }
 
@@ -1300,6 +1137,8 @@ int replay_param_reduce(int T, int B, int S, int d, const float* p1, const float
 using namespace rte;
 
 extern "C" {
+
+int rte_replay_row_tiles(int B, int S) { return replay_row_tiles(B, S); }
 
 int rte_replay_fwd_pass(int B, int S, int d, int H, int F, int n_blk, int h_max, int nb_max, const int32_t* info,
                         const float* h, const float* h0, const float* alpha, const float* w1, const float* g1,
@@ -1317,23 +1156,28 @@ int rte_replay_fwd_pass(int B, int S, int d, int H, int F, int n_blk, int h_max,
                          b16(z), mlp, h_out, b16(z_full), static_cast<hipStream_t>(stream));
 }
 
+int rte_replay_bwd_prep(int B, int S, int d, const float* dh, const float* mlp, const float* s_mlp, void* a_mlp,
+                        float* p_sm, void* stream) {
+  return replay_bwd_prep(B, S, d, dh, mlp, s_mlp, static_cast<bf16*>(a_mlp), p_sm, static_cast<hipStream_t>(stream));
+}
+
 int rte_replay_bwd_pass(int B, int S, int d, int H, int F, int n_blk, int h_max, int nb_max, const int32_t* info,
-                        const float* dh, const float* mlp, const float* s_mlp, const void* wd, const void* ug,
-                        float route_w, void* dug, void* d_mlp, float* p_sm, const void* wug, float* dn2,
-                        void* dug_full, const float* u, const float* rstd2, const float* w2, const float* g2,
-                        const float* attn, const float* s_attn, const void* wo, float* du, void* d_attn, void* dy,
-                        float* p_film2, float* p_sa, const void* q, const void* k, const void* v, const void* y,
-                        const float* lse, const float* cos_t, const float* sin_t, void* dqkv, const void* wqkv,
-                        float* dn1, void* dqkv_full, const float* ht, const float* rstd1, const float* w1,
-                        const float* g1, const float* h0, const float* alpha, int accumulate, float* dh_in,
-                        float* dh0, float* p_film1, float* p_alpha, void* stream) {
+                        const float* dh, const void* a_mlp, const void* wd, const void* ug, float route_w, void* dug,
+                        const void* wug, float* dn2, void* dug_full, const float* u, const float* rstd2,
+                        const float* w2, const float* g2, const float* attn, const float* s_attn, float* du,
+                        void* d_attn, float* p_film2, float* p_sa, const void* wo, void* dy, const void* q,
+                        const void* k, const void* v, const void* y, const float* lse, const float* cos_t,
+                        const float* sin_t, void* dqkv, const void* wqkv, float* dn1, void* dqkv_full,
+                        const float* ht, const float* rstd1, const float* w1, const float* g1, const float* h0,
+                        const float* alpha, int accumulate, float* dh_in, float* dh0, float* p_film1, float* p_alpha,
+                        const float* mlp_next, const float* s_mlp_next, void* a_next, float* p_sm_next, void* stream) {
   auto cb = [](const void* p) { return static_cast<const bf16*>(p); };
   auto b16 = [](void* p) { return static_cast<bf16*>(p); };
-  return replay_bwd_pass(B, S, d, H, F, n_blk, h_max, nb_max, info, dh, mlp, s_mlp, cb(wd), cb(ug), route_w, b16(dug),
-                         b16(d_mlp), p_sm, cb(wug), dn2, b16(dug_full), u, rstd2, w2, g2, attn, s_attn, cb(wo), du,
-                         b16(d_attn), b16(dy), p_film2, p_sa, cb(q), cb(k), cb(v), cb(y), lse, cos_t, sin_t,
-                         b16(dqkv), cb(wqkv), dn1, b16(dqkv_full), ht, rstd1, w1, g1, h0, alpha, accumulate, dh_in,
-                         dh0, p_film1, p_alpha, static_cast<hipStream_t>(stream));
+  return replay_bwd_pass(B, S, d, H, F, n_blk, h_max, nb_max, info, dh, cb(a_mlp), cb(wd), cb(ug), route_w, b16(dug),
+                         cb(wug), dn2, b16(dug_full), u, rstd2, w2, g2, attn, s_attn, du, b16(d_attn), p_film2, p_sa,
+                         cb(wo), b16(dy), cb(q), cb(k), cb(v), cb(y), lse, cos_t, sin_t, b16(dqkv), cb(wqkv), dn1,
+                         b16(dqkv_full), ht, rstd1, w1, g1, h0, alpha, accumulate, dh_in, dh0, p_film1, p_alpha,
+                         mlp_next, s_mlp_next, b16(a_next), p_sm_next, static_cast<hipStream_t>(stream));
 }
 
 int rte_replay_param_reduce(int T, int B, int S, int d, const float* p_film1, const float* p_film2,

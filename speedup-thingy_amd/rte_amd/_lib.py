@@ -122,7 +122,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_mse_workspace_bytes": (_SZ, [_I64]),
     "rte_mse_fwd": (_I, [_P, _P, _I64, _P, _P, _SZ, _P]),
     "rte_replay_fwd_pass": (_I, [_I] * 8 + [_P] * 7 + [_F] + [_P] * 3 + [_F] + [_P] * 2 + [_F] + [_P] * 25),
-    "rte_replay_bwd_pass": (_I, [_I] * 8 + [_P] * 6 + [_F] + [_P] * 35 + [_I] + [_P] * 5),
+    "rte_replay_row_tiles": (_I, [_I, _I]),
+    "rte_replay_bwd_prep": (_I, [_I] * 3 + [_P] * 6),
+    "rte_replay_bwd_pass": (_I, [_I] * 8 + [_P] * 5 + [_F] + [_P] * 33 + [_I] + [_P] * 9),
     "rte_replay_param_reduce": (_I, [_I] * 4 + [_P] * 7),
     "rte_gemm_f32": (_I, [_P, _I64, _I, _P, _P, _P, _I64, _I, _P, _P, _P, _I64, _P, _I, _I, _I, _F, _F, _I, _I,
                           _I64, _I64, _I64, _I64, _I64, _I64, _P]),

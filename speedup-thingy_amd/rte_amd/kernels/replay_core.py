@@ -3,12 +3,14 @@ one autograd node on the HIP replay kernels (csrc/replay.hip).
 
 Reference: BankedRecursiveCore.forward_step (rte/layers.py:806-870) applied pass by pass by
 forward_exact (rte/models.py:416-512) to the audited rows (rte/audit.py:245-387).  Per pass the
-forward is five launches (norm1 + QKV + RoPE over the recipe's heads, attention, O-projection +
-residual, norm2 + up / gate + SwiGLU over the recipe's slabs, down-projection + residual) and the
-backward six; the four weight gradients are one GEMM each over every pass's rows, and the FiLM /
-scale / skip gradients one fixed-order reduction.  Values match the unfused pass (the same bf16
-operands, fp32 accumulation) up to summation order: the down-projection sums all of a token's
-slabs in one fp32 accumulator instead of adding per-cluster bf16 rows.
+forward is seven launches (residual + norm1 rows, QKV + RoPE over the recipe's heads, attention,
+O-projection, residual + norm2 rows, up / gate + SwiGLU over the recipe's slabs, down-projection +
+residual) and the backward seven (down + SwiGLU backward, up / gate backward, norm2 backward rows,
+O-projection backward, attention backward, QKV backward, norm1 backward rows, which also form the
+previous pass's down operand); the four weight gradients are one GEMM each over every pass's rows,
+and the FiLM / scale / skip gradients one fixed-order reduction.  Values match the unfused pass
+(the same bf16 operands, fp32 accumulation) up to summation order: the down-projection sums all
+of a token's slabs in one fp32 accumulator instead of adding per-cluster bf16 rows.
 """
 
 from __future__ import annotations
@@ -137,7 +139,7 @@ class ReplayCoreFn(torch.autograd.Function):
         wqkv, wo, wug, wd = ctx.weights
         dev = hv.device
         M, Hm, NBm = B * S, tabs.h_max, tabs.nb_max
-        nt, nct = B * ((S + 63) // 64), d // 64
+        nt = _lib.load().rte_replay_row_tiles(B, S)
 
         def e(*shape, dt=F32):
             return torch.empty(shape, dtype=dt, device=dev)
@@ -148,27 +150,34 @@ class ReplayCoreFn(torch.autograd.Function):
         wug_p, wd_p = cast_bf16(wug[0]), cast_bf16(wd[0])
         dug, dn2, du, dn1 = e(M, NBm * 2 * BLOCK, dt=BF16), e(M, d), e(M, d), e(M, d)
         dy, dqkv = e(M, Hm * HEAD_DIM, dt=BF16), e(M, 3 * Hm * HEAD_DIM, dt=BF16)
-        d_mlp, d_attn = e(T, M, d, dt=BF16), e(T, M, d, dt=BF16)
+        a_mlp, d_attn = e(T, M, d, dt=BF16), e(T, M, d, dt=BF16)
         dug_full, dqkv_full = e(T, M, 2 * F, dt=BF16), e(T, M, 3 * d, dt=BF16)
         p_film1, p_film2 = e(T, nt, 3 * d), e(T, nt, 3 * d)
-        p_sa, p_alpha, p_sm = e(T, nt, nct), e(T, nt, nct), e(T, nt)
+        p_sa, p_alpha, p_sm = e(T, nt), e(T, nt), e(T, nt)
         bufs = [e(B, S, d), e(B, S, d)]
         dh0 = e(M, d) if has_alpha else None
         st = _s()
+        fresh = True  # dh changed since the last norm1 backward formed the down operand
         for i, t in enumerate(reversed(range(T))):
             if t in extra:
-                dh = dh + extra[t].to(F32)
+                dh, fresh = dh + extra[t].to(F32), True
             dh = dh.contiguous()
+            if fresh:
+                call("rte_replay_bwd_prep", B, S, d, ptr(dh), ptr(mlp[t]), ptr(smc[t]), ptr(a_mlp[t]), ptr(p_sm[t]),
+                     st)
+            # the pass before this one gets its down operand from this call unless a state gradient lands first
+            nxt = t > 0 and (t - 1) not in extra
             dh_in = bufs[i % 2]
             call("rte_replay_bwd_pass", B, S, d, H, F, tabs.NB, tabs.h_max, tabs.nb_max, ptr(info[t]), ptr(dh),
-                 ptr(mlp[t]), ptr(smc[t]), ptr(wd_p), ptr(ug[t]),
-                 route_w, ptr(dug), ptr(d_mlp[t]), ptr(p_sm[t]), ptr(wug_p), ptr(dn2), ptr(dug_full[t]), ptr(u[t]),
-                 ptr(rstd2[t]), ptr(w2c), ptr(g2c[t]), ptr(attn[t]), ptr(sac[t]), ptr(wo_p), ptr(du), ptr(d_attn[t]),
-                 ptr(dy), ptr(p_film2[t]), ptr(p_sa[t]), ptr(q[t]), ptr(k[t]), ptr(v[t]), ptr(y[t]), ptr(lse[t]),
-                 ptr(cs), ptr(sn), ptr(dqkv), ptr(wqkv_p), ptr(dn1), ptr(dqkv_full[t]), ptr(ht[t]), ptr(rstd1[t]),
-                 ptr(w1c), ptr(g1c[t]), ptr(hv) if has_alpha else None, ptr(al), int(i > 0), ptr(dh_in), ptr(dh0),
-                 ptr(p_film1[t]), ptr(p_alpha[t]), st)
-            dh = dh_in
+                 ptr(a_mlp[t]), ptr(wd_p), ptr(ug[t]), route_w, ptr(dug), ptr(wug_p), ptr(dn2), ptr(dug_full[t]),
+                 ptr(u[t]), ptr(rstd2[t]), ptr(w2c), ptr(g2c[t]), ptr(attn[t]), ptr(sac[t]), ptr(du),
+                 ptr(d_attn[t]), ptr(p_film2[t]), ptr(p_sa[t]), ptr(wo_p), ptr(dy), ptr(q[t]), ptr(k[t]), ptr(v[t]),
+                 ptr(y[t]), ptr(lse[t]), ptr(cs), ptr(sn), ptr(dqkv), ptr(wqkv_p), ptr(dn1), ptr(dqkv_full[t]),
+                 ptr(ht[t]), ptr(rstd1[t]), ptr(w1c), ptr(g1c[t]), ptr(hv) if has_alpha else None, ptr(al),
+                 int(i > 0), ptr(dh_in), ptr(dh0), ptr(p_film1[t]), ptr(p_alpha[t]),
+                 ptr(mlp[t - 1]) if nxt else None, ptr(smc[t - 1]) if nxt else None,
+                 ptr(a_mlp[t - 1]) if nxt else None, ptr(p_sm[t - 1]) if nxt else None, st)
+            dh, fresh = dh_in, not nxt
         red = e(T * 6 * d + 2 * d + 2 * T + 1)
         call("rte_replay_param_reduce", T, B, S, d, ptr(p_film1), ptr(p_film2), ptr(p_sa), ptr(p_sm), ptr(p_alpha),
              ptr(red), st)
@@ -189,7 +198,7 @@ class ReplayCoreFn(torch.autograd.Function):
                 tail[2 * d + 2 * T].reshape(()) if (has_alpha and nia[7]) else None,
                 tail[:d] if nia[8] else None, tail[d:2 * d] if nia[9] else None,
                 wgrad(10, n1, dqkv_full, (1, d, 3 * d)), wgrad(11, y_full, d_attn, (1, d, d)),
-                wgrad(12, n2, dug_full, (1, d, 2 * F)), wgrad(13, z_full, d_mlp, (1, F, d)),
+                wgrad(12, n2, dug_full, (1, d, 2 * F)), wgrad(13, z_full, a_mlp, (1, F, d)),
                 None, None, None, None, None, None, None, None, None)
 
 
