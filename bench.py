@@ -226,16 +226,21 @@ def kernel_candidates(B: int, S: int):
         loss = hip_ops.macro_consistency(mh, kf, ks, mv, mu, mg, mb, ms, 0.1, src_lo=0, dst_lo=1)
         torch.autograd.grad(loss, [mh, mv, mu, mg, mb])
 
-    # bytes of the macro consistency: forward reads h (2 reads), writes x2 (bf16 2d per source
-    # row, 1 + pc sources) and both outputs, reads the first output and the MSE reference; the
-    # backward reads h / first twice, the MSE operands twice per application, writes du (bf16)
-    # and dh / dh0 / d_first, the weight reductions read x2, du and da once per (sample, row)
-    rows_src, rows_both, rows_tw = T, 3 * T, 2 * T
+    # bytes of the consistency loss on the one-pass kernels (csrc/macro_cons.hip), nf = 3 first-
+    # application key blocks and pc = 2 pairs over T rows: h read by each of the 6 kernels; x2
+    # ([rmsnorm | h] bf16, 4d bytes per row) written for the 1 + pc inputs and read once by the
+    # weight reductions; du (bf16) written per (key, row) and read once; dh written, read and
+    # rewritten; the rank-32 codes a (fp32) / silu(a) / da (bf16) written and read; the fp32
+    # weights read by the two bf16 weight preparations and their gradients written.
+    rows_both, rows_tw = 3 * T, 2 * T
     f4, b2 = 4.0 * d, 2.0 * d
-    macro_bytes = (rows_src * (2 * f4 + 2 * b2) + rows_both * f4
-                   + rows_tw * (f4 + 2 * b2 + f4 + f4)
-                   + rows_tw * (2 * f4 + 4 * f4 + b2 + 2 * f4) + rows_both * (2 * f4 + b2) + rows_src * f4
-                   + (rows_both + rows_tw) * (2 * b2 + b2))
+    nf, pc, G3 = 3, 2, R3 * K3
+    wbytes = G3 * (3 * d * r + r * d) * 4.0
+    macro_bytes = (6 * T * f4 + 2 * (1 + pc) * T * 2 * b2 + 2 * (nf + pc) * T * b2 + 3 * T * f4
+                   + 2 * (nf + pc) * T * r * (4 + 2 + 2) + 3 * wbytes)
+    # the operation's essential I/O: h in, dh out, the tables (V, U, gain, bias, scale) in and
+    # their gradients out
+    macro_essential = 2 * T * f4 + 2 * (wbytes + 3 * G3 * d * 4.0)
     macro_flop = (rows_both + rows_tw) * 2.0 * (2 * d * r + r * d) * 3
 
     return [
@@ -273,7 +278,7 @@ def kernel_candidates(B: int, S: int):
         dict(name="pack_index", per_step=0, kernels=3, flop=0.0, bytes=8.0 * P + 20.0 * P + 4.0 * (C + 1),
              fn=pack),
         dict(name="macro_consistency_fwd_bwd", per_step=1, kernels=None, flop=macro_flop, bytes=macro_bytes,
-             fn=macro_cons),
+             essential_bytes=macro_essential, fn=macro_cons),
     ]
 
 
@@ -369,6 +374,9 @@ def roofline_rows(B: int, S: int) -> list[dict]:
                      "unit": "TFLOP/s" if bound == "mfma" else "GB/s", "peak": peak, "frac": round(ach / peak, 4),
                      "flop": c["flop"], "bytes": c["bytes"],
                      "tflops": round(c["flop"] / dt / 1e12, 1), "gbs": round(c["bytes"] / dt / 1e9, 1)})
+        if c.get("essential_bytes"):
+            rows[-1]["essential_bytes"] = c["essential_bytes"]
+            rows[-1]["essential_frac"] = round(c["essential_bytes"] / dt / 1e9 / PEAK_HBM_GBS, 4)
     rows.sort(key=lambda r: -r["us_per_step"])
     return rows
 
@@ -766,6 +774,9 @@ def main(argv=None) -> int:
             "flop_per_launch": dom["flop"],
             "algorithmic_bytes_per_launch": dom["bytes"],
         }
+        if "essential_bytes" in dom:
+            out["roofline"]["essential_bytes_per_launch"] = dom["essential_bytes"]
+            out["roofline"]["essential_frac"] = dom["essential_frac"]
         out["kernels"] = rows
         out["svd_ffn_cfg4"] = svd_cfg4_row()
     if not args.no_cpu_baseline:

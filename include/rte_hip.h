@@ -445,6 +445,36 @@ int rte_macro_fused_wgrad(const int64_t* key, int B0, int B_h0, int B1, int B_h1
                           const void* da_sum, const float* part_tab, float* du_w, float* dv_w, float* dgain,
                           float* dbias, float* dscale, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Macro consistency loss in one pass per application for seq <= 64 and d = 256 or 512
+ * (rte/macro.py:342-359 with the operator of rte/macro.py:201-236 at hidden rank 32, h0 = h):
+ * loss = mean over j < pc, samples, rows, columns of (Phi_{j}(out_{src_lo + j}) -
+ * out_{dst_lo + j})^2, out_k = Phi_k(h) for the nf first-application key blocks (key_first
+ * [nf * b], block k of sample i at k * b + i), key_src [pc * b] the second application's keys.
+ * One workgroup per 32 rows of a sample; out and the second application's output are never
+ * stored (recomputed from h and the rank-32 codes).  Buffers, in the layouts of
+ * rte_macro_fused_wgrad with call 0 = the nf * b first-application samples over B_h0 = b source
+ * blocks and call 1 = the pc * b second-application samples over their own pc * b blocks:
+ * x2 bf16 [(b + pc b) seq, 2d], pooled bf16 [b + pc b, d], a f32 / sa bf16 [(nf b + pc b) seq, 32],
+ * rstd f32 [(b + pc b) seq] (h, then the second application's inputs), loss f32 [1];
+ * backward: du bf16 [(nf b + pc b) seq, d], da bf16 [., 32], part_tab f32 [nf b + pc b, tiles, 3, d],
+ * part_da f32 [., tiles, 32], da_sum bf16 [nf b + pc b, 32], dh f32 [b, seq, d] (the whole
+ * gradient of h), tiles = ceil(seq / 32); g f32 [1] the loss gradient, mul = 2 / (pc b seq d).
+ * prep: vq_t bf16 [n_keys, 32, 2d] (V1 | V3 transposed) and u_q bf16 [n_keys, 32, d] with the
+ * middle two 4-column quads of every 16 columns swapped (the kernels' operand order).
+ * Requires 1 <= pc <= nf <= 4 and the src / dst blocks inside the first application. */
+size_t rte_macro_cons_workspace_bytes(int b, int seq, int d, int pc);
+int rte_macro_cons_prep(const float* v, const float* u, int n_keys, int d, void* vq_t, void* u_q, void* stream);
+int rte_macro_cons_fwd(const float* h, int b, int seq, int d, const int64_t* key_first, int nf, const int64_t* key_src,
+                       int pc, int src_lo, int dst_lo, int n_keys, float eps, const void* v_b, const void* vq_t,
+                       const void* u_t, const void* u_q, const float* gain, const float* bias, const float* scale,
+                       float c, void* x2, void* pooled, float* a, void* sa, float* rstd, float* loss,
+                       void* workspace, size_t workspace_bytes, void* stream);
+int rte_macro_cons_bwd(const float* h, int b, int seq, int d, const int64_t* key_first, int nf, const int64_t* key_src,
+                       int pc, int src_lo, int dst_lo, int n_keys, const void* v_b, const void* u_t, const void* u_q,
+                       const float* gain, const float* bias, const float* scale, float c, const float* a,
+                       const void* sa, const float* rstd, const float* g, float mul, void* du, void* da,
+                       float* part_tab, float* part_da, void* da_sum, float* dh, void* stream);
+
 /* ---- mean squared difference (F.mse_loss of the macro consistency loss, rte/macro.py:342-359) ----
  * fwd: out f32 [1] = mean((a - b)^2) over n f32 elements (fixed-order block sums, then one
  * workgroup adds them in order); workspace rte_mse_workspace_bytes(n).

@@ -102,6 +102,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_macro_fused_fwd": (_I, [_P, _P, _I, _I, _P, _I, _I, _I, _I, _F, _P, _P, _P, _P, _P, _P, _F, _P, _P, _P,
                                  _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "rte_macro_fused_sum": (_I, [_P, _I, _F, _P, _P]),
+    "rte_macro_cons_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "rte_macro_cons_prep": (_I, [_P, _P, _I, _I, _P, _P, _P]),
+    "rte_macro_cons_fwd": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _I, _I, _I, _F] + [_P] * 7 + [_F] + [_P] * 7
+                           + [_SZ, _P]),
+    "rte_macro_cons_bwd": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _I, _I, _I] + [_P] * 6 + [_F] + [_P] * 4 + [_F]
+                           + [_P] * 7),
     "rte_macro_fused_bwd": (_I, [_P, _P, _P, _F, _I, _I, _P, _I, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _P, _P, _P, _P, _P,
                                  _P, _P, _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _P, _I, _P, _P, _SZ, _P]),
     "rte_macro_fused_wgrad": (_I, [_P, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,

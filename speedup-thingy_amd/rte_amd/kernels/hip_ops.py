@@ -2213,6 +2213,117 @@ class MacroConsistencyFn(torch.autograd.Function):
         return (dh.to(h_dt) if nia[0] else None, None, None, None, None, *grads, None, None)
 
 
+MACRO_CONS_MAX_KEYS = 4
+# the one-pass consistency kernels (csrc/macro_cons.hip) where their shapes allow; off: the
+# per-application fused operator calls of MacroConsistencyFn
+MACRO_CONS_ONE_PASS = [True]
+
+
+def macro_cons_supported(v: torch.Tensor, u: torch.Tensor, S: int, nf: int, pc: int) -> bool:
+    """Shapes the one-pass consistency kernels take: hidden rank 32, d = 256 or 512, at most 64
+    positions, 1 <= pc <= nf <= 4 key blocks."""
+    if fp32_active():
+        return False
+    d = u.shape[-1]
+    return (v.shape[-1] == MACRO_FUSED_RANK and u.shape[-2] == MACRO_FUSED_RANK and v.shape[-2] == 3 * d
+            and d in (256, 512) and 1 <= S <= 64 and 1 <= pc <= nf <= MACRO_CONS_MAX_KEYS)
+
+
+def macro_cons_weights(v: torch.Tensor, u: torch.Tensor):
+    """bf16 [V1 | V3]^T [G, 32, 2d] and U [G, 32, d] with the middle two 4-column quads of every
+    16 columns swapped (the operand order of the one-pass consistency kernels), once per step
+    and stream while a per-step cache is open."""
+    _lib.require_device_tensors("macro_cons_weights", v, u)
+    G = v.shape[0] * v.shape[1]
+    d = u.shape[-1]
+    key = None
+    if _BF16_CACHE_ON[0] and _whole_param(v) and _whole_param(u):
+        key = ("macro_cons", v.data_ptr(), v._version, u.data_ptr(), u._version, _lib.stream_ptr())
+        hit = _BF16_CACHE.get(key)
+        if hit is not None:
+            return hit
+    vf = v.detach().reshape(G, 3 * d, MACRO_FUSED_RANK).contiguous().to(F32)
+    uf = u.detach().reshape(G, MACRO_FUSED_RANK, d).contiguous().to(F32)
+    vq = torch.empty((G, MACRO_FUSED_RANK, 2 * d), dtype=BF16, device=v.device)
+    uq = torch.empty((G, MACRO_FUSED_RANK, d), dtype=BF16, device=v.device)
+    call("rte_macro_cons_prep", ptr(vf), ptr(uf), G, d, ptr(vq), ptr(uq), _s())
+    out = (vq, uq)
+    if key is not None:
+        _BF16_CACHE[key] = out
+    return out
+
+
+class MacroConsOnePassFn(torch.autograd.Function):
+    """The macro consistency loss (rte/macro.py:342-359) for at most 64 positions and d = 256 or
+    512 on the one-pass kernels: one workgroup per 32 rows of a sample runs the first
+    application's codes, the second application and the squared differences (three launches),
+    and the backward in three more; out and Phi(out) are recomputed from h and the rank-32
+    codes instead of being stored.  Key layout and weight gradients as MacroConsistencyFn (the
+    grouped reductions of the fused operator)."""
+
+    @staticmethod
+    def forward(ctx, h, key_first, key_src, src_lo, dst_lo, v, u, gain, bias, scale, c, eps):
+        _lib.require_device_tensors("macro_cons", h, key_first, key_src, v, u, gain, bias, scale)
+        b, S, d = h.shape
+        kf = key_first.reshape(-1).contiguous().to(torch.int64)
+        ks = key_src.reshape(-1).contiguous().to(torch.int64)
+        if kf.numel() % b or ks.numel() % b:
+            raise ValueError("macro_cons: need nf b first keys and pc b second keys")
+        nf, pc = kf.numel() // b, ks.numel() // b
+        if not macro_cons_supported(v, u, S, nf, pc):
+            raise ValueError("macro_cons: needs rank 32, d = 256 or 512, S <= 64, 1 <= pc <= nf <= 4")
+        if not (0 <= src_lo <= nf - pc and 0 <= dst_lo <= nf - pc):
+            raise ValueError("macro_cons: src / dst key blocks outside the first application")
+        G = v.shape[0] * v.shape[1]
+        dev = h.device
+        hv = h.detach().contiguous().to(F32)
+        vb, _, _, _, ut = macro_fused_weights(v, u)
+        vq, uq = macro_cons_weights(v, u)
+        tabs = _macro_tabs(gain, bias, scale, G, d)
+        R = MACRO_FUSED_RANK
+        x2 = torch.empty(((b + pc * b) * S, 2 * d), dtype=BF16, device=dev)
+        pooled = torch.empty((b + pc * b, d), dtype=BF16, device=dev)
+        a = torch.empty(((nf + pc) * b * S, R), dtype=F32, device=dev)
+        sa = torch.empty(((nf + pc) * b * S, R), dtype=BF16, device=dev)
+        rstd = torch.empty(((1 + pc) * b * S,), dtype=F32, device=dev)
+        loss = torch.empty((), dtype=F32, device=dev)
+        ws, nbytes = workspace(_lib.load().rte_macro_cons_workspace_bytes(b, S, d, pc), dev)
+        call("rte_macro_cons_fwd", ptr(hv), b, S, d, ptr(kf), nf, ptr(ks), pc, int(src_lo), int(dst_lo), G,
+             float(eps), ptr(vb), ptr(vq), ptr(ut), ptr(uq), ptr(tabs[0]), ptr(tabs[1]), ptr(tabs[2]), float(c),
+             ptr(x2), ptr(pooled), ptr(a), ptr(sa), ptr(rstd), ptr(loss), ws, nbytes, _s())
+        ctx.save_for_backward(hv)
+        ctx.bufs = (kf, ks, x2, pooled, a, sa, rstd, vb, ut, uq, tabs)
+        ctx.meta = (G, float(c), b, S, d, nf, pc, int(src_lo), int(dst_lo), v.shape, u.shape, gain.shape, h.dtype)
+        return loss
+
+    @staticmethod
+    def backward(ctx, g):
+        (hv,) = ctx.saved_tensors
+        kf, ks, x2, pooled, a, sa, rstd, vb, ut, uq, tabs = ctx.bufs
+        G, c, b, S, d, nf, pc, src_lo, dst_lo, v_shape, u_shape, t_shape, h_dt = ctx.meta
+        nia = ctx.needs_input_grad
+        dev = hv.device
+        R = MACRO_FUSED_RANK
+        T = (S + 31) // 32
+        nb = (nf + pc) * b
+        gv = g.reshape(1).contiguous().to(F32)
+        du = torch.empty((nb * S, d), dtype=BF16, device=dev)
+        da = torch.empty((nb * S, R), dtype=BF16, device=dev)
+        part_tab = torch.empty((nb * T * 3 * d,), dtype=F32, device=dev)
+        part_da = torch.empty((nb * T * R,), dtype=F32, device=dev)
+        dsum = torch.empty((nb, R), dtype=BF16, device=dev)
+        dh = torch.empty((b, S, d), dtype=F32, device=dev)
+        mul = 2.0 / (pc * b * S * d)
+        call("rte_macro_cons_bwd", ptr(hv), b, S, d, ptr(kf), nf, ptr(ks), pc, src_lo, dst_lo, G, ptr(vb), ptr(ut),
+             ptr(uq), ptr(tabs[0]), ptr(tabs[1]), ptr(tabs[2]), c, ptr(a), ptr(sa), ptr(rstd), ptr(gv), float(mul),
+             ptr(du), ptr(da), ptr(part_tab), ptr(part_da), ptr(dsum), ptr(dh), _s())
+        keys = torch.cat([kf, ks])
+        grads = _macro_wgrad(keys, nf * b, b, pc * b, pc * b, S, d, G, x2, sa, du, da, pooled, dsum, part_tab,
+                             nia[5:10], v_shape, u_shape, t_shape, dev)
+        ctx.bufs = None
+        return (dh.to(h_dt) if nia[0] else None, None, None, None, None, *grads, None, None)
+
+
 def macro_consistency(h, key_first, key_src, v, u, gain, bias, scale, c: float, eps: float = 1e-5, *,
                       src_lo: int | None = None, dst_lo: int = 0):
     """key_first: the first application's nf key blocks of len(h) samples; key_src: the pc src
@@ -2220,8 +2331,10 @@ def macro_consistency(h, key_first, key_src, v, u, gain, bias, scale, c: float, 
     the dst blocks from block dst_lo on."""
     b = h.shape[0]
     nf, pc = key_first.numel() // b, key_src.numel() // b
-    return MacroConsistencyFn.apply(h, key_first, key_src, nf - pc if src_lo is None else int(src_lo), int(dst_lo),
-                                    v, u, gain, bias, scale, c, eps)
+    lo = nf - pc if src_lo is None else int(src_lo)
+    if MACRO_CONS_ONE_PASS[0] and macro_cons_supported(v, u, h.shape[1], nf, pc):
+        return MacroConsOnePassFn.apply(h, key_first, key_src, lo, int(dst_lo), v, u, gain, bias, scale, c, eps)
+    return MacroConsistencyFn.apply(h, key_first, key_src, lo, int(dst_lo), v, u, gain, bias, scale, c, eps)
 
 
 class MseFn(torch.autograd.Function):

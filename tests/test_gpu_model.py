@@ -639,13 +639,19 @@ def test_macro_fused_operator_matches_reference(d, B, S, depths):
     assert rel_err(out.detach().double().cpu().numpy(), ref.detach().numpy()) < 1e-3
 
 
-@pytest.mark.parametrize("d,B,S,depths", [(256, 5, 80, [1, 2, 4, 8]), (512, 16, 64, [1, 2, 4]),
-                                          (256, 6, 40, [1, 2, 3, 6])])
-def test_macro_fused_consistency_matches_reference(d, B, S, depths):
+@pytest.mark.parametrize("d,B,S,depths,one_pass", [(256, 5, 80, [1, 2, 4, 8], False), (512, 16, 64, [1, 2, 4], False),
+                                                   (256, 6, 40, [1, 2, 3, 6], False), (512, 16, 64, [1, 2, 4], True),
+                                                   (256, 6, 40, [1, 2, 3, 6], True), (256, 5, 64, [1, 2, 4, 8], True),
+                                                   (512, 3, 24, [1, 2, 4], True)])
+def test_macro_fused_consistency_matches_reference(d, B, S, depths, one_pass):
     """The fused consistency loss (both operator applications, the MSE and the backward in the
     fused kernels) against fp64 autograd of rte/macro.py:342-359 restated with explicit copies:
     chained stride pairs sharing first-application key blocks (strides 1, 2, 4 (, 8): src and dst
-    blocks overlap), and unchained pairs in the [dst; src] layout (strides 1, 2, 3, 6)."""
+    blocks overlap), and unchained pairs in the [dst; src] layout (strides 1, 2, 3, 6).  one_pass:
+    the one-pass kernels (csrc/macro_cons.hip: a ragged second half at S = 40, one half at S = 24,
+    four first-application blocks with three pairs at strides 1, 2, 4, 8); otherwise the
+    per-application fused operator calls."""
+    from rte_amd.kernels import hip_ops
     from rte_amd.macro import MacroOperators
 
     cfg = _model_cfg(d_model=d, n_heads=d // 64, macro_rank=32, recipe_count=6, depth_choices=depths,
@@ -659,9 +665,16 @@ def test_macro_fused_consistency_matches_reference(d, B, S, depths):
     gen = torch.Generator(device="cuda").manual_seed(14)
     h = torch.randn(B, S, d, device="cuda", generator=gen, requires_grad=True)
     rid = torch.randint(0, 6, (B,), device="cuda", generator=gen)
-    print(f"fused consistency d={d} B={B} S={S} pairs={mac.cons_src_idx.numel()}", flush=True)
-    loss = mac.consistency_loss(h, h, rid)
-    loss.backward()
+    nf, pc = mac.cons_key_idx.numel(), mac.cons_src_idx.numel()
+    if one_pass:
+        assert hip_ops.macro_cons_supported(mac.v, mac.u, S, nf, pc)
+    print(f"fused consistency d={d} B={B} S={S} pairs={pc} one_pass={one_pass}", flush=True)
+    hip_ops.MACRO_CONS_ONE_PASS[0] = one_pass
+    try:
+        loss = mac.consistency_loss(h, h, rid)
+        loss.backward()
+    finally:
+        hip_ops.MACRO_CONS_ONE_PASS[0] = True
     names = ("d_gain", "bias", "v", "u")
     tp = {k: getattr(mac, k).detach().double().cpu().requires_grad_(k != "update_scale")
           for k in names + ("update_scale",)}
