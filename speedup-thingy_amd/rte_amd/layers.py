@@ -280,9 +280,13 @@ class SVDFactorSparseFFN(nn.Module):
     The low-rank factors of W_up and W_gate (refresh_svd) give approximate activations for every
     neuron; each token's candidates are the top up_m / gate_m / product_m neurons by |up|, |silu(gate)|
     and |up silu(gate)| times ||W_down row||, evaluated exactly, reranked to top_k and summed through
-    W_down.  candidate_mode "mask" and "slots" differ in the reference only in how the candidate
-    list is stored (a boolean mask or concatenated slots); both select the same set, which is what
-    the HIP kernel computes (a per-token bitmap), and both train.  "triton" is the inference-only
+    W_down.  candidate_mode "mask" and "slots" store the candidate list as a boolean mask or as
+    concatenated slots; the HIP kernel computes the set as a per-token bitmap for both.  A token
+    with fewer than top_k distinct candidates gets the top_k of its approximate product scores
+    added, as the reference's slots mode does (rte/layers.py:522-526).  The reference's mask mode
+    writes that fill into the copy that boolean indexing returns (rte/layers.py:491), so there it
+    has no effect and such a token ranks non-candidates scored -inf; this build fills in both modes
+    on purpose.  "triton" is the inference-only
     device driver (rte/kernels/svd_sparse_ffn_triton.py:480-714): the "product" strategy takes the
     top top_k of the approximate product scores, "union" reranks the union with exact or
     approximate activations."""
