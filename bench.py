@@ -152,8 +152,13 @@ def kernel_candidates(B: int, S: int):
     def head_wgrad():
         gemm(dlog, V, 1, x, d, 1, dw_head, d, V, d, T, ws_h, wsb_h)
 
+    # the entry points the step's pools call: the fused per-cluster kernels where the shape allows
+    fused = bool(lib.rte_grouped_swiglu_fused_ok(n, d))
+    ffn_fwd_name = "rte_grouped_swiglu_fused_fwd" if fused else "rte_grouped_swiglu_fwd"
+    ffn_bwd_name = "rte_grouped_swiglu_fused_bwd" if fused else "rte_grouped_swiglu_bwd"
+
     def ffn_fwd():
-        _lib.call("rte_grouped_swiglu_fwd", x.data_ptr(), T, d, pk.offsets.data_ptr(), C, n, P,
+        _lib.call(ffn_fwd_name, x.data_ptr(), T, d, pk.offsets.data_ptr(), C, n, P,
                   pk.tok_of_slot.data_ptr(), pk.pair_of_slot.data_ptr(), pk.w_of_slot.data_ptr(), wug.data_ptr(),
                   wd.data_ptr(), F, ug.data_ptr(), zw.data_ptr(), yp.data_ptr(), st())
 
@@ -168,7 +173,7 @@ def kernel_candidates(B: int, S: int):
     gs_ws = torch.empty(max(gsb, 16), device=dev, dtype=torch.uint8)
 
     def ffn_bwd():
-        _lib.call("rte_grouped_swiglu_bwd", dpool.data_ptr(), x.data_ptr(), T, d, pk.offsets.data_ptr(), C, n, P,
+        _lib.call(ffn_bwd_name, dpool.data_ptr(), x.data_ptr(), T, d, pk.offsets.data_ptr(), C, n, P,
                   pk.tok_of_slot.data_ptr(), pk.pair_of_slot.data_ptr(), pk.w_of_slot.data_ptr(), wug.data_ptr(),
                   wd.data_ptr(), F, ug.data_ptr(), zw.data_ptr(), dug.data_ptr(), dw_slot.data_ptr(),
                   dx_pairs.data_ptr(), dwug.data_ptr(), dwd.data_ptr(), 0, 0.0, gs_ws.data_ptr(), gsb, st())
@@ -254,8 +259,8 @@ def kernel_candidates(B: int, S: int):
              bytes=2.0 * T * V + 2.0 * T * d + 4.0 * V * d, fn=head_wgrad),
         dict(name="gemm_wgrad_qkv", per_step=2, kernels=2, flop=2.0 * T * 3 * d * d,
              bytes=2.0 * T * 3 * d + 2.0 * T * d + 4.0 * 3 * d * d, fn=wgrad_qkv),
-        # x@[Wup|Wgate]^T with the SwiGLU epilogue, then zw@Wdown into pair-major rows
-        dict(name="grouped_swiglu_fwd", per_step=2, kernels=2, flop=2.0 * P * d * 2 * n + 2.0 * P * n * d,
+        # x@[Wup|Wgate]^T, SwiGLU, zw@Wdown into pair-major rows (one fused launch at n = 32)
+        dict(name="grouped_swiglu_fwd", per_step=2, kernels=1 if fused else 2, flop=2.0 * P * d * 2 * n + 2.0 * P * n * d,
              bytes=2.0 * T * d + 2.0 * 3 * F * d + 2.0 * P * 3 * n + 2.0 * P * d + 12.0 * P, fn=ffn_fwd),
         # backward: dZ / dW_down, SwiGLU derivative, dX-pairs / dW_up|gate; reads x, dout, weights,
         # ug, zw, slot tables; writes dug, dw_slot, dx_pairs and the fp32 weight gradients

@@ -164,6 +164,25 @@ int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const 
  * still deterministic).  NULL / too small: one workgroup column per cluster. */
 size_t rte_grouped_swiglu_bwd_workspace_bytes(int P, int G, int n, int d);
 
+/* The same two operations as rte_grouped_swiglu_fwd / rte_grouped_swiglu_bwd (same arguments,
+ * same outputs) with the per-cluster products fused: one launch computes ug, zw and y_pairs, one
+ * launch computes dug, dw_slot and dx_pairs (the weight gradients are the same grouped-K
+ * reductions).  Each workgroup stages its cluster's weights in LDS and keeps the [128 x 2n]
+ * up/gate and [128 x n] z blocks of its 128 slots on chip (rte/kernels/cluster_pool_ffn.py:192-241).
+ * Shapes: n = 32 and d in {128, 256, 512} (rte_grouped_swiglu_fused_ok(n, d) returns 1); other
+ * shapes return -1.  ld_wd must be a multiple of 8. */
+int rte_grouped_swiglu_fused_ok(int n, int d);
+int rte_grouped_swiglu_fused_fwd(const void* x, int T, int d, const int32_t* offsets, int G, int n, int P,
+                                 const int32_t* tok_of_slot, const int32_t* pair_of_slot, const float* w_of_slot,
+                                 const void* wug, const void* wd, int64_t ld_wd,
+                                 void* ug, void* zw, void* y_pairs, void* stream);
+int rte_grouped_swiglu_fused_bwd(const void* dout, const void* x, int T, int d, const int32_t* offsets, int G,
+                                 int n, int P, const int32_t* tok_of_slot, const int32_t* pair_of_slot,
+                                 const float* w_of_slot, const void* wug, const void* wd, int64_t ld_wd,
+                                 const void* ug, const void* zw, void* dug, float* dw_slot, void* dx_pairs,
+                                 float* dwug, float* dwd, int w_t, float beta, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
 /* ---- dense SwiGLU (rte/layers.py:78-116 DenseSwiGLU / PackedDenseSwiGLU;
  *      rte/kernels/active_swiglu_triton.py:62-102 fused activation fwd/bwd) ----
  * wug bf16 [2F, d] rows [up ; gate].  wd_rows = 0: wd is [d, F] (nn.Linear(F, d).weight),

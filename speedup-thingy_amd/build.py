@@ -19,7 +19,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 OUT = HERE / "rte_amd" / "librte_hip.so"
 OBJ = HERE / "_build"
-SOURCES = ["gemm.hip", "route.hip", "norm.hip", "loss.hip", "shortlist.hip", "segreduce.hip", "glue.hip", "distill.hip", "macro.hip", "macro_fused.hip", "macro_cons.hip", "adamw.hip", "attention.hip", "noalloc.hip", "dispatch.hip", "svdsel.hip", "svd_fused.hip", "router.hip", "bookkeep.hip", "f32.hip", "replay.hip", "capi.hip"]
+SOURCES = ["gemm.hip", "route.hip", "norm.hip", "loss.hip", "shortlist.hip", "segreduce.hip", "glue.hip", "distill.hip", "macro.hip", "macro_fused.hip", "macro_cons.hip", "adamw.hip", "attention.hip", "noalloc.hip", "dispatch.hip", "svdsel.hip", "svd_fused.hip", "router.hip", "bookkeep.hip", "f32.hip", "replay.hip", "pool_fused.hip", "capi.hip"]
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",

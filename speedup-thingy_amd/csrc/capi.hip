@@ -131,6 +131,13 @@ int shortlist_bwd(const float* dloss, const float* dlext, const bf16* hidden, co
 size_t segreduce_workspace_bytes(int64_t P, int V, int d);
 int segreduce_rows(const int32_t* keys, int64_t P, int V, int row_div, const float* w, const void* rows, int rows_f32,
                    int d, float* out, int accumulate, void* ws, size_t ws_bytes, hipStream_t s);
+bool pool_fused_supported(int n, int d);
+int pool_fused_fwd(const bf16* x, int d, const int32_t* offsets, int G, int n, int P, const int32_t* tok_of_slot,
+                   const int32_t* pair_of_slot, const float* w_of_slot, const bf16* wug, const bf16* wd,
+                   int64_t ld_wd, bf16* ug, bf16* zw, bf16* y_pairs, hipStream_t s);
+int pool_fused_bwd(const bf16* dout, int d, const int32_t* offsets, int G, int n, int P, const int32_t* tok_of_slot,
+                   const int32_t* pair_of_slot, const float* w_of_slot, const bf16* wug, const bf16* wd,
+                   int64_t ld_wd, const bf16* ug, bf16* dug, float* dw_slot, bf16* dx_pairs, hipStream_t s);
 }  // namespace rte
 
 using namespace rte;
@@ -157,6 +164,99 @@ Operand from_layout(const void* p, const int64_t* L) {
   o.cdiv = (int32_t)L[3];
   o.cs_hi = L[4];
   return o;
+}
+
+// Weight gradients of the grouped SwiGLU (grouped-K reductions over each cluster's slots): dWug from
+// x[tok] and dUG, dWd from zw and dout[tok], in the parameters' layout (w_t = 0) or transposed.
+int pool_wgrad(const void* dout, const void* x, int d, const int32_t* offsets, int G, int n, int P,
+               const int32_t* tok_of_slot, int64_t ld_wd, const void* zw, const void* dug, float* dwug, float* dwd,
+               int w_t, float beta, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  const int dff = G * n;
+  if (w_t) {
+    // dWug^T[:, ilv(g*2n + c)] = sum_slot x[tok(slot), :] dUG[slot, c]   ([d, 2F]: columns [up F | gate F])
+    GemmArgs p;
+    p.mode = MODE_GROUP_K;
+    p.goff = offsets;
+    p.G = G;
+    p.M = d;
+    p.N = 2 * n;
+    p.K = P;
+    p.a = plain(x, d);
+    p.a.rows = tok_of_slot;
+    p.a_t = 1;
+    p.b = plain(dug, 2 * n);
+    p.b_t = 1;
+    p.epi.c = dwug;
+    p.epi.ldc = 2 * (int64_t)dff;
+    p.epi.c_f32 = 1;
+    p.epi.c_gstride = 2 * n;
+    p.epi.c_col_ilv = dff;
+    p.epi.beta = beta;
+    RTE_TRY(gemm_launch(p, EPI_STORE, stream, workspace, workspace_bytes));
+  } else {
+    // dWug_g[c, :] = sum_slot dUG[slot, c] x[tok(slot), :]
+    GemmArgs p;
+    p.mode = MODE_GROUP_K;
+    p.goff = offsets;
+    p.G = G;
+    p.M = 2 * n;
+    p.N = d;
+    p.K = P;
+    p.a = plain(dug, 2 * n);
+    p.a_t = 1;
+    p.b = plain(x, d);
+    p.b.rows = tok_of_slot;
+    p.b_t = 1;
+    p.epi.c = dwug;
+    p.epi.ldc = d;
+    p.epi.c_f32 = 1;
+    p.epi.c_growstride = 2 * n;
+    p.epi.c_ilv = dff;
+    p.epi.beta = beta;
+    RTE_TRY(gemm_launch(p, EPI_STORE, stream, workspace, workspace_bytes));
+  }
+  if (w_t) {
+    // dWd^T[g*n + j, :] = sum_slot zw[slot, j] dout[tok(slot), :]   ([F, d])
+    GemmArgs p;
+    p.mode = MODE_GROUP_K;
+    p.goff = offsets;
+    p.G = G;
+    p.M = n;
+    p.N = d;
+    p.K = P;
+    p.a = plain(zw, n);
+    p.a_t = 1;
+    p.b = plain(dout, d);
+    p.b.rows = tok_of_slot;
+    p.b_t = 1;
+    p.epi.c = dwd;
+    p.epi.ldc = d;
+    p.epi.c_f32 = 1;
+    p.epi.c_growstride = n;
+    p.epi.beta = beta;
+    RTE_TRY(gemm_launch(p, EPI_STORE, stream, workspace, workspace_bytes));
+  } else {
+    // dWd[:, g*n + j] = sum_slot dout[tok(slot), :] zw[slot, j]
+    GemmArgs p;
+    p.mode = MODE_GROUP_K;
+    p.goff = offsets;
+    p.G = G;
+    p.M = d;
+    p.N = n;
+    p.K = P;
+    p.a = plain(dout, d);
+    p.a.rows = tok_of_slot;
+    p.a_t = 1;
+    p.b = plain(zw, n);
+    p.b_t = 1;
+    p.epi.c = dwd;
+    p.epi.ldc = ld_wd;
+    p.epi.c_f32 = 1;
+    p.epi.c_gstride = n;
+    p.epi.beta = beta;
+    RTE_TRY(gemm_launch(p, EPI_STORE, stream, workspace, workspace_bytes));
+  }
+  return 0;
 }
 
 }  // namespace
@@ -377,90 +477,8 @@ int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const 
     p.epi.c_rows = pair_of_slot;
     RTE_TRY(gemm_launch(p, EPI_STORE, S(stream)));
   }
-  if (w_t) {
-    // dWug^T[:, ilv(g*2n + c)] = sum_slot x[tok(slot), :] dUG[slot, c]   ([d, 2F]: columns [up F | gate F])
-    GemmArgs p;
-    p.mode = MODE_GROUP_K;
-    p.goff = offsets;
-    p.G = G;
-    p.M = d;
-    p.N = 2 * n;
-    p.K = P;
-    p.a = plain(x, d);
-    p.a.rows = tok_of_slot;
-    p.a_t = 1;
-    p.b = plain(dug, 2 * n);
-    p.b_t = 1;
-    p.epi.c = dwug;
-    p.epi.ldc = 2 * (int64_t)dff;
-    p.epi.c_f32 = 1;
-    p.epi.c_gstride = 2 * n;
-    p.epi.c_col_ilv = dff;
-    p.epi.beta = beta;
-    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
-  } else {
-    // dWug_g[c, :] = sum_slot dUG[slot, c] x[tok(slot), :]
-    GemmArgs p;
-    p.mode = MODE_GROUP_K;
-    p.goff = offsets;
-    p.G = G;
-    p.M = 2 * n;
-    p.N = d;
-    p.K = P;
-    p.a = plain(dug, 2 * n);
-    p.a_t = 1;
-    p.b = plain(x, d);
-    p.b.rows = tok_of_slot;
-    p.b_t = 1;
-    p.epi.c = dwug;
-    p.epi.ldc = d;
-    p.epi.c_f32 = 1;
-    p.epi.c_growstride = 2 * n;
-    p.epi.c_ilv = dff;
-    p.epi.beta = beta;
-    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
-  }
-  if (w_t) {
-    // dWd^T[g*n + j, :] = sum_slot zw[slot, j] dout[tok(slot), :]   ([F, d])
-    GemmArgs p;
-    p.mode = MODE_GROUP_K;
-    p.goff = offsets;
-    p.G = G;
-    p.M = n;
-    p.N = d;
-    p.K = P;
-    p.a = plain(zw, n);
-    p.a_t = 1;
-    p.b = plain(dout, d);
-    p.b.rows = tok_of_slot;
-    p.b_t = 1;
-    p.epi.c = dwd;
-    p.epi.ldc = d;
-    p.epi.c_f32 = 1;
-    p.epi.c_growstride = n;
-    p.epi.beta = beta;
-    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
-  } else {
-    // dWd[:, g*n + j] = sum_slot dout[tok(slot), :] zw[slot, j]
-    GemmArgs p;
-    p.mode = MODE_GROUP_K;
-    p.goff = offsets;
-    p.G = G;
-    p.M = d;
-    p.N = n;
-    p.K = P;
-    p.a = plain(dout, d);
-    p.a.rows = tok_of_slot;
-    p.a_t = 1;
-    p.b = plain(zw, n);
-    p.b_t = 1;
-    p.epi.c = dwd;
-    p.epi.ldc = ld_wd;
-    p.epi.c_f32 = 1;
-    p.epi.c_gstride = n;
-    p.epi.beta = beta;
-    RTE_TRY(gemm_launch(p, EPI_STORE, S(stream), workspace, workspace_bytes));
-  }
+  RTE_TRY(pool_wgrad(dout, x, d, offsets, G, n, P, tok_of_slot, ld_wd, zw, dug, dwug, dwd, w_t, beta, workspace,
+                     workspace_bytes, S(stream)));
   (void)T;
   (void)pair_of_slot;
   return 0;
@@ -469,6 +487,31 @@ int rte_grouped_swiglu_bwd(const void* dout, const void* x, int T, int d, const 
 size_t rte_grouped_swiglu_bwd_workspace_bytes(int P, int G, int n, int d) {
   const size_t a = gemm_groupk_bytes(2 * n, d, P, G), b = gemm_groupk_bytes(d, n, P, G);
   return a > b ? a : b;
+}
+
+int rte_grouped_swiglu_fused_ok(int n, int d) { return pool_fused_supported(n, d) ? 1 : 0; }
+
+int rte_grouped_swiglu_fused_fwd(const void* x, int T, int d, const int32_t* offsets, int G, int n, int P,
+                                 const int32_t* tok_of_slot, const int32_t* pair_of_slot, const float* w_of_slot,
+                                 const void* wug, const void* wd, int64_t ld_wd, void* ug, void* zw, void* y_pairs,
+                                 void* stream) {
+  (void)T;
+  return pool_fused_fwd(B16(x), d, offsets, G, n, P, tok_of_slot, pair_of_slot, w_of_slot, B16(wug), B16(wd), ld_wd,
+                        B16(ug), B16(zw), B16(y_pairs), S(stream));
+}
+
+int rte_grouped_swiglu_fused_bwd(const void* dout, const void* x, int T, int d, const int32_t* offsets, int G, int n,
+                                 int P, const int32_t* tok_of_slot, const int32_t* pair_of_slot,
+                                 const float* w_of_slot, const void* wug, const void* wd, int64_t ld_wd,
+                                 const void* ug, const void* zw, void* dug, float* dw_slot, void* dx_pairs,
+                                 float* dwug, float* dwd, int w_t, float beta, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  RTE_REQUIRE(w_t == 0 || w_t == 1, "grouped_swiglu_bwd: w_t must be 0 or 1");
+  (void)T;
+  RTE_TRY(pool_fused_bwd(B16(dout), d, offsets, G, n, P, tok_of_slot, pair_of_slot, w_of_slot, B16(wug), B16(wd),
+                         ld_wd, B16(ug), B16(dug), dw_slot, B16(dx_pairs), S(stream)));
+  return pool_wgrad(dout, x, d, offsets, G, n, P, tok_of_slot, ld_wd, zw, dug, dwug, dwd, w_t, beta, workspace,
+                    workspace_bytes, S(stream));
 }
 
 int rte_dense_swiglu_fwd(const void* x, int T, int d, int F, const void* wug, const void* wd, int wd_rows,

@@ -50,6 +50,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _P],
     ),
     "rte_grouped_swiglu_bwd_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "rte_grouped_swiglu_fused_ok": (_I, [_I, _I]),
+    "rte_grouped_swiglu_fused_fwd": (
+        _I,
+        [_P, _I, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P],
+    ),
+    "rte_grouped_swiglu_fused_bwd": (
+        _I,
+        [_P, _P, _I, _I, _P, _I, _I, _I, _P, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _I, _F, _P, _SZ,
+         _P],
+    ),
     "rte_dense_swiglu_fwd": (_I, [_P, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P, _I, _P]),
     "rte_dense_swiglu_bwd": (_I, [_P, _P, _I, _I, _I, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _SZ, _P]),
     "rte_qkv_rope_fwd": (_I, [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _P, _P, _SZ, _P]),

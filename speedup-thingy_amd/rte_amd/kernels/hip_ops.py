@@ -995,6 +995,17 @@ def combine_rows(rows: torch.Tensor, T: int, k: int, *, extra=None, resid=None, 
 
 # ----------------------------------------------------------------------------- routed cluster-pool SwiGLU
 
+# 32-neuron clusters at d 128 / 256 / 512 run the fused per-cluster kernels (one launch per direction
+# for the two products and the SwiGLU; rte_grouped_swiglu_fused_*); [False] selects the two-GEMM form
+POOL_FUSED = [True]
+
+
+def _pool_entry(name: str, n: int, d: int) -> str:
+    if POOL_FUSED[0] and _lib.load().rte_grouped_swiglu_fused_ok(n, d):
+        return name.replace("rte_grouped_swiglu_", "rte_grouped_swiglu_fused_")
+    return name
+
+
 def _pool_fwd(xb, ids, w, wugb, wdb, C: int, n: int, resid, masked: bool, pk: PackIndex | None = None):
     """Grouped pool forward over the (token, cluster) pairs of ids [T, k] (id -1 = no pair), or
     of a prebuilt pack pk.  wugb [2F, d] rows [up F ; gate F], wdb [d, F]; cluster g owns
@@ -1008,7 +1019,7 @@ def _pool_fwd(xb, ids, w, wugb, wdb, C: int, n: int, resid, masked: bool, pk: Pa
     ug = torch.empty((P, 2 * n), dtype=BF16, device=xb.device)
     zw = torch.empty((P, n), dtype=BF16, device=xb.device)
     yp = torch.empty((P, d), dtype=BF16, device=xb.device)
-    call("rte_grouped_swiglu_fwd", ptr(xb), T, d, ptr(pk.offsets), C, n, P, ptr(pk.tok_of_slot),
+    call(_pool_entry("rte_grouped_swiglu_fwd", n, d), ptr(xb), T, d, ptr(pk.offsets), C, n, P, ptr(pk.tok_of_slot),
          ptr(pk.pair_of_slot), ptr(pk.w_of_slot), ptr(wugb), ptr(wdb), F, ptr(ug), ptr(zw), ptr(yp), _s())
     out = combine_rows(yp, T, k, resid=resid, out_f32=True, slot_of_pair=pk.slot_of_pair if masked else None)
     return out, pk, ug, zw
@@ -1032,7 +1043,8 @@ def _pool_bwd(db, xb, wugb, wdb, pk, ug, zw, C: int, n: int, k: int, dwug=None, 
     if dwd is None:
         dwd = torch.empty((F, d) if w_t else (d, F), dtype=F32, device=dev)
     ws, nb = workspace(_lib.load().rte_grouped_swiglu_bwd_workspace_bytes(P, C, n, d), dev)
-    call("rte_grouped_swiglu_bwd", ptr(db), ptr(xb), T, d, ptr(pk.offsets), C, n, P, ptr(pk.tok_of_slot),
+    call(_pool_entry("rte_grouped_swiglu_bwd", n, d), ptr(db), ptr(xb), T, d, ptr(pk.offsets), C, n, P,
+         ptr(pk.tok_of_slot),
          ptr(pk.pair_of_slot), ptr(pk.w_of_slot), ptr(wugb), ptr(wdb), F, ptr(ug), ptr(zw), ptr(dug), ptr(dw_slot),
          ptr(dxp), ptr(dwug), ptr(dwd), int(w_t), float(beta), ws, nb, _s())
     return dxp, dwug, dwd, dw_slot

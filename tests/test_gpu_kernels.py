@@ -378,11 +378,16 @@ def test_dense_swiglu_fwd_bwd(T, d, F, wd_rows):
 # ---------------------------------------------------------------- routed cluster pool
 
 @pytest.mark.parametrize(
-    "T,d,C,n,k",
-    [(64, 64, 4, 32, 1), (1024, 256, 32, 32, 4), (8192, 512, 64, 32, 8), (2048, 256, 16, 64, 2)],
+    "T,d,C,n,k,fused",
+    [(64, 64, 4, 32, 1, True), (1024, 256, 32, 32, 4, True), (1024, 256, 32, 32, 4, False),
+     (8192, 512, 64, 32, 8, True), (8192, 512, 64, 32, 8, False), (2048, 256, 16, 64, 2, True),
+     (512, 128, 8, 32, 3, True)],
 )
-def test_routed_cluster_pool_fwd_bwd(T, d, C, n, k):
+def test_routed_cluster_pool_fwd_bwd(T, d, C, n, k, fused, monkeypatch):
+    """fused: the per-cluster fused kernels where the shape allows (n = 32, d 128 / 256 / 512),
+    else the two-GEMM form."""
     H = _ops()
+    monkeypatch.setattr(H, "POOL_FUSED", [fused])
     rng = np.random.default_rng(T + d + C + n + k)
     F = C * n
     x = bf16_round(rng.standard_normal((T, d)).astype(np.float32))
@@ -394,7 +399,7 @@ def test_routed_cluster_pool_fwd_bwd(T, d, C, n, k):
     tx = _bf(x).requires_grad_()
     twr, tug, twd = (torch.from_numpy(a).to(DEV).requires_grad_() for a in (wr, wug, wd))
     tres = torch.from_numpy(res).to(DEV)
-    print(f"routed T={T} d={d} C={C} n={n} k={k}", flush=True)
+    print(f"routed T={T} d={d} C={C} n={n} k={k} fused={fused}", flush=True)
     out, ids, w = H.routed_cluster_pool_swiglu(tx, twr, tug, twd, k, resid=tres)
     out.backward(torch.from_numpy(dy).to(DEV))
     torch.cuda.synchronize()
@@ -430,6 +435,76 @@ def test_routed_cluster_pool_is_deterministic():
         grads.append([tx.grad.clone()] + [p.grad.clone() for p in params] + [out.detach().clone()])
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("d", [128, 256, 512])
+def test_grouped_swiglu_fused_matches_two_gemm(d):
+    """rte_grouped_swiglu_fused_fwd / _bwd against rte_grouped_swiglu_fwd / _bwd on one pack with
+    skewed routing: one cluster spread over several 128-slot tiles, clusters with ragged tails,
+    empty clusters, absent pairs (id -1).  Every output of the fused kernels lies within bf16
+    rounding of the two-GEMM form (their fp32 products add the reduction in another order; ug,
+    zw, dug and the rows are bf16); dw_slot and the weight gradients within the same bound; two
+    fused runs agree bit for bit; rows of absent pairs are left untouched."""
+    from rte_amd import _lib
+
+    H = _ops()
+    lib = _lib.load()
+    assert lib.rte_grouped_swiglu_fused_ok(32, d) == 1 and lib.rte_grouped_swiglu_fused_ok(64, d) == 0
+    rng = np.random.default_rng(d)
+    T, C, n, k = 1000, 24, 32, 4
+    F = C * n
+    ids = np.stack([rng.permutation(C - 4)[:k] for _ in range(T)]).astype(np.int32)  # clusters 20..23 empty
+    ids[: 3 * T // 4, 0] = 0          # cluster 0: 750+ slots (six tiles, ragged tail)
+    ids[::5, 2] = -1                  # absent pairs
+    tid = torch.from_numpy(ids).to(DEV)
+    w = torch.from_numpy(rng.random((T, k)).astype(np.float32)).to(DEV)
+    pk = H.pack_index(tid, C, w)
+    P = T * k
+    bf = torch.bfloat16
+    x = torch.from_numpy(rng.standard_normal((T, d)).astype(np.float32)).to(DEV).to(bf)
+    wug = (torch.from_numpy(rng.standard_normal((2 * F, d)).astype(np.float32)) * 0.05).to(DEV).to(bf)
+    wd = (torch.from_numpy(rng.standard_normal((d, F)).astype(np.float32)) * 0.05).to(DEV).to(bf)
+    dout = torch.from_numpy(rng.standard_normal((T, d)).astype(np.float32)).to(DEV).to(bf)
+    valid = pk.slot_of_pair.cpu().numpy() >= 0
+    nslot = int(pk.offsets[-1])
+    print(f"fused grouped SwiGLU vs two-GEMM d={d} T={T} C={C} k={k} slots={nslot}", flush=True)
+
+    def run(fused):
+        sfx = "fused_" if fused else ""
+        ug = torch.zeros(P, 2 * n, device=DEV, dtype=bf)
+        zw = torch.zeros(P, n, device=DEV, dtype=bf)
+        yp = torch.full((P, d), 7.0, device=DEV, dtype=bf)
+        _lib.call(f"rte_grouped_swiglu_{sfx}fwd", x.data_ptr(), T, d, pk.offsets.data_ptr(), C, n, P,
+                  pk.tok_of_slot.data_ptr(), pk.pair_of_slot.data_ptr(), pk.w_of_slot.data_ptr(), wug.data_ptr(),
+                  wd.data_ptr(), F, ug.data_ptr(), zw.data_ptr(), yp.data_ptr(), None)
+        dug = torch.zeros(P, 2 * n, device=DEV, dtype=bf)
+        dws = torch.zeros(P, device=DEV, dtype=torch.float32)
+        dxp = torch.full((P, d), 7.0, device=DEV, dtype=bf)
+        dwug = torch.empty(2 * F, d, device=DEV, dtype=torch.float32)
+        dwd = torch.empty(d, F, device=DEV, dtype=torch.float32)
+        nb = lib.rte_grouped_swiglu_bwd_workspace_bytes(P, C, n, d)
+        ws = torch.empty(max(nb, 16), device=DEV, dtype=torch.uint8)
+        _lib.call(f"rte_grouped_swiglu_{sfx}bwd", dout.data_ptr(), x.data_ptr(), T, d, pk.offsets.data_ptr(), C, n,
+                  P, pk.tok_of_slot.data_ptr(), pk.pair_of_slot.data_ptr(), pk.w_of_slot.data_ptr(), wug.data_ptr(),
+                  wd.data_ptr(), F, ug.data_ptr(), zw.data_ptr(), dug.data_ptr(), dws.data_ptr(), dxp.data_ptr(),
+                  dwug.data_ptr(), dwd.data_ptr(), 0, 0.0, ws.data_ptr(), nb, None)
+        torch.cuda.synchronize()
+        return [t.float().cpu().numpy() for t in (ug, zw, yp, dug, dws, dxp, dwug, dwd)]
+
+    ref = run(False)
+    got = run(True)
+    again = run(True)
+    names = ("ug", "zw", "y_pairs", "dug", "dw_slot", "dx_pairs", "dwug", "dwd")
+    for name, a, b, c in zip(names, got, ref, again):
+        np.testing.assert_array_equal(a, c, err_msg=f"{name}: fused runs differ")
+        if name in ("y_pairs", "dx_pairs"):
+            assert np.all(a[~valid] == 7.0), f"{name}: rows of absent pairs written"
+            a, b = a[valid], b[valid]
+        elif name in ("ug", "zw", "dug", "dw_slot"):
+            a, b = a[:nslot], b[:nslot]
+        assert_rel(a, b, BF16_RTOL, f"fused {name}")
+        # elementwise: within a few bf16 ulps of the two-GEMM value
+        np.testing.assert_allclose(a, b, rtol=2e-2, atol=2e-2 * float(np.abs(b).max()), err_msg=name)
 
 
 # ---------------------------------------------------------------- attention pieces

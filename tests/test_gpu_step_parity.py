@@ -103,7 +103,7 @@ def _run(cfg, B, S, seed):
               "pool_ids": pools}
     gpu_terms = {"loss": float(loss.detach()), "corrected_ce": float(audit.corrected_loss_per_sample.detach().mean() / scale),
                  **{f"macro_{k_}": float(v.detach()) for k_, v in audit.macro_aux.items()},
-                 **{f"aux_{k_}": float(v) for k_, v in aux.items()}}
+                 **{f"aux_{k_}": float(v.detach()) for k_, v in aux.items()}}
     return params, buffers, tok.cpu(), tgt.cpu(), chosen, usage, forced, gpu_terms, grads
 
 
