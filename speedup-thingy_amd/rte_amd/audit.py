@@ -61,12 +61,38 @@ def main_stream_aliases(*modules):
 
 @dataclass(slots=True)
 class AuditLaunch:
-    """Work started right after routing on side streams: the exact replay of the audited rows
-    and the macro consistency loss.  correction() joins the streams before using them."""
+    """Work started right after routing: the exact replay of the audited rows and the macro
+    consistency loss.  correction() joins the streams before using them.  With a deferred coda
+    the replay stops after its recursive passes and the hot path's coda call runs its coda and
+    head (`coda_extra`), which also builds its output."""
     chosen: torch.Tensor | None
     exact: ModelOutput | None
     cons: torch.Tensor | None
     streams: list
+    coda_extra: "_CodaRows | None" = None
+
+
+class _CodaRows:
+    """The audited samples' final recurrent states handed to the hot path's coda call
+    (RecursiveModel.forward_macro coda_extra): rows() joins the replay's stream and gives the rows
+    and their targets, done() builds the replay's output from its rows of the call's outputs.  It
+    holds no reference to its launch: a launch <-> rows cycle would keep the replay's autograd
+    graph (and the AccumulateGrad nodes in it) alive until the cyclic collector runs."""
+
+    def __init__(self, model: RecursiveModel, core, targets, side):
+        self.model, self.core, self.targets, self.side = model, core, targets, side
+        self.exact: ModelOutput | None = None
+
+    def rows(self):
+        h = self.core.h
+        main = torch.cuda.current_stream(h.device)
+        if self.side != main:
+            main.wait_stream(self.side)
+            h.record_stream(main)
+        return h, self.targets.index_select(0, self.core.idx)
+
+    def done(self, hidden, logits, lps, tok, source):
+        self.exact = self.model.finish_exact(self.core, hidden, logits, lps, tok, logit_source=source)
 
 
 class AuditEngine:
@@ -77,6 +103,8 @@ class AuditEngine:
         self.last_candidate_count = 0
         self.last_capped_fraction = 0.0
         self.last_sample_mode = "bernoulli"
+        # False: the work begin() starts runs on the caller's stream, in order (one stream)
+        self.side_streams = True
 
     def state_dict(self) -> dict[str, object]:
         return {
@@ -120,6 +148,8 @@ class AuditEngine:
         return p.clamp(self.config.audit_p_min, self.config.audit_p_max)
 
     def _side_stream(self, device, slot: int):
+        if not self.side_streams:
+            return torch.cuda.current_stream(device)
         streams = self.__dict__.setdefault("_streams", {})
         key = (device.index if device.index is not None else torch.cuda.current_device(), slot)
         if key not in streams:
@@ -127,11 +157,13 @@ class AuditEngine:
         return streams[key]
 
     def begin(self, model: RecursiveModel, tokens, targets, h0, route, *, seed: int,
-              chosen: torch.Tensor | None = None) -> AuditLaunch | None:
-        """Start the fixed-count audit's exact replay and the macro consistency loss on their own
-        streams as soon as h0 and the routing decisions exist, so they (and their backward) run
-        beside the hot path.  Returns None when nothing can start early (Bernoulli sampler, no
-        device)."""
+              chosen: torch.Tensor | None = None, defer_coda: bool = False) -> AuditLaunch | None:
+        """Start the fixed-count audit's exact replay and the macro consistency loss as soon as h0
+        and the routing decisions exist: on their own streams (side_streams), so they and their
+        backward can run beside the hot path, else in order on the caller's stream.  defer_coda:
+        the replay runs its recursive passes only and hands its coda and head to the hot path's
+        coda call (launch.coda_extra).  Returns None when nothing can start early (Bernoulli
+        sampler, no device)."""
         fixed = self.config.audit_fixed_count_per_batch
         if fixed is None or h0.device.type != "cuda":
             return None
@@ -143,14 +175,21 @@ class AuditEngine:
             if chosen is None:
                 chosen = self.fixed_count_index(n, k, seed, h0.device)
             side = self._side_stream(h0.device, 0)
-            side.wait_stream(main)
+            if side != main:
+                side.wait_stream(main)
             grad_corr = self.config.audit_mode == "gradient_corrected"
-            with (nullcontext() if grad_corr else torch.no_grad()), main_stream_aliases(model):
+            with (nullcontext() if grad_corr else torch.no_grad()), \
+                    (main_stream_aliases(model) if side != main else nullcontext()):
                 with torch.cuda.stream(side):
-                    launch.exact = model.forward_exact_subset(tokens, targets, chosen, reuse_router_decisions=route,
-                                                              cached_h0=h0)
+                    if defer_coda:
+                        core = model.forward_exact_subset_core(chosen, reuse_router_decisions=route, cached_h0=h0)
+                        launch.coda_extra = _CodaRows(model, core, targets, side)
+                    else:
+                        launch.exact = model.forward_exact_subset(tokens, targets, chosen,
+                                                                  reuse_router_decisions=route, cached_h0=h0)
             launch.chosen = chosen
-            launch.streams.append(side)
+            if side != main:
+                launch.streams.append(side)
         if self.config.lambda_cons != 0.0:
             side = self._side_stream(h0.device, 1)
             mac = model.macro
@@ -158,10 +197,12 @@ class AuditEngine:
                     and hip_ops.macro_fused_supported(mac.v, mac.u)):
                 # one bf16 copy of the operator tables per step, shared with the hot path
                 hip_ops.macro_fused_weights_share(mac.v, mac.u, side)
-            side.wait_stream(main)
-            with main_stream_aliases(model.macro), torch.cuda.stream(side):
+            if side != main:
+                side.wait_stream(main)
+            with (main_stream_aliases(model.macro) if side != main else nullcontext()), torch.cuda.stream(side):
                 launch.cons = model.macro.consistency_loss(h0, h0, route.recipe_id)
-            launch.streams.append(side)
+            if side != main:
+                launch.streams.append(side)
         return launch
 
     def _fixed_count_sample(self, meta: ModelMeta, seed: int, chosen: torch.Tensor | None):
@@ -248,6 +289,8 @@ class AuditEngine:
                 main.wait_stream(st)
             if launch.chosen is not None:
                 chosen = launch.chosen
+            if launch.exact is None and launch.coda_extra is not None:
+                launch.exact = launch.coda_extra.exact  # built by the hot path's coda call
             for t in _tensors_of(launch.exact) + ([launch.cons] if launch.cons is not None else []):
                 t.record_stream(main)
         if self.config.audit_fixed_count_per_batch is None:
@@ -307,7 +350,8 @@ class AuditEngine:
             # gradients): reuse them instead of a second full-size selection and its backward
             h0_sub = (exact.meta.h0 if grad_corr and exact.meta.h0 is not None and exact.meta.h0.requires_grad
                       else hip_ops.select_rows(hot.meta.h0, idx))
-            hot_logits = hip_ops.select_logit_rows(hot.meta.logits, idx) if hot.meta.logits is not None else None
+            src = hot.meta.logit_source if hot.meta.logit_source is not None else hot.meta.logits
+            hot_logits = hip_ops.select_logit_rows(src, idx) if src is not None else None
             tr = self.config
             exact_end = exact.meta.recurrent_hidden
             if h0_sub is not None and exact_end is not None:

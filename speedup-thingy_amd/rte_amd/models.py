@@ -38,6 +38,9 @@ class ModelMeta:
     shortlist: ShortlistResult | None = None
     touch_table: torch.Tensor | None = None
     token_loss: torch.Tensor | None = None
+    # the LM head's output these logits are rows of, when the head ran over more rows than this
+    # output's (the hot path's coda call that also carries the audit replay's rows)
+    logit_source: torch.Tensor | None = None
 
     @property
     def active_touches(self) -> torch.Tensor | None:
@@ -45,6 +48,17 @@ class ModelMeta:
         if self.touch_table is None or self.recipe_ids is None:
             return None
         return self.touch_table[self.recipe_ids]
+
+
+@dataclass(slots=True)
+class ExactCore:
+    """The exact replay of the audited samples up to its last recursive pass: their indices, the
+    routing decisions and h0 rows they reuse, the final recurrent state h and the kept states."""
+    idx: torch.Tensor
+    route: RouterOutput
+    h0: torch.Tensor
+    h: torch.Tensor
+    states: dict
 
 
 @dataclass(slots=True)
@@ -161,6 +175,22 @@ class RecursiveModel(nn.Module):
     def forward_exact_from_h0(self, h0, targets=None, return_states=False, return_loss_per_sample=False, *,
                               router_decisions: RouterOutput | None = None, fixed_recipe=None, fixed_depth=None):
         route = router_decisions or self.router(h0, fixed_recipe=fixed_recipe, fixed_depth=fixed_depth)
+        h, states = self._exact_core(h0, route, return_states)
+        hidden = self._coda_hidden(h)
+        logits, lps, tok = head_logits_loss(hidden, self.vocab_weight, targets)
+        return self._exact_output(route, h0, h, states, hidden, logits, lps, tok, return_states,
+                                  return_loss_per_sample)
+
+    def _exact_output(self, route, h0, h, states, hidden, logits, lps, tok, return_states, return_loss_per_sample,
+                      logit_source=None):
+        meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
+                         hidden=hidden, logits=logits, states=states if return_states else None,
+                         touch_table=self.active_touch_table, token_loss=tok, logit_source=logit_source)
+        return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
+                           meta)
+
+    def _exact_core(self, h0, route: RouterOutput, return_states: bool):
+        """The exact recursive passes of rte/models.py:416-512 from h0: (h, kept states)."""
         h = h0
         states: dict[int, torch.Tensor] = {}
         T = self.config.t_max
@@ -190,13 +220,7 @@ class RecursiveModel(nn.Module):
                                            weights=weights, head_scale=head_scales[t])
                 if return_states and (t + 1) in self.config.depth_choices:
                     states[t + 1] = h  # every pass returns a new tensor; nothing writes h in place
-        hidden = self._coda_hidden(h)
-        logits, lps, tok = head_logits_loss(hidden, self.vocab_weight, targets)
-        meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
-                         hidden=hidden, logits=logits, states=states if return_states else None,
-                         touch_table=self.active_touch_table, token_loss=tok)
-        return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
-                           meta)
+        return h, states
 
     def forward_exact(self, tokens, targets=None, return_states=False, return_loss_per_sample=False, **kw):
         return self.forward_exact_from_h0(self._prelude(tokens), targets, return_states, return_loss_per_sample, **kw)
@@ -214,11 +238,32 @@ class RecursiveModel(nn.Module):
         return self.forward_exact_from_h0(h0, targets.index_select(0, idx), return_states, return_loss_per_sample,
                                           router_decisions=route)
 
+    def forward_exact_subset_core(self, audit_index, *, reuse_router_decisions: RouterOutput, cached_h0,
+                                  return_states=True) -> ExactCore:
+        """forward_exact_subset up to the last recursive pass: the coda and the head of these rows
+        can then run in another call (finish_exact builds the replay's output from its rows)."""
+        idx = audit_index.nonzero(as_tuple=False).flatten() if audit_index.dtype == torch.bool else audit_index
+        route = reuse_router_decisions.subset(idx)
+        h0 = hip_ops.select_rows(cached_h0, idx)
+        h, states = self._exact_core(h0, route, return_states)
+        return ExactCore(idx, route, h0, h, states)
+
+    def finish_exact(self, core: ExactCore, hidden, logits, lps, tok, *, logit_source=None,
+                     return_states=True, return_loss_per_sample=True) -> ModelOutput:
+        """The replay's output from its rows of a coda / head call: hidden [A, S, d], logits
+        [A, S, V], per-sample and token cross-entropy; logit_source = the head's whole output."""
+        return self._exact_output(core.route, core.h0, core.h, core.states, hidden, logits, lps, tok, return_states,
+                                  return_loss_per_sample, logit_source=logit_source)
+
     def forward_macro(self, tokens, targets=None, return_states=False, return_loss_per_sample=False, *,
                       shortlist=False, seed=0, fixed_recipe=None, fixed_depth=None,
-                      shortlist_random_negs=None, on_routed=None) -> ModelOutput:
+                      shortlist_random_negs=None, on_routed=None, coda_extra=None) -> ModelOutput:
         """rte/models.py:681-723.  on_routed(h0, route), if given, runs right after routing: the
-        training step uses it to start the audit replay on its own stream while the hot path runs."""
+        training step uses it to start the audit replay on its own stream while the hot path runs.
+        coda_extra(), if given and it returns an object (full-vocabulary head with targets), adds
+        rows to the coda, final norm, head and cross-entropy call: `.rows()` -> (h [A, S, d],
+        targets [A, S]), and `.done(hidden, logits, lps, tok, source)` receives their outputs
+        (the audit replay's rows: one set of launches for both instead of two)."""
         h0 = self._prelude(tokens)
         route = self.router(h0, fixed_recipe=fixed_recipe, fixed_depth=fixed_depth)
         if on_routed is not None:
@@ -227,7 +272,7 @@ class RecursiveModel(nn.Module):
         # depth id (stride_ids_for_depths: first stride equal to the depth)
         sid = route.depth_id if len(set(self.config.depth_choices)) == len(self.config.depth_choices) else None
         h, trace = self.macro(h0, h0, route.recipe_id, route.depth, return_states=return_states, stride_ids=sid)
-        sl = None
+        sl, source = None, None
         if shortlist and targets is not None:
             hidden = self._coda_hidden(h)
             full_logits = None
@@ -235,12 +280,21 @@ class RecursiveModel(nn.Module):
                                           random_negs=shortlist_random_negs)
             lps, logits, tok = sl.loss_per_sample, sl.logits, sl.token_loss
         else:
-            hidden = self._coda_hidden(h)
-            full_logits, lps, tok = head_logits_loss(hidden, self.vocab_weight, targets)
+            extra = coda_extra() if coda_extra is not None and targets is not None else None
+            if extra is not None:
+                hx, tx = extra.rows()
+                B = h.shape[0]
+                hidden_all = self._coda_hidden(torch.cat([h, hx.to(h.dtype)]))
+                source, lps_all, tok_all = head_logits_loss(hidden_all, self.vocab_weight, torch.cat([targets, tx]))
+                hidden, full_logits, lps, tok = hidden_all[:B], source[:B], lps_all[:B], tok_all[:B]
+                extra.done(hidden_all[B:], source[B:], lps_all[B:], tok_all[B:], source)
+            else:
+                hidden = self._coda_hidden(h)
+                full_logits, lps, tok = head_logits_loss(hidden, self.vocab_weight, targets)
             logits = full_logits
         meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
                          hidden=hidden, logits=full_logits, states=trace.states if return_states else None,
                          macro_trace=trace, shortlist=sl, touch_table=self.active_touch_table,
-                         token_loss=tok)
+                         token_loss=tok, logit_source=source)
         return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
                            meta)

@@ -123,8 +123,17 @@ class TrainEngine:
         self.last_grad_metrics: dict[str, Any] = {}
         self.aligned_lm_phase = "A"  # the lm_aligned mode's phase (rte/training.py:128); kept for checkpoints
         self._current_lr = tr.lr
-        # start the audit replay and the consistency loss on side streams right after routing
+        # start the audit replay and the consistency loss right after routing, on side streams;
+        # graph_side_streams False: captured steps issue them in order on the step's stream (a
+        # graph with parallel branches is launched node by node from the host, a one-stream graph
+        # from its recorded packets, but only branches overlap on the device)
         self.audit_streams = self.device.type == "cuda"
+        self.graph_side_streams = True
+        # the replay's coda and head run in the hot path's coda call (its rows appended; the
+        # full-vocabulary head only): one set of launches for both.  Not in captured steps with
+        # side streams: there the replay's own coda overlaps the hot path instead.
+        self.replay_coda_shared = True
+        self._capturing = False
         self._bf16 = hip_ops.Bf16Prefetch(enabled=self.device.type == "cuda" and tr.precision == "bf16")
         self._graph_enabled = False
         self._graph_keep = False
@@ -318,13 +327,18 @@ class TrainEngine:
 
         def on_routed(h0, route):
             # the audit replay and the consistency loss need only h0 and the routing decisions
-            launched.append(self.audit_engine.begin(m, tokens, targets, h0, route, seed=audit_seed, chosen=chosen))
+            share = self.replay_coda_shared and not shortlist and not (self._capturing and self.graph_side_streams)
+            launched.append(self.audit_engine.begin(m, tokens, targets, h0, route, seed=audit_seed, chosen=chosen,
+                                                    defer_coda=share))
+
+        def coda_extra():
+            return launched[0].coda_extra if launched and launched[0] is not None else None
 
         with self._autocast():
             hot = m.forward_macro(tokens, targets, return_states=True, return_loss_per_sample=True,
                                   shortlist=shortlist, seed=tr.seed + self.global_step, fixed_recipe=tr.fixed_recipe,
                                   fixed_depth=tr.fixed_depth, shortlist_random_negs=random_negs,
-                                  on_routed=on_routed if self.audit_streams else None)
+                                  on_routed=on_routed if self.audit_streams else None, coda_extra=coda_extra)
             audit = self.audit_engine.correction(m, tokens, targets, hot, seed=audit_seed, chosen=chosen,
                                                  launch=launched[0] if launched else None)
             aux = self._router_aux(hot)
@@ -475,9 +489,15 @@ class TrainEngine:
         self._bf16.begin()
         tr = self.config.training
         m = self.recursive_model
-        loss, hot, audit, aux, scale = self._macro_loss(st["tokens"], st["targets"], shortlist=shortlist,
-                                                        chosen=st["chosen"] if st["chosen"].numel() else None,
-                                                        random_negs=st["rnd"])
+        side, self.audit_engine.side_streams = self.audit_engine.side_streams, self.graph_side_streams
+        self._capturing = True
+        try:
+            loss, hot, audit, aux, scale = self._macro_loss(st["tokens"], st["targets"], shortlist=shortlist,
+                                                            chosen=st["chosen"] if st["chosen"].numel() else None,
+                                                            random_negs=st["rnd"])
+        finally:
+            self.audit_engine.side_streams = side
+            self._capturing = False
         if check_finite:  # skip flag and "stepped" metric in one launch, no host read
             bad, ok = hip_ops.nonfinite_flags(loss)
         else:

@@ -188,21 +188,26 @@ def _engine_from(cfg):
     return TrainEngine(cfg, device=torch.device("cuda"))
 
 
-def test_cfg3_step_eager_vs_captured():
+@pytest.mark.parametrize("side_streams", [True, False])
+def test_cfg3_step_eager_vs_captured(side_streams):
     """The bench's cfg3 recursive_macro engine (d512, pool 64 x 32 top-8, depth 4, V2048,
     B128 x S64): the eager and captured engines from one seed agree step by step (4 steps: two
     eager warm-ups, the capture, a replay), parameters change, and every gradient of an extra
-    eager forward / backward is finite."""
+    eager forward / backward is finite.  The captured engine runs the replay's own coda on a side
+    stream (side_streams) or appends the replay's rows to the hot coda call with everything on one
+    stream; the eager engine does the same, so both sum in the same order."""
     import bench
 
     cfg = bench.cfg3_config()
     a, b = _engine_from(cfg), _engine_from(cfg)
+    a.replay_coda_shared = not side_streams
+    b.graph_side_streams = side_streams
     b.enable_graph_capture(True)
     gen = torch.Generator().manual_seed(cfg.training.seed)
     batches = [bench.zipf_batch(gen, cfg.model.vocab_size, 128, 64, DEV) for _ in range(4)]
     before = {n_: p.detach().clone() for n_, p in a.recursive_model.named_parameters()}
     for step, batch in enumerate(batches):
-        print(f"cfg3 step {step}", flush=True)
+        print(f"cfg3 step {step} (captured side streams {side_streams})", flush=True)
         with warnings.catch_warnings(record=True) as caught:
             warnings.simplefilter("always")
             ra, rb = a.train_step(batch), b.train_step(batch)

@@ -43,12 +43,13 @@ def _rel(a, b):
     return float((a.double() - b.double()).norm() / b.double().norm().clamp_min(1e-30))
 
 
-def _run(cfg, B, S, seed):
+def _run(cfg, B, S, seed, shared_coda=True):
     import bench
     from rte_amd.kernels import hip_ops
     from rte_amd.training import TrainEngine
 
     eng = TrainEngine(cfg, device=torch.device(DEV))
+    eng.replay_coda_shared = shared_coda
     m = eng.recursive_model
     with torch.no_grad():
         # a macro update well above the rounding of h0: the distillation's delta terms divide by
@@ -79,12 +80,16 @@ def _run(cfg, B, S, seed):
     grads = {n: (p.grad.detach().float().cpu() if p.grad is not None else None) for n, p in m.named_parameters()}
     chosen = audit.audit_mask.nonzero().flatten().cpu()
     # the routed pools' decisions, by call: prelude and hot coda over B S rows, the replay's coda
-    # over the audited rows
+    # over the audited rows (after the hot rows when the two share the coda call)
     pools = {"prelude": [], "coda": [], "replay_coda": []}
     k = cfg.model.ffn_top_k
     for name, x, ids, mod in calls:
-        key = name if x.reshape(-1, x.shape[-1]).shape[0] == B * S else "replay_coda"
-        pools[key].append(ids.long().cpu())
+        n = x.reshape(-1, x.shape[-1]).shape[0]
+        if name == "coda" and n > B * S:
+            pools["coda"].append(ids[:B * S].long().cpu())
+            pools["replay_coda"].append(ids[B * S:].long().cpu())
+        else:
+            pools[name if n == B * S else "replay_coda"].append(ids.long().cpu())
         if cfg.training.precision == "fp32":  # the fp32 router product the pool used
             from rte_amd.kernels import f32_ops
 
@@ -107,8 +112,10 @@ def _run(cfg, B, S, seed):
     return params, buffers, tok.cpu(), tgt.cpu(), chosen, usage, forced, gpu_terms, grads
 
 
-@pytest.mark.parametrize("precision,B", [("bf16", 8), ("fp32", 8)])
-def test_cfg3_step_matches_cpu_port(precision, B):
+@pytest.mark.parametrize("precision,B,shared_coda", [("bf16", 8, True), ("bf16", 8, False), ("fp32", 8, True)])
+def test_cfg3_step_matches_cpu_port(precision, B, shared_coda):
+    """shared_coda: the audit replay's rows go through the hot path's coda / head call, else the
+    replay runs its own (the captured step with side streams)."""
     import dataclasses
 
     import bench
@@ -117,8 +124,8 @@ def test_cfg3_step_matches_cpu_port(precision, B):
     cfg = dataclasses.replace(cfg, training=dataclasses.replace(cfg.training, precision=precision))
     S = 64
     rtol = RTOL[precision]
-    print(f"cfg3 layout step parity, precision {precision}, B={B} S={S}", flush=True)
-    params, buffers, tok, tgt, chosen, usage, forced, gt, grads = _run(cfg, B, S, seed=11)
+    print(f"cfg3 layout step parity, precision {precision}, B={B} S={S}, shared coda {shared_coda}", flush=True)
+    params, buffers, tok, tgt, chosen, usage, forced, gt, grads = _run(cfg, B, S, seed=11, shared_coda=shared_coda)
     assert chosen.numel() == 1
     # the fp32 step is checked against the restatement in float64 (its own rounding is then the
     # only difference), the bf16 step against fp32
@@ -126,9 +133,9 @@ def test_cfg3_step_matches_cpu_port(precision, B):
     terms, pg = port.loss_and_grads(tok, tgt, chosen=chosen, usage_ema=usage, forced=forced)
     # the port's own recipe choice agrees with the GPU's on these samples (no near-tie forced)
     assert torch.equal(terms["route"]["recipe_id"], forced["recipe_id"])
-    ct = {"loss": float(terms["loss"]), "corrected_ce": float(terms["corrected_ce"]),
-          **{f"macro_{k}": float(v) for k, v in terms["macro_aux"].items()},
-          **{f"aux_{k}": float(v) for k, v in terms["router_aux"].items()}}
+    ct = {"loss": float(terms["loss"].detach()), "corrected_ce": float(terms["corrected_ce"].detach()),
+          **{f"macro_{k}": float(torch.as_tensor(v).detach()) for k, v in terms["macro_aux"].items()},
+          **{f"aux_{k}": float(torch.as_tensor(v).detach()) for k, v in terms["router_aux"].items()}}
     lines, bad = [], []
     # load = lambda (R sum mean_p^2 - 1) cancels to ~1e-3 of its terms: compare on their scale
     scale_of = {"aux_load": cfg.training.lambda_load}
