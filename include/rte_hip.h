@@ -572,6 +572,14 @@ int rte_nonfinite(const float* x, float* bad, float* ok, void* stream);
 int rte_step_metrics(const float* hot, const float* corr, const int64_t* depth, int B, float scale, float seq,
                      float* out, void* stream);
 
+/* The step's loss (rte/training.py:1381-1385): out[0] = coef * sum_b x[b] + sum_i *terms[i] (x f32
+ * [n], e.g. the corrected per-sample cross-entropy with coef = 1 / (n * seq); terms: up to 32
+ * device f32 scalars given as a host array of pointers, added in order after the row sum, which
+ * is in a fixed order).  bwd: dx[b] = coef * g[0] (the terms' gradients are g itself). */
+int rte_loss_sum(const float* x, int n, float coef, const float* const* terms, int n_terms, float* out,
+                 void* stream);
+int rte_loss_sum_bwd(const float* g, int n, float coef, float* dx, void* stream);
+
 /* ---- fused AdamW step with the trainer's per-group norms (replaces torch.optim.AdamW.step,
  *      clip_grad_norm_ and _optimizer_grad_metrics of rte/training.py:385-468) ----
  * rows: device array of n_tensors records {p, g, exp_avg, exp_avg_sq, step (f32 scalar) pointers,

@@ -10,6 +10,9 @@
 //     counts[r] = #{i : ids[i] == r and mask[i]};  ema = ema beta + (1 - beta) counts / max(sum counts, 1)
 //   nonfinite (the step's skip test on the loss, rte/training.py:445-468) and step_metrics (the
 //     per-sample means of rte/training.py:1412-1472: hot / corrected loss, nll per token, depth)
+//   loss_sum (the step's loss, rte/training.py:1381-1385): loss = coef sum_b x[b] + sum_i term_i
+//     (term_i device scalars, added in order after the row sum); its backward fills
+//     dx[b] = coef g[0]
 //
 // Row sums run in a fixed order (per-thread row strides, then an LDS tree); the counts are
 // integer LDS atomics, exact in any order.
@@ -131,6 +134,30 @@ __global__ void __launch_bounds__(kBkThreads)
   }
 }
 
+constexpr int kLossTerms = 32;
+
+struct LossTerms {
+  const float* t[kLossTerms];
+};
+
+__global__ void __launch_bounds__(kBkThreads)
+    loss_sum_kernel(const float* x, int n, float coef, LossTerms terms, int nt, float* out) {
+  __shared__ float red[kBkThreads];
+  float s = 0.0f;
+  for (int b = threadIdx.x; b < n; b += kBkThreads) s += x[b];
+  const float tot = bk_block_sum(s, red);
+  if (threadIdx.x == 0) {
+    float r = coef * tot;
+    for (int i = 0; i < nt; ++i) r += *terms.t[i];
+    out[0] = r;
+  }
+}
+
+__global__ void __launch_bounds__(kBkThreads) loss_sum_bwd_kernel(const float* g, int n, float coef, float* dx) {
+  const float v = coef * g[0];
+  for (int b = blockIdx.x * kBkThreads + threadIdx.x; b < n; b += gridDim.x * kBkThreads) dx[b] = v;
+}
+
 }  // namespace
 
 }  // namespace rte
@@ -173,6 +200,29 @@ int rte_step_metrics(const float* hot, const float* corr, const int64_t* depth, 
   hipLaunchKernelGGL(step_metrics_kernel, dim3(1), dim3(kBkThreads), 0, static_cast<hipStream_t>(stream), hot, corr,
                      depth, B, scale, seq, out);
   return check_launch("step_metrics");
+}
+
+int rte_loss_sum(const float* x, int n, float coef, const float* const* terms, int n_terms, float* out,
+                 void* stream) {
+  RTE_REQUIRE(n >= 0 && n_terms >= 0 && n_terms <= kLossTerms, "loss_sum: 0 <= n, 0 <= terms <= 32");
+  RTE_REQUIRE(out && (n == 0 || x) && (n_terms == 0 || terms), "loss_sum: null argument");
+  LossTerms lt{};
+  for (int i = 0; i < n_terms; ++i) {
+    RTE_REQUIRE(terms[i], "loss_sum: null term");
+    lt.t[i] = terms[i];
+  }
+  hipLaunchKernelGGL(loss_sum_kernel, dim3(1), dim3(kBkThreads), 0, static_cast<hipStream_t>(stream), x, n, coef, lt,
+                     n_terms, out);
+  return check_launch("loss_sum");
+}
+
+int rte_loss_sum_bwd(const float* g, int n, float coef, float* dx, void* stream) {
+  RTE_REQUIRE(n >= 0 && g && (n == 0 || dx), "loss_sum_bwd: bad arguments");
+  if (n == 0) return 0;
+  const int blocks = (n + kBkThreads - 1) / kBkThreads;
+  hipLaunchKernelGGL(loss_sum_bwd_kernel, dim3(blocks < 64 ? blocks : 64), dim3(kBkThreads), 0,
+                     static_cast<hipStream_t>(stream), g, n, coef, dx);
+  return check_launch("loss_sum_bwd");
 }
 
 }  // extern "C"

@@ -135,6 +135,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_count_ema": (_I, [_P, _P, _I, _P, _I, _F, _P]),
     "rte_nonfinite": (_I, [_P, _P, _P, _P]),
     "rte_step_metrics": (_I, [_P, _P, _P, _I, _F, _F, _P, _P]),
+    "rte_loss_sum": (_I, [_P, _I, _F, _P, _I, _P, _P]),
+    "rte_loss_sum_bwd": (_I, [_P, _I, _F, _P, _P]),
     "rte_mse_workspace_bytes": (_SZ, [_I64]),
     "rte_mse_fwd": (_I, [_P, _P, _I64, _P, _P, _SZ, _P]),
     "rte_replay_fwd_pass": (_I, [_I] * 8 + [_P] * 7 + [_F] + [_P] * 3 + [_F] + [_P] * 2 + [_F] + [_P] * 25),

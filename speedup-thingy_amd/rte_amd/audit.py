@@ -147,6 +147,15 @@ class AuditEngine:
              + self.config.audit_gamma * self._coverage_deficit(meta.recipe_ids, r.recipe_logits.shape[-1]))
         return p.clamp(self.config.audit_p_min, self.config.audit_p_max)
 
+    def _zero(self, like: torch.Tensor) -> torch.Tensor:
+        """A read-only zero scalar like `like`, made once per device and dtype (the auxiliary
+        terms a step does not form)."""
+        cache = self.__dict__.setdefault("_zeros", {})
+        key = (str(like.device), like.dtype)
+        if key not in cache:
+            cache[key] = like.new_zeros(())
+        return cache[key]
+
     def _side_stream(self, device, slot: int):
         if not self.side_streams:
             return torch.cuda.current_stream(device)
@@ -315,7 +324,7 @@ class AuditEngine:
                 "audit_inclusion_prob": p_mean,
             }
         corrected = None
-        zero = hot.loss_per_sample.new_zeros(())
+        zero = self._zero(hot.loss_per_sample)
         aux = {k: zero for k in ("hid", "cos", "kl", "norm", "cons", "delta_dir", "delta_rms", "endpoint_normed",
                                  "endpoint_raw", "rms_trust")}
         if count is not None:  # fixed-count sampler: rows and count known without reading the mask

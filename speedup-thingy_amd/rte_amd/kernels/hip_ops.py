@@ -1764,6 +1764,41 @@ def step_metrics(hot_lps, corr_lps, depths, *, scale: float, seq: float) -> torc
     return out
 
 
+class LossSumFn(torch.autograd.Function):
+    """coef * sum(x) + sum of the scalar terms (the step's loss, rte/training.py:1381-1385) in
+    one launch; the backward is one fill of dx = coef * g, and each term's gradient is g."""
+
+    @staticmethod
+    def forward(ctx, x, coef, *terms):
+        xs = x.detach().reshape(-1).contiguous().to(F32)
+        ts = [t.detach().reshape(()).to(F32).contiguous() for t in terms]
+        out = torch.empty((), dtype=F32, device=xs.device)
+        table = (ctypes.c_void_p * max(len(ts), 1))(*[t.data_ptr() for t in ts])
+        call("rte_loss_sum", ptr(xs), xs.numel(), float(coef), ctypes.addressof(table), len(ts), ptr(out), _s())
+        ctx.n, ctx.coef, ctx.xshape = xs.numel(), float(coef), x.shape
+        ctx.tshapes = [t.shape for t in terms]
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        g = g.detach().reshape(()).to(F32).contiguous()
+        dx = None
+        if ctx.needs_input_grad[0]:
+            dx = torch.empty((ctx.n,), dtype=F32, device=g.device)
+            call("rte_loss_sum_bwd", ptr(g), ctx.n, ctx.coef, ptr(dx), _s())
+            dx = dx.view(ctx.xshape)
+        return (dx, None, *[g.reshape(sh) if need else None
+                            for sh, need in zip(ctx.tshapes, ctx.needs_input_grad[2:])])
+
+
+def loss_sum(x: torch.Tensor, coef: float, terms) -> torch.Tensor:
+    """coef * x.sum() + sum(terms): terms are scalar tensors (up to 32)."""
+    _lib.require_device_tensors("loss_sum", x, *terms)
+    if len(terms) > 32:
+        raise ValueError("loss_sum: at most 32 terms")
+    return LossSumFn.apply(x, float(coef), *terms)
+
+
 def audit_correct(hot_tok, exact_tok, idx, p, *, clip=None, grad_corrected=True):
     """(corrected per-sample loss [B], exact per-sample loss [A], stats [4] = residual mean, std,
     var, corrected metric loss) from token losses hot_tok [B, S] and exact_tok [A, S]."""

@@ -155,7 +155,7 @@ class MacroOperators(nn.Module):
         v / u are gathered, and their gradients are per-group reductions in a fixed order."""
         _, S, d = h.shape
         R, Kk = self.v.shape[0], self.v.shape[1]
-        key = recipe_ids.long() * Kk + stride_ids.long()
+        key = torch.add(stride_ids.long(), recipe_ids.long(), alpha=Kk)
         B = key.numel()  # may exceed h's samples on the fused path (repeated sources)
         if (self._fused_bounded() and B % h.shape[0] == 0
                 and hip_ops.macro_fused_supported(self.v, self.u, B // h.shape[0])):
@@ -248,13 +248,23 @@ class MacroOperators(nn.Module):
         if stride_ids is None:
             stride_ids = self.stride_ids_for_depths(depths)
         out = self.apply_vectorized(h, h0, recipe_ids, stride_ids)
+        ones, zero = self._trace_constants(depths.shape[0], h.device, h.dtype)
         trace = MacroTrace(
             states={},
             stride_sequence=[],  # filled lazily by callers that need it (avoids a host sync)
-            physical_passes=torch.ones(depths.shape[0], dtype=torch.float32, device=h.device),
-            decomposition_error=h.new_zeros(()),
+            physical_passes=ones,
+            decomposition_error=zero,
         )
         return out, trace
+
+    def _trace_constants(self, n: int, device, dtype):
+        """One physical pass per sample and a zero decomposition error: made once per (n, device,
+        dtype) and shared by the steps (read-only)."""
+        cache = self.__dict__.setdefault("_trace_const", {})
+        key = (n, str(device), dtype)
+        if key not in cache:
+            cache[key] = (torch.ones(n, dtype=torch.float32, device=device), torch.zeros((), dtype=dtype, device=device))
+        return cache[key]
 
     def consistency_loss(self, h, h0, recipe_ids):
         """rte/macro.py:342-359: Phi_{2s}(h) vs Phi_s(Phi_s(h)) for every (s, 2s) stride pair."""

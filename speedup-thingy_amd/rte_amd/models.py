@@ -61,12 +61,22 @@ class ExactCore:
     states: dict
 
 
-@dataclass(slots=True)
 class ModelOutput:
-    loss: torch.Tensor | None
-    loss_per_sample: torch.Tensor | None
-    logits: torch.Tensor | None
-    meta: ModelMeta
+    """loss (the mean of the per-sample losses), loss_per_sample, logits, meta.  Given the
+    per-sample losses as `mean_of`, the mean is taken when `loss` is first read (the training
+    step composes its own loss from the per-sample values and never reads it)."""
+
+    __slots__ = ("_loss", "_mean_of", "loss_per_sample", "logits", "meta")
+
+    def __init__(self, loss, loss_per_sample, logits, meta, *, mean_of=None):
+        self._loss, self._mean_of = loss, mean_of
+        self.loss_per_sample, self.logits, self.meta = loss_per_sample, logits, meta
+
+    @property
+    def loss(self):
+        if self._loss is None and self._mean_of is not None:
+            self._loss, self._mean_of = self._mean_of.mean(), None
+        return self._loss
 
 
 def lm_loss_per_sample(logits: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
@@ -186,8 +196,7 @@ class RecursiveModel(nn.Module):
         meta = ModelMeta(router=route, recipe_ids=route.recipe_id, depths=route.depth, h0=h0, recurrent_hidden=h,
                          hidden=hidden, logits=logits, states=states if return_states else None,
                          touch_table=self.active_touch_table, token_loss=tok, logit_source=logit_source)
-        return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
-                           meta)
+        return ModelOutput(None, lps if return_loss_per_sample else None, logits, meta, mean_of=lps)
 
     def _exact_core(self, h0, route: RouterOutput, return_states: bool):
         """The exact recursive passes of rte/models.py:416-512 from h0: (h, kept states)."""
@@ -296,5 +305,4 @@ class RecursiveModel(nn.Module):
                          hidden=hidden, logits=full_logits, states=trace.states if return_states else None,
                          macro_trace=trace, shortlist=sl, touch_table=self.active_touch_table,
                          token_loss=tok, logit_source=source)
-        return ModelOutput(lps.mean() if lps is not None else None, lps if return_loss_per_sample else None, logits,
-                           meta)
+        return ModelOutput(None, lps if return_loss_per_sample else None, logits, meta, mean_of=lps)

@@ -72,6 +72,10 @@ def _detached(obj, memo: dict | None = None):
         out = type(obj)(_detached(v, memo) for v in obj)
     elif isinstance(obj, RouterSubset):
         out = RouterSubset(_detached(obj._parent, memo), obj._mask)
+    elif isinstance(obj, ModelOutput):
+        out = ModelOutput(_detached(obj._loss, memo), _detached(obj.loss_per_sample, memo),
+                          _detached(obj.logits, memo), _detached(obj.meta, memo),
+                          mean_of=_detached(obj._mean_of, memo))
     elif dataclasses.is_dataclass(obj) and not isinstance(obj, type):
         out = dataclasses.replace(obj, **{f.name: _detached(getattr(obj, f.name), memo)
                                           for f in dataclasses.fields(obj) if f.init})
@@ -343,11 +347,15 @@ class TrainEngine:
                                                  launch=launched[0] if launched else None)
             aux = self._router_aux(hot)
             scale = self._loss_scale(targets)
-            # the auxiliary terms as one stacked sum (two launches instead of one add per term)
-            terms = [audit.corrected_loss_per_sample.mean() / scale, *audit.macro_aux.values(), *aux.values()]
-            dev = terms[0].device
-            loss = torch.stack([(t if isinstance(t, torch.Tensor) else torch.tensor(float(t), device=dev))
-                                .reshape(()).float() for t in terms]).sum()
+            # corrected CE / S + every auxiliary term: one launch (a stacked sum for CPU tensors)
+            corr = audit.corrected_loss_per_sample
+            dev = corr.device
+            extra = [(t if isinstance(t, torch.Tensor) else torch.tensor(float(t), device=dev)).reshape(()).float()
+                     for t in (*audit.macro_aux.values(), *aux.values())]
+            if corr.is_cuda:
+                loss = hip_ops.loss_sum(corr, 1.0 / (corr.numel() * scale), extra)
+            else:
+                loss = torch.stack([corr.mean() / scale, *extra]).sum()
         return loss, hot, audit, aux, scale
 
     def _macro_metrics(self, loss, hot, audit, aux, scale, targets, shortlist, stepped):

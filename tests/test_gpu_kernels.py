@@ -507,6 +507,25 @@ def test_grouped_swiglu_fused_matches_two_gemm(d):
         np.testing.assert_allclose(a, b, rtol=2e-2, atol=2e-2 * float(np.abs(b).max()), err_msg=name)
 
 
+def test_loss_sum_matches_torch():
+    """rte_loss_sum / _bwd: coef * sum(x) + sum of scalar terms, gradient coef for every row of x
+    and 1 for every term, against torch in float64 (30 terms, one not requiring a gradient)."""
+    H = _ops()
+    rng = np.random.default_rng(3)
+    x = torch.from_numpy(rng.standard_normal(131).astype(np.float32)).to(DEV).requires_grad_()
+    terms = [torch.tensor(float(v), device=DEV, requires_grad=i != 7) for i, v in enumerate(rng.standard_normal(30))]
+    coef = 1.0 / (131 * 64)
+    print("loss_sum: 131 rows, 30 terms", flush=True)
+    out = H.loss_sum(x, coef, terms)
+    (out * 3.0).backward()
+    torch.cuda.synchronize()
+    ref = coef * x.detach().double().sum() + sum(t.detach().double() for t in terms)
+    assert abs(float(out.detach()) - float(ref)) <= 1e-6 * max(1.0, abs(float(ref)))
+    np.testing.assert_allclose(_np(x.grad), np.full(131, 3.0 * coef, np.float32), rtol=1e-6)
+    for i, t in enumerate(terms):
+        assert (t.grad is None) if i == 7 else float(t.grad) == 3.0
+
+
 # ---------------------------------------------------------------- attention pieces
 
 @pytest.mark.parametrize("T,d", [(5, 64), (8192, 512)])
