@@ -35,7 +35,17 @@
 namespace rte {
 namespace {
 
-constexpr int kTP = 40;  // LDS pitch (bf16) of a transposed [R][32] tile: 80-byte rows
+// LDS pitch (bf16) of a transposed [R][32] tile: 72-byte rows.  Its reads (sv_ld_perm: 8 bytes per
+// lane from 32 consecutive rows) then start at 32 distinct even banks, so a wave's read covers the
+// 64 banks once (an 80-byte pitch maps rows r and r + 16 to the same banks).  Rows are 8-byte
+// aligned only: the tiles are written with 8-byte stores (sv_st16).
+constexpr int kTP = 36;
+
+// 16 bytes at an 8-byte aligned LDS address
+__device__ __forceinline__ void sv_st16(bf16* dst, uint4 v) {
+  *reinterpret_cast<uint2*>(dst) = make_uint2(v.x, v.y);
+  *reinterpret_cast<uint2*>(dst + 4) = make_uint2(v.z, v.w);
+}
 
 __device__ __forceinline__ f32x16_v sv_mfma(bf16x8_v a, bf16x8_v b, f32x16_v c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -132,7 +142,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       *reinterpret_cast<uint4*>(s_vu + row * P + col) = rv0_0;
       *reinterpret_cast<uint4*>(s_vg + row * P + col) = rv1_0;
       const int j = i >> 2, cj = (i & 3) * 8;
-      *reinterpret_cast<uint4*>(s_vdT + j * kTP + cj) = rv2_0;
+      sv_st16(s_vdT + j * kTP + cj, rv2_0);
     }
     if constexpr (NV > 1) {
       const int i = tid + 256 * 1;
@@ -140,7 +150,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
       *reinterpret_cast<uint4*>(s_vu + row * P + col) = rv0_1;
       *reinterpret_cast<uint4*>(s_vg + row * P + col) = rv1_1;
       const int j = i >> 2, cj = (i & 3) * 8;
-      *reinterpret_cast<uint4*>(s_vdT + j * kTP + cj) = rv2_1;
+      sv_st16(s_vdT + j * kTP + cj, rv2_1);
     }
     __syncthreads();
     if (c + 1 < c1) SVD_FWD_GLOAD(c + 1)  // in flight during this chunk's products
@@ -255,8 +265,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       *reinterpret_cast<uint4*>(s_vg + row * P + col) = rv1_0;
       *reinterpret_cast<uint4*>(s_vd + row * P + col) = rv2_0;
       const int k = i >> 2, ck = (i & 3) * 8;
-      *reinterpret_cast<uint4*>(s_vuT + k * kTP + ck) = rv3_0;
-      *reinterpret_cast<uint4*>(s_vgT + k * kTP + ck) = rv4_0;
+      sv_st16(s_vuT + k * kTP + ck, rv3_0);
+      sv_st16(s_vgT + k * kTP + ck, rv4_0);
     }
     if constexpr (NV > 1) {
       const int i = tid + 256 * 1;
@@ -265,8 +275,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       *reinterpret_cast<uint4*>(s_vg + row * P + col) = rv1_1;
       *reinterpret_cast<uint4*>(s_vd + row * P + col) = rv2_1;
       const int k = i >> 2, ck = (i & 3) * 8;
-      *reinterpret_cast<uint4*>(s_vuT + k * kTP + ck) = rv3_1;
-      *reinterpret_cast<uint4*>(s_vgT + k * kTP + ck) = rv4_1;
+      sv_st16(s_vuT + k * kTP + ck, rv3_1);
+      sv_st16(s_vgT + k * kTP + ck, rv4_1);
     }
     __syncthreads();
     if (c + 1 < c1) SVD_BWDX_GLOAD(c + 1)
@@ -409,9 +419,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       *reinterpret_cast<uint4*>(s_ag + row * P + col) = rv1_0;
       *reinterpret_cast<uint4*>(s_db + row * P + col) = rv2_0;
       const int k = i >> 2, ct = (i & 3) * 8;
-      *reinterpret_cast<uint4*>(s_auT + k * kTP + ct) = rv3_0;
-      *reinterpret_cast<uint4*>(s_agT + k * kTP + ct) = rv4_0;
-      *reinterpret_cast<uint4*>(s_dbT + k * kTP + ct) = rv5_0;
+      sv_st16(s_auT + k * kTP + ct, rv3_0);
+      sv_st16(s_agT + k * kTP + ct, rv4_0);
+      sv_st16(s_dbT + k * kTP + ct, rv5_0);
     }
     if constexpr (NV > 1) {
       const int i = tid + 256 * 1;
@@ -420,9 +430,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       *reinterpret_cast<uint4*>(s_ag + row * P + col) = rv1_1;
       *reinterpret_cast<uint4*>(s_db + row * P + col) = rv2_1;
       const int k = i >> 2, ct = (i & 3) * 8;
-      *reinterpret_cast<uint4*>(s_auT + k * kTP + ct) = rv3_1;
-      *reinterpret_cast<uint4*>(s_agT + k * kTP + ct) = rv4_1;
-      *reinterpret_cast<uint4*>(s_dbT + k * kTP + ct) = rv5_1;
+      sv_st16(s_auT + k * kTP + ct, rv3_1);
+      sv_st16(s_agT + k * kTP + ct, rv4_1);
+      sv_st16(s_dbT + k * kTP + ct, rv5_1);
     }
     __syncthreads();
     if (tt + 1 < t1) SVD_BWDW_GLOAD(tt + 1)
