@@ -304,9 +304,10 @@ int rte_svd_sparse_bwd(const void* dout, int T, int d, int top_k, const void* w_
 int rte_rmsnorm_fwd(const float* x, const float* w, int T, int d, float eps, void* out, float* rstd,
                     void* stream);
 size_t rte_rmsnorm_bwd_workspace_bytes(int T, int d);
-/* dy bf16; dx f32 (= dres + norm backward, dres optional); dw f32 [d] (accumulated if dw_accumulate). */
+/* dy bf16; dx f32 (= dres + norm backward, dres optional); dx_bf16 (optional) the same values in
+ * bf16; dw f32 [d] (accumulated if dw_accumulate). */
 int rte_rmsnorm_bwd(const void* dy, const float* x, const float* w, const float* rstd, const float* dres,
-                    int T, int d, float* dx, float* dw, int dw_accumulate, void* workspace,
+                    int T, int d, float* dx, void* dx_bf16, float* dw, int dw_accumulate, void* workspace,
                     size_t workspace_bytes, void* stream);
 
 /* ---- elementwise dispatch symbols in the caller's dtype ----

@@ -34,7 +34,7 @@ int rmsnorm_fwd(const float* x, const float* w, int T, int d, float eps, bf16* o
                 hipStream_t s);
 size_t rmsnorm_bwd_workspace_bytes(int T, int d);
 int rmsnorm_bwd(const bf16* dy, const float* x, const float* w, const float* rstd, const float* dres, int T,
-                int d, float* dx, float* dw, int dw_accumulate, void* ws, size_t ws_bytes, hipStream_t s);
+                int d, float* dx, bf16* dx_bf16, float* dw, int dw_accumulate, void* ws, size_t ws_bytes, hipStream_t s);
 int rope_bwd_pack(const bf16* dq, const int64_t* sq, const bf16* dk, const int64_t* sk, const bf16* dv,
                   const int64_t* sv, const float* cos_t, const float* sin_t, int B, int H, int S, int hd,
                   bf16* dqkv, hipStream_t s);
@@ -932,10 +932,10 @@ int rte_rmsnorm_fwd(const float* x, const float* w, int T, int d, float eps, voi
 size_t rte_rmsnorm_bwd_workspace_bytes(int T, int d) { return rmsnorm_bwd_workspace_bytes(T, d); }
 
 int rte_rmsnorm_bwd(const void* dy, const float* x, const float* w, const float* rstd, const float* dres, int T,
-                    int d, float* dx, float* dw, int dw_accumulate, void* workspace, size_t workspace_bytes,
-                    void* stream) {
-  return rmsnorm_bwd(B16(dy), x, w, rstd, dres, T, d, dx, dw, dw_accumulate, workspace, workspace_bytes,
-                     S(stream));
+                    int d, float* dx, void* dx_bf16, float* dw, int dw_accumulate, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  return rmsnorm_bwd(B16(dy), x, w, rstd, dres, T, d, dx, B16(dx_bf16), dw, dw_accumulate, workspace,
+                     workspace_bytes, S(stream));
 }
 
 int rte_ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets, float* loss, float* lse,

@@ -72,7 +72,8 @@ __global__ void __launch_bounds__(256) rmsnorm_fwd_kernel(const float* __restric
   }
 }
 
-// dx = rstd * (w*dy) - x * rstd^3 * mean(w*dy*x)  (+ dres);   partial dw per row block.
+// dx = rstd * (w*dy) - x * rstd^3 * mean(w*dy*x)  (+ dres);   partial dw per row block;
+// optionally also dx in bf16 (the operand of the GEMMs that consume it).
 // One wave per row, 8 columns per lane per step (16-byte dy loads, 32-byte x loads);
 // each lane keeps its columns' dw partial in registers across the block's rows, so
 // dw needs no atomics: per-block partials are summed in block order by colsum_kernel.
@@ -118,7 +119,7 @@ template <int NCH>
 __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
     const bf16* __restrict__ dy, const float* __restrict__ x, const float* __restrict__ w,
     const float* __restrict__ rstd, const float* __restrict__ dres, int T, int d,
-    float* __restrict__ dx, float* __restrict__ dw_part, int rpb) {
+    float* __restrict__ dx, bf16* __restrict__ dx_bf16, float* __restrict__ dw_part, int rpb) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   extern __shared__ float sdw[];  // [4][d]
   const int nchunk = d / 8;
@@ -164,6 +165,14 @@ __global__ void __launch_bounds__(256) rmsnorm_bwd_kernel(
         acc[c][i] += g[c][i] * xv[c][i] * rs;
       }
       store8_f32(dx + (int64_t)t * d + col, o);
+      if (dx_bf16) {
+        uint4 ob;
+        ob.x = pack_bf2(o[0], o[1]);
+        ob.y = pack_bf2(o[2], o[3]);
+        ob.z = pack_bf2(o[4], o[5]);
+        ob.w = pack_bf2(o[6], o[7]);
+        *reinterpret_cast<uint4*>(dx_bf16 + (int64_t)t * d + col) = ob;
+      }
     }
   }
 #pragma unroll
@@ -182,8 +191,18 @@ __global__ void __launch_bounds__(256) colsum_kernel(const float* __restrict__ p
   const int l = threadIdx.x & 7, phase = threadIdx.x >> 3;
   const int col = blockIdx.x * 8 + l;
   float s = 0.0f;
-  if (col < d)
-    for (int r = phase; r < nrows; r += 32) s += part[(int64_t)r * d + col];
+  if (col < d) {
+    // eight rows' loads in flight at a time, added in row order
+    int r = phase;
+    for (; r + 7 * 32 < nrows; r += 8 * 32) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) v[u] = part[(int64_t)(r + 32 * u) * d + col];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; r < nrows; r += 32) s += part[(int64_t)r * d + col];
+  }
   sh[phase][l] = s;
   __syncthreads();
   if (threadIdx.x < 8 && col < d) {
@@ -348,7 +367,8 @@ size_t rmsnorm_bwd_workspace_bytes(int T, int d) {
 }
 
 int rmsnorm_bwd(const bf16* dy, const float* x, const float* w, const float* rstd, const float* dres, int T,
-                int d, float* dx, float* dw, int dw_accumulate, void* ws, size_t ws_bytes, hipStream_t s) {
+                int d, float* dx, bf16* dx_bf16, float* dw, int dw_accumulate, void* ws, size_t ws_bytes,
+                hipStream_t s) {
   RTE_REQUIRE(ws_bytes >= rmsnorm_bwd_workspace_bytes(T, d), "rmsnorm_bwd: workspace too small");
   RTE_REQUIRE(d % 8 == 0 && d <= 64 * 8 * kNormMaxChunks, "rmsnorm_bwd: d must be a multiple of 8 and <= 2048");
   const int rpb = norm_rows_per_block(T, d);
@@ -359,15 +379,15 @@ int rmsnorm_bwd(const bf16* dy, const float* x, const float* w, const float* rst
     switch (norm_chunks(d)) {
       case 1:
         hipLaunchKernelGGL(rmsnorm_bwd_kernel<1>, dim3(nblk), dim3(256), lds, s, dy, x, w, rstd, dres, T, d, dx,
-                           part, rpb);
+                           dx_bf16, part, rpb);
         break;
       case 2:
         hipLaunchKernelGGL(rmsnorm_bwd_kernel<2>, dim3(nblk), dim3(256), lds, s, dy, x, w, rstd, dres, T, d, dx,
-                           part, rpb);
+                           dx_bf16, part, rpb);
         break;
       default:
         hipLaunchKernelGGL(rmsnorm_bwd_kernel<kNormMaxChunks>, dim3(nblk), dim3(256), lds, s, dy, x, w, rstd, dres,
-                           T, d, dx, part, rpb);
+                           T, d, dx, dx_bf16, part, rpb);
     }
     RTE_TRY(check_launch("rmsnorm_bwd"));
   }

@@ -83,7 +83,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "rte_svd_sparse_bwd": (_I, [_P, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P]),
     "rte_rmsnorm_fwd": (_I, [_P, _P, _I, _I, _F, _P, _P, _P]),
     "rte_rmsnorm_bwd_workspace_bytes": (_SZ, [_I, _I]),
-    "rte_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _P, _I, _P, _SZ, _P]),
+    "rte_rmsnorm_bwd": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _P, _P, _I, _P, _SZ, _P]),
     "rte_fused_rmsnorm_fwd": (_I, [_P, _P, _I, _P, _I, _I, _F, _P, _P, _I, _P, _P]),
     "rte_fused_rmsnorm_bwd_workspace_bytes": (_SZ, [_I, _I]),
     "rte_fused_rmsnorm_bwd": (_I, [_P, _I, _P, _P, _I, _P, _P, _I, _I, _P, _P, _P, _SZ, _P]),

@@ -200,12 +200,34 @@ def _cache_key(x: torch.Tensor):
     return (x.data_ptr(), tuple(x.shape), tuple(x.stride()), x._version, _lib.stream_ptr())
 
 
+def _attach_bf16(x: torch.Tensor, xb: torch.Tensor) -> None:
+    """Remember xb, the bf16 values of fp32 x written by the same kernel on the current stream,
+    so cast_bf16 of x (or of a whole contiguous view of it) needs no cast launch."""
+    x._rte_bf16 = (xb, x._version, _lib.stream_ptr())
+
+
+def _bf16_companion(x: torch.Tensor):
+    base = x._base if x._base is not None else x
+    comp = getattr(base, "_rte_bf16", None)
+    if comp is None:
+        return None
+    xb, version, stream = comp
+    if (base._version != version or stream != _lib.stream_ptr() or not x.is_contiguous()
+            or x.data_ptr() != base.data_ptr() or x.numel() != xb.numel()):
+        return None
+    return xb.view(x.shape)
+
+
 def cast_bf16(x: torch.Tensor) -> torch.Tensor:
     """fp32 -> bf16 (round to nearest even) with the HIP cast kernel; parameters hit the
-    per-step cache while one is open (bf16_cache_begin)."""
+    per-step cache while one is open (bf16_cache_begin), and tensors whose producing kernel also
+    wrote their bf16 values (_attach_bf16) return those."""
     if x.dtype == BF16:
         return x.contiguous()
     _lib.require_device_tensors("cast_bf16", x)
+    comp = _bf16_companion(x)
+    if comp is not None:
+        return comp
     key = _cache_key(x) if _BF16_CACHE_ON[0] else None
     if key is not None:
         hit = _BF16_CACHE.get(key)
@@ -322,8 +344,10 @@ class RMSNormFn(torch.autograd.Function):
         dw = torch.empty((d,), dtype=F32, device=x2.device)
         nbytes = _lib.load().rte_rmsnorm_bwd_workspace_bytes(T, d)
         ws = torch.empty((max(1, nbytes // 4),), dtype=F32, device=x2.device)
-        call("rte_rmsnorm_bwd", ptr(dy), ptr(x2), ptr(w32), ptr(rstd), None, T, d, ptr(dx), ptr(dw), 0,
+        dxb = torch.empty((T, d), dtype=BF16, device=x2.device)
+        call("rte_rmsnorm_bwd", ptr(dy), ptr(x2), ptr(w32), ptr(rstd), None, T, d, ptr(dx), ptr(dxb), ptr(dw), 0,
              ptr(ws), nbytes, _s())
+        _attach_bf16(dx, dxb)  # the next layer's GEMMs read dx in bf16
         return dx.view(ctx.shape), dw.to(ctx.w_dtype), None
 
 
@@ -367,8 +391,11 @@ class RMSNormResidFn(torch.autograd.Function):
         dw = torch.empty((d,), dtype=F32, device=x2.device)
         nbytes = _lib.load().rte_rmsnorm_bwd_workspace_bytes(T, d)
         ws = torch.empty((max(1, nbytes // 4),), dtype=F32, device=x2.device)
-        call("rte_rmsnorm_bwd", ptr(dy), ptr(x2), ptr(w32), ptr(rstd), ptr(r), T, d, ptr(dx), ptr(dw), 0,
+        dxb = torch.empty((T, d), dtype=BF16, device=x2.device) if ctx.x_dtype == F32 else None
+        call("rte_rmsnorm_bwd", ptr(dy), ptr(x2), ptr(w32), ptr(rstd), ptr(r), T, d, ptr(dx), ptr(dxb), ptr(dw), 0,
              ptr(ws), nbytes, _s())
+        if dxb is not None:
+            _attach_bf16(dx, dxb)  # the previous layer's GEMMs read dx in bf16
         return dx.view(ctx.shape).to(ctx.x_dtype), dw.to(ctx.w_dtype), None
 
 

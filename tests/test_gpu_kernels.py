@@ -507,6 +507,44 @@ def test_grouped_swiglu_fused_matches_two_gemm(d):
         np.testing.assert_allclose(a, b, rtol=2e-2, atol=2e-2 * float(np.abs(b).max()), err_msg=name)
 
 
+def test_rmsnorm_bwd_bf16_companion():
+    """The norm backward also writes dx in bf16: cast_bf16 of dx (or of a whole view of it)
+    returns those values, bit for bit the cast kernel's, without a cast; after an in-place change
+    of dx, or for a partial view, it casts again."""
+    H = _ops()
+    rng = np.random.default_rng(21)
+    T, d = 1000, 256
+    x = torch.from_numpy(rng.standard_normal((T, d)).astype(np.float32)).to(DEV).requires_grad_()
+    w = torch.from_numpy(rng.random(d).astype(np.float32) + 0.5).to(DEV)
+    seen = {}
+
+    def grab(g):
+        seen["g"] = g
+        return g
+
+    x.register_hook(grab)
+    y = H.rmsnorm(x, w)
+    y.float().mul(torch.from_numpy(rng.standard_normal((T, d)).astype(np.float32)).to(DEV)).sum().backward()
+    torch.cuda.synchronize()
+    g = seen["g"]
+    comp = H.cast_bf16(g)
+    ref = torch.empty(T, d, dtype=torch.bfloat16, device=DEV)
+    from rte_amd import _lib
+
+    _lib.call("rte_cast_f32_bf16", g.contiguous().data_ptr(), g.numel(), ref.data_ptr(), None)
+    torch.cuda.synchronize()
+    base = g._base if g._base is not None else g
+    assert getattr(base, "_rte_bf16", None) is not None
+    assert comp.data_ptr() == base._rte_bf16[0].data_ptr()  # the companion, no new cast
+    assert torch.equal(comp, ref)
+    assert H.cast_bf16(g[: T // 2]).data_ptr() != comp.data_ptr()  # a partial view casts
+    g.mul_(2.0)
+    again = H.cast_bf16(g)
+    torch.cuda.synchronize()
+    assert again.data_ptr() != comp.data_ptr()
+    assert torch.equal(again.float(), (ref.float() * 2.0).to(torch.bfloat16).float())
+
+
 def test_loss_sum_matches_torch():
     """rte_loss_sum / _bwd: coef * sum(x) + sum of scalar terms, gradient coef for every row of x
     and 1 for every term, against torch in float64 (30 terms, one not requiring a gradient)."""
