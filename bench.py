@@ -389,7 +389,7 @@ def roofline_rows(B: int, S: int) -> list[dict]:
 def _pmc_per_call(csv_dir: Path, counter: str, calls: int, only=None):
     """Sum of `counter` over the profiled calls' dispatches / calls, in bytes (KiB counters), read
     from rocprofv3's counter_collection.csv; `only` filters kernel names, and kernels dispatched
-    fewer than `calls` times (the candidates' set-up work) are left out."""
+    fewer than `calls` times (the candidates' set-up work) are left out.  `only` takes the CSV row."""
     import csv
     from collections import defaultdict
 
@@ -402,7 +402,7 @@ def _pmc_per_call(csv_dir: Path, counter: str, calls: int, only=None):
             if r.get("Counter_Name") != counter:
                 continue
             k = r.get("Kernel_Name", "")
-            if only is not None and not only(k):
+            if only is not None and not only(r):
                 continue
             tot[k] += float(r["Counter_Value"])
             n[k] += 1
@@ -410,6 +410,12 @@ def _pmc_per_call(csv_dir: Path, counter: str, calls: int, only=None):
 
 
 COPY_ELEMS = 64 << 20  # calibration: rte_cast_f32_bf16 over 64 Mi elements (reads 256 MiB, writes 128 MiB)
+
+
+def _is_copy(r: dict) -> bool:
+    """A counter row of the calibration copy: the cast kernel at the calibration size (its launch
+    runs one thread per 4 elements), told apart from casts the profiled operation makes itself."""
+    return "cast_f32_bf16" in r.get("Kernel_Name", "") and int(r.get("Grid_Size", "0") or 0) == COPY_ELEMS // 4
 
 
 def measure_traffic(name: str, B: int, S: int, iters: int = 20, timeout_s: int = 120) -> dict:
@@ -435,8 +441,8 @@ def measure_traffic(name: str, B: int, S: int, iters: int = 20, timeout_s: int =
             r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s, cwd=str(ROOT))
             if r.returncode != 0:
                 return {"bytes": None, "note": f"rocprofv3 --pmc {counter} exited {r.returncode}"}
-            op = _pmc_per_call(d, counter, iters, lambda k: "cast_f32_bf16" not in k)
-            cp = _pmc_per_call(d, counter, iters, lambda k: "cast_f32_bf16" in k)
+            op = _pmc_per_call(d, counter, iters, lambda r: not _is_copy(r))
+            cp = _pmc_per_call(d, counter, iters, _is_copy)
             known = COPY_ELEMS * (4.0 if counter == "FETCH_SIZE" else 2.0)
             if not op or not cp:
                 return {"bytes": None, "note": f"no {counter} rows in the rocprofv3 output"}
@@ -550,12 +556,13 @@ def pmc_summary(csv_dir: str, calls: int) -> str:
     if not files:
         raise FileNotFoundError(f"no counter_collection.csv under {csv_dir}")
     tot, disp = defaultdict(float), defaultdict(set)
+    copy_name = "calibration copy (cast_f32_bf16, 64 Mi elements)"
     for f in files:
         with open(f) as fh:
             for r in csv.DictReader(fh):
-                key = (r["Kernel_Name"], r["Counter_Name"])
-                tot[key] += float(r["Counter_Value"])
-                disp[r["Kernel_Name"]].add((str(f), r.get("Dispatch_Id", r.get("Correlation_Id", ""))))
+                name = copy_name if _is_copy(r) else r["Kernel_Name"]
+                tot[(name, r["Counter_Name"])] += float(r["Counter_Value"])
+                disp[name].add((str(f), r.get("Dispatch_Id", r.get("Correlation_Id", ""))))
     out = [f"Per call (raw counters: sums over a kernel's dispatches / {calls} calls; derived ratios: mean per "
            "dispatch; kernels dispatched less than once per call, i.e. set-up work, are left out):", "",
            "| kernel | dispatches / call | counter | value / call |", "|---|---:|---|---:|"]
@@ -570,8 +577,8 @@ def pmc_summary(csv_dir: str, calls: int) -> str:
         keys = [k for (k, cc) in tot if cc == c and len(disp[k]) >= calls]
         if not keys:
             continue
-        op = sum(tot[(k, c)] for k in keys if "cast_f32_bf16" not in k) * 1024.0 / calls
-        cp = sum(tot[(k, c)] for k in keys if "cast_f32_bf16" in k) * 1024.0 / calls
+        op = sum(tot[(k, c)] for k in keys if k != copy_name) * 1024.0 / calls
+        cp = sum(tot[(k, c)] for k in keys if k == copy_name) * 1024.0 / calls
         line = f"{c}: operation kernels {op:.4g} B per call (counter KiB x 1024)"
         if cp:
             scale = COPY_ELEMS * per_elem / cp

@@ -259,6 +259,23 @@ def test_bench_trace_and_pmc_summaries(tmp_path):
     assert "| `rte::k` | 1 | FETCH_SIZE | 20 |" in rep
     assert "| `rte::k` | 1 | WRITE_SIZE | 5 |" in rep
 
+    # the calibration copy is the cast at the calibration grid; a smaller cast the operation makes
+    # itself counts as operation traffic
+    cast = "rte::(anonymous namespace)::cast_f32_bf16_kernel(float const*, long, unsigned short*)"
+    g_copy = bench.COPY_ELEMS // 4
+    d2 = tmp_path / "pmc2" / "run"
+    d2.mkdir(parents=True)
+    rows = ["Dispatch_Id,Grid_Size,Kernel_Name,Counter_Name,Counter_Value"]
+    for i in range(2):
+        rows += [f'{3 * i + 1},256,"rte::k(int)",FETCH_SIZE,10', f'{3 * i + 2},4096,"{cast}",FETCH_SIZE,6',
+                 f'{3 * i + 3},{g_copy},"{cast}",FETCH_SIZE,{bench.COPY_ELEMS * 2 // 1024}']
+    (d2 / "p_counter_collection.csv").write_text("\n".join(rows) + "\n")
+    rep = bench.pmc_summary(str(tmp_path / "pmc2"), calls=2)
+    assert "scale 2.0000" in rep
+    assert "operation kernels 1.638e+04 B per call" in rep          # (10 + 6) KiB
+    per = bench._pmc_per_call(tmp_path / "pmc2", "FETCH_SIZE", 2, lambda r: not bench._is_copy(r))
+    assert per == 16 * 1024.0
+
 
 def test_bf16_prefetch_tables():
     """The one-launch weight-cast plan: contiguous views cast flat, 2-D transposed views by
