@@ -28,6 +28,36 @@ class AuditResult:
     metrics: dict[str, torch.Tensor]
 
 
+def make_main_aliases(*modules) -> dict:
+    """The views main_stream_aliases installs, made now on the current stream: the autograd nodes
+    of views made early run late in the backward (the engine runs later-made nodes first), so a
+    launch whose compute is issued later can still join its parameter gradients at the end."""
+    alias: dict[int, torch.Tensor] = {}
+    if torch.is_grad_enabled():
+        for mod in modules:
+            for p in mod.parameters():
+                if p.requires_grad and id(p) not in alias:
+                    alias[id(p)] = p.view_as(p)
+    return alias
+
+
+@contextmanager
+def _aliases_installed(alias: dict, *modules):
+    swaps = []
+    for mod in modules:
+        for m in mod.modules():
+            for name, p in list(m._parameters.items()):
+                if p is None or id(p) not in alias:
+                    continue
+                m._parameters[name] = alias[id(p)]
+                swaps.append((m, name, p))
+    try:
+        yield
+    finally:
+        for m, name, p in swaps:
+            m._parameters[name] = p
+
+
 @contextmanager
 def main_stream_aliases(*modules):
     """Inside the block every trainable parameter of `modules` reads as a view of itself made on
@@ -166,13 +196,18 @@ class AuditEngine:
         return streams[key]
 
     def begin(self, model: RecursiveModel, tokens, targets, h0, route, *, seed: int,
-              chosen: torch.Tensor | None = None, defer_coda: bool = False) -> AuditLaunch | None:
+              chosen: torch.Tensor | None = None, defer_coda: bool = False,
+              ready: torch.cuda.Event | None = None, aliases: dict | None = None) -> AuditLaunch | None:
         """Start the fixed-count audit's exact replay and the macro consistency loss as soon as h0
         and the routing decisions exist: on their own streams (side_streams), so they and their
         backward can run beside the hot path, else in order on the caller's stream.  defer_coda:
         the replay runs its recursive passes only and hands its coda and head to the hot path's
-        coda call (launch.coda_extra).  Returns None when nothing can start early (Bernoulli
-        sampler, no device)."""
+        coda call (launch.coda_extra).  ready / aliases (issued later than routing): the side
+        streams wait for this event, recorded on the main stream when h0 and the routes were
+        made, instead of the main stream's current work, and the parameters read through these
+        views (make_main_aliases at the same point); the main-stream preparation the side streams
+        read (prepare_late: the audited rows, the operator's weight copies) must precede that
+        event.  Returns None when nothing can start early (Bernoulli sampler, no device)."""
         fixed = self.config.audit_fixed_count_per_batch
         if fixed is None or h0.device.type != "cuda":
             return None
@@ -182,13 +217,16 @@ class AuditEngine:
         launch = AuditLaunch(None, None, None, [])
         if k > 0:
             if chosen is None:
+                if ready is not None:
+                    raise ValueError("begin: a late launch takes the audited rows from prepare_late")
                 chosen = self.fixed_count_index(n, k, seed, h0.device)
             side = self._side_stream(h0.device, 0)
             if side != main:
-                side.wait_stream(main)
+                side.wait_event(ready) if ready is not None else side.wait_stream(main)
             grad_corr = self.config.audit_mode == "gradient_corrected"
             with (nullcontext() if grad_corr else torch.no_grad()), \
-                    (main_stream_aliases(model) if side != main else nullcontext()):
+                    (nullcontext() if side == main else
+                     _aliases_installed(aliases, model) if aliases is not None else main_stream_aliases(model)):
                 with torch.cuda.stream(side):
                     if defer_coda:
                         core = model.forward_exact_subset_core(chosen, reuse_router_decisions=route, cached_h0=h0)
@@ -201,18 +239,39 @@ class AuditEngine:
                 launch.streams.append(side)
         if self.config.lambda_cons != 0.0:
             side = self._side_stream(h0.device, 1)
-            mac = model.macro
-            if (getattr(mac, "v", None) is not None and mac._fused_bounded()
-                    and hip_ops.macro_fused_supported(mac.v, mac.u)):
-                # one bf16 copy of the operator tables per step, shared with the hot path
-                hip_ops.macro_fused_weights_share(mac.v, mac.u, side)
+            if ready is None:
+                self._share_macro_weights(model, side)
             if side != main:
-                side.wait_stream(main)
-            with (main_stream_aliases(model.macro) if side != main else nullcontext()), torch.cuda.stream(side):
+                side.wait_event(ready) if ready is not None else side.wait_stream(main)
+            with (nullcontext() if side == main else
+                  _aliases_installed(aliases, model.macro) if aliases is not None
+                  else main_stream_aliases(model.macro)), torch.cuda.stream(side):
                 launch.cons = model.macro.consistency_loss(h0, h0, route.recipe_id)
             if side != main:
                 launch.streams.append(side)
         return launch
+
+    def _share_macro_weights(self, model: RecursiveModel, side) -> None:
+        mac = model.macro
+        if (getattr(mac, "v", None) is not None and mac._fused_bounded()
+                and hip_ops.macro_fused_supported(mac.v, mac.u)):
+            # one bf16 copy of the operator tables per step, shared with the hot path
+            hip_ops.macro_fused_weights_share(mac.v, mac.u, side)
+
+    def prepare_late(self, model: RecursiveModel, h0, *, seed: int, chosen: torch.Tensor | None = None):
+        """The main-stream work a late begin() (ready given) reads on its side streams, issued
+        before the ready event is recorded: the fixed-count audited rows (returned; None when
+        nothing is audited) and the operator's shared weight copies."""
+        fixed = self.config.audit_fixed_count_per_batch
+        if fixed is None or h0.device.type != "cuda":
+            return chosen
+        n = h0.shape[0]
+        k = min(int(fixed), n)
+        if k > 0 and chosen is None:
+            chosen = self.fixed_count_index(n, k, seed, h0.device)
+        if self.config.lambda_cons != 0.0:
+            self._share_macro_weights(model, self._side_stream(h0.device, 1))
+        return chosen
 
     def _fixed_count_sample(self, meta: ModelMeta, seed: int, chosen: torch.Tensor | None):
         """compute_audit_prob followed by the fixed-count branch of sample_mask_with_prob and the

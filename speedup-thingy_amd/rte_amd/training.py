@@ -19,7 +19,7 @@ from typing import Any
 
 import torch
 
-from rte_amd.audit import AuditEngine, AuditResult
+from rte_amd.audit import AuditEngine, AuditResult, make_main_aliases
 from rte_amd.config import ExperimentConfig, TrainingConfig
 from rte_amd.kernels import hip_ops, optimized
 from rte_amd.metrics import hot_budget
@@ -137,6 +137,11 @@ class TrainEngine:
         # full-vocabulary head only): one set of launches for both.  Not in captured steps with
         # side streams: there the replay's own coda overlaps the hot path instead.
         self.replay_coda_shared = True
+        # with side streams and the replay's own coda: issue the replay and the consistency loss
+        # after the hot path's forward (their streams still wait only for the routing point), so
+        # their autograd nodes are newer than the hot path's and the backward issues their work
+        # first, beside the hot path's backward rather than after it
+        self.side_launch_late = True
         self._capturing = False
         self._bf16 = hip_ops.Bf16Prefetch(enabled=self.device.type == "cuda" and tr.precision == "bf16")
         self._graph_enabled = False
@@ -329,9 +334,17 @@ class TrainEngine:
         launched = []
         audit_seed = tr.seed + 10_000 + self.global_step
 
+        late = []
+
         def on_routed(h0, route):
             # the audit replay and the consistency loss need only h0 and the routing decisions
             share = self.replay_coda_shared and not shortlist and not (self._capturing and self.graph_side_streams)
+            if self.side_launch_late and not share:
+                rows = self.audit_engine.prepare_late(m, h0, seed=audit_seed, chosen=chosen)
+                ready = torch.cuda.Event()
+                ready.record(torch.cuda.current_stream(h0.device))
+                late.append((h0, route, ready, make_main_aliases(m), rows))
+                return
             launched.append(self.audit_engine.begin(m, tokens, targets, h0, route, seed=audit_seed, chosen=chosen,
                                                     defer_coda=share))
 
@@ -343,6 +356,9 @@ class TrainEngine:
                                   shortlist=shortlist, seed=tr.seed + self.global_step, fixed_recipe=tr.fixed_recipe,
                                   fixed_depth=tr.fixed_depth, shortlist_random_negs=random_negs,
                                   on_routed=on_routed if self.audit_streams else None, coda_extra=coda_extra)
+            for h0, route, ready, aliases, rows in late:
+                launched.append(self.audit_engine.begin(m, tokens, targets, h0, route, seed=audit_seed, chosen=rows,
+                                                        ready=ready, aliases=aliases))
             audit = self.audit_engine.correction(m, tokens, targets, hot, seed=audit_seed, chosen=chosen,
                                                  launch=launched[0] if launched else None)
             aux = self._router_aux(hot)

@@ -234,6 +234,38 @@ def test_cfg3_step_eager_vs_captured(side_streams):
     a.optimizer.zero_grad(set_to_none=True)
 
 
+def test_cfg3_side_launch_late_vs_early():
+    """Issuing the audit replay and the consistency loss after the hot forward (side_launch_late,
+    their streams waiting on an event from the routing point) against issuing them at routing:
+    the same audited rows (the fixed-count sampler's seeded permutation, drawn on the main stream
+    before that event) and the same losses, step by step, with the replay's own coda on side
+    streams in eager steps."""
+    import bench
+
+    from rte_amd.audit import AuditEngine
+
+    cfg = bench.cfg3_config()
+    late, early = _engine_from(cfg), _engine_from(cfg)
+    for e, flag in ((late, True), (early, False)):
+        e.replay_coda_shared = False
+        e.side_launch_late = flag
+    gen = torch.Generator().manual_seed(cfg.training.seed)
+    batches = [bench.zipf_batch(gen, cfg.model.vocab_size, 128, 64, DEV) for _ in range(3)]
+    k = int(cfg.training.audit_fixed_count_per_batch)
+    for step, batch in enumerate(batches):
+        print(f"cfg3 late/early step {step}", flush=True)
+        want = torch.zeros(128, dtype=torch.bool, device=DEV)
+        want[AuditEngine.fixed_count_index(128, k, cfg.training.seed + 10_000 + late.global_step, DEV)] = True
+        ra, rb = late.train_step(batch), early.train_step(batch)
+        torch.cuda.synchronize()
+        assert torch.equal(ra.audit.audit_mask.reshape(-1), want), step
+        assert torch.equal(rb.audit.audit_mask.reshape(-1), want), step
+        la, lb = float(ra.loss), float(rb.loss)
+        assert math.isfinite(la) and abs(la - lb) <= 1e-6 * max(abs(la), 1.0), (step, la, lb)
+    for (na, pa), (_, pb) in zip(late.recursive_model.named_parameters(), early.recursive_model.named_parameters()):
+        assert torch.allclose(pa, pb, rtol=1e-5, atol=1e-6), na
+
+
 def test_cfg5_shortlist_step():
     """the scaled recursive_macro_shortlist step (d1024, 16 heads, depth 8,
     pool 256 x 64 top-16, V8192 shortlist, B32 x S512): finite losses, parameters change, the
