@@ -28,16 +28,49 @@ class AuditResult:
     metrics: dict[str, torch.Tensor]
 
 
-def make_main_aliases(*modules) -> dict:
+class GradSink:
+    """Parameter gradients of side-stream work, kept apart from the engine's accumulation and
+    added to the parameters' .grad in one multi-tensor launch after the backward (flush()),
+    instead of one add per parameter where the side streams join the main stream."""
+
+    def __init__(self):
+        self.entries: list = []
+
+    def flush(self) -> None:
+        have = [(p, g) for p, g in self.entries if p.grad is not None]
+        if have:
+            torch._foreach_add_([p.grad for p, _ in have], [g for _, g in have])
+        for p, g in self.entries:
+            if p.grad is None:
+                p.grad = g
+        self.entries.clear()
+
+
+class _SinkView(torch.autograd.Function):
+    """A view of parameter p whose gradient goes to a GradSink instead of p's accumulator."""
+
+    @staticmethod
+    def forward(ctx, p, sink):
+        ctx.p, ctx.sink = p, sink
+        return p.view_as(p)
+
+    @staticmethod
+    def backward(ctx, g):
+        ctx.sink.entries.append((ctx.p, g))
+        return None, None
+
+
+def make_main_aliases(*modules, sink: GradSink | None = None) -> dict:
     """The views main_stream_aliases installs, made now on the current stream: the autograd nodes
     of views made early run late in the backward (the engine runs later-made nodes first), so a
-    launch whose compute is issued later can still join its parameter gradients at the end."""
+    launch whose compute is issued later can still join its parameter gradients at the end.
+    With a sink the views' gradients go to it (GradSink.flush adds them after the backward)."""
     alias: dict[int, torch.Tensor] = {}
     if torch.is_grad_enabled():
         for mod in modules:
             for p in mod.parameters():
                 if p.requires_grad and id(p) not in alias:
-                    alias[id(p)] = p.view_as(p)
+                    alias[id(p)] = _SinkView.apply(p, sink) if sink is not None else p.view_as(p)
     return alias
 
 

@@ -19,7 +19,7 @@ from typing import Any
 
 import torch
 
-from rte_amd.audit import AuditEngine, AuditResult, make_main_aliases
+from rte_amd.audit import AuditEngine, AuditResult, GradSink, make_main_aliases
 from rte_amd.config import ExperimentConfig, TrainingConfig
 from rte_amd.kernels import hip_ops, optimized
 from rte_amd.metrics import hot_budget
@@ -142,6 +142,10 @@ class TrainEngine:
         # their autograd nodes are newer than the hot path's and the backward issues their work
         # first, beside the hot path's backward rather than after it
         self.side_launch_late = True
+        # late side work: its parameter gradients are added in one multi-tensor launch after the
+        # backward instead of one add per parameter where the streams join
+        self.side_grad_sink = True
+        self._grad_sink = None
         self._capturing = False
         self._bf16 = hip_ops.Bf16Prefetch(enabled=self.device.type == "cuda" and tr.precision == "bf16")
         self._graph_enabled = False
@@ -250,11 +254,13 @@ class TrainEngine:
         tr = self.config.training
         self.last_grad_metrics = {}
         if check_finite and not bool(torch.isfinite(loss.detach()).item()):
+            self._grad_sink = None
             self.optimizer.zero_grad(set_to_none=True)
             self.global_micro_step += 1
             self.last_grad_metrics = {"skipped_nonfinite_loss": 1.0}
             return False
         (loss / tr.grad_accum_steps).backward()
+        self._flush_grad_sink()
         self.global_micro_step += 1
         step = self.global_micro_step % tr.grad_accum_steps == 0
         fused = isinstance(self.optimizer, FusedAdamW)
@@ -272,6 +278,12 @@ class TrainEngine:
             self.optimizer.zero_grad(set_to_none=True)
             self.global_step += 1
         return step
+
+    def _flush_grad_sink(self) -> None:
+        """Add the side work's parameter gradients (kept by the step's GradSink) to .grad."""
+        sink, self._grad_sink = self._grad_sink, None
+        if sink is not None:
+            sink.flush()
 
     def _move(self, batch):
         return batch[0].to(self.device, non_blocking=True), batch[1].to(self.device, non_blocking=True)
@@ -328,7 +340,9 @@ class TrainEngine:
 
     def _macro_loss(self, tokens, targets, *, shortlist: bool, chosen=None, random_negs=None):
         """Forward of the recursive_macro step (rte/training.py:1336-1385): hot path, audit
-        correction, router aux; loss = corrected CE / S + macro aux + router aux."""
+        correction, router aux; loss = corrected CE / S + macro aux + router aux.  Side work
+        issued late keeps its parameter gradients in the step's GradSink: callers running the
+        backward themselves call _flush_grad_sink() after it."""
         tr = self.config.training
         m = self.recursive_model
         launched = []
@@ -343,7 +357,8 @@ class TrainEngine:
                 rows = self.audit_engine.prepare_late(m, h0, seed=audit_seed, chosen=chosen)
                 ready = torch.cuda.Event()
                 ready.record(torch.cuda.current_stream(h0.device))
-                late.append((h0, route, ready, make_main_aliases(m), rows))
+                sink = self._grad_sink = GradSink() if self.side_grad_sink else None
+                late.append((h0, route, ready, make_main_aliases(m, sink=sink), rows))
                 return
             launched.append(self.audit_engine.begin(m, tokens, targets, h0, route, seed=audit_seed, chosen=chosen,
                                                     defer_coda=share))
@@ -527,6 +542,7 @@ class TrainEngine:
         else:
             bad, ok = torch.zeros((), device=loss.device), torch.ones((), device=loss.device)
         loss.backward()
+        self._flush_grad_sink()
         self._bf16.end()  # parameters change below
         if isinstance(self.optimizer, FusedAdamW):
             # clipping, update (skipped on a non-finite loss) and metrics in three launches

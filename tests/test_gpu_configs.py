@@ -225,6 +225,7 @@ def test_cfg3_step_eager_vs_captured(side_streams):
     tok, tgt = batches[0]
     loss, *_ = a._macro_loss(tok, tgt, shortlist=False)
     loss.backward()
+    a._flush_grad_sink()
     n_grads = 0
     for n_, p in a.recursive_model.named_parameters():
         if p.grad is not None:
@@ -312,6 +313,7 @@ def test_cfg3_side_stream_audit_gradients_match_main_stream():
         eng._bf16.begin()
         loss, *_ = eng._macro_loss(tok, tgt, shortlist=False)
         loss.backward()
+        eng._flush_grad_sink()
         eng._bf16.end()
         torch.cuda.synchronize()
         grads.append({n_: p.grad.detach().clone() for n_, p in eng.recursive_model.named_parameters()

@@ -73,6 +73,7 @@ def _run(cfg, B, S, seed, shared_coda=True):
     eng._bf16.begin()
     loss, hot, audit, aux, scale = eng._macro_loss(tok, tgt, shortlist=False)
     loss.backward()
+    eng._flush_grad_sink()  # the side work's parameter gradients (late launch) into .grad
     eng._bf16.end()
     torch.cuda.synchronize()
     for h in handles:
