@@ -701,13 +701,7 @@ def main(argv=None) -> int:
     ap.add_argument("--pmc-summary", default=None, metavar="DIR",
                     help="print the counters of a rocprofv3 --pmc run of --profile-kernel per call (--iters "
                          "calls), then exit (no GPU)")
-    ap.add_argument("--hw-queues", type=int, default=2,
-                    help="GPU_MAX_HW_QUEUES for this process, read by HIP when it initialises (the step's "
-                         "graph runs the main stream and its side streams on these queues); 0 keeps the "
-                         "environment's value")
     args = ap.parse_args(argv)
-    if args.hw_queues > 0 and "torch" not in sys.modules:
-        os.environ["GPU_MAX_HW_QUEUES"] = str(args.hw_queues)
     if args.trace_summary:
         print(trace_summary(args.trace_summary, args.steps))
         return 0
@@ -771,7 +765,6 @@ def main(argv=None) -> int:
             "seq_len": args.seq,
             "parallelism": "single GPU",
             "launch": "eager" if args.eager else "captured step graph",
-            "hw_queues": os.environ.get("GPU_MAX_HW_QUEUES", "runtime default"),
         },
     }
     if not args.no_roofline:

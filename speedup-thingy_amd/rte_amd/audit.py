@@ -168,6 +168,8 @@ class AuditEngine:
         self.last_sample_mode = "bernoulli"
         # False: the work begin() starts runs on the caller's stream, in order (one stream)
         self.side_streams = True
+        # the consistency loss in order on the caller's stream (the replay alone on a side stream)
+        self.consistency_on_main = True
 
     def state_dict(self) -> dict[str, object]:
         return {
@@ -271,14 +273,13 @@ class AuditEngine:
             if side != main:
                 launch.streams.append(side)
         if self.config.lambda_cons != 0.0:
-            side = self._side_stream(h0.device, 1)
+            side = main if self.consistency_on_main else self._side_stream(h0.device, 1)
             if ready is None:
                 self._share_macro_weights(model, side)
             if side != main:
                 side.wait_event(ready) if ready is not None else side.wait_stream(main)
-            with (nullcontext() if side == main else
-                  _aliases_installed(aliases, model.macro) if aliases is not None
-                  else main_stream_aliases(model.macro)), torch.cuda.stream(side):
+            with (_aliases_installed(aliases, model.macro) if aliases is not None else
+                  nullcontext() if side == main else main_stream_aliases(model.macro)), torch.cuda.stream(side):
                 launch.cons = model.macro.consistency_loss(h0, h0, route.recipe_id)
             if side != main:
                 launch.streams.append(side)
@@ -302,7 +303,7 @@ class AuditEngine:
         k = min(int(fixed), n)
         if k > 0 and chosen is None:
             chosen = self.fixed_count_index(n, k, seed, h0.device)
-        if self.config.lambda_cons != 0.0:
+        if self.config.lambda_cons != 0.0 and not self.consistency_on_main:
             self._share_macro_weights(model, self._side_stream(h0.device, 1))
         return chosen
 
