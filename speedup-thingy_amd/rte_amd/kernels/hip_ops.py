@@ -2391,7 +2391,10 @@ class MacroConsOnePassFn(torch.autograd.Function):
         call("rte_macro_cons_bwd", ptr(hv), b, S, d, ptr(kf), nf, ptr(ks), pc, src_lo, dst_lo, G, ptr(vb), ptr(ut),
              ptr(uq), ptr(tabs[0]), ptr(tabs[1]), ptr(tabs[2]), c, ptr(a), ptr(sa), ptr(rstd), ptr(gv), float(mul),
              ptr(du), ptr(da), ptr(part_tab), ptr(part_da), ptr(dsum), ptr(dh), _s())
-        keys = torch.cat([kf, ks])
+        if ks.data_ptr() == kf.data_ptr() + kf.numel() * kf.element_size():
+            keys = kf.as_strided((kf.numel() + ks.numel(),), (1,))  # ks follows kf in memory
+        else:
+            keys = torch.cat([kf, ks])
         grads = _macro_wgrad(keys, nf * b, b, pc * b, pc * b, S, d, G, x2, sa, du, da, pooled, dsum, part_tab,
                              nia[5:10], v_shape, u_shape, t_shape, dev)
         ctx.bufs = None

@@ -126,6 +126,10 @@ class MacroOperators(nn.Module):
         else:
             first, self.cons_src_lo, self.cons_dst_lo = dst + src, len(pairs), 0
         self.register_buffer("cons_key_idx", torch.tensor(first, dtype=torch.long), persistent=False)
+        # the first call's key offsets followed by the second call's (its src blocks): one key
+        # tensor holds both calls' keys back to back
+        ext = first + first[self.cons_src_lo:self.cons_src_lo + len(pairs)]
+        self.register_buffer("cons_key_ext", torch.tensor(ext, dtype=torch.long), persistent=False)
 
     def stride_ids_for_depths(self, depths: torch.Tensor) -> torch.Tensor:
         matches = depths.unsqueeze(-1) == self.depth_values.to(depths.device).unsqueeze(0)
@@ -274,11 +278,12 @@ class MacroOperators(nn.Module):
         nf = self.cons_key_idx.numel()
         if h is h0 and self._fused_bounded() and hip_ops.macro_fused_supported(self.v, self.u, nf):
             # both operator applications, the MSE and every backward path in the fused kernels;
-            # keys[p, i] = recipe_ids[i] Kk + cons_key_idx[p] in one launch
+            # keys[p, i] = recipe_ids[i] Kk + cons_key_ext[p] in one launch: the first call's nf key
+            # blocks, then the second call's pc (adjacent: the backward's grouped reductions read
+            # both without a copy)
             Kk = self.v.shape[1]
-            keys = torch.add(self.cons_key_idx.unsqueeze(1), recipe_ids.long().unsqueeze(0), alpha=Kk).reshape(-1)
-            s0 = self.cons_src_lo * b
-            return hip_ops.macro_consistency(h, keys, keys[s0:s0 + pc * b], self.v, self.u, self.d_gain, self.bias,
+            keys = torch.add(self.cons_key_ext.unsqueeze(1), recipe_ids.long().unsqueeze(0), alpha=Kk).reshape(-1)
+            return hip_ops.macro_consistency(h, keys[:nf * b], keys[nf * b:], self.v, self.u, self.d_gain, self.bias,
                                              self.update_scale, self.config.macro_update_scale,
                                              src_lo=self.cons_src_lo, dst_lo=self.cons_dst_lo)
         r_rep = recipe_ids.repeat(pc)
