@@ -702,12 +702,12 @@ __global__ void __launch_bounds__(256) route_bwd_kernel(const int32_t* __restric
 // route_gemm_topk: one workgroup per 32 tokens: router logits on MFMA, the top-k and softmax of
 // route_topk (same selections and weights on the same logits), and the block's cluster counts
 // to hist[block][C].
-// pack_place: one workgroup per 128 tokens (four route blocks): cluster offsets and the block's
+// pack_place: one workgroup per 32 tokens (one route block): cluster offsets and the block's
 // base per cluster from the histograms (integer sums), then per 256-pair chunk one ballot per
 // cluster and wave ranks the pairs; slots follow cluster, then ascending pair index, as
 // rte_pack_index.
 constexpr int kRouteTok = 32;     // tokens per route_gemm_topk block
-constexpr int kPlaceTok = 128;    // tokens per pack_place block
+constexpr int kPlaceTok = 32;     // tokens per pack_place block (one route block)
 
 __device__ __forceinline__ f32x16_v rt_mfma(bf16x8_v a, bf16x8_v b, f32x16_v c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -868,7 +868,7 @@ __global__ void __launch_bounds__(256) pack_place_kernel(const int32_t* __restri
   constexpr int VPR = C / 4;          // 16-byte vectors per histogram row
   constexpr int RPP = 256 / VPR;      // histogram rows per pass of the 256 threads
   constexpr int MW = C / 64 > 0 ? C / 64 : 1;  // 64-bit route-mask words per token
-  constexpr int SEG = kPlaceTok / 4;  // tokens per 32-bit segment mask (32)
+  constexpr int SEG = kPlaceTok / 4;  // tokens per segment mask (one per wave, at most 32)
   __shared__ int sb[RPP][C], st[RPP][C];
   __shared__ int base[C];
   __shared__ unsigned long long mask[kPlaceTok][MW];
