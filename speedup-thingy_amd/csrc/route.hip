@@ -761,7 +761,9 @@ __global__ void __launch_bounds__(256) route_gemm_topk_kernel(const bf16* __rest
                                                               int32_t* __restrict__ hist, float* __restrict__ logits) {
   constexpr int C = 32 * CB;
   constexpr int PER = C / 8;  // logits per lane in the top-k
-  __shared__ float part[4][C][kRouteTok + 1];
+  // row pitch 40 floats: the two half-waves' stores (rows 4 apart) and the top-k phase's reads
+  // (8 clusters x 8 tokens per wave) each cover 64 distinct banks
+  __shared__ float part[4][C][kRouteTok + 8];
   __shared__ int hs[C];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, h = lane >> 5, l32 = lane & 31;
   const int t0 = blockIdx.x * kRouteTok;
