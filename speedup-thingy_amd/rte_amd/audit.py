@@ -170,6 +170,10 @@ class AuditEngine:
         self.side_streams = True
         # the consistency loss in order on the caller's stream (the replay alone on a side stream)
         self.consistency_on_main = True
+        # late launch on the caller's stream: the consistency term's backward right after its
+        # forward (it reads neither the replay nor the hot path), so it runs while the step waits
+        # for the replay; its h0 gradient joins the step's at h0 (a hook)
+        self.consistency_backward_early = True
 
     def state_dict(self) -> dict[str, object]:
         return {
@@ -278,9 +282,18 @@ class AuditEngine:
                 self._share_macro_weights(model, side)
             if side != main:
                 side.wait_event(ready) if ready is not None else side.wait_stream(main)
+            early = (self.consistency_backward_early and ready is not None and side == main
+                     and torch.is_grad_enabled() and h0.requires_grad)
+            src = h0.detach().requires_grad_() if early else h0
             with (_aliases_installed(aliases, model.macro) if aliases is not None else
                   nullcontext() if side == main else main_stream_aliases(model.macro)), torch.cuda.stream(side):
-                launch.cons = model.macro.consistency_loss(h0, h0, route.recipe_id)
+                launch.cons = model.macro.consistency_loss(src, src, route.recipe_id)
+            if early:
+                torch.autograd.backward(self.config.lambda_cons * launch.cons)
+                launch.cons = launch.cons.detach()
+                dh0 = src.grad
+                if dh0 is not None:
+                    h0.register_hook(lambda g, dh0=dh0: g + dh0)
             if side != main:
                 launch.streams.append(side)
         return launch
