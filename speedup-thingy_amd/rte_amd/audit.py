@@ -289,7 +289,8 @@ class AuditEngine:
                   nullcontext() if side == main else main_stream_aliases(model.macro)), torch.cuda.stream(side):
                 launch.cons = model.macro.consistency_loss(src, src, route.recipe_id)
             if early:
-                torch.autograd.backward(self.config.lambda_cons * launch.cons)
+                # the step's backward runs on loss / grad_accum_steps
+                torch.autograd.backward(launch.cons * (self.config.lambda_cons / self.config.grad_accum_steps))
                 launch.cons = launch.cons.detach()
                 dh0 = src.grad
                 if dh0 is not None:

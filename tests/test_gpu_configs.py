@@ -267,6 +267,34 @@ def test_cfg3_side_launch_late_vs_early():
         assert torch.allclose(pa, pb, rtol=1e-5, atol=1e-6), na
 
 
+def test_cfg3_consistency_backward_early_grad_accum():
+    """The consistency term's backward issued right after its forward (on a detached h0 joined by
+    a hook) against its backward inside the step's: with two accumulated micro-steps the same
+    losses and, after the update, the same parameters (the early backward carries the step's
+    1 / grad_accum_steps)."""
+    import dataclasses
+
+    import bench
+
+    cfg = bench.cfg3_config(batch=16)
+    cfg = dataclasses.replace(cfg, training=dataclasses.replace(cfg.training, grad_accum_steps=2))
+    early, inside = _engine_from(cfg), _engine_from(cfg)
+    for e, flag in ((early, True), (inside, False)):
+        e.replay_coda_shared = False
+        e.audit_engine.consistency_backward_early = flag
+    gen = torch.Generator().manual_seed(cfg.training.seed)
+    batches = [bench.zipf_batch(gen, cfg.model.vocab_size, 16, 64, DEV) for _ in range(4)]
+    for step, batch in enumerate(batches):
+        print(f"cfg3 consistency early / inside, micro-step {step}", flush=True)
+        ra, rb = early.train_step(batch), inside.train_step(batch)
+        torch.cuda.synchronize()
+        la, lb = float(ra.loss), float(rb.loss)
+        assert math.isfinite(la) and abs(la - lb) <= 1e-5 * max(abs(la), 1.0), (step, la, lb)
+    assert early.global_step == inside.global_step == 2
+    for (na, pa), (_, pb) in zip(early.recursive_model.named_parameters(), inside.recursive_model.named_parameters()):
+        assert torch.allclose(pa, pb, rtol=1e-4, atol=1e-5), na
+
+
 def test_cfg5_shortlist_step():
     """the scaled recursive_macro_shortlist step (d1024, 16 heads, depth 8,
     pool 256 x 64 top-16, V8192 shortlist, B32 x S512): finite losses, parameters change, the
