@@ -223,9 +223,10 @@ def kernel_candidates(B: int, S: int):
     ms = torch.ones(R3, K3, d, device=dev)
     mh = torch.randn(B, S, d, device=dev, generator=g).requires_grad_()
     rid = torch.randint(0, R3, (B,), device=dev, generator=g)
-    # the first application's keys: the union of the strides, src = blocks [0, 2), dst = [1, 3)
-    kf = (rid * K3).repeat(3) + torch.arange(3, device=dev).repeat_interleave(B)
-    ks = kf[:2 * B]
+    # the first application's keys: the union of the strides, src = blocks [0, 2), dst = [1, 3); the
+    # second application's (the src blocks) right after them in one tensor, as the model makes them
+    kall = (rid * K3).repeat(5) + torch.tensor([0, 1, 2, 0, 1], device=dev).repeat_interleave(B)
+    kf, ks = kall[:3 * B], kall[3 * B:]
 
     def macro_cons():
         loss = hip_ops.macro_consistency(mh, kf, ks, mv, mu, mg, mb, ms, 0.1, src_lo=0, dst_lo=1)
