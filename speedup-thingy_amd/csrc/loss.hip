@@ -65,6 +65,41 @@ __global__ void __launch_bounds__(256) ce_fwd_kernel(const float* __restrict__ l
   }
 }
 
+// The same for V <= 4 * 64 * NV with V % 4 == 0: the row is read once into registers and both
+// passes run over them in the order of ce_fwd_kernel (bitwise the same results).
+template <int NV>
+__global__ void __launch_bounds__(256) ce_fwd_reg_kernel(const float* __restrict__ logits, int64_t ld, int T, int V,
+                                                         const int64_t* __restrict__ targets,
+                                                         float* __restrict__ loss, float* __restrict__ lse_out) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const float* row = logits + (int64_t)t * ld;
+  float4 v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane * 4 + 256 * i;
+    v[i] = c < V ? *reinterpret_cast<const float4*>(row + c) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane * 4 + 256 * i < V) mx = fmaxf(mx, fmaxf(fmaxf(v[i].x, v[i].y), fmaxf(v[i].z, v[i].w)));
+  mx = wave_max(mx);
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane * 4 + 256 * i < V)
+      s += __expf(v[i].x - mx) + __expf(v[i].y - mx) + __expf(v[i].z - mx) + __expf(v[i].w - mx);
+  s = wave_sum(s);
+  if (lane == 0) {
+    const float lse = mx + logf(s);
+    const int64_t tg = targets[t];
+    lse_out[t] = lse;
+    loss[t] = (tg >= 0 && tg < V) ? lse - row[tg] : 0.0f;
+  }
+}
+
 __global__ void __launch_bounds__(256) ce_bwd_kernel(const float* __restrict__ logits, int64_t ld, int T, int V,
                                                      const int64_t* __restrict__ targets,
                                                      const float* __restrict__ lse, const float* __restrict__ g,
@@ -271,7 +306,11 @@ int ce_fwd(const float* logits, int64_t ld, int T, int V, const int64_t* targets
   RTE_REQUIRE(V >= 1 && ld >= V && ld % 4 == 0, "ce_fwd: logits row stride must be >= V and a multiple of 4");
   RTE_REQUIRE(((uintptr_t)logits & 15) == 0, "ce_fwd: logits must be 16-byte aligned");
   if (T == 0) return 0;
-  hipLaunchKernelGGL(ce_fwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, ld, T, V, targets, loss, lse);
+  if (V % 4 == 0 && V <= 4 * 64 * 8)
+    hipLaunchKernelGGL(ce_fwd_reg_kernel<8>, dim3((T + 3) / 4), dim3(256), 0, s, logits, ld, T, V, targets, loss,
+                       lse);
+  else
+    hipLaunchKernelGGL(ce_fwd_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, ld, T, V, targets, loss, lse);
   return check_launch("ce_fwd");
 }
 

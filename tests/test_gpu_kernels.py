@@ -732,7 +732,7 @@ def test_svd_ffn_fused_matches_unfused_and_repeats(T, d, F, r):
 
 # ---------------------------------------------------------------- LM head + cross-entropy
 
-@pytest.mark.parametrize("T,d,V", [(64, 64, 128), (8192, 512, 2048)])
+@pytest.mark.parametrize("T,d,V", [(64, 64, 128), (8192, 512, 2048), (256, 64, 3000)])
 def test_lm_head_ce_fwd_bwd(T, d, V):
     from oracle import losses as L
 
