@@ -145,6 +145,70 @@ __global__ void __launch_bounds__(256) kl_rows_kernel(const float* __restrict__ 
   }
 }
 
+// The same for V <= 64 NV: both rows are read once into registers and the three passes run over
+// them in the order of kl_rows_kernel (bitwise the same results).
+template <int NV>
+__global__ void __launch_bounds__(256) kl_rows_reg_kernel(const float* __restrict__ hot, const float* __restrict__ ex,
+                                                          int R, int V, float inv_t, float* __restrict__ kl_row,
+                                                          float* __restrict__ klm_row, float* __restrict__ lse) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= R) return;
+  const float* hr = hot + (int64_t)r * V;
+  const float* er = ex + (int64_t)r * V;
+  float xs[NV], ys[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int c = lane + 64 * i;
+    xs[i] = c < V ? hr[c] : 0.0f;
+    ys[i] = c < V ? er[c] : 0.0f;
+  }
+  float mh = -INFINITY, me = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i < V) {
+      mh = fmaxf(mh, xs[i]);
+      me = fmaxf(me, ys[i]);
+    }
+  mh = wmax(mh);
+  me = wmax(me);
+  float sh_t = 0.0f, se_t = 0.0f, sh_1 = 0.0f, se_1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i < V) {
+      const float x = xs[i], y = ys[i];
+      sh_t += __expf((x - mh) * inv_t);
+      se_t += __expf((y - me) * inv_t);
+      sh_1 += __expf(x - mh);
+      se_1 += __expf(y - me);
+    }
+  sh_t = wsum(sh_t);
+  se_t = wsum(se_t);
+  sh_1 = wsum(sh_1);
+  se_1 = wsum(se_1);
+  const float lq_t = mh * inv_t + logf(sh_t), lp_t = me * inv_t + logf(se_t);
+  const float lq_1 = mh + logf(sh_1), lp_1 = me + logf(se_1);
+  float kt = 0.0f, k1 = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i < V) {
+      const float x = xs[i], y = ys[i];
+      const float logp = y * inv_t - lp_t, logq = x * inv_t - lq_t;
+      const float p = __expf(logp);
+      kt += p > 0.0f ? p * (logp - logq) : 0.0f;
+      const float te = y - lp_1, th = x - lq_1;
+      k1 += __expf(te) * (te - th);
+    }
+  kt = wsum(kt);
+  k1 = wsum(k1);
+  if (lane == 0) {
+    kl_row[r] = kt;
+    klm_row[r] = k1;
+    lse[2 * r] = lq_t;
+    lse[2 * r + 1] = lp_t;
+  }
+}
+
 // losses: [0..4] delta_dir, delta_rms, endpoint_normed, endpoint_raw, rms_trust, [5] kl;
 // metrics: [0] hidden_cosine, [1] hidden_mse, [2] macro_norm, [3] exact_norm,
 // [4] macro_exact_norm_ratio, [5] delta_cosine, [6] delta_rms_exact, [7] delta_rms_pred,
@@ -300,8 +364,12 @@ int distill_fwd(const float* hot, const float* exact, const float* h0, int A, in
   hipLaunchKernelGGL(distill_sample_kernel, dim3(A, kSplit), dim3(256), 0, s, hot, exact, h0, S, d, eps, parts);
   RTE_TRY(check_launch("distill_sample"));
   if (R > 0) {
-    hipLaunchKernelGGL(kl_rows_kernel, dim3((R + 3) / 4), dim3(256), 0, s, hot_logits, exact_logits, R, V, 1.0f / t,
-                       kl_row, klm_row, lse);
+    if (V <= 64 * 32)
+      hipLaunchKernelGGL(kl_rows_reg_kernel<32>, dim3((R + 3) / 4), dim3(256), 0, s, hot_logits, exact_logits, R, V,
+                         1.0f / t, kl_row, klm_row, lse);
+    else
+      hipLaunchKernelGGL(kl_rows_kernel, dim3((R + 3) / 4), dim3(256), 0, s, hot_logits, exact_logits, R, V,
+                         1.0f / t, kl_row, klm_row, lse);
     RTE_TRY(check_launch("distill_kl_rows"));
   }
   LossWeights lw;

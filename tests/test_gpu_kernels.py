@@ -1135,7 +1135,7 @@ def test_axpy_norm_matches_float64(B, S, d, norm, use_mask):
 
 # ---------------------------------------------------------------- audit distillation
 
-@pytest.mark.parametrize("A,S,d,V", [(1, 64, 512, 2048), (3, 17, 96, 100), (2, 8, 64, 0)])
+@pytest.mark.parametrize("A,S,d,V", [(1, 64, 512, 2048), (3, 17, 96, 100), (2, 8, 64, 0), (1, 8, 64, 3000)])
 def test_distill_matches_oracle(A, S, d, V):
     from oracle import distill as DI
 
